@@ -1,0 +1,321 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized paged-KV-cache path on one MI355X.
+
+Prints ONE JSON line (rank 0) with BASELINE.json's metric -- achieved HBM GB/s of the
+headline workload, its fraction of the 8 TB/s peak and tokens/s -- plus the ``roofline``,
+``cpu_baseline`` and ``per_config`` objects.
+
+* A step is one call of the op over one batch of the workload's synthetic input, with the
+  inputs resident in HBM.  Calls rotate over enough independent buffer sets that each
+  launch's working set has been evicted from the 256 MB MALL since its last use; the
+  calls are captured in a HIP graph (so the latency-bound configs measure the GPU, not the
+  Python launch path) and the timed region is bracketed by HIP events recorded on the stream
+  the kernels run on, with device synchronisation on both sides.
+* GB/s counts ALGORITHMIC bytes (rows actually read, codes + scales written, index tensors,
+  the smooth vector once), per BASELINE.md section 2.
+* ``cpu_baseline`` times the CPU oracle (a C restatement of the reference math, pthreads)
+  on a bounded sample of the headline workload, on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg3]
+       [--configs all|headline] [--cpu-seconds S]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+METRIC = "achieved HBM GB/s (% of MI355X peak) + tokens/s quantized into paged KV cache"
+PEAK_GBS = 8000.0          # MI355X HBM3E
+MALL_EVICT_BYTES = 1 << 30  # rotate buffer sets until one pass touches >= 1 GiB
+
+WORKLOADS = {
+    "cfg1": "configs[0]: quant_to_paged_cache, 16 tokens x 8 KV heads x 128, bf16 -> int8 pages (64 blocks x 16)",
+    "cfg2": "configs[1]: quant_to_paged_cache decode step, 256 seqs x 1 token x 8 KV heads x 128, bf16 -> int8 pages (16384 blocks x 16), 10% slots -1",
+    "cfg3": "configs[2]: quant_to_paged_cache prefill chunk, 32768 tokens x 8 KV heads x 128, bf16 -> int8 pages (65536 blocks x 16)",
+    "cfg4": "configs[3]: per_token_smooth_quantize 8192 x 4096 bf16 -> int8 + fp32 per-token scale",
+    "cfg4_moe": "configs[3] MoE: per_token_smooth_quantize over 16384 gathered rows (top-2 of 64 experts), per-expert smooth",
+    "cfg5": "configs[4]: dequant_from_paged_cache, 64 seqs ctx ~U[1024,32768], 8 KV heads x 128, int8 pages -> bf16",
+}
+KERNELS = {"cfg1": "quant_paged_vec<BF16,16>", "cfg2": "quant_paged_vec<BF16,16>",
+           "cfg3": "quant_paged_vec<BF16,16>", "cfg4": "sq_vec<BF16,8>",
+           "cfg4_moe": "sq_vec<BF16,8>", "cfg5": "dequant_paged_vec<BF16,4>"}
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="cfg3", choices=sorted(WORKLOADS))
+    ap.add_argument("--configs", default="all", choices=["all", "headline"])
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------- GPU timing
+
+def time_graph(torch, calls, steps: int, warmup: int) -> float:
+    """Mean ms per call: `calls` (one closure per buffer set) captured once into a HIP graph,
+    replayed until `steps` calls have run; HIP events on the capture stream bracket the timed
+    replays."""
+    n = len(calls)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for c in calls:  # eager warm-up of every set (also loads the code object)
+            c()
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for c in calls:
+            c()
+    reps = max(1, math.ceil(steps / n))
+    wreps = max(1, math.ceil(warmup / n))
+    with torch.cuda.stream(stream):
+        for _ in range(wreps):
+            graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / (reps * n)
+    del graph
+    return ms
+
+
+def n_sets(bytes_per_call: int, cap: int = 512) -> int:
+    return max(1, min(cap, math.ceil(MALL_EVICT_BYTES / max(1, bytes_per_call))))
+
+
+def bench_paged_quant(torch, tmo, W, case, dev, steps, warmup):
+    """quant_to_paged_cache: per set its own K/V rows, slot mapping and caches."""
+    alg = case.algorithmic_bytes()
+    sets = n_sets(alg)
+    g = torch.Generator(device=dev).manual_seed(7)
+    base_k, base_v = case.k.to(dev), case.v.to(dev)
+    slots0 = case.slot_mapping.to(dev)
+    nslots = case.num_blocks * case.block_size
+    # caches: one per set when small, else shared caches with per-set disjoint slot ranges
+    cache_bytes = nslots * case.k.shape[1] * (case.k.shape[2] + 4) * 2
+    calls = []
+    shared = None
+    if cache_bytes * sets > (8 << 30):
+        shared = case.empty_caches(device=dev)
+    for s in range(sets):
+        if s == 0:
+            k, v, slots = base_k, base_v, slots0
+        else:
+            k = torch.randn(base_k.shape, generator=g, device=dev).to(base_k.dtype)
+            v = torch.randn(base_v.shape, generator=g, device=dev).to(base_v.dtype)
+            # same structure (contiguity, -1 entries) at a different page offset
+            shift = (s * 9973 * case.block_size) % nslots
+            slots = torch.where(slots0 >= 0, (slots0 + shift) % nslots, slots0)
+        kc, vc, ks, vs = shared if shared is not None else case.empty_caches(device=dev)
+        calls.append(lambda k=k, v=v, kc=kc, vc=vc, ks=ks, vs=vs, sl=slots:
+                     tmo.quant_to_paged_cache(k, v, kc, vc, ks, vs, sl))
+    ms = time_graph(torch, calls, steps, warmup)
+    return ms, alg, case.valid_tokens(), sets
+
+
+def bench_smooth_quant(torch, tmo, W, case, dev, steps, warmup):
+    alg = case.algorithmic_bytes()
+    sets = n_sets(alg)
+    g = torch.Generator(device=dev).manual_seed(8)
+    calls = []
+    for s in range(sets):
+        x = case.x.to(dev) if s == 0 else \
+            torch.randn(case.x.shape, generator=g, device=dev).to(case.x.dtype)
+        sm = case.smooth.to(dev)
+        tc = case.token_count.to(dev) if case.token_count is not None else None
+        gi = case.gather_index.to(dev) if case.gather_index is not None else None
+        out = torch.empty((case.rows, x.shape[-1]), dtype=torch.int8, device=dev)
+        sc = torch.empty((case.rows,), dtype=torch.float32, device=dev)
+        calls.append(lambda x=x, sm=sm, tc=tc, gi=gi, out=out, sc=sc:
+                     tmo.moe_quantize(x, sm, None, tc, gi, None, out, sc))
+    ms = time_graph(torch, calls, steps, warmup)
+    return ms, alg, case.rows, sets
+
+
+def bench_dequant(torch, tmo, W, layout, dev, steps, warmup):
+    alg = layout.algorithmic_bytes()
+    kc, vc, ks, vs = W.cfg5_fill(layout, dev)
+    total = layout.total_tokens
+    key = torch.empty((total, kc.shape[1], kc.shape[3]), dtype=torch.bfloat16, device=dev)
+    value = torch.empty_like(key)
+    ctx = layout.context_lengths.to(dev)
+    bt = layout.block_tables.to(dev)
+    mctx = layout.max_context_len
+    calls = [lambda: tmo.dequant_from_paged_cache(key, value, kc, vc, ks, vs, ctx, mctx, None,
+                                                  bt, 1, 8)]
+    ms = time_graph(torch, calls, steps, warmup)
+    return ms, alg, total, 1
+
+
+def launch_floor_us(torch, tmo, dev) -> float:
+    """Duration of the smallest quant_to_paged_cache launch (1 token, 1 head) -- the per-call
+    floor that bounds the latency-bound configs."""
+    k = torch.randn(1, 1, 128, device=dev).to(torch.bfloat16)
+    kc = torch.zeros(1, 1, 16, 128, dtype=torch.int8, device=dev)
+    ks = torch.zeros(1, 1, 16, device=dev)
+    sl = torch.zeros(1, dtype=torch.int32, device=dev)
+    calls = [lambda: tmo.quant_to_paged_cache(k, None, kc, None, ks, None, sl)] * 64
+    return 1000.0 * time_graph(torch, calls, 640, 64)
+
+
+# ---------------------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
+    """The CPU oracle on a bounded sample of the headline workload, on this host's cores."""
+    import oracle
+    nthreads = oracle.default_threads()
+    if workload in ("cfg1", "cfg2", "cfg3"):
+        case = getattr(W, workload)()
+        n = min(case.tokens, 4096)
+        sub = W.PagedQuantCase(case.name, case.k[:n].contiguous(), case.v[:n].contiguous(),
+                               case.slot_mapping[:n].contiguous(), case.num_blocks)
+        kc, vc, ks, vs = sub.empty_caches()
+        fn = lambda: oracle.quant_to_paged_cache(sub.k, sub.v, kc, vc, ks, vs, sub.slot_mapping,
+                                                 nthreads=nthreads)
+        alg, units, desc = sub.algorithmic_bytes(), sub.valid_tokens(), \
+            f"quant_to_paged_cache on the first {n} tokens of {workload}"
+    elif workload.startswith("cfg4"):
+        case = getattr(W, workload)()
+        n = min(case.rows, 2048)
+        gi = case.gather_index[:n].contiguous() if case.gather_index is not None else None
+        x = case.x if gi is not None else case.x[:n].contiguous()
+        tc = None
+        if case.token_count is not None:  # the first n rows keep their expert grouping
+            ends = torch.cumsum(case.token_count.to(torch.int64), 0).clamp(max=n)
+            tc = torch.diff(ends, prepend=torch.zeros(1, dtype=torch.int64)).to(torch.int32)
+        sub = W.SmoothQuantCase(case.name, x, case.smooth, tc, gi)
+        out = torch.empty((n, x.shape[-1]), dtype=torch.int8)
+        sc = torch.empty((n,), dtype=torch.float32)
+        fn = lambda: oracle.scaled_quantize_per_token(sub.x, out, sc, sub.smooth, sub.token_count,
+                                                      sub.gather_index, nthreads=nthreads)
+        alg, units, desc = sub.algorithmic_bytes(), n, f"smooth quant of the first {n} rows of {workload}"
+    else:
+        layout = W.cfg5()
+        nseq = 2
+        ctx = layout.context_lengths[:nseq].contiguous()
+        pages = [(int(c) + W.BS - 1) // W.BS for c in ctx.tolist()]
+        bt = torch.zeros(nseq, max(pages), dtype=torch.int32)
+        p0 = 0
+        for i, p in enumerate(pages):  # the sample's pages renumbered into a compact cache
+            bt[i, :p] = torch.arange(p0, p0 + p, dtype=torch.int32)
+            p0 += p
+        sub = W.DequantLayout("cfg5-sample", ctx, bt, p0)
+        g = torch.Generator().manual_seed(5)
+        kc = torch.randint(-127, 128, (p0, W.H, W.BS, W.D), generator=g, dtype=torch.int8)
+        vc = torch.randint(-127, 128, (p0, W.H, W.BS, W.D), generator=g, dtype=torch.int8)
+        ks = torch.rand(p0, W.H, W.BS, generator=g) * 0.05
+        vs = torch.rand(p0, W.H, W.BS, generator=g) * 0.05
+        key = torch.empty(sub.total_tokens, W.H, W.D, dtype=torch.bfloat16)
+        value = torch.empty_like(key)
+        fn = lambda: oracle.dequant_from_paged_cache(key, value, kc, vc, ks, vs, ctx, None, bt, 1,
+                                                     nthreads=nthreads)
+        alg, units = sub.algorithmic_bytes(), sub.total_tokens
+        desc = f"dequant of the first {nseq} sequences of cfg5 ({units} tokens)"
+    fn()  # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(alg / t / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+            "sample": f"{desc}; median of {len(times)} runs, {t * 1e3:.3f} ms each",
+            "tokens_per_s": round(units / t, 1)}
+
+
+# ---------------------------------------------------------------------------- main
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards without any exchange -- see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import domesticated_torch_mlu_ops_amd as tmo
+    from tests import workloads as W
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    todo = [args.workload] if args.configs == "headline" else \
+        ["cfg1", "cfg2", "cfg3", "cfg4", "cfg4_moe", "cfg5"]
+    if args.workload not in todo:
+        todo.append(args.workload)
+    per = {}
+    for name in todo:
+        t0 = time.perf_counter()
+        if name in ("cfg1", "cfg2", "cfg3"):
+            ms, alg, units, sets = bench_paged_quant(torch, tmo, W, getattr(W, name)(), dev,
+                                                     args.steps, args.warmup)
+        elif name.startswith("cfg4"):
+            ms, alg, units, sets = bench_smooth_quant(torch, tmo, W, getattr(W, name)(), dev,
+                                                      args.steps, args.warmup)
+        else:
+            ms, alg, units, sets = bench_dequant(torch, tmo, W, W.cfg5(), dev,
+                                                 max(10, args.steps // 10), max(2, args.warmup // 10))
+        gbs = alg / (ms * 1e-3) / 1e9
+        per[name] = {"kernel": KERNELS[name], "us_per_call": round(ms * 1e3, 3),
+                     "algorithmic_bytes": alg, "GB_s": round(gbs, 1),
+                     "frac_of_peak": round(gbs / PEAK_GBS, 4),
+                     "units_per_s": round(units / (ms * 1e-3), 1), "buffer_sets": sets}
+        print(f"# {name}: {ms * 1e3:.2f} us/call  {gbs:.1f} GB/s  ({100 * gbs / PEAK_GBS:.1f}% of "
+              f"peak)  [{time.perf_counter() - t0:.1f} s]", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+    floor = launch_floor_us(torch, tmo, dev) if args.configs == "all" else None
+
+    head = per[args.workload]
+    traffic = None
+    tfile = REPO / "profiles" / "traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get(args.workload, {}).get("hbm_bytes_per_launch")
+    cpu = cpu_baseline(torch, W, args.workload, args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": head["GB_s"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_call"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded, BASELINE.md section 3)",
+        "config": {"workload": WORKLOADS[args.workload],
+                   "io": "bf16 in; int8 codes + fp32 scales out" if args.workload != "cfg5"
+                   else "int8 codes + fp32 scales in; bf16 out",
+                   "tokens_per_s": head["units_per_s"],
+                   "frac_of_peak": head["frac_of_peak"]},
+        "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": head["frac_of_peak"], "traffic": traffic,
+                     "kernel": head["kernel"]},
+        "cpu_baseline": cpu,
+        "per_config": per,
+        "launch_floor_us": round(floor, 3) if floor is not None else None,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

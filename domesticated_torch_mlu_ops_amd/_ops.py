@@ -1,0 +1,211 @@
+"""Python op surface of the quantized paged-KV-cache path.
+
+Signatures, argument meaning and return conventions are those of the reference wrappers
+(cited per function); each wrapper is a call of the ``torch_mlu_ops::*`` op registered by
+``_lib/_tmo_torch.so``, whose HIP kernel calls the C ABI of ``include/tmo_hip.h``.  Outputs are
+written in place; the wrappers allocate only where the reference wrappers do.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple, Union
+
+import torch
+
+__all__ = [
+    "reshape_paged_cache",
+    "quant_to_paged_cache",
+    "dequant_from_paged_cache",
+    "moe_quantize",
+    "scaled_quantize",
+    "per_token_smooth_quantize",
+]
+
+
+def reshape_paged_cache(
+    k: torch.Tensor,
+    v: Optional[torch.Tensor],
+    k_cache: torch.Tensor,
+    v_cache: Optional[torch.Tensor],
+    slot_mapping: torch.Tensor,
+    direction: bool = False,
+) -> Union[Tuple[torch.Tensor], torch.Tensor]:
+    """Scatter k/v ``[num_tokens, heads, head_size]`` rows into the paged caches
+    ``[num_blocks, heads, block_size, head_size]`` at ``slot_mapping`` (``direction=False``),
+    or gather them back into k/v (``direction=True``).  Tokens whose slot is negative are
+    skipped.  Byte-exact for float, half, bfloat16 and int8.
+
+    Reference: ``_ops.py:1251-1294`` (math ``:1262-1268``).  Returns k (and v) when
+    ``direction`` is True, else k_cache (and v_cache), as the reference does.
+    """
+    torch.ops.torch_mlu_ops.reshape_paged_cache(k, v, k_cache, v_cache, slot_mapping, direction)
+    if direction:
+        return (k, v) if v is not None else k
+    return (k_cache, v_cache) if v_cache is not None else k_cache
+
+
+def quant_to_paged_cache(
+    k: torch.Tensor,
+    v: Optional[torch.Tensor],
+    k_cache: torch.Tensor,
+    v_cache: Optional[torch.Tensor],
+    k_cache_quant_scale: torch.Tensor,
+    v_cache_quant_scale: Optional[torch.Tensor],
+    slot_mapping: torch.Tensor,
+) -> Tuple[torch.Tensor]:
+    """Dynamic per-(token, head) int8 quantisation of k/v into the paged caches.
+
+    For each token ``i`` with ``slot_mapping[i] >= 0`` and each head ``h``:
+    ``scale = fp32(max|k[i, h]|) / 127``, ``code = clip(round_half_even(k[i, h] / scale),
+    -128, 127)``; codes go to ``k_cache[slot // bs, h, slot % bs]`` and the scale to
+    ``k_cache_quant_scale[slot // bs, h, slot % bs]`` (same for v).  An all-zero row stores
+    scale 0 and codes 0.  k/v: float, half or bfloat16 (may be strided views); caches int8.
+
+    Reference: ``_ops.py:1511-1565`` (math ``:1524-1537``).  Returns
+    ``(k_cache, v_cache, k_scale, v_scale)`` or ``(k_cache, k_scale)``.
+    """
+    torch.ops.torch_mlu_ops.quant_to_paged_cache(
+        k, v, k_cache, v_cache, k_cache_quant_scale, v_cache_quant_scale, slot_mapping)
+    if v_cache is not None:
+        return (k_cache, v_cache, k_cache_quant_scale, v_cache_quant_scale)
+    return (k_cache, k_cache_quant_scale)
+
+
+def dequant_from_paged_cache(
+    key: torch.Tensor,
+    value: Optional[torch.Tensor],
+    key_cache: torch.Tensor,
+    value_cache: Optional[torch.Tensor],
+    key_cache_quant_scale: torch.Tensor,
+    value_cache_quant_scale: Optional[torch.Tensor],
+    context_lengths: torch.Tensor,
+    max_context_len: int,
+    context_seq_offset: Optional[torch.Tensor],
+    block_tables: torch.Tensor,
+    quant_mode: int = 0,
+    quant_bit: int = 8,
+) -> None:
+    """Gather each sequence's pages through ``block_tables`` and write
+    ``key[begin_i + t] = (fp32(code) * scale).to(key.dtype)`` for ``t < context_lengths[i]``;
+    ``begin_i`` is ``context_seq_offset[i]`` or the running sum of ``context_lengths``.
+    ``quant_mode`` 0: per-channel scale ``[heads, head_size]``; 1: per-token scale
+    ``[num_blocks, heads, block_size]``.  ``quant_bit`` must be 8 (the mx-fp6 mode 2 is not
+    part of this build).
+
+    Reference: ``_ops.py:3734-3824`` (math ``:3749-3774``).  Returns None.
+    """
+    torch.ops.torch_mlu_ops.dequant_from_paged_cache(
+        key, value, key_cache, value_cache, key_cache_quant_scale, value_cache_quant_scale,
+        context_lengths, max_context_len, context_seq_offset, block_tables, quant_mode, quant_bit)
+
+
+def moe_quantize(
+    x: torch.Tensor,
+    smooth: torch.Tensor,
+    zero: Optional[torch.Tensor] = None,
+    token_count: Optional[torch.Tensor] = None,
+    gather_index: Optional[torch.Tensor] = None,
+    gather_index_start_position: Optional[torch.Tensor] = None,
+    output: Optional[torch.Tensor] = None,
+    output_scale: Optional[torch.Tensor] = None,
+    dynamic_quant: bool = True,
+    act_mode: str = "none",
+    active_coef: float = 1.0,
+    is_gated: bool = False,
+    quant_type: torch.dtype = torch.int8,
+    quant_bit_size=8,
+    scale_type=torch.float32,
+    need_output_scale_trans: bool = False,
+    output_reduced: Optional[torch.Tensor] = None,
+    group_size: int = 1,
+) -> Tuple[torch.Tensor]:
+    """Smooth + dynamic per-token int8 quantisation, optionally over gathered rows
+    (``x[gather_index]``) with per-group smooth rows (``token_count`` splits the rows into
+    groups, group ``g`` uses ``smooth[g]``):
+    ``smoothed = fp32(x) * smooth``; ``scale = max|smoothed| / 127``;
+    ``output = clip(round_half_even(smoothed / scale), -128, 127)``.
+
+    Reference: ``_ops.py:3126-3253`` (math ``:3147-3176``, shapes ``:3220-3248``).  This build
+    implements ``dynamic_quant=True``, ``act_mode="none"``, int8 output and fp32 scales; the
+    other modes raise RuntimeError from the op.  Returns ``(output, output_scale)``.
+    """
+    tokens, ci = x.shape[0], x.shape[-1]
+    if gather_index is not None:
+        tokens = gather_index.size(0)
+    if quant_type == torch.int8 and quant_bit_size == 4:
+        ci = ci // 2 // (1 + is_gated)
+    else:
+        ci = ci // (1 + is_gated)
+    output_shape = ((tokens,) + tuple(x.shape[1:-1]) + (ci,))[: x.dim()]
+    scale_shape = ((tokens,) + tuple(x.shape[1:-1]))[: x.dim() - 1]
+    if output is None:
+        output = torch.empty(output_shape, dtype=quant_type, device=x.device)
+    if output_scale is None and dynamic_quant:
+        output_scale = torch.empty(scale_shape, dtype=scale_type, device=x.device)
+    torch.ops.torch_mlu_ops.scaled_quantize(
+        x, output, output_scale, smooth, zero, token_count, gather_index,
+        gather_index_start_position, None,
+        "dynamic_per_token" if dynamic_quant else "static_per_channel",
+        act_mode, active_coef, is_gated, quant_bit_size, need_output_scale_trans,
+        output_reduced, group_size)
+    return (output, output_scale) if dynamic_quant else (output,)
+
+
+def scaled_quantize(
+    x: torch.Tensor,
+    scale: Optional[torch.Tensor] = None,
+    zero: Optional[torch.Tensor] = None,
+    scale_ub: Optional[torch.Tensor] = None,
+    quant_type=torch.int8,
+    quant_mode: str = "dynamic_per_token",
+    act_mode: str = "none",
+    active_coef: float = 1.0,
+    is_gated: bool = False,
+    quant_bit_size: int = 8,
+    scale_type=torch.float32,
+    need_output_scale_trans: bool = False,
+    output_reduced: Optional[torch.Tensor] = None,
+    group_size: int = 1,
+) -> Tuple[torch.Tensor]:
+    """Per-token int8 quantisation of ``x [..., C]`` with an optional smooth vector
+    ``scale`` (shape ``[C]`` or ``[1]``).
+
+    Reference: ``_ops.py:4407-4492``.  This build implements ``quant_mode="dynamic_per_token"``
+    with int8 output and fp32 scales (``act_mode="none"``).  Returns ``(output, output_scale)``.
+    """
+    is_dynamic = quant_mode in ("dynamic_per_token", "dynamic_per_tensor")
+    cols = x.size(-1) // (1 + is_gated)
+    if quant_type == torch.int8 and quant_bit_size == 4:
+        cols = x.size(-1) // 2 // (1 + is_gated)
+    output = torch.empty(x.size()[:-1] + (cols,), dtype=quant_type, device=x.device)
+    output_scale = None
+    if quant_mode == "dynamic_per_tensor":
+        output_scale = torch.empty(1, dtype=torch.float32, device=x.device)
+    elif quant_mode == "dynamic_per_token":
+        output_scale = torch.empty(x.size()[:-1], dtype=scale_type, device=x.device)
+    torch.ops.torch_mlu_ops.scaled_quantize(
+        x, output, output_scale, scale, zero, None, None, None, scale_ub, quant_mode, act_mode,
+        active_coef, is_gated, quant_bit_size, need_output_scale_trans, output_reduced,
+        group_size)
+    return (output, output_scale) if is_dynamic else output
+
+
+def per_token_smooth_quantize(
+    x: torch.Tensor,
+    smooth: torch.Tensor,
+    zero: Optional[torch.Tensor] = None,
+    token_count: Optional[torch.Tensor] = None,
+    gather_index: Optional[torch.Tensor] = None,
+    gather_index_start_position: Optional[torch.Tensor] = None,
+    output: Optional[torch.Tensor] = None,
+    output_scale: Optional[torch.Tensor] = None,
+    dynamic_quant: bool = True,
+) -> Tuple[torch.Tensor]:
+    """Alias of :func:`moe_quantize` restricted to its smooth-quant arguments.
+
+    Not a reference API: the reference exposes this operation as ``moe_quantize``
+    (``_ops.py:3126-3253``) and ``scaled_quantize`` (``_ops.py:4407-4492``), both lowering to
+    the op ``scaled_quantize`` in mode ``'dynamic_per_token'``.  Returns
+    ``(output, output_scale)``.
+    """
+    return moe_quantize(x, smooth, zero, token_count, gather_index, gather_index_start_position,
+                        output, output_scale, dynamic_quant)

@@ -1,0 +1,58 @@
+"""Fake (meta) kernels of the path's ops, registered unconditionally.
+
+The reference registers its fakes only when ``torch.__version__ >= '2.3.0'`` holds as a
+*string* comparison (reference ``__init__.py:3``), which is False for torch 2.10, so on
+current torch it registers none.  Here they are always registered.  Every op writes its
+outputs in place and returns nothing (reference ``abstract.py:148-152``, ``172-182``,
+``746-761``, ``811-832``); the fake of ``scaled_quantize`` follows the C++ parameter order
+(reference ``include/torch_mlu_ops.h:334-350``), without the extra ``quant_type`` parameter
+of reference ``abstract.py:822``.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+__all__: list = []
+
+
+@torch.library.register_fake("torch_mlu_ops::reshape_paged_cache")
+def reshape_paged_cache_abstract(k: Tensor, v: Optional[Tensor], k_cache: Tensor,
+                                 v_cache: Optional[Tensor], slot_mapping: Tensor,
+                                 direction: bool) -> None:
+    return None
+
+
+@torch.library.register_fake("torch_mlu_ops::quant_to_paged_cache")
+def quant_to_paged_cache_abstract(k: Tensor, v: Optional[Tensor], k_cache: Tensor,
+                                  v_cache: Optional[Tensor], k_cache_scale: Tensor,
+                                  v_cache_scale: Optional[Tensor], slot_mapping: Tensor) -> None:
+    return None
+
+
+@torch.library.register_fake("torch_mlu_ops::dequant_from_paged_cache")
+def dequant_from_paged_cache_abstract(key: Tensor, value: Optional[Tensor], key_cache: Tensor,
+                                      value_cache: Optional[Tensor],
+                                      key_cache_quant_scale: Tensor,
+                                      value_cache_quant_scale: Optional[Tensor],
+                                      context_lengths: Tensor, max_context_len: int,
+                                      context_seq_offset: Optional[Tensor], block_tables: Tensor,
+                                      quant_mode: int = 0, quant_bit: int = 8) -> None:
+    return None
+
+
+@torch.library.register_fake("torch_mlu_ops::scaled_quantize")
+def scaled_quantize_abstract(x: Tensor, output: Tensor, output_scale: Optional[Tensor],
+                             x_scale: Optional[Tensor] = None, x_zero: Optional[Tensor] = None,
+                             m_list: Optional[Tensor] = None,
+                             gather_index: Optional[Tensor] = None,
+                             gather_index_start_position: Optional[Tensor] = None,
+                             scale_upper_bound: Optional[Tensor] = None,
+                             quant_mode: str = "dynamic_per_token", act_mode: str = "none",
+                             active_coef: float = 1.0, is_gated: bool = False,
+                             quant_bit_size: int = 8, need_output_scale_trans: bool = False,
+                             output_reduced: Optional[Tensor] = None,
+                             group_size: int = 1) -> None:
+    return None

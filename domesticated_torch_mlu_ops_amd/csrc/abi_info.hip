@@ -1,0 +1,15 @@
+// Version and status-text entry points of libtmo_hip.so (include/tmo_hip.h).
+#include "tmo_hip.h"
+
+extern "C" int tmo_hip_abi_version(void) { return TMO_HIP_ABI_VERSION; }
+
+extern "C" const char* tmo_hip_status_string(int status) {
+  switch (status) {
+    case TMO_OK: return "ok";
+    case TMO_ERR_INVALID_ARGUMENT: return "invalid argument (null pointer, size or stride)";
+    case TMO_ERR_UNSUPPORTED_DTYPE: return "unsupported dtype";
+    case TMO_ERR_UNSUPPORTED_MODE: return "unsupported quant_mode / quant_bit";
+    case TMO_ERR_LAUNCH: return "HIP kernel launch failed";
+    default: return "unknown status";
+  }
+}

@@ -1,0 +1,260 @@
+// dequant_from_paged_cache for gfx950: gathers each sequence's int8 pages through its block
+// table and writes RNE(fp32(code) * scale) as bf16 / fp16 into packed [sum(ctx), H, D] rows.
+//
+// Semantics: reference _ops.py:3734-3824 (math block :3749-3774; cast order of the linear
+// sibling :3677; quant_mode 0 per-channel scale [H, D], 1 per-token scale [NB, H, BS]).
+// Entry point: tmo_hip_dequant_from_paged_cache (include/tmo_hip.h).
+//
+// One workgroup per (sequence, page).  A page of one head is block_size * head_dim
+// contiguous bytes, and all heads of a block are contiguous, so the workgroup streams the
+// whole [H, BS, D] block (K and V) with 16-byte loads, every thread holding kIters units of
+// each in flight before it converts and stores 32-byte output runs.  The output rows of the
+// page's tokens are consecutive, so the stores are contiguous as well.
+#include "tmo_device.h"
+
+namespace tmo {
+namespace {
+
+struct DequantParams {
+  void* out[2];
+  int64_t out_st[2];  // elements
+  int64_t out_sh[2];  // elements
+  int64_t total_rows;
+  const int8_t* cache[2];
+  const float* scale[2];
+  const int32_t* ctx_len;
+  const int32_t* seq_off;  // nullable
+  const int32_t* block_tables;
+  int64_t batch;
+  int64_t max_blocks;    // row length of block_tables
+  int64_t grid_blocks;   // pages per sequence covered by the grid
+  int64_t num_blocks;
+  int32_t heads;
+  int32_t block_size;
+  int32_t head_dim;
+  int32_t u_shift;   // log2(head_dim / 16)        (vector path)
+  int32_t bs_shift;  // log2(block_size)           (vector path)
+  int32_t mode;      // 0 per-channel, 1 per-token
+  int32_t nkv;
+};
+
+// Exclusive prefix sum of ctx_len[0..i), computed by the whole workgroup.
+__device__ int64_t seq_begin(const DequantParams& p, int64_t i, int64_t* red) {
+  if (p.seq_off) return p.seq_off[i];
+  int64_t acc = 0;
+  for (int64_t k = threadIdx.x; k < i; k += blockDim.x) acc += p.ctx_len[k];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = acc;
+  __syncthreads();
+  int64_t total = 0;
+  for (int w = 0; w < (int)(blockDim.x / kWave); ++w) total += red[w];
+  return total;
+}
+
+template <class Tag>
+__device__ __forceinline__ void store16(Tag, void* base, int64_t elem, const float* f) {
+  u32x4 a, b;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = pack2(Tag{}, f[2 * i], f[2 * i + 1]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b[i] = pack2(Tag{}, f[8 + 2 * i], f[8 + 2 * i + 1]);
+  u32x4* dst = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + elem);
+  __builtin_nontemporal_store(a, dst);
+  __builtin_nontemporal_store(b, dst + 1);
+}
+
+__device__ __forceinline__ void store16(F32, void* base, int64_t elem, const float* f) {
+  u32x4* dst = reinterpret_cast<u32x4*>(static_cast<float*>(base) + elem);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    u32x4 a;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = __float_as_uint(f[4 * i + j]);
+    __builtin_nontemporal_store(a, dst + i);
+  }
+}
+
+// Vector path: head_dim % 16 == 0 with head_dim/16 and block_size powers of two, 16-byte
+// aligned caches and output rows.
+template <class Tag, int kIters>
+__global__ __launch_bounds__(256) void dequant_paged_vec(DequantParams p) {
+  __shared__ int64_t red[256 / kWave];
+  const int64_t i = blockIdx.x / p.grid_blocks;  // sequence
+  const int64_t j = blockIdx.x % p.grid_blocks;  // page of the sequence
+  const int64_t len = p.ctx_len[i];
+  const int64_t first = j * p.block_size;
+  if (first >= len) return;
+  const int64_t blk = p.block_tables[i * p.max_blocks + j];
+  if (blk < 0 || blk >= p.num_blocks) return;
+  const int ntok = (int)min<int64_t>(p.block_size, len - first);
+  const int64_t row0 = seq_begin(p, i, red) + first;
+
+  const int units_per_row = 1 << p.u_shift;               // 16-code units
+  const int units = p.heads << (p.bs_shift + p.u_shift);  // whole block, all heads
+  const int64_t page_base = blk * p.heads * (int64_t)p.block_size * p.head_dim;
+
+  for (int u0 = 0; u0 < units; u0 += 256 * kIters) {
+    u32x4 w[2][kIters];
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      const int u = u0 + it * 256 + threadIdx.x;
+      const int o = (u >> p.u_shift) & (p.block_size - 1);
+      if (u < units && o < ntok) {
+#pragma unroll
+        for (int kv = 0; kv < 2; ++kv)
+          if (kv < p.nkv)
+            w[kv][it] = *reinterpret_cast<const u32x4*>(p.cache[kv] + page_base + (int64_t)u * 16);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      const int u = u0 + it * 256 + threadIdx.x;
+      const int o = (u >> p.u_shift) & (p.block_size - 1);
+      if (u >= units || o >= ntok) continue;
+      const int h = u >> (p.u_shift + p.bs_shift);
+      const int d0 = (u & (units_per_row - 1)) * 16;
+      const int64_t row = row0 + o;
+      if (row < 0 || row >= p.total_rows) continue;
+#pragma unroll
+      for (int kv = 0; kv < 2; ++kv) {
+        if (kv >= p.nkv) continue;
+        float f[16];
+        if (p.mode == 1) {
+          const float s = p.scale[kv][((blk * p.heads + h) << p.bs_shift) + o];
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            f[e] = (float)(int8_t)(w[kv][it][e >> 2] >> (8 * (e & 3))) * s;
+        } else {
+          const u32x4* sp = reinterpret_cast<const u32x4*>(p.scale[kv] + (int64_t)h * p.head_dim + d0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const u32x4 sv = sp[q];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              f[4 * q + e] = (float)(int8_t)(w[kv][it][q] >> (8 * e)) * __uint_as_float(sv[e]);
+          }
+        }
+        store16(Tag{}, p.out[kv], row * p.out_st[kv] + (int64_t)h * p.out_sh[kv] + d0, f);
+      }
+    }
+  }
+}
+
+// Generic path: one wavefront per (token, head) row, scalar loads and stores.
+template <class Tag>
+__global__ __launch_bounds__(256) void dequant_paged_generic(DequantParams p) {
+  __shared__ int64_t red[256 / kWave];
+  const int64_t i = blockIdx.x / p.grid_blocks;
+  const int64_t j = blockIdx.x % p.grid_blocks;
+  const int64_t len = p.ctx_len[i];
+  const int64_t first = j * p.block_size;
+  if (first >= len) return;
+  const int64_t blk = p.block_tables[i * p.max_blocks + j];
+  if (blk < 0 || blk >= p.num_blocks) return;
+  const int ntok = (int)min<int64_t>(p.block_size, len - first);
+  const int64_t row0 = seq_begin(p, i, red) + first;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int nrows = p.heads * ntok;
+  for (int r = threadIdx.x / kWave; r < nrows; r += 256 / kWave) {
+    const int h = r / ntok, o = r % ntok;
+    const int64_t row = row0 + o;
+    if (row < 0 || row >= p.total_rows) continue;
+    const int64_t prow = (blk * p.heads + h) * p.block_size + o;
+    for (int kv = 0; kv < p.nkv; ++kv) {
+      const int8_t* codes = p.cache[kv] + prow * p.head_dim;
+      const int64_t obase = row * p.out_st[kv] + (int64_t)h * p.out_sh[kv];
+      for (int d = lane; d < p.head_dim; d += kWave) {
+        const float s = p.mode == 1 ? p.scale[kv][prow] : p.scale[kv][(int64_t)h * p.head_dim + d];
+        store1(Tag{}, p.out[kv], obase + d, (float)codes[d] * s);
+      }
+    }
+  }
+}
+
+template <class Tag>
+int launch(DequantParams p, hipStream_t stream) {
+  constexpr int kBytes = Tag::kBytes;
+  const int64_t blocks = p.batch * p.grid_blocks;
+  if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
+  const int u_shift = (p.head_dim % 16 == 0) ? ilog2_if_pow2(p.head_dim / 16) : -1;
+  const int bs_shift = ilog2_if_pow2(p.block_size);
+  bool vec = u_shift >= 0 && bs_shift >= 0 &&
+             (int64_t)p.heads * p.block_size * (p.head_dim / 16) < (int64_t(1) << 30);
+  for (int kv = 0; kv < p.nkv && vec; ++kv) {
+    vec = reinterpret_cast<uintptr_t>(p.out[kv]) % 16 == 0 &&
+          reinterpret_cast<uintptr_t>(p.cache[kv]) % 16 == 0 &&
+          (p.out_st[kv] * kBytes) % 16 == 0 && (p.out_sh[kv] * kBytes) % 16 == 0 &&
+          (p.mode == 1 || reinterpret_cast<uintptr_t>(p.scale[kv]) % 16 == 0);
+  }
+  const dim3 grid((unsigned)blocks), block(256);
+  if (!vec) return launch_kernel(dequant_paged_generic<Tag>, grid, block, stream, p);
+  p.u_shift = u_shift;
+  p.bs_shift = bs_shift;
+  return launch_kernel(dequant_paged_vec<Tag, 4>, grid, block, stream, p);
+}
+
+}  // namespace
+}  // namespace tmo
+
+extern "C" int tmo_hip_dequant_from_paged_cache(
+    void* key, void* value, int64_t key_stride_token, int64_t key_stride_head,
+    int64_t value_stride_token, int64_t value_stride_head, int64_t total_rows,
+    const int8_t* key_cache, const int8_t* value_cache, const float* key_scale,
+    const float* value_scale, const int32_t* context_lengths, const int32_t* context_seq_offset,
+    const int32_t* block_tables, int64_t batch, int64_t max_blocks_per_seq,
+    int64_t max_context_len, int64_t num_blocks, int64_t num_heads, int64_t block_size,
+    int64_t head_size, int quant_mode, int quant_bit, int out_dtype, void* stream) {
+  using namespace tmo;
+  if (out_dtype != TMO_DTYPE_F16 && out_dtype != TMO_DTYPE_BF16 && out_dtype != TMO_DTYPE_F32)
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (quant_bit != 8 || (quant_mode != 0 && quant_mode != 1)) return TMO_ERR_UNSUPPORTED_MODE;
+  if (!key || !key_cache || !key_scale || !context_lengths || !block_tables)
+    return TMO_ERR_INVALID_ARGUMENT;
+  const bool has_v = value != nullptr;
+  if (has_v != (value_cache != nullptr) || has_v != (value_scale != nullptr))
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || max_blocks_per_seq < 0 || max_context_len < 0 || num_blocks < 0 ||
+      num_heads <= 0 || block_size <= 0 || head_size <= 0 || total_rows < 0)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (key_stride_token < 0 || key_stride_head < 0 ||
+      (has_v && (value_stride_token < 0 || value_stride_head < 0)))
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (num_heads > 0x7fffffffLL || block_size > 0x7fffffffLL || head_size > 0x7fffffffLL)
+    return TMO_ERR_INVALID_ARGUMENT;
+  int64_t grid_blocks = (max_context_len + block_size - 1) / block_size;
+  if (grid_blocks > max_blocks_per_seq) grid_blocks = max_blocks_per_seq;
+  if (batch == 0 || grid_blocks == 0 || num_blocks == 0 || total_rows == 0) return TMO_OK;
+
+  DequantParams p{};
+  p.out[0] = key;
+  p.out[1] = value;
+  p.out_st[0] = key_stride_token;
+  p.out_st[1] = value_stride_token;
+  p.out_sh[0] = key_stride_head;
+  p.out_sh[1] = value_stride_head;
+  p.total_rows = total_rows;
+  p.cache[0] = key_cache;
+  p.cache[1] = value_cache;
+  p.scale[0] = key_scale;
+  p.scale[1] = value_scale;
+  p.ctx_len = context_lengths;
+  p.seq_off = context_seq_offset;
+  p.block_tables = block_tables;
+  p.batch = batch;
+  p.max_blocks = max_blocks_per_seq;
+  p.grid_blocks = grid_blocks;
+  p.num_blocks = num_blocks;
+  p.heads = (int32_t)num_heads;
+  p.block_size = (int32_t)block_size;
+  p.head_dim = (int32_t)head_size;
+  p.mode = quant_mode;
+  p.nkv = has_v ? 2 : 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (out_dtype) {
+    case TMO_DTYPE_F16: return launch<F16>(p, s);
+    case TMO_DTYPE_BF16: return launch<BF16>(p, s);
+    default: return launch<F32>(p, s);
+  }
+}

@@ -1,0 +1,204 @@
+// quant_to_paged_cache for gfx950: dynamic per-(token, head) int8 quantisation of K/V rows,
+// scattered into [num_blocks, heads, block_size, head_dim] pages through slot_mapping.
+//
+// Semantics: reference _ops.py:1511-1565 (math block :1524-1537, slot convention :1262-1268).
+// Entry point: tmo_hip_quant_to_paged_cache (include/tmo_hip.h).
+//
+// Mapping (vector path): a row of head_dim elements is G = head_dim / (16 B / elem) lanes,
+// one 16-byte load per lane.  A 256-thread workgroup owns 256/G consecutive tokens of ONE
+// head, so with consecutive slots (prefill) its code stores fill whole pages contiguously
+// and its scale stores one contiguous run.  K and V of the same (token, head) are handled by
+// the same lanes, so every lane has two independent 16-byte loads in flight.  The row amax
+// is a DPP reduction inside the lane group; the divide is the reciprocal + two-FMA-step
+// quotient of tmo_device.h (bit-identical to IEEE division); codes and scales are written
+// with non-temporal stores (the cache is written once per step and read by other kernels).
+#include "tmo_device.h"
+
+namespace tmo {
+namespace {
+
+struct QuantPagedParams {
+  const void* src[2];
+  int64_t stride_tok[2];   // elements
+  int64_t stride_head[2];  // elements
+  int8_t* cache[2];
+  float* scale[2];
+  const int32_t* slot;
+  int64_t num_tokens;
+  int64_t num_slots;  // num_blocks * block_size
+  int32_t heads;
+  int32_t head_dim;
+  int32_t block_size;
+  int32_t bs_shift;  // log2(block_size) or -1
+  int32_t nkv;       // 1 (K only) or 2 (K and V)
+};
+
+__device__ __forceinline__ bool locate(const QuantPagedParams& p, int64_t t, int h,
+                                       int64_t& page_row) {
+  const int32_t slot = p.slot[t];
+  if (slot < 0 || (int64_t)slot >= p.num_slots) return false;
+  int32_t blk, off;
+  if (p.bs_shift >= 0) {
+    blk = slot >> p.bs_shift;
+    off = slot & (p.block_size - 1);
+  } else {
+    blk = slot / p.block_size;
+    off = slot - blk * p.block_size;
+  }
+  page_row = ((int64_t)blk * p.heads + h) * p.block_size + off;
+  return true;
+}
+
+// Vector path: head_dim == G * Tag::kPerVec, 16-byte aligned rows.
+template <class Tag, int G>
+__global__ __launch_bounds__(256) void quant_paged_vec(QuantPagedParams p) {
+  constexpr int kRows = 256 / G;  // tokens per workgroup
+  constexpr int kPer = Tag::kPerVec;
+  const int lane = threadIdx.x & (G - 1);
+  // blockIdx.x = token_tile * heads + head (workgroup-uniform, scalar ALU)
+  const int h = blockIdx.x % p.heads;
+  const int64_t tile = blockIdx.x / p.heads;
+  const int64_t t = tile * kRows + threadIdx.x / G;
+  if (t >= p.num_tokens) return;
+  int64_t page_row;
+  if (!locate(p, t, h, page_row)) return;  // whole lane group leaves together
+
+  u32x4 w[2];
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    if (kv < p.nkv) {
+      const char* src = static_cast<const char*>(p.src[kv]) +
+                        (t * p.stride_tok[kv] + (int64_t)h * p.stride_head[kv]) * Tag::kBytes;
+      w[kv] = *reinterpret_cast<const u32x4*>(src + lane * 16);
+    }
+  }
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    if (kv < p.nkv) {
+      float v[kPer];
+      unpack(Tag{}, w[kv], v);
+      float m = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) m = abs_max(m, v[i]);
+      const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<G>(__float_as_uint(m))));
+      int8_t* dst = p.cache[kv] + page_row * p.head_dim + lane * kPer;
+      uint32_t c[kPer / 4];
+      encode_row<kPer>(v, rs, c);
+      if constexpr (kPer == 8) {
+        u32x2 c2;
+        c2[0] = c[0];
+        c2[1] = c[1];
+        __builtin_nontemporal_store(c2, reinterpret_cast<u32x2*>(dst));
+      } else {
+        __builtin_nontemporal_store(c[0], reinterpret_cast<uint32_t*>(dst));
+      }
+      if (lane == 0) __builtin_nontemporal_store(rs.s, p.scale[kv] + page_row);
+    }
+  }
+}
+
+// Generic path (any head_dim / alignment): one wavefront per row, scalar loads, two passes.
+template <class Tag>
+__global__ __launch_bounds__(256) void quant_paged_generic(QuantPagedParams p) {
+  constexpr int kRows = 256 / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int h = blockIdx.x % p.heads;
+  const int64_t tile = blockIdx.x / p.heads;
+  const int64_t t = tile * kRows + threadIdx.x / kWave;
+  if (t >= p.num_tokens) return;
+  int64_t page_row;
+  if (!locate(p, t, h, page_row)) return;
+  for (int kv = 0; kv < p.nkv; ++kv) {
+    const void* src = p.src[kv];
+    const int64_t base = t * p.stride_tok[kv] + (int64_t)h * p.stride_head[kv];
+    float m = 0.0f;
+    for (int d = lane; d < p.head_dim; d += kWave) m = abs_max(m, load1(Tag{}, src, base + d));
+    const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<kWave>(__float_as_uint(m))));
+    int8_t* dst = p.cache[kv] + page_row * p.head_dim;
+    for (int d = lane; d < p.head_dim; d += kWave) dst[d] = encode1(load1(Tag{}, src, base + d), rs);
+    if (lane == 0) p.scale[kv][page_row] = rs.s;
+  }
+}
+
+template <class Tag>
+int launch(const QuantPagedParams& p, hipStream_t stream) {
+  constexpr int kPer = Tag::kPerVec;
+  bool vec = (p.head_dim % kPer) == 0;
+  const int G = vec ? p.head_dim / kPer : 0;
+  vec = vec && G >= 1 && G <= 64 && (G & (G - 1)) == 0;
+  for (int kv = 0; kv < p.nkv && vec; ++kv) {
+    vec = (reinterpret_cast<uintptr_t>(p.src[kv]) % 16 == 0) &&
+          ((p.stride_tok[kv] * Tag::kBytes) % 16 == 0) &&
+          ((p.stride_head[kv] * Tag::kBytes) % 16 == 0) &&
+          (reinterpret_cast<uintptr_t>(p.cache[kv]) % 8 == 0);
+  }
+  const int rows = vec ? 256 / G : 256 / kWave;
+  const int64_t tiles = (p.num_tokens + rows - 1) / rows;
+  const int64_t blocks = tiles * p.heads;
+  if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
+  const dim3 grid((unsigned)blocks), block(256);
+  if (!vec) return launch_kernel(quant_paged_generic<Tag>, grid, block, stream, p);
+  switch (G) {
+    case 1: return launch_kernel(quant_paged_vec<Tag, 1>, grid, block, stream, p);
+    case 2: return launch_kernel(quant_paged_vec<Tag, 2>, grid, block, stream, p);
+    case 4: return launch_kernel(quant_paged_vec<Tag, 4>, grid, block, stream, p);
+    case 8: return launch_kernel(quant_paged_vec<Tag, 8>, grid, block, stream, p);
+    case 16: return launch_kernel(quant_paged_vec<Tag, 16>, grid, block, stream, p);
+    case 32: return launch_kernel(quant_paged_vec<Tag, 32>, grid, block, stream, p);
+    default: return launch_kernel(quant_paged_vec<Tag, 64>, grid, block, stream, p);
+  }
+}
+
+}  // namespace
+}  // namespace tmo
+
+extern "C" int tmo_hip_quant_to_paged_cache(const void* k, const void* v,
+                                            int64_t k_stride_token, int64_t k_stride_head,
+                                            int64_t v_stride_token, int64_t v_stride_head,
+                                            int8_t* k_cache, int8_t* v_cache,
+                                            float* k_cache_scale, float* v_cache_scale,
+                                            const int32_t* slot_mapping, int64_t num_tokens,
+                                            int64_t num_heads, int64_t head_size,
+                                            int64_t num_blocks, int64_t block_size, int dtype,
+                                            void* stream) {
+  using namespace tmo;
+  if (dtype != TMO_DTYPE_F32 && dtype != TMO_DTYPE_F16 && dtype != TMO_DTYPE_BF16)
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (!k || !k_cache || !k_cache_scale || !slot_mapping) return TMO_ERR_INVALID_ARGUMENT;
+  const bool has_v = v != nullptr;
+  if (has_v != (v_cache != nullptr) || has_v != (v_cache_scale != nullptr))
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (num_tokens < 0 || num_heads <= 0 || head_size <= 0 || num_blocks < 0 || block_size <= 0)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (k_stride_token < 0 || k_stride_head < 0 || (has_v && (v_stride_token < 0 || v_stride_head < 0)))
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (num_heads > 0x7fffffffLL || head_size > 0x7fffffffLL || block_size > 0x7fffffffLL)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (num_tokens == 0 || num_blocks == 0) return TMO_OK;
+
+  QuantPagedParams p{};
+  p.src[0] = k;
+  p.src[1] = v;
+  p.stride_tok[0] = k_stride_token;
+  p.stride_tok[1] = v_stride_token;
+  p.stride_head[0] = k_stride_head;
+  p.stride_head[1] = v_stride_head;
+  p.cache[0] = k_cache;
+  p.cache[1] = v_cache;
+  p.scale[0] = k_cache_scale;
+  p.scale[1] = v_cache_scale;
+  p.slot = slot_mapping;
+  p.num_tokens = num_tokens;
+  p.num_slots = num_blocks * block_size;
+  p.heads = (int32_t)num_heads;
+  p.head_dim = (int32_t)head_size;
+  p.block_size = (int32_t)block_size;
+  p.bs_shift = ilog2_if_pow2(block_size);
+  p.nkv = has_v ? 2 : 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TMO_DTYPE_F32: return launch<F32>(p, s);
+    case TMO_DTYPE_F16: return launch<F16>(p, s);
+    default: return launch<BF16>(p, s);
+  }
+}

@@ -1,0 +1,249 @@
+// scaled_quantize, quant_mode "dynamic_per_token", for gfx950: optional row gather, optional
+// (per-group) smooth vector, per-row amax -> fp32 scale -> int8 codes.
+//
+// Semantics: reference _ops.py:3126-3253 (moe_quantize; math block :3147-3176) and
+// _ops.py:4407-4492 (scaled_quantize).  Entry point: tmo_hip_scaled_quantize_per_token
+// (include/tmo_hip.h).
+//
+// One wavefront per output row.  Every lane holds up to kMaxV 16-byte vectors of the row in
+// registers (a 4096-channel bf16 row is 8 vectors per lane, all loads in flight at once), so
+// the row is read from HBM exactly once; the smooth vector (<= 1 MiB even with 64 experts)
+// stays L2-resident and is read as 16-byte vectors alongside.  The row's group (expert) is
+// found with a wavefront prefix scan of token_count and a ballot, with no host round trip.
+#include "tmo_device.h"
+
+namespace tmo {
+namespace {
+
+struct SqParams {
+  const void* x;
+  int64_t n0;
+  int64_t inner;
+  int64_t channels;
+  int64_t row_stride;  // elements
+  int8_t* out;
+  float* out_scale;
+  const float* smooth;
+  int64_t smooth_len;  // 1 or channels (0: no smooth)
+  const int32_t* token_count;
+  int64_t num_groups;
+  const int32_t* gather_index;
+  int64_t gather_len;
+  const int32_t* gather_start;
+  int64_t out_rows;
+  int64_t total_rows;  // out_rows * inner
+};
+
+// Group of row r: the g with prefix(g) <= r < prefix(g + 1) over token_count.  Returns
+// false when r >= sum(token_count) (or gather-start limits apply).  Wave-uniform.
+__device__ __forceinline__ bool find_group(const SqParams& p, int64_t r, int64_t& g) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int64_t carry = 0, below = 0;
+  for (int64_t base = 0; base < p.num_groups; base += kWave) {
+    const int64_t k = base + lane;
+    int64_t c = k < p.num_groups ? (int64_t)p.token_count[k] : 0;
+    // inclusive scan across the wavefront
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int64_t n = __shfl_up(c, o, kWave);
+      if (lane >= o) c += n;
+    }
+    const int64_t incl = carry + c;
+    const uint64_t le = __ballot(k < p.num_groups && incl <= r);
+    below += __popcll(le);
+    carry += __shfl(c, kWave - 1, kWave);
+  }
+  g = below;
+  return r < carry;
+}
+
+template <class Tag>
+__device__ __forceinline__ void load_smooth(const float* sm, int64_t smooth_len, int64_t u,
+                                            float* s) {
+  constexpr int kPer = Tag::kPerVec;
+  if (smooth_len == 1) {
+    const float v = sm[0];
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) s[e] = v;
+  } else {
+    const u32x4* sp = reinterpret_cast<const u32x4*>(sm + u * kPer);
+#pragma unroll
+    for (int q = 0; q < kPer / 4; ++q) {
+      const u32x4 w = sp[q];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[4 * q + e] = __uint_as_float(w[e]);
+    }
+  }
+}
+
+// Vector path: channels % kPerVec == 0, 16-byte aligned rows and smooth, and
+// channels / kPerVec <= 64 * kMaxV.
+template <class Tag, int kMaxV>
+__global__ __launch_bounds__(256) void sq_vec(SqParams p) {
+  constexpr int kPer = Tag::kPerVec;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t orow = (int64_t)blockIdx.x * (256 / kWave) +
+                       __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  if (orow >= p.total_rows) return;
+  const int64_t r = orow / p.inner;
+  const int64_t jn = orow - r * p.inner;
+  int64_t g = 0;
+  if (p.token_count) {
+    if (!find_group(p, r, g)) return;
+  }
+  int64_t src = r;
+  if (p.gather_index) {
+    const int64_t gi = (p.gather_start ? (int64_t)p.gather_start[0] : 0) + r;
+    if (gi < 0 || gi >= p.gather_len) return;
+    src = p.gather_index[gi];
+  }
+  if (src < 0 || src >= p.n0) return;
+
+  const int64_t nvec = p.channels / kPer;
+  const char* xrow = static_cast<const char*>(p.x) + (src * p.inner + jn) * p.row_stride * Tag::kBytes;
+  u32x4 w[kMaxV];
+#pragma unroll
+  for (int i = 0; i < kMaxV; ++i) {
+    const int64_t u = lane + (int64_t)i * kWave;
+    if (u < nvec) w[i] = *reinterpret_cast<const u32x4*>(xrow + u * 16);
+  }
+  const float* sm = p.smooth ? p.smooth + (p.token_count ? g * p.smooth_len : 0) : nullptr;
+  float v[kMaxV][kPer];
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kMaxV; ++i) {
+    const int64_t u = lane + (int64_t)i * kWave;
+    if (u < nvec) {
+      unpack(Tag{}, w[i], v[i]);
+      if (sm) {
+        float s[kPer];
+        load_smooth<Tag>(sm, p.smooth_len, u, s);
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) v[i][e] = v[i][e] * s[e];  // RN(x * smooth), no FMA
+      }
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) m = abs_max(m, v[i][e]);
+    }
+  }
+  const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<kWave>(__float_as_uint(m))));
+  int8_t* orow_ptr = p.out + orow * p.channels;
+#pragma unroll
+  for (int i = 0; i < kMaxV; ++i) {
+    const int64_t u = lane + (int64_t)i * kWave;
+    if (u < nvec) {
+      uint32_t c[kPer / 4];
+      encode_row<kPer>(v[i], rs, c);
+      if constexpr (kPer == 8) {
+        u32x2 c2;
+        c2[0] = c[0];
+        c2[1] = c[1];
+        __builtin_nontemporal_store(c2, reinterpret_cast<u32x2*>(orow_ptr + u * 8));
+      } else {
+        __builtin_nontemporal_store(c[0], reinterpret_cast<uint32_t*>(orow_ptr + u * 4));
+      }
+    }
+  }
+  if (lane == 0) p.out_scale[orow] = rs.s;
+}
+
+// Generic path: any channel count / alignment; one wavefront per row, two passes.
+template <class Tag>
+__global__ __launch_bounds__(256) void sq_generic(SqParams p) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t orow = (int64_t)blockIdx.x * (256 / kWave) +
+                       __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  if (orow >= p.total_rows) return;
+  const int64_t r = orow / p.inner;
+  const int64_t jn = orow - r * p.inner;
+  int64_t g = 0;
+  if (p.token_count) {
+    if (!find_group(p, r, g)) return;
+  }
+  int64_t src = r;
+  if (p.gather_index) {
+    const int64_t gi = (p.gather_start ? (int64_t)p.gather_start[0] : 0) + r;
+    if (gi < 0 || gi >= p.gather_len) return;
+    src = p.gather_index[gi];
+  }
+  if (src < 0 || src >= p.n0) return;
+  const int64_t base = (src * p.inner + jn) * p.row_stride;
+  const float* sm = p.smooth ? p.smooth + (p.token_count ? g * p.smooth_len : 0) : nullptr;
+  float m = 0.0f;
+  for (int64_t d = lane; d < p.channels; d += kWave) {
+    float xv = load1(Tag{}, p.x, base + d);
+    if (sm) xv = xv * sm[p.smooth_len == 1 ? 0 : d];
+    m = abs_max(m, xv);
+  }
+  const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<kWave>(__float_as_uint(m))));
+  int8_t* o = p.out + orow * p.channels;
+  for (int64_t d = lane; d < p.channels; d += kWave) {
+    float xv = load1(Tag{}, p.x, base + d);
+    if (sm) xv = xv * sm[p.smooth_len == 1 ? 0 : d];
+    o[d] = encode1(xv, rs);
+  }
+  if (lane == 0) p.out_scale[orow] = rs.s;
+}
+
+template <class Tag>
+int launch(const SqParams& p, hipStream_t stream) {
+  constexpr int kPer = Tag::kPerVec;
+  const int64_t blocks = (p.total_rows + 3) / 4;
+  if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
+  const dim3 grid((unsigned)blocks), block(256);
+  const bool aligned =
+      p.channels % kPer == 0 && reinterpret_cast<uintptr_t>(p.x) % 16 == 0 &&
+      (p.row_stride * Tag::kBytes) % 16 == 0 && reinterpret_cast<uintptr_t>(p.out) % 8 == 0 &&
+      (!p.smooth || p.smooth_len == 1 || reinterpret_cast<uintptr_t>(p.smooth) % 16 == 0);
+  const int64_t per_lane = (p.channels / kPer + kWave - 1) / kWave;
+  if (!aligned || per_lane > 16) return launch_kernel(sq_generic<Tag>, grid, block, stream, p);
+  if (per_lane <= 1) return launch_kernel(sq_vec<Tag, 1>, grid, block, stream, p);
+  if (per_lane <= 2) return launch_kernel(sq_vec<Tag, 2>, grid, block, stream, p);
+  if (per_lane <= 4) return launch_kernel(sq_vec<Tag, 4>, grid, block, stream, p);
+  if (per_lane <= 8) return launch_kernel(sq_vec<Tag, 8>, grid, block, stream, p);
+  return launch_kernel(sq_vec<Tag, 16>, grid, block, stream, p);
+}
+
+}  // namespace
+}  // namespace tmo
+
+extern "C" int tmo_hip_scaled_quantize_per_token(
+    const void* x, int64_t n0, int64_t inner, int64_t channels, int64_t x_row_stride,
+    int8_t* out, float* out_scale, const float* smooth, int64_t smooth_len,
+    const int32_t* token_count, int64_t num_groups, const int32_t* gather_index,
+    int64_t gather_len, const int32_t* gather_start, int64_t out_rows, int dtype, void* stream) {
+  using namespace tmo;
+  if (dtype != TMO_DTYPE_F32 && dtype != TMO_DTYPE_F16 && dtype != TMO_DTYPE_BF16)
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (!x || !out || !out_scale) return TMO_ERR_INVALID_ARGUMENT;
+  if (n0 < 0 || inner <= 0 || channels <= 0 || x_row_stride < channels || out_rows < 0)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (smooth && smooth_len != 1 && smooth_len != channels) return TMO_ERR_INVALID_ARGUMENT;
+  if (token_count && num_groups <= 0) return TMO_ERR_INVALID_ARGUMENT;
+  if (gather_index && gather_len < 0) return TMO_ERR_INVALID_ARGUMENT;
+  if (gather_start && !gather_index) return TMO_ERR_INVALID_ARGUMENT;
+  if (out_rows == 0 || n0 == 0) return TMO_OK;
+
+  SqParams p{};
+  p.x = x;
+  p.n0 = n0;
+  p.inner = inner;
+  p.channels = channels;
+  p.row_stride = x_row_stride;
+  p.out = out;
+  p.out_scale = out_scale;
+  p.smooth = smooth;
+  p.smooth_len = smooth ? smooth_len : 0;
+  p.token_count = token_count;
+  p.num_groups = token_count ? num_groups : 0;
+  p.gather_index = gather_index;
+  p.gather_len = gather_index ? gather_len : 0;
+  p.gather_start = gather_start;
+  p.out_rows = out_rows;
+  p.total_rows = out_rows * inner;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TMO_DTYPE_F32: return launch<F32>(p, s);
+    case TMO_DTYPE_F16: return launch<F16>(p, s);
+    default: return launch<BF16>(p, s);
+  }
+}

@@ -1,0 +1,241 @@
+// Device-side building blocks shared by the gfx950 kernels of libtmo_hip.so.
+//
+// Everything here is wave64-native: row reductions run inside DPP rows (16 lanes) or
+// across the whole wavefront, loads and stores are 16-byte vectors, and the int8 encoder
+// is written so that the per-element cost stays a handful of VALU ops (the path is
+// HBM-bound, the division must not make it VALU-bound).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tmo_hip.h"
+
+namespace tmo {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------- element types
+
+// Storage tags for the three input/output float formats.  Each maps a 16-byte vector to
+// `kPerVec` fp32 values and back.
+struct F32 {
+  static constexpr int kBytes = 4;
+  static constexpr int kPerVec = 4;
+};
+struct F16 {
+  static constexpr int kBytes = 2;
+  static constexpr int kPerVec = 8;
+};
+struct BF16 {
+  static constexpr int kBytes = 2;
+  static constexpr int kPerVec = 8;
+};
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// Unpack one 16-byte vector into fp32 values (exact for all three formats).
+__device__ __forceinline__ void unpack(F32, const u32x4& w, float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(w[i]);
+}
+__device__ __forceinline__ void unpack(BF16, const u32x4& w, float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void unpack(F16, const u32x4& w, float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+    v[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+  }
+}
+
+// Scalar element load (generic / unaligned paths).
+__device__ __forceinline__ float load1(F32, const void* p, int64_t i) {
+  return static_cast<const float*>(p)[i];
+}
+__device__ __forceinline__ float load1(BF16, const void* p, int64_t i) {
+  return __uint_as_float((uint32_t) static_cast<const uint16_t*>(p)[i] << 16);
+}
+__device__ __forceinline__ float load1(F16, const void* p, int64_t i) {
+  return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+// fp32 -> 16-bit formats, round to nearest even (hardware conversions: v_cvt_pk_bf16_f32
+// on gfx950, v_cvt_f16_f32 for fp16; both honour the default RNE mode).
+//
+// The value is pinned in a VGPR first: without the barrier the backend folds a preceding
+// fp32 multiply into the conversion (v_fma_mixlo_f16), which rounds the exact product once
+// to fp16 instead of rounding it to fp32 and then to fp16 as the reference's
+// `(code.to(float32) * scale).to(dtype)` does -- a 1-ulp difference on double-rounding cases.
+__device__ __forceinline__ float materialize(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ uint16_t to_bits(BF16, float v) {
+  return __builtin_bit_cast(uint16_t, (__bf16)materialize(v));
+}
+__device__ __forceinline__ uint16_t to_bits(F16, float v) {
+  return __builtin_bit_cast(uint16_t, (_Float16)materialize(v));
+}
+template <class Tag>
+__device__ __forceinline__ uint32_t pack2(Tag, float lo, float hi) {
+  return (uint32_t)to_bits(Tag{}, lo) | ((uint32_t)to_bits(Tag{}, hi) << 16);
+}
+__device__ __forceinline__ void store1(F32, void* p, int64_t i, float v) {
+  static_cast<float*>(p)[i] = v;
+}
+template <class Tag>
+__device__ __forceinline__ void store1(Tag, void* p, int64_t i, float v) {
+  static_cast<uint16_t*>(p)[i] = to_bits(Tag{}, v);
+}
+
+// ---------------------------------------------------------------------------- reductions
+
+// DPP controls (GCN/CDNA encoding).
+constexpr int kDppQuadSwap1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <-> 7-i inside each 8-lane half row
+constexpr int kDppRowMirror = 0x140;      // lane i <-> 15-i inside each 16-lane row
+
+// All controls used here permute inside a row, so no lane reads out of bounds and
+// bound_ctrl only lets the compiler fold the move into the consuming max (v_max_u32_dpp).
+template <int Ctrl>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, Ctrl, 0xF, 0xF, true);
+}
+
+// Max over aligned groups of G lanes (G a power of two <= 64).  Every lane of the group
+// receives the result.  Groups of <= 16 lanes never leave their DPP row; 32/64 use
+// cross-row lane shuffles.  The whole group must be active.
+template <int G>
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
+  if constexpr (G >= 2) v = max(v, dpp<kDppQuadSwap1>(v));
+  if constexpr (G >= 4) v = max(v, dpp<kDppQuadSwap2>(v));
+  if constexpr (G >= 8) v = max(v, dpp<kDppRowHalfMirror>(v));
+  if constexpr (G >= 16) v = max(v, dpp<kDppRowMirror>(v));
+  if constexpr (G >= 32) v = max(v, (uint32_t)__shfl_xor((int)v, 16, 64));
+  if constexpr (G >= 64) v = max(v, (uint32_t)__shfl_xor((int)v, 32, 64));
+  return v;
+}
+
+// ---------------------------------------------------------------------------- int8 encoder
+
+// Rows whose scale is below this use a true IEEE divide per element; above it the
+// reciprocal-based quotient below gives the IEEE quotient's int8 code for every x.
+constexpr float kFastDivMinScale = 8.6736174e-19f;  // 2^-60
+
+// x / s given y = RN(1 / s) and kFastDivMinScale <= s < inf.
+// q0 = RN(x*y) is within ~2 ulp of x/s; one FMA correction step makes it faithful; a second
+// (Markstein's theorem: y within 1/2 ulp of 1/s and q faithful => r = x - s*q is exact and
+// RN(q + r*y) = RN(x/s)) makes it the IEEE quotient.  P. Markstein, IBM J. Res. Dev. 34(1),
+// 1990; Muller et al., Handbook of Floating-Point Arithmetic, 2nd ed., ch. 4 (FMA division).
+// The theorem needs the residual not to underflow: for |x| >= 2^-100 the result is the IEEE
+// quotient bit for bit; below that its last bit may differ, but then |x / s| < 2^-40 and the
+// int8 code (0) is the same.  tests/native/div_exhaustive.hip checks both statements on
+// every bf16 and every fp16 (amax, x) pair and on random / near-tie fp32 pairs.
+__host__ __device__ __forceinline__ float div_by_recip(float x, float s, float y) {
+  float q0 = x * y;
+  float r0 = __builtin_fmaf(-s, q0, x);
+  float q1 = __builtin_fmaf(r0, y, q0);
+  float r1 = __builtin_fmaf(-s, q1, x);
+  return __builtin_fmaf(r1, y, q1);
+}
+
+// int8 code of an fp32 quotient: clamp to [-128, 127] (v_med3_f32), then round to nearest
+// even by adding 1.5*2^23 (the sum's ulp is 1, so the hardware RNE add performs the
+// rounding, and the low byte of its bit pattern is the two's-complement code).  Returns the
+// code in bits 0..7 of the result (upper bits are garbage).
+__device__ __forceinline__ uint32_t code_bits(float q) {
+  q = __builtin_amdgcn_fmed3f(q, -128.0f, 127.0f);
+  return __float_as_uint(q + 12582912.0f);
+}
+
+// Per-row quantisation state: the scale and, on the fast path, its reciprocal.
+struct RowScale {
+  float s;     // fp32(amax) / 127
+  float y;     // RN(1 / s) on the fast path; 0 for an all-zero row
+  bool fast;   // kFastDivMinScale <= s < inf, or s == 0
+};
+
+__device__ __forceinline__ RowScale make_row_scale(float amax) {
+  RowScale r;
+  r.s = amax / 127.0f;  // IEEE divide (hipcc default: correctly rounded fp32 division)
+  if (r.s >= kFastDivMinScale && r.s < __builtin_inff()) {
+    r.fast = true;
+    r.y = 1.0f / r.s;
+  } else if (r.s == 0.0f) {
+    // All-zero row: with y = 0 every step of div_by_recip yields +-0, so all codes are 0
+    // and the scale stays 0 (the literal 0/0 of the reference math is not evaluated).
+    r.fast = true;
+    r.y = 0.0f;
+  } else {
+    r.fast = false;
+    r.y = 0.0f;
+  }
+  return r;
+}
+
+// Pack the low bytes of four code_bits() results little-endian into one u32.
+__device__ __forceinline__ uint32_t pack_codes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+  const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);  // [b0.0, b1.0, 0, 0]
+  const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x04000c0cu);  // [0, 0, b2.0, b3.0]
+  return lo | hi;
+}
+
+// Encode N (multiple of 4) fp32 values of one row into N int8 codes, packed 4 per u32.
+// The fast/slow choice is made once per row so the element loop is straight-line code.
+template <int N>
+__device__ __forceinline__ void encode_row(const float* v, const RowScale& r, uint32_t* out) {
+  float q[N];
+  if (r.fast) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = div_by_recip(v[i], r.s, r.y);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = v[i] / r.s;  // IEEE divide (tiny or non-finite scale)
+  }
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i)
+    out[i] = pack_codes(code_bits(q[4 * i]), code_bits(q[4 * i + 1]), code_bits(q[4 * i + 2]),
+                        code_bits(q[4 * i + 3]));
+}
+
+__device__ __forceinline__ int8_t encode1(float v, const RowScale& r) {
+  const float q = r.fast ? div_by_recip(v, r.s, r.y) : v / r.s;
+  return (int8_t)(uint8_t)(code_bits(q) & 0xffu);
+}
+
+// ---------------------------------------------------------------------------- misc
+
+// Launch `kernel(p)` and return TMO_OK or TMO_ERR_LAUNCH from the launch's own status
+// (hipLaunchKernel reports it directly; no sticky-error peeking).
+template <typename Params>
+inline int launch_kernel(void (*kernel)(Params), dim3 grid, dim3 block, hipStream_t stream,
+                         const Params& p, unsigned shared_bytes = 0) {
+  Params copy = p;
+  void* args[] = {&copy};
+  const hipError_t e =
+      hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, args, shared_bytes, stream);
+  return e == hipSuccess ? TMO_OK : TMO_ERR_LAUNCH;
+}
+
+__device__ __forceinline__ float abs_max(float m, float v) { return fmaxf(m, fabsf(v)); }
+
+__host__ __device__ __forceinline__ int ilog2_if_pow2(int64_t v) {
+  if (v <= 0 || (v & (v - 1)) != 0) return -1;
+  int s = 0;
+  while ((int64_t(1) << s) < v) ++s;
+  return s;
+}
+
+}  // namespace tmo

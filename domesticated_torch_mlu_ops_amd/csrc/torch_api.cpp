@@ -1,0 +1,381 @@
+// Thin PyTorch-ROCm glue: tmo::torch_api (include/torch_mlu_ops.h) over the plain C ABI of
+// include/tmo_hip.h, and the torch_mlu_ops::* schemas with their HIP (CUDA-key) kernels.
+//
+// Each function validates everything on the host (shapes, dtypes, devices, contiguity),
+// takes the current HIP stream of the tensors' device, and calls exactly one C-ABI entry
+// point.  Errors surface as c10::Error (Python RuntimeError) before anything is enqueued.
+// The schemas carry the alias/mutation annotations the reference's unshipped extension must
+// have had (its Python wrappers return the written tensors in place: reference
+// _ops.py:1290-1294, 1562-1565, 3821-3824, 3249-3253), so torch.compile functionalisation
+// keeps the cache writes.
+#include <c10/hip/HIPStream.h>
+#include <c10/core/DeviceGuard.h>
+
+#include "tmo_hip.h"
+#include "torch_mlu_ops.h"
+
+namespace tmo {
+namespace torch_api {
+namespace {
+
+int dtype_code(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat: return TMO_DTYPE_F32;
+    case at::kHalf: return TMO_DTYPE_F16;
+    case at::kBFloat16: return TMO_DTYPE_BF16;
+    case at::kChar: return TMO_DTYPE_I8;
+    default: return -1;
+  }
+}
+
+void* stream_of(const at::Tensor& t) {
+  return static_cast<void*>(c10::hip::getCurrentHIPStream(t.get_device()).stream());
+}
+
+void check_status(int status, const char* op) {
+  TORCH_CHECK(status == TMO_OK, "torch_mlu_ops::", op, ": ", tmo_hip_status_string(status),
+              " (status ", status, ")");
+}
+
+void check_device(const at::Tensor& t, const at::Tensor& ref, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a GPU (HIP) tensor, got ", t.device());
+  TORCH_CHECK(t.device() == ref.device(), name, " is on ", t.device(), " but expected ",
+              ref.device());
+}
+
+// [T, H, D] token-major rows with a contiguous last dim (k/v may be views into a fused qkv).
+void check_rows(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.dim() == 3, name, " must be 3-D [tokens, heads, head_size], got ", t.sizes());
+  TORCH_CHECK(t.size(2) <= 1 || t.stride(2) == 1, name, " must have a contiguous last dim");
+  TORCH_CHECK(t.stride(0) >= 0 && t.stride(1) >= 0, name, " has negative strides");
+}
+
+void check_cache(const at::Tensor& c, const char* name) {
+  TORCH_CHECK(c.dim() == 4, name, " must be 4-D [num_blocks, heads, block_size, head_size], got ",
+              c.sizes());
+  TORCH_CHECK(c.is_contiguous(), name, " must be contiguous");
+}
+
+}  // namespace
+
+void reshape_paged_cache(torch::Tensor& k, const c10::optional<torch::Tensor>& v,
+                         torch::Tensor& k_cache, const c10::optional<torch::Tensor>& v_cache,
+                         const torch::Tensor& slot_mapping, bool direction) {
+  check_rows(k, "k");
+  check_cache(k_cache, "k_cache");
+  check_device(k, k, "k");
+  check_device(k_cache, k, "k_cache");
+  check_device(slot_mapping, k, "slot_mapping");
+  TORCH_CHECK(v.has_value() == v_cache.has_value(), "v and v_cache must both be given or both be None");
+  const int dt = dtype_code(k.scalar_type());
+  TORCH_CHECK(dt >= 0, "reshape_paged_cache: unsupported dtype ", k.scalar_type());
+  TORCH_CHECK(k_cache.scalar_type() == k.scalar_type(), "k_cache dtype ", k_cache.scalar_type(),
+              " must match k dtype ", k.scalar_type());
+  const int64_t T = k.size(0), H = k.size(1), D = k.size(2);
+  TORCH_CHECK(k_cache.size(1) == H && k_cache.size(3) == D, "k_cache ", k_cache.sizes(),
+              " does not match k ", k.sizes());
+  TORCH_CHECK(slot_mapping.scalar_type() == at::kInt && slot_mapping.dim() == 1 &&
+                  slot_mapping.size(0) == T && slot_mapping.is_contiguous(),
+              "slot_mapping must be a contiguous int32 [num_tokens] tensor");
+  if (v.has_value()) {
+    check_rows(*v, "v");
+    check_cache(*v_cache, "v_cache");
+    check_device(*v, k, "v");
+    check_device(*v_cache, k, "v_cache");
+    TORCH_CHECK(v->sizes() == k.sizes() && v->scalar_type() == k.scalar_type(), "v must match k");
+    TORCH_CHECK(v_cache->sizes() == k_cache.sizes() && v_cache->scalar_type() == k.scalar_type(),
+                "v_cache must match k_cache");
+  }
+  if (T == 0) return;
+  c10::DeviceGuard guard(k.device());
+  const int st = tmo_hip_reshape_paged_cache(
+      k.data_ptr(), v ? v->data_ptr() : nullptr, k.stride(0), k.stride(1),
+      v ? v->stride(0) : 0, v ? v->stride(1) : 0, k_cache.data_ptr(),
+      v_cache ? v_cache->data_ptr() : nullptr, slot_mapping.data_ptr<int32_t>(), T, H, D,
+      k_cache.size(0), k_cache.size(2), dt, direction ? 1 : 0, stream_of(k));
+  check_status(st, "reshape_paged_cache");
+}
+
+void quant_to_paged_cache(const torch::Tensor& k, const c10::optional<torch::Tensor>& v,
+                          torch::Tensor& k_cache, const c10::optional<torch::Tensor>& v_cache,
+                          torch::Tensor& k_cache_scale,
+                          const c10::optional<torch::Tensor>& v_cache_scale,
+                          const torch::Tensor& slot_mapping) {
+  check_rows(k, "k");
+  check_cache(k_cache, "k_cache");
+  check_device(k, k, "k");
+  check_device(k_cache, k, "k_cache");
+  check_device(k_cache_scale, k, "k_cache_scale");
+  check_device(slot_mapping, k, "slot_mapping");
+  const int dt = dtype_code(k.scalar_type());
+  TORCH_CHECK(dt == TMO_DTYPE_F32 || dt == TMO_DTYPE_F16 || dt == TMO_DTYPE_BF16,
+              "quant_to_paged_cache: k must be float, half or bfloat16, got ", k.scalar_type());
+  TORCH_CHECK(k_cache.scalar_type() == at::kChar,
+              "quant_to_paged_cache: only int8 caches are supported, got ", k_cache.scalar_type());
+  const int64_t T = k.size(0), H = k.size(1), D = k.size(2);
+  const int64_t NB = k_cache.size(0), BS = k_cache.size(2);
+  TORCH_CHECK(k_cache.size(1) == H && k_cache.size(3) == D, "k_cache ", k_cache.sizes(),
+              " does not match k ", k.sizes());
+  TORCH_CHECK(k_cache_scale.scalar_type() == at::kFloat && k_cache_scale.is_contiguous() &&
+                  k_cache_scale.dim() == 3 && k_cache_scale.size(0) == NB &&
+                  k_cache_scale.size(1) == H && k_cache_scale.size(2) == BS,
+              "k_cache_scale must be a contiguous float32 [num_blocks, heads, block_size] tensor");
+  TORCH_CHECK(slot_mapping.scalar_type() == at::kInt && slot_mapping.dim() == 1 &&
+                  slot_mapping.size(0) == T && slot_mapping.is_contiguous(),
+              "slot_mapping must be a contiguous int32 [num_tokens] tensor");
+  const bool has_v = v.has_value();
+  TORCH_CHECK(has_v == v_cache.has_value() && has_v == v_cache_scale.has_value(),
+              "v, v_cache and v_cache_scale must all be given or all be None");
+  if (has_v) {
+    check_rows(*v, "v");
+    check_cache(*v_cache, "v_cache");
+    check_device(*v, k, "v");
+    check_device(*v_cache, k, "v_cache");
+    check_device(*v_cache_scale, k, "v_cache_scale");
+    TORCH_CHECK(v->sizes() == k.sizes() && v->scalar_type() == k.scalar_type(), "v must match k");
+    TORCH_CHECK(v_cache->sizes() == k_cache.sizes() && v_cache->scalar_type() == at::kChar,
+                "v_cache must match k_cache");
+    TORCH_CHECK(v_cache_scale->sizes() == k_cache_scale.sizes() &&
+                    v_cache_scale->scalar_type() == at::kFloat && v_cache_scale->is_contiguous(),
+                "v_cache_scale must match k_cache_scale");
+  }
+  if (T == 0) return;
+  c10::DeviceGuard guard(k.device());
+  const int st = tmo_hip_quant_to_paged_cache(
+      k.data_ptr(), has_v ? v->data_ptr() : nullptr, k.stride(0), k.stride(1),
+      has_v ? v->stride(0) : 0, has_v ? v->stride(1) : 0, k_cache.data_ptr<int8_t>(),
+      has_v ? v_cache->data_ptr<int8_t>() : nullptr, k_cache_scale.data_ptr<float>(),
+      has_v ? v_cache_scale->data_ptr<float>() : nullptr, slot_mapping.data_ptr<int32_t>(), T, H,
+      D, NB, BS, dt, stream_of(k));
+  check_status(st, "quant_to_paged_cache");
+}
+
+void dequant_from_paged_cache(at::Tensor& key, const c10::optional<at::Tensor>& value,
+                              const at::Tensor& key_cache,
+                              const c10::optional<at::Tensor>& value_cache,
+                              const at::Tensor& key_cache_quant_scale,
+                              const c10::optional<at::Tensor>& value_cache_quant_scale,
+                              const at::Tensor& context_lengths, const c10::SymInt max_context_len,
+                              const c10::optional<at::Tensor>& context_seq_offset,
+                              const at::Tensor& block_tables, const int64_t quant_mode,
+                              const int64_t quant_bit) {
+  TORCH_CHECK(quant_mode == 0 || quant_mode == 1,
+              "dequant_from_paged_cache: quant_mode must be 0 (per-channel) or 1 (per-token), got ",
+              quant_mode);
+  TORCH_CHECK(quant_bit == 8, "dequant_from_paged_cache: only quant_bit 8 is supported, got ",
+              quant_bit);
+  check_rows(key, "key");
+  check_cache(key_cache, "key_cache");
+  check_device(key, key, "key");
+  check_device(key_cache, key, "key_cache");
+  check_device(key_cache_quant_scale, key, "key_cache_quant_scale");
+  check_device(context_lengths, key, "context_lengths");
+  check_device(block_tables, key, "block_tables");
+  const int dt = dtype_code(key.scalar_type());
+  TORCH_CHECK(dt == TMO_DTYPE_F16 || dt == TMO_DTYPE_BF16 || dt == TMO_DTYPE_F32,
+              "dequant_from_paged_cache: key must be half, bfloat16 or float, got ",
+              key.scalar_type());
+  TORCH_CHECK(key_cache.scalar_type() == at::kChar, "key_cache must be int8");
+  const int64_t NB = key_cache.size(0), H = key_cache.size(1), BS = key_cache.size(2),
+                D = key_cache.size(3);
+  TORCH_CHECK(key.size(1) == H && key.size(2) == D, "key ", key.sizes(), " does not match key_cache ",
+              key_cache.sizes());
+  auto check_scale = [&](const at::Tensor& s, const char* name) {
+    TORCH_CHECK(s.scalar_type() == at::kFloat && s.is_contiguous(), name,
+                " must be a contiguous float32 tensor");
+    if (quant_mode == 0) {
+      TORCH_CHECK(s.dim() == 2 && s.size(0) == H && s.size(1) == D, name,
+                  " must be [heads, head_size] for quant_mode 0, got ", s.sizes());
+    } else {
+      TORCH_CHECK(s.dim() == 3 && s.size(0) == NB && s.size(1) == H && s.size(2) == BS, name,
+                  " must be [num_blocks, heads, block_size] for quant_mode 1, got ", s.sizes());
+    }
+  };
+  check_scale(key_cache_quant_scale, "key_cache_quant_scale");
+  TORCH_CHECK(context_lengths.scalar_type() == at::kInt && context_lengths.dim() == 1 &&
+                  context_lengths.is_contiguous(),
+              "context_lengths must be a contiguous int32 [batch] tensor");
+  const int64_t B = context_lengths.size(0);
+  TORCH_CHECK(block_tables.scalar_type() == at::kInt && block_tables.dim() == 2 &&
+                  block_tables.size(0) == B && block_tables.is_contiguous(),
+              "block_tables must be a contiguous int32 [batch, max_blocks] tensor");
+  if (context_seq_offset.has_value()) {
+    check_device(*context_seq_offset, key, "context_seq_offset");
+    TORCH_CHECK(context_seq_offset->scalar_type() == at::kInt && context_seq_offset->dim() == 1 &&
+                    context_seq_offset->size(0) == B && context_seq_offset->is_contiguous(),
+                "context_seq_offset must be a contiguous int32 [batch] tensor");
+  }
+  const bool has_v = value.has_value();
+  TORCH_CHECK(has_v == value_cache.has_value() && has_v == value_cache_quant_scale.has_value(),
+              "value, value_cache and value_cache_quant_scale must all be given or all be None");
+  if (has_v) {
+    check_rows(*value, "value");
+    check_cache(*value_cache, "value_cache");
+    check_device(*value, key, "value");
+    check_device(*value_cache, key, "value_cache");
+    check_device(*value_cache_quant_scale, key, "value_cache_quant_scale");
+    TORCH_CHECK(value->sizes() == key.sizes() && value->scalar_type() == key.scalar_type(),
+                "value must match key");
+    TORCH_CHECK(value_cache->sizes() == key_cache.sizes() && value_cache->scalar_type() == at::kChar,
+                "value_cache must match key_cache");
+    check_scale(*value_cache_quant_scale, "value_cache_quant_scale");
+  }
+  const int64_t max_ctx = max_context_len.expect_int();
+  TORCH_CHECK(max_ctx >= 0, "max_context_len must be >= 0");
+  if (B == 0 || key.size(0) == 0) return;
+  c10::DeviceGuard guard(key.device());
+  const int st = tmo_hip_dequant_from_paged_cache(
+      key.data_ptr(), has_v ? value->data_ptr() : nullptr, key.stride(0), key.stride(1),
+      has_v ? value->stride(0) : 0, has_v ? value->stride(1) : 0, key.size(0),
+      key_cache.data_ptr<int8_t>(), has_v ? value_cache->data_ptr<int8_t>() : nullptr,
+      key_cache_quant_scale.data_ptr<float>(),
+      has_v ? value_cache_quant_scale->data_ptr<float>() : nullptr,
+      context_lengths.data_ptr<int32_t>(),
+      context_seq_offset ? context_seq_offset->data_ptr<int32_t>() : nullptr,
+      block_tables.data_ptr<int32_t>(), B, block_tables.size(1), max_ctx, NB, H, BS, D,
+      (int)quant_mode, (int)quant_bit, dt, stream_of(key));
+  check_status(st, "dequant_from_paged_cache");
+}
+
+void scaled_quantize(const at::Tensor& x, const at::Tensor& output,
+                     const c10::optional<at::Tensor>& output_scale,
+                     const c10::optional<at::Tensor>& x_scale,
+                     const c10::optional<at::Tensor>& x_zero,
+                     const c10::optional<at::Tensor>& m_list,
+                     const c10::optional<at::Tensor>& gather_index,
+                     const c10::optional<at::Tensor>& gather_index_start_position,
+                     const c10::optional<at::Tensor>& scale_upper_bound,
+                     const std::string& quant_mode, const std::string& act_mode,
+                     double active_coef, bool is_gated, int64_t quant_bit_size,
+                     bool need_output_scale_trans,
+                     const c10::optional<at::Tensor>& output_reduced, int64_t group_size) {
+  (void)active_coef;
+  (void)group_size;
+  (void)scale_upper_bound;  // only meaningful for fp8 outputs (reference _ops.py:4426-4427)
+  TORCH_CHECK(quant_mode == "dynamic_per_token",
+              "scaled_quantize: only quant_mode 'dynamic_per_token' is implemented, got '",
+              quant_mode, "'");
+  TORCH_CHECK(act_mode == "none", "scaled_quantize: only act_mode 'none' is implemented, got '",
+              act_mode, "'");
+  TORCH_CHECK(!is_gated, "scaled_quantize: is_gated requires an activation (not implemented)");
+  TORCH_CHECK(quant_bit_size == 8, "scaled_quantize: only quant_bit_size 8 is implemented");
+  TORCH_CHECK(!need_output_scale_trans, "scaled_quantize: need_output_scale_trans (mx) is not implemented");
+  TORCH_CHECK(!output_reduced.has_value(), "scaled_quantize: output_reduced is not implemented");
+  TORCH_CHECK(!x_zero.has_value(), "scaled_quantize: zero is not supported, must pass None");
+  TORCH_CHECK(output_scale.has_value(), "scaled_quantize: dynamic_per_token needs output_scale");
+  check_device(x, x, "x");
+  check_device(output, x, "output");
+  check_device(*output_scale, x, "output_scale");
+  const int dt = dtype_code(x.scalar_type());
+  TORCH_CHECK(dt == TMO_DTYPE_F32 || dt == TMO_DTYPE_F16 || dt == TMO_DTYPE_BF16,
+              "scaled_quantize: x must be float, half or bfloat16, got ", x.scalar_type());
+  TORCH_CHECK(output.scalar_type() == at::kChar, "scaled_quantize: only int8 output is implemented, got ",
+              output.scalar_type());
+  TORCH_CHECK(output_scale->scalar_type() == at::kFloat && output_scale->is_contiguous(),
+              "output_scale must be a contiguous float32 tensor");
+  TORCH_CHECK(output.is_contiguous(), "output must be contiguous");
+  TORCH_CHECK(x.dim() >= 1, "x must have at least one dim");
+  const int64_t C = x.size(-1);
+  TORCH_CHECK(x.dim() == 1 || x.size(-1) <= 1 || x.stride(-1) == 1, "x must have a contiguous last dim");
+  // Rows: x is [n0, inner..., C]; dims 0..-2 must collapse into one row index with a uniform
+  // row stride ("continuous between 0 and -2 dimensions", reference _ops.py:3179).
+  const int64_t n0 = x.dim() >= 2 ? x.size(0) : 1;
+  int64_t inner = 1;
+  for (int64_t d = 1; d + 1 < x.dim(); ++d) inner *= x.size(d);
+  int64_t row_stride = -1, span = 1;
+  for (int64_t d = x.dim() - 2; d >= 0; --d) {
+    if (x.size(d) != 1) {
+      if (row_stride < 0) row_stride = x.stride(d);
+      TORCH_CHECK(x.stride(d) == row_stride * span, "x must be contiguous between dims 0 and -2");
+    }
+    span *= x.size(d);
+  }
+  if (row_stride < 0) row_stride = C;  // a single row
+  TORCH_CHECK(row_stride >= C, "x rows overlap (row stride ", row_stride, " < ", C, ")");
+  const float* smooth = nullptr;
+  int64_t smooth_len = 0;
+  if (x_scale.has_value()) {
+    check_device(*x_scale, x, "smooth");
+    TORCH_CHECK(x_scale->scalar_type() == at::kFloat && x_scale->is_contiguous(),
+                "smooth must be a contiguous float32 tensor");
+    smooth = x_scale->data_ptr<float>();
+    if (m_list.has_value()) {
+      TORCH_CHECK(x_scale->dim() == 2 && x_scale->size(0) == m_list->size(0) && x_scale->size(1) == C,
+                  "smooth must be [groups, C] when token_count is given, got ", x_scale->sizes());
+      smooth_len = C;
+    } else {
+      TORCH_CHECK(x_scale->numel() == C || x_scale->numel() == 1,
+                  "smooth must have C or 1 elements, got ", x_scale->sizes());
+      smooth_len = x_scale->numel();
+    }
+  }
+  int64_t groups = 0;
+  if (m_list.has_value()) {
+    check_device(*m_list, x, "token_count");
+    TORCH_CHECK(m_list->scalar_type() == at::kInt && m_list->dim() == 1 && m_list->is_contiguous() &&
+                    m_list->size(0) > 0,
+                "token_count must be a non-empty contiguous int32 [groups] tensor");
+    groups = m_list->size(0);
+  }
+  int64_t rows = n0;
+  int64_t gather_len = 0;
+  if (gather_index.has_value()) {
+    check_device(*gather_index, x, "gather_index");
+    TORCH_CHECK(gather_index->scalar_type() == at::kInt && gather_index->dim() == 1 &&
+                    gather_index->is_contiguous(),
+                "gather_index must be a contiguous int32 [rows] tensor");
+    gather_len = gather_index->size(0);
+    rows = gather_len;
+  }
+  if (gather_index_start_position.has_value()) {
+    TORCH_CHECK(gather_index.has_value(), "gather_index_start_position needs gather_index");
+    check_device(*gather_index_start_position, x, "gather_index_start_position");
+    TORCH_CHECK(gather_index_start_position->scalar_type() == at::kInt &&
+                    gather_index_start_position->numel() == 1,
+                "gather_index_start_position must be an int32 [1] tensor");
+  }
+  TORCH_CHECK(output.numel() == rows * inner * C, "output has ", output.numel(),
+              " elements, expected ", rows * inner * C);
+  TORCH_CHECK(output_scale->numel() == rows * inner, "output_scale has ", output_scale->numel(),
+              " elements, expected ", rows * inner);
+  if (rows == 0 || n0 == 0 || C == 0) return;
+  c10::DeviceGuard guard(x.device());
+  const int st = tmo_hip_scaled_quantize_per_token(
+      x.data_ptr(), n0, inner, C, row_stride, output.data_ptr<int8_t>(),
+      output_scale->data_ptr<float>(), smooth, smooth_len,
+      m_list ? m_list->data_ptr<int32_t>() : nullptr, groups,
+      gather_index ? gather_index->data_ptr<int32_t>() : nullptr, gather_len,
+      gather_index_start_position ? gather_index_start_position->data_ptr<int32_t>() : nullptr, rows,
+      dt, stream_of(x));
+  check_status(st, "scaled_quantize");
+}
+
+}  // namespace torch_api
+}  // namespace tmo
+
+TORCH_LIBRARY(torch_mlu_ops, m) {
+  m.def(
+      "reshape_paged_cache(Tensor(a!) k, Tensor(b!)? v, Tensor(c!) k_cache, Tensor(d!)? v_cache, "
+      "Tensor slot_mapping, bool direction) -> ()");
+  m.def(
+      "quant_to_paged_cache(Tensor k, Tensor? v, Tensor(a!) k_cache, Tensor(b!)? v_cache, "
+      "Tensor(c!) k_cache_scale, Tensor(d!)? v_cache_scale, Tensor slot_mapping) -> ()");
+  m.def(
+      "dequant_from_paged_cache(Tensor(a!) key, Tensor(b!)? value, Tensor key_cache, "
+      "Tensor? value_cache, Tensor key_cache_quant_scale, Tensor? value_cache_quant_scale, "
+      "Tensor context_lengths, SymInt max_context_len, Tensor? context_seq_offset, "
+      "Tensor block_tables, int quant_mode, int quant_bit) -> ()");
+  m.def(
+      "scaled_quantize(Tensor x, Tensor(a!) output, Tensor(b!)? output_scale, Tensor? x_scale, "
+      "Tensor? x_zero, Tensor? m_list, Tensor? gather_index, Tensor? gather_index_start_position, "
+      "Tensor? scale_upper_bound, str quant_mode, str act_mode, float active_coef, bool is_gated, "
+      "int quant_bit_size=8, bool need_output_scale_trans=False, Tensor(c!)? output_reduced=None, "
+      "int group_size=1) -> ()");
+}
+
+TORCH_LIBRARY_IMPL(torch_mlu_ops, CUDA, m) {
+  m.impl("reshape_paged_cache", &tmo::torch_api::reshape_paged_cache);
+  m.impl("quant_to_paged_cache", &tmo::torch_api::quant_to_paged_cache);
+  m.impl("dequant_from_paged_cache", &tmo::torch_api::dequant_from_paged_cache);
+  m.impl("scaled_quantize", &tmo::torch_api::scaled_quantize);
+}

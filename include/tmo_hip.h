@@ -1,0 +1,155 @@
+/*
+ * tmo_hip.h -- plain C ABI of the MI355X (gfx950) quantized paged-KV-cache library
+ * (libtmo_hip.so).
+ *
+ * These entry points replace the device side of torch_mlu_ops' hot path: the closed
+ * MLU kernels that the unshipped native extension `_TMOC` dispatches to behind the
+ * C++ prototypes of reference include/torch_mlu_ops.h.  Each function cites the
+ * prototype and the Python wrapper it stands behind.
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers (HBM).  Tensors laid out [T, H, D] are addressed with
+ *     element strides for the token and head dims; the last dim is contiguous.
+ *     Paged caches are contiguous [num_blocks, num_heads, block_size, head_size]
+ *     (reference KVFormat.NB_HN_BS_HS, _ops.py:1301-1310); per-token scales are
+ *     contiguous [num_blocks, num_heads, block_size] fp32.
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Work is enqueued on it;
+ *     nothing synchronises, nothing allocates, no global mutable state: calls are
+ *     reentrant and thread-safe across streams.
+ *   - The return value is TMO_OK (0) or a negative tmo_status.  Arguments are validated
+ *     before anything is enqueued; a failed call writes no device memory.
+ *   - slot < 0 in slot_mapping means "skip this token" (_ops.py:1264); a slot at or past
+ *     num_blocks*block_size is skipped the same way rather than written out of bounds.
+ */
+#ifndef TMO_HIP_H_
+#define TMO_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TMO_HIP_ABI_VERSION 1
+
+/* element types */
+enum tmo_dtype {
+    TMO_DTYPE_F32 = 0,
+    TMO_DTYPE_F16 = 1,
+    TMO_DTYPE_BF16 = 2,
+    TMO_DTYPE_I8 = 3
+};
+
+/* return codes */
+enum tmo_status {
+    TMO_OK = 0,
+    TMO_ERR_INVALID_ARGUMENT = -1, /* null pointer, negative/zero size, bad stride */
+    TMO_ERR_UNSUPPORTED_DTYPE = -2,
+    TMO_ERR_UNSUPPORTED_MODE = -3, /* quant_mode / quant_bit outside the int8 path */
+    TMO_ERR_LAUNCH = -4            /* the HIP launch itself failed */
+};
+
+/* ABI version of the loaded library (TMO_HIP_ABI_VERSION at build time). */
+int tmo_hip_abi_version(void);
+
+/* Static, human-readable text for a tmo_status value. */
+const char* tmo_hip_status_string(int status);
+
+/*
+ * reshape_paged_cache -- byte-exact scatter (direction == 0) of k/v[T, H, D] rows into the
+ * paged caches at slot_mapping, or gather (direction != 0) of the same rows back.
+ * Replaces tmo::torch_api::reshape_paged_cache (reference include/torch_mlu_ops.h:143-148),
+ * called by torch_mlu_ops.reshape_paged_cache (reference _ops.py:1251-1294).
+ * dtype: any tmo_dtype (caches have the dtype of k/v).  v and v_cache are both NULL or
+ * both non-NULL.
+ */
+int tmo_hip_reshape_paged_cache(void* k, void* v,
+                                int64_t k_stride_token, int64_t k_stride_head,
+                                int64_t v_stride_token, int64_t v_stride_head,
+                                void* k_cache, void* v_cache,
+                                const int32_t* slot_mapping,
+                                int64_t num_tokens, int64_t num_heads, int64_t head_size,
+                                int64_t num_blocks, int64_t block_size,
+                                int dtype, int direction, void* stream);
+
+/*
+ * quant_to_paged_cache -- dynamic per-(token, head) int8 quantisation of k/v[T, H, D] into
+ * the paged caches: scale = fp32(max|row|) / 127 (IEEE), code = RNE(row / scale) clamped
+ * to [-128, 127] (all-zero row: scale 0, codes 0); codes go to
+ * cache[slot / block_size, h, slot % block_size, :] and the scale to the same [.., h, ..]
+ * position of the scale pages.
+ * Replaces tmo::torch_api::quant_to_paged_cache (reference include/torch_mlu_ops.h:176-182),
+ * called by torch_mlu_ops.quant_to_paged_cache (reference _ops.py:1511-1565).
+ * dtype: F32, F16 or BF16 (of k and v).  v, v_cache, v_cache_scale: all NULL or all set.
+ */
+int tmo_hip_quant_to_paged_cache(const void* k, const void* v,
+                                 int64_t k_stride_token, int64_t k_stride_head,
+                                 int64_t v_stride_token, int64_t v_stride_head,
+                                 int8_t* k_cache, int8_t* v_cache,
+                                 float* k_cache_scale, float* v_cache_scale,
+                                 const int32_t* slot_mapping,
+                                 int64_t num_tokens, int64_t num_heads, int64_t head_size,
+                                 int64_t num_blocks, int64_t block_size,
+                                 int dtype, void* stream);
+
+/*
+ * dequant_from_paged_cache -- gathers each sequence's pages through block_tables and writes
+ * out[begin_i + t, h, :] = RNE_out(fp32(code) * scale) for t < context_lengths[i], where
+ * begin_i = context_seq_offset[i], or the exclusive prefix sum of context_lengths when
+ * context_seq_offset is NULL.  quant_mode 0: scale [H, D] (per channel);
+ * quant_mode 1: scale [num_blocks, H, block_size] (per token).  quant_bit must be 8.
+ * Tokens at or past min(max_context_len, max_blocks_per_seq * block_size) are not written;
+ * block-table entries outside [0, num_blocks) and output rows outside [0, total_rows) are
+ * skipped.
+ * Replaces tmo::torch_api::dequant_from_paged_cache (reference include/torch_mlu_ops.h:650-661),
+ * called by torch_mlu_ops.dequant_from_paged_cache (reference _ops.py:3734-3824).
+ * out_dtype: F16, BF16 (or F32).  value, value_cache, value_scale: all NULL or all set.
+ */
+int tmo_hip_dequant_from_paged_cache(void* key, void* value,
+                                     int64_t key_stride_token, int64_t key_stride_head,
+                                     int64_t value_stride_token, int64_t value_stride_head,
+                                     int64_t total_rows,
+                                     const int8_t* key_cache, const int8_t* value_cache,
+                                     const float* key_scale, const float* value_scale,
+                                     const int32_t* context_lengths,
+                                     const int32_t* context_seq_offset,
+                                     const int32_t* block_tables,
+                                     int64_t batch, int64_t max_blocks_per_seq,
+                                     int64_t max_context_len,
+                                     int64_t num_blocks, int64_t num_heads,
+                                     int64_t block_size, int64_t head_size,
+                                     int quant_mode, int quant_bit, int out_dtype,
+                                     void* stream);
+
+/*
+ * scaled_quantize_per_token -- "dynamic_per_token" int8 quantisation with an optional smooth
+ * vector, optional row gather and optional per-group (per-expert) smooth rows:
+ *   src row r   = gather_index[start + r] (start = *gather_start or 0), or r without gather;
+ *   smoothed    = RN(fp32(x[src, j, :]) * smooth_g)   (smooth_g = smooth row of r's group);
+ *   scale[r, j] = fp32(max|smoothed|) / 127;  out[r, j, :] = RNE(smoothed / scale) clamped.
+ * x is [n0, inner, C] (rows of C elements, `x_row_stride` elements apart, row (s, j) at
+ * (s * inner + j) * x_row_stride).  smooth: NULL, length 1 (broadcast), length C, or
+ * [num_groups, C] when token_count is given.  token_count [num_groups]: row r belongs to the
+ * group g with prefix(g) <= r < prefix(g + 1); rows at or past sum(token_count) are not
+ * written (with gather_start given, only sum(token_count) rows are produced).
+ * out [out_rows, inner, C] int8 contiguous, out_scale [out_rows, inner] fp32.
+ * Replaces tmo::torch_api::scaled_quantize (reference include/torch_mlu_ops.h:334-350) in
+ * quant_mode "dynamic_per_token", act_mode "none", int8 output, called by
+ * torch_mlu_ops.moe_quantize (reference _ops.py:3126-3253) and torch_mlu_ops.scaled_quantize
+ * (reference _ops.py:4407-4492).
+ * dtype: F32, F16 or BF16 (of x).
+ */
+int tmo_hip_scaled_quantize_per_token(const void* x, int64_t n0, int64_t inner,
+                                      int64_t channels, int64_t x_row_stride,
+                                      int8_t* out, float* out_scale,
+                                      const float* smooth, int64_t smooth_len,
+                                      const int32_t* token_count, int64_t num_groups,
+                                      const int32_t* gather_index, int64_t gather_len,
+                                      const int32_t* gather_start,
+                                      int64_t out_rows, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TMO_HIP_H_ */

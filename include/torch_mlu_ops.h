@@ -1,0 +1,77 @@
+/*
+ * torch_mlu_ops.h -- C++ torch API of the quantized paged-KV-cache path, MI355X build.
+ *
+ * Same namespace, names and parameter lists as the reference's prototypes
+ * (reference include/torch_mlu_ops.h:21-22 namespace tmo::torch_api), restricted to the
+ * four ops of this path.  The implementations (domesticated_torch_mlu_ops_amd/csrc/
+ * torch_api.cpp) validate shapes/dtypes, take the current HIP stream of the tensors' device
+ * and call the plain C ABI of tmo_hip.h; they are registered as the CUDA-key (HIP on ROCm)
+ * kernels of the torch_mlu_ops::* ops.  All tensors are caller-owned and written in place;
+ * nothing here allocates.
+ */
+#ifndef CSRC_TORCH_API_TORCH_MLU_OPS_H_
+#define CSRC_TORCH_API_TORCH_MLU_OPS_H_
+
+#include <cstdint>
+#include <optional>
+#include <string>
+
+#include "torch/extension.h"
+
+namespace tmo {
+namespace torch_api {
+
+/* reference include/torch_mlu_ops.h:143-148 */
+void reshape_paged_cache(torch::Tensor &k,
+                         const c10::optional<torch::Tensor> &v,
+                         torch::Tensor &k_cache,
+                         const c10::optional<torch::Tensor> &v_cache,
+                         const torch::Tensor &slot_mapping,
+                         bool direction);
+
+/* reference include/torch_mlu_ops.h:176-182 */
+void quant_to_paged_cache(const torch::Tensor &k,
+                          const c10::optional<torch::Tensor> &v,
+                          torch::Tensor &k_cache,
+                          const c10::optional<torch::Tensor> &v_cache,
+                          torch::Tensor &k_cache_scale,
+                          const c10::optional<torch::Tensor> &v_cache_scale,
+                          const torch::Tensor &slot_mapping);
+
+/* reference include/torch_mlu_ops.h:334-350 (int8 "dynamic_per_token", act_mode "none") */
+void scaled_quantize(const at::Tensor &x,
+                     const at::Tensor &output,
+                     const c10::optional<at::Tensor> &output_scale,
+                     const c10::optional<at::Tensor> &x_scale,
+                     const c10::optional<at::Tensor> &x_zero,
+                     const c10::optional<at::Tensor> &m_list,
+                     const c10::optional<at::Tensor> &gather_index,
+                     const c10::optional<at::Tensor> &gather_index_start_position,
+                     const c10::optional<at::Tensor> &scale_upper_bound,
+                     const std::string &quant_mode,
+                     const std::string &act_mode,
+                     double active_coef,
+                     bool is_gated,
+                     int64_t quant_bit_size = 8,
+                     bool need_output_scale_trans = false,
+                     const c10::optional<at::Tensor> &output_reduced = c10::nullopt,
+                     int64_t group_size = 1);
+
+/* reference include/torch_mlu_ops.h:650-661 (quant_mode 0 and 1, quant_bit 8) */
+void dequant_from_paged_cache(at::Tensor &key,
+                              const c10::optional<at::Tensor> &value,
+                              const at::Tensor &key_cache,
+                              const c10::optional<at::Tensor> &value_cache,
+                              const at::Tensor &key_cache_quant_scale,
+                              const c10::optional<at::Tensor> &value_cache_quant_scale,
+                              const at::Tensor &context_lengths,
+                              const c10::SymInt max_context_len,
+                              const c10::optional<at::Tensor> &context_seq_offset,
+                              const at::Tensor &block_tables,
+                              const int64_t quant_mode,
+                              const int64_t quant_bit);
+
+}  // namespace torch_api
+}  // namespace tmo
+
+#endif  // CSRC_TORCH_API_TORCH_MLU_OPS_H_

@@ -1,0 +1,176 @@
+"""CPU oracle of the quantized paged-KV-cache path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import this package, and only as the checker / CPU baseline; the product package
+(``domesticated_torch_mlu_ops_amd``) never touches it.
+
+The arithmetic lives in ``tmo_oracle.c`` (a restatement of the reference's docstring math,
+cited per function there, built by ``Makefile`` into ``_build/libtmo_oracle.so``).  This module
+wraps it for CPU torch tensors with the argument conventions of the reference ops: outputs
+are written in place.  ``nthreads`` defaults to the CPUs this process may run on.
+
+Parity pins: tests/test_oracle_pins.py.  The reference itself cannot be imported or built
+here (it needs torch_mlu and the unshipped _TMOC extension), so ``oracle/_ref`` does not exist.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "_build" / "libtmo_oracle.so"
+
+_DT = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.int8: 3}
+_lib: Optional[ctypes.CDLL] = None
+
+c_void_p, c_int64, c_int, c_float = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.oracle_quant_to_paged_cache.argtypes = [c_void_p, c_void_p, c_int] + [c_int64] * 4 + \
+            [c_void_p] * 5 + [c_int64] * 5 + [c_int]
+        L.oracle_reshape_paged_cache.argtypes = [c_void_p, c_void_p, c_int] + [c_int64] * 4 + \
+            [c_void_p] * 3 + [c_int64] * 5 + [c_int, c_int]
+        L.oracle_dequant_from_paged_cache.argtypes = [c_void_p, c_void_p, c_int] + [c_int64] * 5 + \
+            [c_void_p] * 7 + [c_int64] * 6 + [c_int, c_int]
+        L.oracle_scaled_quantize_per_token.argtypes = [c_void_p, c_int] + [c_int64] * 4 + \
+            [c_void_p] * 3 + [c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                              c_int]
+        for name in ("oracle_f32_to_bf16", "oracle_f32_to_f16", "oracle_f16_to_f32"):
+            getattr(L, name).argtypes = [c_void_p, c_void_p, c_int64]
+        for name in ("oracle_quant_to_paged_cache", "oracle_reshape_paged_cache",
+                     "oracle_dequant_from_paged_cache", "oracle_scaled_quantize_per_token"):
+            getattr(L, name).restype = c_int
+        _lib = L
+    return _lib
+
+
+def default_threads() -> int:
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except AttributeError:  # pragma: no cover
+        return max(1, os.cpu_count() or 1)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    if t is None:
+        return None
+    assert t.device.type == "cpu", "oracle works on CPU tensors"
+    return t.data_ptr()
+
+
+def _check(rc: int, name: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"oracle {name} rejected its arguments (rc={rc})")
+
+
+def quant_to_paged_cache(k, v, k_cache, v_cache, k_scale, v_scale, slot_mapping,
+                         nthreads: Optional[int] = None) -> None:
+    """reference _ops.py:1511-1565 (see tmo_oracle.c); in place on CPU tensors."""
+    assert k.stride(2) == 1 and k_cache.is_contiguous() and k_scale.is_contiguous()
+    T, H, D = k.shape
+    NB, _, BS, _ = k_cache.shape
+    slots = slot_mapping.to(torch.int32).contiguous()  # kept alive across the call
+    rc = lib().oracle_quant_to_paged_cache(
+        _ptr(k), _ptr(v), _DT[k.dtype], k.stride(0), k.stride(1),
+        v.stride(0) if v is not None else 0, v.stride(1) if v is not None else 0,
+        _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+        _ptr(slots), T, H, D, NB, BS, nthreads or default_threads())
+    _check(rc, "quant_to_paged_cache")
+
+
+def reshape_paged_cache(k, v, k_cache, v_cache, slot_mapping, direction: bool = False,
+                        nthreads: Optional[int] = None) -> None:
+    """reference _ops.py:1251-1294; byte copy in place on CPU tensors."""
+    assert k.stride(2) == 1 and k_cache.is_contiguous()
+    T, H, D = k.shape
+    NB, _, BS, _ = k_cache.shape
+    slots = slot_mapping.to(torch.int32).contiguous()  # kept alive across the call
+    rc = lib().oracle_reshape_paged_cache(
+        _ptr(k), _ptr(v), _DT[k.dtype], k.stride(0), k.stride(1),
+        v.stride(0) if v is not None else 0, v.stride(1) if v is not None else 0,
+        _ptr(k_cache), _ptr(v_cache), _ptr(slots),
+        T, H, D, NB, BS, int(bool(direction)), nthreads or default_threads())
+    _check(rc, "reshape_paged_cache")
+
+
+def dequant_from_paged_cache(key, value, key_cache, value_cache, key_scale, value_scale,
+                             context_lengths, context_seq_offset, block_tables,
+                             quant_mode: int, nthreads: Optional[int] = None) -> None:
+    """reference _ops.py:3734-3824 (quant_mode 0/1, 8-bit); in place on CPU tensors."""
+    assert key.stride(2) == 1 and key_cache.is_contiguous() and block_tables.is_contiguous()
+    NB, H, BS, D = key_cache.shape
+    B, MB = block_tables.shape
+    # converted copies are kept alive across the call
+    cso = context_seq_offset.to(torch.int32).contiguous() if context_seq_offset is not None else None
+    ctx = context_lengths.to(torch.int32).contiguous()
+    bt = block_tables.to(torch.int32).contiguous()
+    rc = lib().oracle_dequant_from_paged_cache(
+        _ptr(key), _ptr(value), _DT[key.dtype], key.stride(0), key.stride(1),
+        value.stride(0) if value is not None else 0, value.stride(1) if value is not None else 0,
+        key.shape[0], _ptr(key_cache), _ptr(value_cache), _ptr(key_scale), _ptr(value_scale),
+        _ptr(ctx), _ptr(cso), _ptr(bt), B, MB, NB, H, BS, D, int(quant_mode),
+        nthreads or default_threads())
+    _check(rc, "dequant_from_paged_cache")
+
+
+def scaled_quantize_per_token(x, out, out_scale, smooth=None, token_count=None,
+                              gather_index=None, gather_start=None,
+                              nthreads: Optional[int] = None) -> None:
+    """reference _ops.py:3126-3253 / 4407-4492, mode dynamic_per_token; in place.
+
+    ``x`` is [n0, ..., C] with a contiguous row layout; ``out`` [rows, ..., C] int8 and
+    ``out_scale`` [rows, ...] fp32, rows = gather_index.numel() or n0."""
+    x = x.contiguous()
+    C = x.shape[-1]
+    n0 = x.shape[0] if x.dim() >= 2 else 1
+    inner = 1
+    for s in x.shape[1:-1]:
+        inner *= s
+    rows = gather_index.numel() if gather_index is not None else n0
+    sm = smooth.to(torch.float32).contiguous() if smooth is not None else None
+    smooth_len = 0 if sm is None else (C if (token_count is not None or sm.numel() != 1) else 1)
+    tc = token_count.to(torch.int32).contiguous() if token_count is not None else None
+    gi = gather_index.to(torch.int32).contiguous() if gather_index is not None else None
+    gs = gather_start.to(torch.int32).contiguous() if gather_start is not None else None
+    rc = lib().oracle_scaled_quantize_per_token(
+        _ptr(x), _DT[x.dtype], n0, inner, C, C, _ptr(out), _ptr(out_scale), _ptr(sm),
+        smooth_len, _ptr(tc), tc.numel() if tc is not None else 0, _ptr(gi),
+        gi.numel() if gi is not None else 0, _ptr(gs), rows, nthreads or default_threads())
+    _check(rc, "scaled_quantize_per_token")
+
+
+def f32_to_bf16_bits(x: torch.Tensor) -> torch.Tensor:
+    x = x.to(torch.float32).contiguous()
+    out = torch.empty(x.shape, dtype=torch.int16)
+    lib().oracle_f32_to_bf16(x.data_ptr(), out.data_ptr(), x.numel())
+    return out
+
+
+def f32_to_f16_bits(x: torch.Tensor) -> torch.Tensor:
+    x = x.to(torch.float32).contiguous()
+    out = torch.empty(x.shape, dtype=torch.int16)
+    lib().oracle_f32_to_f16(x.data_ptr(), out.data_ptr(), x.numel())
+    return out
+
+
+def f16_bits_to_f32(bits: torch.Tensor) -> torch.Tensor:
+    bits = bits.to(torch.int16).contiguous()
+    out = torch.empty(bits.shape, dtype=torch.float32)
+    lib().oracle_f16_to_f32(bits.data_ptr(), out.data_ptr(), bits.numel())
+    return out

@@ -1,0 +1,442 @@
+/*
+ * tmo_oracle.c -- CPU restatement of torch_mlu_ops' quantized paged-KV-cache path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP kernels and the
+ * CPU baseline timed by bench.py.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg load it.  The product path (domesticated_torch_mlu_ops_amd) never
+ * links, loads or calls it, and has no CPU fallback.
+ *
+ * The reference ships no kernels and no CPU implementation: its arithmetic is specified
+ * only by the docstring "Math" blocks of /root/reference/_ops.py, cited per function
+ * below.  Where those blocks are ambiguous this file fixes one reading:
+ *
+ *   D1  arithmetic in fp32: scale = RN(fp32(amax) / 127.0f) (IEEE divide), and
+ *       code = RNE(RN(fp32(x) / scale)) with a true IEEE divide per element
+ *       (_ops.py:1532-1533, 3171-3172).
+ *   D2  codes are clamped to [-128, 127] (_ops.py:1535, 3172).
+ *   D3  an all-zero row gives scale 0 and codes 0 (the literal math divides 0/0).
+ *   D4  slot < 0 writes neither codes nor scale (_ops.py:1264, 1656, 6400-6401); a slot
+ *       >= num_blocks*block_size is treated the same way (undefined in the reference).
+ *   D5  NaN / Inf inputs are outside the contract.
+ *   D6  dequant = RNE_out(fp32(code) * scale)   (cast order of _ops.py:3677).
+ *   D7  smoothed = RN(fp32(x) * smooth), materialised before amax and divide (no FMA).
+ *   D8  int8 codes only.
+ *
+ * Parity pins for every function here live in tests/test_oracle_pins.py (torch-CPU
+ * execution of the docstring math, exact rational arithmetic on engineered near-ties,
+ * closed forms and invariants).
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off -fno-fast-math, SSE2 fp32 math).
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_I8 = 3 };
+
+/* ------------------------------------------------------------------ conversions */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+static inline float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+static inline float f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    if (e == 0x1f) return u2f(sign | 0x7f800000u | (m << 13));          /* inf / nan */
+    if (e == 0) {
+        if (m == 0) return u2f(sign);                                    /* +-0 */
+        /* subnormal: m * 2^-24, exact in fp32 */
+        float v = (float)m * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    }
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* round-to-nearest-even fp32 -> bf16 (NaN stays a quiet NaN) */
+static inline uint16_t f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* round-to-nearest-even fp32 -> fp16, IEEE overflow to inf, gradual underflow */
+static inline uint16_t f32_to_f16(float f) {
+    uint32_t x = f2u(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);   /* >= 65520 -> inf */
+    if (ax >= 0x38800000u) {                                     /* normal fp16 */
+        uint32_t r = ax - 0x38000000u;                           /* rebias 127 -> 15 */
+        r += 0xfffu + ((r >> 13) & 1u);
+        return (uint16_t)(sign | (r >> 13));
+    }
+    if (ax < 0x33000000u) return (uint16_t)sign;                 /* < 2^-25 -> 0 */
+    uint32_t e = ax >> 23;                                       /* 102 .. 112 */
+    uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+    uint32_t shift = 126u - e;                                   /* 14 .. 24 */
+    uint32_t q = m >> shift;
+    uint32_t rem = m & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+}
+
+static inline float load_elem(const void* base, int64_t idx, int dtype) {
+    switch (dtype) {
+    case DT_F32: return ((const float*)base)[idx];
+    case DT_F16: return f16_to_f32(((const uint16_t*)base)[idx]);
+    case DT_BF16: return bf16_to_f32(((const uint16_t*)base)[idx]);
+    default: return 0.0f;
+    }
+}
+
+static inline void store_elem(void* base, int64_t idx, int dtype, float v) {
+    switch (dtype) {
+    case DT_F32: ((float*)base)[idx] = v; break;
+    case DT_F16: ((uint16_t*)base)[idx] = f32_to_f16(v); break;
+    case DT_BF16: ((uint16_t*)base)[idx] = f32_to_bf16(v); break;
+    default: break;
+    }
+}
+
+static int elem_size(int dtype) {
+    switch (dtype) {
+    case DT_F32: return 4;
+    case DT_F16: case DT_BF16: return 2;
+    case DT_I8: return 1;
+    default: return 0;
+    }
+}
+
+/* Exposed for the pins in tests/: element conversions over arrays. */
+void oracle_f32_to_bf16(const float* in, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = f32_to_bf16(in[i]);
+}
+void oracle_f32_to_f16(const float* in, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = f32_to_f16(in[i]);
+}
+void oracle_f16_to_f32(const uint16_t* in, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = f16_to_f32(in[i]);
+}
+
+/* ------------------------------------------------------------------ threading */
+
+typedef void (*range_fn)(void* ctx, int64_t lo, int64_t hi);
+typedef struct { range_fn fn; void* ctx; int64_t lo, hi; } range_job;
+
+static void* run_range(void* p) {
+    range_job* j = (range_job*)p;
+    j->fn(j->ctx, j->lo, j->hi);
+    return NULL;
+}
+
+/* Split [0, n) into nthreads contiguous ranges and run fn on each (plain pthreads, so the
+ * library does not bring its own OpenMP runtime into a process that already has torch's). */
+static void parallel_for(int64_t n, int nthreads, range_fn fn, void* ctx) {
+    if (nthreads <= 1 || n < 2 * (int64_t)nthreads) { fn(ctx, 0, n); return; }
+    if (nthreads > 256) nthreads = 256;
+    pthread_t th[256];
+    int created[256];
+    range_job jobs[256];
+    int64_t chunk = (n + nthreads - 1) / nthreads;
+    int nt = 0;
+    for (int t = 0; t < nthreads; ++t) {
+        int64_t lo = (int64_t)t * chunk, hi = lo + chunk;
+        if (lo >= n) break;
+        if (hi > n) hi = n;
+        jobs[t].fn = fn; jobs[t].ctx = ctx; jobs[t].lo = lo; jobs[t].hi = hi;
+        created[t] = pthread_create(&th[t], NULL, run_range, &jobs[t]) == 0;
+        if (!created[t]) fn(ctx, lo, hi);
+        nt = t + 1;
+    }
+    for (int t = 0; t < nt; ++t)
+        if (created[t]) pthread_join(th[t], NULL);
+}
+
+/* ------------------------------------------------------------------ row quantiser */
+
+/*
+ * One row of `n` fp32 values (already converted / smoothed) -> int8 codes + fp32 scale.
+ * _ops.py:1524-1537 (quant_to_paged_cache) and _ops.py:3167-3172 (moe_quantize):
+ *   max_value = max(|x|); scale = max_value / 127; codes = clip(round(x / scale), -128, 127)
+ */
+static float quant_row(const float* x, int64_t n, int8_t* codes) {
+    float amax = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        float a = fabsf(x[i]);
+        if (a > amax) amax = a;
+    }
+    float scale = amax / 127.0f;
+    if (scale == 0.0f) {                                   /* D3 */
+        memset(codes, 0, (size_t)n);
+        return scale;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        float q = rintf(x[i] / scale);                     /* D1: IEEE divide, RNE */
+        if (q < -128.0f) q = -128.0f;                      /* D2 */
+        if (q > 127.0f) q = 127.0f;
+        codes[i] = (int8_t)q;
+    }
+    return scale;
+}
+
+/* ------------------------------------------------------------------ quant_to_paged_cache */
+
+typedef struct {
+    const void* src[2];
+    int64_t st[2], sh[2];
+    int8_t* cache[2];
+    float* scale[2];
+    int nkv;
+    const int32_t* slot;
+    int64_t T, H, D, NB, BS;
+    int dtype;
+} qpc_ctx;
+
+static void qpc_range(void* p, int64_t lo, int64_t hi) {
+    qpc_ctx* c = (qpc_ctx*)p;
+    float* row = (float*)malloc((size_t)c->D * sizeof(float));
+    int8_t* codes = (int8_t*)malloc((size_t)c->D);
+    for (int64_t t = lo; t < hi; ++t) {
+        int64_t slot = c->slot[t];
+        if (slot < 0 || slot >= c->NB * c->BS) continue;            /* D4 */
+        int64_t blk = slot / c->BS, off = slot % c->BS;              /* _ops.py:1265-1266 */
+        for (int kv = 0; kv < c->nkv; ++kv) {
+            for (int64_t h = 0; h < c->H; ++h) {
+                int64_t base = t * c->st[kv] + h * c->sh[kv];
+                for (int64_t d = 0; d < c->D; ++d) row[d] = load_elem(c->src[kv], base + d, c->dtype);
+                float s = quant_row(row, c->D, codes);
+                int64_t page_row = (blk * c->H + h) * c->BS + off;   /* [NB, H, BS] */
+                memcpy(c->cache[kv] + page_row * c->D, codes, (size_t)c->D);
+                c->scale[kv][page_row] = s;
+            }
+        }
+    }
+    free(row);
+    free(codes);
+}
+
+/* _ops.py:1511-1565: quant_to_paged_cache(k, v, k_cache, v_cache, k_scale, v_scale, slot_mapping)
+ * k/v [T, H, D] with element strides (token, head), last dim contiguous;
+ * caches [NB, H, BS, D] int8 contiguous; scales [NB, H, BS] fp32 contiguous. v may be NULL. */
+int oracle_quant_to_paged_cache(const void* k, const void* v, int dtype,
+                                int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh,
+                                int8_t* k_cache, int8_t* v_cache, float* k_scale, float* v_scale,
+                                const int32_t* slot_mapping, int64_t T, int64_t H, int64_t D,
+                                int64_t NB, int64_t BS, int nthreads) {
+    if (elem_size(dtype) == 0 || dtype == DT_I8) return -2;
+    if (T < 0 || H <= 0 || D <= 0 || NB < 0 || BS <= 0) return -1;
+    qpc_ctx c = {{k, v}, {k_st, v_st}, {k_sh, v_sh}, {k_cache, v_cache}, {k_scale, v_scale},
+                 v ? 2 : 1, slot_mapping, T, H, D, NB, BS, dtype};
+    parallel_for(T, nthreads, qpc_range, &c);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ reshape_paged_cache */
+
+typedef struct {
+    char* kv[2];
+    int64_t st[2], sh[2];
+    char* cache[2];
+    int nkv;
+    const int32_t* slot;
+    int64_t T, H, D, NB, BS, es;
+    int direction;
+} rpc_ctx;
+
+static void rpc_range(void* p, int64_t lo, int64_t hi) {
+    rpc_ctx* c = (rpc_ctx*)p;
+    int64_t row_bytes = c->D * c->es;
+    for (int64_t t = lo; t < hi; ++t) {
+        int64_t slot = c->slot[t];
+        if (slot < 0 || slot >= c->NB * c->BS) continue;             /* _ops.py:1264 */
+        int64_t blk = slot / c->BS, off = slot % c->BS;
+        for (int kv = 0; kv < c->nkv; ++kv) {
+            for (int64_t h = 0; h < c->H; ++h) {
+                char* tok = c->kv[kv] + (t * c->st[kv] + h * c->sh[kv]) * c->es;
+                char* page = c->cache[kv] + ((blk * c->H + h) * c->BS + off) * row_bytes;
+                if (c->direction) memcpy(tok, page, (size_t)row_bytes);   /* gather */
+                else memcpy(page, tok, (size_t)row_bytes);               /* scatter */
+            }
+        }
+    }
+}
+
+/* _ops.py:1251-1294: reshape_paged_cache(k, v, k_cache, v_cache, slot_mapping, direction).
+ * direction == 0 scatters k/v into the caches, direction != 0 gathers them back. */
+int oracle_reshape_paged_cache(void* k, void* v, int dtype, int64_t k_st, int64_t k_sh,
+                               int64_t v_st, int64_t v_sh, void* k_cache, void* v_cache,
+                               const int32_t* slot_mapping, int64_t T, int64_t H, int64_t D,
+                               int64_t NB, int64_t BS, int direction, int nthreads) {
+    int es = elem_size(dtype);
+    if (es == 0) return -2;
+    if (T < 0 || H <= 0 || D <= 0 || NB < 0 || BS <= 0) return -1;
+    rpc_ctx c = {{(char*)k, (char*)v}, {k_st, v_st}, {k_sh, v_sh},
+                 {(char*)k_cache, (char*)v_cache}, (v && v_cache) ? 2 : 1, slot_mapping,
+                 T, H, D, NB, BS, es, direction};
+    parallel_for(T, nthreads, rpc_range, &c);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ dequant_from_paged_cache */
+
+typedef struct {
+    void* out[2];
+    int64_t st[2], sh[2];
+    const int8_t* cache[2];
+    const float* scale[2];
+    int nkv;
+    const int32_t* ctx_len;
+    const int64_t* seq_off;
+    const int32_t* bt;
+    int64_t B, MB, NB, H, BS, D, total;
+    int mode, dtype;
+} dpc_ctx;
+
+static void dpc_range(void* p, int64_t lo, int64_t hi) {
+    dpc_ctx* c = (dpc_ctx*)p;
+    for (int64_t i = lo; i < hi; ++i) {
+        int64_t len = c->ctx_len[i];
+        int64_t begin = c->seq_off[i];
+        for (int64_t t = 0; t < len; ++t) {
+            int64_t j = t / c->BS, o = t % c->BS;                  /* _ops.py:3750-3751 */
+            if (j >= c->MB) break;
+            int64_t blk = c->bt[i * c->MB + j];
+            if (blk < 0 || blk >= c->NB) continue;
+            int64_t row = begin + t;
+            if (row < 0 || row >= c->total) continue;
+            for (int kv = 0; kv < c->nkv; ++kv) {
+                for (int64_t h = 0; h < c->H; ++h) {
+                    const int8_t* codes = c->cache[kv] + ((blk * c->H + h) * c->BS + o) * c->D;
+                    int64_t obase = row * c->st[kv] + h * c->sh[kv];
+                    for (int64_t d = 0; d < c->D; ++d) {
+                        float s = c->mode == 0 ? c->scale[kv][h * c->D + d]          /* [H, D] */
+                                               : c->scale[kv][(blk * c->H + h) * c->BS + o];
+                        store_elem(c->out[kv], obase + d, c->dtype, (float)codes[d] * s);  /* D6 */
+                    }
+                }
+            }
+        }
+    }
+}
+
+/* _ops.py:3734-3824: dequant_from_paged_cache(key, value, key_cache, value_cache, key_scale,
+ * value_scale, context_lengths, max_context_len, context_seq_offset, block_tables, quant_mode,
+ * quant_bit).  quant_mode 0: scale [H, D]; 1: scale [NB, H, BS] (_ops.py:3765-3771).
+ * context_seq_offset NULL -> exclusive cumsum of context_lengths (_ops.py:3758). */
+int oracle_dequant_from_paged_cache(void* key, void* value, int out_dtype,
+                                    int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh,
+                                    int64_t total_rows, const int8_t* key_cache,
+                                    const int8_t* value_cache, const float* key_scale,
+                                    const float* value_scale, const int32_t* context_lengths,
+                                    const int32_t* context_seq_offset, const int32_t* block_tables,
+                                    int64_t B, int64_t max_blocks, int64_t NB, int64_t H,
+                                    int64_t BS, int64_t D, int quant_mode, int nthreads) {
+    if (out_dtype != DT_F16 && out_dtype != DT_BF16 && out_dtype != DT_F32) return -2;
+    if (quant_mode != 0 && quant_mode != 1) return -3;
+    if (B < 0 || H <= 0 || D <= 0 || BS <= 0 || max_blocks < 0) return -1;
+    int64_t* off = (int64_t*)malloc((size_t)(B > 0 ? B : 1) * sizeof(int64_t));
+    int64_t acc = 0;
+    for (int64_t i = 0; i < B; ++i) {
+        off[i] = context_seq_offset ? (int64_t)context_seq_offset[i] : acc;
+        acc += context_lengths[i];
+    }
+    dpc_ctx c = {{key, value}, {k_st, v_st}, {k_sh, v_sh}, {key_cache, value_cache},
+                 {key_scale, value_scale}, (value && value_cache) ? 2 : 1, context_lengths, off,
+                 block_tables, B, max_blocks, NB, H, BS, D, total_rows, quant_mode, out_dtype};
+    parallel_for(B, nthreads, dpc_range, &c);
+    free(off);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ scaled_quantize (dynamic per token) */
+
+typedef struct {
+    const void* x;
+    int dtype;
+    int64_t n0, inner, C, row_stride;
+    int8_t* out;
+    float* out_scale;
+    const float* smooth;
+    int64_t smooth_len;
+    const int64_t* group_end;   /* inclusive prefix of token_count, or NULL */
+    int64_t ngroups;
+    const int32_t* gidx;
+    int64_t gstart, glen;
+    int64_t rows, valid_rows;
+} sq_ctx;
+
+static void sq_range(void* p, int64_t lo, int64_t hi) {
+    sq_ctx* c = (sq_ctx*)p;
+    float* row = (float*)malloc((size_t)c->C * sizeof(float));
+    for (int64_t r = lo; r < hi; ++r) {
+        if (r >= c->valid_rows) continue;
+        int64_t src = r;
+        if (c->gidx) {                                                 /* _ops.py:3150-3154 */
+            int64_t gi = c->gstart + r;
+            if (gi < 0 || gi >= c->glen) continue;
+            src = c->gidx[gi];
+        }
+        if (src < 0 || src >= c->n0) continue;
+        const float* sm = c->smooth;
+        if (c->group_end) {                                            /* _ops.py:3156-3162 */
+            int64_t g = 0;
+            while (g < c->ngroups && c->group_end[g] <= r) ++g;
+            if (g >= c->ngroups) continue;   /* r >= sum(token_count): not produced */
+            if (sm) sm += g * c->smooth_len;
+        }
+        for (int64_t j = 0; j < c->inner; ++j) {
+            int64_t ibase = (src * c->inner + j) * c->row_stride;
+            int64_t orow = r * c->inner + j;
+            for (int64_t d = 0; d < c->C; ++d) {
+                float xv = load_elem(c->x, ibase + d, c->dtype);
+                if (sm) xv = xv * sm[c->smooth_len == 1 ? 0 : d];          /* D7 */
+                row[d] = xv;
+            }
+            c->out_scale[orow] = quant_row(row, c->C, c->out + orow * c->C);
+        }
+    }
+    free(row);
+}
+
+/* _ops.py:3126-3253 (moe_quantize) / 4407-4492 (scaled_quantize), quant_mode "dynamic_per_token":
+ *   x [n0, inner..., C] viewed as n0*inner rows of C (row stride `row_stride` elements);
+ *   smooth NULL, [1], [C] or [groups, C] fp32 (smooth_len = 1 or C); token_count [groups] (NULL: no grouping);
+ *   gather_index [gather_len] (NULL: identity); gather_start NULL or [1]; rows whose
+ *   gather position falls outside gather_index are not produced.
+ *   Output rows = `rows` (gather_index.size(0) or n0) x inner; codes [rows*inner, C] int8,
+ *   scales [rows*inner] fp32.  With gather_start given only the first sum(token_count) rows
+ *   are produced (_ops.py:3150-3152); with token_count given, rows at or past
+ *   sum(token_count) are never produced. */
+int oracle_scaled_quantize_per_token(const void* x, int dtype, int64_t n0, int64_t inner,
+                                     int64_t C, int64_t row_stride, int8_t* out, float* out_scale,
+                                     const float* smooth, int64_t smooth_len,
+                                     const int32_t* token_count,
+                                     int64_t ngroups, const int32_t* gather_index,
+                                     int64_t gather_len, const int32_t* gather_start,
+                                     int64_t rows, int nthreads) {
+    if (dtype != DT_F32 && dtype != DT_F16 && dtype != DT_BF16) return -2;
+    if (n0 < 0 || inner <= 0 || C <= 0 || rows < 0) return -1;
+    if (smooth && smooth_len != 1 && smooth_len != C) return -1;
+    int64_t* gend = NULL;
+    int64_t total = rows;
+    if (token_count) {
+        gend = (int64_t*)malloc((size_t)(ngroups > 0 ? ngroups : 1) * sizeof(int64_t));
+        int64_t acc = 0;
+        for (int64_t g = 0; g < ngroups; ++g) { acc += token_count[g]; gend[g] = acc; }
+        if (gather_start) total = acc < rows ? acc : rows;
+    }
+    sq_ctx c = {x, dtype, n0, inner, C, row_stride, out, out_scale, smooth, smooth_len,
+                gend, ngroups, gather_index,
+                gather_start ? (int64_t)gather_start[0] : 0, gather_len, rows, total};
+    parallel_for(rows, nthreads, sq_range, &c);
+    free(gend);
+    return 0;
+}

@@ -1,0 +1,128 @@
+"""The C ABI (include/tmo_hip.h) of libtmo_hip.so, checked on the CPU: the library loads,
+exports every declared entry point, and rejects invalid arguments with the documented status
+codes before touching any device memory (the pointers below are never dereferenced)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "tmo_hip.h"
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+INT = ctypes.c_int
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails validation first
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(tmo_hip_\w+)\s*\(", text, re.M)))
+
+
+def header_enum(name):
+    m = re.search(rf"\b{name}\s*=\s*(-?\d+)", HEADER.read_text())
+    return int(m.group(1))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from domesticated_torch_mlu_ops_amd import _loader
+    L = _loader.c_abi()
+    L.tmo_hip_status_string.restype = ctypes.c_char_p
+    L.tmo_hip_quant_to_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 5 + [I64] * 5 + [INT, P]
+    L.tmo_hip_reshape_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 3 + [I64] * 5 + [INT, INT, P]
+    L.tmo_hip_dequant_from_paged_cache.argtypes = [P, P] + [I64] * 5 + [P] * 7 + [I64] * 7 + \
+        [INT, INT, INT, P]
+    L.tmo_hip_scaled_quantize_per_token.argtypes = [P] + [I64] * 4 + [P] * 3 + [I64, P, I64, P, I64, P, I64, INT, P]
+    return L
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert set(names) == {"tmo_hip_abi_version", "tmo_hip_status_string",
+                          "tmo_hip_reshape_paged_cache", "tmo_hip_quant_to_paged_cache",
+                          "tmo_hip_dequant_from_paged_cache", "tmo_hip_scaled_quantize_per_token"}
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_abi_version_and_status_strings(lib):
+    m = re.search(r"#define\s+TMO_HIP_ABI_VERSION\s+(\d+)", HEADER.read_text())
+    assert lib.tmo_hip_abi_version() == int(m.group(1))
+    for name in ("TMO_OK", "TMO_ERR_INVALID_ARGUMENT", "TMO_ERR_UNSUPPORTED_DTYPE",
+                 "TMO_ERR_UNSUPPORTED_MODE", "TMO_ERR_LAUNCH"):
+        s = lib.tmo_hip_status_string(header_enum(name))
+        assert s and s != b"unknown status"
+    assert lib.tmo_hip_status_string(12345) == b"unknown status"
+
+
+EINVAL = -1
+EDTYPE = -2
+EMODE = -3
+
+
+def quant(lib, k=FAKE, v=None, kc=FAKE, vc=None, ks=FAKE, vs=None, slot=FAKE, T=4, H=8, D=128,
+          NB=4, BS=16, dtype=2, st=1024, sh=128):
+    return lib.tmo_hip_quant_to_paged_cache(k, v, st, sh, st, sh, kc, vc, ks, vs, slot, T, H, D,
+                                            NB, BS, dtype, None)
+
+
+def test_quant_validation(lib):
+    assert quant(lib, dtype=3) == EDTYPE          # int8 input
+    assert quant(lib, dtype=9) == EDTYPE
+    assert quant(lib, k=None) == EINVAL
+    assert quant(lib, slot=None) == EINVAL
+    assert quant(lib, v=FAKE) == EINVAL           # v without v_cache / v_scale
+    assert quant(lib, v=FAKE, vc=FAKE) == EINVAL
+    assert quant(lib, H=0) == EINVAL
+    assert quant(lib, D=-1) == EINVAL
+    assert quant(lib, BS=0) == EINVAL
+    assert quant(lib, T=-1) == EINVAL
+    assert quant(lib, st=-5) == EINVAL
+    assert quant(lib, T=0) == 0                   # nothing to do: success, nothing enqueued
+    assert quant(lib, NB=0) == 0
+
+
+def test_reshape_validation(lib):
+    def call(dtype=2, k=FAKE, v=None, vc=None, H=8, BS=16, T=4):
+        return lib.tmo_hip_reshape_paged_cache(k, v, 1024, 128, 1024, 128, FAKE, vc, FAKE, T, H,
+                                               128, 4, BS, dtype, 0, None)
+    assert call(dtype=7) == EDTYPE
+    assert call(k=None) == EINVAL
+    assert call(v=FAKE) == EINVAL
+    assert call(H=-2) == EINVAL
+    assert call(BS=0) == EINVAL
+    assert call(T=0) == 0
+
+
+def test_dequant_validation(lib):
+    def call(mode=1, bit=8, dtype=2, key=FAKE, value=None, vc=None, vs=None, B=2, H=8, total=10):
+        return lib.tmo_hip_dequant_from_paged_cache(
+            key, value, 1024, 128, 1024, 128, total, FAKE, vc, FAKE, vs, FAKE, None, FAKE, B, 4,
+            64, 16, H, 16, 128, mode, bit, dtype, None)
+    assert call(mode=2) == EMODE
+    assert call(bit=4) == EMODE
+    assert call(dtype=3) == EDTYPE
+    assert call(key=None) == EINVAL
+    assert call(value=FAKE) == EINVAL
+    assert call(H=0) == EINVAL
+    assert call(B=-1) == EINVAL
+    assert call(B=0) == 0
+    assert call(total=0) == 0
+
+
+def test_scaled_quantize_validation(lib):
+    def call(dtype=2, x=FAKE, smooth=None, smooth_len=0, tc=None, groups=0, gi=None, gs=None,
+             C=64, stride=64, rows=4):
+        return lib.tmo_hip_scaled_quantize_per_token(x, 4, 1, C, stride, FAKE, FAKE, smooth,
+                                                     smooth_len, tc, groups, gi, 0, gs, rows,
+                                                     dtype, None)
+    assert call(dtype=3) == EDTYPE
+    assert call(x=None) == EINVAL
+    assert call(smooth=FAKE, smooth_len=7) == EINVAL   # neither 1 nor C
+    assert call(tc=FAKE, groups=0) == EINVAL
+    assert call(gs=FAKE) == EINVAL                     # start position without gather_index
+    assert call(stride=10) == EINVAL                   # rows overlap
+    assert call(rows=0) == 0

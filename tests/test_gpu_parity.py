@@ -1,0 +1,353 @@
+"""GPU parity: the HIP kernels (through the torch_mlu_ops ops -> C ABI) against the CPU oracle.
+
+Bar: bit-exact for everything -- int8 codes, fp32 scales, gathered/scattered bytes and the
+dequantised bf16/fp16/fp32 outputs -- including the bytes a call must NOT write (caches and
+outputs start from a sentinel pattern and are compared whole).  All five BASELINE configs run
+at full size; the edge-case tests cover the other kernel paths (generic layouts, strided
+views, every lane-group width, skipped slots, zero / tiny / huge rows).
+"""
+import pytest
+import torch
+
+from tests import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.float32:
+        return t.view(torch.int32)
+    if t.dtype in (torch.float16, torch.bfloat16):
+        return t.view(torch.int16)
+    return t
+
+
+def assert_bits_equal(got: torch.Tensor, want: torch.Tensor, what: str) -> None:
+    a, b = _bits(got), _bits(want)
+    assert a.shape == b.shape, f"{what}: shape {tuple(a.shape)} != {tuple(b.shape)}"
+    if torch.equal(a, b):
+        return
+    diff = (a != b).nonzero()
+    first = tuple(diff[0].tolist())
+    raise AssertionError(f"{what}: {diff.shape[0]} mismatching elements, first at {first}: "
+                         f"gpu={got.detach().cpu()[first]!r} oracle={want[first]!r}")
+
+
+# ---------------------------------------------------------------------------- quant_to_paged_cache
+
+def run_quant(tmo, ref, dev, case: W.PagedQuantCase, with_v=True, k=None, v=None):
+    """GPU op and oracle on the same inputs; returns (gpu caches, oracle caches)."""
+    k = case.k if k is None else k
+    v = (case.v if v is None else v) if with_v else None
+    kc, vc, ks, vs = case.empty_caches()
+    if not with_v:
+        vc = vs = None
+    ref.quant_to_paged_cache(k, v, kc, vc, ks, vs, case.slot_mapping)
+    gk, gv, gks, gvs = case.empty_caches(device=dev)
+    kd = k.to(dev)
+    vd = v.to(dev) if v is not None else None
+    if not with_v:
+        gv = gvs = None
+    out = tmo.quant_to_paged_cache(kd, vd, gk, gv, gks, gvs, case.slot_mapping.to(dev))
+    assert out[0] is gk
+    torch.cuda.synchronize()
+    return (gk, gv, gks, gvs), (kc, vc, ks, vs)
+
+
+def check_quant(tmo, ref, dev, case, with_v=True, k=None, v=None):
+    got, want = run_quant(tmo, ref, dev, case, with_v, k, v)
+    for g, w, n in zip(got, want, ("k_cache", "v_cache", "k_scale", "v_scale")):
+        if w is not None:
+            assert_bits_equal(g, w, f"{case.name} {n}")
+    return got, want
+
+
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3"])
+def test_quant_to_paged_cache_configs(tmo, ref, dev, cfg):
+    case = getattr(W, cfg)()
+    print(f"[quant_to_paged_cache] {cfg} T={case.tokens}", flush=True)
+    got, want = check_quant(tmo, ref, dev, case)
+    # every valid token wrote its codes; skipped slots kept the sentinel
+    written = (want[2] != W.SCALE_SENTINEL).sum().item()
+    assert written == case.valid_tokens() * case.k.shape[1]
+
+
+def _case(name, T, H, D, NB, BS, dtype, seed, neg_frac=0.0, oob=0):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(T, H, D, generator=g).to(dtype)
+    v = (3.0 * torch.randn(T, H, D, generator=g)).to(dtype)
+    slot = torch.randperm(NB * BS, generator=g)[:T].to(torch.int32)
+    if neg_frac:
+        slot[torch.randperm(T, generator=g)[: int(neg_frac * T)]] = -1
+    if oob:
+        slot[torch.randperm(T, generator=g)[:oob]] = NB * BS + 5
+    return W.PagedQuantCase(name, k, v, slot, NB, BS)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [8, 16, 32, 64, 128, 256, 512])
+def test_quant_lane_group_widths(tmo, ref, dev, dtype, D):
+    """Every lane-group width G = D / (16 B / elem) of the vector kernel (1..64 lanes; the
+    f32 D=512 row takes the generic one-wave path), the row maximum placed in every lane."""
+    T, H = 70, 3
+    case = _case(f"G D={D} {dtype}", T, H, D, 40, 16, dtype, seed=D)
+    k = case.k.clone()
+    for t in range(T):  # put the row max at element t % D (so in lane (t % D) / per_vec)
+        k[t, :, t % D] = 50.0 * (1 if t % 2 else -1)
+    check_quant(tmo, ref, dev, case, k=k)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D,BS", [(128, 16), (128, 7), (80, 16), (96, 32), (72, 5), (1, 16)])
+def test_quant_shapes_and_block_sizes(tmo, ref, dev, dtype, D, BS):
+    """Power-of-two and odd block sizes; head sizes outside the vector path (generic)."""
+    case = _case(f"D={D} BS={BS}", 53, 5, D, 23, BS, dtype, seed=7 * D + BS, neg_frac=0.2, oob=3)
+    check_quant(tmo, ref, dev, case)
+
+
+def test_quant_k_only_and_strided_views(tmo, ref, dev):
+    """v=None, and k/v as column views of a fused [T, 3H, D] qkv tensor."""
+    T, H, D = 64, 4, 128
+    g = torch.Generator().manual_seed(11)
+    qkv = torch.randn(T, 3 * H, D, generator=g).to(torch.bfloat16)
+    k, v = qkv[:, H:2 * H], qkv[:, 2 * H:]
+    slot = torch.randperm(32 * 16, generator=g)[:T].to(torch.int32)
+    case = W.PagedQuantCase("qkv-view", k, v, slot, 32, 16)
+    check_quant(tmo, ref, dev, case)  # vector path with token stride 3*H*D
+    check_quant(tmo, ref, dev, case, with_v=False)
+    # misaligned by one element: falls back to the generic path
+    flat = torch.randn(T * H * D + 1, generator=g).to(torch.bfloat16)
+    km = flat[1:].view(T, H, D)
+    check_quant(tmo, ref, dev, W.PagedQuantCase("misaligned", km, km, slot, 32, 16))
+
+
+def test_quant_special_rows(tmo, ref, dev):
+    """Zero rows (scale 0, codes 0), exact .5 ties, rows whose scale is below the fast-divide
+    range (IEEE path), huge and subnormal magnitudes, single non-zero rows."""
+    T, H, D = 16, 2, 128
+    k = torch.zeros(T, H, D)
+    k[1, 0, :5] = torch.tensor([127.0, 2.5, 3.5, -0.5, 1.5])               # ties, scale 1
+    k[2, 1, 7] = -3.0                                                        # single non-zero
+    k[3, :, :] = torch.linspace(-1, 1, D) * 1e-20                            # scale < 2^-60
+    k[4, :, :] = torch.linspace(-1, 1, D) * 3e38                             # near bf16 max
+    k[5, :, :] = torch.linspace(-1, 1, D) * 1e-39                            # bf16 subnormals
+    k[6, 0, :] = 5.0                                                         # constant row
+    g = torch.Generator().manual_seed(5)
+    k[7:] = torch.randn(T - 7, H, D, generator=g) * torch.logspace(-30, 30, T - 7)[:, None, None]
+    slot = torch.arange(T, dtype=torch.int32) * 3
+    for dtype in (torch.bfloat16, torch.float32):
+        kk = k.to(dtype)
+        case = W.PagedQuantCase(f"special {dtype}", kk, kk.flip(0).contiguous(), slot, 4, 16)
+        got, _ = check_quant(tmo, ref, dev, case)
+        kc = got[0].cpu()
+        assert torch.all(kc[0, :, 0, :] == 0)                     # token 0 (all zeros)
+        assert kc[0, 0, 3, :5].tolist() == [127, 2, 4, 0, 2]      # token 1 at slot 3
+
+
+# ---------------------------------------------------------------------------- reshape_paged_cache
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32, torch.int8])
+@pytest.mark.parametrize("D", [128, 64, 3, 20])
+def test_reshape_paged_cache_roundtrip(tmo, ref, dev, dtype, D):
+    T, H, NB, BS = 100, 4, 30, 16
+    g = torch.Generator().manual_seed(D)
+    if dtype == torch.int8:
+        k = torch.randint(-128, 128, (T, H, D), generator=g, dtype=torch.int8)
+        v = torch.randint(-128, 128, (T, H, D), generator=g, dtype=torch.int8)
+    else:
+        k = torch.randn(T, H, D, generator=g).to(dtype)
+        v = torch.randn(T, H, D, generator=g).to(dtype)
+    slot = torch.randperm(NB * BS, generator=g)[:T].to(torch.int32)
+    slot[::9] = -1
+    slot[5] = NB * BS  # out of range: skipped
+    case = W.PagedQuantCase("reshape", k, v, slot, NB, BS)
+    kc, vc, _, _ = case.empty_caches(dtype=dtype)
+    ref.reshape_paged_cache(k, v, kc, vc, slot, False)
+    gk, gv, _, _ = case.empty_caches(device=dev, dtype=dtype)
+    out = tmo.reshape_paged_cache(k.to(dev), v.to(dev), gk, gv, slot.to(dev), False)
+    assert out[0] is gk and out[1] is gv
+    assert_bits_equal(gk, kc, "scatter k_cache")
+    assert_bits_equal(gv, vc, "scatter v_cache")
+    # gather back into fresh rows
+    kb = torch.zeros_like(k)
+    vb = torch.zeros_like(v)
+    ref.reshape_paged_cache(kb, vb, kc, vc, slot, True)
+    gkb, gvb = torch.zeros_like(k, device=dev), torch.zeros_like(v, device=dev)
+    tmo.reshape_paged_cache(gkb, gvb, gk, gv, slot.to(dev), True)
+    assert_bits_equal(gkb, kb, "gather k")
+    assert_bits_equal(gvb, vb, "gather v")
+    valid = (slot >= 0) & (slot < NB * BS)
+    assert torch.equal(_bits(gkb)[valid], _bits(k)[valid])  # gather(scatter(x)) == x
+
+
+def test_reshape_paged_cache_cfg3(tmo, ref, dev):
+    case = W.cfg3()
+    kc, vc, _, _ = case.empty_caches(dtype=torch.bfloat16)
+    ref.reshape_paged_cache(case.k, case.v, kc, vc, case.slot_mapping, False)
+    gk, gv, _, _ = case.empty_caches(device=dev, dtype=torch.bfloat16)
+    tmo.reshape_paged_cache(case.k.to(dev), case.v.to(dev), gk, gv, case.slot_mapping.to(dev))
+    assert_bits_equal(gk, kc, "cfg3 reshape k_cache")
+    assert_bits_equal(gv, vc, "cfg3 reshape v_cache")
+
+
+# ---------------------------------------------------------------------------- dequant_from_paged_cache
+
+def _dequant_both(tmo, ref, dev, layout, caches, out_dtype, mode, seq_offset=None, total=None,
+                  with_v=True):
+    kc, vc, ks, vs = caches
+    H, D = kc.shape[1], kc.shape[3]
+    total = layout.total_tokens if total is None else total
+    kc_h, vc_h, ks_h, vs_h = (t.cpu() if t is not None else None for t in caches)
+    want_k = torch.full((total, H, D), -3.0).to(out_dtype)
+    want_v = want_k.clone() if with_v else None
+    ref.dequant_from_paged_cache(want_k, want_v, kc_h, vc_h if with_v else None, ks_h,
+                                 vs_h if with_v else None, layout.context_lengths, seq_offset,
+                                 layout.block_tables, mode)
+    got_k = torch.full((total, H, D), -3.0, device=dev).to(out_dtype)
+    got_v = got_k.clone() if with_v else None
+    tmo.dequant_from_paged_cache(
+        got_k, got_v, kc, vc if with_v else None, ks, vs if with_v else None,
+        layout.context_lengths.to(dev), layout.max_context_len,
+        seq_offset.to(dev) if seq_offset is not None else None, layout.block_tables.to(dev), mode, 8)
+    assert_bits_equal(got_k, want_k, f"{layout.name} key")
+    if with_v:
+        assert_bits_equal(got_v, want_v, f"{layout.name} value")
+    return got_k, want_k
+
+
+def test_dequant_cfg5_full(tmo, ref, dev):
+    layout = W.cfg5()
+    print(f"[dequant] cfg5 sum(ctx)={layout.total_tokens}", flush=True)
+    caches = W.cfg5_fill(layout, dev)
+    _dequant_both(tmo, ref, dev, layout, caches, torch.bfloat16, 1)
+
+
+def _small_layout(seed, B=5, NB=40, BS=16, H=4, D=128, max_ctx=100):
+    g = torch.Generator().manual_seed(seed)
+    ctx = torch.randint(1, max_ctx + 1, (B,), generator=g).to(torch.int32)
+    ctx[0] = BS  # exactly one full page
+    MB = (max_ctx + BS - 1) // BS
+    bt = torch.randperm(NB, generator=g)[: B * MB].reshape(B, MB).to(torch.int32) \
+        if B * MB <= NB else torch.randint(0, NB, (B, MB), generator=g).to(torch.int32)
+    kc = torch.randint(-128, 128, (NB, H, BS, D), generator=g, dtype=torch.int8)
+    vc = torch.randint(-128, 128, (NB, H, BS, D), generator=g, dtype=torch.int8)
+    ks = torch.rand(NB, H, BS, generator=g) * 0.1
+    vs = torch.rand(NB, H, BS, generator=g) * 0.1
+    return W.DequantLayout(f"small{seed}", ctx, bt, NB, BS), (kc, vc, ks, vs)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("D,BS", [(128, 16), (64, 32), (80, 16), (128, 12)])
+def test_dequant_modes_dtypes_layouts(tmo, ref, dev, out_dtype, mode, D, BS):
+    layout, (kc, vc, ks, vs) = _small_layout(seed=D + BS + mode, D=D, BS=BS, NB=64)
+    H = kc.shape[1]
+    if mode == 0:
+        g = torch.Generator().manual_seed(99)
+        ks = torch.rand(H, D, generator=g) * 0.05
+        vs = torch.rand(H, D, generator=g) * 0.05
+    caches = tuple(t.to(dev) for t in (kc, vc, ks, vs))
+    _dequant_both(tmo, ref, dev, layout, caches, out_dtype, mode)
+    _dequant_both(tmo, ref, dev, layout, caches, out_dtype, mode, with_v=False)
+
+
+def test_dequant_seq_offset_invalid_blocks_and_extreme_scales(tmo, ref, dev):
+    layout, (kc, vc, ks, vs) = _small_layout(seed=3, B=6, NB=64)
+    bt = layout.block_tables.clone()
+    bt[2, 1] = 64        # out of range: page skipped, its rows keep the sentinel
+    bt[3, 0] = -1
+    layout = W.DequantLayout("offsets", layout.context_lengths, bt, 64)
+    ks[0, 0, 0] = 3e38   # code * scale overflows bf16 -> inf, like the oracle
+    ks[1, 1, 1] = 1e-40  # subnormal scale
+    off = torch.cumsum(layout.context_lengths, 0) - layout.context_lengths
+    off = (off.flip(0) * 0 + off).to(torch.int32) + 7  # shifted start rows
+    caches = tuple(t.to(dev) for t in (kc, vc, ks, vs))
+    _dequant_both(tmo, ref, dev, layout, caches, torch.bfloat16, 1, seq_offset=off,
+                  total=layout.total_tokens + 20)
+
+
+# ---------------------------------------------------------------------------- scaled_quantize
+
+def _sq_both(tmo, ref, dev, case: W.SmoothQuantCase, gather_start=None, smooth=True):
+    x = case.x
+    rows = case.rows
+    shape_scale = (rows,) + tuple(x.shape[1:-1])
+    out_w = torch.full((rows,) + tuple(x.shape[1:]), W.CACHE_SENTINEL, dtype=torch.int8)
+    sc_w = torch.full(shape_scale, W.SCALE_SENTINEL)
+    sm = case.smooth if smooth else None
+    ref.scaled_quantize_per_token(x, out_w, sc_w, sm, case.token_count, case.gather_index,
+                                  gather_start)
+    out_g = out_w.clone().fill_(W.CACHE_SENTINEL).to(dev)
+    sc_g = torch.full_like(sc_w, W.SCALE_SENTINEL).to(dev)
+    d = (lambda t: t.to(dev) if t is not None else None)
+    if smooth:
+        o, s = tmo.moe_quantize(x.to(dev), case.smooth.to(dev), None, d(case.token_count),
+                                d(case.gather_index), d(gather_start), out_g, sc_g)
+        assert o is out_g and s is sc_g
+    else:
+        torch.ops.torch_mlu_ops.scaled_quantize(
+            x.to(dev), out_g, sc_g, None, None, d(case.token_count), d(case.gather_index),
+            d(gather_start), None, "dynamic_per_token", "none", 1.0, False)
+    assert_bits_equal(out_g, out_w, f"{case.name} output")
+    assert_bits_equal(sc_g, sc_w, f"{case.name} output_scale")
+    return out_g, sc_g
+
+
+def test_smooth_quant_cfg4(tmo, ref, dev):
+    _sq_both(tmo, ref, dev, W.cfg4())
+
+
+def test_smooth_quant_cfg4_moe(tmo, ref, dev):
+    case = W.cfg4_moe()
+    _sq_both(tmo, ref, dev, case)
+    # gather_index_start_position: rows gather_index[start : start + sum(token_count)]
+    tc = case.token_count.clone()
+    tc[40:] = 0
+    case2 = W.SmoothQuantCase("moe-start", case.x, case.smooth, tc, case.gather_index)
+    _sq_both(tmo, ref, dev, case2, gather_start=torch.tensor([37], dtype=torch.int32))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("C", [4096, 7168, 512, 64, 16384, 100, 8])
+def test_smooth_quant_widths(tmo, ref, dev, dtype, C):
+    """Register-resident widths (1..16 vectors per lane), the generic path (C not a vector
+    multiple, or more than 16 vectors per lane), and every dtype."""
+    g = torch.Generator().manual_seed(C)
+    x = (torch.randn(37, C, generator=g) * torch.logspace(-3, 3, 37)[:, None]).to(dtype)
+    x[3] = 0
+    smooth = 0.5 + 1.5 * torch.rand(C, generator=g)
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase(f"C={C} {dtype}", x, smooth))
+
+
+def test_smooth_quant_variants(tmo, ref, dev):
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn(24, 3, 256, generator=g).to(torch.bfloat16)   # [n0, inner, C]
+    # scalar smooth, no smooth, 3-D rows
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase("3d scalar smooth", x, torch.tensor([1.75])))
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase("3d no smooth", x, torch.ones(256)), smooth=False)
+    # token_count grouping without gather, sum < rows: trailing rows untouched
+    tc = torch.tensor([5, 0, 9, 6], dtype=torch.int32)
+    sm = 0.5 + torch.rand(4, 256, generator=g)
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase("groups", x, sm, tc))
+    # gather with out-of-range entries: those rows untouched
+    gi = torch.randint(0, 24, (30,), generator=g).to(torch.int32)
+    gi[4] = 24
+    gi[9] = -2
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase("gather oob", x, torch.rand(256, generator=g) + 0.5,
+                                              None, gi))
+
+
+def test_public_wrappers(tmo, ref, dev):
+    """scaled_quantize and the per_token_smooth_quantize alias return what moe_quantize does."""
+    case = W.cfg4()
+    x = case.x[:512].to(dev)
+    sm = case.smooth.to(dev)
+    o1, s1 = tmo.moe_quantize(x, sm)
+    o2, s2 = tmo.scaled_quantize(x, sm)
+    o3, s3 = tmo.per_token_smooth_quantize(x, sm)
+    for o, s in ((o2, s2), (o3, s3)):
+        assert_bits_equal(o, o1, "output")
+        assert_bits_equal(s, s1, "scale")
+    with pytest.raises(RuntimeError):
+        tmo.scaled_quantize(x, sm, quant_mode="dynamic_per_tensor")

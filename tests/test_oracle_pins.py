@@ -1,0 +1,417 @@
+"""Pins of the CPU oracle (oracle/tmo_oracle.c) -- CPU only.
+
+The reference ships no golden vectors, fixtures or runnable implementation, so each oracle
+function is pinned by checks independent of its C code:
+
+* torch-CPU execution of the reference's docstring "Math" block (library routines: abs/amax,
+  IEEE true division, round-half-even, clamp, int8 cast, advanced indexing, bf16/fp16 casts);
+* exact rational arithmetic (fractions.Fraction) on rows engineered so that x/scale lands
+  within a few ulps of a half-integer -- this fixes "IEEE-divide then round-half-even" apart
+  from every cheaper rule (reciprocal multiply, round-half-away, bf16 scale, double rounding);
+* closed forms and invariants: hand-computed ties, zero rows, odd symmetry, power-of-two
+  scaling, the +-127 argmax code, the scale/2 error bound, sentinel bytes of skipped slots;
+* numpy's IEEE float16 casts for the oracle's fp16 conversion.
+
+A plausible mistake in the oracle (divide vs reciprocal, block/offset transposed, wrong
+rounding, smooth applied to the wrong group, off-by-one page) fails at least one of these.
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from tests import workloads as W
+
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+
+
+# ---------------------------------------------------------------------------- torch restatements
+
+def torch_row_quant(x: torch.Tensor):
+    """reference _ops.py:1524-1537 / 3167-3172 executed by torch on the CPU, fp32 (D1),
+    all-zero rows -> scale 0 / codes 0 (D3)."""
+    amax = x.abs().amax(-1)                      # max in the input dtype (exact)
+    scale = amax.to(torch.float32) / 127.0
+    q = (x.to(torch.float32) / scale[..., None]).round().clamp(-128, 127)
+    q = torch.where(scale[..., None] == 0, torch.zeros_like(q), q)
+    return q.to(torch.int8), scale
+
+
+def torch_quant_to_paged(k, v, kc, vc, ks, vs, slot):
+    NB, H, BS, D = kc.shape
+    valid = (slot >= 0) & (slot < NB * BS)
+    s = slot[valid].long()
+    blk, off = s // BS, s % BS
+    for x, c, sc in ((k, kc, ks), (v, vc, vs)):
+        if x is None:
+            continue
+        codes, scale = torch_row_quant(x[valid])
+        c.permute(0, 2, 1, 3)[blk, off] = codes        # [NB, BS, H, D] view of the pages
+        sc.permute(0, 2, 1)[blk, off] = scale
+
+
+def bits(t):
+    if t.dtype == torch.float32:
+        return t.view(torch.int32)
+    if t.dtype in (torch.float16, torch.bfloat16):
+        return t.view(torch.int16)
+    return t
+
+
+# ---------------------------------------------------------------------------- quant_to_paged_cache
+
+def _rand_case(dtype, T=64, H=4, D=128, NB=40, BS=16, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randn(T, H, D, generator=g) * torch.logspace(-4, 4, T)[:, None, None]).to(dtype)
+    v = torch.randn(T, H, D, generator=g).to(dtype)
+    k[3] = 0  # zero rows
+    slot = torch.randperm(NB * BS, generator=g)[:T].to(torch.int32)
+    slot[::7] = -1
+    slot[5] = NB * BS + 1
+    return W.PagedQuantCase("rand", k, v, slot, NB, BS)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_quant_matches_torch_docstring_math(ref, dtype):
+    for seed in range(4):
+        case = _rand_case(dtype, seed=seed)
+        kc, vc, ks, vs = case.empty_caches()
+        ref.quant_to_paged_cache(case.k, case.v, kc, vc, ks, vs, case.slot_mapping)
+        tk, tv, tks, tvs = case.empty_caches()
+        torch_quant_to_paged(case.k, case.v, tk, tv, tks, tvs, case.slot_mapping)
+        for a, b in ((kc, tk), (vc, tv), (ks, tks), (vs, tvs)):
+            assert torch.equal(bits(a), bits(b))
+
+
+def test_quant_cfg1_and_cfg2_match_torch(ref):
+    for case in (W.cfg1(), W.cfg2()):
+        kc, vc, ks, vs = case.empty_caches()
+        ref.quant_to_paged_cache(case.k, case.v, kc, vc, ks, vs, case.slot_mapping)
+        tk, tv, tks, tvs = case.empty_caches()
+        torch_quant_to_paged(case.k, case.v, tk, tv, tks, tvs, case.slot_mapping)
+        for a, b in ((kc, tk), (vc, tv), (ks, tks), (vs, tvs)):
+            assert torch.equal(bits(a), bits(b))
+        assert int((ks != W.SCALE_SENTINEL).sum()) == case.valid_tokens() * case.k.shape[1]
+
+
+def _f32_round(q: Fraction) -> Fraction:
+    """Exact round-to-nearest-even of a rational to binary32 (no overflow in this use)."""
+    if q == 0:
+        return Fraction(0)
+    sign = -1 if q < 0 else 1
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    quantum_exp = max(e - 23, -149)
+    scaled = a / Fraction(2) ** quantum_exp
+    n = scaled.numerator // scaled.denominator
+    rem = scaled - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return sign * n * Fraction(2) ** quantum_exp
+
+
+def _rne_int(q: Fraction) -> int:
+    n = q.numerator // q.denominator
+    rem = q - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return n
+
+
+def _exact_code(x: float, s: float) -> int:
+    return max(-128, min(127, _rne_int(_f32_round(Fraction(x) / Fraction(s)))))
+
+
+def _near_tie_rows(dtype, seed):
+    """Rows (amax first) whose other entries sit within a few ulps of (k + 0.5) * scale."""
+    g = torch.Generator().manual_seed(seed)
+    rows = []
+    for _ in range(6):
+        amax = torch.tensor([float(torch.rand(1, generator=g)) * 8 + 0.01]).to(dtype)
+        s = float(_f32_round(Fraction(float(amax)) / 127))
+        xs = [float(amax)]
+        for kk in torch.randint(-127, 127, (40,), generator=g).tolist():
+            t = torch.tensor([(kk + 0.5) * s], dtype=torch.float32).to(dtype)
+            for d in (-2, -1, 0, 1, 2):
+                # neighbours of t in the input format
+                bitsv = bits(t.clone()).clone()
+                bitsv += d
+                xs.append(float(bitsv.view(dtype)[0]))
+        x = torch.tensor(xs, dtype=torch.float32).to(dtype)
+        x = x[x.abs() <= amax.abs()[0].to(dtype)]
+        rows.append(x)
+    n = max(r.numel() for r in rows)
+    out = torch.zeros(len(rows), n, dtype=dtype)
+    for i, r in enumerate(rows):
+        out[i, : r.numel()] = r
+    return out
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_quant_near_ties_exact_rational(ref, dtype):
+    rows = _near_tie_rows(dtype, seed=DTYPES.index(dtype) + 17)
+    R, D = rows.shape
+    k = rows.reshape(R, 1, D).contiguous()
+    slot = torch.arange(R, dtype=torch.int32)
+    case = W.PagedQuantCase("ties", k, k, slot, (R + 15) // 16, 16)
+    kc, _, ks, _ = case.empty_caches()
+    ref.quant_to_paged_cache(k, None, kc, None, ks, None, slot)
+    n_checked = 0
+    for r in range(R):
+        x = rows[r].to(torch.float32).tolist()
+        s = float(ks[r // 16, 0, r % 16])
+        amax = max(abs(v) for v in x)
+        assert Fraction(s) == _f32_round(Fraction(amax) / 127)
+        for d, xv in enumerate(x):
+            assert int(kc[r // 16, 0, r % 16, d]) == _exact_code(xv, s), (r, d, xv, s)
+            n_checked += 1
+    assert n_checked > 1000
+
+
+def test_quant_closed_forms(ref):
+    row = torch.zeros(1, 2, 16)
+    row[0, 0, :8] = torch.tensor([127.0, 2.5, 3.5, -0.5, 1.5, -2.5, -3.5, 0.25])
+    row[0, 1, :] = 0.0                                         # all-zero row (D3)
+    for dtype in DTYPES:
+        k = row.to(dtype)
+        slot = torch.tensor([5], dtype=torch.int32)
+        case = W.PagedQuantCase("closed", k, k, slot, 1, 8)
+        kc, _, ks, _ = case.empty_caches()
+        ref.quant_to_paged_cache(k, None, kc, None, ks, None, slot)
+        assert kc[0, 0, 5, :8].tolist() == [127, 2, 4, 0, 2, -2, -4, 0]
+        assert float(ks[0, 0, 5]) == 1.0
+        assert kc[0, 1, 5].tolist() == [0] * 16 and float(ks[0, 1, 5]) == 0.0
+        # untouched slots keep the sentinel
+        assert int((kc[0, :, :5] != W.CACHE_SENTINEL).sum()) == 0
+        assert int((ks[0, :, 6:] != W.SCALE_SENTINEL).sum()) == 0
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_quant_invariants(ref, dtype):
+    g = torch.Generator().manual_seed(3)
+    T, H, D = 256, 2, 96
+    x = (torch.randn(T, H, D, generator=g) * torch.logspace(-3, 3, T)[:, None, None]).to(dtype)
+    slot = torch.arange(T, dtype=torch.int32)
+    case = W.PagedQuantCase("inv", x, x, slot, T // 16, 16)
+
+    def quant(inp):
+        kc, _, ks, _ = case.empty_caches()
+        ref.quant_to_paged_cache(inp, None, kc, None, ks, None, slot)
+        codes = kc.permute(0, 2, 1, 3).reshape(T, H, D)
+        scale = ks.permute(0, 2, 1).reshape(T, H)
+        return codes, scale
+
+    codes, scale = quant(x)
+    xf = x.to(torch.float64)
+    s = scale.to(torch.float64)
+    # |x - code * s| <= s/2 (+ the fp32 rounding of x/s)
+    err = (xf - codes.to(torch.float64) * s[..., None]).abs()
+    assert torch.all(err <= s[..., None] * (0.5 + 2.0 ** -15))
+    # the argmax element encodes to +-127; codes never exceed the symmetric range
+    am = xf.abs().argmax(-1, keepdim=True)
+    assert torch.all(codes.gather(-1, am).abs() == 127)
+    assert int(codes.min()) >= -127
+    # sign agreement
+    assert torch.all((codes.sign() == xf.sign()) | (codes == 0))
+    # odd symmetry (RNE is symmetric) and power-of-two scaling (exact in every format here)
+    c_neg, s_neg = quant(-x)
+    assert torch.equal(c_neg, -codes) and torch.equal(s_neg, scale)
+    c2, s2 = quant(x * 2)
+    assert torch.equal(c2, codes) and torch.equal(s2, scale * 2)
+
+
+def test_quant_threads_do_not_change_results(ref):
+    case = W.cfg2()
+    a = case.empty_caches()
+    b = case.empty_caches()
+    ref.quant_to_paged_cache(case.k, case.v, *a, case.slot_mapping, nthreads=1)
+    ref.quant_to_paged_cache(case.k, case.v, *b, case.slot_mapping, nthreads=8)
+    for x, y in zip(a, b):
+        assert torch.equal(bits(x), bits(y))
+
+
+# ---------------------------------------------------------------------------- reshape_paged_cache
+
+@pytest.mark.parametrize("dtype", DTYPES + [torch.int8])
+def test_reshape_matches_torch_indexing(ref, dtype):
+    g = torch.Generator().manual_seed(1)
+    T, H, D, NB, BS = 50, 3, 20, 12, 8
+    src = torch.randint(-100, 100, (T, 2 * H, D), generator=g).to(dtype)
+    k, v = src[:, :H], src[:, H:]                                  # strided views
+    slot = torch.randperm(NB * BS, generator=g)[:T].to(torch.int32)
+    slot[::5] = -1
+    slot[2] = NB * BS
+    kc = torch.full((NB, H, BS, D), 9, dtype=dtype)
+    vc = kc.clone()
+    ref.reshape_paged_cache(k, v, kc, vc, slot, False)
+    tk, tv = torch.full_like(kc, 9), torch.full_like(vc, 9)
+    valid = (slot >= 0) & (slot < NB * BS)
+    s = slot[valid].long()
+    tk.permute(0, 2, 1, 3)[s // BS, s % BS] = k[valid]
+    tv.permute(0, 2, 1, 3)[s // BS, s % BS] = v[valid]
+    assert torch.equal(bits(kc), bits(tk)) and torch.equal(bits(vc), bits(tv))
+    kb = torch.zeros_like(k)
+    ref.reshape_paged_cache(kb, None, kc, None, slot, True)
+    assert torch.equal(bits(kb)[valid], bits(k.contiguous())[valid])      # gather o scatter = id
+    assert torch.all(bits(kb)[~valid] == 0)
+
+
+# ---------------------------------------------------------------------------- dequant_from_paged_cache
+
+def torch_dequant(kc, ks, ctx, bt, mode, out_dtype, offsets):
+    """reference _ops.py:3749-3774 executed by torch (cast order of _ops.py:3677)."""
+    NB, H, BS, D = kc.shape
+    out = {}
+    for i, n in enumerate(ctx.tolist()):
+        nblk = (n + BS - 1) // BS
+        pages = bt[i, :nblk].long()
+        codes = kc[pages].permute(0, 2, 1, 3).reshape(nblk * BS, H, D)[:n]
+        if mode == 1:
+            sc = ks[pages].permute(0, 2, 1).reshape(nblk * BS, H)[:n, :, None]
+        else:
+            sc = ks[None]
+        out[int(offsets[i])] = (codes.to(torch.float32) * sc).to(out_dtype)
+    return out
+
+
+@pytest.mark.parametrize("out_dtype", DTYPES)
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("with_offsets", [False, True])
+def test_dequant_matches_torch_docstring_math(ref, out_dtype, mode, with_offsets):
+    g = torch.Generator().manual_seed(mode * 7 + int(with_offsets))
+    B, NB, H, BS, D = 5, 48, 3, 16, 32
+    ctx = torch.tensor([16, 1, 37, 80, 15], dtype=torch.int32)
+    bt = torch.randperm(NB, generator=g)[: B * 8].reshape(B, 8).to(torch.int32)
+    kc = torch.randint(-128, 128, (NB, H, BS, D), generator=g, dtype=torch.int8)
+    ks = (torch.rand(NB, H, BS, generator=g) * 0.1) if mode == 1 else \
+        (torch.rand(H, D, generator=g) * 0.1)
+    ks.view(-1)[0] = 3e36                   # products beyond fp16 / bf16 range
+    cum = torch.cumsum(ctx, 0) - ctx
+    offsets = (cum.flip(0) if with_offsets else cum).to(torch.int32)
+    if with_offsets:  # non-overlapping, shuffled starting rows
+        order = torch.tensor([4, 2, 0, 3, 1])
+        start = torch.zeros(B, dtype=torch.int64)
+        acc = 0
+        for i in order.tolist():
+            start[i] = acc
+            acc += int(ctx[i])
+        offsets = start.to(torch.int32)
+    total = int(ctx.sum())
+    got = torch.full((total, H, D), -1.0).to(out_dtype)
+    ref.dequant_from_paged_cache(got, None, kc, None, ks, None, ctx,
+                                 offsets if with_offsets else None, bt, mode)
+    want = torch_dequant(kc, ks, ctx, bt, mode, out_dtype, offsets)
+    for start, rows in want.items():
+        assert torch.equal(bits(got[start:start + rows.shape[0]]), bits(rows))
+
+
+def test_dequant_roundtrip_error_bound(ref):
+    """dequant(quant(x)) is within scale/2 (+ bf16 rounding) of x."""
+    case = W.cfg1()
+    kc, vc, ks, vs = case.empty_caches()
+    ref.quant_to_paged_cache(case.k, case.v, kc, vc, ks, vs, case.slot_mapping)
+    ctx = torch.tensor([kc.shape[0] * kc.shape[2]], dtype=torch.int32)
+    bt = torch.arange(kc.shape[0], dtype=torch.int32)[None]
+    out = torch.zeros(int(ctx), 8, 128, dtype=torch.float32)
+    ref.dequant_from_paged_cache(out, None, kc, None, ks, None, ctx, None, bt, 1)
+    s = case.slot_mapping.long()
+    scale = ks.permute(0, 2, 1).reshape(-1, 8)[s]
+    err = (out[s] - case.k.float()).abs()
+    assert torch.all(err <= scale[..., None] * (0.5 + 2.0 ** -15))
+
+
+# ---------------------------------------------------------------------------- scaled_quantize
+
+def torch_moe_quantize(x, smooth, token_count=None, gather_index=None, start=None):
+    """reference _ops.py:3147-3172 executed by torch (dynamic_quant=True, act_mode none)."""
+    inp = x
+    if gather_index is not None and start is not None:
+        inp = x[gather_index[start: start + int(token_count.sum())].long()]
+    elif gather_index is not None:
+        inp = x[gather_index.long()]
+    if token_count is not None:
+        parts = inp.split(token_count.tolist())
+        smoothed = torch.cat([parts[i] * smooth[i] for i in range(len(parts))], 0)
+    elif smooth is not None:
+        smoothed = inp * smooth
+    else:
+        smoothed = inp
+    codes, scale = torch_row_quant(smoothed.to(torch.float32))
+    return codes, scale
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_smooth_quant_matches_torch_docstring_math(ref, dtype):
+    g = torch.Generator().manual_seed(2)
+    x = (torch.randn(40, 3, 64, generator=g) * 5).to(dtype)
+    x[7] = 0
+    sm = 0.5 + 1.5 * torch.rand(64, generator=g)
+    for smooth in (sm, None, torch.tensor([1.25])):
+        out = torch.full((40, 3, 64), 9, dtype=torch.int8)
+        sc = torch.full((40, 3), -1.0)
+        ref.scaled_quantize_per_token(x, out, sc, smooth)
+        w_out, w_sc = torch_moe_quantize(x, smooth)
+        assert torch.equal(out, w_out) and torch.equal(bits(sc), bits(w_sc))
+
+
+def test_smooth_quant_moe_gather_matches_torch(ref):
+    case = W.cfg4_moe()
+    x = case.x[:512]
+    keep = case.gather_index < 512
+    gi = case.gather_index[keep]
+    experts = torch.repeat_interleave(torch.arange(64), case.token_count.long())[keep]
+    tc = torch.bincount(experts, minlength=64).to(torch.int32)
+    out = torch.empty(gi.numel(), 4096, dtype=torch.int8)
+    sc = torch.empty(gi.numel())
+    ref.scaled_quantize_per_token(x, out, sc, case.smooth, tc, gi)
+    w_out, w_sc = torch_moe_quantize(x, case.smooth, tc, gi)
+    assert torch.equal(out, w_out) and torch.equal(bits(sc), bits(w_sc))
+    # gather_index_start_position: rows gather_index[start : start + sum(token_count)]
+    tc2 = tc.clone()
+    tc2[30:] = 0
+    n = int(tc2.sum())
+    out2 = torch.full((gi.numel(), 4096), 9, dtype=torch.int8)
+    sc2 = torch.full((gi.numel(),), -1.0)
+    ref.scaled_quantize_per_token(x, out2, sc2, case.smooth, tc2, gi,
+                                  torch.tensor([11], dtype=torch.int32))
+    w_out2, w_sc2 = torch_moe_quantize(x, case.smooth, tc2, gi, 11)
+    assert torch.equal(out2[:n], w_out2) and torch.equal(bits(sc2[:n]), bits(w_sc2))
+    assert torch.all(out2[n:] == 9) and torch.all(sc2[n:] == -1.0)
+
+
+# ---------------------------------------------------------------------------- conversions
+
+def test_bf16_conversion_matches_torch(ref):
+    g = torch.Generator().manual_seed(0)
+    raw = torch.randint(-2**31, 2**31 - 1, (2_000_000,), generator=g, dtype=torch.int64)
+    f = raw.to(torch.int32).view(torch.float32)
+    f = f[~torch.isnan(f)]
+    specials = torch.tensor([0.0, -0.0, float("inf"), -float("inf"), 3.3895314e38, 1e-45,
+                             1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, 1.0 + 2 ** -9])
+    f = torch.cat([f, specials])
+    assert torch.equal(ref.f32_to_bf16_bits(f), f.to(torch.bfloat16).view(torch.int16))
+
+
+def test_f16_conversions_match_numpy(ref):
+    g = torch.Generator().manual_seed(1)
+    raw = torch.randint(-2**31, 2**31 - 1, (2_000_000,), generator=g, dtype=torch.int64)
+    f = raw.to(torch.int32).view(torch.float32)
+    f = f[~torch.isnan(f)]
+    # every fp16 value, the midpoints between neighbours and their fp32 neighbours
+    h = np.arange(0, 0x7c00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    mid = (h[:-1].astype(np.float64) + h[1:].astype(np.float64)) / 2
+    mids = mid.astype(np.float32)
+    near = np.concatenate([np.nextafter(mids, np.float32(np.inf)),
+                           np.nextafter(mids, np.float32(0)), mids, h, [65520.0, 65519.996]])
+    f = torch.cat([f, torch.from_numpy(near.astype(np.float32)),
+                   -torch.from_numpy(near.astype(np.float32))])
+    want = torch.from_numpy(f.numpy().astype(np.float16).view(np.int16))
+    assert torch.equal(ref.f32_to_f16_bits(f), want)
+    allh = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16)
+    fin = (allh.to(torch.int32) & 0x7c00) != 0x7c00
+    got = ref.f16_bits_to_f32(allh)[fin]
+    want32 = torch.from_numpy(allh.numpy().view(np.float16).astype(np.float32))[fin]
+    assert torch.equal(got.view(torch.int32), want32.view(torch.int32))

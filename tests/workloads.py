@@ -1,0 +1,215 @@
+"""Seeded synthetic inputs of the five benchmark configurations (BASELINE.json ``configs``).
+
+Shared by the parity tests and ``bench.py``.  Everything is drawn on the CPU from
+``torch.Generator().manual_seed(1000 + cfg)`` in the order written below (fp32 normals,
+rounded to bf16 with torch's round-to-nearest-even), so a GPU run and the CPU oracle see
+identical bits after a copy.  Config 5's pages are filled on the device (see ``cfg5_fill``).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+H, D, BS = 8, 128, 16
+CACHE_SENTINEL = 0x5A          # int8 pattern of never-written cache bytes
+SCALE_SENTINEL = -12345.0      # fp32 pattern of never-written scale slots
+
+
+def _gen(cfg: int) -> torch.Generator:
+    return torch.Generator().manual_seed(1000 + cfg)
+
+
+@dataclass
+class PagedQuantCase:
+    """Inputs of quant_to_paged_cache / reshape_paged_cache (CPU tensors)."""
+    name: str
+    k: torch.Tensor
+    v: torch.Tensor
+    slot_mapping: torch.Tensor
+    num_blocks: int
+    block_size: int = BS
+
+    @property
+    def tokens(self) -> int:
+        return self.k.shape[0]
+
+    def empty_caches(self, device="cpu", dtype=torch.int8):
+        shape = (self.num_blocks, self.k.shape[1], self.block_size, self.k.shape[2])
+        if dtype == torch.int8:
+            kc = torch.full(shape, CACHE_SENTINEL, dtype=torch.int8, device=device)
+        else:
+            kc = torch.full(shape, -7.0, dtype=dtype, device=device)
+        vc = kc.clone()
+        ks = torch.full(shape[:3], SCALE_SENTINEL, dtype=torch.float32, device=device)
+        vs = ks.clone()
+        return kc, vc, ks, vs
+
+    def valid_tokens(self) -> int:
+        return int((self.slot_mapping >= 0).sum())
+
+    def algorithmic_bytes(self) -> int:
+        """Bytes quant_to_paged_cache must touch once: valid K/V rows read, codes and scales
+        written, slot_mapping read."""
+        t_valid = self.valid_tokens()
+        heads, dim = self.k.shape[1], self.k.shape[2]
+        es = self.k.element_size()
+        return 2 * t_valid * heads * (dim * es + dim + 4) + 4 * self.tokens
+
+
+def cfg1() -> PagedQuantCase:
+    """16 tokens x 8 heads x 128, bf16 ~N(0,1); 64 blocks x 16; slots = randperm(1024)[:16]."""
+    g = _gen(1)
+    k = torch.randn(16, H, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(16, H, D, generator=g).to(torch.bfloat16)
+    slot = torch.randperm(64 * BS, generator=g)[:16].to(torch.int32)
+    return PagedQuantCase("cfg1", k, v, slot, 64)
+
+
+def cfg2() -> PagedQuantCase:
+    """Decode step: 256 tokens; 16384 blocks; unique random slots, 26 (10%) set to -1."""
+    g = _gen(2)
+    k = torch.randn(256, H, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(256, H, D, generator=g).to(torch.bfloat16)
+    slot = torch.randperm(16384 * BS, generator=g)[:256].to(torch.int32)
+    pad = torch.randperm(256, generator=g)[:26]
+    slot[pad] = -1
+    return PagedQuantCase("cfg2", k, v, slot, 16384)
+
+
+def cfg3() -> PagedQuantCase:
+    """Prefill chunk: 32768 tokens (8 sequences x 4096 contiguous slots at random block
+    offsets); one channel per head scaled x20 in K and V."""
+    g = _gen(3)
+    k = torch.randn(32768, H, D, generator=g)
+    v = torch.randn(32768, H, D, generator=g)
+    ch = torch.randint(0, D, (H,), generator=g)
+    for h in range(H):
+        k[:, h, ch[h]] *= 20.0
+        v[:, h, ch[h]] *= 20.0
+    k, v = k.to(torch.bfloat16), v.to(torch.bfloat16)
+    starts = 256 * torch.randperm(256, generator=g)[:8]
+    slot = torch.cat([BS * s + torch.arange(4096) for s in starts.tolist()]).to(torch.int32)
+    return PagedQuantCase("cfg3", k, v, slot, 65536)
+
+
+@dataclass
+class SmoothQuantCase:
+    name: str
+    x: torch.Tensor
+    smooth: torch.Tensor
+    token_count: Optional[torch.Tensor] = None
+    gather_index: Optional[torch.Tensor] = None
+
+    @property
+    def rows(self) -> int:
+        return self.gather_index.numel() if self.gather_index is not None else self.x.shape[0]
+
+    def algorithmic_bytes(self, per_row_reads: bool = False) -> int:
+        C = self.x.shape[-1]
+        es = self.x.element_size()
+        if self.gather_index is None:
+            reads = self.x.shape[0] * C * es
+        elif per_row_reads:
+            reads = self.rows * C * es
+        else:
+            reads = int(torch.unique(self.gather_index).numel()) * C * es
+        idx = 0
+        if self.gather_index is not None:
+            idx += 4 * self.gather_index.numel()
+        if self.token_count is not None:
+            idx += 4 * self.token_count.numel()
+        return reads + self.rows * (C + 4) + self.smooth.numel() * 4 + idx
+
+
+def _heavy_tail_x(g: torch.Generator, rows: int, C: int) -> torch.Tensor:
+    x = torch.randn(rows, C, generator=g)
+    ch = torch.randperm(C, generator=g)[: round(0.01 * C)]
+    z = torch.randn(rows, ch.numel(), generator=g)
+    chi2 = torch.randn(rows, ch.numel(), 3, generator=g).pow(2).sum(-1)
+    x[:, ch] = z / torch.sqrt(chi2 / 3.0)  # Student-t, 3 degrees of freedom
+    return x.to(torch.bfloat16)
+
+
+def cfg4() -> SmoothQuantCase:
+    """8192 x 4096 bf16 with 41 Student-t(3) channels; smooth ~ U[0.5, 2)."""
+    g = _gen(4)
+    x = _heavy_tail_x(g, 8192, 4096)
+    smooth = 0.5 + 1.5 * torch.rand(4096, generator=g)
+    return SmoothQuantCase("cfg4", x, smooth)
+
+
+def cfg4_moe() -> SmoothQuantCase:
+    """MoE variant: top-2 of 64 experts -> 16384 gathered rows sorted by expert; per-expert
+    smooth [64, 4096]."""
+    g = _gen(4)
+    x = _heavy_tail_x(g, 8192, 4096)
+    _ = torch.rand(4096, generator=g)  # the dense variant's smooth, keeps the streams aligned
+    logits = torch.randn(8192, 64, generator=g)
+    experts = logits.topk(2, dim=-1).indices.reshape(-1)          # token-major [16384]
+    order = torch.sort(experts, stable=True).indices
+    gather_index = (order // 2).to(torch.int32)                     # source token of each row
+    token_count = torch.bincount(experts, minlength=64).to(torch.int32)
+    smooth = 0.5 + 1.5 * torch.rand(64, 4096, generator=g)
+    return SmoothQuantCase("cfg4_moe", x, smooth, token_count, gather_index)
+
+
+@dataclass
+class DequantLayout:
+    """Sequences and block tables of dequant_from_paged_cache (CPU int32 tensors)."""
+    name: str
+    context_lengths: torch.Tensor
+    block_tables: torch.Tensor
+    num_blocks: int
+    block_size: int = BS
+
+    @property
+    def total_tokens(self) -> int:
+        return int(self.context_lengths.sum())
+
+    @property
+    def max_context_len(self) -> int:
+        return int(self.context_lengths.max())
+
+    def algorithmic_bytes(self, heads: int = H, dim: int = D, out_bytes: int = 2) -> int:
+        """Per token and head: K+V codes read, K+V scales read, K+V rows written; plus the
+        block-table entries and context lengths read."""
+        pages = int(((self.context_lengths + self.block_size - 1) // self.block_size).sum())
+        per_tok = 2 * heads * (dim + 4 + dim * out_bytes)
+        return self.total_tokens * per_tok + 4 * pages + 4 * self.context_lengths.numel()
+
+
+def cfg5() -> DequantLayout:
+    """64 sequences, ctx ~ U[1024, 32768]; block_tables [64, 2048] from randperm(131072)."""
+    g = _gen(5)
+    ctx = torch.randint(1024, 32769, (64,), generator=g).to(torch.int32)
+    bt = torch.randperm(131072, generator=g).to(torch.int32).reshape(64, 2048)
+    return DequantLayout("cfg5", ctx, bt, 131072)
+
+
+def cfg5_fill(layout: DequantLayout, device, seed: int = 1005, heads: int = H, dim: int = D):
+    """Int8 pages + fp32 per-token scales for every page a sequence of ``layout`` uses,
+    produced the way a serving engine fills them: config-3-style bf16 K/V (N(0,1), one x20
+    channel per head) quantised with quant_to_paged_cache on ``device``.  Generated on the
+    device (a CPU draw of ~2e9 values would dominate the run); unused pages keep the
+    sentinel.  Returns (k_cache, v_cache, k_scale, v_scale)."""
+    import domesticated_torch_mlu_ops_amd as tmo
+
+    NB, bs = layout.num_blocks, layout.block_size
+    kc = torch.full((NB, heads, bs, dim), CACHE_SENTINEL, dtype=torch.int8, device=device)
+    vc = torch.full_like(kc, CACHE_SENTINEL)
+    ks = torch.full((NB, heads, bs), SCALE_SENTINEL, dtype=torch.float32, device=device)
+    vs = torch.full_like(ks, SCALE_SENTINEL)
+    g = torch.Generator(device=device).manual_seed(seed)
+    bt = layout.block_tables.to(device)
+    ch = torch.randint(0, dim, (heads,), generator=g, device=device)
+    scale = torch.ones(heads, dim, device=device)
+    scale[torch.arange(heads, device=device), ch] = 20.0
+    for i, n in enumerate(layout.context_lengths.tolist()):
+        t = torch.arange(n, device=device)
+        slots = (bt[i, t // bs].to(torch.int64) * bs + t % bs).to(torch.int32)
+        k = (torch.randn(n, heads, dim, generator=g, device=device) * scale).to(torch.bfloat16)
+        v = (torch.randn(n, heads, dim, generator=g, device=device) * scale).to(torch.bfloat16)
+        tmo.quant_to_paged_cache(k, v, kc, vc, ks, vs, slots)
+    return kc, vc, ks, vs
