@@ -58,6 +58,9 @@ def parse_args():
     ap.add_argument("--workload", default="cfg3", choices=sorted(WORKLOADS))
     ap.add_argument("--configs", default="all", choices=["all", "headline"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile-pass", type=int, default=0, metavar="N",
+                    help="for rocprofv3 counter runs: call the selected configs' ops N times "
+                         "eagerly, then a 1 GiB elementwise copy (counter calibration), and exit")
     return ap.parse_args()
 
 
@@ -164,6 +167,44 @@ def bench_dequant(torch, tmo, W, layout, dev, steps, warmup):
     return ms, alg, total, 1
 
 
+def profile_pass(torch, tmo, W, names, dev, n: int) -> None:
+    """Eager calls of each config's op (no graph, no timing) for counter collection, then a
+    plain copy kernel of known size: torch.neg over 1 GiB of fp32 reads 1 GiB and writes 1 GiB,
+    so FETCH_SIZE / WRITE_SIZE of that dispatch calibrate the counters' units."""
+    for name in names:
+        if name in ("cfg1", "cfg2", "cfg3"):
+            case = getattr(W, name)()
+            k, v, sl = case.k.to(dev), case.v.to(dev), case.slot_mapping.to(dev)
+            kc, vc, ks, vs = case.empty_caches(device=dev)
+            fn = lambda: tmo.quant_to_paged_cache(k, v, kc, vc, ks, vs, sl)
+        elif name.startswith("cfg4"):
+            case = getattr(W, name)()
+            x, sm = case.x.to(dev), case.smooth.to(dev)
+            tc = case.token_count.to(dev) if case.token_count is not None else None
+            gi = case.gather_index.to(dev) if case.gather_index is not None else None
+            fn = lambda: tmo.moe_quantize(x, sm, None, tc, gi)
+        else:
+            layout = W.cfg5()
+            kc, vc, ks, vs = W.cfg5_fill(layout, dev)
+            key = torch.empty((layout.total_tokens, W.H, W.D), dtype=torch.bfloat16, device=dev)
+            val = torch.empty_like(key)
+            ctx, bt = layout.context_lengths.to(dev), layout.block_tables.to(dev)
+            mctx = layout.max_context_len
+            fn = lambda: tmo.dequant_from_paged_cache(key, val, kc, vc, ks, vs, ctx, mctx, None,
+                                                      bt, 1, 8)
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        print(f"# profile pass: {name} x{n}", file=sys.stderr, flush=True)
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(n):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(f"# profile pass: calibration copy (neg) of {src.numel() * 4} bytes x{n}",
+          file=sys.stderr, flush=True)
+
+
 def launch_floor_us(torch, tmo, dev) -> float:
     """Duration of the smallest quant_to_paged_cache launch (1 token, 1 head) -- the per-call
     floor that bounds the latency-bound configs."""
@@ -261,6 +302,9 @@ def main():
         ["cfg1", "cfg2", "cfg3", "cfg4", "cfg4_moe", "cfg5"]
     if args.workload not in todo:
         todo.append(args.workload)
+    if args.profile_pass:
+        profile_pass(torch, tmo, W, todo, dev, args.profile_pass)
+        return
     per = {}
     for name in todo:
         t0 = time.perf_counter()

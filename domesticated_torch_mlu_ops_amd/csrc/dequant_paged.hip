@@ -5,11 +5,14 @@
 // sibling :3677; quant_mode 0 per-channel scale [H, D], 1 per-token scale [NB, H, BS]).
 // Entry point: tmo_hip_dequant_from_paged_cache (include/tmo_hip.h).
 //
-// One workgroup per (sequence, page).  A page of one head is block_size * head_dim
-// contiguous bytes, and all heads of a block are contiguous, so the workgroup streams the
-// whole [H, BS, D] block (K and V) with 16-byte loads, every thread holding kIters units of
-// each in flight before it converts and stores 32-byte output runs.  The output rows of the
-// page's tokens are consecutive, so the stores are contiguous as well.
+// A page of one head is block_size * head_dim contiguous bytes, and all heads of a block are
+// contiguous, so a workgroup streams a whole [H, BS, D] block (K and V) with 16-byte loads,
+// every thread holding kIters units of each in flight before it converts and stores 32-byte
+// output runs.  The main (persistent) kernel walks a flat list of all pages; the per-page
+// kernel covers layouts it does not take (non power-of-two heads, very large batches), and a
+// scalar kernel covers head sizes that are not a multiple of 16.
+#include <algorithm>
+
 #include "tmo_device.h"
 
 namespace tmo {
@@ -32,8 +35,9 @@ struct DequantParams {
   int32_t heads;
   int32_t block_size;
   int32_t head_dim;
-  int32_t u_shift;   // log2(head_dim / 16)        (vector path)
-  int32_t bs_shift;  // log2(block_size)           (vector path)
+  int32_t u_shift;   // log2(head_dim / 16)        (vector paths)
+  int32_t bs_shift;  // log2(block_size)           (vector paths)
+  int32_t h_shift;   // log2(heads)                (persistent path)
   int32_t mode;      // 0 per-channel, 1 per-token
   int32_t nkv;
 };
@@ -142,6 +146,149 @@ __global__ __launch_bounds__(256) void dequant_paged_vec(DequantParams p) {
   }
 }
 
+#ifndef TMO_DEQUANT_WG_PER_CU
+#define TMO_DEQUANT_WG_PER_CU 8
+#endif
+constexpr int kPersistentMaxSeqs = 4096;
+
+// Inclusive scan of v over the 256 threads of the workgroup (4 wavefronts); `tmp` holds
+// 4 partials.  Returns the inclusive prefix; `total` receives the workgroup sum.
+template <typename T>
+__device__ __forceinline__ T block_scan(T v, T* tmp, T& total) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const T n = __shfl_up(v, o, kWave);
+    if (lane >= o) v += n;
+  }
+  if (lane == kWave - 1) tmp[wave] = v;
+  __syncthreads();
+  T before = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const T t = tmp[w];
+    if (w < wave) before += t;
+    total += t;
+  }
+  __syncthreads();
+  return v + before;
+}
+
+// Persistent vector path (heads, head_dim / 16 and block_size powers of two, batch <= 4096).
+// All pages of all sequences form one flat list, sequence-major; workgroup b takes pages
+// b, b + gridDim.x, ...  Each workgroup first scans context_lengths once into LDS: the first
+// page and first output row of every sequence.  Inside a page the lanes run d16 fastest, then
+// head, then token, so a wavefront writes one token's [H, D] output row as one contiguous
+// 2 KiB run (reads are H runs of 128 B, one per head page).
+template <class Tag, int kIters>
+__global__ __launch_bounds__(256) void dequant_paged_persistent(DequantParams p) {
+  extern __shared__ int64_t lds[];
+  int64_t* tok_start = lds;                                           // [batch]
+  int32_t* page_start = reinterpret_cast<int32_t*>(lds + p.batch);    // [batch + 1]
+  int32_t* ctx = page_start + p.batch + 1;                            // [batch]
+  __shared__ int64_t scan64[4];
+  __shared__ int32_t scan32[4];
+
+  int64_t tok_run = 0;
+  int32_t page_run = 0;
+  for (int64_t base = 0; base < p.batch; base += 256) {
+    const int64_t i = base + threadIdx.x;
+    int32_t n = i < p.batch ? p.ctx_len[i] : 0;
+    const int64_t cap = p.grid_blocks * (int64_t)p.block_size;  // tokens the launch covers
+    const int32_t covered = n <= 0 ? 0 : (int32_t)min<int64_t>(n, cap);
+    const int32_t pages = (covered + p.block_size - 1) >> p.bs_shift;
+    int64_t tot_tok;
+    int32_t tot_pages;
+    // output rows follow the plain running sum of context_lengths (reference _ops.py:3758)
+    const int64_t incl_tok = block_scan<int64_t>(n, scan64, tot_tok);
+    const int32_t incl_pages = block_scan<int32_t>(pages, scan32, tot_pages);
+    if (i < p.batch) {
+      tok_start[i] = p.seq_off ? (int64_t)p.seq_off[i] : tok_run + incl_tok - n;
+      page_start[i] = page_run + incl_pages - pages;
+      ctx[i] = covered;
+    }
+    tok_run += tot_tok;
+    page_run += tot_pages;
+  }
+  if (threadIdx.x == 0) page_start[p.batch] = page_run;
+  __syncthreads();
+  const int32_t total_pages = page_run;
+
+  const int d_shift = p.u_shift + 4;                 // log2(head_dim)
+  const int units = p.block_size << (p.h_shift + p.u_shift);
+  for (int32_t wpage = blockIdx.x; wpage < total_pages; wpage += gridDim.x) {
+    // sequence of this page: the last i with page_start[i] <= wpage
+    int32_t lo = 0, hi = (int32_t)p.batch;
+    while (hi - lo > 1) {
+      const int32_t mid = (lo + hi) >> 1;
+      if (page_start[mid] <= wpage) lo = mid; else hi = mid;
+    }
+    const int64_t i = lo;
+    const int64_t j = wpage - page_start[i];
+    const int64_t blk = p.block_tables[i * p.max_blocks + j];
+    if (blk < 0 || blk >= p.num_blocks) continue;  // workgroup-uniform
+    const int ntok = min(p.block_size, ctx[i] - (int)(j << p.bs_shift));
+    const int64_t row0 = tok_start[i] + (j << p.bs_shift);
+    const int64_t page_base = blk << (p.h_shift + p.bs_shift + d_shift);
+
+    for (int u0 = 0; u0 < units; u0 += 256 * kIters) {
+      u32x4 w[2][kIters];
+      float sc[2][kIters];
+#pragma unroll
+      for (int it = 0; it < kIters; ++it) {
+        const int u = u0 + it * 256 + threadIdx.x;
+        const int o = u >> (p.u_shift + p.h_shift);
+        if (u < units && o < ntok) {
+          const int d16 = u & ((1 << p.u_shift) - 1);
+          const int h = (u >> p.u_shift) & ((1 << p.h_shift) - 1);
+          const int64_t off = page_base + ((int64_t)((h << p.bs_shift) + o) << d_shift) + d16 * 16;
+          const int64_t srow = ((blk << p.h_shift) + h << p.bs_shift) + o;
+#pragma unroll
+          for (int kv = 0; kv < 2; ++kv) {
+            if (kv < p.nkv) {
+              w[kv][it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.cache[kv] + off));
+              if (p.mode == 1) sc[kv][it] = p.scale[kv][srow];
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < kIters; ++it) {
+        const int u = u0 + it * 256 + threadIdx.x;
+        const int o = u >> (p.u_shift + p.h_shift);
+        if (u >= units || o >= ntok) continue;
+        const int64_t row = row0 + o;
+        if (row < 0 || row >= p.total_rows) continue;
+        const int d0 = (u & ((1 << p.u_shift) - 1)) * 16;
+        const int h = (u >> p.u_shift) & ((1 << p.h_shift) - 1);
+#pragma unroll
+        for (int kv = 0; kv < 2; ++kv) {
+          if (kv >= p.nkv) continue;
+          float f[16];
+          if (p.mode == 1) {
+            const float s = sc[kv][it];
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              f[e] = (float)(int8_t)(w[kv][it][e >> 2] >> (8 * (e & 3))) * s;
+          } else {
+            const u32x4* sp =
+                reinterpret_cast<const u32x4*>(p.scale[kv] + (int64_t)h * p.head_dim + d0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const u32x4 sv = sp[q];
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                f[4 * q + e] = (float)(int8_t)(w[kv][it][q] >> (8 * e)) * __uint_as_float(sv[e]);
+            }
+          }
+          store16(Tag{}, p.out[kv], row * p.out_st[kv] + (int64_t)h * p.out_sh[kv] + d0, f);
+        }
+      }
+    }
+  }
+}
+
 // Generic path: one wavefront per (token, head) row, scalar loads and stores.
 template <class Tag>
 __global__ __launch_bounds__(256) void dequant_paged_generic(DequantParams p) {
@@ -192,6 +339,18 @@ int launch(DequantParams p, hipStream_t stream) {
   if (!vec) return launch_kernel(dequant_paged_generic<Tag>, grid, block, stream, p);
   p.u_shift = u_shift;
   p.bs_shift = bs_shift;
+  p.h_shift = ilog2_if_pow2(p.heads);
+  if (p.h_shift >= 0 && p.batch <= kPersistentMaxSeqs &&
+      ((int64_t)p.heads << (bs_shift + u_shift)) % 256 == 0) {
+    int device = 0, cus = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+      return TMO_ERR_LAUNCH;
+    const int64_t want = std::min<int64_t>(blocks, (int64_t)cus * TMO_DEQUANT_WG_PER_CU);
+    const unsigned lds = (unsigned)(p.batch * 8 + (2 * p.batch + 1) * 4);
+    return launch_kernel(dequant_paged_persistent<Tag, 4>, dim3((unsigned)want), block, stream, p,
+                         lds);
+  }
   return launch_kernel(dequant_paged_vec<Tag, 4>, grid, block, stream, p);
 }
 

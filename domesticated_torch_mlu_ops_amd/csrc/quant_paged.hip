@@ -5,10 +5,11 @@
 // Entry point: tmo_hip_quant_to_paged_cache (include/tmo_hip.h).
 //
 // Mapping (vector path): a row of head_dim elements is G = head_dim / (16 B / elem) lanes,
-// one 16-byte load per lane.  A 256-thread workgroup owns 256/G consecutive tokens of ONE
-// head, so with consecutive slots (prefill) its code stores fill whole pages contiguously
-// and its scale stores one contiguous run.  K and V of the same (token, head) are handled by
-// the same lanes, so every lane has two independent 16-byte loads in flight.  The row amax
+// one 16-byte load per lane.  A 256-thread workgroup owns consecutive tokens of ONE head, so
+// with consecutive slots (prefill) its code stores fill whole pages contiguously and its
+// scale stores one contiguous run.  K and V of the same (token, head) are handled by the same
+// lanes, and each lane group takes several tokens, so every lane has several independent
+// 16-byte loads in flight.  The row amax
 // is a DPP reduction inside the lane group; the divide is the reciprocal + two-FMA-step
 // quotient of tmo_device.h (bit-identical to IEEE division); codes and scales are written
 // with non-temporal stores (the cache is written once per step and read by other kernels).
@@ -33,9 +34,9 @@ struct QuantPagedParams {
   int32_t nkv;       // 1 (K only) or 2 (K and V)
 };
 
-__device__ __forceinline__ bool locate(const QuantPagedParams& p, int64_t t, int h,
-                                       int64_t& page_row) {
-  const int32_t slot = p.slot[t];
+// Page row of (slot, head); false for a skipped slot (negative, or past the last page).
+__device__ __forceinline__ bool locate_slot(const QuantPagedParams& p, int32_t slot, int h,
+                                            int64_t& page_row) {
   if (slot < 0 || (int64_t)slot >= p.num_slots) return false;
   int32_t blk, off;
   if (p.bs_shift >= 0) {
@@ -49,50 +50,72 @@ __device__ __forceinline__ bool locate(const QuantPagedParams& p, int64_t t, int
   return true;
 }
 
+#ifndef TMO_QUANT_TOKENS_PER_THREAD
+#define TMO_QUANT_TOKENS_PER_THREAD 2
+#endif
+constexpr int kTokensPerThread = TMO_QUANT_TOKENS_PER_THREAD;
+
 // Vector path: head_dim == G * Tag::kPerVec, 16-byte aligned rows.
+// A workgroup owns kTokensPerThread * 256/G consecutive tokens of one head; each lane group
+// handles kTokensPerThread of them.  Every load of the group (slots, K rows, V rows) is issued
+// before the first wait, so a wave spends one memory round trip, not two: the input address
+// does not depend on the slot, only the store address does.
 template <class Tag, int G>
 __global__ __launch_bounds__(256) void quant_paged_vec(QuantPagedParams p) {
-  constexpr int kRows = 256 / G;  // tokens per workgroup
+  constexpr int kGroups = 256 / G;  // lane groups per workgroup
   constexpr int kPer = Tag::kPerVec;
+  constexpr int kT = kTokensPerThread;
   const int lane = threadIdx.x & (G - 1);
   // blockIdx.x = token_tile * heads + head (workgroup-uniform, scalar ALU)
   const int h = blockIdx.x % p.heads;
   const int64_t tile = blockIdx.x / p.heads;
-  const int64_t t = tile * kRows + threadIdx.x / G;
-  if (t >= p.num_tokens) return;
-  int64_t page_row;
-  if (!locate(p, t, h, page_row)) return;  // whole lane group leaves together
+  const int64_t t0 = tile * (kGroups * kT) + threadIdx.x / G;
 
-  u32x4 w[2];
+  int32_t slot[kT];
+  u32x4 w[kT][2];
 #pragma unroll
-  for (int kv = 0; kv < 2; ++kv) {
-    if (kv < p.nkv) {
-      const char* src = static_cast<const char*>(p.src[kv]) +
-                        (t * p.stride_tok[kv] + (int64_t)h * p.stride_head[kv]) * Tag::kBytes;
-      w[kv] = *reinterpret_cast<const u32x4*>(src + lane * 16);
+  for (int j = 0; j < kT; ++j) {
+    const int64_t t = t0 + j * kGroups;
+    slot[j] = -1;
+    if (t < p.num_tokens) {
+      slot[j] = p.slot[t];
+#pragma unroll
+      for (int kv = 0; kv < 2; ++kv) {
+        if (kv < p.nkv) {
+          const char* src = static_cast<const char*>(p.src[kv]) +
+                            (t * p.stride_tok[kv] + (int64_t)h * p.stride_head[kv]) * Tag::kBytes;
+          w[j][kv] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + lane * 16));
+        }
+      }
     }
   }
 #pragma unroll
-  for (int kv = 0; kv < 2; ++kv) {
-    if (kv < p.nkv) {
-      float v[kPer];
-      unpack(Tag{}, w[kv], v);
-      float m = 0.0f;
+  for (int j = 0; j < kT; ++j) {
+    int64_t page_row;
+    if (!locate_slot(p, slot[j], h, page_row)) continue;  // uniform per lane group
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) m = abs_max(m, v[i]);
-      const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<G>(__float_as_uint(m))));
-      int8_t* dst = p.cache[kv] + page_row * p.head_dim + lane * kPer;
-      uint32_t c[kPer / 4];
-      encode_row<kPer>(v, rs, c);
-      if constexpr (kPer == 8) {
-        u32x2 c2;
-        c2[0] = c[0];
-        c2[1] = c[1];
-        __builtin_nontemporal_store(c2, reinterpret_cast<u32x2*>(dst));
-      } else {
-        __builtin_nontemporal_store(c[0], reinterpret_cast<uint32_t*>(dst));
+    for (int kv = 0; kv < 2; ++kv) {
+      if (kv < p.nkv) {
+        float v[kPer];
+        unpack(Tag{}, w[j][kv], v);
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) m = abs_max(m, v[i]);
+        const RowScale rs =
+            make_row_scale(__uint_as_float(group_max_u32<G>(__float_as_uint(m))));
+        int8_t* dst = p.cache[kv] + page_row * p.head_dim + lane * kPer;
+        uint32_t c[kPer / 4];
+        encode_row<kPer>(v, rs, c);
+        if constexpr (kPer == 8) {
+          u32x2 c2;
+          c2[0] = c[0];
+          c2[1] = c[1];
+          __builtin_nontemporal_store(c2, reinterpret_cast<u32x2*>(dst));
+        } else {
+          __builtin_nontemporal_store(c[0], reinterpret_cast<uint32_t*>(dst));
+        }
+        if (lane == 0) __builtin_nontemporal_store(rs.s, p.scale[kv] + page_row);
       }
-      if (lane == 0) __builtin_nontemporal_store(rs.s, p.scale[kv] + page_row);
     }
   }
 }
@@ -107,7 +130,7 @@ __global__ __launch_bounds__(256) void quant_paged_generic(QuantPagedParams p) {
   const int64_t t = tile * kRows + threadIdx.x / kWave;
   if (t >= p.num_tokens) return;
   int64_t page_row;
-  if (!locate(p, t, h, page_row)) return;
+  if (!locate_slot(p, p.slot[t], h, page_row)) return;
   for (int kv = 0; kv < p.nkv; ++kv) {
     const void* src = p.src[kv];
     const int64_t base = t * p.stride_tok[kv] + (int64_t)h * p.stride_head[kv];
@@ -132,7 +155,7 @@ int launch(const QuantPagedParams& p, hipStream_t stream) {
           ((p.stride_head[kv] * Tag::kBytes) % 16 == 0) &&
           (reinterpret_cast<uintptr_t>(p.cache[kv]) % 8 == 0);
   }
-  const int rows = vec ? 256 / G : 256 / kWave;
+  const int rows = vec ? (256 / G) * kTokensPerThread : 256 / kWave;
   const int64_t tiles = (p.num_tokens + rows - 1) / rows;
   const int64_t blocks = tiles * p.heads;
   if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;

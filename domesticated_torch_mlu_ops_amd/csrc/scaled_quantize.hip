@@ -35,13 +35,15 @@ struct SqParams {
 };
 
 // Group of row r: the g with prefix(g) <= r < prefix(g + 1) over token_count.  Returns
-// false when r >= sum(token_count) (or gather-start limits apply).  Wave-uniform.
-__device__ __forceinline__ bool find_group(const SqParams& p, int64_t r, int64_t& g) {
+// false when r >= sum(token_count).  Wave-uniform.  `first` is this lane's token_count entry
+// of the first 64 groups, loaded by the caller together with the row's other indices.
+__device__ __forceinline__ bool find_group(const SqParams& p, int64_t r, int32_t first,
+                                           int64_t& g) {
   const int lane = threadIdx.x & (kWave - 1);
   int64_t carry = 0, below = 0;
   for (int64_t base = 0; base < p.num_groups; base += kWave) {
     const int64_t k = base + lane;
-    int64_t c = k < p.num_groups ? (int64_t)p.token_count[k] : 0;
+    int64_t c = base == 0 ? (int64_t)first : (k < p.num_groups ? (int64_t)p.token_count[k] : 0);
     // inclusive scan across the wavefront
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
@@ -57,23 +59,23 @@ __device__ __forceinline__ bool find_group(const SqParams& p, int64_t r, int64_t
   return r < carry;
 }
 
-template <class Tag>
-__device__ __forceinline__ void load_smooth(const float* sm, int64_t smooth_len, int64_t u,
-                                            float* s) {
-  constexpr int kPer = Tag::kPerVec;
-  if (smooth_len == 1) {
-    const float v = sm[0];
-#pragma unroll
-    for (int e = 0; e < kPer; ++e) s[e] = v;
-  } else {
-    const u32x4* sp = reinterpret_cast<const u32x4*>(sm + u * kPer);
-#pragma unroll
-    for (int q = 0; q < kPer / 4; ++q) {
-      const u32x4 w = sp[q];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) s[4 * q + e] = __uint_as_float(w[e]);
-    }
+// Source row and group of output row r (both wave-uniform): the gather-index load and the
+// first token_count load are issued together.  False when the row is not produced.
+__device__ __forceinline__ bool locate_row(const SqParams& p, int64_t r, int64_t& src,
+                                           int64_t& g) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int32_t tc0 = 0;
+  if (p.token_count && lane < p.num_groups) tc0 = p.token_count[lane];
+  src = r;
+  if (p.gather_index) {
+    const int64_t gi = (p.gather_start ? (int64_t)p.gather_start[0] : 0) + r;
+    if (gi < 0 || gi >= p.gather_len) return false;
+    src = p.gather_index[gi];
   }
+  if (src < 0 || src >= p.n0) return false;
+  g = 0;
+  if (p.token_count && !find_group(p, r, tc0, g)) return false;
+  return true;
 }
 
 // Vector path: channels % kPerVec == 0, 16-byte aligned rows and smooth, and
@@ -87,27 +89,30 @@ __global__ __launch_bounds__(256) void sq_vec(SqParams p) {
   if (orow >= p.total_rows) return;
   const int64_t r = orow / p.inner;
   const int64_t jn = orow - r * p.inner;
-  int64_t g = 0;
-  if (p.token_count) {
-    if (!find_group(p, r, g)) return;
-  }
-  int64_t src = r;
-  if (p.gather_index) {
-    const int64_t gi = (p.gather_start ? (int64_t)p.gather_start[0] : 0) + r;
-    if (gi < 0 || gi >= p.gather_len) return;
-    src = p.gather_index[gi];
-  }
-  if (src < 0 || src >= p.n0) return;
+  int64_t src, g;
+  if (!locate_row(p, r, src, g)) return;
 
   const int64_t nvec = p.channels / kPer;
   const char* xrow = static_cast<const char*>(p.x) + (src * p.inner + jn) * p.row_stride * Tag::kBytes;
+  const float* sm = p.smooth ? p.smooth + (p.token_count ? g * p.smooth_len : 0) : nullptr;
+  const bool per_channel = sm && p.smooth_len != 1;
+  // Issue every load of the row -- x vectors and the matching smooth vectors -- before the
+  // first wait, so the row costs one HBM round trip plus one L2 round trip, overlapped.
   u32x4 w[kMaxV];
+  u32x4 sv[kMaxV][kPer / 4];
 #pragma unroll
   for (int i = 0; i < kMaxV; ++i) {
     const int64_t u = lane + (int64_t)i * kWave;
-    if (u < nvec) w[i] = *reinterpret_cast<const u32x4*>(xrow + u * 16);
+    if (u < nvec) {
+      w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xrow + u * 16));
+      if (per_channel) {
+        const u32x4* sp = reinterpret_cast<const u32x4*>(sm + u * kPer);
+#pragma unroll
+        for (int q = 0; q < kPer / 4; ++q) sv[i][q] = sp[q];
+      }
+    }
   }
-  const float* sm = p.smooth ? p.smooth + (p.token_count ? g * p.smooth_len : 0) : nullptr;
+  const float s_scalar = (sm && !per_channel) ? sm[0] : 1.0f;
   float v[kMaxV][kPer];
   float m = 0.0f;
 #pragma unroll
@@ -115,11 +120,12 @@ __global__ __launch_bounds__(256) void sq_vec(SqParams p) {
     const int64_t u = lane + (int64_t)i * kWave;
     if (u < nvec) {
       unpack(Tag{}, w[i], v[i]);
-      if (sm) {
-        float s[kPer];
-        load_smooth<Tag>(sm, p.smooth_len, u, s);
+      if (per_channel) {
 #pragma unroll
-        for (int e = 0; e < kPer; ++e) v[i][e] = v[i][e] * s[e];  // RN(x * smooth), no FMA
+        for (int e = 0; e < kPer; ++e) v[i][e] = v[i][e] * __uint_as_float(sv[i][e / 4][e % 4]);
+      } else if (sm) {
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) v[i][e] = v[i][e] * s_scalar;  // RN(x * smooth), no FMA
       }
 #pragma unroll
       for (int e = 0; e < kPer; ++e) m = abs_max(m, v[i][e]);
@@ -155,17 +161,8 @@ __global__ __launch_bounds__(256) void sq_generic(SqParams p) {
   if (orow >= p.total_rows) return;
   const int64_t r = orow / p.inner;
   const int64_t jn = orow - r * p.inner;
-  int64_t g = 0;
-  if (p.token_count) {
-    if (!find_group(p, r, g)) return;
-  }
-  int64_t src = r;
-  if (p.gather_index) {
-    const int64_t gi = (p.gather_start ? (int64_t)p.gather_start[0] : 0) + r;
-    if (gi < 0 || gi >= p.gather_len) return;
-    src = p.gather_index[gi];
-  }
-  if (src < 0 || src >= p.n0) return;
+  int64_t src, g;
+  if (!locate_row(p, r, src, g)) return;
   const int64_t base = (src * p.inner + jn) * p.row_stride;
   const float* sm = p.smooth ? p.smooth + (p.token_count ? g * p.smooth_len : 0) : nullptr;
   float m = 0.0f;

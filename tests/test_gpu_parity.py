@@ -239,10 +239,13 @@ def _small_layout(seed, B=5, NB=40, BS=16, H=4, D=128, max_ctx=100):
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("mode", [0, 1])
-@pytest.mark.parametrize("D,BS", [(128, 16), (64, 32), (80, 16), (128, 12)])
-def test_dequant_modes_dtypes_layouts(tmo, ref, dev, out_dtype, mode, D, BS):
-    layout, (kc, vc, ks, vs) = _small_layout(seed=D + BS + mode, D=D, BS=BS, NB=64)
-    H = kc.shape[1]
+@pytest.mark.parametrize("D,BS,H", [
+    (128, 16, 4), (64, 32, 4),   # persistent page-list kernel
+    (128, 16, 3), (64, 16, 1),   # per-page kernel (heads not a power of two / small pages)
+    (80, 16, 4), (128, 12, 4),   # scalar kernel (head size / block size off the vector path)
+])
+def test_dequant_modes_dtypes_layouts(tmo, ref, dev, out_dtype, mode, D, BS, H):
+    layout, (kc, vc, ks, vs) = _small_layout(seed=D + BS + mode + H, D=D, BS=BS, NB=64, H=H)
     if mode == 0:
         g = torch.Generator().manual_seed(99)
         ks = torch.rand(H, D, generator=g) * 0.05
@@ -250,6 +253,21 @@ def test_dequant_modes_dtypes_layouts(tmo, ref, dev, out_dtype, mode, D, BS):
     caches = tuple(t.to(dev) for t in (kc, vc, ks, vs))
     _dequant_both(tmo, ref, dev, layout, caches, out_dtype, mode)
     _dequant_both(tmo, ref, dev, layout, caches, out_dtype, mode, with_v=False)
+
+
+def test_dequant_many_sequences(tmo, ref, dev):
+    """More sequences than the persistent kernel keeps in LDS (per-page kernel), and a batch
+    just below that limit (persistent kernel), with empty and single-token sequences."""
+    for B in (4100, 3000):
+        g = torch.Generator().manual_seed(B)
+        ctx = torch.randint(0, 20, (B,), generator=g).to(torch.int32)
+        NB, H, BS, D = 2 * B, 8, 16, 128
+        bt = torch.randperm(NB, generator=g)[: 2 * B].reshape(B, 2).to(torch.int32)
+        kc = torch.randint(-128, 128, (NB, H, BS, D), generator=g, dtype=torch.int8)
+        ks = torch.rand(NB, H, BS, generator=g)
+        layout = W.DequantLayout(f"B={B}", ctx, bt, NB, BS)
+        caches = (kc.to(dev), kc.to(dev), ks.to(dev), ks.to(dev))
+        _dequant_both(tmo, ref, dev, layout, caches, torch.bfloat16, 1)
 
 
 def test_dequant_seq_offset_invalid_blocks_and_extreme_scales(tmo, ref, dev):
