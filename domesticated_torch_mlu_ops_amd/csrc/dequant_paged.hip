@@ -65,8 +65,8 @@ __device__ __forceinline__ void store16(Tag, void* base, int64_t elem, const flo
 #pragma unroll
   for (int i = 0; i < 4; ++i) b[i] = pack2(Tag{}, f[8 + 2 * i], f[8 + 2 * i + 1]);
   u32x4* dst = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + elem);
-  __builtin_nontemporal_store(a, dst);
-  __builtin_nontemporal_store(b, dst + 1);
+  dst[0] = a;  // cached stores: L2 merges the two half-sector streams of a wavefront
+  dst[1] = b;
 }
 
 __device__ __forceinline__ void store16(F32, void* base, int64_t elem, const float* f) {
@@ -76,7 +76,7 @@ __device__ __forceinline__ void store16(F32, void* base, int64_t elem, const flo
     u32x4 a;
 #pragma unroll
     for (int j = 0; j < 4; ++j) a[j] = __float_as_uint(f[4 * i + j]);
-    __builtin_nontemporal_store(a, dst + i);
+    dst[i] = a;
   }
 }
 
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(256) void dequant_paged_persistent(DequantParams p)
           const int d16 = u & ((1 << p.u_shift) - 1);
           const int h = (u >> p.u_shift) & ((1 << p.h_shift) - 1);
           const int64_t off = page_base + ((int64_t)((h << p.bs_shift) + o) << d_shift) + d16 * 16;
-          const int64_t srow = ((blk << p.h_shift) + h << p.bs_shift) + o;
+          const int64_t srow = (((blk << p.h_shift) + h) << p.bs_shift) + o;
 #pragma unroll
           for (int kv = 0; kv < 2; ++kv) {
             if (kv < p.nkv) {

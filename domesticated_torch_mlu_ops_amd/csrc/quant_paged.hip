@@ -51,16 +51,20 @@ __device__ __forceinline__ bool locate_slot(const QuantPagedParams& p, int32_t s
 }
 
 #ifndef TMO_QUANT_TOKENS_PER_THREAD
-#define TMO_QUANT_TOKENS_PER_THREAD 2
+#define TMO_QUANT_TOKENS_PER_THREAD 1
+#endif
+#ifndef TMO_QUANT_VEC_PER_LANE
+#define TMO_QUANT_VEC_PER_LANE 1
 #endif
 constexpr int kTokensPerThread = TMO_QUANT_TOKENS_PER_THREAD;
 
-// Vector path: head_dim == G * Tag::kPerVec, 16-byte aligned rows.
-// A workgroup owns kTokensPerThread * 256/G consecutive tokens of one head; each lane group
-// handles kTokensPerThread of them.  Every load of the group (slots, K rows, V rows) is issued
-// before the first wait, so a wave spends one memory round trip, not two: the input address
-// does not depend on the slot, only the store address does.
-template <class Tag, int G>
+// Vector path: head_dim == G * V * Tag::kPerVec, 16-byte aligned rows.  A row is G lanes,
+// each holding V 16-byte vectors (lane l of the group owns vectors l, l + G, ...), so the
+// per-row work -- the amax reduction, the scale and its reciprocal -- is shared by V * kPerVec
+// elements per lane.  A workgroup owns kTokensPerThread * 256/G consecutive tokens of one head.
+// Every load of the lane group (slots, K rows, V rows) is issued before the first wait: the
+// input address does not depend on the slot, only the store address does.
+template <class Tag, int G, int V>
 __global__ __launch_bounds__(256) void quant_paged_vec(QuantPagedParams p) {
   constexpr int kGroups = 256 / G;  // lane groups per workgroup
   constexpr int kPer = Tag::kPerVec;
@@ -72,7 +76,7 @@ __global__ __launch_bounds__(256) void quant_paged_vec(QuantPagedParams p) {
   const int64_t t0 = tile * (kGroups * kT) + threadIdx.x / G;
 
   int32_t slot[kT];
-  u32x4 w[kT][2];
+  u32x4 w[kT][2][V];
 #pragma unroll
   for (int j = 0; j < kT; ++j) {
     const int64_t t = t0 + j * kGroups;
@@ -84,7 +88,10 @@ __global__ __launch_bounds__(256) void quant_paged_vec(QuantPagedParams p) {
         if (kv < p.nkv) {
           const char* src = static_cast<const char*>(p.src[kv]) +
                             (t * p.stride_tok[kv] + (int64_t)h * p.stride_head[kv]) * Tag::kBytes;
-          w[j][kv] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + lane * 16));
+#pragma unroll
+          for (int i = 0; i < V; ++i)
+            w[j][kv][i] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(src + (lane + i * G) * 16));
         }
       }
     }
@@ -96,23 +103,30 @@ __global__ __launch_bounds__(256) void quant_paged_vec(QuantPagedParams p) {
 #pragma unroll
     for (int kv = 0; kv < 2; ++kv) {
       if (kv < p.nkv) {
-        float v[kPer];
-        unpack(Tag{}, w[j][kv], v);
+        float v[V][kPer];
         float m = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) m = abs_max(m, v[i]);
+        for (int i = 0; i < V; ++i) {
+          unpack(Tag{}, w[j][kv][i], v[i]);
+#pragma unroll
+          for (int e = 0; e < kPer; ++e) m = abs_max(m, v[i][e]);
+        }
         const RowScale rs =
             make_row_scale(__uint_as_float(group_max_u32<G>(__float_as_uint(m))));
-        int8_t* dst = p.cache[kv] + page_row * p.head_dim + lane * kPer;
-        uint32_t c[kPer / 4];
-        encode_row<kPer>(v, rs, c);
-        if constexpr (kPer == 8) {
-          u32x2 c2;
-          c2[0] = c[0];
-          c2[1] = c[1];
-          __builtin_nontemporal_store(c2, reinterpret_cast<u32x2*>(dst));
-        } else {
-          __builtin_nontemporal_store(c[0], reinterpret_cast<uint32_t*>(dst));
+        int8_t* row = p.cache[kv] + page_row * p.head_dim;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          int8_t* dst = row + (lane + i * G) * kPer;
+          uint32_t c[kPer / 4];
+          encode_row<kPer>(v[i], rs, c);
+          if constexpr (kPer == 8) {
+            u32x2 c2;
+            c2[0] = c[0];
+            c2[1] = c[1];
+            store_nt(reinterpret_cast<u32x2*>(dst), c2);
+          } else {
+            store_nt(reinterpret_cast<uint32_t*>(dst), c[0]);
+          }
         }
         if (lane == 0) __builtin_nontemporal_store(rs.s, p.scale[kv] + page_row);
       }
@@ -143,33 +157,42 @@ __global__ __launch_bounds__(256) void quant_paged_generic(QuantPagedParams p) {
   }
 }
 
+template <class Tag, int V>
+int launch_vec(const QuantPagedParams& p, int G, dim3 grid, dim3 block, hipStream_t stream) {
+  switch (G) {
+    case 1: return launch_kernel(quant_paged_vec<Tag, 1, V>, grid, block, stream, p);
+    case 2: return launch_kernel(quant_paged_vec<Tag, 2, V>, grid, block, stream, p);
+    case 4: return launch_kernel(quant_paged_vec<Tag, 4, V>, grid, block, stream, p);
+    case 8: return launch_kernel(quant_paged_vec<Tag, 8, V>, grid, block, stream, p);
+    case 16: return launch_kernel(quant_paged_vec<Tag, 16, V>, grid, block, stream, p);
+    case 32: return launch_kernel(quant_paged_vec<Tag, 32, V>, grid, block, stream, p);
+    default: return launch_kernel(quant_paged_vec<Tag, 64, V>, grid, block, stream, p);
+  }
+}
+
 template <class Tag>
 int launch(const QuantPagedParams& p, hipStream_t stream) {
   constexpr int kPer = Tag::kPerVec;
   bool vec = (p.head_dim % kPer) == 0;
-  const int G = vec ? p.head_dim / kPer : 0;
-  vec = vec && G >= 1 && G <= 64 && (G & (G - 1)) == 0;
+  const int nvec = vec ? p.head_dim / kPer : 0;  // 16-byte vectors per row
+  vec = vec && nvec >= 1 && nvec <= 64 * TMO_QUANT_VEC_PER_LANE && (nvec & (nvec - 1)) == 0;
   for (int kv = 0; kv < p.nkv && vec; ++kv) {
     vec = (reinterpret_cast<uintptr_t>(p.src[kv]) % 16 == 0) &&
           ((p.stride_tok[kv] * Tag::kBytes) % 16 == 0) &&
           ((p.stride_head[kv] * Tag::kBytes) % 16 == 0) &&
           (reinterpret_cast<uintptr_t>(p.cache[kv]) % 8 == 0);
   }
+  // V vectors per lane when the row has at least 4 * V of them, else one
+  const int V = (vec && nvec >= 4 * TMO_QUANT_VEC_PER_LANE) ? TMO_QUANT_VEC_PER_LANE : 1;
+  const int G = vec ? nvec / V : kWave;
   const int rows = vec ? (256 / G) * kTokensPerThread : 256 / kWave;
   const int64_t tiles = (p.num_tokens + rows - 1) / rows;
   const int64_t blocks = tiles * p.heads;
   if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
   const dim3 grid((unsigned)blocks), block(256);
   if (!vec) return launch_kernel(quant_paged_generic<Tag>, grid, block, stream, p);
-  switch (G) {
-    case 1: return launch_kernel(quant_paged_vec<Tag, 1>, grid, block, stream, p);
-    case 2: return launch_kernel(quant_paged_vec<Tag, 2>, grid, block, stream, p);
-    case 4: return launch_kernel(quant_paged_vec<Tag, 4>, grid, block, stream, p);
-    case 8: return launch_kernel(quant_paged_vec<Tag, 8>, grid, block, stream, p);
-    case 16: return launch_kernel(quant_paged_vec<Tag, 16>, grid, block, stream, p);
-    case 32: return launch_kernel(quant_paged_vec<Tag, 32>, grid, block, stream, p);
-    default: return launch_kernel(quant_paged_vec<Tag, 64>, grid, block, stream, p);
-  }
+  if (V == 1) return launch_vec<Tag, 1>(p, G, grid, block, stream);
+  return launch_vec<Tag, TMO_QUANT_VEC_PER_LANE>(p, G, grid, block, stream);
 }
 
 }  // namespace

@@ -79,8 +79,10 @@ __device__ __forceinline__ bool locate_row(const SqParams& p, int64_t r, int64_t
 }
 
 // Vector path: channels % kPerVec == 0, 16-byte aligned rows and smooth, and
-// channels / kPerVec <= 64 * kMaxV.
-template <class Tag, int kMaxV>
+// channels / kPerVec <= 64 * kMaxV.  kStream: the rows are read exactly once (no gather), so
+// they are loaded non-temporally; a gathered row may be read again for another output row
+// (MoE top-k), and then the cached load lets the repeat hit L2 / MALL.
+template <class Tag, int kMaxV, bool kStream>
 __global__ __launch_bounds__(256) void sq_vec(SqParams p) {
   constexpr int kPer = Tag::kPerVec;
   const int lane = threadIdx.x & (kWave - 1);
@@ -104,7 +106,12 @@ __global__ __launch_bounds__(256) void sq_vec(SqParams p) {
   for (int i = 0; i < kMaxV; ++i) {
     const int64_t u = lane + (int64_t)i * kWave;
     if (u < nvec) {
-      w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xrow + u * 16));
+      const u32x4* xp = reinterpret_cast<const u32x4*>(xrow + u * 16);
+      if constexpr (kStream) {
+        w[i] = __builtin_nontemporal_load(xp);
+      } else {
+        w[i] = *xp;
+      }
       if (per_channel) {
         const u32x4* sp = reinterpret_cast<const u32x4*>(sm + u * kPer);
 #pragma unroll
@@ -143,9 +150,9 @@ __global__ __launch_bounds__(256) void sq_vec(SqParams p) {
         u32x2 c2;
         c2[0] = c[0];
         c2[1] = c[1];
-        __builtin_nontemporal_store(c2, reinterpret_cast<u32x2*>(orow_ptr + u * 8));
+        store_nt(reinterpret_cast<u32x2*>(orow_ptr + u * 8), c2);
       } else {
-        __builtin_nontemporal_store(c[0], reinterpret_cast<uint32_t*>(orow_ptr + u * 4));
+        store_nt(reinterpret_cast<uint32_t*>(orow_ptr + u * 4), c[0]);
       }
     }
   }
@@ -181,6 +188,15 @@ __global__ __launch_bounds__(256) void sq_generic(SqParams p) {
   if (lane == 0) p.out_scale[orow] = rs.s;
 }
 
+template <class Tag, bool kStream>
+int launch_vec(const SqParams& p, int64_t per_lane, dim3 grid, dim3 block, hipStream_t stream) {
+  if (per_lane <= 1) return launch_kernel(sq_vec<Tag, 1, kStream>, grid, block, stream, p);
+  if (per_lane <= 2) return launch_kernel(sq_vec<Tag, 2, kStream>, grid, block, stream, p);
+  if (per_lane <= 4) return launch_kernel(sq_vec<Tag, 4, kStream>, grid, block, stream, p);
+  if (per_lane <= 8) return launch_kernel(sq_vec<Tag, 8, kStream>, grid, block, stream, p);
+  return launch_kernel(sq_vec<Tag, 16, kStream>, grid, block, stream, p);
+}
+
 template <class Tag>
 int launch(const SqParams& p, hipStream_t stream) {
   constexpr int kPer = Tag::kPerVec;
@@ -193,11 +209,8 @@ int launch(const SqParams& p, hipStream_t stream) {
       (!p.smooth || p.smooth_len == 1 || reinterpret_cast<uintptr_t>(p.smooth) % 16 == 0);
   const int64_t per_lane = (p.channels / kPer + kWave - 1) / kWave;
   if (!aligned || per_lane > 16) return launch_kernel(sq_generic<Tag>, grid, block, stream, p);
-  if (per_lane <= 1) return launch_kernel(sq_vec<Tag, 1>, grid, block, stream, p);
-  if (per_lane <= 2) return launch_kernel(sq_vec<Tag, 2>, grid, block, stream, p);
-  if (per_lane <= 4) return launch_kernel(sq_vec<Tag, 4>, grid, block, stream, p);
-  if (per_lane <= 8) return launch_kernel(sq_vec<Tag, 8>, grid, block, stream, p);
-  return launch_kernel(sq_vec<Tag, 16>, grid, block, stream, p);
+  if (p.gather_index) return launch_vec<Tag, false>(p, per_lane, grid, block, stream);
+  return launch_vec<Tag, true>(p, per_lane, grid, block, stream);
 }
 
 }  // namespace

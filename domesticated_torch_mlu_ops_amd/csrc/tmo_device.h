@@ -160,6 +160,12 @@ __device__ __forceinline__ uint32_t code_bits(float q) {
   return __float_as_uint(q + 12582912.0f);
 }
 
+// Placed in the rarely-taken IEEE-divide branch.  The IR cost model counts an fdiv as one
+// instruction, so without a side effect in the branch the optimiser speculates it and every
+// lane computes both quotients (an IEEE divide is ~10 VALU ops) and selects -- which more
+// than doubled the quantiser's VALU work in some instantiations.
+__device__ __forceinline__ void keep_branch() { asm volatile(""); }
+
 // Per-row quantisation state: the scale and, on the fast path, its reciprocal.
 struct RowScale {
   float s;     // fp32(amax) / 127
@@ -201,6 +207,7 @@ __device__ __forceinline__ void encode_row(const float* v, const RowScale& r, ui
 #pragma unroll
     for (int i = 0; i < N; ++i) q[i] = div_by_recip(v[i], r.s, r.y);
   } else {
+    keep_branch();
 #pragma unroll
     for (int i = 0; i < N; ++i) q[i] = v[i] / r.s;  // IEEE divide (tiny or non-finite scale)
   }
@@ -211,8 +218,29 @@ __device__ __forceinline__ void encode_row(const float* v, const RowScale& r, ui
 }
 
 __device__ __forceinline__ int8_t encode1(float v, const RowScale& r) {
-  const float q = r.fast ? div_by_recip(v, r.s, r.y) : v / r.s;
+  float q;
+  if (r.fast) {
+    q = div_by_recip(v, r.s, r.y);
+  } else {
+    keep_branch();
+    q = v / r.s;
+  }
   return (int8_t)(uint8_t)(code_bits(q) & 0xffu);
+}
+
+// ---------------------------------------------------------------------------- stores
+
+// Non-temporal 4- and 8-byte vector stores of int8 codes.  __builtin_nontemporal_store carries
+// the hint as IR metadata, and an IR pass drops it when it merges the two 32-bit halves of a
+// code vector in some instantiations (the 16-lane, one-vector-per-lane quantiser lost it and
+// ran ~30% slower on scattered page writes), so these emit the `nt` store form directly.
+// They are plain vector-memory stores; the compiler's waitcnt bookkeeping only ever
+// over-waits around them, and the kernels issue no loads after their stores.
+__device__ __forceinline__ void store_nt(uint32_t* p, uint32_t v) {
+  asm volatile("global_store_dword %0, %1, off nt" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_nt(u32x2* p, u32x2 v) {
+  asm volatile("global_store_dwordx2 %0, %1, off nt" : : "v"(p), "v"(v) : "memory");
 }
 
 // ---------------------------------------------------------------------------- misc
