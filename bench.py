@@ -45,9 +45,9 @@ WORKLOADS = {
     "cfg4_moe": "configs[3] MoE: per_token_smooth_quantize over 16384 gathered rows (top-2 of 64 experts), per-expert smooth",
     "cfg5": "configs[4]: dequant_from_paged_cache, 64 seqs ctx ~U[1024,32768], 8 KV heads x 128, int8 pages -> bf16",
 }
-KERNELS = {"cfg1": "quant_paged_vec<BF16,16>", "cfg2": "quant_paged_vec<BF16,16>",
-           "cfg3": "quant_paged_vec<BF16,16>", "cfg4": "sq_vec<BF16,8>",
-           "cfg4_moe": "sq_vec<BF16,8>", "cfg5": "dequant_paged_vec<BF16,4>"}
+KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1>", "cfg2": "quant_paged_vec<BF16,16,1>",
+           "cfg3": "quant_paged_vec<BF16,16,1>", "cfg4": "sq_vec<BF16,8,true>",
+           "cfg4_moe": "sq_vec<BF16,8,false>", "cfg5": "dequant_paged_persistent<BF16,8>"}
 
 
 def parse_args():
@@ -205,6 +205,15 @@ def profile_pass(torch, tmo, W, names, dev, n: int) -> None:
           file=sys.stderr, flush=True)
 
 
+def copy_ceiling_gbs(torch, dev) -> float:
+    """A plain torch copy-class kernel (neg over 1 GiB fp32: 1 GiB read + 1 GiB written) on the
+    same device: the practical streaming rate the path's kernels can be compared against."""
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    ms = time_graph(torch, [lambda: torch.neg(src, out=dst)], 20, 4)
+    return 2 * src.numel() * 4 / (ms * 1e-3) / 1e9
+
+
 def launch_floor_us(torch, tmo, dev) -> float:
     """Duration of the smallest quant_to_paged_cache launch (1 token, 1 head) -- the per-call
     floor that bounds the latency-bound configs."""
@@ -326,6 +335,7 @@ def main():
               f"peak)  [{time.perf_counter() - t0:.1f} s]", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
     floor = launch_floor_us(torch, tmo, dev) if args.configs == "all" else None
+    ceiling = copy_ceiling_gbs(torch, dev) if args.configs == "all" else None
 
     head = per[args.workload]
     traffic = None
@@ -357,6 +367,7 @@ def main():
         "cpu_baseline": cpu,
         "per_config": per,
         "launch_floor_us": round(floor, 3) if floor is not None else None,
+        "copy_ceiling_GB_s": round(ceiling, 1) if ceiling is not None else None,
     }
     print(json.dumps(line), flush=True)
 
