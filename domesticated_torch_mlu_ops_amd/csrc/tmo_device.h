@@ -155,9 +155,9 @@ __host__ __device__ __forceinline__ float div_by_recip(float x, float s, float y
 // even by adding 1.5*2^23 (the sum's ulp is 1, so the hardware RNE add performs the
 // rounding, and the low byte of its bit pattern is the two's-complement code).  Returns the
 // code in bits 0..7 of the result (upper bits are garbage).
+__device__ __forceinline__ uint32_t rne_bits(float q) { return __float_as_uint(q + 12582912.0f); }
 __device__ __forceinline__ uint32_t code_bits(float q) {
-  q = __builtin_amdgcn_fmed3f(q, -128.0f, 127.0f);
-  return __float_as_uint(q + 12582912.0f);
+  return rne_bits(__builtin_amdgcn_fmed3f(q, -128.0f, 127.0f));
 }
 
 // Placed in the rarely-taken IEEE-divide branch.  The IR cost model counts an fdiv as one
@@ -173,9 +173,27 @@ struct RowScale {
   bool fast;   // kFastDivMinScale <= s < inf, or s == 0
 };
 
+// RN(amax / 127) without a divide: q0 = amax * RN(1/127) is within ~1 ulp, and one FMA
+// correction with the constant reciprocal (Markstein) rounds it correctly.
+// tests/native/div_exhaustive.hip checks it against IEEE division for every fp32 amax from
+// 2^-100 to the largest finite value; below 2^-100 the correction's residual can be
+// inexact, and the IEEE divide is used.
+constexpr float kInv127 = 1.0f / 127.0f;
+constexpr float kScaleDivMin = 7.88860905e-31f;  // 2^-100
+__host__ __device__ __forceinline__ float scale_of(float amax) {
+  const float q0 = amax * kInv127;
+  const float r = __builtin_fmaf(-127.0f, q0, amax);
+  return __builtin_fmaf(r, kInv127, q0);
+}
+
 __device__ __forceinline__ RowScale make_row_scale(float amax) {
   RowScale r;
-  r.s = amax / 127.0f;  // IEEE divide (hipcc default: correctly rounded fp32 division)
+  if (amax >= kScaleDivMin && amax < __builtin_inff()) {
+    r.s = scale_of(amax);
+  } else {
+    keep_branch();
+    r.s = amax / 127.0f;  // IEEE divide (hipcc default: correctly rounded fp32 division)
+  }
   if (r.s >= kFastDivMinScale && r.s < __builtin_inff()) {
     r.fast = true;
     r.y = 1.0f / r.s;
@@ -211,10 +229,19 @@ __device__ __forceinline__ void encode_row(const float* v, const RowScale& r, ui
 #pragma unroll
     for (int i = 0; i < N; ++i) q[i] = v[i] / r.s;  // IEEE divide (tiny or non-finite scale)
   }
+  if (r.fast) {
+    // |x| <= amax and s = RN(amax / 127) bound |q| by 127 * (1 + 2^-23), so the clamp of the
+    // reference math cannot fire here and the round-half-even add alone gives the code.
 #pragma unroll
-  for (int i = 0; i < N / 4; ++i)
-    out[i] = pack_codes(code_bits(q[4 * i]), code_bits(q[4 * i + 1]), code_bits(q[4 * i + 2]),
-                        code_bits(q[4 * i + 3]));
+    for (int i = 0; i < N / 4; ++i)
+      out[i] = pack_codes(rne_bits(q[4 * i]), rne_bits(q[4 * i + 1]), rne_bits(q[4 * i + 2]),
+                          rne_bits(q[4 * i + 3]));
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i)
+      out[i] = pack_codes(code_bits(q[4 * i]), code_bits(q[4 * i + 1]), code_bits(q[4 * i + 2]),
+                          code_bits(q[4 * i + 3]));
+  }
 }
 
 __device__ __forceinline__ int8_t encode1(float v, const RowScale& r) {

@@ -6,6 +6,8 @@
 //   f16  : the same over all finite fp16 values.
 //   f32  : random fp32 (amax, x) pairs over the fast-path exponent range plus, for each
 //          scale, inputs within +-3 ulps of (k + 0.5) * scale for every k in [-127, 127].
+//   scale: the divide-free row scale (scale_of) against IEEE amax / 127 for EVERY fp32 amax
+//          the kernels send through it (2^-100 up to the largest finite value).
 //
 // Two properties are checked on every pair:
 //   * the int8 code (clamp to [-128, 127], round half to even) of the kernel quotient equals
@@ -131,6 +133,32 @@ static Count run_f32(unsigned long long n, int nthreads) {
   return total;
 }
 
+static Count run_scale(int nthreads) {
+  std::vector<Count> per(nthreads);
+  std::vector<std::thread> th;
+  const uint32_t lo = bits_of(tmo::kScaleDivMin), hi = 0x7f7fffffu;
+  for (int t = 0; t < nthreads; ++t)
+    th.emplace_back([&, t] {
+      Count& c = per[t];
+      for (uint32_t b = lo + t; b <= hi; b += nthreads) {
+        const float amax = f_from_bits(b);
+        const float s = tmo::scale_of(amax), r = amax / 127.0f;
+        ++c.checked;
+        if (bits_of(s) != bits_of(r)) {
+          if (c.bad < 5) std::printf("scale mismatch amax=%a fast=%a ieee=%a\n", amax, s, r);
+          ++c.bad;
+        }
+      }
+    });
+  for (auto& x : th) x.join();
+  Count total;
+  for (auto& p : per) {
+    total.bad += p.bad;
+    total.checked += p.checked;
+  }
+  return total;
+}
+
 int main(int argc, char** argv) {
   const char* mode = argc > 1 ? argv[1] : "bf16";
   const int nthreads = argc > 2 ? std::atoi(argv[2]) : 8;
@@ -139,6 +167,8 @@ int main(int argc, char** argv) {
     c = run_format(0x7f7fu, bf16, nthreads);
   } else if (!std::strcmp(mode, "f16")) {
     c = run_format(0x7bffu, f16, nthreads);
+  } else if (!std::strcmp(mode, "scale")) {
+    c = run_scale(nthreads);
   } else {
     const unsigned long long n = argc > 3 ? std::strtoull(argv[3], nullptr, 10) : 20000000ull;
     c = run_f32(n, nthreads);

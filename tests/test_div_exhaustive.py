@@ -1,7 +1,9 @@
 """The kernels' int8 encoder divides through a reciprocal plus two FMA correction steps
-(tmo_device.h: div_by_recip).  This CPU test compiles that same source for the host and
-checks it against IEEE fp32 division on every bf16 and every fp16 (amax, x) pair and on
-random and near-tie fp32 pairs (tests/native/div_exhaustive.hip)."""
+(tmo_device.h: div_by_recip) and computes the row scale amax / 127 with a constant-reciprocal
+correction (scale_of).  This CPU test compiles that same source for the host and checks both
+against IEEE fp32 division: the quotient on every bf16 and every fp16 (amax, x) pair and on
+random and near-tie fp32 pairs, the scale on every fp32 amax it is used for
+(tests/native/div_exhaustive.hip)."""
 import os
 import subprocess
 from pathlib import Path
@@ -26,7 +28,8 @@ def binary(tmp_path_factory):
     return out
 
 
-@pytest.mark.parametrize("mode,extra", [("bf16", []), ("f16", []), ("f32", ["20000000"])])
+@pytest.mark.parametrize("mode,extra", [("bf16", []), ("f16", []), ("f32", ["20000000"]),
+                                        ("scale", [])])
 def test_reciprocal_quotient_matches_ieee(binary, mode, extra):
     threads = str(max(1, min(8, len(os.sched_getaffinity(0)))))
     res = subprocess.run([str(binary), mode, threads, *extra], capture_output=True, text=True,
