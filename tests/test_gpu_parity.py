@@ -338,6 +338,24 @@ def test_smooth_quant_widths(tmo, ref, dev, dtype, C):
     _sq_both(tmo, ref, dev, W.SmoothQuantCase(f"C={C} {dtype}", x, smooth))
 
 
+@pytest.mark.parametrize("dtype,C,smooth", [
+    (torch.bfloat16, 512, "channel"), (torch.bfloat16, 4096, "channel"),
+    (torch.float16, 1024, "scalar"), (torch.float32, 1024, "none"), (torch.bfloat16, 2048, "none"),
+])
+def test_smooth_quant_many_rows_per_wavefront(tmo, ref, dev, dtype, C, smooth):
+    """Large dense row counts that are not a multiple of any launch width (10573 and 4141 rows),
+    with zero rows in the middle and at the very end, per-channel, scalar and no smooth."""
+    g = torch.Generator().manual_seed(C + 7)
+    rows = 2048 * 5 + 333 if C <= 2048 else 2048 * 2 + 45
+    x = (torch.randn(rows, C, generator=g) * torch.logspace(-2, 2, rows)[:, None]).to(dtype)
+    x[rows - 1] = 0
+    x[17] = 0
+    sm = {"channel": 0.5 + 1.5 * torch.rand(C, generator=g), "scalar": torch.tensor([0.625]),
+          "none": torch.ones(C)}[smooth]
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase(f"{rows}x{C} {dtype} {smooth}", x, sm),
+             smooth=smooth != "none")
+
+
 def test_smooth_quant_variants(tmo, ref, dev):
     g = torch.Generator().manual_seed(42)
     x = torch.randn(24, 3, 256, generator=g).to(torch.bfloat16)   # [n0, inner, C]
