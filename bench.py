@@ -49,8 +49,8 @@ WORKLOADS = {
     "cfg5": "configs[4]: dequant_from_paged_cache, 64 seqs ctx ~U[1024,32768], 8 KV heads x 128, int8 pages -> bf16",
 }
 KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1>", "cfg2": "quant_paged_vec<BF16,16,1>",
-           "cfg3": "quant_paged_vec<BF16,16,1>", "cfg4": "sq_vec<BF16,8,true>",
-           "cfg4_moe": "sq_vec<BF16,8,false>", "cfg5": "dequant_paged_persistent<BF16,8>"}
+           "cfg3": "quant_paged_vec<BF16,16,1>", "cfg4": "sq_vec<BF16,8,true,1>",
+           "cfg4_moe": "sq_vec<BF16,8,false,1>", "cfg5": "dequant_paged_persistent<BF16,8>"}
 
 
 def parse_args():
