@@ -32,7 +32,7 @@ def load_native() -> None:
         raise ImportError(
             "domesticated_torch_mlu_ops_amd: native library not built: "
             + ", ".join(str(p) for p in missing)
-            + "  (run `python -m domesticated_torch_mlu_ops_amd._build` or "
+            + "  (run `python domesticated_torch_mlu_ops_amd/_build.py` or "
             "`python -c 'import __graft_entry__ as g; g.build()'` from the repository root)")
     torch.ops.load_library(str(TORCH_EXT_PATH))
     _loaded = True

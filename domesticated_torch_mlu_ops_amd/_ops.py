@@ -14,6 +14,7 @@ import torch
 __all__ = [
     "reshape_paged_cache",
     "quant_to_paged_cache",
+    "offline_quant_to_paged_cache",
     "dequant_from_paged_cache",
     "moe_quantize",
     "scaled_quantize",
@@ -68,6 +69,37 @@ def quant_to_paged_cache(
     if v_cache is not None:
         return (k_cache, v_cache, k_cache_quant_scale, v_cache_quant_scale)
     return (k_cache, k_cache_quant_scale)
+
+
+def offline_quant_to_paged_cache(
+    k: torch.Tensor,
+    v: Optional[torch.Tensor],
+    k_cache_scale: Union[torch.Tensor, float],
+    v_cache_scale: Optional[Union[torch.Tensor, float]],
+    slot_mapping: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: Optional[torch.Tensor],
+) -> Union[Tuple[torch.Tensor], torch.Tensor]:
+    """Static quantisation of k/v into the paged caches with calibrated scales.
+
+    For each token ``i`` with ``slot_mapping[i] >= 0``: ``q = fp32(k[i]) / k_cache_scale``
+    (IEEE divide; a ``[heads, head_size]`` float32 tensor scales per channel, a number per
+    tensor); an int8 cache stores ``clip(round_half_even(q), -128, 127)``, a
+    ``torch.float8_e4m3fn`` cache stores ``clip(q, -448, 448)`` rounded to nearest even, at
+    ``k_cache[slot // bs, :, slot % bs, :]`` (same for v).  No scales are written.
+
+    Reference: ``_ops.py:1639-1706`` (math ``:1652-1670``; the division is the linear
+    sibling's ``key_i /= scale``, ``:1829-1840``).  Returns ``(k_cache, v_cache)`` or
+    ``k_cache``.
+    """
+    if torch.is_tensor(k_cache_scale):
+        torch.ops.torch_mlu_ops.offline_quant_to_paged_cache(
+            k, v, k_cache_scale, v_cache_scale, slot_mapping, k_cache, v_cache, 1.0, 1.0)
+    else:
+        torch.ops.torch_mlu_ops.offline_quant_to_paged_cache(
+            k, v, None, None, slot_mapping, k_cache, v_cache, k_cache_scale,
+            v_cache_scale if v_cache_scale is not None else 1.0)
+    return (k_cache, v_cache) if v_cache is not None else k_cache
 
 
 def dequant_from_paged_cache(

@@ -32,6 +32,17 @@ def quant_to_paged_cache_abstract(k: Tensor, v: Optional[Tensor], k_cache: Tenso
     return None
 
 
+@torch.library.register_fake("torch_mlu_ops::offline_quant_to_paged_cache")
+def offline_quant_to_paged_cache_abstract(k: Tensor, v: Optional[Tensor],
+                                          k_cache_scale_per_channel: Optional[Tensor],
+                                          v_cache_scale_per_channel: Optional[Tensor],
+                                          slot_mapping: Tensor, k_cache: Tensor,
+                                          v_cache: Optional[Tensor],
+                                          k_cache_scale_per_tensor: float,
+                                          v_cache_scale_per_tensor: float) -> None:
+    return None
+
+
 @torch.library.register_fake("torch_mlu_ops::dequant_from_paged_cache")
 def dequant_from_paged_cache_abstract(key: Tensor, value: Optional[Tensor], key_cache: Tensor,
                                       value_cache: Optional[Tensor],

@@ -4,6 +4,10 @@
 // Semantics: reference _ops.py:1511-1565 (math block :1524-1537, slot convention :1262-1268).
 // Entry point: tmo_hip_quant_to_paged_cache (include/tmo_hip.h).
 //
+// Also offline_quant_to_paged_cache (reference _ops.py:1639-1706): the same pages written
+// with static per-channel or per-tensor scales into an int8 or float8_e4m3fn cache
+// (tmo_hip_offline_quant_to_paged_cache), on the same token/head mapping.
+//
 // Mapping (vector path): a row of head_dim elements is G = head_dim / (16 B / elem) lanes,
 // one 16-byte load per lane.  A 256-thread workgroup owns consecutive tokens of ONE head, so
 // with consecutive slots (prefill) its code stores fill whole pages contiguously and its
@@ -157,6 +161,193 @@ __global__ __launch_bounds__(256) void quant_paged_generic(QuantPagedParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------- static scales
+
+struct StaticScales {
+  const float* chan[2];  // [heads, head_dim] fp32 per-channel scales, or null: per tensor
+  float tensor[2];
+};
+struct StaticParams {
+  QuantPagedParams q;
+  StaticScales sc;
+};
+
+#ifndef TMO_STATIC_TOKENS_PER_THREAD
+#define TMO_STATIC_TOKENS_PER_THREAD 4
+#endif
+
+// Bytes of N quotients, packed 4 per u32: int8 codes (clamp, round half even) or
+// float8_e4m3fn (clamp to +-448, round to nearest even).
+template <int N, bool kFp8>
+__device__ __forceinline__ void encode_static(const float* q, uint32_t* out) {
+  uint32_t b[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    b[i] = kFp8 ? fp8e4m3_bits(__builtin_amdgcn_fmed3f(q[i], -448.0f, 448.0f)) : code_bits(q[i]);
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) out[i] = pack_codes(b[4 * i], b[4 * i + 1], b[4 * i + 2], b[4 * i + 3]);
+}
+
+// Vector path of the static quantiser: one 16-byte vector per lane, G lanes per row (as the
+// dynamic kernel with V = 1), a workgroup owns kT * 256/G consecutive tokens of one head.  A
+// lane always covers the same kPerVec channels of its head, so it loads their scales once
+// (before the rows, so that waiting for them does not wait for the rows) and computes the
+// reciprocals once for its kT tokens.  There is no row reduction and no scale store.
+template <class Tag, int G, bool kFp8>
+__global__ __launch_bounds__(256) void quant_paged_static_vec(StaticParams sp) {
+  const QuantPagedParams& p = sp.q;
+  const StaticScales& sc = sp.sc;
+  constexpr int kGroups = 256 / G;
+  constexpr int kPer = Tag::kPerVec;
+  constexpr int kT = TMO_STATIC_TOKENS_PER_THREAD;
+  const int lane = threadIdx.x & (G - 1);
+  const int h = blockIdx.x % p.heads;
+  const int64_t tile = blockIdx.x / p.heads;
+  const int64_t t0 = tile * (kGroups * kT) + threadIdx.x / G;
+
+  float s[2][kPer];
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    if (kv < p.nkv) {
+      if (sc.chan[kv]) {
+        const u32x4* sp = reinterpret_cast<const u32x4*>(sc.chan[kv] + (int64_t)h * p.head_dim +
+                                                         lane * kPer);
+#pragma unroll
+        for (int q = 0; q < kPer / 4; ++q) {
+          const u32x4 t = sp[q];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) s[kv][4 * q + i] = __uint_as_float(t[i]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) s[kv][e] = sc.tensor[kv];
+      }
+    }
+  }
+  // Tokens past the end load the last token's row again (an L2 hit) and are skipped below:
+  // every load is unconditional, so the waits before the first row count exactly.
+  int32_t slot[kT];
+  u32x4 w[kT][2];
+#pragma unroll
+  for (int j = 0; j < kT; ++j) {
+    const int64_t t = t0 + j * kGroups;
+    const int64_t tc = t < p.num_tokens ? t : p.num_tokens - 1;
+    slot[j] = p.slot[tc];
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      if (kv < p.nkv) {
+        const char* src = static_cast<const char*>(p.src[kv]) +
+                          (tc * p.stride_tok[kv] + (int64_t)h * p.stride_head[kv]) * Tag::kBytes;
+        w[j][kv] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + lane * 16));
+      }
+    }
+    if (t >= p.num_tokens) slot[j] = -1;
+  }
+  float y[2][kPer];
+  bool fast[2];
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    if (kv < p.nkv) {
+      fast[kv] = true;
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) fast[kv] &= static_scale_fast(s[kv][e]);  // no short circuit
+      if (!fast[kv]) {
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) y[kv][e] = 0.0f;
+      } else if (sc.chan[kv]) {
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) y[kv][e] = 1.0f / s[kv][e];  // IEEE: RN(1 / s)
+      } else {
+        const float y0 = 1.0f / s[kv][0];
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) y[kv][e] = y0;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kT; ++j) {
+    int64_t page_row;
+    if (!locate_slot(p, slot[j], h, page_row)) continue;  // uniform per lane group
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      if (kv < p.nkv) {
+        float v[kPer], q[kPer];
+        unpack(Tag{}, w[j][kv], v);
+        static_quotients<kPer>(v, s[kv], y[kv], fast[kv], q);
+        uint32_t c[kPer / 4];
+        encode_static<kPer, kFp8>(q, c);
+        int8_t* dst = p.cache[kv] + page_row * p.head_dim + lane * kPer;
+        if constexpr (kPer == 8) {
+          u32x2 c2;
+          c2[0] = c[0];
+          c2[1] = c[1];
+          store_nt(reinterpret_cast<u32x2*>(dst), c2);
+        } else {
+          store_nt(reinterpret_cast<uint32_t*>(dst), c[0]);
+        }
+      }
+    }
+  }
+}
+
+// Generic static path (any head_dim / alignment): one wavefront per row, IEEE divides.
+template <class Tag, bool kFp8>
+__global__ __launch_bounds__(256) void quant_paged_static_generic(StaticParams sp) {
+  const QuantPagedParams& p = sp.q;
+  const StaticScales& sc = sp.sc;
+  constexpr int kRows = 256 / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int h = blockIdx.x % p.heads;
+  const int64_t tile = blockIdx.x / p.heads;
+  const int64_t t = tile * kRows + threadIdx.x / kWave;
+  if (t >= p.num_tokens) return;
+  int64_t page_row;
+  if (!locate_slot(p, p.slot[t], h, page_row)) return;
+  for (int kv = 0; kv < p.nkv; ++kv) {
+    const int64_t base = t * p.stride_tok[kv] + (int64_t)h * p.stride_head[kv];
+    int8_t* dst = p.cache[kv] + page_row * p.head_dim;
+    for (int d = lane; d < p.head_dim; d += kWave) {
+      const float s = sc.chan[kv] ? sc.chan[kv][(int64_t)h * p.head_dim + d] : sc.tensor[kv];
+      const float q = load1(Tag{}, p.src[kv], base + d) / s;  // IEEE divide
+      const uint32_t b =
+          kFp8 ? fp8e4m3_bits(__builtin_amdgcn_fmed3f(q, -448.0f, 448.0f)) : code_bits(q);
+      dst[d] = (int8_t)(uint8_t)(b & 0xffu);
+    }
+  }
+}
+
+template <class Tag, bool kFp8>
+int launch_static(const StaticParams& sp, hipStream_t stream) {
+  const QuantPagedParams& p = sp.q;
+  const StaticScales& sc = sp.sc;
+  constexpr int kPer = Tag::kPerVec;
+  const int nvec = p.head_dim % kPer == 0 ? p.head_dim / kPer : 0;
+  bool vec = nvec >= 1 && nvec <= kWave && (nvec & (nvec - 1)) == 0;
+  for (int kv = 0; kv < p.nkv && vec; ++kv) {
+    vec = (reinterpret_cast<uintptr_t>(p.src[kv]) % 16 == 0) &&
+          ((p.stride_tok[kv] * Tag::kBytes) % 16 == 0) &&
+          ((p.stride_head[kv] * Tag::kBytes) % 16 == 0) &&
+          (reinterpret_cast<uintptr_t>(p.cache[kv]) % 8 == 0) &&
+          (reinterpret_cast<uintptr_t>(sc.chan[kv]) % 16 == 0);  // null passes
+  }
+  const int G = vec ? nvec : kWave;
+  const int rows = vec ? (256 / G) * TMO_STATIC_TOKENS_PER_THREAD : 256 / kWave;
+  const int64_t tiles = (p.num_tokens + rows - 1) / rows;
+  const int64_t blocks = tiles * p.heads;
+  if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
+  const dim3 grid((unsigned)blocks), block(256);
+  if (!vec) return launch_kernel(quant_paged_static_generic<Tag, kFp8>, grid, block, stream, sp);
+  switch (G) {
+    case 1: return launch_kernel(quant_paged_static_vec<Tag, 1, kFp8>, grid, block, stream, sp);
+    case 2: return launch_kernel(quant_paged_static_vec<Tag, 2, kFp8>, grid, block, stream, sp);
+    case 4: return launch_kernel(quant_paged_static_vec<Tag, 4, kFp8>, grid, block, stream, sp);
+    case 8: return launch_kernel(quant_paged_static_vec<Tag, 8, kFp8>, grid, block, stream, sp);
+    case 16: return launch_kernel(quant_paged_static_vec<Tag, 16, kFp8>, grid, block, stream, sp);
+    case 32: return launch_kernel(quant_paged_static_vec<Tag, 32, kFp8>, grid, block, stream, sp);
+    default: return launch_kernel(quant_paged_static_vec<Tag, 64, kFp8>, grid, block, stream, sp);
+  }
+}
+
 template <class Tag, int V>
 int launch_vec(const QuantPagedParams& p, int G, dim3 grid, dim3 block, hipStream_t stream) {
   switch (G) {
@@ -246,5 +437,61 @@ extern "C" int tmo_hip_quant_to_paged_cache(const void* k, const void* v,
     case TMO_DTYPE_F32: return launch<F32>(p, s);
     case TMO_DTYPE_F16: return launch<F16>(p, s);
     default: return launch<BF16>(p, s);
+  }
+}
+
+extern "C" int tmo_hip_offline_quant_to_paged_cache(
+    const void* k, const void* v, int64_t k_stride_token, int64_t k_stride_head,
+    int64_t v_stride_token, int64_t v_stride_head, void* k_cache, void* v_cache,
+    const float* k_scale_channel, const float* v_scale_channel, float k_scale_tensor,
+    float v_scale_tensor, const int32_t* slot_mapping, int64_t num_tokens, int64_t num_heads,
+    int64_t head_size, int64_t num_blocks, int64_t block_size, int dtype, int cache_dtype,
+    void* stream) {
+  using namespace tmo;
+  if (dtype != TMO_DTYPE_F32 && dtype != TMO_DTYPE_F16 && dtype != TMO_DTYPE_BF16)
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (cache_dtype != TMO_DTYPE_I8 && cache_dtype != TMO_DTYPE_F8E4M3)
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (!k || !k_cache || !slot_mapping) return TMO_ERR_INVALID_ARGUMENT;
+  const bool has_v = v != nullptr;
+  if (has_v != (v_cache != nullptr) || (!has_v && v_scale_channel))
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (num_tokens < 0 || num_heads <= 0 || head_size <= 0 || num_blocks < 0 || block_size <= 0)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (k_stride_token < 0 || k_stride_head < 0 || (has_v && (v_stride_token < 0 || v_stride_head < 0)))
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (num_heads > 0x7fffffffLL || head_size > 0x7fffffffLL || block_size > 0x7fffffffLL)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (num_tokens == 0 || num_blocks == 0) return TMO_OK;
+
+  QuantPagedParams p{};
+  p.src[0] = k;
+  p.src[1] = v;
+  p.stride_tok[0] = k_stride_token;
+  p.stride_tok[1] = v_stride_token;
+  p.stride_head[0] = k_stride_head;
+  p.stride_head[1] = v_stride_head;
+  p.cache[0] = static_cast<int8_t*>(k_cache);
+  p.cache[1] = static_cast<int8_t*>(v_cache);
+  p.slot = slot_mapping;
+  p.num_tokens = num_tokens;
+  p.num_slots = num_blocks * block_size;
+  p.heads = (int32_t)num_heads;
+  p.head_dim = (int32_t)head_size;
+  p.block_size = (int32_t)block_size;
+  p.bs_shift = ilog2_if_pow2(block_size);
+  p.nkv = has_v ? 2 : 1;
+  StaticParams sp{};
+  sp.q = p;
+  sp.sc.chan[0] = k_scale_channel;
+  sp.sc.chan[1] = v_scale_channel;
+  sp.sc.tensor[0] = k_scale_tensor;
+  sp.sc.tensor[1] = v_scale_tensor;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool fp8 = cache_dtype == TMO_DTYPE_F8E4M3;
+  switch (dtype) {
+    case TMO_DTYPE_F32: return fp8 ? launch_static<F32, true>(sp, s) : launch_static<F32, false>(sp, s);
+    case TMO_DTYPE_F16: return fp8 ? launch_static<F16, true>(sp, s) : launch_static<F16, false>(sp, s);
+    default: return fp8 ? launch_static<BF16, true>(sp, s) : launch_static<BF16, false>(sp, s);
   }
 }

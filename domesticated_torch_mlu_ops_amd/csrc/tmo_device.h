@@ -164,7 +164,7 @@ __device__ __forceinline__ uint32_t code_bits(float q) {
 // instruction, so without a side effect in the branch the optimiser speculates it and every
 // lane computes both quotients (an IEEE divide is ~10 VALU ops) and selects -- which more
 // than doubled the quantiser's VALU work in some instantiations.
-__device__ __forceinline__ void keep_branch() { asm volatile(""); }
+__host__ __device__ __forceinline__ void keep_branch() { asm volatile(""); }
 
 // Per-row quantisation state: the scale and, on the fast path, its reciprocal.
 struct RowScale {
@@ -253,6 +253,65 @@ __device__ __forceinline__ int8_t encode1(float v, const RowScale& r) {
     q = v / r.s;
   }
   return (int8_t)(uint8_t)(code_bits(q) & 0xffu);
+}
+
+// ---------------------------------------------------------------------------- static scales
+
+// Static (offline) scales: code = clip(RNE(RN(x / s)), lo, hi) with a caller-given s per
+// channel or per tensor.  The reciprocal quotient is used when kStaticMinScale <= |s| <=
+// kStaticMaxScale (y = RN(1/s) is then a normal number and s * q cannot overflow) and every
+// |x * y| of the lane is below kStaticQuotientLimit (beyond it the code saturates either
+// way, and the correction steps could overflow); otherwise an IEEE divide per element.
+// tests/native/div_exhaustive.hip ("static") checks the int8 and fp8 codes, and the quotient
+// bits for |x| >= 2^-100 with a normal quotient, against IEEE division.
+constexpr float kStaticMinScale = 8.6736174e-19f;   // 2^-60
+constexpr float kStaticMaxScale = 1.2676506e30f;    // 2^100
+constexpr float kStaticQuotientLimit = 4194304.0f;  // 2^22
+
+__host__ __device__ __forceinline__ bool static_scale_fast(float s) {
+  const float a = __builtin_fabsf(s);
+  return a >= kStaticMinScale && a <= kStaticMaxScale;
+}
+
+// N quotients x[i] / s[i] (IEEE bits, see above).  y[i] = RN(1 / s[i]) when `fast`
+// (static_scale_fast for every s[i]), ignored otherwise.
+template <int N>
+__host__ __device__ __forceinline__ void static_quotients(const float* x, const float* s,
+                                                          const float* y, bool fast, float* q) {
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) m = fmaxf(m, __builtin_fabsf(x[i] * y[i]));
+  if (fast && m < kStaticQuotientLimit) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = div_by_recip(x[i], s[i], y[i]);
+  } else {
+    keep_branch();
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = x[i] / s[i];  // IEEE divide
+  }
+}
+
+// fp32 -> float8_e4m3fn bits (1-4-3, bias 7, no infinities, max 448), round to nearest
+// even, for finite |f| <= 448 (callers clamp first, as the reference math clips to +-448
+// before the cast).  Below 2^-6 the result is a subnormal multiple of 2^-9: RNE(|f| * 2^9)
+// (exact scaling) is its bit pattern, and 8 lands on the smallest normal, 0x08.  Above, the
+// fp32 pattern is rounded to 3 fraction bits (add half-ulp-minus-one plus the kept lsb) and
+// the exponent rebased from 127 to 7.  Negative values (and -0) set bit 7.
+__host__ __device__ __forceinline__ uint32_t fp8e4m3_bits(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  uint32_t code;
+  if (a < 0x3c800000u) {  // |f| < 2^-6
+    float af;
+    __builtin_memcpy(&af, &a, 4);
+    code = (uint32_t)__builtin_rintf(af * 512.0f);
+  } else {
+    const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+    code = (r >> 20) - (120u << 3);
+  }
+  return sign | code;
 }
 
 // ---------------------------------------------------------------------------- stores

@@ -8,6 +8,8 @@
 // have had (its Python wrappers return the written tensors in place: reference
 // _ops.py:1290-1294, 1562-1565, 3821-3824, 3249-3253), so torch.compile functionalisation
 // keeps the cache writes.
+#include <cmath>
+
 #include <c10/hip/HIPStream.h>
 #include <c10/core/DeviceGuard.h>
 
@@ -24,6 +26,7 @@ int dtype_code(at::ScalarType t) {
     case at::kHalf: return TMO_DTYPE_F16;
     case at::kBFloat16: return TMO_DTYPE_BF16;
     case at::kChar: return TMO_DTYPE_I8;
+    case at::kFloat8_e4m3fn: return TMO_DTYPE_F8E4M3;
     default: return -1;
   }
 }
@@ -148,6 +151,74 @@ void quant_to_paged_cache(const torch::Tensor& k, const c10::optional<torch::Ten
       has_v ? v_cache_scale->data_ptr<float>() : nullptr, slot_mapping.data_ptr<int32_t>(), T, H,
       D, NB, BS, dt, stream_of(k));
   check_status(st, "quant_to_paged_cache");
+}
+
+void offline_quant_to_paged_cache(const torch::Tensor& k, const c10::optional<torch::Tensor>& v,
+                                  const c10::optional<torch::Tensor>& k_cache_scale_per_channel,
+                                  const c10::optional<torch::Tensor>& v_cache_scale_per_channel,
+                                  const torch::Tensor& slot_mapping, torch::Tensor& k_cache,
+                                  const c10::optional<torch::Tensor>& v_cache,
+                                  double k_cache_scale_per_tensor,
+                                  double v_cache_scale_per_tensor) {
+  check_rows(k, "k");
+  check_cache(k_cache, "k_cache");
+  check_device(k, k, "k");
+  check_device(k_cache, k, "k_cache");
+  check_device(slot_mapping, k, "slot_mapping");
+  const int dt = dtype_code(k.scalar_type());
+  TORCH_CHECK(dt == TMO_DTYPE_F32 || dt == TMO_DTYPE_F16 || dt == TMO_DTYPE_BF16,
+              "offline_quant_to_paged_cache: k must be float, half or bfloat16, got ",
+              k.scalar_type());
+  const int cdt = dtype_code(k_cache.scalar_type());
+  TORCH_CHECK(cdt == TMO_DTYPE_I8 || cdt == TMO_DTYPE_F8E4M3,
+              "offline_quant_to_paged_cache: caches must be int8 or float8_e4m3fn, got ",
+              k_cache.scalar_type());
+  const int64_t T = k.size(0), H = k.size(1), D = k.size(2);
+  TORCH_CHECK(k_cache.size(1) == H && k_cache.size(3) == D, "k_cache ", k_cache.sizes(),
+              " does not match k ", k.sizes());
+  TORCH_CHECK(slot_mapping.scalar_type() == at::kInt && slot_mapping.dim() == 1 &&
+                  slot_mapping.size(0) == T && slot_mapping.is_contiguous(),
+              "slot_mapping must be a contiguous int32 [num_tokens] tensor");
+  const bool has_v = v.has_value();
+  TORCH_CHECK(has_v == v_cache.has_value(), "v and v_cache must both be given or both be None");
+  TORCH_CHECK(has_v || !v_cache_scale_per_channel.has_value(),
+              "v_cache_scale given without v");
+  if (has_v) {
+    check_rows(*v, "v");
+    check_cache(*v_cache, "v_cache");
+    check_device(*v, k, "v");
+    check_device(*v_cache, k, "v_cache");
+    TORCH_CHECK(v->sizes() == k.sizes() && v->scalar_type() == k.scalar_type(), "v must match k");
+    TORCH_CHECK(v_cache->sizes() == k_cache.sizes() &&
+                    v_cache->scalar_type() == k_cache.scalar_type(),
+                "v_cache must match k_cache");
+  }
+  // per channel: a float32 [heads, head_size] tensor; per tensor: a finite non-zero number
+  auto channel = [&](const c10::optional<torch::Tensor>& sc, const char* name) -> const float* {
+    if (!sc.has_value()) return nullptr;
+    check_device(*sc, k, name);
+    TORCH_CHECK(sc->scalar_type() == at::kFloat && sc->is_contiguous() && sc->dim() == 2 &&
+                    sc->size(0) == H && sc->size(1) == D,
+                name, " must be a contiguous float32 [heads, head_size] tensor, got ",
+                sc->scalar_type(), " ", sc->sizes());
+    return sc->data_ptr<float>();
+  };
+  const float* kch = channel(k_cache_scale_per_channel, "k_cache_scale");
+  const float* vch = channel(v_cache_scale_per_channel, "v_cache_scale");
+  const float kt = static_cast<float>(k_cache_scale_per_tensor);
+  const float vt = static_cast<float>(v_cache_scale_per_tensor);
+  TORCH_CHECK(kch || (std::isfinite(kt) && kt != 0.0f),
+              "k_cache_scale must be finite and non-zero, got ", k_cache_scale_per_tensor);
+  TORCH_CHECK(!has_v || vch || (std::isfinite(vt) && vt != 0.0f),
+              "v_cache_scale must be finite and non-zero, got ", v_cache_scale_per_tensor);
+  if (T == 0) return;
+  c10::DeviceGuard guard(k.device());
+  const int st = tmo_hip_offline_quant_to_paged_cache(
+      k.data_ptr(), has_v ? v->data_ptr() : nullptr, k.stride(0), k.stride(1),
+      has_v ? v->stride(0) : 0, has_v ? v->stride(1) : 0, k_cache.data_ptr(),
+      has_v ? v_cache->data_ptr() : nullptr, kch, vch, kt, vt, slot_mapping.data_ptr<int32_t>(),
+      T, H, D, k_cache.size(0), k_cache.size(2), dt, cdt, stream_of(k));
+  check_status(st, "offline_quant_to_paged_cache");
 }
 
 void dequant_from_paged_cache(at::Tensor& key, const c10::optional<at::Tensor>& value,
@@ -361,6 +432,10 @@ TORCH_LIBRARY(torch_mlu_ops, m) {
       "quant_to_paged_cache(Tensor k, Tensor? v, Tensor(a!) k_cache, Tensor(b!)? v_cache, "
       "Tensor(c!) k_cache_scale, Tensor(d!)? v_cache_scale, Tensor slot_mapping) -> ()");
   m.def(
+      "offline_quant_to_paged_cache(Tensor k, Tensor? v, Tensor? k_cache_scale_per_channel, "
+      "Tensor? v_cache_scale_per_channel, Tensor slot_mapping, Tensor(a!) k_cache, "
+      "Tensor(b!)? v_cache, float k_cache_scale_per_tensor, float v_cache_scale_per_tensor) -> ()");
+  m.def(
       "dequant_from_paged_cache(Tensor(a!) key, Tensor(b!)? value, Tensor key_cache, "
       "Tensor? value_cache, Tensor key_cache_quant_scale, Tensor? value_cache_quant_scale, "
       "Tensor context_lengths, SymInt max_context_len, Tensor? context_seq_offset, "
@@ -376,6 +451,7 @@ TORCH_LIBRARY(torch_mlu_ops, m) {
 TORCH_LIBRARY_IMPL(torch_mlu_ops, CUDA, m) {
   m.impl("reshape_paged_cache", &tmo::torch_api::reshape_paged_cache);
   m.impl("quant_to_paged_cache", &tmo::torch_api::quant_to_paged_cache);
+  m.impl("offline_quant_to_paged_cache", &tmo::torch_api::offline_quant_to_paged_cache);
   m.impl("dequant_from_paged_cache", &tmo::torch_api::dequant_from_paged_cache);
   m.impl("scaled_quantize", &tmo::torch_api::scaled_quantize);
 }

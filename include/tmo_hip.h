@@ -30,14 +30,15 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 1
+#define TMO_HIP_ABI_VERSION 2
 
 /* element types */
 enum tmo_dtype {
     TMO_DTYPE_F32 = 0,
     TMO_DTYPE_F16 = 1,
     TMO_DTYPE_BF16 = 2,
-    TMO_DTYPE_I8 = 3
+    TMO_DTYPE_I8 = 3,
+    TMO_DTYPE_F8E4M3 = 4 /* float8_e4m3fn: 1-4-3, bias 7, no infinities, max 448 */
 };
 
 /* return codes */
@@ -91,6 +92,32 @@ int tmo_hip_quant_to_paged_cache(const void* k, const void* v,
                                  int64_t num_tokens, int64_t num_heads, int64_t head_size,
                                  int64_t num_blocks, int64_t block_size,
                                  int dtype, void* stream);
+
+/*
+ * offline_quant_to_paged_cache -- static quantisation of k/v[T, H, D] into the paged caches
+ * with caller-given scales: q = RN(fp32(x) / s) (IEEE divide), stored as
+ * clip(RNE(q), -128, 127) in an int8 cache or as float8_e4m3fn(clip(q, -448, 448)) (round to
+ * nearest even) in an fp8 cache, at cache[slot / block_size, h, slot % block_size, :].
+ * s = k_scale_channel[h * head_size + d] when k_scale_channel is set (per channel, [H, D] fp32
+ * contiguous), else k_scale_tensor (per tensor); likewise for v.  No scales are written.
+ * Scales must be finite and non-zero (other values give unspecified codes, never a fault).
+ * Replaces tmo::torch_api::offline_quant_to_paged_cache (reference
+ * include/torch_mlu_ops.h:184-192), called by torch_mlu_ops.offline_quant_to_paged_cache
+ * (reference _ops.py:1639-1706).
+ * dtype: F32, F16 or BF16 (of k and v); cache_dtype: I8 or F8E4M3 (both caches).  v and
+ * v_cache: both NULL or both set; v_scale_channel must be NULL without v.
+ */
+int tmo_hip_offline_quant_to_paged_cache(const void* k, const void* v,
+                                         int64_t k_stride_token, int64_t k_stride_head,
+                                         int64_t v_stride_token, int64_t v_stride_head,
+                                         void* k_cache, void* v_cache,
+                                         const float* k_scale_channel,
+                                         const float* v_scale_channel,
+                                         float k_scale_tensor, float v_scale_tensor,
+                                         const int32_t* slot_mapping,
+                                         int64_t num_tokens, int64_t num_heads, int64_t head_size,
+                                         int64_t num_blocks, int64_t block_size,
+                                         int dtype, int cache_dtype, void* stream);
 
 /*
  * dequant_from_paged_cache -- gathers each sequence's pages through block_tables and writes

@@ -3,7 +3,7 @@
  *
  * Same namespace, names and parameter lists as the reference's prototypes
  * (reference include/torch_mlu_ops.h:21-22 namespace tmo::torch_api), restricted to the
- * four ops of this path.  The implementations (domesticated_torch_mlu_ops_amd/csrc/
+ * ops of this path.  The implementations (domesticated_torch_mlu_ops_amd/csrc/
  * torch_api.cpp) validate shapes/dtypes, take the current HIP stream of the tensors' device
  * and call the plain C ABI of tmo_hip.h; they are registered as the CUDA-key (HIP on ROCm)
  * kernels of the torch_mlu_ops::* ops.  All tensors are caller-owned and written in place;
@@ -37,6 +37,17 @@ void quant_to_paged_cache(const torch::Tensor &k,
                           torch::Tensor &k_cache_scale,
                           const c10::optional<torch::Tensor> &v_cache_scale,
                           const torch::Tensor &slot_mapping);
+
+/* reference include/torch_mlu_ops.h:184-192 (int8 and float8_e4m3fn caches) */
+void offline_quant_to_paged_cache(const torch::Tensor &k,
+                                  const c10::optional<torch::Tensor> &v,
+                                  const c10::optional<torch::Tensor> &k_cache_scale_per_channel,
+                                  const c10::optional<torch::Tensor> &v_cache_scale_per_channel,
+                                  const torch::Tensor &slot_mapping,
+                                  torch::Tensor &k_cache,
+                                  const c10::optional<torch::Tensor> &v_cache,
+                                  double k_cache_scale_per_tensor,
+                                  double v_cache_scale_per_tensor);
 
 /* reference include/torch_mlu_ops.h:334-350 (int8 "dynamic_per_token", act_mode "none") */
 void scaled_quantize(const at::Tensor &x,

@@ -51,10 +51,15 @@ def lib() -> ctypes.CDLL:
         L.oracle_scaled_quantize_per_token.argtypes = [c_void_p, c_int] + [c_int64] * 4 + \
             [c_void_p] * 3 + [c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                               c_int]
-        for name in ("oracle_f32_to_bf16", "oracle_f32_to_f16", "oracle_f16_to_f32"):
+        L.oracle_offline_quant_to_paged_cache.argtypes = [c_void_p, c_void_p, c_int] + \
+            [c_int64] * 4 + [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_float, c_float,
+                             c_void_p] + [c_int64] * 5 + [c_int]
+        for name in ("oracle_f32_to_bf16", "oracle_f32_to_f16", "oracle_f16_to_f32",
+                     "oracle_f32_to_e4m3"):
             getattr(L, name).argtypes = [c_void_p, c_void_p, c_int64]
         for name in ("oracle_quant_to_paged_cache", "oracle_reshape_paged_cache",
-                     "oracle_dequant_from_paged_cache", "oracle_scaled_quantize_per_token"):
+                     "oracle_dequant_from_paged_cache", "oracle_scaled_quantize_per_token",
+                     "oracle_offline_quant_to_paged_cache"):
             getattr(L, name).restype = c_int
         _lib = L
     return _lib
@@ -92,6 +97,40 @@ def quant_to_paged_cache(k, v, k_cache, v_cache, k_scale, v_scale, slot_mapping,
         _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
         _ptr(slots), T, H, D, NB, BS, nthreads or default_threads())
     _check(rc, "quant_to_paged_cache")
+
+
+def offline_quant_to_paged_cache(k, v, k_cache_scale, v_cache_scale, slot_mapping, k_cache,
+                                 v_cache, nthreads: Optional[int] = None) -> None:
+    """reference _ops.py:1639-1706 (decision D9 in tmo_oracle.c); in place on CPU tensors.
+    Each scale is a [H, D] fp32 tensor (per channel) or a Python number (per tensor); the
+    caches are int8 or torch.float8_e4m3fn."""
+    assert k.stride(2) == 1 and k_cache.is_contiguous()
+    T, H, D = k.shape
+    NB, _, BS, _ = k_cache.shape
+    cdt = {torch.int8: 3, torch.float8_e4m3fn: 4}[k_cache.dtype]
+    slots = slot_mapping.to(torch.int32).contiguous()  # kept alive across the call
+
+    def split(sc):
+        if torch.is_tensor(sc):
+            return sc.to(torch.float32).contiguous(), 1.0
+        return None, float(1.0 if sc is None else sc)
+
+    kch, kt = split(k_cache_scale)
+    vch, vt = split(v_cache_scale)
+    rc = lib().oracle_offline_quant_to_paged_cache(
+        _ptr(k), _ptr(v), _DT[k.dtype], k.stride(0), k.stride(1),
+        v.stride(0) if v is not None else 0, v.stride(1) if v is not None else 0,
+        _ptr(k_cache), _ptr(v_cache), cdt, _ptr(kch), _ptr(vch), kt, vt,
+        _ptr(slots), T, H, D, NB, BS, nthreads or default_threads())
+    _check(rc, "offline_quant_to_paged_cache")
+
+
+def f32_to_e4m3(x: torch.Tensor) -> torch.Tensor:
+    """float8_e4m3fn bit patterns (uint8) of fp32 values |x| <= 448, round to nearest even."""
+    x = x.to(torch.float32).contiguous()
+    out = torch.empty(x.shape, dtype=torch.uint8)
+    lib().oracle_f32_to_e4m3(_ptr(x), _ptr(out), x.numel())
+    return out
 
 
 def reshape_paged_cache(k, v, k_cache, v_cache, slot_mapping, direction: bool = False,

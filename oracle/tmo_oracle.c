@@ -20,7 +20,11 @@
  *   D5  NaN / Inf inputs are outside the contract.
  *   D6  dequant = RNE_out(fp32(code) * scale)   (cast order of _ops.py:3677).
  *   D7  smoothed = RN(fp32(x) * smooth), materialised before amax and divide (no FMA).
- *   D8  int8 codes only.
+ *   D8  int8 codes for the dynamic ops.
+ *   D9  offline (static-scale) quantisation divides: code = clip(RNE(RN(fp32(x) / s)), -128, 127)
+ *       for int8, fp8 = e4m3fn_RNE(clip(RN(fp32(x) / s), -448, 448)), s the fp32 per-channel
+ *       scale or the per-tensor scalar rounded to fp32 (_ops.py:1652-1670; the division is
+ *       the linear sibling's `key_i /= scale`, _ops.py:1829-1840).
  *
  * Parity pins for every function here live in tests/test_oracle_pins.py (torch-CPU
  * execution of the docstring math, exact rational arithmetic on engineered near-ties,
@@ -34,7 +38,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_I8 = 3 };
+enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_I8 = 3, DT_F8E4M3 = 4 };
 
 /* ------------------------------------------------------------------ conversions */
 
@@ -160,6 +164,35 @@ static void parallel_for(int64_t n, int nthreads, range_fn fn, void* ctx) {
         if (created[t]) pthread_join(th[t], NULL);
 }
 
+/*
+ * fp32 -> float8_e4m3fn (sign, 4 exponent bits with bias 7, 3 fraction bits, no infinities,
+ * largest finite 448), round to nearest even; defined for finite |f| <= 448 (the callers clip
+ * first, as the reference math does).  Computed in double: the quantum of |f|'s binade
+ * (2^(E-3), E clamped to the subnormal binade -6) divides |f| exactly, nearbyint rounds half
+ * to even, and the rounded value is re-encoded.
+ */
+static uint8_t f32_to_e4m3(float f) {
+    const uint8_t sign = signbit(f) ? 0x80 : 0;
+    const double a = fabs((double)f);
+    if (a == 0.0) return sign;
+    int e;
+    frexp(a, &e);
+    int E = e - 1;                           /* 2^E <= a < 2^(E+1) */
+    if (E < -6) E = -6;
+    const double quantum = ldexp(1.0, E - 3);
+    const double n = nearbyint(a / quantum);
+    const double r = n * quantum;
+    if (r < ldexp(1.0, -6)) return (uint8_t)(sign | (uint8_t)n);   /* subnormal: n * 2^-9 */
+    frexp(r, &e);
+    const int Er = e - 1;
+    const int frac = (int)(r / ldexp(1.0, Er - 3)) - 8;
+    return (uint8_t)(sign | (uint8_t)(((Er + 7) << 3) | frac));
+}
+
+void oracle_f32_to_e4m3(const float* in, uint8_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = f32_to_e4m3(in[i]);
+}
+
 /* ------------------------------------------------------------------ row quantiser */
 
 /*
@@ -236,6 +269,74 @@ int oracle_quant_to_paged_cache(const void* k, const void* v, int dtype,
     qpc_ctx c = {{k, v}, {k_st, v_st}, {k_sh, v_sh}, {k_cache, v_cache}, {k_scale, v_scale},
                  v ? 2 : 1, slot_mapping, T, H, D, NB, BS, dtype};
     parallel_for(T, nthreads, qpc_range, &c);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ offline_quant_to_paged_cache */
+
+typedef struct {
+    const void* src[2];
+    int64_t st[2], sh[2];
+    uint8_t* cache[2];
+    const float* chan[2];
+    float tensor[2];
+    int nkv;
+    const int32_t* slot;
+    int64_t T, H, D, NB, BS;
+    int dtype, cache_dtype;
+} oqpc_ctx;
+
+/* One element: D9. */
+static uint8_t static_code(float x, float s, int cache_dtype) {
+    float q = x / s;                                       /* IEEE divide */
+    if (cache_dtype == DT_F8E4M3) {
+        if (q < -448.0f) q = -448.0f;                      /* clip(key_i, -448, 448) */
+        if (q > 448.0f) q = 448.0f;
+        return f32_to_e4m3(q);
+    }
+    q = rintf(q);                                          /* round half to even */
+    if (q < -128.0f) q = -128.0f;                          /* clip(-128, 127) */
+    if (q > 127.0f) q = 127.0f;
+    return (uint8_t)(int8_t)q;
+}
+
+static void oqpc_range(void* p, int64_t lo, int64_t hi) {
+    oqpc_ctx* c = (oqpc_ctx*)p;
+    for (int64_t t = lo; t < hi; ++t) {
+        int64_t slot = c->slot[t];
+        if (slot < 0 || slot >= c->NB * c->BS) continue;            /* _ops.py:1656, D4 */
+        int64_t blk = slot / c->BS, off = slot % c->BS;              /* _ops.py:1659-1660 */
+        for (int kv = 0; kv < c->nkv; ++kv) {
+            for (int64_t h = 0; h < c->H; ++h) {
+                int64_t base = t * c->st[kv] + h * c->sh[kv];
+                uint8_t* dst = c->cache[kv] + ((blk * c->H + h) * c->BS + off) * c->D;
+                for (int64_t d = 0; d < c->D; ++d) {
+                    float s = c->chan[kv] ? c->chan[kv][h * c->D + d] : c->tensor[kv];
+                    dst[d] = static_code(load_elem(c->src[kv], base + d, c->dtype), s, c->cache_dtype);
+                }
+            }
+        }
+    }
+}
+
+/* _ops.py:1639-1706: offline_quant_to_paged_cache(k, v, k_cache_scale, v_cache_scale,
+ * slot_mapping, k_cache, v_cache).  k/v [T, H, D] with element strides (token, head);
+ * caches [NB, H, BS, D] int8 or float8_e4m3fn (cache_dtype DT_I8 / DT_F8E4M3); each of K and
+ * V uses its per-channel scale [H, D] when given, else its per-tensor scalar. */
+int oracle_offline_quant_to_paged_cache(const void* k, const void* v, int dtype,
+                                        int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh,
+                                        void* k_cache, void* v_cache, int cache_dtype,
+                                        const float* k_chan, const float* v_chan,
+                                        float k_tensor, float v_tensor,
+                                        const int32_t* slot_mapping, int64_t T, int64_t H,
+                                        int64_t D, int64_t NB, int64_t BS, int nthreads) {
+    if (elem_size(dtype) == 0 || dtype == DT_I8) return -2;
+    if (cache_dtype != DT_I8 && cache_dtype != DT_F8E4M3) return -2;
+    if (T < 0 || H <= 0 || D <= 0 || NB < 0 || BS <= 0) return -1;
+    oqpc_ctx c = {{k, v}, {k_st, v_st}, {k_sh, v_sh}, {(uint8_t*)k_cache, (uint8_t*)v_cache},
+                  {k_chan, v_chan}, {k_tensor, v_tensor}, v ? 2 : 1, slot_mapping,
+                  T, H, D, NB, BS, dtype, cache_dtype};
+    parallel_for(T, nthreads, oqpc_range, &c);
     return 0;
 }
 

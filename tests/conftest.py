@@ -21,9 +21,10 @@ def pytest_configure(config):
 
 
 def _ensure_built():
-    from domesticated_torch_mlu_ops_amd import _build
-    if not (_build.HIP_LIB.exists() and _build.TORCH_EXT.exists()):
-        _build.build_all()
+    import __graft_entry__
+    recipe = __graft_entry__._builder()  # by file path: the package import needs the libraries
+    if not (recipe.HIP_LIB.exists() and recipe.TORCH_EXT.exists()):
+        recipe.build_all()
     import oracle
     if not oracle.LIB_PATH.exists():
         oracle.build()

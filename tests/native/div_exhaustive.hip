@@ -8,6 +8,13 @@
 //          scale, inputs within +-3 ulps of (k + 0.5) * scale for every k in [-127, 127].
 //   scale: the divide-free row scale (scale_of) against IEEE amax / 127 for EVERY fp32 amax
 //          the kernels send through it (2^-100 up to the largest finite value).
+//   static: the static-scale quotient (static_quotients, per-element lane logic) for random
+//          scales 2^-60 <= |s| <= 2^100 of both signs, against x with quotients spread over
+//          2^-40 .. 2^24, within +-3 ulps of int8 ties (k + 0.5) * s and of fp8 e4m3 ties
+//          m * s, and near |x| = 2^-100; the int8 code and the fp8 code must always match,
+//          the quotient bits whenever |x| >= 2^-100 and the IEEE quotient is normal.
+//   fp8:   fp8e4m3_bits against a nearest-value search over the 127 positive e4m3 values
+//          (ties to the even code) for EVERY fp32 value in [-448, 448].
 //
 // Two properties are checked on every pair:
 //   * the int8 code (clamp to [-128, 127], round half to even) of the kernel quotient equals
@@ -15,6 +22,7 @@
 //   * the quotient bits themselves are identical whenever |x| >= 2^-100 (below that the FMA
 //     residual can underflow and the last bit may differ, but |x / s| < 2^-40 there).
 // Prints "mismatches=<n> checked=<m>" and exits non-zero on any mismatch.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -159,6 +167,127 @@ static Count run_scale(int nthreads) {
   return total;
 }
 
+// ---- static scales
+
+static uint32_t fp8_of(float q) { return tmo::fp8e4m3_bits(std::fmin(std::fmax(q, -448.0f), 448.0f)); }
+
+// Value of positive e4m3 code c (1..126).
+static double e4m3_value(int c) {
+  const int e = c >> 3, m = c & 7;
+  return e == 0 ? m * std::ldexp(1.0, -9) : (8 + m) * std::ldexp(1.0, e - 10);
+}
+
+static Count run_static(unsigned long long n, int nthreads) {
+  std::vector<Count> per(nthreads);
+  std::vector<std::thread> th;
+  for (int t = 0; t < nthreads; ++t)
+    th.emplace_back([&, t] {
+      std::mt19937_64 rng(777 + t);
+      Count& c = per[t];
+      for (unsigned long long i = t; i < n; i += nthreads) {
+        const uint32_t e = 67 + (uint32_t)(rng() % 161);  // 2^-60 .. 2^100
+        const uint32_t sign = (rng() % 5 == 0) ? 0x80000000u : 0u;
+        const float s = f_from_bits(sign | (e << 23) | (uint32_t)(rng() & 0x7fffff));
+        if (!tmo::static_scale_fast(s)) continue;
+        const float y = 1.0f / s;
+        float xs[16];
+        int nx = 0;
+        // quotient magnitude log-uniform in 2^-40 .. 2^24, either sign
+        const double lq = -40.0 + 64.0 * (double)(rng() >> 11) / 9007199254740992.0;
+        xs[nx++] = (float)(std::ldexp(1.0, 0) * std::exp2(lq) * (double)s * ((rng() & 1) ? -1.0 : 1.0));
+        const int k = (int)(rng() % 261) - 130;
+        const float t0 = (float)((k + 0.5) * (double)s);
+        for (int d = 0; d < 7; ++d) xs[nx++] = f_from_bits(bits_of(t0) + (uint32_t)(d - 3));
+        // midpoint between two adjacent e4m3 values
+        const int c8 = 1 + (int)(rng() % 125);
+        const double mid = 0.5 * (e4m3_value(c8) + e4m3_value(c8 + 1)) * ((rng() & 1) ? -1.0 : 1.0);
+        const float t1 = (float)(mid * (double)s);
+        for (int d = 0; d < 7; ++d) xs[nx++] = f_from_bits(bits_of(t1) + (uint32_t)(d - 3));
+        xs[nx++] = f_from_bits(bits_of(0x1p-100f) + (uint32_t)(rng() % 64)) * ((rng() & 1) ? -1.0f : 1.0f);
+        for (int j = 0; j < nx; ++j) {
+          const float x = xs[j];
+          if (!std::isfinite(x)) continue;
+          float q;
+          tmo::static_quotients<1>(&x, &s, &y, true, &q);
+          const float r = x / s;
+          ++c.checked;
+          const bool bad = code_of(q) != code_of(r) || fp8_of(q) != fp8_of(r) ||
+                           (std::fabs(x) >= 0x1p-100f && std::fabs(r) >= 0x1p-126f &&
+                            bits_of(q) != bits_of(r));
+          if (bad) {
+            if (c.bad < 5) std::printf("static mismatch s=%a x=%a fast=%a ieee=%a\n", s, x, q, r);
+            ++c.bad;
+          }
+        }
+      }
+    });
+  for (auto& x : th) x.join();
+  Count total;
+  for (auto& p : per) {
+    total.bad += p.bad;
+    total.checked += p.checked;
+  }
+  return total;
+}
+
+// ---- fp8 encoder
+
+static uint32_t fp8_reference(float f) {
+  const double a = std::fabs((double)f);
+  int best = 0;
+  double bd = a;  // distance to code 0
+  for (int c = 1; c <= 126; ++c) {
+    const double d = std::fabs(a - e4m3_value(c));
+    if (d < bd || (d == bd && (c & 1) == 0 && (best & 1) == 1)) {
+      bd = d;
+      best = c;
+    }
+  }
+  return (std::signbit(f) ? 0x80u : 0u) | (uint32_t)best;
+}
+
+static Count run_fp8(int nthreads) {
+  // table of the 127 positive values for a binary search
+  std::vector<double> vals(127);
+  for (int c = 0; c <= 126; ++c) vals[c] = c ? e4m3_value(c) : 0.0;
+  std::vector<Count> per(nthreads);
+  std::vector<std::thread> th;
+  const uint32_t hi = bits_of(448.0f);
+  for (int t = 0; t < nthreads; ++t)
+    th.emplace_back([&, t] {
+      Count& c = per[t];
+      for (uint32_t b = t; b <= hi; b += nthreads) {
+        for (uint32_t sgn = 0; sgn < 2; ++sgn) {
+          const float f = f_from_bits(b | (sgn << 31));
+          const double a = std::fabs((double)f);
+          // nearest of vals[lo], vals[lo + 1] with ties to the even code
+          int lo = (int)(std::upper_bound(vals.begin(), vals.end(), a) - vals.begin()) - 1;
+          int best = lo;
+          if (lo < 126) {
+            const double d0 = a - vals[lo], d1 = vals[lo + 1] - a;
+            if (d1 < d0 || (d1 == d0 && ((lo + 1) & 1) == 0)) best = lo + 1;
+          }
+          const uint32_t want = (sgn ? 0x80u : 0u) | (uint32_t)best;
+          ++c.checked;
+          if (tmo::fp8e4m3_bits(f) != want) {
+            if (c.bad < 5) std::printf("fp8 mismatch f=%a got=%#x want=%#x\n", f, tmo::fp8e4m3_bits(f), want);
+            ++c.bad;
+          }
+        }
+      }
+    });
+  for (auto& x : th) x.join();
+  Count total;
+  for (auto& p : per) {
+    total.bad += p.bad;
+    total.checked += p.checked;
+  }
+  // spot-check the search against the brute-force reference
+  for (float f : {0.0f, -0.0f, 1.0f / 1024, 3.0f / 1024, 0.0087890625f, 240.0f, 248.0f, 440.0f, 448.0f, -13.0f})
+    if (fp8_reference(f) != tmo::fp8e4m3_bits(f)) ++total.bad;
+  return total;
+}
+
 int main(int argc, char** argv) {
   const char* mode = argc > 1 ? argv[1] : "bf16";
   const int nthreads = argc > 2 ? std::atoi(argv[2]) : 8;
@@ -169,6 +298,10 @@ int main(int argc, char** argv) {
     c = run_format(0x7bffu, f16, nthreads);
   } else if (!std::strcmp(mode, "scale")) {
     c = run_scale(nthreads);
+  } else if (!std::strcmp(mode, "static")) {
+    c = run_static(argc > 3 ? std::strtoull(argv[3], nullptr, 10) : 4000000ull, nthreads);
+  } else if (!std::strcmp(mode, "fp8")) {
+    c = run_fp8(nthreads);
   } else {
     const unsigned long long n = argc > 3 ? std::strtoull(argv[3], nullptr, 10) : 20000000ull;
     c = run_f32(n, nthreads);

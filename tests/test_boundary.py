@@ -20,6 +20,10 @@ REFERENCE_SIGNATURES = {
     "quant_to_paged_cache": [("k", None), ("v", None), ("k_cache", None), ("v_cache", None),
                              ("k_cache_quant_scale", None), ("v_cache_quant_scale", None),
                              ("slot_mapping", None)],
+    # _ops.py:1639-1647
+    "offline_quant_to_paged_cache": [("k", None), ("v", None), ("k_cache_scale", None),
+                                     ("v_cache_scale", None), ("slot_mapping", None),
+                                     ("k_cache", None), ("v_cache", None)],
     # _ops.py:3734-3745
     "dequant_from_paged_cache": [("key", None), ("value", None), ("key_cache", None),
                                  ("value_cache", None), ("key_cache_quant_scale", None),
@@ -60,6 +64,7 @@ def test_alias_signature(tmo):
 WRITES = {
     "reshape_paged_cache": {"k", "v", "k_cache", "v_cache"},
     "quant_to_paged_cache": {"k_cache", "v_cache", "k_cache_scale", "v_cache_scale"},
+    "offline_quant_to_paged_cache": {"k_cache", "v_cache"},
     "dequant_from_paged_cache": {"key", "value"},
     "scaled_quantize": {"output", "output_scale", "output_reduced"},
 }
@@ -101,6 +106,10 @@ def test_fakes_run_on_meta_tensors(tmo):
     assert o.shape == (48, 4096) and s.shape == (48,)
     o, s = tmo.scaled_quantize(torch.empty(2, 3, 64, device="meta"), torch.empty(64, device="meta"))
     assert o.shape == (2, 3, 64) and s.shape == (2, 3)
+    f8 = kc.to(torch.float8_e4m3fn)
+    assert tmo.offline_quant_to_paged_cache(k, v, 0.5, 0.25, slot, kc, vc) == (kc, vc)
+    chan = torch.empty(8, 128, dtype=torch.float32, device="meta")
+    assert tmo.offline_quant_to_paged_cache(k, None, chan, None, slot, f8, None) is f8
 
 
 def test_fake_tensor_mode(tmo):
@@ -137,6 +146,8 @@ def test_cpu_tensors_fail_loudly(tmo):
         tmo.quant_to_paged_cache(k, v, kc, vc, ks, vs, slot)
     with pytest.raises(NotImplementedError):
         tmo.moe_quantize(torch.zeros(4, 64, dtype=torch.bfloat16), torch.ones(64))
+    with pytest.raises(NotImplementedError):
+        tmo.offline_quant_to_paged_cache(k, v, 0.5, 0.5, slot, kc, vc)
 
 
 def test_product_package_never_imports_the_oracle():

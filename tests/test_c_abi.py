@@ -36,6 +36,8 @@ def lib():
     L.tmo_hip_dequant_from_paged_cache.argtypes = [P, P] + [I64] * 5 + [P] * 7 + [I64] * 7 + \
         [INT, INT, INT, P]
     L.tmo_hip_scaled_quantize_per_token.argtypes = [P] + [I64] * 4 + [P] * 3 + [I64, P, I64, P, I64, P, I64, INT, P]
+    L.tmo_hip_offline_quant_to_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 4 + \
+        [ctypes.c_float] * 2 + [P] + [I64] * 5 + [INT, INT, P]
     return L
 
 
@@ -43,7 +45,8 @@ def test_every_declared_symbol_is_exported(lib):
     names = declared_functions()
     assert set(names) == {"tmo_hip_abi_version", "tmo_hip_status_string",
                           "tmo_hip_reshape_paged_cache", "tmo_hip_quant_to_paged_cache",
-                          "tmo_hip_dequant_from_paged_cache", "tmo_hip_scaled_quantize_per_token"}
+                          "tmo_hip_dequant_from_paged_cache", "tmo_hip_scaled_quantize_per_token",
+                          "tmo_hip_offline_quant_to_paged_cache"}
     for n in names:
         assert hasattr(lib, n), n
 
@@ -126,3 +129,20 @@ def test_scaled_quantize_validation(lib):
     assert call(gs=FAKE) == EINVAL                     # start position without gather_index
     assert call(stride=10) == EINVAL                   # rows overlap
     assert call(rows=0) == 0
+
+
+def test_offline_quant_validation(lib):
+    def call(dtype=2, cdt=3, k=FAKE, v=None, vc=None, vch=None, slot=FAKE, T=4, H=8, D=128, BS=16):
+        return lib.tmo_hip_offline_quant_to_paged_cache(k, v, 1024, 128, 1024, 128, FAKE, vc, None,
+                                                        vch, 0.5, 0.5, slot, T, H, D, 4, BS,
+                                                        dtype, cdt, None)
+    assert call(dtype=3) == EDTYPE          # int8 input
+    assert call(cdt=2) == EDTYPE            # bf16 cache
+    assert call(cdt=header_enum("TMO_DTYPE_F8E4M3"), T=0) == 0
+    assert call(k=None) == EINVAL
+    assert call(slot=None) == EINVAL
+    assert call(v=FAKE) == EINVAL           # v without v_cache
+    assert call(vch=FAKE) == EINVAL         # v scale without v
+    assert call(H=0) == EINVAL
+    assert call(BS=-1) == EINVAL
+    assert call(T=0) == 0

@@ -145,6 +145,124 @@ def test_quant_special_rows(tmo, ref, dev):
         assert kc[0, 0, 3, :5].tolist() == [127, 2, 4, 0, 2]      # token 1 at slot 3
 
 
+# ---------------------------------------------------------------------------- offline_quant_to_paged_cache
+
+def check_offline(tmo, ref, dev, name, k, v, ks, vs, slot, NB, BS, cdt):
+    """GPU offline_quant_to_paged_cache vs the oracle, caches compared whole (sentinel start)."""
+    H, D = k.shape[1], k.shape[2]
+
+    def fresh():
+        return torch.full((NB, H, BS, D), 0x5A, dtype=torch.uint8).view(cdt)
+
+    kc, vc = fresh(), (fresh() if v is not None else None)
+    ref.offline_quant_to_paged_cache(k, v, ks, vs, slot, kc, vc)
+    gk = fresh().to(dev)
+    gv = fresh().to(dev) if v is not None else None
+    d = (lambda t: t.to(dev) if torch.is_tensor(t) else t)
+    out = tmo.offline_quant_to_paged_cache(d(k), d(v), d(ks), d(vs), slot.to(dev), gk, gv)
+    assert (out[0] if v is not None else out) is gk
+    assert_bits_equal(gk.view(torch.uint8), kc.view(torch.uint8), f"{name} k_cache")
+    if v is not None:
+        assert_bits_equal(gv.view(torch.uint8), vc.view(torch.uint8), f"{name} v_cache")
+
+
+def _offline_inputs(T, H, D, NB, BS, dtype, seed, per_channel):
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randn(T, H, D, generator=g) * torch.logspace(-3, 2, T)[:, None, None]).to(dtype)
+    v = (torch.randn(T, H, D, generator=g) * 5).to(dtype)
+    slot = torch.randperm(NB * BS, generator=g)[:T].to(torch.int32)
+    if T > 8:
+        slot[::11] = -1
+        slot[3] = NB * BS + 7
+    if per_channel:
+        ks = 0.01 + 0.2 * torch.rand(H, D, generator=g)
+        vs = 0.02 + 0.1 * torch.rand(H, D, generator=g)
+    else:
+        ks, vs = 0.0371, 0.0523
+    return k, v, ks, vs, slot
+
+
+CACHE_DTYPES = [torch.int8, torch.float8_e4m3fn]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("cdt", CACHE_DTYPES)
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_offline_quant_modes(tmo, ref, dev, dtype, cdt, per_channel):
+    """Per-channel and per-tensor scales, int8 and fp8 caches, every input dtype; magnitudes
+    from 1e-3 to 1e2 so that codes underflow to 0 and saturate; -1 and out-of-range slots."""
+    k, v, ks, vs, slot = _offline_inputs(300, 8, 128, 64, 16, dtype, 31, per_channel)
+    check_offline(tmo, ref, dev, f"offline {dtype} {cdt}", k, v, ks, vs, slot, 64, 16, cdt)
+    check_offline(tmo, ref, dev, "k only", k, None, ks, None, slot, 64, 16, cdt)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D,BS", [(8, 16), (16, 16), (32, 16), (64, 16), (256, 16), (512, 16),
+                                  (80, 16), (3, 16), (128, 7)])
+def test_offline_quant_head_sizes(tmo, ref, dev, dtype, D, BS):
+    """Every lane-group width of the vector kernel (1..64 lanes), the generic kernel (head size
+    not a vector multiple, or more than 64 vectors), and an odd block size."""
+    k, v, ks, vs, slot = _offline_inputs(70, 3, D, 20, BS, dtype, D + BS, True)
+    for cdt in CACHE_DTYPES:
+        check_offline(tmo, ref, dev, f"D={D} BS={BS} {cdt}", k, v, ks, vs, slot, 20, BS, cdt)
+
+
+@pytest.mark.parametrize("T", [1, 63, 64, 65, 1000])
+def test_offline_quant_token_tails(tmo, ref, dev, T):
+    """Token counts around the kernel's tokens-per-workgroup (the last tile re-reads a valid
+    row and must not write it)."""
+    k, v, ks, vs, slot = _offline_inputs(T, 8, 128, 80, 16, torch.bfloat16, T, True)
+    check_offline(tmo, ref, dev, f"T={T}", k, v, ks, vs, slot, 80, 16, torch.int8)
+
+
+def test_offline_quant_scale_ranges(tmo, ref, dev):
+    """Scales outside the reciprocal path's range (tiny, huge) and negative ones, and rows
+    whose quotients exceed 2^22 (IEEE-divide branch of the lane); per channel and per tensor."""
+    T, H, D = 40, 4, 128
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(T, H, D, generator=g) * 3
+    k[5, 1, 17] = 3.0e10            # |x / s| > 2^22 in one lane
+    k[9, 2, :] = 1e-30              # tiny quotients
+    slot = torch.arange(T, dtype=torch.int32)
+    ks = 0.05 + 0.1 * torch.rand(H, D, generator=g)
+    ks[0, :8] = 1e-20               # below 2^-60
+    ks[1, 8:16] = 3e33              # above 2^100
+    ks[2, 16:24] *= -1              # negative
+    for cdt in CACHE_DTYPES:
+        for dtype in (torch.float32, torch.bfloat16):
+            kk = k.to(dtype)
+            check_offline(tmo, ref, dev, f"ranges {cdt} {dtype}", kk, kk.flip(0).contiguous(),
+                          ks, ks.flip(0).contiguous(), slot, 3, 16, cdt)
+            for st in (1e-25, 2.5e34, -0.03):
+                check_offline(tmo, ref, dev, f"tensor {st}", kk, None, st, None, slot, 3, 16, cdt)
+
+
+def test_offline_quant_strided_views(tmo, ref, dev):
+    T, H, D = 64, 4, 128
+    g = torch.Generator().manual_seed(12)
+    qkv = torch.randn(T, 3 * H, D, generator=g).to(torch.bfloat16)
+    k, v = qkv[:, H:2 * H], qkv[:, 2 * H:]
+    slot = torch.randperm(32 * 16, generator=g)[:T].to(torch.int32)
+    ks = 0.01 + 0.02 * torch.rand(H, D, generator=g)
+    for cdt in CACHE_DTYPES:
+        check_offline(tmo, ref, dev, "qkv view", k, v, ks, ks, slot, 32, 16, cdt)
+        flat = torch.randn(T * H * D + 1, generator=g).to(torch.bfloat16)
+        km = flat[1:].view(T, H, D)
+        check_offline(tmo, ref, dev, "misaligned", km, km, 0.02, 0.03, slot, 32, 16, cdt)
+
+
+def test_offline_quant_cfg3_shape(tmo, ref, dev):
+    """configs[2]'s shape (32768 tokens x 8 heads x 128, bf16, 65536 pages) with per-channel
+    scales, both cache types, at full size."""
+    case = W.cfg3()
+    g = torch.Generator().manual_seed(2024)
+    ks = 0.005 + 0.05 * torch.rand(8, 128, generator=g)
+    vs = 0.005 + 0.05 * torch.rand(8, 128, generator=g)
+    for cdt in CACHE_DTYPES:
+        check_offline(tmo, ref, dev, f"cfg3 {cdt}", case.k, case.v, ks, vs, case.slot_mapping,
+                      case.num_blocks, case.block_size, cdt)
+
+
 # ---------------------------------------------------------------------------- reshape_paged_cache
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32, torch.int8])

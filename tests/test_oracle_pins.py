@@ -415,3 +415,137 @@ def test_f16_conversions_match_numpy(ref):
     got = ref.f16_bits_to_f32(allh)[fin]
     want32 = torch.from_numpy(allh.numpy().view(np.float16).astype(np.float32))[fin]
     assert torch.equal(got.view(torch.int32), want32.view(torch.int32))
+
+
+# ---------------------------------------------------------------------------- offline (static) quant
+
+def torch_offline_quant_to_paged(k, v, k_scale, v_scale, slot, kc, vc):
+    """reference _ops.py:1652-1670 executed by torch on the CPU, with quant2int8 / quant2fp8
+    as the linear sibling spells them out (_ops.py:1829-1840): fp32 x / scale (IEEE), then
+    int8 round half even + clip(-128, 127), or clip(-448, 448) + the float8_e4m3fn cast."""
+    NB, H, BS, D = kc.shape
+    valid = (slot >= 0) & (slot < NB * BS)
+    s = slot[valid].long()
+    blk, off = s // BS, s % BS
+    for x, c, sc in ((k, kc, k_scale), (v, vc, v_scale)):
+        if x is None:
+            continue
+        scale = sc.to(torch.float32) if torch.is_tensor(sc) else \
+            torch.tensor(1.0 if sc is None else float(sc), dtype=torch.float32)
+        q = x[valid].to(torch.float32) / scale
+        if c.dtype == torch.int8:
+            codes = q.round().clamp(-128, 127).to(torch.int8).view(torch.uint8)
+        else:
+            codes = q.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+        c.view(torch.uint8).permute(0, 2, 1, 3)[blk, off] = codes
+
+
+def _offline_case(dtype, cache_dtype, per_channel, seed, T=80, H=4, D=64, NB=30, BS=16):
+    g = torch.Generator().manual_seed(seed)
+    # magnitudes spread so that some quotients saturate and some round to zero
+    k = (torch.randn(T, H, D, generator=g) * torch.logspace(-3, 2, T)[:, None, None]).to(dtype)
+    v = (torch.randn(T, H, D, generator=g) * 7).to(dtype)
+    slot = torch.randperm(NB * BS, generator=g)[:T].to(torch.int32)
+    slot[::9] = -1
+    slot[4] = NB * BS + 3
+    if per_channel:
+        ks = 0.01 + torch.rand(H, D, generator=g) * 0.2
+        vs = 0.02 + torch.rand(H, D, generator=g) * 0.1
+    else:
+        ks, vs = 0.0371, 0.0523
+    kc = torch.full((NB, H, BS, D), 0x5A, dtype=torch.uint8).view(cache_dtype)
+    return k, v, ks, vs, slot, kc
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("cache_dtype", [torch.int8, torch.float8_e4m3fn])
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_offline_quant_matches_torch_docstring_math(ref, dtype, cache_dtype, per_channel):
+    for seed in range(3):
+        k, v, ks, vs, slot, kc = _offline_case(dtype, cache_dtype, per_channel, seed)
+        vc = kc.clone()
+        ref.offline_quant_to_paged_cache(k, v, ks, vs, slot, kc, vc)
+        tk = torch.full_like(kc.view(torch.uint8), 0x5A).view(cache_dtype)
+        tv = tk.clone()
+        torch_offline_quant_to_paged(k, v, ks, vs, slot, tk, tv)
+        assert torch.equal(kc.view(torch.uint8), tk.view(torch.uint8))
+        assert torch.equal(vc.view(torch.uint8), tv.view(torch.uint8))
+    # K only, and a strided k (a column view of a fused qkv)
+    qkv = torch.randn(32, 12, 64).to(dtype)
+    kk = qkv[:, 4:8]
+    slot = torch.arange(32, dtype=torch.int32) * 3
+    kc = torch.full((8, 4, 16, 64), 0x5A, dtype=torch.uint8).view(cache_dtype)
+    tk = kc.clone()
+    sc = torch.rand(4, 64) * 0.05 + 0.01 if per_channel else 0.02
+    ref.offline_quant_to_paged_cache(kk, None, sc, None, slot, kc, None)
+    torch_offline_quant_to_paged(kk, None, sc, None, slot, tk, None)
+    assert torch.equal(kc.view(torch.uint8), tk.view(torch.uint8))
+
+
+def _e4m3_value(c: int) -> Fraction:
+    e, m = c >> 3, c & 7
+    return Fraction(m, 512) if e == 0 else Fraction(8 + m, 8) * Fraction(2) ** (e - 7)
+
+
+def _exact_e4m3(q: Fraction) -> int:
+    """float8_e4m3fn code of a rational (clip to +-448, nearest, ties to the even code)."""
+    sign = 0x80 if q < 0 else 0
+    a = min(abs(q), Fraction(448))
+    best, bd = 0, a
+    for c in range(1, 127):
+        d = abs(a - _e4m3_value(c))
+        if d < bd or (d == bd and c % 2 == 0 and best % 2 == 1):
+            best, bd = c, d
+    return sign | best
+
+
+def test_offline_quant_near_ties_exact_rational(ref):
+    """x within +-2 ulps of (k + 0.5) * s (int8) and of e4m3 midpoints * s (fp8), per channel:
+    the oracle must round the IEEE quotient, not a reciprocal product."""
+    g = torch.Generator().manual_seed(99)
+    H, D, T = 2, 64, 10
+    scales = (0.003 + torch.rand(H, D, generator=g) * 0.5).to(torch.float32)
+
+    def nudge(val: float) -> float:
+        t = torch.tensor([val], dtype=torch.float32)
+        t = (t.view(torch.int32) + int(torch.randint(-2, 3, (1,), generator=g))).view(torch.float32)
+        return float(t)
+
+    xi = torch.empty(T, H, D)
+    xf = torch.empty(T, H, D)
+    for t in range(T):
+        for h in range(H):
+            for d in range(D):
+                s = float(scales[h, d])
+                xi[t, h, d] = nudge((int(torch.randint(-130, 130, (1,), generator=g)) + 0.5) * s)
+                c = int(torch.randint(1, 126, (1,), generator=g))
+                mid = (_e4m3_value(c) + _e4m3_value(c + 1)) / 2
+                xf[t, h, d] = nudge(float(mid) * s * (1 if c % 3 else -1))
+    slot = torch.arange(T, dtype=torch.int32)
+    for k, cdt in ((xi, torch.int8), (xf, torch.float8_e4m3fn)):
+        kc = torch.zeros(1, H, 16, D, dtype=torch.uint8).view(cdt)
+        ref.offline_quant_to_paged_cache(k, None, scales, None, slot, kc, None)
+        got = kc.view(torch.uint8)
+        for t in range(T):
+            for h in range(H):
+                for d in range(D):
+                    q = _f32_round(Fraction(float(k[t, h, d])) / Fraction(float(scales[h, d])))
+                    want = (max(-128, min(127, _rne_int(q))) & 0xFF) if cdt == torch.int8 \
+                        else _exact_e4m3(q)
+                    assert int(got[0, h, t, d]) == want, (cdt, t, h, d)
+
+
+def test_fp8_conversion_matches_torch(ref):
+    """The oracle's fp32 -> float8_e4m3fn against torch's cast: every bf16 value in
+    [-448, 448], every midpoint between adjacent e4m3 values and its fp32 neighbours, and 2 M
+    random fp32 values in range."""
+    b = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float()
+    b = b[torch.isfinite(b) & (b.abs() <= 448)]
+    vals = torch.arange(0, 127, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    mids = ((vals[:-1].double() + vals[1:].double()) / 2).float()
+    near = torch.cat([mids, torch.nextafter(mids, torch.full_like(mids, 1e9)),
+                      torch.nextafter(mids, torch.zeros_like(mids)), vals])
+    g = torch.Generator().manual_seed(3)
+    r = (torch.rand(2_000_000, generator=g) * 2 - 1) * 448 * torch.rand(2_000_000, generator=g) ** 6
+    f = torch.cat([b, near, -near, r, torch.tensor([0.0, -0.0, 448.0, -448.0, 1e-30, -1e-30])])
+    assert torch.equal(ref.f32_to_e4m3(f), f.to(torch.float8_e4m3fn).view(torch.uint8))
