@@ -47,10 +47,14 @@ WORKLOADS = {
     "cfg4": "configs[3]: per_token_smooth_quantize 8192 x 4096 bf16 -> int8 + fp32 per-token scale",
     "cfg4_moe": "configs[3] MoE: per_token_smooth_quantize over 16384 gathered rows (top-2 of 64 experts), per-expert smooth",
     "cfg5": "configs[4]: dequant_from_paged_cache, 64 seqs ctx ~U[1024,32768], 8 KV heads x 128, int8 pages -> bf16",
+    "offline_i8": "offline_quant_to_paged_cache on configs[2]'s shape (32768 tokens x 8 KV heads x 128 bf16), static per-channel scales -> int8 pages",
+    "offline_f8": "offline_quant_to_paged_cache on configs[2]'s shape (32768 tokens x 8 KV heads x 128 bf16), static per-channel scales -> float8_e4m3fn pages",
 }
 KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1>", "cfg2": "quant_paged_vec<BF16,16,1>",
            "cfg3": "quant_paged_vec<BF16,16,1>", "cfg4": "sq_vec<BF16,8,true,1>",
-           "cfg4_moe": "sq_vec<BF16,8,false,1>", "cfg5": "dequant_paged_persistent<BF16,8>"}
+           "cfg4_moe": "sq_vec<BF16,8,false,1>", "cfg5": "dequant_paged_persistent<BF16,8>",
+           "offline_i8": "quant_paged_static_vec<BF16,16,false>",
+           "offline_f8": "quant_paged_static_vec<BF16,16,true>"}
 
 
 def parse_args():
@@ -143,6 +147,44 @@ def bench_paged_quant(torch, tmo, W, case, dev, steps, warmup):
     return ms, alg, case.valid_tokens(), sets
 
 
+def offline_bytes(case) -> int:
+    """Algorithmic bytes of offline_quant_to_paged_cache: the valid tokens' K/V rows read,
+    their codes written (no scales), the slot mapping, and the two [H, D] fp32 scale tables."""
+    T, H, D = case.k.shape
+    es = case.k.element_size()
+    return case.valid_tokens() * 2 * H * D * (es + 1) + 4 * T + 2 * H * D * 4
+
+
+def bench_offline(torch, tmo, W, case, cache_dtype, dev, steps, warmup):
+    """offline_quant_to_paged_cache with per-channel scales: per set its own K/V rows and slot
+    mapping, shared caches with per-set disjoint page ranges."""
+    alg = offline_bytes(case)
+    sets = n_sets(alg)
+    g = torch.Generator(device=dev).manual_seed(9)
+    T, H, D = case.k.shape
+    nslots = case.num_blocks * case.block_size
+    slots0 = case.slot_mapping.to(dev)
+    shape = (case.num_blocks, H, case.block_size, D)
+    kc = torch.zeros(shape, dtype=torch.uint8, device=dev).view(cache_dtype)
+    vc = torch.zeros(shape, dtype=torch.uint8, device=dev).view(cache_dtype)
+    gs = torch.Generator().manual_seed(2024)
+    ks = (0.005 + 0.05 * torch.rand(H, D, generator=gs)).to(dev)
+    vs = (0.005 + 0.05 * torch.rand(H, D, generator=gs)).to(dev)
+    calls = []
+    for s in range(sets):
+        if s == 0:
+            k, v, slots = case.k.to(dev), case.v.to(dev), slots0
+        else:
+            k = torch.randn((T, H, D), generator=g, device=dev).to(case.k.dtype)
+            v = torch.randn((T, H, D), generator=g, device=dev).to(case.v.dtype)
+            shift = (s * 9973 * case.block_size) % nslots
+            slots = torch.where(slots0 >= 0, (slots0 + shift) % nslots, slots0)
+        calls.append(lambda k=k, v=v, sl=slots:
+                     tmo.offline_quant_to_paged_cache(k, v, ks, vs, sl, kc, vc))
+    ms = time_graph(torch, calls, steps, warmup)
+    return ms, alg, case.valid_tokens(), sets
+
+
 def bench_smooth_quant(torch, tmo, W, case, dev, steps, warmup):
     alg = case.algorithmic_bytes()
     sets = n_sets(alg)
@@ -187,6 +229,14 @@ def profile_pass(torch, tmo, W, names, dev, n: int) -> None:
             k, v, sl = case.k.to(dev), case.v.to(dev), case.slot_mapping.to(dev)
             kc, vc, ks, vs = case.empty_caches(device=dev)
             fn = lambda: tmo.quant_to_paged_cache(k, v, kc, vc, ks, vs, sl)
+        elif name.startswith("offline"):
+            case = W.cfg3()
+            k, v, sl = case.k.to(dev), case.v.to(dev), case.slot_mapping.to(dev)
+            cdt = torch.int8 if name == "offline_i8" else torch.float8_e4m3fn
+            kc, vc, _, _ = case.empty_caches(device=dev)
+            kc, vc = kc.view(cdt), vc.view(cdt)
+            ks = torch.full((k.shape[1], k.shape[2]), 0.02, device=dev)
+            fn = lambda: tmo.offline_quant_to_paged_cache(k, v, ks, ks, sl, kc, vc)
         elif name.startswith("cfg4"):
             case = getattr(W, name)()
             x, sm = case.x.to(dev), case.smooth.to(dev)
@@ -251,6 +301,19 @@ def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
                                                  nthreads=nthreads)
         alg, units, desc = sub.algorithmic_bytes(), sub.valid_tokens(), \
             f"quant_to_paged_cache on the first {n} tokens of {workload}"
+    elif workload.startswith("offline"):
+        case = W.cfg3()
+        n = 4096
+        sub = W.PagedQuantCase(case.name, case.k[:n].contiguous(), case.v[:n].contiguous(),
+                               case.slot_mapping[:n].contiguous(), case.num_blocks)
+        cdt = torch.int8 if workload == "offline_i8" else torch.float8_e4m3fn
+        kc, vc = (c.view(cdt) for c in sub.empty_caches()[:2])
+        gs = torch.Generator().manual_seed(2024)
+        ks = 0.005 + 0.05 * torch.rand(W.H, W.D, generator=gs)
+        fn = lambda: oracle.offline_quant_to_paged_cache(sub.k, sub.v, ks, ks, sub.slot_mapping,
+                                                         kc, vc, nthreads=nthreads)
+        alg, units, desc = offline_bytes(sub), sub.valid_tokens(), \
+            f"offline_quant_to_paged_cache on the first {n} tokens of cfg3"
     elif workload.startswith("cfg4"):
         case = getattr(W, workload)()
         n = min(case.rows, 2048)
@@ -318,7 +381,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     todo = [args.workload] if args.configs == "headline" else \
-        ["cfg1", "cfg2", "cfg3", "cfg4", "cfg4_moe", "cfg5"]
+        ["cfg1", "cfg2", "cfg3", "cfg4", "cfg4_moe", "cfg5", "offline_i8", "offline_f8"]
     if args.workload not in todo:
         todo.append(args.workload)
     if args.profile_pass:
@@ -333,6 +396,10 @@ def main():
         elif name.startswith("cfg4"):
             ms, alg, units, sets = bench_smooth_quant(torch, tmo, W, getattr(W, name)(), dev,
                                                       args.steps, args.warmup)
+        elif name.startswith("offline"):
+            cdt = torch.int8 if name == "offline_i8" else torch.float8_e4m3fn
+            ms, alg, units, sets = bench_offline(torch, tmo, W, W.cfg3(), cdt, dev, args.steps,
+                                                 args.warmup)
         else:
             ms, alg, units, sets = bench_dequant(torch, tmo, W, W.cfg5(), dev,
                                                  max(10, args.steps // 40), max(2, args.warmup // 10))

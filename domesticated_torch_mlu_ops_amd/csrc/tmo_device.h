@@ -291,6 +291,23 @@ __host__ __device__ __forceinline__ void static_quotients(const float* x, const 
   }
 }
 
+// RN(1 / s) for kStaticMinScale <= |s| <= kStaticMaxScale: v_rcp_f32 (within 1 ulp) and one
+// FMA Newton step, y0 + y0 * (1 - s * y0).  tests/native/gfx950_builtins.hip ("rcp") checks it
+// on the GPU against IEEE 1.0f / s for every fp32 s of the range (the steps are odd in s).
+__device__ __forceinline__ float recip_rn(float s) {
+  const float y0 = __builtin_amdgcn_rcpf(s);
+  return __builtin_fmaf(__builtin_fmaf(-s, y0, 1.0f), y0, y0);
+}
+
+// Four values already clamped to [-448, 448] -> four float8_e4m3fn bytes (little-endian in
+// the result) with gfx950's v_cvt_pk_fp8_f32 (OCP e4m3fn, round to nearest even, two values
+// per instruction).  tests/native/gfx950_builtins.hip ("fp8") checks it on the GPU against
+// fp8e4m3_bits below for every fp32 value in [-448, 448].
+__device__ __forceinline__ uint32_t fp8x4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
 // fp32 -> float8_e4m3fn bits (1-4-3, bias 7, no infinities, max 448), round to nearest
 // even, for finite |f| <= 448 (callers clamp first, as the reference math clips to +-448
 // before the cast).  Below 2^-6 the result is a subnormal multiple of 2^-9: RNE(|f| * 2^9)

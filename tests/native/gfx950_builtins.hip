@@ -1,0 +1,89 @@
+// GPU checks of the two gfx950 hardware operations the static quantiser relies on, against
+// their IEEE / software definitions, over every input the kernels can give them:
+//
+//   rcp: recip_rn(s) (v_rcp_f32 + one FMA Newton step, tmo_device.h) == IEEE 1.0f / s for
+//        every fp32 s with 2^-60 <= s <= 2^100 (the range static_scale_fast admits; the
+//        operations are odd in s, so the negative range follows).
+//   fp8: fp8x4 (v_cvt_pk_fp8_f32) == fp8e4m3_bits (the integer encoder, itself checked on
+//        the host against a nearest-value search by div_exhaustive.hip "fp8") for every fp32
+//        value in [-448, 448].
+//
+// Each mode launches one grid-stride kernel that counts mismatches with vector atomics and
+// prints "mismatches=<n> checked=<m>"; the exit status is non-zero on any mismatch.  Built by
+// __graft_entry__.build() into tests/native/_build/; run by tests/test_gpu_builtins.py.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+
+#include "tmo_device.h"
+
+namespace {
+
+__global__ void check_rcp(uint32_t lo, uint32_t count, unsigned long long* bad) {
+  const uint32_t stride = gridDim.x * blockDim.x;
+  unsigned long long b = 0;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const float s = __uint_as_float(lo + i);
+    if (__float_as_uint(tmo::recip_rn(s)) != __float_as_uint(1.0f / s)) ++b;
+  }
+  if (b) atomicAdd(bad, b);
+}
+
+// Bit patterns 0 .. hi of both signs, four consecutive patterns per conversion.
+__global__ void check_fp8(uint32_t hi, unsigned long long* bad) {
+  const uint32_t stride = gridDim.x * blockDim.x;
+  const uint32_t quads = hi / 4 + 1;
+  unsigned long long b = 0;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < quads; i += stride) {
+    for (uint32_t sign = 0; sign < 2; ++sign) {
+      float f[4];
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t u = 4 * i + j;
+        f[j] = __uint_as_float((u <= hi ? u : hi) | (sign << 31));
+      }
+      const uint32_t hw = tmo::fp8x4(f[0], f[1], f[2], f[3]);
+      for (int j = 0; j < 4; ++j)
+        if (((hw >> (8 * j)) & 0xffu) != tmo::fp8e4m3_bits(f[j])) ++b;
+    }
+  }
+  if (b) atomicAdd(bad, b);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const char* mode = argc > 1 ? argv[1] : "rcp";
+  unsigned long long* d_bad = nullptr;
+  if (hipMalloc(&d_bad, sizeof(unsigned long long)) != hipSuccess ||
+      hipMemset(d_bad, 0, sizeof(unsigned long long)) != hipSuccess) {
+    std::printf("device setup failed\n");
+    return 2;
+  }
+  unsigned long long checked = 0;
+  if (!std::strcmp(mode, "rcp")) {
+    uint32_t lo, hi;
+    const float flo = tmo::kStaticMinScale, fhi = tmo::kStaticMaxScale;
+    std::memcpy(&lo, &flo, 4);
+    std::memcpy(&hi, &fhi, 4);
+    checked = (unsigned long long)(hi - lo) + 1;
+    check_rcp<<<dim3(8192), dim3(256)>>>(lo, hi - lo + 1, d_bad);
+  } else if (!std::strcmp(mode, "fp8")) {
+    uint32_t hi;
+    const float fhi = 448.0f;
+    std::memcpy(&hi, &fhi, 4);
+    checked = 2ull * ((unsigned long long)(hi / 4) + 1) * 4;
+    check_fp8<<<dim3(8192), dim3(256)>>>(hi, d_bad);
+  } else {
+    std::printf("unknown mode %s\n", mode);
+    return 2;
+  }
+  unsigned long long bad = 0;
+  if (hipDeviceSynchronize() != hipSuccess ||
+      hipMemcpy(&bad, d_bad, sizeof(bad), hipMemcpyDeviceToHost) != hipSuccess) {
+    std::printf("kernel failed\n");
+    return 3;
+  }
+  std::printf("mode=%s mismatches=%llu checked=%llu\n", mode, bad, checked);
+  return bad == 0 ? 0 : 1;
+}

@@ -1,0 +1,22 @@
+"""gfx950 hardware operations used by the static (offline) quantiser, checked exhaustively on
+the GPU against their definitions (tests/native/gfx950_builtins.hip, built in-tree by
+__graft_entry__.build()): the v_rcp_f32 + Newton reciprocal is IEEE 1/s for every scale on the
+reciprocal path, and the v_cvt_pk_fp8_f32 conversion is the round-to-nearest-even e4m3fn
+encoding for every fp32 value in [-448, 448]."""
+import subprocess
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+BINARY = Path(__file__).resolve().parent / "native" / "_build" / "gfx950_builtins"
+
+
+@pytest.mark.parametrize("mode", ["rcp", "fp8"])
+def test_gfx950_builtin_exhaustive(dev, mode):
+    assert BINARY.exists(), f"{BINARY} not built (run __graft_entry__.build())"
+    print(f"[gfx950_builtins] {mode}", flush=True)
+    res = subprocess.run([str(BINARY), mode], capture_output=True, text=True, timeout=100)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert "mismatches=0" in res.stdout
