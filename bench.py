@@ -274,6 +274,18 @@ def copy_ceiling_gbs(torch, dev) -> float:
     return 2 * src.numel() * 4 / (ms * 1e-3) / 1e9
 
 
+def cast_ceiling_gbs(torch, dev) -> float:
+    """torch's bf16 -> int8 cast over configs[2]'s K+V volume (134,217,728 B read, 67,108,864 B
+    written per call, rotating over 6 buffer pairs so the MALL holds nothing): the headline's
+    2:1 read:write mix moved by a plain elementwise kernel, timed like the workloads."""
+    n = 1 << 26
+    pairs = [(torch.ones(n, dtype=torch.bfloat16, device=dev),
+              torch.empty(n, dtype=torch.int8, device=dev)) for _ in range(6)]
+    calls = [lambda a=a, b=b: b.copy_(a) for a, b in pairs]
+    ms = time_graph(torch, calls, 240, 24)
+    return 3 * n / (ms * 1e-3) / 1e9
+
+
 def launch_floor_us(torch, tmo, dev) -> float:
     """Duration of the smallest quant_to_paged_cache launch (1 token, 1 head) -- the per-call
     floor that bounds the latency-bound configs."""
@@ -413,6 +425,7 @@ def main():
         torch.cuda.empty_cache()
     floor = launch_floor_us(torch, tmo, dev) if args.configs == "all" else None
     ceiling = copy_ceiling_gbs(torch, dev) if args.configs == "all" else None
+    cast_ceiling = cast_ceiling_gbs(torch, dev) if args.configs == "all" else None
 
     head = per[args.workload]
     traffic = None
@@ -434,8 +447,10 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded, BASELINE.md section 3)",
         "config": {"workload": WORKLOADS[args.workload],
-                   "io": "bf16 in; int8 codes + fp32 scales out" if args.workload != "cfg5"
-                   else "int8 codes + fp32 scales in; bf16 out",
+                   "io": {"cfg5": "int8 codes + fp32 scales in; bf16 out",
+                          "offline_i8": "bf16 in; int8 codes out (static per-channel scales)",
+                          "offline_f8": "bf16 in; float8_e4m3fn codes out (static per-channel scales)"}
+                   .get(args.workload, "bf16 in; int8 codes + fp32 scales out"),
                    "tokens_per_s": head["units_per_s"],
                    "frac_of_peak": head["frac_of_peak"]},
         "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
@@ -446,6 +461,7 @@ def main():
         "settle_s": SETTLE_S,
         "launch_floor_us": round(floor, 3) if floor is not None else None,
         "copy_ceiling_GB_s": round(ceiling, 1) if ceiling is not None else None,
+        "cast_2to1_ceiling_GB_s": round(cast_ceiling, 1) if cast_ceiling is not None else None,
     }
     print(json.dumps(line), flush=True)
 
