@@ -405,7 +405,9 @@ def test_dequant_seq_offset_invalid_blocks_and_extreme_scales(tmo, ref, dev):
 
 # ---------------------------------------------------------------------------- scaled_quantize
 
-def _sq_both(tmo, ref, dev, case: W.SmoothQuantCase, gather_start=None, smooth=True):
+def _sq_both(tmo, ref, dev, case: W.SmoothQuantCase, gather_start=None, smooth=True,
+             x_dev=None):
+    """x_dev: the GPU input when it must keep a layout .to() would not (e.g. a column slice)."""
     x = case.x
     rows = case.rows
     shape_scale = (rows,) + tuple(x.shape[1:-1])
@@ -417,13 +419,14 @@ def _sq_both(tmo, ref, dev, case: W.SmoothQuantCase, gather_start=None, smooth=T
     out_g = out_w.clone().fill_(W.CACHE_SENTINEL).to(dev)
     sc_g = torch.full_like(sc_w, W.SCALE_SENTINEL).to(dev)
     d = (lambda t: t.to(dev) if t is not None else None)
+    xg = x.to(dev) if x_dev is None else x_dev
     if smooth:
-        o, s = tmo.moe_quantize(x.to(dev), case.smooth.to(dev), None, d(case.token_count),
+        o, s = tmo.moe_quantize(xg, case.smooth.to(dev), None, d(case.token_count),
                                 d(case.gather_index), d(gather_start), out_g, sc_g)
         assert o is out_g and s is sc_g
     else:
         torch.ops.torch_mlu_ops.scaled_quantize(
-            x.to(dev), out_g, sc_g, None, None, d(case.token_count), d(case.gather_index),
+            xg, out_g, sc_g, None, None, d(case.token_count), d(case.gather_index),
             d(gather_start), None, "dynamic_per_token", "none", 1.0, False)
     assert_bits_equal(out_g, out_w, f"{case.name} output")
     assert_bits_equal(sc_g, sc_w, f"{case.name} output_scale")
@@ -472,6 +475,22 @@ def test_smooth_quant_many_rows_per_wavefront(tmo, ref, dev, dtype, C, smooth):
           "none": torch.ones(C)}[smooth]
     _sq_both(tmo, ref, dev, W.SmoothQuantCase(f"{rows}x{C} {dtype} {smooth}", x, sm),
              smooth=smooth != "none")
+
+
+@pytest.mark.parametrize("smooth", ["scalar", "none"])
+def test_smooth_quant_dense_layouts(tmo, ref, dev, smooth):
+    """The dense kernel (no gather, no groups, no or scalar smooth): 3-D [n0, inner, C] rows,
+    and rows that are a column slice of wider rows (row stride C + 64)."""
+    g = torch.Generator().manual_seed(77)
+    sm = torch.tensor([0.8125]) if smooth == "scalar" else torch.ones(512)
+    x3 = (torch.randn(300, 3, 512, generator=g) * 4).to(torch.bfloat16)
+    x3[7, 1] = 0
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase(f"3d {smooth}", x3, sm), smooth=smooth == "scalar")
+    wide = (torch.randn(1000, 512 + 64, generator=g) * 2).to(torch.bfloat16)
+    xg = wide.to(dev)[:, :512]
+    assert xg.stride(0) == 576
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase(f"strided {smooth}", wide[:, :512], sm),
+             smooth=smooth == "scalar", x_dev=xg)
 
 
 def test_smooth_quant_variants(tmo, ref, dev):
