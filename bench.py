@@ -51,7 +51,7 @@ WORKLOADS = {
     "offline_f8": "offline_quant_to_paged_cache on configs[2]'s shape (32768 tokens x 8 KV heads x 128 bf16), static per-channel scales -> float8_e4m3fn pages",
 }
 KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1>", "cfg2": "quant_paged_vec<BF16,16,1>",
-           "cfg3": "quant_paged_vec<BF16,16,1>", "cfg4": "sq_vec<BF16,8,true,1>",
+           "cfg3": "quant_paged_vec<BF16,16,1>", "cfg4": "sq_dense<BF16,8,false,true>",
            "cfg4_moe": "sq_vec<BF16,8,false,1>", "cfg5": "dequant_paged_persistent<BF16,8>",
            "offline_i8": "quant_paged_static_vec<BF16,16,false>",
            "offline_f8": "quant_paged_static_vec<BF16,16,true>"}
@@ -274,16 +274,18 @@ def copy_ceiling_gbs(torch, dev) -> float:
     return 2 * src.numel() * 4 / (ms * 1e-3) / 1e9
 
 
-def cast_ceiling_gbs(torch, dev) -> float:
-    """torch's bf16 -> int8 cast over configs[2]'s K+V volume (134,217,728 B read, 67,108,864 B
-    written per call, rotating over 6 buffer pairs so the MALL holds nothing): the headline's
-    2:1 read:write mix moved by a plain elementwise kernel, timed like the workloads."""
-    n = 1 << 26
-    pairs = [(torch.ones(n, dtype=torch.bfloat16, device=dev),
-              torch.empty(n, dtype=torch.int8, device=dev)) for _ in range(6)]
-    calls = [lambda a=a, b=b: b.copy_(a) for a, b in pairs]
-    ms = time_graph(torch, calls, 240, 24)
-    return 3 * n / (ms * 1e-3) / 1e9
+def stream_ceilings() -> dict | None:
+    """Practical HBM ceilings for the workloads' traffic shapes, from the minimal streaming
+    kernels of tests/native/stream_ceiling.hip (built by __graft_entry__.build()); None when
+    that program is not built."""
+    exe = REPO / "tests" / "native" / "_build" / "stream_ceiling"
+    if not exe.exists():
+        return None
+    import subprocess
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    if res.returncode != 0:
+        return {"error": (res.stdout + res.stderr).strip()[-200:]}
+    return json.loads(res.stdout.strip().splitlines()[-1])
 
 
 def launch_floor_us(torch, tmo, dev) -> float:
@@ -425,7 +427,7 @@ def main():
         torch.cuda.empty_cache()
     floor = launch_floor_us(torch, tmo, dev) if args.configs == "all" else None
     ceiling = copy_ceiling_gbs(torch, dev) if args.configs == "all" else None
-    cast_ceiling = cast_ceiling_gbs(torch, dev) if args.configs == "all" else None
+    streams = stream_ceilings() if args.configs == "all" else None
 
     head = per[args.workload]
     traffic = None
@@ -461,7 +463,7 @@ def main():
         "settle_s": SETTLE_S,
         "launch_floor_us": round(floor, 3) if floor is not None else None,
         "copy_ceiling_GB_s": round(ceiling, 1) if ceiling is not None else None,
-        "cast_2to1_ceiling_GB_s": round(cast_ceiling, 1) if cast_ceiling is not None else None,
+        "stream_ceilings": streams,
     }
     print(json.dumps(line), flush=True)
 
