@@ -57,6 +57,10 @@ __device__ int64_t seq_begin(const DequantParams& p, int64_t i, int64_t* red) {
   return total;
 }
 
+#ifndef TMO_DEQUANT_NT_STORE
+#define TMO_DEQUANT_NT_STORE 0
+#endif
+
 template <class Tag>
 __device__ __forceinline__ void store16(Tag, void* base, int64_t elem, const float* f) {
   u32x4 a, b;
@@ -65,8 +69,13 @@ __device__ __forceinline__ void store16(Tag, void* base, int64_t elem, const flo
 #pragma unroll
   for (int i = 0; i < 4; ++i) b[i] = pack2(Tag{}, f[8 + 2 * i], f[8 + 2 * i + 1]);
   u32x4* dst = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + elem);
+#if TMO_DEQUANT_NT_STORE
+  __builtin_nontemporal_store(a, dst);
+  __builtin_nontemporal_store(b, dst + 1);
+#else
   dst[0] = a;  // cached stores: L2 merges the two half-sector streams of a wavefront
   dst[1] = b;
+#endif
 }
 
 __device__ __forceinline__ void store16(F32, void* base, int64_t elem, const float* f) {
@@ -146,8 +155,13 @@ __global__ __launch_bounds__(256) void dequant_paged_vec(DequantParams p) {
   }
 }
 
+// Workgroups launched per CU by the flat-page kernel.  Far more than can be resident (8 per CU
+// at 256 threads): the hardware dispatcher then hands the next workgroup to whichever CU frees
+// a slot, which balances the tail that a fixed page-per-workgroup split leaves.  configs[4]
+// (~75 K pages over 256 CUs): 8 per CU 1541 us, 64: 1442 us, 192-320: ~1400 us, 512 (one page
+// per workgroup) 1476 us.
 #ifndef TMO_DEQUANT_WG_PER_CU
-#define TMO_DEQUANT_WG_PER_CU 8
+#define TMO_DEQUANT_WG_PER_CU 256
 #endif
 #ifndef TMO_DEQUANT_WRITE_CONTIGUOUS
 #define TMO_DEQUANT_WRITE_CONTIGUOUS 0
@@ -202,7 +216,8 @@ __device__ __forceinline__ T block_scan(T v, T* tmp, T& total) {
 
 // Persistent vector path (heads, head_dim / 16 and block_size powers of two, batch <= 4096).
 // All pages of all sequences form one flat list, sequence-major; workgroup b takes pages
-// b, b + gridDim.x, ...  Each workgroup first scans context_lengths once into LDS: the first
+// b, b + gridDim.x, ... (about one page each at the launch size used, see
+// TMO_DEQUANT_WG_PER_CU).  Each workgroup first scans context_lengths once into LDS: the first
 // page and first output row of every sequence.  Inside a page the 16-code units follow the
 // cache layout (d16, then token, then head: a wavefront reads 1 KiB of one head page and
 // writes 256 B runs of 8 output rows), which measured faster on MI355X than the
