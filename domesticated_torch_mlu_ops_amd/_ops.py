@@ -15,6 +15,8 @@ __all__ = [
     "reshape_paged_cache",
     "quant_to_paged_cache",
     "offline_quant_to_paged_cache",
+    "fused_rope",
+    "fused_rmsnorm_rope_store_paged_cache",
     "dequant_from_paged_cache",
     "moe_quantize",
     "scaled_quantize",
@@ -100,6 +102,91 @@ def offline_quant_to_paged_cache(
             k, v, None, None, slot_mapping, k_cache, v_cache, k_cache_scale,
             v_cache_scale if v_cache_scale is not None else 1.0)
     return (k_cache, v_cache) if v_cache is not None else k_cache
+
+
+def fused_rope(
+    qkv: torch.Tensor,
+    k_cache_hp: torch.Tensor,
+    v_cache_hp: torch.Tensor,
+    sin_cache: torch.Tensor,
+    cos_cache: torch.Tensor,
+    position_id: torch.Tensor,
+    k_gamma: torch.Tensor,
+    k_beta: Optional[torch.Tensor],
+    k_cache_lp: Optional[torch.Tensor] = None,
+    v_cache_lp: Optional[torch.Tensor] = None,
+    cache_bs_id_hp: Optional[torch.Tensor] = None,
+    cache_seq_offsets_hp: Optional[torch.Tensor] = None,
+    cache_bs_id_lp: Optional[torch.Tensor] = None,
+    cache_seq_offsets_lp: Optional[torch.Tensor] = None,
+    k_scale_hp: Optional[torch.Tensor] = None,
+    v_scale_hp: Optional[torch.Tensor] = None,
+    k_scale_lp: Optional[torch.Tensor] = None,
+    v_scale_lp: Optional[torch.Tensor] = None,
+    slot_mapping_hp: Optional[torch.Tensor] = None,
+    slot_mapping_lp: Optional[torch.Tensor] = None,
+    norm_type: str = "layernorm",
+    rope_dim_offset: int = 0,
+    eps: float = 1e-5,
+    q_gamma: Optional[torch.Tensor] = None,
+):
+    """RMSNorm (Q optional, K) + fold rotary embedding + store of K and V into paged caches,
+    in one pass over ``qkv [batch, seq_len, q_heads + 2 kv_heads, head_size]``.
+
+    Token ``(b, s)`` is rotated at position ``position_id[b] + s`` with rows of
+    ``sin_cache`` / ``cos_cache [rotary_seq, rope_dim]`` over head dims
+    ``[rope_dim_offset, rope_dim_offset + rope_dim)``; Q is written back into ``qkv``; K and V
+    go to ``k_cache_hp`` / ``v_cache_hp [num_blocks, kv_heads, block_size, head_size]`` at
+    ``slot_mapping_hp`` (negative slots skipped): in qkv's dtype, or int8 with ``k_scale_hp`` /
+    ``v_scale_hp`` either ``[num_blocks, kv_heads, block_size]`` (dynamic per-token scales,
+    written) or ``[kv_heads, head_size]`` (static per-channel scales, read).  fp32 arithmetic
+    with one final rounding.  This build implements ``norm_type="rmsnorm"`` with paged
+    high-precision caches; other modes raise ``RuntimeError``.
+
+    Reference: ``_ops.py:3469-3601`` (math ``:3496-3520``, rotary math ``:1116-1127``).
+    Returns ``(qkv, k_cache_hp, v_cache_hp)`` (plus the low-precision tensors when given).
+    """
+    torch.ops.torch_mlu_ops.fused_rope(qkv, k_cache_hp, v_cache_hp, k_cache_lp, v_cache_lp,
+            sin_cache, cos_cache, position_id, k_gamma, k_beta, k_scale_hp, v_scale_hp,
+            k_scale_lp, v_scale_lp, cache_bs_id_hp, cache_seq_offsets_hp,
+            cache_bs_id_lp, cache_seq_offsets_lp, slot_mapping_hp, slot_mapping_lp,
+            norm_type, rope_dim_offset, eps, q_gamma)
+    out = (qkv, k_cache_hp, v_cache_hp)
+    if k_cache_lp is not None:
+        out += (k_cache_lp, v_cache_lp)
+        if k_scale_lp is not None:
+            out += (k_scale_lp, v_scale_lp)
+    return out
+
+
+def fused_rmsnorm_rope_store_paged_cache(
+    qkv: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    sin_cache: torch.Tensor,
+    cos_cache: torch.Tensor,
+    position_id: torch.Tensor,
+    k_gamma: torch.Tensor,
+    q_gamma: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    k_scale: Optional[torch.Tensor] = None,
+    v_scale: Optional[torch.Tensor] = None,
+    eps: float = 1e-5,
+):
+    """RMSNorm (Q with ``q_gamma`` unless None, K with ``k_gamma``) + RoPE + store of K and V
+    into the paged caches, one kernel; see ``fused_rope`` for the layouts and the quantised
+    cache forms.
+
+    Reference: ``_ops.py:6356-6423``.  Returns ``(qkv, k_cache, v_cache)`` plus
+    ``(k_scale, v_scale)`` when quantising.
+    """
+    torch.ops.torch_mlu_ops.fused_rope(qkv, k_cache, v_cache, None, None,
+        sin_cache, cos_cache, position_id, k_gamma, None, k_scale, v_scale,
+        None, None, None, None, None, None, slot_mapping, None, "rmsnorm", 0, eps, q_gamma)
+    out = (qkv, k_cache, v_cache)
+    if k_scale is not None:
+        out += (k_scale, v_scale)
+    return out
 
 
 def dequant_from_paged_cache(

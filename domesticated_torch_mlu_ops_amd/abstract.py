@@ -43,6 +43,20 @@ def offline_quant_to_paged_cache_abstract(k: Tensor, v: Optional[Tensor],
     return None
 
 
+@torch.library.register_fake("torch_mlu_ops::fused_rope")
+def fused_rope_abstract(qkv: Tensor, key_cache_hp: Tensor, value_cache_hp: Tensor,
+                        key_cache_lp: Optional[Tensor], value_cache_lp: Optional[Tensor],
+                        sin_table: Tensor, cos_table: Tensor, position_ids: Tensor,
+                        gamma: Tensor, k_beta: Optional[Tensor], key_scale_hp: Optional[Tensor],
+                        value_scale_hp: Optional[Tensor], key_scale_lp: Optional[Tensor],
+                        value_scale_lp: Optional[Tensor], cache_bs_id_hp: Optional[Tensor],
+                        cache_seq_offsets_hp: Optional[Tensor], cache_bs_id_lp: Optional[Tensor],
+                        cache_seq_offsets_lp: Optional[Tensor], slot_mapping_hp: Optional[Tensor],
+                        slot_mapping_lp: Optional[Tensor], norm_type: str, rope_dim_offset: int,
+                        eps: float, q_gamma: Optional[Tensor] = None) -> None:
+    return None
+
+
 @torch.library.register_fake("torch_mlu_ops::dequant_from_paged_cache")
 def dequant_from_paged_cache_abstract(key: Tensor, value: Optional[Tensor], key_cache: Tensor,
                                       value_cache: Optional[Tensor],

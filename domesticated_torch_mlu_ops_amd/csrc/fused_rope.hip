@@ -1,0 +1,411 @@
+// fused_rope (norm_type "rmsnorm") into paged caches, for gfx950: one pass over qkv that
+// RMS-normalises Q (optional) and K per head, applies the fold rotary embedding to both, writes
+// Q back into qkv and stores K and V into [num_blocks, kv_heads, block_size, head_size] pages
+// through slot_mapping -- unquantised, or int8 with dynamic per-token or static per-channel
+// scales.
+//
+// Semantics: reference _ops.py:3469-3601 (fused_rope, rmsnorm branch :3504-3509) and
+// _ops.py:6356-6423 (fused_rmsnorm_rope_store_paged_cache); rotary math _ops.py:1116-1127
+// (interleaved False).  Arithmetic is fp32 with one rounding at the end:
+//   ss  = sum of x^2 over 8-element chunks in order, then a balanced tree over the chunk sums
+//   inv = RN(1 / RN(sqrt(RN(RN(ss / D) + eps))));  y = RN(RN(x * inv) * gamma)
+//   out = RN(RN(rot * sin) + RN(y * cos)),  rot = (-y[half:], y[:half]) over the rope window
+// K is quantised (or rounded) from the fp32 result, V from its input values.  A position
+// outside the sin/cos table leaves the row unrotated.
+// Entry point: tmo_hip_fused_rope_paged (include/tmo_hip.h).
+//
+// Vector path: a (token, head) row of D elements is G = D / 8 lanes holding 16 bytes each, so
+// a lane's 8 elements are exactly one chunk of the sum of squares; the chunk tree is the DPP
+// row reduction (its pairings combine adjacent blocks in natural order, and fp32 addition is
+// commutative, so every lane gets the tree's value).  The rotary partner of a lane is
+// lane +- (rope_dim / 2) / 8 inside the group (ds_bpermute).  Rows are numbered token-major
+// (t * (Hq + 2 Hk) + head), which is qkv's memory order, so a workgroup reads contiguous bytes.
+#include <type_traits>
+
+#include "tmo_device.h"
+
+namespace tmo {
+namespace {
+
+struct FusedRopeParams {
+  void* qkv;
+  int64_t tokens;
+  int64_t seq_len;
+  int32_t hq, hk, heads, head_dim;
+  const void* sin_t;
+  const void* cos_t;
+  int64_t table_rows;
+  int64_t table_stride;  // elements
+  int32_t rope_dim, rope_off;
+  const int32_t* position;
+  const void* k_gamma;
+  const void* q_gamma;  // nullable
+  float eps;
+  void* cache[2];
+  float* scale[2];
+  int32_t scale_mode;  // 0 none (caches of qkv's dtype), 1 dynamic per token, 2 static per channel
+  const int32_t* slot;
+  int64_t num_slots;
+  int32_t block_size;
+  int32_t bs_shift;
+};
+
+__device__ __forceinline__ bool page_row_of(const FusedRopeParams& p, int32_t slot, int h,
+                                            int64_t& page_row) {
+  if (slot < 0 || (int64_t)slot >= p.num_slots) return false;
+  int32_t blk, off;
+  if (p.bs_shift >= 0) {
+    blk = slot >> p.bs_shift;
+    off = slot & (p.block_size - 1);
+  } else {
+    blk = slot / p.block_size;
+    off = slot - blk * p.block_size;
+  }
+  page_row = ((int64_t)blk * p.hk + h) * p.block_size + off;
+  return true;
+}
+
+// Sum over aligned groups of G lanes with the same pairings as group_max_u32: adjacent
+// blocks of 1, 2, 4, 8 lanes (DPP inside a row), then 16 and 32 (lane shuffles).
+template <int G>
+__device__ __forceinline__ float group_sum_f32(float v) {
+  auto dppf = [](float x, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value,
+                                                      0xF, 0xF, true));
+  };
+  if constexpr (G >= 2) v = v + dppf(v, std::integral_constant<int, kDppQuadSwap1>{});
+  if constexpr (G >= 4) v = v + dppf(v, std::integral_constant<int, kDppQuadSwap2>{});
+  if constexpr (G >= 8) v = v + dppf(v, std::integral_constant<int, kDppRowHalfMirror>{});
+  if constexpr (G >= 16) v = v + dppf(v, std::integral_constant<int, kDppRowMirror>{});
+  if constexpr (G >= 32) v = v + __shfl_xor(v, 16, 64);
+  if constexpr (G >= 64) v = v + __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// RN(1 / RN(sqrt(RN(RN(ss / D) + eps)))): IEEE division and square root (hipcc's defaults are
+// correctly rounded; tests/native/gfx950_builtins.hip "sqrt" checks the square root).
+__device__ __forceinline__ float rms_inverse(float ss, int d, float eps) {
+  const float mean = ss / (float)d;
+  const float r = __builtin_sqrtf(mean + eps);
+  return 1.0f / r;
+}
+
+template <class Tag>
+__device__ __forceinline__ void pack8(Tag, const float* f, u32x4& w) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = pack2(Tag{}, f[2 * i], f[2 * i + 1]);
+}
+
+// Vector path: head_dim = 8 * G (G a power of two <= 64), rope window on 8-element chunks.
+template <class Tag, int G>
+__global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
+  constexpr int kRows = 256 / G;
+  const int lane = threadIdx.x & (G - 1);
+  const int64_t row = (int64_t)blockIdx.x * kRows + threadIdx.x / G;
+  const int64_t nrows = p.tokens * p.heads;
+  // a group past the last row still runs the shuffles below (with its own lanes only) and
+  // returns before any store
+  const bool live = row < nrows;
+  const int64_t t = live ? row / p.heads : 0;
+  const int hh = live ? (int)(row - t * p.heads) : 0;
+  const int kind = hh < p.hq ? 0 : (hh < p.hq + p.hk ? 1 : 2);  // q, k, v
+  char* xrow = static_cast<char*>(p.qkv) + (row * p.head_dim + lane * 8) * Tag::kBytes;
+
+  // ---- loads: x, then (q/k) gamma and the sin/cos of this lane's window chunk, slot
+  u32x4 xw = {0u, 0u, 0u, 0u}, gw = {0u, 0u, 0u, 0u}, sw = {0u, 0u, 0u, 0u}, cw = {0u, 0u, 0u, 0u};
+  int32_t slot = -1;
+  const int c0 = p.rope_off / 8, nwin = p.rope_dim / 8;  // window in chunks
+  const bool in_win = lane >= c0 && lane < c0 + nwin;
+  int64_t pos = -1;
+  const void* gamma = kind == 0 ? p.q_gamma : p.k_gamma;
+  if (live) {
+    xw = *reinterpret_cast<const u32x4*>(xrow);
+    if (kind != 0) slot = p.slot[t];
+    if (kind != 2) {
+      const int64_t b = t / p.seq_len;
+      pos = (int64_t)p.position[b] + (t - b * p.seq_len);
+      if (gamma) gw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(gamma) + lane * 16);
+      if (pos >= 0 && pos < p.table_rows && in_win) {
+        const int64_t e = pos * p.table_stride + (lane - c0) * 8;
+        sw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.sin_t) + e * Tag::kBytes);
+        cw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.cos_t) + e * Tag::kBytes);
+      }
+    }
+  }
+  float x[8];
+  unpack(Tag{}, xw, x);
+
+  // ---- q / k: rmsnorm, rope
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = x[e];
+  if (kind != 2 && (kind == 1 || p.q_gamma)) {
+    float acc = x[0] * x[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) {
+      const float sq = x[e] * x[e];
+      acc = acc + sq;
+    }
+    const float inv = rms_inverse(group_sum_f32<G>(acc), p.head_dim, p.eps);
+    float g[8];
+    unpack(Tag{}, gw, g);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float n = x[e] * inv;
+      y[e] = n * g[e];
+    }
+  }
+  const bool rotate = kind != 2 && pos >= 0 && pos < p.table_rows;  // group-uniform
+  if (kind != 2) {
+    // partner chunk: +half in the first half of the window, -half in the second
+    const int hc = nwin / 2;
+    const int base = (threadIdx.x & (kWave - 1)) & ~(G - 1);  // the group's first lane
+    const int src = in_win ? (lane < c0 + hc ? lane + hc : lane - hc) : lane;
+    float partner[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) partner[e] = __shfl(y[e], base + src, 64);
+    if (rotate && in_win) {
+      float sn[8], cs[8];
+      unpack(Tag{}, sw, sn);
+      unpack(Tag{}, cw, cs);
+      const bool first = lane < c0 + hc;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float rot = first ? -partner[e] : partner[e];
+        const float a = rot * sn[e];
+        const float b = y[e] * cs[e];
+        y[e] = a + b;
+      }
+    }
+  }
+  if (!live) return;
+  if (kind == 0) {
+    u32x4 o;
+    pack8(Tag{}, y, o);
+    *reinterpret_cast<u32x4*>(xrow) = o;
+    return;
+  }
+
+  // ---- k / v: store into the page
+  const int h = kind == 1 ? hh - p.hq : hh - p.hq - p.hk;
+  const int kv = kind - 1;
+  int64_t page_row;
+  if (!page_row_of(p, slot, h, page_row)) return;  // group-uniform
+  if (p.scale_mode == 0) {
+    u32x4 o;
+    pack8(Tag{}, y, o);
+    *reinterpret_cast<u32x4*>(static_cast<char*>(p.cache[kv]) +
+                              (page_row * p.head_dim + lane * 8) * Tag::kBytes) = o;
+    return;
+  }
+  uint32_t c[2];
+  if (p.scale_mode == 1) {
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m = abs_max(m, y[e]);
+    const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<G>(__float_as_uint(m))));
+    encode_row<8>(y, rs, c);
+    if (lane == 0) p.scale[kv][page_row] = rs.s;
+  } else {
+    const float* sp = p.scale[kv] + (int64_t)h * p.head_dim + lane * 8;
+    float s[8], yr[8], q[8];
+    bool fast = true;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s[e] = sp[e];
+      fast &= static_scale_fast(s[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) yr[e] = fast ? recip_rn(s[e]) : 0.0f;
+    static_quotients<8>(y, s, yr, fast, q);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      c[i] = pack_codes(code_bits(q[4 * i]), code_bits(q[4 * i + 1]), code_bits(q[4 * i + 2]),
+                        code_bits(q[4 * i + 3]));
+  }
+  u32x2 c2;
+  c2[0] = c[0];
+  c2[1] = c[1];
+  *reinterpret_cast<u32x2*>(static_cast<int8_t*>(p.cache[kv]) + page_row * p.head_dim + lane * 8) = c2;
+}
+
+// Generic path (any head_dim <= 512, any even rope window): one wavefront per row, the row
+// staged in LDS as fp32 (all reads of the row finish before Q is written back in place).
+template <class Tag>
+__global__ __launch_bounds__(256) void fused_rope_generic(FusedRopeParams p) {
+  __shared__ float stage[4][512];
+  __shared__ float normed[4][512];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  // every wave reaches both barriers; a wave past the last row only skips the work
+  const bool active = row < p.tokens * p.heads;
+  const int64_t t = active ? row / p.heads : 0;
+  const int hh = active ? (int)(row - t * p.heads) : 0;
+  const int kind = hh < p.hq ? 0 : (hh < p.hq + p.hk ? 1 : 2);
+  const int D = p.head_dim;
+  float* xs = stage[wave];
+  float* ys = normed[wave];
+  const int64_t base = row * D;
+  if (active)
+    for (int d = lane; d < D; d += kWave) xs[d] = load1(Tag{}, p.qkv, base + d);
+  __syncthreads();
+  const void* gamma = kind == 0 ? p.q_gamma : p.k_gamma;
+  const bool norm = kind == 1 || (kind == 0 && p.q_gamma);
+  if (active) {
+    float inv = 1.0f;
+    if (kind != 2 && norm) {
+      // chunk `lane` of the sum of squares, then the 64-lane tree (zeros past the last chunk)
+      float acc = 0.0f;
+      const int e0 = lane * 8;
+      if (e0 < D) {
+        acc = xs[e0] * xs[e0];
+        for (int e = e0 + 1; e < e0 + 8 && e < D; ++e) {
+          const float sq = xs[e] * xs[e];
+          acc = acc + sq;
+        }
+      }
+      inv = rms_inverse(group_sum_f32<kWave>(acc), D, p.eps);
+    }
+    for (int d = lane; d < D; d += kWave) {
+      float v = xs[d];
+      if (kind != 2 && norm) {
+        const float n = v * inv;
+        v = n * load1(Tag{}, gamma, d);
+      }
+      ys[d] = v;
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+  int64_t pos = -1;
+  if (kind != 2) {
+    const int64_t b = t / p.seq_len;
+    pos = (int64_t)p.position[b] + (t - b * p.seq_len);
+  }
+  const bool rotate = kind != 2 && pos >= 0 && pos < p.table_rows;
+  const int half = p.rope_dim / 2;
+  auto out_at = [&](int d) -> float {
+    const float yv = ys[d];
+    if (!rotate || d < p.rope_off || d >= p.rope_off + p.rope_dim) return yv;
+    const int j = d - p.rope_off;
+    const float rot = j < half ? -ys[d + half] : ys[d - half];
+    const float sn = load1(Tag{}, p.sin_t, pos * p.table_stride + j);
+    const float cs = load1(Tag{}, p.cos_t, pos * p.table_stride + j);
+    const float a = rot * sn;
+    const float b = yv * cs;
+    return a + b;
+  };
+  if (kind == 0) {
+    for (int d = lane; d < D; d += kWave) store1(Tag{}, p.qkv, base + d, out_at(d));
+    return;
+  }
+  const int h = kind == 1 ? hh - p.hq : hh - p.hq - p.hk;
+  const int kv = kind - 1;
+  int64_t page_row;
+  if (!page_row_of(p, p.slot[t], h, page_row)) return;
+  if (p.scale_mode == 0) {
+    for (int d = lane; d < D; d += kWave) store1(Tag{}, p.cache[kv], page_row * D + d, out_at(d));
+    return;
+  }
+  int8_t* dst = static_cast<int8_t*>(p.cache[kv]) + page_row * D;
+  if (p.scale_mode == 1) {
+    float m = 0.0f;
+    for (int d = lane; d < D; d += kWave) m = abs_max(m, out_at(d));
+    const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<kWave>(__float_as_uint(m))));
+    for (int d = lane; d < D; d += kWave) dst[d] = encode1(out_at(d), rs);
+    if (lane == 0) p.scale[kv][page_row] = rs.s;
+  } else {
+    for (int d = lane; d < D; d += kWave) {
+      const float q = out_at(d) / p.scale[kv][(int64_t)h * D + d];  // IEEE divide
+      dst[d] = (int8_t)(uint8_t)(code_bits(q) & 0xffu);
+    }
+  }
+}
+
+template <class Tag>
+int launch(const FusedRopeParams& p, hipStream_t stream) {
+  const int D = p.head_dim;
+  const int G = D / 8;
+  auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+  bool vec = D % 8 == 0 && G >= 1 && G <= kWave && (G & (G - 1)) == 0 &&
+             p.rope_off % 8 == 0 && p.rope_dim % 16 == 0 && al16(p.qkv) && al16(p.k_gamma) &&
+             (!p.q_gamma || al16(p.q_gamma)) && al16(p.sin_t) && al16(p.cos_t) &&
+             (p.table_stride * Tag::kBytes) % 16 == 0 && al16(p.cache[0]) && al16(p.cache[1]) &&
+             (p.scale_mode != 2 || (al16(p.scale[0]) && al16(p.scale[1])));
+  const int64_t nrows = p.tokens * p.heads;
+  const int rows = vec ? 256 / G : 4;
+  const int64_t blocks = (nrows + rows - 1) / rows;
+  if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
+  const dim3 grid((unsigned)blocks), block(256);
+  if (!vec) return launch_kernel(fused_rope_generic<Tag>, grid, block, stream, p);
+  switch (G) {
+    case 1: return launch_kernel(fused_rope_vec<Tag, 1>, grid, block, stream, p);
+    case 2: return launch_kernel(fused_rope_vec<Tag, 2>, grid, block, stream, p);
+    case 4: return launch_kernel(fused_rope_vec<Tag, 4>, grid, block, stream, p);
+    case 8: return launch_kernel(fused_rope_vec<Tag, 8>, grid, block, stream, p);
+    case 16: return launch_kernel(fused_rope_vec<Tag, 16>, grid, block, stream, p);
+    case 32: return launch_kernel(fused_rope_vec<Tag, 32>, grid, block, stream, p);
+    default: return launch_kernel(fused_rope_vec<Tag, 64>, grid, block, stream, p);
+  }
+}
+
+}  // namespace
+}  // namespace tmo
+
+extern "C" int tmo_hip_fused_rope_paged(
+    void* qkv, int64_t num_tokens, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
+    int64_t head_size, const void* sin_table, const void* cos_table, int64_t table_rows,
+    int64_t table_stride, int64_t rope_dim, int64_t rope_offset, const int32_t* position_ids,
+    int64_t batch, const void* k_gamma, const void* q_gamma, float eps, void* k_cache,
+    void* v_cache, float* k_scale, float* v_scale, int scale_mode,
+    const int32_t* slot_mapping, int64_t num_blocks, int64_t block_size, int dtype,
+    void* stream) {
+  using namespace tmo;
+  if (dtype != TMO_DTYPE_F16 && dtype != TMO_DTYPE_BF16) return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (scale_mode < 0 || scale_mode > 2) return TMO_ERR_UNSUPPORTED_MODE;
+  if (!qkv || !sin_table || !cos_table || !position_ids || !k_gamma || !k_cache || !v_cache ||
+      !slot_mapping)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (scale_mode != 0 && (!k_scale || !v_scale)) return TMO_ERR_INVALID_ARGUMENT;
+  if (num_tokens < 0 || seq_len <= 0 || q_heads < 0 || kv_heads <= 0 || head_size <= 0 ||
+      head_size > 512 || num_blocks < 0 || block_size <= 0 || batch < 0 || table_rows < 0 ||
+      table_stride < rope_dim)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (rope_dim < 0 || rope_dim % 2 != 0 || rope_offset < 0 || rope_offset + rope_dim > head_size)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (num_tokens > batch * seq_len) return TMO_ERR_INVALID_ARGUMENT;  // position_ids[t / seq_len]
+  if (q_heads + 2 * kv_heads > 0x7fffffffLL || block_size > 0x7fffffffLL)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (num_tokens == 0) return TMO_OK;
+
+  FusedRopeParams p{};
+  p.qkv = qkv;
+  p.tokens = num_tokens;
+  p.seq_len = seq_len;
+  p.hq = (int32_t)q_heads;
+  p.hk = (int32_t)kv_heads;
+  p.heads = (int32_t)(q_heads + 2 * kv_heads);
+  p.head_dim = (int32_t)head_size;
+  p.sin_t = sin_table;
+  p.cos_t = cos_table;
+  p.table_rows = table_rows;
+  p.table_stride = table_stride;
+  p.rope_dim = (int32_t)rope_dim;
+  p.rope_off = (int32_t)rope_offset;
+  p.position = position_ids;
+  p.k_gamma = k_gamma;
+  p.q_gamma = q_gamma;
+  p.eps = eps;
+  p.cache[0] = k_cache;
+  p.cache[1] = v_cache;
+  p.scale[0] = k_scale;
+  p.scale[1] = v_scale;
+  p.scale_mode = scale_mode;
+  p.slot = slot_mapping;
+  p.num_slots = num_blocks * block_size;
+  p.block_size = (int32_t)block_size;
+  p.bs_shift = ilog2_if_pow2(block_size);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == TMO_DTYPE_F16 ? launch<F16>(p, s) : launch<BF16>(p, s);
+}

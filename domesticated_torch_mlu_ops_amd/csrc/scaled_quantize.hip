@@ -100,7 +100,8 @@ __global__ __launch_bounds__(256) void sq_vec(SqParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int part = wave % kWPR;
   const int64_t orow = (int64_t)blockIdx.x * kRowsPerWG + wave / kWPR;
-  const int64_t r = orow / p.inner;
+  // 2-D inputs (inner == 1, the common case) skip the 64-bit division
+  const int64_t r = p.inner == 1 ? orow : orow / p.inner;
   const int64_t jn = orow - r * p.inner;
   int64_t src = 0, g = 0;
   const bool valid = orow < p.total_rows && locate_row(p, r, src, g);  // wave-uniform
@@ -180,13 +181,13 @@ __global__ __launch_bounds__(256) void sq_vec(SqParams p) {
   if (lane == 0 && part == 0) p.out_scale[orow] = rs.s;
 }
 
-// Dense rows (no gather, no groups) of exactly 64 * kV 16-byte vectors, with no smooth or a
-// scalar one (kScalar): output row r reads input row r (r = s * inner + j), so the row
-// address needs no division and every lane loads exactly kV vectors with no bounds checks.
-// configs[3]'s shape: 19.2 us without smooth vs 20.6 us through sq_vec.  A per-channel smooth
-// vector stays on sq_vec: delivering its 4 bytes per element from L1 or LDS made this
-// kernel slower than sq_vec there (21.0-21.2 us vs 20.5 us).
-template <class Tag, int kV, bool kScalar>
+// Dense rows (no gather, no groups) of exactly 64 * kV 16-byte vectors: output row r reads
+// input row r (r = s * inner + j), so the row address needs no division, every lane loads
+// exactly kV vectors with no bounds checks, and the smooth mode is fixed at compile time
+// (kScalar: one smooth value; kChan: a per-channel vector, loaded beside the row vectors it
+// scales).  configs[3]'s shape: 19.3 us with no or a scalar smooth, 20.8 us per channel (the
+// per-channel vector's 4 bytes per element come from L1; staging it in LDS measured slower).
+template <class Tag, int kV, bool kScalar, bool kChan>
 __global__ __launch_bounds__(256) void sq_dense(SqParams p) {
   constexpr int kPer = Tag::kPerVec;
   const int lane = threadIdx.x & (kWave - 1);
@@ -194,9 +195,20 @@ __global__ __launch_bounds__(256) void sq_dense(SqParams p) {
   if (row >= p.dense_rows) return;
   const char* xrow = static_cast<const char*>(p.x) + row * p.row_stride * Tag::kBytes + lane * 16;
   u32x4 w[kV];
+  u32x4 sv[kV][kPer / 4];
+  const u32x4* sp = reinterpret_cast<const u32x4*>(p.smooth) + lane * (kPer / 4);
 #pragma unroll
-  for (int i = 0; i < kV; ++i)
+  for (int i = 0; i < kV; ++i) {
     w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xrow + i * kWave * 16));
+    if constexpr (kChan) {
+#pragma unroll
+      for (int q = 0; q < kPer / 4; ++q) sv[i][q] = sp[i * kWave * (kPer / 4) + q];
+    }
+  }
+  // Keep every load of the row ahead of the first use: without this barrier the scheduler
+  // moved the unpack of the first vector (and its wait) between the loads, so the second half
+  // of the row was requested only after the first vector had arrived.
+  __builtin_amdgcn_sched_barrier(0);
   const float s_scalar = kScalar ? p.smooth[0] : 1.0f;
   float v[kV][kPer];
   float m = 0.0f;
@@ -205,7 +217,9 @@ __global__ __launch_bounds__(256) void sq_dense(SqParams p) {
     unpack(Tag{}, w[i], v[i]);
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-      if constexpr (kScalar) v[i][e] = v[i][e] * s_scalar;  // RN(x * smooth), no FMA
+      // RN(x * smooth), no FMA
+      if constexpr (kScalar) v[i][e] = v[i][e] * s_scalar;
+      if constexpr (kChan) v[i][e] = v[i][e] * __uint_as_float(sv[i][e / 4][e % 4]);
       m = abs_max(m, v[i][e]);
     }
   }
@@ -232,8 +246,10 @@ int launch_dense(const SqParams& p, hipStream_t stream) {
   const int64_t blocks = (p.dense_rows + 3) / 4;
   if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
   const dim3 grid((unsigned)blocks), block(256);
-  if (p.smooth) return launch_kernel(sq_dense<Tag, kV, true>, grid, block, stream, p);
-  return launch_kernel(sq_dense<Tag, kV, false>, grid, block, stream, p);
+  if (p.smooth && p.smooth_len != 1)
+    return launch_kernel(sq_dense<Tag, kV, false, true>, grid, block, stream, p);
+  if (p.smooth) return launch_kernel(sq_dense<Tag, kV, true, false>, grid, block, stream, p);
+  return launch_kernel(sq_dense<Tag, kV, false, false>, grid, block, stream, p);
 }
 
 // Generic path: any channel count / alignment; one wavefront per row, two passes.
@@ -300,7 +316,7 @@ int launch(const SqParams& p, hipStream_t stream) {
     if (p.gather_index) return launch_vec<Tag, false, kW>(p, per_lane, stream);
     return launch_vec<Tag, true, kW>(p, per_lane, stream);
   }
-  if (!p.gather_index && !p.token_count && (!p.smooth || p.smooth_len == 1) && nvec % kWave == 0) {
+  if (!p.gather_index && !p.token_count && nvec % kWave == 0) {
     switch (nvec / kWave) {
       case 1: return launch_dense<Tag, 1>(p, stream);
       case 2: return launch_dense<Tag, 2>(p, stream);

@@ -221,6 +221,121 @@ void offline_quant_to_paged_cache(const torch::Tensor& k, const c10::optional<to
   check_status(st, "offline_quant_to_paged_cache");
 }
 
+void fused_rope(at::Tensor& qkv, at::Tensor& key_cache_hp, at::Tensor& value_cache_hp,
+                const c10::optional<at::Tensor>& key_cache_lp,
+                const c10::optional<at::Tensor>& value_cache_lp, const at::Tensor& sin_table,
+                const at::Tensor& cos_table, const at::Tensor& position_ids,
+                const at::Tensor& gamma, const c10::optional<at::Tensor>& k_beta,
+                const c10::optional<at::Tensor>& key_scale_hp,
+                const c10::optional<at::Tensor>& value_scale_hp,
+                const c10::optional<at::Tensor>& key_scale_lp,
+                const c10::optional<at::Tensor>& value_scale_lp,
+                const c10::optional<at::Tensor>& cache_bs_id_hp,
+                const c10::optional<at::Tensor>& cache_seq_offsets_hp,
+                const c10::optional<at::Tensor>& cache_bs_id_lp,
+                const c10::optional<at::Tensor>& cache_seq_offsets_lp,
+                const c10::optional<at::Tensor>& slot_mapping_hp,
+                const c10::optional<at::Tensor>& slot_mapping_lp, const std::string& norm_type,
+                c10::SymInt rope_dim_offset, const double eps,
+                const c10::optional<at::Tensor>& q_gamma) {
+  TORCH_CHECK(norm_type == "rmsnorm",
+              "fused_rope: this build implements norm_type \"rmsnorm\", got \"", norm_type, "\"");
+  TORCH_CHECK(!key_cache_lp && !value_cache_lp && !key_scale_lp && !value_scale_lp &&
+                  !slot_mapping_lp && !cache_bs_id_lp && !cache_seq_offsets_lp,
+              "fused_rope: low-precision (int4) caches are not supported by this build");
+  TORCH_CHECK(!cache_bs_id_hp && !cache_seq_offsets_hp,
+              "fused_rope: linear caches (cache_bs_id / cache_seq_offsets) are not supported by "
+              "this build; pass slot_mapping_hp for paged caches");
+  TORCH_CHECK(slot_mapping_hp.has_value(), "fused_rope: slot_mapping_hp is required");
+  TORCH_CHECK(!k_beta.has_value(), "fused_rope: k_beta applies to layernorm only");
+  check_device(qkv, qkv, "qkv");
+  TORCH_CHECK(qkv.dim() == 4 && qkv.is_contiguous(),
+              "qkv must be a contiguous [batch, seq_len, heads, head_size] tensor, got ",
+              qkv.sizes());
+  const int dt = dtype_code(qkv.scalar_type());
+  TORCH_CHECK(dt == TMO_DTYPE_F16 || dt == TMO_DTYPE_BF16,
+              "fused_rope: qkv must be half or bfloat16, got ", qkv.scalar_type());
+  const int64_t B = qkv.size(0), S = qkv.size(1), H = qkv.size(2), D = qkv.size(3);
+  check_cache(key_cache_hp, "key_cache_hp");
+  check_cache(value_cache_hp, "value_cache_hp");
+  check_device(key_cache_hp, qkv, "key_cache_hp");
+  check_device(value_cache_hp, qkv, "value_cache_hp");
+  const int64_t NB = key_cache_hp.size(0), Hk = key_cache_hp.size(1), BS = key_cache_hp.size(2);
+  TORCH_CHECK(key_cache_hp.size(3) == D && value_cache_hp.sizes() == key_cache_hp.sizes() &&
+                  value_cache_hp.scalar_type() == key_cache_hp.scalar_type(),
+              "key/value caches must be [num_blocks, kv_heads, block_size, head_size] alike");
+  TORCH_CHECK(H > 2 * Hk, "qkv has ", H, " heads, fewer than 2 * kv_heads + 1");
+  const int64_t Hq = H - 2 * Hk;
+  int mode = 0;
+  float* ks = nullptr;
+  float* vs = nullptr;
+  if (key_scale_hp.has_value() || value_scale_hp.has_value()) {
+    TORCH_CHECK(key_scale_hp.has_value() && value_scale_hp.has_value(),
+                "key_scale and value_scale must both be given or both be None");
+    TORCH_CHECK(key_cache_hp.scalar_type() == at::kChar,
+                "fused_rope: quantised caches must be int8, got ", key_cache_hp.scalar_type());
+    for (const at::Tensor* sc : {&*key_scale_hp, &*value_scale_hp}) {
+      check_device(*sc, qkv, "scale");
+      TORCH_CHECK(sc->scalar_type() == at::kFloat && sc->is_contiguous(),
+                  "fused_rope: scales must be contiguous float32");
+    }
+    if (key_scale_hp->dim() == 3) {
+      mode = 1;  // dynamic per (token, head): written
+      TORCH_CHECK(key_scale_hp->size(0) == NB && key_scale_hp->size(1) == Hk &&
+                      key_scale_hp->size(2) == BS &&
+                      value_scale_hp->sizes() == key_scale_hp->sizes(),
+                  "dynamic scales must be [num_blocks, kv_heads, block_size]");
+    } else {
+      mode = 2;  // static per channel: read
+      TORCH_CHECK(key_scale_hp->dim() == 2 && key_scale_hp->size(0) == Hk &&
+                      key_scale_hp->size(1) == D && value_scale_hp->sizes() == key_scale_hp->sizes(),
+                  "static scales must be [kv_heads, head_size]");
+    }
+    ks = key_scale_hp->data_ptr<float>();
+    vs = value_scale_hp->data_ptr<float>();
+  } else {
+    TORCH_CHECK(key_cache_hp.scalar_type() == qkv.scalar_type(),
+                "fused_rope: unquantised caches must have qkv's dtype");
+  }
+  for (const at::Tensor* tb : {&sin_table, &cos_table}) {
+    check_device(*tb, qkv, "sin/cos table");
+    TORCH_CHECK(tb->dim() == 2 && tb->scalar_type() == qkv.scalar_type() &&
+                    (tb->size(1) <= 1 || tb->stride(1) == 1),
+                "sin/cos tables must be [rotary_seq, rope_dim] of qkv's dtype, last dim contiguous");
+  }
+  TORCH_CHECK(sin_table.sizes() == cos_table.sizes() && sin_table.stride(0) == cos_table.stride(0),
+              "sin and cos tables must have the same shape and row stride");
+  const int64_t rope_dim = sin_table.size(1);
+  const int64_t off = rope_dim_offset.expect_int();
+  TORCH_CHECK(rope_dim % 2 == 0 && off >= 0 && off + rope_dim <= D,
+              "rope_dim (", rope_dim, ") must be even and rope_dim + rope_dim_offset <= head_size");
+  check_device(position_ids, qkv, "position_ids");
+  TORCH_CHECK(position_ids.scalar_type() == at::kInt && position_ids.dim() == 1 &&
+                  position_ids.size(0) == B && position_ids.is_contiguous(),
+              "position_ids must be a contiguous int32 [batch] tensor");
+  for (const at::Tensor* g : {&gamma, q_gamma ? &*q_gamma : nullptr}) {
+    if (!g) continue;
+    check_device(*g, qkv, "gamma");
+    TORCH_CHECK(g->dim() == 1 && g->size(0) == D && g->scalar_type() == qkv.scalar_type() &&
+                    g->is_contiguous(),
+                "gammas must be contiguous [head_size] tensors of qkv's dtype");
+  }
+  const at::Tensor& slot = *slot_mapping_hp;
+  check_device(slot, qkv, "slot_mapping");
+  TORCH_CHECK(slot.scalar_type() == at::kInt && slot.numel() == B * S && slot.is_contiguous(),
+              "slot_mapping must be a contiguous int32 tensor of batch * seq_len entries");
+  TORCH_CHECK(D <= 512, "fused_rope: head_size must be <= 512");
+  if (B * S == 0) return;
+  c10::DeviceGuard guard(qkv.device());
+  const int st = tmo_hip_fused_rope_paged(
+      qkv.data_ptr(), B * S, S, Hq, Hk, D, sin_table.data_ptr(), cos_table.data_ptr(),
+      sin_table.size(0), sin_table.stride(0), rope_dim, off, position_ids.data_ptr<int32_t>(), B,
+      gamma.data_ptr(), q_gamma ? q_gamma->data_ptr() : nullptr, static_cast<float>(eps),
+      key_cache_hp.data_ptr(), value_cache_hp.data_ptr(), ks, vs, mode,
+      slot.data_ptr<int32_t>(), NB, BS, dt, stream_of(qkv));
+  check_status(st, "fused_rope");
+}
+
 void dequant_from_paged_cache(at::Tensor& key, const c10::optional<at::Tensor>& value,
                               const at::Tensor& key_cache,
                               const c10::optional<at::Tensor>& value_cache,
@@ -436,6 +551,14 @@ TORCH_LIBRARY(torch_mlu_ops, m) {
       "Tensor? v_cache_scale_per_channel, Tensor slot_mapping, Tensor(a!) k_cache, "
       "Tensor(b!)? v_cache, float k_cache_scale_per_tensor, float v_cache_scale_per_tensor) -> ()");
   m.def(
+      "fused_rope(Tensor(a!) qkv, Tensor(b!) key_cache_hp, Tensor(c!) value_cache_hp, "
+      "Tensor(d!)? key_cache_lp, Tensor(e!)? value_cache_lp, Tensor sin_table, Tensor cos_table, "
+      "Tensor position_ids, Tensor gamma, Tensor? k_beta, Tensor(f!)? key_scale_hp, "
+      "Tensor(g!)? value_scale_hp, Tensor(h!)? key_scale_lp, Tensor(i!)? value_scale_lp, "
+      "Tensor? cache_bs_id_hp, Tensor? cache_seq_offsets_hp, Tensor? cache_bs_id_lp, "
+      "Tensor? cache_seq_offsets_lp, Tensor? slot_mapping_hp, Tensor? slot_mapping_lp, "
+      "str norm_type, SymInt rope_dim_offset, float eps, Tensor? q_gamma=None) -> ()");
+  m.def(
       "dequant_from_paged_cache(Tensor(a!) key, Tensor(b!)? value, Tensor key_cache, "
       "Tensor? value_cache, Tensor key_cache_quant_scale, Tensor? value_cache_quant_scale, "
       "Tensor context_lengths, SymInt max_context_len, Tensor? context_seq_offset, "
@@ -453,5 +576,6 @@ TORCH_LIBRARY_IMPL(torch_mlu_ops, CUDA, m) {
   m.impl("quant_to_paged_cache", &tmo::torch_api::quant_to_paged_cache);
   m.impl("offline_quant_to_paged_cache", &tmo::torch_api::offline_quant_to_paged_cache);
   m.impl("dequant_from_paged_cache", &tmo::torch_api::dequant_from_paged_cache);
+  m.impl("fused_rope", &tmo::torch_api::fused_rope);
   m.impl("scaled_quantize", &tmo::torch_api::scaled_quantize);
 }

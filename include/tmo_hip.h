@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 2
+#define TMO_HIP_ABI_VERSION 3
 
 /* element types */
 enum tmo_dtype {
@@ -118,6 +118,36 @@ int tmo_hip_offline_quant_to_paged_cache(const void* k, const void* v,
                                          int64_t num_tokens, int64_t num_heads, int64_t head_size,
                                          int64_t num_blocks, int64_t block_size,
                                          int dtype, int cache_dtype, void* stream);
+
+/*
+ * fused_rope_paged -- one pass over qkv [num_tokens, q_heads + 2 kv_heads, head_size]
+ * (contiguous, token t = b * seq_len + s at rotary position position_ids[b] + s): RMS-normalise
+ * Q (when q_gamma is set) and K per head with eps and gamma [head_size], apply the fold rotary
+ * embedding over [rope_offset, rope_offset + rope_dim) with rows of sin_table / cos_table
+ * [table_rows, table_stride] (a position outside the table leaves the row unrotated), write Q
+ * back into qkv, and store K and V rows at slot_mapping into [num_blocks, kv_heads, block_size,
+ * head_size] pages: scale_mode 0 stores them in qkv's dtype; 1 quantises to int8 with a
+ * dynamic per-(token, head) scale written to k_scale / v_scale [num_blocks, kv_heads,
+ * block_size]; 2 quantises to int8 with static per-channel scales read from [kv_heads,
+ * head_size].  fp32 arithmetic, one final rounding; the sum of squares is taken over
+ * 8-element chunks in order, then a balanced tree over the chunks; 1/rms = RN(1 / RN(sqrt(
+ * RN(RN(ss / head_size) + eps)))).
+ * Replaces tmo::torch_api::fused_rope (reference include/torch_mlu_ops.h:562-585) with
+ * norm_type "rmsnorm" and paged high-precision caches, called by torch_mlu_ops.fused_rope
+ * (reference _ops.py:3469-3601) and torch_mlu_ops.fused_rmsnorm_rope_store_paged_cache
+ * (reference _ops.py:6356-6423).
+ * dtype: F16 or BF16 (qkv, tables, gammas); head_size <= 512; num_tokens <= batch * seq_len.
+ */
+int tmo_hip_fused_rope_paged(void* qkv, int64_t num_tokens, int64_t seq_len,
+                             int64_t q_heads, int64_t kv_heads, int64_t head_size,
+                             const void* sin_table, const void* cos_table,
+                             int64_t table_rows, int64_t table_stride,
+                             int64_t rope_dim, int64_t rope_offset,
+                             const int32_t* position_ids, int64_t batch,
+                             const void* k_gamma, const void* q_gamma, float eps,
+                             void* k_cache, void* v_cache, float* k_scale, float* v_scale,
+                             int scale_mode, const int32_t* slot_mapping,
+                             int64_t num_blocks, int64_t block_size, int dtype, void* stream);
 
 /*
  * dequant_from_paged_cache -- gathers each sequence's pages through block_tables and writes

@@ -49,6 +49,33 @@ void offline_quant_to_paged_cache(const torch::Tensor &k,
                                   double k_cache_scale_per_tensor,
                                   double v_cache_scale_per_tensor);
 
+/* reference include/torch_mlu_ops.h:562-585 (norm_type "rmsnorm", paged high-precision
+ * caches: unquantised, or int8 with dynamic per-token / static per-channel scales) */
+void fused_rope(at::Tensor &qkv,
+                at::Tensor &key_cache_hp,
+                at::Tensor &value_cache_hp,
+                const c10::optional<at::Tensor> &key_cache_lp,
+                const c10::optional<at::Tensor> &value_cache_lp,
+                const at::Tensor &sin_table,
+                const at::Tensor &cos_table,
+                const at::Tensor &position_ids,
+                const at::Tensor &gamma,
+                const c10::optional<at::Tensor> &k_beta,
+                const c10::optional<at::Tensor> &key_scale_hp,
+                const c10::optional<at::Tensor> &value_scale_hp,
+                const c10::optional<at::Tensor> &key_scale_lp,
+                const c10::optional<at::Tensor> &value_scale_lp,
+                const c10::optional<at::Tensor> &cache_bs_id_hp,
+                const c10::optional<at::Tensor> &cache_seq_offsets_hp,
+                const c10::optional<at::Tensor> &cache_bs_id_lp,
+                const c10::optional<at::Tensor> &cache_seq_offsets_lp,
+                const c10::optional<at::Tensor> &slot_mapping_hp,
+                const c10::optional<at::Tensor> &slot_mapping_lp,
+                const std::string &norm_type,
+                c10::SymInt rope_dim_offset,
+                const double eps,
+                const c10::optional<at::Tensor> &q_gamma = c10::nullopt);
+
 /* reference include/torch_mlu_ops.h:334-350 (int8 "dynamic_per_token", act_mode "none") */
 void scaled_quantize(const at::Tensor &x,
                      const at::Tensor &output,

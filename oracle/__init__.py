@@ -51,6 +51,10 @@ def lib() -> ctypes.CDLL:
         L.oracle_scaled_quantize_per_token.argtypes = [c_void_p, c_int] + [c_int64] * 4 + \
             [c_void_p] * 3 + [c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                               c_int]
+        L.oracle_fused_rope_paged.argtypes = [c_void_p, c_int] + [c_int64] * 5 + \
+            [c_void_p, c_void_p] + [c_int64] * 4 + [c_void_p] * 3 + [c_float] + [c_void_p] * 4 + \
+            [c_int, c_void_p, c_int64, c_int64, c_int]
+        L.oracle_fused_rope_paged.restype = c_int
         L.oracle_offline_quant_to_paged_cache.argtypes = [c_void_p, c_void_p, c_int] + \
             [c_int64] * 4 + [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_float, c_float,
                              c_void_p] + [c_int64] * 5 + [c_int]
@@ -123,6 +127,37 @@ def offline_quant_to_paged_cache(k, v, k_cache_scale, v_cache_scale, slot_mappin
         _ptr(k_cache), _ptr(v_cache), cdt, _ptr(kch), _ptr(vch), kt, vt,
         _ptr(slots), T, H, D, NB, BS, nthreads or default_threads())
     _check(rc, "offline_quant_to_paged_cache")
+
+
+def fused_rope_paged(qkv, k_cache, v_cache, sin_cache, cos_cache, position_id, k_gamma, k_scale,
+                     v_scale, slot_mapping, eps: float = 1e-5, q_gamma=None, rope_dim_offset: int = 0,
+                     nthreads: Optional[int] = None) -> None:
+    """reference _ops.py:3469-3601 (fused_rope, norm_type "rmsnorm", paged hp caches) under
+    decision D10 of tmo_oracle.c; in place on CPU tensors (q back into qkv, K/V into the pages).
+    qkv [B, S, Hq + 2 Hk, D] (or [T, Hq + 2 Hk, D] with S = T); caches [NB, Hk, BS, D] of qkv's
+    dtype (no scales) or int8 with k_scale/v_scale [NB, Hk, BS] (dynamic, written) or [Hk, D]
+    (static, read)."""
+    assert qkv.is_contiguous() and k_cache.is_contiguous() and v_cache.is_contiguous()
+    S = qkv.shape[1] if qkv.dim() == 4 else qkv.shape[0]
+    T = qkv.shape[0] * S if qkv.dim() == 4 else qkv.shape[0]
+    H, D = qkv.shape[-2], qkv.shape[-1]
+    NB, Hk, BS, _ = k_cache.shape
+    Hq = H - 2 * Hk
+    if k_scale is None:
+        mode = 0
+    else:
+        mode = 1 if k_scale.dim() == 3 else 2
+    assert sin_cache.stride(-1) == 1 and cos_cache.stride(-1) == 1
+    assert sin_cache.stride(0) == cos_cache.stride(0)
+    pos = position_id.to(torch.int32).contiguous()
+    slots = slot_mapping.to(torch.int32).contiguous()
+    rc = lib().oracle_fused_rope_paged(
+        _ptr(qkv), _DT[qkv.dtype], T, S, Hq, Hk, D, _ptr(sin_cache), _ptr(cos_cache),
+        sin_cache.shape[-1], rope_dim_offset, sin_cache.stride(0), sin_cache.shape[0],
+        _ptr(pos), _ptr(k_gamma),
+        _ptr(q_gamma), float(eps), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+        mode, _ptr(slots), NB, BS, nthreads or default_threads())
+    _check(rc, "fused_rope_paged")
 
 
 def f32_to_e4m3(x: torch.Tensor) -> torch.Tensor:

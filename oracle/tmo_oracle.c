@@ -21,6 +21,15 @@
  *   D6  dequant = RNE_out(fp32(code) * scale)   (cast order of _ops.py:3677).
  *   D7  smoothed = RN(fp32(x) * smooth), materialised before amax and divide (no FMA).
  *   D8  int8 codes for the dynamic ops.
+ *   D10 fused_rope (rmsnorm mode) in fp32 with one final rounding: the sum of squares of a
+ *       row is taken over chunks of 8 consecutive elements (each chunk summed in order, every
+ *       product and sum rounded), then over the chunk sums as a balanced binary tree in
+ *       natural order (padded with zeros to a power of two); inv = RN(1 / RN(sqrt(RN(RN(ss/D)
+ *       + eps)))); y = RN(RN(x * inv) * gamma); rope (fold) out = RN(RN(rot * sin) +
+ *       RN(y * cos)) with rot = (-y2, y1) over [off, off + rope_dim) (a position outside the
+ *       table's rows leaves the row unrotated -- undefined in the reference); K is quantised (or
+ *       rounded) from the fp32 result, V from its input values (_ops.py:3493-3520,
+ *       6356-6423; rotary math _ops.py:1116-1127).
  *   D9  offline (static-scale) quantisation divides: code = clip(RNE(RN(fp32(x) / s)), -128, 127)
  *       for int8, fp8 = e4m3fn_RNE(clip(RN(fp32(x) / s), -448, 448)), s the fp32 per-channel
  *       scale or the per-tensor scalar rounded to fp32 (_ops.py:1652-1670; the division is
@@ -337,6 +346,153 @@ int oracle_offline_quant_to_paged_cache(const void* k, const void* v, int dtype,
                   {k_chan, v_chan}, {k_tensor, v_tensor}, v ? 2 : 1, slot_mapping,
                   T, H, D, NB, BS, dtype, cache_dtype};
     parallel_for(T, nthreads, oqpc_range, &c);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ fused_rope (rmsnorm, paged) */
+
+typedef struct {
+    void* qkv;
+    int dtype;
+    int64_t T, S, Hq, Hk, D;
+    const void* sin_t;
+    const void* cos_t;
+    int64_t rope_dim, rope_off, table_stride, table_rows;
+    const int32_t* position;
+    const void* k_gamma;
+    const void* q_gamma;
+    float eps;
+    void* cache[2];
+    int cache_dtype;
+    float* scale[2];
+    int scale_mode;                 /* 0 none, 1 dynamic per token [NB, Hk, BS], 2 static [Hk, D] */
+    const int32_t* slot;
+    int64_t NB, BS;
+} frope_ctx;
+
+/* D10: sum of squares in 8-element chunks, then a balanced tree over the chunk sums. */
+static float rms_sum_squares(const float* x, int64_t n) {
+    float part[64];
+    int64_t nchunks = (n + 7) / 8, width = 1;
+    while (width < nchunks) width *= 2;
+    for (int64_t c = 0; c < width; ++c) {
+        float acc = 0.0f;
+        if (c < nchunks) {
+            int64_t e0 = 8 * c, e1 = e0 + 8 < n ? e0 + 8 : n;
+            acc = x[e0] * x[e0];
+            for (int64_t e = e0 + 1; e < e1; ++e) {
+                float sq = x[e] * x[e];
+                acc = acc + sq;
+            }
+        }
+        part[c] = acc;
+    }
+    for (int64_t w = width; w > 1; w /= 2)
+        for (int64_t c = 0; c < w / 2; ++c) part[c] = part[2 * c] + part[2 * c + 1];
+    return part[0];
+}
+
+/* rmsnorm with gamma (in place on fp32 row) */
+static void rmsnorm_row(float* x, int64_t D, const void* gamma, int dtype, float eps) {
+    float ss = rms_sum_squares(x, D);
+    float mean = ss / (float)D;
+    float r = sqrtf(mean + eps);
+    float inv = 1.0f / r;
+    for (int64_t d = 0; d < D; ++d) {
+        float t = x[d] * inv;
+        x[d] = t * load_elem(gamma, d, dtype);
+    }
+}
+
+/* fold rope over [off, off + rope_dim) of the row (_ops.py:1120-1127, interleaved False) */
+static void rope_row(float* y, float* tmp, const frope_ctx* c, int64_t pos) {
+    int64_t half = c->rope_dim / 2;
+    if (pos < 0 || pos >= c->table_rows) return;   /* D10: no table row, no rotation */
+    for (int64_t d = 0; d < c->D; ++d) tmp[d] = y[d];
+    for (int64_t j = 0; j < c->rope_dim; ++j) {
+        float rot = j < half ? -tmp[c->rope_off + j + half] : tmp[c->rope_off + j - half];
+        float sn = load_elem(c->sin_t, pos * c->table_stride + j, c->dtype);
+        float cs = load_elem(c->cos_t, pos * c->table_stride + j, c->dtype);
+        float a = rot * sn;
+        float b = tmp[c->rope_off + j] * cs;
+        y[c->rope_off + j] = a + b;
+    }
+}
+
+static void frope_store(const frope_ctx* c, int kv, const float* row, int64_t page_row, int64_t h) {
+    int64_t D = c->D;
+    if (c->scale_mode == 0) {
+        for (int64_t d = 0; d < D; ++d) store_elem(c->cache[kv], page_row * D + d, c->dtype, row[d]);
+        return;
+    }
+    int8_t* dst = (int8_t*)c->cache[kv] + page_row * D;
+    if (c->scale_mode == 1) {
+        c->scale[kv][page_row] = quant_row(row, D, dst);
+        return;
+    }
+    for (int64_t d = 0; d < D; ++d) {
+        float q = row[d] / c->scale[kv][h * D + d];
+        q = rintf(q);
+        if (q < -128.0f) q = -128.0f;
+        if (q > 127.0f) q = 127.0f;
+        dst[d] = (int8_t)q;
+    }
+}
+
+static void frope_range(void* p, int64_t lo, int64_t hi) {
+    frope_ctx* c = (frope_ctx*)p;
+    int64_t D = c->D, H = c->Hq + 2 * c->Hk;
+    float* row = (float*)malloc((size_t)D * sizeof(float));
+    float* tmp = (float*)malloc((size_t)D * sizeof(float));
+    for (int64_t t = lo; t < hi; ++t) {
+        int64_t pos = (int64_t)c->position[t / c->S] + t % c->S;
+        int64_t slot = c->slot[t];
+        int valid = slot >= 0 && slot < c->NB * c->BS;
+        int64_t blk = valid ? slot / c->BS : 0, off = valid ? slot % c->BS : 0;
+        for (int64_t hh = 0; hh < H; ++hh) {
+            int64_t base = (t * H + hh) * D;
+            for (int64_t d = 0; d < D; ++d) row[d] = load_elem(c->qkv, base + d, c->dtype);
+            if (hh < c->Hq) {                                   /* q: rmsnorm (if q_gamma), rope */
+                if (c->q_gamma) rmsnorm_row(row, D, c->q_gamma, c->dtype, c->eps);
+                rope_row(row, tmp, c, pos);
+                for (int64_t d = 0; d < D; ++d) store_elem(c->qkv, base + d, c->dtype, row[d]);
+            } else if (hh < c->Hq + c->Hk) {                   /* k: rmsnorm, rope, store */
+                if (!valid) continue;
+                int64_t h = hh - c->Hq;
+                rmsnorm_row(row, D, c->k_gamma, c->dtype, c->eps);
+                rope_row(row, tmp, c, pos);
+                frope_store(c, 0, row, (blk * c->Hk + h) * c->BS + off, h);
+            } else {                                             /* v: store */
+                if (!valid) continue;
+                int64_t h = hh - c->Hq - c->Hk;
+                frope_store(c, 1, row, (blk * c->Hk + h) * c->BS + off, h);
+            }
+        }
+    }
+    free(row);
+    free(tmp);
+}
+
+/* _ops.py:3469-3601 fused_rope / 6356-6423 fused_rmsnorm_rope_store_paged_cache, norm_type
+ * "rmsnorm", paged high-precision caches.  qkv [T, Hq + 2 Hk, D] contiguous (T = batch * S,
+ * token t at position position[t / S] + t % S); sin/cos [rows, table_stride] of qkv's dtype;
+ * caches [NB, Hk, BS, D] of qkv's dtype (scale_mode 0) or int8 (1: dynamic per-token scales
+ * written to [NB, Hk, BS]; 2: static per-channel scales read from [Hk, D]). */
+int oracle_fused_rope_paged(void* qkv, int dtype, int64_t T, int64_t S, int64_t Hq, int64_t Hk,
+                            int64_t D, const void* sin_t, const void* cos_t, int64_t rope_dim,
+                            int64_t rope_off, int64_t table_stride, int64_t table_rows,
+                            const int32_t* position,
+                            const void* k_gamma, const void* q_gamma, float eps,
+                            void* k_cache, void* v_cache, float* k_scale, float* v_scale,
+                            int scale_mode, const int32_t* slot, int64_t NB, int64_t BS,
+                            int nthreads) {
+    if (dtype != DT_F16 && dtype != DT_BF16 && dtype != DT_F32) return -2;
+    if (T < 0 || S <= 0 || Hq < 0 || Hk <= 0 || D <= 0 || D > 512 || NB < 0 || BS <= 0) return -1;
+    if (rope_dim < 0 || rope_dim % 2 || rope_off < 0 || rope_off + rope_dim > D) return -1;
+    frope_ctx c = {qkv, dtype, T, S, Hq, Hk, D, sin_t, cos_t, rope_dim, rope_off, table_stride,
+                   table_rows, position, k_gamma, q_gamma, eps, {k_cache, v_cache}, DT_I8, {k_scale, v_scale},
+                   scale_mode, slot, NB, BS};
+    parallel_for(T, nthreads, frope_range, &c);
     return 0;
 }
 

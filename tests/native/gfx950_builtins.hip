@@ -7,6 +7,9 @@
 //   fp8: fp8x4 (v_cvt_pk_fp8_f32) == fp8e4m3_bits (the integer encoder, itself checked on
 //        the host against a nearest-value search by div_exhaustive.hip "fp8") for every fp32
 //        value in [-448, 448].
+//   sqrt: __builtin_sqrtf (the fused rope's rms) is correctly rounded for every positive
+//        finite fp32 x: with m- and m+ the midpoints between r = sqrtf(x) and its neighbours,
+//        m-^2 < x < m+^2 (25-bit midpoints square exactly in fp64; no x sits on a midpoint).
 //
 // Each mode launches one grid-stride kernel that counts mismatches with vector atomics and
 // prints "mismatches=<n> checked=<m>"; the exit status is non-zero on any mismatch.  Built by
@@ -50,6 +53,22 @@ __global__ void check_fp8(uint32_t hi, unsigned long long* bad) {
   if (b) atomicAdd(bad, b);
 }
 
+__global__ void check_sqrt(unsigned long long* bad) {
+  const uint32_t stride = gridDim.x * blockDim.x;
+  unsigned long long b = 0;
+  for (uint32_t u = 1 + blockIdx.x * blockDim.x + threadIdx.x; u < 0x7f800000u; u += stride) {
+    const float x = __uint_as_float(u);
+    const float r = __builtin_sqrtf(x);
+    const uint32_t rb = __float_as_uint(r);
+    const double rd = (double)r;
+    const double lo = 0.5 * (rd + (double)__uint_as_float(rb - 1));
+    const double hi = 0.5 * (rd + (double)__uint_as_float(rb + 1));
+    const double xd = (double)x;
+    if (!(lo * lo < xd && xd < hi * hi)) ++b;
+  }
+  if (b) atomicAdd(bad, b);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -74,6 +93,9 @@ int main(int argc, char** argv) {
     std::memcpy(&hi, &fhi, 4);
     checked = 2ull * ((unsigned long long)(hi / 4) + 1) * 4;
     check_fp8<<<dim3(8192), dim3(256)>>>(hi, d_bad);
+  } else if (!std::strcmp(mode, "sqrt")) {
+    checked = 0x7f800000ull - 1;
+    check_sqrt<<<dim3(8192), dim3(256)>>>(d_bad);
   } else {
     std::printf("unknown mode %s\n", mode);
     return 2;

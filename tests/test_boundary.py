@@ -24,6 +24,21 @@ REFERENCE_SIGNATURES = {
     "offline_quant_to_paged_cache": [("k", None), ("v", None), ("k_cache_scale", None),
                                      ("v_cache_scale", None), ("slot_mapping", None),
                                      ("k_cache", None), ("v_cache", None)],
+    # _ops.py:3469-3492
+    "fused_rope": [("qkv", None), ("k_cache_hp", None), ("v_cache_hp", None), ("sin_cache", None),
+                   ("cos_cache", None), ("position_id", None), ("k_gamma", None), ("k_beta", None),
+                   ("k_cache_lp", None), ("v_cache_lp", None), ("cache_bs_id_hp", None),
+                   ("cache_seq_offsets_hp", None), ("cache_bs_id_lp", None),
+                   ("cache_seq_offsets_lp", None), ("k_scale_hp", None), ("v_scale_hp", None),
+                   ("k_scale_lp", None), ("v_scale_lp", None), ("slot_mapping_hp", None),
+                   ("slot_mapping_lp", None), ("norm_type", "layernorm"), ("rope_dim_offset", 0),
+                   ("eps", 1e-5), ("q_gamma", None)],
+    # _ops.py:6356-6367
+    "fused_rmsnorm_rope_store_paged_cache": [("qkv", None), ("k_cache", None), ("v_cache", None),
+                                             ("sin_cache", None), ("cos_cache", None),
+                                             ("position_id", None), ("k_gamma", None),
+                                             ("q_gamma", None), ("slot_mapping", None),
+                                             ("k_scale", None), ("v_scale", None), ("eps", 1e-5)],
     # _ops.py:3734-3745
     "dequant_from_paged_cache": [("key", None), ("value", None), ("key_cache", None),
                                  ("value_cache", None), ("key_cache_quant_scale", None),
@@ -66,6 +81,8 @@ WRITES = {
     "quant_to_paged_cache": {"k_cache", "v_cache", "k_cache_scale", "v_cache_scale"},
     "offline_quant_to_paged_cache": {"k_cache", "v_cache"},
     "dequant_from_paged_cache": {"key", "value"},
+    "fused_rope": {"qkv", "key_cache_hp", "value_cache_hp", "key_cache_lp", "value_cache_lp",
+                   "key_scale_hp", "value_scale_hp", "key_scale_lp", "value_scale_lp"},
     "scaled_quantize": {"output", "output_scale", "output_reduced"},
 }
 
@@ -110,6 +127,15 @@ def test_fakes_run_on_meta_tensors(tmo):
     assert tmo.offline_quant_to_paged_cache(k, v, 0.5, 0.25, slot, kc, vc) == (kc, vc)
     chan = torch.empty(8, 128, dtype=torch.float32, device="meta")
     assert tmo.offline_quant_to_paged_cache(k, None, chan, None, slot, f8, None) is f8
+    qkv = torch.empty(2, 8, 48, 128, dtype=torch.bfloat16, device="meta")
+    kcb = torch.empty(64, 8, 16, 128, dtype=torch.bfloat16, device="meta")
+    tab = torch.empty(64, 128, dtype=torch.bfloat16, device="meta")
+    pid = torch.empty(2, dtype=torch.int32, device="meta")
+    g = torch.empty(128, dtype=torch.bfloat16, device="meta")
+    out = tmo.fused_rmsnorm_rope_store_paged_cache(qkv, kcb, kcb.clone(), tab, tab, pid, g, g, slot)
+    assert len(out) == 3 and out[0] is qkv
+    out = tmo.fused_rmsnorm_rope_store_paged_cache(qkv, kc, vc, tab, tab, pid, g, None, slot, ks, vs)
+    assert len(out) == 5 and out[3] is ks
 
 
 def test_fake_tensor_mode(tmo):

@@ -36,6 +36,8 @@ def lib():
     L.tmo_hip_dequant_from_paged_cache.argtypes = [P, P] + [I64] * 5 + [P] * 7 + [I64] * 7 + \
         [INT, INT, INT, P]
     L.tmo_hip_scaled_quantize_per_token.argtypes = [P] + [I64] * 4 + [P] * 3 + [I64, P, I64, P, I64, P, I64, INT, P]
+    L.tmo_hip_fused_rope_paged.argtypes = [P] + [I64] * 5 + [P, P] + [I64] * 4 + [P, I64, P, P] + \
+        [ctypes.c_float] + [P] * 4 + [INT, P, I64, I64, INT, P]
     L.tmo_hip_offline_quant_to_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 4 + \
         [ctypes.c_float] * 2 + [P] + [I64] * 5 + [INT, INT, P]
     return L
@@ -46,7 +48,7 @@ def test_every_declared_symbol_is_exported(lib):
     assert set(names) == {"tmo_hip_abi_version", "tmo_hip_status_string",
                           "tmo_hip_reshape_paged_cache", "tmo_hip_quant_to_paged_cache",
                           "tmo_hip_dequant_from_paged_cache", "tmo_hip_scaled_quantize_per_token",
-                          "tmo_hip_offline_quant_to_paged_cache"}
+                          "tmo_hip_offline_quant_to_paged_cache", "tmo_hip_fused_rope_paged"}
     for n in names:
         assert hasattr(lib, n), n
 
@@ -145,4 +147,22 @@ def test_offline_quant_validation(lib):
     assert call(vch=FAKE) == EINVAL         # v scale without v
     assert call(H=0) == EINVAL
     assert call(BS=-1) == EINVAL
+    assert call(T=0) == 0
+
+
+def test_fused_rope_validation(lib):
+    def call(dtype=2, mode=0, qkv=FAKE, ks=None, T=8, S=8, D=128, rope=128, off=0, B=1, stride=128,
+             rows=64):
+        return lib.tmo_hip_fused_rope_paged(qkv, T, S, 4, 2, D, FAKE, FAKE, rows, stride, rope, off,
+                                            FAKE, B, FAKE, None, 1e-5, FAKE, FAKE, ks, ks, mode,
+                                            FAKE, 4, 16, dtype, None)
+    assert call(dtype=0) == EDTYPE           # fp32 qkv
+    assert call(mode=3) == EMODE
+    assert call(mode=1) == EINVAL            # quantised without scales
+    assert call(qkv=None) == EINVAL
+    assert call(D=1024, rope=128) == EINVAL  # head_size > 512
+    assert call(rope=127) == EINVAL          # odd rope_dim
+    assert call(off=8) == EINVAL             # window past head_size
+    assert call(stride=64) == EINVAL         # table rows shorter than rope_dim
+    assert call(T=9) == EINVAL               # more tokens than batch * seq_len
     assert call(T=0) == 0

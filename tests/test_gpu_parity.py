@@ -263,6 +263,71 @@ def test_offline_quant_cfg3_shape(tmo, ref, dev):
                       case.num_blocks, case.block_size, cdt)
 
 
+# ---------------------------------------------------------------------------- fused rope (rmsnorm)
+
+def check_fused_rope(tmo, ref, dev, name, case, with_q_gamma=True, off=0, api="rmsnorm_store"):
+    """GPU fused rope vs the oracle on the same inputs: qkv (Q written back), both caches and
+    the dynamic scales compared whole, from a sentinel start."""
+    qkv, kc, vc, sin, cos, pid, kg, qg, ks, vs, slot = case
+    qg = qg if with_q_gamma else None
+    kc = kc.view(torch.uint8).fill_(0x5A).view(kc.dtype)
+    vc = vc.view(torch.uint8).fill_(0x5A).view(vc.dtype)
+    if ks is not None and ks.dim() == 3:
+        ks.fill_(W.SCALE_SENTINEL)
+        vs.fill_(W.SCALE_SENTINEL)
+    want = [qkv.clone(), kc.clone(), vc.clone(),
+            ks.clone() if ks is not None else None, vs.clone() if vs is not None else None]
+    ref.fused_rope_paged(want[0], want[1], want[2], sin, cos, pid, kg, want[3], want[4], slot,
+                         1e-5, qg, off)
+    d = (lambda t: t.to(dev) if t is not None else None)
+    got = [d(qkv), d(kc), d(vc), d(ks), d(vs)]
+    if api == "rmsnorm_store":
+        assert off == 0
+        out = tmo.fused_rmsnorm_rope_store_paged_cache(got[0], got[1], got[2], d(sin), d(cos), d(pid),
+                                                       d(kg), d(qg), d(slot), got[3], got[4], 1e-5)
+        assert out[0] is got[0] and out[1] is got[1]
+    else:
+        out = tmo.fused_rope(got[0], got[1], got[2], d(sin), d(cos), d(pid), d(kg), None,
+                             k_scale_hp=got[3], v_scale_hp=got[4], slot_mapping_hp=d(slot),
+                             norm_type="rmsnorm", rope_dim_offset=off, eps=1e-5, q_gamma=d(qg))
+        assert len(out) == 3 and out[0] is got[0]
+    for g, w, n in zip(got, want, ("qkv", "k_cache", "v_cache", "k_scale", "v_scale")):
+        if w is not None:
+            assert_bits_equal(g.view(torch.int8) if g.dtype == torch.int8 else g, w,
+                              f"{name} {n}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mode", ["none", "dynamic", "static"])
+@pytest.mark.parametrize("with_q_gamma", [True, False])
+def test_fused_rope_modes(tmo, ref, dev, dtype, mode, with_q_gamma):
+    """Unquantised, dynamic and static int8 caches; Q with and without its RMSNorm; four
+    sequences, the last running past the sin/cos table (unrotated); -1 slots; a zero K row."""
+    case = W.fused_rope_case(dtype, mode, 21, B=4, S=24, Hq=8, Hk=2, NB=16)
+    check_fused_rope(tmo, ref, dev, f"{dtype} {mode}", case, with_q_gamma)
+
+
+@pytest.mark.parametrize("D,rope,off", [(128, 64, 32), (64, 32, 0), (256, 256, 0), (512, 128, 64),
+                                        (16, 16, 0), (8, 8, 0), (96, 64, 16), (100, 40, 6),
+                                        (128, 24, 8), (128, 2, 126)])
+def test_fused_rope_head_sizes_and_windows(tmo, ref, dev, D, rope, off):
+    """Vector path widths (8..512 channels, windows on 8-element chunks) and the generic path
+    (head sizes not a power-of-two multiple of 8, windows not on chunk boundaries)."""
+    for mode in ("none", "dynamic"):
+        case = W.fused_rope_case(torch.bfloat16, mode, D + rope + off, B=2, S=9, Hq=3, Hk=1, D=D,
+                                 rope=rope, NB=4)
+        check_fused_rope(tmo, ref, dev, f"D={D} rope={rope}+{off} {mode}", case, True, off,
+                         api="fused_rope")
+
+
+def test_fused_rope_llama_prefill_shape(tmo, ref, dev):
+    """A Llama-3-8B-shaped prefill chunk: 8 x 512 tokens, 32 Q + 8 KV heads x 128, bf16,
+    dynamic int8 caches, table of 4096 positions."""
+    case = W.fused_rope_case(torch.bfloat16, "dynamic", 5, B=8, S=512, Hq=32, Hk=8, NB=512,
+                             maxpos=4096, positions=(0, 512, 1024, 1536, 2048, 2560, 3072, 3584))
+    check_fused_rope(tmo, ref, dev, "llama prefill", case, True)
+
+
 # ---------------------------------------------------------------------------- reshape_paged_cache
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32, torch.int8])

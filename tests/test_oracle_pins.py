@@ -549,3 +549,129 @@ def test_fp8_conversion_matches_torch(ref):
     r = (torch.rand(2_000_000, generator=g) * 2 - 1) * 448 * torch.rand(2_000_000, generator=g) ** 6
     f = torch.cat([b, near, -near, r, torch.tensor([0.0, -0.0, 448.0, -448.0, 1e-30, -1e-30])])
     assert torch.equal(ref.f32_to_e4m3(f), f.to(torch.float8_e4m3fn).view(torch.uint8))
+
+
+# ---------------------------------------------------------------------------- fused rope (rmsnorm)
+
+def _sum_squares_chunked(x: torch.Tensor) -> torch.Tensor:
+    """D10's order with elementwise torch ops: 8-element chunks summed in order, then a
+    balanced tree over the chunk sums (every product and sum a separate IEEE operation)."""
+    D = x.shape[-1]
+    n = (D + 7) // 8
+    width = 1 << (n - 1).bit_length()
+    parts = []
+    for c in range(width):
+        if c < n:
+            e0, e1 = 8 * c, min(8 * c + 8, D)
+            acc = x[..., e0] * x[..., e0]
+            for e in range(e0 + 1, e1):
+                acc = acc + x[..., e] * x[..., e]
+        else:
+            acc = torch.zeros_like(x[..., 0])
+        parts.append(acc)
+    while len(parts) > 1:
+        parts = [parts[2 * i] + parts[2 * i + 1] for i in range(len(parts) // 2)]
+    return parts[0]
+
+
+def torch_fused_rope(qkv, k_cache, v_cache, sin, cos, position_id, k_gamma, k_scale, v_scale,
+                     slot, eps, q_gamma, off, exact=True, wide=torch.float32):
+    """reference _ops.py:3493-3520 (rmsnorm branch) with apply_rotary's fold math
+    (_ops.py:1116-1127), executed by torch on the CPU in `wide` precision.  exact=True uses
+    D10's summation order (then the result must equal the oracle bit for bit); exact=False
+    uses torch's own mean of squares (the docstring literally)."""
+    B, S, H, D = qkv.shape
+    NB, Hk, BS, _ = k_cache.shape
+    Hq = H - 2 * Hk
+    x = qkv.to(wide)
+    rope = sin.shape[-1]
+    half = rope // 2
+    pos = (position_id.long()[:, None] + torch.arange(S)[None, :])          # [B, S]
+    inside = ((pos >= 0) & (pos < sin.shape[0]))[:, :, None, None]           # else: no rotation
+    pc = pos.clamp(0, sin.shape[0] - 1)
+    sn, cs = sin[pc].to(wide)[:, :, None, :], cos[pc].to(wide)[:, :, None, :]
+
+    def rmsnorm(t, gamma):
+        ss = _sum_squares_chunked(t) if exact else (t * t).sum(-1)
+        mean = ss / D
+        # sqrt and 1/r through float64, rounded once: the correctly rounded fp32 results
+        # (binary64 has more than twice binary32's precision).  torch's own fp32 sqrt is not
+        # always correctly rounded on the CPU (59.49298858642578 -> 7.713169574737549, the
+        # nearest float being 7.713170051574707).
+        r = torch.sqrt((mean + eps).double()).to(wide)
+        inv = (1.0 / r.double()).to(wide)
+        return (t * inv[..., None]) * gamma.to(wide)
+
+    def rotary(y):
+        y = y.clone()
+        seg = y[..., off:off + rope].clone()
+        rot = torch.cat((-seg[..., half:], seg[..., :half]), dim=-1)
+        y[..., off:off + rope] = torch.where(inside, rot * sn + seg * cs, seg)
+        return y
+
+    q = x[:, :, :Hq]
+    if q_gamma is not None:
+        q = rmsnorm(q, q_gamma)
+    q = rotary(q)
+    k = rotary(rmsnorm(x[:, :, Hq:Hq + Hk], k_gamma))
+    v = x[:, :, Hq + Hk:]
+    q_out = qkv.clone()
+    q_out[:, :, :Hq] = q.to(qkv.dtype)
+    flat = slot.reshape(-1)
+    valid = (flat >= 0) & (flat < NB * BS)
+    s_ = flat[valid].long()
+    blk, o = s_ // BS, s_ % BS
+    for t, c, sc in ((k, k_cache, k_scale), (v, v_cache, v_scale)):
+        rows = t.reshape(B * S, Hk, D)[valid]
+        if sc is None:
+            c.permute(0, 2, 1, 3)[blk, o] = rows.to(c.dtype)
+        elif sc.dim() == 3:
+            codes, scale = torch_row_quant(rows.to(torch.float32))
+            c.permute(0, 2, 1, 3)[blk, o] = codes
+            sc.permute(0, 2, 1)[blk, o] = scale
+        else:
+            c.permute(0, 2, 1, 3)[blk, o] = (rows.to(torch.float32) / sc).round().clamp(-128, 127).to(torch.int8)
+    return q_out
+
+
+_frope_case = W.fused_rope_case
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("mode", ["none", "dynamic", "static"])
+@pytest.mark.parametrize("with_q_gamma", [True, False])
+def test_fused_rope_matches_torch_bitwise(ref, dtype, mode, with_q_gamma):
+    """The oracle against the torch-CPU restatement that uses D10's summation order: equal
+    bit for bit (q written back, K/V pages, dynamic scales)."""
+    for rope, off, D in ((128, 0, 128), (64, 32, 128), (32, 0, 64)):
+        # B = 4 on the last shape: its fourth sequence runs past the sin/cos table
+        qkv, kc, vc, sin, cos, pid, kg, qg, ks, vs, slot = _frope_case(dtype, mode, 3, D=D, rope=rope,
+                                                                       B=4 if D == 64 else 3)
+        qg = qg if with_q_gamma else None
+        want_kc, want_vc = kc.clone(), vc.clone()
+        want_ks = ks.clone() if mode == "dynamic" else ks
+        want_vs = vs.clone() if mode == "dynamic" else vs
+        want_q = torch_fused_rope(qkv, want_kc, want_vc, sin, cos, pid, kg, want_ks, want_vs, slot,
+                                  1e-5, qg, off)
+        got = qkv.clone()
+        ref.fused_rope_paged(got, kc, vc, sin, cos, pid, kg, ks, vs, slot, 1e-5, qg, off)
+        assert torch.equal(bits(got), bits(want_q)), (rope, off)
+        assert torch.equal(bits(kc), bits(want_kc)) and torch.equal(bits(vc), bits(want_vc))
+        if mode == "dynamic":
+            assert torch.equal(bits(ks), bits(want_ks)) and torch.equal(bits(vs), bits(want_vs))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fused_rope_within_one_ulp_of_float64(ref, dtype):
+    """Against the docstring computed in float64 (torch's own sum of squares): q and K differ
+    by at most one ulp of the output type, and only rarely."""
+    qkv, kc, vc, sin, cos, pid, kg, qg, ks, vs, slot = _frope_case(dtype, "none", 9, B=3, S=30)
+    want_kc, want_vc = kc.clone(), vc.clone()
+    want_q = torch_fused_rope(qkv, want_kc, want_vc, sin, cos, pid, kg, None, None, slot, 1e-5, qg,
+                              0, exact=False, wide=torch.float64)
+    got = qkv.clone()
+    ref.fused_rope_paged(got, kc, vc, sin, cos, pid, kg, None, None, slot, 1e-5, qg)
+    for a, b in ((got, want_q), (kc, want_kc)):
+        d = (bits(a).to(torch.int32) - bits(b).to(torch.int32)).abs()
+        assert int(d.max()) <= 1
+        assert float((d > 0).float().mean()) < 0.05

@@ -213,3 +213,33 @@ def cfg5_fill(layout: DequantLayout, device, seed: int = 1005, heads: int = H, d
         v = (torch.randn(n, heads, dim, generator=g, device=device) * scale).to(torch.bfloat16)
         tmo.quant_to_paged_cache(k, v, kc, vc, ks, vs, slots)
     return kc, vc, ks, vs
+
+
+def fused_rope_case(dtype, mode, seed, B=3, S=20, Hq=4, Hk=2, D=128, rope=128, NB=12, BS=16,
+                    maxpos=128, positions=(0, 7, 40, 120)):
+    """Inputs of a fused_rope / fused_rmsnorm_rope_store_paged_cache call: qkv [B, S, Hq+2Hk, D]
+    with magnitudes spread over S, a zero K row, sin/cos tables of `maxpos` rows (a sequence
+    starting at 120 runs past the table), gammas ~U[0.5, 1.5), slots with -1 entries, and
+    caches / scales for mode "none" (qkv's dtype), "dynamic" or "static" (int8)."""
+    g = torch.Generator().manual_seed(seed)
+    qkv = (torch.randn(B, S, Hq + 2 * Hk, D, generator=g) * torch.logspace(-2, 1, S)[None, :, None, None]).to(dtype)
+    qkv[1, 3, Hq] = 0                                        # a zero K row
+    ang = torch.arange(maxpos)[:, None] * (0.5 ** (torch.arange(rope // 2) / 8.0))[None, :]
+    ang = torch.cat((ang, ang), dim=-1)
+    sin, cos = torch.sin(ang).to(dtype), torch.cos(ang).to(dtype)
+    position_id = torch.tensor(list(positions)[:B], dtype=torch.int32)
+    k_gamma = (0.5 + torch.rand(D, generator=g)).to(dtype)
+    q_gamma = (0.5 + torch.rand(D, generator=g)).to(dtype)
+    slot = torch.randperm(NB * BS, generator=g)[:B * S].to(torch.int32)
+    slot[::7] = -1
+    cdt = dtype if mode == "none" else torch.int8
+    kc = torch.zeros(NB, Hk, BS, D, dtype=cdt)
+    vc = torch.zeros_like(kc)
+    if mode == "dynamic":
+        ks, vs = torch.full((NB, Hk, BS), -1.0), torch.full((NB, Hk, BS), -1.0)
+    elif mode == "static":
+        ks = 0.005 + 0.02 * torch.rand(Hk, D, generator=g)
+        vs = 0.005 + 0.02 * torch.rand(Hk, D, generator=g)
+    else:
+        ks = vs = None
+    return qkv, kc, vc, sin, cos, position_id, k_gamma, q_gamma, ks, vs, slot
