@@ -49,12 +49,14 @@ WORKLOADS = {
     "cfg5": "configs[4]: dequant_from_paged_cache, 64 seqs ctx ~U[1024,32768], 8 KV heads x 128, int8 pages -> bf16",
     "offline_i8": "offline_quant_to_paged_cache on configs[2]'s shape (32768 tokens x 8 KV heads x 128 bf16), static per-channel scales -> int8 pages",
     "offline_f8": "offline_quant_to_paged_cache on configs[2]'s shape (32768 tokens x 8 KV heads x 128 bf16), static per-channel scales -> float8_e4m3fn pages",
+    "fused_rope": "fused_rmsnorm_rope_store_paged_cache, Llama-3-8B prefill chunk: 8 x 4096 tokens, 32 Q + 8 KV heads x 128 bf16, Q written back, K/V -> int8 pages with dynamic per-token scales (65536 blocks x 16)",
 }
 KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1>", "cfg2": "quant_paged_vec<BF16,16,1>",
            "cfg3": "quant_paged_vec<BF16,16,1>", "cfg4": "sq_dense<BF16,8,false,true>",
            "cfg4_moe": "sq_vec<BF16,8,false,1>", "cfg5": "dequant_paged_persistent<BF16,8>",
            "offline_i8": "quant_paged_static_vec<BF16,16,false>",
-           "offline_f8": "quant_paged_static_vec<BF16,16,true>"}
+           "offline_f8": "quant_paged_static_vec<BF16,16,true>",
+           "fused_rope": "fused_rope_tok<BF16,16,4>"}
 
 
 def parse_args():
@@ -185,6 +187,54 @@ def bench_offline(torch, tmo, W, case, cache_dtype, dev, steps, warmup):
     return ms, alg, case.valid_tokens(), sets
 
 
+FR_B, FR_S, FR_HQ, FR_HK = 8, 4096, 32, 8
+
+
+def fused_rope_bytes(T: int, rope: int = 128) -> int:
+    """Algorithmic bytes of the fused_rope workload: qkv read once, Q written back, K/V codes
+    and scales written, the slot mapping, one sin and one cos row per token, the gammas."""
+    D, H = W_D, FR_HQ + 2 * FR_HK
+    return (T * H * D * 2 + T * FR_HQ * D * 2 + 2 * T * FR_HK * (D + 4) + 4 * T
+            + 2 * T * rope * 2 + 2 * D * 2 + 4 * FR_B)
+
+
+W_D = 128
+
+
+def bench_fused_rope(torch, tmo, W, dev, steps, warmup):
+    """fused_rmsnorm_rope_store_paged_cache on a Llama-3-8B-shaped prefill chunk: per set its
+    own qkv; shared int8 caches and scales, configs[2]-style slots shifted per set."""
+    T = FR_B * FR_S
+    alg = fused_rope_bytes(T)
+    sets = n_sets(alg)
+    g = torch.Generator(device=dev).manual_seed(11)
+    case3 = W.cfg3()
+    nslots = case3.num_blocks * case3.block_size
+    slots0 = case3.slot_mapping.to(dev)
+    shape = (case3.num_blocks, FR_HK, case3.block_size, W_D)
+    kc = torch.zeros(shape, dtype=torch.int8, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros(shape[:3], dtype=torch.float32, device=dev)
+    vs = torch.zeros_like(ks)
+    maxpos = 8192
+    ang = torch.arange(maxpos, device=dev)[:, None] * \
+        (1e4 ** (-torch.arange(64, device=dev) / 64.0))[None, :]
+    ang = torch.cat((ang, ang), dim=-1)
+    sin, cos = torch.sin(ang).to(torch.bfloat16), torch.cos(ang).to(torch.bfloat16)
+    pid = torch.arange(FR_B, dtype=torch.int32, device=dev) * 512
+    kg = (0.5 + torch.rand(W_D, generator=g, device=dev)).to(torch.bfloat16)
+    qg = (0.5 + torch.rand(W_D, generator=g, device=dev)).to(torch.bfloat16)
+    calls = []
+    for s in range(sets):
+        qkv = torch.randn((FR_B, FR_S, FR_HQ + 2 * FR_HK, W_D), generator=g, device=dev).to(torch.bfloat16)
+        shift = (s * 9973 * case3.block_size) % nslots
+        slots = (slots0 + shift) % nslots
+        calls.append(lambda qkv=qkv, sl=slots: tmo.fused_rmsnorm_rope_store_paged_cache(
+            qkv, kc, vc, sin, cos, pid, kg, qg, sl, ks, vs, 1e-5))
+    ms = time_graph(torch, calls, steps, warmup)
+    return ms, alg, T, sets
+
+
 def bench_smooth_quant(torch, tmo, W, case, dev, steps, warmup):
     alg = case.algorithmic_bytes()
     sets = n_sets(alg)
@@ -237,6 +287,19 @@ def profile_pass(torch, tmo, W, names, dev, n: int) -> None:
             kc, vc = kc.view(cdt), vc.view(cdt)
             ks = torch.full((k.shape[1], k.shape[2]), 0.02, device=dev)
             fn = lambda: tmo.offline_quant_to_paged_cache(k, v, ks, ks, sl, kc, vc)
+        elif name == "fused_rope":
+            case3 = W.cfg3()
+            qkv = torch.randn((FR_B, FR_S, FR_HQ + 2 * FR_HK, W_D), device=dev).to(torch.bfloat16)
+            kc = torch.zeros((case3.num_blocks, FR_HK, 16, W_D), dtype=torch.int8, device=dev)
+            vc = torch.zeros_like(kc)
+            ks = torch.zeros(kc.shape[:3], device=dev)
+            vs = torch.zeros_like(ks)
+            tab = torch.rand((8192, W_D), device=dev).to(torch.bfloat16)
+            pid = torch.arange(FR_B, dtype=torch.int32, device=dev) * 512
+            gm = torch.ones(W_D, device=dev).to(torch.bfloat16)
+            sl = case3.slot_mapping.to(dev)
+            fn = lambda: tmo.fused_rmsnorm_rope_store_paged_cache(qkv, kc, vc, tab, tab, pid, gm, gm,
+                                                                  sl, ks, vs)
         elif name.startswith("cfg4"):
             case = getattr(W, name)()
             x, sm = case.x.to(dev), case.smooth.to(dev)
@@ -328,6 +391,21 @@ def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
                                                          kc, vc, nthreads=nthreads)
         alg, units, desc = offline_bytes(sub), sub.valid_tokens(), \
             f"offline_quant_to_paged_cache on the first {n} tokens of cfg3"
+    elif workload == "fused_rope":
+        n = 512
+        g = torch.Generator().manual_seed(3)
+        qkv = torch.randn((1, n, FR_HQ + 2 * FR_HK, W_D), generator=g).to(torch.bfloat16)
+        kc = torch.zeros((n // 16, FR_HK, 16, W_D), dtype=torch.int8)
+        vc = torch.zeros_like(kc)
+        ks = torch.zeros(kc.shape[:3])
+        vs = torch.zeros_like(ks)
+        tab = torch.rand((n, W_D), generator=g).to(torch.bfloat16)
+        pid = torch.zeros(1, dtype=torch.int32)
+        gm = torch.ones(W_D).to(torch.bfloat16)
+        sl = torch.arange(n, dtype=torch.int32)
+        fn = lambda: oracle.fused_rope_paged(qkv, kc, vc, tab, tab, pid, gm, ks, vs, sl, 1e-5, gm,
+                                             nthreads=nthreads)
+        alg, units, desc = fused_rope_bytes(n), n, f"fused rope of one {n}-token sequence"
     elif workload.startswith("cfg4"):
         case = getattr(W, workload)()
         n = min(case.rows, 2048)
@@ -395,7 +473,8 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     todo = [args.workload] if args.configs == "headline" else \
-        ["cfg1", "cfg2", "cfg3", "cfg4", "cfg4_moe", "cfg5", "offline_i8", "offline_f8"]
+        ["cfg1", "cfg2", "cfg3", "cfg4", "cfg4_moe", "cfg5", "offline_i8", "offline_f8",
+         "fused_rope"]
     if args.workload not in todo:
         todo.append(args.workload)
     if args.profile_pass:
@@ -414,6 +493,9 @@ def main():
             cdt = torch.int8 if name == "offline_i8" else torch.float8_e4m3fn
             ms, alg, units, sets = bench_offline(torch, tmo, W, W.cfg3(), cdt, dev, args.steps,
                                                  args.warmup)
+        elif name == "fused_rope":
+            ms, alg, units, sets = bench_fused_rope(torch, tmo, W, dev, max(20, args.steps // 4),
+                                                    args.warmup // 4)
         else:
             ms, alg, units, sets = bench_dequant(torch, tmo, W, W.cfg5(), dev,
                                                  max(10, args.steps // 40), max(2, args.warmup // 10))
@@ -451,7 +533,8 @@ def main():
         "config": {"workload": WORKLOADS[args.workload],
                    "io": {"cfg5": "int8 codes + fp32 scales in; bf16 out",
                           "offline_i8": "bf16 in; int8 codes out (static per-channel scales)",
-                          "offline_f8": "bf16 in; float8_e4m3fn codes out (static per-channel scales)"}
+                          "offline_f8": "bf16 in; float8_e4m3fn codes out (static per-channel scales)",
+                          "fused_rope": "bf16 qkv in; bf16 Q written back; int8 K/V codes + fp32 scales out"}
                    .get(args.workload, "bf16 in; int8 codes + fp32 scales out"),
                    "tokens_per_s": head["units_per_s"],
                    "frac_of_peak": head["frac_of_peak"]},

@@ -90,6 +90,12 @@ __device__ __forceinline__ float rms_inverse(float ss, int d, float eps) {
   return 1.0f / r;
 }
 
+constexpr int kDppRowRor8 = 0x128;  // rotate right by 8 lanes inside each 16-lane row
+
+#ifndef TMO_FUSED_ROPE_TOKEN_MAJOR
+#define TMO_FUSED_ROPE_TOKEN_MAJOR 1
+#endif
+
 template <class Tag>
 __device__ __forceinline__ void pack8(Tag, const float* f, u32x4& w) {
 #pragma unroll
@@ -159,20 +165,28 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
   if (kind != 2) {
     // partner chunk: +half in the first half of the window, -half in the second
     const int hc = nwin / 2;
-    const int base = (threadIdx.x & (kWave - 1)) & ~(G - 1);  // the group's first lane
-    const int src = in_win ? (lane < c0 + hc ? lane + hc : lane - hc) : lane;
     float partner[8];
+    if (G == 16 && nwin == 16) {
+      // whole 16-lane row: the partner is lane +- 8 = lane ^ 8, a DPP row rotation by 8
 #pragma unroll
-    for (int e = 0; e < 8; ++e) partner[e] = __shfl(y[e], base + src, 64);
+      for (int e = 0; e < 8; ++e)
+        partner[e] = __int_as_float(
+            __builtin_amdgcn_update_dpp(0, __float_as_int(y[e]), kDppRowRor8, 0xF, 0xF, true));
+    } else {
+      const int base = (threadIdx.x & (kWave - 1)) & ~(G - 1);  // the group's first lane
+      const int src = in_win ? (lane < c0 + hc ? lane + hc : lane - hc) : lane;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) partner[e] = __shfl(y[e], base + src, 64);
+    }
     if (rotate && in_win) {
       float sn[8], cs[8];
       unpack(Tag{}, sw, sn);
       unpack(Tag{}, cw, cs);
-      const bool first = lane < c0 + hc;
+      // rot = -partner in the first half of the window: fold the sign into sin (exact)
+      const float sign = lane < c0 + hc ? -1.0f : 1.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float rot = first ? -partner[e] : partner[e];
-        const float a = rot * sn[e];
+        const float a = partner[e] * (sn[e] * sign);
         const float b = y[e] * cs[e];
         y[e] = a + b;
       }
@@ -227,6 +241,145 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
   c2[0] = c[0];
   c2[1] = c[1];
   *reinterpret_cast<u32x2*>(static_cast<int8_t*>(p.cache[kv]) + page_row * p.head_dim + lane * 8) = c2;
+}
+
+// Token-major vector path: a workgroup owns one token (its position and slot are scalar loads,
+// no per-lane index division) and the 256/G lane groups walk its heads, kR rows per group,
+// all kR rows loaded before the first is processed.  sin/cos (with the rotation's sign folded
+// in) and both gammas are loaded and unpacked once per workgroup instead of once per row.
+// Same arithmetic, in the same order, as fused_rope_vec.
+template <class Tag, int G, int kR>
+__global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
+  constexpr int kGroups = 256 / G;
+  const int lane = threadIdx.x & (G - 1);
+  const int grp = threadIdx.x / G;
+  const int64_t t = blockIdx.x;
+  const int64_t b = t / p.seq_len;  // workgroup-uniform (scalar)
+  const int64_t pos = (int64_t)p.position[b] + (t - b * p.seq_len);
+  const int32_t slot = p.slot[t];
+  const int c0 = p.rope_off / 8, nwin = p.rope_dim / 8, hc = nwin / 2;
+  const bool in_win = lane >= c0 && lane < c0 + nwin;
+  const bool rotate = pos >= 0 && pos < p.table_rows;  // workgroup-uniform
+
+  // rows of this group: heads grp, grp + kGroups, ... (kR of them at most)
+  char* xbase = static_cast<char*>(p.qkv) + (t * p.heads * p.head_dim + lane * 8) * Tag::kBytes;
+  u32x4 xw[kR];
+#pragma unroll
+  for (int j = 0; j < kR; ++j) {
+    const int hh = grp + j * kGroups;
+    if (hh < p.heads)
+      xw[j] = *reinterpret_cast<const u32x4*>(xbase + (int64_t)hh * p.head_dim * Tag::kBytes);
+  }
+  u32x4 sw = {0u, 0u, 0u, 0u}, cw = {0u, 0u, 0u, 0u}, kgw = {0u, 0u, 0u, 0u}, qgw = {0u, 0u, 0u, 0u};
+  if (rotate && in_win) {
+    const int64_t e = pos * p.table_stride + (lane - c0) * 8;
+    sw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.sin_t) + e * Tag::kBytes);
+    cw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.cos_t) + e * Tag::kBytes);
+  }
+  kgw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_gamma) + lane * 16);
+  if (p.q_gamma) qgw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.q_gamma) + lane * 16);
+  float sn[8], cs[8], kg[8], qg[8];
+  unpack(Tag{}, sw, sn);
+  unpack(Tag{}, cw, cs);
+  unpack(Tag{}, kgw, kg);
+  unpack(Tag{}, qgw, qg);
+  const float sign = lane < c0 + hc ? -1.0f : 1.0f;  // rot = -partner in the window's first half
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sn[e] = sn[e] * sign;
+  const bool store_kv = slot >= 0 && (int64_t)slot < p.num_slots;  // workgroup-uniform
+
+#pragma unroll
+  for (int j = 0; j < kR; ++j) {
+    const int hh = grp + j * kGroups;
+    if (hh >= p.heads) break;  // group-uniform
+    const int kind = hh < p.hq ? 0 : (hh < p.hq + p.hk ? 1 : 2);
+    if (kind != 0 && !store_kv) continue;
+    float y[8];
+    unpack(Tag{}, xw[j], y);
+    if (kind != 2) {
+      if (kind == 1 || p.q_gamma) {
+        float acc = y[0] * y[0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) {
+          const float sq = y[e] * y[e];
+          acc = acc + sq;
+        }
+        const float inv = rms_inverse(group_sum_f32<G>(acc), p.head_dim, p.eps);
+        const float* g = kind == 1 ? kg : qg;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float n = y[e] * inv;
+          y[e] = n * g[e];
+        }
+      }
+      float partner[8];
+      if (G == 16 && nwin == 16) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          partner[e] = __int_as_float(
+              __builtin_amdgcn_update_dpp(0, __float_as_int(y[e]), kDppRowRor8, 0xF, 0xF, true));
+      } else {
+        const int base = (threadIdx.x & (kWave - 1)) & ~(G - 1);
+        const int src = in_win ? (lane < c0 + hc ? lane + hc : lane - hc) : lane;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) partner[e] = __shfl(y[e], base + src, 64);
+      }
+      if (rotate && in_win) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float a = partner[e] * sn[e];
+          const float c = y[e] * cs[e];
+          y[e] = a + c;
+        }
+      }
+    }
+    if (kind == 0) {
+      u32x4 o;
+      pack8(Tag{}, y, o);
+      *reinterpret_cast<u32x4*>(xbase + (int64_t)hh * p.head_dim * Tag::kBytes) = o;
+      continue;
+    }
+    const int h = kind == 1 ? hh - p.hq : hh - p.hq - p.hk;
+    const int kv = kind - 1;
+    int64_t page_row;
+    page_row_of(p, slot, h, page_row);
+    if (p.scale_mode == 0) {
+      u32x4 o;
+      pack8(Tag{}, y, o);
+      *reinterpret_cast<u32x4*>(static_cast<char*>(p.cache[kv]) +
+                                (page_row * p.head_dim + lane * 8) * Tag::kBytes) = o;
+      continue;
+    }
+    uint32_t c[2];
+    if (p.scale_mode == 1) {
+      float m = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = abs_max(m, y[e]);
+      const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<G>(__float_as_uint(m))));
+      encode_row<8>(y, rs, c);
+      if (lane == 0) p.scale[kv][page_row] = rs.s;
+    } else {
+      const float* sp = p.scale[kv] + (int64_t)h * p.head_dim + lane * 8;
+      float sc[8], yr[8], q[8];
+      bool fast = true;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sc[e] = sp[e];
+        fast &= static_scale_fast(sc[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) yr[e] = fast ? recip_rn(sc[e]) : 0.0f;
+      static_quotients<8>(y, sc, yr, fast, q);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        c[i] = pack_codes(code_bits(q[4 * i]), code_bits(q[4 * i + 1]), code_bits(q[4 * i + 2]),
+                          code_bits(q[4 * i + 3]));
+    }
+    u32x2 c2;
+    c2[0] = c[0];
+    c2[1] = c[1];
+    *reinterpret_cast<u32x2*>(static_cast<int8_t*>(p.cache[kv]) + page_row * p.head_dim + lane * 8) = c2;
+  }
 }
 
 // Generic path (any head_dim <= 512, any even rope window): one wavefront per row, the row
@@ -333,6 +486,28 @@ int launch(const FusedRopeParams& p, hipStream_t stream) {
              (!p.q_gamma || al16(p.q_gamma)) && al16(p.sin_t) && al16(p.cos_t) &&
              (p.table_stride * Tag::kBytes) % 16 == 0 && al16(p.cache[0]) && al16(p.cache[1]) &&
              (p.scale_mode != 2 || (al16(p.scale[0]) && al16(p.scale[1])));
+  // token-major kernel when one workgroup covers a token's heads in at most 4 rows per group
+  if (TMO_FUSED_ROPE_TOKEN_MAJOR && vec && (int64_t)(256 / G) * 4 >= p.heads &&
+      p.tokens <= 0x7fffffffLL) {
+    const dim3 grid((unsigned)p.tokens), block(256);
+    const int r = (p.heads + 256 / G - 1) / (256 / G);
+    switch (G) {
+#define TMO_FR_CASE(g)                                                                    \
+  case g:                                                                                 \
+    if (r <= 1) return launch_kernel(fused_rope_tok<Tag, g, 1>, grid, block, stream, p);  \
+    if (r <= 2) return launch_kernel(fused_rope_tok<Tag, g, 2>, grid, block, stream, p);  \
+    return launch_kernel(fused_rope_tok<Tag, g, 4>, grid, block, stream, p);
+      TMO_FR_CASE(1)
+      TMO_FR_CASE(2)
+      TMO_FR_CASE(4)
+      TMO_FR_CASE(8)
+      TMO_FR_CASE(16)
+      TMO_FR_CASE(32)
+      TMO_FR_CASE(64)
+#undef TMO_FR_CASE
+      default: break;
+    }
+  }
   const int64_t nrows = p.tokens * p.heads;
   const int rows = vec ? 256 / G : 4;
   const int64_t blocks = (nrows + rows - 1) / rows;

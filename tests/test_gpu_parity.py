@@ -320,6 +320,16 @@ def test_fused_rope_head_sizes_and_windows(tmo, ref, dev, D, rope, off):
                          api="fused_rope")
 
 
+@pytest.mark.parametrize("D,Hq,Hk", [(128, 64, 8), (512, 16, 2), (64, 120, 8)])
+def test_fused_rope_many_heads(tmo, ref, dev, D, Hq, Hk):
+    """More heads than one workgroup's lane groups cover in four rows each: the row-major
+    kernel (one lane group per (token, head) row) instead of the token-major one."""
+    for mode in ("dynamic", "static"):
+        case = W.fused_rope_case(torch.bfloat16, mode, D + Hq, B=2, S=11, Hq=Hq, Hk=Hk, D=D,
+                                 rope=min(D, 128), NB=4)
+        check_fused_rope(tmo, ref, dev, f"D={D} Hq={Hq} Hk={Hk} {mode}", case, True)
+
+
 def test_fused_rope_llama_prefill_shape(tmo, ref, dev):
     """A Llama-3-8B-shaped prefill chunk: 8 x 512 tokens, 32 Q + 8 KV heads x 128, bf16,
     dynamic int8 caches, table of 4096 positions."""
