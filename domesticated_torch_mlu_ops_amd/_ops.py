@@ -21,6 +21,11 @@ __all__ = [
     "moe_quantize",
     "scaled_quantize",
     "per_token_smooth_quantize",
+    "reshape_linear_cache",
+    "quant_to_linear_cache",
+    "offline_quant_to_linear_cache",
+    "dequant_from_linear_cache",
+    "reshape_from_cache",
 ]
 
 
@@ -328,3 +333,162 @@ def per_token_smooth_quantize(
     """
     return moe_quantize(x, smooth, zero, token_count, gather_index, gather_index_start_position,
                         output, output_scale, dynamic_quant)
+
+
+# ---------------------------------------------------------------------------- linear caches
+#
+# Linear caches are [max_batch, heads, cache_len, head_size], one cache batch per sequence.
+# Sequence i covers min(len_i, max_context_len) tokens; token j is row start_i + j of the
+# token-major tensor (start_i = context_seq_offset[i], else the packed prefix offset / i *
+# seqlen for padded input / the running sum of the lengths for outputs) and sits at cache
+# position cache_seq_offset[i] + j of cache batch cache_bs_id[i] (default i; negative: skip).
+# Tokens outside the cache or the token tensor are skipped.
+
+
+def reshape_linear_cache(
+    key: torch.Tensor,
+    value: Optional[torch.Tensor],
+    key_cache: torch.Tensor,
+    value_cache: Optional[torch.Tensor],
+    context_lengths: torch.Tensor,
+    max_context_len: int,
+    packed: bool,
+    context_seq_offset: Optional[torch.Tensor],
+    cache_bs_id: Optional[torch.Tensor],
+    cache_seqlen_offset: Optional[torch.Tensor],
+) -> Union[Tuple[torch.Tensor], torch.Tensor]:
+    """Copy key/value token rows (packed ``[total, heads, head_size]`` with ``context_lengths``
+    holding batch + 1 offsets, or padded ``[batch, seqlen, heads, head_size]`` with lengths)
+    into the linear caches, byte for byte (float, half, bfloat16, int8).
+
+    Reference: ``_ops.py:1189-1249``.  Returns ``(key_cache, value_cache)`` or ``key_cache``.
+    """
+    torch.ops.torch_mlu_ops.reshape_linear_cache(
+        key, value, key_cache, value_cache, context_lengths, max_context_len, packed,
+        context_seq_offset, cache_bs_id, cache_seqlen_offset)
+    return (key_cache, value_cache) if value_cache is not None else key_cache
+
+
+def quant_to_linear_cache(
+    key: torch.Tensor,
+    value: Optional[torch.Tensor],
+    key_cache: torch.Tensor,
+    value_cache: Optional[torch.Tensor],
+    key_cache_quant_scale: torch.Tensor,
+    value_cache_quant_scale: Optional[torch.Tensor],
+    context_lengths: torch.Tensor,
+    max_context_len: int,
+    packed: bool,
+    context_seq_offset: Optional[torch.Tensor],
+    cache_bs_id: Optional[torch.Tensor],
+    cache_seqlen_offset: Optional[torch.Tensor],
+    quant_bit: int = 8,
+) -> Tuple[torch.Tensor]:
+    """Dynamic quantisation of key/value into the linear caches, per (token, head) (scale
+    ``[max_batch, heads, cache_len]``) or per group of ``head_size / group_num`` channels (scale
+    ``[..., group_num]``).  int8 caches: ``scale = fp32(amax) / 127``, ``code =
+    clip(round_half_even(x / scale), -128, 127)``; float8_e4m3fn caches: ``scale = fp32(amax) /
+    448``, ``code = clip(x / scale, -448, 448)`` rounded to nearest even.  An all-zero group
+    stores scale 0 and codes 0.  ``quant_bit`` must be 8.
+
+    Reference: ``_ops.py:1708-1806`` (math ``:1725-1750``).  Returns
+    ``(key_cache, value_cache, key_scale, value_scale)`` or ``(key_cache, key_scale)``.
+    """
+    torch.ops.torch_mlu_ops.quant_to_linear_cache(
+        key, value, key_cache, value_cache, key_cache_quant_scale, value_cache_quant_scale,
+        context_lengths, max_context_len, packed, context_seq_offset, cache_bs_id,
+        cache_seqlen_offset, quant_bit)
+    if value_cache is not None:
+        return (key_cache, value_cache, key_cache_quant_scale, value_cache_quant_scale)
+    return (key_cache, key_cache_quant_scale)
+
+
+def offline_quant_to_linear_cache(
+    key: torch.Tensor,
+    value: Optional[torch.Tensor],
+    key_cache: torch.Tensor,
+    value_cache: Optional[torch.Tensor],
+    key_cache_quant_scale: Union[torch.Tensor, float],
+    value_cache_quant_scale: Optional[Union[torch.Tensor, float]],
+    context_lengths: torch.Tensor,
+    max_context_len: int,
+    quant_mode: int,
+    packed: bool,
+    context_seq_offset: Optional[torch.Tensor],
+    cache_bs_id: Optional[torch.Tensor],
+    cache_seqlen_offset: Optional[torch.Tensor],
+) -> Tuple[torch.Tensor]:
+    """Static quantisation of key/value into the linear caches: ``q = fp32(x) / scale`` (IEEE
+    divide) with ``quant_mode`` 0: a ``[heads, head_size]`` scale per channel, 1: a
+    ``[heads, cache_len]`` scale per head and cache position, 2/3: a number; int8 caches store
+    ``clip(round_half_even(q), -128, 127)``, float8_e4m3fn caches ``clip(q, -448, 448)``
+    rounded to nearest even.  No scales are written.
+
+    Reference: ``_ops.py:1808-1919`` (math ``:1829-1840``).  Returns
+    ``(key_cache, value_cache, key_scale, value_scale)`` or ``(key_cache, key_scale)``.
+    """
+    if torch.is_tensor(key_cache_quant_scale):
+        torch.ops.torch_mlu_ops.offline_quant_to_linear_cache(
+            key, value, key_cache, value_cache, key_cache_quant_scale, value_cache_quant_scale,
+            context_lengths, max_context_len, quant_mode, packed, context_seq_offset,
+            cache_bs_id, cache_seqlen_offset, 1.0, 1.0)
+    else:
+        torch.ops.torch_mlu_ops.offline_quant_to_linear_cache(
+            key, value, key_cache, value_cache, None, None, context_lengths, max_context_len,
+            quant_mode, packed, context_seq_offset, cache_bs_id, cache_seqlen_offset,
+            key_cache_quant_scale,
+            value_cache_quant_scale if value_cache_quant_scale is not None else 1.0)
+    if value_cache is not None:
+        return (key_cache, value_cache, key_cache_quant_scale, value_cache_quant_scale)
+    return (key_cache, key_cache_quant_scale)
+
+
+def dequant_from_linear_cache(
+    key: torch.Tensor,
+    value: Optional[torch.Tensor],
+    key_cache: torch.Tensor,
+    value_cache: Optional[torch.Tensor],
+    key_cache_quant_scale: torch.Tensor,
+    value_cache_quant_scale: Optional[torch.Tensor],
+    context_lengths: torch.Tensor,
+    max_context_len: int,
+    context_seq_offset: Optional[torch.Tensor],
+    cache_bs_id: Optional[torch.Tensor],
+    cache_seq_offset: Optional[torch.Tensor],
+    quant_mode: int = 0,
+    quant_bit: int = 8,
+) -> None:
+    """``key[start_i + j] = (fp32(code) * scale).to(key.dtype)`` from the int8 linear caches,
+    ``quant_mode`` 0: scale ``[heads, head_size]``; 1: per-token ``[max_batch, heads,
+    cache_len]``.  ``context_lengths`` holds ``[batch]`` lengths; ``quant_bit`` must be 8.
+
+    Reference: ``_ops.py:3642-3732`` (math ``:3663-3683``).  Returns None.
+    """
+    torch.ops.torch_mlu_ops.dequant_from_linear_cache(
+        key, value, key_cache, value_cache, key_cache_quant_scale, value_cache_quant_scale,
+        context_lengths, max_context_len, context_seq_offset, cache_bs_id, cache_seq_offset,
+        quant_mode, quant_bit)
+
+
+def reshape_from_cache(
+    key: torch.Tensor,
+    value: Optional[torch.Tensor],
+    key_cache: torch.Tensor,
+    value_cache: Optional[torch.Tensor],
+    context_lengths: torch.Tensor,
+    max_context_len: int,
+    context_seq_offset: Optional[torch.Tensor] = None,
+    block_tables: Optional[torch.Tensor] = None,
+    cache_seq_offset: Optional[torch.Tensor] = None,
+) -> None:
+    """Copy cache rows back to token-major ``key [total, heads, head_size]`` (and value).
+    Linear mode (no ``block_tables``, or a ``[batch, 1]`` table naming each sequence's cache
+    batch): sequence i reads positions ``cache_seq_offset[i] + j``.  Paged mode (``[batch,
+    max_blocks]`` table over ``[num_blocks, heads, block_size, head_size]`` caches): position p
+    is row ``p % block_size`` of page ``block_tables[i, p // block_size]``.
+
+    Reference: ``_ops.py:3898-3969`` (math ``:3905-3926``).  Returns None.
+    """
+    torch.ops.torch_mlu_ops.reshape_from_cache(
+        key, value, key_cache, value_cache, context_lengths, max_context_len,
+        context_seq_offset, block_tables, cache_seq_offset)

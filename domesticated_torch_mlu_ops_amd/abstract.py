@@ -81,3 +81,63 @@ def scaled_quantize_abstract(x: Tensor, output: Tensor, output_scale: Optional[T
                              output_reduced: Optional[Tensor] = None,
                              group_size: int = 1) -> None:
     return None
+
+
+@torch.library.register_fake("torch_mlu_ops::reshape_linear_cache")
+def reshape_linear_cache_abstract(key: Tensor, value: Optional[Tensor], key_cache: Tensor,
+                                  value_cache: Optional[Tensor], context_lengths: Tensor,
+                                  max_context_len: int, packed: bool,
+                                  context_seq_offset: Optional[Tensor],
+                                  cache_bs_id: Optional[Tensor],
+                                  cache_seqlen_offset: Optional[Tensor]) -> None:
+    return None
+
+
+@torch.library.register_fake("torch_mlu_ops::quant_to_linear_cache")
+def quant_to_linear_cache_abstract(key: Tensor, value: Optional[Tensor], key_cache: Tensor,
+                                   value_cache: Optional[Tensor], key_cache_scale: Tensor,
+                                   value_cache_scale: Optional[Tensor], context_lengths: Tensor,
+                                   max_context_len: int, packed: bool,
+                                   context_seq_offset: Optional[Tensor],
+                                   cache_bs_id: Optional[Tensor],
+                                   cache_seqlen_offset: Optional[Tensor],
+                                   quant_bit: int = 8) -> None:
+    return None
+
+
+@torch.library.register_fake("torch_mlu_ops::offline_quant_to_linear_cache")
+def offline_quant_to_linear_cache_abstract(key: Tensor, value: Optional[Tensor],
+                                           key_cache: Tensor, value_cache: Optional[Tensor],
+                                           key_cache_scale: Optional[Tensor],
+                                           value_cache_scale: Optional[Tensor],
+                                           context_lengths: Tensor, max_context_len: int,
+                                           quant_mode: int, packed: bool,
+                                           context_seq_offset: Optional[Tensor],
+                                           cache_bs_id: Optional[Tensor],
+                                           cache_seqlen_offset: Optional[Tensor],
+                                           key_cache_scale_per_tensor: float,
+                                           value_cache_scale_per_tensor: float) -> None:
+    return None
+
+
+@torch.library.register_fake("torch_mlu_ops::dequant_from_linear_cache")
+def dequant_from_linear_cache_abstract(key: Tensor, value: Optional[Tensor], key_cache: Tensor,
+                                       value_cache: Optional[Tensor],
+                                       key_cache_quant_scale: Tensor,
+                                       value_cache_quant_scale: Optional[Tensor],
+                                       context_lengths: Tensor, max_context_len: int,
+                                       context_seq_offset: Optional[Tensor],
+                                       cache_bs_id: Optional[Tensor],
+                                       cache_seq_offset: Optional[Tensor],
+                                       quant_mode: int = 0, quant_bit: int = 8) -> None:
+    return None
+
+
+@torch.library.register_fake("torch_mlu_ops::reshape_from_cache")
+def reshape_from_cache_abstract(key: Tensor, value: Optional[Tensor], key_cache: Tensor,
+                                value_cache: Optional[Tensor], context_lengths: Tensor,
+                                max_context_len: int, context_seq_offset: Optional[Tensor] = None,
+                                block_tables: Optional[Tensor] = None,
+                                cache_seq_offset: Optional[Tensor] = None) -> None:
+    return None
+

@@ -1,0 +1,739 @@
+// The linear-cache siblings of the paged path, for gfx950.  A linear cache is
+// [max_batch, heads, cache_len, head_dim]: one cache batch per sequence, tokens at
+// consecutive positions.  Five reference ops share one addressing model:
+//
+//   reshape_linear_cache            token rows -> cache, byte copy     _ops.py:1189-1249
+//   quant_to_linear_cache           dynamic int8 / fp8 per token/group _ops.py:1708-1806
+//   offline_quant_to_linear_cache   static int8 / fp8                  _ops.py:1808-1919
+//   dequant_from_linear_cache       int8 cache -> token rows           _ops.py:3642-3732
+//   reshape_from_cache              cache -> token rows, byte copy     _ops.py:3898-3969
+//
+// Sequence i covers len_i = min(context_lengths[i], max_context_len) tokens (with packed
+// input context_lengths holds batch + 1 prefix offsets and len_i = cu[i + 1] - cu[i]).  Its
+// token j is row start_i + j of the token-major tensor [rows, heads, head_dim]: start_i =
+// context_seq_offset[i] if given, else cu[i] (packed input), i * seqlen (padded input) or
+// the exclusive prefix sum of the lengths (the outputs of the two read ops).  Its cache
+// position is pos = cache_seq_offset[i] + j (else j), in cache batch cache_bs_id[i] (else i;
+// negative: the sequence is skipped).  reshape_from_cache's block table [batch, max_blocks]
+// generalises this to pages of block_rows positions: position pos lives in row
+// pos % block_rows of page block_tables[i, pos / block_rows]; a one-column table is the
+// linear layout with the table naming the cache batch.  Tokens whose row, cache batch / page
+// or position falls outside its tensor are skipped.
+//
+// Per-token scales are [max_batch, heads, cache_len] (x groups for group-wise dynamic
+// quantisation), static scales per channel [heads, head_dim], per head [heads, cache_len]
+// (indexed by cache position) or one number.  The arithmetic is the paged kernels'
+// (tmo_device.h): int8 dynamic = RN(amax / 127) + IEEE quotients, fp8 dynamic = RN(amax / 448)
+// + IEEE quotients clamped to +-448 and rounded to e4m3fn, static = IEEE quotients,
+// dequant = RN(fp32(code) * scale).
+//
+// Grid: y = sequence, x = (token tile, head) with the head fastest, so the workgroups of one
+// token tile read neighbouring parts of the same token rows, and a workgroup's cache rows are
+// consecutive.  Copies move 16 bytes per lane (G = row bytes / 16 lanes per row); the
+// quantising kernels take 8 elements per lane (G = head_dim / 8).
+#include "tmo_device.h"
+
+namespace tmo {
+namespace {
+
+struct LinParams {
+  void* tok[2];          // token-major tensors: input of the write ops, output of the reads
+  void* cache[2];
+  int64_t st[2], sh[2];  // token / head strides of the token tensors (elements)
+  int64_t rows;          // rows of the token tensors
+  int32_t heads, head_dim;
+  int32_t nkv;
+  int32_t in_dir;        // 1: token rows -> cache
+  int64_t blocks;        // cache batches (linear) or pages (block table)
+  int64_t block_rows;    // cache_len (linear) or rows per page
+  const int32_t* lens;
+  int32_t packed;
+  int64_t pad_seqlen;
+  const int32_t* seq_off;
+  const int32_t* bs_id;
+  const int32_t* cache_off;
+  const int32_t* block_tables;
+  int64_t max_blocks;
+  int64_t max_len;
+  float* scale[2];        // per-token scales: written by the dynamic quantiser, read by dequant
+  const float* chan[2];   // static / dequant per-channel [H, D] or static per-head [H, cache_len]
+  float tscale[2];        // static per-tensor scales
+  int32_t smode;          // 0 channel, 1 head (static) or token (dequant), 2 tensor
+  int32_t groups;         // dynamic scale groups per row
+  int32_t op;             // generic kernel: 0 copy, 1 dynamic quant, 2 static quant, 3 dequant
+  int32_t es;             // copies: bytes per element
+};
+
+// Workgroup-uniform addressing of one sequence.
+struct Seq {
+  int64_t len, start, pos0;
+};
+
+// Exclusive prefix sum of the lengths before sequence i, by the whole workgroup.
+__device__ int64_t length_prefix(const LinParams& p, int64_t i) {
+  __shared__ int64_t part[256 / kWave];
+  int64_t acc = 0;
+  for (int64_t k = threadIdx.x; k < i; k += 256) acc += p.lens[k];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, kWave);
+  if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = acc;
+  __syncthreads();
+  int64_t total = 0;
+#pragma unroll
+  for (int w = 0; w < 256 / kWave; ++w) total += part[w];
+  return total;
+}
+
+// Every thread of the workgroup must call this (the prefix sum synchronises).
+__device__ Seq sequence(const LinParams& p, int64_t i) {
+  Seq s;
+  const int64_t len = p.packed ? (int64_t)p.lens[i + 1] - p.lens[i] : (int64_t)p.lens[i];
+  s.len = len < p.max_len ? len : p.max_len;
+  if (p.seq_off) {
+    s.start = p.seq_off[i];
+  } else if (p.in_dir) {
+    s.start = p.packed ? (int64_t)p.lens[i] : i * p.pad_seqlen;
+  } else {
+    s.start = length_prefix(p, i);
+  }
+  s.pos0 = p.cache_off ? (int64_t)p.cache_off[i] : 0;
+  return s;
+}
+
+// Cache row of the token at cache position `pos` for head h, or -1 when it is skipped.
+__device__ __forceinline__ int64_t cache_row(const LinParams& p, int64_t i, int64_t pos, int h) {
+  if (pos < 0) return -1;
+  int64_t blk, r;
+  if (p.block_tables) {
+    const int64_t col = pos / p.block_rows;
+    if (col >= p.max_blocks) return -1;
+    blk = p.block_tables[i * p.max_blocks + col];
+    r = pos - col * p.block_rows;
+  } else {
+    if (pos >= p.block_rows) return -1;
+    blk = p.bs_id ? (int64_t)p.bs_id[i] : i;
+    r = pos;
+  }
+  if (blk < 0 || blk >= p.blocks) return -1;
+  return (blk * p.heads + h) * p.block_rows + r;
+}
+
+// ------------------------------------------------------------------------------ byte copies
+
+// reshape_linear_cache / reshape_from_cache: G lanes x 16 bytes per row.
+template <int G>
+__global__ __launch_bounds__(256) void lin_copy(LinParams p) {
+  constexpr int kRows = 256 / G;
+  const int64_t es = p.es, row_bytes = (int64_t)p.head_dim * p.es;
+  const int lane = threadIdx.x & (G - 1);
+  const int64_t i = blockIdx.y;
+  const int h = blockIdx.x % p.heads;
+  const int64_t tile = blockIdx.x / p.heads;
+  const Seq s = sequence(p, i);
+  const int64_t j = tile * kRows + threadIdx.x / G;
+  if (j >= s.len) return;
+  const int64_t r = s.start + j;
+  const int64_t crow = cache_row(p, i, s.pos0 + j, h);
+  if (r < 0 || r >= p.rows || crow < 0) return;
+  u32x4 v[2];
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    if (kv >= p.nkv) continue;
+    const char* t =
+        static_cast<const char*>(p.tok[kv]) + (r * p.st[kv] + (int64_t)h * p.sh[kv]) * es;
+    const char* c = static_cast<const char*>(p.cache[kv]) + crow * row_bytes;
+    v[kv] = *reinterpret_cast<const u32x4*>((p.in_dir ? t : c) + lane * 16);
+  }
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    if (kv >= p.nkv) continue;
+    char* t = static_cast<char*>(p.tok[kv]) + (r * p.st[kv] + (int64_t)h * p.sh[kv]) * es;
+    char* c = static_cast<char*>(p.cache[kv]) + crow * row_bytes;
+    *reinterpret_cast<u32x4*>((p.in_dir ? c : t) + lane * 16) = v[kv];
+  }
+}
+
+// ------------------------------------------------------------------------------ 8-element I/O
+
+template <class Tag>
+__device__ __forceinline__ void load8(const void* base, int64_t e, float* v) {
+  if constexpr (Tag::kBytes == 4) {
+    const u32x4* q = reinterpret_cast<const u32x4*>(static_cast<const float*>(base) + e);
+    const u32x4 a = q[0], b = q[1];
+    unpack(F32{}, a, v);
+    unpack(F32{}, b, v + 4);
+  } else {
+    unpack(Tag{}, *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + e), v);
+  }
+}
+
+template <class Tag>
+__device__ __forceinline__ void store8(void* base, int64_t e, const float* v) {
+  if constexpr (Tag::kBytes == 4) {
+    u32x4 a, b;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      a[k] = __float_as_uint(v[k]);
+      b[k] = __float_as_uint(v[4 + k]);
+    }
+    u32x4* q = reinterpret_cast<u32x4*>(static_cast<float*>(base) + e);
+    q[0] = a;
+    q[1] = b;
+  } else {
+    u32x4 w;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = pack2(Tag{}, v[2 * k], v[2 * k + 1]);
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + e) = w;
+  }
+}
+
+// Max over aligned groups of `gl` lanes (a power of two <= G, the same in every lane).
+template <int G>
+__device__ __forceinline__ uint32_t lane_group_max(uint32_t v, int gl) {
+  if (G >= 2 && gl >= 2) v = max(v, dpp<kDppQuadSwap1>(v));
+  if (G >= 4 && gl >= 4) v = max(v, dpp<kDppQuadSwap2>(v));
+  if (G >= 8 && gl >= 8) v = max(v, dpp<kDppRowHalfMirror>(v));
+  if (G >= 16 && gl >= 16) v = max(v, dpp<kDppRowMirror>(v));
+  if (G >= 32 && gl >= 32) v = max(v, (uint32_t)__shfl_xor((int)v, 16, kWave));
+  if (G >= 64 && gl >= 64) v = max(v, (uint32_t)__shfl_xor((int)v, 32, kWave));
+  return v;
+}
+
+// fp8 dynamic scale of a group: RN(amax / 448) (IEEE divide, once per group) and, when
+// kFastDivMinScale <= s < inf, y = RN(1 / s) for the reciprocal quotient (div_by_recip gives
+// the IEEE quotient there, as for the int8 scale).  s == 0: every code is +0.
+__device__ __forceinline__ RowScale make_fp8_scale(float amax) {
+  RowScale r;
+  r.s = amax / 448.0f;
+  r.fast = r.s >= kFastDivMinScale && r.s < __builtin_inff();
+  r.y = r.fast ? 1.0f / r.s : 0.0f;
+  return r;
+}
+
+// ------------------------------------------------------------------------------ quantisers
+
+// quant_to_linear_cache (kStatic false) / offline_quant_to_linear_cache (kStatic true):
+// G = head_dim / 8 lanes per row, 8 channels per lane.
+template <class Tag, int G, bool kFp8, bool kStatic>
+__global__ __launch_bounds__(256) void lin_quant(LinParams p) {
+  constexpr int kRows = 256 / G;
+  const int lane = threadIdx.x & (G - 1);
+  const int64_t i = blockIdx.y;
+  const int h = blockIdx.x % p.heads;
+  const int64_t tile = blockIdx.x / p.heads;
+  const Seq s = sequence(p, i);
+  const int64_t j = tile * kRows + threadIdx.x / G;
+  if (j >= s.len) return;  // the same in all lanes of a row
+  const int64_t r = s.start + j;
+  const int64_t pos = s.pos0 + j;
+  const int64_t crow = cache_row(p, i, pos, h);
+  if (r < 0 || r >= p.rows || crow < 0) return;
+  const int d0 = lane * 8;
+
+  float x[2][8];
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv)
+    if (kv < p.nkv) load8<Tag>(p.tok[kv], r * p.st[kv] + (int64_t)h * p.sh[kv] + d0, x[kv]);
+
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    if (kv >= p.nkv) continue;
+    uint32_t c[2];
+    if constexpr (kStatic) {
+      float sc[8], y[8], q[8];
+      if (p.smode == 0) {
+        const u32x4* sp =
+            reinterpret_cast<const u32x4*>(p.chan[kv] + (int64_t)h * p.head_dim + d0);
+        const u32x4 a = sp[0], b = sp[1];
+        unpack(F32{}, a, sc);
+        unpack(F32{}, b, sc + 4);
+      } else {
+        const float one =
+            p.smode == 1 ? p.chan[kv][(int64_t)h * p.block_rows + pos] : p.tscale[kv];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sc[e] = one;
+      }
+      bool fast = true;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) fast &= static_scale_fast(sc[e]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = fast ? recip_rn(sc[e]) : 0.0f;
+      static_quotients<8>(x[kv], sc, y, fast, q);
+      encode_static<8, kFp8>(q, c);
+    } else {
+      const int gl = G / p.groups;  // lanes per scale group
+      float m = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = abs_max(m, x[kv][e]);
+      const float amax = __uint_as_float(lane_group_max<G>(__float_as_uint(m), gl));
+      float scale;
+      if constexpr (kFp8) {
+        const RowScale rs = make_fp8_scale(amax);
+        float q[8];
+        if (rs.fast) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) q[e] = div_by_recip(x[kv][e], rs.s, rs.y);
+        } else {
+          keep_branch();
+#pragma unroll
+          for (int e = 0; e < 8; ++e) q[e] = x[kv][e] / rs.s;  // IEEE divide
+        }
+        encode_static<8, true>(q, c);
+        if (rs.s == 0.0f) c[0] = c[1] = 0u;  // all-zero group: +0 codes, as the int8 path
+        scale = rs.s;
+      } else {
+        const RowScale rs = make_row_scale(amax);
+        encode_row<8>(x[kv], rs, c);
+        scale = rs.s;
+      }
+      if ((lane & (gl - 1)) == 0) p.scale[kv][crow * p.groups + lane / gl] = scale;
+    }
+    u32x2 c2;
+    c2[0] = c[0];
+    c2[1] = c[1];
+    *reinterpret_cast<u32x2*>(static_cast<int8_t*>(p.cache[kv]) + crow * p.head_dim + d0) = c2;
+  }
+}
+
+// dequant_from_linear_cache: out = RN(fp32(code) * scale), 8 channels per lane.
+template <class Tag, int G>
+__global__ __launch_bounds__(256) void lin_dequant(LinParams p) {
+  constexpr int kRows = 256 / G;
+  const int lane = threadIdx.x & (G - 1);
+  const int64_t i = blockIdx.y;
+  const int h = blockIdx.x % p.heads;
+  const int64_t tile = blockIdx.x / p.heads;
+  const Seq s = sequence(p, i);
+  const int64_t j = tile * kRows + threadIdx.x / G;
+  if (j >= s.len) return;
+  const int64_t r = s.start + j;
+  const int64_t crow = cache_row(p, i, s.pos0 + j, h);
+  if (r < 0 || r >= p.rows || crow < 0) return;
+  const int d0 = lane * 8;
+  u32x2 code[2];
+  float sc[2][8];
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    if (kv >= p.nkv) continue;
+    code[kv] = *reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(p.cache[kv]) +
+                                               crow * p.head_dim + d0);
+    if (p.smode == 0) {
+      const u32x4* sp = reinterpret_cast<const u32x4*>(p.chan[kv] + (int64_t)h * p.head_dim + d0);
+      const u32x4 a = sp[0], b = sp[1];
+      unpack(F32{}, a, sc[kv]);
+      unpack(F32{}, b, sc[kv] + 4);
+    } else {
+      const float one = p.scale[kv][crow];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sc[kv][e] = one;
+    }
+  }
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    if (kv >= p.nkv) continue;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      v[e] = (float)(int8_t)(code[kv][e >> 2] >> (8 * (e & 3))) * sc[kv][e];
+    store8<Tag>(p.tok[kv], r * p.st[kv] + (int64_t)h * p.sh[kv] + d0, v);
+  }
+}
+
+// ------------------------------------------------------------------------------ generic path
+
+// Any head_dim / alignment: one wavefront per (token, head) row, element by element, IEEE
+// divides.  p.op: 0 copy (p.es bytes per element), 1 dynamic quant, 2 static quant, 3 dequant.
+template <class Tag, bool kFp8>
+__global__ __launch_bounds__(256) void lin_generic(LinParams p) {
+  const int op = p.op;
+  const int64_t es = p.es;
+  constexpr int kRows = 256 / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t i = blockIdx.y;
+  const int h = blockIdx.x % p.heads;
+  const int64_t tile = blockIdx.x / p.heads;
+  const Seq s = sequence(p, i);
+  const int64_t j = tile * kRows + threadIdx.x / kWave;
+  if (j >= s.len) return;
+  const int64_t r = s.start + j;
+  const int64_t pos = s.pos0 + j;
+  const int64_t crow = cache_row(p, i, pos, h);
+  if (r < 0 || r >= p.rows || crow < 0) return;
+  const int D = p.head_dim;
+  for (int kv = 0; kv < p.nkv; ++kv) {
+    const int64_t te = r * p.st[kv] + (int64_t)h * p.sh[kv];
+    if (op == 0) {
+      char* t = static_cast<char*>(p.tok[kv]) + te * es;
+      char* c = static_cast<char*>(p.cache[kv]) + crow * D * es;
+      char* to = p.in_dir ? c : t;
+      const char* from = p.in_dir ? t : c;
+      for (int b = lane; b < D * es; b += kWave) to[b] = from[b];
+      continue;
+    }
+    uint8_t* codes = static_cast<uint8_t*>(p.cache[kv]) + crow * D;
+    if (op == 3) {
+      for (int d = lane; d < D; d += kWave) {
+        const float sc = p.smode == 0 ? p.chan[kv][(int64_t)h * D + d] : p.scale[kv][crow];
+        store1(Tag{}, p.tok[kv], te + d, (float)(int8_t)codes[d] * sc);
+      }
+    } else if (op == 2) {
+      for (int d = lane; d < D; d += kWave) {
+        const float sc = p.smode == 0 ? p.chan[kv][(int64_t)h * D + d]
+                       : p.smode == 1 ? p.chan[kv][(int64_t)h * p.block_rows + pos]
+                                      : p.tscale[kv];
+        const float q = load1(Tag{}, p.tok[kv], te + d) / sc;  // IEEE divide
+        const uint32_t b =
+            kFp8 ? fp8e4m3_bits(__builtin_amdgcn_fmed3f(q, -448.0f, 448.0f)) : code_bits(q);
+        codes[d] = (uint8_t)(b & 0xffu);
+      }
+    } else {
+      const int gs = D / p.groups;
+      for (int g = 0; g < p.groups; ++g) {
+        float m = 0.0f;
+        for (int d = lane; d < gs; d += kWave)
+          m = abs_max(m, load1(Tag{}, p.tok[kv], te + g * gs + d));
+        const float amax = __uint_as_float(group_max_u32<kWave>(__float_as_uint(m)));
+        const float sc = amax / (kFp8 ? 448.0f : 127.0f);  // IEEE divide
+        for (int d = lane; d < gs; d += kWave) {
+          const float q = load1(Tag{}, p.tok[kv], te + g * gs + d) / sc;
+          uint32_t b;
+          if (sc == 0.0f) {
+            b = 0u;
+          } else if (kFp8) {
+            b = fp8e4m3_bits(__builtin_amdgcn_fmed3f(q, -448.0f, 448.0f));
+          } else {
+            b = code_bits(q);
+          }
+          codes[g * gs + d] = (uint8_t)(b & 0xffu);
+        }
+        if (lane == 0) p.scale[kv][crow * p.groups + g] = sc;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------ launchers
+
+bool aligned(const void* q, int a) { return reinterpret_cast<uintptr_t>(q) % a == 0; }
+
+int grid_for(const LinParams& p, int64_t batch, int rows_per_wg, dim3& grid) {
+  const int64_t tiles = (p.max_len + rows_per_wg - 1) / rows_per_wg;
+  const int64_t gx = tiles * p.heads;
+  if (gx > 0x7fffffffLL || batch > 65535) return TMO_ERR_INVALID_ARGUMENT;
+  grid = dim3((unsigned)gx, (unsigned)batch);
+  return TMO_OK;
+}
+
+// 16-byte vector access to the token tensors: base, token and head strides aligned.
+bool token_vec_ok(const LinParams& p, int es) {
+  for (int kv = 0; kv < p.nkv; ++kv)
+    if (!aligned(p.tok[kv], 16) || (p.st[kv] * es) % 16 != 0 || (p.sh[kv] * es) % 16 != 0)
+      return false;
+  return true;
+}
+
+template <class Tag>
+int launch_generic(const LinParams& p, int64_t batch, int op, int es, bool fp8, hipStream_t st) {
+  dim3 grid;
+  const int rc = grid_for(p, batch, 256 / kWave, grid);
+  if (rc != TMO_OK) return rc;
+  LinParams q = p;
+  q.op = op;
+  q.es = es;
+  return fp8 ? launch_kernel(lin_generic<Tag, true>, grid, dim3(256), st, q)
+             : launch_kernel(lin_generic<Tag, false>, grid, dim3(256), st, q);
+}
+
+int launch_copy(const LinParams& p, int64_t batch, int es, hipStream_t st) {
+  const int64_t row_bytes = (int64_t)p.head_dim * es;
+  const int G = row_bytes % 16 == 0 && row_bytes / 16 <= kWave ? (int)(row_bytes / 16) : 0;
+  bool vec = G >= 1 && (G & (G - 1)) == 0 && token_vec_ok(p, es);
+  for (int kv = 0; kv < p.nkv && vec; ++kv) vec = aligned(p.cache[kv], 16);
+  if (!vec) return launch_generic<BF16>(p, batch, 0, es, false, st);
+  dim3 grid;
+  const int rc = grid_for(p, batch, 256 / G, grid);
+  if (rc != TMO_OK) return rc;
+  LinParams q = p;
+  q.es = es;
+  switch (G) {
+    case 1: return launch_kernel(lin_copy<1>, grid, dim3(256), st, q);
+    case 2: return launch_kernel(lin_copy<2>, grid, dim3(256), st, q);
+    case 4: return launch_kernel(lin_copy<4>, grid, dim3(256), st, q);
+    case 8: return launch_kernel(lin_copy<8>, grid, dim3(256), st, q);
+    case 16: return launch_kernel(lin_copy<16>, grid, dim3(256), st, q);
+    case 32: return launch_kernel(lin_copy<32>, grid, dim3(256), st, q);
+    default: return launch_kernel(lin_copy<64>, grid, dim3(256), st, q);
+  }
+}
+
+// Lanes per row of the 8-channels-per-lane kernels, or 0 when the generic path must run.
+int lanes8(const LinParams& p, int es) {
+  const int G = p.head_dim % 8 == 0 ? p.head_dim / 8 : 0;
+  if (G < 1 || G > kWave || (G & (G - 1)) != 0 || !token_vec_ok(p, es)) return 0;
+  for (int kv = 0; kv < p.nkv; ++kv) {
+    if (!aligned(p.cache[kv], 8)) return 0;
+    if (p.smode == 0 && p.chan[kv] && !aligned(p.chan[kv], 16)) return 0;
+  }
+  return G;
+}
+
+template <class Tag, bool kFp8, bool kStatic>
+int launch_quant(const LinParams& p, int64_t batch, hipStream_t st) {
+  const int G = lanes8(p, Tag::kBytes);
+  bool vec = G > 0;
+  if (vec && !kStatic) {  // scale groups must be whole, aligned sets of lanes
+    const int gl = G % p.groups == 0 ? G / p.groups : 0;
+    vec = gl >= 1 && (gl & (gl - 1)) == 0;
+  }
+  if (!vec) return launch_generic<Tag>(p, batch, kStatic ? 2 : 1, Tag::kBytes, kFp8, st);
+  dim3 grid;
+  const int rc = grid_for(p, batch, 256 / G, grid);
+  if (rc != TMO_OK) return rc;
+  switch (G) {
+    case 1: return launch_kernel(lin_quant<Tag, 1, kFp8, kStatic>, grid, dim3(256), st, p);
+    case 2: return launch_kernel(lin_quant<Tag, 2, kFp8, kStatic>, grid, dim3(256), st, p);
+    case 4: return launch_kernel(lin_quant<Tag, 4, kFp8, kStatic>, grid, dim3(256), st, p);
+    case 8: return launch_kernel(lin_quant<Tag, 8, kFp8, kStatic>, grid, dim3(256), st, p);
+    case 16: return launch_kernel(lin_quant<Tag, 16, kFp8, kStatic>, grid, dim3(256), st, p);
+    case 32: return launch_kernel(lin_quant<Tag, 32, kFp8, kStatic>, grid, dim3(256), st, p);
+    default: return launch_kernel(lin_quant<Tag, 64, kFp8, kStatic>, grid, dim3(256), st, p);
+  }
+}
+
+template <bool kStatic>
+int dispatch_quant(const LinParams& p, int64_t batch, int dtype, bool fp8, hipStream_t st) {
+  switch (dtype) {
+    case TMO_DTYPE_F16:
+      return fp8 ? launch_quant<F16, true, kStatic>(p, batch, st)
+                 : launch_quant<F16, false, kStatic>(p, batch, st);
+    case TMO_DTYPE_BF16:
+      return fp8 ? launch_quant<BF16, true, kStatic>(p, batch, st)
+                 : launch_quant<BF16, false, kStatic>(p, batch, st);
+    default:
+      return fp8 ? launch_quant<F32, true, kStatic>(p, batch, st)
+                 : launch_quant<F32, false, kStatic>(p, batch, st);
+  }
+}
+
+template <class Tag>
+int launch_dequant(const LinParams& p, int64_t batch, hipStream_t st) {
+  const int G = lanes8(p, Tag::kBytes);
+  if (G == 0) return launch_generic<Tag>(p, batch, 3, Tag::kBytes, false, st);
+  dim3 grid;
+  const int rc = grid_for(p, batch, 256 / G, grid);
+  if (rc != TMO_OK) return rc;
+  switch (G) {
+    case 1: return launch_kernel(lin_dequant<Tag, 1>, grid, dim3(256), st, p);
+    case 2: return launch_kernel(lin_dequant<Tag, 2>, grid, dim3(256), st, p);
+    case 4: return launch_kernel(lin_dequant<Tag, 4>, grid, dim3(256), st, p);
+    case 8: return launch_kernel(lin_dequant<Tag, 8>, grid, dim3(256), st, p);
+    case 16: return launch_kernel(lin_dequant<Tag, 16>, grid, dim3(256), st, p);
+    case 32: return launch_kernel(lin_dequant<Tag, 32>, grid, dim3(256), st, p);
+    default: return launch_kernel(lin_dequant<Tag, 64>, grid, dim3(256), st, p);
+  }
+}
+
+int elem_bytes(int dtype) {
+  switch (dtype) {
+    case TMO_DTYPE_F32: return 4;
+    case TMO_DTYPE_F16:
+    case TMO_DTYPE_BF16: return 2;
+    case TMO_DTYPE_I8: return 1;
+    default: return 0;
+  }
+}
+
+bool float_dtype(int dtype) {
+  return dtype == TMO_DTYPE_F32 || dtype == TMO_DTYPE_F16 || dtype == TMO_DTYPE_BF16;
+}
+
+// Checks shared by the five entry points; fills the addressing part of `p`.
+int common_setup(LinParams& p, void* key, void* value, int64_t kst, int64_t ksh, int64_t vst,
+                 int64_t vsh, int64_t rows, void* kc, void* vc, int64_t blocks, int64_t heads,
+                 int64_t block_rows, int64_t head_size, const int32_t* lens, int64_t batch,
+                 int64_t max_len, int packed, int64_t seqlen, const int32_t* seq_off,
+                 const int32_t* bs_id, const int32_t* cache_off, bool in_dir) {
+  if (!key || !kc || !lens) return TMO_ERR_INVALID_ARGUMENT;
+  const bool has_v = value != nullptr;
+  if (has_v != (vc != nullptr)) return TMO_ERR_INVALID_ARGUMENT;
+  if (rows < 0 || blocks < 0 || heads <= 0 || block_rows < 0 || head_size <= 0 || batch < 0 ||
+      max_len < 0 || seqlen < 0)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (kst < 0 || ksh < 0 || (has_v && (vst < 0 || vsh < 0))) return TMO_ERR_INVALID_ARGUMENT;
+  if (heads > 0x7fffffffLL || head_size > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
+  p.tok[0] = key;
+  p.tok[1] = value;
+  p.cache[0] = kc;
+  p.cache[1] = vc;
+  p.st[0] = kst;
+  p.sh[0] = ksh;
+  p.st[1] = vst;
+  p.sh[1] = vsh;
+  p.rows = rows;
+  p.heads = (int32_t)heads;
+  p.head_dim = (int32_t)head_size;
+  p.nkv = has_v ? 2 : 1;
+  p.in_dir = in_dir ? 1 : 0;
+  p.blocks = blocks;
+  p.block_rows = block_rows;
+  p.lens = lens;
+  p.packed = packed ? 1 : 0;
+  p.pad_seqlen = seqlen;
+  p.seq_off = seq_off;
+  p.bs_id = bs_id;
+  p.cache_off = cache_off;
+  p.max_len = max_len;
+  p.groups = 1;
+  return TMO_OK;
+}
+
+bool nothing_to_do(const LinParams& p, int64_t batch) {
+  return batch == 0 || p.max_len == 0 || p.rows == 0 || p.blocks == 0 || p.block_rows == 0;
+}
+
+}  // namespace
+}  // namespace tmo
+
+using namespace tmo;
+
+extern "C" int tmo_hip_reshape_linear_cache(
+    const void* key, const void* value, int64_t key_stride_token, int64_t key_stride_head,
+    int64_t value_stride_token, int64_t value_stride_head, int64_t rows, void* key_cache,
+    void* value_cache, int64_t max_batch, int64_t num_heads, int64_t cache_len, int64_t head_size,
+    const int32_t* context_lengths, int64_t batch, int64_t max_context_len, int packed,
+    int64_t seqlen, const int32_t* context_seq_offset, const int32_t* cache_bs_id,
+    const int32_t* cache_seqlen_offset, int dtype, void* stream) {
+  const int es = elem_bytes(dtype);
+  if (es == 0) return TMO_ERR_UNSUPPORTED_DTYPE;
+  LinParams p{};
+  const int rc = common_setup(p, const_cast<void*>(key), const_cast<void*>(value),
+                              key_stride_token, key_stride_head, value_stride_token,
+                              value_stride_head, rows, key_cache, value_cache, max_batch,
+                              num_heads, cache_len, head_size, context_lengths, batch,
+                              max_context_len, packed, seqlen, context_seq_offset, cache_bs_id,
+                              cache_seqlen_offset, true);
+  if (rc != TMO_OK) return rc;
+  if (nothing_to_do(p, batch)) return TMO_OK;
+  return launch_copy(p, batch, es, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tmo_hip_quant_to_linear_cache(
+    const void* key, const void* value, int64_t key_stride_token, int64_t key_stride_head,
+    int64_t value_stride_token, int64_t value_stride_head, int64_t rows, void* key_cache,
+    void* value_cache, float* key_scale, float* value_scale, int64_t max_batch,
+    int64_t num_heads, int64_t cache_len, int64_t head_size, int64_t group_num,
+    const int32_t* context_lengths, int64_t batch, int64_t max_context_len, int packed,
+    int64_t seqlen, const int32_t* context_seq_offset, const int32_t* cache_bs_id,
+    const int32_t* cache_seqlen_offset, int quant_bit, int dtype, int cache_dtype, void* stream) {
+  if (!float_dtype(dtype) || (cache_dtype != TMO_DTYPE_I8 && cache_dtype != TMO_DTYPE_F8E4M3))
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (quant_bit != 8) return TMO_ERR_UNSUPPORTED_MODE;
+  if (group_num <= 0 || head_size % group_num != 0) return TMO_ERR_INVALID_ARGUMENT;
+  if (!key_scale || ((value != nullptr) != (value_scale != nullptr)))
+    return TMO_ERR_INVALID_ARGUMENT;
+  LinParams p{};
+  const int rc = common_setup(p, const_cast<void*>(key), const_cast<void*>(value),
+                              key_stride_token, key_stride_head, value_stride_token,
+                              value_stride_head, rows, key_cache, value_cache, max_batch,
+                              num_heads, cache_len, head_size, context_lengths, batch,
+                              max_context_len, packed, seqlen, context_seq_offset, cache_bs_id,
+                              cache_seqlen_offset, true);
+  if (rc != TMO_OK) return rc;
+  p.scale[0] = key_scale;
+  p.scale[1] = value_scale;
+  p.groups = (int32_t)group_num;
+  if (nothing_to_do(p, batch)) return TMO_OK;
+  return dispatch_quant<false>(p, batch, dtype, cache_dtype == TMO_DTYPE_F8E4M3,
+                               static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tmo_hip_offline_quant_to_linear_cache(
+    const void* key, const void* value, int64_t key_stride_token, int64_t key_stride_head,
+    int64_t value_stride_token, int64_t value_stride_head, int64_t rows, void* key_cache,
+    void* value_cache, const float* key_scale, const float* value_scale,
+    float key_scale_per_tensor, float value_scale_per_tensor, int quant_mode, int64_t max_batch,
+    int64_t num_heads, int64_t cache_len, int64_t head_size, const int32_t* context_lengths,
+    int64_t batch, int64_t max_context_len, int packed, int64_t seqlen,
+    const int32_t* context_seq_offset, const int32_t* cache_bs_id,
+    const int32_t* cache_seqlen_offset, int dtype, int cache_dtype, void* stream) {
+  if (!float_dtype(dtype) || (cache_dtype != TMO_DTYPE_I8 && cache_dtype != TMO_DTYPE_F8E4M3))
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (quant_mode < 0 || quant_mode > 3) return TMO_ERR_UNSUPPORTED_MODE;
+  const int smode = quant_mode >= 2 ? 2 : quant_mode;
+  if (smode < 2 && (!key_scale || ((value != nullptr) != (value_scale != nullptr))))
+    return TMO_ERR_INVALID_ARGUMENT;
+  LinParams p{};
+  const int rc = common_setup(p, const_cast<void*>(key), const_cast<void*>(value),
+                              key_stride_token, key_stride_head, value_stride_token,
+                              value_stride_head, rows, key_cache, value_cache, max_batch,
+                              num_heads, cache_len, head_size, context_lengths, batch,
+                              max_context_len, packed, seqlen, context_seq_offset, cache_bs_id,
+                              cache_seqlen_offset, true);
+  if (rc != TMO_OK) return rc;
+  p.smode = smode;
+  p.chan[0] = smode < 2 ? key_scale : nullptr;
+  p.chan[1] = smode < 2 ? value_scale : nullptr;
+  p.tscale[0] = key_scale_per_tensor;
+  p.tscale[1] = value_scale_per_tensor;
+  if (nothing_to_do(p, batch)) return TMO_OK;
+  return dispatch_quant<true>(p, batch, dtype, cache_dtype == TMO_DTYPE_F8E4M3,
+                              static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tmo_hip_dequant_from_linear_cache(
+    void* key, void* value, int64_t key_stride_token, int64_t key_stride_head,
+    int64_t value_stride_token, int64_t value_stride_head, int64_t rows, const int8_t* key_cache,
+    const int8_t* value_cache, const float* key_scale, const float* value_scale,
+    int64_t max_batch, int64_t num_heads, int64_t cache_len, int64_t head_size,
+    const int32_t* context_lengths, int64_t batch, int64_t max_context_len,
+    const int32_t* context_seq_offset, const int32_t* cache_bs_id, const int32_t* cache_seq_offset,
+    int quant_mode, int quant_bit, int out_dtype, void* stream) {
+  if (!float_dtype(out_dtype)) return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (quant_bit != 8 || (quant_mode != 0 && quant_mode != 1)) return TMO_ERR_UNSUPPORTED_MODE;
+  if (!key_scale || ((value != nullptr) != (value_scale != nullptr)))
+    return TMO_ERR_INVALID_ARGUMENT;
+  LinParams p{};
+  const int rc = common_setup(p, key, value, key_stride_token, key_stride_head,
+                              value_stride_token, value_stride_head, rows,
+                              const_cast<int8_t*>(key_cache), const_cast<int8_t*>(value_cache),
+                              max_batch, num_heads, cache_len, head_size, context_lengths, batch,
+                              max_context_len, 0, 0, context_seq_offset, cache_bs_id,
+                              cache_seq_offset, false);
+  if (rc != TMO_OK) return rc;
+  p.smode = quant_mode;
+  p.chan[0] = quant_mode == 0 ? key_scale : nullptr;
+  p.chan[1] = quant_mode == 0 ? value_scale : nullptr;
+  p.scale[0] = quant_mode == 1 ? const_cast<float*>(key_scale) : nullptr;
+  p.scale[1] = quant_mode == 1 ? const_cast<float*>(value_scale) : nullptr;
+  if (nothing_to_do(p, batch)) return TMO_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (out_dtype) {
+    case TMO_DTYPE_F16: return launch_dequant<F16>(p, batch, s);
+    case TMO_DTYPE_BF16: return launch_dequant<BF16>(p, batch, s);
+    default: return launch_dequant<F32>(p, batch, s);
+  }
+}
+
+extern "C" int tmo_hip_reshape_from_cache(
+    void* key, void* value, int64_t key_stride_token, int64_t key_stride_head,
+    int64_t value_stride_token, int64_t value_stride_head, int64_t rows, const void* key_cache,
+    const void* value_cache, int64_t num_blocks, int64_t num_heads, int64_t block_rows,
+    int64_t head_size, const int32_t* context_lengths, int64_t batch, int64_t max_context_len,
+    const int32_t* context_seq_offset, const int32_t* block_tables, int64_t max_blocks,
+    const int32_t* cache_seq_offset, int dtype, void* stream) {
+  const int es = elem_bytes(dtype);
+  if (es == 0) return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (block_tables && max_blocks <= 0) return TMO_ERR_INVALID_ARGUMENT;
+  LinParams p{};
+  const int rc = common_setup(p, key, value, key_stride_token, key_stride_head,
+                              value_stride_token, value_stride_head, rows,
+                              const_cast<void*>(key_cache), const_cast<void*>(value_cache),
+                              num_blocks, num_heads, block_rows, head_size, context_lengths,
+                              batch, max_context_len, 0, 0, context_seq_offset, nullptr,
+                              cache_seq_offset, false);
+  if (rc != TMO_OK) return rc;
+  p.block_tables = block_tables;
+  p.max_blocks = block_tables ? max_blocks : 0;
+  if (nothing_to_do(p, batch)) return TMO_OK;
+  return launch_copy(p, batch, es, static_cast<hipStream_t>(stream));
+}

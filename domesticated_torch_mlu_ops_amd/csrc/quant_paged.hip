@@ -178,24 +178,6 @@ struct StaticParams {
 #define TMO_STATIC_TOKENS_PER_THREAD 2
 #endif
 
-// Bytes of N quotients, packed 4 per u32: int8 codes (clamp, round half even) or
-// float8_e4m3fn (clamp to +-448, round to nearest even; hardware conversion).
-template <int N, bool kFp8>
-__device__ __forceinline__ void encode_static(const float* q, uint32_t* out) {
-#pragma unroll
-  for (int i = 0; i < N / 4; ++i) {
-    if constexpr (kFp8) {
-      float c[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) c[j] = __builtin_amdgcn_fmed3f(q[4 * i + j], -448.0f, 448.0f);
-      out[i] = fp8x4(c[0], c[1], c[2], c[3]);
-    } else {
-      out[i] = pack_codes(code_bits(q[4 * i]), code_bits(q[4 * i + 1]), code_bits(q[4 * i + 2]),
-                          code_bits(q[4 * i + 3]));
-    }
-  }
-}
-
 // Vector path of the static quantiser: one 16-byte vector per lane, G lanes per row (as the
 // dynamic kernel with V = 1), a workgroup owns kT * 256/G consecutive tokens of one head.  A
 // lane always covers the same kPerVec channels of its head, so it loads their scales once

@@ -536,6 +536,392 @@ void scaled_quantize(const at::Tensor& x, const at::Tensor& output,
   check_status(st, "scaled_quantize");
 }
 
+// ------------------------------------------------------------------------------ linear caches
+
+namespace {
+
+// Token-major tensor of a linear-cache op as rows of [heads, head_size]: [T, H, D], or padded
+// [B, S, H, D] (write ops) flattened to B * S rows.  A padded tensor whose batch stride is not
+// S row strides is copied first (it is an input).
+struct TokenRows {
+  at::Tensor t;
+  int64_t rows, st, sh, seqlen, H, D;
+};
+
+TokenRows token_rows(const at::Tensor& x, bool allow_padded, const char* name) {
+  TokenRows r;
+  if (x.dim() == 4 && allow_padded) {
+    at::Tensor t = x;
+    if (t.size(3) > 1 && t.stride(3) != 1) t = t.contiguous();
+    if (t.stride(0) != t.size(1) * t.stride(1) || t.stride(1) < 0 || t.stride(2) < 0)
+      t = t.contiguous();
+    r.t = t;
+    r.rows = t.size(0) * t.size(1);
+    r.st = t.stride(1);
+    r.sh = t.stride(2);
+    r.seqlen = t.size(1);
+    r.H = t.size(2);
+    r.D = t.size(3);
+    return r;
+  }
+  TORCH_CHECK(x.dim() == 3, name, " must be 3-D [tokens, heads, head_size]",
+              allow_padded ? " or 4-D [batch, seqlen, heads, head_size]" : "", ", got ",
+              x.sizes());
+  check_rows(x, name);
+  r.t = x;
+  r.rows = x.size(0);
+  r.st = x.stride(0);
+  r.sh = x.stride(1);
+  r.seqlen = 0;
+  r.H = x.size(1);
+  r.D = x.size(2);
+  return r;
+}
+
+void check_linear_cache(const at::Tensor& c, const at::Tensor& ref, int64_t H, int64_t D,
+                        const char* name) {
+  check_device(c, ref, name);
+  TORCH_CHECK(c.dim() == 4 && c.is_contiguous(), name,
+              " must be a contiguous 4-D [max_batch, heads, cache_len, head_size] tensor, got ",
+              c.sizes());
+  TORCH_CHECK(c.size(1) == H && c.size(3) == D, name, " ", c.sizes(),
+              " does not match the token rows' [heads, head_size] = [", H, ", ", D, "]");
+}
+
+// Optional int32 [n] tensor -> device pointer (NULL when absent).
+const int32_t* i32_vec(const c10::optional<at::Tensor>& t, const at::Tensor& ref, int64_t n,
+                       const char* name) {
+  if (!t.has_value()) return nullptr;
+  check_device(*t, ref, name);
+  TORCH_CHECK(t->scalar_type() == at::kInt && t->dim() == 1 && t->size(0) == n &&
+                  t->is_contiguous(),
+              name, " must be a contiguous int32 [", n, "] tensor, got ", t->scalar_type(), " ",
+              t->sizes());
+  return t->data_ptr<int32_t>();
+}
+
+int64_t check_lengths(const at::Tensor& lens, const at::Tensor& ref, bool packed) {
+  check_device(lens, ref, "context_lengths");
+  TORCH_CHECK(lens.scalar_type() == at::kInt && lens.dim() == 1 && lens.is_contiguous(),
+              "context_lengths must be a contiguous int32 1-D tensor");
+  TORCH_CHECK(!packed || lens.size(0) >= 1,
+              "context_lengths must hold batch + 1 offsets in packed mode");
+  return packed ? lens.size(0) - 1 : lens.size(0);
+}
+
+// The K/V pair of a write op (value and value_cache both given or both None).
+struct KvPair {
+  TokenRows k, v;
+  bool has_v;
+};
+
+KvPair write_rows(const at::Tensor& key, const c10::optional<at::Tensor>& value,
+                  const at::Tensor& key_cache, const c10::optional<at::Tensor>& value_cache) {
+  KvPair kv;
+  check_device(key, key, "key");
+  kv.k = token_rows(key, true, "key");
+  kv.has_v = value.has_value();
+  TORCH_CHECK(kv.has_v == value_cache.has_value(),
+              "value and value_cache must both be given or both be None");
+  check_linear_cache(key_cache, key, kv.k.H, kv.k.D, "key_cache");
+  if (kv.has_v) {
+    check_device(*value, key, "value");
+    TORCH_CHECK(value->sizes() == key.sizes() && value->scalar_type() == key.scalar_type(),
+                "value must match key");
+    kv.v = token_rows(*value, true, "value");
+    check_linear_cache(*value_cache, key, kv.k.H, kv.k.D, "value_cache");
+    TORCH_CHECK(value_cache->sizes() == key_cache.sizes() &&
+                    value_cache->scalar_type() == key_cache.scalar_type(),
+                "value_cache must match key_cache");
+  }
+  return kv;
+}
+
+}  // namespace
+
+void reshape_linear_cache(const at::Tensor& key, const c10::optional<at::Tensor>& value,
+                          at::Tensor& key_cache, const c10::optional<at::Tensor>& value_cache,
+                          const at::Tensor& context_lengths, const c10::SymInt max_context_len,
+                          bool packed, const c10::optional<at::Tensor>& context_seq_offset,
+                          const c10::optional<at::Tensor>& cache_bs_id,
+                          const c10::optional<at::Tensor>& cache_seqlen_offset) {
+  const KvPair kv = write_rows(key, value, key_cache, value_cache);
+  const int dt = dtype_code(key.scalar_type());
+  TORCH_CHECK(dt >= 0 && dt != TMO_DTYPE_F8E4M3, "reshape_linear_cache: unsupported dtype ",
+              key.scalar_type());
+  TORCH_CHECK(key_cache.scalar_type() == key.scalar_type(), "key_cache dtype ",
+              key_cache.scalar_type(), " must match key dtype ", key.scalar_type());
+  TORCH_CHECK(packed || key.dim() == 4, "padded (packed=False) key must be 4-D");
+  const int64_t B = check_lengths(context_lengths, key, packed);
+  const int32_t* cso = i32_vec(context_seq_offset, key, B, "context_seq_offset");
+  const int32_t* bsi = i32_vec(cache_bs_id, key, B, "cache_bs_id");
+  const int32_t* coff = i32_vec(cache_seqlen_offset, key, B, "cache_seqlen_offset");
+  const int64_t max_ctx = max_context_len.expect_int();
+  TORCH_CHECK(max_ctx >= 0, "max_context_len must be >= 0");
+  c10::DeviceGuard guard(key.device());
+  const int st = tmo_hip_reshape_linear_cache(
+      kv.k.t.data_ptr(), kv.has_v ? kv.v.t.data_ptr() : nullptr, kv.k.st, kv.k.sh,
+      kv.has_v ? kv.v.st : 0, kv.has_v ? kv.v.sh : 0, kv.k.rows, key_cache.data_ptr(),
+      kv.has_v ? value_cache->data_ptr() : nullptr, key_cache.size(0), kv.k.H,
+      key_cache.size(2), kv.k.D, context_lengths.data_ptr<int32_t>(), B, max_ctx, packed ? 1 : 0,
+      kv.k.seqlen, cso, bsi, coff, dt, stream_of(key));
+  check_status(st, "reshape_linear_cache");
+}
+
+void quant_to_linear_cache(const at::Tensor& key, const c10::optional<at::Tensor>& value,
+                           at::Tensor& key_cache, const c10::optional<at::Tensor>& value_cache,
+                           at::Tensor& key_cache_scale,
+                           const c10::optional<at::Tensor>& value_cache_scale,
+                           const at::Tensor& context_lengths, const c10::SymInt max_context_len,
+                           bool packed, const c10::optional<at::Tensor>& context_seq_offset,
+                           const c10::optional<at::Tensor>& cache_bs_id,
+                           const c10::optional<at::Tensor>& cache_seqlen_offset,
+                           const int64_t quant_bit) {
+  TORCH_CHECK(quant_bit == 8, "quant_to_linear_cache: only quant_bit 8 is supported, got ",
+              quant_bit);
+  const KvPair kv = write_rows(key, value, key_cache, value_cache);
+  const int dt = dtype_code(key.scalar_type());
+  TORCH_CHECK(dt == TMO_DTYPE_F32 || dt == TMO_DTYPE_F16 || dt == TMO_DTYPE_BF16,
+              "quant_to_linear_cache: key must be float, half or bfloat16, got ",
+              key.scalar_type());
+  const int cdt = dtype_code(key_cache.scalar_type());
+  TORCH_CHECK(cdt == TMO_DTYPE_I8 || cdt == TMO_DTYPE_F8E4M3,
+              "quant_to_linear_cache: caches must be int8 or float8_e4m3fn, got ",
+              key_cache.scalar_type());
+  TORCH_CHECK(packed || key.dim() == 4, "padded (packed=False) key must be 4-D");
+  TORCH_CHECK(kv.has_v == value_cache_scale.has_value(),
+              "value_cache_scale must be given exactly when value is");
+  const int64_t MB = key_cache.size(0), L = key_cache.size(2);
+  auto check_scale = [&](const at::Tensor& s, const char* name) -> int64_t {
+    check_device(s, key, name);
+    TORCH_CHECK(s.scalar_type() == at::kFloat && s.is_contiguous(), name,
+                " must be a contiguous float32 tensor");
+    TORCH_CHECK((s.dim() == 3 || s.dim() == 4) && s.size(0) == MB && s.size(1) == kv.k.H &&
+                    s.size(2) == L,
+                name, " must be [max_batch, heads, cache_len] or [max_batch, heads, cache_len, "
+                "group_num], got ", s.sizes());
+    const int64_t g = s.dim() == 4 ? s.size(3) : 1;
+    TORCH_CHECK(g >= 1 && kv.k.D % g == 0, name, ": head_size ", kv.k.D,
+                " is not a multiple of group_num ", g);
+    return g;
+  };
+  const int64_t groups = check_scale(key_cache_scale, "key_cache_scale");
+  if (kv.has_v) {
+    TORCH_CHECK(check_scale(*value_cache_scale, "value_cache_scale") == groups &&
+                    value_cache_scale->sizes() == key_cache_scale.sizes(),
+                "value_cache_scale must match key_cache_scale");
+  }
+  const int64_t B = check_lengths(context_lengths, key, packed);
+  const int32_t* cso = i32_vec(context_seq_offset, key, B, "context_seq_offset");
+  const int32_t* bsi = i32_vec(cache_bs_id, key, B, "cache_bs_id");
+  const int32_t* coff = i32_vec(cache_seqlen_offset, key, B, "cache_seqlen_offset");
+  const int64_t max_ctx = max_context_len.expect_int();
+  TORCH_CHECK(max_ctx >= 0, "max_context_len must be >= 0");
+  c10::DeviceGuard guard(key.device());
+  const int st = tmo_hip_quant_to_linear_cache(
+      kv.k.t.data_ptr(), kv.has_v ? kv.v.t.data_ptr() : nullptr, kv.k.st, kv.k.sh,
+      kv.has_v ? kv.v.st : 0, kv.has_v ? kv.v.sh : 0, kv.k.rows, key_cache.data_ptr(),
+      kv.has_v ? value_cache->data_ptr() : nullptr, key_cache_scale.data_ptr<float>(),
+      kv.has_v ? value_cache_scale->data_ptr<float>() : nullptr, MB, kv.k.H, L, kv.k.D, groups,
+      context_lengths.data_ptr<int32_t>(), B, max_ctx, packed ? 1 : 0, kv.k.seqlen, cso, bsi,
+      coff, (int)quant_bit, dt, cdt, stream_of(key));
+  check_status(st, "quant_to_linear_cache");
+}
+
+void offline_quant_to_linear_cache(const at::Tensor& key, const c10::optional<at::Tensor>& value,
+                                   at::Tensor& key_cache,
+                                   const c10::optional<at::Tensor>& value_cache,
+                                   const c10::optional<at::Tensor>& key_cache_scale,
+                                   const c10::optional<at::Tensor>& value_cache_scale,
+                                   const at::Tensor& context_lengths,
+                                   const c10::SymInt max_context_len, const int64_t quant_mode,
+                                   const bool packed,
+                                   const c10::optional<at::Tensor>& context_seq_offset,
+                                   const c10::optional<at::Tensor>& cache_bs_id,
+                                   const c10::optional<at::Tensor>& cache_seqlen_offset,
+                                   double key_cache_scale_per_tensor,
+                                   double value_cache_scale_per_tensor) {
+  TORCH_CHECK(quant_mode >= 0 && quant_mode <= 3,
+              "offline_quant_to_linear_cache: quant_mode must be 0 (per channel), 1 (per head) "
+              "or 2/3 (per tensor), got ", quant_mode);
+  const KvPair kv = write_rows(key, value, key_cache, value_cache);
+  const int dt = dtype_code(key.scalar_type());
+  TORCH_CHECK(dt == TMO_DTYPE_F32 || dt == TMO_DTYPE_F16 || dt == TMO_DTYPE_BF16,
+              "offline_quant_to_linear_cache: key must be float, half or bfloat16, got ",
+              key.scalar_type());
+  const int cdt = dtype_code(key_cache.scalar_type());
+  TORCH_CHECK(cdt == TMO_DTYPE_I8 || cdt == TMO_DTYPE_F8E4M3,
+              "offline_quant_to_linear_cache: caches must be int8 or float8_e4m3fn, got ",
+              key_cache.scalar_type());
+  TORCH_CHECK(packed || key.dim() == 4, "padded (packed=False) key must be 4-D");
+  const int64_t H = kv.k.H, D = kv.k.D, L = key_cache.size(2);
+  const float* ks = nullptr;
+  const float* vs = nullptr;
+  const float kt = static_cast<float>(key_cache_scale_per_tensor);
+  const float vt = static_cast<float>(value_cache_scale_per_tensor);
+  if (quant_mode < 2) {
+    const int64_t cols = quant_mode == 0 ? D : L;
+    auto check_scale = [&](const c10::optional<at::Tensor>& s, const char* name) {
+      TORCH_CHECK(s.has_value(), name, " is required for quant_mode ", quant_mode);
+      check_device(*s, key, name);
+      TORCH_CHECK(s->scalar_type() == at::kFloat && s->is_contiguous() && s->dim() == 2 &&
+                      s->size(0) == H && s->size(1) == cols,
+                  name, " must be a contiguous float32 [heads, ",
+                  quant_mode == 0 ? "head_size" : "cache_len", "] tensor, got ",
+                  s->scalar_type(), " ", s->sizes());
+      return s->data_ptr<float>();
+    };
+    ks = check_scale(key_cache_scale, "key_cache_scale");
+    if (kv.has_v) vs = check_scale(value_cache_scale, "value_cache_scale");
+  } else {
+    TORCH_CHECK(!key_cache_scale.has_value() && !value_cache_scale.has_value(),
+                "offline_quant_to_linear_cache: per-tensor quant_mode ", quant_mode,
+                " takes the scales as numbers");
+    TORCH_CHECK(std::isfinite(kt) && kt != 0.0f, "key_cache_scale must be finite and non-zero, got ",
+                key_cache_scale_per_tensor);
+    TORCH_CHECK(!kv.has_v || (std::isfinite(vt) && vt != 0.0f),
+                "value_cache_scale must be finite and non-zero, got ",
+                value_cache_scale_per_tensor);
+  }
+  const int64_t B = check_lengths(context_lengths, key, packed);
+  const int32_t* cso = i32_vec(context_seq_offset, key, B, "context_seq_offset");
+  const int32_t* bsi = i32_vec(cache_bs_id, key, B, "cache_bs_id");
+  const int32_t* coff = i32_vec(cache_seqlen_offset, key, B, "cache_seqlen_offset");
+  const int64_t max_ctx = max_context_len.expect_int();
+  TORCH_CHECK(max_ctx >= 0, "max_context_len must be >= 0");
+  c10::DeviceGuard guard(key.device());
+  const int st = tmo_hip_offline_quant_to_linear_cache(
+      kv.k.t.data_ptr(), kv.has_v ? kv.v.t.data_ptr() : nullptr, kv.k.st, kv.k.sh,
+      kv.has_v ? kv.v.st : 0, kv.has_v ? kv.v.sh : 0, kv.k.rows, key_cache.data_ptr(),
+      kv.has_v ? value_cache->data_ptr() : nullptr, ks, vs, kt, vt, (int)quant_mode,
+      key_cache.size(0), H, L, D, context_lengths.data_ptr<int32_t>(), B, max_ctx,
+      packed ? 1 : 0, kv.k.seqlen, cso, bsi, coff, dt, cdt, stream_of(key));
+  check_status(st, "offline_quant_to_linear_cache");
+}
+
+void dequant_from_linear_cache(at::Tensor& key, const c10::optional<at::Tensor>& value,
+                               const at::Tensor& key_cache,
+                               const c10::optional<at::Tensor>& value_cache,
+                               const at::Tensor& key_quant_scale,
+                               const c10::optional<at::Tensor>& value_quant_scale,
+                               const at::Tensor& context_lengths,
+                               const c10::SymInt max_context_len,
+                               const c10::optional<at::Tensor>& context_seq_offset,
+                               const c10::optional<at::Tensor>& cache_bs_id,
+                               const c10::optional<at::Tensor>& cache_seq_offset,
+                               const int64_t quant_mode, const int64_t quant_bit) {
+  TORCH_CHECK(quant_mode == 0 || quant_mode == 1,
+              "dequant_from_linear_cache: quant_mode must be 0 (per-channel) or 1 (per-token), "
+              "got ", quant_mode);
+  TORCH_CHECK(quant_bit == 8, "dequant_from_linear_cache: only quant_bit 8 is supported, got ",
+              quant_bit);
+  check_device(key, key, "key");
+  const TokenRows k = token_rows(key, false, "key");
+  const int dt = dtype_code(key.scalar_type());
+  TORCH_CHECK(dt == TMO_DTYPE_F16 || dt == TMO_DTYPE_BF16 || dt == TMO_DTYPE_F32,
+              "dequant_from_linear_cache: key must be half, bfloat16 or float, got ",
+              key.scalar_type());
+  check_linear_cache(key_cache, key, k.H, k.D, "key_cache");
+  TORCH_CHECK(key_cache.scalar_type() == at::kChar, "key_cache must be int8");
+  const int64_t MB = key_cache.size(0), L = key_cache.size(2);
+  auto check_scale = [&](const at::Tensor& s, const char* name) {
+    check_device(s, key, name);
+    TORCH_CHECK(s.scalar_type() == at::kFloat && s.is_contiguous(), name,
+                " must be a contiguous float32 tensor");
+    if (quant_mode == 0) {
+      TORCH_CHECK(s.dim() == 2 && s.size(0) == k.H && s.size(1) == k.D, name,
+                  " must be [heads, head_size] for quant_mode 0, got ", s.sizes());
+    } else {
+      TORCH_CHECK(s.dim() == 3 && s.size(0) == MB && s.size(1) == k.H && s.size(2) == L, name,
+                  " must be [max_batch, heads, cache_len] for quant_mode 1, got ", s.sizes());
+    }
+  };
+  check_scale(key_quant_scale, "key_cache_quant_scale");
+  const bool has_v = value.has_value();
+  TORCH_CHECK(has_v == value_cache.has_value() && has_v == value_quant_scale.has_value(),
+              "value, value_cache and value_cache_quant_scale must all be given or all be None");
+  TokenRows v{};
+  if (has_v) {
+    check_device(*value, key, "value");
+    TORCH_CHECK(value->sizes() == key.sizes() && value->scalar_type() == key.scalar_type(),
+                "value must match key");
+    v = token_rows(*value, false, "value");
+    check_linear_cache(*value_cache, key, k.H, k.D, "value_cache");
+    TORCH_CHECK(value_cache->sizes() == key_cache.sizes() && value_cache->scalar_type() == at::kChar,
+                "value_cache must match key_cache");
+    check_scale(*value_quant_scale, "value_cache_quant_scale");
+  }
+  const int64_t B = check_lengths(context_lengths, key, false);
+  const int32_t* cso = i32_vec(context_seq_offset, key, B, "context_seq_offset");
+  const int32_t* bsi = i32_vec(cache_bs_id, key, B, "cache_bs_id");
+  const int32_t* coff = i32_vec(cache_seq_offset, key, B, "cache_seq_offset");
+  const int64_t max_ctx = max_context_len.expect_int();
+  TORCH_CHECK(max_ctx >= 0, "max_context_len must be >= 0");
+  c10::DeviceGuard guard(key.device());
+  const int st = tmo_hip_dequant_from_linear_cache(
+      key.data_ptr(), has_v ? value->data_ptr() : nullptr, k.st, k.sh, has_v ? v.st : 0,
+      has_v ? v.sh : 0, k.rows, key_cache.data_ptr<int8_t>(),
+      has_v ? value_cache->data_ptr<int8_t>() : nullptr, key_quant_scale.data_ptr<float>(),
+      has_v ? value_quant_scale->data_ptr<float>() : nullptr, MB, k.H, L, k.D,
+      context_lengths.data_ptr<int32_t>(), B, max_ctx, cso, bsi, coff, (int)quant_mode,
+      (int)quant_bit, dt, stream_of(key));
+  check_status(st, "dequant_from_linear_cache");
+}
+
+void reshape_from_cache(at::Tensor& key, const c10::optional<at::Tensor>& value,
+                        const at::Tensor& key_cache, const c10::optional<at::Tensor>& value_cache,
+                        const at::Tensor& context_lengths, c10::SymInt max_context_len,
+                        const c10::optional<at::Tensor>& context_seq_offset,
+                        const c10::optional<at::Tensor>& block_tables,
+                        const c10::optional<at::Tensor>& cache_seq_offset) {
+  check_device(key, key, "key");
+  const TokenRows k = token_rows(key, false, "key");
+  const int dt = dtype_code(key.scalar_type());
+  TORCH_CHECK(dt >= 0 && dt != TMO_DTYPE_F8E4M3, "reshape_from_cache: unsupported dtype ",
+              key.scalar_type());
+  check_linear_cache(key_cache, key, k.H, k.D, "key_cache");
+  TORCH_CHECK(key_cache.scalar_type() == key.scalar_type(), "key_cache dtype ",
+              key_cache.scalar_type(), " must match key dtype ", key.scalar_type());
+  const bool has_v = value.has_value();
+  TORCH_CHECK(has_v == value_cache.has_value(),
+              "value and value_cache must both be given or both be None");
+  TokenRows v{};
+  if (has_v) {
+    check_device(*value, key, "value");
+    TORCH_CHECK(value->sizes() == key.sizes() && value->scalar_type() == key.scalar_type(),
+                "value must match key");
+    v = token_rows(*value, false, "value");
+    check_linear_cache(*value_cache, key, k.H, k.D, "value_cache");
+    TORCH_CHECK(value_cache->sizes() == key_cache.sizes() &&
+                    value_cache->scalar_type() == key_cache.scalar_type(),
+                "value_cache must match key_cache");
+  }
+  const int64_t B = check_lengths(context_lengths, key, false);
+  const int32_t* cso = i32_vec(context_seq_offset, key, B, "context_seq_offset");
+  const int32_t* coff = i32_vec(cache_seq_offset, key, B, "cache_seq_offset");
+  const int32_t* bt = nullptr;
+  int64_t max_blocks = 0;
+  if (block_tables.has_value()) {
+    check_device(*block_tables, key, "block_tables");
+    TORCH_CHECK(block_tables->scalar_type() == at::kInt && block_tables->dim() == 2 &&
+                    block_tables->size(0) == B && block_tables->size(1) >= 1 &&
+                    block_tables->is_contiguous(),
+                "block_tables must be a contiguous int32 [batch, max_blocks] tensor, got ",
+                block_tables->sizes());
+    bt = block_tables->data_ptr<int32_t>();
+    max_blocks = block_tables->size(1);
+  }
+  const int64_t max_ctx = max_context_len.expect_int();
+  TORCH_CHECK(max_ctx >= 0, "max_context_len must be >= 0");
+  c10::DeviceGuard guard(key.device());
+  const int st = tmo_hip_reshape_from_cache(
+      key.data_ptr(), has_v ? value->data_ptr() : nullptr, k.st, k.sh, has_v ? v.st : 0,
+      has_v ? v.sh : 0, k.rows, key_cache.data_ptr(), has_v ? value_cache->data_ptr() : nullptr,
+      key_cache.size(0), k.H, key_cache.size(2), k.D, context_lengths.data_ptr<int32_t>(), B,
+      max_ctx, cso, bt, max_blocks, coff, dt, stream_of(key));
+  check_status(st, "reshape_from_cache");
+}
+
 }  // namespace torch_api
 }  // namespace tmo
 
@@ -569,6 +955,31 @@ TORCH_LIBRARY(torch_mlu_ops, m) {
       "Tensor? scale_upper_bound, str quant_mode, str act_mode, float active_coef, bool is_gated, "
       "int quant_bit_size=8, bool need_output_scale_trans=False, Tensor(c!)? output_reduced=None, "
       "int group_size=1) -> ()");
+  m.def(
+      "reshape_linear_cache(Tensor key, Tensor? value, Tensor(a!) key_cache, "
+      "Tensor(b!)? value_cache, Tensor context_lengths, SymInt max_context_len, bool packed, "
+      "Tensor? context_seq_offset, Tensor? cache_bs_id, Tensor? cache_seqlen_offset) -> ()");
+  m.def(
+      "quant_to_linear_cache(Tensor key, Tensor? value, Tensor(a!) key_cache, "
+      "Tensor(b!)? value_cache, Tensor(c!) key_cache_scale, Tensor(d!)? value_cache_scale, "
+      "Tensor context_lengths, SymInt max_context_len, bool packed, Tensor? context_seq_offset, "
+      "Tensor? cache_bs_id, Tensor? cache_seqlen_offset, int quant_bit=8) -> ()");
+  m.def(
+      "offline_quant_to_linear_cache(Tensor key, Tensor? value, Tensor(a!) key_cache, "
+      "Tensor(b!)? value_cache, Tensor? key_cache_scale, Tensor? value_cache_scale, "
+      "Tensor context_lengths, SymInt max_context_len, int quant_mode, bool packed, "
+      "Tensor? context_seq_offset, Tensor? cache_bs_id, Tensor? cache_seqlen_offset, "
+      "float key_cache_scale_per_tensor, float value_cache_scale_per_tensor) -> ()");
+  m.def(
+      "dequant_from_linear_cache(Tensor(a!) key, Tensor(b!)? value, Tensor key_cache, "
+      "Tensor? value_cache, Tensor key_cache_quant_scale, Tensor? value_cache_quant_scale, "
+      "Tensor context_lengths, SymInt max_context_len, Tensor? context_seq_offset, "
+      "Tensor? cache_bs_id, Tensor? cache_seq_offset, int quant_mode=0, int quant_bit=8) -> ()");
+  m.def(
+      "reshape_from_cache(Tensor(a!) key, Tensor(b!)? value, Tensor key_cache, "
+      "Tensor? value_cache, Tensor context_lengths, SymInt max_context_len, "
+      "Tensor? context_seq_offset=None, Tensor? block_tables=None, "
+      "Tensor? cache_seq_offset=None) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(torch_mlu_ops, CUDA, m) {
@@ -578,4 +989,9 @@ TORCH_LIBRARY_IMPL(torch_mlu_ops, CUDA, m) {
   m.impl("dequant_from_paged_cache", &tmo::torch_api::dequant_from_paged_cache);
   m.impl("fused_rope", &tmo::torch_api::fused_rope);
   m.impl("scaled_quantize", &tmo::torch_api::scaled_quantize);
+  m.impl("reshape_linear_cache", &tmo::torch_api::reshape_linear_cache);
+  m.impl("quant_to_linear_cache", &tmo::torch_api::quant_to_linear_cache);
+  m.impl("offline_quant_to_linear_cache", &tmo::torch_api::offline_quant_to_linear_cache);
+  m.impl("dequant_from_linear_cache", &tmo::torch_api::dequant_from_linear_cache);
+  m.impl("reshape_from_cache", &tmo::torch_api::reshape_from_cache);
 }

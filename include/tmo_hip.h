@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 3
+#define TMO_HIP_ABI_VERSION 4
 
 /* element types */
 enum tmo_dtype {
@@ -204,6 +204,132 @@ int tmo_hip_scaled_quantize_per_token(const void* x, int64_t n0, int64_t inner,
                                       const int32_t* gather_index, int64_t gather_len,
                                       const int32_t* gather_start,
                                       int64_t out_rows, int dtype, void* stream);
+
+/*
+ * Linear caches [max_batch, num_heads, cache_len, head_size] (contiguous), one cache batch per
+ * sequence.  Shared addressing of the five entry points below, for sequence i < batch:
+ *   len_i  = min(context_lengths[i], max_context_len); with packed input context_lengths holds
+ *            batch + 1 prefix offsets cu and len_i = min(cu[i + 1] - cu[i], max_context_len);
+ *   token j < len_i is row start_i + j of the token-major tensor (rows x [num_heads,
+ *            head_size] with the given element strides): start_i = context_seq_offset[i] if
+ *            non-NULL, else cu[i] (packed input), i * seqlen (padded [batch, seqlen, H, D]
+ *            input flattened to rows), or sum(len_k, k < i) for the outputs of the read ops;
+ *   its cache position is cache_seq_offset[i] + j (0 + j when NULL) in cache batch
+ *            cache_bs_id[i] (i when NULL; a negative id skips the sequence).
+ * A token whose row, cache batch or position lies outside its tensor is skipped.  Different
+ * sequences must not map to the same cache rows (write ops) or token rows (read ops).
+ * Per-token scales are contiguous [max_batch, num_heads, cache_len] fp32.
+ */
+
+/*
+ * reshape_linear_cache -- byte copy of key/value token rows into the linear caches.
+ * Replaces tmo::torch_api::reshape_linear_cache (reference include/torch_mlu_ops.h:132-141),
+ * called by torch_mlu_ops.reshape_linear_cache (reference _ops.py:1189-1249).
+ * dtype: F32, F16, BF16 or I8 (caches have the dtype of key).  value and value_cache are
+ * both NULL or both set.
+ */
+int tmo_hip_reshape_linear_cache(const void* key, const void* value,
+                                 int64_t key_stride_token, int64_t key_stride_head,
+                                 int64_t value_stride_token, int64_t value_stride_head,
+                                 int64_t rows, void* key_cache, void* value_cache,
+                                 int64_t max_batch, int64_t num_heads, int64_t cache_len,
+                                 int64_t head_size, const int32_t* context_lengths,
+                                 int64_t batch, int64_t max_context_len, int packed,
+                                 int64_t seqlen, const int32_t* context_seq_offset,
+                                 const int32_t* cache_bs_id, const int32_t* cache_seqlen_offset,
+                                 int dtype, void* stream);
+
+/*
+ * quant_to_linear_cache -- dynamic quantisation of key/value token rows into the linear
+ * caches, per (token, head) or per group of head_size / group_num channels: int8 as
+ * quant_to_paged_cache (scale = fp32(amax) / 127), or float8_e4m3fn with scale =
+ * fp32(amax) / 448 and code = e4m3fn_RNE(clip(x / scale, -448, 448)) (all-zero group: scale 0,
+ * codes +0).  Scales go to key_scale[b, h, pos, g] ([max_batch, H, cache_len, group_num]).
+ * Replaces tmo::torch_api::quant_to_linear_cache (reference include/torch_mlu_ops.h:194-206),
+ * called by torch_mlu_ops.quant_to_linear_cache (reference _ops.py:1708-1806).
+ * dtype: F32, F16 or BF16; cache_dtype: I8 or F8E4M3; quant_bit: 8 (4-bit packing is
+ * TMO_ERR_UNSUPPORTED_MODE).
+ */
+int tmo_hip_quant_to_linear_cache(const void* key, const void* value,
+                                  int64_t key_stride_token, int64_t key_stride_head,
+                                  int64_t value_stride_token, int64_t value_stride_head,
+                                  int64_t rows, void* key_cache, void* value_cache,
+                                  float* key_scale, float* value_scale, int64_t max_batch,
+                                  int64_t num_heads, int64_t cache_len, int64_t head_size,
+                                  int64_t group_num, const int32_t* context_lengths,
+                                  int64_t batch, int64_t max_context_len, int packed,
+                                  int64_t seqlen, const int32_t* context_seq_offset,
+                                  const int32_t* cache_bs_id,
+                                  const int32_t* cache_seqlen_offset, int quant_bit, int dtype,
+                                  int cache_dtype, void* stream);
+
+/*
+ * offline_quant_to_linear_cache -- static quantisation (code = clip(RNE(fp32(x) / s), -128,
+ * 127), or e4m3fn_RNE(clip(fp32(x) / s, -448, 448)), IEEE quotients) into the linear caches.
+ * quant_mode 0: key_scale [num_heads, head_size] per channel; 1: [num_heads, cache_len] per
+ * head and cache position; 2 or 3: the per-tensor scalars (key_scale may be NULL).
+ * Replaces tmo::torch_api::offline_quant_to_linear_cache (reference
+ * include/torch_mlu_ops.h:208-222), called by torch_mlu_ops.offline_quant_to_linear_cache
+ * (reference _ops.py:1808-1919).  dtype: F32, F16 or BF16; cache_dtype: I8 or F8E4M3.
+ */
+int tmo_hip_offline_quant_to_linear_cache(const void* key, const void* value,
+                                          int64_t key_stride_token, int64_t key_stride_head,
+                                          int64_t value_stride_token, int64_t value_stride_head,
+                                          int64_t rows, void* key_cache, void* value_cache,
+                                          const float* key_scale, const float* value_scale,
+                                          float key_scale_per_tensor,
+                                          float value_scale_per_tensor, int quant_mode,
+                                          int64_t max_batch, int64_t num_heads,
+                                          int64_t cache_len, int64_t head_size,
+                                          const int32_t* context_lengths, int64_t batch,
+                                          int64_t max_context_len, int packed, int64_t seqlen,
+                                          const int32_t* context_seq_offset,
+                                          const int32_t* cache_bs_id,
+                                          const int32_t* cache_seqlen_offset, int dtype,
+                                          int cache_dtype, void* stream);
+
+/*
+ * dequant_from_linear_cache -- out[row, h, :] = RN_out(fp32(code) * scale) from the int8
+ * linear caches; quant_mode 0: key_scale [num_heads, head_size]; 1: per-token
+ * [max_batch, num_heads, cache_len].  context_lengths holds [batch] lengths.
+ * Replaces tmo::torch_api::dequant_from_linear_cache (reference
+ * include/torch_mlu_ops.h:636-648), called by torch_mlu_ops.dequant_from_linear_cache
+ * (reference _ops.py:3642-3732).  out_dtype: F16, BF16 (or F32); quant_bit: 8.
+ */
+int tmo_hip_dequant_from_linear_cache(void* key, void* value,
+                                      int64_t key_stride_token, int64_t key_stride_head,
+                                      int64_t value_stride_token, int64_t value_stride_head,
+                                      int64_t rows, const int8_t* key_cache,
+                                      const int8_t* value_cache, const float* key_scale,
+                                      const float* value_scale, int64_t max_batch,
+                                      int64_t num_heads, int64_t cache_len, int64_t head_size,
+                                      const int32_t* context_lengths, int64_t batch,
+                                      int64_t max_context_len,
+                                      const int32_t* context_seq_offset,
+                                      const int32_t* cache_bs_id,
+                                      const int32_t* cache_seq_offset, int quant_mode,
+                                      int quant_bit, int out_dtype, void* stream);
+
+/*
+ * reshape_from_cache -- byte copy of cache rows back to token-major key/value rows.
+ * Without block_tables the cache is linear [num_blocks = max_batch, H, block_rows = cache_len,
+ * D] and sequence i reads cache batch i; with block_tables [batch, max_blocks] position pos of
+ * sequence i is row pos % block_rows of page block_tables[i, pos / block_rows] (paged mode;
+ * a [batch, 1] table is the linear mode with the table naming the cache batch).  Position =
+ * cache_seq_offset[i] + j.  context_lengths holds [batch] lengths.
+ * Replaces tmo::torch_api::reshape_from_cache (reference include/torch_mlu_ops.h:663-671),
+ * called by torch_mlu_ops.reshape_from_cache (reference _ops.py:3898-3969).
+ * dtype: F32, F16, BF16 or I8.
+ */
+int tmo_hip_reshape_from_cache(void* key, void* value,
+                               int64_t key_stride_token, int64_t key_stride_head,
+                               int64_t value_stride_token, int64_t value_stride_head,
+                               int64_t rows, const void* key_cache, const void* value_cache,
+                               int64_t num_blocks, int64_t num_heads, int64_t block_rows,
+                               int64_t head_size, const int32_t* context_lengths, int64_t batch,
+                               int64_t max_context_len, const int32_t* context_seq_offset,
+                               const int32_t* block_tables, int64_t max_blocks,
+                               const int32_t* cache_seq_offset, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

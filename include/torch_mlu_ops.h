@@ -109,6 +109,76 @@ void dequant_from_paged_cache(at::Tensor &key,
                               const int64_t quant_mode,
                               const int64_t quant_bit);
 
+/* reference include/torch_mlu_ops.h:132-141 */
+void reshape_linear_cache(const at::Tensor &key,
+                          const c10::optional<at::Tensor> &value,
+                          at::Tensor &key_cache,
+                          const c10::optional<at::Tensor> &value_cache,
+                          const at::Tensor &context_lengths,
+                          const c10::SymInt max_context_len,
+                          bool packed,
+                          const c10::optional<at::Tensor> &context_seq_offset,
+                          const c10::optional<at::Tensor> &cache_bs_id,
+                          const c10::optional<at::Tensor> &cache_seqlen_offset);
+
+/* reference include/torch_mlu_ops.h:194-206 */
+void quant_to_linear_cache(const at::Tensor &key,
+                           const c10::optional<at::Tensor> &value,
+                           at::Tensor &key_cache,
+                           const c10::optional<at::Tensor> &value_cache,
+                           at::Tensor &key_cache_scale,
+                           const c10::optional<at::Tensor> &value_cache_scale,
+                           const at::Tensor &context_lengths,
+                           const c10::SymInt max_context_len,
+                           bool packed,
+                           const c10::optional<at::Tensor> &context_seq_offset,
+                           const c10::optional<at::Tensor> &cache_bs_id,
+                           const c10::optional<at::Tensor> &cache_seqlen_offset,
+                           const int64_t quant_bit);
+
+/* reference include/torch_mlu_ops.h:208-222 */
+void offline_quant_to_linear_cache(const at::Tensor &key,
+                                   const c10::optional<at::Tensor> &value,
+                                   at::Tensor &key_cache,
+                                   const c10::optional<at::Tensor> &value_cache,
+                                   const c10::optional<at::Tensor> &key_cache_scale,
+                                   const c10::optional<at::Tensor> &value_cache_scale,
+                                   const at::Tensor &context_lengths,
+                                   const c10::SymInt max_context_len,
+                                   const int64_t quant_mode,
+                                   const bool packed,
+                                   const c10::optional<at::Tensor> &context_seq_offset,
+                                   const c10::optional<at::Tensor> &cache_bs_id,
+                                   const c10::optional<at::Tensor> &cache_seqlen_offset,
+                                   double key_cache_scale_per_tensor,
+                                   double value_cache_scale_per_tensor);
+
+/* reference include/torch_mlu_ops.h:636-648 */
+void dequant_from_linear_cache(at::Tensor &key,
+                               const c10::optional<at::Tensor> &value,
+                               const at::Tensor &key_cache,
+                               const c10::optional<at::Tensor> &value_cache,
+                               const at::Tensor &key_quant_scale,
+                               const c10::optional<at::Tensor> &value_quant_scale,
+                               const at::Tensor &context_lengths,
+                               const c10::SymInt max_context_len,
+                               const c10::optional<at::Tensor> &context_seq_offset,
+                               const c10::optional<at::Tensor> &cache_bs_id,
+                               const c10::optional<at::Tensor> &cache_seq_offset,
+                               const int64_t quant_mode,
+                               const int64_t quant_bit);
+
+/* reference include/torch_mlu_ops.h:663-671 */
+void reshape_from_cache(at::Tensor &key,
+                        const c10::optional<at::Tensor> &value,
+                        const at::Tensor &key_cache,
+                        const c10::optional<at::Tensor> &value_cache,
+                        const at::Tensor &context_lengths,
+                        c10::SymInt max_context_len,
+                        const c10::optional<at::Tensor> &context_seq_offset,
+                        const c10::optional<at::Tensor> &block_tables,
+                        const c10::optional<at::Tensor> &cache_seq_offset);
+
 }  // namespace torch_api
 }  // namespace tmo
 

@@ -58,6 +58,11 @@ def lib() -> ctypes.CDLL:
         L.oracle_offline_quant_to_paged_cache.argtypes = [c_void_p, c_void_p, c_int] + \
             [c_int64] * 4 + [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_float, c_float,
                              c_void_p] + [c_int64] * 5 + [c_int]
+        L.oracle_linear_cache.argtypes = [c_int, c_void_p, c_void_p, c_int] + [c_int64] * 5 + \
+            [c_void_p, c_void_p, c_int] + [c_int64] * 4 + [c_void_p] * 4 + \
+            [c_float, c_float, c_int, c_int64, c_void_p, c_int64, c_int64, c_int, c_int64] + \
+            [c_void_p] * 4 + [c_int64, c_int]
+        L.oracle_linear_cache.restype = c_int
         for name in ("oracle_f32_to_bf16", "oracle_f32_to_f16", "oracle_f16_to_f32",
                      "oracle_f32_to_e4m3"):
             getattr(L, name).argtypes = [c_void_p, c_void_p, c_int64]
@@ -166,6 +171,55 @@ def f32_to_e4m3(x: torch.Tensor) -> torch.Tensor:
     out = torch.empty(x.shape, dtype=torch.uint8)
     lib().oracle_f32_to_e4m3(_ptr(x), _ptr(out), x.numel())
     return out
+
+
+_CACHE_DT = {torch.int8: 3, torch.float8_e4m3fn: 4}
+
+
+def _rows_view(t: Optional[torch.Tensor]):
+    """[B, S, H, D] (padded) or [T, H, D] token tensor -> its [rows, H, D] view."""
+    if t is None or t.dim() == 3:
+        return t
+    assert t.dim() == 4 and t.stride(0) == t.shape[1] * t.stride(1), "padded tensor must flatten"
+    return t.reshape(-1, t.shape[2], t.shape[3])
+
+
+def _i32(t: Optional[torch.Tensor]):
+    return t.to(torch.int32).contiguous() if t is not None else None
+
+
+def linear_cache(op: int, key, value, key_cache, value_cache, context_lengths, max_context_len,
+                 packed: bool = False, context_seq_offset=None, cache_bs_id=None,
+                 cache_seq_offset=None, key_scale=None, value_scale=None, key_chan=None,
+                 value_chan=None, key_tensor: float = 1.0, value_tensor: float = 1.0,
+                 smode: int = 0, groups: int = 1, block_tables=None,
+                 nthreads: Optional[int] = None) -> None:
+    """The five linear-cache ops of tmo_oracle.c (decision D11), in place on CPU tensors.
+
+    op 0 reshape_linear_cache, 1 quant_to_linear_cache, 2 offline_quant_to_linear_cache,
+    3 dequant_from_linear_cache, 4 reshape_from_cache.  ``key``/``value`` are the token-major
+    tensors ([T, H, D], or [B, S, H, D] padded input for ops 0-2); caches [NB, H, L, D];
+    ``key_scale`` per-token scales (op 1 written, op 3 mode 1 read), ``key_chan`` static /
+    per-channel scales, ``key_tensor`` a per-tensor scale."""
+    k, v = _rows_view(key), _rows_view(value)
+    assert k.stride(2) == 1 and key_cache.is_contiguous()
+    pad = key.shape[1] if key.dim() == 4 else 0
+    NB, H, L, D = key_cache.shape
+    ctx = _i32(context_lengths)
+    B = ctx.numel() - 1 if packed else ctx.numel()
+    cso, bsi, coff, bt = _i32(context_seq_offset), _i32(cache_bs_id), _i32(cache_seq_offset), \
+        _i32(block_tables)
+    kch = key_chan.to(torch.float32).contiguous() if key_chan is not None else None
+    vch = value_chan.to(torch.float32).contiguous() if value_chan is not None else None
+    rc = lib().oracle_linear_cache(
+        op, _ptr(k), _ptr(v), _DT[k.dtype], k.stride(0), k.stride(1),
+        v.stride(0) if v is not None else 0, v.stride(1) if v is not None else 0, k.shape[0],
+        _ptr(key_cache), _ptr(value_cache), _CACHE_DT.get(key_cache.dtype, 3), NB, H, L, D,
+        _ptr(key_scale), _ptr(value_scale), _ptr(kch), _ptr(vch), float(key_tensor),
+        float(value_tensor), int(smode), int(groups), _ptr(ctx), B, int(max_context_len),
+        int(bool(packed)), pad, _ptr(cso), _ptr(bsi), _ptr(coff), _ptr(bt),
+        bt.shape[1] if bt is not None else 0, nthreads or default_threads())
+    _check(rc, "linear_cache")
 
 
 def reshape_paged_cache(k, v, k_cache, v_cache, slot_mapping, direction: bool = False,

@@ -30,6 +30,23 @@
  *       table's rows leaves the row unrotated -- undefined in the reference); K is quantised (or
  *       rounded) from the fp32 result, V from its input values (_ops.py:3493-3520,
  *       6356-6423; rotary math _ops.py:1116-1127).
+ *   D11 linear caches [max_batch, H, cache_len, D] (_ops.py:1189-1249, 1708-1919, 3642-3732,
+ *       3898-3969): sequence i covers len_i tokens -- cu[i+1] - cu[i] when the input is
+ *       packed (context_lengths holds batch + 1 prefix offsets), else context_lengths[i]; its
+ *       token j is input row start_i + j (start_i = context_seq_offset[i], else cu[i] when
+ *       packed, else i * seqlen for padded [batch, seqlen, H, D] input) or output row
+ *       start_i + j (start_i = context_seq_offset[i], else the exclusive prefix sum of the
+ *       lengths); it lives in cache batch cache_bs_id[i] (else i; negative: the sequence is
+ *       skipped) at position cache_seq_offset[i] + j (else j); reshape_from_cache's block
+ *       table [batch, max_blocks] instead maps position p to row p % block_size of block
+ *       block_tables[i, p / block_size] (a one-column table is the linear layout with the
+ *       table naming the cache batch, _ops.py:3906-3915).  Rows whose cache batch or
+ *       position falls outside the cache, or whose input / output row falls outside its
+ *       tensor, are skipped, as are tokens j >= max_context_len.  Per-head static scales
+ *       [H, cache_len] are indexed by cache position.  The dynamic quantiser works per token
+ *       or per group of D / group_num channels (scale [max_batch, H, cache_len, group_num]):
+ *       int8 as D1-D3, fp8 e4m3fn with scale = RN(amax / 448), codes e4m3fn_RNE(clip(RN(x /
+ *       scale), -448, 448)) and an all-zero group giving scale 0 and codes 0 (_ops.py:1728-1745).
  *   D9  offline (static-scale) quantisation divides: code = clip(RNE(RN(fp32(x) / s)), -128, 127)
  *       for int8, fp8 = e4m3fn_RNE(clip(RN(fp32(x) / s), -448, 448)), s the fp32 per-channel
  *       scale or the per-tensor scalar rounded to fp32 (_ops.py:1652-1670; the division is
@@ -493,6 +510,188 @@ int oracle_fused_rope_paged(void* qkv, int dtype, int64_t T, int64_t S, int64_t 
                    table_rows, position, k_gamma, q_gamma, eps, {k_cache, v_cache}, DT_I8, {k_scale, v_scale},
                    scale_mode, slot, NB, BS};
     parallel_for(T, nthreads, frope_range, &c);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ linear caches (D11) */
+
+/* One group of n values -> codes (int8 bytes or e4m3fn bytes) + fp32 scale (_ops.py:1728-1745). */
+static float quant_group(const float* x, int64_t n, uint8_t* codes, int cache_dtype) {
+    if (cache_dtype == DT_I8) return quant_row(x, n, (int8_t*)codes);
+    float amax = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        float a = fabsf(x[i]);
+        if (a > amax) amax = a;
+    }
+    float scale = amax / 448.0f;                           /* IEEE divide */
+    if (scale == 0.0f) {                                   /* as D3 */
+        memset(codes, 0, (size_t)n);
+        return scale;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        float q = x[i] / scale;
+        if (q < -448.0f) q = -448.0f;                      /* clip(key_i, -448, 448) */
+        if (q > 448.0f) q = 448.0f;
+        codes[i] = f32_to_e4m3(q);
+    }
+    return scale;
+}
+
+typedef struct {
+    int64_t batch, H, D, cache_batch, cache_len, rows;   /* rows: input / output tensor rows */
+    const int32_t* lens;       /* [batch] or [batch + 1] when packed */
+    int packed;
+    int64_t pad_seqlen;        /* padded input: rows per sequence */
+    const int32_t* seq_off;    /* nullable */
+    const int32_t* bs_id;      /* nullable */
+    const int32_t* cache_off;  /* nullable */
+    const int32_t* bt;         /* nullable: block table [batch, max_blocks] of cache_len-row blocks */
+    int64_t max_blocks;
+} lin_addr;
+
+static int64_t lin_len(const lin_addr* a, int64_t i) {
+    return a->packed ? (int64_t)a->lens[i + 1] - a->lens[i] : a->lens[i];
+}
+
+/* first row of sequence i in the token-major tensor; in_dir: it is the input of a cache write */
+static int64_t lin_start(const lin_addr* a, int64_t i, int in_dir) {
+    if (a->seq_off) return a->seq_off[i];
+    if (in_dir && a->packed) return a->lens[i];
+    if (in_dir) return i * a->pad_seqlen;
+    int64_t s = 0;
+    for (int64_t k = 0; k < i; ++k) s += lin_len(a, k);
+    return s;
+}
+
+/* cache row (b * H + h) * cache_len + pos % cache_len of token j of sequence i, or -1 when
+ * skipped.  pos = cache_offset[i] + j; without a block table b = cache_bs_id[i] (else i) and
+ * pos must lie in [0, cache_len); with one, b = bt[i, pos / cache_len] (a paged cache of
+ * cache_len-row blocks; a one-column table is the linear layout, _ops.py:3906-3909). */
+static int64_t lin_cache_row(const lin_addr* a, int64_t i, int64_t j, int64_t h) {
+    int64_t pos = (a->cache_off ? a->cache_off[i] : 0) + j;
+    if (pos < 0 || a->cache_len <= 0) return -1;
+    int64_t bi = pos / a->cache_len, b;
+    if (a->bt) {
+        if (bi >= a->max_blocks) return -1;
+        b = a->bt[i * a->max_blocks + bi];
+    } else {
+        if (bi != 0) return -1;
+        b = a->bs_id ? a->bs_id[i] : i;
+    }
+    if (b < 0 || b >= a->cache_batch) return -1;
+    return (b * a->H + h) * a->cache_len + pos % a->cache_len;
+}
+
+typedef struct {
+    lin_addr a;
+    int op;                   /* 0 copy in, 1 dynamic quant in, 2 static quant in, 3 dequant out, 4 copy out */
+    const void* src[2];
+    void* dst[2];
+    int64_t st[2], sh[2];     /* token-major tensor strides (elements) */
+    int dtype;                /* token-major tensor dtype */
+    float* scale[2];          /* dynamic: [cache_batch, H, cache_len] */
+    const float* chan[2];     /* static mode 0 [H, D]; mode 1 [H, cache_len] */
+    float tensor_scale[2];    /* static modes 2/3 */
+    int smode;                /* static / dequant scale mode: 0 channel, 1 head (static) or token (dequant), 2 tensor */
+    int nkv;
+    int cache_dtype;          /* quantising ops: DT_I8 or DT_F8E4M3 */
+    int64_t groups;           /* dynamic: scale groups per (token, head) */
+    int64_t max_len;          /* tokens j >= max_len are skipped */
+} lin_ctx;
+
+static void lin_range(void* p, int64_t lo, int64_t hi) {
+    lin_ctx* c = (lin_ctx*)p;
+    const lin_addr* a = &c->a;
+    int64_t D = a->D;
+    int in_dir = c->op <= 2;
+    float* row = (float*)malloc((size_t)D * sizeof(float));
+    uint8_t* codes = (uint8_t*)malloc((size_t)D);
+    for (int64_t i = lo; i < hi; ++i) {
+        int64_t len = lin_len(a, i), start = lin_start(a, i, in_dir);
+        if (len > c->max_len) len = c->max_len;
+        for (int64_t j = 0; j < len; ++j) {
+            int64_t r = start + j;
+            if (r < 0 || r >= a->rows) continue;
+            for (int kv = 0; kv < c->nkv; ++kv) {
+                for (int64_t h = 0; h < a->H; ++h) {
+                    int64_t cr = lin_cache_row(a, i, j, h);
+                    if (cr < 0) continue;
+                    int64_t tok = r * c->st[kv] + h * c->sh[kv];
+                    int64_t pos = cr % a->cache_len;
+                    if (c->op == 0 || c->op == 4) {                 /* byte copy */
+                        int es = elem_size(c->dtype);
+                        const char* from = c->op == 0 ? (const char*)c->src[kv] + tok * es
+                                                      : (const char*)c->src[kv] + cr * D * es;
+                        char* to = c->op == 0 ? (char*)c->dst[kv] + cr * D * es
+                                              : (char*)c->dst[kv] + tok * es;
+                        memcpy(to, from, (size_t)(D * es));
+                    } else if (c->op == 1) {                        /* dynamic per token / group */
+                        int64_t gs = D / c->groups;
+                        for (int64_t d = 0; d < D; ++d) row[d] = load_elem(c->src[kv], tok + d, c->dtype);
+                        for (int64_t g = 0; g < c->groups; ++g)
+                            c->scale[kv][cr * c->groups + g] =
+                                quant_group(row + g * gs, gs, codes + g * gs, c->cache_dtype);
+                        memcpy((uint8_t*)c->dst[kv] + cr * D, codes, (size_t)D);
+                    } else if (c->op == 2) {                        /* static */
+                        uint8_t* out = (uint8_t*)c->dst[kv] + cr * D;
+                        for (int64_t d = 0; d < D; ++d) {
+                            float s = c->smode == 0 ? c->chan[kv][h * D + d]
+                                    : c->smode == 1 ? c->chan[kv][h * a->cache_len + pos]
+                                                    : c->tensor_scale[kv];
+                            out[d] = static_code(load_elem(c->src[kv], tok + d, c->dtype), s, c->cache_dtype);
+                        }
+                    } else {                                        /* dequant */
+                        const int8_t* in = (const int8_t*)c->src[kv] + cr * D;
+                        for (int64_t d = 0; d < D; ++d) {
+                            float s = c->smode == 0 ? c->chan[kv][h * D + d] : c->scale[kv][cr];
+                            store_elem(c->dst[kv], tok + d, c->dtype, (float)in[d] * s);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    free(row);
+    free(codes);
+}
+
+/* One entry for the five linear-cache ops (the op code selects the direction and arithmetic):
+ *   op 0 reshape_linear_cache (_ops.py:1189-1249), 1 quant_to_linear_cache (:1708-1806),
+ *   2 offline_quant_to_linear_cache (:1808-1919), 3 dequant_from_linear_cache (:3642-3732),
+ *   4 reshape_from_cache, linear mode (:3898-3969).
+ * tok[2] / tok_st / tok_sh: the token-major tensors (input for ops 0-2, output for 3-4).
+ * cache_dtype: the cache's element type for ops 1-2 (DT_I8 or DT_F8E4M3; op 3 reads int8);
+ * groups: scale groups per (token, head) for op 1.  block_tables [batch, max_blocks] (nullable)
+ * turns the cache into pages of cache_len rows: op 4 with it is reshape_from_cache's paged mode,
+ * op 3 with it reads per-token scales [num_blocks, H, cache_len]. */
+int oracle_linear_cache(int op, void* tok_k, void* tok_v, int dtype, int64_t k_st, int64_t k_sh,
+                        int64_t v_st, int64_t v_sh, int64_t rows, void* cache_k, void* cache_v,
+                        int cache_dtype, int64_t cache_batch, int64_t H, int64_t cache_len, int64_t D,
+                        float* k_scale, float* v_scale, const float* k_chan, const float* v_chan,
+                        float k_tensor, float v_tensor, int smode, int64_t groups,
+                        const int32_t* lens, int64_t batch, int64_t max_len, int packed,
+                        int64_t pad_seqlen, const int32_t* seq_off, const int32_t* bs_id,
+                        const int32_t* cache_off, const int32_t* block_tables,
+                        int64_t max_blocks, int nthreads) {
+    if (op < 0 || op > 4 || elem_size(dtype) == 0) return -2;
+    if ((op == 1 || op == 2 || op == 3) && dtype == DT_I8) return -2;
+    if ((op == 1 || op == 2) && cache_dtype != DT_I8 && cache_dtype != DT_F8E4M3) return -2;
+    if (op == 1 && (groups <= 0 || D % groups != 0)) return -1;
+    if (batch < 0 || H <= 0 || D <= 0 || cache_batch < 0 || cache_len < 0 || rows < 0) return -1;
+    lin_ctx c;
+    memset(&c, 0, sizeof c);
+    c.a.batch = batch; c.a.H = H; c.a.D = D; c.a.cache_batch = cache_batch; c.a.cache_len = cache_len;
+    c.a.rows = rows; c.a.lens = lens; c.a.packed = packed; c.a.pad_seqlen = pad_seqlen;
+    c.a.seq_off = seq_off; c.a.bs_id = bs_id; c.a.cache_off = cache_off;
+    c.a.bt = block_tables; c.a.max_blocks = max_blocks;
+    c.op = op; c.dtype = dtype; c.nkv = tok_v ? 2 : 1;
+    c.st[0] = k_st; c.st[1] = v_st; c.sh[0] = k_sh; c.sh[1] = v_sh;
+    c.scale[0] = k_scale; c.scale[1] = v_scale; c.chan[0] = k_chan; c.chan[1] = v_chan;
+    c.tensor_scale[0] = k_tensor; c.tensor_scale[1] = v_tensor; c.smode = smode;
+    c.cache_dtype = cache_dtype; c.groups = groups > 0 ? groups : 1; c.max_len = max_len;
+    if (op <= 2) { c.src[0] = tok_k; c.src[1] = tok_v; c.dst[0] = cache_k; c.dst[1] = cache_v; }
+    else { c.src[0] = cache_k; c.src[1] = cache_v; c.dst[0] = tok_k; c.dst[1] = tok_v; }
+    parallel_for(batch, nthreads, lin_range, &c);
     return 0;
 }
 

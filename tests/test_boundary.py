@@ -60,6 +60,39 @@ REFERENCE_SIGNATURES = {
                         ("quant_bit_size", 8), ("scale_type", torch.float32),
                         ("need_output_scale_trans", False), ("output_reduced", None),
                         ("group_size", 1)],
+    # _ops.py:1189-1200
+    "reshape_linear_cache": [("key", None), ("value", None), ("key_cache", None),
+                             ("value_cache", None), ("context_lengths", None),
+                             ("max_context_len", None), ("packed", None),
+                             ("context_seq_offset", None), ("cache_bs_id", None),
+                             ("cache_seqlen_offset", None)],
+    # _ops.py:1708-1722
+    "quant_to_linear_cache": [("key", None), ("value", None), ("key_cache", None),
+                              ("value_cache", None), ("key_cache_quant_scale", None),
+                              ("value_cache_quant_scale", None), ("context_lengths", None),
+                              ("max_context_len", None), ("packed", None),
+                              ("context_seq_offset", None), ("cache_bs_id", None),
+                              ("cache_seqlen_offset", None), ("quant_bit", 8)],
+    # _ops.py:1808-1822
+    "offline_quant_to_linear_cache": [("key", None), ("value", None), ("key_cache", None),
+                                      ("value_cache", None), ("key_cache_quant_scale", None),
+                                      ("value_cache_quant_scale", None),
+                                      ("context_lengths", None), ("max_context_len", None),
+                                      ("quant_mode", None), ("packed", None),
+                                      ("context_seq_offset", None), ("cache_bs_id", None),
+                                      ("cache_seqlen_offset", None)],
+    # _ops.py:3642-3654
+    "dequant_from_linear_cache": [("key", None), ("value", None), ("key_cache", None),
+                                  ("value_cache", None), ("key_cache_quant_scale", None),
+                                  ("value_cache_quant_scale", None), ("context_lengths", None),
+                                  ("max_context_len", None), ("context_seq_offset", None),
+                                  ("cache_bs_id", None), ("cache_seq_offset", None),
+                                  ("quant_mode", 0), ("quant_bit", 8)],
+    # _ops.py:3898-3906
+    "reshape_from_cache": [("key", None), ("value", None), ("key_cache", None),
+                           ("value_cache", None), ("context_lengths", None),
+                           ("max_context_len", None), ("context_seq_offset", None),
+                           ("block_tables", None), ("cache_seq_offset", None)],
 }
 
 
@@ -84,6 +117,11 @@ WRITES = {
     "fused_rope": {"qkv", "key_cache_hp", "value_cache_hp", "key_cache_lp", "value_cache_lp",
                    "key_scale_hp", "value_scale_hp", "key_scale_lp", "value_scale_lp"},
     "scaled_quantize": {"output", "output_scale", "output_reduced"},
+    "reshape_linear_cache": {"key_cache", "value_cache"},
+    "quant_to_linear_cache": {"key_cache", "value_cache", "key_cache_scale", "value_cache_scale"},
+    "offline_quant_to_linear_cache": {"key_cache", "value_cache"},
+    "dequant_from_linear_cache": {"key", "value"},
+    "reshape_from_cache": {"key", "value"},
 }
 
 
@@ -136,6 +174,25 @@ def test_fakes_run_on_meta_tensors(tmo):
     assert len(out) == 3 and out[0] is qkv
     out = tmo.fused_rmsnorm_rope_store_paged_cache(qkv, kc, vc, tab, tab, pid, g, None, slot, ks, vs)
     assert len(out) == 5 and out[3] is ks
+
+
+def test_linear_fakes_run_on_meta_tensors(tmo):
+    m = dict(device="meta")
+    key = torch.empty(40, 8, 128, dtype=torch.bfloat16, **m)
+    kc = torch.empty(4, 8, 64, 128, dtype=torch.int8, **m)
+    ks = torch.empty(4, 8, 64, dtype=torch.float32, **m)
+    cu = torch.empty(5, dtype=torch.int32, **m)
+    lens = torch.empty(4, dtype=torch.int32, **m)
+    kb = kc.to(torch.bfloat16)
+    assert tmo.reshape_linear_cache(key, key, kb, kb, cu, 16, True, None, None, None) == (kb, kb)
+    assert tmo.reshape_linear_cache(key, None, kb, None, cu, 16, True, None, None, None) is kb
+    assert tmo.quant_to_linear_cache(key, key, kc, kc, ks, ks, cu, 16, True, None, None,
+                                     None) == (kc, kc, ks, ks)
+    assert tmo.offline_quant_to_linear_cache(key, None, kc, None, 0.5, None, cu, 16, 2, True,
+                                             None, None, None) == (kc, 0.5)
+    assert tmo.dequant_from_linear_cache(key, None, kc, None, ks, None, lens, 16, None, None,
+                                         None, 1, 8) is None
+    assert tmo.reshape_from_cache(key, key, kb, kb, lens, 16) is None
 
 
 def test_fake_tensor_mode(tmo):

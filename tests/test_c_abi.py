@@ -40,6 +40,16 @@ def lib():
         [ctypes.c_float] + [P] * 4 + [INT, P, I64, I64, INT, P]
     L.tmo_hip_offline_quant_to_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 4 + \
         [ctypes.c_float] * 2 + [P] + [I64] * 5 + [INT, INT, P]
+    L.tmo_hip_reshape_linear_cache.argtypes = [P, P] + [I64] * 5 + [P, P] + [I64] * 4 + \
+        [P, I64, I64, INT, I64, P, P, P, INT, P]
+    L.tmo_hip_quant_to_linear_cache.argtypes = [P, P] + [I64] * 5 + [P] * 4 + [I64] * 5 + \
+        [P, I64, I64, INT, I64, P, P, P, INT, INT, INT, P]
+    L.tmo_hip_offline_quant_to_linear_cache.argtypes = [P, P] + [I64] * 5 + [P] * 4 + \
+        [ctypes.c_float] * 2 + [INT] + [I64] * 4 + [P, I64, I64, INT, I64, P, P, P, INT, INT, P]
+    L.tmo_hip_dequant_from_linear_cache.argtypes = [P, P] + [I64] * 5 + [P] * 4 + [I64] * 4 + \
+        [P, I64, I64, P, P, P, INT, INT, INT, P]
+    L.tmo_hip_reshape_from_cache.argtypes = [P, P] + [I64] * 5 + [P, P] + [I64] * 4 + \
+        [P, I64, I64, P, P, I64, P, INT, P]
     return L
 
 
@@ -48,7 +58,10 @@ def test_every_declared_symbol_is_exported(lib):
     assert set(names) == {"tmo_hip_abi_version", "tmo_hip_status_string",
                           "tmo_hip_reshape_paged_cache", "tmo_hip_quant_to_paged_cache",
                           "tmo_hip_dequant_from_paged_cache", "tmo_hip_scaled_quantize_per_token",
-                          "tmo_hip_offline_quant_to_paged_cache", "tmo_hip_fused_rope_paged"}
+                          "tmo_hip_offline_quant_to_paged_cache", "tmo_hip_fused_rope_paged",
+                          "tmo_hip_reshape_linear_cache", "tmo_hip_quant_to_linear_cache",
+                          "tmo_hip_offline_quant_to_linear_cache",
+                          "tmo_hip_dequant_from_linear_cache", "tmo_hip_reshape_from_cache"}
     for n in names:
         assert hasattr(lib, n), n
 
@@ -166,3 +179,65 @@ def test_fused_rope_validation(lib):
     assert call(stride=64) == EINVAL         # table rows shorter than rope_dim
     assert call(T=9) == EINVAL               # more tokens than batch * seq_len
     assert call(T=0) == 0
+
+
+def lin_write(lib, fn, *, key=FAKE, value=None, kc=FAKE, vc=None, rows=64, MB=4, H=8, L=32,
+              D=128, lens=FAKE, B=2, max_len=16, packed=1, seqlen=0, dtype=2, extra=()):
+    head = (key, value, 1024, 128, 1024, 128, rows, kc, vc)
+    tail = (lens, B, max_len, packed, seqlen, None, None, None)
+    if fn == "reshape":
+        return lib.tmo_hip_reshape_linear_cache(*head, MB, H, L, D, *tail, dtype, None)
+    if fn == "quant":
+        ks, vs, groups, bit, cdt = extra or (FAKE, None, 1, 8, 3)
+        return lib.tmo_hip_quant_to_linear_cache(*head, ks, vs, MB, H, L, D, groups, *tail, bit,
+                                                 dtype, cdt, None)
+    ks, vs, mode, cdt = extra or (FAKE, None, 0, 3)
+    return lib.tmo_hip_offline_quant_to_linear_cache(*head, ks, vs, 1.0, 1.0, mode, MB, H, L, D,
+                                                     *tail, dtype, cdt, None)
+
+
+def test_linear_write_validation(lib):
+    for fn in ("reshape", "quant", "offline"):
+        assert lin_write(lib, fn, key=None) == EINVAL, fn
+        assert lin_write(lib, fn, lens=None) == EINVAL, fn
+        assert lin_write(lib, fn, value=FAKE) == EINVAL, fn     # value without value_cache
+        assert lin_write(lib, fn, H=0) == EINVAL, fn
+        assert lin_write(lib, fn, B=-1) == EINVAL, fn
+        assert lin_write(lib, fn, max_len=-1) == EINVAL, fn
+        assert lin_write(lib, fn, dtype=9) == EDTYPE, fn
+        assert lin_write(lib, fn, B=0) == 0, fn                  # nothing to do
+        assert lin_write(lib, fn, max_len=0) == 0, fn
+        assert lin_write(lib, fn, rows=0) == 0, fn
+    assert lin_write(lib, "quant", dtype=3) == EDTYPE          # int8 input
+    assert lin_write(lib, "quant", extra=(FAKE, None, 1, 4, 3)) == EMODE   # 4-bit
+    assert lin_write(lib, "quant", extra=(FAKE, None, 1, 8, 2)) == EDTYPE  # bf16 cache
+    assert lin_write(lib, "quant", extra=(FAKE, None, 3, 8, 3)) == EINVAL  # 128 % 3 != 0
+    assert lin_write(lib, "quant", extra=(None, None, 1, 8, 3)) == EINVAL  # no scale
+    assert lin_write(lib, "offline", extra=(FAKE, None, 4, 3)) == EMODE
+    assert lin_write(lib, "offline", extra=(None, None, 0, 3)) == EINVAL   # per channel, no scale
+    assert lin_write(lib, "offline", extra=(None, None, 2, 4), B=0) == 0  # per tensor: no tensor
+
+
+def test_linear_read_validation(lib):
+    def deq(mode=1, bit=8, dtype=2, key=FAKE, value=None, vc=None, vs=None, B=2, H=8, rows=10):
+        return lib.tmo_hip_dequant_from_linear_cache(
+            key, value, 1024, 128, 1024, 128, rows, FAKE, vc, FAKE, vs, 4, H, 32, 128, FAKE, B,
+            16, None, None, None, mode, bit, dtype, None)
+    assert deq(mode=2) == EMODE
+    assert deq(bit=4) == EMODE
+    assert deq(dtype=3) == EDTYPE
+    assert deq(key=None) == EINVAL
+    assert deq(value=FAKE, vc=FAKE) == EINVAL                    # value without value scale
+    assert deq(H=0) == EINVAL
+    assert deq(B=0) == 0 and deq(rows=0) == 0
+
+    def rfc(dtype=2, key=FAKE, value=None, vc=None, bt=None, mb=0, B=2, NB=4):
+        return lib.tmo_hip_reshape_from_cache(key, value, 1024, 128, 1024, 128, 10, FAKE, vc, NB,
+                                              8, 16, 128, FAKE, B, 16, None, bt, mb, None, dtype,
+                                              None)
+    assert rfc(dtype=8) == EDTYPE
+    assert rfc(key=None) == EINVAL
+    assert rfc(value=FAKE) == EINVAL
+    assert rfc(bt=FAKE, mb=0) == EINVAL                          # a table needs columns
+    assert rfc(B=0) == 0 and rfc(NB=0) == 0
+

@@ -675,3 +675,288 @@ def test_fused_rope_within_one_ulp_of_float64(ref, dtype):
         d = (bits(a).to(torch.int32) - bits(b).to(torch.int32)).abs()
         assert int(d.max()) <= 1
         assert float((d > 0).float().mean()) < 0.05
+
+
+# ---------------------------------------------------------------------------- linear caches (D11)
+
+def _lin_segments(case, max_len, out_dir, block_tables=None, lens=None):
+    """Per sequence: (token rows, cache batch / block per token, cache positions) of the tokens
+    that are written, by the docstring math of _ops.py:1203-1206, 3663-3668, 3906-3909."""
+    lens = case.lens if lens is None else lens
+    rows = case.key.shape[0] * (case.key.shape[1] if case.key.dim() == 4 else 1)
+    if out_dir:
+        rows = case.key.shape[0] if case.key.dim() == 3 else rows
+    starts = torch.cumsum(lens, 0) - lens            # exclusive prefix sums
+    out = []
+    for i in range(lens.numel()):
+        n = min(int(lens[i]), max_len)
+        if case.context_seq_offset is not None:
+            start = int(case.context_seq_offset[i])
+        elif out_dir or case.packed:
+            start = int(starts[i])
+        else:
+            start = i * case.key.shape[1]
+        j = torch.arange(n)
+        r = start + j
+        pos = j + (int(case.cache_seq_offset[i]) if case.cache_seq_offset is not None else 0)
+        if block_tables is not None:
+            L = case.cache_len
+            col = pos // L
+            ok = col < block_tables.shape[1]
+            b = torch.where(ok, block_tables[i, col.clamp(max=block_tables.shape[1] - 1)].long(),
+                            torch.full_like(col, -1))
+            pos = pos % L
+        else:
+            b = torch.full_like(j, int(case.cache_bs_id[i]) if case.cache_bs_id is not None else i)
+            b = torch.where(pos < case.cache_len, b, torch.full_like(b, -1))
+        keep = (r >= 0) & (r < rows) & (b >= 0) & (b < case.cache_batch) & (pos >= 0)
+        out.append((r[keep], b[keep], pos[keep]))
+    return out
+
+
+def torch_linear_write(case, op, kc, vc, ks=None, vs=None, kchan=None, vchan=None, smode=0,
+                       groups=1, max_len=None):
+    """Ops 0-2 (reshape / dynamic quant / static quant into the linear cache) by torch."""
+    max_len = case.max_context_len if max_len is None else max_len
+    segs = _lin_segments(case, max_len, out_dir=False)
+    for x, c, sc, ch in ((case.key, kc, ks, kchan), (case.value, vc, vs, vchan)):
+        x = x.reshape(-1, x.shape[-2], x.shape[-1])
+        for r, b, pos in segs:
+            if r.numel() == 0:
+                continue
+            rows = x[r]                                          # [n, H, D]
+            if op == 0:
+                c[b, :, pos] = rows
+                continue
+            xf = rows.to(torch.float32)
+            if op == 1:
+                n, H, D = rows.shape
+                grp = xf.reshape(n, H, groups, D // groups)
+                amax = rows.reshape(n, H, groups, D // groups).abs().amax(-1).to(torch.float32)
+                if c.dtype == torch.int8:
+                    scale = amax / 127.0
+                    q = (grp / scale[..., None]).round().clamp(-128, 127)
+                    q = torch.where(scale[..., None] == 0, torch.zeros_like(q), q)
+                    codes = q.to(torch.int8).view(torch.uint8)
+                else:
+                    scale = amax / 448.0
+                    q = (grp / scale[..., None]).clamp(-448, 448)
+                    q = torch.where(scale[..., None] == 0, torch.zeros_like(q), q)
+                    codes = q.to(torch.float8_e4m3fn).view(torch.uint8)
+                c.view(torch.uint8)[b, :, pos] = codes.reshape(n, H, D)
+                if sc.dim() == 4:
+                    sc[b, :, pos] = scale
+                else:
+                    sc[b, :, pos] = scale[..., 0]
+                continue
+            if smode == 0:
+                s = ch.to(torch.float32)[None]                          # [1, H, D]
+            elif smode == 1:
+                s = ch.to(torch.float32)[:, pos].transpose(0, 1)[..., None]  # [n, H, 1]
+            else:
+                s = torch.tensor(float(ch), dtype=torch.float32)
+            q = xf / s
+            if c.dtype == torch.int8:
+                codes = q.round().clamp(-128, 127).to(torch.int8).view(torch.uint8)
+            else:
+                codes = q.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+            c.view(torch.uint8)[b, :, pos] = codes
+
+
+def torch_linear_read(case, op, key, value, kc, vc, ks=None, vs=None, smode=0, lens=None,
+                      block_tables=None, max_len=None):
+    """Ops 3-4 (dequant / copy out of the cache into token-major [T, H, D]) by torch."""
+    lens = case.lens if lens is None else lens
+    max_len = int(lens.max()) if max_len is None else max_len
+    segs = _lin_segments(case, max_len, out_dir=True, block_tables=block_tables, lens=lens)
+    for out, c, sc in ((key, kc, ks), (value, vc, vs)):
+        if out is None:
+            continue
+        for r, b, pos in segs:
+            if r.numel() == 0:
+                continue
+            rows = c[b, :, pos]                                   # [n, H, D]
+            if op == 4:
+                out[r] = rows
+            else:
+                s = sc[None] if smode == 0 else sc[b, :, pos][..., None]
+                out[r] = (rows.to(torch.float32) * s).to(out.dtype)
+
+
+def _lin_bits(t):
+    return t.view(torch.uint8) if t.dtype in (torch.int8, torch.float8_e4m3fn) else bits(t)
+
+
+LIN_CASES = [(p, o) for p in (True, False) for o in (False, True)]
+
+
+@pytest.mark.parametrize("packed,offsets", LIN_CASES)
+@pytest.mark.parametrize("dtype", DTYPES + [torch.int8])
+def test_linear_reshape_matches_torch(ref, dtype, packed, offsets):
+    case = W.linear_case(torch.float32, 11, packed=packed, offsets=offsets)
+    if dtype == torch.int8:
+        case.key = (case.key.clamp(-100, 100)).to(torch.int8)
+        case.value = (case.value * 10).clamp(-100, 100).to(torch.int8)
+    else:
+        case.key, case.value = case.key.to(dtype), case.value.to(dtype)
+    kc, vc = case.caches(dtype)
+    want_k, want_v = kc.clone(), vc.clone()
+    torch_linear_write(case, 0, want_k, want_v)
+    ref.linear_cache(0, case.key, case.value, kc, vc, case.context_lengths, case.max_context_len,
+                     packed=packed, context_seq_offset=case.context_seq_offset,
+                     cache_bs_id=case.cache_bs_id, cache_seq_offset=case.cache_seq_offset)
+    assert torch.equal(_lin_bits(kc), _lin_bits(want_k)) and torch.equal(_lin_bits(vc), _lin_bits(want_v))
+    # some rows were written and, with offsets, some were skipped
+    assert not torch.equal(_lin_bits(kc), _lin_bits(case.caches(dtype)[0]))
+
+
+@pytest.mark.parametrize("packed,offsets", LIN_CASES)
+@pytest.mark.parametrize("cache_dtype", [torch.int8, torch.float8_e4m3fn])
+@pytest.mark.parametrize("groups", [1, 4, 0])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_linear_dynamic_quant_matches_torch(ref, dtype, groups, cache_dtype, packed, offsets):
+    case = W.linear_case(dtype, 12, packed=packed, offsets=offsets)
+    kc, vc = case.caches(cache_dtype)
+    ks, vs = case.scales(groups)
+    wk, wv, wks, wvs = kc.clone(), vc.clone(), ks.clone(), vs.clone()
+    torch_linear_write(case, 1, wk, wv, wks, wvs, groups=max(groups, 1))
+    ref.linear_cache(1, case.key, case.value, kc, vc, case.context_lengths, case.max_context_len,
+                     packed=packed, context_seq_offset=case.context_seq_offset,
+                     cache_bs_id=case.cache_bs_id, cache_seq_offset=case.cache_seq_offset,
+                     key_scale=ks, value_scale=vs, groups=max(groups, 1))
+    assert torch.equal(_lin_bits(kc), _lin_bits(wk)) and torch.equal(_lin_bits(vc), _lin_bits(wv))
+    assert torch.equal(ks.view(torch.int32), wks.view(torch.int32))
+    assert torch.equal(vs.view(torch.int32), wvs.view(torch.int32))
+
+
+@pytest.mark.parametrize("smode", [0, 1, 2])
+@pytest.mark.parametrize("cache_dtype", [torch.int8, torch.float8_e4m3fn])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_linear_static_quant_matches_torch(ref, dtype, cache_dtype, smode):
+    case = W.linear_case(dtype, 13, packed=True, offsets=True)
+    g = torch.Generator().manual_seed(5)
+    H, D = case.key.shape[-2:]
+    if smode == 0:
+        kch, vch = 0.01 + 0.2 * torch.rand(H, D, generator=g), 0.02 + 0.1 * torch.rand(H, D, generator=g)
+        kt = vt = 1.0
+    elif smode == 1:
+        kch = 0.01 + 0.2 * torch.rand(H, case.cache_len, generator=g)
+        vch = 0.02 + 0.1 * torch.rand(H, case.cache_len, generator=g)
+        kt = vt = 1.0
+    else:
+        kch, vch, kt, vt = None, None, 0.0371, 0.0523
+    kc, vc = case.caches(cache_dtype)
+    wk, wv = kc.clone(), vc.clone()
+    torch_linear_write(case, 2, wk, wv, kchan=kch if smode < 2 else kt,
+                       vchan=vch if smode < 2 else vt, smode=smode)
+    ref.linear_cache(2, case.key, case.value, kc, vc, case.context_lengths, case.max_context_len,
+                     packed=True, context_seq_offset=case.context_seq_offset,
+                     cache_bs_id=case.cache_bs_id, cache_seq_offset=case.cache_seq_offset,
+                     key_chan=kch, value_chan=vch, key_tensor=kt, value_tensor=vt, smode=smode)
+    assert torch.equal(_lin_bits(kc), _lin_bits(wk)) and torch.equal(_lin_bits(vc), _lin_bits(wv))
+
+
+def _filled_linear_cache(case, seed=21):
+    g = torch.Generator().manual_seed(seed)
+    H, D = case.key.shape[-2:]
+    kc = torch.randint(-128, 128, (case.cache_batch, H, case.cache_len, D), generator=g,
+                       dtype=torch.int8)
+    vc = torch.randint(-128, 128, kc.shape, generator=g, dtype=torch.int8)
+    kt = torch.rand(case.cache_batch, H, case.cache_len, generator=g) * 0.05
+    vt = torch.rand(case.cache_batch, H, case.cache_len, generator=g) * 0.05
+    kch = torch.rand(H, D, generator=g) * 0.05
+    vch = torch.rand(H, D, generator=g) * 0.05
+    return kc, vc, kt, vt, kch, vch
+
+
+@pytest.mark.parametrize("offsets", [False, True])
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_linear_dequant_matches_torch(ref, dtype, mode, offsets):
+    case = W.linear_case(dtype, 14, packed=True, offsets=offsets)
+    kc, vc, kt, vt, kch, vch = _filled_linear_cache(case)
+    T = case.key.shape[0]
+    H, D = case.key.shape[-2:]
+    key = torch.full((T, H, D), -3.0, dtype=dtype)
+    value = key.clone()
+    wk, wv = key.clone(), value.clone()
+    ks, vs = (kch, vch) if mode == 0 else (kt, vt)
+    torch_linear_read(case, 3, wk, wv, kc, vc, ks, vs, smode=mode)
+    ref.linear_cache(3, key, value, kc, vc, case.lens, case.max_context_len,
+                     context_seq_offset=case.context_seq_offset, cache_bs_id=case.cache_bs_id,
+                     cache_seq_offset=case.cache_seq_offset,
+                     key_scale=kt if mode == 1 else None, value_scale=vt if mode == 1 else None,
+                     key_chan=kch if mode == 0 else None, value_chan=vch if mode == 0 else None,
+                     smode=mode)
+    assert torch.equal(bits(key), bits(wk)) and torch.equal(bits(value), bits(wv))
+
+
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("dtype", DTYPES + [torch.int8])
+def test_reshape_from_cache_matches_torch(ref, dtype, paged):
+    case = W.linear_case(torch.float32, 15, packed=True, offsets=not paged)
+    kc8, vc8 = _filled_linear_cache(case)[:2]
+    kc, vc = (kc8, vc8) if dtype == torch.int8 else (kc8.to(dtype) / 7, vc8.to(dtype) / 3)
+    T = case.key.shape[0]
+    H, D = case.key.shape[-2:]
+    key = torch.full((T, H, D), -3, dtype=dtype)
+    value = key.clone()
+    bt = None
+    if paged:  # pages of cache_len rows: sequence i uses a column of shuffled pages (-1: unused)
+        g = torch.Generator().manual_seed(3)
+        L, MB = case.cache_len, 2
+        case.cache_len = L // 4                                  # block_size 10
+        kc = kc.reshape(case.cache_batch * 4, H, L // 4, D) if False else \
+            kc[:, :, :L // 4 * 4].reshape(case.cache_batch, H, 4, L // 4, D).permute(0, 2, 1, 3, 4) \
+            .reshape(case.cache_batch * 4, H, L // 4, D).contiguous()
+        vc = vc[:, :, :L // 4 * 4].reshape(case.cache_batch, H, 4, L // 4, D).permute(0, 2, 1, 3, 4) \
+            .reshape(case.cache_batch * 4, H, L // 4, D).contiguous()
+        case.cache_batch *= 4
+        MB = 3
+        bt = torch.randperm(case.cache_batch, generator=g)[:case.lens.numel() * MB] \
+            .reshape(-1, MB).to(torch.int32)
+        bt[0, 2] = -1                                            # a missing page
+    wk, wv = key.clone(), value.clone()
+    torch_linear_read(case, 4, wk, wv, kc, vc, block_tables=bt)
+    ref.linear_cache(4, key, value, kc, vc, case.lens, case.max_context_len,
+                     context_seq_offset=case.context_seq_offset, cache_bs_id=case.cache_bs_id,
+                     cache_seq_offset=case.cache_seq_offset, block_tables=bt)
+    assert torch.equal(bits(key), bits(wk)) and torch.equal(bits(value), bits(wv))
+
+
+def test_linear_round_trips(ref):
+    """reshape_linear_cache then reshape_from_cache is the identity on the tokens it wrote;
+    quant then dequant is within scale / 2 per element (closed forms, not restatements)."""
+    case = W.linear_case(torch.bfloat16, 16, packed=True, offsets=False)
+    kc, vc = case.caches(torch.bfloat16)
+    ref.linear_cache(0, case.key, case.value, kc, vc, case.context_lengths, case.max_context_len,
+                     packed=True)
+    back_k = torch.zeros_like(case.key)
+    back_v = torch.zeros_like(case.value)
+    ref.linear_cache(4, back_k, back_v, kc, vc, case.lens, case.max_context_len)
+    n = int(case.lens.sum())
+    assert torch.equal(bits(back_k[:n]), bits(case.key[:n]))
+    assert torch.equal(bits(back_v[:n]), bits(case.value[:n]))
+    qk, qv = case.caches(torch.int8)
+    ks, vs = case.scales()
+    ref.linear_cache(1, case.key, case.value, qk, qv, case.context_lengths, case.max_context_len,
+                     packed=True, key_scale=ks, value_scale=vs)
+    deq = torch.zeros(case.key.shape, dtype=torch.float32)
+    ref.linear_cache(3, deq, None, qk, None, case.lens, case.max_context_len, key_scale=ks, smode=1)
+    starts = torch.cumsum(case.lens, 0) - case.lens
+    for i, (s0, n_i) in enumerate(zip(starts.tolist(), case.lens.tolist())):
+        x = case.key[s0:s0 + n_i].to(torch.float32)
+        sc = ks[i, :, :n_i].transpose(0, 1)[..., None]
+        # |x - code * s| <= s / 2 (1 + 2^-23), plus RN(code * s)'s half ulp <= 127 s 2^-24
+        assert ((deq[s0:s0 + n_i] - x).abs() <= sc * (0.5 + 2.0 ** -15)).all()
+
+
+def test_linear_max_context_len_truncates(ref):
+    case = W.linear_case(torch.float16, 17, packed=True, offsets=True)
+    kc, vc = case.caches(torch.float16)
+    wk, wv = kc.clone(), vc.clone()
+    torch_linear_write(case, 0, wk, wv, max_len=7)
+    ref.linear_cache(0, case.key, case.value, kc, vc, case.context_lengths, 7, packed=True,
+                     context_seq_offset=case.context_seq_offset, cache_bs_id=case.cache_bs_id,
+                     cache_seq_offset=case.cache_seq_offset)
+    assert torch.equal(bits(kc), bits(wk)) and torch.equal(bits(vc), bits(wv))

@@ -243,3 +243,91 @@ def fused_rope_case(dtype, mode, seed, B=3, S=20, Hq=4, Hk=2, D=128, rope=128, N
     else:
         ks = vs = None
     return qkv, kc, vc, sin, cos, position_id, k_gamma, q_gamma, ks, vs, slot
+
+
+@dataclass
+class LinearCase:
+    """Inputs of the linear-cache ops: token-major K/V (packed [T, H, D] or padded
+    [B, S, H, D]), sequence lengths and the optional offset / batch-id tensors (CPU)."""
+    key: torch.Tensor
+    value: torch.Tensor
+    lens: torch.Tensor                        # [B] lengths
+    packed: bool
+    context_seq_offset: Optional[torch.Tensor]
+    cache_bs_id: Optional[torch.Tensor]
+    cache_seq_offset: Optional[torch.Tensor]
+    cache_batch: int
+    cache_len: int
+
+    @property
+    def context_lengths(self) -> torch.Tensor:
+        """The write ops' context_lengths: batch + 1 prefix offsets when packed."""
+        if not self.packed:
+            return self.lens
+        return torch.cat((torch.zeros(1, dtype=torch.int32), self.lens.cumsum(0).to(torch.int32)))
+
+    @property
+    def max_context_len(self) -> int:
+        return int(self.lens.max()) if self.lens.numel() else 0
+
+    def caches(self, dtype, fill=CACHE_SENTINEL):
+        """Sentinel-filled [cache_batch, H, cache_len, D] caches of `dtype`."""
+        H, D = self.key.shape[-2], self.key.shape[-1]
+        shape = (self.cache_batch, H, self.cache_len, D)
+        if dtype in (torch.int8, torch.float8_e4m3fn):
+            return tuple(torch.full(shape, fill, dtype=torch.uint8).view(dtype) for _ in range(2))
+        return tuple(torch.full(shape, -7.0, dtype=dtype) for _ in range(2))
+
+    def scales(self, groups: int = 0):
+        """Sentinel-filled per-token scales [cache_batch, H, cache_len] (or [..., groups])."""
+        H = self.key.shape[-2]
+        shape = (self.cache_batch, H, self.cache_len) + ((groups,) if groups else ())
+        return torch.full(shape, SCALE_SENTINEL), torch.full(shape, SCALE_SENTINEL)
+
+
+def linear_case(dtype, seed: int, packed: bool = True, offsets: bool = False, B: int = 5,
+                H: int = 2, D: int = 64, S: int = 24, cache_batch: int = 7,
+                cache_len: int = 40) -> LinearCase:
+    """Sequences of random lengths in [0, S] (the first full, the second empty) with
+    magnitudes spread over tokens and a zero row.  With `offsets`: non-overlapping shuffled
+    token segments with gaps (context_seq_offset), a cache batch permutation with one
+    negative id, and cache position offsets of which one runs past cache_len."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(0, S + 1, (B,), generator=g).to(torch.int32)
+    lens[0] = S
+    if B > 1:
+        lens[1] = 0
+    cso = bsi = coff = None
+    if packed:
+        rows = int(lens.sum())
+        if offsets:
+            order = torch.randperm(B, generator=g).tolist()
+            gaps = torch.randint(0, 4, (B,), generator=g).tolist()
+            cso = torch.zeros(B, dtype=torch.int32)
+            at = 0
+            for i, gap in zip(order, gaps):
+                at += gap
+                cso[i] = at
+                at += int(lens[i])
+            rows = at + 2
+        scale = torch.logspace(-3, 2, rows)[:, None, None]
+        key = (torch.randn(rows, H, D, generator=g) * scale).to(dtype)
+        value = (torch.randn(rows, H, D, generator=g) * 3).to(dtype)
+        key[min(2, rows - 1)] = 0
+    else:
+        scale = torch.logspace(-3, 2, S)[None, :, None, None]
+        key = (torch.randn(B, S, H, D, generator=g) * scale).to(dtype)
+        value = (torch.randn(B, S, H, D, generator=g) * 3).to(dtype)
+        key[0, 1] = 0
+        if offsets:  # absolute rows of the flattened [B * S] tensor, inside each sequence
+            cso = torch.tensor([i * S + int(torch.randint(0, S - int(lens[i]) + 1, (1,),
+                                                           generator=g)) for i in range(B)],
+                               dtype=torch.int32)
+    if offsets:
+        bsi = torch.randperm(cache_batch, generator=g)[:B].to(torch.int32)
+        bsi[-1] = -1
+        coff = torch.tensor([int(torch.randint(0, max(1, cache_len - int(n) + 1), (1,), generator=g))
+                             for n in lens], dtype=torch.int32)
+        if B > 2:
+            coff[2] = cache_len - max(1, int(lens[2]) // 2)     # runs past the cache's end
+    return LinearCase(key, value, lens, packed, cso, bsi, coff, cache_batch, cache_len)
