@@ -50,13 +50,18 @@ WORKLOADS = {
     "offline_i8": "offline_quant_to_paged_cache on configs[2]'s shape (32768 tokens x 8 KV heads x 128 bf16), static per-channel scales -> int8 pages",
     "offline_f8": "offline_quant_to_paged_cache on configs[2]'s shape (32768 tokens x 8 KV heads x 128 bf16), static per-channel scales -> float8_e4m3fn pages",
     "fused_rope": "fused_rmsnorm_rope_store_paged_cache, Llama-3-8B prefill chunk: 8 x 4096 tokens, 32 Q + 8 KV heads x 128 bf16, Q written back, K/V -> int8 pages with dynamic per-token scales (65536 blocks x 16)",
+    "linear_quant": "quant_to_linear_cache on configs[2]'s volume: 8 packed sequences x 4096 tokens x 8 KV heads x 128 bf16 -> int8 linear cache [8, 8, 8192, 128] + fp32 per-token scales",
+    "linear_dequant": "dequant_from_linear_cache (per-token scales), 8 sequences x 4096 tokens x 8 KV heads x 128: int8 linear cache [8, 8, 8192, 128] -> bf16",
+    "linear_reshape": "reshape_linear_cache, 8 packed sequences x 4096 tokens x 8 KV heads x 128 bf16 -> bf16 linear cache [8, 8, 8192, 128]",
 }
 KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1>", "cfg2": "quant_paged_vec<BF16,16,1>",
            "cfg3": "quant_paged_vec<BF16,16,1>", "cfg4": "sq_dense<BF16,8,false,true>",
            "cfg4_moe": "sq_vec<BF16,8,false,1>", "cfg5": "dequant_paged_persistent<BF16,8>",
            "offline_i8": "quant_paged_static_vec<BF16,16,false>",
            "offline_f8": "quant_paged_static_vec<BF16,16,true>",
-           "fused_rope": "fused_rope_tok<BF16,16,4>"}
+           "fused_rope": "fused_rope_tok<BF16,16,4>",
+           "linear_quant": "lin_quant<BF16,16,false,false>", "linear_dequant": "lin_dequant<BF16,16>",
+           "linear_reshape": "lin_copy<16>"}
 
 
 def parse_args():
@@ -235,6 +240,58 @@ def bench_fused_rope(torch, tmo, W, dev, steps, warmup):
     return ms, alg, T, sets
 
 
+LIN_B, LIN_S, LIN_L = 8, 4096, 8192
+
+
+def linear_bytes(op: str, B: int = LIN_B, S: int = LIN_S, H: int = 8, D: int = W_D) -> int:
+    """Algorithmic bytes of a linear-cache workload (K and V): quant reads the bf16 rows and
+    writes codes + per-token scales; dequant reads codes + scales and writes bf16 rows; reshape
+    reads and writes bf16 rows; plus the context lengths."""
+    T = B * S
+    per_row = {"linear_quant": D * 2 + D + 4, "linear_dequant": D + 4 + D * 2,
+               "linear_reshape": 2 * D * 2}[op]
+    return 2 * T * H * per_row + 4 * (B + 1)
+
+
+def linear_call(torch, tmo, op: str, dev, g, B: int = LIN_B, S: int = LIN_S, L: int = LIN_L,
+                H: int = 8, D: int = W_D):
+    """One buffer set of a linear-cache workload and the closure that runs it."""
+    T = B * S
+    lens = torch.full((B,), S, dtype=torch.int32, device=dev)
+    cu = torch.arange(B + 1, dtype=torch.int32, device=dev) * S
+    if op == "linear_dequant":
+        kc = torch.randint(-127, 128, (B, H, L, D), generator=g, device=dev, dtype=torch.int8)
+        vc = torch.randint(-127, 128, (B, H, L, D), generator=g, device=dev, dtype=torch.int8)
+        ks = torch.rand((B, H, L), generator=g, device=dev) * 0.05
+        vs = torch.rand((B, H, L), generator=g, device=dev) * 0.05
+        key = torch.empty((T, H, D), dtype=torch.bfloat16, device=dev)
+        value = torch.empty_like(key)
+        return lambda: tmo.dequant_from_linear_cache(key, value, kc, vc, ks, vs, lens, S, None,
+                                                     None, None, 1, 8)
+    key = torch.randn((T, H, D), generator=g, device=dev).to(torch.bfloat16)
+    value = torch.randn((T, H, D), generator=g, device=dev).to(torch.bfloat16)
+    if op == "linear_reshape":
+        kc = torch.zeros((B, H, L, D), dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        return lambda: tmo.reshape_linear_cache(key, value, kc, vc, cu, S, True, None, None, None)
+    kc = torch.zeros((B, H, L, D), dtype=torch.int8, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((B, H, L), device=dev)
+    vs = torch.zeros_like(ks)
+    return lambda: tmo.quant_to_linear_cache(key, value, kc, vc, ks, vs, cu, S, True, None, None,
+                                             None)
+
+
+def bench_linear(torch, tmo, op: str, dev, steps, warmup):
+    """A linear-cache op over 8 x 4096 packed tokens: per set its own rows and caches."""
+    alg = linear_bytes(op)
+    sets = n_sets(alg)
+    g = torch.Generator(device=dev).manual_seed(13)
+    calls = [linear_call(torch, tmo, op, dev, g) for _ in range(sets)]
+    ms = time_graph(torch, calls, steps, warmup)
+    return ms, alg, LIN_B * LIN_S, sets
+
+
 def bench_smooth_quant(torch, tmo, W, case, dev, steps, warmup):
     alg = case.algorithmic_bytes()
     sets = n_sets(alg)
@@ -300,6 +357,8 @@ def profile_pass(torch, tmo, W, names, dev, n: int) -> None:
             sl = case3.slot_mapping.to(dev)
             fn = lambda: tmo.fused_rmsnorm_rope_store_paged_cache(qkv, kc, vc, tab, tab, pid, gm, gm,
                                                                   sl, ks, vs)
+        elif name.startswith("linear"):
+            fn = linear_call(torch, tmo, name, dev, torch.Generator(device=dev).manual_seed(13))
         elif name.startswith("cfg4"):
             case = getattr(W, name)()
             x, sm = case.x.to(dev), case.smooth.to(dev)
@@ -406,6 +465,27 @@ def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
         fn = lambda: oracle.fused_rope_paged(qkv, kc, vc, tab, tab, pid, gm, ks, vs, sl, 1e-5, gm,
                                              nthreads=nthreads)
         alg, units, desc = fused_rope_bytes(n), n, f"fused rope of one {n}-token sequence"
+    elif workload.startswith("linear"):
+        nb, S, H = LIN_B, 1024, W.H   # every sequence (the oracle threads over sequences)
+        op = {"linear_reshape": 0, "linear_quant": 1, "linear_dequant": 3}[workload]
+        g = torch.Generator().manual_seed(13)
+        lens = torch.full((nb,), S, dtype=torch.int32)
+        cu = torch.arange(nb + 1, dtype=torch.int32) * S
+        key = torch.randn((nb * S, H, W.D), generator=g).to(torch.bfloat16)
+        value = torch.randn((nb * S, H, W.D), generator=g).to(torch.bfloat16)
+        cdt = torch.bfloat16 if op == 0 else torch.int8
+        kc = torch.zeros((nb, H, LIN_L, W.D), dtype=cdt)
+        vc = torch.zeros_like(kc)
+        ks = torch.rand((nb, H, LIN_L), generator=g) * 0.05
+        vs = torch.rand((nb, H, LIN_L), generator=g) * 0.05
+        if op == 3:
+            kc.random_(-127, 128, generator=g)
+            vc.random_(-127, 128, generator=g)
+        fn = lambda: oracle.linear_cache(op, key, value, kc, vc, lens if op == 3 else cu, S,
+                                         packed=op != 3, key_scale=ks, value_scale=vs, smode=1,
+                                         nthreads=nthreads)
+        alg, units = linear_bytes(workload, B=nb, S=S), nb * S
+        desc = f"{workload} on the first {S} tokens of each of the {nb} sequences"
     elif workload.startswith("cfg4"):
         case = getattr(W, workload)()
         n = min(case.rows, 2048)
@@ -474,7 +554,7 @@ def main():
     dev = torch.device("cuda", 0)
     todo = [args.workload] if args.configs == "headline" else \
         ["cfg1", "cfg2", "cfg3", "cfg4", "cfg4_moe", "cfg5", "offline_i8", "offline_f8",
-         "fused_rope"]
+         "fused_rope", "linear_quant", "linear_dequant", "linear_reshape"]
     if args.workload not in todo:
         todo.append(args.workload)
     if args.profile_pass:
@@ -496,6 +576,9 @@ def main():
         elif name == "fused_rope":
             ms, alg, units, sets = bench_fused_rope(torch, tmo, W, dev, max(20, args.steps // 4),
                                                     args.warmup // 4)
+        elif name.startswith("linear"):
+            ms, alg, units, sets = bench_linear(torch, tmo, name, dev, max(20, args.steps // 4),
+                                                max(4, args.warmup // 4))
         else:
             ms, alg, units, sets = bench_dequant(torch, tmo, W, W.cfg5(), dev,
                                                  max(10, args.steps // 40), max(2, args.warmup // 10))
@@ -534,7 +617,9 @@ def main():
                    "io": {"cfg5": "int8 codes + fp32 scales in; bf16 out",
                           "offline_i8": "bf16 in; int8 codes out (static per-channel scales)",
                           "offline_f8": "bf16 in; float8_e4m3fn codes out (static per-channel scales)",
-                          "fused_rope": "bf16 qkv in; bf16 Q written back; int8 K/V codes + fp32 scales out"}
+                          "fused_rope": "bf16 qkv in; bf16 Q written back; int8 K/V codes + fp32 scales out",
+                          "linear_dequant": "int8 codes + fp32 scales in; bf16 out",
+                          "linear_reshape": "bf16 in; bf16 out"}
                    .get(args.workload, "bf16 in; int8 codes + fp32 scales out"),
                    "tokens_per_s": head["units_per_s"],
                    "frac_of_peak": head["frac_of_peak"]},

@@ -69,35 +69,71 @@ struct Seq {
   int64_t len, start, pos0;
 };
 
-// Exclusive prefix sum of the lengths before sequence i, by the whole workgroup.
-__device__ int64_t length_prefix(const LinParams& p, int64_t i) {
-  __shared__ int64_t part[256 / kWave];
-  int64_t acc = 0;
-  for (int64_t k = threadIdx.x; k < i; k += 256) acc += p.lens[k];
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, kWave);
-  if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = acc;
-  __syncthreads();
-  int64_t total = 0;
-#pragma unroll
-  for (int w = 0; w < 256 / kWave; ++w) total += part[w];
-  return total;
+// Exclusive prefix sum of the (int32) lengths before sequence i, computed by each wavefront on
+// its own (no LDS, no barrier): lane l adds lens[l], lens[l + 64], ... split into a signed high
+// and an unsigned low 16-bit half, so that both lane sums and both wavefront totals stay exact
+// in 32 bits for any batch the grid allows (<= 65535 sequences); DPP row sums and four lane
+// reads combine them.
+__device__ __forceinline__ int32_t row_sum_i32(int32_t v) {
+  v += (int32_t)dpp<kDppQuadSwap1>((uint32_t)v);
+  v += (int32_t)dpp<kDppQuadSwap2>((uint32_t)v);
+  v += (int32_t)dpp<kDppRowHalfMirror>((uint32_t)v);
+  v += (int32_t)dpp<kDppRowMirror>((uint32_t)v);
+  return v;  // every lane: the sum over its 16-lane row
 }
 
-// Every thread of the workgroup must call this (the prefix sum synchronises).
-__device__ Seq sequence(const LinParams& p, int64_t i) {
+__device__ int64_t length_prefix(const LinParams& p, int64_t i) {
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t lo = 0;
+  int32_t hi = 0;
+  for (int64_t k0 = 0; k0 < i; k0 += kWave) {
+    const int64_t k = k0 + lane;
+    const int32_t v = k < i ? p.lens[k] : 0;
+    lo += (uint32_t)v & 0xffffu;
+    hi += v >> 16;
+  }
+  const uint32_t lo_r = (uint32_t)row_sum_i32((int32_t)lo);
+  const int32_t hi_r = row_sum_i32(hi);
+  uint64_t lo_t = 0;
+  int64_t hi_t = 0;
+#pragma unroll
+  for (int r = 0; r < kWave; r += 16) {
+    lo_t += (uint32_t)__builtin_amdgcn_readlane((int)lo_r, r);
+    hi_t += __builtin_amdgcn_readlane(hi_r, r);
+  }
+  return hi_t * 65536 + (int64_t)lo_t;
+}
+
+// Called by whole wavefronts (the prefix sum reads across lanes).  The four
+// per-sequence numbers are loaded from valid addresses whether or not their tensor is given
+// (an absent one reads lens[i] and is discarded), so the loads issue together and the
+// workgroup waits for memory once before its rows' addresses are known.
+__device__ Seq sequence(const LinParams& p, int64_t i, bool defer_prefix = false) {
   Seq s;
-  const int64_t len = p.packed ? (int64_t)p.lens[i + 1] - p.lens[i] : (int64_t)p.lens[i];
+  const int32_t* so = p.seq_off ? p.seq_off + i : p.lens + i;
+  const int32_t* co = p.cache_off ? p.cache_off + i : p.lens + i;
+  const int32_t l0 = p.lens[i];
+  const int32_t l1 = p.lens[i + p.packed];
+  const int32_t so_v = *so;
+  const int32_t co_v = *co;
+  const int64_t len = p.packed ? (int64_t)l1 - l0 : (int64_t)l0;
   s.len = len < p.max_len ? len : p.max_len;
   if (p.seq_off) {
-    s.start = p.seq_off[i];
+    s.start = so_v;
   } else if (p.in_dir) {
-    s.start = p.packed ? (int64_t)p.lens[i] : i * p.pad_seqlen;
+    s.start = p.packed ? (int64_t)l0 : i * p.pad_seqlen;
   } else {
-    s.start = length_prefix(p, i);
+    s.start = defer_prefix ? 0 : length_prefix(p, i);
   }
-  s.pos0 = p.cache_off ? (int64_t)p.cache_off[i] : 0;
+  s.pos0 = p.cache_off ? (int64_t)co_v : 0;
   return s;
+}
+
+// Read ops: the cache rows (load addresses) do not depend on where the sequence's output rows
+// start, so the kernels issue their loads first and take the prefix sum (when no
+// context_seq_offset is given) while the loads are in flight.
+__device__ __forceinline__ void finish_start(const LinParams& p, int64_t i, Seq& s) {
+  if (!p.seq_off && !p.in_dir) s.start = length_prefix(p, i);
 }
 
 // Cache row of the token at cache position `pos` for head h, or -1 when it is skipped.
@@ -118,9 +154,42 @@ __device__ __forceinline__ int64_t cache_row(const LinParams& p, int64_t i, int6
   return (blk * p.heads + h) * p.block_rows + r;
 }
 
+// Tokens per thread of the vector kernels: every load of a thread's tokens is issued before
+// the first is used, so a workgroup keeps kT rows per lane group in flight and the
+// per-workgroup prologue (sequence lengths / offsets) is paid once per kT tokens.
+#ifndef TMO_LIN_TOKENS_PER_THREAD
+#define TMO_LIN_TOKENS_PER_THREAD 1
+#endif
+constexpr int kLinT = TMO_LIN_TOKENS_PER_THREAD;
+
+// Input rows are read once: non-temporal loads keep them from displacing the written rows.
+#ifndef TMO_LIN_NT_LOAD
+#define TMO_LIN_NT_LOAD 1
+#endif
+template <class T>
+__device__ __forceinline__ T stream_load(const T* q) {
+  if constexpr (TMO_LIN_NT_LOAD) return __builtin_nontemporal_load(q);
+  return *q;
+}
+
+// Codes are written once and not read back by the kernel: non-temporal stores.
+#ifndef TMO_LIN_NT_STORE
+#define TMO_LIN_NT_STORE 1
+#endif
+
+// Token j (< len) of thread slot t, its row and its cache row; false when skipped.
+__device__ __forceinline__ bool locate(const LinParams& p, const Seq& s, int64_t i, int h,
+                                       int64_t j, int64_t& r, int64_t& crow) {
+  if (j >= s.len) return false;
+  r = s.start + j;
+  crow = cache_row(p, i, s.pos0 + j, h);
+  return r >= 0 && r < p.rows && crow >= 0;
+}
+
 // ------------------------------------------------------------------------------ byte copies
 
-// reshape_linear_cache / reshape_from_cache: G lanes x 16 bytes per row.
+// reshape_linear_cache / reshape_from_cache: G lanes x 16 bytes per row, kLinT rows per lane
+// group.
 template <int G>
 __global__ __launch_bounds__(256) void lin_copy(LinParams p) {
   constexpr int kRows = 256 / G;
@@ -129,41 +198,83 @@ __global__ __launch_bounds__(256) void lin_copy(LinParams p) {
   const int64_t i = blockIdx.y;
   const int h = blockIdx.x % p.heads;
   const int64_t tile = blockIdx.x / p.heads;
-  const Seq s = sequence(p, i);
-  const int64_t j = tile * kRows + threadIdx.x / G;
-  if (j >= s.len) return;
-  const int64_t r = s.start + j;
-  const int64_t crow = cache_row(p, i, s.pos0 + j, h);
-  if (r < 0 || r >= p.rows || crow < 0) return;
-  u32x4 v[2];
+  Seq s = sequence(p, i, true);
+  const int64_t j0 = tile * (kRows * kLinT) + threadIdx.x / G;
+  bool ok[kLinT];
+  int64_t r[kLinT], crow[kLinT];
+  u32x4 v[kLinT][2];
+  if (p.in_dir) {  // token rows -> cache: the loads need the rows
 #pragma unroll
-  for (int kv = 0; kv < 2; ++kv) {
-    if (kv >= p.nkv) continue;
-    const char* t =
-        static_cast<const char*>(p.tok[kv]) + (r * p.st[kv] + (int64_t)h * p.sh[kv]) * es;
-    const char* c = static_cast<const char*>(p.cache[kv]) + crow * row_bytes;
-    v[kv] = *reinterpret_cast<const u32x4*>((p.in_dir ? t : c) + lane * 16);
+    for (int t = 0; t < kLinT; ++t) {
+      ok[t] = locate(p, s, i, h, j0 + t * kRows, r[t], crow[t]);
+      if (!ok[t]) continue;
+#pragma unroll
+      for (int kv = 0; kv < 2; ++kv) {
+        if (kv >= p.nkv) continue;
+        const char* tk = static_cast<const char*>(p.tok[kv]) +
+                         (r[t] * p.st[kv] + (int64_t)h * p.sh[kv]) * es;
+        v[t][kv] = stream_load(reinterpret_cast<const u32x4*>(tk + lane * 16));
+      }
+    }
+  } else {  // cache -> token rows: load first, place the rows afterwards
+#pragma unroll
+    for (int t = 0; t < kLinT; ++t) {
+      const int64_t j = j0 + t * kRows;
+      ok[t] = j < s.len;
+      crow[t] = ok[t] ? cache_row(p, i, s.pos0 + j, h) : -1;
+      ok[t] = crow[t] >= 0;
+      if (!ok[t]) continue;
+#pragma unroll
+      for (int kv = 0; kv < 2; ++kv) {
+        if (kv >= p.nkv) continue;
+        const char* c = static_cast<const char*>(p.cache[kv]) + crow[t] * row_bytes;
+        v[t][kv] = stream_load(reinterpret_cast<const u32x4*>(c + lane * 16));
+      }
+    }
+    finish_start(p, i, s);
+#pragma unroll
+    for (int t = 0; t < kLinT; ++t) {
+      r[t] = s.start + j0 + t * kRows;
+      ok[t] = ok[t] && r[t] >= 0 && r[t] < p.rows;
+    }
   }
 #pragma unroll
-  for (int kv = 0; kv < 2; ++kv) {
-    if (kv >= p.nkv) continue;
-    char* t = static_cast<char*>(p.tok[kv]) + (r * p.st[kv] + (int64_t)h * p.sh[kv]) * es;
-    char* c = static_cast<char*>(p.cache[kv]) + crow * row_bytes;
-    *reinterpret_cast<u32x4*>((p.in_dir ? c : t) + lane * 16) = v[kv];
+  for (int t = 0; t < kLinT; ++t) {
+    if (!ok[t]) continue;
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      if (kv >= p.nkv) continue;
+      char* tk = static_cast<char*>(p.tok[kv]) + (r[t] * p.st[kv] + (int64_t)h * p.sh[kv]) * es;
+      char* c = static_cast<char*>(p.cache[kv]) + crow[t] * row_bytes;
+      *reinterpret_cast<u32x4*>((p.in_dir ? c : tk) + lane * 16) = v[t][kv];
+    }
   }
 }
 
 // ------------------------------------------------------------------------------ 8-element I/O
 
+// 8 elements of a token row as raw 16-byte vectors (one for 16-bit types, two for fp32).
 template <class Tag>
-__device__ __forceinline__ void load8(const void* base, int64_t e, float* v) {
+struct Raw8 {
+  u32x4 w[Tag::kBytes == 4 ? 2 : 1];
+};
+
+template <class Tag>
+__device__ __forceinline__ Raw8<Tag> load8(const void* base, int64_t e) {
+  Raw8<Tag> x;
+  const u32x4* q = reinterpret_cast<const u32x4*>(static_cast<const char*>(base) + e * Tag::kBytes);
+  x.w[0] = stream_load(q);
+  if constexpr (Tag::kBytes == 4) x.w[1] = stream_load(q + 1);
+  return x;
+}
+
+template <class Tag>
+__device__ __forceinline__ void unpack8(const Raw8<Tag>& x, float* v) {
   if constexpr (Tag::kBytes == 4) {
-    const u32x4* q = reinterpret_cast<const u32x4*>(static_cast<const float*>(base) + e);
-    const u32x4 a = q[0], b = q[1];
-    unpack(F32{}, a, v);
-    unpack(F32{}, b, v + 4);
+    unpack(F32{}, x.w[0], v);
+    unpack(F32{}, x.w[1], v + 4);
   } else {
-    unpack(Tag{}, *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + e), v);
+    unpack(Tag{}, x.w[0], v);
   }
 }
 
@@ -213,7 +324,7 @@ __device__ __forceinline__ RowScale make_fp8_scale(float amax) {
 // ------------------------------------------------------------------------------ quantisers
 
 // quant_to_linear_cache (kStatic false) / offline_quant_to_linear_cache (kStatic true):
-// G = head_dim / 8 lanes per row, 8 channels per lane.
+// G = head_dim / 8 lanes per row, 8 channels per lane, kLinT rows per lane group.
 template <class Tag, int G, bool kFp8, bool kStatic>
 __global__ __launch_bounds__(256) void lin_quant(LinParams p) {
   constexpr int kRows = 256 / G;
@@ -221,81 +332,112 @@ __global__ __launch_bounds__(256) void lin_quant(LinParams p) {
   const int64_t i = blockIdx.y;
   const int h = blockIdx.x % p.heads;
   const int64_t tile = blockIdx.x / p.heads;
-  const Seq s = sequence(p, i);
-  const int64_t j = tile * kRows + threadIdx.x / G;
-  if (j >= s.len) return;  // the same in all lanes of a row
-  const int64_t r = s.start + j;
-  const int64_t pos = s.pos0 + j;
-  const int64_t crow = cache_row(p, i, pos, h);
-  if (r < 0 || r >= p.rows || crow < 0) return;
   const int d0 = lane * 8;
-
-  float x[2][8];
+  const float tscale0 = p.tscale[0], tscale1 = p.tscale[1];
+  // per-channel static scales: the same 8 channels for every token of the thread
+  float chan[2][8];
+  if constexpr (kStatic) {
 #pragma unroll
-  for (int kv = 0; kv < 2; ++kv)
-    if (kv < p.nkv) load8<Tag>(p.tok[kv], r * p.st[kv] + (int64_t)h * p.sh[kv] + d0, x[kv]);
-
-#pragma unroll
-  for (int kv = 0; kv < 2; ++kv) {
-    if (kv >= p.nkv) continue;
-    uint32_t c[2];
-    if constexpr (kStatic) {
-      float sc[8], y[8], q[8];
-      if (p.smode == 0) {
+    for (int kv = 0; kv < 2; ++kv) {
+      if (kv < p.nkv && p.smode == 0) {
         const u32x4* sp =
             reinterpret_cast<const u32x4*>(p.chan[kv] + (int64_t)h * p.head_dim + d0);
         const u32x4 a = sp[0], b = sp[1];
-        unpack(F32{}, a, sc);
-        unpack(F32{}, b, sc + 4);
-      } else {
-        const float one =
-            p.smode == 1 ? p.chan[kv][(int64_t)h * p.block_rows + pos] : p.tscale[kv];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sc[e] = one;
+        unpack(F32{}, a, chan[kv]);
+        unpack(F32{}, b, chan[kv] + 4);
       }
-      bool fast = true;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) fast &= static_scale_fast(sc[e]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = fast ? recip_rn(sc[e]) : 0.0f;
-      static_quotients<8>(x[kv], sc, y, fast, q);
-      encode_static<8, kFp8>(q, c);
-    } else {
-      const int gl = G / p.groups;  // lanes per scale group
-      float m = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) m = abs_max(m, x[kv][e]);
-      const float amax = __uint_as_float(lane_group_max<G>(__float_as_uint(m), gl));
-      float scale;
-      if constexpr (kFp8) {
-        const RowScale rs = make_fp8_scale(amax);
-        float q[8];
-        if (rs.fast) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) q[e] = div_by_recip(x[kv][e], rs.s, rs.y);
-        } else {
-          keep_branch();
-#pragma unroll
-          for (int e = 0; e < 8; ++e) q[e] = x[kv][e] / rs.s;  // IEEE divide
-        }
-        encode_static<8, true>(q, c);
-        if (rs.s == 0.0f) c[0] = c[1] = 0u;  // all-zero group: +0 codes, as the int8 path
-        scale = rs.s;
-      } else {
-        const RowScale rs = make_row_scale(amax);
-        encode_row<8>(x[kv], rs, c);
-        scale = rs.s;
-      }
-      if ((lane & (gl - 1)) == 0) p.scale[kv][crow * p.groups + lane / gl] = scale;
     }
-    u32x2 c2;
-    c2[0] = c[0];
-    c2[1] = c[1];
-    *reinterpret_cast<u32x2*>(static_cast<int8_t*>(p.cache[kv]) + crow * p.head_dim + d0) = c2;
+  }
+  const Seq s = sequence(p, i);
+  const int64_t j0 = tile * (kRows * kLinT) + threadIdx.x / G;
+  bool ok[kLinT];
+  int64_t r[kLinT], crow[kLinT];
+  Raw8<Tag> x[kLinT][2];
+#pragma unroll
+  for (int t = 0; t < kLinT; ++t) {
+    ok[t] = locate(p, s, i, h, j0 + t * kRows, r[t], crow[t]);  // the same in a row's lanes
+    if (!ok[t]) continue;
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv)
+      if (kv < p.nkv) x[t][kv] = load8<Tag>(p.tok[kv], r[t] * p.st[kv] + (int64_t)h * p.sh[kv] + d0);
+  }
+
+#pragma unroll
+  for (int t = 0; t < kLinT; ++t) {
+    if (!ok[t]) continue;
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      if (kv >= p.nkv) continue;
+      float v[8];
+      unpack8<Tag>(x[t][kv], v);
+      uint32_t c[2];
+      if constexpr (kStatic) {
+        float sc[8], y[8], q[8];
+        if (p.smode == 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sc[e] = chan[kv][e];
+        } else {
+          // the per-tensor scale as a value: a conditional expression choosing between the
+          // address of a kernel-argument field and a global address compiles to a flat load
+          // whose address the argument-field path never set (it faulted), so the two are
+          // read separately
+          float one = kv == 0 ? tscale0 : tscale1;
+          if (p.smode == 1) one = p.chan[kv][(int64_t)h * p.block_rows + (s.pos0 + j0 + t * kRows)];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sc[e] = one;
+        }
+        bool fast = true;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fast &= static_scale_fast(sc[e]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = fast ? recip_rn(sc[e]) : 0.0f;
+        static_quotients<8>(v, sc, y, fast, q);
+        encode_static<8, kFp8>(q, c);
+      } else {
+        const int gl = G / p.groups;  // lanes per scale group
+        float m = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = abs_max(m, v[e]);
+        const float amax = __uint_as_float(lane_group_max<G>(__float_as_uint(m), gl));
+        float scale;
+        if constexpr (kFp8) {
+          const RowScale rs = make_fp8_scale(amax);
+          float q[8];
+          if (rs.fast) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[e] = div_by_recip(v[e], rs.s, rs.y);
+          } else {
+            keep_branch();
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[e] = v[e] / rs.s;  // IEEE divide
+          }
+          encode_static<8, true>(q, c);
+          if (rs.s == 0.0f) c[0] = c[1] = 0u;  // all-zero group: +0 codes, as the int8 path
+          scale = rs.s;
+        } else {
+          const RowScale rs = make_row_scale(amax);
+          encode_row<8>(v, rs, c);
+          scale = rs.s;
+        }
+        if ((lane & (gl - 1)) == 0)
+          __builtin_nontemporal_store(scale, p.scale[kv] + crow[t] * p.groups + lane / gl);
+      }
+      u32x2 c2;
+      c2[0] = c[0];
+      c2[1] = c[1];
+      u32x2* dst = reinterpret_cast<u32x2*>(static_cast<int8_t*>(p.cache[kv]) +
+                                            crow[t] * p.head_dim + d0);
+      if constexpr (TMO_LIN_NT_STORE) {
+        store_nt(dst, c2);
+      } else {
+        *dst = c2;
+      }
+    }
   }
 }
 
-// dequant_from_linear_cache: out = RN(fp32(code) * scale), 8 channels per lane.
+// dequant_from_linear_cache: out = RN(fp32(code) * scale), 8 channels per lane, kLinT rows
+// per lane group.
 template <class Tag, int G>
 __global__ __launch_bounds__(256) void lin_dequant(LinParams p) {
   constexpr int kRows = 256 / G;
@@ -303,39 +445,57 @@ __global__ __launch_bounds__(256) void lin_dequant(LinParams p) {
   const int64_t i = blockIdx.y;
   const int h = blockIdx.x % p.heads;
   const int64_t tile = blockIdx.x / p.heads;
-  const Seq s = sequence(p, i);
-  const int64_t j = tile * kRows + threadIdx.x / G;
-  if (j >= s.len) return;
-  const int64_t r = s.start + j;
-  const int64_t crow = cache_row(p, i, s.pos0 + j, h);
-  if (r < 0 || r >= p.rows || crow < 0) return;
   const int d0 = lane * 8;
-  u32x2 code[2];
-  float sc[2][8];
+  float chan[2][8];
 #pragma unroll
   for (int kv = 0; kv < 2; ++kv) {
-    if (kv >= p.nkv) continue;
-    code[kv] = *reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(p.cache[kv]) +
-                                               crow * p.head_dim + d0);
-    if (p.smode == 0) {
+    if (kv < p.nkv && p.smode == 0) {
       const u32x4* sp = reinterpret_cast<const u32x4*>(p.chan[kv] + (int64_t)h * p.head_dim + d0);
       const u32x4 a = sp[0], b = sp[1];
-      unpack(F32{}, a, sc[kv]);
-      unpack(F32{}, b, sc[kv] + 4);
-    } else {
-      const float one = p.scale[kv][crow];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sc[kv][e] = one;
+      unpack(F32{}, a, chan[kv]);
+      unpack(F32{}, b, chan[kv] + 4);
     }
   }
+  Seq s = sequence(p, i, true);
+  const int64_t j0 = tile * (kRows * kLinT) + threadIdx.x / G;
+  bool ok[kLinT];
+  int64_t r[kLinT], crow[kLinT];
+  u32x2 code[kLinT][2];
+  float tok_scale[kLinT][2];
 #pragma unroll
-  for (int kv = 0; kv < 2; ++kv) {
-    if (kv >= p.nkv) continue;
-    float v[8];
+  for (int t = 0; t < kLinT; ++t) {
+    const int64_t j = j0 + t * kRows;
+    crow[t] = j < s.len ? cache_row(p, i, s.pos0 + j, h) : -1;
+    ok[t] = crow[t] >= 0;
+    if (!ok[t]) continue;
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      v[e] = (float)(int8_t)(code[kv][e >> 2] >> (8 * (e & 3))) * sc[kv][e];
-    store8<Tag>(p.tok[kv], r * p.st[kv] + (int64_t)h * p.sh[kv] + d0, v);
+    for (int kv = 0; kv < 2; ++kv) {
+      if (kv >= p.nkv) continue;
+      code[t][kv] = stream_load(reinterpret_cast<const u32x2*>(
+          static_cast<const int8_t*>(p.cache[kv]) + crow[t] * p.head_dim + d0));
+      if (p.smode != 0) tok_scale[t][kv] = p.scale[kv][crow[t]];
+    }
+  }
+  finish_start(p, i, s);
+#pragma unroll
+  for (int t = 0; t < kLinT; ++t) {
+    r[t] = s.start + j0 + t * kRows;
+    ok[t] = ok[t] && r[t] >= 0 && r[t] < p.rows;
+  }
+#pragma unroll
+  for (int t = 0; t < kLinT; ++t) {
+    if (!ok[t]) continue;
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      if (kv >= p.nkv) continue;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float sc = p.smode == 0 ? chan[kv][e] : tok_scale[t][kv];
+        v[e] = (float)(int8_t)(code[t][kv][e >> 2] >> (8 * (e & 3))) * sc;
+      }
+      store8<Tag>(p.tok[kv], r[t] * p.st[kv] + (int64_t)h * p.sh[kv] + d0, v);
+    }
   }
 }
 
@@ -377,10 +537,11 @@ __global__ __launch_bounds__(256) void lin_generic(LinParams p) {
         store1(Tag{}, p.tok[kv], te + d, (float)(int8_t)codes[d] * sc);
       }
     } else if (op == 2) {
+      const float tsc = kv == 0 ? p.tscale[0] : p.tscale[1];  // a value, not an address
       for (int d = lane; d < D; d += kWave) {
-        const float sc = p.smode == 0 ? p.chan[kv][(int64_t)h * D + d]
-                       : p.smode == 1 ? p.chan[kv][(int64_t)h * p.block_rows + pos]
-                                      : p.tscale[kv];
+        float sc = tsc;
+        if (p.smode == 0) sc = p.chan[kv][(int64_t)h * D + d];
+        if (p.smode == 1) sc = p.chan[kv][(int64_t)h * p.block_rows + pos];
         const float q = load1(Tag{}, p.tok[kv], te + d) / sc;  // IEEE divide
         const uint32_t b =
             kFp8 ? fp8e4m3_bits(__builtin_amdgcn_fmed3f(q, -448.0f, 448.0f)) : code_bits(q);
@@ -451,7 +612,7 @@ int launch_copy(const LinParams& p, int64_t batch, int es, hipStream_t st) {
   for (int kv = 0; kv < p.nkv && vec; ++kv) vec = aligned(p.cache[kv], 16);
   if (!vec) return launch_generic<BF16>(p, batch, 0, es, false, st);
   dim3 grid;
-  const int rc = grid_for(p, batch, 256 / G, grid);
+  const int rc = grid_for(p, batch, (256 / G) * kLinT, grid);
   if (rc != TMO_OK) return rc;
   LinParams q = p;
   q.es = es;
@@ -487,7 +648,7 @@ int launch_quant(const LinParams& p, int64_t batch, hipStream_t st) {
   }
   if (!vec) return launch_generic<Tag>(p, batch, kStatic ? 2 : 1, Tag::kBytes, kFp8, st);
   dim3 grid;
-  const int rc = grid_for(p, batch, 256 / G, grid);
+  const int rc = grid_for(p, batch, (256 / G) * kLinT, grid);
   if (rc != TMO_OK) return rc;
   switch (G) {
     case 1: return launch_kernel(lin_quant<Tag, 1, kFp8, kStatic>, grid, dim3(256), st, p);
@@ -520,7 +681,7 @@ int launch_dequant(const LinParams& p, int64_t batch, hipStream_t st) {
   const int G = lanes8(p, Tag::kBytes);
   if (G == 0) return launch_generic<Tag>(p, batch, 3, Tag::kBytes, false, st);
   dim3 grid;
-  const int rc = grid_for(p, batch, 256 / G, grid);
+  const int rc = grid_for(p, batch, (256 / G) * kLinT, grid);
   if (rc != TMO_OK) return rc;
   switch (G) {
     case 1: return launch_kernel(lin_dequant<Tag, 1>, grid, dim3(256), st, p);

@@ -297,7 +297,10 @@ __global__ __launch_bounds__(256) void quant_paged_static_generic(StaticParams s
     const int64_t base = t * p.stride_tok[kv] + (int64_t)h * p.stride_head[kv];
     int8_t* dst = p.cache[kv] + page_row * p.head_dim;
     for (int d = lane; d < p.head_dim; d += kWave) {
-      const float s = sc.chan[kv] ? sc.chan[kv][(int64_t)h * p.head_dim + d] : sc.tensor[kv];
+      // the per-tensor scale is read as a value: choosing between its kernel-argument address
+      // and a global address would make the load a flat load of a selected pointer
+      float s = kv == 0 ? sc.tensor[0] : sc.tensor[1];
+      if (sc.chan[kv]) s = sc.chan[kv][(int64_t)h * p.head_dim + d];
       const float q = load1(Tag{}, p.src[kv], base + d) / s;  // IEEE divide
       const uint32_t b =
           kFp8 ? fp8e4m3_bits(__builtin_amdgcn_fmed3f(q, -448.0f, 448.0f)) : code_bits(q);

@@ -365,3 +365,28 @@ def test_linear_prefill_roundtrips(tmo, ref, dev):
     tmo.reshape_from_cache(out, None, bc, None, lensd, L)
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), key.view(torch.int16))
+
+
+@pytest.mark.parametrize("B", [1, 63, 64, 65, 150, 700])
+def test_output_rows_follow_the_length_prefix(tmo, ref, dev, B):
+    """Reads without context_seq_offset place sequence i at the sum of the lengths before it
+    (per-wavefront prefix over 64-length chunks: 1, 2 and 11 chunks), zero lengths included."""
+    g = torch.Generator().manual_seed(90 + B)
+    lens = torch.randint(0, 9, (B,), generator=g).to(torch.int32)
+    case = W.LinearCase(torch.zeros(1, 2, 64), torch.zeros(1, 2, 64), lens, False, None, None,
+                        None, B, 8)
+    kc, vc, kt, vt, _, _ = _filled(case, seed=B)
+    T = int(lens.sum()) + 5
+    key = torch.full((T, 2, 64), -3.0, dtype=torch.bfloat16)
+    ref.linear_cache(3, key, None, kc, None, lens, 8, key_scale=kt, smode=1)
+    gkey = torch.full((T, 2, 64), -3.0, dtype=torch.bfloat16, device=dev)
+    tmo.dequant_from_linear_cache(gkey, None, kc.to(dev), None, kt.to(dev), None, lens.to(dev), 8,
+                                  None, None, None, 1, 8)
+    torch.cuda.synchronize()
+    _cmp(gkey, key, "key")
+    out = torch.full((T, 2, 64), 7, dtype=torch.int8)
+    ref.linear_cache(4, out, None, kc, None, lens, 8)
+    gout = torch.full((T, 2, 64), 7, dtype=torch.int8, device=dev)
+    tmo.reshape_from_cache(gout, None, kc.to(dev), None, lens.to(dev), 8)
+    torch.cuda.synchronize()
+    _cmp(gout, out, "reshape_from_cache key")
