@@ -7,6 +7,10 @@
 //   fp8: fp8x4 (v_cvt_pk_fp8_f32) == fp8e4m3_bits (the integer encoder, itself checked on
 //        the host against a nearest-value search by div_exhaustive.hip "fp8") for every fp32
 //        value in [-448, 448].
+//   mfma: the operand / result lane layouts of v_mfma_f32_16x16x16_bf16 and _f16 that the
+//        decode-attention kernel assumes -- lane l holds A[l % 16][4 (l / 16) + e],
+//        B[4 (l / 16) + e][l % 16] and C[4 (l / 16) + e][l % 16], e = 0..3 -- on small integer
+//        matrices whose products are exact, against the host's matrix product.
 //   sqrt: __builtin_sqrtf (the fused rope's rms) is correctly rounded for every positive
 //        finite fp32 x: with m- and m+ the midpoints between r = sqrtf(x) and its neighbours,
 //        m-^2 < x < m+^2 (25-bit midpoints square exactly in fp64; no x sits on a midpoint).
@@ -69,6 +73,75 @@ __global__ void check_sqrt(unsigned long long* bad) {
   if (b) atomicAdd(bad, b);
 }
 
+typedef short bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// One wavefront: operands gathered from row-major 16x16 A and B by the assumed layout, the
+// four result registers of every lane written to c[lane][e].  kF16: f16 inputs, else bf16.
+template <bool kF16>
+__global__ void mfma_layout(const float* a, const float* b, float* c) {
+  const int l = threadIdx.x;
+  const int r = l % 16, g = l / 16;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (kF16) {
+    f16x4 av, bv;
+    for (int e = 0; e < 4; ++e) {
+      av[e] = (_Float16)a[r * 16 + 4 * g + e];
+      bv[e] = (_Float16)b[(4 * g + e) * 16 + r];
+    }
+    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bv, acc, 0, 0, 0);
+  } else {
+    bf16x4 av, bv;
+    for (int e = 0; e < 4; ++e) {  // small integers: the upper half of the fp32 is exact bf16
+      av[e] = (short)(__float_as_uint(a[r * 16 + 4 * g + e]) >> 16);
+      bv[e] = (short)(__float_as_uint(b[(4 * g + e) * 16 + r]) >> 16);
+    }
+    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv, acc, 0, 0, 0);
+  }
+  for (int e = 0; e < 4; ++e) c[l * 4 + e] = acc[e];
+}
+
+// Host side of "mfma": both input types; returns the mismatch count.
+unsigned long long run_mfma(unsigned long long& checked) {
+  float ha[256], hb[256], want[256], got[256];
+  for (int m = 0; m < 16; ++m)
+    for (int k = 0; k < 16; ++k) {
+      ha[m * 16 + k] = (float)((m * 3 + k * 7) % 17 - 8);
+      hb[m * 16 + k] = (float)((m * 5 + k * 11) % 13 - 6);
+    }
+  for (int m = 0; m < 16; ++m)
+    for (int n = 0; n < 16; ++n) {
+      float s = 0.0f;
+      for (int k = 0; k < 16; ++k) s += ha[m * 16 + k] * hb[k * 16 + n];
+      want[m * 16 + n] = s;
+    }
+  float *da = nullptr, *db = nullptr, *dc = nullptr;
+  if (hipMalloc(&da, sizeof ha) != hipSuccess || hipMalloc(&db, sizeof hb) != hipSuccess ||
+      hipMalloc(&dc, sizeof got) != hipSuccess ||
+      hipMemcpy(da, ha, sizeof ha, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(db, hb, sizeof hb, hipMemcpyHostToDevice) != hipSuccess)
+    return ~0ull;
+  unsigned long long bad = 0;
+  for (int variant = 0; variant < 2; ++variant) {
+    if (variant == 0) {
+      mfma_layout<false><<<dim3(1), dim3(64)>>>(da, db, dc);
+    } else {
+      mfma_layout<true><<<dim3(1), dim3(64)>>>(da, db, dc);
+    }
+    if (hipMemcpy(got, dc, sizeof got, hipMemcpyDeviceToHost) != hipSuccess) return ~0ull;
+    for (int l = 0; l < 64; ++l)
+      for (int e = 0; e < 4; ++e) {
+        ++checked;
+        if (got[l * 4 + e] != want[(4 * (l / 16) + e) * 16 + l % 16]) ++bad;
+      }
+  }
+  hipFree(da);
+  hipFree(db);
+  hipFree(dc);
+  return bad;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -93,6 +166,14 @@ int main(int argc, char** argv) {
     std::memcpy(&hi, &fhi, 4);
     checked = 2ull * ((unsigned long long)(hi / 4) + 1) * 4;
     check_fp8<<<dim3(8192), dim3(256)>>>(hi, d_bad);
+  } else if (!std::strcmp(mode, "mfma")) {
+    const unsigned long long b = run_mfma(checked);
+    if (b == ~0ull) {
+      std::printf("mfma setup failed\n");
+      return 2;
+    }
+    std::printf("mode=%s mismatches=%llu checked=%llu\n", mode, b, checked);
+    return b == 0 ? 0 : 1;
   } else if (!std::strcmp(mode, "sqrt")) {
     checked = 0x7f800000ull - 1;
     check_sqrt<<<dim3(8192), dim3(256)>>>(d_bad);
