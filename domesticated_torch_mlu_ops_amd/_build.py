@@ -30,7 +30,7 @@ HIP_LIB = LIB_DIR / "libtmo_hip.so"
 TORCH_EXT = LIB_DIR / "_tmo_torch.so"
 
 HIP_SOURCES = ["quant_paged.hip", "reshape_paged.hip", "dequant_paged.hip", "fused_rope.hip",
-               "linear_cache.hip",
+               "linear_cache.hip", "decode_attn.hip",
                "scaled_quantize.hip", "abi_info.hip"]
 
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))

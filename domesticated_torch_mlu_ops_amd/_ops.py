@@ -26,6 +26,7 @@ __all__ = [
     "offline_quant_to_linear_cache",
     "dequant_from_linear_cache",
     "reshape_from_cache",
+    "single_query_cached_kv_attn",
 ]
 
 
@@ -492,3 +493,68 @@ def reshape_from_cache(
     torch.ops.torch_mlu_ops.reshape_from_cache(
         key, value, key_cache, value_cache, context_lengths, max_context_len,
         context_seq_offset, block_tables, cache_seq_offset)
+
+
+# ---------------------------------------------------------------------------- decode attention
+
+_DTYPE_STR = {torch.half: "half", torch.float: "float", torch.bfloat16: "bfloat16"}
+
+
+def single_query_cached_kv_attn(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: Optional[torch.Tensor],
+    out: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    k_cache_quant_scale: Optional[torch.Tensor],
+    v_cache_quant_scale: Optional[torch.Tensor],
+    alibi_slopes: Optional[torch.Tensor],
+    max_context_len: int,
+    windows_size_left: int,
+    windows_size_right: int,
+    softmax_scale: float,
+    return_lse: bool = False,
+    kv_cache_quant_bit_size=-1,
+    q_quant_scale: Optional[torch.Tensor] = None,
+    out_quant_scale: Optional[torch.Tensor] = None,
+    out_dtype: torch.dtype = torch.half,
+    compute_dtype: torch.dtype = torch.float,
+    head_size_v: int = -1,
+    mask: Optional[torch.Tensor] = None,
+    cu_seq_q: Optional[torch.Tensor] = None,
+    max_seq_q: int = -1,
+    sink: Optional[torch.Tensor] = None,
+):
+    """Decode attention of one query token per sequence (``q [batch, 1, heads, head_size]`` or
+    ``[batch, heads, head_size]``) over its paged KV cache: ``softmax(softmax_scale * q K^T
+    (+ alibi)) V`` over the keys ``[max(0, L - 1 - windows_size_left), L)`` of each sequence,
+    keys gathered through ``block_tables`` from ``[num_blocks, kv_heads, block_size,
+    head_size]`` caches -- int8 (``kv_cache_quant_bit_size=8``) with per-token, per-channel or
+    per-tensor scales, or of q's dtype (``-1``); query head h reads KV head
+    ``h // (heads / kv_heads)``.  Computed in fp32 (MFMA with exact bf16/f16 operands).  With
+    ``return_lse`` also returns ``ln sum exp`` of the logits, ``[batch, heads, 1]`` (or
+    ``[heads, total_q]`` for 3-D q).  One query token per sequence only: ``cu_seq_q``,
+    ``mask``, ``sink`` and quantised q / output raise ``RuntimeError``.
+
+    Reference: ``_ops.py:777-900`` (math ``:800-817``).  Returns ``out`` or ``(out, lse)``.
+    """
+    tmo_out = out
+    if out is None:
+        if v_cache is not None:
+            head_size_v = v_cache.shape[-1]
+        if q.dtype not in {torch.float8_e4m3fn, torch.int8}:
+            out_dtype = q.dtype
+        tmo_out = torch.empty(q.size()[:-1] + (head_size_v,), dtype=out_dtype, device=q.device)
+    out_lse = None
+    if return_lse:
+        lse_shape = q.shape[:-3] + (q.shape[-2],) + (q.shape[-3],)
+        out_lse = torch.empty(lse_shape, dtype=torch.float, device=q.device)
+    torch.ops.torch_mlu_ops.single_query_cached_kv_attn(
+        q, k_cache, tmo_out, block_tables, context_lens, v_cache, out_lse, q_quant_scale,
+        k_cache_quant_scale, v_cache_quant_scale, out_quant_scale, alibi_slopes, mask,
+        _DTYPE_STR.get(compute_dtype, str(compute_dtype)), max_context_len, windows_size_left,
+        windows_size_right, softmax_scale, return_lse, kv_cache_quant_bit_size, cu_seq_q,
+        max_seq_q, sink)
+    return (tmo_out, out_lse) if return_lse else tmo_out
+

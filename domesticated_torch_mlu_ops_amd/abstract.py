@@ -141,3 +141,21 @@ def reshape_from_cache_abstract(key: Tensor, value: Optional[Tensor], key_cache:
                                 cache_seq_offset: Optional[Tensor] = None) -> None:
     return None
 
+
+@torch.library.register_fake("torch_mlu_ops::single_query_cached_kv_attn")
+def single_query_cached_kv_attn_abstract(q_ori: Tensor, k_cache: Tensor, output: Tensor,
+                                         block_tables: Tensor, context_lens: Tensor,
+                                         v_cache: Optional[Tensor], output_lse: Optional[Tensor],
+                                         q_quant_scale: Optional[Tensor],
+                                         k_cache_quant_scale: Optional[Tensor],
+                                         v_cache_quant_scale: Optional[Tensor],
+                                         out_quant_scale: Optional[Tensor],
+                                         alibi_slopes: Optional[Tensor], mask: Optional[Tensor],
+                                         compute_dtype: str, max_context_len: int,
+                                         windows_size_left: int, windows_size_right: int,
+                                         softmax_scale: float, return_lse: bool,
+                                         kv_cache_quant_bit_size: int,
+                                         cu_seq_q: Optional[Tensor] = None, max_seq_q: int = -1,
+                                         sink: Optional[Tensor] = None) -> None:
+    return None
+

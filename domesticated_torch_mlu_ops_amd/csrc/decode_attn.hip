@@ -1,0 +1,660 @@
+// single_query_cached_kv_attn for gfx950: one query token per sequence against its paged KV
+// cache (reference _ops.py:777-900; header include/torch_mlu_ops.h:107-130).
+//
+//   s_j = softmax_scale * q . k_j (+ alibi_slope * (j - (L - 1))),  out = softmax(s) @ V,
+//   lse = log sum_j exp(s_j),  keys j in [max(0, L - 1 - window_left), L),
+//
+// key j at row j % BS of page block_tables[i, j / BS] (pages outside [0, NB) are masked); query
+// head hq reads KV head hq / (Hq / Hkv).  Caches are int8 with per-token [NB, Hkv, BS] or
+// per-channel [Hkv, D] fp32 scales (k = code * scale), or of q's dtype.
+//
+// MFMA path (bf16 or f16 operands, fp32 accumulation; head_size 64 / 128 / 256, block_size a
+// multiple of 16, at most 16 query heads per KV head): a workgroup of four wavefronts owns one
+// (sequence, KV head, split) and its wavefronts take every fourth 16-token tile.  Per tile:
+//   * S^T = K Q^T with v_mfma_f32_16x16x16 (tokens are the rows, the group's query heads the
+//     columns, zero-padded to 16): lane (t = l % 16, c = l / 16) holds token t's channels
+//     [c D/4, (c + 1) D/4), so the K tile is read as contiguous row pieces, and MFMA m takes
+//     channels c D/4 + 4m .. + 3 of every lane group (a permutation of the reduction order).
+//     Int8 codes convert to bf16 exactly (|code| <= 128 has 8 significant bits); the per-token
+//     scale and softmax_scale * log2(e) multiply the fp32 result.
+//   * The result layout (lane holds tokens 4c .. 4c + 3 of query column l % 16) IS the B
+//     operand layout of O^T = V^T P^T, so the probabilities feed the second product without a
+//     shuffle.  V^T's operand needs four tokens of one channel per lane: lane (n, c) reads
+//     D/16 bytes of tokens 4c .. 4c + 3 at channels n D/16 .., and MFMA j uses channel
+//     n D/16 + j of them, so lane (q, c) accumulates channels [4c D/16, (4c + 4) D/16) -- one
+//     contiguous run of the output row.
+//   * p is split into hi + lo operands of the MFMA type (16 significant bits with bf16) and
+//     two products accumulate; q likewise when it is not exactly representable (fp16 q on the
+//     bf16 path, or q folded with per-channel key scales).
+//   * Online softmax in base 2 per query column; a lane keeps a partial sum over its own four
+//     tokens, summed over the lane groups at the end.
+// The four wavefronts combine through LDS; with more than one split per (sequence, KV head)
+// the partials (max, sum, normalised row) go to a caller-provided workspace and a combine
+// kernel merges them.  A generic kernel (one wavefront per (sequence, query head), VALU)
+// serves every other shape and dtype.
+#include "tmo_device.h"
+
+namespace tmo {
+namespace {
+
+typedef short bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct AttnParams {
+  const void* q;
+  int64_t q_sb, q_sh;            // q [B, Hq, D] strides (elements); last dim contiguous
+  const void* kc;
+  const void* vc;                // caches [NB, Hkv, BS, D] contiguous
+  const float* ks;
+  const float* vs;
+  int32_t smode;                 // 0 plain caches, 1 per-token scales, 2 per-channel scales
+  const int32_t* bt;
+  int64_t max_blocks;
+  const int32_t* lens;
+  const float* alibi;            // [B, Hq] or null
+  int64_t window;                // < 0: unlimited
+  float scale_log2;              // softmax_scale * log2(e)
+  void* out;
+  int64_t o_sb, o_sh;
+  float* lse;                    // null when not requested
+  int64_t lse_sb, lse_sh;
+  int32_t B, Hq, Hkv, g, D, BS;
+  int64_t NB;
+  int32_t q_dtype;               // TMO_DTYPE_*
+  int32_t c_dtype;               // cache TMO_DTYPE_*
+  int32_t splits;
+  int64_t split_tokens;          // multiple of 64
+  float* ws;                     // [B, Hkv, splits, g, D + 2] when splits > 1
+};
+
+// ------------------------------------------------------------------------------ small helpers
+
+__device__ __forceinline__ uint16_t bf16_bits_rne(float x) {
+  return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+__device__ __forceinline__ float bf16_value(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+__device__ __forceinline__ float load_q(const AttnParams& p, int64_t e) {
+  switch (p.q_dtype) {
+    case TMO_DTYPE_BF16: return load1(BF16{}, p.q, e);
+    case TMO_DTYPE_F16: return load1(F16{}, p.q, e);
+    default: return load1(F32{}, p.q, e);
+  }
+}
+
+__device__ __forceinline__ void store_out(const AttnParams& p, int64_t e, float v) {
+  switch (p.q_dtype) {
+    case TMO_DTYPE_BF16: store1(BF16{}, p.out, e, v); break;
+    case TMO_DTYPE_F16: store1(F16{}, p.out, e, v); break;
+    default: store1(F32{}, p.out, e, v); break;
+  }
+}
+
+// Token range of sequence i (after the window) and of split s within it.
+struct Range {
+  int64_t L, begin, end;
+};
+
+__device__ __forceinline__ Range token_range(const AttnParams& p, int64_t i, int s) {
+  Range r;
+  int64_t L = p.lens[i];
+  const int64_t cap = p.max_blocks * (int64_t)p.BS;
+  if (L > cap) L = cap;
+  if (L < 0) L = 0;
+  r.L = L;
+  int64_t j0 = 0;
+  if (p.window >= 0 && L - 1 - p.window > 0) j0 = L - 1 - p.window;
+  r.begin = j0 + (int64_t)s * p.split_tokens;
+  r.end = r.begin + p.split_tokens < L ? r.begin + p.split_tokens : L;
+  if (s == p.splits - 1) r.end = L;  // the last split takes any tokens past max_context_len
+  if (p.splits == 1) r.begin = j0;
+  return r;
+}
+
+// Max / sum over the four lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48) of a column.
+__device__ __forceinline__ float col_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  return fmaxf(v, __shfl_xor(v, 32, kWave));
+}
+__device__ __forceinline__ float col_sum(float v) {
+  v += __shfl_xor(v, 16, kWave);
+  return v + __shfl_xor(v, 32, kWave);
+}
+
+// ------------------------------------------------------------------------------ MFMA kernel
+
+template <bool kF16>
+struct Mfma;
+template <>
+struct Mfma<false> {  // bf16 operands
+  typedef bf16x4 V4;
+  static __device__ __forceinline__ f32x4 run(V4 a, V4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ short bits(float x) { return (short)bf16_bits_rne(x); }
+  static __device__ __forceinline__ float value(short b) { return bf16_value((uint16_t)b); }
+};
+template <>
+struct Mfma<true> {  // f16 operands
+  typedef f16x4 V4;
+  static __device__ __forceinline__ f32x4 run(V4 a, V4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Four int8 codes (one dword) -> four exact bf16 operands.
+__device__ __forceinline__ bf16x4 codes_bf16(uint32_t w) {
+  bf16x4 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    r[e] = (short)(__float_as_uint((float)(int8_t)(w >> (8 * e))) >> 16);
+  return r;
+}
+
+// kKind: 0 int8 caches (bf16 MFMA), 1 bf16 caches, 2 f16 caches.  kQLo: q needs a lo part.
+template <int kD, int kKind, bool kQLo>
+__global__ __launch_bounds__(256) void attn_mfma(AttnParams p) {
+  constexpr bool kF16 = kKind == 2;
+  using M = Mfma<kF16>;
+  using V4 = typename M::V4;
+  constexpr int kDC = kD / 4;       // channels per lane group in the K layout
+  constexpr int kDV = kD / 16;      // channels per lane in the V layout
+  constexpr int kQK = kD / 16;      // QK MFMAs per tile
+  constexpr int kEs = kKind == 0 ? 1 : 2;  // cache element bytes
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int col = lane & 15;        // query column (query head within the group) / token row
+  const int grp = lane >> 4;        // lane group c
+  const int64_t i = blockIdx.z;
+  const int hk = blockIdx.y;
+  const int split = blockIdx.x;
+  const Range rg = token_range(p, i, split);
+  const int hq = hk * p.g + col;
+  const bool qvalid = col < p.g;
+
+  // ---- Q operand (B of S^T = K Q^T): column `col`, channels grp * kDC + 4m .. + 3
+  V4 qhi[kQK], qlo[kQLo ? kQK : 1];
+#pragma unroll
+  for (int m = 0; m < kQK; ++m) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = grp * kDC + 4 * m + e;
+      float x = qvalid ? load_q(p, i * p.q_sb + (int64_t)hq * p.q_sh + d) : 0.0f;
+      if (kKind == 0 && p.smode == 2) x *= p.ks[(int64_t)hk * kD + d];
+      if constexpr (kF16) {
+        qhi[m][e] = (_Float16)x;
+      } else {
+        const short hb = M::bits(x);
+        qhi[m][e] = hb;
+        if constexpr (kQLo) qlo[m][e] = M::bits(x - M::value(hb));
+      }
+    }
+  }
+  const float alibi = (p.alibi && qvalid) ? p.alibi[i * p.Hq + hq] * kLog2e : 0.0f;
+
+  float mrun = -__builtin_inff();   // running max (base 2) of this lane's column
+  float lpart = 0.0f;               // this lane's share of the running sum
+  f32x4 acc[kDV];
+#pragma unroll
+  for (int j = 0; j < kDV; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int64_t first_tile = rg.begin >> 4;
+  const int64_t end_tile = (rg.end + 15) >> 4;
+  const char* kbase = static_cast<const char*>(p.kc);
+  const char* vbase = static_cast<const char*>(p.vc);
+  const int64_t page_bytes = (int64_t)p.BS * kD * kEs;      // one head's page
+  for (int64_t tile = first_tile + wave; tile < end_tile; tile += 4) {
+    const int64_t t0 = tile * 16;
+    const int64_t blk = p.bt[i * p.max_blocks + t0 / p.BS];
+    if (blk < 0 || blk >= p.NB) continue;                  // missing page: its keys are masked
+    const int64_t row0 = t0 % p.BS;
+    const int64_t head_off = (blk * p.Hkv + hk) * page_bytes;
+    // K: token `col`, channels grp * kDC ..; V: tokens 4 grp .. + 3, channels col * kDV ..
+    const char* krow = kbase + head_off + (row0 + col) * kD * kEs + grp * kDC * kEs;
+    uint32_t kw[kDC * kEs / 4];
+#pragma unroll
+    for (int u = 0; u < kDC * kEs / 16; ++u) {
+      const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(krow) + u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kw[4 * u + e] = w[e];
+    }
+    uint32_t vw[4][kDV * kEs / 4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const char* vrow = vbase + head_off + (row0 + 4 * grp + e) * kD * kEs + col * kDV * kEs;
+      if constexpr (kDV * kEs == 16) {
+        const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vrow));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) vw[e][u] = w[u];
+      } else if constexpr (kDV * kEs == 8) {
+        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vrow));
+        vw[e][0] = w[0];
+        vw[e][1] = w[1];
+      } else if constexpr (kDV * kEs == 4) {
+        vw[e][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vrow));
+      } else {  // 32 bytes
+        const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vrow));
+        const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vrow) + 1);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          vw[e][u] = a[u];
+          vw[e][4 + u] = b[u];
+        }
+      }
+    }
+    float ksc[4] = {1.0f, 1.0f, 1.0f, 1.0f}, vsc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if (kKind == 0 && p.smode == 1) {
+      const int64_t so = (blk * p.Hkv + hk) * p.BS + row0 + 4 * grp;
+      const u32x4 a = *reinterpret_cast<const u32x4*>(p.ks + so);
+      const u32x4 b = *reinterpret_cast<const u32x4*>(p.vs + so);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ksc[e] = __uint_as_float(a[e]);
+        vsc[e] = __uint_as_float(b[e]);
+      }
+    }
+
+    // ---- S^T = K Q^T
+    f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int m = 0; m < kQK; ++m) {
+      V4 a;
+      if constexpr (kKind == 0) {
+        a = codes_bf16(kw[m]);
+      } else {
+        const uint32_t w0 = kw[2 * m], w1 = kw[2 * m + 1];
+        typedef short s4 __attribute__((ext_vector_type(4)));
+        s4 b4;
+        b4[0] = (short)(w0 & 0xffffu);
+        b4[1] = (short)(w0 >> 16);
+        b4[2] = (short)(w1 & 0xffffu);
+        b4[3] = (short)(w1 >> 16);
+        a = __builtin_bit_cast(V4, b4);
+      }
+      s = M::run(a, qhi[m], s);
+      if constexpr (kQLo) s = M::run(a, qlo[m], s);
+    }
+
+    // ---- scores (base 2), masking, online softmax
+    float sc[4];
+    float tmax = -__builtin_inff();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t j = t0 + 4 * grp + e;
+      float v = s[e] * ksc[e] * p.scale_log2;
+      if (p.alibi) v += alibi * (float)(j - (rg.L - 1));
+      if (j < rg.begin || j >= rg.end || !qvalid) v = -__builtin_inff();
+      sc[e] = v;
+      tmax = fmaxf(tmax, v);
+    }
+    tmax = col_max(tmax);
+    // no branch on the column's state: the MFMAs below need the whole wavefront
+    const float mnew = fmaxf(mrun, tmax);
+    const bool live = mnew != -__builtin_inff();            // some key of this column so far
+    const float corr = live ? __builtin_amdgcn_exp2f(mrun - mnew) : 1.0f;  // mrun = -inf -> 0
+    mrun = mnew;
+    float pe[4];
+    float psum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      pe[e] = live ? __builtin_amdgcn_exp2f(sc[e] - mnew) : 0.0f;  // masked: -inf -> 0
+      psum += pe[e];
+    }
+    lpart = lpart * corr + psum;
+    if (__ballot(corr != 1.0f)) {
+#pragma unroll
+      for (int j = 0; j < kDV; ++j) acc[j] *= corr;
+    }
+
+    // ---- P^T operands (hi + lo) with the per-token V scale folded in
+    V4 phi, plo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float pv = pe[e] * vsc[e];
+      if constexpr (kF16) {
+        const _Float16 h = (_Float16)pv;
+        phi[e] = h;
+        plo[e] = (_Float16)(pv - (float)h);
+      } else {
+        const short hb = M::bits(pv);
+        phi[e] = hb;
+        plo[e] = M::bits(pv - M::value(hb));
+      }
+    }
+
+    // ---- O^T += V^T P^T: MFMA j takes channel col * kDV + j of tokens 4 grp .. + 3
+#pragma unroll
+    for (int j = 0; j < kDV; ++j) {
+      V4 a;
+      if constexpr (kKind == 0) {
+        typedef short s4 __attribute__((ext_vector_type(4)));
+        s4 b4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int8_t code = (int8_t)(vw[e][j >> 2] >> (8 * (j & 3)));
+          b4[e] = (short)(__float_as_uint((float)code) >> 16);
+        }
+        a = __builtin_bit_cast(V4, b4);
+      } else {
+        typedef short s4 __attribute__((ext_vector_type(4)));
+        s4 b4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b4[e] = (short)(vw[e][j >> 1] >> (16 * (j & 1)));
+        a = __builtin_bit_cast(V4, b4);
+      }
+      acc[j] = M::run(a, phi, acc[j]);
+      acc[j] = M::run(a, plo, acc[j]);
+    }
+  }
+
+  // ---- combine the four wavefronts: waves 1..3 leave (max, sum, accumulators) in LDS in
+  // their lane layout, wave 0 merges them into its own registers lane by lane and writes
+  const float lsum = col_sum(lpart);
+  __shared__ float lds_m[4][16];
+  __shared__ float lds_l[4][16];
+  __shared__ float lds_o[3][16][kD];
+  if (grp == 0) {
+    lds_m[wave][col] = mrun;
+    lds_l[wave][col] = lsum;
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < kDV; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lds_o[wave - 1][col][kDV * (4 * grp + e) + j] = acc[j][e];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int w = 0; w < 4; ++w) mx = fmaxf(mx, lds_m[w][col]);
+  float f[4];
+  float lt = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    f[w] = mx == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(lds_m[w][col] - mx);
+    lt += lds_l[w][col] * f[w];
+  }
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  if (!qvalid) return;
+  const bool direct = p.splits == 1;
+  float* ws_row = p.ws + ((((i * p.Hkv + hk) * p.splits + split) * p.g + col) * (int64_t)(kD + 2));
+  if (!direct && grp == 0) {
+    ws_row[0] = mx;
+    ws_row[1] = lt;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+#pragma unroll
+    for (int j = 0; j < kDV; ++j) {
+      const int d = kDV * (4 * grp + e) + j;
+      float o = acc[j][e] * f[0];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) o += lds_o[w - 1][col][d] * f[w];
+      o *= inv;
+      if (kKind == 0 && p.smode == 2) o *= p.vs[(int64_t)hk * kD + d];  // per-channel V scale
+      if (direct) {
+        store_out(p, i * p.o_sb + (int64_t)hq * p.o_sh + d, o);
+      } else {
+        ws_row[2 + d] = o;
+      }
+    }
+  }
+  if (direct && grp == 0 && p.lse)
+    p.lse[i * p.lse_sb + (int64_t)hq * p.lse_sh] =
+        lt > 0.0f ? (mx + log2f(lt)) * kLn2 : -__builtin_inff();
+}
+
+// Merge the splits of one (sequence, query head): one wavefront per row.
+__global__ __launch_bounds__(256) void attn_combine(AttnParams p) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;  // i * Hq + hq
+  if (row >= (int64_t)p.B * p.Hq) return;
+  const int64_t i = row / p.Hq;
+  const int hq = (int)(row - i * p.Hq);
+  const int hk = hq / p.g, qc = hq - hk * p.g;
+  const int64_t stride = (int64_t)p.g * (p.D + 2);
+  const float* base = p.ws + ((i * p.Hkv + hk) * p.splits * (int64_t)p.g + qc) * (p.D + 2);
+  float mx = -__builtin_inff();
+  for (int s = 0; s < p.splits; ++s) mx = fmaxf(mx, base[s * stride]);
+  float lt = 0.0f;
+  for (int s = 0; s < p.splits; ++s) {
+    const float m = base[s * stride];
+    if (m != -__builtin_inff()) lt += base[s * stride + 1] * __builtin_amdgcn_exp2f(m - mx);
+  }
+  for (int d = lane; d < p.D; d += kWave) {
+    float o = 0.0f;
+    for (int s = 0; s < p.splits; ++s) {
+      const float m = base[s * stride];
+      if (m != -__builtin_inff())
+        o += base[s * stride + 2 + d] * base[s * stride + 1] * __builtin_amdgcn_exp2f(m - mx);
+    }
+    store_out(p, i * p.o_sb + (int64_t)hq * p.o_sh + d, lt > 0.0f ? o / lt : 0.0f);
+  }
+  if (lane == 0 && p.lse)
+    p.lse[i * p.lse_sb + (int64_t)hq * p.lse_sh] =
+        lt > 0.0f ? (mx + log2f(lt)) * kLn2 : -__builtin_inff();
+}
+
+// ------------------------------------------------------------------------------ generic kernel
+
+__device__ __forceinline__ float cache_value(const AttnParams& p, const void* base, const float* sc,
+                                             int64_t blk, int hk, int64_t row, int d,
+                                             int cache_dtype) {
+  const int64_t e = ((blk * p.Hkv + hk) * p.BS + row) * p.D + d;
+  switch (cache_dtype) {
+    case TMO_DTYPE_I8: {
+      const float code = (float)static_cast<const int8_t*>(base)[e];
+      if (p.smode == 1) return code * sc[(blk * p.Hkv + hk) * p.BS + row];
+      return code * sc[(int64_t)hk * p.D + d];
+    }
+    case TMO_DTYPE_BF16: return load1(BF16{}, base, e);
+    case TMO_DTYPE_F16: return load1(F16{}, base, e);
+    default: return load1(F32{}, base, e);
+  }
+}
+
+// One wavefront per (sequence, query head): 64 keys at a time, one per lane (a lane computes
+// its key's full dot product), then every lane accumulates its channels over the 64 keys.
+// Dimensions up to 512 (8 accumulators per lane).
+__global__ __launch_bounds__(256) void attn_generic(AttnParams p) {
+  const int cache_dtype = p.c_dtype;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+  if (row >= (int64_t)p.B * p.Hq) return;
+  const int64_t i = row / p.Hq;
+  const int hq = (int)(row - i * p.Hq);
+  const int hk = hq / p.g;
+  const Range rg = token_range(p, i, 0);
+  const float alibi = p.alibi ? p.alibi[i * p.Hq + hq] * kLog2e : 0.0f;
+  float mrun = -__builtin_inff(), l = 0.0f;
+  float acc[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
+  const int64_t qe = i * p.q_sb + (int64_t)hq * p.q_sh;
+  for (int64_t j0 = rg.begin; j0 < rg.end; j0 += kWave) {
+    const int64_t j = j0 + lane;
+    float s = -__builtin_inff();
+    int blk = -1, r = 0;
+    if (j < rg.end) {
+      blk = p.bt[i * p.max_blocks + j / p.BS];
+      r = (int)(j % p.BS);
+      if (blk >= 0 && blk < p.NB) {
+        float dot = 0.0f;
+        for (int d = 0; d < p.D; ++d)
+          dot += load_q(p, qe + d) * cache_value(p, p.kc, p.ks, blk, hk, r, d, cache_dtype);
+        s = dot * p.scale_log2;
+        if (p.alibi) s += alibi * (float)(j - (rg.L - 1));
+      } else {
+        blk = -1;
+      }
+    }
+    float tmax = s;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, kWave));
+    const float mnew = fmaxf(mrun, tmax);
+    if (mnew == -__builtin_inff()) continue;
+    const float corr = __builtin_amdgcn_exp2f(mrun - mnew);
+    mrun = mnew;
+    const float pj = __builtin_amdgcn_exp2f(s - mnew);
+    float ps = pj;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ps += __shfl_xor(ps, o, kWave);
+    l = l * corr + ps;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] *= corr;
+    for (int t = 0; t < kWave; ++t) {
+      const float pt = __shfl(pj, t, kWave);
+      const int bt_ = __shfl(blk, t, kWave);
+      const int rt = __shfl(r, t, kWave);
+      if (pt == 0.0f || bt_ < 0) continue;  // the same in every lane
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int d = lane + u * kWave;
+        if (d < p.D) acc[u] += pt * cache_value(p, p.vc, p.vs, bt_, hk, rt, d, cache_dtype);
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int d = lane + u * kWave;
+    if (d < p.D) store_out(p, i * p.o_sb + (int64_t)hq * p.o_sh + d, l > 0.0f ? acc[u] / l : 0.0f);
+  }
+  if (lane == 0 && p.lse)
+    p.lse[i * p.lse_sb + (int64_t)hq * p.lse_sh] =
+        l > 0.0f ? (mrun + log2f(l)) * kLn2 : -__builtin_inff();
+}
+
+// ------------------------------------------------------------------------------ launch
+
+template <int kD, int kKind>
+int launch_mfma_d(const AttnParams& p, bool qlo, hipStream_t st) {
+  const dim3 grid((unsigned)p.splits, (unsigned)p.Hkv, (unsigned)p.B), block(256);
+  int rc = qlo ? launch_kernel(attn_mfma<kD, kKind, true>, grid, block, st, p)
+               : launch_kernel(attn_mfma<kD, kKind, false>, grid, block, st, p);
+  if (rc != TMO_OK || p.splits == 1) return rc;
+  const int64_t rows = (int64_t)p.B * p.Hq;
+  return launch_kernel(attn_combine, dim3((unsigned)((rows + 3) / 4)), block, st, p);
+}
+
+template <int kKind>
+int launch_mfma(const AttnParams& p, bool qlo, hipStream_t st) {
+  switch (p.D) {
+    case 64: return launch_mfma_d<64, kKind>(p, qlo, st);
+    case 128: return launch_mfma_d<128, kKind>(p, qlo, st);
+    default: return launch_mfma_d<256, kKind>(p, qlo, st);
+  }
+}
+
+}  // namespace
+}  // namespace tmo
+
+using namespace tmo;
+
+extern "C" int64_t tmo_hip_attn_workspace_bytes(int64_t batch, int64_t num_kv_heads,
+                                                int64_t num_q_heads, int64_t head_size,
+                                                int64_t max_context_len, int64_t splits) {
+  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || head_size <= 0 || splits <= 1)
+    return 0;
+  (void)max_context_len;
+  return batch * num_kv_heads * splits * (num_q_heads / num_kv_heads) * (head_size + 2) *
+         (int64_t)sizeof(float);
+}
+
+extern "C" int tmo_hip_single_query_cached_kv_attn(
+    const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* k_cache,
+    const void* v_cache, const float* k_scale, const float* v_scale, int scale_mode,
+    const int32_t* block_tables, int64_t max_blocks, const int32_t* context_lens,
+    const float* alibi_slopes, void* out, int64_t out_stride_seq, int64_t out_stride_head,
+    float* lse, int64_t lse_stride_seq, int64_t lse_stride_head, int64_t batch,
+    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_size, int64_t num_blocks,
+    int64_t block_size, int64_t max_context_len, int64_t window_left, float softmax_scale,
+    int q_dtype, int cache_dtype, int64_t splits, void* workspace, int64_t workspace_bytes,
+    void* stream) {
+  if (q_dtype != TMO_DTYPE_BF16 && q_dtype != TMO_DTYPE_F16 && q_dtype != TMO_DTYPE_F32)
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (cache_dtype != TMO_DTYPE_I8 && cache_dtype != q_dtype) return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (cache_dtype == TMO_DTYPE_I8 && scale_mode != 1 && scale_mode != 2)
+    return TMO_ERR_UNSUPPORTED_MODE;
+  if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (cache_dtype == TMO_DTYPE_I8 && (!k_scale || !v_scale)) return TMO_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
+      head_size <= 0 || head_size > 512 || num_blocks < 0 || block_size <= 0 || max_blocks < 0 ||
+      max_context_len < 0 || splits < 1 || q_stride_seq < 0 || q_stride_head < 0 ||
+      out_stride_seq < 0 || out_stride_head < 0)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (batch > 65535 || num_kv_heads > 65535 || splits > 65535 || num_q_heads > 0x7fffffffLL)
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (splits > 1 && (!workspace ||
+                     workspace_bytes < tmo_hip_attn_workspace_bytes(batch, num_kv_heads,
+                                                                     num_q_heads, head_size,
+                                                                     max_context_len, splits)))
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (batch == 0 || num_q_heads == 0) return TMO_OK;
+
+  AttnParams p{};
+  p.q = q;
+  p.q_sb = q_stride_seq;
+  p.q_sh = q_stride_head;
+  p.kc = k_cache;
+  p.vc = v_cache;
+  p.ks = k_scale;
+  p.vs = v_scale;
+  p.smode = cache_dtype == TMO_DTYPE_I8 ? scale_mode : 0;
+  p.bt = block_tables;
+  p.max_blocks = max_blocks;
+  p.lens = context_lens;
+  p.alibi = alibi_slopes;
+  p.window = window_left;
+  p.scale_log2 = softmax_scale * kLog2e;
+  p.out = out;
+  p.o_sb = out_stride_seq;
+  p.o_sh = out_stride_head;
+  p.lse = lse;
+  p.lse_sb = lse_stride_seq;
+  p.lse_sh = lse_stride_head;
+  p.B = (int32_t)batch;
+  p.Hq = (int32_t)num_q_heads;
+  p.Hkv = (int32_t)num_kv_heads;
+  p.g = (int32_t)(num_q_heads / num_kv_heads);
+  p.D = (int32_t)head_size;
+  p.BS = (int32_t)block_size;
+  p.NB = num_blocks;
+  p.q_dtype = q_dtype;
+  p.ws = static_cast<float*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  // MFMA path eligibility: head size, page rows, group size, 16-byte aligned rows and scales,
+  // q's dtype representable by the operands (int8 caches: bf16 with a lo part when needed).
+  auto al = [](const void* x, int a) { return reinterpret_cast<uintptr_t>(x) % a == 0; };
+  bool mfma = (head_size == 64 || head_size == 128 || head_size == 256) && block_size % 16 == 0 &&
+              p.g <= 16 && al(k_cache, 16) && al(v_cache, 16);
+  if (cache_dtype == TMO_DTYPE_I8) {
+    mfma = mfma && q_dtype != TMO_DTYPE_F32 && (scale_mode != 1 || (al(k_scale, 16) && al(v_scale, 16)));
+  } else {
+    mfma = mfma && q_dtype != TMO_DTYPE_F32;
+  }
+  p.c_dtype = cache_dtype;
+  if (!mfma) {
+    p.splits = 1;
+    p.split_tokens = 1;
+    const int64_t rows = batch * num_q_heads;
+    if ((rows + 3) / 4 > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
+    return launch_kernel(attn_generic, dim3((unsigned)((rows + 3) / 4)), dim3(256), st, p);
+  }
+  p.splits = (int32_t)splits;
+  // tokens per split: the context divided evenly, rounded up to whole 64-token steps (four
+  // wavefronts x 16-token tiles)
+  int64_t per = (max_context_len + splits - 1) / splits;
+  per = (per + 63) / 64 * 64;
+  p.split_tokens = per > 0 ? per : 64;
+  if (cache_dtype == TMO_DTYPE_I8) return launch_mfma<0>(p, q_dtype != TMO_DTYPE_BF16 || scale_mode == 2, st);
+  if (cache_dtype == TMO_DTYPE_BF16) return launch_mfma<1>(p, false, st);
+  return launch_mfma<2>(p, false, st);
+}

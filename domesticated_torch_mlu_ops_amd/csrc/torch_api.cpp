@@ -8,6 +8,7 @@
 // have had (its Python wrappers return the written tensors in place: reference
 // _ops.py:1290-1294, 1562-1565, 3821-3824, 3249-3253), so torch.compile functionalisation
 // keeps the cache writes.
+#include <algorithm>
 #include <cmath>
 
 #include <c10/hip/HIPStream.h>
@@ -922,6 +923,165 @@ void reshape_from_cache(at::Tensor& key, const c10::optional<at::Tensor>& value,
   check_status(st, "reshape_from_cache");
 }
 
+// ------------------------------------------------------------------------------ decode attention
+
+void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor& k_cache,
+                                 const torch::Tensor& output, const torch::Tensor& block_tables,
+                                 const torch::Tensor& context_lens,
+                                 const c10::optional<torch::Tensor>& v_cache,
+                                 const c10::optional<torch::Tensor>& output_lse,
+                                 const c10::optional<torch::Tensor>& q_quant_scale,
+                                 const c10::optional<torch::Tensor>& k_cache_quant_scale,
+                                 const c10::optional<torch::Tensor>& v_cache_quant_scale,
+                                 const c10::optional<torch::Tensor>& out_quant_scale,
+                                 const c10::optional<torch::Tensor>& alibi_slopes,
+                                 const c10::optional<torch::Tensor>& mask,
+                                 const std::string& compute_dtype, c10::SymInt max_context_len,
+                                 c10::SymInt windows_size_left, c10::SymInt windows_size_right,
+                                 double softmax_scale, bool return_lse,
+                                 int64_t kv_cache_quant_bit_size,
+                                 const c10::optional<torch::Tensor>& cu_seq_q,
+                                 c10::SymInt max_seq_q, const c10::optional<torch::Tensor>& sink) {
+  const char* op = "single_query_cached_kv_attn";
+  TORCH_CHECK(!q_quant_scale.has_value() && !out_quant_scale.has_value(), op,
+              ": quantised q / output are not supported by this build");
+  TORCH_CHECK(!mask.has_value() && !sink.has_value(), op, ": mask and sink are not supported");
+  TORCH_CHECK(!cu_seq_q.has_value(), op,
+              ": one query token per sequence only (cu_seq_q is not supported)");
+  TORCH_CHECK(v_cache.has_value(), op, ": a separate v_cache is required");
+  TORCH_CHECK(compute_dtype == "float" || compute_dtype == "half" || compute_dtype == "bfloat16",
+              op, ": compute_dtype must be float, half or bfloat16 (the softmax runs in fp32)");
+  TORCH_CHECK(windows_size_right.expect_int() == -1, op, ": windows_size_right must be -1");
+  TORCH_CHECK(kv_cache_quant_bit_size == -1 || kv_cache_quant_bit_size == 8, op,
+              ": kv_cache_quant_bit_size must be -1 or 8, got ", kv_cache_quant_bit_size);
+  (void)max_seq_q;
+  check_device(q_ori, q_ori, "q");
+  TORCH_CHECK(q_ori.dim() == 3 || (q_ori.dim() == 4 && q_ori.size(1) == 1), op,
+              ": q must be [batch, 1, heads, head_size] or [batch, heads, head_size], got ",
+              q_ori.sizes());
+  const at::Tensor q = q_ori.dim() == 4 ? q_ori.select(1, 0) : q_ori;
+  TORCH_CHECK(q.size(2) <= 1 || q.stride(2) == 1, "q must have a contiguous last dim");
+  const int qdt = dtype_code(q.scalar_type());
+  TORCH_CHECK(qdt == TMO_DTYPE_F32 || qdt == TMO_DTYPE_F16 || qdt == TMO_DTYPE_BF16, op,
+              ": q must be float, half or bfloat16, got ", q.scalar_type());
+  const int64_t B = q.size(0), Hq = q.size(1), D = q.size(2);
+  const at::Tensor& vc = *v_cache;
+  check_device(k_cache, q_ori, "k_cache");
+  check_device(vc, q_ori, "v_cache");
+  TORCH_CHECK(k_cache.dim() == 4 && k_cache.is_contiguous() && vc.sizes() == k_cache.sizes() &&
+                  vc.is_contiguous() && vc.scalar_type() == k_cache.scalar_type(),
+              op, ": k_cache / v_cache must be contiguous [num_blocks, kv_heads, block_size, ",
+              "head_size] tensors of one dtype, got ", k_cache.sizes(), " and ", vc.sizes());
+  const int64_t NB = k_cache.size(0), Hkv = k_cache.size(1), BS = k_cache.size(2);
+  TORCH_CHECK(k_cache.size(3) == D, op, ": cache head_size ", k_cache.size(3), " != q's ", D);
+  TORCH_CHECK(Hkv > 0 && Hq % Hkv == 0, op, ": query heads ", Hq,
+              " must be a multiple of the KV heads ", Hkv);
+  const int cdt = dtype_code(k_cache.scalar_type());
+  const bool int8 = cdt == TMO_DTYPE_I8;
+  TORCH_CHECK(int8 == (kv_cache_quant_bit_size == 8), op,
+              ": kv_cache_quant_bit_size 8 goes with int8 caches, -1 with caches of q's dtype");
+  TORCH_CHECK(int8 || cdt == qdt, op, ": unquantised caches must have q's dtype");
+  // scales: per token [NB, Hkv, BS] (or [..., 1]), per channel [Hkv, D], per tensor [1]
+  int smode = 0;
+  at::Tensor ks, vs;
+  if (int8) {
+    TORCH_CHECK(k_cache_quant_scale.has_value() && v_cache_quant_scale.has_value(), op,
+                ": int8 caches need k_cache_quant_scale and v_cache_quant_scale");
+    auto norm = [&](const at::Tensor& sc, const char* name) -> at::Tensor {
+      check_device(sc, q_ori, name);
+      TORCH_CHECK(sc.scalar_type() == at::kFloat, name, " must be float32");
+      if ((sc.dim() == 3 || (sc.dim() == 4 && sc.size(3) == 1)) && sc.size(0) == NB &&
+          sc.size(1) == Hkv && sc.size(2) == BS) {
+        TORCH_CHECK(smode == 0 || smode == 1, op, ": K and V scales must use one mode");
+        smode = 1;
+        return sc.reshape({NB, Hkv, BS}).contiguous();
+      }
+      if (sc.dim() == 2 && sc.size(0) == Hkv && sc.size(1) == D) {
+        TORCH_CHECK(smode == 0 || smode == 2, op, ": K and V scales must use one mode");
+        smode = 2;
+        return sc.contiguous();
+      }
+      if (sc.numel() == 1) {  // per tensor: one number for every channel
+        TORCH_CHECK(smode == 0 || smode == 2, op, ": K and V scales must use one mode");
+        smode = 2;
+        return sc.reshape({1, 1}).expand({Hkv, D}).contiguous();
+      }
+      TORCH_CHECK(false, name, ": expected [num_blocks, kv_heads, block_size], [kv_heads, ",
+                  "head_size] or [1] (group-wise scales are not supported), got ", sc.sizes());
+      return sc;
+    };
+    ks = norm(*k_cache_quant_scale, "k_cache_quant_scale");
+    vs = norm(*v_cache_quant_scale, "v_cache_quant_scale");
+  }
+  check_device(block_tables, q_ori, "block_tables");
+  TORCH_CHECK(block_tables.scalar_type() == at::kInt && block_tables.dim() == 2 &&
+                  block_tables.size(0) == B && block_tables.is_contiguous(),
+              op, ": block_tables must be a contiguous int32 [batch, max_blocks] tensor, got ",
+              block_tables.sizes());
+  check_device(context_lens, q_ori, "context_lens");
+  TORCH_CHECK(context_lens.scalar_type() == at::kInt && context_lens.dim() == 1 &&
+                  context_lens.size(0) == B && context_lens.is_contiguous(),
+              op, ": context_lens must be a contiguous int32 [batch] tensor");
+  const float* alibi = nullptr;
+  if (alibi_slopes.has_value()) {
+    check_device(*alibi_slopes, q_ori, "alibi_slopes");
+    TORCH_CHECK(alibi_slopes->scalar_type() == at::kFloat && alibi_slopes->is_contiguous() &&
+                    alibi_slopes->numel() == B * Hq,
+                op, ": alibi_slopes must be a contiguous float32 [batch, heads] tensor");
+    alibi = alibi_slopes->data_ptr<float>();
+  }
+  check_device(output, q_ori, "output");
+  TORCH_CHECK(output.sizes() == q_ori.sizes() && output.scalar_type() == q.scalar_type(), op,
+              ": output must have q's shape and dtype");
+  const at::Tensor out = output.dim() == 4 ? output.select(1, 0) : output;
+  TORCH_CHECK(out.size(2) <= 1 || out.stride(2) == 1, "output must have a contiguous last dim");
+  float* lse = nullptr;
+  int64_t lse_sb = 0, lse_sh = 0;
+  if (return_lse) {
+    TORCH_CHECK(output_lse.has_value(), op, ": return_lse needs output_lse");
+    const at::Tensor& l = *output_lse;
+    check_device(l, q_ori, "output_lse");
+    TORCH_CHECK(l.scalar_type() == at::kFloat, "output_lse must be float32");
+    if (q_ori.dim() == 4) {  // [batch, heads, 1]
+      TORCH_CHECK(l.dim() == 3 && l.size(0) == B && l.size(1) == Hq && l.size(2) == 1, op,
+                  ": output_lse must be [batch, heads, 1], got ", l.sizes());
+      lse_sb = l.stride(0);
+      lse_sh = l.stride(1);
+    } else {  // [heads, total_q]
+      TORCH_CHECK(l.dim() == 2 && l.size(0) == Hq && l.size(1) == B, op,
+                  ": output_lse must be [heads, total_q], got ", l.sizes());
+      lse_sb = l.stride(1);
+      lse_sh = l.stride(0);
+    }
+    lse = l.data_ptr<float>();
+  }
+  const int64_t max_ctx = max_context_len.expect_int();
+  const int64_t window = windows_size_left.expect_int();
+  if (B == 0) return;
+  // Splits: enough workgroups for the GPU (>= ~2 per CU) when the batch alone does not give
+  // them, whole 256-token steps at least, no more than 64.
+  int64_t splits = 1;
+  const int64_t pairs = B * Hkv;
+  if (max_ctx > 0 && pairs < 1024) {
+    const int64_t want = (1024 + pairs - 1) / pairs;
+    const int64_t cap = (max_ctx + 255) / 256;
+    splits = std::max<int64_t>(1, std::min<int64_t>({want, cap, 64}));
+  }
+  c10::DeviceGuard guard(q_ori.device());
+  at::Tensor ws;
+  const int64_t ws_bytes = tmo_hip_attn_workspace_bytes(B, Hkv, Hq, D, max_ctx, splits);
+  if (ws_bytes > 0)
+    ws = at::empty({(ws_bytes + 3) / 4}, q_ori.options().dtype(at::kFloat));
+  const int st = tmo_hip_single_query_cached_kv_attn(
+      q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), vc.data_ptr(),
+      int8 ? ks.data_ptr<float>() : nullptr, int8 ? vs.data_ptr<float>() : nullptr, smode,
+      block_tables.data_ptr<int32_t>(), block_tables.size(1), context_lens.data_ptr<int32_t>(),
+      alibi, out.data_ptr(), out.stride(0), out.stride(1), lse, lse_sb, lse_sh, B, Hq, Hkv, D,
+      NB, BS, max_ctx, window, static_cast<float>(softmax_scale), qdt, cdt, splits,
+      ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(q_ori));
+  check_status(st, op);
+}
+
 }  // namespace torch_api
 }  // namespace tmo
 
@@ -976,6 +1136,14 @@ TORCH_LIBRARY(torch_mlu_ops, m) {
       "Tensor context_lengths, SymInt max_context_len, Tensor? context_seq_offset, "
       "Tensor? cache_bs_id, Tensor? cache_seq_offset, int quant_mode=0, int quant_bit=8) -> ()");
   m.def(
+      "single_query_cached_kv_attn(Tensor q_ori, Tensor k_cache, Tensor(a!) output, "
+      "Tensor block_tables, Tensor context_lens, Tensor? v_cache, Tensor(b!)? output_lse, "
+      "Tensor? q_quant_scale, Tensor? k_cache_quant_scale, Tensor? v_cache_quant_scale, "
+      "Tensor? out_quant_scale, Tensor? alibi_slopes, Tensor? mask, str compute_dtype, "
+      "SymInt max_context_len, SymInt windows_size_left, SymInt windows_size_right, "
+      "float softmax_scale, bool return_lse, int kv_cache_quant_bit_size, "
+      "Tensor? cu_seq_q=None, SymInt max_seq_q=-1, Tensor? sink=None) -> ()");
+  m.def(
       "reshape_from_cache(Tensor(a!) key, Tensor(b!)? value, Tensor key_cache, "
       "Tensor? value_cache, Tensor context_lengths, SymInt max_context_len, "
       "Tensor? context_seq_offset=None, Tensor? block_tables=None, "
@@ -994,4 +1162,5 @@ TORCH_LIBRARY_IMPL(torch_mlu_ops, CUDA, m) {
   m.impl("offline_quant_to_linear_cache", &tmo::torch_api::offline_quant_to_linear_cache);
   m.impl("dequant_from_linear_cache", &tmo::torch_api::dequant_from_linear_cache);
   m.impl("reshape_from_cache", &tmo::torch_api::reshape_from_cache);
+  m.impl("single_query_cached_kv_attn", &tmo::torch_api::single_query_cached_kv_attn);
 }

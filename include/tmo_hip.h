@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 4
+#define TMO_HIP_ABI_VERSION 5
 
 /* element types */
 enum tmo_dtype {
@@ -330,6 +330,47 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
                                int64_t max_context_len, const int32_t* context_seq_offset,
                                const int32_t* block_tables, int64_t max_blocks,
                                const int32_t* cache_seq_offset, int dtype, void* stream);
+
+/*
+ * single_query_cached_kv_attn -- decode attention of one query token per sequence over its
+ * paged KV cache: for query head hq of sequence i (KV head hk = hq / (Hq / Hkv)),
+ *   s_j = softmax_scale * q . k_j (+ alibi_slopes[i, hq] * (j - (L - 1))),
+ *   out = softmax(s) @ V,  lse = ln sum_j exp(s_j),
+ * keys j in [max(0, L - 1 - window_left), L) (all when window_left < 0), L = context_lens[i],
+ * key j at row j % block_size of page block_tables[i, j / block_size]; pages outside
+ * [0, num_blocks) are masked.  Caches [num_blocks, Hkv, block_size, head_size] contiguous:
+ * int8 (cache_dtype TMO_DTYPE_I8) with k = code * scale, scale_mode 1: per-token scales
+ * [num_blocks, Hkv, block_size], 2: per-channel [Hkv, head_size]; or of q's dtype.
+ * q / out: [batch, Hq, head_size] rows with the given strides (last dim contiguous), dtype
+ * F32, F16 or BF16; lse (nullable) fp32 at i * lse_stride_seq + hq * lse_stride_head.
+ * Arithmetic: fp32 accumulation (MFMA with bf16/f16 operands: int8 codes are exact; q and the
+ * probabilities are split into two operands when one is not exact), softmax in fp32.
+ * splits > 1 divides each sequence's keys over that many workgroups per KV head; it needs
+ * `workspace` of at least tmo_hip_attn_workspace_bytes(...) bytes (device memory).
+ * Replaces tmo::torch_api::single_query_cached_kv_attn (reference
+ * include/torch_mlu_ops.h:107-130) for one query token per sequence, without q/out
+ * quantisation, mask or sink, called by torch_mlu_ops.single_query_cached_kv_attn (reference
+ * _ops.py:777-900).
+ */
+int tmo_hip_single_query_cached_kv_attn(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+                                        const void* k_cache, const void* v_cache,
+                                        const float* k_scale, const float* v_scale,
+                                        int scale_mode, const int32_t* block_tables,
+                                        int64_t max_blocks, const int32_t* context_lens,
+                                        const float* alibi_slopes, void* out,
+                                        int64_t out_stride_seq, int64_t out_stride_head,
+                                        float* lse, int64_t lse_stride_seq,
+                                        int64_t lse_stride_head, int64_t batch,
+                                        int64_t num_q_heads, int64_t num_kv_heads,
+                                        int64_t head_size, int64_t num_blocks,
+                                        int64_t block_size, int64_t max_context_len,
+                                        int64_t window_left, float softmax_scale, int q_dtype,
+                                        int cache_dtype, int64_t splits, void* workspace,
+                                        int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes tmo_hip_single_query_cached_kv_attn needs for `splits` (0 when splits <= 1). */
+int64_t tmo_hip_attn_workspace_bytes(int64_t batch, int64_t num_kv_heads, int64_t num_q_heads,
+                                     int64_t head_size, int64_t max_context_len, int64_t splits);
 
 #ifdef __cplusplus
 }

@@ -179,6 +179,31 @@ void reshape_from_cache(at::Tensor &key,
                         const c10::optional<at::Tensor> &block_tables,
                         const c10::optional<at::Tensor> &cache_seq_offset);
 
+/* reference include/torch_mlu_ops.h:107-130 */
+void single_query_cached_kv_attn(const torch::Tensor &q_ori,
+                                 const torch::Tensor &k_cache,
+                                 const torch::Tensor &output,
+                                 const torch::Tensor &block_tables,
+                                 const torch::Tensor &context_lens,
+                                 const c10::optional<torch::Tensor> &v_cache,
+                                 const c10::optional<torch::Tensor> &output_lse,
+                                 const c10::optional<torch::Tensor> &q_quant_scale,
+                                 const c10::optional<torch::Tensor> &k_cache_quant_scale,
+                                 const c10::optional<torch::Tensor> &v_cache_quant_scale,
+                                 const c10::optional<torch::Tensor> &out_quant_scale,
+                                 const c10::optional<torch::Tensor> &alibi_slopes,
+                                 const c10::optional<torch::Tensor> &mask,
+                                 const std::string &compute_dtype,
+                                 c10::SymInt max_context_len,
+                                 c10::SymInt windows_size_left,
+                                 c10::SymInt windows_size_right,
+                                 double softmax_scale,
+                                 bool return_lse,
+                                 int64_t kv_cache_quant_bit_size,
+                                 const c10::optional<torch::Tensor> &cu_seq_q = c10::nullopt,
+                                 c10::SymInt max_seq_q = -1,
+                                 const c10::optional<torch::Tensor> &sink = c10::nullopt);
+
 }  // namespace torch_api
 }  // namespace tmo
 

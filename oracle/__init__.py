@@ -63,6 +63,12 @@ def lib() -> ctypes.CDLL:
             [c_float, c_float, c_int, c_int64, c_void_p, c_int64, c_int64, c_int, c_int64] + \
             [c_void_p] * 4 + [c_int64, c_int]
         L.oracle_linear_cache.restype = c_int
+        c_double = ctypes.c_double
+        L.oracle_single_query_attn.argtypes = [c_void_p, c_int, c_int64, c_int64, c_void_p,
+                                               c_void_p, c_int] + [c_int64] * 4 + \
+            [c_void_p, c_void_p, c_int, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p,
+             c_int64, c_double, c_void_p, c_void_p, c_int]
+        L.oracle_single_query_attn.restype = c_int
         for name in ("oracle_f32_to_bf16", "oracle_f32_to_f16", "oracle_f16_to_f32",
                      "oracle_f32_to_e4m3"):
             getattr(L, name).argtypes = [c_void_p, c_void_p, c_int64]
@@ -220,6 +226,40 @@ def linear_cache(op: int, key, value, key_cache, value_cache, context_lengths, m
         int(bool(packed)), pad, _ptr(cso), _ptr(bsi), _ptr(coff), _ptr(bt),
         bt.shape[1] if bt is not None else 0, nthreads or default_threads())
     _check(rc, "linear_cache")
+
+
+def single_query_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scale: float,
+                      k_scale=None, v_scale=None, alibi_slopes=None, window_left: int = -1,
+                      nthreads: Optional[int] = None):
+    """reference _ops.py:777-900 for one query token per sequence (decision D12 of
+    tmo_oracle.c), in float64.  q [B, Hq, D] or [B, 1, Hq, D]; caches [NB, Hkv, BS, D] (int8
+    with k_scale/v_scale [NB, Hkv, BS] per token or [Hkv, D] per channel, or float);
+    block_tables [B, max_blocks]; returns (out [B, Hq, D] float64, lse [B, Hq] float64)."""
+    if q.dim() == 4:
+        assert q.shape[1] == 1
+        q = q[:, 0]
+    assert q.stride(-1) == 1 and k_cache.is_contiguous() and v_cache.is_contiguous()
+    B, Hq, D = q.shape
+    NB, Hkv, BS, _ = k_cache.shape
+    cdt = _DT[k_cache.dtype]
+    mode = 0
+    ks = vs = None
+    if k_cache.dtype == torch.int8:
+        ks = k_scale.to(torch.float32).contiguous()
+        vs = v_scale.to(torch.float32).contiguous()
+        mode = 2 if ks.dim() == 2 else 1
+    bt = block_tables.to(torch.int32).contiguous()
+    lens = context_lens.to(torch.int32).contiguous()
+    al = alibi_slopes.to(torch.float32).contiguous() if alibi_slopes is not None else None
+    out = torch.empty((B, Hq, D), dtype=torch.float64)
+    lse = torch.empty((B, Hq), dtype=torch.float64)
+    rc = lib().oracle_single_query_attn(
+        _ptr(q), _DT[q.dtype], q.stride(0), q.stride(1), _ptr(k_cache), _ptr(v_cache), cdt,
+        NB, Hkv, BS, D, _ptr(ks), _ptr(vs), mode, _ptr(bt), bt.shape[1], _ptr(lens), B, Hq,
+        _ptr(al), int(window_left), float(softmax_scale), _ptr(out), _ptr(lse),
+        nthreads or default_threads())
+    _check(rc, "single_query_attn")
+    return out, lse
 
 
 def reshape_paged_cache(k, v, k_cache, v_cache, slot_mapping, direction: bool = False,

@@ -88,6 +88,18 @@ REFERENCE_SIGNATURES = {
                                   ("max_context_len", None), ("context_seq_offset", None),
                                   ("cache_bs_id", None), ("cache_seq_offset", None),
                                   ("quant_mode", 0), ("quant_bit", 8)],
+    # _ops.py:777-801
+    "single_query_cached_kv_attn": [("q", None), ("k_cache", None), ("v_cache", None),
+                                    ("out", None), ("block_tables", None),
+                                    ("context_lens", None), ("k_cache_quant_scale", None),
+                                    ("v_cache_quant_scale", None), ("alibi_slopes", None),
+                                    ("max_context_len", None), ("windows_size_left", None),
+                                    ("windows_size_right", None), ("softmax_scale", None),
+                                    ("return_lse", False), ("kv_cache_quant_bit_size", -1),
+                                    ("q_quant_scale", None), ("out_quant_scale", None),
+                                    ("out_dtype", torch.half), ("compute_dtype", torch.float),
+                                    ("head_size_v", -1), ("mask", None), ("cu_seq_q", None),
+                                    ("max_seq_q", -1), ("sink", None)],
     # _ops.py:3898-3906
     "reshape_from_cache": [("key", None), ("value", None), ("key_cache", None),
                            ("value_cache", None), ("context_lengths", None),
@@ -122,6 +134,7 @@ WRITES = {
     "offline_quant_to_linear_cache": {"key_cache", "value_cache"},
     "dequant_from_linear_cache": {"key", "value"},
     "reshape_from_cache": {"key", "value"},
+    "single_query_cached_kv_attn": {"output", "output_lse"},
 }
 
 
@@ -193,6 +206,22 @@ def test_linear_fakes_run_on_meta_tensors(tmo):
     assert tmo.dequant_from_linear_cache(key, None, kc, None, ks, None, lens, 16, None, None,
                                          None, 1, 8) is None
     assert tmo.reshape_from_cache(key, key, kb, kb, lens, 16) is None
+
+
+def test_attention_fake_returns_the_reference_shapes(tmo):
+    m = dict(device="meta")
+    q = torch.empty(4, 1, 32, 128, dtype=torch.bfloat16, **m)
+    kc = torch.empty(64, 8, 16, 128, dtype=torch.int8, **m)
+    ks = torch.empty(64, 8, 16, **m)
+    bt = torch.empty(4, 8, dtype=torch.int32, **m)
+    lens = torch.empty(4, dtype=torch.int32, **m)
+    out, lse = tmo.single_query_cached_kv_attn(q, kc, kc, None, bt, lens, ks, ks, None, 128, -1,
+                                               -1, 0.088, True, 8)
+    assert out.shape == q.shape and out.dtype == torch.bfloat16 and lse.shape == (4, 32, 1)
+    q3 = torch.empty(4, 32, 128, dtype=torch.float16, **m)
+    out = tmo.single_query_cached_kv_attn(q3, kc, kc, None, bt, lens, ks, ks, None, 128, -1, -1,
+                                          0.088, False, 8)
+    assert out.shape == q3.shape and out.dtype == torch.float16
 
 
 def test_fake_tensor_mode(tmo):

@@ -18,7 +18,8 @@ FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails val
 
 def declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(tmo_hip_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(tmo_hip_\w+)\s*\(",
+                                 text, re.M)))
 
 
 def header_enum(name):
@@ -50,6 +51,11 @@ def lib():
         [P, I64, I64, P, P, P, INT, INT, INT, P]
     L.tmo_hip_reshape_from_cache.argtypes = [P, P] + [I64] * 5 + [P, P] + [I64] * 4 + \
         [P, I64, I64, P, P, I64, P, INT, P]
+    L.tmo_hip_single_query_cached_kv_attn.argtypes = [P, I64, I64, P, P, P, P, INT, P, I64, P, P,
+                                                      P, I64, I64, P, I64, I64] + [I64] * 8 + \
+        [ctypes.c_float, INT, INT, I64, P, I64, P]
+    L.tmo_hip_attn_workspace_bytes.argtypes = [I64] * 6
+    L.tmo_hip_attn_workspace_bytes.restype = I64
     return L
 
 
@@ -61,7 +67,8 @@ def test_every_declared_symbol_is_exported(lib):
                           "tmo_hip_offline_quant_to_paged_cache", "tmo_hip_fused_rope_paged",
                           "tmo_hip_reshape_linear_cache", "tmo_hip_quant_to_linear_cache",
                           "tmo_hip_offline_quant_to_linear_cache",
-                          "tmo_hip_dequant_from_linear_cache", "tmo_hip_reshape_from_cache"}
+                          "tmo_hip_dequant_from_linear_cache", "tmo_hip_reshape_from_cache",
+                          "tmo_hip_single_query_cached_kv_attn", "tmo_hip_attn_workspace_bytes"}
     for n in names:
         assert hasattr(lib, n), n
 
@@ -240,4 +247,27 @@ def test_linear_read_validation(lib):
     assert rfc(value=FAKE) == EINVAL
     assert rfc(bt=FAKE, mb=0) == EINVAL                          # a table needs columns
     assert rfc(B=0) == 0 and rfc(NB=0) == 0
+
+
+def test_attention_validation(lib):
+    def call(q=FAKE, kc=FAKE, vc=FAKE, ks=FAKE, vs=FAKE, smode=1, bt=FAKE, lens=FAKE, out=FAKE,
+             B=2, Hq=8, Hkv=2, D=128, NB=16, BS=16, qdt=2, cdt=3, splits=1, ws=None, wsb=0):
+        return lib.tmo_hip_single_query_cached_kv_attn(
+            q, 1024, 128, kc, vc, ks, vs, smode, bt, 4, lens, None, out, 1024, 128, None, 0, 0,
+            B, Hq, Hkv, D, NB, BS, 64, -1, 0.1, qdt, cdt, splits, ws, wsb, None)
+    assert call(qdt=3) == EDTYPE                   # int8 q
+    assert call(cdt=1) == EDTYPE                   # fp16 cache with bf16 q
+    assert call(smode=0) == EMODE                  # int8 cache without a scale mode
+    assert call(q=None) == EINVAL
+    assert call(ks=None) == EINVAL
+    assert call(Hq=7) == EINVAL                    # not a multiple of the KV heads
+    assert call(D=600) == EINVAL
+    assert call(BS=0) == EINVAL
+    assert call(splits=0) == EINVAL
+    assert call(splits=4) == EINVAL                # splits without a workspace
+    need = lib.tmo_hip_attn_workspace_bytes(2, 2, 8, 128, 64, 4)
+    assert need == 2 * 2 * 4 * 4 * 130 * 4
+    assert lib.tmo_hip_attn_workspace_bytes(2, 2, 8, 128, 64, 1) == 0
+    assert call(splits=4, ws=FAKE, wsb=need - 4) == EINVAL
+    assert call(B=0) == 0
 

@@ -960,3 +960,92 @@ def test_linear_max_context_len_truncates(ref):
                      context_seq_offset=case.context_seq_offset, cache_bs_id=case.cache_bs_id,
                      cache_seq_offset=case.cache_seq_offset)
     assert torch.equal(bits(kc), bits(wk)) and torch.equal(bits(vc), bits(wv))
+
+
+# ---------------------------------------------------------------------------- decode attention (D12)
+
+def torch_attn(case, scale, window=-1):
+    """_ops.py:786-800 in float64 by torch: gather each sequence's keys through its block table,
+    dequantise (code * scale), repeat KV heads over their query-head group, softmax, @ V."""
+    q, kc, vc = case.q.double(), case.k_cache, case.v_cache
+    B, Hq, D = q.shape
+    NB, Hkv, BS, _ = kc.shape
+    g = Hq // Hkv
+    out = torch.zeros(B, Hq, D, dtype=torch.float64)
+    lse = torch.full((B, Hq), float("-inf"), dtype=torch.float64)
+    for i in range(B):
+        L = int(case.context_lens[i])
+        j = torch.arange(L)
+        if window >= 0:
+            j = j[j >= L - 1 - window]
+        blk = case.block_tables[i, j // BS].long()
+        row = j % BS
+        keep = (blk >= 0) & (blk < NB)
+        j, blk, row = j[keep], blk[keep], row[keep]
+        if j.numel() == 0:
+            continue
+        K, V = kc[blk, :, row].double(), vc[blk, :, row].double()        # [n, Hkv, D]
+        if case.k_scale is not None:
+            if case.k_scale.dim() == 3:
+                K = K * case.k_scale[blk, :, row].double()[..., None]
+                V = V * case.v_scale[blk, :, row].double()[..., None]
+            else:
+                K = K * case.k_scale.double()[None]
+                V = V * case.v_scale.double()[None]
+        K, V = K.repeat_interleave(g, dim=1), V.repeat_interleave(g, dim=1)  # [n, Hq, D]
+        s = (K * q[i][None]).sum(-1).transpose(0, 1) * scale                 # [Hq, n]
+        if case.alibi is not None:
+            s = s + case.alibi[i].double()[:, None] * (j - (L - 1)).double()[None, :]
+        p = torch.softmax(s, dim=-1)
+        out[i] = (p[:, :, None] * V.transpose(0, 1)).sum(1)
+        lse[i] = torch.logsumexp(s, dim=-1)
+    return out, lse
+
+
+@pytest.mark.parametrize("kv", ["int8_token", "int8_channel", "plain"])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_attn_matches_torch_float64(ref, dtype, kv):
+    case = W.attn_case(dtype, 3, kv=kv, Hq=8, Hkv=2, D=64, max_ctx=70)
+    case.block_tables[2, 1] = -1                     # a missing page: its keys are masked
+    for window, alibi in ((-1, False), (9, False), (-1, True)):
+        case.alibi = (0.5 ** torch.arange(1, 9, dtype=torch.float32)).repeat(5, 1) if alibi else None
+        out, lse = ref.single_query_attn(case.q, case.k_cache, case.v_cache, case.block_tables,
+                                         case.context_lens, 0.125, case.k_scale, case.v_scale,
+                                         case.alibi, window)
+        want, wlse = torch_attn(case, 0.125, window)
+        assert torch.allclose(out, want, rtol=1e-12, atol=1e-12)
+        assert torch.allclose(lse, wlse, rtol=1e-12, atol=1e-12)
+
+
+def test_attn_closed_forms(ref):
+    """One key: out = that key's value row exactly, lse = its logit.  A window of 0: the last
+    key's value.  Identical keys: the mean of the value rows.  A dominant ALiBi slope: the last
+    value row."""
+    case = W.attn_case(torch.bfloat16, 4, kv="int8_token", B=3, Hq=4, Hkv=4, D=32, max_ctx=40)
+    NB, Hkv, BS, D = case.k_cache.shape
+    out, lse = ref.single_query_attn(case.q, case.k_cache, case.v_cache, case.block_tables,
+                                     case.context_lens, 0.3, case.k_scale, case.v_scale)
+    blk = int(case.block_tables[1, 0])                               # sequence 1 has one key
+    v0 = case.v_cache[blk, :, 0].double() * case.v_scale[blk, :, 0].double()[:, None]
+    assert torch.equal(out[1], v0)
+    k0 = case.k_cache[blk, :, 0].double() * case.k_scale[blk, :, 0].double()[:, None]
+    assert torch.allclose(lse[1], 0.3 * (case.q[1].double() * k0).sum(-1), rtol=1e-14)
+    out, _ = ref.single_query_attn(case.q, case.k_cache, case.v_cache, case.block_tables,
+                                   case.context_lens, 0.3, case.k_scale, case.v_scale,
+                                   window_left=0)
+    L = int(case.context_lens[0])
+    blk, row = int(case.block_tables[0, (L - 1) // BS]), (L - 1) % BS
+    vl = case.v_cache[blk, :, row].double() * case.v_scale[blk, :, row].double()[:, None]
+    assert torch.equal(out[0], vl)
+    same = W.attn_case(torch.float32, 5, kv="plain", B=1, Hq=2, Hkv=1, D=16, max_ctx=33)
+    same.k_cache[:] = same.k_cache[0, :, 0][None, :, None, :]
+    out, _ = ref.single_query_attn(same.q, same.k_cache, same.v_cache, same.block_tables,
+                                   same.context_lens, 1.0)
+    bt = same.block_tables[0]
+    j = torch.arange(33)
+    V = same.v_cache[bt[j // 16].long(), :, j % 16].double()          # [33, 1, 16]
+    assert torch.allclose(out[0], V.mean(0).expand(2, 16), rtol=1e-13, atol=1e-15)
+    al = torch.full((1, 2), 1e4)
+    out, _ = ref.single_query_attn(same.q, same.k_cache, same.v_cache, same.block_tables,
+                                   same.context_lens, 1.0, alibi_slopes=al)
+    assert torch.allclose(out[0], V[-1].expand(2, 16), rtol=0, atol=1e-300)

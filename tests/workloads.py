@@ -331,3 +331,50 @@ def linear_case(dtype, seed: int, packed: bool = True, offsets: bool = False, B:
         if B > 2:
             coff[2] = cache_len - max(1, int(lens[2]) // 2)     # runs past the cache's end
     return LinearCase(key, value, lens, packed, cso, bsi, coff, cache_batch, cache_len)
+
+
+@dataclass
+class AttnCase:
+    """Inputs of single_query_cached_kv_attn for one query token per sequence (CPU)."""
+    q: torch.Tensor                  # [B, Hq, D]
+    k_cache: torch.Tensor            # [NB, Hkv, BS, D]
+    v_cache: torch.Tensor
+    k_scale: Optional[torch.Tensor]  # int8 caches: [NB, Hkv, BS] per token or [Hkv, D] per channel
+    v_scale: Optional[torch.Tensor]
+    block_tables: torch.Tensor       # [B, max_blocks] int32
+    context_lens: torch.Tensor       # [B] int32
+    alibi: Optional[torch.Tensor] = None
+
+    @property
+    def max_context_len(self) -> int:
+        return int(self.context_lens.max()) if self.context_lens.numel() else 0
+
+
+def attn_case(dtype, seed: int, kv: str = "int8_token", B: int = 5, Hq: int = 8, Hkv: int = 2,
+              D: int = 128, BS: int = 16, NB: int = 64, max_ctx: int = 200,
+              alibi: bool = False) -> AttnCase:
+    """Decode attention inputs: q ~ N(0, 1) in `dtype`; caches int8 (`kv` "int8_token" /
+    "int8_channel", codes uniform in [-127, 127] with scales ~U[0.005, 0.03)) or of q's dtype
+    (`kv` "plain", N(0, 1)); context lengths in [1, max_ctx] (the first max_ctx, one 1); each
+    sequence's pages a random choice of distinct blocks."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, D, generator=g).to(dtype)
+    lens = torch.randint(1, max_ctx + 1, (B,), generator=g).to(torch.int32)
+    lens[0] = max_ctx
+    if B > 1:
+        lens[1] = 1
+    MB = (max_ctx + BS - 1) // BS
+    assert B * MB <= NB, "not enough blocks for distinct pages"
+    bt = torch.randperm(NB, generator=g)[:B * MB].reshape(B, MB).to(torch.int32)
+    ks = vs = None
+    if kv.startswith("int8"):
+        kc = torch.randint(-127, 128, (NB, Hkv, BS, D), generator=g, dtype=torch.int8)
+        vc = torch.randint(-127, 128, (NB, Hkv, BS, D), generator=g, dtype=torch.int8)
+        shape = (NB, Hkv, BS) if kv == "int8_token" else (Hkv, D)
+        ks = 0.005 + 0.025 * torch.rand(shape, generator=g)
+        vs = 0.005 + 0.025 * torch.rand(shape, generator=g)
+    else:
+        kc = torch.randn(NB, Hkv, BS, D, generator=g).to(dtype)
+        vc = torch.randn(NB, Hkv, BS, D, generator=g).to(dtype)
+    al = (0.5 ** torch.arange(1, Hq + 1, dtype=torch.float32)).repeat(B, 1) if alibi else None
+    return AttnCase(q, kc, vc, ks, vs, bt, lens, al)
