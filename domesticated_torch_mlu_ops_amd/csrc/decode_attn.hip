@@ -42,6 +42,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazy = 8.0f;  // log2 headroom of the lazily moved softmax maximum
 constexpr float kLn2 = 0.6931471805599453f;
 
 struct AttnParams {
@@ -63,6 +64,7 @@ struct AttnParams {
   float* lse;                    // null when not requested
   int64_t lse_sb, lse_sh;
   int32_t B, Hq, Hkv, g, D, BS;
+  int32_t bs_shift;              // log2(BS) when BS is a power of two, else -1
   int64_t NB;
   int32_t q_dtype;               // TMO_DTYPE_*
   int32_t c_dtype;               // cache TMO_DTYPE_*
@@ -203,153 +205,215 @@ __global__ __launch_bounds__(256) void attn_mfma(AttnParams p) {
 #pragma unroll
   for (int j = 0; j < kDV; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int64_t first_tile = rg.begin >> 4;
-  const int64_t end_tile = (rg.end + 15) >> 4;
+  // token positions fit in 32 bits (context lengths are int32)
+  const int32_t begin32 = (int32_t)rg.begin, end32 = (int32_t)rg.end, last32 = (int32_t)(rg.L - 1);
+  const int32_t first_tile = (int32_t)(rg.begin >> 4);
+  const int32_t end_tile = (int32_t)((rg.end + 15) >> 4);
+  const int32_t* bt_row = p.bt + i * p.max_blocks;
   const char* kbase = static_cast<const char*>(p.kc);
   const char* vbase = static_cast<const char*>(p.vc);
   const int64_t page_bytes = (int64_t)p.BS * kD * kEs;      // one head's page
-  for (int64_t tile = first_tile + wave; tile < end_tile; tile += 4) {
-    const int64_t t0 = tile * 16;
-    const int64_t blk = p.bt[i * p.max_blocks + t0 / p.BS];
-    if (blk < 0 || blk >= p.NB) continue;                  // missing page: its keys are masked
-    const int64_t row0 = t0 % p.BS;
-    const int64_t head_off = (blk * p.Hkv + hk) * page_bytes;
-    // K: token `col`, channels grp * kDC ..; V: tokens 4 grp .. + 3, channels col * kDV ..
-    const char* krow = kbase + head_off + (row0 + col) * kD * kEs + grp * kDC * kEs;
-    uint32_t kw[kDC * kEs / 4];
+  // per-lane offsets inside a 16-row piece of a page: K token `col`, channels grp * kDC ..;
+  // V tokens 4 grp .. + 3, channels col * kDV ..
+  const int32_t k_lane = col * kD * kEs + grp * kDC * kEs;
+  const int32_t v_lane = 4 * grp * kD * kEs + col * kDV * kEs;
+  constexpr int kKW = kDC * kEs / 4, kVW = kDV * kEs / 4;   // dwords per lane
+
+  // Raw tile: this lane's K piece, its V pieces of four tokens, the per-token scales.
+  struct Raw {
+    uint32_t kw[kKW];
+    uint32_t vw[4][kVW];
+    float ksc[4], vsc[4];
+  };
+  auto page_of = [&](int32_t tl) -> int32_t {
+    const int32_t t0 = tl * 16;
+    return p.bs_shift >= 0 ? t0 >> p.bs_shift : t0 / p.BS;
+  };
+  auto load_tile = [&](Raw& r, int32_t tl, int64_t blk) {
+    const int32_t t0 = tl * 16;
+    const int32_t row0 = t0 - page_of(tl) * p.BS;
+    const int64_t piece = (blk * p.Hkv + hk) * page_bytes + (int64_t)row0 * kD * kEs;
+    const char* krow = kbase + piece + k_lane;
 #pragma unroll
-    for (int u = 0; u < kDC * kEs / 16; ++u) {
+    for (int u = 0; u < kKW / 4; ++u) {
       const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(krow) + u);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) kw[4 * u + e] = w[e];
+      for (int e = 0; e < 4; ++e) r.kw[4 * u + e] = w[e];
     }
-    uint32_t vw[4][kDV * kEs / 4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const char* vrow = vbase + head_off + (row0 + 4 * grp + e) * kD * kEs + col * kDV * kEs;
-      if constexpr (kDV * kEs == 16) {
+      const char* vrow = vbase + piece + v_lane + e * kD * kEs;
+      if constexpr (kVW == 4) {
         const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vrow));
 #pragma unroll
-        for (int u = 0; u < 4; ++u) vw[e][u] = w[u];
-      } else if constexpr (kDV * kEs == 8) {
+        for (int u = 0; u < 4; ++u) r.vw[e][u] = w[u];
+      } else if constexpr (kVW == 2) {
         const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vrow));
-        vw[e][0] = w[0];
-        vw[e][1] = w[1];
-      } else if constexpr (kDV * kEs == 4) {
-        vw[e][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vrow));
+        r.vw[e][0] = w[0];
+        r.vw[e][1] = w[1];
+      } else if constexpr (kVW == 1) {
+        r.vw[e][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vrow));
       } else {  // 32 bytes
         const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vrow));
         const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vrow) + 1);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          vw[e][u] = a[u];
-          vw[e][4 + u] = b[u];
+          r.vw[e][u] = a[u];
+          r.vw[e][4 + u] = b[u];
         }
       }
     }
-    float ksc[4] = {1.0f, 1.0f, 1.0f, 1.0f}, vsc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r.ksc[e] = r.vsc[e] = 1.0f;
     if (kKind == 0 && p.smode == 1) {
       const int64_t so = (blk * p.Hkv + hk) * p.BS + row0 + 4 * grp;
       const u32x4 a = *reinterpret_cast<const u32x4*>(p.ks + so);
       const u32x4 b = *reinterpret_cast<const u32x4*>(p.vs + so);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        ksc[e] = __uint_as_float(a[e]);
-        vsc[e] = __uint_as_float(b[e]);
+        r.ksc[e] = __uint_as_float(a[e]);
+        r.vsc[e] = __uint_as_float(b[e]);
       }
     }
+  };
 
-    // ---- S^T = K Q^T
-    f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+  // The wave's tiles are first_tile + wave + 4n.  Lane l holds the block of the window's
+  // tile n = l (64 tiles per refill), read per tile with v_readlane; each tile's loads are
+  // issued one iteration before its arithmetic.
+  int32_t lane_blk = -1;
+  int32_t win_base = first_tile + wave;
+  auto refill = [&]() {
+    const int32_t tl = win_base + 4 * lane;
+    lane_blk = tl < end_tile ? bt_row[page_of(tl)] : -1;
+  };
+  refill();
+  // Arithmetic of one loaded tile (the whole wavefront: the MFMAs need every lane).
+  auto compute_tile = [&](const Raw& r, int32_t tile) {
+      const int32_t t0 = tile * 16;
+      // ---- S^T = K Q^T
+      f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int m = 0; m < kQK; ++m) {
-      V4 a;
-      if constexpr (kKind == 0) {
-        a = codes_bf16(kw[m]);
-      } else {
-        const uint32_t w0 = kw[2 * m], w1 = kw[2 * m + 1];
-        typedef short s4 __attribute__((ext_vector_type(4)));
-        s4 b4;
-        b4[0] = (short)(w0 & 0xffffu);
-        b4[1] = (short)(w0 >> 16);
-        b4[2] = (short)(w1 & 0xffffu);
-        b4[3] = (short)(w1 >> 16);
-        a = __builtin_bit_cast(V4, b4);
-      }
-      s = M::run(a, qhi[m], s);
-      if constexpr (kQLo) s = M::run(a, qlo[m], s);
-    }
-
-    // ---- scores (base 2), masking, online softmax
-    float sc[4];
-    float tmax = -__builtin_inff();
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int64_t j = t0 + 4 * grp + e;
-      float v = s[e] * ksc[e] * p.scale_log2;
-      if (p.alibi) v += alibi * (float)(j - (rg.L - 1));
-      if (j < rg.begin || j >= rg.end || !qvalid) v = -__builtin_inff();
-      sc[e] = v;
-      tmax = fmaxf(tmax, v);
-    }
-    tmax = col_max(tmax);
-    // no branch on the column's state: the MFMAs below need the whole wavefront
-    const float mnew = fmaxf(mrun, tmax);
-    const bool live = mnew != -__builtin_inff();            // some key of this column so far
-    const float corr = live ? __builtin_amdgcn_exp2f(mrun - mnew) : 1.0f;  // mrun = -inf -> 0
-    mrun = mnew;
-    float pe[4];
-    float psum = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      pe[e] = live ? __builtin_amdgcn_exp2f(sc[e] - mnew) : 0.0f;  // masked: -inf -> 0
-      psum += pe[e];
-    }
-    lpart = lpart * corr + psum;
-    if (__ballot(corr != 1.0f)) {
-#pragma unroll
-      for (int j = 0; j < kDV; ++j) acc[j] *= corr;
-    }
-
-    // ---- P^T operands (hi + lo) with the per-token V scale folded in
-    V4 phi, plo;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float pv = pe[e] * vsc[e];
-      if constexpr (kF16) {
-        const _Float16 h = (_Float16)pv;
-        phi[e] = h;
-        plo[e] = (_Float16)(pv - (float)h);
-      } else {
-        const short hb = M::bits(pv);
-        phi[e] = hb;
-        plo[e] = M::bits(pv - M::value(hb));
-      }
-    }
-
-    // ---- O^T += V^T P^T: MFMA j takes channel col * kDV + j of tokens 4 grp .. + 3
-#pragma unroll
-    for (int j = 0; j < kDV; ++j) {
-      V4 a;
-      if constexpr (kKind == 0) {
-        typedef short s4 __attribute__((ext_vector_type(4)));
-        s4 b4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int8_t code = (int8_t)(vw[e][j >> 2] >> (8 * (j & 3)));
-          b4[e] = (short)(__float_as_uint((float)code) >> 16);
+      for (int m = 0; m < kQK; ++m) {
+        V4 a;
+        if constexpr (kKind == 0) {
+          a = codes_bf16(r.kw[m]);
+        } else {
+          const uint32_t w0 = r.kw[2 * m], w1 = r.kw[2 * m + 1];
+          typedef short s4 __attribute__((ext_vector_type(4)));
+          s4 b4;
+          b4[0] = (short)(w0 & 0xffffu);
+          b4[1] = (short)(w0 >> 16);
+          b4[2] = (short)(w1 & 0xffffu);
+          b4[3] = (short)(w1 >> 16);
+          a = __builtin_bit_cast(V4, b4);
         }
-        a = __builtin_bit_cast(V4, b4);
-      } else {
+        s = M::run(a, qhi[m], s);
+        if constexpr (kQLo) s = M::run(a, qlo[m], s);
+      }
+
+      // ---- scores (base 2), masking, online softmax
+      float sc[4];
+      float tmax = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int32_t j = t0 + 4 * grp + e;
+        float v = s[e] * r.ksc[e] * p.scale_log2;
+        if (p.alibi) v += alibi * (float)(j - last32);
+        if (j < begin32 || j >= end32 || !qvalid) v = -__builtin_inff();
+        sc[e] = v;
+        tmax = fmaxf(tmax, v);
+      }
+      tmax = col_max(tmax);
+      // No branch on the column's state: the MFMAs below need the whole wavefront.  The
+      // reference maximum moves only when a score exceeds it by more than kLazy (base 2), so
+      // the probabilities stay below 2^kLazy and the accumulators are rarely rescaled; the
+      // first finite score sets it.
+      const bool was_empty = mrun == -__builtin_inff();
+      const bool raise = tmax > mrun + kLazy || (was_empty && tmax != -__builtin_inff());
+      const float mnew = raise ? tmax : mrun;
+      const bool live = mnew != -__builtin_inff();          // some key of this column so far
+      const float corr = raise ? __builtin_amdgcn_exp2f(mrun - mnew) : 1.0f;  // -inf -> 0
+      mrun = mnew;
+      float pe[4];
+      float psum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pe[e] = live ? __builtin_amdgcn_exp2f(sc[e] - mnew) : 0.0f;  // masked: -inf -> 0
+        psum += pe[e];
+      }
+      lpart = lpart * corr + psum;
+      if (__ballot(corr != 1.0f && !was_empty)) {  // an empty column's accumulators are zero
+#pragma unroll
+        for (int j = 0; j < kDV; ++j) acc[j] *= corr;
+      }
+
+      // ---- P^T operands (hi + lo) with the per-token V scale folded in
+      V4 phi, plo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float pv = pe[e] * r.vsc[e];
+        if constexpr (kF16) {
+          const _Float16 h = (_Float16)pv;
+          phi[e] = h;
+          plo[e] = (_Float16)(pv - (float)h);
+        } else {
+          const short hb = M::bits(pv);
+          phi[e] = hb;
+          plo[e] = M::bits(pv - M::value(hb));
+        }
+      }
+
+      // ---- O^T += V^T P^T: MFMA j takes channel col * kDV + j of tokens 4 grp .. + 3
+#pragma unroll
+      for (int j = 0; j < kDV; ++j) {
         typedef short s4 __attribute__((ext_vector_type(4)));
         s4 b4;
+        if constexpr (kKind == 0) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) b4[e] = (short)(vw[e][j >> 1] >> (16 * (j & 1)));
-        a = __builtin_bit_cast(V4, b4);
+          for (int e = 0; e < 4; ++e) {
+            const int8_t code = (int8_t)(r.vw[e][j >> 2] >> (8 * (j & 3)));
+            b4[e] = (short)(__float_as_uint((float)code) >> 16);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) b4[e] = (short)(r.vw[e][j >> 1] >> (16 * (j & 1)));
+        }
+        const V4 a = __builtin_bit_cast(V4, b4);
+        acc[j] = M::run(a, phi, acc[j]);
+        acc[j] = M::run(a, plo, acc[j]);
       }
-      acc[j] = M::run(a, phi, acc[j]);
-      acc[j] = M::run(a, plo, acc[j]);
+  };
+
+  // Two register sets alternate: while one tile is computed the next one's loads are in
+  // flight (no copies between the sets).
+  int32_t slot = 0;  // index in the window of the most recently loaded tile
+  Raw ra, rb;
+  int32_t tile = first_tile + wave;
+  auto try_load = [&](Raw& r, int32_t tl) -> bool {
+    if (tl >= end_tile) return false;
+    const int64_t blk = __builtin_amdgcn_readlane(lane_blk, slot);
+    if (blk < 0 || blk >= p.NB) return false;               // missing page: keys masked
+    load_tile(r, tl, blk);
+    return true;
+  };
+  auto advance = [&]() {
+    if (++slot == kWave) {
+      win_base += 4 * kWave;
+      refill();
+      slot = 0;
     }
+  };
+  bool ok_a = try_load(ra, tile);
+  while (tile < end_tile) {
+    advance();
+    const bool ok_b = try_load(rb, tile + 4);
+    if (ok_a) compute_tile(ra, tile);
+    tile += 4;
+    if (tile >= end_tile) break;
+    advance();
+    ok_a = try_load(ra, tile + 4);
+    if (ok_b) compute_tile(rb, tile);
+    tile += 4;
   }
 
   // ---- combine the four wavefronts: waves 1..3 leave (max, sum, accumulators) in LDS in
@@ -625,6 +689,7 @@ extern "C" int tmo_hip_single_query_cached_kv_attn(
   p.g = (int32_t)(num_q_heads / num_kv_heads);
   p.D = (int32_t)head_size;
   p.BS = (int32_t)block_size;
+  p.bs_shift = ilog2_if_pow2(block_size);
   p.NB = num_blocks;
   p.q_dtype = q_dtype;
   p.ws = static_cast<float*>(workspace);
