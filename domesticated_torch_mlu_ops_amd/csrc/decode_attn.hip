@@ -148,18 +148,27 @@ struct Mfma<true> {  // f16 operands
   }
 };
 
-// Four int8 codes (one dword) -> four exact bf16 operands.
-__device__ __forceinline__ bf16x4 codes_bf16(uint32_t w) {
-  bf16x4 r;
-#pragma unroll
-  for (int e = 0; e < 4; ++e)
-    r[e] = (short)(__float_as_uint((float)(int8_t)(w >> (8 * e))) >> 16);
-  return r;
+// Four int8 codes (one dword) -> four f16 operands holding 1152 + code exactly: with
+// u = code + 128 (the byte with its top bit flipped), the f16 pattern 0x6400 | u is 1024 + u
+// (ulp 1 in [1024, 2048)), so two byte permutes build the four values.  The QK product then
+// carries 1152 * sum(q), which is subtracted per query column.
+constexpr float kCodeBias = 1152.0f;
+__device__ __forceinline__ f16x4 codes_f16(uint32_t w) {
+  const uint32_t u = w ^ 0x80808080u;
+  u32x2 h;
+  h[0] = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // [u0, 0x64, u1, 0x64]
+  h[1] = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // [u2, 0x64, u3, 0x64]
+  return __builtin_bit_cast(f16x4, h);
 }
 
-// kKind: 0 int8 caches (bf16 MFMA), 1 bf16 caches, 2 f16 caches.  kQLo: q needs a lo part.
+// kKind: 0 int8 caches (f16 QK, bf16 PV), 1 bf16 caches, 2 f16 caches.  kQLo: q needs a lo
+// operand.
+// Workgroups per CU the register allocation must allow: three (168 registers per lane) for
+// the int8 kernels up to head_size 128, fewer where that would spill.
+constexpr int attn_min_blocks(int d, int kind) { return d == 256 ? 1 : (kind != 0 && d == 128 ? 2 : 3); }
+
 template <int kD, int kKind, bool kQLo>
-__global__ __launch_bounds__(256) void attn_mfma(AttnParams p) {
+__global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(AttnParams p) {
   constexpr bool kF16 = kKind == 2;
   using M = Mfma<kF16>;
   using V4 = typename M::V4;
@@ -179,8 +188,16 @@ __global__ __launch_bounds__(256) void attn_mfma(AttnParams p) {
   const int hq = hk * p.g + col;
   const bool qvalid = col < p.g;
 
-  // ---- Q operand (B of S^T = K Q^T): column `col`, channels grp * kDC + 4m .. + 3
-  V4 qhi[kQK], qlo[kQLo ? kQK : 1];
+  // ---- Q operand (B of S^T = K Q^T): column `col`, channels grp * kDC + 4m .. + 3.  The QK
+  // product runs on f16 operands: int8 codes as 1152 + code (codes_f16), q scaled by a power
+  // of two sigma that puts the column's largest |q| in [2^14, 2^15) (an f16 holds every bf16
+  // and f16 value of that column exactly down to 2^-29 of the largest), with a second (lo)
+  // operand when q is folded with per-channel key scales.  Plain caches use their own type.
+  using MQ = Mfma<kKind == 0 ? true : kF16>;
+  using VQ = typename MQ::V4;
+  VQ qhi[kQK], qlo[kQLo ? kQK : 1];
+  float qx[kQK][4];
+  float qabs = 0.0f;
 #pragma unroll
   for (int m = 0; m < kQK; ++m) {
 #pragma unroll
@@ -188,16 +205,48 @@ __global__ __launch_bounds__(256) void attn_mfma(AttnParams p) {
       const int d = grp * kDC + 4 * m + e;
       float x = qvalid ? load_q(p, i * p.q_sb + (int64_t)hq * p.q_sh + d) : 0.0f;
       if (kKind == 0 && p.smode == 2) x *= p.ks[(int64_t)hk * kD + d];
-      if constexpr (kF16) {
-        qhi[m][e] = (_Float16)x;
-      } else {
-        const short hb = M::bits(x);
-        qhi[m][e] = hb;
-        if constexpr (kQLo) qlo[m][e] = M::bits(x - M::value(hb));
+      qx[m][e] = x;
+      qabs = fmaxf(qabs, fabsf(x));
+    }
+  }
+  float inv_sigma = 1.0f, qk_off = 0.0f;
+  if constexpr (kKind == 0) {
+    qabs = col_max(qabs);
+    const int ex = qabs > 0.0f ? __builtin_amdgcn_frexp_expf(qabs) : 1;  // qabs in [2^(ex-1), 2^ex)
+    const float sigma = __builtin_ldexpf(1.0f, 15 - ex);
+    inv_sigma = __builtin_ldexpf(1.0f, ex - 15);
+    float qsum = 0.0f;
+#pragma unroll
+    for (int m = 0; m < kQK; ++m) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float y = qx[m][e] * sigma;
+        const _Float16 h = (_Float16)y;
+        qhi[m][e] = h;
+        qsum += (float)h;
+        if constexpr (kQLo) {
+          const _Float16 l = (_Float16)(y - (float)h);
+          qlo[m][e] = l;
+          qsum += (float)l;
+        }
+      }
+    }
+    qk_off = kCodeBias * col_sum(qsum);
+  } else {
+#pragma unroll
+    for (int m = 0; m < kQK; ++m) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (kF16) {
+          qhi[m][e] = (_Float16)qx[m][e];
+        } else {
+          qhi[m][e] = M::bits(qx[m][e]);
+        }
       }
     }
   }
   const float alibi = (p.alibi && qvalid) ? p.alibi[i * p.Hq + hq] * kLog2e : 0.0f;
+  const float score_scale = p.scale_log2 * inv_sigma;  // inv_sigma: an exact power of two
 
   float mrun = -__builtin_inff();   // running max (base 2) of this lane's column
   float lpart = 0.0f;               // this lane's share of the running sum
@@ -294,21 +343,17 @@ __global__ __launch_bounds__(256) void attn_mfma(AttnParams p) {
       f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int m = 0; m < kQK; ++m) {
-        V4 a;
+        VQ a;
         if constexpr (kKind == 0) {
-          a = codes_bf16(r.kw[m]);
+          a = codes_f16(r.kw[m]);
         } else {
-          const uint32_t w0 = r.kw[2 * m], w1 = r.kw[2 * m + 1];
-          typedef short s4 __attribute__((ext_vector_type(4)));
-          s4 b4;
-          b4[0] = (short)(w0 & 0xffffu);
-          b4[1] = (short)(w0 >> 16);
-          b4[2] = (short)(w1 & 0xffffu);
-          b4[3] = (short)(w1 >> 16);
-          a = __builtin_bit_cast(V4, b4);
+          u32x2 w;
+          w[0] = r.kw[2 * m];
+          w[1] = r.kw[2 * m + 1];
+          a = __builtin_bit_cast(VQ, w);
         }
-        s = M::run(a, qhi[m], s);
-        if constexpr (kQLo) s = M::run(a, qlo[m], s);
+        s = MQ::run(a, qhi[m], s);
+        if constexpr (kQLo) s = MQ::run(a, qlo[m], s);
       }
 
       // ---- scores (base 2), masking, online softmax
@@ -317,7 +362,7 @@ __global__ __launch_bounds__(256) void attn_mfma(AttnParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int32_t j = t0 + 4 * grp + e;
-        float v = s[e] * r.ksc[e] * p.scale_log2;
+        float v = (s[e] - qk_off) * (r.ksc[e] * score_scale);
         if (p.alibi) v += alibi * (float)(j - last32);
         if (j < begin32 || j >= end32 || !qvalid) v = -__builtin_inff();
         sc[e] = v;
@@ -719,7 +764,9 @@ extern "C" int tmo_hip_single_query_cached_kv_attn(
   int64_t per = (max_context_len + splits - 1) / splits;
   per = (per + 63) / 64 * 64;
   p.split_tokens = per > 0 ? per : 64;
-  if (cache_dtype == TMO_DTYPE_I8) return launch_mfma<0>(p, q_dtype != TMO_DTYPE_BF16 || scale_mode == 2, st);
+  // int8 caches: bf16 and f16 q are exact f16 operands after the power-of-two scaling; q
+  // folded with per-channel key scales needs the lo operand
+  if (cache_dtype == TMO_DTYPE_I8) return launch_mfma<0>(p, scale_mode == 2, st);
   if (cache_dtype == TMO_DTYPE_BF16) return launch_mfma<1>(p, false, st);
   return launch_mfma<2>(p, false, st);
 }
