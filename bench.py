@@ -53,6 +53,7 @@ WORKLOADS = {
     "linear_quant": "quant_to_linear_cache on configs[2]'s volume: 8 packed sequences x 4096 tokens x 8 KV heads x 128 bf16 -> int8 linear cache [8, 8, 8192, 128] + fp32 per-token scales",
     "linear_dequant": "dequant_from_linear_cache (per-token scales), 8 sequences x 4096 tokens x 8 KV heads x 128: int8 linear cache [8, 8, 8192, 128] -> bf16",
     "linear_reshape": "reshape_linear_cache, 8 packed sequences x 4096 tokens x 8 KV heads x 128 bf16 -> bf16 linear cache [8, 8, 8192, 128]",
+    "decode_attn": "single_query_cached_kv_attn, one bf16 query token x 32 heads per sequence over configs[4]'s int8 pages (64 seqs, ctx ~U[1024,32768], 8 KV heads x 128, per-token scales)",
 }
 KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1>", "cfg2": "quant_paged_vec<BF16,16,1>",
            "cfg3": "quant_paged_vec<BF16,16,1>", "cfg4": "sq_dense<BF16,8,false,true>",
@@ -61,7 +62,7 @@ KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1>", "cfg2": "quant_paged_vec<BF16,1
            "offline_f8": "quant_paged_static_vec<BF16,16,true>",
            "fused_rope": "fused_rope_tok<BF16,16,4>",
            "linear_quant": "lin_quant<BF16,16,false,false>", "linear_dequant": "lin_dequant<BF16,16>",
-           "linear_reshape": "lin_copy<16>"}
+           "linear_reshape": "lin_copy<16>", "decode_attn": "attn_mfma<128,0,false>"}
 
 
 def parse_args():
@@ -292,6 +293,36 @@ def bench_linear(torch, tmo, op: str, dev, steps, warmup):
     return ms, alg, LIN_B * LIN_S, sets
 
 
+ATTN_HQ = 32
+
+
+def attn_bytes(layout, hq: int = ATTN_HQ, heads: int = 8, dim: int = W_D) -> int:
+    """Algorithmic bytes of decode attention over `layout`: every key's K and V codes and
+    scales once per KV head, q read and out written, block-table entries and lengths."""
+    pages = int(((layout.context_lengths + layout.block_size - 1) // layout.block_size).sum())
+    B = layout.context_lengths.numel()
+    return (layout.total_tokens * heads * 2 * (dim + 4) + 2 * B * hq * dim * 2 + 4 * pages
+            + 4 * B)
+
+
+def bench_decode_attn(torch, tmo, W, layout, dev, steps, warmup):
+    """single_query_cached_kv_attn over configs[4]'s filled pages: one call per step (the pages
+    are ~2.4 GB, far beyond the MALL)."""
+    alg = attn_bytes(layout)
+    kc, vc, ks, vs = W.cfg5_fill(layout, dev)
+    B = layout.context_lengths.numel()
+    g = torch.Generator(device=dev).manual_seed(17)
+    q = torch.randn((B, 1, ATTN_HQ, W_D), generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    ctx = layout.context_lengths.to(dev)
+    bt = layout.block_tables.to(dev)
+    mctx = layout.max_context_len
+    calls = [lambda: tmo.single_query_cached_kv_attn(q, kc, vc, out, bt, ctx, ks, vs, None, mctx,
+                                                     -1, -1, W_D ** -0.5, False, 8)]
+    ms = time_graph(torch, calls, steps, warmup)
+    return ms, alg, layout.total_tokens, 1
+
+
 def bench_smooth_quant(torch, tmo, W, case, dev, steps, warmup):
     alg = case.algorithmic_bytes()
     sets = n_sets(alg)
@@ -359,6 +390,15 @@ def profile_pass(torch, tmo, W, names, dev, n: int) -> None:
                                                                   sl, ks, vs)
         elif name.startswith("linear"):
             fn = linear_call(torch, tmo, name, dev, torch.Generator(device=dev).manual_seed(13))
+        elif name == "decode_attn":
+            layout = W.cfg5()
+            kc, vc, ks, vs = W.cfg5_fill(layout, dev)
+            q = torch.randn((64, 1, ATTN_HQ, W_D), device=dev).to(torch.bfloat16)
+            out = torch.empty_like(q)
+            ctx, bt = layout.context_lengths.to(dev), layout.block_tables.to(dev)
+            mctx = layout.max_context_len
+            fn = lambda: tmo.single_query_cached_kv_attn(q, kc, vc, out, bt, ctx, ks, vs, None,
+                                                         mctx, -1, -1, W_D ** -0.5, False, 8)
         elif name.startswith("cfg4"):
             case = getattr(W, name)()
             x, sm = case.x.to(dev), case.smooth.to(dev)
@@ -465,6 +505,28 @@ def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
         fn = lambda: oracle.fused_rope_paged(qkv, kc, vc, tab, tab, pid, gm, ks, vs, sl, 1e-5, gm,
                                              nthreads=nthreads)
         alg, units, desc = fused_rope_bytes(n), n, f"fused rope of one {n}-token sequence"
+    elif workload == "decode_attn":
+        layout = W.cfg5()
+        nseq = 2
+        ctx = layout.context_lengths[:nseq].contiguous()
+        pages = [(int(c) + W.BS - 1) // W.BS for c in ctx.tolist()]
+        bt = torch.zeros(nseq, max(pages), dtype=torch.int32)
+        p0 = 0
+        for i, pn in enumerate(pages):  # the sample's pages renumbered into a compact cache
+            bt[i, :pn] = torch.arange(p0, p0 + pn, dtype=torch.int32)
+            p0 += pn
+        sub = W.DequantLayout("cfg5-sample", ctx, bt, p0)
+        g = torch.Generator().manual_seed(5)
+        kc = torch.randint(-127, 128, (p0, W.H, W.BS, W.D), generator=g, dtype=torch.int8)
+        vc = torch.randint(-127, 128, (p0, W.H, W.BS, W.D), generator=g, dtype=torch.int8)
+        ks = torch.rand(p0, W.H, W.BS, generator=g) * 0.05
+        vs = torch.rand(p0, W.H, W.BS, generator=g) * 0.05
+        q = torch.randn(nseq, ATTN_HQ, W.D, generator=g).to(torch.bfloat16)
+        fn = lambda: oracle.single_query_attn(q, kc, vc, bt, ctx, W.D ** -0.5, ks, vs,
+                                              nthreads=nthreads)
+        alg, units = attn_bytes(sub), sub.total_tokens
+        desc = (f"float64 decode attention of the first {nseq} sequences of cfg5 ({units} keys, "
+                f"{ATTN_HQ} query heads)")
     elif workload.startswith("linear"):
         nb, S, H = LIN_B, 1024, W.H   # every sequence (the oracle threads over sequences)
         op = {"linear_reshape": 0, "linear_quant": 1, "linear_dequant": 3}[workload]
@@ -554,7 +616,7 @@ def main():
     dev = torch.device("cuda", 0)
     todo = [args.workload] if args.configs == "headline" else \
         ["cfg1", "cfg2", "cfg3", "cfg4", "cfg4_moe", "cfg5", "offline_i8", "offline_f8",
-         "fused_rope", "linear_quant", "linear_dequant", "linear_reshape"]
+         "fused_rope", "linear_quant", "linear_dequant", "linear_reshape", "decode_attn"]
     if args.workload not in todo:
         todo.append(args.workload)
     if args.profile_pass:
@@ -579,6 +641,10 @@ def main():
         elif name.startswith("linear"):
             ms, alg, units, sets = bench_linear(torch, tmo, name, dev, max(20, args.steps // 4),
                                                 max(4, args.warmup // 4))
+        elif name == "decode_attn":
+            ms, alg, units, sets = bench_decode_attn(torch, tmo, W, W.cfg5(), dev,
+                                                     max(10, args.steps // 40),
+                                                     max(2, args.warmup // 10))
         else:
             ms, alg, units, sets = bench_dequant(torch, tmo, W, W.cfg5(), dev,
                                                  max(10, args.steps // 40), max(2, args.warmup // 10))
@@ -619,7 +685,8 @@ def main():
                           "offline_f8": "bf16 in; float8_e4m3fn codes out (static per-channel scales)",
                           "fused_rope": "bf16 qkv in; bf16 Q written back; int8 K/V codes + fp32 scales out",
                           "linear_dequant": "int8 codes + fp32 scales in; bf16 out",
-                          "linear_reshape": "bf16 in; bf16 out"}
+                          "linear_reshape": "bf16 in; bf16 out",
+                          "decode_attn": "bf16 q, int8 K/V pages + fp32 scales in; bf16 out; fp32 softmax"}
                    .get(args.workload, "bf16 in; int8 codes + fp32 scales out"),
                    "tokens_per_s": head["units_per_s"],
                    "frac_of_peak": head["frac_of_peak"]},

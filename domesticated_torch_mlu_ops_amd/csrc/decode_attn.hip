@@ -15,17 +15,18 @@
 //     columns, zero-padded to 16): lane (t = l % 16, c = l / 16) holds token t's channels
 //     [c D/4, (c + 1) D/4), so the K tile is read as contiguous row pieces, and MFMA m takes
 //     channels c D/4 + 4m .. + 3 of every lane group (a permutation of the reduction order).
-//     Int8 codes convert to bf16 exactly (|code| <= 128 has 8 significant bits); the per-token
-//     scale and softmax_scale * log2(e) multiply the fp32 result.
+//     Int8 codes enter as exact f16 values 1152 + code (two byte permutes per four codes) against
+//     a power-of-two scaled f16 q, and 1152 * sum(q) is subtracted from the fp32 result; the
+//     per-token scale and softmax_scale * log2(e) then multiply it.
 //   * The result layout (lane holds tokens 4c .. 4c + 3 of query column l % 16) IS the B
 //     operand layout of O^T = V^T P^T, so the probabilities feed the second product without a
 //     shuffle.  V^T's operand needs four tokens of one channel per lane: lane (n, c) reads
 //     D/16 bytes of tokens 4c .. 4c + 3 at channels n D/16 .., and MFMA j uses channel
 //     n D/16 + j of them, so lane (q, c) accumulates channels [4c D/16, (4c + 4) D/16) -- one
 //     contiguous run of the output row.
-//   * p is split into hi + lo operands of the MFMA type (16 significant bits with bf16) and
-//     two products accumulate; q likewise when it is not exactly representable (fp16 q on the
-//     bf16 path, or q folded with per-channel key scales).
+//   * p (times the per-token V scale) is split into hi + lo bf16 operands (16 significant
+//     bits) and two products accumulate, against V codes converted to bf16 exactly; q gets a
+//     lo operand too when it is folded with per-channel key scales.
 //   * Online softmax in base 2 per query column; a lane keeps a partial sum over its own four
 //     tokens, summed over the lane groups at the end.
 // The four wavefronts combine through LDS; with more than one split per (sequence, KV head)
