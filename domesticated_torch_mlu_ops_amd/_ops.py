@@ -61,13 +61,15 @@ def quant_to_paged_cache(
     v_cache_quant_scale: Optional[torch.Tensor],
     slot_mapping: torch.Tensor,
 ) -> Tuple[torch.Tensor]:
-    """Dynamic per-(token, head) int8 quantisation of k/v into the paged caches.
+    """Dynamic per-(token, head) quantisation of k/v into the paged caches.
 
-    For each token ``i`` with ``slot_mapping[i] >= 0`` and each head ``h``:
+    For each token ``i`` with ``slot_mapping[i] >= 0`` and each head ``h``: int8 caches
     ``scale = fp32(max|k[i, h]|) / 127``, ``code = clip(round_half_even(k[i, h] / scale),
-    -128, 127)``; codes go to ``k_cache[slot // bs, h, slot % bs]`` and the scale to
-    ``k_cache_quant_scale[slot // bs, h, slot % bs]`` (same for v).  An all-zero row stores
-    scale 0 and codes 0.  k/v: float, half or bfloat16 (may be strided views); caches int8.
+    -128, 127)``; ``torch.float8_e4m3fn`` caches ``scale = fp32(max|k[i, h]|) / 448``,
+    ``code = clip(k[i, h] / scale, -448, 448)`` rounded to nearest even.  Codes go to
+    ``k_cache[slot // bs, h, slot % bs]`` and the scale to ``k_cache_quant_scale[slot // bs,
+    h, slot % bs]`` (same for v).  An all-zero row stores scale 0 and codes 0.  k/v: float,
+    half or bfloat16 (may be strided views).
 
     Reference: ``_ops.py:1511-1565`` (math ``:1524-1537``).  Returns
     ``(k_cache, v_cache, k_scale, v_scale)`` or ``(k_cache, k_scale)``.

@@ -310,17 +310,6 @@ __device__ __forceinline__ uint32_t lane_group_max(uint32_t v, int gl) {
   return v;
 }
 
-// fp8 dynamic scale of a group: RN(amax / 448) (IEEE divide, once per group) and, when
-// kFastDivMinScale <= s < inf, y = RN(1 / s) for the reciprocal quotient (div_by_recip gives
-// the IEEE quotient there, as for the int8 scale).  s == 0: every code is +0.
-__device__ __forceinline__ RowScale make_fp8_scale(float amax) {
-  RowScale r;
-  r.s = amax / 448.0f;
-  r.fast = r.s >= kFastDivMinScale && r.s < __builtin_inff();
-  r.y = r.fast ? 1.0f / r.s : 0.0f;
-  return r;
-}
-
 // ------------------------------------------------------------------------------ quantisers
 
 // quant_to_linear_cache (kStatic false) / offline_quant_to_linear_cache (kStatic true):
@@ -391,7 +380,7 @@ __global__ __launch_bounds__(256) void lin_quant(LinParams p) {
         for (int e = 0; e < 8; ++e) fast &= static_scale_fast(sc[e]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) y[e] = fast ? recip_rn(sc[e]) : 0.0f;
-        static_quotients<8>(v, sc, y, fast, q);
+        static_quotients<8, kFp8>(v, sc, y, fast, q);
         encode_static<8, kFp8>(q, c);
       } else {
         const int gl = G / p.groups;  // lanes per scale group
@@ -402,17 +391,7 @@ __global__ __launch_bounds__(256) void lin_quant(LinParams p) {
         float scale;
         if constexpr (kFp8) {
           const RowScale rs = make_fp8_scale(amax);
-          float q[8];
-          if (rs.fast) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) q[e] = div_by_recip(v[e], rs.s, rs.y);
-          } else {
-            keep_branch();
-#pragma unroll
-            for (int e = 0; e < 8; ++e) q[e] = v[e] / rs.s;  // IEEE divide
-          }
-          encode_static<8, true>(q, c);
-          if (rs.s == 0.0f) c[0] = c[1] = 0u;  // all-zero group: +0 codes, as the int8 path
+          encode_fp8_row<8>(v, rs, c);
           scale = rs.s;
         } else {
           const RowScale rs = make_row_scale(amax);

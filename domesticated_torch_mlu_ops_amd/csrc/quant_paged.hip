@@ -1,5 +1,6 @@
-// quant_to_paged_cache for gfx950: dynamic per-(token, head) int8 quantisation of K/V rows,
-// scattered into [num_blocks, heads, block_size, head_dim] pages through slot_mapping.
+// quant_to_paged_cache for gfx950: dynamic per-(token, head) quantisation of K/V rows into
+// int8 (scale = amax / 127) or float8_e4m3fn (scale = amax / 448) codes, scattered into
+// [num_blocks, heads, block_size, head_dim] pages through slot_mapping.
 //
 // Semantics: reference _ops.py:1511-1565 (math block :1524-1537, slot convention :1262-1268).
 // Entry point: tmo_hip_quant_to_paged_cache (include/tmo_hip.h).
@@ -68,7 +69,7 @@ constexpr int kTokensPerThread = TMO_QUANT_TOKENS_PER_THREAD;
 // elements per lane.  A workgroup owns kTokensPerThread * 256/G consecutive tokens of one head.
 // Every load of the lane group (slots, K rows, V rows) is issued before the first wait: the
 // input address does not depend on the slot, only the store address does.
-template <class Tag, int G, int V>
+template <class Tag, int G, int V, bool kFp8>
 __global__ __launch_bounds__(256) void quant_paged_vec(QuantPagedParams p) {
   constexpr int kGroups = 256 / G;  // lane groups per workgroup
   constexpr int kPer = Tag::kPerVec;
@@ -115,14 +116,18 @@ __global__ __launch_bounds__(256) void quant_paged_vec(QuantPagedParams p) {
 #pragma unroll
           for (int e = 0; e < kPer; ++e) m = abs_max(m, v[i][e]);
         }
-        const RowScale rs =
-            make_row_scale(__uint_as_float(group_max_u32<G>(__float_as_uint(m))));
+        const float amax = __uint_as_float(group_max_u32<G>(__float_as_uint(m)));
+        const RowScale rs = kFp8 ? make_fp8_scale(amax) : make_row_scale(amax);
         int8_t* row = p.cache[kv] + page_row * p.head_dim;
 #pragma unroll
         for (int i = 0; i < V; ++i) {
           int8_t* dst = row + (lane + i * G) * kPer;
           uint32_t c[kPer / 4];
-          encode_row<kPer>(v[i], rs, c);
+          if constexpr (kFp8) {
+            encode_fp8_row<kPer>(v[i], rs, c);
+          } else {
+            encode_row<kPer>(v[i], rs, c);
+          }
           if constexpr (kPer == 8) {
             u32x2 c2;
             c2[0] = c[0];
@@ -139,7 +144,7 @@ __global__ __launch_bounds__(256) void quant_paged_vec(QuantPagedParams p) {
 }
 
 // Generic path (any head_dim / alignment): one wavefront per row, scalar loads, two passes.
-template <class Tag>
+template <class Tag, bool kFp8>
 __global__ __launch_bounds__(256) void quant_paged_generic(QuantPagedParams p) {
   constexpr int kRows = 256 / kWave;
   const int lane = threadIdx.x & (kWave - 1);
@@ -154,10 +159,19 @@ __global__ __launch_bounds__(256) void quant_paged_generic(QuantPagedParams p) {
     const int64_t base = t * p.stride_tok[kv] + (int64_t)h * p.stride_head[kv];
     float m = 0.0f;
     for (int d = lane; d < p.head_dim; d += kWave) m = abs_max(m, load1(Tag{}, src, base + d));
-    const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<kWave>(__float_as_uint(m))));
+    const float amax = __uint_as_float(group_max_u32<kWave>(__float_as_uint(m)));
     int8_t* dst = p.cache[kv] + page_row * p.head_dim;
-    for (int d = lane; d < p.head_dim; d += kWave) dst[d] = encode1(load1(Tag{}, src, base + d), rs);
-    if (lane == 0) p.scale[kv][page_row] = rs.s;
+    float s;
+    if constexpr (kFp8) {
+      s = amax / 448.0f;  // IEEE divide
+      for (int d = lane; d < p.head_dim; d += kWave)
+        dst[d] = (int8_t)encode1_fp8(load1(Tag{}, src, base + d), s);
+    } else {
+      const RowScale rs = make_row_scale(amax);
+      s = rs.s;
+      for (int d = lane; d < p.head_dim; d += kWave) dst[d] = encode1(load1(Tag{}, src, base + d), rs);
+    }
+    if (lane == 0) p.scale[kv][page_row] = s;
   }
 }
 
@@ -263,7 +277,7 @@ __global__ __launch_bounds__(256) void quant_paged_static_vec(StaticParams sp) {
       if (kv < p.nkv) {
         float v[kPer], q[kPer];
         unpack(Tag{}, w[j][kv], v);
-        static_quotients<kPer>(v, s[kv], y[kv], fast[kv], q);
+        static_quotients<kPer, kFp8>(v, s[kv], y[kv], fast[kv], q);
         uint32_t c[kPer / 4];
         encode_static<kPer, kFp8>(q, c);
         int8_t* dst = p.cache[kv] + page_row * p.head_dim + lane * kPer;
@@ -341,20 +355,20 @@ int launch_static(const StaticParams& sp, hipStream_t stream) {
   }
 }
 
-template <class Tag, int V>
+template <class Tag, int V, bool kFp8>
 int launch_vec(const QuantPagedParams& p, int G, dim3 grid, dim3 block, hipStream_t stream) {
   switch (G) {
-    case 1: return launch_kernel(quant_paged_vec<Tag, 1, V>, grid, block, stream, p);
-    case 2: return launch_kernel(quant_paged_vec<Tag, 2, V>, grid, block, stream, p);
-    case 4: return launch_kernel(quant_paged_vec<Tag, 4, V>, grid, block, stream, p);
-    case 8: return launch_kernel(quant_paged_vec<Tag, 8, V>, grid, block, stream, p);
-    case 16: return launch_kernel(quant_paged_vec<Tag, 16, V>, grid, block, stream, p);
-    case 32: return launch_kernel(quant_paged_vec<Tag, 32, V>, grid, block, stream, p);
-    default: return launch_kernel(quant_paged_vec<Tag, 64, V>, grid, block, stream, p);
+    case 1: return launch_kernel(quant_paged_vec<Tag, 1, V, kFp8>, grid, block, stream, p);
+    case 2: return launch_kernel(quant_paged_vec<Tag, 2, V, kFp8>, grid, block, stream, p);
+    case 4: return launch_kernel(quant_paged_vec<Tag, 4, V, kFp8>, grid, block, stream, p);
+    case 8: return launch_kernel(quant_paged_vec<Tag, 8, V, kFp8>, grid, block, stream, p);
+    case 16: return launch_kernel(quant_paged_vec<Tag, 16, V, kFp8>, grid, block, stream, p);
+    case 32: return launch_kernel(quant_paged_vec<Tag, 32, V, kFp8>, grid, block, stream, p);
+    default: return launch_kernel(quant_paged_vec<Tag, 64, V, kFp8>, grid, block, stream, p);
   }
 }
 
-template <class Tag>
+template <class Tag, bool kFp8>
 int launch(const QuantPagedParams& p, hipStream_t stream) {
   constexpr int kPer = Tag::kPerVec;
   bool vec = (p.head_dim % kPer) == 0;
@@ -374,9 +388,9 @@ int launch(const QuantPagedParams& p, hipStream_t stream) {
   const int64_t blocks = tiles * p.heads;
   if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
   const dim3 grid((unsigned)blocks), block(256);
-  if (!vec) return launch_kernel(quant_paged_generic<Tag>, grid, block, stream, p);
-  if (V == 1) return launch_vec<Tag, 1>(p, G, grid, block, stream);
-  return launch_vec<Tag, TMO_QUANT_VEC_PER_LANE>(p, G, grid, block, stream);
+  if (!vec) return launch_kernel(quant_paged_generic<Tag, kFp8>, grid, block, stream, p);
+  if (V == 1) return launch_vec<Tag, 1, kFp8>(p, G, grid, block, stream);
+  return launch_vec<Tag, TMO_QUANT_VEC_PER_LANE, kFp8>(p, G, grid, block, stream);
 }
 
 }  // namespace
@@ -385,14 +399,16 @@ int launch(const QuantPagedParams& p, hipStream_t stream) {
 extern "C" int tmo_hip_quant_to_paged_cache(const void* k, const void* v,
                                             int64_t k_stride_token, int64_t k_stride_head,
                                             int64_t v_stride_token, int64_t v_stride_head,
-                                            int8_t* k_cache, int8_t* v_cache,
+                                            void* k_cache, void* v_cache,
                                             float* k_cache_scale, float* v_cache_scale,
                                             const int32_t* slot_mapping, int64_t num_tokens,
                                             int64_t num_heads, int64_t head_size,
                                             int64_t num_blocks, int64_t block_size, int dtype,
-                                            void* stream) {
+                                            int cache_dtype, void* stream) {
   using namespace tmo;
   if (dtype != TMO_DTYPE_F32 && dtype != TMO_DTYPE_F16 && dtype != TMO_DTYPE_BF16)
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (cache_dtype != TMO_DTYPE_I8 && cache_dtype != TMO_DTYPE_F8E4M3)
     return TMO_ERR_UNSUPPORTED_DTYPE;
   if (!k || !k_cache || !k_cache_scale || !slot_mapping) return TMO_ERR_INVALID_ARGUMENT;
   const bool has_v = v != nullptr;
@@ -413,8 +429,8 @@ extern "C" int tmo_hip_quant_to_paged_cache(const void* k, const void* v,
   p.stride_tok[1] = v_stride_token;
   p.stride_head[0] = k_stride_head;
   p.stride_head[1] = v_stride_head;
-  p.cache[0] = k_cache;
-  p.cache[1] = v_cache;
+  p.cache[0] = static_cast<int8_t*>(k_cache);
+  p.cache[1] = static_cast<int8_t*>(v_cache);
   p.scale[0] = k_cache_scale;
   p.scale[1] = v_cache_scale;
   p.slot = slot_mapping;
@@ -426,10 +442,11 @@ extern "C" int tmo_hip_quant_to_paged_cache(const void* k, const void* v,
   p.bs_shift = ilog2_if_pow2(block_size);
   p.nkv = has_v ? 2 : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool fp8 = cache_dtype == TMO_DTYPE_F8E4M3;
   switch (dtype) {
-    case TMO_DTYPE_F32: return launch<F32>(p, s);
-    case TMO_DTYPE_F16: return launch<F16>(p, s);
-    default: return launch<BF16>(p, s);
+    case TMO_DTYPE_F32: return fp8 ? launch<F32, true>(p, s) : launch<F32, false>(p, s);
+    case TMO_DTYPE_F16: return fp8 ? launch<F16, true>(p, s) : launch<F16, false>(p, s);
+    default: return fp8 ? launch<BF16, true>(p, s) : launch<BF16, false>(p, s);
   }
 }
 

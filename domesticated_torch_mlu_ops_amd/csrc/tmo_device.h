@@ -273,9 +273,31 @@ __host__ __device__ __forceinline__ bool static_scale_fast(float s) {
   return a >= kStaticMinScale && a <= kStaticMaxScale;
 }
 
-// N quotients x[i] / s[i] (IEEE bits, see above).  y[i] = RN(1 / s[i]) when `fast`
-// (static_scale_fast for every s[i]), ignored otherwise.
+// The IEEE quotient x / s carries the sign sign(x) ^ sign(s) also when it is zero; the FMA
+// steps of div_by_recip return +0 for x = -0 and s > 0 (r0 = (-s)(-0) + (-0) = +0).  int8
+// codes do not see the difference; float8_e4m3fn has a -0 code, so the fp8 paths put the sign
+// back after div_by_recip (for a non-zero finite s and a non-zero quotient it is already right).
+__host__ __device__ __forceinline__ uint32_t fbits(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  return u;
+}
+__host__ __device__ __forceinline__ float bitsf(uint32_t u) {
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
 template <int N>
+__host__ __device__ __forceinline__ void quotient_signs(float* q, const float* x, const float* s) {
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    q[i] = bitsf((fbits(q[i]) & 0x7fffffffu) | ((fbits(x[i]) ^ fbits(s[i])) & 0x80000000u));
+}
+
+// N quotients x[i] / s[i] (IEEE bits, see above; with kSignedZero also the sign of a zero
+// quotient, for fp8 codes).  y[i] = RN(1 / s[i]) when `fast` (static_scale_fast for every
+// s[i]), ignored otherwise.
+template <int N, bool kSignedZero = false>
 __host__ __device__ __forceinline__ void static_quotients(const float* x, const float* s,
                                                           const float* y, bool fast, float* q) {
   float m = 0.0f;
@@ -284,6 +306,7 @@ __host__ __device__ __forceinline__ void static_quotients(const float* x, const 
   if (fast && m < kStaticQuotientLimit) {
 #pragma unroll
     for (int i = 0; i < N; ++i) q[i] = div_by_recip(x[i], s[i], y[i]);
+    if constexpr (kSignedZero) quotient_signs<N>(q, x, s);
   } else {
     keep_branch();
 #pragma unroll
@@ -347,6 +370,49 @@ __device__ __forceinline__ void encode_static(const float* q, uint32_t* out) {
                           code_bits(q[4 * i + 3]));
     }
   }
+}
+
+// ---------------------------------------------------------------------------- fp8 dynamic scales
+
+// float8_e4m3fn dynamic scale of a row / group: RN(amax / 448) (IEEE divide, once per row) and,
+// when kFastDivMinScale <= s < inf, y = RN(1 / s) for the reciprocal quotient (div_by_recip gives
+// the IEEE quotient there, as for the int8 scale).  s == 0 (an all-zero row): every code is +0.
+__device__ __forceinline__ RowScale make_fp8_scale(float amax) {
+  RowScale r;
+  r.s = amax / 448.0f;
+  r.fast = r.s >= kFastDivMinScale && r.s < __builtin_inff();
+  r.y = r.fast ? 1.0f / r.s : 0.0f;
+  return r;
+}
+
+// N values (multiple of 4) -> N e4m3fn codes packed 4 per u32: e4m3fn_RNE(clip(RN(x / s), +-448)),
+// all +0 when s == 0.
+template <int N>
+__device__ __forceinline__ void encode_fp8_row(const float* v, const RowScale& r, uint32_t* out) {
+  float q[N];
+  if (r.fast) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = div_by_recip(v[i], r.s, r.y);
+    float sv[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) sv[i] = r.s;
+    quotient_signs<N>(q, v, sv);
+  } else {
+    keep_branch();
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = v[i] / r.s;  // IEEE divide
+  }
+  encode_static<N, true>(q, out);
+  if (r.s == 0.0f) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) out[i] = 0u;
+  }
+}
+
+// One value of the same encoding (generic paths).
+__device__ __forceinline__ uint8_t encode1_fp8(float v, float s) {
+  if (s == 0.0f) return 0;
+  return (uint8_t)fp8e4m3_bits(__builtin_amdgcn_fmed3f(v / s, -448.0f, 448.0f));  // IEEE divide
 }
 
 // ---------------------------------------------------------------------------- stores

@@ -114,8 +114,10 @@ void quant_to_paged_cache(const torch::Tensor& k, const c10::optional<torch::Ten
   const int dt = dtype_code(k.scalar_type());
   TORCH_CHECK(dt == TMO_DTYPE_F32 || dt == TMO_DTYPE_F16 || dt == TMO_DTYPE_BF16,
               "quant_to_paged_cache: k must be float, half or bfloat16, got ", k.scalar_type());
-  TORCH_CHECK(k_cache.scalar_type() == at::kChar,
-              "quant_to_paged_cache: only int8 caches are supported, got ", k_cache.scalar_type());
+  const int cdt = dtype_code(k_cache.scalar_type());
+  TORCH_CHECK(cdt == TMO_DTYPE_I8 || cdt == TMO_DTYPE_F8E4M3,
+              "quant_to_paged_cache: caches must be int8 or float8_e4m3fn, got ",
+              k_cache.scalar_type());
   const int64_t T = k.size(0), H = k.size(1), D = k.size(2);
   const int64_t NB = k_cache.size(0), BS = k_cache.size(2);
   TORCH_CHECK(k_cache.size(1) == H && k_cache.size(3) == D, "k_cache ", k_cache.sizes(),
@@ -137,7 +139,8 @@ void quant_to_paged_cache(const torch::Tensor& k, const c10::optional<torch::Ten
     check_device(*v_cache, k, "v_cache");
     check_device(*v_cache_scale, k, "v_cache_scale");
     TORCH_CHECK(v->sizes() == k.sizes() && v->scalar_type() == k.scalar_type(), "v must match k");
-    TORCH_CHECK(v_cache->sizes() == k_cache.sizes() && v_cache->scalar_type() == at::kChar,
+    TORCH_CHECK(v_cache->sizes() == k_cache.sizes() &&
+                    v_cache->scalar_type() == k_cache.scalar_type(),
                 "v_cache must match k_cache");
     TORCH_CHECK(v_cache_scale->sizes() == k_cache_scale.sizes() &&
                     v_cache_scale->scalar_type() == at::kFloat && v_cache_scale->is_contiguous(),
@@ -147,10 +150,10 @@ void quant_to_paged_cache(const torch::Tensor& k, const c10::optional<torch::Ten
   c10::DeviceGuard guard(k.device());
   const int st = tmo_hip_quant_to_paged_cache(
       k.data_ptr(), has_v ? v->data_ptr() : nullptr, k.stride(0), k.stride(1),
-      has_v ? v->stride(0) : 0, has_v ? v->stride(1) : 0, k_cache.data_ptr<int8_t>(),
-      has_v ? v_cache->data_ptr<int8_t>() : nullptr, k_cache_scale.data_ptr<float>(),
+      has_v ? v->stride(0) : 0, has_v ? v->stride(1) : 0, k_cache.data_ptr(),
+      has_v ? v_cache->data_ptr() : nullptr, k_cache_scale.data_ptr<float>(),
       has_v ? v_cache_scale->data_ptr<float>() : nullptr, slot_mapping.data_ptr<int32_t>(), T, H,
-      D, NB, BS, dt, stream_of(k));
+      D, NB, BS, dt, cdt, stream_of(k));
   check_status(st, "quant_to_paged_cache");
 }
 

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 5
+#define TMO_HIP_ABI_VERSION 6
 
 /* element types */
 enum tmo_dtype {
@@ -74,11 +74,12 @@ int tmo_hip_reshape_paged_cache(void* k, void* v,
                                 int dtype, int direction, void* stream);
 
 /*
- * quant_to_paged_cache -- dynamic per-(token, head) int8 quantisation of k/v[T, H, D] into
- * the paged caches: scale = fp32(max|row|) / 127 (IEEE), code = RNE(row / scale) clamped
- * to [-128, 127] (all-zero row: scale 0, codes 0); codes go to
- * cache[slot / block_size, h, slot % block_size, :] and the scale to the same [.., h, ..]
- * position of the scale pages.
+ * quant_to_paged_cache -- dynamic per-(token, head) quantisation of k/v[T, H, D] into the
+ * paged caches.  cache_dtype I8: scale = fp32(max|row|) / 127 (IEEE), code = RNE(row / scale)
+ * clamped to [-128, 127]; cache_dtype F8E4M3: scale = fp32(max|row|) / 448, code =
+ * e4m3fn_RNE(clip(row / scale, -448, 448)); an all-zero row gives scale 0 and codes 0.
+ * Codes go to cache[slot / block_size, h, slot % block_size, :] and the scale to the same
+ * [.., h, ..] position of the scale pages.
  * Replaces tmo::torch_api::quant_to_paged_cache (reference include/torch_mlu_ops.h:176-182),
  * called by torch_mlu_ops.quant_to_paged_cache (reference _ops.py:1511-1565).
  * dtype: F32, F16 or BF16 (of k and v).  v, v_cache, v_cache_scale: all NULL or all set.
@@ -86,12 +87,12 @@ int tmo_hip_reshape_paged_cache(void* k, void* v,
 int tmo_hip_quant_to_paged_cache(const void* k, const void* v,
                                  int64_t k_stride_token, int64_t k_stride_head,
                                  int64_t v_stride_token, int64_t v_stride_head,
-                                 int8_t* k_cache, int8_t* v_cache,
+                                 void* k_cache, void* v_cache,
                                  float* k_cache_scale, float* v_cache_scale,
                                  const int32_t* slot_mapping,
                                  int64_t num_tokens, int64_t num_heads, int64_t head_size,
                                  int64_t num_blocks, int64_t block_size,
-                                 int dtype, void* stream);
+                                 int dtype, int cache_dtype, void* stream);
 
 /*
  * offline_quant_to_paged_cache -- static quantisation of k/v[T, H, D] into the paged caches

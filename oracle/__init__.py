@@ -43,7 +43,7 @@ def lib() -> ctypes.CDLL:
             build()
         L = ctypes.CDLL(str(LIB_PATH))
         L.oracle_quant_to_paged_cache.argtypes = [c_void_p, c_void_p, c_int] + [c_int64] * 4 + \
-            [c_void_p] * 5 + [c_int64] * 5 + [c_int]
+            [c_void_p] * 5 + [c_int64] * 5 + [c_int, c_int]
         L.oracle_reshape_paged_cache.argtypes = [c_void_p, c_void_p, c_int] + [c_int64] * 4 + \
             [c_void_p] * 3 + [c_int64] * 5 + [c_int, c_int]
         L.oracle_dequant_from_paged_cache.argtypes = [c_void_p, c_void_p, c_int] + [c_int64] * 5 + \
@@ -101,7 +101,8 @@ def _check(rc: int, name: str) -> None:
 
 def quant_to_paged_cache(k, v, k_cache, v_cache, k_scale, v_scale, slot_mapping,
                          nthreads: Optional[int] = None) -> None:
-    """reference _ops.py:1511-1565 (see tmo_oracle.c); in place on CPU tensors."""
+    """reference _ops.py:1511-1565 (see tmo_oracle.c); in place on CPU tensors; int8 or
+    torch.float8_e4m3fn caches."""
     assert k.stride(2) == 1 and k_cache.is_contiguous() and k_scale.is_contiguous()
     T, H, D = k.shape
     NB, _, BS, _ = k_cache.shape
@@ -110,7 +111,8 @@ def quant_to_paged_cache(k, v, k_cache, v_cache, k_scale, v_scale, slot_mapping,
         _ptr(k), _ptr(v), _DT[k.dtype], k.stride(0), k.stride(1),
         v.stride(0) if v is not None else 0, v.stride(1) if v is not None else 0,
         _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
-        _ptr(slots), T, H, D, NB, BS, nthreads or default_threads())
+        _ptr(slots), T, H, D, NB, BS, {torch.int8: 3, torch.float8_e4m3fn: 4}[k_cache.dtype],
+        nthreads or default_threads())
     _check(rc, "quant_to_paged_cache")
 
 

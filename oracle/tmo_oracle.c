@@ -252,23 +252,47 @@ static float quant_row(const float* x, int64_t n, int8_t* codes) {
     return scale;
 }
 
+/* One row / group of n values -> codes (int8 bytes, or e4m3fn bytes with scale = RN(amax / 448)
+ * and codes e4m3fn_RNE(clip(RN(x / scale), -448, 448))) + fp32 scale (_ops.py:1524-1537,
+ * 1728-1745). */
+static float quant_group(const float* x, int64_t n, uint8_t* codes, int cache_dtype) {
+    if (cache_dtype == DT_I8) return quant_row(x, n, (int8_t*)codes);
+    float amax = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        float a = fabsf(x[i]);
+        if (a > amax) amax = a;
+    }
+    float scale = amax / 448.0f;                           /* IEEE divide */
+    if (scale == 0.0f) {                                   /* as D3 */
+        memset(codes, 0, (size_t)n);
+        return scale;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        float q = x[i] / scale;
+        if (q < -448.0f) q = -448.0f;                      /* clip(key_i, -448, 448) */
+        if (q > 448.0f) q = 448.0f;
+        codes[i] = f32_to_e4m3(q);
+    }
+    return scale;
+}
+
 /* ------------------------------------------------------------------ quant_to_paged_cache */
 
 typedef struct {
     const void* src[2];
     int64_t st[2], sh[2];
-    int8_t* cache[2];
+    uint8_t* cache[2];
     float* scale[2];
     int nkv;
     const int32_t* slot;
     int64_t T, H, D, NB, BS;
-    int dtype;
+    int dtype, cache_dtype;
 } qpc_ctx;
 
 static void qpc_range(void* p, int64_t lo, int64_t hi) {
     qpc_ctx* c = (qpc_ctx*)p;
     float* row = (float*)malloc((size_t)c->D * sizeof(float));
-    int8_t* codes = (int8_t*)malloc((size_t)c->D);
+    uint8_t* codes = (uint8_t*)malloc((size_t)c->D);
     for (int64_t t = lo; t < hi; ++t) {
         int64_t slot = c->slot[t];
         if (slot < 0 || slot >= c->NB * c->BS) continue;            /* D4 */
@@ -277,7 +301,7 @@ static void qpc_range(void* p, int64_t lo, int64_t hi) {
             for (int64_t h = 0; h < c->H; ++h) {
                 int64_t base = t * c->st[kv] + h * c->sh[kv];
                 for (int64_t d = 0; d < c->D; ++d) row[d] = load_elem(c->src[kv], base + d, c->dtype);
-                float s = quant_row(row, c->D, codes);
+                float s = quant_group(row, c->D, codes, c->cache_dtype);
                 int64_t page_row = (blk * c->H + h) * c->BS + off;   /* [NB, H, BS] */
                 memcpy(c->cache[kv] + page_row * c->D, codes, (size_t)c->D);
                 c->scale[kv][page_row] = s;
@@ -290,16 +314,18 @@ static void qpc_range(void* p, int64_t lo, int64_t hi) {
 
 /* _ops.py:1511-1565: quant_to_paged_cache(k, v, k_cache, v_cache, k_scale, v_scale, slot_mapping)
  * k/v [T, H, D] with element strides (token, head), last dim contiguous;
- * caches [NB, H, BS, D] int8 contiguous; scales [NB, H, BS] fp32 contiguous. v may be NULL. */
+ * caches [NB, H, BS, D] int8 or float8_e4m3fn (cache_dtype) contiguous; scales [NB, H, BS] fp32
+ * contiguous. v may be NULL. */
 int oracle_quant_to_paged_cache(const void* k, const void* v, int dtype,
                                 int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh,
-                                int8_t* k_cache, int8_t* v_cache, float* k_scale, float* v_scale,
+                                void* k_cache, void* v_cache, float* k_scale, float* v_scale,
                                 const int32_t* slot_mapping, int64_t T, int64_t H, int64_t D,
-                                int64_t NB, int64_t BS, int nthreads) {
+                                int64_t NB, int64_t BS, int cache_dtype, int nthreads) {
     if (elem_size(dtype) == 0 || dtype == DT_I8) return -2;
+    if (cache_dtype != DT_I8 && cache_dtype != DT_F8E4M3) return -2;
     if (T < 0 || H <= 0 || D <= 0 || NB < 0 || BS <= 0) return -1;
-    qpc_ctx c = {{k, v}, {k_st, v_st}, {k_sh, v_sh}, {k_cache, v_cache}, {k_scale, v_scale},
-                 v ? 2 : 1, slot_mapping, T, H, D, NB, BS, dtype};
+    qpc_ctx c = {{k, v}, {k_st, v_st}, {k_sh, v_sh}, {(uint8_t*)k_cache, (uint8_t*)v_cache},
+                 {k_scale, v_scale}, v ? 2 : 1, slot_mapping, T, H, D, NB, BS, dtype, cache_dtype};
     parallel_for(T, nthreads, qpc_range, &c);
     return 0;
 }
@@ -520,28 +546,6 @@ int oracle_fused_rope_paged(void* qkv, int dtype, int64_t T, int64_t S, int64_t 
 }
 
 /* ------------------------------------------------------------------ linear caches (D11) */
-
-/* One group of n values -> codes (int8 bytes or e4m3fn bytes) + fp32 scale (_ops.py:1728-1745). */
-static float quant_group(const float* x, int64_t n, uint8_t* codes, int cache_dtype) {
-    if (cache_dtype == DT_I8) return quant_row(x, n, (int8_t*)codes);
-    float amax = 0.0f;
-    for (int64_t i = 0; i < n; ++i) {
-        float a = fabsf(x[i]);
-        if (a > amax) amax = a;
-    }
-    float scale = amax / 448.0f;                           /* IEEE divide */
-    if (scale == 0.0f) {                                   /* as D3 */
-        memset(codes, 0, (size_t)n);
-        return scale;
-    }
-    for (int64_t i = 0; i < n; ++i) {
-        float q = x[i] / scale;
-        if (q < -448.0f) q = -448.0f;                      /* clip(key_i, -448, 448) */
-        if (q > 448.0f) q = 448.0f;
-        codes[i] = f32_to_e4m3(q);
-    }
-    return scale;
-}
 
 typedef struct {
     int64_t batch, H, D, cache_batch, cache_len, rows;   /* rows: input / output tensor rows */

@@ -11,8 +11,9 @@
 //   static: the static-scale quotient (static_quotients, per-element lane logic) for random
 //          scales 2^-60 <= |s| <= 2^100 of both signs, against x with quotients spread over
 //          2^-40 .. 2^24, within +-3 ulps of int8 ties (k + 0.5) * s and of fp8 e4m3 ties
-//          m * s, and near |x| = 2^-100; the int8 code and the fp8 code must always match,
-//          the quotient bits whenever |x| >= 2^-100 and the IEEE quotient is normal.
+//          m * s, near |x| = 2^-100, and +-0; the int8 code and the fp8 code (with the sign
+//          of a zero quotient put back, as the fp8 paths do) must always match, the quotient
+//          bits whenever |x| >= 2^-100 and the IEEE quotient is normal, or x is zero.
 //   fp8:   fp8e4m3_bits against a nearest-value search over the 127 positive e4m3 values
 //          (ties to the even code) for EVERY fp32 value in [-448, 448].
 //
@@ -190,7 +191,7 @@ static Count run_static(unsigned long long n, int nthreads) {
         const float s = f_from_bits(sign | (e << 23) | (uint32_t)(rng() & 0x7fffff));
         if (!tmo::static_scale_fast(s)) continue;
         const float y = 1.0f / s;
-        float xs[16];
+        float xs[20];
         int nx = 0;
         // quotient magnitude log-uniform in 2^-40 .. 2^24, either sign
         const double lq = -40.0 + 64.0 * (double)(rng() >> 11) / 9007199254740992.0;
@@ -204,18 +205,22 @@ static Count run_static(unsigned long long n, int nthreads) {
         const float t1 = (float)(mid * (double)s);
         for (int d = 0; d < 7; ++d) xs[nx++] = f_from_bits(bits_of(t1) + (uint32_t)(d - 3));
         xs[nx++] = f_from_bits(bits_of(0x1p-100f) + (uint32_t)(rng() % 64)) * ((rng() & 1) ? -1.0f : 1.0f);
+        xs[nx++] = 0.0f;
+        xs[nx++] = -0.0f;
         for (int j = 0; j < nx; ++j) {
           const float x = xs[j];
           if (!std::isfinite(x)) continue;
-          float q;
+          float q, qs;
           tmo::static_quotients<1>(&x, &s, &y, true, &q);
+          tmo::static_quotients<1, true>(&x, &s, &y, true, &qs);  // the fp8 paths' quotient
           const float r = x / s;
           ++c.checked;
-          const bool bad = code_of(q) != code_of(r) || fp8_of(q) != fp8_of(r) ||
-                           (std::fabs(x) >= 0x1p-100f && std::fabs(r) >= 0x1p-126f &&
-                            bits_of(q) != bits_of(r));
+          const bool exact = std::fabs(x) >= 0x1p-100f && std::fabs(r) >= 0x1p-126f;
+          const bool bad = code_of(q) != code_of(r) || fp8_of(qs) != fp8_of(r) ||
+                           (exact && bits_of(q) != bits_of(r)) ||
+                           ((exact || x == 0.0f) && bits_of(qs) != bits_of(r));
           if (bad) {
-            if (c.bad < 5) std::printf("static mismatch s=%a x=%a fast=%a ieee=%a\n", s, x, q, r);
+            if (c.bad < 5) std::printf("static mismatch s=%a x=%a fast=%a ieee=%a\n", s, x, qs, r);
             ++c.bad;
           }
         }

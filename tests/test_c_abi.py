@@ -32,7 +32,7 @@ def lib():
     from domesticated_torch_mlu_ops_amd import _loader
     L = _loader.c_abi()
     L.tmo_hip_status_string.restype = ctypes.c_char_p
-    L.tmo_hip_quant_to_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 5 + [I64] * 5 + [INT, P]
+    L.tmo_hip_quant_to_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 5 + [I64] * 5 + [INT, INT, P]
     L.tmo_hip_reshape_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 3 + [I64] * 5 + [INT, INT, P]
     L.tmo_hip_dequant_from_paged_cache.argtypes = [P, P] + [I64] * 5 + [P] * 7 + [I64] * 7 + \
         [INT, INT, INT, P]
@@ -89,13 +89,15 @@ EMODE = -3
 
 
 def quant(lib, k=FAKE, v=None, kc=FAKE, vc=None, ks=FAKE, vs=None, slot=FAKE, T=4, H=8, D=128,
-          NB=4, BS=16, dtype=2, st=1024, sh=128):
+          NB=4, BS=16, dtype=2, st=1024, sh=128, cdt=3):
     return lib.tmo_hip_quant_to_paged_cache(k, v, st, sh, st, sh, kc, vc, ks, vs, slot, T, H, D,
-                                            NB, BS, dtype, None)
+                                            NB, BS, dtype, cdt, None)
 
 
 def test_quant_validation(lib):
     assert quant(lib, dtype=3) == EDTYPE          # int8 input
+    assert quant(lib, cdt=2) == EDTYPE            # bf16 cache
+    assert quant(lib, cdt=4, T=0) == 0            # float8_e4m3fn cache
     assert quant(lib, dtype=9) == EDTYPE
     assert quant(lib, k=None) == EINVAL
     assert quant(lib, slot=None) == EINVAL

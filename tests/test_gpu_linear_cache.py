@@ -153,6 +153,27 @@ def test_quant_to_linear_cache_extreme_rows(tmo, ref, dev):
             _quant_both(tmo, ref, dev, case, cdt)
 
 
+def _with_signed_zeros(case):
+    """Rows of both signs of zero among ordinary values: the IEEE quotient -0 / s is -0, the
+    float8_e4m3fn byte 0x80 (int8 codes are 0 either way)."""
+    k = case.key.clone()
+    k[0::3, ..., ::2] = -0.0
+    k[1::3, ..., 1::3] = 0.0
+    k[2::7] = -0.0
+    case.key = k
+    return case
+
+
+@pytest.mark.parametrize("dtype", FLOATS)
+def test_linear_signed_zeros(tmo, ref, dev, dtype):
+    case = _with_signed_zeros(W.linear_case(dtype, 44, packed=True, offsets=True, S=12))
+    for cdt in (torch.int8, torch.float8_e4m3fn):
+        _quant_both(tmo, ref, dev, case, cdt)
+        _quant_both(tmo, ref, dev, case, cdt, groups=4)
+    for mode in (0, 1, 2):
+        _offline_both(tmo, ref, dev, case, torch.float8_e4m3fn, mode)
+
+
 # ---------------------------------------------------------------------------- offline (static)
 
 def _static_scales(H, D, L, smode, g):

@@ -16,6 +16,8 @@ pytestmark = pytest.mark.gpu
 
 def _bits(t: torch.Tensor) -> torch.Tensor:
     t = t.detach().cpu().contiguous()
+    if t.dtype == torch.float8_e4m3fn:
+        return t.view(torch.uint8)
     if t.dtype == torch.float32:
         return t.view(torch.int32)
     if t.dtype in (torch.float16, torch.bfloat16):
@@ -36,15 +38,19 @@ def assert_bits_equal(got: torch.Tensor, want: torch.Tensor, what: str) -> None:
 
 # ---------------------------------------------------------------------------- quant_to_paged_cache
 
-def run_quant(tmo, ref, dev, case: W.PagedQuantCase, with_v=True, k=None, v=None):
-    """GPU op and oracle on the same inputs; returns (gpu caches, oracle caches)."""
+def run_quant(tmo, ref, dev, case: W.PagedQuantCase, with_v=True, k=None, v=None,
+              cache_dtype=torch.int8):
+    """GPU op and oracle on the same inputs; returns (gpu caches, oracle caches).  fp8 caches
+    start from the same sentinel bytes as int8 ones."""
     k = case.k if k is None else k
     v = (case.v if v is None else v) if with_v else None
     kc, vc, ks, vs = case.empty_caches()
+    kc, vc = kc.view(cache_dtype), vc.view(cache_dtype)
     if not with_v:
         vc = vs = None
     ref.quant_to_paged_cache(k, v, kc, vc, ks, vs, case.slot_mapping)
     gk, gv, gks, gvs = case.empty_caches(device=dev)
+    gk, gv = gk.view(cache_dtype), gv.view(cache_dtype)
     kd = k.to(dev)
     vd = v.to(dev) if v is not None else None
     if not with_v:
@@ -55,8 +61,8 @@ def run_quant(tmo, ref, dev, case: W.PagedQuantCase, with_v=True, k=None, v=None
     return (gk, gv, gks, gvs), (kc, vc, ks, vs)
 
 
-def check_quant(tmo, ref, dev, case, with_v=True, k=None, v=None):
-    got, want = run_quant(tmo, ref, dev, case, with_v, k, v)
+def check_quant(tmo, ref, dev, case, with_v=True, k=None, v=None, cache_dtype=torch.int8):
+    got, want = run_quant(tmo, ref, dev, case, with_v, k, v, cache_dtype)
     for g, w, n in zip(got, want, ("k_cache", "v_cache", "k_scale", "v_scale")):
         if w is not None:
             assert_bits_equal(g, w, f"{case.name} {n}")
@@ -71,6 +77,30 @@ def test_quant_to_paged_cache_configs(tmo, ref, dev, cfg):
     # every valid token wrote its codes; skipped slots kept the sentinel
     written = (want[2] != W.SCALE_SENTINEL).sum().item()
     assert written == case.valid_tokens() * case.k.shape[1]
+
+
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3"])
+def test_quant_to_paged_cache_fp8_configs(tmo, ref, dev, cfg):
+    """The float8_e4m3fn cache branch of the same op (scale = amax / 448) on every config."""
+    case = getattr(W, cfg)()
+    print(f"[quant_to_paged_cache fp8] {cfg} T={case.tokens}", flush=True)
+    check_quant(tmo, ref, dev, case, cache_dtype=torch.float8_e4m3fn)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D,BS", [(8, 16), (64, 16), (128, 16), (512, 16), (128, 7), (72, 5)])
+def test_quant_fp8_widths_and_generic(tmo, ref, dev, dtype, D, BS):
+    case = _case(f"fp8 D={D} BS={BS}", 61, 3, D, 40, BS, dtype, seed=3 * D + BS, neg_frac=0.1,
+                 oob=2)
+    k = case.k.to(torch.float32)
+    k[0] = 0                                                                # zero row
+    k[1] *= 1e-25 if dtype != torch.float16 else 1e-6                       # tiny scales
+    k[2] *= 1e25 if dtype != torch.float16 else 1e3                         # huge (finite)
+    k[3, :, ::3] = -0.0                                                     # signed zeros:
+    k[4, :, 1::2] = 0.0                                                     # fp8 0x80 / 0x00
+    k = k.to(dtype)
+    check_quant(tmo, ref, dev, case, k=k, cache_dtype=torch.float8_e4m3fn)
+    check_quant(tmo, ref, dev, case, k=k, with_v=False, cache_dtype=torch.float8_e4m3fn)
 
 
 def _case(name, T, H, D, NB, BS, dtype, seed, neg_frac=0.0, oob=0):
@@ -228,6 +258,8 @@ def test_offline_quant_scale_ranges(tmo, ref, dev):
     ks[0, :8] = 1e-20               # below 2^-60
     ks[1, 8:16] = 3e33              # above 2^100
     ks[2, 16:24] *= -1              # negative
+    k[11, :, ::2] = -0.0            # signed zeros (fp8 codes 0x80 / 0x00, by the scale's sign)
+    k[12, :, 1::2] = 0.0
     for cdt in CACHE_DTYPES:
         for dtype in (torch.float32, torch.bfloat16):
             kk = k.to(dtype)

@@ -84,6 +84,41 @@ def test_quant_matches_torch_docstring_math(ref, dtype):
             assert torch.equal(bits(a), bits(b))
 
 
+def torch_quant_to_paged_fp8(k, v, kc, vc, ks, vs, slot):
+    """The fp8 branch of _ops.py:1524-1537 by torch: scale = fp32(amax) / 448, codes =
+    float8_e4m3fn(clip(x / scale, -448, 448)) (the clip of the linear sibling, _ops.py:1741);
+    all-zero rows: scale 0, codes 0."""
+    NB, H, BS, D = kc.shape
+    valid = (slot >= 0) & (slot < NB * BS)
+    s = slot[valid].long()
+    blk, off = s // BS, s % BS
+    for x, c, sc in ((k, kc, ks), (v, vc, vs)):
+        if x is None:
+            continue
+        xv = x[valid]
+        scale = xv.abs().amax(-1).to(torch.float32) / 448.0
+        q = (xv.to(torch.float32) / scale[..., None]).clamp(-448, 448)
+        q = torch.where(scale[..., None] == 0, torch.zeros_like(q), q)
+        c.view(torch.uint8).permute(0, 2, 1, 3)[blk, off] = q.to(torch.float8_e4m3fn).view(torch.uint8)
+        sc.permute(0, 2, 1)[blk, off] = scale
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_quant_fp8_matches_torch_docstring_math(ref, dtype):
+    for seed in range(3):
+        case = _rand_case(dtype, seed=seed)
+        kc, vc, ks, vs = case.empty_caches()
+        kc, vc = kc.view(torch.float8_e4m3fn), vc.view(torch.float8_e4m3fn)
+        ref.quant_to_paged_cache(case.k, case.v, kc, vc, ks, vs, case.slot_mapping)
+        tk, tv, tks, tvs = case.empty_caches()
+        tk, tv = tk.view(torch.float8_e4m3fn), tv.view(torch.float8_e4m3fn)
+        torch_quant_to_paged_fp8(case.k, case.v, tk, tv, tks, tvs, case.slot_mapping)
+        for a, b in ((kc, tk), (vc, tv)):
+            assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+        for a, b in ((ks, tks), (vs, tvs)):
+            assert torch.equal(bits(a), bits(b))
+
+
 def test_quant_cfg1_and_cfg2_match_torch(ref):
     for case in (W.cfg1(), W.cfg2()):
         kc, vc, ks, vs = case.empty_caches()
