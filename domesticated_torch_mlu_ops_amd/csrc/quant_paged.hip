@@ -58,6 +58,9 @@ __device__ __forceinline__ bool locate_slot(const QuantPagedParams& p, int32_t s
 #ifndef TMO_QUANT_TOKENS_PER_THREAD
 #define TMO_QUANT_TOKENS_PER_THREAD 1
 #endif
+#ifndef TMO_QUANT_XCD
+#define TMO_QUANT_XCD 1
+#endif
 #ifndef TMO_QUANT_VEC_PER_LANE
 #define TMO_QUANT_VEC_PER_LANE 1
 #endif
@@ -75,9 +78,17 @@ __global__ __launch_bounds__(256) void quant_paged_vec(QuantPagedParams p) {
   constexpr int kPer = Tag::kPerVec;
   constexpr int kT = kTokensPerThread;
   const int lane = threadIdx.x & (G - 1);
+#if TMO_QUANT_XCD
+  // XCD-aware order: the tile's per-token scale lines (64 bytes of each of two heads in one
+  // 128-byte line for block size 16) are written whole from one L2
+  int h;
+  int64_t tile;
+  xcd_tile_head(blockIdx.x, p.heads, h, tile);
+#else
   // blockIdx.x = token_tile * heads + head (workgroup-uniform, scalar ALU)
   const int h = blockIdx.x % p.heads;
   const int64_t tile = blockIdx.x / p.heads;
+#endif
   const int64_t t0 = tile * (kGroups * kT) + threadIdx.x / G;
 
   int32_t slot[kT];
@@ -205,8 +216,14 @@ __global__ __launch_bounds__(256) void quant_paged_static_vec(StaticParams sp) {
   constexpr int kPer = Tag::kPerVec;
   constexpr int kT = TMO_STATIC_TOKENS_PER_THREAD;
   const int lane = threadIdx.x & (G - 1);
+#if TMO_QUANT_XCD
+  int h;
+  int64_t tile;
+  xcd_tile_head(blockIdx.x, p.heads, h, tile);
+#else
   const int h = blockIdx.x % p.heads;
   const int64_t tile = blockIdx.x / p.heads;
+#endif
   const int64_t t0 = tile * (kGroups * kT) + threadIdx.x / G;
 
   float s[2][kPer];
@@ -341,9 +358,13 @@ int launch_static(const StaticParams& sp, hipStream_t stream) {
   const int rows = vec ? (256 / G) * TMO_STATIC_TOKENS_PER_THREAD : 256 / kWave;
   const int64_t tiles = (p.num_tokens + rows - 1) / rows;
   const int64_t blocks = tiles * p.heads;
-  if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
-  const dim3 grid((unsigned)blocks), block(256);
-  if (!vec) return launch_kernel(quant_paged_static_generic<Tag, kFp8>, grid, block, stream, sp);
+  const int64_t vec_blocks = TMO_QUANT_XCD ? xcd_grid_tiles(tiles) * p.heads : blocks;
+  if (vec_blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
+  const dim3 block(256);
+  if (!vec)
+    return launch_kernel(quant_paged_static_generic<Tag, kFp8>, dim3((unsigned)blocks), block,
+                         stream, sp);
+  const dim3 grid((unsigned)vec_blocks);
   switch (G) {
     case 1: return launch_kernel(quant_paged_static_vec<Tag, 1, kFp8>, grid, block, stream, sp);
     case 2: return launch_kernel(quant_paged_static_vec<Tag, 2, kFp8>, grid, block, stream, sp);
@@ -386,9 +407,13 @@ int launch(const QuantPagedParams& p, hipStream_t stream) {
   const int rows = vec ? (256 / G) * kTokensPerThread : 256 / kWave;
   const int64_t tiles = (p.num_tokens + rows - 1) / rows;
   const int64_t blocks = tiles * p.heads;
-  if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
-  const dim3 grid((unsigned)blocks), block(256);
-  if (!vec) return launch_kernel(quant_paged_generic<Tag, kFp8>, grid, block, stream, p);
+  // the vector kernel's XCD-aware order takes whole groups of 8 tiles (extra tiles have no
+  // tokens and write nothing)
+  const int64_t vec_blocks = TMO_QUANT_XCD ? xcd_grid_tiles(tiles) * p.heads : blocks;
+  if (vec_blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
+  const dim3 block(256);
+  if (!vec) return launch_kernel(quant_paged_generic<Tag, kFp8>, dim3((unsigned)blocks), block, stream, p);
+  const dim3 grid((unsigned)vec_blocks);
   if (V == 1) return launch_vec<Tag, 1, kFp8>(p, G, grid, block, stream);
   return launch_vec<Tag, TMO_QUANT_VEC_PER_LANE, kFp8>(p, G, grid, block, stream);
 }

@@ -51,8 +51,9 @@ __global__ __launch_bounds__(256) void reshape_paged_kernel(ReshapeParams p) {
   const int G = 1 << p.g_shift;
   const int lane = threadIdx.x & (G - 1);
   const int rows = 256 >> p.g_shift;
-  const int h = blockIdx.x % p.heads;
-  const int64_t tile = blockIdx.x / p.heads;
+  int h;
+  int64_t tile;
+  xcd_tile_head(blockIdx.x, p.heads, h, tile);  // the grid holds whole groups of 8 tiles
   const int64_t t = tile * rows + (threadIdx.x >> p.g_shift);
   if (t >= p.num_tokens) return;
   const int32_t slot = p.slot[t];
@@ -83,7 +84,7 @@ int launch(const ReshapeParams& p0, hipStream_t stream) {
   while (g * 2 <= p.units && g < 64) g *= 2;
   p.g_shift = ilog2_if_pow2(g);
   const int rows = 256 / g;
-  const int64_t blocks = ((p.num_tokens + rows - 1) / rows) * p.heads;
+  const int64_t blocks = xcd_grid_tiles((p.num_tokens + rows - 1) / rows) * p.heads;
   if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
   return launch_kernel(reshape_paged_kernel<VW>, dim3((unsigned)blocks), dim3(256), stream, p);
 }

@@ -7,6 +7,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <stdint.h>
 
 #include "tmo_hip.h"
@@ -17,6 +19,21 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
+// MI355X: 8 XCDs of 32 CUs, each with its own L2; workgroups are dispatched round-robin over
+// them, so workgroup b runs on XCD b % kXcds.
+constexpr int kXcds = 8;
+
+// XCD-aware (token tile, head) of workgroup b for kernels whose grid is tiles x heads: the
+// heads of one tile run on one XCD (slot = b / 8, head = slot % heads, tile = 8 * (slot /
+// heads) + b % 8), so a tile's bytes meet in one L2 -- per-token scale lines shared by
+// neighbouring heads are written or read whole, and the tile's rows go to HBM from one XCD.
+// The grid must hold a whole number of groups of 8 tiles (xcd_grid_tiles).
+__device__ __forceinline__ void xcd_tile_head(uint32_t b, int heads, int& h, int64_t& tile) {
+  const uint32_t slot = b / kXcds;
+  h = (int)(slot % (uint32_t)heads);
+  tile = (int64_t)(slot / (uint32_t)heads) * kXcds + b % kXcds;
+}
+inline int64_t xcd_grid_tiles(int64_t tiles) { return (tiles + kXcds - 1) / kXcds * kXcds; }
 
 // ---------------------------------------------------------------------------- element types
 
@@ -441,6 +458,20 @@ inline int launch_kernel(void (*kernel)(Params), dim3 grid, dim3 block, hipStrea
   void* args[] = {&copy};
   const hipError_t e =
       hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, args, shared_bytes, stream);
+  return e == hipSuccess ? TMO_OK : TMO_ERR_LAUNCH;
+}
+
+// Kernels of three parameters (the params struct and two pointers); the argument types are
+// taken from the kernel (non-deduced), so pointers convert to the kernel's const-qualified ones.
+template <class A, class B, class C>
+inline int launch_kernel(void (*kernel)(A, B, C), dim3 grid, dim3 block, hipStream_t stream,
+                         const typename std::common_type<A>::type& a,
+                         typename std::common_type<B>::type b,
+                         typename std::common_type<C>::type c) {
+  A a_copy = a;
+  void* args[] = {&a_copy, &b, &c};
+  const hipError_t e =
+      hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, args, 0, stream);
   return e == hipSuccess ? TMO_OK : TMO_ERR_LAUNCH;
 }
 

@@ -414,6 +414,10 @@ void dequant_from_paged_cache(at::Tensor& key, const c10::optional<at::Tensor>& 
   TORCH_CHECK(max_ctx >= 0, "max_context_len must be >= 0");
   if (B == 0 || key.size(0) == 0) return;
   c10::DeviceGuard guard(key.device());
+  const int64_t ws_bytes =
+      tmo_hip_dequant_workspace_bytes(B, block_tables.size(1), max_ctx, BS);
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({ws_bytes}, key.options().dtype(at::kByte));
   const int st = tmo_hip_dequant_from_paged_cache(
       key.data_ptr(), has_v ? value->data_ptr() : nullptr, key.stride(0), key.stride(1),
       has_v ? value->stride(0) : 0, has_v ? value->stride(1) : 0, key.size(0),
@@ -423,7 +427,8 @@ void dequant_from_paged_cache(at::Tensor& key, const c10::optional<at::Tensor>& 
       context_lengths.data_ptr<int32_t>(),
       context_seq_offset ? context_seq_offset->data_ptr<int32_t>() : nullptr,
       block_tables.data_ptr<int32_t>(), B, block_tables.size(1), max_ctx, NB, H, BS, D,
-      (int)quant_mode, (int)quant_bit, dt, stream_of(key));
+      (int)quant_mode, (int)quant_bit, dt, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
+      stream_of(key));
   check_status(st, "dequant_from_paged_cache");
 }
 

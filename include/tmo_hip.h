@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 6
+#define TMO_HIP_ABI_VERSION 7
 
 /* element types */
 enum tmo_dtype {
@@ -162,6 +162,11 @@ int tmo_hip_fused_rope_paged(void* qkv, int64_t num_tokens, int64_t seq_len,
  * Replaces tmo::torch_api::dequant_from_paged_cache (reference include/torch_mlu_ops.h:650-661),
  * called by torch_mlu_ops.dequant_from_paged_cache (reference _ops.py:3734-3824).
  * out_dtype: F16, BF16 (or F32).  value, value_cache, value_scale: all NULL or all set.
+ * `workspace`: NULL (workspace_bytes 0), or device memory of at least
+ * tmo_hip_dequant_workspace_bytes(...) bytes, 16-byte aligned, used by this call only (calls
+ * that share one workspace must be ordered on a stream).  With it the call runs as a small
+ * page-list kernel followed by the main kernel, which is the faster layout on MI355X; without
+ * it (or with a smaller one) a single kernel runs.  The results are identical.
  */
 int tmo_hip_dequant_from_paged_cache(void* key, void* value,
                                      int64_t key_stride_token, int64_t key_stride_head,
@@ -177,7 +182,14 @@ int tmo_hip_dequant_from_paged_cache(void* key, void* value,
                                      int64_t num_blocks, int64_t num_heads,
                                      int64_t block_size, int64_t head_size,
                                      int quant_mode, int quant_bit, int out_dtype,
-                                     void* stream);
+                                     void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes for tmo_hip_dequant_from_paged_cache's page-list path: 16 + 16 per page the
+ * call can cover (batch * min(ceil(max_context_len / block_size), max_blocks_per_seq), rounded
+ * up to a multiple of 8); 0 when there is nothing to do.  No reference counterpart (the MLU
+ * kernels take none). */
+int64_t tmo_hip_dequant_workspace_bytes(int64_t batch, int64_t max_blocks_per_seq,
+                                        int64_t max_context_len, int64_t block_size);
 
 /*
  * scaled_quantize_per_token -- "dynamic_per_token" int8 quantisation with an optional smooth

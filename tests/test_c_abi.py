@@ -35,7 +35,9 @@ def lib():
     L.tmo_hip_quant_to_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 5 + [I64] * 5 + [INT, INT, P]
     L.tmo_hip_reshape_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 3 + [I64] * 5 + [INT, INT, P]
     L.tmo_hip_dequant_from_paged_cache.argtypes = [P, P] + [I64] * 5 + [P] * 7 + [I64] * 7 + \
-        [INT, INT, INT, P]
+        [INT, INT, INT, P, I64, P]
+    L.tmo_hip_dequant_workspace_bytes.argtypes = [I64] * 4
+    L.tmo_hip_dequant_workspace_bytes.restype = I64
     L.tmo_hip_scaled_quantize_per_token.argtypes = [P] + [I64] * 4 + [P] * 3 + [I64, P, I64, P, I64, P, I64, INT, P]
     L.tmo_hip_fused_rope_paged.argtypes = [P] + [I64] * 5 + [P, P] + [I64] * 4 + [P, I64, P, P] + \
         [ctypes.c_float] + [P] * 4 + [INT, P, I64, I64, INT, P]
@@ -63,7 +65,8 @@ def test_every_declared_symbol_is_exported(lib):
     names = declared_functions()
     assert set(names) == {"tmo_hip_abi_version", "tmo_hip_status_string",
                           "tmo_hip_reshape_paged_cache", "tmo_hip_quant_to_paged_cache",
-                          "tmo_hip_dequant_from_paged_cache", "tmo_hip_scaled_quantize_per_token",
+                          "tmo_hip_dequant_from_paged_cache", "tmo_hip_dequant_workspace_bytes",
+                          "tmo_hip_scaled_quantize_per_token",
                           "tmo_hip_offline_quant_to_paged_cache", "tmo_hip_fused_rope_paged",
                           "tmo_hip_reshape_linear_cache", "tmo_hip_quant_to_linear_cache",
                           "tmo_hip_offline_quant_to_linear_cache",
@@ -125,10 +128,13 @@ def test_reshape_validation(lib):
 
 
 def test_dequant_validation(lib):
-    def call(mode=1, bit=8, dtype=2, key=FAKE, value=None, vc=None, vs=None, B=2, H=8, total=10):
+    def call(mode=1, bit=8, dtype=2, key=FAKE, value=None, vc=None, vs=None, B=2, H=8, total=10,
+             ws=None, ws_bytes=0):
         return lib.tmo_hip_dequant_from_paged_cache(
             key, value, 1024, 128, 1024, 128, total, FAKE, vc, FAKE, vs, FAKE, None, FAKE, B, 4,
-            64, 16, H, 16, 128, mode, bit, dtype, None)
+            64, 16, H, 16, 128, mode, bit, dtype, ws, ws_bytes, None)
+    assert call(ws_bytes=-1) == EINVAL
+    assert call(ws_bytes=64) == EINVAL          # bytes without a pointer
     assert call(mode=2) == EMODE
     assert call(bit=4) == EMODE
     assert call(dtype=3) == EDTYPE
@@ -138,6 +144,16 @@ def test_dequant_validation(lib):
     assert call(B=-1) == EINVAL
     assert call(B=0) == 0
     assert call(total=0) == 0
+
+
+def test_dequant_workspace_bytes(lib):
+    # 16-byte header + 16 bytes per page the call covers, batch * min(ceil(ctx / BS),
+    # max_blocks) rounded up to a multiple of 8
+    assert lib.tmo_hip_dequant_workspace_bytes(64, 2048, 32768, 16) == 16 + 16 * 64 * 2048
+    assert lib.tmo_hip_dequant_workspace_bytes(3, 4, 1000, 16) == 16 + 16 * 16
+    assert lib.tmo_hip_dequant_workspace_bytes(3, 100, 17, 16) == 16 + 16 * 8
+    assert lib.tmo_hip_dequant_workspace_bytes(0, 4, 64, 16) == 0
+    assert lib.tmo_hip_dequant_workspace_bytes(2, 4, 0, 16) == 0
 
 
 def test_scaled_quantize_validation(lib):

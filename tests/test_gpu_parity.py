@@ -465,7 +465,7 @@ def _small_layout(seed, B=5, NB=40, BS=16, H=4, D=128, max_ctx=100):
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("mode", [0, 1])
 @pytest.mark.parametrize("D,BS,H", [
-    (128, 16, 4), (64, 32, 4),   # persistent page-list kernel
+    (128, 16, 4), (64, 32, 4),   # page-list kernels (the op passes a workspace)
     (128, 16, 3), (64, 16, 1),   # per-page kernel (heads not a power of two / small pages)
     (80, 16, 4), (128, 12, 4),   # scalar kernel (head size / block size off the vector path)
 ])
@@ -493,6 +493,93 @@ def test_dequant_many_sequences(tmo, ref, dev):
         layout = W.DequantLayout(f"B={B}", ctx, bt, NB, BS)
         caches = (kc.to(dev), kc.to(dev), ks.to(dev), ks.to(dev))
         _dequant_both(tmo, ref, dev, layout, caches, torch.bfloat16, 1)
+
+
+@pytest.mark.parametrize("B", [64, 65])
+def test_dequant_batches_and_truncated_output(tmo, ref, dev, B):
+    """Empty and one-token sequences, a missing page, both scale modes, K only, fp32 output,
+    and fewer output rows than the context lengths sum (later rows are dropped)."""
+    g = torch.Generator().manual_seed(B)
+    ctx = torch.randint(0, 90, (B,), generator=g).to(torch.int32)
+    ctx[3], ctx[5], ctx[B - 1] = 0, 1, 0
+    NB, H, BS, D = 8 * B, 8, 16, 128
+    bt = torch.randperm(NB, generator=g)[: 6 * B].reshape(B, 6).to(torch.int32)
+    bt[7, 2] = -1                                   # a missing page inside a sequence
+    kc = torch.randint(-128, 128, (NB, H, BS, D), generator=g, dtype=torch.int8)
+    vc = torch.randint(-128, 128, (NB, H, BS, D), generator=g, dtype=torch.int8)
+    ks = torch.rand(NB, H, BS, generator=g) * 0.1
+    vs = torch.rand(NB, H, BS, generator=g) * 0.1
+    layout = W.DequantLayout(f"B={B}", ctx, bt, NB, BS)
+    caches = tuple(t.to(dev) for t in (kc, vc, ks, vs))
+    print(f"[dequant] fine/persistent B={B} sum(ctx)={layout.total_tokens}", flush=True)
+    _dequant_both(tmo, ref, dev, layout, caches, torch.bfloat16, 1)
+    _dequant_both(tmo, ref, dev, layout, caches, torch.float32, 1, with_v=False)
+    _dequant_both(tmo, ref, dev, layout, caches, torch.float16, 1, total=layout.total_tokens - 37)
+    chan = (torch.rand(H, D, generator=g) * 0.05).to(dev), (torch.rand(H, D, generator=g) * 0.05).to(dev)
+    _dequant_both(tmo, ref, dev, layout, (caches[0], caches[1]) + chan, torch.bfloat16, 0)
+
+
+def _dequant_c_abi(out_k, out_v, caches, layout, mode, seq_offset, max_ctx, workspace):
+    """tmo_hip_dequant_from_paged_cache through ctypes, with or without a workspace."""
+    import ctypes
+    from domesticated_torch_mlu_ops_amd import _loader
+    L = _loader.c_abi()
+    P, I64, INT = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    L.tmo_hip_dequant_from_paged_cache.argtypes = [P, P] + [I64] * 5 + [P] * 7 + [I64] * 7 + \
+        [INT, INT, INT, P, I64, P]
+    L.tmo_hip_dequant_workspace_bytes.argtypes = [I64] * 4
+    L.tmo_hip_dequant_workspace_bytes.restype = I64
+    kc, vc, ks, vs = caches
+    NB, H, BS, D = kc.shape
+    ctx = layout.context_lengths.to(out_k.device)
+    bt = layout.block_tables.to(out_k.device)
+    off = seq_offset.to(out_k.device) if seq_offset is not None else None
+    B, MB = bt.shape
+    ws, ws_bytes = None, 0
+    if workspace:
+        ws_bytes = L.tmo_hip_dequant_workspace_bytes(B, MB, max_ctx, BS)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=out_k.device)
+    dt = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[out_k.dtype]
+    torch.cuda.synchronize()
+    st = L.tmo_hip_dequant_from_paged_cache(
+        out_k.data_ptr(), out_v.data_ptr() if out_v is not None else None, out_k.stride(0),
+        out_k.stride(1), out_v.stride(0) if out_v is not None else 0,
+        out_v.stride(1) if out_v is not None else 0, out_k.shape[0], kc.data_ptr(),
+        vc.data_ptr() if out_v is not None else None, ks.data_ptr(),
+        vs.data_ptr() if out_v is not None else None, ctx.data_ptr(),
+        off.data_ptr() if off is not None else None, bt.data_ptr(), B, MB, max_ctx, NB, H, BS, D,
+        mode, 8, dt, ws.data_ptr() if ws is not None else None, ws_bytes, None)
+    torch.cuda.synchronize()
+    assert st == 0
+
+
+@pytest.mark.parametrize("B", [5, 70])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_dequant_workspace_and_single_kernel_paths_agree(tmo, ref, dev, B, mode):
+    """The C ABI without a workspace (one kernel: the persistent page-list kernel, or the
+    per-page one) and with one (page-list pre-pass + item kernel) write identical bytes, and
+    both match the oracle; with and without context_seq_offset."""
+    layout, (kc, vc, ks, vs) = _small_layout(seed=40 + B + mode, B=B, NB=8 * B)
+    if mode == 0:
+        g = torch.Generator().manual_seed(7)
+        ks, vs = torch.rand(4, 128, generator=g) * 0.05, torch.rand(4, 128, generator=g) * 0.05
+    caches = tuple(t.to(dev) for t in (kc, vc, ks, vs))
+    total = layout.total_tokens + 5
+    for off in (None, (torch.cumsum(layout.context_lengths, 0) - layout.context_lengths
+                       + 3).to(torch.int32)):
+        want_k = torch.full((total, 4, 128), -3.0).to(torch.bfloat16)
+        want_v = want_k.clone()
+        ref.dequant_from_paged_cache(want_k, want_v, kc, vc, ks, vs, layout.context_lengths, off,
+                                     layout.block_tables, mode)
+        for workspace in (False, True):
+            got_k = torch.full((total, 4, 128), -3.0, device=dev).to(torch.bfloat16)
+            got_v = got_k.clone()
+            print(f"[dequant c-abi] B={B} mode={mode} offsets={off is not None} "
+                  f"workspace={workspace}", flush=True)
+            _dequant_c_abi(got_k, got_v, caches, layout, mode, off, layout.max_context_len,
+                           workspace)
+            assert_bits_equal(got_k, want_k, f"B={B} ws={workspace} key")
+            assert_bits_equal(got_v, want_v, f"B={B} ws={workspace} value")
 
 
 def test_dequant_seq_offset_invalid_blocks_and_extreme_scales(tmo, ref, dev):
