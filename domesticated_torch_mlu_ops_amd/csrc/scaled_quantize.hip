@@ -11,6 +11,8 @@
 // the smooth vector (<= 1 MiB even with 64 experts) stays L2-resident and is read as 16-byte
 // vectors alongside.  The row's group (expert) is
 // found with a wavefront prefix scan of token_count and a ballot, with no host round trip.
+#include <algorithm>
+
 #include "tmo_device.h"
 
 namespace tmo {
@@ -80,6 +82,16 @@ __device__ __forceinline__ bool locate_row(const SqParams& p, int64_t r, int64_t
   return true;
 }
 
+#ifndef TMO_SQ_LDS_SMOOTH
+#define TMO_SQ_LDS_SMOOTH 1
+#endif
+// Workgroups per CU of the dense kernel's grid-stride launch (0: one workgroup per 4 rows).
+// configs[3] (8192 x 4096 bf16) on MI355X, per-channel / scalar / no smooth: one-shot grid
+// 22.9 / 19.4 / 19.2 us; 1: 24.9 / 23.9 / 23.2; 2: 19.6 / 18.9 / 18.8; 3: 19.4 / 18.8 / 18.7;
+// 6: 20.2 / 19.7 / 19.5 (with the smooth vector staged in LDS).
+#ifndef TMO_SQ_WG_PER_CU
+#define TMO_SQ_WG_PER_CU 3
+#endif
 #ifndef TMO_SQ_WAVES_PER_ROW
 #define TMO_SQ_WAVES_PER_ROW 2
 #endif
@@ -184,66 +196,89 @@ __global__ __launch_bounds__(256) void sq_vec(SqParams p) {
 // Dense rows (no gather, no groups) of exactly 64 * kV 16-byte vectors: output row r reads
 // input row r (r = s * inner + j), so the row address needs no division, every lane loads
 // exactly kV vectors with no bounds checks, and the smooth mode is fixed at compile time
-// (kScalar: one smooth value; kChan: a per-channel vector, loaded beside the row vectors it
-// scales).  configs[3]'s shape: 19.3 us with no or a scalar smooth, 20.8 us per channel (the
-// per-channel vector's 4 bytes per element come from L1; staging it in LDS measured slower).
+// (kScalar: one smooth value; kChan: a per-channel vector).  The grid is a few workgroups per
+// CU that stride over the rows (TMO_SQ_WG_PER_CU); each first copies a per-channel smooth
+// vector into LDS, since every row reads all of it (16 KiB for 4096 channels: twice the row's
+// own bytes) and L1 could not serve that beside the row loads -- 22.9 -> 19.4 us on
+// configs[3]'s shape.
 template <class Tag, int kV, bool kScalar, bool kChan>
 __global__ __launch_bounds__(256) void sq_dense(SqParams p) {
   constexpr int kPer = Tag::kPerVec;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  if (row >= p.dense_rows) return;
-  const char* xrow = static_cast<const char*>(p.x) + row * p.row_stride * Tag::kBytes + lane * 16;
-  u32x4 w[kV];
-  u32x4 sv[kV][kPer / 4];
+#if TMO_SQ_LDS_SMOOTH
+  // per-channel smooth vector staged in LDS once per workgroup (kV * 64 * kPer floats)
+  __shared__ u32x4 lds_smooth[kChan ? kV * kWave * (kPer / 4) : 1];
+  if constexpr (kChan) {
+    const u32x4* g = reinterpret_cast<const u32x4*>(p.smooth);
+    for (int k = threadIdx.x; k < kV * kWave * (kPer / 4); k += 256) lds_smooth[k] = g[k];
+    __syncthreads();
+  }
+  const u32x4* sp = lds_smooth + lane * (kPer / 4);
+#else
   const u32x4* sp = reinterpret_cast<const u32x4*>(p.smooth) + lane * (kPer / 4);
+#endif
+  for (int64_t wg = blockIdx.x;; wg += gridDim.x) {
+    const int64_t row = wg * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    if (row >= p.dense_rows) return;
+    const char* xrow = static_cast<const char*>(p.x) + row * p.row_stride * Tag::kBytes + lane * 16;
+    u32x4 w[kV];
+    u32x4 sv[kV][kPer / 4];
 #pragma unroll
-  for (int i = 0; i < kV; ++i) {
-    w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xrow + i * kWave * 16));
+    for (int i = 0; i < kV; ++i)
+      w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xrow + i * kWave * 16));
     if constexpr (kChan) {
 #pragma unroll
-      for (int q = 0; q < kPer / 4; ++q) sv[i][q] = sp[i * kWave * (kPer / 4) + q];
-    }
-  }
-  // Keep every load of the row ahead of the first use: without this barrier the scheduler
-  // moved the unpack of the first vector (and its wait) between the loads, so the second half
-  // of the row was requested only after the first vector had arrived.
-  __builtin_amdgcn_sched_barrier(0);
-  const float s_scalar = kScalar ? p.smooth[0] : 1.0f;
-  float v[kV][kPer];
-  float m = 0.0f;
+      for (int i = 0; i < kV; ++i)
 #pragma unroll
-  for (int i = 0; i < kV; ++i) {
-    unpack(Tag{}, w[i], v[i]);
-#pragma unroll
-    for (int e = 0; e < kPer; ++e) {
-      // RN(x * smooth), no FMA
-      if constexpr (kScalar) v[i][e] = v[i][e] * s_scalar;
-      if constexpr (kChan) v[i][e] = v[i][e] * __uint_as_float(sv[i][e / 4][e % 4]);
-      m = abs_max(m, v[i][e]);
+        for (int q = 0; q < kPer / 4; ++q) sv[i][q] = sp[i * kWave * (kPer / 4) + q];
     }
-  }
-  const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<kWave>(__float_as_uint(m))));
-  int8_t* orow = p.out + row * p.channels + lane * kPer;
+    // Keep every load of the row ahead of the first use: without this barrier the scheduler
+    // moved the unpack of the first vector (and its wait) between the loads, so the second half
+    // of the row was requested only after the first vector had arrived.
+    __builtin_amdgcn_sched_barrier(0);
+    const float s_scalar = kScalar ? p.smooth[0] : 1.0f;
+    float v[kV][kPer];
+    float m = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kV; ++i) {
-    uint32_t c[kPer / 4];
-    encode_row<kPer>(v[i], rs, c);
-    if constexpr (kPer == 8) {
-      u32x2 c2;
-      c2[0] = c[0];
-      c2[1] = c[1];
-      store_nt(reinterpret_cast<u32x2*>(orow + i * kWave * 8), c2);
-    } else {
-      store_nt(reinterpret_cast<uint32_t*>(orow + i * kWave * 4), c[0]);
+    for (int i = 0; i < kV; ++i) {
+      unpack(Tag{}, w[i], v[i]);
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        // RN(x * smooth), no FMA
+        if constexpr (kScalar) v[i][e] = v[i][e] * s_scalar;
+        if constexpr (kChan) v[i][e] = v[i][e] * __uint_as_float(sv[i][e / 4][e % 4]);
+        m = abs_max(m, v[i][e]);
+      }
     }
+    const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<kWave>(__float_as_uint(m))));
+    int8_t* orow = p.out + row * p.channels + lane * kPer;
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+      uint32_t c[kPer / 4];
+      encode_row<kPer>(v[i], rs, c);
+      if constexpr (kPer == 8) {
+        u32x2 c2;
+        c2[0] = c[0];
+        c2[1] = c[1];
+        store_nt(reinterpret_cast<u32x2*>(orow + i * kWave * 8), c2);
+      } else {
+        store_nt(reinterpret_cast<uint32_t*>(orow + i * kWave * 4), c[0]);
+      }
+    }
+    if (lane == 0) p.out_scale[row] = rs.s;
   }
-  if (lane == 0) p.out_scale[row] = rs.s;
 }
 
 template <class Tag, int kV>
 int launch_dense(const SqParams& p, hipStream_t stream) {
-  const int64_t blocks = (p.dense_rows + 3) / 4;
+  int64_t blocks = (p.dense_rows + 3) / 4;
+  if (TMO_SQ_WG_PER_CU > 0) {
+    int device = 0, cus = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+      return TMO_ERR_LAUNCH;
+    blocks = std::min<int64_t>(blocks, (int64_t)cus * TMO_SQ_WG_PER_CU);
+  }
   if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
   const dim3 grid((unsigned)blocks), block(256);
   if (p.smooth && p.smooth_len != 1)
