@@ -55,9 +55,9 @@ WORKLOADS = {
     "linear_reshape": "reshape_linear_cache, 8 packed sequences x 4096 tokens x 8 KV heads x 128 bf16 -> bf16 linear cache [8, 8, 8192, 128]",
     "decode_attn": "single_query_cached_kv_attn, one bf16 query token x 32 heads per sequence over configs[4]'s int8 pages (64 seqs, ctx ~U[1024,32768], 8 KV heads x 128, per-token scales)",
 }
-KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1>", "cfg2": "quant_paged_vec<BF16,16,1>",
-           "cfg3": "quant_paged_vec<BF16,16,1>", "cfg4": "sq_dense<BF16,8,false,true>",
-           "cfg4_moe": "sq_vec<BF16,8,false,1>", "cfg5": "dequant_paged_persistent<BF16,8>",
+KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<BF16,16,1,false>",
+           "cfg3": "quant_paged_vec<BF16,16,1,false>", "cfg4": "sq_dense<BF16,8,false,true>",
+           "cfg4_moe": "sq_vec<BF16,8,false,1>", "cfg5": "dequant_paged_list<BF16,1,2>",
            "offline_i8": "quant_paged_static_vec<BF16,16,false>",
            "offline_f8": "quant_paged_static_vec<BF16,16,true>",
            "fused_rope": "fused_rope_tok<BF16,16,4>",
