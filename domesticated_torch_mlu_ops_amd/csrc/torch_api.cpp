@@ -1066,17 +1066,17 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   const int64_t max_ctx = max_context_len.expect_int();
   const int64_t window = windows_size_left.expect_int();
   if (B == 0) return;
-  // Splits: about eight workgroups per CU (2048) when the batch alone does not give them, at
+  // Splits: about twelve workgroups per CU (3072) when the batch alone does not give them, at
   // least 256 keys per split, at most 63 splits -- and an odd count.  The kernel's grid runs
   // the splits of one (sequence, KV head) on consecutive workgroups, which the dispatcher deals
   // round-robin to the 8 XCDs: with 8 (or 4) splits every first chunk lands on one XCD (or
   // two) and the mostly empty last chunks of short contexts on another, while a count coprime
   // with 8 spreads them.  configs[4]'s 512 (sequence, KV head) pairs, splits 1..10: 681, 726,
-  // 595, 673, 556, 571, 550, 713, 561, 590 us.
+  // 595, 673, 556, 571, 550, 713, 561, 590 us (5 vs 7 repeated on one box: 560 vs 545).
   int64_t splits = 1;
   const int64_t pairs = B * Hkv;
-  if (max_ctx > 0 && pairs < 2048) {
-    const int64_t want = (2048 + pairs - 1) / pairs;
+  if (max_ctx > 0 && pairs < 3072) {
+    const int64_t want = (3072 + pairs - 1) / pairs;
     const int64_t cap = (max_ctx + 255) / 256;
     splits = std::max<int64_t>(1, std::min<int64_t>({want, cap, 63}));
     if (splits > 1 && splits % 2 == 0) splits += splits + 1 <= cap ? 1 : -1;
