@@ -138,8 +138,11 @@ def fused_rope(
     eps: float = 1e-5,
     q_gamma: Optional[torch.Tensor] = None,
 ):
-    """RMSNorm (Q optional, K) + fold rotary embedding + store of K and V into paged caches,
-    in one pass over ``qkv [batch, seq_len, q_heads + 2 kv_heads, head_size]``.
+    """Fold rotary embedding + a norm + store of K and V into paged caches, in one pass over
+    ``qkv [batch, seq_len, q_heads + 2 kv_heads, head_size]``.  ``norm_type="rmsnorm"``: RMSNorm
+    of Q (with ``q_gamma`` unless None) and of K (``k_gamma``), then the rotation.
+    ``norm_type="layernorm"``: Q and K rotated, then K layer-normalised (biased variance) with
+    ``k_gamma`` and ``k_beta`` (None: no shift); ``q_gamma`` is not used.  V is stored as it is.
 
     Token ``(b, s)`` is rotated at position ``position_id[b] + s`` with rows of
     ``sin_cache`` / ``cos_cache [rotary_seq, rope_dim]`` over head dims
@@ -148,8 +151,8 @@ def fused_rope(
     ``slot_mapping_hp`` (negative slots skipped): in qkv's dtype, or int8 with ``k_scale_hp`` /
     ``v_scale_hp`` either ``[num_blocks, kv_heads, block_size]`` (dynamic per-token scales,
     written) or ``[kv_heads, head_size]`` (static per-channel scales, read).  fp32 arithmetic
-    with one final rounding.  This build implements ``norm_type="rmsnorm"`` with paged
-    high-precision caches; other modes raise ``RuntimeError``.
+    with one final rounding.  This build implements both norm types with paged high-precision
+    caches; the linear-cache and low-precision-cache targets raise ``RuntimeError``.
 
     Reference: ``_ops.py:3469-3601`` (math ``:3496-3520``, rotary math ``:1116-1127``).
     Returns ``(qkv, k_cache_hp, v_cache_hp)`` (plus the low-precision tensors when given).

@@ -39,8 +39,10 @@ struct FusedRopeParams {
   int32_t rope_dim, rope_off;
   const int32_t* position;
   const void* k_gamma;
-  const void* q_gamma;  // nullable
+  const void* k_beta;   // nullable (layernorm only)
+  const void* q_gamma;  // nullable (rmsnorm only)
   float eps;
+  int32_t norm;         // 0 rmsnorm (before the rotation), 1 layernorm of K (after it)
   void* cache[2];
   float* scale[2];
   int32_t scale_mode;  // 0 none (caches of qkv's dtype), 1 dynamic per token, 2 static per channel
@@ -90,6 +92,34 @@ __device__ __forceinline__ float rms_inverse(float ss, int d, float eps) {
   return 1.0f / r;
 }
 
+// Layernorm of a row held as G lanes x 8 values (D13): mean = RN(s1 / D), s1 the chunked sum
+// of the values; d = RN(y - mean); var = RN(s2 / D), s2 the chunked sum of RN(d * d);
+// inv = RN(1 / RN(sqrt(RN(var + eps)))); y = RN(RN(d * inv) * gamma) [+ beta, rounded].
+template <int G>
+__device__ __forceinline__ void layernorm8(float* y, const float* g, const float* b, bool has_beta,
+                                           int d_model, float eps) {
+  float s1 = y[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) s1 = s1 + y[e];
+  const float mean = group_sum_f32<G>(s1) / (float)d_model;
+  float dv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dv[e] = y[e] - mean;
+  float s2 = dv[0] * dv[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) {
+    const float sq = dv[e] * dv[e];
+    s2 = s2 + sq;
+  }
+  const float inv = rms_inverse(group_sum_f32<G>(s2), d_model, eps);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float n = dv[e] * inv;
+    y[e] = n * g[e];
+    if (has_beta) y[e] = y[e] + b[e];
+  }
+}
+
 constexpr int kDppRowRor8 = 0x128;  // rotate right by 8 lanes inside each 16-lane row
 
 #ifndef TMO_FUSED_ROPE_TOKEN_MAJOR
@@ -119,6 +149,7 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
 
   // ---- loads: x, then (q/k) gamma and the sin/cos of this lane's window chunk, slot
   u32x4 xw = {0u, 0u, 0u, 0u}, gw = {0u, 0u, 0u, 0u}, sw = {0u, 0u, 0u, 0u}, cw = {0u, 0u, 0u, 0u};
+  u32x4 bw = {0u, 0u, 0u, 0u};
   int32_t slot = -1;
   const int c0 = p.rope_off / 8, nwin = p.rope_dim / 8;  // window in chunks
   const bool in_win = lane >= c0 && lane < c0 + nwin;
@@ -131,6 +162,8 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
       const int64_t b = t / p.seq_len;
       pos = (int64_t)p.position[b] + (t - b * p.seq_len);
       if (gamma) gw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(gamma) + lane * 16);
+      if (kind == 1 && p.norm == 1 && p.k_beta)
+        bw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_beta) + lane * 16);
       if (pos >= 0 && pos < p.table_rows && in_win) {
         const int64_t e = pos * p.table_stride + (lane - c0) * 8;
         sw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.sin_t) + e * Tag::kBytes);
@@ -145,7 +178,7 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
   float y[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = x[e];
-  if (kind != 2 && (kind == 1 || p.q_gamma)) {
+  if (kind != 2 && p.norm == 0 && (kind == 1 || p.q_gamma)) {
     float acc = x[0] * x[0];
 #pragma unroll
     for (int e = 1; e < 8; ++e) {
@@ -190,6 +223,12 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
         const float b = y[e] * cs[e];
         y[e] = a + b;
       }
+    }
+    if (kind == 1 && p.norm == 1) {  // layernorm of K after its rotation
+      float g[8], bt[8];
+      unpack(Tag{}, gw, g);
+      unpack(Tag{}, bw, bt);
+      layernorm8<G>(y, g, bt, p.k_beta != nullptr, p.head_dim, p.eps);
     }
   }
   if (!live) return;
@@ -278,11 +317,15 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
   }
   kgw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_gamma) + lane * 16);
   if (p.q_gamma) qgw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.q_gamma) + lane * 16);
-  float sn[8], cs[8], kg[8], qg[8];
+  u32x4 kbw = {0u, 0u, 0u, 0u};
+  if (p.norm == 1 && p.k_beta)
+    kbw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_beta) + lane * 16);
+  float sn[8], cs[8], kg[8], qg[8], kb[8];
   unpack(Tag{}, sw, sn);
   unpack(Tag{}, cw, cs);
   unpack(Tag{}, kgw, kg);
   unpack(Tag{}, qgw, qg);
+  unpack(Tag{}, kbw, kb);
   const float sign = lane < c0 + hc ? -1.0f : 1.0f;  // rot = -partner in the window's first half
 #pragma unroll
   for (int e = 0; e < 8; ++e) sn[e] = sn[e] * sign;
@@ -297,7 +340,7 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
     float y[8];
     unpack(Tag{}, xw[j], y);
     if (kind != 2) {
-      if (kind == 1 || p.q_gamma) {
+      if (p.norm == 0 && (kind == 1 || p.q_gamma)) {
         float acc = y[0] * y[0];
 #pragma unroll
         for (int e = 1; e < 8; ++e) {
@@ -332,6 +375,7 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
           y[e] = a + c;
         }
       }
+      if (kind == 1 && p.norm == 1) layernorm8<G>(y, kg, kb, p.k_beta != nullptr, p.head_dim, p.eps);
     }
     if (kind == 0) {
       u32x4 o;
@@ -404,7 +448,7 @@ __global__ __launch_bounds__(256) void fused_rope_generic(FusedRopeParams p) {
     for (int d = lane; d < D; d += kWave) xs[d] = load1(Tag{}, p.qkv, base + d);
   __syncthreads();
   const void* gamma = kind == 0 ? p.q_gamma : p.k_gamma;
-  const bool norm = kind == 1 || (kind == 0 && p.q_gamma);
+  const bool norm = p.norm == 0 && (kind == 1 || (kind == 0 && p.q_gamma));
   if (active) {
     float inv = 1.0f;
     if (kind != 2 && norm) {
@@ -436,8 +480,57 @@ __global__ __launch_bounds__(256) void fused_rope_generic(FusedRopeParams p) {
     const int64_t b = t / p.seq_len;
     pos = (int64_t)p.position[b] + (t - b * p.seq_len);
   }
-  const bool rotate = kind != 2 && pos >= 0 && pos < p.table_rows;
+  const bool rotate0 = kind != 2 && pos >= 0 && pos < p.table_rows;
   const int half = p.rope_dim / 2;
+  bool rotate = rotate0;
+  if (kind == 1 && p.norm == 1) {
+    // layernorm of K after its rotation: rotate into xs (the row's stage, free after the copy
+    // into ys), then normalise there; out_at then reads the finished values unrotated
+    for (int d = lane; d < D; d += kWave) {
+      float v = ys[d];
+      if (rotate0 && d >= p.rope_off && d < p.rope_off + p.rope_dim) {
+        const int j = d - p.rope_off;
+        const float rot = j < half ? -ys[d + half] : ys[d - half];
+        const float a = rot * load1(Tag{}, p.sin_t, pos * p.table_stride + j);
+        const float b = v * load1(Tag{}, p.cos_t, pos * p.table_stride + j);
+        v = a + b;
+      }
+      xs[d] = v;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // chunk `lane` of the sums, then the 64-lane tree (zeros past the last chunk)
+    const int e0 = lane * 8;
+    float s1 = 0.0f;
+    if (e0 < D) {
+      s1 = xs[e0];
+      for (int e = e0 + 1; e < e0 + 8 && e < D; ++e) s1 = s1 + xs[e];
+    }
+    const float mean = group_sum_f32<kWave>(s1) / (float)D;
+    float s2 = 0.0f;
+    if (e0 < D) {
+      const float d0 = xs[e0] - mean;
+      s2 = d0 * d0;
+      for (int e = e0 + 1; e < e0 + 8 && e < D; ++e) {
+        const float de = xs[e] - mean;
+        const float sq = de * de;
+        s2 = s2 + sq;
+      }
+    }
+    const float inv = rms_inverse(group_sum_f32<kWave>(s2), D, p.eps);
+    for (int d = lane; d < D; d += kWave) {
+      const float dv = xs[d] - mean;
+      const float n = dv * inv;
+      float v = n * load1(Tag{}, p.k_gamma, d);
+      if (p.k_beta) v = v + load1(Tag{}, p.k_beta, d);
+      ys[d] = v;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    rotate = false;
+  }
   auto out_at = [&](int d) -> float {
     const float yv = ys[d];
     if (!rotate || d < p.rope_off || d >= p.rope_off + p.rope_dim) return yv;
@@ -482,7 +575,7 @@ int launch(const FusedRopeParams& p, hipStream_t stream) {
   const int G = D / 8;
   auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
   bool vec = D % 8 == 0 && G >= 1 && G <= kWave && (G & (G - 1)) == 0 &&
-             p.rope_off % 8 == 0 && p.rope_dim % 16 == 0 && al16(p.qkv) && al16(p.k_gamma) &&
+             p.rope_off % 8 == 0 && p.rope_dim % 16 == 0 && al16(p.qkv) && al16(p.k_gamma) && (!p.k_beta || al16(p.k_beta)) &&
              (!p.q_gamma || al16(p.q_gamma)) && al16(p.sin_t) && al16(p.cos_t) &&
              (p.table_stride * Tag::kBytes) % 16 == 0 && al16(p.cache[0]) && al16(p.cache[1]) &&
              (p.scale_mode != 2 || (al16(p.scale[0]) && al16(p.scale[1])));
@@ -532,13 +625,16 @@ extern "C" int tmo_hip_fused_rope_paged(
     void* qkv, int64_t num_tokens, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
     int64_t head_size, const void* sin_table, const void* cos_table, int64_t table_rows,
     int64_t table_stride, int64_t rope_dim, int64_t rope_offset, const int32_t* position_ids,
-    int64_t batch, const void* k_gamma, const void* q_gamma, float eps, void* k_cache,
-    void* v_cache, float* k_scale, float* v_scale, int scale_mode,
+    int64_t batch, const void* k_gamma, const void* k_beta, const void* q_gamma, float eps,
+    int norm_type, void* k_cache, void* v_cache, float* k_scale, float* v_scale, int scale_mode,
     const int32_t* slot_mapping, int64_t num_blocks, int64_t block_size, int dtype,
     void* stream) {
   using namespace tmo;
   if (dtype != TMO_DTYPE_F16 && dtype != TMO_DTYPE_BF16) return TMO_ERR_UNSUPPORTED_DTYPE;
-  if (scale_mode < 0 || scale_mode > 2) return TMO_ERR_UNSUPPORTED_MODE;
+  if (scale_mode < 0 || scale_mode > 2 || norm_type < 0 || norm_type > 1)
+    return TMO_ERR_UNSUPPORTED_MODE;
+  if (norm_type == 1 && q_gamma) return TMO_ERR_INVALID_ARGUMENT;  // rmsnorm-only argument
+  if (norm_type == 0 && k_beta) return TMO_ERR_INVALID_ARGUMENT;   // layernorm-only argument
   if (!qkv || !sin_table || !cos_table || !position_ids || !k_gamma || !k_cache || !v_cache ||
       !slot_mapping)
     return TMO_ERR_INVALID_ARGUMENT;
@@ -570,8 +666,10 @@ extern "C" int tmo_hip_fused_rope_paged(
   p.rope_off = (int32_t)rope_offset;
   p.position = position_ids;
   p.k_gamma = k_gamma;
+  p.k_beta = k_beta;
   p.q_gamma = q_gamma;
   p.eps = eps;
+  p.norm = norm_type;
   p.cache[0] = k_cache;
   p.cache[1] = v_cache;
   p.scale[0] = k_scale;

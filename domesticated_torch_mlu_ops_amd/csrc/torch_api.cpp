@@ -242,8 +242,10 @@ void fused_rope(at::Tensor& qkv, at::Tensor& key_cache_hp, at::Tensor& value_cac
                 const c10::optional<at::Tensor>& slot_mapping_lp, const std::string& norm_type,
                 c10::SymInt rope_dim_offset, const double eps,
                 const c10::optional<at::Tensor>& q_gamma) {
-  TORCH_CHECK(norm_type == "rmsnorm",
-              "fused_rope: this build implements norm_type \"rmsnorm\", got \"", norm_type, "\"");
+  TORCH_CHECK(norm_type == "rmsnorm" || norm_type == "layernorm",
+              "fused_rope: norm_type must be \"rmsnorm\" or \"layernorm\", got \"", norm_type,
+              "\"");
+  const bool layernorm = norm_type == "layernorm";
   TORCH_CHECK(!key_cache_lp && !value_cache_lp && !key_scale_lp && !value_scale_lp &&
                   !slot_mapping_lp && !cache_bs_id_lp && !cache_seq_offsets_lp,
               "fused_rope: low-precision (int4) caches are not supported by this build");
@@ -251,7 +253,7 @@ void fused_rope(at::Tensor& qkv, at::Tensor& key_cache_hp, at::Tensor& value_cac
               "fused_rope: linear caches (cache_bs_id / cache_seq_offsets) are not supported by "
               "this build; pass slot_mapping_hp for paged caches");
   TORCH_CHECK(slot_mapping_hp.has_value(), "fused_rope: slot_mapping_hp is required");
-  TORCH_CHECK(!k_beta.has_value(), "fused_rope: k_beta applies to layernorm only");
+  TORCH_CHECK(layernorm || !k_beta.has_value(), "fused_rope: k_beta applies to layernorm only");
   check_device(qkv, qkv, "qkv");
   TORCH_CHECK(qkv.dim() == 4 && qkv.is_contiguous(),
               "qkv must be a contiguous [batch, seq_len, heads, head_size] tensor, got ",
@@ -317,12 +319,16 @@ void fused_rope(at::Tensor& qkv, at::Tensor& key_cache_hp, at::Tensor& value_cac
   TORCH_CHECK(position_ids.scalar_type() == at::kInt && position_ids.dim() == 1 &&
                   position_ids.size(0) == B && position_ids.is_contiguous(),
               "position_ids must be a contiguous int32 [batch] tensor");
-  for (const at::Tensor* g : {&gamma, q_gamma ? &*q_gamma : nullptr}) {
+  // layernorm normalises K only (after its rotation); q_gamma belongs to the rmsnorm branch
+  // (reference _ops.py:3501-3509) and is not read there
+  const at::Tensor* qg = (!layernorm && q_gamma) ? &*q_gamma : nullptr;
+  const at::Tensor* kb = (layernorm && k_beta) ? &*k_beta : nullptr;
+  for (const at::Tensor* g : {&gamma, qg, kb}) {
     if (!g) continue;
     check_device(*g, qkv, "gamma");
     TORCH_CHECK(g->dim() == 1 && g->size(0) == D && g->scalar_type() == qkv.scalar_type() &&
                     g->is_contiguous(),
-                "gammas must be contiguous [head_size] tensors of qkv's dtype");
+                "gammas and k_beta must be contiguous [head_size] tensors of qkv's dtype");
   }
   const at::Tensor& slot = *slot_mapping_hp;
   check_device(slot, qkv, "slot_mapping");
@@ -334,8 +340,9 @@ void fused_rope(at::Tensor& qkv, at::Tensor& key_cache_hp, at::Tensor& value_cac
   const int st = tmo_hip_fused_rope_paged(
       qkv.data_ptr(), B * S, S, Hq, Hk, D, sin_table.data_ptr(), cos_table.data_ptr(),
       sin_table.size(0), sin_table.stride(0), rope_dim, off, position_ids.data_ptr<int32_t>(), B,
-      gamma.data_ptr(), q_gamma ? q_gamma->data_ptr() : nullptr, static_cast<float>(eps),
-      key_cache_hp.data_ptr(), value_cache_hp.data_ptr(), ks, vs, mode,
+      gamma.data_ptr(), kb ? kb->data_ptr() : nullptr, qg ? qg->data_ptr() : nullptr,
+      static_cast<float>(eps), layernorm ? 1 : 0, key_cache_hp.data_ptr(),
+      value_cache_hp.data_ptr(), ks, vs, mode,
       slot.data_ptr<int32_t>(), NB, BS, dt, stream_of(qkv));
   check_status(st, "fused_rope");
 }

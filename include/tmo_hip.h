@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 7
+#define TMO_HIP_ABI_VERSION 8
 
 /* element types */
 enum tmo_dtype {
@@ -122,8 +122,11 @@ int tmo_hip_offline_quant_to_paged_cache(const void* k, const void* v,
 
 /*
  * fused_rope_paged -- one pass over qkv [num_tokens, q_heads + 2 kv_heads, head_size]
- * (contiguous, token t = b * seq_len + s at rotary position position_ids[b] + s): RMS-normalise
- * Q (when q_gamma is set) and K per head with eps and gamma [head_size], apply the fold rotary
+ * (contiguous, token t = b * seq_len + s at rotary position position_ids[b] + s).  norm_type 0
+ * (rmsnorm): RMS-normalise Q (when q_gamma is set) and K per head with eps and gamma
+ * [head_size], then rotate; norm_type 1 (layernorm): rotate, then layer-normalise K with
+ * k_gamma and an optional k_beta (two-pass mean / variance over the same chunk order, see
+ * below; q_gamma must be NULL).  The rotation is the fold rotary
  * embedding over [rope_offset, rope_offset + rope_dim) with rows of sin_table / cos_table
  * [table_rows, table_stride] (a position outside the table leaves the row unrotated), write Q
  * back into qkv, and store K and V rows at slot_mapping into [num_blocks, kv_heads, block_size,
@@ -133,8 +136,11 @@ int tmo_hip_offline_quant_to_paged_cache(const void* k, const void* v,
  * head_size].  fp32 arithmetic, one final rounding; the sum of squares is taken over
  * 8-element chunks in order, then a balanced tree over the chunks; 1/rms = RN(1 / RN(sqrt(
  * RN(RN(ss / head_size) + eps)))).
+ * Layernorm: mean = RN(s1 / head_size) over the chunked sum s1 of the rotated row, var =
+ * RN(s2 / head_size) over the chunked sum of RN(d * d), d = RN(x - mean), out = RN(RN(d *
+ * RN(1 / RN(sqrt(RN(var + eps))))) * gamma) (+ beta, rounded).
  * Replaces tmo::torch_api::fused_rope (reference include/torch_mlu_ops.h:562-585) with
- * norm_type "rmsnorm" and paged high-precision caches, called by torch_mlu_ops.fused_rope
+ * paged high-precision caches, called by torch_mlu_ops.fused_rope
  * (reference _ops.py:3469-3601) and torch_mlu_ops.fused_rmsnorm_rope_store_paged_cache
  * (reference _ops.py:6356-6423).
  * dtype: F16 or BF16 (qkv, tables, gammas); head_size <= 512; num_tokens <= batch * seq_len.
@@ -145,7 +151,8 @@ int tmo_hip_fused_rope_paged(void* qkv, int64_t num_tokens, int64_t seq_len,
                              int64_t table_rows, int64_t table_stride,
                              int64_t rope_dim, int64_t rope_offset,
                              const int32_t* position_ids, int64_t batch,
-                             const void* k_gamma, const void* q_gamma, float eps,
+                             const void* k_gamma, const void* k_beta, const void* q_gamma,
+                             float eps, int norm_type,
                              void* k_cache, void* v_cache, float* k_scale, float* v_scale,
                              int scale_mode, const int32_t* slot_mapping,
                              int64_t num_blocks, int64_t block_size, int dtype, void* stream);

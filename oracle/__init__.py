@@ -52,8 +52,8 @@ def lib() -> ctypes.CDLL:
             [c_void_p] * 3 + [c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                               c_int]
         L.oracle_fused_rope_paged.argtypes = [c_void_p, c_int] + [c_int64] * 5 + \
-            [c_void_p, c_void_p] + [c_int64] * 4 + [c_void_p] * 3 + [c_float] + [c_void_p] * 4 + \
-            [c_int, c_void_p, c_int64, c_int64, c_int]
+            [c_void_p, c_void_p] + [c_int64] * 4 + [c_void_p] * 3 + [c_float, c_void_p, c_int] + \
+            [c_void_p] * 4 + [c_int, c_void_p, c_int64, c_int64, c_int]
         L.oracle_fused_rope_paged.restype = c_int
         L.oracle_offline_quant_to_paged_cache.argtypes = [c_void_p, c_void_p, c_int] + \
             [c_int64] * 4 + [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_float, c_float,
@@ -144,9 +144,11 @@ def offline_quant_to_paged_cache(k, v, k_cache_scale, v_cache_scale, slot_mappin
 
 def fused_rope_paged(qkv, k_cache, v_cache, sin_cache, cos_cache, position_id, k_gamma, k_scale,
                      v_scale, slot_mapping, eps: float = 1e-5, q_gamma=None, rope_dim_offset: int = 0,
-                     nthreads: Optional[int] = None) -> None:
-    """reference _ops.py:3469-3601 (fused_rope, norm_type "rmsnorm", paged hp caches) under
-    decision D10 of tmo_oracle.c; in place on CPU tensors (q back into qkv, K/V into the pages).
+                     nthreads: Optional[int] = None, norm_type: str = "rmsnorm",
+                     k_beta=None) -> None:
+    """reference _ops.py:3469-3601 (fused_rope, paged hp caches) under decisions D10
+    (norm_type "rmsnorm") and D13 ("layernorm": rope, then layernorm of K with k_gamma and
+    k_beta) of tmo_oracle.c; in place on CPU tensors (q back into qkv, K/V into the pages).
     qkv [B, S, Hq + 2 Hk, D] (or [T, Hq + 2 Hk, D] with S = T); caches [NB, Hk, BS, D] of qkv's
     dtype (no scales) or int8 with k_scale/v_scale [NB, Hk, BS] (dynamic, written) or [Hk, D]
     (static, read)."""
@@ -168,7 +170,8 @@ def fused_rope_paged(qkv, k_cache, v_cache, sin_cache, cos_cache, position_id, k
         _ptr(qkv), _DT[qkv.dtype], T, S, Hq, Hk, D, _ptr(sin_cache), _ptr(cos_cache),
         sin_cache.shape[-1], rope_dim_offset, sin_cache.stride(0), sin_cache.shape[0],
         _ptr(pos), _ptr(k_gamma),
-        _ptr(q_gamma), float(eps), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+        _ptr(q_gamma), float(eps), _ptr(k_beta), {"rmsnorm": 0, "layernorm": 1}[norm_type],
+        _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
         mode, _ptr(slots), NB, BS, nthreads or default_threads())
     _check(rc, "fused_rope_paged")
 

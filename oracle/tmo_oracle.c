@@ -30,6 +30,12 @@
  *       table's rows leaves the row unrotated -- undefined in the reference); K is quantised (or
  *       rounded) from the fp32 result, V from its input values (_ops.py:3493-3520,
  *       6356-6423; rotary math _ops.py:1116-1127).
+ *   D13 fused_rope, norm_type "layernorm" (_ops.py:3501-3504): Q and K are rotated (D10's rope
+ *       on the raw fp32 row), then K alone is layer-normalised in fp32, two passes over the
+ *       D10 chunk order: mean = RN(s1 / D) with s1 the chunked sum of the rotated row;
+ *       d = RN(x - mean); var = RN(s2 / D) with s2 the chunked sum of RN(d * d) (biased, as
+ *       torch's layer_norm); inv = RN(1 / RN(sqrt(RN(var + eps)))); y = RN(RN(d * inv) *
+ *       gamma), then RN(y + beta) when beta is given.  q_gamma is not used.
  *   D11 linear caches [max_batch, H, cache_len, D] (_ops.py:1189-1249, 1708-1919, 3642-3732,
  *       3898-3969): sequence i covers len_i tokens -- cu[i+1] - cu[i] when the input is
  *       packed (context_lengths holds batch + 1 prefix offsets), else context_lengths[i]; its
@@ -411,6 +417,8 @@ typedef struct {
     const void* k_gamma;
     const void* q_gamma;
     float eps;
+    const void* k_beta;             /* layernorm only, nullable */
+    int norm;                       /* 0 rmsnorm, 1 layernorm */
     void* cache[2];
     int cache_dtype;
     float* scale[2];
@@ -439,6 +447,41 @@ static float rms_sum_squares(const float* x, int64_t n) {
     for (int64_t w = width; w > 1; w /= 2)
         for (int64_t c = 0; c < w / 2; ++c) part[c] = part[2 * c] + part[2 * c + 1];
     return part[0];
+}
+
+/* D13: the chunked sum (D10 order) of the values themselves. */
+static float chunk_sum(const float* x, int64_t n) {
+    float part[64];
+    int64_t nchunks = (n + 7) / 8, width = 1;
+    while (width < nchunks) width *= 2;
+    for (int64_t c = 0; c < width; ++c) {
+        float acc = 0.0f;
+        if (c < nchunks) {
+            int64_t e0 = 8 * c, e1 = e0 + 8 < n ? e0 + 8 : n;
+            acc = x[e0];
+            for (int64_t e = e0 + 1; e < e1; ++e) acc = acc + x[e];
+        }
+        part[c] = acc;
+    }
+    for (int64_t w = width; w > 1; w /= 2)
+        for (int64_t c = 0; c < w / 2; ++c) part[c] = part[2 * c] + part[2 * c + 1];
+    return part[0];
+}
+
+/* D13 layernorm with gamma and optional beta (in place on fp32 row; tmp: D floats) */
+static void layernorm_row(float* x, float* tmp, int64_t D, const void* gamma, const void* beta,
+                          int dtype, float eps) {
+    float mean = chunk_sum(x, D) / (float)D;
+    for (int64_t d = 0; d < D; ++d) tmp[d] = x[d] - mean;
+    float var = rms_sum_squares(tmp, D) / (float)D;
+    float r = sqrtf(var + eps);
+    float inv = 1.0f / r;
+    for (int64_t d = 0; d < D; ++d) {
+        float t = tmp[d] * inv;
+        float y = t * load_elem(gamma, d, dtype);
+        if (beta) y = y + load_elem(beta, d, dtype);
+        x[d] = y;
+    }
 }
 
 /* rmsnorm with gamma (in place on fp32 row) */
@@ -501,15 +544,20 @@ static void frope_range(void* p, int64_t lo, int64_t hi) {
         for (int64_t hh = 0; hh < H; ++hh) {
             int64_t base = (t * H + hh) * D;
             for (int64_t d = 0; d < D; ++d) row[d] = load_elem(c->qkv, base + d, c->dtype);
-            if (hh < c->Hq) {                                   /* q: rmsnorm (if q_gamma), rope */
-                if (c->q_gamma) rmsnorm_row(row, D, c->q_gamma, c->dtype, c->eps);
+            if (hh < c->Hq) {                     /* q: rmsnorm (if q_gamma, rmsnorm only), rope */
+                if (c->norm == 0 && c->q_gamma) rmsnorm_row(row, D, c->q_gamma, c->dtype, c->eps);
                 rope_row(row, tmp, c, pos);
                 for (int64_t d = 0; d < D; ++d) store_elem(c->qkv, base + d, c->dtype, row[d]);
-            } else if (hh < c->Hq + c->Hk) {                   /* k: rmsnorm, rope, store */
+            } else if (hh < c->Hq + c->Hk) {     /* k: rmsnorm + rope, or rope + layernorm; store */
                 if (!valid) continue;
                 int64_t h = hh - c->Hq;
-                rmsnorm_row(row, D, c->k_gamma, c->dtype, c->eps);
-                rope_row(row, tmp, c, pos);
+                if (c->norm == 0) {
+                    rmsnorm_row(row, D, c->k_gamma, c->dtype, c->eps);
+                    rope_row(row, tmp, c, pos);
+                } else {
+                    rope_row(row, tmp, c, pos);
+                    layernorm_row(row, tmp, D, c->k_gamma, c->k_beta, c->dtype, c->eps);
+                }
                 frope_store(c, 0, row, (blk * c->Hk + h) * c->BS + off, h);
             } else {                                             /* v: store */
                 if (!valid) continue;
@@ -523,7 +571,7 @@ static void frope_range(void* p, int64_t lo, int64_t hi) {
 }
 
 /* _ops.py:3469-3601 fused_rope / 6356-6423 fused_rmsnorm_rope_store_paged_cache, norm_type
- * "rmsnorm", paged high-precision caches.  qkv [T, Hq + 2 Hk, D] contiguous (T = batch * S,
+ * "rmsnorm" (norm 0, D10) or "layernorm" (norm 1, D13), paged high-precision caches.  qkv [T, Hq + 2 Hk, D] contiguous (T = batch * S,
  * token t at position position[t / S] + t % S); sin/cos [rows, table_stride] of qkv's dtype;
  * caches [NB, Hk, BS, D] of qkv's dtype (scale_mode 0) or int8 (1: dynamic per-token scales
  * written to [NB, Hk, BS]; 2: static per-channel scales read from [Hk, D]). */
@@ -532,15 +580,17 @@ int oracle_fused_rope_paged(void* qkv, int dtype, int64_t T, int64_t S, int64_t 
                             int64_t rope_off, int64_t table_stride, int64_t table_rows,
                             const int32_t* position,
                             const void* k_gamma, const void* q_gamma, float eps,
+                            const void* k_beta, int norm,
                             void* k_cache, void* v_cache, float* k_scale, float* v_scale,
                             int scale_mode, const int32_t* slot, int64_t NB, int64_t BS,
                             int nthreads) {
     if (dtype != DT_F16 && dtype != DT_BF16 && dtype != DT_F32) return -2;
     if (T < 0 || S <= 0 || Hq < 0 || Hk <= 0 || D <= 0 || D > 512 || NB < 0 || BS <= 0) return -1;
     if (rope_dim < 0 || rope_dim % 2 || rope_off < 0 || rope_off + rope_dim > D) return -1;
+    if (norm != 0 && norm != 1) return -3;
     frope_ctx c = {qkv, dtype, T, S, Hq, Hk, D, sin_t, cos_t, rope_dim, rope_off, table_stride,
-                   table_rows, position, k_gamma, q_gamma, eps, {k_cache, v_cache}, DT_I8, {k_scale, v_scale},
-                   scale_mode, slot, NB, BS};
+                   table_rows, position, k_gamma, q_gamma, eps, k_beta, norm, {k_cache, v_cache},
+                   DT_I8, {k_scale, v_scale}, scale_mode, slot, NB, BS};
     parallel_for(T, nthreads, frope_range, &c);
     return 0;
 }

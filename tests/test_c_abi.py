@@ -39,8 +39,8 @@ def lib():
     L.tmo_hip_dequant_workspace_bytes.argtypes = [I64] * 4
     L.tmo_hip_dequant_workspace_bytes.restype = I64
     L.tmo_hip_scaled_quantize_per_token.argtypes = [P] + [I64] * 4 + [P] * 3 + [I64, P, I64, P, I64, P, I64, INT, P]
-    L.tmo_hip_fused_rope_paged.argtypes = [P] + [I64] * 5 + [P, P] + [I64] * 4 + [P, I64, P, P] + \
-        [ctypes.c_float] + [P] * 4 + [INT, P, I64, I64, INT, P]
+    L.tmo_hip_fused_rope_paged.argtypes = [P] + [I64] * 5 + [P, P] + [I64] * 4 + [P, I64, P, P, P] + \
+        [ctypes.c_float, INT] + [P] * 4 + [INT, P, I64, I64, INT, P]
     L.tmo_hip_offline_quant_to_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 4 + \
         [ctypes.c_float] * 2 + [P] + [I64] * 5 + [INT, INT, P]
     L.tmo_hip_reshape_linear_cache.argtypes = [P, P] + [I64] * 5 + [P, P] + [I64] * 4 + \
@@ -190,12 +190,15 @@ def test_offline_quant_validation(lib):
 
 def test_fused_rope_validation(lib):
     def call(dtype=2, mode=0, qkv=FAKE, ks=None, T=8, S=8, D=128, rope=128, off=0, B=1, stride=128,
-             rows=64):
+             rows=64, beta=None, qg=None, norm=0):
         return lib.tmo_hip_fused_rope_paged(qkv, T, S, 4, 2, D, FAKE, FAKE, rows, stride, rope, off,
-                                            FAKE, B, FAKE, None, 1e-5, FAKE, FAKE, ks, ks, mode,
-                                            FAKE, 4, 16, dtype, None)
+                                            FAKE, B, FAKE, beta, qg, 1e-5, norm, FAKE, FAKE, ks,
+                                            ks, mode, FAKE, 4, 16, dtype, None)
     assert call(dtype=0) == EDTYPE           # fp32 qkv
     assert call(mode=3) == EMODE
+    assert call(norm=2) == EMODE             # neither rmsnorm nor layernorm
+    assert call(norm=1, qg=FAKE) == EINVAL   # q_gamma belongs to rmsnorm
+    assert call(norm=0, beta=FAKE) == EINVAL  # k_beta belongs to layernorm
     assert call(mode=1) == EINVAL            # quantised without scales
     assert call(qkv=None) == EINVAL
     assert call(D=1024, rope=128) == EINVAL  # head_size > 512

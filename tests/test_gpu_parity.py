@@ -297,11 +297,15 @@ def test_offline_quant_cfg3_shape(tmo, ref, dev):
 
 # ---------------------------------------------------------------------------- fused rope (rmsnorm)
 
-def check_fused_rope(tmo, ref, dev, name, case, with_q_gamma=True, off=0, api="rmsnorm_store"):
+def check_fused_rope(tmo, ref, dev, name, case, with_q_gamma=True, off=0, api="rmsnorm_store",
+                     norm_type="rmsnorm", k_beta=None):
     """GPU fused rope vs the oracle on the same inputs: qkv (Q written back), both caches and
-    the dynamic scales compared whole, from a sentinel start."""
+    the dynamic scales compared whole, from a sentinel start.  norm_type "layernorm" goes
+    through fused_rope with k_beta; q_gamma is passed but not used there."""
     qkv, kc, vc, sin, cos, pid, kg, qg, ks, vs, slot = case
     qg = qg if with_q_gamma else None
+    layernorm = norm_type == "layernorm"
+    assert not layernorm or api == "fused_rope"
     kc = kc.view(torch.uint8).fill_(0x5A).view(kc.dtype)
     vc = vc.view(torch.uint8).fill_(0x5A).view(vc.dtype)
     if ks is not None and ks.dim() == 3:
@@ -310,7 +314,7 @@ def check_fused_rope(tmo, ref, dev, name, case, with_q_gamma=True, off=0, api="r
     want = [qkv.clone(), kc.clone(), vc.clone(),
             ks.clone() if ks is not None else None, vs.clone() if vs is not None else None]
     ref.fused_rope_paged(want[0], want[1], want[2], sin, cos, pid, kg, want[3], want[4], slot,
-                         1e-5, qg, off)
+                         1e-5, None if layernorm else qg, off, norm_type=norm_type, k_beta=k_beta)
     d = (lambda t: t.to(dev) if t is not None else None)
     got = [d(qkv), d(kc), d(vc), d(ks), d(vs)]
     if api == "rmsnorm_store":
@@ -319,9 +323,9 @@ def check_fused_rope(tmo, ref, dev, name, case, with_q_gamma=True, off=0, api="r
                                                        d(kg), d(qg), d(slot), got[3], got[4], 1e-5)
         assert out[0] is got[0] and out[1] is got[1]
     else:
-        out = tmo.fused_rope(got[0], got[1], got[2], d(sin), d(cos), d(pid), d(kg), None,
+        out = tmo.fused_rope(got[0], got[1], got[2], d(sin), d(cos), d(pid), d(kg), d(k_beta),
                              k_scale_hp=got[3], v_scale_hp=got[4], slot_mapping_hp=d(slot),
-                             norm_type="rmsnorm", rope_dim_offset=off, eps=1e-5, q_gamma=d(qg))
+                             norm_type=norm_type, rope_dim_offset=off, eps=1e-5, q_gamma=d(qg))
         assert len(out) == 3 and out[0] is got[0]
     for g, w, n in zip(got, want, ("qkv", "k_cache", "v_cache", "k_scale", "v_scale")):
         if w is not None:
@@ -368,6 +372,46 @@ def test_fused_rope_llama_prefill_shape(tmo, ref, dev):
     case = W.fused_rope_case(torch.bfloat16, "dynamic", 5, B=8, S=512, Hq=32, Hk=8, NB=512,
                              maxpos=4096, positions=(0, 512, 1024, 1536, 2048, 2560, 3072, 3584))
     check_fused_rope(tmo, ref, dev, "llama prefill", case, True)
+
+
+def _beta(D, dtype, seed):
+    return (torch.rand(D, generator=torch.Generator().manual_seed(seed)) - 0.5).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mode", ["none", "dynamic", "static"])
+@pytest.mark.parametrize("with_beta", [True, False])
+def test_fused_rope_layernorm_modes(tmo, ref, dev, dtype, mode, with_beta):
+    """norm_type "layernorm" (the reference's default): Q and K rotated, then K layer-normalised
+    with k_gamma and k_beta; unquantised, dynamic and static int8 caches; a sequence past the
+    sin/cos table; -1 slots; a zero K row (stored as beta)."""
+    case = W.fused_rope_case(dtype, mode, 23, B=4, S=24, Hq=8, Hk=2, NB=16)
+    check_fused_rope(tmo, ref, dev, f"layernorm {dtype} {mode} beta={with_beta}", case, True,
+                     api="fused_rope", norm_type="layernorm",
+                     k_beta=_beta(128, dtype, 7) if with_beta else None)
+
+
+@pytest.mark.parametrize("D,rope,off", [(128, 64, 32), (64, 32, 0), (256, 256, 0), (512, 128, 64),
+                                        (16, 16, 0), (8, 8, 0), (96, 64, 16), (100, 40, 6),
+                                        (128, 2, 126), (40, 40, 0)])
+def test_fused_rope_layernorm_head_sizes_and_windows(tmo, ref, dev, D, rope, off):
+    """Layernorm through the vector path (head sizes 8..512) and the generic path (head sizes
+    not a power-of-two multiple of 8, windows off chunk boundaries)."""
+    for mode in ("none", "dynamic"):
+        case = W.fused_rope_case(torch.bfloat16, mode, 3 * D + rope + off, B=2, S=9, Hq=3, Hk=1, D=D,
+                                 rope=rope, NB=4)
+        check_fused_rope(tmo, ref, dev, f"layernorm D={D} rope={rope}+{off} {mode}", case, True,
+                         off, api="fused_rope", norm_type="layernorm",
+                         k_beta=_beta(D, torch.bfloat16, D))
+
+
+@pytest.mark.parametrize("D,Hq,Hk", [(128, 64, 8), (64, 120, 8)])
+def test_fused_rope_layernorm_many_heads(tmo, ref, dev, D, Hq, Hk):
+    """Layernorm in the row-major kernel (more heads than the token-major kernel takes)."""
+    case = W.fused_rope_case(torch.bfloat16, "dynamic", D + Hq + 1, B=2, S=11, Hq=Hq, Hk=Hk, D=D,
+                             rope=min(D, 128), NB=4)
+    check_fused_rope(tmo, ref, dev, f"layernorm D={D} Hq={Hq} Hk={Hk}", case, True,
+                     api="fused_rope", norm_type="layernorm", k_beta=_beta(D, torch.bfloat16, 1))
 
 
 # ---------------------------------------------------------------------------- reshape_paged_cache

@@ -588,19 +588,21 @@ def test_fp8_conversion_matches_torch(ref):
 
 # ---------------------------------------------------------------------------- fused rope (rmsnorm)
 
-def _sum_squares_chunked(x: torch.Tensor) -> torch.Tensor:
+def _sum_squares_chunked(x: torch.Tensor, square: bool = True) -> torch.Tensor:
     """D10's order with elementwise torch ops: 8-element chunks summed in order, then a
-    balanced tree over the chunk sums (every product and sum a separate IEEE operation)."""
+    balanced tree over the chunk sums (every product and sum a separate IEEE operation).
+    square=False sums the values themselves (D13's mean)."""
     D = x.shape[-1]
     n = (D + 7) // 8
     width = 1 << (n - 1).bit_length()
+    term = (lambda e: x[..., e] * x[..., e]) if square else (lambda e: x[..., e])
     parts = []
     for c in range(width):
         if c < n:
             e0, e1 = 8 * c, min(8 * c + 8, D)
-            acc = x[..., e0] * x[..., e0]
+            acc = term(e0)
             for e in range(e0 + 1, e1):
-                acc = acc + x[..., e] * x[..., e]
+                acc = acc + term(e)
         else:
             acc = torch.zeros_like(x[..., 0])
         parts.append(acc)
@@ -610,11 +612,13 @@ def _sum_squares_chunked(x: torch.Tensor) -> torch.Tensor:
 
 
 def torch_fused_rope(qkv, k_cache, v_cache, sin, cos, position_id, k_gamma, k_scale, v_scale,
-                     slot, eps, q_gamma, off, exact=True, wide=torch.float32):
-    """reference _ops.py:3493-3520 (rmsnorm branch) with apply_rotary's fold math
-    (_ops.py:1116-1127), executed by torch on the CPU in `wide` precision.  exact=True uses
-    D10's summation order (then the result must equal the oracle bit for bit); exact=False
-    uses torch's own mean of squares (the docstring literally)."""
+                     slot, eps, q_gamma, off, exact=True, wide=torch.float32, norm_type="rmsnorm",
+                     k_beta=None):
+    """reference _ops.py:3493-3520 (rmsnorm branch; layernorm branch: rotate, then layer_norm
+    of K, _ops.py:3501-3504) with apply_rotary's fold math (_ops.py:1116-1127), executed by
+    torch on the CPU in `wide` precision.  exact=True uses D10's / D13's summation order (then
+    the result must equal the oracle bit for bit); exact=False uses torch's own mean of
+    squares and torch.nn.functional.layer_norm (the docstring literally)."""
     B, S, H, D = qkv.shape
     NB, Hk, BS, _ = k_cache.shape
     Hq = H - 2 * Hk
@@ -637,6 +641,18 @@ def torch_fused_rope(qkv, k_cache, v_cache, sin, cos, position_id, k_gamma, k_sc
         inv = (1.0 / r.double()).to(wide)
         return (t * inv[..., None]) * gamma.to(wide)
 
+    def layernorm(t):
+        if not exact:
+            b = None if k_beta is None else k_beta.to(wide)
+            return torch.nn.functional.layer_norm(t, (D,), k_gamma.to(wide), b, eps)
+        mean = _sum_squares_chunked(t, square=False) / D
+        d = t - mean[..., None]
+        var = _sum_squares_chunked(d) / D
+        r = torch.sqrt((var + eps).double()).to(wide)
+        inv = (1.0 / r.double()).to(wide)
+        y = (d * inv[..., None]) * k_gamma.to(wide)
+        return y if k_beta is None else y + k_beta.to(wide)
+
     def rotary(y):
         y = y.clone()
         seg = y[..., off:off + rope].clone()
@@ -645,10 +661,14 @@ def torch_fused_rope(qkv, k_cache, v_cache, sin, cos, position_id, k_gamma, k_sc
         return y
 
     q = x[:, :, :Hq]
-    if q_gamma is not None:
-        q = rmsnorm(q, q_gamma)
-    q = rotary(q)
-    k = rotary(rmsnorm(x[:, :, Hq:Hq + Hk], k_gamma))
+    if norm_type == "layernorm":
+        q = rotary(q)
+        k = layernorm(rotary(x[:, :, Hq:Hq + Hk]))
+    else:
+        if q_gamma is not None:
+            q = rmsnorm(q, q_gamma)
+        q = rotary(q)
+        k = rotary(rmsnorm(x[:, :, Hq:Hq + Hk], k_gamma))
     v = x[:, :, Hq + Hk:]
     q_out = qkv.clone()
     q_out[:, :, :Hq] = q.to(qkv.dtype)
@@ -710,6 +730,58 @@ def test_fused_rope_within_one_ulp_of_float64(ref, dtype):
         d = (bits(a).to(torch.int32) - bits(b).to(torch.int32)).abs()
         assert int(d.max()) <= 1
         assert float((d > 0).float().mean()) < 0.05
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("mode", ["none", "dynamic", "static"])
+@pytest.mark.parametrize("with_beta", [True, False])
+def test_fused_rope_layernorm_matches_torch_bitwise(ref, dtype, mode, with_beta):
+    """norm_type "layernorm" (D13): the oracle against the torch-CPU restatement in D13's
+    summation order, bit for bit; q is rotated only (q_gamma is not used), a zero K row
+    becomes beta (or zeros), V is stored unchanged."""
+    for rope, off, D in ((128, 0, 128), (64, 32, 128), (32, 0, 64), (32, 8, 72)):
+        qkv, kc, vc, sin, cos, pid, kg, qg, ks, vs, slot = _frope_case(dtype, mode, 5, D=D, rope=rope,
+                                                                       B=4 if D == 64 else 3)
+        kb = (torch.rand(D, generator=torch.Generator().manual_seed(D)) - 0.5).to(dtype) \
+            if with_beta else None
+        want_kc, want_vc = kc.clone(), vc.clone()
+        want_ks = ks.clone() if mode == "dynamic" else ks
+        want_vs = vs.clone() if mode == "dynamic" else vs
+        want_q = torch_fused_rope(qkv, want_kc, want_vc, sin, cos, pid, kg, want_ks, want_vs, slot,
+                                  1e-5, None, off, norm_type="layernorm", k_beta=kb)
+        got = qkv.clone()
+        ref.fused_rope_paged(got, kc, vc, sin, cos, pid, kg, ks, vs, slot, 1e-5, None, off,
+                             norm_type="layernorm", k_beta=kb)
+        assert torch.equal(bits(got), bits(want_q)), (rope, off)
+        assert torch.equal(bits(kc), bits(want_kc)) and torch.equal(bits(vc), bits(want_vc))
+        if mode == "dynamic":
+            assert torch.equal(bits(ks), bits(want_ks)) and torch.equal(bits(vs), bits(want_vs))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fused_rope_layernorm_within_one_ulp_of_float64(ref, dtype):
+    """norm_type "layernorm" against rotation + torch.nn.functional.layer_norm in float64: q
+    and K at most one ulp of the output type apart, and rarely; for every stored K row of
+    input scale >= 0.3 (eps then below 1e-3 of the variance), (y - beta) / gamma has mean ~0
+    and variance ~1."""
+    qkv, kc, vc, sin, cos, pid, kg, qg, ks, vs, slot = _frope_case(dtype, "none", 11, B=3, S=30)
+    kb = (torch.rand(128, generator=torch.Generator().manual_seed(3)) - 0.5).to(dtype)
+    want_kc, want_vc = kc.clone(), vc.clone()
+    want_q = torch_fused_rope(qkv, want_kc, want_vc, sin, cos, pid, kg, None, None, slot, 1e-5, None,
+                              0, exact=False, wide=torch.float64, norm_type="layernorm", k_beta=kb)
+    got = qkv.clone()
+    ref.fused_rope_paged(got, kc, vc, sin, cos, pid, kg, None, None, slot, 1e-5, None,
+                         norm_type="layernorm", k_beta=kb)
+    for a, b in ((got, want_q), (kc, want_kc)):
+        d = (bits(a).to(torch.int32) - bits(b).to(torch.int32)).abs()
+        assert int(d.max()) <= 1
+        assert float((d > 0).float().mean()) < 0.05
+    flat = slot.reshape(-1)
+    keep = (flat >= 0) & (torch.arange(flat.numel()) % 30 >= 15)   # torch.logspace(-2, 1, 30)[15] ~ 0.32
+    rows = kc.permute(0, 2, 1, 3).reshape(-1, 2, 128)[flat[keep].long()].double()
+    z = (rows - kb.double()) / kg.double()
+    assert float(z.mean(-1).abs().max()) < 0.02
+    assert float((z.var(-1, unbiased=False) - 1).abs().max()) < 0.03
 
 
 # ---------------------------------------------------------------------------- linear caches (D11)
