@@ -133,7 +133,9 @@ __device__ __forceinline__ void pack8(Tag, const float* f, u32x4& w) {
 }
 
 // Vector path: head_dim = 8 * G (G a power of two <= 64), rope window on 8-element chunks.
-template <class Tag, int G>
+// kNorm (0 rmsnorm, 1 layernorm) is p.norm as a template argument, so the rmsnorm instance
+// carries no layernorm registers (p.norm is still what the generic kernel reads).
+template <class Tag, int G, int kNorm>
 __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
   constexpr int kRows = 256 / G;
   const int lane = threadIdx.x & (G - 1);
@@ -162,7 +164,7 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
       const int64_t b = t / p.seq_len;
       pos = (int64_t)p.position[b] + (t - b * p.seq_len);
       if (gamma) gw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(gamma) + lane * 16);
-      if (kind == 1 && p.norm == 1 && p.k_beta)
+      if (kind == 1 && kNorm == 1 && p.k_beta)
         bw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_beta) + lane * 16);
       if (pos >= 0 && pos < p.table_rows && in_win) {
         const int64_t e = pos * p.table_stride + (lane - c0) * 8;
@@ -178,7 +180,7 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
   float y[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = x[e];
-  if (kind != 2 && p.norm == 0 && (kind == 1 || p.q_gamma)) {
+  if (kind != 2 && kNorm == 0 && (kind == 1 || p.q_gamma)) {
     float acc = x[0] * x[0];
 #pragma unroll
     for (int e = 1; e < 8; ++e) {
@@ -224,7 +226,7 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
         y[e] = a + b;
       }
     }
-    if (kind == 1 && p.norm == 1) {  // layernorm of K after its rotation
+    if (kind == 1 && kNorm == 1) {  // layernorm of K after its rotation
       float g[8], bt[8];
       unpack(Tag{}, gw, g);
       unpack(Tag{}, bw, bt);
@@ -287,7 +289,7 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
 // all kR rows loaded before the first is processed.  sin/cos (with the rotation's sign folded
 // in) and both gammas are loaded and unpacked once per workgroup instead of once per row.
 // Same arithmetic, in the same order, as fused_rope_vec.
-template <class Tag, int G, int kR>
+template <class Tag, int G, int kR, int kNorm>
 __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
   constexpr int kGroups = 256 / G;
   const int lane = threadIdx.x & (G - 1);
@@ -318,7 +320,7 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
   kgw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_gamma) + lane * 16);
   if (p.q_gamma) qgw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.q_gamma) + lane * 16);
   u32x4 kbw = {0u, 0u, 0u, 0u};
-  if (p.norm == 1 && p.k_beta)
+  if (kNorm == 1 && p.k_beta)
     kbw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_beta) + lane * 16);
   float sn[8], cs[8], kg[8], qg[8], kb[8];
   unpack(Tag{}, sw, sn);
@@ -340,7 +342,7 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
     float y[8];
     unpack(Tag{}, xw[j], y);
     if (kind != 2) {
-      if (p.norm == 0 && (kind == 1 || p.q_gamma)) {
+      if (kNorm == 0 && (kind == 1 || p.q_gamma)) {
         float acc = y[0] * y[0];
 #pragma unroll
         for (int e = 1; e < 8; ++e) {
@@ -375,7 +377,7 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
           y[e] = a + c;
         }
       }
-      if (kind == 1 && p.norm == 1) layernorm8<G>(y, kg, kb, p.k_beta != nullptr, p.head_dim, p.eps);
+      if (kind == 1 && kNorm == 1) layernorm8<G>(y, kg, kb, p.k_beta != nullptr, p.head_dim, p.eps);
     }
     if (kind == 0) {
       u32x4 o;
@@ -569,7 +571,7 @@ __global__ __launch_bounds__(256) void fused_rope_generic(FusedRopeParams p) {
   }
 }
 
-template <class Tag>
+template <class Tag, int kNorm>
 int launch(const FusedRopeParams& p, hipStream_t stream) {
   const int D = p.head_dim;
   const int G = D / 8;
@@ -587,9 +589,9 @@ int launch(const FusedRopeParams& p, hipStream_t stream) {
     switch (G) {
 #define TMO_FR_CASE(g)                                                                    \
   case g:                                                                                 \
-    if (r <= 1) return launch_kernel(fused_rope_tok<Tag, g, 1>, grid, block, stream, p);  \
-    if (r <= 2) return launch_kernel(fused_rope_tok<Tag, g, 2>, grid, block, stream, p);  \
-    return launch_kernel(fused_rope_tok<Tag, g, 4>, grid, block, stream, p);
+    if (r <= 1) return launch_kernel(fused_rope_tok<Tag, g, 1, kNorm>, grid, block, stream, p);  \
+    if (r <= 2) return launch_kernel(fused_rope_tok<Tag, g, 2, kNorm>, grid, block, stream, p);  \
+    return launch_kernel(fused_rope_tok<Tag, g, 4, kNorm>, grid, block, stream, p);
       TMO_FR_CASE(1)
       TMO_FR_CASE(2)
       TMO_FR_CASE(4)
@@ -608,13 +610,13 @@ int launch(const FusedRopeParams& p, hipStream_t stream) {
   const dim3 grid((unsigned)blocks), block(256);
   if (!vec) return launch_kernel(fused_rope_generic<Tag>, grid, block, stream, p);
   switch (G) {
-    case 1: return launch_kernel(fused_rope_vec<Tag, 1>, grid, block, stream, p);
-    case 2: return launch_kernel(fused_rope_vec<Tag, 2>, grid, block, stream, p);
-    case 4: return launch_kernel(fused_rope_vec<Tag, 4>, grid, block, stream, p);
-    case 8: return launch_kernel(fused_rope_vec<Tag, 8>, grid, block, stream, p);
-    case 16: return launch_kernel(fused_rope_vec<Tag, 16>, grid, block, stream, p);
-    case 32: return launch_kernel(fused_rope_vec<Tag, 32>, grid, block, stream, p);
-    default: return launch_kernel(fused_rope_vec<Tag, 64>, grid, block, stream, p);
+    case 1: return launch_kernel(fused_rope_vec<Tag, 1, kNorm>, grid, block, stream, p);
+    case 2: return launch_kernel(fused_rope_vec<Tag, 2, kNorm>, grid, block, stream, p);
+    case 4: return launch_kernel(fused_rope_vec<Tag, 4, kNorm>, grid, block, stream, p);
+    case 8: return launch_kernel(fused_rope_vec<Tag, 8, kNorm>, grid, block, stream, p);
+    case 16: return launch_kernel(fused_rope_vec<Tag, 16, kNorm>, grid, block, stream, p);
+    case 32: return launch_kernel(fused_rope_vec<Tag, 32, kNorm>, grid, block, stream, p);
+    default: return launch_kernel(fused_rope_vec<Tag, 64, kNorm>, grid, block, stream, p);
   }
 }
 
@@ -680,5 +682,7 @@ extern "C" int tmo_hip_fused_rope_paged(
   p.block_size = (int32_t)block_size;
   p.bs_shift = ilog2_if_pow2(block_size);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return dtype == TMO_DTYPE_F16 ? launch<F16>(p, s) : launch<BF16>(p, s);
+  if (norm_type == 1)
+    return dtype == TMO_DTYPE_F16 ? launch<F16, 1>(p, s) : launch<BF16, 1>(p, s);
+  return dtype == TMO_DTYPE_F16 ? launch<F16, 0>(p, s) : launch<BF16, 0>(p, s);
 }
