@@ -151,8 +151,11 @@ def fused_rope(
     ``slot_mapping_hp`` (negative slots skipped): in qkv's dtype, or int8 with ``k_scale_hp`` /
     ``v_scale_hp`` either ``[num_blocks, kv_heads, block_size]`` (dynamic per-token scales,
     written) or ``[kv_heads, head_size]`` (static per-channel scales, read).  fp32 arithmetic
-    with one final rounding.  This build implements both norm types with paged high-precision
-    caches; the linear-cache and low-precision-cache targets raise ``RuntimeError``.
+    with one final rounding.  Without ``slot_mapping_hp`` the caches are linear ``[max_batch,
+    kv_heads, cache_len, head_size]``: sequence b goes to cache batch ``cache_bs_id_hp[b]``
+    (default b) from position ``cache_seq_offsets_hp[b]`` (default 0), rows outside the cache
+    skipped, dynamic scales ``[max_batch, kv_heads, cache_len]``.  The low-precision (int4)
+    caches raise ``RuntimeError``.
 
     Reference: ``_ops.py:3469-3601`` (math ``:3496-3520``, rotary math ``:1116-1127``).
     Returns ``(qkv, k_cache_hp, v_cache_hp)`` (plus the low-precision tensors when given).

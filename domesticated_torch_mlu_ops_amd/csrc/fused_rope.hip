@@ -46,11 +46,28 @@ struct FusedRopeParams {
   void* cache[2];
   float* scale[2];
   int32_t scale_mode;  // 0 none (caches of qkv's dtype), 1 dynamic per token, 2 static per channel
-  const int32_t* slot;
+  const int32_t* slot;       // paged target: slot per token
+  const int32_t* bs_id;      // linear target: cache batch per sequence (nullable: b)
+  const int32_t* seq_off;    // linear target: first cache position per sequence (nullable: 0)
+  int64_t max_batch;         // linear target: cache batches
+  int32_t linear;            // 1: linear target, 0: paged
   int64_t num_slots;
-  int32_t block_size;
+  int32_t block_size;        // page rows, or the linear cache's length
   int32_t bs_shift;
 };
+
+// Slot of token t.  A linear cache [max_batch, kv_heads, cache_len, head_size] is the paged
+// layout with one page of cache_len rows per cache batch, so token s of sequence b goes to
+// slot cache_bs_id[b] * cache_len + cache_seq_offsets[b] + s, or nowhere (-1) when the cache
+// batch or the position falls outside the cache.
+__device__ __forceinline__ int32_t token_slot(const FusedRopeParams& p, int64_t t) {
+  if (!p.linear) return p.slot[t];
+  const int64_t b = t / p.seq_len;
+  const int64_t cb = p.bs_id ? (int64_t)p.bs_id[b] : b;
+  const int64_t pos = (p.seq_off ? (int64_t)p.seq_off[b] : 0) + (t - b * p.seq_len);
+  if (cb < 0 || cb >= p.max_batch || pos < 0 || pos >= p.block_size) return -1;
+  return (int32_t)(cb * p.block_size + pos);
+}
 
 __device__ __forceinline__ bool page_row_of(const FusedRopeParams& p, int32_t slot, int h,
                                             int64_t& page_row) {
@@ -159,7 +176,7 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
   const void* gamma = kind == 0 ? p.q_gamma : p.k_gamma;
   if (live) {
     xw = *reinterpret_cast<const u32x4*>(xrow);
-    if (kind != 0) slot = p.slot[t];
+    if (kind != 0) slot = token_slot(p, t);
     if (kind != 2) {
       const int64_t b = t / p.seq_len;
       pos = (int64_t)p.position[b] + (t - b * p.seq_len);
@@ -297,7 +314,7 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
   const int64_t t = blockIdx.x;
   const int64_t b = t / p.seq_len;  // workgroup-uniform (scalar)
   const int64_t pos = (int64_t)p.position[b] + (t - b * p.seq_len);
-  const int32_t slot = p.slot[t];
+  const int32_t slot = token_slot(p, t);
   const int c0 = p.rope_off / 8, nwin = p.rope_dim / 8, hc = nwin / 2;
   const bool in_win = lane >= c0 && lane < c0 + nwin;
   const bool rotate = pos >= 0 && pos < p.table_rows;  // workgroup-uniform
@@ -551,7 +568,7 @@ __global__ __launch_bounds__(256) void fused_rope_generic(FusedRopeParams p) {
   const int h = kind == 1 ? hh - p.hq : hh - p.hq - p.hk;
   const int kv = kind - 1;
   int64_t page_row;
-  if (!page_row_of(p, p.slot[t], h, page_row)) return;
+  if (!page_row_of(p, token_slot(p, t), h, page_row)) return;
   if (p.scale_mode == 0) {
     for (int d = lane; d < D; d += kWave) store1(Tag{}, p.cache[kv], page_row * D + d, out_at(d));
     return;
@@ -623,14 +640,19 @@ int launch(const FusedRopeParams& p, hipStream_t stream) {
 }  // namespace
 }  // namespace tmo
 
-extern "C" int tmo_hip_fused_rope_paged(
+namespace {
+
+// Both targets: slot_mapping (paged) or, with `linear`, cache_bs_id / cache_seq_offsets over
+// max_batch cache batches of block_size = cache_len rows.
+int fused_rope_run(
     void* qkv, int64_t num_tokens, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
     int64_t head_size, const void* sin_table, const void* cos_table, int64_t table_rows,
     int64_t table_stride, int64_t rope_dim, int64_t rope_offset, const int32_t* position_ids,
     int64_t batch, const void* k_gamma, const void* k_beta, const void* q_gamma, float eps,
     int norm_type, void* k_cache, void* v_cache, float* k_scale, float* v_scale, int scale_mode,
-    const int32_t* slot_mapping, int64_t num_blocks, int64_t block_size, int dtype,
-    void* stream) {
+    bool linear, const int32_t* slot_mapping, const int32_t* cache_bs_id,
+    const int32_t* cache_seq_offsets, int64_t max_batch, int64_t num_blocks, int64_t block_size,
+    int dtype, void* stream) {
   using namespace tmo;
   if (dtype != TMO_DTYPE_F16 && dtype != TMO_DTYPE_BF16) return TMO_ERR_UNSUPPORTED_DTYPE;
   if (scale_mode < 0 || scale_mode > 2 || norm_type < 0 || norm_type > 1)
@@ -638,7 +660,10 @@ extern "C" int tmo_hip_fused_rope_paged(
   if (norm_type == 1 && q_gamma) return TMO_ERR_INVALID_ARGUMENT;  // rmsnorm-only argument
   if (norm_type == 0 && k_beta) return TMO_ERR_INVALID_ARGUMENT;   // layernorm-only argument
   if (!qkv || !sin_table || !cos_table || !position_ids || !k_gamma || !k_cache || !v_cache ||
-      !slot_mapping)
+      (!linear && !slot_mapping))
+    return TMO_ERR_INVALID_ARGUMENT;
+  // linear target: every slot cache_batch * cache_len + position must fit an int32
+  if (linear && block_size > 0 && num_blocks > 0x7fffffffLL / block_size)
     return TMO_ERR_INVALID_ARGUMENT;
   if (scale_mode != 0 && (!k_scale || !v_scale)) return TMO_ERR_INVALID_ARGUMENT;
   if (num_tokens < 0 || seq_len <= 0 || q_heads < 0 || kv_heads <= 0 || head_size <= 0 ||
@@ -678,6 +703,10 @@ extern "C" int tmo_hip_fused_rope_paged(
   p.scale[1] = v_scale;
   p.scale_mode = scale_mode;
   p.slot = slot_mapping;
+  p.bs_id = cache_bs_id;
+  p.seq_off = cache_seq_offsets;
+  p.max_batch = max_batch;
+  p.linear = linear ? 1 : 0;
   p.num_slots = num_blocks * block_size;
   p.block_size = (int32_t)block_size;
   p.bs_shift = ilog2_if_pow2(block_size);
@@ -685,4 +714,36 @@ extern "C" int tmo_hip_fused_rope_paged(
   if (norm_type == 1)
     return dtype == TMO_DTYPE_F16 ? launch<F16, 1>(p, s) : launch<BF16, 1>(p, s);
   return dtype == TMO_DTYPE_F16 ? launch<F16, 0>(p, s) : launch<BF16, 0>(p, s);
+}
+
+}  // namespace
+
+extern "C" int tmo_hip_fused_rope_paged(
+    void* qkv, int64_t num_tokens, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
+    int64_t head_size, const void* sin_table, const void* cos_table, int64_t table_rows,
+    int64_t table_stride, int64_t rope_dim, int64_t rope_offset, const int32_t* position_ids,
+    int64_t batch, const void* k_gamma, const void* k_beta, const void* q_gamma, float eps,
+    int norm_type, void* k_cache, void* v_cache, float* k_scale, float* v_scale, int scale_mode,
+    const int32_t* slot_mapping, int64_t num_blocks, int64_t block_size, int dtype,
+    void* stream) {
+  return fused_rope_run(qkv, num_tokens, seq_len, q_heads, kv_heads, head_size, sin_table,
+                        cos_table, table_rows, table_stride, rope_dim, rope_offset, position_ids,
+                        batch, k_gamma, k_beta, q_gamma, eps, norm_type, k_cache, v_cache, k_scale,
+                        v_scale, scale_mode, false, slot_mapping, nullptr, nullptr, 0,
+                        num_blocks, block_size, dtype, stream);
+}
+
+extern "C" int tmo_hip_fused_rope_linear(
+    void* qkv, int64_t num_tokens, int64_t seq_len, int64_t q_heads, int64_t kv_heads,
+    int64_t head_size, const void* sin_table, const void* cos_table, int64_t table_rows,
+    int64_t table_stride, int64_t rope_dim, int64_t rope_offset, const int32_t* position_ids,
+    int64_t batch, const void* k_gamma, const void* k_beta, const void* q_gamma, float eps,
+    int norm_type, void* k_cache, void* v_cache, float* k_scale, float* v_scale, int scale_mode,
+    const int32_t* cache_bs_id, const int32_t* cache_seq_offsets, int64_t max_batch,
+    int64_t cache_len, int dtype, void* stream) {
+  return fused_rope_run(qkv, num_tokens, seq_len, q_heads, kv_heads, head_size, sin_table,
+                        cos_table, table_rows, table_stride, rope_dim, rope_offset, position_ids,
+                        batch, k_gamma, k_beta, q_gamma, eps, norm_type, k_cache, v_cache, k_scale,
+                        v_scale, scale_mode, true, nullptr, cache_bs_id, cache_seq_offsets,
+                        max_batch, max_batch, cache_len, dtype, stream);
 }

@@ -249,10 +249,12 @@ void fused_rope(at::Tensor& qkv, at::Tensor& key_cache_hp, at::Tensor& value_cac
   TORCH_CHECK(!key_cache_lp && !value_cache_lp && !key_scale_lp && !value_scale_lp &&
                   !slot_mapping_lp && !cache_bs_id_lp && !cache_seq_offsets_lp,
               "fused_rope: low-precision (int4) caches are not supported by this build");
-  TORCH_CHECK(!cache_bs_id_hp && !cache_seq_offsets_hp,
-              "fused_rope: linear caches (cache_bs_id / cache_seq_offsets) are not supported by "
-              "this build; pass slot_mapping_hp for paged caches");
-  TORCH_CHECK(slot_mapping_hp.has_value(), "fused_rope: slot_mapping_hp is required");
+  // the target: paged caches through slot_mapping_hp, else linear caches [max_batch, kv_heads,
+  // cache_len, head_size] through cache_bs_id_hp / cache_seq_offsets_hp (either may be None)
+  const bool linear = !slot_mapping_hp.has_value();
+  TORCH_CHECK(linear || (!cache_bs_id_hp && !cache_seq_offsets_hp),
+              "fused_rope: pass slot_mapping_hp (paged caches) or cache_bs_id_hp / "
+              "cache_seq_offsets_hp (linear caches), not both");
   TORCH_CHECK(layernorm || !k_beta.has_value(), "fused_rope: k_beta applies to layernorm only");
   check_device(qkv, qkv, "qkv");
   TORCH_CHECK(qkv.dim() == 4 && qkv.is_contiguous(),
@@ -269,7 +271,8 @@ void fused_rope(at::Tensor& qkv, at::Tensor& key_cache_hp, at::Tensor& value_cac
   const int64_t NB = key_cache_hp.size(0), Hk = key_cache_hp.size(1), BS = key_cache_hp.size(2);
   TORCH_CHECK(key_cache_hp.size(3) == D && value_cache_hp.sizes() == key_cache_hp.sizes() &&
                   value_cache_hp.scalar_type() == key_cache_hp.scalar_type(),
-              "key/value caches must be [num_blocks, kv_heads, block_size, head_size] alike");
+              "key/value caches must be [num_blocks, kv_heads, block_size, head_size] (or "
+              "[max_batch, kv_heads, cache_len, head_size]) alike");
   TORCH_CHECK(H > 2 * Hk, "qkv has ", H, " heads, fewer than 2 * kv_heads + 1");
   const int64_t Hq = H - 2 * Hk;
   int mode = 0;
@@ -290,7 +293,7 @@ void fused_rope(at::Tensor& qkv, at::Tensor& key_cache_hp, at::Tensor& value_cac
       TORCH_CHECK(key_scale_hp->size(0) == NB && key_scale_hp->size(1) == Hk &&
                       key_scale_hp->size(2) == BS &&
                       value_scale_hp->sizes() == key_scale_hp->sizes(),
-                  "dynamic scales must be [num_blocks, kv_heads, block_size]");
+                  "dynamic scales must be [num_blocks, kv_heads, block_size] ([max_batch, kv_heads, cache_len] for linear caches)");
     } else {
       mode = 2;  // static per channel: read
       TORCH_CHECK(key_scale_hp->dim() == 2 && key_scale_hp->size(0) == Hk &&
@@ -330,20 +333,45 @@ void fused_rope(at::Tensor& qkv, at::Tensor& key_cache_hp, at::Tensor& value_cac
                     g->is_contiguous(),
                 "gammas and k_beta must be contiguous [head_size] tensors of qkv's dtype");
   }
-  const at::Tensor& slot = *slot_mapping_hp;
-  check_device(slot, qkv, "slot_mapping");
-  TORCH_CHECK(slot.scalar_type() == at::kInt && slot.numel() == B * S && slot.is_contiguous(),
-              "slot_mapping must be a contiguous int32 tensor of batch * seq_len entries");
   TORCH_CHECK(D <= 512, "fused_rope: head_size must be <= 512");
+  if (linear) {
+    for (const c10::optional<at::Tensor>* t : {&cache_bs_id_hp, &cache_seq_offsets_hp}) {
+      if (!t->has_value()) continue;
+      check_device(**t, qkv, "cache_bs_id / cache_seq_offsets");
+      TORCH_CHECK((*t)->scalar_type() == at::kInt && (*t)->dim() == 1 && (*t)->size(0) == B &&
+                      (*t)->is_contiguous(),
+                  "cache_bs_id_hp / cache_seq_offsets_hp must be contiguous int32 [batch] tensors");
+    }
+    TORCH_CHECK(NB * BS <= 0x7fffffffLL,
+                "fused_rope: linear caches of more than 2^31 - 1 rows per head are not supported");
+  } else {
+    const at::Tensor& slot = *slot_mapping_hp;
+    check_device(slot, qkv, "slot_mapping");
+    TORCH_CHECK(slot.scalar_type() == at::kInt && slot.numel() == B * S && slot.is_contiguous(),
+                "slot_mapping must be a contiguous int32 tensor of batch * seq_len entries");
+  }
   if (B * S == 0) return;
   c10::DeviceGuard guard(qkv.device());
-  const int st = tmo_hip_fused_rope_paged(
-      qkv.data_ptr(), B * S, S, Hq, Hk, D, sin_table.data_ptr(), cos_table.data_ptr(),
-      sin_table.size(0), sin_table.stride(0), rope_dim, off, position_ids.data_ptr<int32_t>(), B,
-      gamma.data_ptr(), kb ? kb->data_ptr() : nullptr, qg ? qg->data_ptr() : nullptr,
-      static_cast<float>(eps), layernorm ? 1 : 0, key_cache_hp.data_ptr(),
-      value_cache_hp.data_ptr(), ks, vs, mode,
-      slot.data_ptr<int32_t>(), NB, BS, dt, stream_of(qkv));
+  auto i32 = [](const c10::optional<at::Tensor>& t) -> const int32_t* {
+    return t.has_value() ? t->data_ptr<int32_t>() : nullptr;
+  };
+  const int st =
+      linear ? tmo_hip_fused_rope_linear(
+                   qkv.data_ptr(), B * S, S, Hq, Hk, D, sin_table.data_ptr(), cos_table.data_ptr(),
+                   sin_table.size(0), sin_table.stride(0), rope_dim, off,
+                   position_ids.data_ptr<int32_t>(), B, gamma.data_ptr(),
+                   kb ? kb->data_ptr() : nullptr, qg ? qg->data_ptr() : nullptr,
+                   static_cast<float>(eps), layernorm ? 1 : 0, key_cache_hp.data_ptr(),
+                   value_cache_hp.data_ptr(), ks, vs, mode, i32(cache_bs_id_hp),
+                   i32(cache_seq_offsets_hp), NB, BS, dt, stream_of(qkv))
+             : tmo_hip_fused_rope_paged(
+                   qkv.data_ptr(), B * S, S, Hq, Hk, D, sin_table.data_ptr(), cos_table.data_ptr(),
+                   sin_table.size(0), sin_table.stride(0), rope_dim, off,
+                   position_ids.data_ptr<int32_t>(), B, gamma.data_ptr(),
+                   kb ? kb->data_ptr() : nullptr, qg ? qg->data_ptr() : nullptr,
+                   static_cast<float>(eps), layernorm ? 1 : 0, key_cache_hp.data_ptr(),
+                   value_cache_hp.data_ptr(), ks, vs, mode, slot_mapping_hp->data_ptr<int32_t>(),
+                   NB, BS, dt, stream_of(qkv));
   check_status(st, "fused_rope");
 }
 

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 8
+#define TMO_HIP_ABI_VERSION 9
 
 /* element types */
 enum tmo_dtype {
@@ -156,6 +156,31 @@ int tmo_hip_fused_rope_paged(void* qkv, int64_t num_tokens, int64_t seq_len,
                              void* k_cache, void* v_cache, float* k_scale, float* v_scale,
                              int scale_mode, const int32_t* slot_mapping,
                              int64_t num_blocks, int64_t block_size, int dtype, void* stream);
+
+/*
+ * fused_rope_linear -- fused_rope_paged's arithmetic with linear high-precision caches
+ * k_cache / v_cache [max_batch, kv_heads, cache_len, head_size] as the target: token s of
+ * sequence b (token t = b * seq_len + s) is stored at cache batch cb = cache_bs_id[b] (b when
+ * cache_bs_id is NULL), position cache_seq_offsets[b] + s (s when cache_seq_offsets is NULL);
+ * rows whose cb is outside [0, max_batch) or whose position is outside [0, cache_len) are not
+ * stored (Q is still written back).  Dynamic scales (scale_mode 1) are [max_batch, kv_heads,
+ * cache_len]; static ones (2) [kv_heads, head_size].  max_batch * cache_len must fit an int32.
+ * Replaces tmo::torch_api::fused_rope (reference include/torch_mlu_ops.h:562-585) with
+ * cache_bs_id_hp / cache_seq_offsets_hp, called by torch_mlu_ops.fused_rope (reference
+ * _ops.py:3469-3601, "reshape_linear_cache" branch of its Math).
+ */
+int tmo_hip_fused_rope_linear(void* qkv, int64_t num_tokens, int64_t seq_len,
+                              int64_t q_heads, int64_t kv_heads, int64_t head_size,
+                              const void* sin_table, const void* cos_table,
+                              int64_t table_rows, int64_t table_stride,
+                              int64_t rope_dim, int64_t rope_offset,
+                              const int32_t* position_ids, int64_t batch,
+                              const void* k_gamma, const void* k_beta, const void* q_gamma,
+                              float eps, int norm_type,
+                              void* k_cache, void* v_cache, float* k_scale, float* v_scale,
+                              int scale_mode, const int32_t* cache_bs_id,
+                              const int32_t* cache_seq_offsets, int64_t max_batch,
+                              int64_t cache_len, int dtype, void* stream);
 
 /*
  * dequant_from_paged_cache -- gathers each sequence's pages through block_tables and writes

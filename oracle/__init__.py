@@ -176,6 +176,27 @@ def fused_rope_paged(qkv, k_cache, v_cache, sin_cache, cos_cache, position_id, k
     _check(rc, "fused_rope_paged")
 
 
+def fused_rope_linear(qkv, k_cache, v_cache, sin_cache, cos_cache, position_id, k_gamma, k_scale,
+                      v_scale, cache_bs_id, cache_seq_offsets, eps: float = 1e-5, q_gamma=None,
+                      rope_dim_offset: int = 0, nthreads: Optional[int] = None,
+                      norm_type: str = "rmsnorm", k_beta=None) -> None:
+    """reference _ops.py:3469-3601 with linear hp caches [max_batch, kv_heads, cache_len,
+    head_size] (decision D14 of tmo_oracle.c): token s of sequence b goes to cache batch
+    cache_bs_id[b] (default b) at position cache_seq_offsets[b] + s (default s), and nowhere
+    when either falls outside the cache.  That layout is the paged one with one page of
+    cache_len rows per cache batch, so the rows are mapped to those slots and stored by
+    fused_rope_paged."""
+    B, S = qkv.shape[:2]
+    MB, _, L, _ = k_cache.shape
+    cb = (cache_bs_id.long() if cache_bs_id is not None else torch.arange(B))[:, None].expand(B, S)
+    pos = torch.arange(S)[None, :] + (cache_seq_offsets.long()[:, None]
+                                      if cache_seq_offsets is not None else 0)
+    ok = (cb >= 0) & (cb < MB) & (pos >= 0) & (pos < L)
+    slot = torch.where(ok, cb * L + pos, torch.full_like(pos, -1)).to(torch.int32)
+    fused_rope_paged(qkv, k_cache, v_cache, sin_cache, cos_cache, position_id, k_gamma, k_scale,
+                     v_scale, slot, eps, q_gamma, rope_dim_offset, nthreads, norm_type, k_beta)
+
+
 def f32_to_e4m3(x: torch.Tensor) -> torch.Tensor:
     """float8_e4m3fn bit patterns (uint8) of fp32 values |x| <= 448, round to nearest even."""
     x = x.to(torch.float32).contiguous()

@@ -36,6 +36,13 @@
  *       d = RN(x - mean); var = RN(s2 / D) with s2 the chunked sum of RN(d * d) (biased, as
  *       torch's layer_norm); inv = RN(1 / RN(sqrt(RN(var + eps)))); y = RN(RN(d * inv) *
  *       gamma), then RN(y + beta) when beta is given.  q_gamma is not used.
+ *   D14 fused_rope with linear caches [max_batch, kv_heads, cache_len, head_size]
+ *       (cache_bs_id_hp / cache_seq_offsets_hp, _ops.py:3469-3601 "reshape_linear_cache"
+ *       branch): token s of sequence b is stored at cache batch cache_bs_id[b] (b when absent),
+ *       position cache_seq_offsets[b] + s (s when absent), and not at all when the batch or the
+ *       position is outside the cache; dynamic scales [max_batch, kv_heads, cache_len].  The
+ *       layout equals the paged one with cache_len-row pages, one per cache batch: the Python
+ *       wrapper (fused_rope_linear) maps each token to that slot and runs this function.
  *   D11 linear caches [max_batch, H, cache_len, D] (_ops.py:1189-1249, 1708-1919, 3642-3732,
  *       3898-3969): sequence i covers len_i tokens -- cu[i+1] - cu[i] when the input is
  *       packed (context_lengths holds batch + 1 prefix offsets), else context_lengths[i]; its

@@ -41,6 +41,8 @@ def lib():
     L.tmo_hip_scaled_quantize_per_token.argtypes = [P] + [I64] * 4 + [P] * 3 + [I64, P, I64, P, I64, P, I64, INT, P]
     L.tmo_hip_fused_rope_paged.argtypes = [P] + [I64] * 5 + [P, P] + [I64] * 4 + [P, I64, P, P, P] + \
         [ctypes.c_float, INT] + [P] * 4 + [INT, P, I64, I64, INT, P]
+    L.tmo_hip_fused_rope_linear.argtypes = [P] + [I64] * 5 + [P, P] + [I64] * 4 + [P, I64, P, P, P] + \
+        [ctypes.c_float, INT] + [P] * 4 + [INT, P, P, I64, I64, INT, P]
     L.tmo_hip_offline_quant_to_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 4 + \
         [ctypes.c_float] * 2 + [P] + [I64] * 5 + [INT, INT, P]
     L.tmo_hip_reshape_linear_cache.argtypes = [P, P] + [I64] * 5 + [P, P] + [I64] * 4 + \
@@ -68,7 +70,7 @@ def test_every_declared_symbol_is_exported(lib):
                           "tmo_hip_dequant_from_paged_cache", "tmo_hip_dequant_workspace_bytes",
                           "tmo_hip_scaled_quantize_per_token",
                           "tmo_hip_offline_quant_to_paged_cache", "tmo_hip_fused_rope_paged",
-                          "tmo_hip_reshape_linear_cache", "tmo_hip_quant_to_linear_cache",
+                          "tmo_hip_fused_rope_linear", "tmo_hip_reshape_linear_cache", "tmo_hip_quant_to_linear_cache",
                           "tmo_hip_offline_quant_to_linear_cache",
                           "tmo_hip_dequant_from_linear_cache", "tmo_hip_reshape_from_cache",
                           "tmo_hip_single_query_cached_kv_attn", "tmo_hip_attn_workspace_bytes"}
@@ -207,6 +209,21 @@ def test_fused_rope_validation(lib):
     assert call(stride=64) == EINVAL         # table rows shorter than rope_dim
     assert call(T=9) == EINVAL               # more tokens than batch * seq_len
     assert call(T=0) == 0
+
+
+def test_fused_rope_linear_validation(lib):
+    def call(mode=0, ks=None, T=8, MB=4, L=64, bs_id=None, off=None, norm=0, qg=None):
+        return lib.tmo_hip_fused_rope_linear(FAKE, T, 8, 4, 2, 128, FAKE, FAKE, 64, 128, 128, 0,
+                                             FAKE, 1, FAKE, None, qg, 1e-5, norm, FAKE, FAKE, ks,
+                                             ks, mode, bs_id, off, MB, L, 2, None)
+    assert call(mode=3) == EMODE
+    assert call(mode=2) == EINVAL            # quantised without scales
+    assert call(norm=1, qg=FAKE) == EINVAL
+    assert call(L=0) == EINVAL               # cache_len must be positive
+    assert call(MB=-1) == EINVAL
+    assert call(MB=1 << 20, L=1 << 12) == EINVAL  # slots past int32
+    assert call(T=0) == 0
+    assert call(T=0, MB=0) == 0              # no cache batches: nothing to store
 
 
 def lin_write(lib, fn, *, key=FAKE, value=None, kc=FAKE, vc=None, rows=64, MB=4, H=8, L=32,

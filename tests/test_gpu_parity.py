@@ -414,6 +414,58 @@ def test_fused_rope_layernorm_many_heads(tmo, ref, dev, D, Hq, Hk):
                      api="fused_rope", norm_type="layernorm", k_beta=_beta(D, torch.bfloat16, 1))
 
 
+@pytest.mark.parametrize("mode", ["none", "dynamic", "static"])
+@pytest.mark.parametrize("norm_type", ["rmsnorm", "layernorm"])
+@pytest.mark.parametrize("D,Hq,ids", [(128, 8, "given"), (128, 8, "default"), (64, 200, "given"),
+                                      (96, 4, "given")])
+def test_fused_rope_linear_caches(tmo, ref, dev, mode, norm_type, D, Hq, ids):
+    """fused_rope into linear caches [max_batch, kv_heads, cache_len, head_size] through
+    cache_bs_id_hp / cache_seq_offsets_hp (token-major, row-major and generic kernels): a -1
+    cache batch, a batch id past the cache, positions past cache_len; from sentinel caches."""
+    qkv, _, _, sin, cos, pid, kg, qg, ks, vs, _ = W.fused_rope_case(
+        torch.bfloat16, mode, D + Hq, B=4, S=13, Hq=Hq, Hk=2, D=D, rope=min(D, 64))
+    MB, L = 6, 40
+    cdt = torch.bfloat16 if mode == "none" else torch.int8
+    kc = torch.zeros(MB, 2, L, D, dtype=cdt).view(torch.uint8).fill_(0x5A).view(cdt)
+    vc = kc.clone()
+    if mode == "dynamic":
+        ks = torch.full((MB, 2, L), W.SCALE_SENTINEL)
+        vs = ks.clone()
+    if ids == "given":
+        bs_id = torch.tensor([5, -1, 0, 9], dtype=torch.int32)
+        offs = torch.tensor([0, 4, 33, 20], dtype=torch.int32)
+    else:
+        bs_id = offs = None
+    kb = (torch.rand(D, generator=torch.Generator().manual_seed(4)) - 0.5).to(torch.bfloat16) \
+        if norm_type == "layernorm" else None
+    qg = qg if norm_type == "rmsnorm" else None
+    want = [qkv.clone(), kc.clone(), vc.clone(),
+            ks.clone() if ks is not None else None, vs.clone() if vs is not None else None]
+    ref.fused_rope_linear(want[0], want[1], want[2], sin, cos, pid, kg, want[3], want[4], bs_id,
+                          offs, 1e-5, qg, norm_type=norm_type, k_beta=kb)
+    d = (lambda t: t.to(dev) if t is not None else None)
+    got = [d(qkv), d(kc), d(vc), d(ks), d(vs)]
+    name = f"linear {mode} {norm_type} D={D} Hq={Hq} ids={ids}"
+    print(f"[fused_rope linear] {name}", flush=True)
+    out = tmo.fused_rope(got[0], got[1], got[2], d(sin), d(cos), d(pid), d(kg), d(kb),
+                         cache_bs_id_hp=d(bs_id), cache_seq_offsets_hp=d(offs),
+                         k_scale_hp=got[3], v_scale_hp=got[4], norm_type=norm_type, eps=1e-5,
+                         q_gamma=d(qg))
+    assert len(out) == 3 and out[0] is got[0]
+    for g, w, n in zip(got, want, ("qkv", "k_cache", "v_cache", "k_scale", "v_scale")):
+        if w is not None:
+            assert_bits_equal(g, w, f"{name} {n}")
+
+
+def test_fused_rope_rejects_both_targets(tmo, dev):
+    qkv, kc, vc, sin, cos, pid, kg, qg, ks, vs, slot = W.fused_rope_case(torch.bfloat16, "none", 1)
+    d = (lambda t: t.to(dev))
+    with pytest.raises(RuntimeError, match="not both"):
+        tmo.fused_rope(d(qkv), d(kc), d(vc), d(sin), d(cos), d(pid), d(kg), None,
+                       slot_mapping_hp=d(slot), cache_bs_id_hp=d(torch.zeros(3, dtype=torch.int32)),
+                       norm_type="rmsnorm")
+
+
 # ---------------------------------------------------------------------------- reshape_paged_cache
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32, torch.int8])

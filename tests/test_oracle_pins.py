@@ -613,7 +613,7 @@ def _sum_squares_chunked(x: torch.Tensor, square: bool = True) -> torch.Tensor:
 
 def torch_fused_rope(qkv, k_cache, v_cache, sin, cos, position_id, k_gamma, k_scale, v_scale,
                      slot, eps, q_gamma, off, exact=True, wide=torch.float32, norm_type="rmsnorm",
-                     k_beta=None):
+                     k_beta=None, linear=None):
     """reference _ops.py:3493-3520 (rmsnorm branch; layernorm branch: rotate, then layer_norm
     of K, _ops.py:3501-3504) with apply_rotary's fold math (_ops.py:1116-1127), executed by
     torch on the CPU in `wide` precision.  exact=True uses D10's / D13's summation order (then
@@ -672,6 +672,23 @@ def torch_fused_rope(qkv, k_cache, v_cache, sin, cos, position_id, k_gamma, k_sc
     v = x[:, :, Hq + Hk:]
     q_out = qkv.clone()
     q_out[:, :, :Hq] = q.to(qkv.dtype)
+    if linear is not None:  # linear caches [max_batch, Hk, cache_len, D], indexed directly
+        bs_id, offs = linear
+        for b in range(B):
+            cb = int(bs_id[b]) if bs_id is not None else b
+            for s_ in range(S):
+                p = (int(offs[b]) if offs is not None else 0) + s_
+                if not (0 <= cb < NB and 0 <= p < BS):
+                    continue
+                for t, c, sc in ((k, k_cache, k_scale), (v, v_cache, v_scale)):
+                    row = t[b, s_]
+                    if sc is None:
+                        c[cb, :, p] = row.to(c.dtype)
+                    elif sc.dim() == 3:
+                        c[cb, :, p], sc[cb, :, p] = torch_row_quant(row.to(torch.float32))
+                    else:
+                        c[cb, :, p] = (row.to(torch.float32) / sc).round().clamp(-128, 127).to(torch.int8)
+        return q_out
     flat = slot.reshape(-1)
     valid = (flat >= 0) & (flat < NB * BS)
     s_ = flat[valid].long()
@@ -782,6 +799,44 @@ def test_fused_rope_layernorm_within_one_ulp_of_float64(ref, dtype):
     z = (rows - kb.double()) / kg.double()
     assert float(z.mean(-1).abs().max()) < 0.02
     assert float((z.var(-1, unbiased=False) - 1).abs().max()) < 0.03
+
+
+@pytest.mark.parametrize("mode", ["none", "dynamic", "static"])
+@pytest.mark.parametrize("norm_type", ["rmsnorm", "layernorm"])
+@pytest.mark.parametrize("ids", ["given", "default"])
+def test_fused_rope_linear_matches_torch_indexing(ref, mode, norm_type, ids):
+    """D14: linear caches through cache_bs_id / cache_seq_offsets.  The oracle's slot mapping
+    against the torch restatement that indexes cache[cache_bs_id[b], :, offset[b] + s]
+    directly: caches and scales equal bit for bit, rows of a -1 cache batch, a batch id past
+    the cache and positions past cache_len not stored (their sentinel survives)."""
+    qkv, kc, vc, sin, cos, pid, kg, qg, ks, vs, _ = _frope_case(torch.bfloat16, mode, 13, B=4, S=12)
+    MB, L = 5, 30
+    kc = torch.full((MB, 2, L, 128), 7, dtype=kc.dtype)
+    vc = torch.full_like(kc, 9)
+    if mode == "dynamic":
+        ks, vs = torch.full((MB, 2, L), -1.0), torch.full((MB, 2, L), -1.0)
+    if ids == "given":
+        bs_id = torch.tensor([3, -1, 0, 7], dtype=torch.int32)   # 7: past the cache's 5 batches
+        offs = torch.tensor([0, 4, 25, 10], dtype=torch.int32)   # 25 + 11 runs past cache_len
+    else:
+        bs_id = offs = None
+    kb = torch.rand(128, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16) \
+        if norm_type == "layernorm" else None
+    qg = qg if norm_type == "rmsnorm" else None
+    want_kc, want_vc = kc.clone(), vc.clone()
+    want_ks = ks.clone() if mode == "dynamic" else ks
+    want_vs = vs.clone() if mode == "dynamic" else vs
+    want_q = torch_fused_rope(qkv, want_kc, want_vc, sin, cos, pid, kg, want_ks, want_vs, None,
+                              1e-5, qg, 0, norm_type=norm_type, k_beta=kb, linear=(bs_id, offs))
+    got = qkv.clone()
+    ref.fused_rope_linear(got, kc, vc, sin, cos, pid, kg, ks, vs, bs_id, offs, 1e-5, qg,
+                          norm_type=norm_type, k_beta=kb)
+    assert torch.equal(bits(got), bits(want_q))
+    assert torch.equal(bits(kc), bits(want_kc)) and torch.equal(bits(vc), bits(want_vc))
+    if mode == "dynamic":
+        assert torch.equal(bits(ks), bits(want_ks)) and torch.equal(bits(vs), bits(want_vs))
+    if ids == "given":
+        assert bool((kc[1] == 7).all()) and bool((kc[4] == 7).all())  # no sequence maps there
 
 
 # ---------------------------------------------------------------------------- linear caches (D11)
