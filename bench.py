@@ -60,7 +60,7 @@ KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<
            "cfg4_moe": "sq_vec<BF16,8,false,1>", "cfg5": "dequant_paged_list<BF16,1,2>",
            "offline_i8": "quant_paged_static_vec<BF16,16,false>",
            "offline_f8": "quant_paged_static_vec<BF16,16,true>",
-           "fused_rope": "fused_rope_tok<BF16,16,4,0>",
+           "fused_rope": "fused_rope_tok<BF16,16,3,0>",
            "linear_quant": "lin_quant<BF16,16,false,false>", "linear_dequant": "lin_dequant<BF16,16>",
            "linear_reshape": "lin_copy<16>", "decode_attn": "attn_mfma<128,0,false>"}
 

@@ -339,15 +339,8 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
   u32x4 kbw = {0u, 0u, 0u, 0u};
   if (kNorm == 1 && p.k_beta)
     kbw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_beta) + lane * 16);
-  float sn[8], cs[8], kg[8], qg[8], kb[8];
-  unpack(Tag{}, sw, sn);
-  unpack(Tag{}, cw, cs);
-  unpack(Tag{}, kgw, kg);
-  unpack(Tag{}, qgw, qg);
-  unpack(Tag{}, kbw, kb);
+  // sin/cos, gammas and beta stay packed until their use in each row (fewer live VGPRs)
   const float sign = lane < c0 + hc ? -1.0f : 1.0f;  // rot = -partner in the window's first half
-#pragma unroll
-  for (int e = 0; e < 8; ++e) sn[e] = sn[e] * sign;
   const bool store_kv = slot >= 0 && (int64_t)slot < p.num_slots;  // workgroup-uniform
 
 #pragma unroll
@@ -367,7 +360,8 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
           acc = acc + sq;
         }
         const float inv = rms_inverse(group_sum_f32<G>(acc), p.head_dim, p.eps);
-        const float* g = kind == 1 ? kg : qg;
+        float g[8];
+        unpack(Tag{}, kind == 1 ? kgw : qgw, g);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float n = y[e] * inv;
@@ -387,14 +381,22 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
         for (int e = 0; e < 8; ++e) partner[e] = __shfl(y[e], base + src, 64);
       }
       if (rotate && in_win) {
+        float sn[8], cs[8];
+        unpack(Tag{}, sw, sn);
+        unpack(Tag{}, cw, cs);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float a = partner[e] * sn[e];
+          const float a = partner[e] * (sn[e] * sign);
           const float c = y[e] * cs[e];
           y[e] = a + c;
         }
       }
-      if (kind == 1 && kNorm == 1) layernorm8<G>(y, kg, kb, p.k_beta != nullptr, p.head_dim, p.eps);
+      if (kind == 1 && kNorm == 1) {
+        float kg[8], kb[8];
+        unpack(Tag{}, kgw, kg);
+        unpack(Tag{}, kbw, kb);
+        layernorm8<G>(y, kg, kb, p.k_beta != nullptr, p.head_dim, p.eps);
+      }
     }
     if (kind == 0) {
       u32x4 o;
@@ -608,6 +610,7 @@ int launch(const FusedRopeParams& p, hipStream_t stream) {
   case g:                                                                                 \
     if (r <= 1) return launch_kernel(fused_rope_tok<Tag, g, 1, kNorm>, grid, block, stream, p);  \
     if (r <= 2) return launch_kernel(fused_rope_tok<Tag, g, 2, kNorm>, grid, block, stream, p);  \
+    if (r <= 3) return launch_kernel(fused_rope_tok<Tag, g, 3, kNorm>, grid, block, stream, p);  \
     return launch_kernel(fused_rope_tok<Tag, g, 4, kNorm>, grid, block, stream, p);
       TMO_FR_CASE(1)
       TMO_FR_CASE(2)
