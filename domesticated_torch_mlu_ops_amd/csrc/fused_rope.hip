@@ -321,12 +321,14 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
 
   // rows of this group: heads grp, grp + kGroups, ... (kR of them at most)
   char* xbase = static_cast<char*>(p.qkv) + (t * p.heads * p.head_dim + lane * 8) * Tag::kBytes;
+  // unconditional loads (a row past the last head re-reads the last head, in bounds, and is
+  // not used): with the loads under a branch the compiler merged the array through register
+  // copies that waited for each load before the next was issued
   u32x4 xw[kR];
 #pragma unroll
   for (int j = 0; j < kR; ++j) {
-    const int hh = grp + j * kGroups;
-    if (hh < p.heads)
-      xw[j] = *reinterpret_cast<const u32x4*>(xbase + (int64_t)hh * p.head_dim * Tag::kBytes);
+    const int hh = min(grp + j * kGroups, p.heads - 1);
+    xw[j] = *reinterpret_cast<const u32x4*>(xbase + (int64_t)hh * p.head_dim * Tag::kBytes);
   }
   u32x4 sw = {0u, 0u, 0u, 0u}, cw = {0u, 0u, 0u, 0u}, kgw = {0u, 0u, 0u, 0u}, qgw = {0u, 0u, 0u, 0u};
   if (rotate && in_win) {
