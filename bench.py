@@ -50,6 +50,7 @@ WORKLOADS = {
     "offline_i8": "offline_quant_to_paged_cache on configs[2]'s shape (32768 tokens x 8 KV heads x 128 bf16), static per-channel scales -> int8 pages",
     "offline_f8": "offline_quant_to_paged_cache on configs[2]'s shape (32768 tokens x 8 KV heads x 128 bf16), static per-channel scales -> float8_e4m3fn pages",
     "fused_rope": "fused_rmsnorm_rope_store_paged_cache, Llama-3-8B prefill chunk: 8 x 4096 tokens, 32 Q + 8 KV heads x 128 bf16, Q written back, K/V -> int8 pages with dynamic per-token scales (65536 blocks x 16)",
+    "fused_rope_ln": "fused_rope, norm_type layernorm (rotate, then layer_norm of K with gamma and beta) on the fused_rope workload's shape: 8 x 4096 tokens, 32 Q + 8 KV heads x 128 bf16 -> int8 pages with dynamic per-token scales",
     "linear_quant": "quant_to_linear_cache on configs[2]'s volume: 8 packed sequences x 4096 tokens x 8 KV heads x 128 bf16 -> int8 linear cache [8, 8, 8192, 128] + fp32 per-token scales",
     "linear_dequant": "dequant_from_linear_cache (per-token scales), 8 sequences x 4096 tokens x 8 KV heads x 128: int8 linear cache [8, 8, 8192, 128] -> bf16",
     "linear_reshape": "reshape_linear_cache, 8 packed sequences x 4096 tokens x 8 KV heads x 128 bf16 -> bf16 linear cache [8, 8, 8192, 128]",
@@ -60,7 +61,7 @@ KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<
            "cfg4_moe": "sq_vec<BF16,8,false,1>", "cfg5": "dequant_paged_list<BF16,1,2>",
            "offline_i8": "quant_paged_static_vec<BF16,16,false>",
            "offline_f8": "quant_paged_static_vec<BF16,16,true>",
-           "fused_rope": "fused_rope_tok<BF16,16,3,0>",
+           "fused_rope": "fused_rope_tok<BF16,16,3,0>", "fused_rope_ln": "fused_rope_tok<BF16,16,3,1>",
            "linear_quant": "lin_quant<BF16,16,false,false>", "linear_dequant": "lin_dequant<BF16,16>",
            "linear_reshape": "lin_copy<16>", "decode_attn": "attn_mfma<128,0,false>"}
 
@@ -207,9 +208,10 @@ def fused_rope_bytes(T: int, rope: int = 128) -> int:
 W_D = 128
 
 
-def bench_fused_rope(torch, tmo, W, dev, steps, warmup):
-    """fused_rmsnorm_rope_store_paged_cache on a Llama-3-8B-shaped prefill chunk: per set its
-    own qkv; shared int8 caches and scales, configs[2]-style slots shifted per set."""
+def bench_fused_rope(torch, tmo, W, dev, steps, warmup, layernorm=False):
+    """fused_rmsnorm_rope_store_paged_cache (or fused_rope with norm_type "layernorm") on a
+    Llama-3-8B-shaped prefill chunk: per set its own qkv; shared int8 caches and scales,
+    configs[2]-style slots shifted per set."""
     T = FR_B * FR_S
     alg = fused_rope_bytes(T)
     sets = n_sets(alg)
@@ -235,8 +237,13 @@ def bench_fused_rope(torch, tmo, W, dev, steps, warmup):
         qkv = torch.randn((FR_B, FR_S, FR_HQ + 2 * FR_HK, W_D), generator=g, device=dev).to(torch.bfloat16)
         shift = (s * 9973 * case3.block_size) % nslots
         slots = (slots0 + shift) % nslots
-        calls.append(lambda qkv=qkv, sl=slots: tmo.fused_rmsnorm_rope_store_paged_cache(
-            qkv, kc, vc, sin, cos, pid, kg, qg, sl, ks, vs, 1e-5))
+        if layernorm:  # qg serves as k_beta
+            calls.append(lambda qkv=qkv, sl=slots: tmo.fused_rope(
+                qkv, kc, vc, sin, cos, pid, kg, qg, k_scale_hp=ks, v_scale_hp=vs,
+                slot_mapping_hp=sl, norm_type="layernorm", eps=1e-5))
+        else:
+            calls.append(lambda qkv=qkv, sl=slots: tmo.fused_rmsnorm_rope_store_paged_cache(
+                qkv, kc, vc, sin, cos, pid, kg, qg, sl, ks, vs, 1e-5))
     ms = time_graph(torch, calls, steps, warmup)
     return ms, alg, T, sets
 
@@ -375,7 +382,7 @@ def profile_pass(torch, tmo, W, names, dev, n: int) -> None:
             kc, vc = kc.view(cdt), vc.view(cdt)
             ks = torch.full((k.shape[1], k.shape[2]), 0.02, device=dev)
             fn = lambda: tmo.offline_quant_to_paged_cache(k, v, ks, ks, sl, kc, vc)
-        elif name == "fused_rope":
+        elif name.startswith("fused_rope"):
             case3 = W.cfg3()
             qkv = torch.randn((FR_B, FR_S, FR_HQ + 2 * FR_HK, W_D), device=dev).to(torch.bfloat16)
             kc = torch.zeros((case3.num_blocks, FR_HK, 16, W_D), dtype=torch.int8, device=dev)
@@ -386,8 +393,13 @@ def profile_pass(torch, tmo, W, names, dev, n: int) -> None:
             pid = torch.arange(FR_B, dtype=torch.int32, device=dev) * 512
             gm = torch.ones(W_D, device=dev).to(torch.bfloat16)
             sl = case3.slot_mapping.to(dev)
-            fn = lambda: tmo.fused_rmsnorm_rope_store_paged_cache(qkv, kc, vc, tab, tab, pid, gm, gm,
-                                                                  sl, ks, vs)
+            if name == "fused_rope_ln":
+                fn = lambda: tmo.fused_rope(qkv, kc, vc, tab, tab, pid, gm, gm, k_scale_hp=ks,
+                                            v_scale_hp=vs, slot_mapping_hp=sl,
+                                            norm_type="layernorm")
+            else:
+                fn = lambda: tmo.fused_rmsnorm_rope_store_paged_cache(qkv, kc, vc, tab, tab, pid,
+                                                                      gm, gm, sl, ks, vs)
         elif name.startswith("linear"):
             fn = linear_call(torch, tmo, name, dev, torch.Generator(device=dev).manual_seed(13))
         elif name == "decode_attn":
@@ -490,7 +502,8 @@ def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
                                                          kc, vc, nthreads=nthreads)
         alg, units, desc = offline_bytes(sub), sub.valid_tokens(), \
             f"offline_quant_to_paged_cache on the first {n} tokens of cfg3"
-    elif workload == "fused_rope":
+    elif workload.startswith("fused_rope"):
+        ln = workload == "fused_rope_ln"
         n = 512
         g = torch.Generator().manual_seed(3)
         qkv = torch.randn((1, n, FR_HQ + 2 * FR_HK, W_D), generator=g).to(torch.bfloat16)
@@ -502,8 +515,10 @@ def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
         pid = torch.zeros(1, dtype=torch.int32)
         gm = torch.ones(W_D).to(torch.bfloat16)
         sl = torch.arange(n, dtype=torch.int32)
-        fn = lambda: oracle.fused_rope_paged(qkv, kc, vc, tab, tab, pid, gm, ks, vs, sl, 1e-5, gm,
-                                             nthreads=nthreads)
+        fn = lambda: oracle.fused_rope_paged(qkv, kc, vc, tab, tab, pid, gm, ks, vs, sl, 1e-5,
+                                             None if ln else gm, nthreads=nthreads,
+                                             norm_type="layernorm" if ln else "rmsnorm",
+                                             k_beta=gm if ln else None)
         alg, units, desc = fused_rope_bytes(n), n, f"fused rope of one {n}-token sequence"
     elif workload == "decode_attn":
         layout = W.cfg5()
@@ -616,7 +631,8 @@ def main():
     dev = torch.device("cuda", 0)
     todo = [args.workload] if args.configs == "headline" else \
         ["cfg1", "cfg2", "cfg3", "cfg4", "cfg4_moe", "cfg5", "offline_i8", "offline_f8",
-         "fused_rope", "linear_quant", "linear_dequant", "linear_reshape", "decode_attn"]
+         "fused_rope", "fused_rope_ln", "linear_quant", "linear_dequant", "linear_reshape",
+         "decode_attn"]
     if args.workload not in todo:
         todo.append(args.workload)
     if args.profile_pass:
@@ -635,9 +651,9 @@ def main():
             cdt = torch.int8 if name == "offline_i8" else torch.float8_e4m3fn
             ms, alg, units, sets = bench_offline(torch, tmo, W, W.cfg3(), cdt, dev, args.steps,
                                                  args.warmup)
-        elif name == "fused_rope":
+        elif name.startswith("fused_rope"):
             ms, alg, units, sets = bench_fused_rope(torch, tmo, W, dev, max(20, args.steps // 4),
-                                                    args.warmup // 4)
+                                                    args.warmup // 4, name == "fused_rope_ln")
         elif name.startswith("linear"):
             ms, alg, units, sets = bench_linear(torch, tmo, name, dev, max(20, args.steps // 4),
                                                 max(4, args.warmup // 4))
@@ -684,6 +700,7 @@ def main():
                           "offline_i8": "bf16 in; int8 codes out (static per-channel scales)",
                           "offline_f8": "bf16 in; float8_e4m3fn codes out (static per-channel scales)",
                           "fused_rope": "bf16 qkv in; bf16 Q written back; int8 K/V codes + fp32 scales out",
+                          "fused_rope_ln": "bf16 qkv in; bf16 Q written back; int8 K/V codes + fp32 scales out",
                           "linear_dequant": "int8 codes + fp32 scales in; bf16 out",
                           "linear_reshape": "bf16 in; bf16 out",
                           "decode_attn": "bf16 q, int8 K/V pages + fp32 scales in; bf16 out; fp32 softmax"}
