@@ -58,7 +58,7 @@ WORKLOADS = {
 }
 KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<BF16,16,1,false>",
            "cfg3": "quant_paged_vec<BF16,16,1,false>", "cfg4": "sq_dense<BF16,8,false,true>",
-           "cfg4_moe": "sq_vec<BF16,8,false,1>", "cfg5": "dequant_paged_list<BF16,1,2>",
+           "cfg4_moe": "sq_grp<BF16,8,4,true,true>", "cfg5": "dequant_paged_list<BF16,1,2>",
            "offline_i8": "quant_paged_static_vec<BF16,16,false>",
            "offline_f8": "quant_paged_static_vec<BF16,16,true>",
            "fused_rope": "fused_rope_tok<BF16,16,3,0>", "fused_rope_ln": "fused_rope_tok<BF16,16,3,1>",

@@ -5,12 +5,14 @@
 // _ops.py:4407-4492 (scaled_quantize).  Entry point: tmo_hip_scaled_quantize_per_token
 // (include/tmo_hip.h).
 //
-// One or two wavefronts per output row (sq_vec; sq_dense for rows without gather, groups or a
-// per-channel smooth vector).  Every lane holds up to kMaxV 16-byte vectors of the
-// row in registers (all loads in flight at once), so the row is read from HBM exactly once;
-// the smooth vector (<= 1 MiB even with 64 experts) stays L2-resident and is read as 16-byte
-// vectors alongside.  The row's group (expert) is
-// found with a wavefront prefix scan of token_count and a ballot, with no host round trip.
+// One or two wavefronts per output row.  Every lane holds up to 16 16-byte vectors of the row
+// in registers (all loads in flight at once), so the row is read from HBM exactly once.
+// sq_dense: rows without gather or groups, a grid-stride launch with a per-channel smooth
+// vector staged in LDS.  sq_grp: gathered / grouped rows (MoE) with per-channel smooth rows,
+// one staging of the group's smooth row in LDS per workgroup.  sq_vec: the remaining vector
+// cases (other widths, 3-D rows, scalar or no smooth with gather / groups), the smooth vector
+// read from L2 beside the row.  A row's group (expert) is found with a wavefront prefix scan
+// of token_count and a ballot, with no host round trip.
 #include <algorithm>
 
 #include "tmo_device.h"
@@ -36,6 +38,7 @@ struct SqParams {
   int64_t out_rows;
   int64_t total_rows;  // out_rows * inner
   int64_t dense_rows;  // min(out_rows, n0) * inner: rows produced without gather / groups
+  int64_t grp_main;    // sq_grp: workgroups of the row-major part of the grid
 };
 
 // Group of row r: the g with prefix(g) <= r < prefix(g + 1) over token_count.  Returns
@@ -172,7 +175,7 @@ __global__ __launch_bounds__(256) void sq_vec(SqParams p) {
     for (int k = 0; k < kWPR; ++k) mb = max(mb, red[first + k]);
     if (!valid) return;
   }
-  const RowScale rs = make_row_scale(__uint_as_float(mb));
+  const RowScale rs = make_row_scale(__uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)mb)));
   int8_t* orow_ptr = p.out + orow * p.channels;
 #pragma unroll
   for (int i = 0; i < kMaxV; ++i) {
@@ -191,6 +194,241 @@ __global__ __launch_bounds__(256) void sq_vec(SqParams p) {
     }
   }
   if (lane == 0 && part == 0) p.out_scale[orow] = rs.s;
+}
+
+// Smooth values (u32x4 quarter q of vector i of this lane) from a staged LDS row (lane-major,
+// see sq_grp).
+template <int kSV>
+struct SmoothLds {
+  const u32x4* lds;
+  int lane;
+  __device__ __forceinline__ u32x4 operator()(int i, int q) const {
+    return lds[(i * kSV + q) * kWave + lane];
+  }
+};
+
+// One row of 64 * kV 16-byte vectors (this lane's vectors lane + 64 * i in w) -> smoothed
+// int8 codes (RN(x * smooth) per element, no FMA) and the row scale.
+template <class Tag, int kV, class SmoothAt>
+__device__ __forceinline__ void quant_row(const u32x4 (&w)[kV], SmoothAt sm, int8_t* orow,
+                                             float* scale_out, int lane) {
+  constexpr int kPer = Tag::kPerVec;
+  constexpr int kSV = kPer / 4;
+  float v[kV][kPer];
+  float mx = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kV; ++i) {
+    unpack(Tag{}, w[i], v[i]);
+#pragma unroll
+    for (int q = 0; q < kSV; ++q) {
+      const u32x4 sv = sm(i, q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[i][4 * q + e] = v[i][4 * q + e] * __uint_as_float(sv[e]);
+        mx = abs_max(mx, v[i][4 * q + e]);
+      }
+    }
+  }
+  const RowScale rs = make_row_scale(wave_max_uniform(mx));
+#pragma unroll
+  for (int i = 0; i < kV; ++i) {
+    uint32_t c[kPer / 4];
+    encode_row<kPer>(v[i], rs, c);
+    if constexpr (kPer == 8) {
+      u32x2 c2;
+      c2[0] = c[0];
+      c2[1] = c[1];
+      store_nt(reinterpret_cast<u32x2*>(orow + i * kWave * 8), c2);
+    } else {
+      store_nt(reinterpret_cast<uint32_t*>(orow + i * kWave * 4), c[0]);
+    }
+  }
+  if (lane == 0) *scale_out = rs.s;
+}
+
+#ifndef TMO_SQ_GRP_WAVES
+#define TMO_SQ_GRP_WAVES 4
+#endif
+
+// Groups over token_count, wave-uniform results from one pass (a wavefront prefix scan per 64
+// groups, a ballot per row): ga / gb = the first group whose inclusive prefix exceeds row a /
+// row b (-1 when none: the row is at or past sum(token_count)); for group gq its exclusive and
+// inclusive prefixes; total = sum(token_count).  `first` is this lane's entry of the first 64
+// groups.  The whole wavefront must be active.
+__device__ __forceinline__ void group_scan(const SqParams& p, int32_t first, int64_t a, int64_t b,
+                                           int64_t gq, int64_t& ga, int64_t& gb,
+                                           int64_t& q_excl, int64_t& q_incl, int64_t& total) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int64_t carry = 0;
+  ga = gb = -1;
+  q_excl = q_incl = 0;
+  for (int64_t base = 0; base < p.num_groups; base += kWave) {
+    const int64_t k = base + lane;
+    int64_t c = base == 0 ? (int64_t)first : (k < p.num_groups ? (int64_t)p.token_count[k] : 0);
+    const int64_t own = c;
+    // counts in [0, 2^25) sum to below 2^31 over 64 lanes: a 32-bit DPP scan; otherwise
+    // (negative or huge counts) 64-bit lane shuffles
+    if (!__ballot(c < 0 || c >= (1 << 25))) {
+      c = (int64_t)wave_incl_sum_u32((uint32_t)c);
+    } else {
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int64_t n = __shfl_up(c, o, kWave);
+        if (lane >= o) c += n;
+      }
+    }
+    const int64_t incl = carry + c;
+    const bool in = k < p.num_groups;
+    const uint64_t ha = __ballot(in && incl > a);
+    const uint64_t hb = __ballot(in && incl > b);
+    if (ga < 0 && ha) ga = base + __builtin_ctzll(ha);
+    if (gb < 0 && hb) gb = base + __builtin_ctzll(hb);
+    if (gq >= base && gq < base + kWave) {
+      const int f = (int)(gq - base);
+      q_incl = __shfl(incl, f, kWave);
+      q_excl = q_incl - __shfl(own, f, kWave);
+    }
+    carry += __shfl(c, kWave - 1, kWave);
+  }
+  total = carry;
+}
+
+// The part of sq_grp after the indices: stage smooth row g_stage in LDS, load row `src`, encode
+// it into output row r when `valid`.  Every thread of the workgroup calls it (it holds a
+// barrier).  The staging loads (L2 hits) are issued before the row loads: the memory counter
+// is in order, so the LDS writes then wait for the staging data only, and the barrier does
+// not wait for the slowest row of the workgroup to arrive from HBM.  The row loads are
+// unconditional (a row that is not produced reads row 0, which exists since n0 > 0): under a
+// branch, the wait before the LDS writes would have to assume the loads were issued on one
+// path and not on the other, and would wait for them as well.
+template <class Tag, int kV, int kW, bool kGather>
+__device__ __forceinline__ void sq_grp_row(const SqParams& p, u32x4* lds, int64_t g_stage,
+                                           int64_t r, int64_t src, bool valid) {
+  constexpr int kPer = Tag::kPerVec;
+  constexpr int kSV = kPer / 4;              // u32x4 of smooth values per x vector
+  constexpr int kSlot = kV * kSV * kWave;    // u32x4 of one staged smooth row
+  constexpr int kStage = (kSlot + kWave * kW - 1) / (kWave * kW);  // staged u32x4 per thread
+  const int lane = threadIdx.x & (kWave - 1);
+  const u32x4* sg = reinterpret_cast<const u32x4*>(p.smooth + g_stage * p.smooth_len);
+  u32x4 st[kStage];
+#pragma unroll
+  for (int j = 0; j < kStage; ++j) {
+    const int m = threadIdx.x + j * kWave * kW;
+    const int i = m / (kSV * kWave), rem = m % (kSV * kWave);
+    if (kSlot % (kWave * kW) == 0 || m < kSlot)
+      st[j] = sg[(i * kWave + rem % kWave) * kSV + rem / kWave];
+  }
+  u32x4 w[kV];
+  {
+    const int64_t lsrc = valid ? src : 0;
+    const char* xrow = static_cast<const char*>(p.x) + lsrc * p.row_stride * Tag::kBytes + lane * 16;
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+      const u32x4* xp = reinterpret_cast<const u32x4*>(xrow + i * kWave * 16);
+      // a gathered row may be read again for another output row (top-k): cached loads let the
+      // repeat hit L2 / MALL
+      w[i] = kGather ? *xp : __builtin_nontemporal_load(xp);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kStage; ++j) {
+    const int m = threadIdx.x + j * kWave * kW;
+    if (kSlot % (kWave * kW) == 0 || m < kSlot) lds[m] = st[j];
+  }
+  __syncthreads();
+  if (!valid) return;
+  quant_row<Tag, kV>(w, SmoothLds<kSV>{lds, lane}, p.out + r * p.channels + lane * kPer,
+                     p.out_scale + r, lane);
+}
+
+// Gathered and / or grouped rows (MoE) with a per-channel smooth vector, rows of exactly
+// 64 * kV 16-byte vectors, 2-D input, one output row per wavefront.  The grid has two parts.
+//
+// Row-major workgroups (blockIdx.x < grp_main) own rows [kW * b, kW * b + kW).  A wavefront
+// issues its index loads (its gather index and its lane's token_count entry, together), finds
+// the groups of its row and of the workgroup's first row with one DPP prefix scan, and the
+// workgroup stages the smooth row of the first row's group in LDS and encodes the rows of that
+// group.  Rows of a later group inside the workgroup (a group starting mid-workgroup: with
+// expert-sorted rows, the moe_gen_idx order, at most kW - 1 rows per group) are left to the
+// boundary workgroups, one per group (blockIdx.x = grp_main + g), which encode rows
+// [excl_g, min(incl_g, kW * ceil(excl_g / kW))).  Every produced row is written by exactly one
+// wavefront.
+//
+// From LDS the smooth row costs one staging per workgroup; read from L2 instead, every row
+// fetches its whole smooth row -- twice the row's own bytes, and twice its vector loads.
+// configs[3]-MoE on MI355X: 38.6 us with per-row L2 smooth reads (one wavefront per row,
+// index and group lookups serialised in front of the row loads), 34.0 us here.  Measured and
+// rejected: a fifth, staging-only wavefront per workgroup (37.0 us), 8 rows per workgroup
+// (35.8 us), a two-pass encoder that keeps only the raw row (60 VGPRs, 8 waves per SIMD,
+// 35.0 us).  A minimal kernel that only gathers and copies the same bytes takes 27.4 us.
+template <class Tag, int kV, int kW, bool kGroups, bool kGather>
+__global__ __launch_bounds__(64 * kW) void sq_grp(SqParams p) {
+  constexpr int kSlot = kV * (Tag::kPerVec / 4) * kWave;
+  // staged smooth row, lane-major: vector i, quarter q of lane l at (i * kSV + q) * 64 + l, so
+  // a wavefront's 16-byte reads of one (i, q) are 64 consecutive vectors
+  __shared__ u32x4 lds[kSlot];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int64_t gstart = (kGather && p.gather_start) ? (int64_t)p.gather_start[0] : 0;
+  if (kGroups && blockIdx.x >= p.grp_main) {  // boundary workgroup (workgroup-uniform)
+    const int32_t t = p.token_count[lane < p.num_groups ? lane : 0];
+    const int32_t tc0 = lane < p.num_groups ? t : 0;
+    const int64_t g = (int64_t)blockIdx.x - p.grp_main;
+    int64_t unused, excl, incl, total;
+    group_scan(p, tc0, 0, 0, g, unused, unused, excl, incl, total);
+    const int64_t r = excl + wave;
+    const int64_t aligned = (excl + kW - 1) / kW * kW;
+    bool valid = r < incl && r < aligned && r < p.total_rows;
+    int64_t src = r;
+    if constexpr (kGather) {
+      const int64_t gi = gstart + r;
+      const bool in = gi >= 0 && gi < p.gather_len;
+      src = p.gather_index[in ? gi : 0];
+      valid = valid && in;
+    }
+    valid = valid && src >= 0 && src < p.n0;
+    sq_grp_row<Tag, kV, kW, kGather>(p, lds, g, r, src, valid);
+    return;
+  }
+  // Row-major workgroup.  The index loads come first, all unconditional (clamped in-bounds
+  // addresses, masked afterwards), so they issue back to back and one wait covers them.
+  int32_t tc0 = 0;
+  if constexpr (kGroups) {
+    const int32_t t = p.token_count[lane < p.num_groups ? lane : 0];
+    tc0 = lane < p.num_groups ? t : 0;
+  }
+  const int64_t r = (int64_t)blockIdx.x * kW + wave;
+  bool valid = r < p.total_rows;
+  int64_t src = r;
+  if constexpr (kGather) {
+    const int64_t gi = gstart + r;
+    const bool in = gi >= 0 && gi < p.gather_len;
+    src = p.gather_index[in ? gi : 0];
+    valid = valid && in;
+  }
+  int64_t g_stage = 0;
+  if constexpr (kGroups) {
+    int64_t g_row, excl, incl, total;
+    group_scan(p, tc0, (int64_t)blockIdx.x * kW, r, -1, g_stage, g_row, excl, incl, total);
+    valid = valid && g_row >= 0 && g_row == g_stage && r < total;
+    if (g_stage < 0) g_stage = 0;  // no row of this workgroup is produced
+  }
+  valid = valid && src >= 0 && src < p.n0;
+  sq_grp_row<Tag, kV, kW, kGather>(p, lds, g_stage, r, src, valid);
+}
+
+template <class Tag, int kV>
+int launch_grp(SqParams p, hipStream_t stream) {
+  constexpr int kW = TMO_SQ_GRP_WAVES;
+  if (p.gather_index && p.gather_len == 0) return TMO_OK;  // no row is produced
+  p.grp_main = (p.total_rows + kW - 1) / kW;
+  const int64_t blocks = p.grp_main + (p.token_count ? p.num_groups : 0);
+  if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
+  const dim3 grid((unsigned)blocks), block(64 * kW);
+  if (p.token_count && p.gather_index)
+    return launch_kernel(sq_grp<Tag, kV, kW, true, true>, grid, block, stream, p);
+  if (p.token_count) return launch_kernel(sq_grp<Tag, kV, kW, true, false>, grid, block, stream, p);
+  return launch_kernel(sq_grp<Tag, kV, kW, false, true>, grid, block, stream, p);
 }
 
 // Dense rows (no gather, no groups) of exactly 64 * kV 16-byte vectors: output row r reads
@@ -250,7 +488,7 @@ __global__ __launch_bounds__(256) void sq_dense(SqParams p) {
         m = abs_max(m, v[i][e]);
       }
     }
-    const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<kWave>(__float_as_uint(m))));
+    const RowScale rs = make_row_scale(wave_max_uniform(m));
     int8_t* orow = p.out + row * p.channels + lane * kPer;
 #pragma unroll
     for (int i = 0; i < kV; ++i) {
@@ -306,7 +544,7 @@ __global__ __launch_bounds__(256) void sq_generic(SqParams p) {
     if (sm) xv = xv * sm[p.smooth_len == 1 ? 0 : d];
     m = abs_max(m, xv);
   }
-  const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<kWave>(__float_as_uint(m))));
+  const RowScale rs = make_row_scale(wave_max_uniform(m));
   int8_t* o = p.out + orow * p.channels;
   for (int64_t d = lane; d < p.channels; d += kWave) {
     float xv = load1(Tag{}, p.x, base + d);
@@ -358,6 +596,16 @@ int launch(const SqParams& p, hipStream_t stream) {
       case 4: return launch_dense<Tag, 4>(p, stream);
       case 8: return launch_dense<Tag, 8>(p, stream);
       case 16: return launch_dense<Tag, 16>(p, stream);
+      default: break;
+    }
+  }
+  if ((p.gather_index || p.token_count) && p.inner == 1 && p.smooth && p.channels > 1 &&
+      p.smooth_len == p.channels && nvec % kWave == 0) {
+    switch (nvec / kWave) {
+      case 1: return launch_grp<Tag, 1>(p, stream);
+      case 2: return launch_grp<Tag, 2>(p, stream);
+      case 4: return launch_grp<Tag, 4>(p, stream);
+      case 8: return launch_grp<Tag, 8>(p, stream);
       default: break;
     }
   }

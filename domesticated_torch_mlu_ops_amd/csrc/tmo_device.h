@@ -145,6 +145,35 @@ __device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
   return v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wavefront, in DPP steps (no LDS round trips):
+// sums inside each 16-lane row (row_shr 1, 2, 4, 8, lanes shifted in from outside the row
+// read 0), then row 1 and row 3 add the last lane of the row before them (row_bcast:15), then
+// rows 2 and 3 add lane 31 (row_bcast:31).  The whole wavefront must be active.
+constexpr int kDppRowShr1 = 0x111;
+constexpr int kDppRowShr2 = 0x112;
+constexpr int kDppRowShr4 = 0x114;
+constexpr int kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+__device__ __forceinline__ uint32_t wave_incl_sum_u32(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowShr1, 0xF, 0xF, true);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowShr2, 0xF, 0xF, true);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowShr4, 0xF, 0xF, true);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowShr8, 0xF, 0xF, true);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowBcast15, 0xA, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowBcast31, 0xC, 0xF, false);
+  return v;
+}
+
+// Maximum over the whole wavefront, returned as a wave-uniform value: every lane holds the
+// same result after group_max_u32<64>, and readfirstlane tells the compiler so, which turns
+// branches on values derived from it (the encoder's fast / IEEE path choice) into scalar
+// branches instead of exec-masked code that keeps both paths' registers live.
+__device__ __forceinline__ float wave_max_uniform(float m) {
+  return __uint_as_float(
+      (uint32_t)__builtin_amdgcn_readfirstlane((int)group_max_u32<kWave>(__float_as_uint(m))));
+}
+
 // ---------------------------------------------------------------------------- int8 encoder
 
 // Rows whose scale is below this use a true IEEE divide per element; above it the

@@ -11,6 +11,9 @@
 //        decode-attention kernel assumes -- lane l holds A[l % 16][4 (l / 16) + e],
 //        B[4 (l / 16) + e][l % 16] and C[4 (l / 16) + e][l % 16], e = 0..3 -- on small integer
 //        matrices whose products are exact, against the host's matrix product.
+//   scan: wave_incl_sum_u32 (the DPP prefix sum of the grouped smooth quantiser) equals the
+//        serial inclusive prefix sum over the 64 lanes, on 2^21 wavefronts of hashed counts in
+//        [0, 2^25) (and on all-ones, to catch a lane that reads the wrong row).
 //   sqrt: __builtin_sqrtf (the fused rope's rms) is correctly rounded for every positive
 //        finite fp32 x: with m- and m+ the midpoints between r = sqrtf(x) and its neighbours,
 //        m-^2 < x < m+^2 (25-bit midpoints square exactly in fp64; no x sits on a midpoint).
@@ -53,6 +56,29 @@ __global__ void check_fp8(uint32_t hi, unsigned long long* bad) {
       for (int j = 0; j < 4; ++j)
         if (((hw >> (8 * j)) & 0xffu) != tmo::fp8e4m3_bits(f[j])) ++b;
     }
+  }
+  if (b) atomicAdd(bad, b);
+}
+
+__device__ __forceinline__ uint32_t scan_value(uint32_t wave, uint32_t lane) {
+  if (wave == 0) return 1u;  // all ones: lane l must hold l + 1
+  uint32_t h = wave * 0x9E3779B1u ^ (lane + 0x7F4A7C15u) * 0x85EBCA77u;
+  h ^= h >> 15;
+  h *= 0x2C1B3C6Du;
+  h ^= h >> 12;
+  // mostly small counts, sometimes zero, sometimes near the 2^25 bound
+  const uint32_t k = h & 3u;
+  return k == 0 ? 0u : (k == 1 ? (h >> 8) & 0x1FFu : (k == 2 ? (h >> 7) & 0x1FFFFFFu : 1u));
+}
+
+__global__ __launch_bounds__(256) void check_scan(uint32_t waves, unsigned long long* bad) {
+  const uint32_t lane = threadIdx.x & 63u;
+  unsigned long long b = 0;
+  for (uint32_t w = blockIdx.x * 4 + threadIdx.x / 64; w < waves; w += gridDim.x * 4) {
+    const uint32_t got = tmo::wave_incl_sum_u32(scan_value(w, lane));
+    uint32_t want = 0;
+    for (uint32_t j = 0; j <= lane; ++j) want += scan_value(w, j);
+    if (got != want) ++b;
   }
   if (b) atomicAdd(bad, b);
 }
@@ -174,6 +200,10 @@ int main(int argc, char** argv) {
     }
     std::printf("mode=%s mismatches=%llu checked=%llu\n", mode, b, checked);
     return b == 0 ? 0 : 1;
+  } else if (!std::strcmp(mode, "scan")) {
+    const uint32_t waves = 1u << 21;
+    checked = 64ull * waves;
+    check_scan<<<dim3(4096), dim3(256)>>>(waves, d_bad);
   } else if (!std::strcmp(mode, "sqrt")) {
     checked = 0x7f800000ull - 1;
     check_sqrt<<<dim3(8192), dim3(256)>>>(d_bad);

@@ -3,8 +3,8 @@ the GPU against their definitions (tests/native/gfx950_builtins.hip, built in-tr
 __graft_entry__.build()): the v_rcp_f32 + Newton reciprocal is IEEE 1/s for every scale on the
 reciprocal path, the v_cvt_pk_fp8_f32 conversion is the round-to-nearest-even e4m3fn
 encoding for every fp32 value in [-448, 448], and the fused rope's square root is correctly
-rounded for every positive finite fp32 value; and the MFMA lane layouts the decode-attention
-kernel assumes."""
+rounded for every positive finite fp32 value; the MFMA lane layouts the decode-attention
+kernel assumes; and the DPP wavefront prefix sum of the grouped smooth quantiser."""
 import subprocess
 from pathlib import Path
 
@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 BINARY = Path(__file__).resolve().parent / "native" / "_build" / "gfx950_builtins"
 
 
-@pytest.mark.parametrize("mode", ["rcp", "fp8", "sqrt", "mfma"])
+@pytest.mark.parametrize("mode", ["rcp", "fp8", "sqrt", "mfma", "scan"])
 def test_gfx950_builtin_exhaustive(dev, mode):
     assert BINARY.exists(), f"{BINARY} not built (run __graft_entry__.build())"
     print(f"[gfx950_builtins] {mode}", flush=True)

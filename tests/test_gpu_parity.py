@@ -801,6 +801,48 @@ def test_smooth_quant_variants(tmo, ref, dev):
                                               None, gi))
 
 
+@pytest.mark.parametrize("dtype,C", [(torch.bfloat16, 512), (torch.bfloat16, 4096),
+                                     (torch.float16, 2048), (torch.float32, 1024),
+                                     (torch.float32, 2048), (torch.bfloat16, 8192)])
+def test_smooth_quant_grouped_rows(tmo, ref, dev, dtype, C):
+    """Gathered / grouped rows with per-group smooth rows (the per-workgroup LDS staging path):
+    groups of 0-3 rows so that groups start and end inside workgroups of 4 rows, long groups,
+    more than 64 groups, token_count summing past and short of the row count,
+    gather_index_start_position, out-of-range gather entries, groups without gather, and
+    gather without groups (one per-channel smooth vector)."""
+    g = torch.Generator().manual_seed(C + 11)
+    n0 = 97
+    x = (torch.randn(n0, C, generator=g) * torch.logspace(-2, 2, n0)[:, None]).to(dtype)
+    x[5] = 0
+    counts = [0, 1, 2, 3, 0, 0, 5, 1, 1, 17, 2, 0, 3, 40, 1, 2] * 9  # 144 groups, 702 rows
+    tc = torch.tensor(counts, dtype=torch.int32)
+    E = tc.numel()
+    rows = int(tc.sum())
+    gi = torch.randint(0, n0, (rows,), generator=g).to(torch.int32)
+    gi[7] = n0          # out of range: row not produced
+    gi[300] = -1
+    sm = 0.5 + torch.rand(E, C, generator=g)
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase(f"groups {dtype} C={C}", x, sm, tc, gi))
+    # token_count summing short of the gathered rows (trailing rows untouched) and past them
+    tc_short = tc.clone()
+    tc_short[100:] = 0
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase("short", x, sm, tc_short, gi))
+    tc_long = tc.clone()
+    tc_long[-1] += 50
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase("long", x, sm, tc_long, gi))
+    # gather_index_start_position: rows gather_index[start : start + sum(token_count)]
+    tc_start = tc.clone()
+    tc_start[120:] = 0
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase("start", x, sm, tc_start, gi),
+             gather_start=torch.tensor([29], dtype=torch.int32))
+    # groups without gather (rows of x in order), and gather without groups
+    tc_rows = torch.tensor([0, 3, 1, 0, 2, 40, 7, 1, 1, 30], dtype=torch.int32)  # 85 of 97 rows
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase("groups, no gather", x,
+                                              0.5 + torch.rand(10, C, generator=g), tc_rows))
+    _sq_both(tmo, ref, dev, W.SmoothQuantCase("gather, no groups", x,
+                                              0.5 + torch.rand(C, generator=g), None, gi))
+
+
 def test_public_wrappers(tmo, ref, dev):
     """scaled_quantize and the per_token_smooth_quantize alias return what moe_quantize does."""
     case = W.cfg4()
