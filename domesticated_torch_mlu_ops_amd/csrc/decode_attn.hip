@@ -694,9 +694,13 @@ extern "C" int tmo_hip_single_query_cached_kv_attn(
   if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out)
     return TMO_ERR_INVALID_ARGUMENT;
   if (cache_dtype == TMO_DTYPE_I8 && (!k_scale || !v_scale)) return TMO_ERR_INVALID_ARGUMENT;
+  // max_context_len <= 0: "an uncertain maximum value of context_lens" (reference _ops.py,
+  // single_query_cached_kv_attn's max_context_len); it only sizes the splits, so a negative
+  // value is taken as 0 (the last split always runs to the sequence's own length)
+  if (max_context_len < 0) max_context_len = 0;
   if (batch < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
       head_size <= 0 || head_size > 512 || num_blocks < 0 || block_size <= 0 || max_blocks < 0 ||
-      max_context_len < 0 || splits < 1 || q_stride_seq < 0 || q_stride_head < 0 ||
+      splits < 1 || q_stride_seq < 0 || q_stride_head < 0 ||
       out_stride_seq < 0 || out_stride_head < 0)
     return TMO_ERR_INVALID_ARGUMENT;
   if (batch > 65535 || num_kv_heads > 65535 || splits > 65535 || num_q_heads > 0x7fffffffLL)

@@ -608,7 +608,10 @@ extern "C" int tmo_hip_dequant_from_paged_cache(
   const bool has_v = value != nullptr;
   if (has_v != (value_cache != nullptr) || has_v != (value_scale != nullptr))
     return TMO_ERR_INVALID_ARGUMENT;
-  if (batch < 0 || max_blocks_per_seq < 0 || max_context_len < 0 || num_blocks < 0 ||
+  // max_context_len is not used: the reference's math (_ops.py:3749-3774) dequantises every
+  // context_lengths[i] token its block table holds, whatever the maximum says
+  (void)max_context_len;
+  if (batch < 0 || max_blocks_per_seq < 0 || num_blocks < 0 ||
       num_heads <= 0 || block_size <= 0 || head_size <= 0 || total_rows < 0)
     return TMO_ERR_INVALID_ARGUMENT;
   if (key_stride_token < 0 || key_stride_head < 0 ||
@@ -616,8 +619,7 @@ extern "C" int tmo_hip_dequant_from_paged_cache(
     return TMO_ERR_INVALID_ARGUMENT;
   if (num_heads > 0x7fffffffLL || block_size > 0x7fffffffLL || head_size > 0x7fffffffLL)
     return TMO_ERR_INVALID_ARGUMENT;
-  int64_t grid_blocks = (max_context_len + block_size - 1) / block_size;
-  if (grid_blocks > max_blocks_per_seq) grid_blocks = max_blocks_per_seq;
+  const int64_t grid_blocks = max_blocks_per_seq;
   if (batch == 0 || grid_blocks == 0 || num_blocks == 0 || total_rows == 0) return TMO_OK;
 
   DequantParams p{};
@@ -654,8 +656,7 @@ extern "C" int tmo_hip_dequant_from_paged_cache(
 
 extern "C" int64_t tmo_hip_dequant_workspace_bytes(int64_t batch, int64_t max_blocks_per_seq,
                                                    int64_t max_context_len, int64_t block_size) {
-  if (batch <= 0 || max_blocks_per_seq <= 0 || max_context_len <= 0 || block_size <= 0) return 0;
-  const int64_t grid_blocks =
-      std::min((max_context_len + block_size - 1) / block_size, max_blocks_per_seq);
-  return tmo::list_workspace_bytes(batch, grid_blocks);
+  (void)max_context_len;  // the dequant covers every page of the block table (see above)
+  if (batch <= 0 || max_blocks_per_seq <= 0 || block_size <= 0) return 0;
+  return tmo::list_workspace_bytes(batch, max_blocks_per_seq);
 }

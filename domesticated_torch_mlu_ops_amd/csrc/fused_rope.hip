@@ -662,7 +662,9 @@ int fused_rope_run(
   if (dtype != TMO_DTYPE_F16 && dtype != TMO_DTYPE_BF16) return TMO_ERR_UNSUPPORTED_DTYPE;
   if (scale_mode < 0 || scale_mode > 2 || norm_type < 0 || norm_type > 1)
     return TMO_ERR_UNSUPPORTED_MODE;
-  if (norm_type == 1 && q_gamma) return TMO_ERR_INVALID_ARGUMENT;  // rmsnorm-only argument
+  // q_gamma is an rmsnorm-only argument: layernorm ignores it, as the reference does
+  // (_ops.py:3469-3601 normalises Q only in the rmsnorm branch)
+  if (norm_type == 1) q_gamma = nullptr;
   if (norm_type == 0 && k_beta) return TMO_ERR_INVALID_ARGUMENT;   // layernorm-only argument
   if (!qkv || !sin_table || !cos_table || !position_ids || !k_gamma || !k_cache || !v_cache ||
       (!linear && !slot_mapping))

@@ -445,8 +445,8 @@ void dequant_from_paged_cache(at::Tensor& key, const c10::optional<at::Tensor>& 
                 "value_cache must match key_cache");
     check_scale(*value_cache_quant_scale, "value_cache_quant_scale");
   }
+  // max_context_len is not used by the dequant (the reference math reads context_lengths)
   const int64_t max_ctx = max_context_len.expect_int();
-  TORCH_CHECK(max_ctx >= 0, "max_context_len must be >= 0");
   if (B == 0 || key.size(0) == 0) return;
   c10::DeviceGuard guard(key.device());
   const int64_t ws_bytes =
@@ -1098,7 +1098,8 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
     }
     lse = l.data_ptr<float>();
   }
-  const int64_t max_ctx = max_context_len.expect_int();
+  // max_context_len <= 0: an uncertain maximum (reference docstring); negative counts as 0
+  const int64_t max_ctx = std::max<int64_t>(0, max_context_len.expect_int());
   const int64_t window = windows_size_left.expect_int();
   if (B == 0) return;
   // Splits: about twelve workgroups per CU (3072) when the batch alone does not give them, at

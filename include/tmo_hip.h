@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 9
+#define TMO_HIP_ABI_VERSION 10
 
 /* element types */
 enum tmo_dtype {
@@ -126,7 +126,7 @@ int tmo_hip_offline_quant_to_paged_cache(const void* k, const void* v,
  * (rmsnorm): RMS-normalise Q (when q_gamma is set) and K per head with eps and gamma
  * [head_size], then rotate; norm_type 1 (layernorm): rotate, then layer-normalise K with
  * k_gamma and an optional k_beta (two-pass mean / variance over the same chunk order, see
- * below; q_gamma must be NULL).  The rotation is the fold rotary
+ * below; q_gamma is ignored).  The rotation is the fold rotary
  * embedding over [rope_offset, rope_offset + rope_dim) with rows of sin_table / cos_table
  * [table_rows, table_stride] (a position outside the table leaves the row unrotated), write Q
  * back into qkv, and store K and V rows at slot_mapping into [num_blocks, kv_heads, block_size,
@@ -188,9 +188,10 @@ int tmo_hip_fused_rope_linear(void* qkv, int64_t num_tokens, int64_t seq_len,
  * begin_i = context_seq_offset[i], or the exclusive prefix sum of context_lengths when
  * context_seq_offset is NULL.  quant_mode 0: scale [H, D] (per channel);
  * quant_mode 1: scale [num_blocks, H, block_size] (per token).  quant_bit must be 8.
- * Tokens at or past min(max_context_len, max_blocks_per_seq * block_size) are not written;
- * block-table entries outside [0, num_blocks) and output rows outside [0, total_rows) are
- * skipped.
+ * Tokens at or past max_blocks_per_seq * block_size are not written; block-table entries
+ * outside [0, num_blocks) and output rows outside [0, total_rows) are skipped.
+ * max_context_len is accepted for the reference signature and not used: the reference math
+ * (_ops.py:3749-3774) reads context_lengths only.
  * Replaces tmo::torch_api::dequant_from_paged_cache (reference include/torch_mlu_ops.h:650-661),
  * called by torch_mlu_ops.dequant_from_paged_cache (reference _ops.py:3734-3824).
  * out_dtype: F16, BF16 (or F32).  value, value_cache, value_scale: all NULL or all set.
@@ -217,9 +218,9 @@ int tmo_hip_dequant_from_paged_cache(void* key, void* value,
                                      void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes for tmo_hip_dequant_from_paged_cache's page-list path: 16 + 16 per page the
- * call can cover (batch * min(ceil(max_context_len / block_size), max_blocks_per_seq), rounded
- * up to a multiple of 8); 0 when there is nothing to do.  No reference counterpart (the MLU
- * kernels take none). */
+ * call can cover (batch * max_blocks_per_seq, rounded up to a multiple of 8); 0 when there is
+ * nothing to do.  max_context_len is not used.  No reference counterpart (the MLU kernels take
+ * none). */
 int64_t tmo_hip_dequant_workspace_bytes(int64_t batch, int64_t max_blocks_per_seq,
                                         int64_t max_context_len, int64_t block_size);
 
@@ -392,6 +393,8 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
  * probabilities are split into two operands when one is not exact), softmax in fp32.
  * splits > 1 divides each sequence's keys over that many workgroups per KV head; it needs
  * `workspace` of at least tmo_hip_attn_workspace_bytes(...) bytes (device memory).
+ * max_context_len <= 0 (negative included) means an unknown maximum: one split per sequence
+ * unless `splits` says otherwise; it never limits the keys read.
  * Replaces tmo::torch_api::single_query_cached_kv_attn (reference
  * include/torch_mlu_ops.h:107-130) for one query token per sequence, without q/out
  * quantisation, mask or sink, called by torch_mlu_ops.single_query_cached_kv_attn (reference

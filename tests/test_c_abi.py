@@ -149,13 +149,16 @@ def test_dequant_validation(lib):
 
 
 def test_dequant_workspace_bytes(lib):
-    # 16-byte header + 16 bytes per page the call covers, batch * min(ceil(ctx / BS),
-    # max_blocks) rounded up to a multiple of 8
+    # 16-byte header + 16 bytes per page the call can cover, batch * max_blocks rounded up to
+    # a multiple of 8; max_context_len does not limit the pages (the reference math reads
+    # context_lengths only)
     assert lib.tmo_hip_dequant_workspace_bytes(64, 2048, 32768, 16) == 16 + 16 * 64 * 2048
     assert lib.tmo_hip_dequant_workspace_bytes(3, 4, 1000, 16) == 16 + 16 * 16
-    assert lib.tmo_hip_dequant_workspace_bytes(3, 100, 17, 16) == 16 + 16 * 8
+    assert lib.tmo_hip_dequant_workspace_bytes(3, 100, 17, 16) == 16 + 16 * 304
     assert lib.tmo_hip_dequant_workspace_bytes(0, 4, 64, 16) == 0
-    assert lib.tmo_hip_dequant_workspace_bytes(2, 4, 0, 16) == 0
+    assert lib.tmo_hip_dequant_workspace_bytes(2, 4, 0, 16) == 16 + 16 * 8
+    assert lib.tmo_hip_dequant_workspace_bytes(2, 4, -1, 16) == 16 + 16 * 8
+    assert lib.tmo_hip_dequant_workspace_bytes(2, 0, 64, 16) == 0
 
 
 def test_scaled_quantize_validation(lib):
@@ -199,7 +202,8 @@ def test_fused_rope_validation(lib):
     assert call(dtype=0) == EDTYPE           # fp32 qkv
     assert call(mode=3) == EMODE
     assert call(norm=2) == EMODE             # neither rmsnorm nor layernorm
-    assert call(norm=1, qg=FAKE) == EINVAL   # q_gamma belongs to rmsnorm
+    assert call(norm=1, qg=FAKE, T=0) == 0   # q_gamma is ignored by layernorm (as the torch op)
+    assert call(norm=1, qg=FAKE, mode=1) == EINVAL  # ... the missing scales still fail
     assert call(norm=0, beta=FAKE) == EINVAL  # k_beta belongs to layernorm
     assert call(mode=1) == EINVAL            # quantised without scales
     assert call(qkv=None) == EINVAL
@@ -218,7 +222,7 @@ def test_fused_rope_linear_validation(lib):
                                              ks, mode, bs_id, off, MB, L, 2, None)
     assert call(mode=3) == EMODE
     assert call(mode=2) == EINVAL            # quantised without scales
-    assert call(norm=1, qg=FAKE) == EINVAL
+    assert call(norm=1, qg=FAKE, T=0) == 0   # q_gamma is ignored by layernorm
     assert call(L=0) == EINVAL               # cache_len must be positive
     assert call(MB=-1) == EINVAL
     assert call(MB=1 << 20, L=1 << 12) == EINVAL  # slots past int32
@@ -289,10 +293,11 @@ def test_linear_read_validation(lib):
 
 def test_attention_validation(lib):
     def call(q=FAKE, kc=FAKE, vc=FAKE, ks=FAKE, vs=FAKE, smode=1, bt=FAKE, lens=FAKE, out=FAKE,
-             B=2, Hq=8, Hkv=2, D=128, NB=16, BS=16, qdt=2, cdt=3, splits=1, ws=None, wsb=0):
+             B=2, Hq=8, Hkv=2, D=128, NB=16, BS=16, qdt=2, cdt=3, splits=1, ws=None, wsb=0,
+             mctx=64):
         return lib.tmo_hip_single_query_cached_kv_attn(
             q, 1024, 128, kc, vc, ks, vs, smode, bt, 4, lens, None, out, 1024, 128, None, 0, 0,
-            B, Hq, Hkv, D, NB, BS, 64, -1, 0.1, qdt, cdt, splits, ws, wsb, None)
+            B, Hq, Hkv, D, NB, BS, mctx, -1, 0.1, qdt, cdt, splits, ws, wsb, None)
     assert call(qdt=3) == EDTYPE                   # int8 q
     assert call(cdt=1) == EDTYPE                   # fp16 cache with bf16 q
     assert call(smode=0) == EMODE                  # int8 cache without a scale mode
@@ -308,4 +313,5 @@ def test_attention_validation(lib):
     assert lib.tmo_hip_attn_workspace_bytes(2, 2, 8, 128, 64, 1) == 0
     assert call(splits=4, ws=FAKE, wsb=need - 4) == EINVAL
     assert call(B=0) == 0
+    assert call(B=0, mctx=-1) == 0                 # negative max_context_len: unknown, like 0
 

@@ -125,6 +125,7 @@ def test_attn_windows_alibi_missing_pages_and_layouts(tmo, ref, dev):
     run_attn(tmo, ref, dev, case, four_d=False)
     run_attn(tmo, ref, dev, case, with_lse=False)
     run_attn(tmo, ref, dev, case, max_ctx=0)       # "uncertain maximum": one split
+    run_attn(tmo, ref, dev, case, max_ctx=-1)      # negative counts as unknown, like 0
 
 
 @pytest.mark.parametrize("kv", ["int8_token", "int8_channel", "plain"])

@@ -515,7 +515,7 @@ def test_reshape_paged_cache_cfg3(tmo, ref, dev):
 # ---------------------------------------------------------------------------- dequant_from_paged_cache
 
 def _dequant_both(tmo, ref, dev, layout, caches, out_dtype, mode, seq_offset=None, total=None,
-                  with_v=True):
+                  with_v=True, max_ctx=None):
     kc, vc, ks, vs = caches
     H, D = kc.shape[1], kc.shape[3]
     total = layout.total_tokens if total is None else total
@@ -529,7 +529,7 @@ def _dequant_both(tmo, ref, dev, layout, caches, out_dtype, mode, seq_offset=Non
     got_v = got_k.clone() if with_v else None
     tmo.dequant_from_paged_cache(
         got_k, got_v, kc, vc if with_v else None, ks, vs if with_v else None,
-        layout.context_lengths.to(dev), layout.max_context_len,
+        layout.context_lengths.to(dev), layout.max_context_len if max_ctx is None else max_ctx,
         seq_offset.to(dev) if seq_offset is not None else None, layout.block_tables.to(dev), mode, 8)
     assert_bits_equal(got_k, want_k, f"{layout.name} key")
     if with_v:
@@ -574,6 +574,18 @@ def test_dequant_modes_dtypes_layouts(tmo, ref, dev, out_dtype, mode, D, BS, H):
     caches = tuple(t.to(dev) for t in (kc, vc, ks, vs))
     _dequant_both(tmo, ref, dev, layout, caches, out_dtype, mode)
     _dequant_both(tmo, ref, dev, layout, caches, out_dtype, mode, with_v=False)
+
+
+@pytest.mark.parametrize("D,BS,H", [(128, 16, 4), (128, 16, 3), (80, 16, 4)])
+def test_dequant_ignores_max_context_len(tmo, ref, dev, D, BS, H):
+    """max_context_len understated, 0 and negative: every context_lengths[i] token is still
+    dequantised (the reference math reads context_lengths only), on the page-list, per-page
+    and scalar kernels."""
+    layout, (kc, vc, ks, vs) = _small_layout(seed=7 * D + H, D=D, BS=BS, NB=64, H=H)
+    caches = tuple(t.to(dev) for t in (kc, vc, ks, vs))
+    for mctx in (layout.max_context_len // 3, 1, 0, -1):
+        print(f"[dequant] max_context_len={mctx} (true max {layout.max_context_len})", flush=True)
+        _dequant_both(tmo, ref, dev, layout, caches, torch.bfloat16, 1, max_ctx=mctx)
 
 
 def test_dequant_many_sequences(tmo, ref, dev):
