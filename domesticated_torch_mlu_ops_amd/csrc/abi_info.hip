@@ -10,6 +10,9 @@ extern "C" const char* tmo_hip_status_string(int status) {
     case TMO_ERR_UNSUPPORTED_DTYPE: return "unsupported dtype";
     case TMO_ERR_UNSUPPORTED_MODE: return "unsupported quant_mode / quant_bit";
     case TMO_ERR_LAUNCH: return "HIP kernel launch failed";
+    case TMO_ERR_SCRATCH_TOO_SMALL:
+      return "the call needs more than the library's static scratch "
+             "(TMO_HIP_DEQUANT_SCRATCH_BYTES); pass a workspace to the allocating entry point";
     default: return "unknown status";
   }
 }

@@ -12,6 +12,8 @@
 // kernel covers layouts it does not take (non power-of-two heads, very large batches), and a
 // scalar kernel covers head sizes that are not a multiple of 16.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "tmo_device.h"
 
@@ -585,6 +587,16 @@ int launch(DequantParams p, void* workspace, int64_t workspace_bytes, hipStream_
   return launch_kernel(dequant_paged_vec<Tag, 4>, grid, block, stream, p);
 }
 
+int dequant_paged(void* key, void* value, int64_t key_stride_token, int64_t key_stride_head,
+                  int64_t value_stride_token, int64_t value_stride_head, int64_t total_rows,
+                  const int8_t* key_cache, const int8_t* value_cache, const float* key_scale,
+                  const float* value_scale, const int32_t* context_lengths,
+                  const int32_t* context_seq_offset, const int32_t* block_tables, int64_t batch,
+                  int64_t max_blocks_per_seq, int64_t max_context_len, int64_t num_blocks,
+                  int64_t num_heads, int64_t block_size, int64_t head_size, int quant_mode,
+                  int quant_bit, int out_dtype, void* workspace, int64_t workspace_bytes,
+                  void* stream);
+
 }  // namespace
 }  // namespace tmo
 
@@ -597,7 +609,95 @@ extern "C" int tmo_hip_dequant_from_paged_cache(
     int64_t max_context_len, int64_t num_blocks, int64_t num_heads, int64_t block_size,
     int64_t head_size, int quant_mode, int quant_bit, int out_dtype, void* workspace,
     int64_t workspace_bytes, void* stream) {
+  return tmo::dequant_paged(key, value, key_stride_token, key_stride_head, value_stride_token,
+                            value_stride_head, total_rows, key_cache, value_cache, key_scale,
+                            value_scale, context_lengths, context_seq_offset, block_tables, batch,
+                            max_blocks_per_seq, max_context_len, num_blocks, num_heads,
+                            block_size, head_size, quant_mode, quant_bit, out_dtype, workspace,
+                            workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------- allocation-free entry
+//
+// The page list of tmo_hip_dequant_from_paged_cache_noalloc lives in `scratch`, a file-scope
+// device array: each GPU the library runs on holds one (TMO_HIP_DEQUANT_SCRATCH_BYTES) until the
+// process ends, and every call on that GPU shares it.  In host code `scratch` names a host-side
+// stand-in, not device memory: its device address is taken once per device with
+// hipGetSymbolAddress (that device current) and kept in scratch_addr[]; host code passes only
+// that address to kernels.  Nothing in it has to start at zero: the pre-pass writes the page
+// count and every entry the main kernel uses before that kernel runs (stream order).  Calls
+// that overlap on one GPU (different streams, or other host threads) race on it.
+static __device__ __align__(256) unsigned char scratch[TMO_HIP_DEQUANT_SCRATCH_BYTES];
+
+namespace tmo {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> scratch_addr[kMaxScratchDevices];
+std::mutex scratch_mu;
+
+// Device address of the current device's `scratch`, looked up on the first call per device.
+int scratch_of_current_device(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return TMO_ERR_LAUNCH;
+  if (dev < 0 || dev >= kMaxScratchDevices) return TMO_ERR_INVALID_ARGUMENT;
+  void* p = scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    p = scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return TMO_ERR_LAUNCH;
+      scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return TMO_OK;
+}
+
+}  // namespace
+}  // namespace tmo
+
+extern "C" int tmo_hip_dequant_from_paged_cache_noalloc(
+    void* key, void* value, int64_t key_stride_token, int64_t key_stride_head,
+    int64_t value_stride_token, int64_t value_stride_head, int64_t total_rows,
+    const int8_t* key_cache, const int8_t* value_cache, const float* key_scale,
+    const float* value_scale, const int32_t* context_lengths, const int32_t* context_seq_offset,
+    const int32_t* block_tables, int64_t batch, int64_t max_blocks_per_seq,
+    int64_t max_context_len, int64_t num_blocks, int64_t num_heads, int64_t block_size,
+    int64_t head_size, int quant_mode, int quant_bit, int out_dtype, void* stream) {
   using namespace tmo;
+  if (batch < 0 || max_blocks_per_seq < 0) return TMO_ERR_INVALID_ARGUMENT;
+  if (batch > 0 && max_blocks_per_seq > (TMO_HIP_DEQUANT_SCRATCH_BYTES - kListHeader) /
+                                             (int64_t)sizeof(PageEntry) / batch)
+    return TMO_ERR_SCRATCH_TOO_SMALL;
+  const int64_t need = tmo_hip_dequant_workspace_bytes(batch, max_blocks_per_seq,
+                                                       max_context_len, block_size);
+  if (need > TMO_HIP_DEQUANT_SCRATCH_BYTES) return TMO_ERR_SCRATCH_TOO_SMALL;
+  void* ws = nullptr;
+  if (need > 0) {
+    const int st = scratch_of_current_device(&ws);
+    if (st != TMO_OK) return st;
+  }
+  return dequant_paged(key, value, key_stride_token, key_stride_head, value_stride_token,
+                       value_stride_head, total_rows, key_cache, value_cache, key_scale,
+                       value_scale, context_lengths, context_seq_offset, block_tables, batch,
+                       max_blocks_per_seq, max_context_len, num_blocks, num_heads, block_size,
+                       head_size, quant_mode, quant_bit, out_dtype, ws,
+                       need > 0 ? (int64_t)TMO_HIP_DEQUANT_SCRATCH_BYTES : 0, stream);
+}
+
+namespace tmo {
+namespace {
+
+int dequant_paged(void* key, void* value, int64_t key_stride_token, int64_t key_stride_head,
+                  int64_t value_stride_token, int64_t value_stride_head, int64_t total_rows,
+                  const int8_t* key_cache, const int8_t* value_cache, const float* key_scale,
+                  const float* value_scale, const int32_t* context_lengths,
+                  const int32_t* context_seq_offset, const int32_t* block_tables, int64_t batch,
+                  int64_t max_blocks_per_seq, int64_t max_context_len, int64_t num_blocks,
+                  int64_t num_heads, int64_t block_size, int64_t head_size, int quant_mode,
+                  int quant_bit, int out_dtype, void* workspace, int64_t workspace_bytes,
+                  void* stream) {
   if (workspace_bytes < 0 || (workspace_bytes > 0 && workspace == nullptr))
     return TMO_ERR_INVALID_ARGUMENT;
   if (out_dtype != TMO_DTYPE_F16 && out_dtype != TMO_DTYPE_BF16 && out_dtype != TMO_DTYPE_F32)
@@ -653,6 +753,9 @@ extern "C" int tmo_hip_dequant_from_paged_cache(
     default: return launch<F32>(p, workspace, workspace_bytes, s);
   }
 }
+
+}  // namespace
+}  // namespace tmo
 
 extern "C" int64_t tmo_hip_dequant_workspace_bytes(int64_t batch, int64_t max_blocks_per_seq,
                                                    int64_t max_context_len, int64_t block_size) {

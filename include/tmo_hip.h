@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 10
+#define TMO_HIP_ABI_VERSION 11
 
 /* element types */
 enum tmo_dtype {
@@ -47,7 +47,8 @@ enum tmo_status {
     TMO_ERR_INVALID_ARGUMENT = -1, /* null pointer, negative/zero size, bad stride */
     TMO_ERR_UNSUPPORTED_DTYPE = -2,
     TMO_ERR_UNSUPPORTED_MODE = -3, /* quant_mode / quant_bit outside the int8 path */
-    TMO_ERR_LAUNCH = -4            /* the HIP launch itself failed */
+    TMO_ERR_LAUNCH = -4,           /* the HIP launch itself failed */
+    TMO_ERR_SCRATCH_TOO_SMALL = -5 /* the call needs more than the library's static scratch */
 };
 
 /* ABI version of the loaded library (TMO_HIP_ABI_VERSION at build time). */
@@ -223,6 +224,37 @@ int tmo_hip_dequant_from_paged_cache(void* key, void* value,
  * none). */
 int64_t tmo_hip_dequant_workspace_bytes(int64_t batch, int64_t max_blocks_per_seq,
                                         int64_t max_context_len, int64_t block_size);
+
+/* Bytes of the static device scratch of tmo_hip_dequant_from_paged_cache_noalloc (per GPU). */
+#define TMO_HIP_DEQUANT_SCRATCH_BYTES 4194304
+
+/*
+ * dequant_from_paged_cache_noalloc -- tmo_hip_dequant_from_paged_cache (same arguments and
+ * results, the page-list path's workspace left out) for callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * No counterpart in the reference.  It allocates nothing: the page list lives in a static
+ * device array of TMO_HIP_DEQUANT_SCRATCH_BYTES (4 MiB) that each GPU the library runs on holds
+ * until the process ends, so batch * max_blocks_per_seq may be at most 262136 pages; a larger
+ * call returns TMO_ERR_SCRATCH_TOO_SMALL before enqueueing anything (use the entry point above
+ * with a workspace).  `stream` must belong to the current device.  Every call on one GPU
+ * shares that array: calls that overlap on a GPU (other streams, other host threads) race, so
+ * order them on one stream.
+ */
+int tmo_hip_dequant_from_paged_cache_noalloc(void* key, void* value,
+                                             int64_t key_stride_token, int64_t key_stride_head,
+                                             int64_t value_stride_token, int64_t value_stride_head,
+                                             int64_t total_rows,
+                                             const int8_t* key_cache, const int8_t* value_cache,
+                                             const float* key_scale, const float* value_scale,
+                                             const int32_t* context_lengths,
+                                             const int32_t* context_seq_offset,
+                                             const int32_t* block_tables,
+                                             int64_t batch, int64_t max_blocks_per_seq,
+                                             int64_t max_context_len,
+                                             int64_t num_blocks, int64_t num_heads,
+                                             int64_t block_size, int64_t head_size,
+                                             int quant_mode, int quant_bit, int out_dtype,
+                                             void* stream);
 
 /*
  * scaled_quantize_per_token -- "dynamic_per_token" int8 quantisation with an optional smooth

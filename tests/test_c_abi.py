@@ -68,6 +68,7 @@ def test_every_declared_symbol_is_exported(lib):
     assert set(names) == {"tmo_hip_abi_version", "tmo_hip_status_string",
                           "tmo_hip_reshape_paged_cache", "tmo_hip_quant_to_paged_cache",
                           "tmo_hip_dequant_from_paged_cache", "tmo_hip_dequant_workspace_bytes",
+                          "tmo_hip_dequant_from_paged_cache_noalloc",
                           "tmo_hip_scaled_quantize_per_token",
                           "tmo_hip_offline_quant_to_paged_cache", "tmo_hip_fused_rope_paged",
                           "tmo_hip_fused_rope_linear", "tmo_hip_reshape_linear_cache", "tmo_hip_quant_to_linear_cache",
@@ -146,6 +147,28 @@ def test_dequant_validation(lib):
     assert call(B=-1) == EINVAL
     assert call(B=0) == 0
     assert call(total=0) == 0
+
+
+def test_dequant_noalloc_validation(lib):
+    """The allocation-free dequant refuses, before touching the GPU, a call whose page list
+    would not fit the library's static scratch (TMO_HIP_DEQUANT_SCRATCH_BYTES)."""
+    fn = lib.tmo_hip_dequant_from_paged_cache_noalloc
+    fn.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 5 + [ctypes.c_void_p] * 7 + \
+        [ctypes.c_int64] * 7 + [ctypes.c_int] * 3 + [ctypes.c_void_p]
+    m = re.search(r"#define\s+TMO_HIP_DEQUANT_SCRATCH_BYTES\s+(\d+)", HEADER.read_text())
+    pages = (int(m.group(1)) - 16) // 16 // 8 * 8      # 262136 with 4 MiB
+    too_small = header_enum("TMO_ERR_SCRATCH_TOO_SMALL")
+
+    def call(B, MB):
+        return fn(FAKE, None, 1024, 128, 0, 0, 10, FAKE, None, FAKE, None, FAKE, None, FAKE, B,
+                  MB, 64, 16, 8, 16, 128, 1, 8, 2, None)
+    assert pages == 262136
+    assert call(1, pages + 1) == too_small
+    assert call(pages // 8 + 1, 8) == too_small
+    assert call(1 << 40, 1 << 30) == too_small          # no overflow in batch * max_blocks
+    assert call(-1, 4) == EINVAL
+    assert call(0, 4) == 0
+    assert "scratch" in lib.tmo_hip_status_string(too_small).decode()
 
 
 def test_dequant_workspace_bytes(lib):
