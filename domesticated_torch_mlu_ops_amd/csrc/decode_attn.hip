@@ -68,6 +68,7 @@ struct AttnParams {
   int32_t bs_shift;              // log2(BS) when BS is a power of two, else -1
   int64_t NB;
   int32_t q_dtype;               // TMO_DTYPE_*
+  int32_t q_vec;                 // q rows 16-byte aligned 2-byte values: vector q loads
   int32_t c_dtype;               // cache TMO_DTYPE_*
   int32_t splits;
   int64_t split_tokens;          // multiple of 64
@@ -168,8 +169,15 @@ __device__ __forceinline__ f16x4 codes_f16(uint32_t w) {
 // the int8 kernels up to head_size 128, fewer where that would spill.
 constexpr int attn_min_blocks(int d, int kind) { return d == 256 ? 1 : (kind != 0 && d == 128 ? 2 : 3); }
 
+#ifndef TMO_ATTN_DEPTH
+#define TMO_ATTN_DEPTH 2
+#endif
+
 template <int kD, int kKind, bool kQLo>
 __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(AttnParams p) {
+  // tiles in flight per wavefront: three register sets where they fit the register budget of
+  // attn_min_blocks (the int8 kernels up to head_size 128)
+  constexpr int kDepth = (kKind == 0 && kD <= 128 && !kQLo) ? TMO_ATTN_DEPTH : 2;
   constexpr bool kF16 = kKind == 2;
   using M = Mfma<kF16>;
   using V4 = typename M::V4;
@@ -186,6 +194,9 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   const int hk = blockIdx.y;
   const int split = blockIdx.x;
   const Range rg = token_range(p, i, split);
+  // An empty split (past the sequence's keys) writes no partial; the combine skips it.  With
+  // one split the (zero) output and lse are still written below.
+  if (p.splits > 1 && rg.begin >= rg.end) return;
   const int hq = hk * p.g + col;
   const bool qvalid = col < p.g;
 
@@ -199,16 +210,67 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   VQ qhi[kQK], qlo[kQLo ? kQK : 1];
   float qx[kQK][4];
   float qabs = 0.0f;
+  // token positions fit in 32 bits (context lengths are int32)
+  const int32_t begin32 = (int32_t)rg.begin, end32 = (int32_t)rg.end, last32 = (int32_t)(rg.L - 1);
+  const int32_t first_tile = (int32_t)(rg.begin >> 4);
+  const int32_t end_tile = (int32_t)((rg.end + 15) >> 4);
+  const int32_t* bt_row = p.bt + i * p.max_blocks;
+  auto page_of = [&](int32_t tl) -> int32_t {
+    const int32_t t0 = tl * 16;
+    return p.bs_shift >= 0 ? t0 >> p.bs_shift : t0 / p.BS;
+  };
+  // The wave's tiles are first_tile + wave + 4n.  Lane l holds the block of the window's
+  // tile n = l (64 tiles per refill), read per tile with v_readlane.
+  int32_t lane_blk = -1;
+  int32_t win_base = first_tile + wave;
+  auto refill = [&]() {
+    const int32_t tl = win_base + 4 * lane;
+    lane_blk = tl < end_tile ? bt_row[page_of(tl)] : -1;
+  };
+  // Start-up: the q row (and per-channel key scales) and the first block-table window are
+  // independent reads, issued together -- q first, so the q arithmetic waits for q only and
+  // the block ids arrive meanwhile; the first tile loads wait for the block ids alone.
+  if (p.q_vec) {  // 16-byte aligned q rows of a 2-byte type: kDC / 8 vectors per lane
+    constexpr int kQV = kDC / 8;
+    u32x4 qraw[kQV];
+    const u32x4* qp = reinterpret_cast<const u32x4*>(
+        static_cast<const uint16_t*>(p.q) + i * p.q_sb + (int64_t)hq * p.q_sh + grp * kDC);
 #pragma unroll
-  for (int m = 0; m < kQK; ++m) {
+    for (int v = 0; v < kQV; ++v) qraw[v] = qvalid ? qp[v] : u32x4{0u, 0u, 0u, 0u};
+    u32x4 kcs[kKind == 0 ? kDC / 4 : 1];
+    if (kKind == 0 && p.smode == 2) {
+      const u32x4* sp = reinterpret_cast<const u32x4*>(p.ks + (int64_t)hk * kD + grp * kDC);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int d = grp * kDC + 4 * m + e;
-      float x = qvalid ? load_q(p, i * p.q_sb + (int64_t)hq * p.q_sh + d) : 0.0f;
-      if (kKind == 0 && p.smode == 2) x *= p.ks[(int64_t)hk * kD + d];
-      qx[m][e] = x;
-      qabs = fmaxf(qabs, fabsf(x));
+      for (int v = 0; v < (kKind == 0 ? kDC / 4 : 1); ++v) kcs[v] = sp[v];
     }
+    refill();
+    const bool bf = p.q_dtype == TMO_DTYPE_BF16;
+#pragma unroll
+    for (int m = 0; m < kQK; ++m) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = 4 * m + e;  // channel within the lane's run
+        const uint32_t w = qraw[c / 8][(c % 8) / 2];
+        const uint32_t h = (c & 1) ? (w >> 16) : (w & 0xffffu);
+        float x = bf ? __uint_as_float(h << 16) : f16_bits_to_f32(h);
+        if (kKind == 0 && p.smode == 2) x *= __uint_as_float(kcs[c / 4][c % 4]);
+        qx[m][e] = x;
+        qabs = fmaxf(qabs, fabsf(x));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < kQK; ++m) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = grp * kDC + 4 * m + e;
+        float x = qvalid ? load_q(p, i * p.q_sb + (int64_t)hq * p.q_sh + d) : 0.0f;
+        if (kKind == 0 && p.smode == 2) x *= p.ks[(int64_t)hk * kD + d];
+        qx[m][e] = x;
+        qabs = fmaxf(qabs, fabsf(x));
+      }
+    }
+    refill();
   }
   float inv_sigma = 1.0f, qk_off = 0.0f;
   if constexpr (kKind == 0) {
@@ -255,11 +317,6 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
 #pragma unroll
   for (int j = 0; j < kDV; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // token positions fit in 32 bits (context lengths are int32)
-  const int32_t begin32 = (int32_t)rg.begin, end32 = (int32_t)rg.end, last32 = (int32_t)(rg.L - 1);
-  const int32_t first_tile = (int32_t)(rg.begin >> 4);
-  const int32_t end_tile = (int32_t)((rg.end + 15) >> 4);
-  const int32_t* bt_row = p.bt + i * p.max_blocks;
   const char* kbase = static_cast<const char*>(p.kc);
   const char* vbase = static_cast<const char*>(p.vc);
   const int64_t page_bytes = (int64_t)p.BS * kD * kEs;      // one head's page
@@ -274,10 +331,6 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
     uint32_t kw[kKW];
     uint32_t vw[4][kVW];
     float ksc[4], vsc[4];
-  };
-  auto page_of = [&](int32_t tl) -> int32_t {
-    const int32_t t0 = tl * 16;
-    return p.bs_shift >= 0 ? t0 >> p.bs_shift : t0 / p.BS;
   };
   auto load_tile = [&](Raw& r, int32_t tl, int64_t blk) {
     const int32_t t0 = tl * 16;
@@ -327,16 +380,6 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
     }
   };
 
-  // The wave's tiles are first_tile + wave + 4n.  Lane l holds the block of the window's
-  // tile n = l (64 tiles per refill), read per tile with v_readlane; each tile's loads are
-  // issued one iteration before its arithmetic.
-  int32_t lane_blk = -1;
-  int32_t win_base = first_tile + wave;
-  auto refill = [&]() {
-    const int32_t tl = win_base + 4 * lane;
-    lane_blk = tl < end_tile ? bt_row[page_of(tl)] : -1;
-  };
-  refill();
   // Arithmetic of one loaded tile (the whole wavefront: the MFMAs need every lane).
   auto compute_tile = [&](const Raw& r, int32_t tile) {
       const int32_t t0 = tile * 16;
@@ -430,8 +473,8 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
       }
   };
 
-  // Two register sets alternate: while one tile is computed the next one's loads are in
-  // flight (no copies between the sets).
+  // Register sets rotate: while one tile is computed the loads of the next kDepth - 1 tiles
+  // are in flight (no copies between the sets).
   int32_t slot = 0;  // index in the window of the most recently loaded tile
   Raw ra, rb;
   int32_t tile = first_tile + wave;
@@ -450,16 +493,38 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
     }
   };
   bool ok_a = try_load(ra, tile);
-  while (tile < end_tile) {
+  if constexpr (kDepth == 3) {
+    Raw rc;
     advance();
-    const bool ok_b = try_load(rb, tile + 4);
-    if (ok_a) compute_tile(ra, tile);
-    tile += 4;
-    if (tile >= end_tile) break;
-    advance();
-    ok_a = try_load(ra, tile + 4);
-    if (ok_b) compute_tile(rb, tile);
-    tile += 4;
+    bool ok_b = try_load(rb, tile + 4);
+    while (tile < end_tile) {
+      advance();
+      const bool ok_c = try_load(rc, tile + 8);
+      if (ok_a) compute_tile(ra, tile);
+      tile += 4;
+      if (tile >= end_tile) break;
+      advance();
+      ok_a = try_load(ra, tile + 8);
+      if (ok_b) compute_tile(rb, tile);
+      tile += 4;
+      if (tile >= end_tile) break;
+      advance();
+      ok_b = try_load(rb, tile + 8);
+      if (ok_c) compute_tile(rc, tile);
+      tile += 4;
+    }
+  } else {
+    while (tile < end_tile) {
+      advance();
+      const bool ok_b = try_load(rb, tile + 4);
+      if (ok_a) compute_tile(ra, tile);
+      tile += 4;
+      if (tile >= end_tile) break;
+      advance();
+      ok_a = try_load(ra, tile + 4);
+      if (ok_b) compute_tile(rb, tile);
+      tile += 4;
+    }
   }
 
   // ---- combine the four wavefronts: waves 1..3 leave (max, sum, accumulators) in LDS in
@@ -467,7 +532,11 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   const float lsum = col_sum(lpart);
   __shared__ float lds_m[4][16];
   __shared__ float lds_l[4][16];
-  __shared__ float lds_o[3][16][kD];
+  // lane-major partial rows, padded by one float: lane l's value k at l * (4 kDV + 1) + k, so
+  // the 64 lanes of one store or load hit 64 different banks (a [col][channel] layout put the
+  // 16 columns of a wavefront on one bank)
+  constexpr int kRow = 4 * kDV + 1;
+  __shared__ float lds_o[3][kWave * kRow];
   if (grp == 0) {
     lds_m[wave][col] = mrun;
     lds_l[wave][col] = lsum;
@@ -476,7 +545,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
 #pragma unroll
     for (int j = 0; j < kDV; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) lds_o[wave - 1][col][kDV * (4 * grp + e) + j] = acc[j][e];
+      for (int e = 0; e < 4; ++e) lds_o[wave - 1][lane * kRow + e * kDV + j] = acc[j][e];
   }
   __syncthreads();
   if (wave != 0) return;
@@ -505,7 +574,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
       const int d = kDV * (4 * grp + e) + j;
       float o = acc[j][e] * f[0];
 #pragma unroll
-      for (int w = 1; w < 4; ++w) o += lds_o[w - 1][col][d] * f[w];
+      for (int w = 1; w < 4; ++w) o += lds_o[w - 1][lane * kRow + e * kDV + j] * f[w];
       o *= inv;
       if (kKind == 0 && p.smode == 2) o *= p.vs[(int64_t)hk * kD + d];  // per-channel V scale
       if (direct) {
@@ -520,7 +589,9 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
         lt > 0.0f ? (mx + log2f(lt)) * kLn2 : -__builtin_inff();
 }
 
-// Merge the splits of one (sequence, query head): one wavefront per row.
+// Merge the splits of one (sequence, query head): one wavefront per row.  Lane s holds split
+// s's (max, sum) and turns them into the split's weight sum_s * 2^(max_s - max), once; the
+// output channels then read each split's row once, weighted through a lane broadcast.
 __global__ __launch_bounds__(256) void attn_combine(AttnParams p) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;  // i * Hq + hq
@@ -530,21 +601,45 @@ __global__ __launch_bounds__(256) void attn_combine(AttnParams p) {
   const int hk = hq / p.g, qc = hq - hk * p.g;
   const int64_t stride = (int64_t)p.g * (p.D + 2);
   const float* base = p.ws + ((i * p.Hkv + hk) * p.splits * (int64_t)p.g + qc) * (p.D + 2);
-  float mx = -__builtin_inff();
-  for (int s = 0; s < p.splits; ++s) mx = fmaxf(mx, base[s * stride]);
-  float lt = 0.0f;
-  for (int s = 0; s < p.splits; ++s) {
-    const float m = base[s * stride];
-    if (m != -__builtin_inff()) lt += base[s * stride + 1] * __builtin_amdgcn_exp2f(m - mx);
+  // splits past the sequence's keys wrote nothing (the main kernel returned early): the
+  // non-empty splits are a prefix, of length `live`
+  const Range r0 = token_range(p, i, 0);
+  int live = p.splits;
+  if (p.split_tokens > 0) {
+    const int64_t n = (r0.L - r0.begin + p.split_tokens - 1) / p.split_tokens;
+    live = (int)(n < p.splits ? n : p.splits);
+    if (live < 1 && p.splits > 0) live = r0.begin < r0.L ? 1 : 0;
   }
-  for (int d = lane; d < p.D; d += kWave) {
+  float mx = -__builtin_inff();
+  for (int s0 = 0; s0 < live; s0 += kWave) {
+    const int s = s0 + lane;
+    mx = fmaxf(mx, s < live ? base[s * stride] : -__builtin_inff());
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  float lt = 0.0f;
+  for (int s0 = 0; s0 < live; s0 += kWave) {
+    const int s = s0 + lane;
+    const float m = s < live ? base[s * stride] : -__builtin_inff();
+    lt += m != -__builtin_inff() ? base[s * stride + 1] * __builtin_amdgcn_exp2f(m - mx) : 0.0f;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) lt += __shfl_xor(lt, o, kWave);
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  for (int d0 = 0; d0 < p.D; d0 += kWave) {
+    const int d = d0 + lane;
     float o = 0.0f;
-    for (int s = 0; s < p.splits; ++s) {
-      const float m = base[s * stride];
-      if (m != -__builtin_inff())
-        o += base[s * stride + 2 + d] * base[s * stride + 1] * __builtin_amdgcn_exp2f(m - mx);
+    for (int s0 = 0; s0 < live; s0 += kWave) {
+      const int sl = s0 + lane;
+      const float m = sl < live ? base[sl * stride] : -__builtin_inff();
+      const float wgt = m != -__builtin_inff() ? base[sl * stride + 1] * __builtin_amdgcn_exp2f(m - mx) : 0.0f;
+      const int n = live - s0 < kWave ? live - s0 : kWave;
+      for (int k = 0; k < n; ++k) {
+        const float wk = __shfl(wgt, k, kWave);
+        if (wk != 0.0f && d < p.D) o += base[(s0 + k) * stride + 2 + d] * wk;
+      }
     }
-    store_out(p, i * p.o_sb + (int64_t)hq * p.o_sh + d, lt > 0.0f ? o / lt : 0.0f);
+    if (d < p.D) store_out(p, i * p.o_sb + (int64_t)hq * p.o_sh + d, o * inv);
   }
   if (lane == 0 && p.lse)
     p.lse[i * p.lse_sb + (int64_t)hq * p.lse_sh] =
@@ -742,6 +837,10 @@ extern "C" int tmo_hip_single_query_cached_kv_attn(
   p.bs_shift = ilog2_if_pow2(block_size);
   p.NB = num_blocks;
   p.q_dtype = q_dtype;
+  p.q_vec = q_dtype != TMO_DTYPE_F32 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+            q_stride_seq % 8 == 0 && q_stride_head % 8 == 0 &&
+            (cache_dtype != TMO_DTYPE_I8 || scale_mode != 2 ||
+             reinterpret_cast<uintptr_t>(k_scale) % 16 == 0);
   p.ws = static_cast<float*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
