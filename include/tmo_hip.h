@@ -295,7 +295,8 @@ int tmo_hip_scaled_quantize_per_token(const void* x, int64_t n0, int64_t inner,
  *   its cache position is cache_seq_offset[i] + j (0 + j when NULL) in cache batch
  *            cache_bs_id[i] (i when NULL; a negative id skips the sequence).
  * A token whose row, cache batch or position lies outside its tensor is skipped.  Different
- * sequences must not map to the same cache rows (write ops) or token rows (read ops).
+ * sequences must not map to the same cache rows (write ops) or token rows (read ops), and
+ * packed prefix offsets are non-decreasing.
  * Per-token scales are contiguous [max_batch, num_heads, cache_len] fp32.
  */
 

@@ -90,6 +90,25 @@ def test_reshape_linear_cache_truncation_and_views(tmo, ref, dev):
     _reshape_both(tmo, ref, dev, case, torch.float16)
 
 
+# ---------------------------------------------------------------------------- token-major launches
+
+@pytest.mark.parametrize("B", [5, 70])
+def test_linear_write_ops_token_major_targets(tmo, ref, dev, B):
+    """The write ops' token-major launches (packed input without context_seq_offset: rows found
+    from the prefix offsets) with cache batch ids (one negative), cache position offsets (one
+    running past the cache's end), a max_context_len shorter than some sequences, and more
+    sequences than one wavefront holds (the lookup's second path)."""
+    case = W.linear_case(torch.bfloat16, 61 + B, packed=True, offsets=True, B=B,
+                         cache_batch=B + 3)
+    case.context_seq_offset = None  # rows at the prefix offsets of the lengths
+    print(f"[linear token-major] B={B}", flush=True)
+    _reshape_both(tmo, ref, dev, case, torch.bfloat16)
+    _reshape_both(tmo, ref, dev, case, torch.bfloat16, max_len=7)
+    for cdt in (torch.int8, torch.float8_e4m3fn):
+        _quant_both(tmo, ref, dev, case, cdt)
+    _quant_both(tmo, ref, dev, case, torch.int8, groups=4)
+
+
 # ---------------------------------------------------------------------------- quant_to_linear_cache
 
 def _quant_both(tmo, ref, dev, case, cache_dtype, groups=0, with_v=True):
