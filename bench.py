@@ -55,6 +55,7 @@ WORKLOADS = {
     "linear_dequant": "dequant_from_linear_cache (per-token scales), 8 sequences x 4096 tokens x 8 KV heads x 128: int8 linear cache [8, 8, 8192, 128] -> bf16",
     "linear_reshape": "reshape_linear_cache, 8 packed sequences x 4096 tokens x 8 KV heads x 128 bf16 -> bf16 linear cache [8, 8, 8192, 128]",
     "decode_attn": "single_query_cached_kv_attn, one bf16 query token x 32 heads per sequence over configs[4]'s int8 pages (64 seqs, ctx ~U[1024,32768], 8 KV heads x 128, per-token scales)",
+    "reshape_paged": "reshape_paged_cache on configs[2]'s shape: 32768 tokens x 8 KV heads x 128 bf16 K/V scattered into bf16 pages (65536 blocks x 16)",
 }
 KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<BF16,16,1,false>",
            "cfg3": "quant_paged_vec<BF16,16,1,false>", "cfg4": "sq_dense<BF16,8,false,true>",
@@ -63,7 +64,8 @@ KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<
            "offline_f8": "quant_paged_static_vec<BF16,16,true>",
            "fused_rope": "fused_rope_tok<BF16,16,3,0>", "fused_rope_ln": "fused_rope_tok<BF16,16,3,1>",
            "linear_quant": "lin_quant<BF16,16,false,false>", "linear_dequant": "lin_dequant<BF16,16>",
-           "linear_reshape": "lin_copy<16>", "decode_attn": "attn_mfma<128,0,false>"}
+           "linear_reshape": "lin_copy<16>", "decode_attn": "attn_mfma<128,0,false>",
+           "reshape_paged": "reshape_paged_kernel<16>"}
 
 
 def parse_args():
@@ -83,9 +85,10 @@ def parse_args():
 # ---------------------------------------------------------------------------- GPU timing
 
 def time_graph(torch, calls, steps: int, warmup: int) -> float:
-    """Mean ms per call: `calls` (one closure per buffer set) captured once into a HIP graph,
-    replayed until `steps` calls have run; HIP events on the capture stream bracket the timed
-    replays."""
+    """Median ms per call: `calls` (one closure per buffer set) captured once into a HIP graph,
+    replayed until `steps` calls have run; HIP events on the capture stream bracket each timed
+    replay (at least 20 of them), and the median replay's time per call is returned (the mean
+    over all timed replays is kept in LAST_MEAN_MS)."""
     n = len(calls)
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
@@ -97,7 +100,7 @@ def time_graph(torch, calls, steps: int, warmup: int) -> float:
     with torch.cuda.graph(graph, stream=stream):
         for c in calls:
             c()
-    reps = max(1, math.ceil(steps / n))
+    reps = max(20, math.ceil(steps / n))
     wreps = max(1, math.ceil(warmup / n))
     with torch.cuda.stream(stream):
         # Clock settling: after idle the GPU takes ~10 ms of load to reach its steady clocks
@@ -110,16 +113,20 @@ def time_graph(torch, calls, steps: int, warmup: int) -> float:
         for _ in range(wreps):
             graph.replay()
         torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(reps):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        evs[0].record(stream)
+        for i in range(reps):
             graph.replay()
-        end.record(stream)
+            evs[i + 1].record(stream)
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / (reps * n)
+    per = [evs[i].elapsed_time(evs[i + 1]) / n for i in range(reps)]
+    global LAST_MEAN_MS
+    LAST_MEAN_MS = evs[0].elapsed_time(evs[reps]) / (reps * n)
     del graph
-    return ms
+    return statistics.median(per)
+
+
+LAST_MEAN_MS = None
 
 
 def n_sets(bytes_per_call: int, cap: int = 512) -> int:
@@ -152,6 +159,28 @@ def bench_paged_quant(torch, tmo, W, case, dev, steps, warmup):
         kc, vc, ks, vs = shared if shared is not None else case.empty_caches(device=dev)
         calls.append(lambda k=k, v=v, kc=kc, vc=vc, ks=ks, vs=vs, sl=slots:
                      tmo.quant_to_paged_cache(k, v, kc, vc, ks, vs, sl))
+    ms = time_graph(torch, calls, steps, warmup)
+    return ms, alg, case.valid_tokens(), sets
+
+
+def bench_reshape(torch, tmo, W, case, dev, steps, warmup):
+    """reshape_paged_cache (scatter, direction False) of configs[2]'s K/V as bf16 into bf16
+    pages: per set its own K/V rows; shared caches with per-set shifted slots."""
+    T, H, D = case.k.shape
+    alg = 2 * 2 * case.valid_tokens() * H * D * case.k.element_size() + 4 * T
+    sets = n_sets(alg)
+    g = torch.Generator(device=dev).manual_seed(19)
+    nslots = case.num_blocks * case.block_size
+    slots0 = case.slot_mapping.to(dev)
+    kc = torch.zeros((case.num_blocks, H, case.block_size, D), dtype=case.k.dtype, device=dev)
+    vc = torch.zeros_like(kc)
+    calls = []
+    for s in range(sets):
+        k = torch.randn((T, H, D), generator=g, device=dev).to(case.k.dtype)
+        v = torch.randn((T, H, D), generator=g, device=dev).to(case.k.dtype)
+        shift = (s * 9973 * case.block_size) % nslots
+        slots = torch.where(slots0 >= 0, (slots0 + shift) % nslots, slots0)
+        calls.append(lambda k=k, v=v, sl=slots: tmo.reshape_paged_cache(k, v, kc, vc, sl, False))
     ms = time_graph(torch, calls, steps, warmup)
     return ms, alg, case.valid_tokens(), sets
 
@@ -374,6 +403,13 @@ def profile_pass(torch, tmo, W, names, dev, n: int) -> None:
             k, v, sl = case.k.to(dev), case.v.to(dev), case.slot_mapping.to(dev)
             kc, vc, ks, vs = case.empty_caches(device=dev)
             fn = lambda: tmo.quant_to_paged_cache(k, v, kc, vc, ks, vs, sl)
+        elif name == "reshape_paged":
+            case = W.cfg3()
+            k, v, sl = case.k.to(dev), case.v.to(dev), case.slot_mapping.to(dev)
+            shape = (case.num_blocks, k.shape[1], case.block_size, k.shape[2])
+            kc = torch.zeros(shape, dtype=k.dtype, device=dev)
+            vc = torch.zeros_like(kc)
+            fn = lambda: tmo.reshape_paged_cache(k, v, kc, vc, sl, False)
         elif name.startswith("offline"):
             case = W.cfg3()
             k, v, sl = case.k.to(dev), case.v.to(dev), case.slot_mapping.to(dev)
@@ -489,6 +525,18 @@ def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
                                                  nthreads=nthreads)
         alg, units, desc = sub.algorithmic_bytes(), sub.valid_tokens(), \
             f"quant_to_paged_cache on the first {n} tokens of {workload}"
+    elif workload == "reshape_paged":
+        case = W.cfg3()
+        n = 4096
+        sub = W.PagedQuantCase(case.name, case.k[:n].contiguous(), case.v[:n].contiguous(),
+                               case.slot_mapping[:n].contiguous(), case.num_blocks)
+        shape = (case.num_blocks, W.H, case.block_size, W.D)
+        kc = torch.zeros(shape, dtype=case.k.dtype)
+        vc = torch.zeros_like(kc)
+        fn = lambda: oracle.reshape_paged_cache(sub.k, sub.v, kc, vc, sub.slot_mapping,
+                                                nthreads=nthreads)
+        alg = 2 * 2 * n * W.H * W.D * case.k.element_size() + 4 * n
+        units, desc = n, f"reshape_paged_cache on the first {n} tokens of cfg3"
     elif workload.startswith("offline"):
         case = W.cfg3()
         n = 4096
@@ -610,7 +658,18 @@ def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
     t = statistics.median(times)
     return {"value": round(alg / t / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
             "sample": f"{desc}; median of {len(times)} runs, {t * 1e3:.3f} ms each",
-            "tokens_per_s": round(units / t, 1)}
+            "tokens_per_s": round(units / t, 1), "cpu_model": cpu_model()}
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), as the baseline's hardware."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 # ---------------------------------------------------------------------------- main
@@ -632,18 +691,28 @@ def main():
     todo = [args.workload] if args.configs == "headline" else \
         ["cfg1", "cfg2", "cfg3", "cfg4", "cfg4_moe", "cfg5", "offline_i8", "offline_f8",
          "fused_rope", "fused_rope_ln", "linear_quant", "linear_dequant", "linear_reshape",
-         "decode_attn"]
+         "decode_attn", "reshape_paged"]
     if args.workload not in todo:
         todo.append(args.workload)
     if args.profile_pass:
         profile_pass(torch, tmo, W, todo, dev, args.profile_pass)
         return
+    # rocprofv3 per-dispatch mean duration of each workload's kernel, from the committed
+    # profile summary: graph replays overlap consecutive small calls, so for the decode-sized
+    # configs the per-call figure and the per-dispatch figure differ
+    tfile = REPO / "profiles" / "traffic.json"
+    tjson = json.loads(tfile.read_text()) if tfile.exists() else {}
+    profiled = {k: v["dispatch_us"] for k, v in tjson.items()
+                if isinstance(v, dict) and "dispatch_us" in v}
     per = {}
     for name in todo:
         t0 = time.perf_counter()
         if name in ("cfg1", "cfg2", "cfg3"):
             ms, alg, units, sets = bench_paged_quant(torch, tmo, W, getattr(W, name)(), dev,
                                                      args.steps, args.warmup)
+        elif name == "reshape_paged":
+            ms, alg, units, sets = bench_reshape(torch, tmo, W, W.cfg3(), dev,
+                                                 max(20, args.steps // 4), max(4, args.warmup // 4))
         elif name.startswith("cfg4"):
             ms, alg, units, sets = bench_smooth_quant(torch, tmo, W, getattr(W, name)(), dev,
                                                       args.steps, args.warmup)
@@ -666,9 +735,16 @@ def main():
                                                  max(10, args.steps // 40), max(2, args.warmup // 10))
         gbs = alg / (ms * 1e-3) / 1e9
         per[name] = {"kernel": KERNELS[name], "us_per_call": round(ms * 1e3, 3),
+                     "us_per_call_mean": round(LAST_MEAN_MS * 1e3, 3),
                      "algorithmic_bytes": alg, "GB_s": round(gbs, 1),
                      "frac_of_peak": round(gbs / PEAK_GBS, 4),
                      "units_per_s": round(units / (ms * 1e-3), 1), "buffer_sets": sets}
+        if name in profiled:  # per-dispatch duration of the same kernel in the committed profile
+            per[name]["us_per_dispatch_rocprof"] = profiled[name]
+        if name == "cfg4_moe":  # every gathered row counted as read (top-2 reads a token twice)
+            rb = W.cfg4_moe().algorithmic_bytes(per_row_reads=True)
+            per[name]["per_row_read_bytes"] = rb
+            per[name]["per_row_read_GB_s"] = round(rb / (ms * 1e-3) / 1e9, 1)
         print(f"# {name}: {ms * 1e3:.2f} us/call  {gbs:.1f} GB/s  ({100 * gbs / PEAK_GBS:.1f}% of "
               f"peak)  [{time.perf_counter() - t0:.1f} s]", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
@@ -677,10 +753,7 @@ def main():
     streams = stream_ceilings() if args.configs == "all" else None
 
     head = per[args.workload]
-    traffic = None
-    tfile = REPO / "profiles" / "traffic.json"
-    if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get(args.workload, {}).get("hbm_bytes_per_launch")
+    traffic = tjson.get(args.workload, {}).get("hbm_bytes_per_launch")
     cpu = cpu_baseline(torch, W, args.workload, args.cpu_seconds)
     line = {
         "metric": METRIC,
@@ -703,6 +776,7 @@ def main():
                           "fused_rope_ln": "bf16 qkv in; bf16 Q written back; int8 K/V codes + fp32 scales out",
                           "linear_dequant": "int8 codes + fp32 scales in; bf16 out",
                           "linear_reshape": "bf16 in; bf16 out",
+                          "reshape_paged": "bf16 K/V rows in; bf16 pages out",
                           "decode_attn": "bf16 q, int8 K/V pages + fp32 scales in; bf16 out; fp32 softmax"}
                    .get(args.workload, "bf16 in; int8 codes + fp32 scales out"),
                    "tokens_per_s": head["units_per_s"],
