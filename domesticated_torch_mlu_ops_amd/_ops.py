@@ -534,16 +534,20 @@ def single_query_cached_kv_attn(
     max_seq_q: int = -1,
     sink: Optional[torch.Tensor] = None,
 ):
-    """Decode attention of one query token per sequence (``q [batch, 1, heads, head_size]`` or
-    ``[batch, heads, head_size]``) over its paged KV cache: ``softmax(softmax_scale * q K^T
-    (+ alibi)) V`` over the keys ``[max(0, L - 1 - windows_size_left), L)`` of each sequence,
-    keys gathered through ``block_tables`` from ``[num_blocks, kv_heads, block_size,
-    head_size]`` caches -- int8 (``kv_cache_quant_bit_size=8``) with per-token, per-channel or
-    per-tensor scales, or of q's dtype (``-1``); query head h reads KV head
-    ``h // (heads / kv_heads)``.  Computed in fp32 (MFMA with exact bf16/f16 operands).  With
-    ``return_lse`` also returns ``ln sum exp`` of the logits, ``[batch, heads, 1]`` (or
-    ``[heads, total_q]`` for 3-D q).  One query token per sequence only: ``cu_seq_q``,
-    ``mask``, ``sink`` and quantised q / output raise ``RuntimeError``.
+    """Attention of each sequence's query tokens over its paged KV cache:
+    ``softmax(softmax_scale * q K^T (+ alibi)) V`` per query head, keys gathered through
+    ``block_tables`` from ``[num_blocks, kv_heads, block_size, head_size]`` caches -- int8
+    (``kv_cache_quant_bit_size=8``) with per-token, per-channel or per-tensor scales, or of q's
+    dtype (``-1``); query head h reads KV head ``h // (heads / kv_heads)``.  q is ``[batch,
+    seq_q, heads, head_size]``, ``[total_q, heads, head_size]`` with ``cu_seq_q`` (``[batch +
+    1]``, ``max_seq_q`` an upper bound of the counts or <= 0 for unknown) or ``[batch, heads,
+    head_size]``.  A sequence's nq tokens are its last nq positions: token s (position
+    ``P = L - nq + s``) sees keys ``[max(0, P - windows_size_left), P]``, ALiBi adds
+    ``slope * (j - P)``, and ``sink`` (``[heads]`` float logits) joins the softmax
+    denominator only.  Computed in fp32 (MFMA with exact bf16/f16 operands).  With
+    ``return_lse`` also returns ``ln`` of the softmax denominator, ``[batch, heads, seq_q]``
+    (or ``[heads, total_q]`` for 3-D q).  ``mask``, ``v_cache=None`` and quantised q / output
+    raise ``RuntimeError``.
 
     Reference: ``_ops.py:777-900`` (math ``:800-817``).  Returns ``out`` or ``(out, lse)``.
     """

@@ -1,17 +1,21 @@
-// single_query_cached_kv_attn for gfx950: one query token per sequence against its paged KV
-// cache (reference _ops.py:777-900; header include/torch_mlu_ops.h:107-130).
+// single_query_cached_kv_attn for gfx950: the query tokens of each sequence against its paged
+// KV cache (reference _ops.py:777-900; header include/torch_mlu_ops.h:107-130).
 //
-//   s_j = softmax_scale * q . k_j (+ alibi_slope * (j - (L - 1))),  out = softmax(s) @ V,
-//   lse = log sum_j exp(s_j),  keys j in [max(0, L - 1 - window_left), L),
+//   s_j = softmax_scale * q . k_j (+ alibi_slope * (j - P)),
+//   out = sum_j e^(s_j) v_j / (sum_j e^(s_j) (+ e^sink)),  lse = log of that denominator,
 //
-// key j at row j % BS of page block_tables[i, j / BS] (pages outside [0, NB) are masked); query
-// head hq reads KV head hq / (Hq / Hkv).  Caches are int8 with per-token [NB, Hkv, BS] or
-// per-channel [Hkv, D] fp32 scales (k = code * scale), or of q's dtype.
+// for query token s of a sequence with nq tokens and L keys at position P = L - nq + s (one
+// token: P = L - 1), over keys j in [max(0, P - window_left), P]; key j at row j % BS of page
+// block_tables[i, j / BS] (pages outside [0, NB) are masked); query head hq reads KV head
+// hq / (Hq / Hkv).  Caches are int8 with per-token [NB, Hkv, BS] or per-channel [Hkv, D] fp32
+// scales (k = code * scale), or of q's dtype.
 //
 // MFMA path (bf16 or f16 operands, fp32 accumulation; head_size 64 / 128 / 256, block_size a
-// multiple of 16, at most 16 query heads per KV head): a workgroup of four wavefronts owns one
-// (sequence, KV head, split) and its wavefronts take every fourth 16-token tile.  Per tile:
-//   * S^T = K Q^T with v_mfma_f32_16x16x16 (tokens are the rows, the group's query heads the
+// multiple of 16): the query columns of a (sequence, KV head) are its (token, query head)
+// pairs, c = s * g + head-in-group (g = Hq / Hkv), in blocks of 16.  A workgroup of four
+// wavefronts owns one (sequence, KV head, split, column block) and its wavefronts take every
+// fourth 16-token tile.  Per tile:
+//   * S^T = K Q^T with v_mfma_f32_16x16x16 (tokens are the rows, the block's query columns the
 //     columns, zero-padded to 16): lane (t = l % 16, c = l / 16) holds token t's channels
 //     [c D/4, (c + 1) D/4), so the K tile is read as contiguous row pieces, and MFMA m takes
 //     channels c D/4 + 4m .. + 3 of every lane group (a permutation of the reduction order).
@@ -27,11 +31,12 @@
 //   * p (times the per-token V scale) is split into hi + lo bf16 operands (16 significant
 //     bits) and two products accumulate, against V codes converted to bf16 exactly; q gets a
 //     lo operand too when it is folded with per-channel key scales.
-//   * Online softmax in base 2 per query column; a lane keeps a partial sum over its own four
-//     tokens, summed over the lane groups at the end.
+//   * Online softmax in base 2 per query column, each column masked to its own key range; a
+//     lane keeps a partial sum over its own four tokens, summed over the lane groups at the
+//     end.  The sink joins the denominator when the output is written.
 // The four wavefronts combine through LDS; with more than one split per (sequence, KV head)
 // the partials (max, sum, normalised row) go to a caller-provided workspace and a combine
-// kernel merges them.  A generic kernel (one wavefront per (sequence, query head), VALU)
+// kernel merges them.  A generic kernel (one wavefront per (query token, query head), VALU)
 // serves every other shape and dtype.
 #include "tmo_device.h"
 
@@ -46,9 +51,17 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;  // log2 headroom of the lazily moved softmax maximum
 constexpr float kLn2 = 0.6931471805599453f;
 
+// Query rows: token s of sequence i is at element i * q_sb + (row0_i + s) * q_ss + hq * q_sh,
+// row0_i = cu[i] with cu_seq_q (q_sb 0 then) and 0 without; out and lse alike.
 struct AttnParams {
   const void* q;
-  int64_t q_sb, q_sh;            // q [B, Hq, D] strides (elements); last dim contiguous
+  int64_t q_sb, q_ss, q_sh;      // strides (elements); last dim contiguous
+  const int32_t* cu;             // cu_seq_q [B + 1], or null: S tokens per sequence
+  int32_t S;                     // tokens per sequence (at most, with cu)
+  int32_t ncols;                 // S * g query columns per (sequence, KV head)
+  int32_t ncb;                   // column blocks of 16
+  int64_t total_q;               // q rows with cu: rows outside [0, total_q) are skipped
+  const float* sink;             // [Hq] natural-log logits, or null
   const void* kc;
   const void* vc;                // caches [NB, Hkv, BS, D] contiguous
   const float* ks;
@@ -61,9 +74,9 @@ struct AttnParams {
   int64_t window;                // < 0: unlimited
   float scale_log2;              // softmax_scale * log2(e)
   void* out;
-  int64_t o_sb, o_sh;
+  int64_t o_sb, o_ss, o_sh;
   float* lse;                    // null when not requested
-  int64_t lse_sb, lse_sh;
+  int64_t lse_sb, lse_ss, lse_sh;
   int32_t B, Hq, Hkv, g, D, BS;
   int32_t bs_shift;              // log2(BS) when BS is a power of two, else -1
   int64_t NB;
@@ -72,7 +85,7 @@ struct AttnParams {
   int32_t c_dtype;               // cache TMO_DTYPE_*
   int32_t splits;
   int64_t split_tokens;          // multiple of 64
-  float* ws;                     // [B, Hkv, splits, g, D + 2] when splits > 1
+  float* ws;                     // [B, Hkv, splits, ncols, D + 2] when splits > 1
 };
 
 // ------------------------------------------------------------------------------ small helpers
@@ -98,25 +111,69 @@ __device__ __forceinline__ void store_out(const AttnParams& p, int64_t e, float 
   }
 }
 
-// Token range of sequence i (after the window) and of split s within it.
-struct Range {
-  int64_t L, begin, end;
+// Sequence i: its keys L (clamped to its block table), its query tokens nq (the first
+// min(nq, S) are computed) and the row of its token 0.
+struct Seq {
+  int64_t L, nq, row0;
 };
 
-__device__ __forceinline__ Range token_range(const AttnParams& p, int64_t i, int s) {
-  Range r;
+__device__ __forceinline__ Seq seq_of(const AttnParams& p, int64_t i) {
+  Seq q;
   int64_t L = p.lens[i];
   const int64_t cap = p.max_blocks * (int64_t)p.BS;
   if (L > cap) L = cap;
   if (L < 0) L = 0;
-  r.L = L;
+  q.L = L;
+  if (p.cu) {
+    q.row0 = p.cu[i];
+    q.nq = (int64_t)p.cu[i + 1] - q.row0;
+  } else {
+    q.row0 = 0;
+    q.nq = p.S;
+  }
+  return q;
+}
+
+// Token s of the sequence is computed: within S and nq, and (with cu_seq_q) a row of q.
+__device__ __forceinline__ bool token_valid(const AttnParams& p, const Seq& q, int64_t s) {
+  return s < p.S && s < q.nq && (!p.cu || (q.row0 + s >= 0 && q.row0 + s < p.total_q));
+}
+
+// Key range of the sequence (token 0's window start to L) and of split s within it.
+struct Range {
+  int64_t begin, end;
+};
+
+__device__ __forceinline__ Range token_range(const AttnParams& p, const Seq& q, int s) {
+  Range r;
+  const int64_t L = q.L;
   int64_t j0 = 0;
-  if (p.window >= 0 && L - 1 - p.window > 0) j0 = L - 1 - p.window;
+  if (p.window >= 0 && L - q.nq - p.window > 0) j0 = L - q.nq - p.window;
   r.begin = j0 + (int64_t)s * p.split_tokens;
   r.end = r.begin + p.split_tokens < L ? r.begin + p.split_tokens : L;
   if (s == p.splits - 1) r.end = L;  // the last split takes any tokens past max_context_len
   if (p.splits == 1) r.begin = j0;
   return r;
+}
+
+// Final normalisation with the sink: m, l the column's maximum (base 2) and sum over its keys
+// (l = 0: none).  Returns the factor of the unnormalised accumulators and writes the lse.
+__device__ __forceinline__ float finish(const AttnParams& p, int hq, float m, float l, float* lse) {
+  float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  float lg = l > 0.0f ? m + log2f(l) : -__builtin_inff();
+  if (p.sink) {
+    const float sk = p.sink[hq] * kLog2e;
+    if (l > 0.0f) {
+      const float mm = fmaxf(m, sk);
+      const float lt = l * __builtin_amdgcn_exp2f(m - mm) + __builtin_amdgcn_exp2f(sk - mm);
+      inv = __builtin_amdgcn_exp2f(m - mm) / lt;
+      lg = mm + log2f(lt);
+    } else {
+      lg = sk;
+    }
+  }
+  *lse = lg * kLn2;
+  return inv;
 }
 
 // Max / sum over the four lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48) of a column.
@@ -188,17 +245,23 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int col = lane & 15;        // query column (query head within the group) / token row
+  const int col = lane & 15;        // query column within the block / token row
   const int grp = lane >> 4;        // lane group c
   const int64_t i = blockIdx.z;
   const int hk = blockIdx.y;
-  const int split = blockIdx.x;
-  const Range rg = token_range(p, i, split);
+  const int cb = (int)(blockIdx.x / (unsigned)p.splits);   // column block
+  const int split = (int)blockIdx.x - cb * p.splits;
+  const Seq sq = seq_of(p, i);
+  const Range rg = token_range(p, sq, split);
   // An empty split (past the sequence's keys) writes no partial; the combine skips it.  With
   // one split the (zero) output and lse are still written below.
   if (p.splits > 1 && rg.begin >= rg.end) return;
-  const int hq = hk * p.g + col;
-  const bool qvalid = col < p.g;
+  // column c = token s * g + head hc: query head hk * g + hc of token s at position P
+  const int c = cb * 16 + col;
+  const int tok = c / p.g;
+  const int hq = hk * p.g + (c - tok * p.g);
+  const bool qvalid = c < p.ncols && token_valid(p, sq, tok);
+  const int64_t qrow = sq.row0 + tok;
 
   // ---- Q operand (B of S^T = K Q^T): column `col`, channels grp * kDC + 4m .. + 3.  The QK
   // product runs on f16 operands: int8 codes as 1152 + code (codes_f16), q scaled by a power
@@ -210,10 +273,28 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   VQ qhi[kQK], qlo[kQLo ? kQK : 1];
   float qx[kQK][4];
   float qabs = 0.0f;
-  // token positions fit in 32 bits (context lengths are int32)
-  const int32_t begin32 = (int32_t)rg.begin, end32 = (int32_t)rg.end, last32 = (int32_t)(rg.L - 1);
-  const int32_t first_tile = (int32_t)(rg.begin >> 4);
-  const int32_t end_tile = (int32_t)((rg.end + 15) >> 4);
+  // token positions fit in 32 bits (context lengths are int32).  Column keys: [klo, khi]
+  // within the split, khi < klo when the column has none (or is padding).
+  const int32_t pos = (int32_t)(sq.L - sq.nq) + tok;                 // the column's P
+  int32_t klo = (int32_t)rg.begin, khi = (int32_t)rg.end - 1;
+  if (p.window >= 0 && pos - (int32_t)p.window > klo) klo = pos - (int32_t)p.window;
+  if (pos < khi) khi = pos;
+  if (!qvalid) khi = klo - 1;
+  // The block's tiles: from its first valid token's window start to its last token's P
+  // (wave-uniform: every lane computes the same numbers)
+  int64_t bbeg = rg.begin, bend = rg.end;
+  {
+    const int64_t ntok = sq.nq < p.S ? sq.nq : p.S;
+    const int64_t s_first = (int64_t)cb * 16 / p.g;
+    int64_t s_last = ((int64_t)cb * 16 + 15) / p.g;
+    if (s_last > ntok - 1) s_last = ntok - 1;
+    const int64_t p_first = sq.L - sq.nq + s_first, p_last = sq.L - sq.nq + s_last;
+    if (p.window >= 0 && p_first - p.window > bbeg) bbeg = p_first - p.window;
+    if (p_last + 1 < bend) bend = p_last + 1;
+    if (s_last < s_first || bend <= bbeg) bbeg = bend = 0;   // no key for the block: no tile
+  }
+  const int32_t first_tile = (int32_t)(bbeg >> 4);
+  const int32_t end_tile = (int32_t)((bend + 15) >> 4);
   const int32_t* bt_row = p.bt + i * p.max_blocks;
   auto page_of = [&](int32_t tl) -> int32_t {
     const int32_t t0 = tl * 16;
@@ -234,7 +315,8 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
     constexpr int kQV = kDC / 8;
     u32x4 qraw[kQV];
     const u32x4* qp = reinterpret_cast<const u32x4*>(
-        static_cast<const uint16_t*>(p.q) + i * p.q_sb + (int64_t)hq * p.q_sh + grp * kDC);
+        static_cast<const uint16_t*>(p.q) + i * p.q_sb + qrow * p.q_ss + (int64_t)hq * p.q_sh +
+        grp * kDC);
 #pragma unroll
     for (int v = 0; v < kQV; ++v) qraw[v] = qvalid ? qp[v] : u32x4{0u, 0u, 0u, 0u};
     u32x4 kcs[kKind == 0 ? kDC / 4 : 1];
@@ -264,7 +346,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int d = grp * kDC + 4 * m + e;
-        float x = qvalid ? load_q(p, i * p.q_sb + (int64_t)hq * p.q_sh + d) : 0.0f;
+        float x = qvalid ? load_q(p, i * p.q_sb + qrow * p.q_ss + (int64_t)hq * p.q_sh + d) : 0.0f;
         if (kKind == 0 && p.smode == 2) x *= p.ks[(int64_t)hk * kD + d];
         qx[m][e] = x;
         qabs = fmaxf(qabs, fabsf(x));
@@ -407,8 +489,8 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
       for (int e = 0; e < 4; ++e) {
         const int32_t j = t0 + 4 * grp + e;
         float v = (s[e] - qk_off) * (r.ksc[e] * score_scale);
-        if (p.alibi) v += alibi * (float)(j - last32);
-        if (j < begin32 || j >= end32 || !qvalid) v = -__builtin_inff();
+        if (p.alibi) v += alibi * (float)(j - pos);
+        if (j < klo || j > khi) v = -__builtin_inff();
         sc[e] = v;
         tmax = fmaxf(tmax, v);
       }
@@ -559,14 +641,16 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
     f[w] = mx == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(lds_m[w][col] - mx);
     lt += lds_l[w][col] * f[w];
   }
-  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
   if (!qvalid) return;
   const bool direct = p.splits == 1;
-  float* ws_row = p.ws + ((((i * p.Hkv + hk) * p.splits + split) * p.g + col) * (int64_t)(kD + 2));
+  float lse_v;
+  const float inv = direct ? finish(p, hq, mx, lt, &lse_v) : (lt > 0.0f ? 1.0f / lt : 0.0f);
+  float* ws_row = p.ws + ((((i * p.Hkv + hk) * p.splits + split) * p.ncols + c) * (int64_t)(kD + 2));
   if (!direct && grp == 0) {
     ws_row[0] = mx;
     ws_row[1] = lt;
   }
+  const int64_t orow = i * p.o_sb + qrow * p.o_ss + (int64_t)hq * p.o_sh;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
 #pragma unroll
@@ -578,37 +662,40 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
       o *= inv;
       if (kKind == 0 && p.smode == 2) o *= p.vs[(int64_t)hk * kD + d];  // per-channel V scale
       if (direct) {
-        store_out(p, i * p.o_sb + (int64_t)hq * p.o_sh + d, o);
+        store_out(p, orow + d, o);
       } else {
         ws_row[2 + d] = o;
       }
     }
   }
-  if (direct && grp == 0 && p.lse)
-    p.lse[i * p.lse_sb + (int64_t)hq * p.lse_sh] =
-        lt > 0.0f ? (mx + log2f(lt)) * kLn2 : -__builtin_inff();
+  if (direct && grp == 0 && p.lse) p.lse[i * p.lse_sb + qrow * p.lse_ss + (int64_t)hq * p.lse_sh] = lse_v;
 }
 
-// Merge the splits of one (sequence, query head): one wavefront per row.  Lane s holds split
-// s's (max, sum) and turns them into the split's weight sum_s * 2^(max_s - max), once; the
-// output channels then read each split's row once, weighted through a lane broadcast.
+// Merge the splits of one (query token, query head): one wavefront per row.  Lane s holds
+// split s's (max, sum) and turns them into the split's weight sum_s * 2^(max_s - max), once;
+// the output channels then read each split's row once, weighted through a lane broadcast.
 __global__ __launch_bounds__(256) void attn_combine(AttnParams p) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;  // i * Hq + hq
-  if (row >= (int64_t)p.B * p.Hq) return;
-  const int64_t i = row / p.Hq;
-  const int hq = (int)(row - i * p.Hq);
-  const int hk = hq / p.g, qc = hq - hk * p.g;
-  const int64_t stride = (int64_t)p.g * (p.D + 2);
-  const float* base = p.ws + ((i * p.Hkv + hk) * p.splits * (int64_t)p.g + qc) * (p.D + 2);
+  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;  // (i * S + s) * Hq + hq
+  if (row >= (int64_t)p.B * p.S * p.Hq) return;
+  const int64_t it = row / p.Hq;
+  const int hq = (int)(row - it * p.Hq);
+  const int64_t i = it / p.S;
+  const int tok = (int)(it - i * p.S);
+  const Seq sq = seq_of(p, i);
+  if (!token_valid(p, sq, tok)) return;
+  const int hk = hq / p.g;
+  const int c = tok * p.g + (hq - hk * p.g);
+  const int64_t stride = (int64_t)p.ncols * (p.D + 2);
+  const float* base = p.ws + ((i * p.Hkv + hk) * p.splits * (int64_t)p.ncols + c) * (p.D + 2);
   // splits past the sequence's keys wrote nothing (the main kernel returned early): the
   // non-empty splits are a prefix, of length `live`
-  const Range r0 = token_range(p, i, 0);
+  const Range r0 = token_range(p, sq, 0);
   int live = p.splits;
   if (p.split_tokens > 0) {
-    const int64_t n = (r0.L - r0.begin + p.split_tokens - 1) / p.split_tokens;
+    const int64_t n = (sq.L - r0.begin + p.split_tokens - 1) / p.split_tokens;
     live = (int)(n < p.splits ? n : p.splits);
-    if (live < 1 && p.splits > 0) live = r0.begin < r0.L ? 1 : 0;
+    if (live < 1 && p.splits > 0) live = r0.begin < sq.L ? 1 : 0;
   }
   float mx = -__builtin_inff();
   for (int s0 = 0; s0 < live; s0 += kWave) {
@@ -625,7 +712,10 @@ __global__ __launch_bounds__(256) void attn_combine(AttnParams p) {
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) lt += __shfl_xor(lt, o, kWave);
-  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  float lse_v;
+  const float inv = finish(p, hq, mx, lt, &lse_v);
+  const int64_t qrow = sq.row0 + tok;
+  const int64_t orow = i * p.o_sb + qrow * p.o_ss + (int64_t)hq * p.o_sh;
   for (int d0 = 0; d0 < p.D; d0 += kWave) {
     const int d = d0 + lane;
     float o = 0.0f;
@@ -639,11 +729,9 @@ __global__ __launch_bounds__(256) void attn_combine(AttnParams p) {
         if (wk != 0.0f && d < p.D) o += base[(s0 + k) * stride + 2 + d] * wk;
       }
     }
-    if (d < p.D) store_out(p, i * p.o_sb + (int64_t)hq * p.o_sh + d, o * inv);
+    if (d < p.D) store_out(p, orow + d, o * inv);
   }
-  if (lane == 0 && p.lse)
-    p.lse[i * p.lse_sb + (int64_t)hq * p.lse_sh] =
-        lt > 0.0f ? (mx + log2f(lt)) * kLn2 : -__builtin_inff();
+  if (lane == 0 && p.lse) p.lse[i * p.lse_sb + qrow * p.lse_ss + (int64_t)hq * p.lse_sh] = lse_v;
 }
 
 // ------------------------------------------------------------------------------ generic kernel
@@ -664,29 +752,37 @@ __device__ __forceinline__ float cache_value(const AttnParams& p, const void* ba
   }
 }
 
-// One wavefront per (sequence, query head): 64 keys at a time, one per lane (a lane computes
-// its key's full dot product), then every lane accumulates its channels over the 64 keys.
-// Dimensions up to 512 (8 accumulators per lane).
+// One wavefront per (query token, query head): 64 keys at a time, one per lane (a lane
+// computes its key's full dot product), then every lane accumulates its channels over the 64
+// keys.  Dimensions up to 512 (8 accumulators per lane).
 __global__ __launch_bounds__(256) void attn_generic(AttnParams p) {
   const int cache_dtype = p.c_dtype;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
-  if (row >= (int64_t)p.B * p.Hq) return;
-  const int64_t i = row / p.Hq;
-  const int hq = (int)(row - i * p.Hq);
+  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;  // (i * S + s) * Hq + hq
+  if (row >= (int64_t)p.B * p.S * p.Hq) return;
+  const int64_t it = row / p.Hq;
+  const int hq = (int)(row - it * p.Hq);
+  const int64_t i = it / p.S;
+  const int64_t tok = it - i * p.S;
+  const Seq sq = seq_of(p, i);
+  if (!token_valid(p, sq, tok)) return;
   const int hk = hq / p.g;
-  const Range rg = token_range(p, i, 0);
+  // keys [jb, je) of the token at position P
+  const int64_t P = sq.L - sq.nq + tok;
+  const int64_t je = P + 1 < sq.L ? P + 1 : sq.L;
+  const int64_t jb = p.window >= 0 && P - p.window > 0 ? P - p.window : 0;
   const float alibi = p.alibi ? p.alibi[i * p.Hq + hq] * kLog2e : 0.0f;
   float mrun = -__builtin_inff(), l = 0.0f;
   float acc[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
-  const int64_t qe = i * p.q_sb + (int64_t)hq * p.q_sh;
-  for (int64_t j0 = rg.begin; j0 < rg.end; j0 += kWave) {
+  const int64_t qrow = sq.row0 + tok;
+  const int64_t qe = i * p.q_sb + qrow * p.q_ss + (int64_t)hq * p.q_sh;
+  for (int64_t j0 = jb; j0 < je; j0 += kWave) {
     const int64_t j = j0 + lane;
     float s = -__builtin_inff();
     int blk = -1, r = 0;
-    if (j < rg.end) {
+    if (j < je) {
       blk = p.bt[i * p.max_blocks + j / p.BS];
       r = (int)(j % p.BS);
       if (blk >= 0 && blk < p.NB) {
@@ -694,7 +790,7 @@ __global__ __launch_bounds__(256) void attn_generic(AttnParams p) {
         for (int d = 0; d < p.D; ++d)
           dot += load_q(p, qe + d) * cache_value(p, p.kc, p.ks, blk, hk, r, d, cache_dtype);
         s = dot * p.scale_log2;
-        if (p.alibi) s += alibi * (float)(j - (rg.L - 1));
+        if (p.alibi) s += alibi * (float)(j - P);
       } else {
         blk = -1;
       }
@@ -725,25 +821,26 @@ __global__ __launch_bounds__(256) void attn_generic(AttnParams p) {
       }
     }
   }
+  float lse_v;
+  const float inv = finish(p, hq, mrun, l, &lse_v);
+  const int64_t orow = i * p.o_sb + qrow * p.o_ss + (int64_t)hq * p.o_sh;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int d = lane + u * kWave;
-    if (d < p.D) store_out(p, i * p.o_sb + (int64_t)hq * p.o_sh + d, l > 0.0f ? acc[u] / l : 0.0f);
+    if (d < p.D) store_out(p, orow + d, p.sink ? acc[u] * inv : (l > 0.0f ? acc[u] / l : 0.0f));
   }
-  if (lane == 0 && p.lse)
-    p.lse[i * p.lse_sb + (int64_t)hq * p.lse_sh] =
-        l > 0.0f ? (mrun + log2f(l)) * kLn2 : -__builtin_inff();
+  if (lane == 0 && p.lse) p.lse[i * p.lse_sb + qrow * p.lse_ss + (int64_t)hq * p.lse_sh] = lse_v;
 }
 
 // ------------------------------------------------------------------------------ launch
 
 template <int kD, int kKind>
 int launch_mfma_d(const AttnParams& p, bool qlo, hipStream_t st) {
-  const dim3 grid((unsigned)p.splits, (unsigned)p.Hkv, (unsigned)p.B), block(256);
+  const dim3 grid((unsigned)(p.splits * p.ncb), (unsigned)p.Hkv, (unsigned)p.B), block(256);
   int rc = qlo ? launch_kernel(attn_mfma<kD, kKind, true>, grid, block, st, p)
                : launch_kernel(attn_mfma<kD, kKind, false>, grid, block, st, p);
   if (rc != TMO_OK || p.splits == 1) return rc;
-  const int64_t rows = (int64_t)p.B * p.Hq;
+  const int64_t rows = (int64_t)p.B * p.S * p.Hq;
   return launch_kernel(attn_combine, dim3((unsigned)((rows + 3) / 4)), block, st, p);
 }
 
@@ -761,26 +858,35 @@ int launch_mfma(const AttnParams& p, bool qlo, hipStream_t st) {
 
 using namespace tmo;
 
-extern "C" int64_t tmo_hip_attn_workspace_bytes(int64_t batch, int64_t num_kv_heads,
-                                                int64_t num_q_heads, int64_t head_size,
-                                                int64_t max_context_len, int64_t splits) {
-  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || head_size <= 0 || splits <= 1)
+extern "C" int64_t tmo_hip_cached_kv_attn_workspace_bytes(int64_t batch, int64_t num_kv_heads,
+                                                          int64_t num_q_heads, int64_t head_size,
+                                                          int64_t seq_q, int64_t splits) {
+  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || head_size <= 0 || seq_q <= 0 ||
+      splits <= 1)
     return 0;
-  (void)max_context_len;
-  return batch * num_kv_heads * splits * (num_q_heads / num_kv_heads) * (head_size + 2) *
+  return batch * num_kv_heads * splits * seq_q * (num_q_heads / num_kv_heads) * (head_size + 2) *
          (int64_t)sizeof(float);
 }
 
-extern "C" int tmo_hip_single_query_cached_kv_attn(
-    const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* k_cache,
+extern "C" int64_t tmo_hip_attn_workspace_bytes(int64_t batch, int64_t num_kv_heads,
+                                                int64_t num_q_heads, int64_t head_size,
+                                                int64_t max_context_len, int64_t splits) {
+  (void)max_context_len;
+  return tmo_hip_cached_kv_attn_workspace_bytes(batch, num_kv_heads, num_q_heads, head_size, 1,
+                                                splits);
+}
+
+extern "C" int tmo_hip_cached_kv_attn(
+    const void* q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head,
+    const int32_t* cu_seq_q, int64_t seq_q, int64_t total_q, const void* k_cache,
     const void* v_cache, const float* k_scale, const float* v_scale, int scale_mode,
     const int32_t* block_tables, int64_t max_blocks, const int32_t* context_lens,
-    const float* alibi_slopes, void* out, int64_t out_stride_seq, int64_t out_stride_head,
-    float* lse, int64_t lse_stride_seq, int64_t lse_stride_head, int64_t batch,
-    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_size, int64_t num_blocks,
-    int64_t block_size, int64_t max_context_len, int64_t window_left, float softmax_scale,
-    int q_dtype, int cache_dtype, int64_t splits, void* workspace, int64_t workspace_bytes,
-    void* stream) {
+    const float* alibi_slopes, const float* sink, void* out, int64_t out_stride_batch,
+    int64_t out_stride_token, int64_t out_stride_head, float* lse, int64_t lse_stride_batch,
+    int64_t lse_stride_token, int64_t lse_stride_head, int64_t batch, int64_t num_q_heads,
+    int64_t num_kv_heads, int64_t head_size, int64_t num_blocks, int64_t block_size,
+    int64_t max_context_len, int64_t window_left, float softmax_scale, int q_dtype,
+    int cache_dtype, int64_t splits, void* workspace, int64_t workspace_bytes, void* stream) {
   if (q_dtype != TMO_DTYPE_BF16 && q_dtype != TMO_DTYPE_F16 && q_dtype != TMO_DTYPE_F32)
     return TMO_ERR_UNSUPPORTED_DTYPE;
   if (cache_dtype != TMO_DTYPE_I8 && cache_dtype != q_dtype) return TMO_ERR_UNSUPPORTED_DTYPE;
@@ -795,22 +901,35 @@ extern "C" int tmo_hip_single_query_cached_kv_attn(
   if (max_context_len < 0) max_context_len = 0;
   if (batch < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
       head_size <= 0 || head_size > 512 || num_blocks < 0 || block_size <= 0 || max_blocks < 0 ||
-      splits < 1 || q_stride_seq < 0 || q_stride_head < 0 ||
-      out_stride_seq < 0 || out_stride_head < 0)
+      splits < 1 || seq_q < 0 || q_stride_batch < 0 || q_stride_token < 0 || q_stride_head < 0 ||
+      out_stride_batch < 0 || out_stride_token < 0 || out_stride_head < 0 ||
+      (cu_seq_q && total_q < 0))
     return TMO_ERR_INVALID_ARGUMENT;
-  if (batch > 65535 || num_kv_heads > 65535 || splits > 65535 || num_q_heads > 0x7fffffffLL)
+  const int64_t g = num_q_heads / num_kv_heads;
+  if (batch > 65535 || num_kv_heads > 65535 || splits > 65535 || num_q_heads > 0x7fffffffLL ||
+      seq_q > 0x7fffffffLL / num_q_heads)
+    return TMO_ERR_INVALID_ARGUMENT;
+  const int64_t ncb = (seq_q * g + 15) / 16;
+  if (splits * ncb > 0x7fffffffLL || (batch * seq_q * num_q_heads + 3) / 4 > 0x7fffffffLL)
     return TMO_ERR_INVALID_ARGUMENT;
   if (splits > 1 && (!workspace ||
-                     workspace_bytes < tmo_hip_attn_workspace_bytes(batch, num_kv_heads,
-                                                                     num_q_heads, head_size,
-                                                                     max_context_len, splits)))
+                     workspace_bytes < tmo_hip_cached_kv_attn_workspace_bytes(
+                                           batch, num_kv_heads, num_q_heads, head_size, seq_q,
+                                           splits)))
     return TMO_ERR_INVALID_ARGUMENT;
-  if (batch == 0 || num_q_heads == 0) return TMO_OK;
+  if (batch == 0 || seq_q == 0) return TMO_OK;
 
   AttnParams p{};
   p.q = q;
-  p.q_sb = q_stride_seq;
+  p.q_sb = cu_seq_q ? 0 : q_stride_batch;
+  p.q_ss = q_stride_token;
   p.q_sh = q_stride_head;
+  p.cu = cu_seq_q;
+  p.S = (int32_t)seq_q;
+  p.ncols = (int32_t)(seq_q * g);
+  p.ncb = (int32_t)ncb;
+  p.total_q = cu_seq_q ? total_q : batch * seq_q;
+  p.sink = sink;
   p.kc = k_cache;
   p.vc = v_cache;
   p.ks = k_scale;
@@ -823,42 +942,41 @@ extern "C" int tmo_hip_single_query_cached_kv_attn(
   p.window = window_left;
   p.scale_log2 = softmax_scale * kLog2e;
   p.out = out;
-  p.o_sb = out_stride_seq;
+  p.o_sb = cu_seq_q ? 0 : out_stride_batch;
+  p.o_ss = out_stride_token;
   p.o_sh = out_stride_head;
   p.lse = lse;
-  p.lse_sb = lse_stride_seq;
+  p.lse_sb = cu_seq_q ? 0 : lse_stride_batch;
+  p.lse_ss = lse_stride_token;
   p.lse_sh = lse_stride_head;
   p.B = (int32_t)batch;
   p.Hq = (int32_t)num_q_heads;
   p.Hkv = (int32_t)num_kv_heads;
-  p.g = (int32_t)(num_q_heads / num_kv_heads);
+  p.g = (int32_t)g;
   p.D = (int32_t)head_size;
   p.BS = (int32_t)block_size;
   p.bs_shift = ilog2_if_pow2(block_size);
   p.NB = num_blocks;
   p.q_dtype = q_dtype;
   p.q_vec = q_dtype != TMO_DTYPE_F32 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
-            q_stride_seq % 8 == 0 && q_stride_head % 8 == 0 &&
+            p.q_sb % 8 == 0 && q_stride_token % 8 == 0 && q_stride_head % 8 == 0 &&
             (cache_dtype != TMO_DTYPE_I8 || scale_mode != 2 ||
              reinterpret_cast<uintptr_t>(k_scale) % 16 == 0);
   p.ws = static_cast<float*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
-  // MFMA path eligibility: head size, page rows, group size, 16-byte aligned rows and scales,
-  // q's dtype representable by the operands (int8 caches: bf16 with a lo part when needed).
+  // MFMA path eligibility: head size, page rows, 16-byte aligned rows and scales, q's dtype
+  // representable by the operands (int8 caches: bf16 with a lo part when needed).
   auto al = [](const void* x, int a) { return reinterpret_cast<uintptr_t>(x) % a == 0; };
   bool mfma = (head_size == 64 || head_size == 128 || head_size == 256) && block_size % 16 == 0 &&
-              p.g <= 16 && al(k_cache, 16) && al(v_cache, 16);
-  if (cache_dtype == TMO_DTYPE_I8) {
-    mfma = mfma && q_dtype != TMO_DTYPE_F32 && (scale_mode != 1 || (al(k_scale, 16) && al(v_scale, 16)));
-  } else {
-    mfma = mfma && q_dtype != TMO_DTYPE_F32;
-  }
+              al(k_cache, 16) && al(v_cache, 16) && q_dtype != TMO_DTYPE_F32;
+  if (cache_dtype == TMO_DTYPE_I8)
+    mfma = mfma && (scale_mode != 1 || (al(k_scale, 16) && al(v_scale, 16)));
   p.c_dtype = cache_dtype;
   if (!mfma) {
     p.splits = 1;
     p.split_tokens = 1;
-    const int64_t rows = batch * num_q_heads;
+    const int64_t rows = batch * seq_q * num_q_heads;
     if ((rows + 3) / 4 > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
     return launch_kernel(attn_generic, dim3((unsigned)((rows + 3) / 4)), dim3(256), st, p);
   }
@@ -873,4 +991,23 @@ extern "C" int tmo_hip_single_query_cached_kv_attn(
   if (cache_dtype == TMO_DTYPE_I8) return launch_mfma<0>(p, scale_mode == 2, st);
   if (cache_dtype == TMO_DTYPE_BF16) return launch_mfma<1>(p, false, st);
   return launch_mfma<2>(p, false, st);
+}
+
+extern "C" int tmo_hip_single_query_cached_kv_attn(
+    const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* k_cache,
+    const void* v_cache, const float* k_scale, const float* v_scale, int scale_mode,
+    const int32_t* block_tables, int64_t max_blocks, const int32_t* context_lens,
+    const float* alibi_slopes, void* out, int64_t out_stride_seq, int64_t out_stride_head,
+    float* lse, int64_t lse_stride_seq, int64_t lse_stride_head, int64_t batch,
+    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_size, int64_t num_blocks,
+    int64_t block_size, int64_t max_context_len, int64_t window_left, float softmax_scale,
+    int q_dtype, int cache_dtype, int64_t splits, void* workspace, int64_t workspace_bytes,
+    void* stream) {
+  return tmo_hip_cached_kv_attn(
+      q, q_stride_seq, 0, q_stride_head, nullptr, 1, 0, k_cache, v_cache, k_scale, v_scale,
+      scale_mode, block_tables, max_blocks, context_lens, alibi_slopes, nullptr, out,
+      out_stride_seq, 0, out_stride_head, lse, lse_stride_seq, 0, lse_stride_head, batch,
+      num_q_heads, num_kv_heads, head_size, num_blocks, block_size, max_context_len,
+      window_left, softmax_scale, q_dtype, cache_dtype, splits, workspace, workspace_bytes,
+      stream);
 }

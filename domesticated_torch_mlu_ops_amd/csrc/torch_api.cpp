@@ -988,26 +988,63 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   const char* op = "single_query_cached_kv_attn";
   TORCH_CHECK(!q_quant_scale.has_value() && !out_quant_scale.has_value(), op,
               ": quantised q / output are not supported by this build");
-  TORCH_CHECK(!mask.has_value() && !sink.has_value(), op, ": mask and sink are not supported");
-  TORCH_CHECK(!cu_seq_q.has_value(), op,
-              ": one query token per sequence only (cu_seq_q is not supported)");
+  TORCH_CHECK(!mask.has_value(), op, ": mask is not supported by this build");
   TORCH_CHECK(v_cache.has_value(), op, ": a separate v_cache is required");
   TORCH_CHECK(compute_dtype == "float" || compute_dtype == "half" || compute_dtype == "bfloat16",
               op, ": compute_dtype must be float, half or bfloat16 (the softmax runs in fp32)");
   TORCH_CHECK(windows_size_right.expect_int() == -1, op, ": windows_size_right must be -1");
   TORCH_CHECK(kv_cache_quant_bit_size == -1 || kv_cache_quant_bit_size == 8, op,
               ": kv_cache_quant_bit_size must be -1 or 8, got ", kv_cache_quant_bit_size);
-  (void)max_seq_q;
   check_device(q_ori, q_ori, "q");
-  TORCH_CHECK(q_ori.dim() == 3 || (q_ori.dim() == 4 && q_ori.size(1) == 1), op,
-              ": q must be [batch, 1, heads, head_size] or [batch, heads, head_size], got ",
+  // q forms (reference _ops.py:824): [batch, seq_q, heads, head_size] (seq_q tokens for every
+  // sequence), [total_q, heads, head_size] with cu_seq_q [batch + 1], or [batch, heads,
+  // head_size] (one token each).  Token s of a sequence with nq tokens sits at position
+  // L - nq + s and sees the keys up to it.
+  const bool four = q_ori.dim() == 4;
+  TORCH_CHECK(four || q_ori.dim() == 3, op,
+              ": q must be [batch, seq_q, heads, head_size] or [total_q, heads, head_size], got ",
               q_ori.sizes());
-  const at::Tensor q = q_ori.dim() == 4 ? q_ori.select(1, 0) : q_ori;
-  TORCH_CHECK(q.size(2) <= 1 || q.stride(2) == 1, "q must have a contiguous last dim");
+  TORCH_CHECK(!(four && cu_seq_q.has_value()), op, ": cu_seq_q goes with a 3-D q");
+  const at::Tensor& q = q_ori;
+  TORCH_CHECK(q.size(-1) <= 1 || q.stride(-1) == 1, "q must have a contiguous last dim");
   const int qdt = dtype_code(q.scalar_type());
   TORCH_CHECK(qdt == TMO_DTYPE_F32 || qdt == TMO_DTYPE_F16 || qdt == TMO_DTYPE_BF16, op,
               ": q must be float, half or bfloat16, got ", q.scalar_type());
-  const int64_t B = q.size(0), Hq = q.size(1), D = q.size(2);
+  const int64_t Hq = q.size(-2), D = q.size(-1);
+  check_device(context_lens, q_ori, "context_lens");
+  TORCH_CHECK(context_lens.scalar_type() == at::kInt && context_lens.dim() == 1 &&
+                  context_lens.is_contiguous(),
+              op, ": context_lens must be a contiguous int32 [batch] tensor");
+  const int64_t B = context_lens.size(0);
+  const int32_t* cu = nullptr;
+  int64_t seq_q = 1, total_q = 0;
+  if (four) {
+    TORCH_CHECK(q.size(0) == B, op, ": q's batch ", q.size(0), " != context_lens' ", B);
+    seq_q = q.size(1);
+  } else if (cu_seq_q.has_value()) {
+    const at::Tensor& c = *cu_seq_q;
+    check_device(c, q_ori, "cu_seq_q");
+    TORCH_CHECK(c.scalar_type() == at::kInt && c.dim() == 1 && c.size(0) == B + 1 &&
+                    c.is_contiguous(),
+                op, ": cu_seq_q must be a contiguous int32 [batch + 1] tensor, got ", c.sizes());
+    cu = c.data_ptr<int32_t>();
+    total_q = q.size(0);
+    // max_seq_q <= 0: unknown, read from cu_seq_q (one device-to-host copy)
+    seq_q = max_seq_q.expect_int();
+    if (seq_q <= 0)
+      seq_q = B == 0 ? 0 : std::max<int64_t>(0, (c.slice(0, 1) - c.slice(0, 0, B)).max().item<int64_t>());
+  } else {
+    TORCH_CHECK(q.size(0) == B, op, ": q's rows ", q.size(0), " != context_lens' batch ", B,
+                " (pass cu_seq_q for several tokens per sequence)");
+  }
+  const float* sink_p = nullptr;
+  if (sink.has_value()) {
+    check_device(*sink, q_ori, "sink");
+    TORCH_CHECK(sink->scalar_type() == at::kFloat && sink->is_contiguous() &&
+                    sink->numel() == Hq,
+                op, ": sink must be a contiguous float32 [heads] tensor");
+    sink_p = sink->data_ptr<float>();
+  }
   const at::Tensor& vc = *v_cache;
   check_device(k_cache, q_ori, "k_cache");
   check_device(vc, q_ori, "v_cache");
@@ -1061,10 +1098,6 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
                   block_tables.size(0) == B && block_tables.is_contiguous(),
               op, ": block_tables must be a contiguous int32 [batch, max_blocks] tensor, got ",
               block_tables.sizes());
-  check_device(context_lens, q_ori, "context_lens");
-  TORCH_CHECK(context_lens.scalar_type() == at::kInt && context_lens.dim() == 1 &&
-                  context_lens.size(0) == B && context_lens.is_contiguous(),
-              op, ": context_lens must be a contiguous int32 [batch] tensor");
   const float* alibi = nullptr;
   if (alibi_slopes.has_value()) {
     check_device(*alibi_slopes, q_ori, "alibi_slopes");
@@ -1076,32 +1109,36 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   check_device(output, q_ori, "output");
   TORCH_CHECK(output.sizes() == q_ori.sizes() && output.scalar_type() == q.scalar_type(), op,
               ": output must have q's shape and dtype");
-  const at::Tensor out = output.dim() == 4 ? output.select(1, 0) : output;
-  TORCH_CHECK(out.size(2) <= 1 || out.stride(2) == 1, "output must have a contiguous last dim");
+  const at::Tensor& out = output;
+  TORCH_CHECK(out.size(-1) <= 1 || out.stride(-1) == 1, "output must have a contiguous last dim");
+  // element strides (batch, token, head) of q, out and lse
+  const int64_t q_sb = four || !cu ? q.stride(0) : 0, q_ss = four ? q.stride(1) : (cu ? q.stride(0) : 0);
+  const int64_t o_sb = four || !cu ? out.stride(0) : 0, o_ss = four ? out.stride(1) : (cu ? out.stride(0) : 0);
   float* lse = nullptr;
-  int64_t lse_sb = 0, lse_sh = 0;
+  int64_t lse_sb = 0, lse_ss = 0, lse_sh = 0;
   if (return_lse) {
     TORCH_CHECK(output_lse.has_value(), op, ": return_lse needs output_lse");
     const at::Tensor& l = *output_lse;
     check_device(l, q_ori, "output_lse");
     TORCH_CHECK(l.scalar_type() == at::kFloat, "output_lse must be float32");
-    if (q_ori.dim() == 4) {  // [batch, heads, 1]
-      TORCH_CHECK(l.dim() == 3 && l.size(0) == B && l.size(1) == Hq && l.size(2) == 1, op,
-                  ": output_lse must be [batch, heads, 1], got ", l.sizes());
+    if (four) {  // [batch, heads, seq_q]
+      TORCH_CHECK(l.dim() == 3 && l.size(0) == B && l.size(1) == Hq && l.size(2) == seq_q, op,
+                  ": output_lse must be [batch, heads, seq_q], got ", l.sizes());
       lse_sb = l.stride(0);
       lse_sh = l.stride(1);
+      lse_ss = l.stride(2);
     } else {  // [heads, total_q]
-      TORCH_CHECK(l.dim() == 2 && l.size(0) == Hq && l.size(1) == B, op,
+      TORCH_CHECK(l.dim() == 2 && l.size(0) == Hq && l.size(1) == q.size(0), op,
                   ": output_lse must be [heads, total_q], got ", l.sizes());
-      lse_sb = l.stride(1);
       lse_sh = l.stride(0);
+      (cu ? lse_ss : lse_sb) = l.stride(1);
     }
     lse = l.data_ptr<float>();
   }
   // max_context_len <= 0: an uncertain maximum (reference docstring); negative counts as 0
   const int64_t max_ctx = std::max<int64_t>(0, max_context_len.expect_int());
   const int64_t window = windows_size_left.expect_int();
-  if (B == 0) return;
+  if (B == 0 || seq_q == 0) return;
   // Splits: about twelve workgroups per CU (3072) when the batch alone does not give them, at
   // least 256 keys per split, at most 63 splits -- and an odd count.  The kernel's grid runs
   // the splits of one (sequence, KV head) on consecutive workgroups, which the dispatcher deals
@@ -1110,7 +1147,7 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   // with 8 spreads them.  configs[4]'s 512 (sequence, KV head) pairs, splits 1..10: 681, 726,
   // 595, 673, 556, 571, 550, 713, 561, 590 us (5 vs 7 repeated on one box: 560 vs 545).
   int64_t splits = 1;
-  const int64_t pairs = B * Hkv;
+  const int64_t pairs = B * Hkv * ((seq_q * (Hq / Hkv) + 15) / 16);  // x column blocks
   if (max_ctx > 0 && pairs < 3072) {
     const int64_t want = (3072 + pairs - 1) / pairs;
     const int64_t cap = (max_ctx + 255) / 256;
@@ -1119,16 +1156,17 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   }
   c10::DeviceGuard guard(q_ori.device());
   at::Tensor ws;
-  const int64_t ws_bytes = tmo_hip_attn_workspace_bytes(B, Hkv, Hq, D, max_ctx, splits);
+  const int64_t ws_bytes = tmo_hip_cached_kv_attn_workspace_bytes(B, Hkv, Hq, D, seq_q, splits);
   if (ws_bytes > 0)
     ws = at::empty({(ws_bytes + 3) / 4}, q_ori.options().dtype(at::kFloat));
-  const int st = tmo_hip_single_query_cached_kv_attn(
-      q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), vc.data_ptr(),
-      int8 ? ks.data_ptr<float>() : nullptr, int8 ? vs.data_ptr<float>() : nullptr, smode,
-      block_tables.data_ptr<int32_t>(), block_tables.size(1), context_lens.data_ptr<int32_t>(),
-      alibi, out.data_ptr(), out.stride(0), out.stride(1), lse, lse_sb, lse_sh, B, Hq, Hkv, D,
-      NB, BS, max_ctx, window, static_cast<float>(softmax_scale), qdt, cdt, splits,
-      ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(q_ori));
+  const int st = tmo_hip_cached_kv_attn(
+      q.data_ptr(), q_sb, q_ss, q.stride(-2), cu, seq_q, total_q, k_cache.data_ptr(),
+      vc.data_ptr(), int8 ? ks.data_ptr<float>() : nullptr, int8 ? vs.data_ptr<float>() : nullptr,
+      smode, block_tables.data_ptr<int32_t>(), block_tables.size(1),
+      context_lens.data_ptr<int32_t>(), alibi, sink_p, out.data_ptr(), o_sb, o_ss,
+      out.stride(-2), lse, lse_sb, lse_ss, lse_sh, B, Hq, Hkv, D, NB, BS, max_ctx, window,
+      static_cast<float>(softmax_scale), qdt, cdt, splits, ws_bytes > 0 ? ws.data_ptr() : nullptr,
+      ws_bytes, stream_of(q_ori));
   check_status(st, op);
 }
 

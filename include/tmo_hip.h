@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 11
+#define TMO_HIP_ABI_VERSION 12
 
 /* element types */
 enum tmo_dtype {
@@ -411,27 +411,64 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
                                const int32_t* cache_seq_offset, int dtype, void* stream);
 
 /*
- * single_query_cached_kv_attn -- decode attention of one query token per sequence over its
- * paged KV cache: for query head hq of sequence i (KV head hk = hq / (Hq / Hkv)),
- *   s_j = softmax_scale * q . k_j (+ alibi_slopes[i, hq] * (j - (L - 1))),
- *   out = softmax(s) @ V,  lse = ln sum_j exp(s_j),
- * keys j in [max(0, L - 1 - window_left), L) (all when window_left < 0), L = context_lens[i],
- * key j at row j % block_size of page block_tables[i, j / block_size]; pages outside
- * [0, num_blocks) are masked.  Caches [num_blocks, Hkv, block_size, head_size] contiguous:
- * int8 (cache_dtype TMO_DTYPE_I8) with k = code * scale, scale_mode 1: per-token scales
- * [num_blocks, Hkv, block_size], 2: per-channel [Hkv, head_size]; or of q's dtype.
- * q / out: [batch, Hq, head_size] rows with the given strides (last dim contiguous), dtype
- * F32, F16 or BF16; lse (nullable) fp32 at i * lse_stride_seq + hq * lse_stride_head.
+ * cached_kv_attn -- single_query_cached_kv_attn for the query tokens of each sequence over its
+ * paged KV cache.  Sequence i has nq_i query tokens, the last nq_i of its L = context_lens[i]
+ * positions: token s sits at P = L - nq_i + s.  For query head hq of token s (KV head
+ * hk = hq / (Hq / Hkv)),
+ *   s_j = softmax_scale * q . k_j (+ alibi_slopes[i, hq] * (j - P)),
+ *   out = sum_j e^(s_j) v_j / (sum_j e^(s_j) (+ e^sink[hq])),  lse = ln of that denominator,
+ * over keys j in [max(0, P - window_left), P] (from 0 when window_left < 0): causal within
+ * the new tokens.  Key j sits at row j % block_size of page block_tables[i, j / block_size];
+ * pages outside [0, num_blocks) are masked.  A token with no key: out 0, lse = sink or -inf.
+ * Query rows, two forms:
+ *   cu_seq_q null: seq_q tokens per sequence; token s of sequence i at element
+ *     i * q_stride_batch + s * q_stride_token + hq * q_stride_head (q [batch, seq_q, Hq, D]);
+ *   cu_seq_q [batch + 1] int32: sequence i's tokens are rows cu_seq_q[i] .. cu_seq_q[i+1] - 1
+ *     of a [total_q, Hq, D] q, row t at t * q_stride_token (q_stride_batch unused); seq_q is
+ *     an upper bound of the counts (tokens past it are not computed) and rows outside
+ *     [0, total_q) are skipped.
+ * out (q's dtype) and lse (nullable, fp32) are addressed the same way with their own strides.
+ * Caches [num_blocks, Hkv, block_size, head_size] contiguous: int8 (cache_dtype TMO_DTYPE_I8)
+ * with k = code * scale, scale_mode 1: per-token scales [num_blocks, Hkv, block_size], 2:
+ * per-channel [Hkv, head_size]; or of q's dtype (F32, F16 or BF16).  sink (nullable): [Hq]
+ * fp32 natural-log logits.
  * Arithmetic: fp32 accumulation (MFMA with bf16/f16 operands: int8 codes are exact; q and the
  * probabilities are split into two operands when one is not exact), softmax in fp32.
  * splits > 1 divides each sequence's keys over that many workgroups per KV head; it needs
- * `workspace` of at least tmo_hip_attn_workspace_bytes(...) bytes (device memory).
+ * `workspace` of at least tmo_hip_cached_kv_attn_workspace_bytes(...) bytes (device memory).
  * max_context_len <= 0 (negative included) means an unknown maximum: one split per sequence
  * unless `splits` says otherwise; it never limits the keys read.
  * Replaces tmo::torch_api::single_query_cached_kv_attn (reference
- * include/torch_mlu_ops.h:107-130) for one query token per sequence, without q/out
- * quantisation, mask or sink, called by torch_mlu_ops.single_query_cached_kv_attn (reference
- * _ops.py:777-900).
+ * include/torch_mlu_ops.h:107-130) without q/out quantisation or mask, called by
+ * torch_mlu_ops.single_query_cached_kv_attn (reference _ops.py:777-900; q forms :824,
+ * cu_seq_q / max_seq_q :860-861, sink :864).
+ */
+int tmo_hip_cached_kv_attn(const void* q, int64_t q_stride_batch, int64_t q_stride_token,
+                           int64_t q_stride_head, const int32_t* cu_seq_q, int64_t seq_q,
+                           int64_t total_q, const void* k_cache, const void* v_cache,
+                           const float* k_scale, const float* v_scale, int scale_mode,
+                           const int32_t* block_tables, int64_t max_blocks,
+                           const int32_t* context_lens, const float* alibi_slopes,
+                           const float* sink, void* out, int64_t out_stride_batch,
+                           int64_t out_stride_token, int64_t out_stride_head, float* lse,
+                           int64_t lse_stride_batch, int64_t lse_stride_token,
+                           int64_t lse_stride_head, int64_t batch, int64_t num_q_heads,
+                           int64_t num_kv_heads, int64_t head_size, int64_t num_blocks,
+                           int64_t block_size, int64_t max_context_len, int64_t window_left,
+                           float softmax_scale, int q_dtype, int cache_dtype, int64_t splits,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes tmo_hip_cached_kv_attn needs for `splits` with up to seq_q tokens per
+ * sequence (0 when splits <= 1). */
+int64_t tmo_hip_cached_kv_attn_workspace_bytes(int64_t batch, int64_t num_kv_heads,
+                                               int64_t num_q_heads, int64_t head_size,
+                                               int64_t seq_q, int64_t splits);
+
+/*
+ * single_query_cached_kv_attn -- tmo_hip_cached_kv_attn with one query token per sequence
+ * (seq_q 1, no cu_seq_q, no sink): q / out [batch, Hq, head_size] rows with the given strides,
+ * lse (nullable) at i * lse_stride_seq + hq * lse_stride_head.  Replaces the same reference
+ * interface for the decode step (reference include/torch_mlu_ops.h:107-130, _ops.py:777-900).
  */
 int tmo_hip_single_query_cached_kv_attn(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
                                         const void* k_cache, const void* v_cache,
@@ -449,7 +486,8 @@ int tmo_hip_single_query_cached_kv_attn(const void* q, int64_t q_stride_seq, int
                                         int cache_dtype, int64_t splits, void* workspace,
                                         int64_t workspace_bytes, void* stream);
 
-/* Workspace bytes tmo_hip_single_query_cached_kv_attn needs for `splits` (0 when splits <= 1). */
+/* Workspace bytes tmo_hip_single_query_cached_kv_attn needs for `splits` (0 when splits <= 1);
+ * max_context_len is not used. */
 int64_t tmo_hip_attn_workspace_bytes(int64_t batch, int64_t num_kv_heads, int64_t num_q_heads,
                                      int64_t head_size, int64_t max_context_len, int64_t splits);
 

@@ -69,6 +69,12 @@ def lib() -> ctypes.CDLL:
             [c_void_p, c_void_p, c_int, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p,
              c_int64, c_double, c_void_p, c_void_p, c_int]
         L.oracle_single_query_attn.restype = c_int
+        L.oracle_cached_kv_attn.argtypes = [c_void_p, c_int, c_int64, c_int64, c_void_p,
+                                            c_int64, c_int64, c_void_p, c_void_p, c_int] + \
+            [c_int64] * 4 + [c_void_p, c_void_p, c_int, c_void_p, c_int64, c_void_p, c_int64,
+                             c_int64, c_void_p, c_void_p, c_int64, c_double, c_void_p,
+                             c_void_p, c_int]
+        L.oracle_cached_kv_attn.restype = c_int
         for name in ("oracle_f32_to_bf16", "oracle_f32_to_f16", "oracle_f16_to_f32",
                      "oracle_f32_to_e4m3"):
             getattr(L, name).argtypes = [c_void_p, c_void_p, c_int64]
@@ -285,6 +291,52 @@ def single_query_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_s
         _ptr(al), int(window_left), float(softmax_scale), _ptr(out), _ptr(lse),
         nthreads or default_threads())
     _check(rc, "single_query_attn")
+    return out, lse
+
+
+def cached_kv_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scale: float,
+                   k_scale=None, v_scale=None, alibi_slopes=None, window_left: int = -1,
+                   cu_seq_q=None, sink=None, nthreads: Optional[int] = None):
+    """reference _ops.py:777-900 with several query tokens per sequence (decision D12 of
+    tmo_oracle.c), in float64.  q [B, S, Hq, D] (S tokens per sequence), or [T, Hq, D] with
+    cu_seq_q [B + 1] (rows cu_seq_q[i] .. cu_seq_q[i + 1] - 1 are sequence i's), or [B, Hq, D]
+    (one token each); token s of a sequence with nq tokens and L keys sits at position
+    L - nq + s.  sink [Hq] or None.  Returns (out, lse) float64 of q's leading shape:
+    [B, S, Hq, D] / [B, S, Hq] for 4-D q, [T, Hq, D] / [T, Hq] otherwise; rows that no
+    sequence of cu_seq_q holds are NaN."""
+    four = q.dim() == 4
+    if four:
+        B, S = q.shape[:2]
+        q = q.reshape(B * S, q.shape[2], q.shape[3])
+    else:
+        B = context_lens.shape[0]
+        S = 1
+    assert q.stride(-1) == 1 and k_cache.is_contiguous() and v_cache.is_contiguous()
+    T, Hq, D = q.shape
+    NB, Hkv, BS, _ = k_cache.shape
+    cdt = _DT[k_cache.dtype]
+    mode = 0
+    ks = vs = None
+    if k_cache.dtype == torch.int8:
+        ks = k_scale.to(torch.float32).contiguous()
+        vs = v_scale.to(torch.float32).contiguous()
+        mode = 2 if ks.dim() == 2 else 1
+    bt = block_tables.to(torch.int32).contiguous()
+    lens = context_lens.to(torch.int32).contiguous()
+    cu = cu_seq_q.to(torch.int32).contiguous() if cu_seq_q is not None else None
+    assert cu is None or (not four and cu.numel() == B + 1)
+    al = alibi_slopes.to(torch.float32).contiguous() if alibi_slopes is not None else None
+    sk = sink.to(torch.float32).contiguous() if sink is not None else None
+    out = torch.full((T, Hq, D), float("nan"), dtype=torch.float64)
+    lse = torch.full((T, Hq), float("nan"), dtype=torch.float64)
+    rc = lib().oracle_cached_kv_attn(
+        _ptr(q), _DT[q.dtype], q.stride(0), q.stride(1), _ptr(cu), S, T, _ptr(k_cache),
+        _ptr(v_cache), cdt, NB, Hkv, BS, D, _ptr(ks), _ptr(vs), mode, _ptr(bt), bt.shape[1],
+        _ptr(lens), B, Hq, _ptr(al), _ptr(sk), int(window_left), float(softmax_scale),
+        _ptr(out), _ptr(lse), nthreads or default_threads())
+    _check(rc, "cached_kv_attn")
+    if four:
+        return out.reshape(B, S, Hq, D), lse.reshape(B, S, Hq)
     return out, lse
 
 

@@ -60,12 +60,17 @@
  *       or per group of D / group_num channels (scale [max_batch, H, cache_len, group_num]):
  *       int8 as D1-D3, fp8 e4m3fn with scale = RN(amax / 448), codes e4m3fn_RNE(clip(RN(x /
  *       scale), -448, 448)) and an all-zero group giving scale 0 and codes 0 (_ops.py:1728-1745).
- *   D12 single_query_cached_kv_attn (_ops.py:777-900), one query token per sequence: the
- *       docstring math in double with k = code * scale exact; alibi adds
- *       slope * (j - (L - 1)) (key position relative to the query, the usual decode form;
- *       create_alibi is not defined in the reference); lse = log sum exp of the logits the
- *       softmax uses (the docstring writes logsumexp(qk), which equals it without alibi); a
- *       key on a page outside [0, NB) is masked; an empty window gives out 0, lse -inf.
+ *   D12 single_query_cached_kv_attn (_ops.py:777-900): the docstring math in double with
+ *       k = code * scale exact.  A sequence's nq query tokens (q [batch, seq_q, ...] or rows
+ *       cu_seq_q[i] .. cu_seq_q[i+1] - 1 of a [total_q, ...] q, _ops.py:824, 860-861) are its
+ *       last nq positions: token s sits at position P = L - nq + s and sees keys j <= P
+ *       (causal within the new tokens; one token: P = L - 1), and with a left window keys
+ *       j >= P - window_left; alibi adds slope * (j - P) (key position relative to the
+ *       query, the usual decode form; create_alibi is not defined in the reference); the
+ *       sink (_ops.py:864, one logit per query head) joins the softmax denominator only:
+ *       out = sum_j e^(s_j) v_j / (sum_j e^(s_j) + e^sink); lse = log of that denominator
+ *       (the docstring writes logsumexp(qk), which equals it without alibi and sink); a key
+ *       on a page outside [0, NB) is masked; no key and no sink gives out 0, lse -inf.
  *   D9  offline (static-scale) quantisation divides: code = clip(RNE(RN(fp32(x) / s)), -128, 127)
  *       for int8, fp8 = e4m3fn_RNE(clip(RN(fp32(x) / s), -448, 448)), s the fp32 per-channel
  *       scale or the per-tensor scalar rounded to fp32 (_ops.py:1652-1670; the division is
@@ -967,13 +972,14 @@ int oracle_scaled_quantize_per_token(const void* x, int dtype, int64_t n0, int64
 /* ------------------------------------------------------------------ single_query_cached_kv_attn (D12) */
 
 typedef struct {
-    const void* q; int q_dtype; int64_t q_sb, q_sh;      /* q [B, Hq, D], element strides */
+    const void* q; int q_dtype; int64_t q_st, q_sh;      /* q rows [T, Hq, D], element strides */
+    const int32_t* cu; int64_t S, T;                     /* cu_seq_q [B + 1], or S tokens each */
     const void* kc; const void* vc; int c_dtype;         /* caches [NB, Hkv, BS, D] */
-    int64_t NB, Hkv, BS, D, Hq, MB;
+    int64_t NB, Hkv, BS, D, Hq, MB, B;
     const float* ks; const float* vs; int smode;         /* 0 none, 1 per token, 2 per channel */
     const int32_t* bt; const int32_t* lens;
-    const float* alibi; int64_t window; double scale;
-    double* out; double* lse;
+    const float* alibi; const float* sink; int64_t window; double scale;
+    double* out; double* lse;                            /* [T, Hq, D], [T, Hq] */
 } sqa_ctx;
 
 static double cache_val(const sqa_ctx* c, const void* base, const float* sc, int64_t blk,
@@ -988,32 +994,53 @@ static double cache_val(const sqa_ctx* c, const void* base, const float* sc, int
     return (double)load_elem(base, e, c->c_dtype);
 }
 
+/* The sequence of query row t and the row's token index in it; -1 when no sequence holds t. */
+static int64_t sqa_seq(const sqa_ctx* c, int64_t t, int64_t* s, int64_t* nq) {
+    if (!c->cu) {
+        *s = t % c->S;
+        *nq = c->S;
+        return t / c->S;
+    }
+    for (int64_t i = 0; i < c->B; ++i)
+        if (c->cu[i] <= t && t < c->cu[i + 1]) {
+            *s = t - c->cu[i];
+            *nq = c->cu[i + 1] - c->cu[i];
+            return i;
+        }
+    return -1;
+}
+
 static void sqa_range(void* p, int64_t lo, int64_t hi) {
     sqa_ctx* c = (sqa_ctx*)p;
     int64_t g = c->Hq / c->Hkv;
     double* s = (double*)malloc((size_t)(c->MB * c->BS > 0 ? c->MB * c->BS : 1) * sizeof(double));
-    for (int64_t w = lo; w < hi; ++w) {             /* w = i * Hq + hq */
-        int64_t i = w / c->Hq, hq = w % c->Hq, hk = hq / g;
+    for (int64_t w = lo; w < hi; ++w) {             /* w = t * Hq + hq */
+        int64_t t = w / c->Hq, hq = w % c->Hq, hk = hq / g, tok, nq;
+        int64_t i = sqa_seq(c, t, &tok, &nq);
+        if (i < 0) continue;                        /* a row no sequence holds: untouched */
         int64_t L = c->lens[i];
         if (L > c->MB * c->BS) L = c->MB * c->BS;
-        int64_t j0 = c->window >= 0 && L - 1 - c->window > 0 ? L - 1 - c->window : 0;
+        const int64_t P = L - nq + tok;             /* the token's position: keys j <= P */
+        const int64_t jend = P + 1 < L ? P + 1 : L;
+        int64_t j0 = c->window >= 0 && P - c->window > 0 ? P - c->window : 0;
         double* o = c->out + w * c->D;
         for (int64_t d = 0; d < c->D; ++d) o[d] = 0.0;
-        double m = -INFINITY;
-        for (int64_t j = j0; j < L; ++j) {
+        double m = c->sink ? (double)c->sink[hq] : -INFINITY;
+        for (int64_t j = j0; j < jend; ++j) {
             int64_t blk = c->bt[i * c->MB + j / c->BS], row = j % c->BS;
             if (blk < 0 || blk >= c->NB) { s[j] = -INFINITY; continue; }   /* missing page: masked */
             double acc = 0.0;
             for (int64_t d = 0; d < c->D; ++d)
-                acc += (double)load_elem(c->q, i * c->q_sb + hq * c->q_sh + d, c->q_dtype) *
+                acc += (double)load_elem(c->q, t * c->q_st + hq * c->q_sh + d, c->q_dtype) *
                        cache_val(c, c->kc, c->ks, blk, hk, row, d);
             s[j] = c->scale * acc;
-            if (c->alibi) s[j] += (double)c->alibi[i * c->Hq + hq] * (double)(j - (L - 1));
+            if (c->alibi) s[j] += (double)c->alibi[i * c->Hq + hq] * (double)(j - P);
             if (s[j] > m) m = s[j];
         }
         double l = 0.0;
         if (m > -INFINITY) {
-            for (int64_t j = j0; j < L; ++j) {
+            if (c->sink) l = exp((double)c->sink[hq] - m);
+            for (int64_t j = j0; j < jend; ++j) {
                 if (s[j] == -INFINITY) continue;
                 double pj = exp(s[j] - m);
                 l += pj;
@@ -1027,13 +1054,40 @@ static void sqa_range(void* p, int64_t lo, int64_t hi) {
     free(s);
 }
 
-/* _ops.py:777-900, single_query_cached_kv_attn for one query token per sequence, in double:
- *   s_j = softmax_scale * sum_d q_d k_jd (+ alibi_slope[i, hq] * (j - (L - 1))),
- *   out = softmax(s) @ V, lse = log sum_j exp(s_j)     (natural log, of the logits used)
- * over keys j in [max(0, L - 1 - window_left), L) (all of [0, L) when window_left < 0), key j
- * at row j % BS of page block_tables[i, j / BS]; k_jd = code * scale exactly (per token
- * [NB, Hkv, BS] or per channel [Hkv, D]) for int8 caches, the stored value otherwise; query
- * head hq reads KV head hq / (Hq / Hkv).  L = 0: out 0, lse -inf.  out [B, Hq, D], lse [B, Hq]. */
+/* _ops.py:777-900, single_query_cached_kv_attn in double (D12):
+ *   s_j = softmax_scale * sum_d q_d k_jd (+ alibi_slope[i, hq] * (j - P)),
+ *   out = sum_j e^(s_j) v_j / (sum_j e^(s_j) (+ e^sink[hq])),  lse = log of that denominator,
+ * for query token s of sequence i at position P = L - nq + s (L = context_lens[i], nq its
+ * query tokens) over keys j in [max(0, P - window_left), min(P, L - 1)] (all of [0, P] when
+ * window_left < 0), key j at row j % BS of page block_tables[i, j / BS]; k_jd = code * scale
+ * exactly (per token [NB, Hkv, BS] or per channel [Hkv, D]) for int8 caches, the stored value
+ * otherwise; query head hq reads KV head hq / (Hq / Hkv).  Query rows: q [T, Hq, D] with row t
+ * at t * q_st; cu_seq_q null: S tokens per sequence, sequence i's at rows i S .. i S + S - 1
+ * (T = B S); else rows cu_seq_q[i] .. cu_seq_q[i + 1] - 1 (rows of no sequence untouched).
+ * No key: out 0, lse = sink or -inf.  out [T, Hq, D], lse [T, Hq]. */
+int oracle_cached_kv_attn(const void* q, int q_dtype, int64_t q_st, int64_t q_sh,
+                          const int32_t* cu_seq_q, int64_t S, int64_t T,
+                          const void* k_cache, const void* v_cache, int cache_dtype,
+                          int64_t NB, int64_t Hkv, int64_t BS, int64_t D,
+                          const float* k_scale, const float* v_scale, int scale_mode,
+                          const int32_t* block_tables, int64_t max_blocks,
+                          const int32_t* context_lens, int64_t B, int64_t Hq,
+                          const float* alibi, const float* sink, int64_t window_left,
+                          double softmax_scale, double* out, double* lse, int nthreads) {
+    if (elem_size(q_dtype) == 0 || q_dtype == DT_I8 || elem_size(cache_dtype) == 0) return -2;
+    if (cache_dtype == DT_I8 && scale_mode != 1 && scale_mode != 2) return -3;
+    if (B < 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || BS <= 0 || D <= 0 || max_blocks < 0 ||
+        T < 0 || (!cu_seq_q && (S <= 0 || T != B * S)))
+        return -1;
+    sqa_ctx c = {q, q_dtype, q_st, q_sh, cu_seq_q, S, T, k_cache, v_cache, cache_dtype, NB, Hkv,
+                 BS, D, Hq, max_blocks, B, k_scale, v_scale, cache_dtype == DT_I8 ? scale_mode : 0,
+                 block_tables, context_lens, alibi, sink, window_left, softmax_scale, out, lse};
+    parallel_for(T * Hq, nthreads, sqa_range, &c);
+    return 0;
+}
+
+/* One query token per sequence (q [B, Hq, D], row i at i * q_sb): oracle_cached_kv_attn with
+ * S = 1 and no sink.  out [B, Hq, D], lse [B, Hq]. */
 int oracle_single_query_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                              const void* k_cache, const void* v_cache, int cache_dtype,
                              int64_t NB, int64_t Hkv, int64_t BS, int64_t D,
@@ -1042,12 +1096,8 @@ int oracle_single_query_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q
                              const int32_t* context_lens, int64_t B, int64_t Hq,
                              const float* alibi, int64_t window_left, double softmax_scale,
                              double* out, double* lse, int nthreads) {
-    if (elem_size(q_dtype) == 0 || q_dtype == DT_I8 || elem_size(cache_dtype) == 0) return -2;
-    if (cache_dtype == DT_I8 && scale_mode != 1 && scale_mode != 2) return -3;
-    if (B < 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || BS <= 0 || D <= 0 || max_blocks < 0) return -1;
-    sqa_ctx c = {q, q_dtype, q_sb, q_sh, k_cache, v_cache, cache_dtype, NB, Hkv, BS, D, Hq,
-                 max_blocks, k_scale, v_scale, cache_dtype == DT_I8 ? scale_mode : 0,
-                 block_tables, context_lens, alibi, window_left, softmax_scale, out, lse};
-    parallel_for(B * Hq, nthreads, sqa_range, &c);
-    return 0;
+    return oracle_cached_kv_attn(q, q_dtype, q_sb, q_sh, NULL, 1, B < 0 ? 0 : B, k_cache,
+                                 v_cache, cache_dtype, NB, Hkv, BS, D, k_scale, v_scale,
+                                 scale_mode, block_tables, max_blocks, context_lens, B, Hq,
+                                 alibi, NULL, window_left, softmax_scale, out, lse, nthreads);
 }

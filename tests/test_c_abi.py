@@ -60,6 +60,11 @@ def lib():
         [ctypes.c_float, INT, INT, I64, P, I64, P]
     L.tmo_hip_attn_workspace_bytes.argtypes = [I64] * 6
     L.tmo_hip_attn_workspace_bytes.restype = I64
+    L.tmo_hip_cached_kv_attn.argtypes = [P, I64, I64, I64, P, I64, I64, P, P, P, P, INT, P, I64,
+                                         P, P, P, P, I64, I64, I64, P, I64, I64, I64] + \
+        [I64] * 8 + [ctypes.c_float, INT, INT, I64, P, I64, P]
+    L.tmo_hip_cached_kv_attn_workspace_bytes.argtypes = [I64] * 6
+    L.tmo_hip_cached_kv_attn_workspace_bytes.restype = I64
     return L
 
 
@@ -74,7 +79,8 @@ def test_every_declared_symbol_is_exported(lib):
                           "tmo_hip_fused_rope_linear", "tmo_hip_reshape_linear_cache", "tmo_hip_quant_to_linear_cache",
                           "tmo_hip_offline_quant_to_linear_cache",
                           "tmo_hip_dequant_from_linear_cache", "tmo_hip_reshape_from_cache",
-                          "tmo_hip_single_query_cached_kv_attn", "tmo_hip_attn_workspace_bytes"}
+                          "tmo_hip_single_query_cached_kv_attn", "tmo_hip_attn_workspace_bytes",
+                          "tmo_hip_cached_kv_attn", "tmo_hip_cached_kv_attn_workspace_bytes"}
     for n in names:
         assert hasattr(lib, n), n
 
@@ -337,4 +343,29 @@ def test_attention_validation(lib):
     assert call(splits=4, ws=FAKE, wsb=need - 4) == EINVAL
     assert call(B=0) == 0
     assert call(B=0, mctx=-1) == 0                 # negative max_context_len: unknown, like 0
+
+
+def test_multi_token_attention_validation(lib):
+    def call(q=FAKE, cu=None, S=4, T=0, B=2, Hq=8, Hkv=2, D=128, splits=1, ws=None, wsb=0,
+             qdt=2, cdt=3, qss=128 * 8, oss=128 * 8, sink=None):
+        return lib.tmo_hip_cached_kv_attn(
+            q, 4 * 1024, qss, 128, cu, S, T, FAKE, FAKE, FAKE, FAKE, 1, FAKE, 4, FAKE, None,
+            sink, FAKE, 4 * 1024, oss, 128, None, 0, 0, 0, B, Hq, Hkv, D, 16, 16, 64, -1, 0.1,
+            qdt, cdt, splits, ws, wsb, None)
+    assert call(qdt=3) == EDTYPE
+    assert call(q=None) == EINVAL
+    assert call(S=-1) == EINVAL
+    assert call(qss=-1) == EINVAL and call(oss=-1) == EINVAL
+    assert call(cu=FAKE, T=-1) == EINVAL           # cu_seq_q with a negative row count
+    assert call(S=2 ** 31 // 8) == EINVAL          # seq_q * heads beyond 32 bits
+    assert call(splits=3) == EINVAL                # splits without a workspace
+    # workspace [batch, kv_heads, splits, seq_q * group, head_size + 2] floats
+    need = lib.tmo_hip_cached_kv_attn_workspace_bytes(2, 2, 8, 128, 4, 3)
+    assert need == 2 * 2 * 3 * 4 * 4 * 130 * 4
+    assert lib.tmo_hip_cached_kv_attn_workspace_bytes(2, 2, 8, 128, 1, 3) == \
+        lib.tmo_hip_attn_workspace_bytes(2, 2, 8, 128, 999, 3)
+    assert lib.tmo_hip_cached_kv_attn_workspace_bytes(2, 2, 8, 128, 0, 3) == 0
+    assert call(splits=3, ws=FAKE, wsb=need - 4) == EINVAL
+    assert call(B=0) == 0 and call(S=0) == 0       # nothing to compute
+    assert call(S=0, cu=FAKE, T=5, sink=FAKE) == 0
 

@@ -1211,3 +1211,131 @@ def test_attn_closed_forms(ref):
     out, _ = ref.single_query_attn(same.q, same.k_cache, same.v_cache, same.block_tables,
                                    same.context_lens, 1.0, alibi_slopes=al)
     assert torch.allclose(out[0], V[-1].expand(2, 16), rtol=0, atol=1e-300)
+
+
+def torch_attn_mq(case, q, scale, window=-1, cu=None, sink=None):
+    """_ops.py:786-800 for several query tokens per sequence, in float64 by torch: every
+    sequence's keys dequantised through its block table, a [heads, tokens, keys] logit matrix
+    with query token s of nq at position P = L - nq + s seeing keys j in [P - window, P], ALiBi
+    slope * (j - P), the sink as an extra logit column whose value row is zero.  q [B, S, Hq,
+    D], or [T, Hq, D] with cu [B + 1]; returns out / lse shaped like q's leading dims (rows of
+    no sequence NaN)."""
+    kc, vc, bt = case.k_cache, case.v_cache, case.block_tables
+    NB, Hkv, BS, D = kc.shape
+    B = case.context_lens.shape[0]
+    Hq = q.shape[-2]
+    g = Hq // Hkv
+    qf = q.reshape(-1, Hq, D).double()
+    T = qf.shape[0]
+    out = torch.full((T, Hq, D), float("nan"), dtype=torch.float64)
+    lse = torch.full((T, Hq), float("nan"), dtype=torch.float64)
+    for i in range(B):
+        r0, nq = (i * q.shape[1], q.shape[1]) if cu is None else (int(cu[i]), int(cu[i + 1] - cu[i]))
+        if nq <= 0:
+            continue
+        L = min(int(case.context_lens[i]), bt.shape[1] * BS)
+        j = torch.arange(max(L, 0))
+        blk, row = bt[i, j // BS].long(), j % BS
+        keep = (blk >= 0) & (blk < NB)
+        K = torch.zeros(j.numel(), Hkv, D, dtype=torch.float64)
+        V = torch.zeros_like(K)
+        b, r = blk[keep], row[keep]
+        K[keep], V[keep] = kc[b, :, r].double(), vc[b, :, r].double()
+        if case.k_scale is not None:
+            if case.k_scale.dim() == 3:
+                K[keep] *= case.k_scale[b, :, r].double()[..., None]
+                V[keep] *= case.v_scale[b, :, r].double()[..., None]
+            else:
+                K[keep] *= case.k_scale.double()[None]
+                V[keep] *= case.v_scale.double()[None]
+        K, V = K.repeat_interleave(g, dim=1), V.repeat_interleave(g, dim=1)   # [L, Hq, D]
+        s = torch.einsum("thd,jhd->htj", qf[r0:r0 + nq], K) * scale             # [Hq, nq, L]
+        P = L - nq + torch.arange(nq)
+        if case.alibi is not None:
+            s = s + case.alibi[i].double()[:, None, None] * (j[None, :] - P[:, None]).double()[None]
+        ok = (j[None, :] <= P[:, None]) & keep[None, :]
+        if window >= 0:
+            ok &= j[None, :] >= P[:, None] - window
+        s = s.masked_fill(~ok[None], float("-inf"))
+        if sink is not None:
+            s = torch.cat([s, sink.double()[:, None, None].expand(Hq, nq, 1)], dim=-1)
+            V = torch.cat([V, torch.zeros(1, Hq, D, dtype=torch.float64)], dim=0)
+        l = torch.logsumexp(s, dim=-1)                                           # [Hq, nq]
+        p = torch.exp(s - l[..., None]).nan_to_num(0.0)
+        out[r0:r0 + nq] = torch.einsum("htj,jhd->thd", p, V)
+        lse[r0:r0 + nq] = l.transpose(0, 1)
+    if cu is None:
+        return out.reshape(q.shape[:2] + (Hq, D)), lse.reshape(q.shape[:2] + (Hq,))
+    return out, lse
+
+
+@pytest.mark.parametrize("kv", ["int8_token", "int8_channel", "plain"])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_attn_multi_token_matches_torch_float64(ref, dtype, kv):
+    """Several query tokens per sequence (4-D q, and 3-D q with cu_seq_q, ragged with an empty
+    sequence), with windows, ALiBi, a sink and a missing page, against torch in float64."""
+    case = W.attn_case(dtype, 11, kv=kv, Hq=8, Hkv=2, D=64, max_ctx=70)
+    case.block_tables[2, 1] = -1
+    q4 = W.attn_queries(dtype, 12, B=5, Hq=8, D=64, S=3)
+    q3, cu = W.attn_queries(dtype, 13, B=5, Hq=8, D=64, counts=[4, 2, 0, 7, 1])
+    sink = torch.tensor([0.5, -1.0, 3.0, 0.0, -20.0, 1.5, 2.0, -0.25])
+    for window, alibi, sk in ((-1, False, None), (9, False, sink), (-1, True, sink), (0, True, None)):
+        case.alibi = (0.5 ** torch.arange(1, 9, dtype=torch.float32)).repeat(5, 1) if alibi else None
+        for q, c in ((q4, None), (q3, cu)):
+            out, lse = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables,
+                                          case.context_lens, 0.125, case.k_scale, case.v_scale,
+                                          case.alibi, window, cu_seq_q=c, sink=sk)
+            want, wlse = torch_attn_mq(case, q, 0.125, window, c, sk)
+            assert torch.allclose(out, want, rtol=1e-12, atol=1e-12)
+            assert torch.allclose(lse, wlse, rtol=1e-12, atol=1e-12)
+
+
+def test_attn_multi_token_forms(ref):
+    """Token s of nq equals one query token against the first L - nq + s + 1 keys (the causal
+    rule), bit for bit; ragged cu_seq_q rows equal the per-sequence 4-D calls; the sink scales
+    the output by Z / (Z + e^sink) and adds e^sink under the lse's log; a token with no key
+    gives out 0 and lse = sink; rows of no sequence stay untouched."""
+    case = W.attn_case(torch.bfloat16, 21, kv="int8_token", B=4, Hq=8, Hkv=2, D=32, max_ctx=50,
+                       alibi=True)
+    S = 4
+    q4 = W.attn_queries(torch.bfloat16, 22, B=4, Hq=8, D=32, S=S)
+    for window in (-1, 5):
+        out, lse = ref.cached_kv_attn(q4, case.k_cache, case.v_cache, case.block_tables,
+                                      case.context_lens, 0.2, case.k_scale, case.v_scale,
+                                      case.alibi, window)
+        for s in range(S):
+            lens_s = (case.context_lens - S + s + 1).clamp(min=0)
+            o1, l1 = ref.single_query_attn(q4[:, s], case.k_cache, case.v_cache,
+                                           case.block_tables, lens_s, 0.2, case.k_scale,
+                                           case.v_scale, case.alibi, window)
+            assert torch.equal(out[:, s], o1) and torch.equal(lse[:, s], l1)
+    # sequence 1 holds one key: its first three tokens see none
+    assert (out[1, :3] == 0).all() and (lse[1, :3] == float("-inf")).all()
+    sink = torch.linspace(-3.0, 4.0, 8)
+    o_s, l_s = ref.cached_kv_attn(q4, case.k_cache, case.v_cache, case.block_tables,
+                                  case.context_lens, 0.2, case.k_scale, case.v_scale, case.alibi,
+                                  sink=sink)
+    o_0, l_0 = ref.cached_kv_attn(q4, case.k_cache, case.v_cache, case.block_tables,
+                                  case.context_lens, 0.2, case.k_scale, case.v_scale, case.alibi)
+    live = l_0 > float("-inf")
+    sk = sink.double().expand_as(l_0)
+    assert torch.allclose(l_s[live], torch.logaddexp(l_0, sk)[live], rtol=1e-14)
+    assert torch.allclose(o_s[live], (o_0 * torch.exp(l_0 - l_s)[..., None])[live], rtol=1e-13,
+                          atol=1e-15)
+    assert (o_s[~live] == 0).all() and torch.equal(l_s[~live], sk[~live])
+    counts = [3, 0, 5, 1]
+    q3, cu = W.attn_queries(torch.bfloat16, 23, B=4, Hq=8, D=32, counts=counts)
+    q3 = torch.cat([q3, q3[:2]])                                  # two rows of no sequence
+    out, lse = ref.cached_kv_attn(q3, case.k_cache, case.v_cache, case.block_tables,
+                                  case.context_lens, 0.2, case.k_scale, case.v_scale,
+                                  case.alibi, 7, cu_seq_q=cu, sink=sink)
+    for i, n in enumerate(counts):
+        if n == 0:
+            continue
+        a, b = int(cu[i]), int(cu[i + 1])
+        o1, l1 = ref.cached_kv_attn(q3[a:b][None], case.k_cache, case.v_cache,
+                                    case.block_tables[i:i + 1], case.context_lens[i:i + 1], 0.2,
+                                    case.k_scale, case.v_scale, case.alibi[i:i + 1], 7,
+                                    sink=sink)
+        assert torch.equal(out[a:b], o1[0]) and torch.equal(lse[a:b], l1[0])
+    assert out[-2:].isnan().all() and lse[-2:].isnan().all()

@@ -378,3 +378,17 @@ def attn_case(dtype, seed: int, kv: str = "int8_token", B: int = 5, Hq: int = 8,
         vc = torch.randn(NB, Hkv, BS, D, generator=g).to(dtype)
     al = (0.5 ** torch.arange(1, Hq + 1, dtype=torch.float32)).repeat(B, 1) if alibi else None
     return AttnCase(q, kc, vc, ks, vs, bt, lens, al)
+
+
+def attn_queries(dtype, seed: int, B: int, Hq: int, D: int, S: Optional[int] = None,
+                 counts: Optional[list] = None):
+    """Query tokens for several per sequence, q ~ N(0, 1) in `dtype`: S each -> q [B, S, Hq,
+    D] (the reference's 4-D form); or `counts[i]` for sequence i -> (q [T, Hq, D], cu_seq_q
+    [B + 1] int32), T = sum(counts) (the 3-D form with cu_seq_q)."""
+    g = torch.Generator().manual_seed(seed)
+    if counts is None:
+        return torch.randn(B, S, Hq, D, generator=g).to(dtype)
+    assert len(counts) == B
+    cu = torch.zeros(B + 1, dtype=torch.int32)
+    cu[1:] = torch.tensor(counts, dtype=torch.int32).cumsum(0)
+    return torch.randn(int(cu[-1]), Hq, D, generator=g).to(dtype), cu
