@@ -6,12 +6,14 @@
 //
 // for query token s of a sequence with nq tokens and L keys at position P = L - nq + s (one
 // token: P = L - 1), over keys j in [max(0, P - window_left), P]; key j at row j % BS of page
-// block_tables[i, j / BS] (pages outside [0, NB) are masked); query head hq reads KV head
-// hq / (Hq / Hkv).  Caches are int8 with per-token [NB, Hkv, BS] or per-channel [Hkv, D] fp32
-// scales (k = code * scale), or of q's dtype.
+// block_tables[i, j / BS] (pages outside [0, NB) are masked): k_j its first D channels, v_j
+// the first Dv of the V cache's row, or of the K row when both live in one cache; query head
+// hq reads KV head hq / (Hq / Hkv).  Caches are int8 with fp32 scales (k = code * scale) per
+// token [NB, Hkv, BS] (strided in the first two dims), per channel [Hkv, D], or per group
+// (K [NB, Hkv, BS, D / 32], V [NB, Hkv, BS / 32, Dv]), or of q's dtype.
 //
-// MFMA path (bf16 or f16 operands, fp32 accumulation; head_size 64 / 128 / 256, block_size a
-// multiple of 16): the query columns of a (sequence, KV head) are its (token, query head)
+// MFMA path (bf16 or f16 operands, fp32 accumulation; K and V head sizes and cache rows all 64
+// / 128 / 256, block_size a multiple of 16, per-token or per-channel scales): the query columns of a (sequence, KV head) are its (token, query head)
 // pairs, c = s * g + head-in-group (g = Hq / Hkv), in blocks of 16.  A workgroup of four
 // wavefronts owns one (sequence, KV head, split, column block) and its wavefronts take every
 // fourth 16-token tile.  Per tile:
@@ -37,7 +39,7 @@
 // The four wavefronts combine through LDS; with more than one split per (sequence, KV head)
 // the partials (max, sum, normalised row) go to a caller-provided workspace and a combine
 // kernel merges them.  A generic kernel (one wavefront per (query token, query head), VALU)
-// serves every other shape and dtype.
+// serves every other shape, dtype and scale layout.
 #include "tmo_device.h"
 
 namespace tmo {
@@ -63,10 +65,12 @@ struct AttnParams {
   int64_t total_q;               // q rows with cu: rows outside [0, total_q) are skipped
   const float* sink;             // [Hq] natural-log logits, or null
   const void* kc;
-  const void* vc;                // caches [NB, Hkv, BS, D] contiguous
+  const void* vc;                // caches [NB, Hkv, BS, k_row / v_row] contiguous
+  int64_t k_row, v_row;          // cache row lengths (elements)
   const float* ks;
   const float* vs;
-  int32_t smode;                 // 0 plain caches, 1 per-token scales, 2 per-channel scales
+  int32_t smode;                 // 0 plain caches, 1 per token, 2 per channel, 3 per group
+  int64_t ks_sb, ks_sh, vs_sb, vs_sh;  // per-token scale strides (page, head)
   const int32_t* bt;
   int64_t max_blocks;
   const int32_t* lens;
@@ -77,7 +81,7 @@ struct AttnParams {
   int64_t o_sb, o_ss, o_sh;
   float* lse;                    // null when not requested
   int64_t lse_sb, lse_ss, lse_sh;
-  int32_t B, Hq, Hkv, g, D, BS;
+  int32_t B, Hq, Hkv, g, D, Dv, BS;  // D: query / key head size, Dv: value head size
   int32_t bs_shift;              // log2(BS) when BS is a power of two, else -1
   int64_t NB;
   int32_t q_dtype;               // TMO_DTYPE_*
@@ -85,7 +89,7 @@ struct AttnParams {
   int32_t c_dtype;               // cache TMO_DTYPE_*
   int32_t splits;
   int64_t split_tokens;          // multiple of 64
-  float* ws;                     // [B, Hkv, splits, ncols, D + 2] when splits > 1
+  float* ws;                     // [B, Hkv, splits, ncols, Dv + 2] when splits > 1
 };
 
 // ------------------------------------------------------------------------------ small helpers
@@ -451,9 +455,9 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
 #pragma unroll
     for (int e = 0; e < 4; ++e) r.ksc[e] = r.vsc[e] = 1.0f;
     if (kKind == 0 && p.smode == 1) {
-      const int64_t so = (blk * p.Hkv + hk) * p.BS + row0 + 4 * grp;
-      const u32x4 a = *reinterpret_cast<const u32x4*>(p.ks + so);
-      const u32x4 b = *reinterpret_cast<const u32x4*>(p.vs + so);
+      const int32_t so = row0 + 4 * grp;
+      const u32x4 a = *reinterpret_cast<const u32x4*>(p.ks + (blk * p.ks_sb + hk * p.ks_sh) + so);
+      const u32x4 b = *reinterpret_cast<const u32x4*>(p.vs + (blk * p.vs_sb + hk * p.vs_sh) + so);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         r.ksc[e] = __uint_as_float(a[e]);
@@ -686,8 +690,8 @@ __global__ __launch_bounds__(256) void attn_combine(AttnParams p) {
   if (!token_valid(p, sq, tok)) return;
   const int hk = hq / p.g;
   const int c = tok * p.g + (hq - hk * p.g);
-  const int64_t stride = (int64_t)p.ncols * (p.D + 2);
-  const float* base = p.ws + ((i * p.Hkv + hk) * p.splits * (int64_t)p.ncols + c) * (p.D + 2);
+  const int64_t stride = (int64_t)p.ncols * (p.Dv + 2);
+  const float* base = p.ws + ((i * p.Hkv + hk) * p.splits * (int64_t)p.ncols + c) * (p.Dv + 2);
   // splits past the sequence's keys wrote nothing (the main kernel returned early): the
   // non-empty splits are a prefix, of length `live`
   const Range r0 = token_range(p, sq, 0);
@@ -716,7 +720,7 @@ __global__ __launch_bounds__(256) void attn_combine(AttnParams p) {
   const float inv = finish(p, hq, mx, lt, &lse_v);
   const int64_t qrow = sq.row0 + tok;
   const int64_t orow = i * p.o_sb + qrow * p.o_ss + (int64_t)hq * p.o_sh;
-  for (int d0 = 0; d0 < p.D; d0 += kWave) {
+  for (int d0 = 0; d0 < p.Dv; d0 += kWave) {
     const int d = d0 + lane;
     float o = 0.0f;
     for (int s0 = 0; s0 < live; s0 += kWave) {
@@ -726,35 +730,53 @@ __global__ __launch_bounds__(256) void attn_combine(AttnParams p) {
       const int n = live - s0 < kWave ? live - s0 : kWave;
       for (int k = 0; k < n; ++k) {
         const float wk = __shfl(wgt, k, kWave);
-        if (wk != 0.0f && d < p.D) o += base[(s0 + k) * stride + 2 + d] * wk;
+        if (wk != 0.0f && d < p.Dv) o += base[(s0 + k) * stride + 2 + d] * wk;
       }
     }
-    if (d < p.D) store_out(p, orow + d, o * inv);
+    if (d < p.Dv) store_out(p, orow + d, o * inv);
   }
   if (lane == 0 && p.lse) p.lse[i * p.lse_sb + qrow * p.lse_ss + (int64_t)hq * p.lse_sh] = lse_v;
 }
 
 // ------------------------------------------------------------------------------ generic kernel
 
-__device__ __forceinline__ float cache_value(const AttnParams& p, const void* base, const float* sc,
-                                             int64_t blk, int hk, int64_t row, int d,
-                                             int cache_dtype) {
-  const int64_t e = ((blk * p.Hkv + hk) * p.BS + row) * p.D + d;
+__device__ __forceinline__ float plain_value(const void* base, int64_t e, int cache_dtype) {
   switch (cache_dtype) {
-    case TMO_DTYPE_I8: {
-      const float code = (float)static_cast<const int8_t*>(base)[e];
-      if (p.smode == 1) return code * sc[(blk * p.Hkv + hk) * p.BS + row];
-      return code * sc[(int64_t)hk * p.D + d];
-    }
     case TMO_DTYPE_BF16: return load1(BF16{}, base, e);
     case TMO_DTYPE_F16: return load1(F16{}, base, e);
     default: return load1(F32{}, base, e);
   }
 }
 
+// Key channel d of row `row` of page blk, KV head hk.
+__device__ __forceinline__ float key_value(const AttnParams& p, int64_t blk, int hk, int64_t row,
+                                           int d, int cache_dtype) {
+  const int64_t r = (blk * p.Hkv + hk) * p.BS + row;
+  if (cache_dtype != TMO_DTYPE_I8) return plain_value(p.kc, r * p.k_row + d, cache_dtype);
+  const float code = (float)static_cast<const int8_t*>(p.kc)[r * p.k_row + d];
+  switch (p.smode) {
+    case 1: return code * p.ks[blk * p.ks_sb + hk * p.ks_sh + row];
+    case 2: return code * p.ks[(int64_t)hk * p.D + d];
+    default: return code * p.ks[r * (p.D >> 5) + (d >> 5)];
+  }
+}
+
+// Value channel d: per-group V scales hold one number per 32 rows of a page and channel.
+__device__ __forceinline__ float value_value(const AttnParams& p, int64_t blk, int hk, int64_t row,
+                                             int d, int cache_dtype) {
+  const int64_t r = (blk * p.Hkv + hk) * p.BS + row;
+  if (cache_dtype != TMO_DTYPE_I8) return plain_value(p.vc, r * p.v_row + d, cache_dtype);
+  const float code = (float)static_cast<const int8_t*>(p.vc)[r * p.v_row + d];
+  switch (p.smode) {
+    case 1: return code * p.vs[blk * p.vs_sb + hk * p.vs_sh + row];
+    case 2: return code * p.vs[(int64_t)hk * p.Dv + d];
+    default: return code * p.vs[((blk * p.Hkv + hk) * (p.BS >> 5) + (row >> 5)) * p.Dv + d];
+  }
+}
+
 // One wavefront per (query token, query head): 64 keys at a time, one per lane (a lane
 // computes its key's full dot product), then every lane accumulates its channels over the 64
-// keys.  Dimensions up to 512 (8 accumulators per lane).
+// keys.  Value head sizes up to 512 (8 accumulators per lane); any key head size.
 __global__ __launch_bounds__(256) void attn_generic(AttnParams p) {
   const int cache_dtype = p.c_dtype;
   const int lane = threadIdx.x & (kWave - 1);
@@ -788,7 +810,7 @@ __global__ __launch_bounds__(256) void attn_generic(AttnParams p) {
       if (blk >= 0 && blk < p.NB) {
         float dot = 0.0f;
         for (int d = 0; d < p.D; ++d)
-          dot += load_q(p, qe + d) * cache_value(p, p.kc, p.ks, blk, hk, r, d, cache_dtype);
+          dot += load_q(p, qe + d) * key_value(p, blk, hk, r, d, cache_dtype);
         s = dot * p.scale_log2;
         if (p.alibi) s += alibi * (float)(j - P);
       } else {
@@ -817,7 +839,7 @@ __global__ __launch_bounds__(256) void attn_generic(AttnParams p) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int d = lane + u * kWave;
-        if (d < p.D) acc[u] += pt * cache_value(p, p.vc, p.vs, bt_, hk, rt, d, cache_dtype);
+        if (d < p.Dv) acc[u] += pt * value_value(p, bt_, hk, rt, d, cache_dtype);
       }
     }
   }
@@ -827,7 +849,7 @@ __global__ __launch_bounds__(256) void attn_generic(AttnParams p) {
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int d = lane + u * kWave;
-    if (d < p.D) store_out(p, orow + d, p.sink ? acc[u] * inv : (l > 0.0f ? acc[u] / l : 0.0f));
+    if (d < p.Dv) store_out(p, orow + d, p.sink ? acc[u] * inv : (l > 0.0f ? acc[u] / l : 0.0f));
   }
   if (lane == 0 && p.lse) p.lse[i * p.lse_sb + qrow * p.lse_ss + (int64_t)hq * p.lse_sh] = lse_v;
 }
@@ -859,13 +881,14 @@ int launch_mfma(const AttnParams& p, bool qlo, hipStream_t st) {
 using namespace tmo;
 
 extern "C" int64_t tmo_hip_cached_kv_attn_workspace_bytes(int64_t batch, int64_t num_kv_heads,
-                                                          int64_t num_q_heads, int64_t head_size,
-                                                          int64_t seq_q, int64_t splits) {
-  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || head_size <= 0 || seq_q <= 0 ||
+                                                          int64_t num_q_heads,
+                                                          int64_t head_size_v, int64_t seq_q,
+                                                          int64_t splits) {
+  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || head_size_v <= 0 || seq_q <= 0 ||
       splits <= 1)
     return 0;
-  return batch * num_kv_heads * splits * seq_q * (num_q_heads / num_kv_heads) * (head_size + 2) *
-         (int64_t)sizeof(float);
+  return batch * num_kv_heads * splits * seq_q * (num_q_heads / num_kv_heads) *
+         (head_size_v + 2) * (int64_t)sizeof(float);
 }
 
 extern "C" int64_t tmo_hip_attn_workspace_bytes(int64_t batch, int64_t num_kv_heads,
@@ -879,31 +902,46 @@ extern "C" int64_t tmo_hip_attn_workspace_bytes(int64_t batch, int64_t num_kv_he
 extern "C" int tmo_hip_cached_kv_attn(
     const void* q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head,
     const int32_t* cu_seq_q, int64_t seq_q, int64_t total_q, const void* k_cache,
-    const void* v_cache, const float* k_scale, const float* v_scale, int scale_mode,
+    const void* v_cache, int64_t k_cache_dim, int64_t v_cache_dim, const float* k_scale,
+    const float* v_scale, int scale_mode, int64_t k_scale_stride_block,
+    int64_t k_scale_stride_head, int64_t v_scale_stride_block, int64_t v_scale_stride_head,
     const int32_t* block_tables, int64_t max_blocks, const int32_t* context_lens,
     const float* alibi_slopes, const float* sink, void* out, int64_t out_stride_batch,
     int64_t out_stride_token, int64_t out_stride_head, float* lse, int64_t lse_stride_batch,
     int64_t lse_stride_token, int64_t lse_stride_head, int64_t batch, int64_t num_q_heads,
-    int64_t num_kv_heads, int64_t head_size, int64_t num_blocks, int64_t block_size,
-    int64_t max_context_len, int64_t window_left, float softmax_scale, int q_dtype,
-    int cache_dtype, int64_t splits, void* workspace, int64_t workspace_bytes, void* stream) {
+    int64_t num_kv_heads, int64_t head_size, int64_t head_size_v, int64_t num_blocks,
+    int64_t block_size, int64_t max_context_len, int64_t window_left, float softmax_scale,
+    int q_dtype, int cache_dtype, int64_t splits, void* workspace, int64_t workspace_bytes,
+    void* stream) {
   if (q_dtype != TMO_DTYPE_BF16 && q_dtype != TMO_DTYPE_F16 && q_dtype != TMO_DTYPE_F32)
     return TMO_ERR_UNSUPPORTED_DTYPE;
   if (cache_dtype != TMO_DTYPE_I8 && cache_dtype != q_dtype) return TMO_ERR_UNSUPPORTED_DTYPE;
-  if (cache_dtype == TMO_DTYPE_I8 && scale_mode != 1 && scale_mode != 2)
+  if (cache_dtype == TMO_DTYPE_I8 && (scale_mode < 1 || scale_mode > 3))
     return TMO_ERR_UNSUPPORTED_MODE;
-  if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out)
-    return TMO_ERR_INVALID_ARGUMENT;
+  if (!q || !k_cache || !block_tables || !context_lens || !out) return TMO_ERR_INVALID_ARGUMENT;
   if (cache_dtype == TMO_DTYPE_I8 && (!k_scale || !v_scale)) return TMO_ERR_INVALID_ARGUMENT;
+  // v_cache null: the values are the first head_size_v channels of the K cache's rows
+  if (!v_cache) {
+    v_cache = k_cache;
+    v_cache_dim = k_cache_dim;
+  }
   // max_context_len <= 0: "an uncertain maximum value of context_lens" (reference _ops.py,
   // single_query_cached_kv_attn's max_context_len); it only sizes the splits, so a negative
   // value is taken as 0 (the last split always runs to the sequence's own length)
   if (max_context_len < 0) max_context_len = 0;
   if (batch < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
-      head_size <= 0 || head_size > 512 || num_blocks < 0 || block_size <= 0 || max_blocks < 0 ||
-      splits < 1 || seq_q < 0 || q_stride_batch < 0 || q_stride_token < 0 || q_stride_head < 0 ||
-      out_stride_batch < 0 || out_stride_token < 0 || out_stride_head < 0 ||
-      (cu_seq_q && total_q < 0))
+      head_size <= 0 || head_size > 4096 || head_size_v <= 0 || head_size_v > 512 ||
+      k_cache_dim < head_size || v_cache_dim < head_size_v || num_blocks < 0 ||
+      block_size <= 0 || max_blocks < 0 || splits < 1 || seq_q < 0 || q_stride_batch < 0 ||
+      q_stride_token < 0 || q_stride_head < 0 || out_stride_batch < 0 || out_stride_token < 0 ||
+      out_stride_head < 0 || (cu_seq_q && total_q < 0))
+    return TMO_ERR_INVALID_ARGUMENT;
+  const bool int8 = cache_dtype == TMO_DTYPE_I8;
+  if (int8 && scale_mode == 1 &&
+      (k_scale_stride_block < 0 || k_scale_stride_head < 0 || v_scale_stride_block < 0 ||
+       v_scale_stride_head < 0))
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (int8 && scale_mode == 3 && (head_size % 32 != 0 || block_size % 32 != 0))
     return TMO_ERR_INVALID_ARGUMENT;
   const int64_t g = num_q_heads / num_kv_heads;
   if (batch > 65535 || num_kv_heads > 65535 || splits > 65535 || num_q_heads > 0x7fffffffLL ||
@@ -914,7 +952,7 @@ extern "C" int tmo_hip_cached_kv_attn(
     return TMO_ERR_INVALID_ARGUMENT;
   if (splits > 1 && (!workspace ||
                      workspace_bytes < tmo_hip_cached_kv_attn_workspace_bytes(
-                                           batch, num_kv_heads, num_q_heads, head_size, seq_q,
+                                           batch, num_kv_heads, num_q_heads, head_size_v, seq_q,
                                            splits)))
     return TMO_ERR_INVALID_ARGUMENT;
   if (batch == 0 || seq_q == 0) return TMO_OK;
@@ -932,9 +970,15 @@ extern "C" int tmo_hip_cached_kv_attn(
   p.sink = sink;
   p.kc = k_cache;
   p.vc = v_cache;
+  p.k_row = k_cache_dim;
+  p.v_row = v_cache_dim;
   p.ks = k_scale;
   p.vs = v_scale;
-  p.smode = cache_dtype == TMO_DTYPE_I8 ? scale_mode : 0;
+  p.smode = int8 ? scale_mode : 0;
+  p.ks_sb = k_scale_stride_block;
+  p.ks_sh = k_scale_stride_head;
+  p.vs_sb = v_scale_stride_block;
+  p.vs_sh = v_scale_stride_head;
   p.bt = block_tables;
   p.max_blocks = max_blocks;
   p.lens = context_lens;
@@ -954,30 +998,37 @@ extern "C" int tmo_hip_cached_kv_attn(
   p.Hkv = (int32_t)num_kv_heads;
   p.g = (int32_t)g;
   p.D = (int32_t)head_size;
+  p.Dv = (int32_t)head_size_v;
   p.BS = (int32_t)block_size;
   p.bs_shift = ilog2_if_pow2(block_size);
   p.NB = num_blocks;
   p.q_dtype = q_dtype;
   p.q_vec = q_dtype != TMO_DTYPE_F32 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
             p.q_sb % 8 == 0 && q_stride_token % 8 == 0 && q_stride_head % 8 == 0 &&
-            (cache_dtype != TMO_DTYPE_I8 || scale_mode != 2 ||
-             reinterpret_cast<uintptr_t>(k_scale) % 16 == 0);
+            (!int8 || scale_mode != 2 || reinterpret_cast<uintptr_t>(k_scale) % 16 == 0);
   p.ws = static_cast<float*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
-  // MFMA path eligibility: head size, page rows, 16-byte aligned rows and scales, q's dtype
-  // representable by the operands (int8 caches: bf16 with a lo part when needed).
+  // MFMA path eligibility: one head size for K and V that is also both caches' row length,
+  // page rows in whole 16-token tiles, 16-byte aligned rows and scale vectors (per-token scale
+  // offsets of a page and head in multiples of four), q's dtype representable by the operands
+  // (int8 caches: bf16 with a lo part when needed), per-token or per-channel scales.
   auto al = [](const void* x, int a) { return reinterpret_cast<uintptr_t>(x) % a == 0; };
-  bool mfma = (head_size == 64 || head_size == 128 || head_size == 256) && block_size % 16 == 0 &&
-              al(k_cache, 16) && al(v_cache, 16) && q_dtype != TMO_DTYPE_F32;
-  if (cache_dtype == TMO_DTYPE_I8)
-    mfma = mfma && (scale_mode != 1 || (al(k_scale, 16) && al(v_scale, 16)));
+  bool mfma = (head_size == 64 || head_size == 128 || head_size == 256) &&
+              head_size_v == head_size && k_cache_dim == head_size &&
+              v_cache_dim == head_size && block_size % 16 == 0 && al(k_cache, 16) &&
+              al(v_cache, 16) && q_dtype != TMO_DTYPE_F32;
+  if (int8)
+    mfma = mfma && scale_mode != 3 &&
+           (scale_mode != 1 ||
+            (al(k_scale, 16) && al(v_scale, 16) && k_scale_stride_block % 4 == 0 &&
+             k_scale_stride_head % 4 == 0 && v_scale_stride_block % 4 == 0 &&
+             v_scale_stride_head % 4 == 0));
   p.c_dtype = cache_dtype;
   if (!mfma) {
     p.splits = 1;
     p.split_tokens = 1;
     const int64_t rows = batch * seq_q * num_q_heads;
-    if ((rows + 3) / 4 > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
     return launch_kernel(attn_generic, dim3((unsigned)((rows + 3) / 4)), dim3(256), st, p);
   }
   p.splits = (int32_t)splits;
@@ -988,7 +1039,7 @@ extern "C" int tmo_hip_cached_kv_attn(
   p.split_tokens = per > 0 ? per : 64;
   // int8 caches: bf16 and f16 q are exact f16 operands after the power-of-two scaling; q
   // folded with per-channel key scales needs the lo operand
-  if (cache_dtype == TMO_DTYPE_I8) return launch_mfma<0>(p, scale_mode == 2, st);
+  if (int8) return launch_mfma<0>(p, scale_mode == 2, st);
   if (cache_dtype == TMO_DTYPE_BF16) return launch_mfma<1>(p, false, st);
   return launch_mfma<2>(p, false, st);
 }
@@ -1003,11 +1054,16 @@ extern "C" int tmo_hip_single_query_cached_kv_attn(
     int64_t block_size, int64_t max_context_len, int64_t window_left, float softmax_scale,
     int q_dtype, int cache_dtype, int64_t splits, void* workspace, int64_t workspace_bytes,
     void* stream) {
+  if (cache_dtype == TMO_DTYPE_I8 && scale_mode == 3) return TMO_ERR_UNSUPPORTED_MODE;
+  if (!v_cache) return TMO_ERR_INVALID_ARGUMENT;
+  if (head_size > 512) return TMO_ERR_INVALID_ARGUMENT;
+  // contiguous per-token scales [num_blocks, Hkv, block_size]
+  const int64_t sb = num_kv_heads * block_size, sh = block_size;
   return tmo_hip_cached_kv_attn(
-      q, q_stride_seq, 0, q_stride_head, nullptr, 1, 0, k_cache, v_cache, k_scale, v_scale,
-      scale_mode, block_tables, max_blocks, context_lens, alibi_slopes, nullptr, out,
-      out_stride_seq, 0, out_stride_head, lse, lse_stride_seq, 0, lse_stride_head, batch,
-      num_q_heads, num_kv_heads, head_size, num_blocks, block_size, max_context_len,
-      window_left, softmax_scale, q_dtype, cache_dtype, splits, workspace, workspace_bytes,
-      stream);
+      q, q_stride_seq, 0, q_stride_head, nullptr, 1, 0, k_cache, v_cache, head_size, head_size,
+      k_scale, v_scale, scale_mode, sb, sh, sb, sh, block_tables, max_blocks, context_lens,
+      alibi_slopes, nullptr, out, out_stride_seq, 0, out_stride_head, lse, lse_stride_seq, 0,
+      lse_stride_head, batch, num_q_heads, num_kv_heads, head_size, head_size, num_blocks,
+      block_size, max_context_len, window_left, softmax_scale, q_dtype, cache_dtype, splits,
+      workspace, workspace_bytes, stream);
 }

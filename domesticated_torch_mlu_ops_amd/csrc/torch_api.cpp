@@ -989,7 +989,6 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   TORCH_CHECK(!q_quant_scale.has_value() && !out_quant_scale.has_value(), op,
               ": quantised q / output are not supported by this build");
   TORCH_CHECK(!mask.has_value(), op, ": mask is not supported by this build");
-  TORCH_CHECK(v_cache.has_value(), op, ": a separate v_cache is required");
   TORCH_CHECK(compute_dtype == "float" || compute_dtype == "half" || compute_dtype == "bfloat16",
               op, ": compute_dtype must be float, half or bfloat16 (the softmax runs in fp32)");
   TORCH_CHECK(windows_size_right.expect_int() == -1, op, ": windows_size_right must be -1");
@@ -1045,53 +1044,100 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
                 op, ": sink must be a contiguous float32 [heads] tensor");
     sink_p = sink->data_ptr<float>();
   }
-  const at::Tensor& vc = *v_cache;
+  // caches [num_blocks, kv_heads, block_size, cache_dim]: keys are the first head_size
+  // channels of a K row, values the first head_size_v (out's last dim) of a V row, or of the
+  // K row when v_cache is None (cache_dim = max(head_size_qk, head_size_v), _ops.py:828-831)
   check_device(k_cache, q_ori, "k_cache");
-  check_device(vc, q_ori, "v_cache");
-  TORCH_CHECK(k_cache.dim() == 4 && k_cache.is_contiguous() && vc.sizes() == k_cache.sizes() &&
-                  vc.is_contiguous() && vc.scalar_type() == k_cache.scalar_type(),
-              op, ": k_cache / v_cache must be contiguous [num_blocks, kv_heads, block_size, ",
-              "head_size] tensors of one dtype, got ", k_cache.sizes(), " and ", vc.sizes());
+  TORCH_CHECK(k_cache.dim() == 4 && k_cache.is_contiguous(), op,
+              ": k_cache must be a contiguous [num_blocks, kv_heads, block_size, cache_dim] ",
+              "tensor, got ", k_cache.sizes());
   const int64_t NB = k_cache.size(0), Hkv = k_cache.size(1), BS = k_cache.size(2);
-  TORCH_CHECK(k_cache.size(3) == D, op, ": cache head_size ", k_cache.size(3), " != q's ", D);
+  const int64_t kdim = k_cache.size(3);
+  check_device(output, q_ori, "output");
+  TORCH_CHECK(output.dim() == q_ori.dim() &&
+                  output.sizes().slice(0, q_ori.dim() - 1) == q_ori.sizes().slice(0, q_ori.dim() - 1) &&
+                  output.scalar_type() == q.scalar_type(),
+              op, ": output must be q's shape with head_size_v channels, in q's dtype");
+  const int64_t Dv = output.size(-1);
+  int64_t vdim = kdim;
+  if (v_cache.has_value()) {
+    const at::Tensor& vc = *v_cache;
+    check_device(vc, q_ori, "v_cache");
+    TORCH_CHECK(vc.dim() == 4 && vc.is_contiguous() && vc.size(0) == NB && vc.size(1) == Hkv &&
+                    vc.size(2) == BS && vc.scalar_type() == k_cache.scalar_type(),
+                op, ": v_cache must be a contiguous [num_blocks, kv_heads, block_size, ",
+                "head_size_v] tensor of k_cache's dtype, got ", vc.sizes());
+    vdim = vc.size(3);
+    TORCH_CHECK(kdim == D, op, ": k_cache head_size ", kdim, " != q's ", D);
+    TORCH_CHECK(vdim == Dv, op, ": v_cache head_size ", vdim, " != output's ", Dv);
+  } else {
+    TORCH_CHECK(kdim == std::max(D, Dv), op, ": with v_cache None, k_cache's last dim must be ",
+                "max(head_size_qk, head_size_v) = ", std::max(D, Dv), ", got ", kdim);
+  }
   TORCH_CHECK(Hkv > 0 && Hq % Hkv == 0, op, ": query heads ", Hq,
               " must be a multiple of the KV heads ", Hkv);
+  TORCH_CHECK(D <= 4096 && Dv <= 512, op, ": head sizes up to 4096 (keys) and 512 (values)");
   const int cdt = dtype_code(k_cache.scalar_type());
   const bool int8 = cdt == TMO_DTYPE_I8;
   TORCH_CHECK(int8 == (kv_cache_quant_bit_size == 8), op,
               ": kv_cache_quant_bit_size 8 goes with int8 caches, -1 with caches of q's dtype");
   TORCH_CHECK(int8 || cdt == qdt, op, ": unquantised caches must have q's dtype");
-  // scales: per token [NB, Hkv, BS] (or [..., 1]), per channel [Hkv, D], per tensor [1]
+  // scales: per token [NB, Hkv, BS] (or [..., 1]; any strides in the first two dims), per
+  // channel [Hkv, D] / [Hkv, Dv], per tensor [1], per group K [NB, Hkv, BS, D / 32] with
+  // V [NB, Hkv, BS / 32, Dv] (_ops.py:838-842)
   int smode = 0;
   at::Tensor ks, vs;
+  int64_t ks_sb = 0, ks_sh = 0, vs_sb = 0, vs_sh = 0;
   if (int8) {
     TORCH_CHECK(k_cache_quant_scale.has_value() && v_cache_quant_scale.has_value(), op,
                 ": int8 caches need k_cache_quant_scale and v_cache_quant_scale");
-    auto norm = [&](const at::Tensor& sc, const char* name) -> at::Tensor {
-      check_device(sc, q_ori, name);
-      TORCH_CHECK(sc.scalar_type() == at::kFloat, name, " must be float32");
-      if ((sc.dim() == 3 || (sc.dim() == 4 && sc.size(3) == 1)) && sc.size(0) == NB &&
-          sc.size(1) == Hkv && sc.size(2) == BS) {
-        TORCH_CHECK(smode == 0 || smode == 1, op, ": K and V scales must use one mode");
-        smode = 1;
-        return sc.reshape({NB, Hkv, BS}).contiguous();
-      }
-      if (sc.dim() == 2 && sc.size(0) == Hkv && sc.size(1) == D) {
-        TORCH_CHECK(smode == 0 || smode == 2, op, ": K and V scales must use one mode");
-        smode = 2;
-        return sc.contiguous();
-      }
-      if (sc.numel() == 1) {  // per tensor: one number for every channel
-        TORCH_CHECK(smode == 0 || smode == 2, op, ": K and V scales must use one mode");
-        smode = 2;
-        return sc.reshape({1, 1}).expand({Hkv, D}).contiguous();
-      }
-      TORCH_CHECK(false, name, ": expected [num_blocks, kv_heads, block_size], [kv_heads, ",
-                  "head_size] or [1] (group-wise scales are not supported), got ", sc.sizes());
-      return sc;
-    };
-    ks = norm(*k_cache_quant_scale, "k_cache_quant_scale");
-    vs = norm(*v_cache_quant_scale, "v_cache_quant_scale");
+    const at::Tensor& ksc = *k_cache_quant_scale;
+    const at::Tensor& vsc = *v_cache_quant_scale;
+    check_device(ksc, q_ori, "k_cache_quant_scale");
+    check_device(vsc, q_ori, "v_cache_quant_scale");
+    TORCH_CHECK(ksc.scalar_type() == at::kFloat && vsc.scalar_type() == at::kFloat, op,
+                ": cache scales must be float32");
+    const bool group = ksc.dim() == 4 && vsc.dim() == 4 && D % 32 == 0 && BS % 32 == 0 &&
+                       ksc.sizes() == at::IntArrayRef({NB, Hkv, BS, D / 32}) &&
+                       vsc.sizes() == at::IntArrayRef({NB, Hkv, BS / 32, Dv});
+    if (group) {
+      TORCH_CHECK(ksc.is_contiguous() && vsc.is_contiguous(), op,
+                  ": per-group scales must be contiguous");
+      smode = 3;
+      ks = ksc;
+      vs = vsc;
+    } else {
+      auto norm = [&](const at::Tensor& sc, int64_t dims, int64_t& sb, int64_t& sh,
+                      const char* name) -> at::Tensor {
+        if ((sc.dim() == 3 || (sc.dim() == 4 && sc.size(3) == 1)) && sc.size(0) == NB &&
+            sc.size(1) == Hkv && sc.size(2) == BS) {
+          TORCH_CHECK(smode == 0 || smode == 1, op, ": K and V scales must use one mode");
+          smode = 1;
+          at::Tensor t = sc.dim() == 4 ? sc.select(3, 0) : sc;
+          if (BS > 1 && t.stride(2) != 1) t = t.contiguous();
+          sb = t.stride(0);
+          sh = t.stride(1);
+          return t;
+        }
+        if (sc.dim() == 2 && sc.size(0) == Hkv && sc.size(1) == dims) {
+          TORCH_CHECK(smode == 0 || smode == 2, op, ": K and V scales must use one mode");
+          smode = 2;
+          return sc.contiguous();
+        }
+        if (sc.numel() == 1) {  // per tensor: one number for every channel
+          TORCH_CHECK(smode == 0 || smode == 2, op, ": K and V scales must use one mode");
+          smode = 2;
+          return sc.reshape({1, 1}).expand({Hkv, dims}).contiguous();
+        }
+        TORCH_CHECK(false, name, ": expected [num_blocks, kv_heads, block_size], [kv_heads, ",
+                    "head_size], [1] or per-group K [num_blocks, kv_heads, block_size, ",
+                    "head_size / 32] with V [num_blocks, kv_heads, block_size / 32, ",
+                    "head_size_v], got ", sc.sizes());
+        return sc;
+      };
+      ks = norm(ksc, D, ks_sb, ks_sh, "k_cache_quant_scale");
+      vs = norm(vsc, Dv, vs_sb, vs_sh, "v_cache_quant_scale");
+    }
   }
   check_device(block_tables, q_ori, "block_tables");
   TORCH_CHECK(block_tables.scalar_type() == at::kInt && block_tables.dim() == 2 &&
@@ -1106,9 +1152,6 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
                 op, ": alibi_slopes must be a contiguous float32 [batch, heads] tensor");
     alibi = alibi_slopes->data_ptr<float>();
   }
-  check_device(output, q_ori, "output");
-  TORCH_CHECK(output.sizes() == q_ori.sizes() && output.scalar_type() == q.scalar_type(), op,
-              ": output must have q's shape and dtype");
   const at::Tensor& out = output;
   TORCH_CHECK(out.size(-1) <= 1 || out.stride(-1) == 1, "output must have a contiguous last dim");
   // element strides (batch, token, head) of q, out and lse
@@ -1156,15 +1199,16 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   }
   c10::DeviceGuard guard(q_ori.device());
   at::Tensor ws;
-  const int64_t ws_bytes = tmo_hip_cached_kv_attn_workspace_bytes(B, Hkv, Hq, D, seq_q, splits);
+  const int64_t ws_bytes = tmo_hip_cached_kv_attn_workspace_bytes(B, Hkv, Hq, Dv, seq_q, splits);
   if (ws_bytes > 0)
     ws = at::empty({(ws_bytes + 3) / 4}, q_ori.options().dtype(at::kFloat));
   const int st = tmo_hip_cached_kv_attn(
       q.data_ptr(), q_sb, q_ss, q.stride(-2), cu, seq_q, total_q, k_cache.data_ptr(),
-      vc.data_ptr(), int8 ? ks.data_ptr<float>() : nullptr, int8 ? vs.data_ptr<float>() : nullptr,
-      smode, block_tables.data_ptr<int32_t>(), block_tables.size(1),
+      v_cache.has_value() ? v_cache->data_ptr() : nullptr, kdim, vdim,
+      int8 ? ks.data_ptr<float>() : nullptr, int8 ? vs.data_ptr<float>() : nullptr, smode,
+      ks_sb, ks_sh, vs_sb, vs_sh, block_tables.data_ptr<int32_t>(), block_tables.size(1),
       context_lens.data_ptr<int32_t>(), alibi, sink_p, out.data_ptr(), o_sb, o_ss,
-      out.stride(-2), lse, lse_sb, lse_ss, lse_sh, B, Hq, Hkv, D, NB, BS, max_ctx, window,
+      out.stride(-2), lse, lse_sb, lse_ss, lse_sh, B, Hq, Hkv, D, Dv, NB, BS, max_ctx, window,
       static_cast<float>(softmax_scale), qdt, cdt, splits, ws_bytes > 0 ? ws.data_ptr() : nullptr,
       ws_bytes, stream_of(q_ori));
   check_status(st, op);

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 12
+#define TMO_HIP_ABI_VERSION 13
 
 /* element types */
 enum tmo_dtype {
@@ -427,11 +427,22 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
  *     of a [total_q, Hq, D] q, row t at t * q_stride_token (q_stride_batch unused); seq_q is
  *     an upper bound of the counts (tokens past it are not computed) and rows outside
  *     [0, total_q) are skipped.
- * out (q's dtype) and lse (nullable, fp32) are addressed the same way with their own strides.
- * Caches [num_blocks, Hkv, block_size, head_size] contiguous: int8 (cache_dtype TMO_DTYPE_I8)
- * with k = code * scale, scale_mode 1: per-token scales [num_blocks, Hkv, block_size], 2:
- * per-channel [Hkv, head_size]; or of q's dtype (F32, F16 or BF16).  sink (nullable): [Hq]
- * fp32 natural-log logits.
+ * out (q's dtype, head_size_v channels) and lse (nullable, fp32) are addressed the same way
+ * with their own strides.
+ * Caches [num_blocks, Hkv, block_size, k_cache_dim / v_cache_dim] contiguous: k_j is the first
+ * head_size channels of its K row, v_j the first head_size_v of its V row -- of its K row when
+ * v_cache is null (K and V in one cache, reference _ops.py:828-831; v_cache_dim unused).  Int8
+ * caches (cache_dtype TMO_DTYPE_I8) hold k = code * scale, fp32 scales by scale_mode:
+ *   1 per token: [num_blocks, Hkv, block_size] with element strides (scale_stride_block,
+ *     scale_stride_head, 1) -- any strides in the first two dims (_ops.py:838);
+ *   2 per channel: [Hkv, head_size] (K) and [Hkv, head_size_v] (V), contiguous;
+ *   3 per group (_ops.py:841-842): K [num_blocks, Hkv, block_size, head_size / 32] (one per
+ *     token and 32 channels), V [num_blocks, Hkv, block_size / 32, head_size_v] (one per 32 rows
+ *     of a page and channel), contiguous; head_size and block_size multiples of 32.
+ * Other caches are of q's dtype (F32, F16 or BF16).  sink (nullable): [Hq] fp32 natural-log
+ * logits.  Head sizes: head_size up to 4096, head_size_v up to 512; the MFMA kernels take K and
+ * V head sizes and cache rows all equal to 64, 128 or 256 with per-token or per-channel
+ * scales, a VALU kernel the rest.
  * Arithmetic: fp32 accumulation (MFMA with bf16/f16 operands: int8 codes are exact; q and the
  * probabilities are split into two operands when one is not exact), softmax in fp32.
  * splits > 1 divides each sequence's keys over that many workgroups per KV head; it needs
@@ -446,29 +457,34 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
 int tmo_hip_cached_kv_attn(const void* q, int64_t q_stride_batch, int64_t q_stride_token,
                            int64_t q_stride_head, const int32_t* cu_seq_q, int64_t seq_q,
                            int64_t total_q, const void* k_cache, const void* v_cache,
-                           const float* k_scale, const float* v_scale, int scale_mode,
-                           const int32_t* block_tables, int64_t max_blocks,
-                           const int32_t* context_lens, const float* alibi_slopes,
-                           const float* sink, void* out, int64_t out_stride_batch,
-                           int64_t out_stride_token, int64_t out_stride_head, float* lse,
-                           int64_t lse_stride_batch, int64_t lse_stride_token,
-                           int64_t lse_stride_head, int64_t batch, int64_t num_q_heads,
-                           int64_t num_kv_heads, int64_t head_size, int64_t num_blocks,
-                           int64_t block_size, int64_t max_context_len, int64_t window_left,
-                           float softmax_scale, int q_dtype, int cache_dtype, int64_t splits,
-                           void* workspace, int64_t workspace_bytes, void* stream);
+                           int64_t k_cache_dim, int64_t v_cache_dim, const float* k_scale,
+                           const float* v_scale, int scale_mode, int64_t k_scale_stride_block,
+                           int64_t k_scale_stride_head, int64_t v_scale_stride_block,
+                           int64_t v_scale_stride_head, const int32_t* block_tables,
+                           int64_t max_blocks, const int32_t* context_lens,
+                           const float* alibi_slopes, const float* sink, void* out,
+                           int64_t out_stride_batch, int64_t out_stride_token,
+                           int64_t out_stride_head, float* lse, int64_t lse_stride_batch,
+                           int64_t lse_stride_token, int64_t lse_stride_head, int64_t batch,
+                           int64_t num_q_heads, int64_t num_kv_heads, int64_t head_size,
+                           int64_t head_size_v, int64_t num_blocks, int64_t block_size,
+                           int64_t max_context_len, int64_t window_left, float softmax_scale,
+                           int q_dtype, int cache_dtype, int64_t splits, void* workspace,
+                           int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes tmo_hip_cached_kv_attn needs for `splits` with up to seq_q tokens per
  * sequence (0 when splits <= 1). */
 int64_t tmo_hip_cached_kv_attn_workspace_bytes(int64_t batch, int64_t num_kv_heads,
-                                               int64_t num_q_heads, int64_t head_size,
+                                               int64_t num_q_heads, int64_t head_size_v,
                                                int64_t seq_q, int64_t splits);
 
 /*
  * single_query_cached_kv_attn -- tmo_hip_cached_kv_attn with one query token per sequence
- * (seq_q 1, no cu_seq_q, no sink): q / out [batch, Hq, head_size] rows with the given strides,
- * lse (nullable) at i * lse_stride_seq + hq * lse_stride_head.  Replaces the same reference
- * interface for the decode step (reference include/torch_mlu_ops.h:107-130, _ops.py:777-900).
+ * (seq_q 1, no cu_seq_q, no sink), separate K and V caches [num_blocks, Hkv, block_size,
+ * head_size], scale_mode 1 (contiguous per-token scales) or 2: q / out [batch, Hq, head_size]
+ * rows with the given strides, lse (nullable) at i * lse_stride_seq + hq * lse_stride_head;
+ * head_size up to 512.  Replaces the same reference interface for the decode step (reference
+ * include/torch_mlu_ops.h:107-130, _ops.py:777-900).
  */
 int tmo_hip_single_query_cached_kv_attn(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
                                         const void* k_cache, const void* v_cache,

@@ -71,9 +71,9 @@ def lib() -> ctypes.CDLL:
         L.oracle_single_query_attn.restype = c_int
         L.oracle_cached_kv_attn.argtypes = [c_void_p, c_int, c_int64, c_int64, c_void_p,
                                             c_int64, c_int64, c_void_p, c_void_p, c_int] + \
-            [c_int64] * 4 + [c_void_p, c_void_p, c_int, c_void_p, c_int64, c_void_p, c_int64,
-                             c_int64, c_void_p, c_void_p, c_int64, c_double, c_void_p,
-                             c_void_p, c_int]
+            [c_int64] * 7 + [c_void_p, c_void_p, c_int] + [c_int64] * 4 + \
+            [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+             c_double, c_void_p, c_void_p, c_int]
         L.oracle_cached_kv_attn.restype = c_int
         for name in ("oracle_f32_to_bf16", "oracle_f32_to_f16", "oracle_f16_to_f32",
                      "oracle_f32_to_e4m3"):
@@ -296,13 +296,18 @@ def single_query_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_s
 
 def cached_kv_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scale: float,
                    k_scale=None, v_scale=None, alibi_slopes=None, window_left: int = -1,
-                   cu_seq_q=None, sink=None, nthreads: Optional[int] = None):
+                   cu_seq_q=None, sink=None, head_size_v: Optional[int] = None,
+                   nthreads: Optional[int] = None):
     """reference _ops.py:777-900 with several query tokens per sequence (decision D12 of
     tmo_oracle.c), in float64.  q [B, S, Hq, D] (S tokens per sequence), or [T, Hq, D] with
     cu_seq_q [B + 1] (rows cu_seq_q[i] .. cu_seq_q[i + 1] - 1 are sequence i's), or [B, Hq, D]
     (one token each); token s of a sequence with nq tokens and L keys sits at position
-    L - nq + s.  sink [Hq] or None.  Returns (out, lse) float64 of q's leading shape:
-    [B, S, Hq, D] / [B, S, Hq] for 4-D q, [T, Hq, D] / [T, Hq] otherwise; rows that no
+    L - nq + s.  Keys are the first D channels of k_cache's rows; values the first
+    head_size_v (default: v_cache's last dim, or D) of v_cache's, or of k_cache's when v_cache
+    is None.  Int8 scales: [NB, Hkv, BS] (or [..., 1]; any strides in the first two dims) per
+    token, [Hkv, D or Dv] per channel, or per group K [NB, Hkv, BS, D / 32] and V [NB, Hkv,
+    BS / 32, Dv].  sink [Hq] or None.  Returns (out, lse) float64 of q's leading shape:
+    [B, S, Hq, Dv] / [B, S, Hq] for 4-D q, [T, Hq, Dv] / [T, Hq] otherwise; rows that no
     sequence of cu_seq_q holds are NaN."""
     four = q.dim() == 4
     if four:
@@ -311,32 +316,44 @@ def cached_kv_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scal
     else:
         B = context_lens.shape[0]
         S = 1
-    assert q.stride(-1) == 1 and k_cache.is_contiguous() and v_cache.is_contiguous()
+    vc = k_cache if v_cache is None else v_cache
+    assert q.stride(-1) == 1 and k_cache.is_contiguous() and vc.is_contiguous()
     T, Hq, D = q.shape
-    NB, Hkv, BS, _ = k_cache.shape
+    NB, Hkv, BS, krow = k_cache.shape
+    vrow = vc.shape[3]
+    Dv = head_size_v if head_size_v is not None else (vrow if v_cache is not None else D)
     cdt = _DT[k_cache.dtype]
     mode = 0
     ks = vs = None
+    strides = [0, 0, 0, 0]
     if k_cache.dtype == torch.int8:
-        ks = k_scale.to(torch.float32).contiguous()
-        vs = v_scale.to(torch.float32).contiguous()
-        mode = 2 if ks.dim() == 2 else 1
+        def one(sc):
+            sc = sc.to(torch.float32)
+            if sc.dim() == 4 and sc.shape[3] == 1:
+                sc = sc[..., 0]
+            if sc.dim() == 3:
+                assert sc.stride(2) == 1
+                return sc, 1, (sc.stride(0), sc.stride(1))
+            return sc.contiguous(), (2 if sc.dim() == 2 else 3), (0, 0)
+        ks, mode, strides[0:2] = one(k_scale)
+        vs, vmode, strides[2:4] = one(v_scale)
+        assert vmode == mode
     bt = block_tables.to(torch.int32).contiguous()
     lens = context_lens.to(torch.int32).contiguous()
     cu = cu_seq_q.to(torch.int32).contiguous() if cu_seq_q is not None else None
     assert cu is None or (not four and cu.numel() == B + 1)
     al = alibi_slopes.to(torch.float32).contiguous() if alibi_slopes is not None else None
     sk = sink.to(torch.float32).contiguous() if sink is not None else None
-    out = torch.full((T, Hq, D), float("nan"), dtype=torch.float64)
+    out = torch.full((T, Hq, Dv), float("nan"), dtype=torch.float64)
     lse = torch.full((T, Hq), float("nan"), dtype=torch.float64)
     rc = lib().oracle_cached_kv_attn(
         _ptr(q), _DT[q.dtype], q.stride(0), q.stride(1), _ptr(cu), S, T, _ptr(k_cache),
-        _ptr(v_cache), cdt, NB, Hkv, BS, D, _ptr(ks), _ptr(vs), mode, _ptr(bt), bt.shape[1],
-        _ptr(lens), B, Hq, _ptr(al), _ptr(sk), int(window_left), float(softmax_scale),
-        _ptr(out), _ptr(lse), nthreads or default_threads())
+        _ptr(vc), cdt, NB, Hkv, BS, D, Dv, krow, vrow, _ptr(ks), _ptr(vs), mode, *strides,
+        _ptr(bt), bt.shape[1], _ptr(lens), B, Hq, _ptr(al), _ptr(sk), int(window_left),
+        float(softmax_scale), _ptr(out), _ptr(lse), nthreads or default_threads())
     _check(rc, "cached_kv_attn")
     if four:
-        return out.reshape(B, S, Hq, D), lse.reshape(B, S, Hq)
+        return out.reshape(B, S, Hq, Dv), lse.reshape(B, S, Hq)
     return out, lse
 
 

@@ -71,6 +71,10 @@
  *       out = sum_j e^(s_j) v_j / (sum_j e^(s_j) + e^sink); lse = log of that denominator
  *       (the docstring writes logsumexp(qk), which equals it without alibi and sink); a key
  *       on a page outside [0, NB) is masked; no key and no sink gives out 0, lse -inf.
+ *       Keys are the first head_size_qk channels of a K cache row, values the first
+ *       head_size_v of a V cache row -- of the K row itself when v_cache is None
+ *       (_ops.py:828-831); per-group scales (_ops.py:841-842) cover 32 channels of one key
+ *       (K) or 32 rows of one page and channel (V: block_size // 32 per page).
  *   D9  offline (static-scale) quantisation divides: code = clip(RNE(RN(fp32(x) / s)), -128, 127)
  *       for int8, fp8 = e4m3fn_RNE(clip(RN(fp32(x) / s), -448, 448)), s the fp32 per-channel
  *       scale or the per-tensor scalar rounded to fp32 (_ops.py:1652-1670; the division is
@@ -974,24 +978,40 @@ int oracle_scaled_quantize_per_token(const void* x, int dtype, int64_t n0, int64
 typedef struct {
     const void* q; int q_dtype; int64_t q_st, q_sh;      /* q rows [T, Hq, D], element strides */
     const int32_t* cu; int64_t S, T;                     /* cu_seq_q [B + 1], or S tokens each */
-    const void* kc; const void* vc; int c_dtype;         /* caches [NB, Hkv, BS, D] */
-    int64_t NB, Hkv, BS, D, Hq, MB, B;
-    const float* ks; const float* vs; int smode;         /* 0 none, 1 per token, 2 per channel */
+    const void* kc; const void* vc; int c_dtype;         /* caches [NB, Hkv, BS, krow / vrow] */
+    int64_t NB, Hkv, BS, D, Dv, krow, vrow, Hq, MB, B;
+    const float* ks; const float* vs; int smode;         /* 0 none, 1 token, 2 channel, 3 group */
+    int64_t ks_sb, ks_sh, vs_sb, vs_sh;                  /* per-token scale strides */
     const int32_t* bt; const int32_t* lens;
     const float* alibi; const float* sink; int64_t window; double scale;
-    double* out; double* lse;                            /* [T, Hq, D], [T, Hq] */
+    double* out; double* lse;                            /* [T, Hq, Dv], [T, Hq] */
 } sqa_ctx;
 
-static double cache_val(const sqa_ctx* c, const void* base, const float* sc, int64_t blk,
-                        int64_t hk, int64_t row, int64_t d) {
-    int64_t e = ((blk * c->Hkv + hk) * c->BS + row) * c->D + d;
+/* Key channel d (< D) of row `row` of page blk, KV head hk: the first D of the row's krow. */
+static double key_val(const sqa_ctx* c, int64_t blk, int64_t hk, int64_t row, int64_t d) {
+    const int64_t r = (blk * c->Hkv + hk) * c->BS + row;
     if (c->c_dtype == DT_I8) {
-        double code = (double)((const int8_t*)base)[e];
-        if (c->smode == 1) return code * (double)sc[(blk * c->Hkv + hk) * c->BS + row];
-        if (c->smode == 2) return code * (double)sc[hk * c->D + d];
+        double code = (double)((const int8_t*)c->kc)[r * c->krow + d];
+        if (c->smode == 1) return code * (double)c->ks[blk * c->ks_sb + hk * c->ks_sh + row];
+        if (c->smode == 2) return code * (double)c->ks[hk * c->D + d];
+        if (c->smode == 3) return code * (double)c->ks[r * (c->D / 32) + d / 32];
         return code;
     }
-    return (double)load_elem(base, e, c->c_dtype);
+    return (double)load_elem(c->kc, r * c->krow + d, c->c_dtype);
+}
+
+/* Value channel d (< Dv): per-group V scales hold one number per 32 rows of a page and channel. */
+static double value_val(const sqa_ctx* c, int64_t blk, int64_t hk, int64_t row, int64_t d) {
+    const int64_t r = (blk * c->Hkv + hk) * c->BS + row;
+    if (c->c_dtype == DT_I8) {
+        double code = (double)((const int8_t*)c->vc)[r * c->vrow + d];
+        if (c->smode == 1) return code * (double)c->vs[blk * c->vs_sb + hk * c->vs_sh + row];
+        if (c->smode == 2) return code * (double)c->vs[hk * c->Dv + d];
+        if (c->smode == 3)
+            return code * (double)c->vs[((blk * c->Hkv + hk) * (c->BS / 32) + row / 32) * c->Dv + d];
+        return code;
+    }
+    return (double)load_elem(c->vc, r * c->vrow + d, c->c_dtype);
 }
 
 /* The sequence of query row t and the row's token index in it; -1 when no sequence holds t. */
@@ -1023,8 +1043,8 @@ static void sqa_range(void* p, int64_t lo, int64_t hi) {
         const int64_t P = L - nq + tok;             /* the token's position: keys j <= P */
         const int64_t jend = P + 1 < L ? P + 1 : L;
         int64_t j0 = c->window >= 0 && P - c->window > 0 ? P - c->window : 0;
-        double* o = c->out + w * c->D;
-        for (int64_t d = 0; d < c->D; ++d) o[d] = 0.0;
+        double* o = c->out + w * c->Dv;
+        for (int64_t d = 0; d < c->Dv; ++d) o[d] = 0.0;
         double m = c->sink ? (double)c->sink[hq] : -INFINITY;
         for (int64_t j = j0; j < jend; ++j) {
             int64_t blk = c->bt[i * c->MB + j / c->BS], row = j % c->BS;
@@ -1032,7 +1052,7 @@ static void sqa_range(void* p, int64_t lo, int64_t hi) {
             double acc = 0.0;
             for (int64_t d = 0; d < c->D; ++d)
                 acc += (double)load_elem(c->q, t * c->q_st + hq * c->q_sh + d, c->q_dtype) *
-                       cache_val(c, c->kc, c->ks, blk, hk, row, d);
+                       key_val(c, blk, hk, row, d);
             s[j] = c->scale * acc;
             if (c->alibi) s[j] += (double)c->alibi[i * c->Hq + hq] * (double)(j - P);
             if (s[j] > m) m = s[j];
@@ -1045,9 +1065,9 @@ static void sqa_range(void* p, int64_t lo, int64_t hi) {
                 double pj = exp(s[j] - m);
                 l += pj;
                 int64_t blk = c->bt[i * c->MB + j / c->BS], row = j % c->BS;
-                for (int64_t d = 0; d < c->D; ++d) o[d] += pj * cache_val(c, c->vc, c->vs, blk, hk, row, d);
+                for (int64_t d = 0; d < c->Dv; ++d) o[d] += pj * value_val(c, blk, hk, row, d);
             }
-            for (int64_t d = 0; d < c->D; ++d) o[d] /= l;
+            for (int64_t d = 0; d < c->Dv; ++d) o[d] /= l;
         }
         if (c->lse) c->lse[w] = m > -INFINITY ? m + log(l) : -INFINITY;
     }
@@ -1059,28 +1079,37 @@ static void sqa_range(void* p, int64_t lo, int64_t hi) {
  *   out = sum_j e^(s_j) v_j / (sum_j e^(s_j) (+ e^sink[hq])),  lse = log of that denominator,
  * for query token s of sequence i at position P = L - nq + s (L = context_lens[i], nq its
  * query tokens) over keys j in [max(0, P - window_left), min(P, L - 1)] (all of [0, P] when
- * window_left < 0), key j at row j % BS of page block_tables[i, j / BS]; k_jd = code * scale
- * exactly (per token [NB, Hkv, BS] or per channel [Hkv, D]) for int8 caches, the stored value
- * otherwise; query head hq reads KV head hq / (Hq / Hkv).  Query rows: q [T, Hq, D] with row t
+ * window_left < 0), key j at row j % BS of page block_tables[i, j / BS]: its first D channels
+ * are k_j, the first Dv of the V cache's row (or of the same K row, _ops.py:828-831, when the
+ * caller passes the K cache as V) v_j.  Int8 caches hold code * scale exactly, scale_mode 1:
+ * per token, [NB, Hkv, BS] at blk * s_sb + hk * s_sh + row; 2: per channel [Hkv, D] / [Hkv,
+ * Dv]; 3: per group (_ops.py:841-842), K [NB, Hkv, BS, D / 32] (one per token and 32
+ * channels), V [NB, Hkv, BS / 32, Dv] (one per 32 rows of a page and channel); other caches
+ * the stored value.  Query head hq reads KV head hq / (Hq / Hkv).  Query rows: q [T, Hq, D] with row t
  * at t * q_st; cu_seq_q null: S tokens per sequence, sequence i's at rows i S .. i S + S - 1
  * (T = B S); else rows cu_seq_q[i] .. cu_seq_q[i + 1] - 1 (rows of no sequence untouched).
- * No key: out 0, lse = sink or -inf.  out [T, Hq, D], lse [T, Hq]. */
+ * No key: out 0, lse = sink or -inf.  out [T, Hq, Dv], lse [T, Hq]. */
 int oracle_cached_kv_attn(const void* q, int q_dtype, int64_t q_st, int64_t q_sh,
                           const int32_t* cu_seq_q, int64_t S, int64_t T,
                           const void* k_cache, const void* v_cache, int cache_dtype,
-                          int64_t NB, int64_t Hkv, int64_t BS, int64_t D,
+                          int64_t NB, int64_t Hkv, int64_t BS, int64_t D, int64_t Dv,
+                          int64_t k_row, int64_t v_row,
                           const float* k_scale, const float* v_scale, int scale_mode,
+                          int64_t ks_sb, int64_t ks_sh, int64_t vs_sb, int64_t vs_sh,
                           const int32_t* block_tables, int64_t max_blocks,
                           const int32_t* context_lens, int64_t B, int64_t Hq,
                           const float* alibi, const float* sink, int64_t window_left,
                           double softmax_scale, double* out, double* lse, int nthreads) {
     if (elem_size(q_dtype) == 0 || q_dtype == DT_I8 || elem_size(cache_dtype) == 0) return -2;
-    if (cache_dtype == DT_I8 && scale_mode != 1 && scale_mode != 2) return -3;
-    if (B < 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || BS <= 0 || D <= 0 || max_blocks < 0 ||
-        T < 0 || (!cu_seq_q && (S <= 0 || T != B * S)))
+    if (cache_dtype == DT_I8 && (scale_mode < 1 || scale_mode > 3)) return -3;
+    if (B < 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || BS <= 0 || D <= 0 || Dv <= 0 ||
+        k_row < D || v_row < Dv || max_blocks < 0 || T < 0 ||
+        (!cu_seq_q && (S <= 0 || T != B * S)))
         return -1;
+    if (cache_dtype == DT_I8 && scale_mode == 3 && (D % 32 != 0 || BS % 32 != 0)) return -1;
     sqa_ctx c = {q, q_dtype, q_st, q_sh, cu_seq_q, S, T, k_cache, v_cache, cache_dtype, NB, Hkv,
-                 BS, D, Hq, max_blocks, B, k_scale, v_scale, cache_dtype == DT_I8 ? scale_mode : 0,
+                 BS, D, Dv, k_row, v_row, Hq, max_blocks, B, k_scale, v_scale,
+                 cache_dtype == DT_I8 ? scale_mode : 0, ks_sb, ks_sh, vs_sb, vs_sh,
                  block_tables, context_lens, alibi, sink, window_left, softmax_scale, out, lse};
     parallel_for(T * Hq, nthreads, sqa_range, &c);
     return 0;
@@ -1096,8 +1125,10 @@ int oracle_single_query_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q
                              const int32_t* context_lens, int64_t B, int64_t Hq,
                              const float* alibi, int64_t window_left, double softmax_scale,
                              double* out, double* lse, int nthreads) {
+    if (scale_mode == 3) return -3;
     return oracle_cached_kv_attn(q, q_dtype, q_sb, q_sh, NULL, 1, B < 0 ? 0 : B, k_cache,
-                                 v_cache, cache_dtype, NB, Hkv, BS, D, k_scale, v_scale,
-                                 scale_mode, block_tables, max_blocks, context_lens, B, Hq,
-                                 alibi, NULL, window_left, softmax_scale, out, lse, nthreads);
+                                 v_cache, cache_dtype, NB, Hkv, BS, D, D, D, D, k_scale, v_scale,
+                                 scale_mode, Hkv * BS, BS, Hkv * BS, BS, block_tables,
+                                 max_blocks, context_lens, B, Hq, alibi, NULL, window_left,
+                                 softmax_scale, out, lse, nthreads);
 }

@@ -60,9 +60,10 @@ def lib():
         [ctypes.c_float, INT, INT, I64, P, I64, P]
     L.tmo_hip_attn_workspace_bytes.argtypes = [I64] * 6
     L.tmo_hip_attn_workspace_bytes.restype = I64
-    L.tmo_hip_cached_kv_attn.argtypes = [P, I64, I64, I64, P, I64, I64, P, P, P, P, INT, P, I64,
-                                         P, P, P, P, I64, I64, I64, P, I64, I64, I64] + \
-        [I64] * 8 + [ctypes.c_float, INT, INT, I64, P, I64, P]
+    L.tmo_hip_cached_kv_attn.argtypes = [P, I64, I64, I64, P, I64, I64, P, P, I64, I64, P, P, INT,
+                                         I64, I64, I64, I64, P, I64, P, P, P, P, I64, I64, I64,
+                                         P, I64, I64, I64] + [I64] * 9 + \
+        [ctypes.c_float, INT, INT, I64, P, I64, P]
     L.tmo_hip_cached_kv_attn_workspace_bytes.argtypes = [I64] * 6
     L.tmo_hip_cached_kv_attn_workspace_bytes.restype = I64
     return L
@@ -346,20 +347,31 @@ def test_attention_validation(lib):
 
 
 def test_multi_token_attention_validation(lib):
-    def call(q=FAKE, cu=None, S=4, T=0, B=2, Hq=8, Hkv=2, D=128, splits=1, ws=None, wsb=0,
-             qdt=2, cdt=3, qss=128 * 8, oss=128 * 8, sink=None):
+    def call(q=FAKE, cu=None, S=4, T=0, B=2, Hq=8, Hkv=2, D=128, Dv=128, kdim=128, vdim=128,
+             vc=FAKE, smode=1, ssb=32, BS=16, splits=1, ws=None, wsb=0, qdt=2, cdt=3,
+             qss=128 * 8, oss=128 * 8, sink=None):
         return lib.tmo_hip_cached_kv_attn(
-            q, 4 * 1024, qss, 128, cu, S, T, FAKE, FAKE, FAKE, FAKE, 1, FAKE, 4, FAKE, None,
-            sink, FAKE, 4 * 1024, oss, 128, None, 0, 0, 0, B, Hq, Hkv, D, 16, 16, 64, -1, 0.1,
-            qdt, cdt, splits, ws, wsb, None)
+            q, 4 * 1024, qss, 128, cu, S, T, FAKE, vc, kdim, vdim, FAKE, FAKE, smode, ssb, 16,
+            32, 16, FAKE, 4, FAKE, None, sink, FAKE, 4 * 1024, oss, 128, None, 0, 0, 0, B, Hq,
+            Hkv, D, Dv, 16, BS, 64, -1, 0.1, qdt, cdt, splits, ws, wsb, None)
     assert call(qdt=3) == EDTYPE
+    assert call(smode=4) == EMODE and call(smode=0) == EMODE
     assert call(q=None) == EINVAL
+    assert call(kdim=64) == EINVAL                 # a K row shorter than the key head size
+    assert call(vdim=64) == EINVAL                 # a V row shorter than the value head size
+    assert call(vc=None, kdim=128, Dv=192, B=0) == EINVAL   # one cache: row >= both head sizes
+    assert call(vc=None, kdim=192, Dv=192, B=0) == 0
+    assert call(Dv=600, vdim=600) == EINVAL and call(D=5000, kdim=5000) == EINVAL
+    assert call(ssb=-1) == EINVAL                  # negative per-token scale stride
+    assert call(smode=3, BS=16) == EINVAL          # per-group scales: 32-row pages
+    assert call(smode=3, BS=32, D=48, kdim=48) == EINVAL    # ... and 32-channel groups
+    assert call(smode=3, BS=32, B=0) == 0
     assert call(S=-1) == EINVAL
     assert call(qss=-1) == EINVAL and call(oss=-1) == EINVAL
     assert call(cu=FAKE, T=-1) == EINVAL           # cu_seq_q with a negative row count
     assert call(S=2 ** 31 // 8) == EINVAL          # seq_q * heads beyond 32 bits
     assert call(splits=3) == EINVAL                # splits without a workspace
-    # workspace [batch, kv_heads, splits, seq_q * group, head_size + 2] floats
+    # workspace [batch, kv_heads, splits, seq_q * group, head_size_v + 2] floats
     need = lib.tmo_hip_cached_kv_attn_workspace_bytes(2, 2, 8, 128, 4, 3)
     assert need == 2 * 2 * 3 * 4 * 4 * 130 * 4
     assert lib.tmo_hip_cached_kv_attn_workspace_bytes(2, 2, 8, 128, 1, 3) == \

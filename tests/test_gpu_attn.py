@@ -14,7 +14,10 @@ and off-grid ones (generic kernel), query-head groups 1..16 and 20, block sizes 
 windows, ALiBi, missing pages, long contexts over several splits, 3-D q, and configs[4]'s
 pages with 32 query heads.  Several query tokens per sequence (the 4-D q [batch, seq_q, heads,
 D] and the 3-D q with cu_seq_q, causal within the new tokens) and the sink are held to the
-same bar against the oracle's cached_kv_attn, with rows of no sequence left untouched.
+same bar against the oracle's cached_kv_attn, with rows of no sequence left untouched; so are
+the other cache forms: K and V in one cache (v_cache None, value head size below, equal to or
+above the key's, a 576 / 512 latent-cache shape), value head sizes other than the key's,
+per-group scales and per-token scales with strides in their first two dims.
 """
 import math
 
@@ -29,13 +32,21 @@ RTOL = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10, torch.float32: 2.0
 ATOL = {torch.bfloat16: 2.0 ** -14, torch.float16: 2.0 ** -14, torch.float32: 2.0 ** -16}
 
 
-def _vmax(case, vs):
-    v = case.v_cache.double()
+def _vmax(case, vs, Dv=None):
+    """The largest |v| entry: the first Dv channels of the V cache (of the K cache when the
+    case has none), dequantised."""
+    v = (case.k_cache if case.v_cache is None else case.v_cache).double()
+    if Dv is not None:
+        v = v[..., :Dv]
     if vs is not None:
+        if vs.dim() == 4 and vs.shape[3] == 1:
+            vs = vs[..., 0]
         if vs.dim() == 3:
             v = v * vs.double()[..., None]
         elif vs.dim() == 2:
             v = v * vs.double()[None, :, None, :]
+        elif vs.dim() == 4:                           # per group of 32 rows
+            v = v * vs.double().repeat_interleave(32, dim=2)
         else:
             v = v * float(vs)
     return float(v.abs().max())
@@ -167,18 +178,24 @@ def test_attn_decode_on_configs4_pages(tmo, ref, dev):
 
 
 def run_attn_mq(tmo, ref, dev, case, q, cu=None, sink=None, scale=0.0883883, window=-1,
-                max_seq_q=-1, max_ctx=None, with_lse=True):
+                max_seq_q=-1, max_ctx=None, with_lse=True, Dv=None):
     """Several query tokens per sequence: q [B, S, Hq, D] or [T, Hq, D] with cu.  The output
-    starts as a sentinel, which rows of no sequence must keep."""
+    ([..., Dv], Dv the V cache's head size or q's by default) starts as a sentinel, which rows
+    of no sequence must keep.  case.v_cache None: K and V in one cache."""
     kbit = 8 if case.k_cache.dtype == torch.int8 else -1
+    Dv = Dv or (case.v_cache.shape[-1] if case.v_cache is not None else q.shape[-1])
+    cpu = lambda t: t.cpu() if t is not None else None            # noqa: E731
+    on_dev = lambda t: t if t is None or t.is_cuda else t.to(dev)  # noqa: E731  (views kept)
+    ks, vs = cpu(case.k_scale), cpu(case.v_scale)
     want, wlse = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables,
-                                    case.context_lens, scale, case.k_scale, case.v_scale,
-                                    case.alibi, window, cu_seq_q=cu, sink=sink)
-    out = torch.full(q.shape, 7.0, dtype=q.dtype, device=dev)
+                                    case.context_lens, scale, ks, vs, case.alibi, window,
+                                    cu_seq_q=cu, sink=sink, head_size_v=Dv)
+    out = torch.full(q.shape[:-1] + (Dv,), 7.0, dtype=q.dtype, device=dev)
     res = tmo.single_query_cached_kv_attn(
-        q.to(dev), case.k_cache.to(dev), case.v_cache.to(dev), out, case.block_tables.to(dev),
-        case.context_lens.to(dev), case.k_scale.to(dev) if case.k_scale is not None else None,
-        case.v_scale.to(dev) if case.v_scale is not None else None,
+        q.to(dev), case.k_cache.to(dev),
+        case.v_cache.to(dev) if case.v_cache is not None else None, out,
+        case.block_tables.to(dev), case.context_lens.to(dev), on_dev(case.k_scale),
+        on_dev(case.v_scale),
         case.alibi.to(dev) if case.alibi is not None else None,
         case.max_context_len if max_ctx is None else max_ctx, window, -1, scale,
         return_lse=with_lse, kv_cache_quant_bit_size=kbit,
@@ -188,7 +205,7 @@ def run_attn_mq(tmo, ref, dev, case, q, cu=None, sink=None, scale=0.0883883, win
     got = out.cpu().double()
     held = ~want.isnan()
     assert (got[~held] == 7.0).all(), "a row of no sequence was written"
-    vmax = _vmax(case, case.v_scale)
+    vmax = _vmax(case, vs, Dv)
     err = (got - want).abs()
     lim = RTOL[q.dtype] * want.abs() + ATOL[q.dtype] * vmax
     bad = (err > lim) & held
@@ -292,3 +309,80 @@ def test_attn_multi_token_on_configs4_pages(tmo, ref, dev):
     q = torch.randn(len(sel), 4, 32, 128, generator=g).to(torch.bfloat16)
     case = W.AttnCase(q[:, 0], kc, vc, ks, vs, bt2, ctx)
     run_attn_mq(tmo, ref, dev, case, q, sink=torch.linspace(-1.0, 3.0, 32))
+
+
+def _one_cache(case, D, Dv, seed):
+    """K and V in one cache of max(D, Dv) channels (_ops.py:828-831): the case's K cache widened
+    with random channels; values are the first Dv channels of each row."""
+    g = torch.Generator().manual_seed(seed)
+    NB, Hkv, BS, Dk = case.k_cache.shape
+    Wd = max(D, Dv)
+    if case.k_cache.dtype == torch.int8:
+        extra = torch.randint(-127, 128, (NB, Hkv, BS, Wd - Dk), generator=g, dtype=torch.int8)
+    else:
+        extra = torch.randn(NB, Hkv, BS, Wd - Dk, generator=g).to(case.k_cache.dtype)
+    kc = torch.cat([case.k_cache, extra], dim=-1) if Wd > Dk else case.k_cache
+    return W.AttnCase(case.q, kc, None, case.k_scale, case.v_scale, case.block_tables,
+                      case.context_lens, case.alibi)
+
+
+@pytest.mark.parametrize("kv", ["int8_token", "plain"])
+@pytest.mark.parametrize("Dv", [128, 64, 192])
+def test_attn_one_kv_cache(tmo, ref, dev, kv, Dv):
+    """v_cache None: equal head sizes run the MFMA kernel on the one cache, others the VALU
+    kernel."""
+    case = W.attn_case(torch.bfloat16, 61, kv=kv, B=4, Hq=8, Hkv=2, D=128, NB=64, max_ctx=200)
+    one = _one_cache(case, 128, Dv, 62)
+    q = W.attn_queries(torch.bfloat16, 63, B=4, Hq=8, D=128, S=2)
+    run_attn_mq(tmo, ref, dev, one, q, Dv=Dv, sink=SINK8)
+    run_attn_mq(tmo, ref, dev, one, q[:, :1], Dv=Dv)
+
+
+def test_attn_latent_cache_shape(tmo, ref, dev):
+    """A latent-cache shape: one KV head of 576 channels holding 512-channel values, 16 query
+    heads, two query tokens (VALU kernel)."""
+    case = W.attn_case(torch.bfloat16, 64, kv="plain", B=2, Hq=16, Hkv=1, D=576, NB=24,
+                       max_ctx=150)
+    one = W.AttnCase(case.q, case.k_cache, None, None, None, case.block_tables,
+                     case.context_lens)
+    q = W.attn_queries(torch.bfloat16, 65, B=2, Hq=16, D=576, S=2)
+    run_attn_mq(tmo, ref, dev, one, q, scale=576 ** -0.5, Dv=512)
+
+
+def test_attn_value_head_size(tmo, ref, dev):
+    case = W.attn_case(torch.float16, 66, kv="int8_token", B=3, Hq=8, Hkv=2, D=128, NB=48,
+                       max_ctx=150)
+    case.v_cache = case.v_cache[..., :64].contiguous()
+    q = W.attn_queries(torch.float16, 67, B=3, Hq=8, D=128, S=3)
+    run_attn_mq(tmo, ref, dev, case, q)
+
+
+@pytest.mark.parametrize("S", [1, 3])
+def test_attn_group_scales(tmo, ref, dev, S):
+    """Per-group scales: K one per token and 32 channels, V one per 32 rows and channel."""
+    case = W.attn_case(torch.bfloat16, 68, kv="int8_group", B=3, Hq=8, Hkv=2, D=128, BS=32,
+                       NB=32, max_ctx=200, alibi=True)
+    q = W.attn_queries(torch.bfloat16, 69, B=3, Hq=8, D=128, S=S)
+    run_attn_mq(tmo, ref, dev, case, q, sink=SINK8)
+
+
+@pytest.mark.parametrize("pad", [4, 3])
+def test_attn_strided_token_scales(tmo, ref, dev, pad):
+    """Per-token scales as a view with strides in the first two dims (pages padded by `pad`
+    scales, heads outermost): strides in multiples of four keep the MFMA kernel's vector
+    loads, others take the VALU kernel; no copy either way."""
+    case = W.attn_case(torch.bfloat16, 70, kv="int8_token", B=4, Hq=8, Hkv=2, D=128, NB=64,
+                       max_ctx=200)
+    NB, Hkv, BS = case.k_scale.shape
+    views = []
+    for sc in (case.k_scale, case.v_scale):
+        big = torch.rand(Hkv, NB, BS + pad)
+        big[:, :, :BS] = sc.transpose(0, 1)
+        # the view is built on the device (a copy of a view to the device would be contiguous)
+        views.append(big.to(dev).transpose(0, 1)[:, :, :BS])
+    assert views[0].stride() == (BS + pad, NB * (BS + pad), 1)
+    assert torch.equal(views[0].cpu(), case.k_scale)
+    q = W.attn_queries(torch.bfloat16, 71, B=4, Hq=8, D=128, S=2)
+    strided = W.AttnCase(case.q, case.k_cache, case.v_cache, *views, case.block_tables,
+                         case.context_lens)
+    run_attn_mq(tmo, ref, dev, strided, q)

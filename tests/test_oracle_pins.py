@@ -1213,21 +1213,25 @@ def test_attn_closed_forms(ref):
     assert torch.allclose(out[0], V[-1].expand(2, 16), rtol=0, atol=1e-300)
 
 
-def torch_attn_mq(case, q, scale, window=-1, cu=None, sink=None):
+def torch_attn_mq(case, q, scale, window=-1, cu=None, sink=None, Dv=None):
     """_ops.py:786-800 for several query tokens per sequence, in float64 by torch: every
     sequence's keys dequantised through its block table, a [heads, tokens, keys] logit matrix
     with query token s of nq at position P = L - nq + s seeing keys j in [P - window, P], ALiBi
     slope * (j - P), the sink as an extra logit column whose value row is zero.  q [B, S, Hq,
-    D], or [T, Hq, D] with cu [B + 1]; returns out / lse shaped like q's leading dims (rows of
-    no sequence NaN)."""
-    kc, vc, bt = case.k_cache, case.v_cache, case.block_tables
-    NB, Hkv, BS, D = kc.shape
+    D], or [T, Hq, D] with cu [B + 1]; keys the first D channels of k_cache rows, values the
+    first Dv of v_cache rows (k_cache's when v_cache is None); returns out / lse shaped like
+    q's leading dims (rows of no sequence NaN)."""
+    kc, bt = case.k_cache, case.block_tables
+    vc = kc if case.v_cache is None else case.v_cache
+    NB, Hkv, BS, _ = kc.shape
+    D = q.shape[-1]
+    Dv = Dv or (D if case.v_cache is None else vc.shape[3])
     B = case.context_lens.shape[0]
     Hq = q.shape[-2]
     g = Hq // Hkv
     qf = q.reshape(-1, Hq, D).double()
     T = qf.shape[0]
-    out = torch.full((T, Hq, D), float("nan"), dtype=torch.float64)
+    out = torch.full((T, Hq, Dv), float("nan"), dtype=torch.float64)
     lse = torch.full((T, Hq), float("nan"), dtype=torch.float64)
     for i in range(B):
         r0, nq = (i * q.shape[1], q.shape[1]) if cu is None else (int(cu[i]), int(cu[i + 1] - cu[i]))
@@ -1238,16 +1242,22 @@ def torch_attn_mq(case, q, scale, window=-1, cu=None, sink=None):
         blk, row = bt[i, j // BS].long(), j % BS
         keep = (blk >= 0) & (blk < NB)
         K = torch.zeros(j.numel(), Hkv, D, dtype=torch.float64)
-        V = torch.zeros_like(K)
+        V = torch.zeros(j.numel(), Hkv, Dv, dtype=torch.float64)
         b, r = blk[keep], row[keep]
-        K[keep], V[keep] = kc[b, :, r].double(), vc[b, :, r].double()
-        if case.k_scale is not None:
-            if case.k_scale.dim() == 3:
-                K[keep] *= case.k_scale[b, :, r].double()[..., None]
-                V[keep] *= case.v_scale[b, :, r].double()[..., None]
-            else:
-                K[keep] *= case.k_scale.double()[None]
-                V[keep] *= case.v_scale.double()[None]
+        K[keep], V[keep] = kc[b, :, r, :D].double(), vc[b, :, r, :Dv].double()
+        ks, vs = case.k_scale, case.v_scale
+        if ks is not None:
+            if ks.dim() == 4 and ks.shape[3] == 1:
+                ks, vs = ks[..., 0], vs[..., 0]
+            if ks.dim() == 3:                                   # per token
+                K[keep] *= ks[b, :, r].double()[..., None]
+                V[keep] *= vs[b, :, r].double()[..., None]
+            elif ks.dim() == 2:                                 # per channel
+                K[keep] *= ks.double()[None]
+                V[keep] *= vs.double()[None]
+            else:                                               # per group of 32
+                K[keep] *= ks[b, :, r].double().repeat_interleave(32, dim=-1)
+                V[keep] *= vs[b, :, r // 32].double()
         K, V = K.repeat_interleave(g, dim=1), V.repeat_interleave(g, dim=1)   # [L, Hq, D]
         s = torch.einsum("thd,jhd->htj", qf[r0:r0 + nq], K) * scale             # [Hq, nq, L]
         P = L - nq + torch.arange(nq)
@@ -1259,13 +1269,13 @@ def torch_attn_mq(case, q, scale, window=-1, cu=None, sink=None):
         s = s.masked_fill(~ok[None], float("-inf"))
         if sink is not None:
             s = torch.cat([s, sink.double()[:, None, None].expand(Hq, nq, 1)], dim=-1)
-            V = torch.cat([V, torch.zeros(1, Hq, D, dtype=torch.float64)], dim=0)
+            V = torch.cat([V, torch.zeros(1, Hq, Dv, dtype=torch.float64)], dim=0)
         l = torch.logsumexp(s, dim=-1)                                           # [Hq, nq]
         p = torch.exp(s - l[..., None]).nan_to_num(0.0)
         out[r0:r0 + nq] = torch.einsum("htj,jhd->thd", p, V)
         lse[r0:r0 + nq] = l.transpose(0, 1)
     if cu is None:
-        return out.reshape(q.shape[:2] + (Hq, D)), lse.reshape(q.shape[:2] + (Hq,))
+        return out.reshape(q.shape[:2] + (Hq, Dv)), lse.reshape(q.shape[:2] + (Hq,))
     return out, lse
 
 
@@ -1339,3 +1349,86 @@ def test_attn_multi_token_forms(ref):
                                     sink=sink)
         assert torch.equal(out[a:b], o1[0]) and torch.equal(lse[a:b], l1[0])
     assert out[-2:].isnan().all() and lse[-2:].isnan().all()
+
+
+def _shared_cache(case, D, Dv, seed):
+    """The case's K cache widened to max(D, Dv) channels (new channels random), V dropped: the
+    value is the first Dv channels of each K row (_ops.py:828-831)."""
+    g = torch.Generator().manual_seed(seed)
+    NB, Hkv, BS, Dk = case.k_cache.shape
+    W_ = max(D, Dv)
+    if case.k_cache.dtype == torch.int8:
+        extra = torch.randint(-127, 128, (NB, Hkv, BS, W_ - Dk), generator=g, dtype=torch.int8)
+    else:
+        extra = torch.randn(NB, Hkv, BS, W_ - Dk, generator=g).to(case.k_cache.dtype)
+    return W.AttnCase(case.q, torch.cat([case.k_cache, extra], dim=-1), None, case.k_scale,
+                      case.v_scale, case.block_tables, case.context_lens, case.alibi)
+
+
+@pytest.mark.parametrize("kv", ["int8_token", "int8_channel", "int8_group", "plain"])
+def test_attn_cache_forms_match_torch_float64(ref, kv):
+    """K and V in one cache (v_cache None, value head size below, equal to or above the key's),
+    separate caches of different head sizes, per-group scales, per-token scales with strides
+    in the first two dims -- against torch in float64."""
+    D = 64
+    case = W.attn_case(torch.bfloat16, 51, kv=kv, B=4, Hq=8, Hkv=2, D=D, BS=32, NB=24,
+                       max_ctx=150)
+    q = W.attn_queries(torch.bfloat16, 52, B=4, Hq=8, D=D, S=2)
+    sink = torch.linspace(-1.0, 2.0, 8)
+    for Dv in (32, 64, 96):
+        if kv == "int8_channel" and Dv != D:
+            continue                       # per-channel V scales are [Hkv, Dv]: built below
+        if kv == "int8_group" and Dv > D:
+            continue
+        sh = _shared_cache(case, D, Dv, 53)
+        if kv == "int8_group":
+            sh.v_scale = case.v_scale[..., :Dv].contiguous()
+        out, lse = ref.cached_kv_attn(q, sh.k_cache, None, sh.block_tables, sh.context_lens,
+                                      0.125, sh.k_scale, sh.v_scale, None, -1, sink=sink,
+                                      head_size_v=Dv)
+        want, wlse = torch_attn_mq(sh, q, 0.125, sink=sink, Dv=Dv)
+        assert torch.allclose(out, want, rtol=1e-12, atol=1e-12)
+        assert torch.allclose(lse, wlse, rtol=1e-12, atol=1e-12)
+    if kv in ("int8_token", "plain"):      # separate V cache of 40 channels
+        vc = case.v_cache[..., :40].contiguous()
+        c2 = W.AttnCase(case.q, case.k_cache, vc, case.k_scale, case.v_scale, case.block_tables,
+                        case.context_lens)
+        out, _ = ref.cached_kv_attn(q, c2.k_cache, vc, c2.block_tables, c2.context_lens, 0.125,
+                                    c2.k_scale, c2.v_scale)
+        want, _ = torch_attn_mq(c2, q, 0.125)
+        assert out.shape[-1] == 40 and torch.allclose(out, want, rtol=1e-12, atol=1e-12)
+    if kv == "int8_token":                 # strided per-token scales
+        NB, Hkv, BS = case.k_scale.shape
+        big = torch.rand(Hkv, NB, BS + 7, generator=torch.Generator().manual_seed(54))
+        big[:, :, :BS] = case.k_scale.transpose(0, 1)
+        ks = big.transpose(0, 1)[:, :, :BS]                  # strides (BS + 7, NB (BS + 7), 1)
+        assert not ks.is_contiguous()
+        out, lse = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables,
+                                      case.context_lens, 0.125, ks, case.v_scale[..., None])
+        o0, l0 = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables,
+                                    case.context_lens, 0.125, case.k_scale, case.v_scale)
+        assert torch.equal(out, o0) and torch.equal(lse, l0)
+
+
+def test_attn_cache_form_identities(ref):
+    """v_cache None with equal head sizes is v_cache = k_cache; per-group scales equal across
+    a token's groups (K) and across a 32-row group's channels (V) give the per-token result bit
+    for bit."""
+    case = W.attn_case(torch.float16, 55, kv="int8_token", B=3, Hq=8, Hkv=2, D=64, BS=32,
+                       NB=16, max_ctx=120)
+    q = W.attn_queries(torch.float16, 56, B=3, Hq=8, D=64, S=3)
+    a = ref.cached_kv_attn(q, case.k_cache, None, case.block_tables, case.context_lens, 0.1,
+                           case.k_scale, case.v_scale)
+    b = ref.cached_kv_attn(q, case.k_cache, case.k_cache, case.block_tables, case.context_lens,
+                           0.1, case.k_scale, case.v_scale)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    NB, Hkv, BS = case.k_scale.shape
+    vs_tok = case.v_scale.reshape(NB, Hkv, BS // 32, 32)[..., :1].expand(NB, Hkv, BS // 32, 32)
+    vs_tok = vs_tok.reshape(NB, Hkv, BS).contiguous()          # constant over 32-row groups
+    ks_grp = case.k_scale[..., None].expand(NB, Hkv, BS, 2).contiguous()
+    vs_grp = vs_tok.reshape(NB, Hkv, BS // 32, 32)[..., 0:1].expand(NB, Hkv, BS // 32, 64).contiguous()
+    a = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables, case.context_lens,
+                           0.1, ks_grp, vs_grp)
+    b = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables, case.context_lens,
+                           0.1, case.k_scale, vs_tok)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])

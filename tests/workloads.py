@@ -339,7 +339,8 @@ class AttnCase:
     q: torch.Tensor                  # [B, Hq, D]
     k_cache: torch.Tensor            # [NB, Hkv, BS, D]
     v_cache: torch.Tensor
-    k_scale: Optional[torch.Tensor]  # int8 caches: [NB, Hkv, BS] per token or [Hkv, D] per channel
+    k_scale: Optional[torch.Tensor]  # int8: [NB, Hkv, BS] per token, [Hkv, D] per channel, or
+                                     # per group K [NB, Hkv, BS, D / 32], V [NB, Hkv, BS / 32, D]
     v_scale: Optional[torch.Tensor]
     block_tables: torch.Tensor       # [B, max_blocks] int32
     context_lens: torch.Tensor       # [B] int32
@@ -354,7 +355,8 @@ def attn_case(dtype, seed: int, kv: str = "int8_token", B: int = 5, Hq: int = 8,
               D: int = 128, BS: int = 16, NB: int = 64, max_ctx: int = 200,
               alibi: bool = False) -> AttnCase:
     """Decode attention inputs: q ~ N(0, 1) in `dtype`; caches int8 (`kv` "int8_token" /
-    "int8_channel", codes uniform in [-127, 127] with scales ~U[0.005, 0.03)) or of q's dtype
+    "int8_channel" / "int8_group", codes uniform in [-127, 127] with scales ~U[0.005, 0.03))
+    or of q's dtype
     (`kv` "plain", N(0, 1)); context lengths in [1, max_ctx] (the first max_ctx, one 1); each
     sequence's pages a random choice of distinct blocks."""
     g = torch.Generator().manual_seed(seed)
@@ -370,9 +372,11 @@ def attn_case(dtype, seed: int, kv: str = "int8_token", B: int = 5, Hq: int = 8,
     if kv.startswith("int8"):
         kc = torch.randint(-127, 128, (NB, Hkv, BS, D), generator=g, dtype=torch.int8)
         vc = torch.randint(-127, 128, (NB, Hkv, BS, D), generator=g, dtype=torch.int8)
-        shape = (NB, Hkv, BS) if kv == "int8_token" else (Hkv, D)
+        shape = {"int8_token": (NB, Hkv, BS), "int8_channel": (Hkv, D),
+                 "int8_group": (NB, Hkv, BS, D // 32)}[kv]
         ks = 0.005 + 0.025 * torch.rand(shape, generator=g)
-        vs = 0.005 + 0.025 * torch.rand(shape, generator=g)
+        vshape = (NB, Hkv, BS // 32, D) if kv == "int8_group" else shape
+        vs = 0.005 + 0.025 * torch.rand(vshape, generator=g)
     else:
         kc = torch.randn(NB, Hkv, BS, D, generator=g).to(dtype)
         vc = torch.randn(NB, Hkv, BS, D, generator=g).to(dtype)
