@@ -187,26 +187,33 @@ __device__ __forceinline__ bool locate(const LinParams& p, const Seq& s, int64_t
   return r >= 0 && r < p.rows && crow >= 0;
 }
 
-// Token-major write launches (packed input, no context_seq_offset): the grid walks the token
-// rows themselves, so a row's load address needs no per-sequence number; the sequence is found
-// while the row loads are in flight.  With at most 64 sequences the per-sequence numbers are
-// read into lanes before the row loads (TmSeqs: lane l holds cu[l], cache_seq_offset[l] and
-// cache_bs_id[l]), so the only wait in front of the lookup is for those L2-resident values
-// (the memory counter is in order: loads issued after the row loads would wait for the rows
-// too); with more sequences the lookup reads them after the row loads.
+// Token-major write launches (packed input, no context_seq_offset, at most 63 sequences): the
+// grid walks the token rows themselves, so a row's load address needs no per-sequence number;
+// the sequence is found while the row loads are in flight.  The per-sequence numbers are read
+// into lanes first (lane l holds cu[l], cache_seq_offset[l] and cache_bs_id[l]) with
+// unconditional loads, then the row loads are issued, also unconditionally: the code between
+// them is straight-line, so the only wait in front of the lookup is for the first three loads
+// (the memory counter is in order and the compiler counts the row loads issued after them).
+// With a branch among these loads the compiler waited for every load there, and the lookup ran
+// after the row data had arrived (quant_to_linear_cache, 8 x 4096 tokens: 2.4 us of the
+// kernel's 41 us).
 struct TmSeqs {
   int32_t cu, off, id;
 };
 __device__ __forceinline__ TmSeqs tm_prefetch(const LinParams& p) {
   const int lane = threadIdx.x & (kWave - 1);
-  TmSeqs t{0, 0, 0};
-  if (p.batch <= kWave - 1) {  // one value per lane, from clamped (in-bounds) addresses
-    const int k = lane <= p.batch ? lane : 0;      // cu has batch + 1 entries
-    const int ks = lane < p.batch ? lane : 0;      // the per-sequence arrays have batch
-    t.cu = p.lens[k];
-    t.off = p.cache_off ? p.cache_off[ks] : 0;
-    t.id = p.bs_id ? p.bs_id[ks] : lane;
-  }
+  const int k = lane <= p.batch ? lane : 0;   // cu has batch + 1 entries
+  const int ks = lane < p.batch ? lane : 0;   // the per-sequence arrays have batch
+  // an absent array reads cu instead (the value is discarded in tm_locate); the pointers are
+  // device pointers, read through the global address space (a selected generic pointer would
+  // compile to a flat load, which the compiler waits for together with every other load)
+  typedef const __attribute__((address_space(1))) int32_t* gptr;
+  const gptr offp = (gptr)(p.cache_off ? p.cache_off : p.lens);
+  const gptr idp = (gptr)(p.bs_id ? p.bs_id : p.lens);
+  TmSeqs t;
+  t.cu = ((gptr)p.lens)[k];
+  t.off = offp[ks];
+  t.id = idp[ks];
   return t;
 }
 
@@ -220,38 +227,20 @@ __device__ __forceinline__ bool tm_locate(const LinParams& p, const TmSeqs& t, i
                                           int h, int64_t& crow, int64_t& pos) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t r = rbase + lane / G;
-  int64_t i, c0, c1, off, id;
-  if (p.batch <= kWave - 1) {
-    int cnt = 0;
+  int cnt = 0;
 #pragma unroll
-    for (int q = 0; q < kWave / G; ++q) {
-      const uint64_t hit = __ballot(lane >= 1 && lane <= p.batch && (int64_t)t.cu <= rbase + q);
-      if (q == lane / G) cnt = __popcll(hit);
-    }
-    i = cnt;
-    c0 = __shfl(t.cu, cnt, kWave);
-    c1 = __shfl(t.cu, cnt + 1 < kWave ? cnt + 1 : cnt, kWave);
-    off = __shfl(t.off, cnt, kWave);
-    id = __shfl(t.id, cnt, kWave);
-    if (i >= p.batch) return false;
-  } else {
-    int64_t cnt = 0;
-    for (int64_t k0 = 1; k0 <= p.batch; k0 += kWave) {
-      const int64_t k = k0 + lane;
-      const int32_t ck = k <= p.batch ? p.lens[k] : 0x7fffffff;
-#pragma unroll
-      for (int q = 0; q < kWave / G; ++q) {
-        const uint64_t hit = __ballot((int64_t)ck <= rbase + q);
-        if (q == lane / G) cnt += __popcll(hit);
-      }
-    }
-    i = cnt;
-    if (i >= p.batch) return false;
-    c0 = p.lens[i];
-    c1 = p.lens[i + 1];
-    off = p.cache_off ? p.cache_off[i] : 0;
-    id = p.bs_id ? p.bs_id[i] : i;
+  for (int q = 0; q < kWave / G; ++q) {
+    const uint64_t hit = __ballot(lane >= 1 && lane <= p.batch && (int64_t)t.cu <= rbase + q);
+    if (q == lane / G) cnt = __popcll(hit);
   }
+  const int64_t i = cnt;
+  const int64_t c0 = __shfl(t.cu, cnt, kWave);
+  const int64_t c1 = __shfl(t.cu, cnt + 1 < kWave ? cnt + 1 : cnt, kWave);
+  const int32_t off_i = __shfl(t.off, cnt, kWave);
+  const int32_t id_i = __shfl(t.id, cnt, kWave);
+  if (i >= p.batch) return false;
+  const int64_t off = p.cache_off ? (int64_t)off_i : 0;
+  const int64_t id = p.bs_id ? (int64_t)id_i : i;
   const int64_t j = r - c0;
   int64_t len = c1 - c0;
   if (len > p.max_len) len = p.max_len;
@@ -458,14 +447,16 @@ __global__ __launch_bounds__(256) void lin_quant(LinParams p) {
   Raw8<Tag> x[kLinT][2];
   if constexpr (kTM) {  // the grid over the token rows: loads first, the sequence afterwards
     const TmSeqs seqs = tm_prefetch(p);
+    // unconditional row loads, as in lin_copy
+    const void* vsrc = p.nkv > 1 ? p.tok[1] : p.tok[0];
+    const int64_t vst = p.nkv > 1 ? p.st[1] : p.st[0], vsh = p.nkv > 1 ? p.sh[1] : p.sh[0];
 #pragma unroll
     for (int t = 0; t < kLinT; ++t) {
       r[t] = j0 + t * kRows;
       ok[t] = r[t] < p.rows;
-      if (!ok[t]) continue;
-#pragma unroll
-      for (int kv = 0; kv < 2; ++kv)
-        if (kv < p.nkv) x[t][kv] = load8<Tag>(p.tok[kv], r[t] * p.st[kv] + (int64_t)h * p.sh[kv] + d0);
+      const int64_t rl = ok[t] ? r[t] : 0;
+      x[t][0] = load8<Tag>(p.tok[0], rl * p.st[0] + (int64_t)h * p.sh[0] + d0);
+      x[t][1] = load8<Tag>(vsrc, rl * vst + (int64_t)h * vsh + d0);
     }
     const int64_t wbase = tile * (kRows * kLinT) + (threadIdx.x / kWave) * (kWave / G);
 #pragma unroll
@@ -708,7 +699,8 @@ int grid_for(const LinParams& p, int64_t batch, int rows_per_wg, dim3& grid) {
 bool token_major_grid(const LinParams& p, int rows_per_wg, dim3& grid) {
   // packed input only: a padded layout with a length past seqlen would give that sequence
   // rows of the next one, which a row-to-sequence mapping cannot reproduce
-  if (!TMO_LIN_TOKEN_MAJOR || !p.in_dir || p.seq_off || p.block_tables || !p.packed)
+  if (!TMO_LIN_TOKEN_MAJOR || !p.in_dir || p.seq_off || p.block_tables || !p.packed ||
+      p.batch > kWave - 1)
     return false;
   // whole groups of 8 tiles for the XCD-aware order (tiles past the rows do nothing)
   const int64_t gx = xcd_grid_tiles((p.rows + rows_per_wg - 1) / rows_per_wg) * p.heads;

@@ -69,12 +69,13 @@ constexpr int kTokensPerThread = TMO_QUANT_TOKENS_PER_THREAD;
 // Vector path: head_dim == G * V * Tag::kPerVec, 16-byte aligned rows.  A row is G lanes,
 // each holding V 16-byte vectors (lane l of the group owns vectors l, l + G, ...), so the
 // per-row work -- the amax reduction, the scale and its reciprocal -- is shared by V * kPerVec
-// elements per lane.  A workgroup owns kTokensPerThread * 256/G consecutive tokens of one head.
+// elements per lane.  A workgroup (256 threads, or 64 for decode-sized launches, see launch())
+// owns kTokensPerThread * blockDim.x / G consecutive tokens of one head.
 // Every load of the lane group (slots, K rows, V rows) is issued before the first wait: the
 // input address does not depend on the slot, only the store address does.
 template <class Tag, int G, int V, bool kFp8>
 __global__ __launch_bounds__(256) void quant_paged_vec(QuantPagedParams p) {
-  constexpr int kGroups = 256 / G;  // lane groups per workgroup
+  const int kGroups = blockDim.x / G;  // lane groups per workgroup
   constexpr int kPer = Tag::kPerVec;
   constexpr int kT = kTokensPerThread;
   const int lane = threadIdx.x & (G - 1);
@@ -404,7 +405,18 @@ int launch(const QuantPagedParams& p, hipStream_t stream) {
   // V vectors per lane when the row has at least 4 * V of them, else one
   const int V = (vec && nvec >= 4 * TMO_QUANT_VEC_PER_LANE) ? TMO_QUANT_VEC_PER_LANE : 1;
   const int G = vec ? nvec / V : kWave;
-  const int rows = vec ? (256 / G) * kTokensPerThread : 256 / kWave;
+  // Decode-sized launches (fewer than two 256-thread workgroups per CU of a 256-CU part) use
+  // 64-thread workgroups: four times as many workgroups spread the row loads and the
+  // scattered page stores over more CUs.  configs[1] (256 tokens x 8 heads, 128 -> 512
+  // workgroups) 3.58 -> 3.43 us per call, configs[0] 3.15 -> 2.88 us on MI355X; prefill-sized
+  // launches lose with small workgroups (configs[2]: 35.6 -> 38.9 us), so they keep 256.
+  int wg = 256;
+  if (vec && G <= 64) {
+    const int64_t tiles256 = (p.num_tokens + (256 / G) * kTokensPerThread - 1) /
+                             ((256 / G) * kTokensPerThread);
+    if (tiles256 * p.heads < 512) wg = 64;
+  }
+  const int rows = vec ? (wg / G) * kTokensPerThread : 256 / kWave;
   const int64_t tiles = (p.num_tokens + rows - 1) / rows;
   const int64_t blocks = tiles * p.heads;
   // the vector kernel's XCD-aware order takes whole groups of 8 tiles (extra tiles have no
@@ -413,9 +425,9 @@ int launch(const QuantPagedParams& p, hipStream_t stream) {
   if (vec_blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
   const dim3 block(256);
   if (!vec) return launch_kernel(quant_paged_generic<Tag, kFp8>, dim3((unsigned)blocks), block, stream, p);
-  const dim3 grid((unsigned)vec_blocks);
-  if (V == 1) return launch_vec<Tag, 1, kFp8>(p, G, grid, block, stream);
-  return launch_vec<Tag, TMO_QUANT_VEC_PER_LANE, kFp8>(p, G, grid, block, stream);
+  const dim3 grid((unsigned)vec_blocks), vblock(wg);
+  if (V == 1) return launch_vec<Tag, 1, kFp8>(p, G, grid, vblock, stream);
+  return launch_vec<Tag, TMO_QUANT_VEC_PER_LANE, kFp8>(p, G, grid, vblock, stream);
 }
 
 }  // namespace
