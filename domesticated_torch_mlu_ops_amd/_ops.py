@@ -398,7 +398,12 @@ def quant_to_linear_cache(
     ``[..., group_num]``).  int8 caches: ``scale = fp32(amax) / 127``, ``code =
     clip(round_half_even(x / scale), -128, 127)``; float8_e4m3fn caches: ``scale = fp32(amax) /
     448``, ``code = clip(x / scale, -448, 448)`` rounded to nearest even.  An all-zero group
-    stores scale 0 and codes 0.  ``quant_bit`` must be 8.
+    stores scale 0 and codes 0.  ``quant_bit`` 4 (int8 caches of int4 pairs): ``scale =
+    fp32(amax) / 7``, ``code = clip(round_half_even(x / scale), -8, 7)``, two codes per byte with
+    the even element in the high nibble; ``key_cache`` ``[max_batch, heads, cache_len,
+    head_size / 2]`` pairs channels, ``value_cache`` ``[max_batch, heads, cache_len / 2,
+    head_size]`` pairs cache positions (a position written alone keeps its partner's nibble);
+    ``head_size`` a multiple of 8, at most 512.
 
     Reference: ``_ops.py:1708-1806`` (math ``:1725-1750``).  Returns
     ``(key_cache, value_cache, key_scale, value_scale)`` or ``(key_cache, key_scale)``.
@@ -469,7 +474,10 @@ def dequant_from_linear_cache(
 ) -> None:
     """``key[start_i + j] = (fp32(code) * scale).to(key.dtype)`` from the int8 linear caches,
     ``quant_mode`` 0: scale ``[heads, head_size]``; 1: per-token ``[max_batch, heads,
-    cache_len]``.  ``context_lengths`` holds ``[batch]`` lengths; ``quant_bit`` must be 8.
+    cache_len]``.  ``context_lengths`` holds ``[batch]`` lengths.  ``quant_bit`` 4 reads int4
+    pairs (even element in the high nibble, sign-extended): ``key_cache`` ``[max_batch, heads,
+    cache_len, head_size / 2]`` (channel pairs), ``value_cache`` ``[max_batch, heads, cache_len
+    / 2, head_size]`` (position pairs).
 
     Reference: ``_ops.py:3642-3732`` (math ``:3663-3683``).  Returns None.
     """

@@ -603,6 +603,199 @@ __global__ __launch_bounds__(256) void lin_dequant(LinParams p) {
   }
 }
 
+// ------------------------------------------------------------------------------ 4-bit caches
+
+// int8 caches of signed 4-bit pairs (quant_bit 4, _ops.py:1723-1750, 3664-3700): the even element
+// of a pair in the high nibble, the odd one in the low nibble (the dequant math's unpack[0::2] =
+// byte >> 4, unpack[1::2] = byte << 4 >> 4).  K pairs adjacent channels ([.., cache_len, D / 2]),
+// V pairs adjacent cache positions ([.., cache_len / 2, D]).  scale = RN(amax / 7) (one IEEE
+// divide per row or group), code = clip(RNE(RN(x / scale)), -8, 7).
+struct Scale4 {
+  float s, y;
+  bool fast;
+};
+__device__ __forceinline__ Scale4 make_scale4(float amax) {
+  Scale4 r;
+  r.s = amax / 7.0f;  // IEEE divide, once per row / group
+  const bool normal = r.s >= kFastDivMinScale && r.s < __builtin_inff();
+  r.fast = normal || r.s == 0.0f;  // y = 0 gives quotients +-0 (codes 0) for an all-zero row
+  r.y = normal ? 1.0f / r.s : 0.0f;
+  return r;
+}
+// 4-bit code (two's complement nibble) of x.  On the fast path |x| <= amax bounds |q| by 7, so
+// the clamp to [-8, 7] of the reference math only acts on the IEEE-divide path.
+__device__ __forceinline__ uint32_t nibble4(float x, const Scale4& r) {
+  float q;
+  if (r.fast) {
+    q = div_by_recip(x, r.s, r.y);
+  } else {
+    keep_branch();
+    q = x / r.s;
+  }
+  return rne_bits(__builtin_amdgcn_fmed3f(q, -8.0f, 7.0f)) & 0xFu;
+}
+__device__ __forceinline__ int32_t sext4(uint32_t n) { return ((int32_t)(n << 28)) >> 28; }
+
+// Floor of v / 2 for any sign.
+__device__ __forceinline__ int64_t floor_half(int64_t v) { return v >= 0 ? v / 2 : -((1 - v) / 2); }
+
+// quant_to_linear_cache with quant_bit 4: G lanes per row (a power of two >= head_dim / 8;
+// lanes past the row idle), 8 channels per lane, one lane group per pair of cache positions
+// (2P, 2P + 1) of one head, so the two tokens that share the V bytes are encoded together and
+// every V byte is written by one lane.  A position of the pair outside the sequence's tokens
+// keeps its nibble: the lane reads the V bytes first and writes back the nibble unchanged.
+template <class Tag, int G>
+__global__ __launch_bounds__(256) void lin_quant4(LinParams p) {
+  constexpr int kPairs = 256 / G;
+  const int lane = threadIdx.x & (G - 1);
+  const int64_t i = blockIdx.y;
+  int h;
+  int64_t tile;
+  lin_tile_head<false>(p, h, tile);
+  const Seq s = sequence(p, i);
+  const int d0 = lane * 8;
+  const bool lane_in = d0 < p.head_dim;
+  const int64_t P = floor_half(s.pos0) + tile * kPairs + threadIdx.x / G;
+  const int64_t L = p.block_rows, D = p.head_dim;
+  const int gl = G / p.groups;  // lanes per scale group (power of two)
+  bool tin[2];
+  int64_t r[2], crow[2];
+  Raw8<Tag> x[2][2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int64_t j = 2 * P + e - s.pos0;
+    tin[e] = j >= 0 && locate(p, s, i, h, j, r[e], crow[e]);
+    if (!tin[e] || !lane_in) continue;
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv)
+      if (kv < p.nkv) x[e][kv] = load8<Tag>(p.tok[kv], r[e] * p.st[kv] + (int64_t)h * p.sh[kv] + d0);
+  }
+  if (!tin[0] && !tin[1]) return;  // uniform per lane group; no barrier below
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    if (kv >= p.nkv) continue;
+    uint32_t nib[2][8];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      float v[8];
+      if (tin[e] && lane_in) {
+        unpack8<Tag>(x[e][kv], v);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = 0.0f;
+      }
+      float m = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) m = abs_max(m, v[k]);
+      const float amax = __uint_as_float(lane_group_max<G>(__float_as_uint(m), gl));
+      const Scale4 sc = make_scale4(amax);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) nib[e][k] = nibble4(v[k], sc);
+      if (tin[e] && lane_in && (lane & (gl - 1)) == 0)
+        __builtin_nontemporal_store(sc.s, p.scale[kv] + crow[e] * p.groups + lane / gl);
+      if (kv == 0 && tin[e] && lane_in) {  // K: channel pairs, 4 bytes per lane
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w |= ((nib[e][2 * k] << 4) | nib[e][2 * k + 1]) << (8 * k);
+        store_nt(reinterpret_cast<uint32_t*>(static_cast<int8_t*>(p.cache[0]) + crow[e] * (D / 2) + d0 / 2), w);
+      }
+    }
+    if (kv == 1 && lane_in) {  // V: position pairs, 8 bytes per lane at byte row P
+      const int64_t cr = tin[0] ? crow[0] : crow[1];
+      const int64_t pos = tin[0] ? 2 * P : 2 * P + 1;
+      const int64_t vrow = (cr - pos) / L * (L / 2) + P;  // (batch * H + h) * (L / 2) + P
+      u32x2* dst = reinterpret_cast<u32x2*>(static_cast<int8_t*>(p.cache[1]) + vrow * D + d0);
+      u32x2 old = {0u, 0u};
+      if (!tin[0] || !tin[1]) old = *dst;
+      u32x2 w;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        uint32_t acc = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t ob = (old[q] >> (8 * k)) & 0xFFu;
+          const uint32_t hi = tin[0] ? nib[0][4 * q + k] : ob >> 4;
+          const uint32_t lo = tin[1] ? nib[1][4 * q + k] : ob & 0xFu;
+          acc |= ((hi << 4) | lo) << (8 * k);
+        }
+        w[q] = acc;
+      }
+      *dst = w;
+    }
+  }
+}
+
+// dequant_from_linear_cache with quant_bit 4: G lanes per row, 8 channels per lane, kLinT tokens
+// per lane group; K reads the row's 4 bytes of the lane's channel pairs, V the 8 bytes of byte
+// row pos / 2 and the nibble of the position's parity.
+template <class Tag, int G>
+__global__ __launch_bounds__(256) void lin_dequant4(LinParams p) {
+  constexpr int kRows = 256 / G;
+  const int lane = threadIdx.x & (G - 1);
+  const int64_t i = blockIdx.y;
+  int h;
+  int64_t tile;
+  lin_tile_head<false>(p, h, tile);
+  const int d0 = lane * 8;
+  const bool lane_in = d0 < p.head_dim;
+  const int64_t L = p.block_rows, D = p.head_dim;
+  float chan[2][8];
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    if (kv < p.nkv && p.smode == 0 && lane_in) {
+      const u32x4* sp = reinterpret_cast<const u32x4*>(p.chan[kv] + (int64_t)h * D + d0);
+      const u32x4 a = sp[0], b = sp[1];
+      unpack(F32{}, a, chan[kv]);
+      unpack(F32{}, b, chan[kv] + 4);
+    }
+  }
+  // every lane stays until finish_start (its prefix sum reads across the wavefront)
+  Seq s = sequence(p, i, true);
+  const int64_t j = tile * kRows + threadIdx.x / G;
+  const int64_t crow = j < s.len ? cache_row(p, i, s.pos0 + j, h) : -1;
+  const bool ok = crow >= 0 && lane_in;
+  const int64_t pos = s.pos0 + j;
+  uint32_t kw = 0;
+  u32x2 vw = {0u, 0u};
+  float tsc[2] = {0.0f, 0.0f};
+  if (ok) {
+    kw = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(
+        static_cast<const int8_t*>(p.cache[0]) + crow * (D / 2) + d0 / 2));
+    if (p.nkv > 1) {
+      const int64_t vrow = (crow - pos) / L * (L / 2) + pos / 2;
+      vw = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(
+          static_cast<const int8_t*>(p.cache[1]) + vrow * D + d0));
+    }
+    if (p.smode != 0) {
+      tsc[0] = p.scale[0][crow];
+      if (p.nkv > 1) tsc[1] = p.scale[1][crow];
+    }
+  }
+  finish_start(p, i, s);
+  const int64_t r = s.start + j;
+  if (!ok || r < 0 || r >= p.rows) return;
+  const int vshift = (pos & 1) ? 0 : 4;
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    if (kv >= p.nkv) continue;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint32_t n;
+      if (kv == 0) {
+        const uint32_t byte = (kw >> (8 * (e / 2))) & 0xFFu;
+        n = (e & 1) ? byte & 0xFu : byte >> 4;
+      } else {
+        const uint32_t byte = (vw[e / 4] >> (8 * (e % 4))) & 0xFFu;
+        n = (byte >> vshift) & 0xFu;
+      }
+      const float sc = p.smode == 0 ? chan[kv][e] : tsc[kv];
+      v[e] = (float)sext4(n) * sc;
+    }
+    store8<Tag>(p.tok[kv], r * p.st[kv] + (int64_t)h * p.sh[kv] + d0, v);
+  }
+}
+
 // ------------------------------------------------------------------------------ generic path
 
 // Any head_dim / alignment: one wavefront per (token, head) row, element by element, IEEE
@@ -807,6 +1000,63 @@ int launch_quant(const LinParams& p, int64_t batch, hipStream_t st) {
   }
 }
 
+// 4-bit launches: G = the power of two >= head_dim / 8 lanes per row; 0 when the shape or the
+// alignment is outside the 4-bit kernels (head_dim % 8 != 0 or > 512, scale groups that are not
+// whole aligned lane groups, unaligned tensors, an odd V cache length).
+int lanes4(const LinParams& p, int es) {
+  const int D = p.head_dim;
+  if (D % 8 != 0 || D > 8 * kWave) return 0;
+  int G = 1;
+  while (G * 8 < D) G *= 2;
+  if (p.groups > 1) {  // each group a whole, aligned, power-of-two set of lanes
+    const int gl = G % p.groups == 0 ? G / p.groups : 0;
+    if (G * 8 != D || gl < 1 || (gl & (gl - 1)) != 0) return 0;
+  }
+  if (!token_vec_ok(p, es) || !aligned(p.cache[0], 4)) return 0;
+  if (p.nkv > 1 && (!aligned(p.cache[1], 8) || p.block_rows % 2 != 0)) return 0;
+  for (int kv = 0; kv < p.nkv; ++kv)
+    if (p.smode == 0 && p.chan[kv] && !aligned(p.chan[kv], 16)) return 0;
+  return G;
+}
+
+template <class Tag>
+int launch_quant4(const LinParams& p, int64_t batch, hipStream_t st) {
+  const int G = lanes4(p, Tag::kBytes);
+  if (G == 0) return TMO_ERR_UNSUPPORTED_MODE;
+  // position pairs of a sequence: at most max_len / 2 + 1
+  const int64_t pairs = p.max_len / 2 + 1, per_wg = 256 / G;
+  const int64_t gx = (pairs + per_wg - 1) / per_wg * p.heads;
+  if (gx > 0x7fffffffLL || batch > 65535) return TMO_ERR_INVALID_ARGUMENT;
+  const dim3 grid((unsigned)gx, (unsigned)batch), block(256);
+  switch (G) {
+    case 1: return launch_kernel(lin_quant4<Tag, 1>, grid, block, st, p);
+    case 2: return launch_kernel(lin_quant4<Tag, 2>, grid, block, st, p);
+    case 4: return launch_kernel(lin_quant4<Tag, 4>, grid, block, st, p);
+    case 8: return launch_kernel(lin_quant4<Tag, 8>, grid, block, st, p);
+    case 16: return launch_kernel(lin_quant4<Tag, 16>, grid, block, st, p);
+    case 32: return launch_kernel(lin_quant4<Tag, 32>, grid, block, st, p);
+    default: return launch_kernel(lin_quant4<Tag, 64>, grid, block, st, p);
+  }
+}
+
+template <class Tag>
+int launch_dequant4(const LinParams& p, int64_t batch, hipStream_t st) {
+  const int G = lanes4(p, Tag::kBytes);
+  if (G == 0) return TMO_ERR_UNSUPPORTED_MODE;
+  dim3 grid;
+  const int rc = grid_for(p, batch, 256 / G, grid);
+  if (rc != TMO_OK) return rc;
+  switch (G) {
+    case 1: return launch_kernel(lin_dequant4<Tag, 1>, grid, dim3(256), st, p);
+    case 2: return launch_kernel(lin_dequant4<Tag, 2>, grid, dim3(256), st, p);
+    case 4: return launch_kernel(lin_dequant4<Tag, 4>, grid, dim3(256), st, p);
+    case 8: return launch_kernel(lin_dequant4<Tag, 8>, grid, dim3(256), st, p);
+    case 16: return launch_kernel(lin_dequant4<Tag, 16>, grid, dim3(256), st, p);
+    case 32: return launch_kernel(lin_dequant4<Tag, 32>, grid, dim3(256), st, p);
+    default: return launch_kernel(lin_dequant4<Tag, 64>, grid, dim3(256), st, p);
+  }
+}
+
 template <bool kStatic>
 int dispatch_quant(const LinParams& p, int64_t batch, int dtype, bool fp8, hipStream_t st) {
   switch (dtype) {
@@ -935,7 +1185,8 @@ extern "C" int tmo_hip_quant_to_linear_cache(
     const int32_t* cache_seqlen_offset, int quant_bit, int dtype, int cache_dtype, void* stream) {
   if (!float_dtype(dtype) || (cache_dtype != TMO_DTYPE_I8 && cache_dtype != TMO_DTYPE_F8E4M3))
     return TMO_ERR_UNSUPPORTED_DTYPE;
-  if (quant_bit != 8) return TMO_ERR_UNSUPPORTED_MODE;
+  if (quant_bit != 8 && quant_bit != 4) return TMO_ERR_UNSUPPORTED_MODE;
+  if (quant_bit == 4 && cache_dtype != TMO_DTYPE_I8) return TMO_ERR_UNSUPPORTED_DTYPE;
   if (group_num <= 0 || head_size % group_num != 0) return TMO_ERR_INVALID_ARGUMENT;
   if (!key_scale || ((value != nullptr) != (value_scale != nullptr)))
     return TMO_ERR_INVALID_ARGUMENT;
@@ -950,6 +1201,16 @@ extern "C" int tmo_hip_quant_to_linear_cache(
   p.scale[0] = key_scale;
   p.scale[1] = value_scale;
   p.groups = (int32_t)group_num;
+  if (quant_bit == 4) {
+    if (lanes4(p, dtype == TMO_DTYPE_F32 ? 4 : 2) == 0) return TMO_ERR_UNSUPPORTED_MODE;
+    if (nothing_to_do(p, batch)) return TMO_OK;
+    hipStream_t s4 = static_cast<hipStream_t>(stream);
+    switch (dtype) {
+      case TMO_DTYPE_F16: return launch_quant4<F16>(p, batch, s4);
+      case TMO_DTYPE_BF16: return launch_quant4<BF16>(p, batch, s4);
+      default: return launch_quant4<F32>(p, batch, s4);
+    }
+  }
   if (nothing_to_do(p, batch)) return TMO_OK;
   return dispatch_quant<false>(p, batch, dtype, cache_dtype == TMO_DTYPE_F8E4M3,
                                static_cast<hipStream_t>(stream));
@@ -997,7 +1258,8 @@ extern "C" int tmo_hip_dequant_from_linear_cache(
     const int32_t* context_seq_offset, const int32_t* cache_bs_id, const int32_t* cache_seq_offset,
     int quant_mode, int quant_bit, int out_dtype, void* stream) {
   if (!float_dtype(out_dtype)) return TMO_ERR_UNSUPPORTED_DTYPE;
-  if (quant_bit != 8 || (quant_mode != 0 && quant_mode != 1)) return TMO_ERR_UNSUPPORTED_MODE;
+  if ((quant_bit != 8 && quant_bit != 4) || (quant_mode != 0 && quant_mode != 1))
+    return TMO_ERR_UNSUPPORTED_MODE;
   if (!key_scale || ((value != nullptr) != (value_scale != nullptr)))
     return TMO_ERR_INVALID_ARGUMENT;
   LinParams p{};
@@ -1013,8 +1275,17 @@ extern "C" int tmo_hip_dequant_from_linear_cache(
   p.chan[1] = quant_mode == 0 ? value_scale : nullptr;
   p.scale[0] = quant_mode == 1 ? const_cast<float*>(key_scale) : nullptr;
   p.scale[1] = quant_mode == 1 ? const_cast<float*>(value_scale) : nullptr;
+  if (quant_bit == 4 && lanes4(p, out_dtype == TMO_DTYPE_F32 ? 4 : 2) == 0)
+    return TMO_ERR_UNSUPPORTED_MODE;
   if (nothing_to_do(p, batch)) return TMO_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (quant_bit == 4) {
+    switch (out_dtype) {
+      case TMO_DTYPE_F16: return launch_dequant4<F16>(p, batch, s);
+      case TMO_DTYPE_BF16: return launch_dequant4<BF16>(p, batch, s);
+      default: return launch_dequant4<F32>(p, batch, s);
+    }
+  }
   switch (out_dtype) {
     case TMO_DTYPE_F16: return launch_dequant<F16>(p, batch, s);
     case TMO_DTYPE_BF16: return launch_dequant<BF16>(p, batch, s);

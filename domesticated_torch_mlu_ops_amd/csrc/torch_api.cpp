@@ -659,24 +659,56 @@ struct KvPair {
   bool has_v;
 };
 
+// 4-bit linear caches (int8 holding int4 pairs): key_cache [max_batch, heads, cache_len,
+// head_size / 2] (channel pairs), value_cache [max_batch, heads, cache_len / 2, head_size]
+// (position pairs), both int8 (reference _ops.py:3690-3697).
+void check_linear_cache4(const at::Tensor& kc, const c10::optional<at::Tensor>& vc,
+                         const at::Tensor& ref, int64_t H, int64_t D) {
+  check_device(kc, ref, "key_cache");
+  TORCH_CHECK(D % 2 == 0, "quant_bit 4 needs an even head_size, got ", D);
+  TORCH_CHECK(kc.dim() == 4 && kc.is_contiguous() && kc.scalar_type() == at::kChar,
+              "key_cache must be a contiguous int8 [max_batch, heads, cache_len, head_size / 2] "
+              "tensor for quant_bit 4, got ", kc.sizes(), " ", kc.scalar_type());
+  TORCH_CHECK(kc.size(1) == H && kc.size(3) * 2 == D, "key_cache ", kc.sizes(),
+              " does not match [heads, head_size / 2] = [", H, ", ", D / 2, "] for quant_bit 4");
+  if (vc.has_value()) {
+    check_device(*vc, ref, "value_cache");
+    TORCH_CHECK(vc->dim() == 4 && vc->is_contiguous() && vc->scalar_type() == at::kChar,
+                "value_cache must be a contiguous int8 [max_batch, heads, cache_len / 2, "
+                "head_size] tensor for quant_bit 4, got ", vc->sizes(), " ", vc->scalar_type());
+    TORCH_CHECK(vc->size(0) == kc.size(0) && vc->size(1) == H && vc->size(2) * 2 == kc.size(2) &&
+                    vc->size(3) == D,
+                "value_cache ", vc->sizes(), " must be [max_batch, heads, cache_len / 2, "
+                "head_size] = [", kc.size(0), ", ", H, ", ", kc.size(2) / 2, ", ", D,
+                "] for quant_bit 4 (cache_len even)");
+  }
+}
+
 KvPair write_rows(const at::Tensor& key, const c10::optional<at::Tensor>& value,
-                  const at::Tensor& key_cache, const c10::optional<at::Tensor>& value_cache) {
+                  const at::Tensor& key_cache, const c10::optional<at::Tensor>& value_cache,
+                  int64_t bits = 8) {
   KvPair kv;
   check_device(key, key, "key");
   kv.k = token_rows(key, true, "key");
   kv.has_v = value.has_value();
   TORCH_CHECK(kv.has_v == value_cache.has_value(),
               "value and value_cache must both be given or both be None");
-  check_linear_cache(key_cache, key, kv.k.H, kv.k.D, "key_cache");
+  if (bits == 4) {
+    check_linear_cache4(key_cache, value_cache, key, kv.k.H, kv.k.D);
+  } else {
+    check_linear_cache(key_cache, key, kv.k.H, kv.k.D, "key_cache");
+  }
   if (kv.has_v) {
     check_device(*value, key, "value");
     TORCH_CHECK(value->sizes() == key.sizes() && value->scalar_type() == key.scalar_type(),
                 "value must match key");
     kv.v = token_rows(*value, true, "value");
-    check_linear_cache(*value_cache, key, kv.k.H, kv.k.D, "value_cache");
-    TORCH_CHECK(value_cache->sizes() == key_cache.sizes() &&
-                    value_cache->scalar_type() == key_cache.scalar_type(),
-                "value_cache must match key_cache");
+    if (bits != 4) {
+      check_linear_cache(*value_cache, key, kv.k.H, kv.k.D, "value_cache");
+      TORCH_CHECK(value_cache->sizes() == key_cache.sizes() &&
+                      value_cache->scalar_type() == key_cache.scalar_type(),
+                  "value_cache must match key_cache");
+    }
   }
   return kv;
 }
@@ -721,9 +753,9 @@ void quant_to_linear_cache(const at::Tensor& key, const c10::optional<at::Tensor
                            const c10::optional<at::Tensor>& cache_bs_id,
                            const c10::optional<at::Tensor>& cache_seqlen_offset,
                            const int64_t quant_bit) {
-  TORCH_CHECK(quant_bit == 8, "quant_to_linear_cache: only quant_bit 8 is supported, got ",
-              quant_bit);
-  const KvPair kv = write_rows(key, value, key_cache, value_cache);
+  TORCH_CHECK(quant_bit == 8 || quant_bit == 4,
+              "quant_to_linear_cache: quant_bit must be 8 or 4, got ", quant_bit);
+  const KvPair kv = write_rows(key, value, key_cache, value_cache, quant_bit);
   const int dt = dtype_code(key.scalar_type());
   TORCH_CHECK(dt == TMO_DTYPE_F32 || dt == TMO_DTYPE_F16 || dt == TMO_DTYPE_BF16,
               "quant_to_linear_cache: key must be float, half or bfloat16, got ",
@@ -857,15 +889,19 @@ void dequant_from_linear_cache(at::Tensor& key, const c10::optional<at::Tensor>&
   TORCH_CHECK(quant_mode == 0 || quant_mode == 1,
               "dequant_from_linear_cache: quant_mode must be 0 (per-channel) or 1 (per-token), "
               "got ", quant_mode);
-  TORCH_CHECK(quant_bit == 8, "dequant_from_linear_cache: only quant_bit 8 is supported, got ",
-              quant_bit);
+  TORCH_CHECK(quant_bit == 8 || quant_bit == 4,
+              "dequant_from_linear_cache: quant_bit must be 8 or 4, got ", quant_bit);
   check_device(key, key, "key");
   const TokenRows k = token_rows(key, false, "key");
   const int dt = dtype_code(key.scalar_type());
   TORCH_CHECK(dt == TMO_DTYPE_F16 || dt == TMO_DTYPE_BF16 || dt == TMO_DTYPE_F32,
               "dequant_from_linear_cache: key must be half, bfloat16 or float, got ",
               key.scalar_type());
-  check_linear_cache(key_cache, key, k.H, k.D, "key_cache");
+  if (quant_bit == 4) {
+    check_linear_cache4(key_cache, value_cache, key, k.H, k.D);
+  } else {
+    check_linear_cache(key_cache, key, k.H, k.D, "key_cache");
+  }
   TORCH_CHECK(key_cache.scalar_type() == at::kChar, "key_cache must be int8");
   const int64_t MB = key_cache.size(0), L = key_cache.size(2);
   auto check_scale = [&](const at::Tensor& s, const char* name) {
@@ -890,9 +926,12 @@ void dequant_from_linear_cache(at::Tensor& key, const c10::optional<at::Tensor>&
     TORCH_CHECK(value->sizes() == key.sizes() && value->scalar_type() == key.scalar_type(),
                 "value must match key");
     v = token_rows(*value, false, "value");
-    check_linear_cache(*value_cache, key, k.H, k.D, "value_cache");
-    TORCH_CHECK(value_cache->sizes() == key_cache.sizes() && value_cache->scalar_type() == at::kChar,
-                "value_cache must match key_cache");
+    if (quant_bit != 4) {
+      check_linear_cache(*value_cache, key, k.H, k.D, "value_cache");
+      TORCH_CHECK(value_cache->sizes() == key_cache.sizes() &&
+                      value_cache->scalar_type() == at::kChar,
+                  "value_cache must match key_cache");
+    }
     check_scale(*value_quant_scale, "value_cache_quant_scale");
   }
   const int64_t B = check_lengths(context_lengths, key, false);

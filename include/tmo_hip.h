@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 13
+#define TMO_HIP_ABI_VERSION 14
 
 /* element types */
 enum tmo_dtype {
@@ -326,8 +326,15 @@ int tmo_hip_reshape_linear_cache(const void* key, const void* value,
  * codes +0).  Scales go to key_scale[b, h, pos, g] ([max_batch, H, cache_len, group_num]).
  * Replaces tmo::torch_api::quant_to_linear_cache (reference include/torch_mlu_ops.h:194-206),
  * called by torch_mlu_ops.quant_to_linear_cache (reference _ops.py:1708-1806).
- * dtype: F32, F16 or BF16; cache_dtype: I8 or F8E4M3; quant_bit: 8 (4-bit packing is
- * TMO_ERR_UNSUPPORTED_MODE).
+ * dtype: F32, F16 or BF16; cache_dtype: I8 or F8E4M3; quant_bit: 8, or 4 with an I8 cache:
+ * scale = RN(fp32(amax) / 7), code = clip(RNE(x / scale), -8, 7), two codes per byte with the
+ * even element of a pair in the high nibble; key_cache [max_batch, H, cache_len, head_size / 2]
+ * pairs channels, value_cache [max_batch, H, cache_len / 2, head_size] pairs cache positions
+ * (cache_len even; a position written without its partner keeps the partner's nibble, so two
+ * sequences of one call must not write the two positions of one pair).  4-bit needs head_size
+ * % 8 == 0 and <= 512, 16-byte aligned token rows, a 4-byte aligned key_cache, an 8-byte aligned
+ * value_cache and, for group_num > 1, head_size / 8 a power of two that group_num divides into
+ * powers of two; otherwise TMO_ERR_UNSUPPORTED_MODE.
  */
 int tmo_hip_quant_to_linear_cache(const void* key, const void* value,
                                   int64_t key_stride_token, int64_t key_stride_head,
@@ -373,7 +380,10 @@ int tmo_hip_offline_quant_to_linear_cache(const void* key, const void* value,
  * [max_batch, num_heads, cache_len].  context_lengths holds [batch] lengths.
  * Replaces tmo::torch_api::dequant_from_linear_cache (reference
  * include/torch_mlu_ops.h:636-648), called by torch_mlu_ops.dequant_from_linear_cache
- * (reference _ops.py:3642-3732).  out_dtype: F16, BF16 (or F32); quant_bit: 8.
+ * (reference _ops.py:3642-3732).  out_dtype: F16, BF16 (or F32); quant_bit: 8, or 4 for the
+ * caches quant_to_linear_cache writes with quant_bit 4 (key_cache [max_batch, H, cache_len,
+ * head_size / 2], value_cache [max_batch, H, cache_len / 2, head_size]; nibbles sign-extended,
+ * the even element in the high nibble), with the same shape limits.
  */
 int tmo_hip_dequant_from_linear_cache(void* key, void* value,
                                       int64_t key_stride_token, int64_t key_stride_head,

@@ -63,6 +63,8 @@ def lib() -> ctypes.CDLL:
             [c_float, c_float, c_int, c_int64, c_void_p, c_int64, c_int64, c_int, c_int64] + \
             [c_void_p] * 4 + [c_int64, c_int]
         L.oracle_linear_cache.restype = c_int
+        L.oracle_linear_cache_bits.argtypes = L.oracle_linear_cache.argtypes[:-1] + [c_int, c_int]
+        L.oracle_linear_cache_bits.restype = c_int
         c_double = ctypes.c_double
         L.oracle_single_query_attn.argtypes = [c_void_p, c_int, c_int64, c_int64, c_void_p,
                                                c_void_p, c_int] + [c_int64] * 4 + \
@@ -231,32 +233,37 @@ def linear_cache(op: int, key, value, key_cache, value_cache, context_lengths, m
                  cache_seq_offset=None, key_scale=None, value_scale=None, key_chan=None,
                  value_chan=None, key_tensor: float = 1.0, value_tensor: float = 1.0,
                  smode: int = 0, groups: int = 1, block_tables=None,
-                 nthreads: Optional[int] = None) -> None:
+                 nthreads: Optional[int] = None, bits: int = 8) -> None:
     """The five linear-cache ops of tmo_oracle.c (decision D11), in place on CPU tensors.
 
     op 0 reshape_linear_cache, 1 quant_to_linear_cache, 2 offline_quant_to_linear_cache,
     3 dequant_from_linear_cache, 4 reshape_from_cache.  ``key``/``value`` are the token-major
     tensors ([T, H, D], or [B, S, H, D] padded input for ops 0-2); caches [NB, H, L, D];
     ``key_scale`` per-token scales (op 1 written, op 3 mode 1 read), ``key_chan`` static /
-    per-channel scales, ``key_tensor`` a per-tensor scale."""
+    per-channel scales, ``key_tensor`` a per-tensor scale.  ``bits`` 4 (ops 1 and 3, decision
+    D15): int8 caches of int4 pairs, key_cache [NB, H, L, D / 2], value_cache [NB, H, L / 2, D]."""
     k, v = _rows_view(key), _rows_view(value)
     assert k.stride(2) == 1 and key_cache.is_contiguous()
     pad = key.shape[1] if key.dim() == 4 else 0
     NB, H, L, D = key_cache.shape
+    if bits == 4:
+        D = k.shape[2]
+        assert key_cache.shape[3] * 2 == D, "4-bit key cache is [NB, H, L, D / 2]"
+        assert value_cache is None or tuple(value_cache.shape) == (NB, H, L // 2, D)
     ctx = _i32(context_lengths)
     B = ctx.numel() - 1 if packed else ctx.numel()
     cso, bsi, coff, bt = _i32(context_seq_offset), _i32(cache_bs_id), _i32(cache_seq_offset), \
         _i32(block_tables)
     kch = key_chan.to(torch.float32).contiguous() if key_chan is not None else None
     vch = value_chan.to(torch.float32).contiguous() if value_chan is not None else None
-    rc = lib().oracle_linear_cache(
+    rc = lib().oracle_linear_cache_bits(
         op, _ptr(k), _ptr(v), _DT[k.dtype], k.stride(0), k.stride(1),
         v.stride(0) if v is not None else 0, v.stride(1) if v is not None else 0, k.shape[0],
         _ptr(key_cache), _ptr(value_cache), _CACHE_DT.get(key_cache.dtype, 3), NB, H, L, D,
         _ptr(key_scale), _ptr(value_scale), _ptr(kch), _ptr(vch), float(key_tensor),
         float(value_tensor), int(smode), int(groups), _ptr(ctx), B, int(max_context_len),
         int(bool(packed)), pad, _ptr(cso), _ptr(bsi), _ptr(coff), _ptr(bt),
-        bt.shape[1] if bt is not None else 0, nthreads or default_threads())
+        bt.shape[1] if bt is not None else 0, int(bits), nthreads or default_threads())
     _check(rc, "linear_cache")
 
 

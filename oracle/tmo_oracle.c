@@ -75,6 +75,20 @@
  *       head_size_v of a V cache row -- of the K row itself when v_cache is None
  *       (_ops.py:828-831); per-group scales (_ops.py:841-842) cover 32 channels of one key
  *       (K) or 32 rows of one page and channel (V: block_size // 32 per page).
+ *   D15 4-bit linear caches (quant_to_linear_cache / dequant_from_linear_cache with quant_bit
+ *       4, _ops.py:1723-1750, 3664-3700): int8 caches hold two signed 4-bit codes per byte.
+ *       Codes: scale = RN(amax / 7) (int_max = 2^(4-1) - 1), code = clip(RNE(RN(x / scale)),
+ *       -8, 7), an all-zero row or group giving scale 0 and codes 0.  Nibble order: the even
+ *       element of a pair in the high nibble, the odd one in the low nibble -- the dequant
+ *       math's `unpack[0::2] = byte >> 4; unpack[1::2] = byte << 4 >> 4` (arithmetic shifts
+ *       of int8), which the quant math's `(d1 << 4) + (d0 & 0x0f)` also gives when its
+ *       repeated `[0::2]` is read as d1 = even, d0 = odd elements.  K pairs adjacent
+ *       channels: key_cache [max_batch, H, cache_len, D / 2], byte c of a row = (code[2c],
+ *       code[2c + 1]).  V pairs adjacent cache positions (value_cache [max_batch, H,
+ *       cache_len / 2, D], the dequant docstring's and fused_rope's v_cache_lp shape): byte
+ *       [p / 2, d] = (code of position 2 (p / 2), code of position 2 (p / 2) + 1) at channel
+ *       d; writing one position leaves the other nibble of its byte as it was.  Scales stay
+ *       one per (position, head) (or per group of D / group_num channels) for K and V.
  *   D9  offline (static-scale) quantisation divides: code = clip(RNE(RN(fp32(x) / s)), -128, 127)
  *       for int8, fp8 = e4m3fn_RNE(clip(RN(fp32(x) / s), -448, 448)), s the fp32 per-channel
  *       scale or the per-tensor scalar rounded to fp32 (_ops.py:1652-1670; the division is
@@ -296,6 +310,39 @@ static float quant_group(const float* x, int64_t n, uint8_t* codes, int cache_dt
         codes[i] = f32_to_e4m3(q);
     }
     return scale;
+}
+
+/* D15: one row / group of n values -> signed 4-bit codes (one per int8, -8..7) + fp32 scale:
+ * scale = RN(amax / 7), code = clip(RNE(RN(x / scale)), -8, 7) (_ops.py:1736-1742). */
+static float quant_group4(const float* x, int64_t n, int8_t* codes) {
+    float amax = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        float a = fabsf(x[i]);
+        if (a > amax) amax = a;
+    }
+    float scale = amax / 7.0f;                             /* IEEE divide */
+    if (scale == 0.0f) {                                   /* as D3 */
+        memset(codes, 0, (size_t)n);
+        return scale;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        float q = rintf(x[i] / scale);                     /* IEEE divide, RNE */
+        if (q < -8.0f) q = -8.0f;
+        if (q > 7.0f) q = 7.0f;
+        codes[i] = (int8_t)q;
+    }
+    return scale;
+}
+
+/* D15 nibble access: the even element of a pair in the high nibble, the odd one in the low
+ * nibble; a read sign-extends (int8 arithmetic shifts). */
+static inline void put_nibble(uint8_t* byte, int odd, int8_t code) {
+    uint8_t c = (uint8_t)code & 0x0Fu;
+    *byte = odd ? (uint8_t)((*byte & 0xF0u) | c) : (uint8_t)((*byte & 0x0Fu) | (c << 4));
+}
+static inline int8_t get_nibble(uint8_t byte, int odd) {
+    int8_t b = (int8_t)byte;
+    return odd ? (int8_t)((int8_t)(b << 4) >> 4) : (int8_t)(b >> 4);
 }
 
 /* ------------------------------------------------------------------ quant_to_paged_cache */
@@ -673,6 +720,7 @@ typedef struct {
     int cache_dtype;          /* quantising ops: DT_I8 or DT_F8E4M3 */
     int64_t groups;           /* dynamic: scale groups per (token, head) */
     int64_t max_len;          /* tokens j >= max_len are skipped */
+    int bits;                 /* ops 1 and 3: 8, or 4 (D15: packed int4 pairs) */
 } lin_ctx;
 
 static void lin_range(void* p, int64_t lo, int64_t hi) {
@@ -701,6 +749,20 @@ static void lin_range(void* p, int64_t lo, int64_t hi) {
                         char* to = c->op == 0 ? (char*)c->dst[kv] + cr * D * es
                                               : (char*)c->dst[kv] + tok * es;
                         memcpy(to, from, (size_t)(D * es));
+                    } else if (c->op == 1 && c->bits == 4) {        /* D15: int4 pairs */
+                        int64_t gs = D / c->groups;
+                        for (int64_t d = 0; d < D; ++d) row[d] = load_elem(c->src[kv], tok + d, c->dtype);
+                        for (int64_t g = 0; g < c->groups; ++g)
+                            c->scale[kv][cr * c->groups + g] =
+                                quant_group4(row + g * gs, gs, (int8_t*)codes + g * gs);
+                        if (kv == 0) {                              /* K: channel pairs */
+                            uint8_t* out = (uint8_t*)c->dst[kv] + cr * (D / 2);
+                            for (int64_t d = 0; d < D; ++d) put_nibble(out + d / 2, (int)(d & 1), (int8_t)codes[d]);
+                        } else {                                    /* V: position pairs */
+                            int64_t bh = (cr - pos) / a->cache_len;
+                            uint8_t* out = (uint8_t*)c->dst[kv] + (bh * (a->cache_len / 2) + pos / 2) * D;
+                            for (int64_t d = 0; d < D; ++d) put_nibble(out + d, (int)(pos & 1), (int8_t)codes[d]);
+                        }
                     } else if (c->op == 1) {                        /* dynamic per token / group */
                         int64_t gs = D / c->groups;
                         for (int64_t d = 0; d < D; ++d) row[d] = load_elem(c->src[kv], tok + d, c->dtype);
@@ -715,6 +777,19 @@ static void lin_range(void* p, int64_t lo, int64_t hi) {
                                     : c->smode == 1 ? c->chan[kv][h * a->cache_len + pos]
                                                     : c->tensor_scale[kv];
                             out[d] = static_code(load_elem(c->src[kv], tok + d, c->dtype), s, c->cache_dtype);
+                        }
+                    } else if (c->bits == 4) {                      /* dequant, D15 int4 pairs */
+                        for (int64_t d = 0; d < D; ++d) {
+                            int8_t code;
+                            if (kv == 0) {
+                                code = get_nibble(((const uint8_t*)c->src[kv])[cr * (D / 2) + d / 2], (int)(d & 1));
+                            } else {
+                                int64_t bh = (cr - pos) / a->cache_len;
+                                code = get_nibble(((const uint8_t*)c->src[kv])[(bh * (a->cache_len / 2) + pos / 2) * D + d],
+                                                  (int)(pos & 1));
+                            }
+                            float s = c->smode == 0 ? c->chan[kv][h * D + d] : c->scale[kv][cr];
+                            store_elem(c->dst[kv], tok + d, c->dtype, (float)code * s);
                         }
                     } else {                                        /* dequant */
                         const int8_t* in = (const int8_t*)c->src[kv] + cr * D;
@@ -740,6 +815,16 @@ static void lin_range(void* p, int64_t lo, int64_t hi) {
  * groups: scale groups per (token, head) for op 1.  block_tables [batch, max_blocks] (nullable)
  * turns the cache into pages of cache_len rows: op 4 with it is reshape_from_cache's paged mode,
  * op 3 with it reads per-token scales [num_blocks, H, cache_len]. */
+int oracle_linear_cache_bits(int op, void* tok_k, void* tok_v, int dtype, int64_t k_st, int64_t k_sh,
+                             int64_t v_st, int64_t v_sh, int64_t rows, void* cache_k, void* cache_v,
+                             int cache_dtype, int64_t cache_batch, int64_t H, int64_t cache_len, int64_t D,
+                             float* k_scale, float* v_scale, const float* k_chan, const float* v_chan,
+                             float k_tensor, float v_tensor, int smode, int64_t groups,
+                             const int32_t* lens, int64_t batch, int64_t max_len, int packed,
+                             int64_t pad_seqlen, const int32_t* seq_off, const int32_t* bs_id,
+                             const int32_t* cache_off, const int32_t* block_tables,
+                             int64_t max_blocks, int bits, int nthreads);
+
 int oracle_linear_cache(int op, void* tok_k, void* tok_v, int dtype, int64_t k_st, int64_t k_sh,
                         int64_t v_st, int64_t v_sh, int64_t rows, void* cache_k, void* cache_v,
                         int cache_dtype, int64_t cache_batch, int64_t H, int64_t cache_len, int64_t D,
@@ -749,6 +834,28 @@ int oracle_linear_cache(int op, void* tok_k, void* tok_v, int dtype, int64_t k_s
                         int64_t pad_seqlen, const int32_t* seq_off, const int32_t* bs_id,
                         const int32_t* cache_off, const int32_t* block_tables,
                         int64_t max_blocks, int nthreads) {
+    return oracle_linear_cache_bits(op, tok_k, tok_v, dtype, k_st, k_sh, v_st, v_sh, rows, cache_k,
+                                    cache_v, cache_dtype, cache_batch, H, cache_len, D, k_scale,
+                                    v_scale, k_chan, v_chan, k_tensor, v_tensor, smode, groups, lens,
+                                    batch, max_len, packed, pad_seqlen, seq_off, bs_id, cache_off,
+                                    block_tables, max_blocks, 8, nthreads);
+}
+
+/* The same with quant_bit `bits` for ops 1 and 3: 8, or 4 (D15: int8 caches of int4 pairs, K
+ * [cache_batch, H, cache_len, D / 2], V [cache_batch, H, cache_len / 2, D] with cache_len
+ * even; no block table, int8 caches only). */
+int oracle_linear_cache_bits(int op, void* tok_k, void* tok_v, int dtype, int64_t k_st, int64_t k_sh,
+                             int64_t v_st, int64_t v_sh, int64_t rows, void* cache_k, void* cache_v,
+                             int cache_dtype, int64_t cache_batch, int64_t H, int64_t cache_len, int64_t D,
+                             float* k_scale, float* v_scale, const float* k_chan, const float* v_chan,
+                             float k_tensor, float v_tensor, int smode, int64_t groups,
+                             const int32_t* lens, int64_t batch, int64_t max_len, int packed,
+                             int64_t pad_seqlen, const int32_t* seq_off, const int32_t* bs_id,
+                             const int32_t* cache_off, const int32_t* block_tables,
+                             int64_t max_blocks, int bits, int nthreads) {
+    if (bits != 8 && bits != 4) return -3;
+    if (bits == 4 && ((op != 1 && op != 3) || (op == 1 && cache_dtype != DT_I8) || D % 2 != 0 ||
+                      (tok_v && cache_len % 2 != 0) || block_tables)) return -3;
     if (op < 0 || op > 4 || elem_size(dtype) == 0) return -2;
     if ((op == 1 || op == 2 || op == 3) && dtype == DT_I8) return -2;
     if ((op == 1 || op == 2) && cache_dtype != DT_I8 && cache_dtype != DT_F8E4M3) return -2;
@@ -765,6 +872,7 @@ int oracle_linear_cache(int op, void* tok_k, void* tok_v, int dtype, int64_t k_s
     c.scale[0] = k_scale; c.scale[1] = v_scale; c.chan[0] = k_chan; c.chan[1] = v_chan;
     c.tensor_scale[0] = k_tensor; c.tensor_scale[1] = v_tensor; c.smode = smode;
     c.cache_dtype = cache_dtype; c.groups = groups > 0 ? groups : 1; c.max_len = max_len;
+    c.bits = bits;
     if (op <= 2) { c.src[0] = tok_k; c.src[1] = tok_v; c.dst[0] = cache_k; c.dst[1] = cache_v; }
     else { c.src[0] = cache_k; c.src[1] = cache_v; c.dst[0] = tok_k; c.dst[1] = tok_v; }
     parallel_for(batch, nthreads, lin_range, &c);

@@ -288,7 +288,16 @@ def test_linear_write_validation(lib):
         assert lin_write(lib, fn, max_len=0) == 0, fn
         assert lin_write(lib, fn, rows=0) == 0, fn
     assert lin_write(lib, "quant", dtype=3) == EDTYPE          # int8 input
-    assert lin_write(lib, "quant", extra=(FAKE, None, 1, 4, 3)) == EMODE   # 4-bit
+    assert lin_write(lib, "quant", extra=(FAKE, None, 1, 5, 3)) == EMODE   # quant_bit 5
+    # 4-bit: int8 caches only; head_size a multiple of 8; an even cache_len for V pairs; scale
+    # groups over whole aligned lane groups (head_size 80: 10 lanes of 8 channels); valid
+    # arguments with nothing to do return 0 before anything is launched
+    assert lin_write(lib, "quant", extra=(FAKE, None, 1, 4, 4)) == EDTYPE
+    assert lin_write(lib, "quant", D=20, extra=(FAKE, None, 1, 4, 3)) == EMODE
+    assert lin_write(lib, "quant", value=FAKE, vc=FAKE, L=33, extra=(FAKE, FAKE, 1, 4, 3)) == EMODE
+    assert lin_write(lib, "quant", D=80, extra=(FAKE, None, 2, 4, 3)) == EMODE
+    assert lin_write(lib, "quant", D=1024, extra=(FAKE, None, 1, 4, 3)) == EMODE
+    assert lin_write(lib, "quant", B=0, extra=(FAKE, None, 1, 4, 3)) == 0
     assert lin_write(lib, "quant", extra=(FAKE, None, 1, 8, 2)) == EDTYPE  # bf16 cache
     assert lin_write(lib, "quant", extra=(FAKE, None, 3, 8, 3)) == EINVAL  # 128 % 3 != 0
     assert lin_write(lib, "quant", extra=(None, None, 1, 8, 3)) == EINVAL  # no scale
@@ -298,12 +307,16 @@ def test_linear_write_validation(lib):
 
 
 def test_linear_read_validation(lib):
-    def deq(mode=1, bit=8, dtype=2, key=FAKE, value=None, vc=None, vs=None, B=2, H=8, rows=10):
+    def deq(mode=1, bit=8, dtype=2, key=FAKE, value=None, vc=None, vs=None, B=2, H=8, rows=10,
+            D=128, L=32):
         return lib.tmo_hip_dequant_from_linear_cache(
-            key, value, 1024, 128, 1024, 128, rows, FAKE, vc, FAKE, vs, 4, H, 32, 128, FAKE, B,
+            key, value, 1024, 128, 1024, 128, rows, FAKE, vc, FAKE, vs, 4, H, L, D, FAKE, B,
             16, None, None, None, mode, bit, dtype, None)
     assert deq(mode=2) == EMODE
-    assert deq(bit=4) == EMODE
+    assert deq(bit=5) == EMODE
+    assert deq(bit=4, D=20) == EMODE                              # head_size % 8 != 0
+    assert deq(bit=4, value=FAKE, vc=FAKE, vs=FAKE, L=33) == EMODE  # odd cache_len with V
+    assert deq(bit=4, B=0) == 0
     assert deq(dtype=3) == EDTYPE
     assert deq(key=None) == EINVAL
     assert deq(value=FAKE, vc=FAKE) == EINVAL                    # value without value scale

@@ -430,3 +430,150 @@ def test_output_rows_follow_the_length_prefix(tmo, ref, dev, B):
     tmo.reshape_from_cache(gout, None, kc.to(dev), None, lens.to(dev), 8)
     torch.cuda.synchronize()
     _cmp(gout, out, "reshape_from_cache key")
+
+
+# ---------------------------------------------------------------------------- 4-bit linear caches
+
+def _int4_caches(case, D, device="cpu", fill=0x5A):
+    H = case.key.shape[-2]
+    kc = torch.full((case.cache_batch, H, case.cache_len, D // 2), fill, dtype=torch.uint8,
+                    device=device).view(torch.int8)
+    vc = torch.full((case.cache_batch, H, case.cache_len // 2, D), fill, dtype=torch.uint8,
+                    device=device).view(torch.int8)
+    return kc, vc
+
+
+def _quant4_both(tmo, ref, dev, case, groups=1, with_v=True):
+    H, D = case.key.shape[-2:]
+    kc, vc = _int4_caches(case, D)
+    ks, vs = case.scales(groups if groups > 1 else 0)
+    v = case.value if with_v else None
+    if not with_v:
+        vc = vs = None
+    ref.linear_cache(1, case.key, v, kc, vc, case.context_lengths, case.max_context_len,
+                     packed=case.packed, context_seq_offset=case.context_seq_offset,
+                     cache_bs_id=case.cache_bs_id, cache_seq_offset=case.cache_seq_offset,
+                     key_scale=ks, value_scale=vs, groups=groups, bits=4)
+    gk, gv = _int4_caches(case, D, dev)
+    gks, gvs = (t.to(dev) for t in case.scales(groups if groups > 1 else 0))
+    if not with_v:
+        gv = gvs = None
+    tmo.quant_to_linear_cache(case.key.to(dev), _d(v, dev), gk, gv, gks, gvs,
+                              case.context_lengths.to(dev), case.max_context_len, case.packed,
+                              _d(case.context_seq_offset, dev), _d(case.cache_bs_id, dev),
+                              _d(case.cache_seq_offset, dev), 4)
+    torch.cuda.synchronize()
+    _cmp(gk, kc, "key_cache (int4)")
+    _cmp(gks, ks, "key_scale (int4)")
+    if with_v:
+        _cmp(gv, vc, "value_cache (int4)")
+        _cmp(gvs, vs, "value_scale (int4)")
+
+
+@pytest.mark.parametrize("packed,offsets", [(True, False), (True, True), (False, True)])
+@pytest.mark.parametrize("dtype", FLOATS)
+def test_quant_to_linear_cache_int4(tmo, ref, dev, dtype, packed, offsets):
+    """Codes, nibble order, V position pairs (odd cache offsets keep the partner nibble), scales."""
+    case = W.linear_case(dtype, 81, packed=packed, offsets=offsets)
+    _quant4_both(tmo, ref, dev, case)
+    _quant4_both(tmo, ref, dev, case, with_v=False)
+
+
+@pytest.mark.parametrize("D,groups", [(128, 1), (128, 4), (128, 16), (64, 8), (512, 2),
+                                      (8, 1), (16, 2), (80, 1), (24, 1)])
+def test_quant_to_linear_cache_int4_groups_and_widths(tmo, ref, dev, D, groups):
+    case = W.linear_case(torch.bfloat16, 82 + D, packed=True, offsets=True, D=D)
+    _quant4_both(tmo, ref, dev, case, groups)
+
+
+def test_quant_to_linear_cache_int4_odd_offsets_and_shapes_rejected(tmo, ref, dev):
+    """Every cache offset parity; shapes outside the 4-bit kernels raise instead of writing."""
+    case = W.linear_case(torch.float16, 83, packed=True, offsets=False, B=4, S=9, cache_len=24)
+    for off in ([1, 0, 3, 2], [0, 1, 2, 3], [5, 7, 1, 1]):
+        case.cache_seq_offset = torch.tensor(off, dtype=torch.int32)
+        _quant4_both(tmo, ref, dev, case)
+    bad = W.linear_case(torch.float16, 84, packed=True, D=20)          # head_size % 8 != 0
+    H = bad.key.shape[-2]
+    kc = torch.zeros(bad.cache_batch, H, bad.cache_len, 10, dtype=torch.int8, device=dev)
+    ks = torch.zeros(bad.cache_batch, H, bad.cache_len, device=dev)
+    with pytest.raises(RuntimeError):
+        tmo.quant_to_linear_cache(bad.key.to(dev), None, kc, None, ks, None,
+                                  bad.context_lengths.to(dev), bad.max_context_len, True, None,
+                                  None, None, 4)
+
+
+def _dequant4_both(tmo, ref, dev, case, dtype, mode, with_v=True):
+    g = torch.Generator().manual_seed(85)
+    H, D = case.key.shape[-2:]
+    L = case.cache_len
+    kc = torch.randint(-128, 128, (case.cache_batch, H, L, D // 2), generator=g, dtype=torch.int8)
+    vc = torch.randint(-128, 128, (case.cache_batch, H, L // 2, D), generator=g, dtype=torch.int8)
+    kt = torch.rand(case.cache_batch, H, L, generator=g) * 0.05
+    vt = torch.rand(case.cache_batch, H, L, generator=g) * 0.05
+    kch, vch = torch.rand(H, D, generator=g) * 0.05, torch.rand(H, D, generator=g) * 0.05
+    ks, vs = (kch, vch) if mode == 0 else (kt, vt)
+    T = int(case.lens.sum()) + 3
+    if case.context_seq_offset is not None:
+        T = max(T, int((case.context_seq_offset + case.lens).max()) + 1)
+    key = torch.full((T, H, D), -3.0, dtype=dtype)
+    value = key.clone() if with_v else None
+    if not with_v:
+        vc = vs = None
+    ref.linear_cache(3, key, value, kc, vc, case.lens, case.max_context_len,
+                     context_seq_offset=case.context_seq_offset, cache_bs_id=case.cache_bs_id,
+                     cache_seq_offset=case.cache_seq_offset,
+                     key_scale=ks if mode == 1 else None, value_scale=vs if mode == 1 else None,
+                     key_chan=ks if mode == 0 else None, value_chan=vs if mode == 0 else None,
+                     smode=mode, bits=4)
+    gkey = torch.full((T, H, D), -3.0, dtype=dtype, device=dev)
+    gval = gkey.clone() if with_v else None
+    tmo.dequant_from_linear_cache(gkey, gval, kc.to(dev), _d(vc, dev), ks.to(dev), _d(vs, dev),
+                                  case.lens.to(dev), case.max_context_len,
+                                  _d(case.context_seq_offset, dev), _d(case.cache_bs_id, dev),
+                                  _d(case.cache_seq_offset, dev), mode, 4)
+    torch.cuda.synchronize()
+    _cmp(gkey, key, "key (int4)")
+    if with_v:
+        _cmp(gval, value, "value (int4)")
+
+
+@pytest.mark.parametrize("offsets", [False, True])
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("dtype", FLOATS)
+def test_dequant_from_linear_cache_int4(tmo, ref, dev, dtype, mode, offsets):
+    case = W.linear_case(dtype, 86, packed=True, offsets=offsets)
+    _dequant4_both(tmo, ref, dev, case, dtype, mode)
+    _dequant4_both(tmo, ref, dev, case, dtype, mode, with_v=False)
+
+
+@pytest.mark.parametrize("D", [8, 16, 80, 128, 512])
+def test_dequant_from_linear_cache_int4_widths(tmo, ref, dev, D):
+    case = W.linear_case(torch.bfloat16, 87 + D, packed=True, offsets=True, D=D)
+    _dequant4_both(tmo, ref, dev, case, torch.bfloat16, 1)
+
+
+def test_int4_round_trip_prefill(tmo, ref, dev):
+    """8 x 512 packed tokens, 8 heads x 128, bf16: quant (4 bit) then dequant is within scale / 2
+    per element, and bit-exact against the oracle."""
+    B, S, H, D, L = 8, 512, 8, 128, 1024
+    g = torch.Generator().manual_seed(88)
+    key = torch.randn(B * S, H, D, generator=g).to(torch.bfloat16)
+    value = torch.randn(B * S, H, D, generator=g).to(torch.bfloat16)
+    cu = torch.arange(B + 1, dtype=torch.int32) * S
+    case = W.LinearCase(key, value, torch.full((B,), S, dtype=torch.int32), True, None, None,
+                        None, B, L)
+    _quant4_both(tmo, ref, dev, case)
+    kc, vc = _int4_caches(case, D, dev)
+    ks = torch.zeros(B, H, L, device=dev)
+    vs = torch.zeros_like(ks)
+    tmo.quant_to_linear_cache(key.to(dev), value.to(dev), kc, vc, ks, vs, cu.to(dev), S, True,
+                              None, None, None, 4)
+    bk = torch.empty(B * S, H, D, device=dev)
+    bv = torch.empty_like(bk)
+    lens = torch.full((B,), S, dtype=torch.int32, device=dev)
+    tmo.dequant_from_linear_cache(bk, bv, kc, vc, ks, vs, lens, S, None, None, None, 1, 4)
+    torch.cuda.synchronize()
+    for x, back, sc in ((key, bk, ks), (value, bv, vs)):
+        err = (back.cpu() - x.float()).abs().reshape(B, S, H, D)
+        s = sc[:, :, :S].cpu().permute(0, 2, 1)[..., None]
+        assert (err <= s * (0.5 + 2.0 ** -15)).all()

@@ -1124,6 +1124,154 @@ def test_linear_max_context_len_truncates(ref):
     assert torch.equal(bits(kc), bits(wk)) and torch.equal(bits(vc), bits(wv))
 
 
+# ---------------------------------------------------------------------------- 4-bit linear caches (D15)
+
+def unpack_docstring(flat_bytes: torch.Tensor) -> torch.Tensor:
+    """dequant_from_linear_cache's int4 unpack, as written in its Math block (_ops.py:3680-3682):
+    unpack[0::2] = flat >> 4; unpack[1::2] = flat << 4 >> 4, on int8 tensors."""
+    flat = flat_bytes.reshape(-1).view(torch.int8)
+    out = torch.empty(flat.numel() * 2, dtype=torch.int8)
+    out[0::2] = flat >> 4
+    out[1::2] = flat << 4 >> 4
+    return out
+
+
+def torch_int4_codes(rows: torch.Tensor, groups: int = 1):
+    """quant_to_linear_cache's math with quant_bit 4 (_ops.py:1728-1742) by torch: int_max =
+    2^(4-1) - 1 = 7, scale = amax / 7, code = clip(round(x / scale), -8, 7); [n, H, D] ->
+    (int8 codes [n, H, D], scales [n, H, groups])."""
+    n, H, D = rows.shape
+    xf = rows.to(torch.float32).reshape(n, H, groups, D // groups)
+    amax = rows.reshape(n, H, groups, D // groups).abs().amax(-1).to(torch.float32)
+    scale = amax / 7.0
+    q = (xf / scale[..., None]).round().clamp(-8, 7)
+    q = torch.where(scale[..., None] == 0, torch.zeros_like(q), q)
+    return q.to(torch.int8).reshape(n, H, D), scale
+
+
+def pack_pairs(codes: torch.Tensor) -> torch.Tensor:
+    """Pairs along the last dim into bytes, the inverse of unpack_docstring: (even << 4) | (odd
+    & 0xF)."""
+    hi = codes[..., 0::2].to(torch.int16) << 4
+    lo = codes[..., 1::2].to(torch.int16) & 0xF
+    return ((hi | lo) & 0xFF).to(torch.uint8)
+
+
+def torch_linear_write4(case, kc, vc, ks, vs, groups=1):
+    """D15 write by torch: K rows packed along channels; V codes placed by cache position into
+    the nibble of byte [pos // 2, d] (even position: high nibble), the other nibble kept."""
+    segs = _lin_segments(case, case.max_context_len, out_dir=False)
+    k = case.key.reshape(-1, *case.key.shape[-2:])
+    v = case.value.reshape(-1, *case.value.shape[-2:])
+    kb, vb = kc.view(torch.uint8), vc.view(torch.uint8)
+    for r, b, pos in segs:
+        if r.numel() == 0:
+            continue
+        codes, scale = torch_int4_codes(k[r], groups)
+        kb[b, :, pos] = pack_pairs(codes)
+        ks[b, :, pos] = scale if ks.dim() == 4 else scale[..., 0]
+        codes, scale = torch_int4_codes(v[r], groups)
+        vs[b, :, pos] = scale if vs.dim() == 4 else scale[..., 0]
+        for t in range(r.numel()):
+            bt, pt = int(b[t]), int(pos[t])
+            old = vb[bt, :, pt // 2].to(torch.int16)
+            c = codes[t].to(torch.int16) & 0xF
+            new = (old & 0xF0) | c if pt % 2 else (old & 0x0F) | (c << 4)
+            vb[bt, :, pt // 2] = new.to(torch.uint8)
+
+
+@pytest.mark.parametrize("packed,offsets", LIN_CASES)
+@pytest.mark.parametrize("groups", [1, 4])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_linear_int4_quant_matches_torch(ref, dtype, groups, packed, offsets):
+    case = W.linear_case(dtype, 31, packed=packed, offsets=offsets)
+    H, D = case.key.shape[-2:]
+    kc = torch.full((case.cache_batch, H, case.cache_len, D // 2), 0x5A, dtype=torch.uint8).view(torch.int8)
+    vc = torch.full((case.cache_batch, H, case.cache_len // 2, D), 0x5A, dtype=torch.uint8).view(torch.int8)
+    ks, vs = case.scales(groups if groups > 1 else 0)
+    wk, wv, wks, wvs = kc.clone(), vc.clone(), ks.clone(), vs.clone()
+    torch_linear_write4(case, wk, wv, wks, wvs, groups)
+    ref.linear_cache(1, case.key, case.value, kc, vc, case.context_lengths, case.max_context_len,
+                     packed=packed, context_seq_offset=case.context_seq_offset,
+                     cache_bs_id=case.cache_bs_id, cache_seq_offset=case.cache_seq_offset,
+                     key_scale=ks, value_scale=vs, groups=groups, bits=4)
+    assert torch.equal(kc, wk) and torch.equal(vc, wv)
+    assert torch.equal(ks.view(torch.int32), wks.view(torch.int32))
+    assert torch.equal(vs.view(torch.int32), wvs.view(torch.int32))
+    assert not torch.equal(kc, torch.full_like(kc, 0x5A))
+
+
+@pytest.mark.parametrize("offsets", [False, True])
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_linear_int4_dequant_matches_docstring(ref, dtype, mode, offsets):
+    """The K side executes the reference's own unpack expression on each cache row; V applies
+    the same unpack along its packed dimension (position pairs of one channel)."""
+    case = W.linear_case(dtype, 32, packed=True, offsets=offsets)
+    g = torch.Generator().manual_seed(33)
+    H, D = case.key.shape[-2:]
+    L = case.cache_len
+    kc = torch.randint(-128, 128, (case.cache_batch, H, L, D // 2), generator=g, dtype=torch.int8)
+    vc = torch.randint(-128, 128, (case.cache_batch, H, L // 2, D), generator=g, dtype=torch.int8)
+    kt = torch.rand(case.cache_batch, H, L, generator=g) * 0.05
+    vt = torch.rand(case.cache_batch, H, L, generator=g) * 0.05
+    kch, vch = torch.rand(H, D, generator=g) * 0.05, torch.rand(H, D, generator=g) * 0.05
+    T = case.key.shape[0]
+    key = torch.full((T, H, D), -3.0, dtype=dtype)
+    value = key.clone()
+    wk, wv = key.clone(), value.clone()
+    # unpacked caches by the docstring's expression: K per row, V along positions per channel
+    ku = unpack_docstring(kc).reshape(case.cache_batch, H, L, D)
+    vu = unpack_docstring(vc.permute(0, 1, 3, 2).contiguous()) \
+        .reshape(case.cache_batch, H, D, L).permute(0, 1, 3, 2)
+    torch_linear_read(case, 3, wk, wv, ku, vu, kch if mode == 0 else kt, vch if mode == 0 else vt,
+                      smode=mode)
+    ref.linear_cache(3, key, value, kc, vc, case.lens, case.max_context_len,
+                     context_seq_offset=case.context_seq_offset, cache_bs_id=case.cache_bs_id,
+                     cache_seq_offset=case.cache_seq_offset,
+                     key_scale=kt if mode == 1 else None, value_scale=vt if mode == 1 else None,
+                     key_chan=kch if mode == 0 else None, value_chan=vch if mode == 0 else None,
+                     smode=mode, bits=4)
+    assert torch.equal(bits(key), bits(wk)) and torch.equal(bits(value), bits(wv))
+
+
+def test_linear_int4_round_trip_and_closed_forms(ref):
+    """quant (4 bit) then dequant: |x - deq| <= scale / 2 per element; codes stay in [-7, 7]
+    (|x| <= amax bounds |x / scale| by 7) and the largest element of a row reaches +-7; writing
+    from an odd cache position keeps the other nibble of the first V byte."""
+    case = W.linear_case(torch.bfloat16, 34, packed=True, offsets=False)
+    H, D = case.key.shape[-2:]
+    L = case.cache_len
+    kc = torch.zeros((case.cache_batch, H, L, D // 2), dtype=torch.int8)
+    vc = torch.full((case.cache_batch, H, L // 2, D), 0x5A, dtype=torch.uint8).view(torch.int8)
+    ks, vs = case.scales()
+    case.cache_seq_offset = torch.ones(case.lens.numel(), dtype=torch.int32)   # odd first position
+    ref.linear_cache(1, case.key, case.value, kc, vc, case.context_lengths, case.max_context_len,
+                     packed=True, cache_seq_offset=case.cache_seq_offset, key_scale=ks,
+                     value_scale=vs, bits=4)
+    # byte 0 of every written sequence's V rows: its high nibble (position 0) untouched
+    for i, n in enumerate(case.lens.tolist()):
+        if n:
+            assert torch.equal((vc[i, :, 0].view(torch.uint8) >> 4), torch.full((H, D), 5, dtype=torch.uint8))
+    ku = unpack_docstring(kc).reshape(case.cache_batch, H, L, D)
+    assert int(ku.min()) >= -7 and int(ku.max()) <= 7
+    deq_k = torch.zeros(case.key.shape, dtype=torch.float32)
+    deq_v = torch.zeros(case.key.shape, dtype=torch.float32)
+    ref.linear_cache(3, deq_k, deq_v, kc, vc, case.lens, case.max_context_len,
+                     cache_seq_offset=case.cache_seq_offset, key_scale=ks, value_scale=vs,
+                     smode=1, bits=4)
+    starts = torch.cumsum(case.lens, 0) - case.lens
+    for i, (s0, n_i) in enumerate(zip(starts.tolist(), case.lens.tolist())):
+        for x, deq, sc in ((case.key, deq_k, ks), (case.value, deq_v, vs)):
+            xs = x[s0:s0 + n_i].to(torch.float32)
+            s = sc[i, :, 1:1 + n_i].transpose(0, 1)[..., None]
+            assert ((deq[s0:s0 + n_i] - xs).abs() <= s * (0.5 + 2.0 ** -15)).all()
+            # the row maximum maps to +-7 exactly: |deq| == 7 * scale there
+            top = xs.abs().argmax(-1, keepdim=True)
+            got = deq[s0:s0 + n_i].gather(-1, top).abs()
+            assert torch.equal(got, (7 * s).to(torch.float32)) or (s == 0).all()
+
+
 # ---------------------------------------------------------------------------- decode attention (D12)
 
 def torch_attn(case, scale, window=-1):
