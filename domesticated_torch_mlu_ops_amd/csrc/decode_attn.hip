@@ -248,7 +248,9 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   constexpr int kEs = kKind == 0 ? 1 : 2;  // cache element bytes
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  // wave-uniform (readfirstlane): the tile indices, page numbers and page offsets derived from it
+  // stay in scalar registers, and the tile loads take a scalar base plus a per-lane offset
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int col = lane & 15;        // query column within the block / token row
   const int grp = lane >> 4;        // lane group c
   const int64_t i = blockIdx.z;
@@ -524,6 +526,23 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
 
       // ---- P^T operands (hi + lo) with the per-token V scale folded in
       V4 phi, plo;
+      if constexpr (!kF16) {
+        // bf16 pairs: one v_cvt_pk_bf16_f32 rounds two probabilities (hi), the hi values are
+        // read back from the packed bits, and one more rounds the two remainders (lo)
+        typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        u32x2 hv, lv;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const f2 a = {pe[2 * k] * r.vsc[2 * k], pe[2 * k + 1] * r.vsc[2 * k + 1]};
+          const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(a, bf2));
+          const f2 l = {a[0] - __uint_as_float(h << 16), a[1] - __uint_as_float(h & 0xffff0000u)};
+          hv[k] = h;
+          lv[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(l, bf2));
+        }
+        phi = __builtin_bit_cast(V4, hv);
+        plo = __builtin_bit_cast(V4, lv);
+      } else
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float pv = pe[e] * r.vsc[e];
