@@ -611,15 +611,16 @@ __global__ __launch_bounds__(256) void lin_dequant(LinParams p) {
 // V pairs adjacent cache positions ([.., cache_len / 2, D]).  scale = RN(amax / 7) (one IEEE
 // divide per row or group), code = clip(RNE(RN(x / scale)), -8, 7).
 struct Scale4 {
-  float s, y;
+  float s;
+  double y64;  // recip64(s) for div_recip64
   bool fast;
 };
 __device__ __forceinline__ Scale4 make_scale4(float amax) {
   Scale4 r;
   r.s = amax / 7.0f;  // IEEE divide, once per row / group
   const bool normal = r.s >= kFastDivMinScale && r.s < __builtin_inff();
-  r.fast = normal || r.s == 0.0f;  // y = 0 gives quotients +-0 (codes 0) for an all-zero row
-  r.y = normal ? 1.0f / r.s : 0.0f;
+  r.fast = normal || r.s == 0.0f;  // y64 = 0 gives quotients +-0 (codes 0) for an all-zero row
+  r.y64 = normal ? recip64(r.s) : 0.0;
   return r;
 }
 // 4-bit code (two's complement nibble) of x.  On the fast path |x| <= amax bounds |q| by 7, so
@@ -627,7 +628,7 @@ __device__ __forceinline__ Scale4 make_scale4(float amax) {
 __device__ __forceinline__ uint32_t nibble4(float x, const Scale4& r) {
   float q;
   if (r.fast) {
-    q = div_by_recip(x, r.s, r.y);
+    q = div_recip64(x, r.y64);
   } else {
     keep_branch();
     q = x / r.s;

@@ -177,10 +177,11 @@ __device__ __forceinline__ float wave_max_uniform(float m) {
 // ---------------------------------------------------------------------------- int8 encoder
 
 // Rows whose scale is below this use a true IEEE divide per element; above it the
-// reciprocal-based quotient below gives the IEEE quotient's int8 code for every x.
+// reciprocal-based quotient div_recip64 below gives the IEEE quotient for every x.
 constexpr float kFastDivMinScale = 8.6736174e-19f;  // 2^-60
 
-// x / s given y = RN(1 / s) and kFastDivMinScale <= s < inf.
+// x / s given y = RN(1 / s) and kFastDivMinScale <= s < inf, in fp32 arithmetic (the static
+// scales' quotient, where y is computed per channel).
 // q0 = RN(x*y) is within ~2 ulp of x/s; one FMA correction step makes it faithful; a second
 // (Markstein's theorem: y within 1/2 ulp of 1/s and q faithful => r = x - s*q is exact and
 // RN(q + r*y) = RN(x/s)) makes it the IEEE quotient.  P. Markstein, IBM J. Res. Dev. 34(1),
@@ -195,6 +196,39 @@ __host__ __device__ __forceinline__ float div_by_recip(float x, float s, float y
   float q1 = __builtin_fmaf(r0, y, q0);
   float r1 = __builtin_fmaf(-s, q1, x);
   return __builtin_fmaf(r1, y, q1);
+}
+
+// x / s given y64 within 2^-51 (relative) of 1 / s (recip64 below), for finite x and finite
+// s > 0: the fp64 product rounded to fp32 is the IEEE fp32 quotient.  Why: a quotient x / s of
+// two fp32 numbers is either an fp32 number or at least 2^-49 (relative) away from every
+// midpoint m = M * 2^c between adjacent fp32 numbers (M odd, 2^24 < M < 2^25).  x - s * m is
+// never 0, since its odd part would need x's 24-bit significand to hold the odd factor
+// M > 2^24.  It is a multiple of 2^min(e_x, e_s + c), which bounds |x / s - m| / m below by
+// 1 / (S * M) > 2^-49 or by 1 / X > 2^-24, with X, S the 24-bit significands.  y64 and the
+// RN64 product add at most 2^-51 + 2^-53 relative error, so x * y64 lies on the same side of
+// every midpoint as x / s, and within 2^-50 of x / s where that is an fp32 number.  Where the
+// IEEE quotient is subnormal (|x / s| < 2^-126) the last bit may differ.  The int8, int4 and
+// fp8 codes are 0 there either way, and the sign is x's, as in the IEEE quotient, zero
+// quotients included.  Three VALU instructions (v_cvt_f64_f32, v_mul_f64, v_cvt_f32_f64, all
+// full rate on gfx950) against div_by_recip's five.  tests/native/div_exhaustive.hip checks it
+// with y64 = RN64(1 / s) against IEEE division on every bf16 and every fp16 (amax, x) pair and
+// on random and near-tie fp32 pairs; tests/native/gfx950_builtins.hip ("div64") checks it on
+// the GPU with recip64 on every bf16 and fp16 pair.
+__host__ __device__ __forceinline__ float div_recip64(float x, double y64) {
+  return (float)((double)x * y64);
+}
+
+// 1 / s in fp64 for the dynamic scales, 2^-60 <= s <= 2^126 (kFastDivMinScale up to amax / 7,
+// amax / 127 or amax / 448 of a finite amax): v_rcp_f32 (within 1 ulp, a normal number over
+// this range) and two fp64 Newton steps y + y * (1 - s * y), each squaring the relative error
+// and adding at most 2^-53: 2^-23 -> ~2^-46 -> ~2^-53.
+// tests/native/gfx950_builtins.hip ("recip64") checks |1 - s * y| <= 2^-52 on the GPU for
+// every fp32 s of the range.
+__device__ __forceinline__ double recip64(float s) {
+  const double s64 = (double)s;
+  double y = (double)__builtin_amdgcn_rcpf(s);
+  y = __builtin_fma(__builtin_fma(-s64, y, 1.0), y, y);
+  return __builtin_fma(__builtin_fma(-s64, y, 1.0), y, y);
 }
 
 // int8 code of an fp32 quotient: clamp to [-128, 127] (v_med3_f32), then round to nearest
@@ -214,9 +248,9 @@ __host__ __device__ __forceinline__ void keep_branch() { asm volatile(""); }
 
 // Per-row quantisation state: the scale and, on the fast path, its reciprocal.
 struct RowScale {
-  float s;     // fp32(amax) / 127
-  float y;     // RN(1 / s) on the fast path; 0 for an all-zero row
-  bool fast;   // kFastDivMinScale <= s < inf, or s == 0
+  float s;      // fp32(amax) / 127
+  double y64;   // recip64(s) on the fast path (div_recip64); 0 for an all-zero row
+  bool fast;    // kFastDivMinScale <= s < inf, or s == 0
 };
 
 // RN(amax / 127) without a divide: q0 = amax * RN(1/127) is within ~1 ulp, and one FMA
@@ -242,15 +276,15 @@ __device__ __forceinline__ RowScale make_row_scale(float amax) {
   }
   if (r.s >= kFastDivMinScale && r.s < __builtin_inff()) {
     r.fast = true;
-    r.y = 1.0f / r.s;
+    r.y64 = recip64(r.s);  // once per row
   } else if (r.s == 0.0f) {
-    // All-zero row: with y = 0 every step of div_by_recip yields +-0, so all codes are 0
-    // and the scale stays 0 (the literal 0/0 of the reference math is not evaluated).
+    // All-zero row: with y64 = 0 every quotient is +-0, so all codes are 0 and the scale
+    // stays 0 (the literal 0/0 of the reference math is not evaluated).
     r.fast = true;
-    r.y = 0.0f;
+    r.y64 = 0.0;
   } else {
     r.fast = false;
-    r.y = 0.0f;
+    r.y64 = 0.0;
   }
   return r;
 }
@@ -269,7 +303,7 @@ __device__ __forceinline__ void encode_row(const float* v, const RowScale& r, ui
   float q[N];
   if (r.fast) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) q[i] = div_by_recip(v[i], r.s, r.y);
+    for (int i = 0; i < N; ++i) q[i] = div_recip64(v[i], r.y64);
   } else {
     keep_branch();
 #pragma unroll
@@ -293,7 +327,7 @@ __device__ __forceinline__ void encode_row(const float* v, const RowScale& r, ui
 __device__ __forceinline__ int8_t encode1(float v, const RowScale& r) {
   float q;
   if (r.fast) {
-    q = div_by_recip(v, r.s, r.y);
+    q = div_recip64(v, r.y64);
   } else {
     keep_branch();
     q = v / r.s;
@@ -421,13 +455,13 @@ __device__ __forceinline__ void encode_static(const float* q, uint32_t* out) {
 // ---------------------------------------------------------------------------- fp8 dynamic scales
 
 // float8_e4m3fn dynamic scale of a row / group: RN(amax / 448) (IEEE divide, once per row) and,
-// when kFastDivMinScale <= s < inf, y = RN(1 / s) for the reciprocal quotient (div_by_recip gives
-// the IEEE quotient there, as for the int8 scale).  s == 0 (an all-zero row): every code is +0.
+// when kFastDivMinScale <= s < inf, y64 = recip64(s) for the quotient div_recip64 (the IEEE
+// quotient there, as for the int8 scale).  s == 0 (an all-zero row): every code is +0.
 __device__ __forceinline__ RowScale make_fp8_scale(float amax) {
   RowScale r;
   r.s = amax / 448.0f;
   r.fast = r.s >= kFastDivMinScale && r.s < __builtin_inff();
-  r.y = r.fast ? 1.0f / r.s : 0.0f;
+  r.y64 = r.fast ? recip64(r.s) : 0.0;
   return r;
 }
 
@@ -437,12 +471,9 @@ template <int N>
 __device__ __forceinline__ void encode_fp8_row(const float* v, const RowScale& r, uint32_t* out) {
   float q[N];
   if (r.fast) {
+    // div_recip64 keeps the sign of a zero quotient (x * y64 with y64 > 0), as IEEE x / s
 #pragma unroll
-    for (int i = 0; i < N; ++i) q[i] = div_by_recip(v[i], r.s, r.y);
-    float sv[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) sv[i] = r.s;
-    quotient_signs<N>(q, v, sv);
+    for (int i = 0; i < N; ++i) q[i] = div_recip64(v[i], r.y64);
   } else {
     keep_branch();
 #pragma unroll

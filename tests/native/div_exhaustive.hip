@@ -1,11 +1,14 @@
-// Host-side check of the kernels' quotient (div_by_recip in tmo_device.h, the same source the
-// gfx950 kernels compile) against IEEE fp32 division.
+// Host-side check of the kernels' quotients (div_recip64, the fp64-product quotient of the
+// dynamic-scale encoders, and div_by_recip, the fp32 FMA quotient of the static scales, in
+// tmo_device.h, the same source the gfx950 kernels compile) against IEEE fp32 division.
 //
 //   bf16 : every positive finite bf16 amax whose scale amax/127 is on the fast path, against
-//          every bf16 x with 0 <= x <= amax (the quotient is odd in x, so this covers -x).
+//          every bf16 x with 0 <= x <= amax (the quotient is odd in x, so this covers -x);
+//          both quotients.
 //   f16  : the same over all finite fp16 values.
 //   f32  : random fp32 (amax, x) pairs over the fast-path exponent range plus, for each
-//          scale, inputs within +-3 ulps of (k + 0.5) * scale for every k in [-127, 127].
+//          scale, inputs within +-3 ulps of (k + 0.5) * scale for every k in [-127, 127];
+//          both quotients.
 //   scale: the divide-free row scale (scale_of) against IEEE amax / 127 for EVERY fp32 amax
 //          the kernels send through it (2^-100 up to the largest finite value).
 //   static: the static-scale quotient (static_quotients, per-element lane logic) for random
@@ -20,8 +23,9 @@
 // Two properties are checked on every pair:
 //   * the int8 code (clamp to [-128, 127], round half to even) of the kernel quotient equals
 //     the code of the IEEE quotient -- always;
-//   * the quotient bits themselves are identical whenever |x| >= 2^-100 (below that the FMA
-//     residual can underflow and the last bit may differ, but |x / s| < 2^-40 there).
+//   * the quotient bits themselves are identical: for div_by_recip whenever |x| >= 2^-100
+//     (below that the FMA residual can underflow and the last bit may differ, but
+//     |x / s| < 2^-40 there), for div_recip64 whenever the IEEE quotient is normal or zero.
 // Prints "mismatches=<n> checked=<m>" and exits non-zero on any mismatch.
 #include <algorithm>
 #include <cmath>
@@ -62,6 +66,23 @@ static bool differs(float x, float q, float r) {
   if (code_of(q) != code_of(r)) return true;
   return std::fabs(x) >= 0x1p-100f && bits_of(q) != bits_of(r);
 }
+static bool differs64(float q, float r) {
+  if (code_of(q) != code_of(r)) return true;
+  return (std::fabs(r) >= 0x1p-126f || r == 0.0f) && bits_of(q) != bits_of(r);
+}
+
+// Both quotients of one pair against the IEEE quotient r.
+static void check_pair(float amax, float x, float s, float y, double y64, Count& c) {
+  const float q = tmo::div_by_recip(x, s, y);
+  const float q64 = tmo::div_recip64(x, y64);
+  const float r = x / s;
+  ++c.checked;
+  if (differs(x, q, r) || differs64(q64, r)) {
+    if (c.bad < 5)
+      std::printf("mismatch amax=%a x=%a s=%a fma=%a fp64=%a ieee=%a\n", amax, x, s, q, q64, r);
+    ++c.bad;
+  }
+}
 
 // One amax: all x in [0, amax] of the format.
 template <class Conv>
@@ -70,17 +91,8 @@ static void check_amax(uint32_t a, Conv conv, Count& c) {
   const float s = amax / 127.0f;
   if (!(s >= tmo::kFastDivMinScale) || !(s < INFINITY)) return;  // IEEE path in the kernel
   const float y = 1.0f / s;
-  for (uint32_t xb = 0; xb <= a; ++xb) {
-    const float x = conv(xb);
-    const float q = tmo::div_by_recip(x, s, y);
-    const float r = x / s;
-    ++c.checked;
-    if (differs(x, q, r)) {
-      if (c.bad < 5)
-        std::printf("mismatch amax=%a x=%a s=%a fast=%a ieee=%a\n", amax, x, s, q, r);
-      ++c.bad;
-    }
-  }
+  const double y64 = 1.0 / (double)s;
+  for (uint32_t xb = 0; xb <= a; ++xb) check_pair(amax, conv(xb), s, y, y64, c);
 }
 
 template <class Conv>
@@ -114,22 +126,23 @@ static Count run_f32(unsigned long long n, int nthreads) {
         const float s = amax / 127.0f;
         if (!(s >= tmo::kFastDivMinScale) || !(s < INFINITY)) continue;
         const float y = 1.0f / s;
-        float xs[8];
+        const double y64 = 1.0 / (double)s;
+        float xs[15];
         // random x in [-amax, amax] and near-ties around (k + 0.5) * s
         const double u = (double)(rng() >> 11) / 9007199254740992.0;
         xs[0] = (float)((2.0 * u - 1.0) * amax);
         const int k = (int)(rng() % 255) - 127;
         const float t0 = (float)((k + 0.5) * (double)s);
         for (int d = 0; d < 7; ++d) xs[1 + d] = f_from_bits(bits_of(t0) + (uint32_t)(d - 3));
+        // x near m * s for a midpoint m between two adjacent fp32 quotients in (0, 127]: the
+        // quotient's own rounding boundary
+        const float qa = f_from_bits(0x3f800000u + (uint32_t)(rng() % (0x42fe0000u - 0x3f800000u)));
+        const double mq = 0.5 * ((double)qa + (double)f_from_bits(bits_of(qa) + 1u));
+        const float t1 = (float)(mq * (double)s) * ((rng() & 1) ? -1.0f : 1.0f);
+        for (int d = 0; d < 7; ++d) xs[8 + d] = f_from_bits(bits_of(t1) + (uint32_t)(d - 3));
         for (float x : xs) {
           if (!(std::fabs(x) <= amax)) continue;
-          const float q = tmo::div_by_recip(x, s, y);
-          const float r = x / s;
-          ++c.checked;
-          if (differs(x, q, r)) {
-            if (c.bad < 5) std::printf("mismatch amax=%a x=%a s=%a fast=%a ieee=%a\n", amax, x, s, q, r);
-            ++c.bad;
-          }
+          check_pair(amax, x, s, y, y64, c);
         }
       }
     });

@@ -14,6 +14,12 @@
 //   scan: wave_incl_sum_u32 (the DPP prefix sum of the grouped smooth quantiser) equals the
 //        serial inclusive prefix sum over the 64 lanes, on 2^21 wavefronts of hashed counts in
 //        [0, 2^25) (and on all-ones, to catch a lane that reads the wrong row).
+//   recip64: the dynamic scales' fp64 reciprocal (v_rcp_f32 + two fp64 Newton steps) has
+//        |1 - s * recip64(s)| <= 2^-52 for every fp32 s with 2^-60 <= s <= 2^126.
+//   div64: div_recip64 (the dynamic-scale encoders' quotient: v_cvt_f64_f32, v_mul_f64,
+//        v_cvt_f32_f64 with y64 = recip64(s)) against the IEEE quotient x / s for every bf16
+//        and every fp16 pair 0 <= x <= amax with s = amax / 127 on the fast path: the int8
+//        codes always, the quotient bits wherever the IEEE quotient is normal or 0.
 //   sqrt: __builtin_sqrtf (the fused rope's rms) is correctly rounded for every positive
 //        finite fp32 x: with m- and m+ the midpoints between r = sqrtf(x) and its neighbours,
 //        m-^2 < x < m+^2 (25-bit midpoints square exactly in fp64; no x sits on a midpoint).
@@ -81,6 +87,61 @@ __global__ __launch_bounds__(256) void check_scan(uint32_t waves, unsigned long 
     if (got != want) ++b;
   }
   if (b) atomicAdd(bad, b);
+}
+
+__global__ void check_recip64(uint32_t lo, uint32_t count, unsigned long long* bad) {
+  const uint32_t stride = gridDim.x * blockDim.x;
+  unsigned long long b = 0;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const float s = __uint_as_float(lo + i);
+    const double e = __builtin_fma(-(double)s, tmo::recip64(s), 1.0);  // exact 1 - s*y, rounded once
+    if (!(__builtin_fabs(e) <= 0x1p-52)) ++b;
+  }
+  if (b) atomicAdd(bad, b);
+}
+
+// One workgroup per amax bit pattern (blockIdx.x + 1), its threads striding over x in [0, amax].
+template <bool kF16>
+__global__ __launch_bounds__(256) void check_div64(uint32_t max_bits, unsigned long long* bad) {
+  const uint32_t a = blockIdx.x + 1;
+  if (a > max_bits) return;
+  const float amax = kF16 ? tmo::f16_bits_to_f32(a) : __uint_as_float(a << 16);
+  const float s = amax / 127.0f;
+  if (!(s >= tmo::kFastDivMinScale) || !(s < __builtin_inff())) return;
+  const double y64 = tmo::recip64(s);
+  unsigned long long b = 0;
+  for (uint32_t xb = threadIdx.x; xb <= a; xb += blockDim.x) {
+    const float x = kF16 ? tmo::f16_bits_to_f32(xb) : __uint_as_float(xb << 16);
+    const float q = tmo::div_recip64(x, y64), r = x / s;
+    const float cq = __builtin_rintf(__builtin_amdgcn_fmed3f(q, -128.0f, 127.0f));
+    const float cr = __builtin_rintf(__builtin_amdgcn_fmed3f(r, -128.0f, 127.0f));
+    const bool exact = __builtin_fabsf(r) >= 0x1p-126f || r == 0.0f;
+    if (cq != cr || (exact && __float_as_uint(q) != __float_as_uint(r))) ++b;
+  }
+  if (b) atomicAdd(bad, b);
+}
+
+// Pairs check_div64 compares (the same fast-path test on the host's IEEE division).
+unsigned long long div64_pairs(uint32_t max_bits, bool f16) {
+  unsigned long long n = 0;
+  for (uint32_t a = 1; a <= max_bits; ++a) {
+    float amax;
+    if (f16) {
+      const uint32_t e = (a >> 10) & 0x1f, m = a & 0x3ff;
+      if (e == 0) {
+        amax = (float)m * 5.9604644775390625e-08f;
+      } else {
+        const uint32_t u = ((e + 112u) << 23) | (m << 13);
+        std::memcpy(&amax, &u, 4);
+      }
+    } else {
+      const uint32_t u = a << 16;
+      std::memcpy(&amax, &u, 4);
+    }
+    const float s = amax / 127.0f;
+    if (s >= tmo::kFastDivMinScale && s < __builtin_inff()) n += a + 1;
+  }
+  return n;
 }
 
 __global__ void check_sqrt(unsigned long long* bad) {
@@ -204,6 +265,17 @@ int main(int argc, char** argv) {
     const uint32_t waves = 1u << 21;
     checked = 64ull * waves;
     check_scan<<<dim3(4096), dim3(256)>>>(waves, d_bad);
+  } else if (!std::strcmp(mode, "recip64")) {
+    uint32_t lo, hi;
+    const float flo = tmo::kFastDivMinScale, fhi = 0x1p126f;
+    std::memcpy(&lo, &flo, 4);
+    std::memcpy(&hi, &fhi, 4);
+    checked = (unsigned long long)(hi - lo) + 1;
+    check_recip64<<<dim3(8192), dim3(256)>>>(lo, hi - lo + 1, d_bad);
+  } else if (!std::strcmp(mode, "div64")) {
+    checked = div64_pairs(0x7f7fu, false) + div64_pairs(0x7bffu, true);
+    check_div64<false><<<dim3(0x7f7fu), dim3(256)>>>(0x7f7fu, d_bad);
+    check_div64<true><<<dim3(0x7bffu), dim3(256)>>>(0x7bffu, d_bad);
   } else if (!std::strcmp(mode, "sqrt")) {
     checked = 0x7f800000ull - 1;
     check_sqrt<<<dim3(8192), dim3(256)>>>(d_bad);
