@@ -560,24 +560,49 @@ __global__ __launch_bounds__(256) void lin_dequant(LinParams p) {
       unpack(F32{}, b, chan[kv] + 4);
     }
   }
-  Seq s = sequence(p, i, true);
   const int64_t j0 = tile * (kRows * kLinT) + threadIdx.x / G;
   bool ok[kLinT];
   int64_t r[kLinT], crow[kLinT];
   u32x2 code[kLinT][2];
   float tok_scale[kLinT][2];
+  Seq s;
+  if (!p.cache_off && !p.block_tables && !p.bs_id && i < p.blocks && p.block_rows > 0) {
+    // Cache row (i, h, j) needs no per-sequence number: the row loads go out together with the
+    // sequence's numbers, from the row clamped into the cache (a position past the sequence
+    // is read and not written), instead of waiting for the length first.
 #pragma unroll
-  for (int t = 0; t < kLinT; ++t) {
-    const int64_t j = j0 + t * kRows;
-    crow[t] = j < s.len ? cache_row(p, i, s.pos0 + j, h) : -1;
-    ok[t] = crow[t] >= 0;
-    if (!ok[t]) continue;
+    for (int t = 0; t < kLinT; ++t) {
+      const int64_t j = j0 + t * kRows;
+      const int64_t row = (i * p.heads + h) * p.block_rows + (j < p.block_rows ? j : p.block_rows - 1);
 #pragma unroll
-    for (int kv = 0; kv < 2; ++kv) {
-      if (kv >= p.nkv) continue;
-      code[t][kv] = stream_load(reinterpret_cast<const u32x2*>(
-          static_cast<const int8_t*>(p.cache[kv]) + crow[t] * p.head_dim + d0));
-      if (p.smode != 0) tok_scale[t][kv] = p.scale[kv][crow[t]];
+      for (int kv = 0; kv < 2; ++kv) {
+        if (kv >= p.nkv) continue;
+        code[t][kv] = stream_load(reinterpret_cast<const u32x2*>(
+            static_cast<const int8_t*>(p.cache[kv]) + row * p.head_dim + d0));
+        if (p.smode != 0) tok_scale[t][kv] = p.scale[kv][row];
+      }
+    }
+    s = sequence(p, i, true);
+#pragma unroll
+    for (int t = 0; t < kLinT; ++t) {
+      const int64_t j = j0 + t * kRows;
+      ok[t] = j < s.len && j < p.block_rows;
+    }
+  } else {
+    s = sequence(p, i, true);
+#pragma unroll
+    for (int t = 0; t < kLinT; ++t) {
+      const int64_t j = j0 + t * kRows;
+      crow[t] = j < s.len ? cache_row(p, i, s.pos0 + j, h) : -1;
+      ok[t] = crow[t] >= 0;
+      if (!ok[t]) continue;
+#pragma unroll
+      for (int kv = 0; kv < 2; ++kv) {
+        if (kv >= p.nkv) continue;
+        code[t][kv] = stream_load(reinterpret_cast<const u32x2*>(
+            static_cast<const int8_t*>(p.cache[kv]) + crow[t] * p.head_dim + d0));
+        if (p.smode != 0) tok_scale[t][kv] = p.scale[kv][crow[t]];
+      }
     }
   }
   finish_start(p, i, s);
