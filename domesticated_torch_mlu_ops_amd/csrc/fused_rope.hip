@@ -56,6 +56,17 @@ struct FusedRopeParams {
   int32_t bs_shift;
 };
 
+// K (kv 0) or V (kv 1) cache and scale pointers by value.  kv differs between the lane groups
+// of a wavefront, and indexing the kernel argument's array with it reads the pointer from
+// argument memory with a vector load, whose wait (the memory counter is in order) also waited
+// for the stores of the rows before it.
+__device__ __forceinline__ void* cache_of(const FusedRopeParams& p, int kv) {
+  return kv == 0 ? p.cache[0] : p.cache[1];
+}
+__device__ __forceinline__ float* scale_of_kv(const FusedRopeParams& p, int kv) {
+  return kv == 0 ? p.scale[0] : p.scale[1];
+}
+
 // Slot of token t.  A linear cache [max_batch, kv_heads, cache_len, head_size] is the paged
 // layout with one page of cache_len rows per cache batch, so token s of sequence b goes to
 // slot cache_bs_id[b] * cache_len + cache_seq_offsets[b] + s, or nowhere (-1) when the cache
@@ -266,7 +277,7 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
   if (p.scale_mode == 0) {
     u32x4 o;
     pack8(Tag{}, y, o);
-    *reinterpret_cast<u32x4*>(static_cast<char*>(p.cache[kv]) +
+    *reinterpret_cast<u32x4*>(static_cast<char*>(cache_of(p, kv)) +
                               (page_row * p.head_dim + lane * 8) * Tag::kBytes) = o;
     return;
   }
@@ -277,9 +288,9 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
     for (int e = 0; e < 8; ++e) m = abs_max(m, y[e]);
     const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<G>(__float_as_uint(m))));
     encode_row<8>(y, rs, c);
-    if (lane == 0) p.scale[kv][page_row] = rs.s;
+    if (lane == 0) scale_of_kv(p, kv)[page_row] = rs.s;
   } else {
-    const float* sp = p.scale[kv] + (int64_t)h * p.head_dim + lane * 8;
+    const float* sp = scale_of_kv(p, kv) + (int64_t)h * p.head_dim + lane * 8;
     float s[8], yr[8], q[8];
     bool fast = true;
 #pragma unroll
@@ -298,7 +309,7 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
   u32x2 c2;
   c2[0] = c[0];
   c2[1] = c[1];
-  *reinterpret_cast<u32x2*>(static_cast<int8_t*>(p.cache[kv]) + page_row * p.head_dim + lane * 8) = c2;
+  *reinterpret_cast<u32x2*>(static_cast<int8_t*>(cache_of(p, kv)) + page_row * p.head_dim + lane * 8) = c2;
 }
 
 // Token-major vector path: a workgroup owns one token (its position and slot are scalar loads,
@@ -341,6 +352,13 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
   u32x4 kbw = {0u, 0u, 0u, 0u};
   if (kNorm == 1 && p.k_beta)
     kbw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.k_beta) + lane * 16);
+  // Every loaded register is used once here, before the first store: the stores count in the
+  // same in-order memory counter as the loads, and a first use after a store (the rows after
+  // the first, the gammas and sin/cos loaded under branches) made the compiler wait for that
+  // store as well.
+#pragma unroll
+  for (int j = 0; j < kR; ++j) asm volatile("" ::"v"(xw[j]));
+  asm volatile("" ::"v"(sw), "v"(cw), "v"(kgw), "v"(qgw), "v"(kbw));
   // sin/cos, gammas and beta stay packed until their use in each row (fewer live VGPRs)
   const float sign = lane < c0 + hc ? -1.0f : 1.0f;  // rot = -partner in the window's first half
   const bool store_kv = slot >= 0 && (int64_t)slot < p.num_slots;  // workgroup-uniform
@@ -413,7 +431,7 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
     if (p.scale_mode == 0) {
       u32x4 o;
       pack8(Tag{}, y, o);
-      *reinterpret_cast<u32x4*>(static_cast<char*>(p.cache[kv]) +
+      *reinterpret_cast<u32x4*>(static_cast<char*>(cache_of(p, kv)) +
                                 (page_row * p.head_dim + lane * 8) * Tag::kBytes) = o;
       continue;
     }
@@ -424,9 +442,9 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
       for (int e = 0; e < 8; ++e) m = abs_max(m, y[e]);
       const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<G>(__float_as_uint(m))));
       encode_row<8>(y, rs, c);
-      if (lane == 0) p.scale[kv][page_row] = rs.s;
+      if (lane == 0) scale_of_kv(p, kv)[page_row] = rs.s;
     } else {
-      const float* sp = p.scale[kv] + (int64_t)h * p.head_dim + lane * 8;
+      const float* sp = scale_of_kv(p, kv) + (int64_t)h * p.head_dim + lane * 8;
       float sc[8], yr[8], q[8];
       bool fast = true;
 #pragma unroll
@@ -445,7 +463,7 @@ __global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
     u32x2 c2;
     c2[0] = c[0];
     c2[1] = c[1];
-    *reinterpret_cast<u32x2*>(static_cast<int8_t*>(p.cache[kv]) + page_row * p.head_dim + lane * 8) = c2;
+    *reinterpret_cast<u32x2*>(static_cast<int8_t*>(cache_of(p, kv)) + page_row * p.head_dim + lane * 8) = c2;
   }
 }
 
@@ -574,19 +592,19 @@ __global__ __launch_bounds__(256) void fused_rope_generic(FusedRopeParams p) {
   int64_t page_row;
   if (!page_row_of(p, token_slot(p, t), h, page_row)) return;
   if (p.scale_mode == 0) {
-    for (int d = lane; d < D; d += kWave) store1(Tag{}, p.cache[kv], page_row * D + d, out_at(d));
+    for (int d = lane; d < D; d += kWave) store1(Tag{}, cache_of(p, kv), page_row * D + d, out_at(d));
     return;
   }
-  int8_t* dst = static_cast<int8_t*>(p.cache[kv]) + page_row * D;
+  int8_t* dst = static_cast<int8_t*>(cache_of(p, kv)) + page_row * D;
   if (p.scale_mode == 1) {
     float m = 0.0f;
     for (int d = lane; d < D; d += kWave) m = abs_max(m, out_at(d));
     const RowScale rs = make_row_scale(__uint_as_float(group_max_u32<kWave>(__float_as_uint(m))));
     for (int d = lane; d < D; d += kWave) dst[d] = encode1(out_at(d), rs);
-    if (lane == 0) p.scale[kv][page_row] = rs.s;
+    if (lane == 0) scale_of_kv(p, kv)[page_row] = rs.s;
   } else {
     for (int d = lane; d < D; d += kWave) {
-      const float q = out_at(d) / p.scale[kv][(int64_t)h * D + d];  // IEEE divide
+      const float q = out_at(d) / scale_of_kv(p, kv)[(int64_t)h * D + d];  // IEEE divide
       dst[d] = (int8_t)(uint8_t)(code_bits(q) & 0xffu);
     }
   }

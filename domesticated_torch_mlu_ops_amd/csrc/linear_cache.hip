@@ -475,6 +475,10 @@ __global__ __launch_bounds__(256) void lin_quant(LinParams p) {
     }
   }
 
+  // Every row is encoded before the first store: the stores count in the same memory counter
+  // as the loads, so a row still to be read behind a store would wait for that store too.
+  u32x2 code[kLinT][2];
+  float rscale[kLinT][2];
 #pragma unroll
   for (int t = 0; t < kLinT; ++t) {
     if (!ok[t]) continue;
@@ -522,18 +526,29 @@ __global__ __launch_bounds__(256) void lin_quant(LinParams p) {
           encode_row<8>(v, rs, c);
           scale = rs.s;
         }
-        if ((lane & (gl - 1)) == 0)
-          __builtin_nontemporal_store(scale, p.scale[kv] + crow[t] * p.groups + lane / gl);
+        rscale[t][kv] = scale;
       }
-      u32x2 c2;
-      c2[0] = c[0];
-      c2[1] = c[1];
+      code[t][kv][0] = c[0];
+      code[t][kv][1] = c[1];
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kLinT; ++t) {
+    if (!ok[t]) continue;
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      if (kv >= p.nkv) continue;
+      if constexpr (!kStatic) {
+        const int gl = G / p.groups;
+        if ((lane & (gl - 1)) == 0)
+          __builtin_nontemporal_store(rscale[t][kv], p.scale[kv] + crow[t] * p.groups + lane / gl);
+      }
       u32x2* dst = reinterpret_cast<u32x2*>(static_cast<int8_t*>(p.cache[kv]) +
                                             crow[t] * p.head_dim + d0);
       if constexpr (TMO_LIN_NT_STORE) {
-        store_nt(dst, c2);
+        store_nt(dst, code[t][kv]);
       } else {
-        *dst = c2;
+        *dst = code[t][kv];
       }
     }
   }
