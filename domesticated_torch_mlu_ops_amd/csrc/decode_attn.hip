@@ -583,12 +583,22 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   int32_t slot = 0;  // index in the window of the most recently loaded tile
   Raw ra, rb;
   int32_t tile = first_tile + wave;
+  // Every call issues a tile's loads: a tile past the wave's range or on a missing page (its
+  // keys masked) re-reads the wave's last valid tile (in bounds and just read; page 0 before
+  // any) and is not computed.  With the loads under a branch, the register set was assigned
+  // on one path only, and the copies that merged it waited for the loads just issued -- the
+  // next tile's -- before the current tile was computed.
+  int32_t safe_tl = first_tile + wave;
+  int64_t safe_blk = 0;
   auto try_load = [&](Raw& r, int32_t tl) -> bool {
-    if (tl >= end_tile) return false;
     const int64_t blk = __builtin_amdgcn_readlane(lane_blk, slot);
-    if (blk < 0 || blk >= p.NB) return false;               // missing page: keys masked
-    load_tile(r, tl, blk);
-    return true;
+    const bool ok = tl < end_tile && blk >= 0 && blk < p.NB;  // wave-uniform
+    if (ok) {
+      safe_tl = tl;
+      safe_blk = blk;
+    }
+    load_tile(r, safe_tl, safe_blk);
+    return ok;
   };
   auto advance = [&]() {
     if (++slot == kWave) {
