@@ -76,6 +76,55 @@ __global__ __launch_bounds__(256) void reshape_paged_kernel(ReshapeParams p) {
   }
 }
 
+// Rows of exactly G vectors (one per lane), K and V: every load of a lane is issued before the
+// first wait.  Scatter: the token rows do not depend on the slot, so the slot and both rows
+// are read together (a V row that is absent re-reads K's).  Gather: the slot first, then both
+// page rows.  In the general kernel above the rows are moved one after the other, each load
+// waited for before its store, and the memory counter is in order: a thread paid the slot's,
+// K's and V's round trips in turn, V's behind K's store.
+template <int VW>
+__global__ __launch_bounds__(256) void reshape_paged_rows(ReshapeParams p) {
+  using V = typename VecOf<VW>::T;
+  const int G = 1 << p.g_shift;
+  const int lane = threadIdx.x & (G - 1);
+  const int rows = 256 >> p.g_shift;
+  int h;
+  int64_t tile;
+  xcd_tile_head(blockIdx.x, p.heads, h, tile);
+  const int64_t t = tile * rows + (threadIdx.x >> p.g_shift);
+  if (t >= p.num_tokens) return;
+  const int kv1 = p.nkv > 1 ? 1 : 0;
+  char* tk = p.kv[0] + t * p.stride_tok[0] + (int64_t)h * p.stride_head[0];
+  char* tv = p.kv[kv1] + t * p.stride_tok[kv1] + (int64_t)h * p.stride_head[kv1];
+  const int32_t slot = p.slot[t];
+  V a, b;
+  if (!p.gather) {
+    a = __builtin_nontemporal_load(reinterpret_cast<const V*>(tk) + lane);
+    b = __builtin_nontemporal_load(reinterpret_cast<const V*>(tv) + lane);
+  }
+  if (slot < 0 || (int64_t)slot >= p.num_slots) return;
+  int32_t blk, off;
+  if (p.bs_shift >= 0) {
+    blk = slot >> p.bs_shift;
+    off = slot & (p.block_size - 1);
+  } else {
+    blk = slot / p.block_size;
+    off = slot - blk * p.block_size;
+  }
+  const int64_t page_off = (((int64_t)blk * p.heads + h) * p.block_size + off) * p.row_bytes;
+  char* pk = p.cache[0] + page_off;
+  char* pv = p.cache[kv1] + page_off;
+  if (p.gather) {
+    a = __builtin_nontemporal_load(reinterpret_cast<const V*>(pk) + lane);
+    b = __builtin_nontemporal_load(reinterpret_cast<const V*>(pv) + lane);
+    __builtin_nontemporal_store(a, reinterpret_cast<V*>(tk) + lane);
+    if (p.nkv > 1) __builtin_nontemporal_store(b, reinterpret_cast<V*>(tv) + lane);
+  } else {
+    __builtin_nontemporal_store(a, reinterpret_cast<V*>(pk) + lane);
+    if (p.nkv > 1) __builtin_nontemporal_store(b, reinterpret_cast<V*>(pv) + lane);
+  }
+}
+
 template <int VW>
 int launch(const ReshapeParams& p0, hipStream_t stream) {
   ReshapeParams p = p0;
@@ -86,6 +135,8 @@ int launch(const ReshapeParams& p0, hipStream_t stream) {
   const int rows = 256 / g;
   const int64_t blocks = xcd_grid_tiles((p.num_tokens + rows - 1) / rows) * p.heads;
   if (blocks > 0x7fffffffLL) return TMO_ERR_INVALID_ARGUMENT;
+  if (p.units == g)
+    return launch_kernel(reshape_paged_rows<VW>, dim3((unsigned)blocks), dim3(256), stream, p);
   return launch_kernel(reshape_paged_kernel<VW>, dim3((unsigned)blocks), dim3(256), stream, p);
 }
 
