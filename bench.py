@@ -65,7 +65,7 @@ KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<
            "fused_rope": "fused_rope_tok<BF16,16,3,0>", "fused_rope_ln": "fused_rope_tok<BF16,16,3,1>",
            "linear_quant": "lin_quant<BF16,16,false,false,true>", "linear_dequant": "lin_dequant<BF16,16>",
            "linear_reshape": "lin_copy<16,true>", "decode_attn": "attn_mfma<128,0,false>",
-           "reshape_paged": "reshape_paged_kernel<16>"}
+           "reshape_paged": "reshape_paged_rows<16>"}
 
 
 def parse_args():

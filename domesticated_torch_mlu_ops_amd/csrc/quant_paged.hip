@@ -193,6 +193,9 @@ struct StaticScales {
   const float* chan[2];  // [heads, head_dim] fp32 per-channel scales, or null: per tensor
   float tensor[2];
 };
+// Read in place of an absent per-channel scale table (at most 64 lanes of at most 8 floats).
+__device__ __align__(16) const float kNoScales[512] = {};
+
 struct StaticParams {
   QuantPagedParams q;
   StaticScales sc;
@@ -207,8 +210,8 @@ struct StaticParams {
 // Vector path of the static quantiser: one 16-byte vector per lane, G lanes per row (as the
 // dynamic kernel with V = 1), a workgroup owns kT * 256/G consecutive tokens of one head.  A
 // lane always covers the same kPerVec channels of its head, so it loads their scales once
-// (before the rows, so that waiting for them does not wait for the rows) and computes the
-// reciprocals once for its kT tokens.  There is no row reduction and no scale store.
+// and computes the reciprocals once for its kT tokens.  There is no row reduction and no
+// scale store.
 template <class Tag, int G, bool kFp8>
 __global__ __launch_bounds__(256) void quant_paged_static_vec(StaticParams sp) {
   const QuantPagedParams& p = sp.q;
@@ -227,25 +230,6 @@ __global__ __launch_bounds__(256) void quant_paged_static_vec(StaticParams sp) {
 #endif
   const int64_t t0 = tile * (kGroups * kT) + threadIdx.x / G;
 
-  float s[2][kPer];
-#pragma unroll
-  for (int kv = 0; kv < 2; ++kv) {
-    if (kv < p.nkv) {
-      if (sc.chan[kv]) {
-        const u32x4* sp = reinterpret_cast<const u32x4*>(sc.chan[kv] + (int64_t)h * p.head_dim +
-                                                         lane * kPer);
-#pragma unroll
-        for (int q = 0; q < kPer / 4; ++q) {
-          const u32x4 t = sp[q];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) s[kv][4 * q + i] = __uint_as_float(t[i]);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < kPer; ++e) s[kv][e] = sc.tensor[kv];
-      }
-    }
-  }
   // Tokens past the end load the last token's row again (an L2 hit) and are skipped below:
   // every load is unconditional, so the waits before the first row count exactly.
   int32_t slot[kT];
@@ -264,6 +248,29 @@ __global__ __launch_bounds__(256) void quant_paged_static_vec(StaticParams sp) {
       }
     }
     if (t >= p.num_tokens) slot[j] = -1;
+  }
+  float s[2][kPer];
+  {
+    // Both tables' loads go out with the rows, before the first wait: an absent table (a
+    // per-tensor scale, or no V) reads kNoScales instead, and the values are chosen
+    // afterwards.  Loaded under a per-channel / per-tensor branch, each table was waited for
+    // where the branch merged, K's before V's loads were issued (37.2 -> 36.6 us on configs[2]'s
+    // shape per channel).
+    u32x4 raw[2][kPer / 4];
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      typedef const __attribute__((address_space(1))) float* gptr;
+      const gptr base = sc.chan[kv] ? (gptr)(sc.chan[kv] + (int64_t)h * p.head_dim + lane * kPer)
+                                    : (gptr)(kNoScales + lane * kPer);
+#pragma unroll
+      for (int q = 0; q < kPer / 4; ++q)
+        raw[kv][q] = reinterpret_cast<const __attribute__((address_space(1))) u32x4*>(base)[q];
+    }
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv)
+#pragma unroll
+      for (int e = 0; e < kPer; ++e)
+        s[kv][e] = sc.chan[kv] ? __uint_as_float(raw[kv][e / 4][e % 4]) : sc.tensor[kv];
   }
   float y[2][kPer];
   bool fast[2];
