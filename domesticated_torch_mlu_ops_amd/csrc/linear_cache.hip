@@ -349,7 +349,7 @@ __global__ __launch_bounds__(256) void lin_copy(LinParams p) {
       if (kv >= p.nkv) continue;
       char* tk = static_cast<char*>(p.tok[kv]) + (r[t] * p.st[kv] + (int64_t)h * p.sh[kv]) * es;
       char* c = static_cast<char*>(p.cache[kv]) + crow[t] * row_bytes;
-      *reinterpret_cast<u32x4*>((kTM || p.in_dir ? c : tk) + lane * 16) = v[t][kv];
+      __builtin_nontemporal_store(v[t][kv], reinterpret_cast<u32x4*>((kTM || p.in_dir ? c : tk) + lane * 16));
     }
   }
 }
@@ -391,13 +391,13 @@ __device__ __forceinline__ void store8(void* base, int64_t e, const float* v) {
       b[k] = __float_as_uint(v[4 + k]);
     }
     u32x4* q = reinterpret_cast<u32x4*>(static_cast<float*>(base) + e);
-    q[0] = a;
-    q[1] = b;
+    __builtin_nontemporal_store(a, q);
+    __builtin_nontemporal_store(b, q + 1);
   } else {
     u32x4 w;
 #pragma unroll
     for (int k = 0; k < 4; ++k) w[k] = pack2(Tag{}, v[2 * k], v[2 * k + 1]);
-    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + e) = w;
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + e));
   }
 }
 
@@ -626,19 +626,32 @@ __global__ __launch_bounds__(256) void lin_dequant(LinParams p) {
     r[t] = s.start + j0 + t * kRows;
     ok[t] = ok[t] && r[t] >= 0 && r[t] < p.rows;
   }
+  // Both rows are converted before the first store: the stores count in the same in-order
+  // memory counter as the loads, and a wait for V's codes placed after K's store (the
+  // compiler cannot count across the two load paths above) waited for that store as well.
+  float out[kLinT][2][8];
+#pragma unroll
+  for (int t = 0; t < kLinT; ++t) {
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float sc = p.smode == 0 ? chan[kv][e] : tok_scale[t][kv];
+        out[t][kv][e] = (float)(int8_t)(code[t][kv][e >> 2] >> (8 * (e & 3))) * sc;
+      }
+      // used here, so the scheduler cannot move the conversion (and its wait) past a store
+      asm volatile("" ::"v"(out[t][kv][0]), "v"(out[t][kv][1]), "v"(out[t][kv][2]),
+                   "v"(out[t][kv][3]), "v"(out[t][kv][4]), "v"(out[t][kv][5]),
+                   "v"(out[t][kv][6]), "v"(out[t][kv][7]));
+    }
+  }
 #pragma unroll
   for (int t = 0; t < kLinT; ++t) {
     if (!ok[t]) continue;
 #pragma unroll
     for (int kv = 0; kv < 2; ++kv) {
       if (kv >= p.nkv) continue;
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float sc = p.smode == 0 ? chan[kv][e] : tok_scale[t][kv];
-        v[e] = (float)(int8_t)(code[t][kv][e >> 2] >> (8 * (e & 3))) * sc;
-      }
-      store8<Tag>(p.tok[kv], r[t] * p.st[kv] + (int64_t)h * p.sh[kv] + d0, v);
+      store8<Tag>(p.tok[kv], r[t] * p.st[kv] + (int64_t)h * p.sh[kv] + d0, out[t][kv]);
     }
   }
 }
