@@ -308,6 +308,19 @@ def test_dequant_from_linear_cache(tmo, ref, dev, dtype, mode, offsets):
     _dequant_both(tmo, ref, dev, case, dtype, mode)
 
 
+@pytest.mark.parametrize("mode", [0, 1])
+def test_dequant_from_linear_cache_direct_rows_edges(tmo, ref, dev, mode):
+    """No cache offsets, batch ids or block tables (cache row (i, h, j) read before the length
+    arrives): sequences longer than cache_len (positions past it are not written) and more
+    sequences than cache batches (the extra ones write nothing)."""
+    case = W.linear_case(torch.bfloat16, 405, packed=True, offsets=False, B=6, S=24)
+    case.cache_len = 16
+    case.cache_batch = 4
+    assert int(case.lens.max()) > case.cache_len
+    _dequant_both(tmo, ref, dev, case, torch.bfloat16, mode)
+    _dequant_both(tmo, ref, dev, case, torch.float16, mode, with_v=False)
+
+
 @pytest.mark.parametrize("D", [8, 16, 64, 256, 512, 72, 20])
 def test_dequant_from_linear_cache_widths(tmo, ref, dev, D):
     case = W.linear_case(torch.bfloat16, 63 + D, packed=True, offsets=True, D=D)

@@ -502,6 +502,41 @@ def test_reshape_paged_cache_roundtrip(tmo, ref, dev, dtype, D):
     assert torch.equal(_bits(gkb)[valid], _bits(k)[valid])  # gather(scatter(x)) == x
 
 
+@pytest.mark.parametrize("with_v", [True, False])
+def test_reshape_paged_cache_views_and_k_only(tmo, ref, dev, with_v):
+    """K and V as strided views into a fused [T, 3H, D] qkv tensor (one 16-byte vector per
+    lane: the rows kernel), with and without V, scatter and then gather, against the oracle."""
+    T, H, NB, BS, D = 70, 4, 20, 16, 128
+    g = torch.Generator().manual_seed(404)
+    qkv = torch.randn(T, 3 * H, D, generator=g).to(torch.bfloat16)
+    slot = torch.randperm(NB * BS, generator=g)[:T].to(torch.int32)
+    slot[::7] = -1
+    slot[3] = NB * BS
+    k, v = qkv[:, H:2 * H], qkv[:, 2 * H:]
+    case = W.PagedQuantCase("reshape", k.contiguous(), v.contiguous(), slot, NB, BS)
+    kc, vc, _, _ = case.empty_caches(dtype=torch.bfloat16)
+    ref.reshape_paged_cache(k, v if with_v else None, kc, vc if with_v else None, slot, False)
+    gq = qkv.to(dev)
+    gk, gv, _, _ = case.empty_caches(device=dev, dtype=torch.bfloat16)
+    gvv = gq[:, 2 * H:] if with_v else None
+    tmo.reshape_paged_cache(gq[:, H:2 * H], gvv, gk, gv if with_v else None, slot.to(dev), False)
+    torch.cuda.synchronize()
+    assert_bits_equal(gk, kc, "scatter k_cache (view)")
+    if with_v:
+        assert_bits_equal(gv, vc, "scatter v_cache (view)")
+    else:
+        assert_bits_equal(gv, vc, "v_cache untouched")  # both still the sentinel fill
+    # gather back into the views of a fresh qkv: the Q slice and the skipped rows keep their bytes
+    back = torch.full_like(qkv, -7.0)
+    ref.reshape_paged_cache(back[:, H:2 * H], back[:, 2 * H:] if with_v else None, kc,
+                            vc if with_v else None, slot, True)
+    gback = torch.full_like(gq, -7.0)
+    tmo.reshape_paged_cache(gback[:, H:2 * H], gback[:, 2 * H:] if with_v else None, gk,
+                            gv if with_v else None, slot.to(dev), True)
+    torch.cuda.synchronize()
+    assert_bits_equal(gback, back, "gather into qkv views")
+
+
 def test_reshape_paged_cache_cfg3(tmo, ref, dev):
     case = W.cfg3()
     kc, vc, _, _ = case.empty_caches(dtype=torch.bfloat16)
