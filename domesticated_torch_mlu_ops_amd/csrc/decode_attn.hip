@@ -730,36 +730,89 @@ __global__ __launch_bounds__(256) void attn_combine(AttnParams p) {
     live = (int)(n < p.splits ? n : p.splits);
     if (live < 1 && p.splits > 0) live = r0.begin < sq.L ? 1 : 0;
   }
+  // Every load is unconditional (split and channel indices clamped into this column's rows of
+  // the workspace; an empty split's row is read and given weight 0), so the loads of a batch
+  // issue together.  Under the per-split weight test each row load waited for the previous
+  // one: up to 2 x live round trips per wavefront.
+  const int last = live > 0 ? live - 1 : 0;
+  const int64_t qrow = sq.row0 + tok;
+  const int64_t orow = i * p.o_sb + qrow * p.o_ss + (int64_t)hq * p.o_sh;
+  constexpr int kBatch = 8;
+  if (live <= kWave) {  // wave-uniform; every launch of the torch op (at most 63 splits)
+    // lane s holds split s's (max, sum), loaded once; the values in batches of kBatch splits
+    const int sc = lane < live ? lane : last;
+    const float m_raw = base[sc * stride], l_raw = base[sc * stride + 1];
+    const float m = lane < live ? m_raw : -__builtin_inff();
+    float mx = m;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+    const float wgt = m != -__builtin_inff() ? l_raw * __builtin_amdgcn_exp2f(m - mx) : 0.0f;
+    float lt = wgt;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) lt += __shfl_xor(lt, o, kWave);
+    float lse_v;
+    const float inv = finish(p, hq, mx, lt, &lse_v);
+    for (int d0 = 0; d0 < p.Dv; d0 += kWave) {
+      const int d = d0 + lane;
+      const int dc = d < p.Dv ? d : p.Dv - 1;
+      float o = 0.0f;
+      for (int k0 = 0; k0 < live; k0 += kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) v[k] = base[(k0 + k < live ? k0 + k : last) * stride + 2 + dc];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const float wk = __shfl(wgt, k0 + k < live ? k0 + k : 0, kWave);
+          if (k0 + k < live && wk != 0.0f) o += v[k] * wk;
+        }
+      }
+      if (d < p.Dv) store_out(p, orow + d, o * inv);
+    }
+    if (lane == 0 && p.lse) p.lse[i * p.lse_sb + qrow * p.lse_ss + (int64_t)hq * p.lse_sh] = lse_v;
+    return;
+  }
   float mx = -__builtin_inff();
   for (int s0 = 0; s0 < live; s0 += kWave) {
     const int s = s0 + lane;
-    mx = fmaxf(mx, s < live ? base[s * stride] : -__builtin_inff());
+    const float m = base[(s < live ? s : last) * stride];
+    mx = fmaxf(mx, s < live ? m : -__builtin_inff());
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
   float lt = 0.0f;
   for (int s0 = 0; s0 < live; s0 += kWave) {
     const int s = s0 + lane;
-    const float m = s < live ? base[s * stride] : -__builtin_inff();
-    lt += m != -__builtin_inff() ? base[s * stride + 1] * __builtin_amdgcn_exp2f(m - mx) : 0.0f;
+    const int sc = s < live ? s : last;
+    const float m = s < live ? base[sc * stride] : -__builtin_inff();
+    const float l = base[sc * stride + 1];
+    lt += m != -__builtin_inff() ? l * __builtin_amdgcn_exp2f(m - mx) : 0.0f;
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) lt += __shfl_xor(lt, o, kWave);
   float lse_v;
   const float inv = finish(p, hq, mx, lt, &lse_v);
-  const int64_t qrow = sq.row0 + tok;
-  const int64_t orow = i * p.o_sb + qrow * p.o_ss + (int64_t)hq * p.o_sh;
   for (int d0 = 0; d0 < p.Dv; d0 += kWave) {
     const int d = d0 + lane;
+    const int dc = d < p.Dv ? d : p.Dv - 1;
     float o = 0.0f;
     for (int s0 = 0; s0 < live; s0 += kWave) {
       const int sl = s0 + lane;
-      const float m = sl < live ? base[sl * stride] : -__builtin_inff();
-      const float wgt = m != -__builtin_inff() ? base[sl * stride + 1] * __builtin_amdgcn_exp2f(m - mx) : 0.0f;
+      const int sc = sl < live ? sl : last;
+      const float m = sl < live ? base[sc * stride] : -__builtin_inff();
+      const float wgt = m != -__builtin_inff() ? base[sc * stride + 1] * __builtin_amdgcn_exp2f(m - mx) : 0.0f;
       const int n = live - s0 < kWave ? live - s0 : kWave;
-      for (int k = 0; k < n; ++k) {
-        const float wk = __shfl(wgt, k, kWave);
-        if (wk != 0.0f && d < p.Dv) o += base[(s0 + k) * stride + 2 + d] * wk;
+      for (int k0 = 0; k0 < n; k0 += kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const int s = s0 + (k0 + k < n ? k0 + k : n - 1);
+          v[k] = base[s * stride + 2 + dc];
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const float wk = __shfl(wgt, k0 + k < n ? k0 + k : 0, kWave);
+          if (k0 + k < n && wk != 0.0f) o += v[k] * wk;
+        }
       }
     }
     if (d < p.Dv) store_out(p, orow + d, o * inv);
