@@ -50,6 +50,7 @@ WORKLOADS = {
     "offline_i8": "offline_quant_to_paged_cache on configs[2]'s shape (32768 tokens x 8 KV heads x 128 bf16), static per-channel scales -> int8 pages",
     "offline_f8": "offline_quant_to_paged_cache on configs[2]'s shape (32768 tokens x 8 KV heads x 128 bf16), static per-channel scales -> float8_e4m3fn pages",
     "fused_rope": "fused_rmsnorm_rope_store_paged_cache, Llama-3-8B prefill chunk: 8 x 4096 tokens, 32 Q + 8 KV heads x 128 bf16, Q written back, K/V -> int8 pages with dynamic per-token scales (65536 blocks x 16)",
+    "fused_rope_70b": "fused_rmsnorm_rope_store_paged_cache, Llama-3-70B prefill chunk: 8 x 4096 tokens, 64 Q + 8 KV heads x 128 bf16, Q written back, K/V -> int8 pages with dynamic per-token scales (65536 blocks x 16)",
     "fused_rope_ln": "fused_rope, norm_type layernorm (rotate, then layer_norm of K with gamma and beta) on the fused_rope workload's shape: 8 x 4096 tokens, 32 Q + 8 KV heads x 128 bf16 -> int8 pages with dynamic per-token scales",
     "linear_quant": "quant_to_linear_cache on configs[2]'s volume: 8 packed sequences x 4096 tokens x 8 KV heads x 128 bf16 -> int8 linear cache [8, 8, 8192, 128] + fp32 per-token scales",
     "linear_dequant": "dequant_from_linear_cache (per-token scales), 8 sequences x 4096 tokens x 8 KV heads x 128: int8 linear cache [8, 8, 8192, 128] -> bf16",
@@ -63,6 +64,7 @@ KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<
            "offline_i8": "quant_paged_static_vec<BF16,16,false>",
            "offline_f8": "quant_paged_static_vec<BF16,16,true>",
            "fused_rope": "fused_rope_tok<BF16,16,3,0>", "fused_rope_ln": "fused_rope_tok<BF16,16,3,1>",
+           "fused_rope_70b": "fused_rope_tok<BF16,16,5,0>",
            "linear_quant": "lin_quant<BF16,16,false,false,true>", "linear_dequant": "lin_dequant<BF16,16>",
            "linear_reshape": "lin_copy<16,true>", "decode_attn": "attn_mfma<128,0,false>",
            "reshape_paged": "reshape_paged_rows<16>"}
@@ -224,25 +226,30 @@ def bench_offline(torch, tmo, W, case, cache_dtype, dev, steps, warmup):
 
 
 FR_B, FR_S, FR_HQ, FR_HK = 8, 4096, 32, 8
+FR_HQ_70B = 64  # Llama-3-70B: 64 query heads, 8 KV heads
 
 
-def fused_rope_bytes(T: int, rope: int = 128) -> int:
+def fr_q_heads(name: str) -> int:
+    return FR_HQ_70B if name == "fused_rope_70b" else FR_HQ
+
+
+def fused_rope_bytes(T: int, rope: int = 128, hq: int = FR_HQ) -> int:
     """Algorithmic bytes of the fused_rope workload: qkv read once, Q written back, K/V codes
     and scales written, the slot mapping, one sin and one cos row per token, the gammas."""
-    D, H = W_D, FR_HQ + 2 * FR_HK
-    return (T * H * D * 2 + T * FR_HQ * D * 2 + 2 * T * FR_HK * (D + 4) + 4 * T
+    D, H = W_D, hq + 2 * FR_HK
+    return (T * H * D * 2 + T * hq * D * 2 + 2 * T * FR_HK * (D + 4) + 4 * T
             + 2 * T * rope * 2 + 2 * D * 2 + 4 * FR_B)
 
 
 W_D = 128
 
 
-def bench_fused_rope(torch, tmo, W, dev, steps, warmup, layernorm=False):
+def bench_fused_rope(torch, tmo, W, dev, steps, warmup, layernorm=False, hq=FR_HQ):
     """fused_rmsnorm_rope_store_paged_cache (or fused_rope with norm_type "layernorm") on a
-    Llama-3-8B-shaped prefill chunk: per set its own qkv; shared int8 caches and scales,
-    configs[2]-style slots shifted per set."""
+    Llama-3-8B-shaped prefill chunk (hq = 64: Llama-3-70B): per set its own qkv; shared int8
+    caches and scales, configs[2]-style slots shifted per set."""
     T = FR_B * FR_S
-    alg = fused_rope_bytes(T)
+    alg = fused_rope_bytes(T, hq=hq)
     sets = n_sets(alg)
     g = torch.Generator(device=dev).manual_seed(11)
     case3 = W.cfg3()
@@ -263,7 +270,7 @@ def bench_fused_rope(torch, tmo, W, dev, steps, warmup, layernorm=False):
     qg = (0.5 + torch.rand(W_D, generator=g, device=dev)).to(torch.bfloat16)
     calls = []
     for s in range(sets):
-        qkv = torch.randn((FR_B, FR_S, FR_HQ + 2 * FR_HK, W_D), generator=g, device=dev).to(torch.bfloat16)
+        qkv = torch.randn((FR_B, FR_S, hq + 2 * FR_HK, W_D), generator=g, device=dev).to(torch.bfloat16)
         shift = (s * 9973 * case3.block_size) % nslots
         slots = (slots0 + shift) % nslots
         if layernorm:  # qg serves as k_beta
@@ -420,7 +427,8 @@ def profile_pass(torch, tmo, W, names, dev, n: int) -> None:
             fn = lambda: tmo.offline_quant_to_paged_cache(k, v, ks, ks, sl, kc, vc)
         elif name.startswith("fused_rope"):
             case3 = W.cfg3()
-            qkv = torch.randn((FR_B, FR_S, FR_HQ + 2 * FR_HK, W_D), device=dev).to(torch.bfloat16)
+            qkv = torch.randn((FR_B, FR_S, fr_q_heads(name) + 2 * FR_HK, W_D),
+                              device=dev).to(torch.bfloat16)
             kc = torch.zeros((case3.num_blocks, FR_HK, 16, W_D), dtype=torch.int8, device=dev)
             vc = torch.zeros_like(kc)
             ks = torch.zeros(kc.shape[:3], device=dev)
@@ -554,7 +562,8 @@ def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
         ln = workload == "fused_rope_ln"
         n = 512
         g = torch.Generator().manual_seed(3)
-        qkv = torch.randn((1, n, FR_HQ + 2 * FR_HK, W_D), generator=g).to(torch.bfloat16)
+        hq = fr_q_heads(workload)
+        qkv = torch.randn((1, n, hq + 2 * FR_HK, W_D), generator=g).to(torch.bfloat16)
         kc = torch.zeros((n // 16, FR_HK, 16, W_D), dtype=torch.int8)
         vc = torch.zeros_like(kc)
         ks = torch.zeros(kc.shape[:3])
@@ -567,7 +576,7 @@ def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
                                              None if ln else gm, nthreads=nthreads,
                                              norm_type="layernorm" if ln else "rmsnorm",
                                              k_beta=gm if ln else None)
-        alg, units, desc = fused_rope_bytes(n), n, f"fused rope of one {n}-token sequence"
+        alg, units, desc = fused_rope_bytes(n, hq=hq), n, f"fused rope of one {n}-token sequence"
     elif workload == "decode_attn":
         layout = W.cfg5()
         nseq = 2
@@ -690,8 +699,8 @@ def main():
     dev = torch.device("cuda", 0)
     todo = [args.workload] if args.configs == "headline" else \
         ["cfg1", "cfg2", "cfg3", "cfg4", "cfg4_moe", "cfg5", "offline_i8", "offline_f8",
-         "fused_rope", "fused_rope_ln", "linear_quant", "linear_dequant", "linear_reshape",
-         "decode_attn", "reshape_paged"]
+         "fused_rope", "fused_rope_ln", "fused_rope_70b", "linear_quant", "linear_dequant",
+         "linear_reshape", "decode_attn", "reshape_paged"]
     if args.workload not in todo:
         todo.append(args.workload)
     if args.profile_pass:
@@ -722,7 +731,8 @@ def main():
                                                  args.warmup)
         elif name.startswith("fused_rope"):
             ms, alg, units, sets = bench_fused_rope(torch, tmo, W, dev, max(20, args.steps // 4),
-                                                    args.warmup // 4, name == "fused_rope_ln")
+                                                    args.warmup // 4, name == "fused_rope_ln",
+                                                    fr_q_heads(name))
         elif name.startswith("linear"):
             ms, alg, units, sets = bench_linear(torch, tmo, name, dev, max(20, args.steps // 4),
                                                 max(4, args.warmup // 4))
@@ -774,6 +784,7 @@ def main():
                           "offline_f8": "bf16 in; float8_e4m3fn codes out (static per-channel scales)",
                           "fused_rope": "bf16 qkv in; bf16 Q written back; int8 K/V codes + fp32 scales out",
                           "fused_rope_ln": "bf16 qkv in; bf16 Q written back; int8 K/V codes + fp32 scales out",
+                          "fused_rope_70b": "bf16 qkv in; bf16 Q written back; int8 K/V codes + fp32 scales out",
                           "linear_dequant": "int8 codes + fp32 scales in; bf16 out",
                           "linear_reshape": "bf16 in; bf16 out",
                           "reshape_paged": "bf16 K/V rows in; bf16 pages out",

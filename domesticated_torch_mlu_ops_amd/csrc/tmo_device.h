@@ -402,6 +402,30 @@ __device__ __forceinline__ float recip_rn(float s) {
   return __builtin_fmaf(__builtin_fmaf(-s, y0, 1.0f), y0, y0);
 }
 
+// RN(sqrt(a)) for kSqrtMin <= a <= FLT_MAX in 8 VALU instructions (the IEEE square root
+// adds input scaling for tiny a and special-value handling, 17 in all): v_sqrt_f32 (within
+// 1 ulp), then s, its lower neighbour or its upper neighbour by the signs of the exact FMA
+// residuals a - c * c+ of the adjacent pairs (c, c+) = (s-, s) and (s, s+).  With u = ulp(c),
+// c = C u, the midpoint satisfies (c + u/2)^2 = c * c+ + u^2 / 4, and a, an fp32 number of
+// about c^2, is a multiple of 2^23 u^2, so it never lies strictly between c * c+ and the
+// squared midpoint: a > c * c+ exactly when sqrt(a) is above the midpoint, and a = c * c+
+// (possible, e.g. C = 2^23) is below it.  The residuals are multiples of u^2 >= 2^-144 for
+// a >= 2^-96, so their signs survive the FMA's rounding (fp32 denormals are kept).
+// tests/native/div_exhaustive.hip ("sqrt") checks the choice on the CPU, given the correctly
+// rounded root or either neighbour as s; tests/native/gfx950_builtins.hip ("sqrt") checks
+// sqrt_rn on the GPU for every fp32 a of the range.
+constexpr float kSqrtMin = 1.26217745e-29f;  // 2^-96
+__host__ __device__ __forceinline__ float sqrt_choose(float a, float s) {
+  const float dn = bitsf(fbits(s) - 1u);
+  const float up = bitsf(fbits(s) + 1u);
+  float r = __builtin_fmaf(-dn, s, a) <= 0.0f ? dn : s;
+  r = __builtin_fmaf(-up, s, a) > 0.0f ? up : r;
+  return r;
+}
+__device__ __forceinline__ float sqrt_rn(float a) {
+  return sqrt_choose(a, __builtin_amdgcn_sqrtf(a));
+}
+
 // Four values already clamped to [-448, 448] -> four float8_e4m3fn bytes (little-endian in
 // the result) with gfx950's v_cvt_pk_fp8_f32 (OCP e4m3fn, round to nearest even, two values
 // per instruction).  tests/native/gfx950_builtins.hip ("fp8") checks it on the GPU against

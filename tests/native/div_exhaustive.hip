@@ -19,6 +19,8 @@
 //          bits whenever |x| >= 2^-100 and the IEEE quotient is normal, or x is zero.
 //   fp8:   fp8e4m3_bits against a nearest-value search over the 127 positive e4m3 values
 //          (ties to the even code) for EVERY fp32 value in [-448, 448].
+//   sqrt:  sqrt_choose (the correction step of the fused rope's square root) for EVERY fp32
+//          a in [2^-96, FLT_MAX], given the correctly rounded root or a neighbour of it.
 //
 // Two properties are checked on every pair:
 //   * the int8 code (clamp to [-128, 127], round half to even) of the kernel quotient equals
@@ -181,6 +183,41 @@ static Count run_scale(int nthreads) {
   return total;
 }
 
+// ---- square root choice
+
+// sqrt_choose (the kernels' sqrt_rn after v_sqrt_f32) for EVERY fp32 a in [2^-96, FLT_MAX]:
+// given the correctly rounded root r = sqrtf(a) or either of its neighbours as the approximate
+// root s, it must return r.
+static Count run_sqrt(int nthreads) {
+  std::vector<Count> per(nthreads);
+  std::vector<std::thread> th;
+  const uint32_t lo = bits_of(tmo::kSqrtMin), hi = 0x7f7fffffu;
+  for (int t = 0; t < nthreads; ++t)
+    th.emplace_back([&, t] {
+      Count& c = per[t];
+      for (uint32_t b = lo + t; b <= hi; b += nthreads) {
+        const float a = f_from_bits(b);
+        const float r = std::sqrt(a);
+        for (int d = -1; d <= 1; ++d) {
+          const float s = f_from_bits(bits_of(r) + (uint32_t)d);
+          const float got = tmo::sqrt_choose(a, s);
+          ++c.checked;
+          if (bits_of(got) != bits_of(r)) {
+            if (c.bad < 5) std::printf("sqrt mismatch a=%a s=%a got=%a ieee=%a\n", a, s, got, r);
+            ++c.bad;
+          }
+        }
+      }
+    });
+  for (auto& x : th) x.join();
+  Count total;
+  for (auto& p : per) {
+    total.bad += p.bad;
+    total.checked += p.checked;
+  }
+  return total;
+}
+
 // ---- static scales
 
 static uint32_t fp8_of(float q) { return tmo::fp8e4m3_bits(std::fmin(std::fmax(q, -448.0f), 448.0f)); }
@@ -320,6 +357,8 @@ int main(int argc, char** argv) {
     c = run_static(argc > 3 ? std::strtoull(argv[3], nullptr, 10) : 4000000ull, nthreads);
   } else if (!std::strcmp(mode, "fp8")) {
     c = run_fp8(nthreads);
+  } else if (!std::strcmp(mode, "sqrt")) {
+    c = run_sqrt(nthreads);
   } else {
     const unsigned long long n = argc > 3 ? std::strtoull(argv[3], nullptr, 10) : 20000000ull;
     c = run_f32(n, nthreads);

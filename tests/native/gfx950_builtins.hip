@@ -22,7 +22,8 @@
 //        codes always, the quotient bits wherever the IEEE quotient is normal or 0.
 //   sqrt: __builtin_sqrtf (the fused rope's rms) is correctly rounded for every positive
 //        finite fp32 x: with m- and m+ the midpoints between r = sqrtf(x) and its neighbours,
-//        m-^2 < x < m+^2 (25-bit midpoints square exactly in fp64; no x sits on a midpoint).
+//        m-^2 < x < m+^2 (25-bit midpoints square exactly in fp64; no x sits on a midpoint);
+//        and so is sqrt_rn (v_sqrt_f32 + residual choice) for every x in [2^-96, FLT_MAX].
 //
 // Each mode launches one grid-stride kernel that counts mismatches with vector atomics and
 // prints "mismatches=<n> checked=<m>"; the exit status is non-zero on any mismatch.  Built by
@@ -149,13 +150,16 @@ __global__ void check_sqrt(unsigned long long* bad) {
   unsigned long long b = 0;
   for (uint32_t u = 1 + blockIdx.x * blockDim.x + threadIdx.x; u < 0x7f800000u; u += stride) {
     const float x = __uint_as_float(u);
-    const float r = __builtin_sqrtf(x);
-    const uint32_t rb = __float_as_uint(r);
-    const double rd = (double)r;
-    const double lo = 0.5 * (rd + (double)__uint_as_float(rb - 1));
-    const double hi = 0.5 * (rd + (double)__uint_as_float(rb + 1));
     const double xd = (double)x;
-    if (!(lo * lo < xd && xd < hi * hi)) ++b;
+    auto rounded = [xd](float r) {
+      const uint32_t rb = __float_as_uint(r);
+      const double rd = (double)r;
+      const double lo = 0.5 * (rd + (double)__uint_as_float(rb - 1));
+      const double hi = 0.5 * (rd + (double)__uint_as_float(rb + 1));
+      return lo * lo < xd && xd < hi * hi;
+    };
+    if (!rounded(__builtin_sqrtf(x))) ++b;
+    if (x >= tmo::kSqrtMin && !rounded(tmo::sqrt_rn(x))) ++b;
   }
   if (b) atomicAdd(bad, b);
 }
@@ -277,7 +281,10 @@ int main(int argc, char** argv) {
     check_div64<false><<<dim3(0x7f7fu), dim3(256)>>>(0x7f7fu, d_bad);
     check_div64<true><<<dim3(0x7bffu), dim3(256)>>>(0x7bffu, d_bad);
   } else if (!std::strcmp(mode, "sqrt")) {
-    checked = 0x7f800000ull - 1;
+    float smin = tmo::kSqrtMin;
+    uint32_t umin;
+    std::memcpy(&umin, &smin, 4);
+    checked = (0x7f800000ull - 1) + (0x7f800000ull - umin);
     check_sqrt<<<dim3(8192), dim3(256)>>>(d_bad);
   } else {
     std::printf("unknown mode %s\n", mode);

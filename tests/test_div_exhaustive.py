@@ -3,8 +3,9 @@
 correction (scale_of).  This CPU test compiles that same source for the host and checks both
 against IEEE fp32 division: the quotient on every bf16 and every fp16 (amax, x) pair and on
 random and near-tie fp32 pairs, the scale on every fp32 amax it is used for, the static-scale
-quotient (offline quantisation, int8 and fp8 codes) on random scales and near-ties, and the
-fp8 e4m3 encoder on every fp32 value in [-448, 448] (tests/native/div_exhaustive.hip)."""
+quotient (offline quantisation, int8 and fp8 codes) on random scales and near-ties, the
+fp8 e4m3 encoder on every fp32 value in [-448, 448], and the fused rope's square-root
+correction on every fp32 value in [2^-96, FLT_MAX] (tests/native/div_exhaustive.hip)."""
 import os
 import subprocess
 from pathlib import Path
@@ -30,7 +31,8 @@ def binary(tmp_path_factory):
 
 
 @pytest.mark.parametrize("mode,extra", [("bf16", []), ("f16", []), ("f32", ["20000000"]),
-                                        ("scale", []), ("static", ["4000000"]), ("fp8", [])])
+                                        ("scale", []), ("static", ["4000000"]), ("fp8", []),
+                                        ("sqrt", [])])
 def test_reciprocal_quotient_matches_ieee(binary, mode, extra):
     threads = str(max(1, min(8, len(os.sched_getaffinity(0)))))
     res = subprocess.run([str(binary), mode, threads, *extra], capture_output=True, text=True,

@@ -356,10 +356,13 @@ def test_fused_rope_head_sizes_and_windows(tmo, ref, dev, D, rope, off):
                          api="fused_rope")
 
 
-@pytest.mark.parametrize("D,Hq,Hk", [(128, 64, 8), (512, 16, 2), (64, 120, 8)])
+@pytest.mark.parametrize("D,Hq,Hk", [(128, 64, 8), (128, 96, 16), (512, 16, 2), (64, 120, 8),
+                                    (128, 136, 8), (512, 32, 4), (64, 248, 8)])
 def test_fused_rope_many_heads(tmo, ref, dev, D, Hq, Hk):
-    """More heads than one workgroup's lane groups cover in four rows each: the row-major
-    kernel (one lane group per (token, head) row) instead of the token-major one."""
+    """Many heads: the token-major kernel with 5 to 8 rows per lane group (80 and 128 heads at
+    D = 128, 20 at D = 512, 136 at D = 64), and more heads than one workgroup's lane groups
+    cover in eight rows each (152 at D = 128, 40 at D = 512, 264 at D = 64): the row-major
+    kernel, one lane group per (token, head) row."""
     for mode in ("dynamic", "static"):
         case = W.fused_rope_case(torch.bfloat16, mode, D + Hq, B=2, S=11, Hq=Hq, Hk=Hk, D=D,
                                  rope=min(D, 128), NB=4)
@@ -405,9 +408,10 @@ def test_fused_rope_layernorm_head_sizes_and_windows(tmo, ref, dev, D, rope, off
                          k_beta=_beta(D, torch.bfloat16, D))
 
 
-@pytest.mark.parametrize("D,Hq,Hk", [(128, 64, 8), (64, 120, 8)])
+@pytest.mark.parametrize("D,Hq,Hk", [(128, 64, 8), (64, 120, 8), (128, 136, 8), (512, 32, 4)])
 def test_fused_rope_layernorm_many_heads(tmo, ref, dev, D, Hq, Hk):
-    """Layernorm in the row-major kernel (more heads than the token-major kernel takes)."""
+    """Layernorm with many heads: the token-major kernel at 5 rows per lane group (80 heads at
+    D = 128, 136 at D = 64) and the row-major kernel (152 heads at D = 128, 40 at D = 512)."""
     case = W.fused_rope_case(torch.bfloat16, "dynamic", D + Hq + 1, B=2, S=11, Hq=Hq, Hk=Hk, D=D,
                              rope=min(D, 128), NB=4)
     check_fused_rope(tmo, ref, dev, f"layernorm D={D} Hq={Hq} Hk={Hk}", case, True,
