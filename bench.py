@@ -63,8 +63,9 @@ KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<
            "cfg4_moe": "sq_grp<BF16,8,4,true,true>", "cfg5": "dequant_paged_list<BF16,1,2>",
            "offline_i8": "quant_paged_static_vec<BF16,16,false>",
            "offline_f8": "quant_paged_static_vec<BF16,16,true>",
-           "fused_rope": "fused_rope_tok<BF16,16,3,0>", "fused_rope_ln": "fused_rope_tok<BF16,16,3,1>",
-           "fused_rope_70b": "fused_rope_tok<BF16,16,5,0>",
+           "fused_rope": "fused_rope_tok<BF16,16,3,0,256>",
+           "fused_rope_ln": "fused_rope_tok<BF16,16,3,1,256>",
+           "fused_rope_70b": "fused_rope_tok<BF16,16,3,0,512>",
            "linear_quant": "lin_quant<BF16,16,false,false,true>", "linear_dequant": "lin_dequant<BF16,16>",
            "linear_reshape": "lin_copy<16,true>", "decode_attn": "attn_mfma<128,0,false>",
            "reshape_paged": "reshape_paged_rows<16>"}

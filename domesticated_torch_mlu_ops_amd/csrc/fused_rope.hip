@@ -333,14 +333,14 @@ __global__ __launch_bounds__(256) void fused_rope_vec(FusedRopeParams p) {
   *reinterpret_cast<u32x2*>(static_cast<int8_t*>(cache_of(p, kv)) + page_row * p.head_dim + lane * 8) = c2;
 }
 
-// Token-major vector path: a workgroup owns one token (its position and slot are scalar loads,
-// no per-lane index division) and the 256/G lane groups walk its heads, kR rows per group,
-// all kR rows loaded before the first is processed.  sin/cos (with the rotation's sign folded
-// in) and both gammas are loaded and unpacked once per workgroup instead of once per row.
-// Same arithmetic, in the same order, as fused_rope_vec.
-template <class Tag, int G, int kR, int kNorm>
-__global__ __launch_bounds__(256) void fused_rope_tok(FusedRopeParams p) {
-  constexpr int kGroups = 256 / G;
+// Token-major vector path: a workgroup of kThreads (256 or 512) owns one token (its position
+// and slot are scalar loads, no per-lane index division) and the kThreads/G lane groups walk
+// its heads, kR rows per group, all kR rows loaded before the first is processed.  sin/cos
+// (with the rotation's sign folded in) are unpacked once per workgroup, both gammas loaded
+// once.  Same arithmetic, in the same order, as fused_rope_vec.
+template <class Tag, int G, int kR, int kNorm, int kThreads>
+__global__ __launch_bounds__(kThreads) void fused_rope_tok(FusedRopeParams p) {
+  constexpr int kGroups = kThreads / G;
   const int lane = threadIdx.x & (G - 1);
   const int grp = threadIdx.x / G;
   const int64_t t = blockIdx.x;
@@ -642,13 +642,15 @@ __global__ __launch_bounds__(256) void fused_rope_generic(FusedRopeParams p) {
 #endif
 constexpr int kFusedRopeMaxRows = TMO_FUSED_ROPE_MAX_ROWS;
 
-// fused_rope_tok with the smallest row count R >= r of its instances (R <= kFusedRopeMaxRows)
-template <class Tag, int G, int kNorm, int R = 1>
-int launch_tok(int r, dim3 grid, dim3 block, hipStream_t stream, const FusedRopeParams& p) {
-  if constexpr (R < kFusedRopeMaxRows) {
-    if (r > R) return launch_tok<Tag, G, kNorm, R + 1>(r, grid, block, stream, p);
+// fused_rope_tok in kThreads-thread workgroups (one per token) with the smallest row count
+// R >= r of its instances (R <= kMaxR)
+template <class Tag, int G, int kNorm, int kThreads, int kMaxR, int R = 1>
+int launch_tok(int r, hipStream_t stream, const FusedRopeParams& p) {
+  if constexpr (R < kMaxR) {
+    if (r > R) return launch_tok<Tag, G, kNorm, kThreads, kMaxR, R + 1>(r, stream, p);
   }
-  return launch_kernel(fused_rope_tok<Tag, G, R, kNorm>, grid, block, stream, p);
+  return launch_kernel(fused_rope_tok<Tag, G, R, kNorm, kThreads>, dim3((unsigned)p.tokens),
+                       dim3(kThreads), stream, p);
 }
 
 template <class Tag, int kNorm>
@@ -661,21 +663,34 @@ int launch(const FusedRopeParams& p, hipStream_t stream) {
              (!p.q_gamma || al16(p.q_gamma)) && al16(p.sin_t) && al16(p.cos_t) &&
              (p.table_stride * Tag::kBytes) % 16 == 0 && al16(p.cache[0]) && al16(p.cache[1]) &&
              (p.scale_mode != 2 || (al16(p.scale[0]) && al16(p.scale[1])));
-  // token-major kernel when one workgroup covers a token's heads in at most
-  // kFusedRopeMaxRows rows per lane group
-  if (TMO_FUSED_ROPE_TOKEN_MAJOR && vec && (int64_t)(256 / G) * kFusedRopeMaxRows >= p.heads &&
-      p.tokens <= 0x7fffffffLL) {
-    const dim3 grid((unsigned)p.tokens), block(256);
-    const int r = (p.heads + 256 / G - 1) / (256 / G);
-    switch (G) {
-      case 1: return launch_tok<Tag, 1, kNorm>(r, grid, block, stream, p);
-      case 2: return launch_tok<Tag, 2, kNorm>(r, grid, block, stream, p);
-      case 4: return launch_tok<Tag, 4, kNorm>(r, grid, block, stream, p);
-      case 8: return launch_tok<Tag, 8, kNorm>(r, grid, block, stream, p);
-      case 16: return launch_tok<Tag, 16, kNorm>(r, grid, block, stream, p);
-      case 32: return launch_tok<Tag, 32, kNorm>(r, grid, block, stream, p);
-      case 64: return launch_tok<Tag, 64, kNorm>(r, grid, block, stream, p);
-      default: break;
+  // Token-major kernel, one workgroup per token: 256 threads while the token's heads take at
+  // most 3 rows per lane group, else 512 threads (twice the lane groups, half the rows, fewer
+  // VGPRs per thread) up to kFusedRopeMaxRows rows; more heads take the row-major kernel.
+  if (TMO_FUSED_ROPE_TOKEN_MAJOR && vec && p.tokens <= 0x7fffffffLL) {
+    const int64_t r = (p.heads + 256 / G - 1) / (256 / G);
+    const int64_t r2 = (p.heads + 512 / G - 1) / (512 / G);
+    if (r <= 3) {
+      switch (G) {
+        case 1: return launch_tok<Tag, 1, kNorm, 256, 3>((int)r, stream, p);
+        case 2: return launch_tok<Tag, 2, kNorm, 256, 3>((int)r, stream, p);
+        case 4: return launch_tok<Tag, 4, kNorm, 256, 3>((int)r, stream, p);
+        case 8: return launch_tok<Tag, 8, kNorm, 256, 3>((int)r, stream, p);
+        case 16: return launch_tok<Tag, 16, kNorm, 256, 3>((int)r, stream, p);
+        case 32: return launch_tok<Tag, 32, kNorm, 256, 3>((int)r, stream, p);
+        case 64: return launch_tok<Tag, 64, kNorm, 256, 3>((int)r, stream, p);
+        default: break;
+      }
+    } else if (r2 <= kFusedRopeMaxRows) {
+      switch (G) {
+        case 1: return launch_tok<Tag, 1, kNorm, 512, kFusedRopeMaxRows, 2>((int)r2, stream, p);
+        case 2: return launch_tok<Tag, 2, kNorm, 512, kFusedRopeMaxRows, 2>((int)r2, stream, p);
+        case 4: return launch_tok<Tag, 4, kNorm, 512, kFusedRopeMaxRows, 2>((int)r2, stream, p);
+        case 8: return launch_tok<Tag, 8, kNorm, 512, kFusedRopeMaxRows, 2>((int)r2, stream, p);
+        case 16: return launch_tok<Tag, 16, kNorm, 512, kFusedRopeMaxRows, 2>((int)r2, stream, p);
+        case 32: return launch_tok<Tag, 32, kNorm, 512, kFusedRopeMaxRows, 2>((int)r2, stream, p);
+        case 64: return launch_tok<Tag, 64, kNorm, 512, kFusedRopeMaxRows, 2>((int)r2, stream, p);
+        default: break;
+      }
     }
   }
   const int64_t nrows = p.tokens * p.heads;

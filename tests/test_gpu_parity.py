@@ -357,12 +357,13 @@ def test_fused_rope_head_sizes_and_windows(tmo, ref, dev, D, rope, off):
 
 
 @pytest.mark.parametrize("D,Hq,Hk", [(128, 64, 8), (128, 96, 16), (512, 16, 2), (64, 120, 8),
-                                    (128, 136, 8), (512, 32, 4), (64, 248, 8)])
+                                    (128, 136, 8), (512, 32, 4), (64, 248, 8), (128, 240, 8),
+                                    (128, 264, 8), (512, 64, 4), (64, 512, 8)])
 def test_fused_rope_many_heads(tmo, ref, dev, D, Hq, Hk):
-    """Many heads: the token-major kernel with 5 to 8 rows per lane group (80 and 128 heads at
-    D = 128, 20 at D = 512, 136 at D = 64), and more heads than one workgroup's lane groups
-    cover in eight rows each (152 at D = 128, 40 at D = 512, 264 at D = 64): the row-major
-    kernel, one lane group per (token, head) row."""
+    """Many heads: the token-major kernel in 512-thread workgroups with 3 to 8 rows per lane
+    group (80, 128, 152 and 256 heads at D = 128; 20 and 40 at D = 512; 136 and 264 at D = 64),
+    and more heads than those cover in eight rows each (280 at D = 128, 72 at D = 512, 528 at
+    D = 64): the row-major kernel, one lane group per (token, head) row."""
     for mode in ("dynamic", "static"):
         case = W.fused_rope_case(torch.bfloat16, mode, D + Hq, B=2, S=11, Hq=Hq, Hk=Hk, D=D,
                                  rope=min(D, 128), NB=4)
@@ -408,10 +409,12 @@ def test_fused_rope_layernorm_head_sizes_and_windows(tmo, ref, dev, D, rope, off
                          k_beta=_beta(D, torch.bfloat16, D))
 
 
-@pytest.mark.parametrize("D,Hq,Hk", [(128, 64, 8), (64, 120, 8), (128, 136, 8), (512, 32, 4)])
+@pytest.mark.parametrize("D,Hq,Hk", [(128, 64, 8), (64, 120, 8), (128, 136, 8), (512, 32, 4),
+                                    (128, 264, 8), (512, 64, 4)])
 def test_fused_rope_layernorm_many_heads(tmo, ref, dev, D, Hq, Hk):
-    """Layernorm with many heads: the token-major kernel at 5 rows per lane group (80 heads at
-    D = 128, 136 at D = 64) and the row-major kernel (152 heads at D = 128, 40 at D = 512)."""
+    """Layernorm with many heads: the token-major kernel in 512-thread workgroups (80 and 152
+    heads at D = 128, 136 at D = 64, 40 at D = 512) and the row-major kernel (280 heads at
+    D = 128, 72 at D = 512)."""
     case = W.fused_rope_case(torch.bfloat16, "dynamic", D + Hq + 1, B=2, S=11, Hq=Hq, Hk=Hk, D=D,
                              rope=min(D, 128), NB=4)
     check_fused_rope(tmo, ref, dev, f"layernorm D={D} Hq={Hq} Hk={Hk}", case, True,
