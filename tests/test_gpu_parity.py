@@ -358,12 +358,14 @@ def test_fused_rope_head_sizes_and_windows(tmo, ref, dev, D, rope, off):
 
 @pytest.mark.parametrize("D,Hq,Hk", [(128, 64, 8), (128, 96, 16), (512, 16, 2), (64, 120, 8),
                                     (128, 136, 8), (512, 32, 4), (64, 248, 8), (128, 240, 8),
-                                    (128, 264, 8), (512, 64, 4), (64, 512, 8)])
+                                    (128, 264, 8), (512, 64, 4), (64, 512, 8), (256, 40, 4),
+                                    (16, 1000, 12), (32, 300, 10)])
 def test_fused_rope_many_heads(tmo, ref, dev, D, Hq, Hk):
     """Many heads: the token-major kernel in 512-thread workgroups with 3 to 8 rows per lane
-    group (80, 128, 152 and 256 heads at D = 128; 20 and 40 at D = 512; 136 and 264 at D = 64),
-    and more heads than those cover in eight rows each (280 at D = 128, 72 at D = 512, 528 at
-    D = 64): the row-major kernel, one lane group per (token, head) row."""
+    group (80, 128, 152 and 256 heads at D = 128; 20 and 40 at D = 512; 136 and 264 at D = 64;
+    48 at D = 256, 1024 at D = 16, 320 at D = 32), and more heads than those cover in eight
+    rows each (280 at D = 128, 72 at D = 512, 528 at D = 64): the row-major kernel, one lane
+    group per (token, head) row."""
     for mode in ("dynamic", "static"):
         case = W.fused_rope_case(torch.bfloat16, mode, D + Hq, B=2, S=11, Hq=Hq, Hk=Hk, D=D,
                                  rope=min(D, 128), NB=4)
