@@ -688,7 +688,8 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards by KV heads or sequences with no exchange between GPUs)", file=sys.stderr)
+              "(the path shards by KV heads or sequences with no exchange between GPUs)",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     import domesticated_torch_mlu_ops_amd as tmo
