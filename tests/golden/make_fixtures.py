@@ -140,6 +140,29 @@ def main() -> None:
                                "k_cache": as_np(k4), "v_cache": as_np(v4),
                                "k_scale": as_np(k4s), "v_scale": as_np(v4s)}
 
+    # fused rope into dynamic int8 pages, rmsnorm (Q and K normalised) and layernorm (K, with
+    # beta): -1 slots, a zero K row, the second sequence running past the sin/cos table
+    for name, norm, seed in (("fused_rope_rmsnorm", "rmsnorm", 29),
+                             ("fused_rope_layernorm", "layernorm", 31)):
+        ln = norm == "layernorm"
+        qkv, kc, vc, sin, cos, pid, kg, qg, ks, vs, slot = W.fused_rope_case(
+            torch.bfloat16, "dynamic", seed, B=2, S=12, Hq=4, Hk=2, NB=4, positions=(0, 120))
+        kb = (torch.rand(128, generator=torch.Generator().manual_seed(seed)) - 0.5).to(
+            torch.bfloat16)
+        kc.view(torch.uint8).fill_(0x5A)
+        vc.view(torch.uint8).fill_(0x5A)
+        ks.fill_(W.SCALE_SENTINEL)
+        vs.fill_(W.SCALE_SENTINEL)
+        out = qkv.clone()
+        oracle.fused_rope_paged(out, kc, vc, sin, cos, pid, kg, ks, vs, slot, 1e-5,
+                                None if ln else qg, 0, norm_type=norm, k_beta=kb if ln else None)
+        fixtures[name] = {"qkv": as_np(qkv), "sin": as_np(sin), "cos": as_np(cos),
+                          "position_id": pid.numpy(), "k_gamma": as_np(kg),
+                          "q_gamma": as_np(qg), "k_beta": as_np(kb), "slot_mapping": slot.numpy(),
+                          "norm_type": np.array(norm), "qkv_out": as_np(out),
+                          "k_cache": as_np(kc), "v_cache": as_np(vc), "k_scale": as_np(ks),
+                          "v_scale": as_np(vs)}
+
     lines = []
     for name, arrays in fixtures.items():
         path = HERE / f"{name}.npz"

@@ -119,3 +119,27 @@ def run_linear_int4(fn, device="cpu"):
        i32("cache_seq_offset"))
     return [(n, g, w) for n, g, w in zip(("k_cache", "v_cache", "k_scale", "v_scale"),
                                          (kc, vc, ks, vs), want)]
+
+
+FUSED_ROPE = ["fused_rope_rmsnorm", "fused_rope_layernorm"]
+
+
+def run_fused_rope(name, fn, device="cpu"):
+    """fn(qkv, k_cache, v_cache, sin, cos, position_id, k_gamma, q_gamma, k_beta, k_scale,
+    v_scale, slot_mapping, norm_type): Q written back into qkv, K / V into the pages."""
+    z = load(name)
+    bf = torch.bfloat16
+    want = [t16(z["qkv_out"], bf), t8(z["k_cache"]), t8(z["v_cache"]), t32f(z["k_scale"]),
+            t32f(z["v_scale"])]
+    from tests import workloads as W
+    qkv = t16(z["qkv"], bf).to(device)
+    kc = torch.full(want[1].shape, 0x5A, dtype=torch.uint8, device=device).view(torch.int8)
+    vc = kc.clone()
+    ks = torch.full(want[3].shape, W.SCALE_SENTINEL, device=device)
+    vs = ks.clone()
+    d = lambda a: t16(a, bf).to(device)
+    fn(qkv, kc, vc, d(z["sin"]), d(z["cos"]), torch.from_numpy(z["position_id"].copy()).to(device),
+       d(z["k_gamma"]), d(z["q_gamma"]), d(z["k_beta"]), ks, vs,
+       torch.from_numpy(z["slot_mapping"].copy()).to(device), str(z["norm_type"]))
+    return [(n, g, w) for n, g, w in zip(("qkv", "k_cache", "v_cache", "k_scale", "v_scale"),
+                                         (qkv, kc, vc, ks, vs), want)]

@@ -14,7 +14,7 @@ def _assert_all(triples):
 
 def test_manifest_hashes():
     m = G.manifest()
-    assert len(m) == 7
+    assert len(m) == 9
     for fname, digest in m.items():
         assert G.sha256(fname) == digest, fname
 
@@ -40,3 +40,12 @@ def test_oracle_linear_int4_fixture():
         lambda key, val, kc, vc, ks, vs, ctx, mctx, cso, bsi, coff: oracle.linear_cache(
             1, key, val, kc, vc, ctx, mctx, packed=True, context_seq_offset=cso,
             cache_bs_id=bsi, cache_seq_offset=coff, key_scale=ks, value_scale=vs, bits=4)))
+
+
+@pytest.mark.parametrize("name", G.FUSED_ROPE)
+def test_oracle_fused_rope_fixtures(name):
+    def fn(qkv, kc, vc, sin, cos, pid, kg, qg, kb, ks, vs, slot, norm):
+        ln = norm == "layernorm"
+        oracle.fused_rope_paged(qkv, kc, vc, sin, cos, pid, kg, ks, vs, slot, 1e-5,
+                                None if ln else qg, 0, norm_type=norm, k_beta=kb if ln else None)
+    _assert_all(G.run_fused_rope(name, fn))

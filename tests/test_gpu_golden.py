@@ -34,3 +34,15 @@ def test_linear_int4_fixture(tmo, dev):
     _assert_all(G.run_linear_int4(
         lambda key, val, kc, vc, ks, vs, ctx, mctx, cso, bsi, coff: tmo.quant_to_linear_cache(
             key, val, kc, vc, ks, vs, ctx, mctx, True, cso, bsi, coff, 4), dev))
+
+
+@pytest.mark.parametrize("name", G.FUSED_ROPE)
+def test_fused_rope_fixtures(tmo, dev, name):
+    def fn(qkv, kc, vc, sin, cos, pid, kg, qg, kb, ks, vs, slot, norm):
+        if norm == "layernorm":
+            tmo.fused_rope(qkv, kc, vc, sin, cos, pid, kg, kb, k_scale_hp=ks, v_scale_hp=vs,
+                           slot_mapping_hp=slot, norm_type="layernorm", eps=1e-5)
+        else:
+            tmo.fused_rmsnorm_rope_store_paged_cache(qkv, kc, vc, sin, cos, pid, kg, qg, slot,
+                                                     ks, vs, 1e-5)
+    _assert_all(G.run_fused_rope(name, fn, dev))
