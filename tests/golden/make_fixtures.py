@@ -163,6 +163,28 @@ def main() -> None:
                           "k_cache": as_np(kc), "v_cache": as_np(vc), "k_scale": as_np(ks),
                           "v_scale": as_np(vs)}
 
+    # offline (static per-channel) quant into int8 and fp8 e4m3 pages: special rows, scales of
+    # both signs (a negative scale flips the codes and the sign of zero quotients), a -1 slot
+    for name, cdt, seed in (("offline_int8", torch.int8, 43), ("offline_fp8", torch.float8_e4m3fn, 47)):
+        gs = torch.Generator().manual_seed(seed)
+        rk, rv = special_rows(torch.bfloat16, seed), special_rows(torch.bfloat16, seed + 1)
+        k = torch.stack((rk, torch.flip(rk, dims=[0])), dim=1).contiguous()   # [9, 2, 128]
+        v = torch.stack((rv, torch.flip(rv, dims=[0])), dim=1).contiguous()
+        ks = 0.005 + 0.05 * torch.rand(2, 128, generator=gs)
+        vs = 0.005 + 0.05 * torch.rand(2, 128, generator=gs)
+        ks[:, ::17] = -ks[:, ::17]
+        vs[:, 5::23] = -vs[:, 5::23]
+        T = k.shape[0]
+        slot = torch.arange(T, dtype=torch.int32) * 2 + 1
+        slot[4] = -1
+        NB = (2 * T + 16) // 16
+        kc = torch.full((NB, 2, 16, 128), 0x5A, dtype=torch.uint8).view(cdt)
+        vc = kc.clone()
+        oracle.offline_quant_to_paged_cache(k, v, ks, vs, slot, kc, vc)
+        fixtures[name] = {"k": as_np(k), "v": as_np(v), "k_scale": as_np(ks), "v_scale": as_np(vs),
+                          "slot_mapping": slot.numpy(), "cache_dtype": np.array(str(cdt)),
+                          "k_cache": as_np(kc), "v_cache": as_np(vc)}
+
     lines = []
     for name, arrays in fixtures.items():
         path = HERE / f"{name}.npz"

@@ -143,3 +143,20 @@ def run_fused_rope(name, fn, device="cpu"):
        torch.from_numpy(z["slot_mapping"].copy()).to(device), str(z["norm_type"]))
     return [(n, g, w) for n, g, w in zip(("qkv", "k_cache", "v_cache", "k_scale", "v_scale"),
                                          (qkv, kc, vc, ks, vs), want)]
+
+
+OFFLINE = ["offline_int8", "offline_fp8"]
+CDT = {"torch.int8": torch.int8, "torch.float8_e4m3fn": torch.float8_e4m3fn}
+
+
+def run_offline(name, fn, device="cpu"):
+    """fn(k, v, k_scale, v_scale, slot_mapping, k_cache, v_cache)"""
+    z = load(name)
+    cdt = CDT[str(z["cache_dtype"])]
+    want = [torch.from_numpy(z["k_cache"].copy()).view(cdt), torch.from_numpy(z["v_cache"].copy()).view(cdt)]
+    kc = torch.full(want[0].shape, 0x5A, dtype=torch.uint8, device=device).view(cdt)
+    vc = kc.clone()
+    d = lambda a: t16(a, torch.bfloat16).to(device)
+    fn(d(z["k"]), d(z["v"]), t32f(z["k_scale"]).to(device), t32f(z["v_scale"]).to(device),
+       torch.from_numpy(z["slot_mapping"].copy()).to(device), kc, vc)
+    return [("k_cache", kc, want[0]), ("v_cache", vc, want[1])]

@@ -14,7 +14,7 @@ def _assert_all(triples):
 
 def test_manifest_hashes():
     m = G.manifest()
-    assert len(m) == 9
+    assert len(m) == 11
     for fname, digest in m.items():
         assert G.sha256(fname) == digest, fname
 
@@ -49,3 +49,8 @@ def test_oracle_fused_rope_fixtures(name):
         oracle.fused_rope_paged(qkv, kc, vc, sin, cos, pid, kg, ks, vs, slot, 1e-5,
                                 None if ln else qg, 0, norm_type=norm, k_beta=kb if ln else None)
     _assert_all(G.run_fused_rope(name, fn))
+
+
+@pytest.mark.parametrize("name", G.OFFLINE)
+def test_oracle_offline_quant_fixtures(name):
+    _assert_all(G.run_offline(name, oracle.offline_quant_to_paged_cache))

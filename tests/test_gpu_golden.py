@@ -46,3 +46,8 @@ def test_fused_rope_fixtures(tmo, dev, name):
             tmo.fused_rmsnorm_rope_store_paged_cache(qkv, kc, vc, sin, cos, pid, kg, qg, slot,
                                                      ks, vs, 1e-5)
     _assert_all(G.run_fused_rope(name, fn, dev))
+
+
+@pytest.mark.parametrize("name", G.OFFLINE)
+def test_offline_quant_fixtures(tmo, dev, name):
+    _assert_all(G.run_offline(name, tmo.offline_quant_to_paged_cache, dev))
