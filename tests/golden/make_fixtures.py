@@ -163,6 +163,25 @@ def main() -> None:
                           "k_cache": as_np(kc), "v_cache": as_np(vc), "k_scale": as_np(ks),
                           "v_scale": as_np(vs)}
 
+    # 8-bit linear caches: packed input, cache offsets and batch ids
+    lc8 = W.linear_case(torch.bfloat16, 53, packed=True, offsets=True, D=64)
+    H8 = lc8.key.shape[-2]
+    k8 = torch.full((lc8.cache_batch, H8, lc8.cache_len, 64), 0x5A, dtype=torch.uint8).view(torch.int8)
+    v8 = k8.clone()
+    k8s, v8s = lc8.scales()
+    oracle.linear_cache(1, lc8.key, lc8.value, k8, v8, lc8.context_lengths, lc8.max_context_len,
+                        packed=True, context_seq_offset=lc8.context_seq_offset,
+                        cache_bs_id=lc8.cache_bs_id, cache_seq_offset=lc8.cache_seq_offset,
+                        key_scale=k8s, value_scale=v8s, bits=8)
+    fixtures["linear_int8"] = {"key": as_np(lc8.key), "value": as_np(lc8.value),
+                               "context_lengths": lc8.context_lengths.numpy(),
+                               "max_context_len": np.int64(lc8.max_context_len),
+                               "context_seq_offset": lc8.context_seq_offset.numpy(),
+                               "cache_bs_id": lc8.cache_bs_id.numpy(),
+                               "cache_seq_offset": lc8.cache_seq_offset.numpy(),
+                               "k_cache": as_np(k8), "v_cache": as_np(v8),
+                               "k_scale": as_np(k8s), "v_scale": as_np(v8s)}
+
     # offline (static per-channel) quant into int8 and fp8 e4m3 pages: special rows, scales of
     # both signs (a negative scale flips the codes and the sign of zero quotients), a -1 slot
     for name, cdt, seed in (("offline_int8", torch.int8, 43), ("offline_fp8", torch.float8_e4m3fn, 47)):

@@ -102,10 +102,11 @@ def run_dequant_paged(fn, device="cpu"):
     return [("key", key, want_k), ("value", val, want_v)]
 
 
-def run_linear_int4(fn, device="cpu"):
+def run_linear_int4(fn, device="cpu", name="linear_int4"):
     """fn(key, value, k_cache, v_cache, k_scale, v_scale, context_lengths, max_context_len,
-    context_seq_offset, cache_bs_id, cache_seq_offset)"""
-    z = load("linear_int4")
+    context_seq_offset, cache_bs_id, cache_seq_offset); `name` = "linear_int8" for the 8-bit
+    fixture"""
+    z = load(name)
     key, value = t16(z["key"], torch.bfloat16), t16(z["value"], torch.bfloat16)
     want = [t8(z["k_cache"]), t8(z["v_cache"]), t32f(z["k_scale"]), t32f(z["v_scale"])]
     kc = torch.full(want[0].shape, 0x5A, dtype=torch.uint8, device=device).view(torch.int8)

@@ -14,7 +14,7 @@ def _assert_all(triples):
 
 def test_manifest_hashes():
     m = G.manifest()
-    assert len(m) == 11
+    assert len(m) == 12
     for fname, digest in m.items():
         assert G.sha256(fname) == digest, fname
 
@@ -54,3 +54,11 @@ def test_oracle_fused_rope_fixtures(name):
 @pytest.mark.parametrize("name", G.OFFLINE)
 def test_oracle_offline_quant_fixtures(name):
     _assert_all(G.run_offline(name, oracle.offline_quant_to_paged_cache))
+
+
+def test_oracle_linear_int8_fixture():
+    _assert_all(G.run_linear_int4(
+        lambda key, val, kc, vc, ks, vs, ctx, mctx, cso, bsi, coff: oracle.linear_cache(
+            1, key, val, kc, vc, ctx, mctx, packed=True, context_seq_offset=cso,
+            cache_bs_id=bsi, cache_seq_offset=coff, key_scale=ks, value_scale=vs, bits=8),
+        name="linear_int8"))

@@ -51,3 +51,9 @@ def test_fused_rope_fixtures(tmo, dev, name):
 @pytest.mark.parametrize("name", G.OFFLINE)
 def test_offline_quant_fixtures(tmo, dev, name):
     _assert_all(G.run_offline(name, tmo.offline_quant_to_paged_cache, dev))
+
+
+def test_linear_int8_fixture(tmo, dev):
+    _assert_all(G.run_linear_int4(
+        lambda key, val, kc, vc, ks, vs, ctx, mctx, cso, bsi, coff: tmo.quant_to_linear_cache(
+            key, val, kc, vc, ks, vs, ctx, mctx, True, cso, bsi, coff, 8), dev, name="linear_int8"))
