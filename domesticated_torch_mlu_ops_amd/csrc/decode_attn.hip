@@ -1000,8 +1000,14 @@ extern "C" int tmo_hip_cached_kv_attn(
   if (cache_dtype != TMO_DTYPE_I8 && cache_dtype != q_dtype) return TMO_ERR_UNSUPPORTED_DTYPE;
   if (cache_dtype == TMO_DTYPE_I8 && (scale_mode < 1 || scale_mode > 3))
     return TMO_ERR_UNSUPPORTED_MODE;
-  if (!q || !k_cache || !block_tables || !context_lens || !out) return TMO_ERR_INVALID_ARGUMENT;
-  if (cache_dtype == TMO_DTYPE_I8 && (!k_scale || !v_scale)) return TMO_ERR_INVALID_ARGUMENT;
+  // An empty cache (num_blocks 0: every block-table entry is outside it, so every key is
+  // masked) may come with null cache and per-token scale pointers; nothing reads them.
+  // Likewise an empty block table (max_blocks 0 caps every context at 0 keys).
+  if (!q || !context_lens || !out) return TMO_ERR_INVALID_ARGUMENT;
+  if ((num_blocks > 0 && !k_cache) || (max_blocks > 0 && !block_tables))
+    return TMO_ERR_INVALID_ARGUMENT;
+  if (cache_dtype == TMO_DTYPE_I8 && (!k_scale || !v_scale) && (num_blocks > 0 || scale_mode != 1))
+    return TMO_ERR_INVALID_ARGUMENT;
   // v_cache null: the values are the first head_size_v channels of the K cache's rows
   if (!v_cache) {
     v_cache = k_cache;
@@ -1096,7 +1102,10 @@ extern "C" int tmo_hip_cached_kv_attn(
   // offsets of a page and head in multiples of four), q's dtype representable by the operands
   // (int8 caches: bf16 with a lo part when needed), per-token or per-channel scales.
   auto al = [](const void* x, int a) { return reinterpret_cast<uintptr_t>(x) % a == 0; };
-  bool mfma = (head_size == 64 || head_size == 128 || head_size == 256) &&
+  // The MFMA kernel always issues its tile loads (a wave with no valid page yet reads page 0,
+  // see attn_mfma), so an empty cache takes attn_generic, whose loads are all under the page
+  // check: every output row is then 0 and its lse -inf (nothing to attend to).
+  bool mfma = num_blocks > 0 && (head_size == 64 || head_size == 128 || head_size == 256) &&
               head_size_v == head_size && k_cache_dim == head_size &&
               v_cache_dim == head_size && block_size % 16 == 0 && al(k_cache, 16) &&
               al(v_cache, 16) && q_dtype != TMO_DTYPE_F32;
@@ -1137,7 +1146,7 @@ extern "C" int tmo_hip_single_query_cached_kv_attn(
     int q_dtype, int cache_dtype, int64_t splits, void* workspace, int64_t workspace_bytes,
     void* stream) {
   if (cache_dtype == TMO_DTYPE_I8 && scale_mode == 3) return TMO_ERR_UNSUPPORTED_MODE;
-  if (!v_cache) return TMO_ERR_INVALID_ARGUMENT;
+  if (!v_cache && num_blocks > 0) return TMO_ERR_INVALID_ARGUMENT;
   if (head_size > 512) return TMO_ERR_INVALID_ARGUMENT;
   // contiguous per-token scales [num_blocks, Hkv, block_size]
   const int64_t sb = num_kv_heads * block_size, sh = block_size;

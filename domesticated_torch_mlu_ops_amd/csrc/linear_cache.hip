@@ -728,7 +728,7 @@ __device__ __forceinline__ int64_t floor_half(int64_t v) { return v >= 0 ? v / 2
 // lanes past the row idle), 8 channels per lane, one lane group per pair of cache positions
 // (2P, 2P + 1) of one head, so the two tokens that share the V bytes are encoded together and
 // every V byte is written by one lane.  A position of the pair outside the sequence's tokens
-// keeps its nibble: the lane reads the V bytes first and writes back the nibble unchanged.
+// keeps its nibble: the lane merges only its own nibbles into the V bytes, with atomics.
 template <class Tag, int G>
 __global__ __launch_bounds__(256) void lin_quant4(LinParams p) {
   constexpr int kPairs = 256 / G;
@@ -791,22 +791,34 @@ __global__ __launch_bounds__(256) void lin_quant4(LinParams p) {
       const int64_t pos = tin[0] ? 2 * P : 2 * P + 1;
       const int64_t vrow = (cr - pos) / L * (L / 2) + P;  // (batch * H + h) * (L / 2) + P
       u32x2* dst = reinterpret_cast<u32x2*>(static_cast<int8_t*>(p.cache[1]) + vrow * D + d0);
-      u32x2 old = {0u, 0u};
-      if (!tin[0] || !tin[1]) old = *dst;
       u32x2 w;
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         uint32_t acc = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const uint32_t ob = (old[q] >> (8 * k)) & 0xFFu;
-          const uint32_t hi = tin[0] ? nib[0][4 * q + k] : ob >> 4;
-          const uint32_t lo = tin[1] ? nib[1][4 * q + k] : ob & 0xFu;
+          const uint32_t hi = tin[0] ? nib[0][4 * q + k] : 0u;
+          const uint32_t lo = tin[1] ? nib[1][4 * q + k] : 0u;
           acc |= ((hi << 4) | lo) << (8 * k);
         }
         w[q] = acc;
       }
-      *dst = w;
+      if (tin[0] && tin[1]) {
+        *dst = w;
+      } else {
+        // One position of the pair belongs to this call's sequence, the other may belong to
+        // another sequence of the same call (the same cache batch, adjacent position ranges
+        // meeting at an odd position), written by another workgroup at the same time.  Each
+        // side clears and sets only its own nibbles with 32-bit vector atomics, so the two
+        // merges commute; a read-modify-write of the whole bytes could lose the other's.
+        const uint32_t own = tin[0] ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+        uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          atomicAnd(d32 + q, ~own);
+          atomicOr(d32 + q, w[q] & own);
+        }
+      }
     }
   }
 }

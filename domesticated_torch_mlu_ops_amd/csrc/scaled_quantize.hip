@@ -5,10 +5,12 @@
 // _ops.py:4407-4492 (scaled_quantize).  Entry point: tmo_hip_scaled_quantize_per_token
 // (include/tmo_hip.h).
 //
-// One or two wavefronts per output row.  Every lane holds up to 16 16-byte vectors of the row
-// in registers (all loads in flight at once), so the row is read from HBM exactly once.
-// sq_dense: rows without gather or groups, a grid-stride launch with a per-channel smooth
-// vector staged in LDS.  sq_grp: gathered / grouped rows (MoE) with per-channel smooth rows,
+// One or two wavefronts per output row, or one workgroup per row.  Every lane holds its
+// 16-byte vectors of the row in registers (all loads in flight at once), so the row is read
+// from HBM exactly once.  sq_dense_wg: rows without gather or groups of 256 * k vectors, one
+// row per workgroup at a time in a persistent grid, the smooth values of a thread's channels in
+// registers.  sq_dense: other dense rows, a grid-stride launch with a per-channel smooth vector
+// staged in LDS.  sq_grp: gathered / grouped rows (MoE) with per-channel smooth rows,
 // one staging of the group's smooth row in LDS per workgroup.  sq_vec: the remaining vector
 // cases (other widths, 3-D rows, scalar or no smooth with gather / groups), the smooth vector
 // read from L2 beside the row.  A row's group (expert) is found with a wavefront prefix scan
@@ -525,6 +527,169 @@ int launch_dense(const SqParams& p, hipStream_t stream) {
   return launch_kernel(sq_dense<Tag, kV, false, false>, grid, block, stream, p);
 }
 
+#ifndef TMO_SQ_DENSE_WG
+#define TMO_SQ_DENSE_WG 1
+#endif
+// Workgroups per CU of sq_dense_wg's persistent grid.  configs[3] (8192 x 4096 bf16,
+// per-channel smooth) on MI355X, us per call in HIP-graph replays, against 19.38 for sq_dense:
+// 2: 20.86, 3: 18.99, 4: 19.18, 5: 20.56, 6: 20.10, 8: 20.95.
+#ifndef TMO_SQ_WG_ROW_PER_CU
+#define TMO_SQ_WG_ROW_PER_CU 3
+#endif
+
+// Dense rows of exactly 256 * kV 16-byte vectors, one row per workgroup at a time: thread t
+// owns vectors t + 256 * i of every row, so its smooth values are fixed and held in registers
+// (kV * 8 floats), a row is kV fully coalesced 4 KiB load instructions, and the workgroup's
+// next row is loaded while the current one is reduced, scaled and encoded.  The row maximum
+// meets across the four wavefronts in LDS (two slots, alternating by row, so one barrier per
+// row suffices: a wavefront writes slot k again only after the barrier of the row in between,
+// which every wavefront reaches after reading slot k).  The grid is persistent, a few
+// workgroups per CU striding over the rows.  When no row follows, the prefetch reads the first
+// 16 bytes of x (one line for the whole workgroup, in bounds) so the loads carry no branch.
+// Measured against sq_dense (side by side, identical output): 19.38 -> 18.99 us on configs[3].
+// What it is not: a build of this kernel with all arithmetic removed (no smooth, reduction,
+// barrier or encoder; the row bytes xor-folded into the stores) takes 19.3 us, and one without
+// the scale stores 19.1 us, while a bare streaming copy of the same bytes in the same grid
+// (two 16-byte loads and two 8-byte stores per thread per row) takes 17.8 us.  Rows mapped to
+// workgroups in contiguous blocks instead of strides, or loaded without the prefetch, were
+// 0.5-3 us slower.
+template <class Tag, int kV, bool kScalar, bool kChan>
+__global__ __launch_bounds__(256) void sq_dense_wg(SqParams p) {
+  constexpr int kPer = Tag::kPerVec;
+  constexpr int kT = 256;
+  __shared__ uint32_t red[2][4];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int64_t rows = p.dense_rows;
+  int64_t row = blockIdx.x;
+  if (row >= rows) return;  // workgroup-uniform
+  const int64_t row_bytes = p.row_stride * Tag::kBytes;
+  const char* xb = static_cast<const char*>(p.x);
+
+  // Offsets are masked rather than branched on: a branch let the compiler merge the two paths'
+  // loads through register copies (and drop the non-temporal hint of one of them).
+  auto load_row = [&](u32x4 (&w)[kV], int64_t r, bool real) {
+    const int64_t mask = -(int64_t)real;
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+      const int64_t off = (r * row_bytes + (int64_t)(tid + kT * i) * 16) & mask;
+      w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xb + off));
+    }
+  };
+  // The first row's loads go out before the smooth values' (which every workgroup reads from
+  // L2 at once when the kernel starts), so the two round trips overlap: with the smooth loads
+  // first and waited for, each workgroup started its row stream one round trip late -- about
+  // 1.5 us of configs[3]'s 19 us.
+  u32x4 wa[kV], wb[kV];
+  load_row(wa, row, true);
+  __builtin_amdgcn_sched_barrier(0);
+  float smv[kV][kPer];
+  if constexpr (kChan) {
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+      const u32x4* sp = reinterpret_cast<const u32x4*>(p.smooth + (int64_t)(tid + kT * i) * kPer);
+#pragma unroll
+      for (int q = 0; q < kPer / 4; ++q) {
+        const u32x4 s4 = sp[q];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) smv[i][4 * q + e] = __uint_as_float(s4[e]);
+      }
+    }
+  }
+  float s_scalar = kScalar ? p.smooth[0] : 1.0f;
+  // Wait for the smooth values here, once: left pending into the row loop, they made the
+  // compiler's wait analysis flush every outstanding load and store at the loop head.
+  if constexpr (kChan) {
+#pragma unroll
+    for (int i = 0; i < kV; ++i)
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) asm volatile("" : "+v"(smv[i][e]));
+  }
+  if constexpr (kScalar) asm volatile("" : "+v"(s_scalar));
+
+  // Prefetch the next row into `nxt`, then quantise `cur` (row r) and write it; its codes stay
+  // in `keep` until the end of the next row's step.
+  //
+  // Why the stores and the keep: the compiler's wait analysis does not let a register that
+  // held a pending store's data be overwritten before that store completes, and with the
+  // memory counter in order such a wait also waits for every load issued before the store --
+  // the next row's prefetch included.  Holding each row's codes until the following row's
+  // codes are stored means their registers are only reused a whole row later, when the store
+  // has long completed.  The stores are the compiler's own (not inline assembly), so that the
+  // same analysis counts them and waits for a row's loads with the exact number of later
+  // memory operations outstanding.
+  constexpr int kC = kV * kPer / 4;
+  auto step = [&](u32x4 (&cur)[kV], u32x4 (&nxt)[kV], int64_t r, int par, uint32_t (&keep)[kC],
+                  uint32_t (&prev)[kC]) -> bool {
+    const int64_t nr = r + gridDim.x;
+    const bool more = nr < rows;  // workgroup-uniform
+    load_row(nxt, nr, more);
+    __builtin_amdgcn_sched_barrier(0);
+    float v[kV][kPer];
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+      unpack(Tag{}, cur[i], v[i]);
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        // RN(x * smooth), no FMA
+        if constexpr (kScalar) v[i][e] = v[i][e] * s_scalar;
+        if constexpr (kChan) v[i][e] = v[i][e] * smv[i][e];
+        m = abs_max(m, v[i][e]);
+      }
+    }
+    const uint32_t mw = wave_max_u32_sgpr(__float_as_uint(m));
+    if (lane == 0) red[par][wave] = mw;
+    __syncthreads();
+    const uint32_t mb = max(max(red[par][0], red[par][1]), max(red[par][2], red[par][3]));
+    const RowScale rs =
+        make_row_scale(__uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)mb)));
+    int8_t* orow = p.out + r * p.channels;  // uniform base, 32-bit lane offsets
+#pragma unroll
+    for (int i = 0; i < kV; ++i) encode_row<kPer>(v[i], rs, keep + i * (kPer / 4));
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+      const uint32_t off = (uint32_t)(tid + kT * i) * kPer;
+      if constexpr (kPer == 8) {
+        u32x2 c2;
+        c2[0] = keep[2 * i];
+        c2[1] = keep[2 * i + 1];
+        __builtin_nontemporal_store(c2, reinterpret_cast<u32x2*>(orow + off));
+      } else {
+        __builtin_nontemporal_store(keep[i], reinterpret_cast<uint32_t*>(orow + off));
+      }
+    }
+    if (tid == 0) p.out_scale[r] = rs.s;
+#pragma unroll
+    for (int j = 0; j < kC; ++j) asm volatile("" : : "v"(prev[j]));
+    return more;
+  };
+  uint32_t ka[kC], kb[kC];
+#pragma unroll
+  for (int j = 0; j < kC; ++j) kb[j] = 0;
+  for (;;) {
+    if (!step(wa, wb, row, 0, ka, kb)) return;
+    row += gridDim.x;
+    if (!step(wb, wa, row, 1, kb, ka)) return;
+    row += gridDim.x;
+  }
+}
+
+template <class Tag, int kV>
+int launch_dense_wg(const SqParams& p, hipStream_t stream) {
+  int device = 0, cus = 0;
+  if (hipGetDevice(&device) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    return TMO_ERR_LAUNCH;
+  const int64_t blocks = std::min<int64_t>(p.dense_rows, (int64_t)cus * TMO_SQ_WG_ROW_PER_CU);
+  const dim3 grid((unsigned)blocks), block(256);
+  if (p.smooth && p.smooth_len != 1)
+    return launch_kernel(sq_dense_wg<Tag, kV, false, true>, grid, block, stream, p);
+  if (p.smooth) return launch_kernel(sq_dense_wg<Tag, kV, true, false>, grid, block, stream, p);
+  return launch_kernel(sq_dense_wg<Tag, kV, false, false>, grid, block, stream, p);
+}
+
 // Generic path: any channel count / alignment; one wavefront per row, two passes.
 template <class Tag>
 __global__ __launch_bounds__(256) void sq_generic(SqParams p) {
@@ -588,6 +753,14 @@ int launch(const SqParams& p, hipStream_t stream) {
   if (split) {
     if (p.gather_index) return launch_vec<Tag, false, kW>(p, per_lane, stream);
     return launch_vec<Tag, true, kW>(p, per_lane, stream);
+  }
+  if (TMO_SQ_DENSE_WG && !p.gather_index && !p.token_count && nvec % 256 == 0) {
+    switch (nvec / 256) {
+      case 1: return launch_dense_wg<Tag, 1>(p, stream);
+      case 2: return launch_dense_wg<Tag, 2>(p, stream);
+      case 4: return launch_dense_wg<Tag, 4>(p, stream);
+      default: break;
+    }
   }
   if (!p.gather_index && !p.token_count && nvec % kWave == 0) {
     switch (nvec / kWave) {

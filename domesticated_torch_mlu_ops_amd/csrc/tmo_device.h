@@ -165,6 +165,17 @@ __device__ __forceinline__ uint32_t wave_incl_sum_u32(uint32_t v) {
   return v;
 }
 
+// Maximum over the whole wavefront as a scalar: the 16-lane DPP reduction, then the four row
+// results read into scalar registers (no cross-row lane shuffle through LDS).
+__device__ __forceinline__ uint32_t wave_max_u32_sgpr(uint32_t v) {
+  v = group_max_u32<16>(v);
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+
 // Maximum over the whole wavefront, returned as a wave-uniform value: every lane holds the
 // same result after group_max_u32<64>, and readfirstlane tells the compiler so, which turns
 // branches on values derived from it (the encoder's fast / IEEE path choice) into scalar

@@ -357,6 +357,13 @@ def test_attention_validation(lib):
     assert call(splits=4, ws=FAKE, wsb=need - 4) == EINVAL
     assert call(B=0) == 0
     assert call(B=0, mctx=-1) == 0                 # negative max_context_len: unknown, like 0
+    # an empty cache may come with null cache and per-token scale pointers (nothing reads
+    # them); a non-empty one may not
+    assert call(kc=None, vc=None, ks=None, vs=None, NB=0, B=0) == 0
+    assert call(kc=None, NB=16) == EINVAL
+    assert call(vc=None, NB=16) == EINVAL
+    assert call(ks=None, NB=0, smode=2) == EINVAL  # per-channel scales are never empty
+    assert call(bt=None) == EINVAL
 
 
 def test_multi_token_attention_validation(lib):

@@ -105,6 +105,31 @@ def test_attn_per_tensor_scales(tmo, ref, dev):
     run_attn(tmo, ref, dev, case, per_tensor=True)
 
 
+@pytest.mark.parametrize("kv", ["int8_token", "plain"])
+def test_attn_empty_cache(tmo, dev, kv):
+    """num_blocks 0 with positive context lengths: every block-table entry lies outside the
+    (zero-size) cache, so every key is masked -- D12's empty window, output 0 and lse -inf.
+    The shape is one the MFMA kernel takes for a non-empty cache; it must not read the cache."""
+    B, Hq, Hkv, D, BS = 3, 8, 2, 128, 16
+    int8 = kv == "int8_token"
+    cdt = torch.int8 if int8 else torch.bfloat16
+    q = torch.randn(B, 1, Hq, D, device=dev).to(torch.bfloat16)
+    kc = torch.empty(0, Hkv, BS, D, dtype=cdt, device=dev)
+    vc = torch.empty(0, Hkv, BS, D, dtype=cdt, device=dev)
+    ks = torch.empty(0, Hkv, BS, device=dev) if int8 else None
+    vs = torch.empty(0, Hkv, BS, device=dev) if int8 else None
+    bt = torch.tensor([[0, 1, 2, 3], [5, -1, 0, 2], [1, 1, 1, 1]], dtype=torch.int32, device=dev)
+    lens = torch.tensor([50, 17, 64], dtype=torch.int32, device=dev)
+    out = torch.full_like(q, 7.0)
+    res, lse = tmo.single_query_cached_kv_attn(q, kc, vc, out, bt, lens, ks, vs, None, 64, -1,
+                                               -1, 0.088, return_lse=True,
+                                               kv_cache_quant_bit_size=8 if int8 else -1)
+    torch.cuda.synchronize()
+    assert res is out
+    assert bool((out == 0).all())
+    assert bool(torch.isneginf(lse).all())
+
+
 @pytest.mark.parametrize("D", [64, 128, 256, 96, 40])
 @pytest.mark.parametrize("kv", ["int8_token", "plain"])
 def test_attn_head_sizes(tmo, ref, dev, D, kv):

@@ -515,6 +515,27 @@ def test_quant_to_linear_cache_int4_odd_offsets_and_shapes_rejected(tmo, ref, de
                                   None, None, 4)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_quant_to_linear_cache_int4_shared_batch_odd_boundaries(tmo, ref, dev, dtype):
+    """Many sequences written into ONE cache batch, back to back, with odd lengths: every
+    boundary between two sequences falls inside a V position pair, so two workgroups write
+    the two nibbles of the same V bytes in the same call.  Each must keep the other's nibble
+    (the reference writes every sequence's positions independently)."""
+    g = torch.Generator().manual_seed(87)
+    B, H, D = 48, 2, 128
+    lens = (2 * torch.randint(0, 5, (B,), generator=g) + 1).to(torch.int32)   # 1, 3, ..., 9
+    starts = torch.cat((torch.zeros(1, dtype=torch.int64), lens.cumsum(0)[:-1].long()))
+    T = int(lens.sum())
+    key = (torch.randn(T, H, D, generator=g) * 2).to(dtype)
+    value = (torch.randn(T, H, D, generator=g) * 3).to(dtype)
+    case = W.LinearCase(key, value, lens, True, None,
+                        torch.zeros(B, dtype=torch.int32),           # one cache batch for all
+                        (starts + 1).to(torch.int32),                # odd first position
+                        cache_batch=2, cache_len=T + 4)
+    for _ in range(3):
+        _quant4_both(tmo, ref, dev, case)
+
+
 def _dequant4_both(tmo, ref, dev, case, dtype, mode, with_v=True):
     g = torch.Generator().manual_seed(85)
     H, D = case.key.shape[-2:]
