@@ -221,8 +221,9 @@ def dequant_from_paged_cache(
     ``key[begin_i + t] = (fp32(code) * scale).to(key.dtype)`` for ``t < context_lengths[i]``;
     ``begin_i`` is ``context_seq_offset[i]`` or the running sum of ``context_lengths``.
     ``quant_mode`` 0: per-channel scale ``[heads, head_size]``; 1: per-token scale
-    ``[num_blocks, heads, block_size]``.  ``quant_bit`` must be 8 (the mx-fp6 mode 2 is not
-    part of this build).
+    ``[num_blocks, heads, block_size]``; scales float32 or bfloat16.  The caches are int8, or
+    the ``torch.float8_e4m3fn`` pages ``quant_to_paged_cache`` writes (code = the e4m3fn
+    value).  ``quant_bit`` must be 8 (the mx-fp6 mode 2 is not part of this build).
 
     Reference: ``_ops.py:3734-3824`` (math ``:3749-3774``).  Returns None.
     """
@@ -544,9 +545,10 @@ def single_query_cached_kv_attn(
 ):
     """Attention of each sequence's query tokens over its paged KV cache:
     ``softmax(softmax_scale * q K^T (+ alibi)) V`` per query head, keys gathered through
-    ``block_tables`` from ``[num_blocks, kv_heads, block_size, head_size]`` caches -- int8
-    (``kv_cache_quant_bit_size=8``) with per-token, per-channel or per-tensor scales, or of q's
-    dtype (``-1``); query head h reads KV head ``h // (heads / kv_heads)``.  q is ``[batch,
+    ``block_tables`` from ``[num_blocks, kv_heads, block_size, head_size]`` caches -- int8 or
+    ``torch.float8_e4m3fn`` (``kv_cache_quant_bit_size=8``) with per-token, per-channel,
+    per-group or per-tensor float32 / bfloat16 scales, or of q's dtype (``-1``); query head h
+    reads KV head ``h // (heads / kv_heads)``.  q is ``[batch,
     seq_q, heads, head_size]``, ``[total_q, heads, head_size]`` with ``cu_seq_q`` (``[batch +
     1]``, ``max_seq_q`` an upper bound of the counts or <= 0 for unknown) or ``[batch, heads,
     head_size]``.  A sequence's nq tokens are its last nq positions: token s (position
@@ -554,8 +556,9 @@ def single_query_cached_kv_attn(
     ``slope * (j - P)``, and ``sink`` (``[heads]`` float logits) joins the softmax
     denominator only.  Computed in fp32 (MFMA with exact bf16/f16 operands).  With
     ``return_lse`` also returns ``ln`` of the softmax denominator, ``[batch, heads, seq_q]``
-    (or ``[heads, total_q]`` for 3-D q).  ``mask``, ``v_cache=None`` and quantised q / output
-    raise ``RuntimeError``.
+    (or ``[heads, total_q]`` for 3-D q).  ``mask`` and quantised q / output raise
+    ``RuntimeError``.  A positive ``max_seq_q`` is trusted: query tokens past it are not
+    computed (as the reference says of an understated ``max_context_len``).
 
     Reference: ``_ops.py:777-900`` (math ``:800-817``).  Returns ``out`` or ``(out, lse)``.
     """

@@ -8,9 +8,10 @@
 // token: P = L - 1), over keys j in [max(0, P - window_left), P]; key j at row j % BS of page
 // block_tables[i, j / BS] (pages outside [0, NB) are masked): k_j its first D channels, v_j
 // the first Dv of the V cache's row, or of the K row when both live in one cache; query head
-// hq reads KV head hq / (Hq / Hkv).  Caches are int8 with fp32 scales (k = code * scale) per
-// token [NB, Hkv, BS] (strided in the first two dims), per channel [Hkv, D], or per group
-// (K [NB, Hkv, BS, D / 32], V [NB, Hkv, BS / 32, Dv]), or of q's dtype.
+// hq reads KV head hq / (Hq / Hkv).  Caches are int8 codes or float8_e4m3fn values with fp32 or
+// bf16 scales (k = code * scale) per token [NB, Hkv, BS] (strided in the first two dims), per
+// channel [Hkv, D], or per group (K [NB, Hkv, BS, D / 32], V [NB, Hkv, BS / 32, Dv]), or of
+// q's dtype.
 //
 // MFMA path (bf16 or f16 operands, fp32 accumulation; K and V head sizes and cache rows all 64
 // / 128 / 256, block_size a multiple of 16, per-token or per-channel scales): the query columns of a (sequence, KV head) are its (token, query head)
@@ -67,8 +68,9 @@ struct AttnParams {
   const void* kc;
   const void* vc;                // caches [NB, Hkv, BS, k_row / v_row] contiguous
   int64_t k_row, v_row;          // cache row lengths (elements)
-  const float* ks;
-  const float* vs;
+  const void* ks;                // scales: fp32, or bf16 when s_bf16
+  const void* vs;
+  int32_t s_bf16;
   int32_t smode;                 // 0 plain caches, 1 per token, 2 per channel, 3 per group
   int64_t ks_sb, ks_sh, vs_sb, vs_sh;  // per-token scale strides (page, head)
   const int32_t* bt;
@@ -93,6 +95,7 @@ struct AttnParams {
 };
 
 // ------------------------------------------------------------------------------ small helpers
+
 
 __device__ __forceinline__ uint16_t bf16_bits_rne(float x) {
   return __builtin_bit_cast(uint16_t, (__bf16)x);
@@ -224,28 +227,47 @@ __device__ __forceinline__ f16x4 codes_f16(uint32_t w) {
   return __builtin_bit_cast(f16x4, h);
 }
 
-// kKind: 0 int8 caches (f16 QK, bf16 PV), 1 bf16 caches, 2 f16 caches.  kQLo: q needs a lo
-// operand.
+// Four float8_e4m3fn codes (one dword) -> four f16 operands holding their values exactly:
+// v_cvt_pk_f32_fp8 decodes two codes to fp32, v_cvt_pkrtz_f16_f32 packs two fp32 into f16
+// (every e4m3fn value -- at most 4 significant bits, 2^-9 .. 448 -- is an f16 value, so the
+// conversion's rounding never acts).
+__device__ __forceinline__ f16x4 fp8_f16(uint32_t w) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const f2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const f2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  u32x2 h;
+  h[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a[0], a[1]));
+  h[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(b[0], b[1]));
+  return __builtin_bit_cast(f16x4, h);
+}
+
+// kKind: 0 int8 caches (f16 QK, bf16 PV), 1 bf16 caches, 2 f16 caches, 3 float8_e4m3fn caches
+// (as int8: f16 QK against the exact code values, no bias; bf16 PV).  kQLo: q needs a lo
+// operand.  kSB: the scale tensors are bf16 (else fp32).
 // Workgroups per CU the register allocation must allow: three (168 registers per lane) for
-// the int8 kernels up to head_size 128, fewer where that would spill.
-constexpr int attn_min_blocks(int d, int kind) { return d == 256 ? 1 : (kind != 0 && d == 128 ? 2 : 3); }
+// the quantised-cache kernels up to head_size 128, fewer where that would spill.
+constexpr bool attn_quant(int kind) { return kind == 0 || kind == 3; }
+constexpr int attn_min_blocks(int d, int kind) {
+  return d == 256 ? 1 : (!attn_quant(kind) && d == 128 ? 2 : 3);
+}
 
 #ifndef TMO_ATTN_DEPTH
 #define TMO_ATTN_DEPTH 2
 #endif
 
-template <int kD, int kKind, bool kQLo>
+template <int kD, int kKind, bool kQLo, bool kSB>
 __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(AttnParams p) {
+  constexpr bool kQuant = attn_quant(kKind);  // codes with per-token / per-channel scales
   // tiles in flight per wavefront: three register sets where they fit the register budget of
-  // attn_min_blocks (the int8 kernels up to head_size 128)
-  constexpr int kDepth = (kKind == 0 && kD <= 128 && !kQLo) ? TMO_ATTN_DEPTH : 2;
+  // attn_min_blocks (the quantised-cache kernels up to head_size 128)
+  constexpr int kDepth = (kQuant && kD <= 128 && !kQLo) ? TMO_ATTN_DEPTH : 2;
   constexpr bool kF16 = kKind == 2;
   using M = Mfma<kF16>;
   using V4 = typename M::V4;
   constexpr int kDC = kD / 4;       // channels per lane group in the K layout
   constexpr int kDV = kD / 16;      // channels per lane in the V layout
   constexpr int kQK = kD / 16;      // QK MFMAs per tile
-  constexpr int kEs = kKind == 0 ? 1 : 2;  // cache element bytes
+  constexpr int kEs = kQuant ? 1 : 2;  // cache element bytes
 
   const int lane = threadIdx.x & (kWave - 1);
   // wave-uniform (readfirstlane): the tile indices, page numbers and page offsets derived from it
@@ -274,7 +296,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   // of two sigma that puts the column's largest |q| in [2^14, 2^15) (an f16 holds every bf16
   // and f16 value of that column exactly down to 2^-29 of the largest), with a second (lo)
   // operand when q is folded with per-channel key scales.  Plain caches use their own type.
-  using MQ = Mfma<kKind == 0 ? true : kF16>;
+  using MQ = Mfma<kQuant ? true : kF16>;
   using VQ = typename MQ::V4;
   VQ qhi[kQK], qlo[kQLo ? kQK : 1];
   float qx[kQK][4];
@@ -325,11 +347,15 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
         grp * kDC);
 #pragma unroll
     for (int v = 0; v < kQV; ++v) qraw[v] = qvalid ? qp[v] : u32x4{0u, 0u, 0u, 0u};
-    u32x4 kcs[kKind == 0 ? kDC / 4 : 1];
-    if (kKind == 0 && p.smode == 2) {
-      const u32x4* sp = reinterpret_cast<const u32x4*>(p.ks + (int64_t)hk * kD + grp * kDC);
+    // per-channel key scales of the lane's channels, raw: fp32 (4 per vector) or bf16 (8)
+    constexpr int kCS = kQuant ? (kSB ? kDC / 8 : kDC / 4) : 1;
+    u32x4 kcs[kCS];
+    if (kQuant && p.smode == 2) {
+      const int64_t e0 = (int64_t)hk * kD + grp * kDC;
+      const u32x4* sp = kSB ? reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.ks) + e0)
+                            : reinterpret_cast<const u32x4*>(static_cast<const float*>(p.ks) + e0);
 #pragma unroll
-      for (int v = 0; v < (kKind == 0 ? kDC / 4 : 1); ++v) kcs[v] = sp[v];
+      for (int v = 0; v < kCS; ++v) kcs[v] = sp[v];
     }
     refill();
     const bool bf = p.q_dtype == TMO_DTYPE_BF16;
@@ -341,7 +367,14 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
         const uint32_t w = qraw[c / 8][(c % 8) / 2];
         const uint32_t h = (c & 1) ? (w >> 16) : (w & 0xffffu);
         float x = bf ? __uint_as_float(h << 16) : f16_bits_to_f32(h);
-        if (kKind == 0 && p.smode == 2) x *= __uint_as_float(kcs[c / 4][c % 4]);
+        if (kQuant && p.smode == 2) {
+          if constexpr (kSB) {
+            const uint32_t sw = kcs[c / 8][(c % 8) / 2];
+            x *= __uint_as_float((c & 1) ? (sw & 0xffff0000u) : (sw << 16));
+          } else {
+            x *= __uint_as_float(kcs[c / 4][c % 4]);
+          }
+        }
         qx[m][e] = x;
         qabs = fmaxf(qabs, fabsf(x));
       }
@@ -353,7 +386,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
       for (int e = 0; e < 4; ++e) {
         const int d = grp * kDC + 4 * m + e;
         float x = qvalid ? load_q(p, i * p.q_sb + qrow * p.q_ss + (int64_t)hq * p.q_sh + d) : 0.0f;
-        if (kKind == 0 && p.smode == 2) x *= p.ks[(int64_t)hk * kD + d];
+        if (kQuant && p.smode == 2) x *= scale_at(p.ks, (int64_t)hk * kD + d, kSB);
         qx[m][e] = x;
         qabs = fmaxf(qabs, fabsf(x));
       }
@@ -361,7 +394,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
     refill();
   }
   float inv_sigma = 1.0f, qk_off = 0.0f;
-  if constexpr (kKind == 0) {
+  if constexpr (kQuant) {
     qabs = col_max(qabs);
     const int ex = qabs > 0.0f ? __builtin_amdgcn_frexp_expf(qabs) : 1;  // qabs in [2^(ex-1), 2^ex)
     const float sigma = __builtin_ldexpf(1.0f, 15 - ex);
@@ -382,7 +415,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
         }
       }
     }
-    qk_off = kCodeBias * col_sum(qsum);
+    if constexpr (kKind == 0) qk_off = kCodeBias * col_sum(qsum);
   } else {
 #pragma unroll
     for (int m = 0; m < kQK; ++m) {
@@ -415,10 +448,16 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   constexpr int kKW = kDC * kEs / 4, kVW = kDV * kEs / 4;   // dwords per lane
 
   // Raw tile: this lane's K piece, its V pieces of four tokens, the per-token scales.
+  // The per-token scales stay raw until the tile is computed (fp32 words, or bf16 pairs in
+  // ks[0..1] / vs[0..1]): widening them at load time would wait for the loads there.
   struct Raw {
     uint32_t kw[kKW];
     uint32_t vw[4][kVW];
-    float ksc[4], vsc[4];
+    uint32_t ks[4], vs[4];
+  };
+  auto raw_scale = [](const uint32_t (&w)[4], int e) -> float {
+    if constexpr (kSB) return __uint_as_float((e & 1) ? (w[e / 2] & 0xffff0000u) : (w[e / 2] << 16));
+    return __uint_as_float(w[e]);
   };
   auto load_tile = [&](Raw& r, int32_t tl, int64_t blk) {
     const int32_t t0 = tl * 16;
@@ -454,16 +493,27 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
         }
       }
     }
+    constexpr uint32_t kOne = kSB ? 0x3f803f80u : 0x3f800000u;  // 1.0 (a bf16 pair)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r.ksc[e] = r.vsc[e] = 1.0f;
-    if (kKind == 0 && p.smode == 1) {
+    for (int e = 0; e < 4; ++e) r.ks[e] = r.vs[e] = kOne;
+    if (kQuant && p.smode == 1) {
       const int32_t so = row0 + 4 * grp;
-      const u32x4 a = *reinterpret_cast<const u32x4*>(p.ks + (blk * p.ks_sb + hk * p.ks_sh) + so);
-      const u32x4 b = *reinterpret_cast<const u32x4*>(p.vs + (blk * p.vs_sb + hk * p.vs_sh) + so);
+      const int64_t ka = blk * p.ks_sb + hk * p.ks_sh + so, va = blk * p.vs_sb + hk * p.vs_sh + so;
+      if constexpr (kSB) {
+        const u32x2 a = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(p.ks) + ka);
+        const u32x2 b = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(p.vs) + va);
+        r.ks[0] = a[0];
+        r.ks[1] = a[1];
+        r.vs[0] = b[0];
+        r.vs[1] = b[1];
+      } else {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(static_cast<const float*>(p.ks) + ka);
+        const u32x4 b = *reinterpret_cast<const u32x4*>(static_cast<const float*>(p.vs) + va);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        r.ksc[e] = __uint_as_float(a[e]);
-        r.vsc[e] = __uint_as_float(b[e]);
+        for (int e = 0; e < 4; ++e) {
+          r.ks[e] = a[e];
+          r.vs[e] = b[e];
+        }
       }
     }
   };
@@ -478,6 +528,8 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
         VQ a;
         if constexpr (kKind == 0) {
           a = codes_f16(r.kw[m]);
+        } else if constexpr (kKind == 3) {
+          a = fp8_f16(r.kw[m]);
         } else {
           u32x2 w;
           w[0] = r.kw[2 * m];
@@ -494,7 +546,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int32_t j = t0 + 4 * grp + e;
-        float v = (s[e] - qk_off) * (r.ksc[e] * score_scale);
+        float v = (s[e] - qk_off) * (raw_scale(r.ks, e) * score_scale);
         if (p.alibi) v += alibi * (float)(j - pos);
         if (j < klo || j > khi) v = -__builtin_inff();
         sc[e] = v;
@@ -534,7 +586,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
         u32x2 hv, lv;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-          const f2 a = {pe[2 * k] * r.vsc[2 * k], pe[2 * k + 1] * r.vsc[2 * k + 1]};
+          const f2 a = {pe[2 * k] * raw_scale(r.vs, 2 * k), pe[2 * k + 1] * raw_scale(r.vs, 2 * k + 1)};
           const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(a, bf2));
           const f2 l = {a[0] - __uint_as_float(h << 16), a[1] - __uint_as_float(h & 0xffff0000u)};
           hv[k] = h;
@@ -545,7 +597,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
       } else
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float pv = pe[e] * r.vsc[e];
+        const float pv = pe[e] * raw_scale(r.vs, e);
         if constexpr (kF16) {
           const _Float16 h = (_Float16)pv;
           phi[e] = h;
@@ -568,6 +620,10 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
             const int8_t code = (int8_t)(r.vw[e][j >> 2] >> (8 * (j & 3)));
             b4[e] = (short)(__float_as_uint((float)code) >> 16);
           }
+        } else if constexpr (kKind == 3) {
+          // the e4m3fn value's fp32 pattern truncated to bf16 is exact (<= 4 significant bits)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) b4[e] = (short)(__float_as_uint(fp8_value(r.vw[e][j >> 2], j & 3)) >> 16);
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e) b4[e] = (short)(r.vw[e][j >> 1] >> (16 * (j & 1)));
@@ -693,7 +749,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
 #pragma unroll
       for (int w = 1; w < 4; ++w) o += lds_o[w - 1][lane * kRow + e * kDV + j] * f[w];
       o *= inv;
-      if (kKind == 0 && p.smode == 2) o *= p.vs[(int64_t)hk * kD + d];  // per-channel V scale
+      if (kQuant && p.smode == 2) o *= scale_at(p.vs, (int64_t)hk * kD + d, kSB);  // per-channel V
       if (direct) {
         store_out(p, orow + d, o);
       } else {
@@ -830,16 +886,23 @@ __device__ __forceinline__ float plain_value(const void* base, int64_t e, int ca
   }
 }
 
+// Code e of a quantised cache as fp32: an int8 code, or a float8_e4m3fn value.
+__device__ __forceinline__ float code_value(const void* base, int64_t e, int cache_dtype) {
+  if (cache_dtype == TMO_DTYPE_I8) return (float)static_cast<const int8_t*>(base)[e];
+  return fp8_value(static_cast<const uint8_t*>(base)[e], 0);
+}
+
 // Key channel d of row `row` of page blk, KV head hk.
 __device__ __forceinline__ float key_value(const AttnParams& p, int64_t blk, int hk, int64_t row,
                                            int d, int cache_dtype) {
   const int64_t r = (blk * p.Hkv + hk) * p.BS + row;
-  if (cache_dtype != TMO_DTYPE_I8) return plain_value(p.kc, r * p.k_row + d, cache_dtype);
-  const float code = (float)static_cast<const int8_t*>(p.kc)[r * p.k_row + d];
+  if (cache_dtype != TMO_DTYPE_I8 && cache_dtype != TMO_DTYPE_F8E4M3)
+    return plain_value(p.kc, r * p.k_row + d, cache_dtype);
+  const float code = code_value(p.kc, r * p.k_row + d, cache_dtype);
   switch (p.smode) {
-    case 1: return code * p.ks[blk * p.ks_sb + hk * p.ks_sh + row];
-    case 2: return code * p.ks[(int64_t)hk * p.D + d];
-    default: return code * p.ks[r * (p.D >> 5) + (d >> 5)];
+    case 1: return code * scale_at(p.ks, blk * p.ks_sb + hk * p.ks_sh + row, p.s_bf16);
+    case 2: return code * scale_at(p.ks, (int64_t)hk * p.D + d, p.s_bf16);
+    default: return code * scale_at(p.ks, r * (p.D >> 5) + (d >> 5), p.s_bf16);
   }
 }
 
@@ -847,12 +910,15 @@ __device__ __forceinline__ float key_value(const AttnParams& p, int64_t blk, int
 __device__ __forceinline__ float value_value(const AttnParams& p, int64_t blk, int hk, int64_t row,
                                              int d, int cache_dtype) {
   const int64_t r = (blk * p.Hkv + hk) * p.BS + row;
-  if (cache_dtype != TMO_DTYPE_I8) return plain_value(p.vc, r * p.v_row + d, cache_dtype);
-  const float code = (float)static_cast<const int8_t*>(p.vc)[r * p.v_row + d];
+  if (cache_dtype != TMO_DTYPE_I8 && cache_dtype != TMO_DTYPE_F8E4M3)
+    return plain_value(p.vc, r * p.v_row + d, cache_dtype);
+  const float code = code_value(p.vc, r * p.v_row + d, cache_dtype);
   switch (p.smode) {
-    case 1: return code * p.vs[blk * p.vs_sb + hk * p.vs_sh + row];
-    case 2: return code * p.vs[(int64_t)hk * p.Dv + d];
-    default: return code * p.vs[((blk * p.Hkv + hk) * (p.BS >> 5) + (row >> 5)) * p.Dv + d];
+    case 1: return code * scale_at(p.vs, blk * p.vs_sb + hk * p.vs_sh + row, p.s_bf16);
+    case 2: return code * scale_at(p.vs, (int64_t)hk * p.Dv + d, p.s_bf16);
+    default:
+      return code * scale_at(p.vs, ((blk * p.Hkv + hk) * (p.BS >> 5) + (row >> 5)) * p.Dv + d,
+                             p.s_bf16);
   }
 }
 
@@ -938,22 +1004,22 @@ __global__ __launch_bounds__(256) void attn_generic(AttnParams p) {
 
 // ------------------------------------------------------------------------------ launch
 
-template <int kD, int kKind>
+template <int kD, int kKind, bool kSB>
 int launch_mfma_d(const AttnParams& p, bool qlo, hipStream_t st) {
   const dim3 grid((unsigned)(p.splits * p.ncb), (unsigned)p.Hkv, (unsigned)p.B), block(256);
-  int rc = qlo ? launch_kernel(attn_mfma<kD, kKind, true>, grid, block, st, p)
-               : launch_kernel(attn_mfma<kD, kKind, false>, grid, block, st, p);
+  int rc = qlo ? launch_kernel(attn_mfma<kD, kKind, true, kSB>, grid, block, st, p)
+               : launch_kernel(attn_mfma<kD, kKind, false, kSB>, grid, block, st, p);
   if (rc != TMO_OK || p.splits == 1) return rc;
   const int64_t rows = (int64_t)p.B * p.S * p.Hq;
   return launch_kernel(attn_combine, dim3((unsigned)((rows + 3) / 4)), block, st, p);
 }
 
-template <int kKind>
+template <int kKind, bool kSB>
 int launch_mfma(const AttnParams& p, bool qlo, hipStream_t st) {
   switch (p.D) {
-    case 64: return launch_mfma_d<64, kKind>(p, qlo, st);
-    case 128: return launch_mfma_d<128, kKind>(p, qlo, st);
-    default: return launch_mfma_d<256, kKind>(p, qlo, st);
+    case 64: return launch_mfma_d<64, kKind, kSB>(p, qlo, st);
+    case 128: return launch_mfma_d<128, kKind, kSB>(p, qlo, st);
+    default: return launch_mfma_d<256, kKind, kSB>(p, qlo, st);
   }
 }
 
@@ -984,8 +1050,8 @@ extern "C" int64_t tmo_hip_attn_workspace_bytes(int64_t batch, int64_t num_kv_he
 extern "C" int tmo_hip_cached_kv_attn(
     const void* q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head,
     const int32_t* cu_seq_q, int64_t seq_q, int64_t total_q, const void* k_cache,
-    const void* v_cache, int64_t k_cache_dim, int64_t v_cache_dim, const float* k_scale,
-    const float* v_scale, int scale_mode, int64_t k_scale_stride_block,
+    const void* v_cache, int64_t k_cache_dim, int64_t v_cache_dim, const void* k_scale,
+    const void* v_scale, int scale_mode, int scale_dtype, int64_t k_scale_stride_block,
     int64_t k_scale_stride_head, int64_t v_scale_stride_block, int64_t v_scale_stride_head,
     const int32_t* block_tables, int64_t max_blocks, const int32_t* context_lens,
     const float* alibi_slopes, const float* sink, void* out, int64_t out_stride_batch,
@@ -997,16 +1063,19 @@ extern "C" int tmo_hip_cached_kv_attn(
     void* stream) {
   if (q_dtype != TMO_DTYPE_BF16 && q_dtype != TMO_DTYPE_F16 && q_dtype != TMO_DTYPE_F32)
     return TMO_ERR_UNSUPPORTED_DTYPE;
-  if (cache_dtype != TMO_DTYPE_I8 && cache_dtype != q_dtype) return TMO_ERR_UNSUPPORTED_DTYPE;
-  if (cache_dtype == TMO_DTYPE_I8 && (scale_mode < 1 || scale_mode > 3))
-    return TMO_ERR_UNSUPPORTED_MODE;
+  // quantised caches: int8 codes or float8_e4m3fn values, times fp32 or bf16 scales
+  const bool quant = cache_dtype == TMO_DTYPE_I8 || cache_dtype == TMO_DTYPE_F8E4M3;
+  if (!quant && cache_dtype != q_dtype) return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (quant && scale_dtype != TMO_DTYPE_F32 && scale_dtype != TMO_DTYPE_BF16)
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (quant && (scale_mode < 1 || scale_mode > 3)) return TMO_ERR_UNSUPPORTED_MODE;
   // An empty cache (num_blocks 0: every block-table entry is outside it, so every key is
   // masked) may come with null cache and per-token scale pointers; nothing reads them.
   // Likewise an empty block table (max_blocks 0 caps every context at 0 keys).
   if (!q || !context_lens || !out) return TMO_ERR_INVALID_ARGUMENT;
   if ((num_blocks > 0 && !k_cache) || (max_blocks > 0 && !block_tables))
     return TMO_ERR_INVALID_ARGUMENT;
-  if (cache_dtype == TMO_DTYPE_I8 && (!k_scale || !v_scale) && (num_blocks > 0 || scale_mode != 1))
+  if (quant && (!k_scale || !v_scale) && (num_blocks > 0 || scale_mode != 1))
     return TMO_ERR_INVALID_ARGUMENT;
   // v_cache null: the values are the first head_size_v channels of the K cache's rows
   if (!v_cache) {
@@ -1024,12 +1093,11 @@ extern "C" int tmo_hip_cached_kv_attn(
       q_stride_token < 0 || q_stride_head < 0 || out_stride_batch < 0 || out_stride_token < 0 ||
       out_stride_head < 0 || (cu_seq_q && total_q < 0))
     return TMO_ERR_INVALID_ARGUMENT;
-  const bool int8 = cache_dtype == TMO_DTYPE_I8;
-  if (int8 && scale_mode == 1 &&
+  if (quant && scale_mode == 1 &&
       (k_scale_stride_block < 0 || k_scale_stride_head < 0 || v_scale_stride_block < 0 ||
        v_scale_stride_head < 0))
     return TMO_ERR_INVALID_ARGUMENT;
-  if (int8 && scale_mode == 3 && (head_size % 32 != 0 || block_size % 32 != 0))
+  if (quant && scale_mode == 3 && (head_size % 32 != 0 || block_size % 32 != 0))
     return TMO_ERR_INVALID_ARGUMENT;
   const int64_t g = num_q_heads / num_kv_heads;
   if (batch > 65535 || num_kv_heads > 65535 || splits > 65535 || num_q_heads > 0x7fffffffLL ||
@@ -1062,7 +1130,8 @@ extern "C" int tmo_hip_cached_kv_attn(
   p.v_row = v_cache_dim;
   p.ks = k_scale;
   p.vs = v_scale;
-  p.smode = int8 ? scale_mode : 0;
+  p.smode = quant ? scale_mode : 0;
+  p.s_bf16 = quant && scale_dtype == TMO_DTYPE_BF16;
   p.ks_sb = k_scale_stride_block;
   p.ks_sh = k_scale_stride_head;
   p.vs_sb = v_scale_stride_block;
@@ -1093,14 +1162,14 @@ extern "C" int tmo_hip_cached_kv_attn(
   p.q_dtype = q_dtype;
   p.q_vec = q_dtype != TMO_DTYPE_F32 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
             p.q_sb % 8 == 0 && q_stride_token % 8 == 0 && q_stride_head % 8 == 0 &&
-            (!int8 || scale_mode != 2 || reinterpret_cast<uintptr_t>(k_scale) % 16 == 0);
+            (!quant || scale_mode != 2 || reinterpret_cast<uintptr_t>(k_scale) % 16 == 0);
   p.ws = static_cast<float*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   // MFMA path eligibility: one head size for K and V that is also both caches' row length,
   // page rows in whole 16-token tiles, 16-byte aligned rows and scale vectors (per-token scale
   // offsets of a page and head in multiples of four), q's dtype representable by the operands
-  // (int8 caches: bf16 with a lo part when needed), per-token or per-channel scales.
+  // (quantised caches: f16 with a lo part when needed), per-token or per-channel scales.
   auto al = [](const void* x, int a) { return reinterpret_cast<uintptr_t>(x) % a == 0; };
   // The MFMA kernel always issues its tile loads (a wave with no valid page yet reads page 0,
   // see attn_mfma), so an empty cache takes attn_generic, whose loads are all under the page
@@ -1109,10 +1178,11 @@ extern "C" int tmo_hip_cached_kv_attn(
               head_size_v == head_size && k_cache_dim == head_size &&
               v_cache_dim == head_size && block_size % 16 == 0 && al(k_cache, 16) &&
               al(v_cache, 16) && q_dtype != TMO_DTYPE_F32;
-  if (int8)
+  if (quant)
     mfma = mfma && scale_mode != 3 &&
            (scale_mode != 1 ||
-            (al(k_scale, 16) && al(v_scale, 16) && k_scale_stride_block % 4 == 0 &&
+            (al(k_scale, p.s_bf16 ? 8 : 16) && al(v_scale, p.s_bf16 ? 8 : 16) &&
+             k_scale_stride_block % 4 == 0 &&
              k_scale_stride_head % 4 == 0 && v_scale_stride_block % 4 == 0 &&
              v_scale_stride_head % 4 == 0));
   p.c_dtype = cache_dtype;
@@ -1128,11 +1198,16 @@ extern "C" int tmo_hip_cached_kv_attn(
   int64_t per = (max_context_len + splits - 1) / splits;
   per = (per + 63) / 64 * 64;
   p.split_tokens = per > 0 ? per : 64;
-  // int8 caches: bf16 and f16 q are exact f16 operands after the power-of-two scaling; q
+  // quantised caches: bf16 and f16 q are exact f16 operands after the power-of-two scaling; q
   // folded with per-channel key scales needs the lo operand
-  if (int8) return launch_mfma<0>(p, scale_mode == 2, st);
-  if (cache_dtype == TMO_DTYPE_BF16) return launch_mfma<1>(p, false, st);
-  return launch_mfma<2>(p, false, st);
+  if (cache_dtype == TMO_DTYPE_I8)
+    return p.s_bf16 ? launch_mfma<0, true>(p, scale_mode == 2, st)
+                    : launch_mfma<0, false>(p, scale_mode == 2, st);
+  if (cache_dtype == TMO_DTYPE_F8E4M3)
+    return p.s_bf16 ? launch_mfma<3, true>(p, scale_mode == 2, st)
+                    : launch_mfma<3, false>(p, scale_mode == 2, st);
+  if (cache_dtype == TMO_DTYPE_BF16) return launch_mfma<1, false>(p, false, st);
+  return launch_mfma<2, false>(p, false, st);
 }
 
 extern "C" int tmo_hip_single_query_cached_kv_attn(
@@ -1145,14 +1220,16 @@ extern "C" int tmo_hip_single_query_cached_kv_attn(
     int64_t block_size, int64_t max_context_len, int64_t window_left, float softmax_scale,
     int q_dtype, int cache_dtype, int64_t splits, void* workspace, int64_t workspace_bytes,
     void* stream) {
-  if (cache_dtype == TMO_DTYPE_I8 && scale_mode == 3) return TMO_ERR_UNSUPPORTED_MODE;
+  if ((cache_dtype == TMO_DTYPE_I8 || cache_dtype == TMO_DTYPE_F8E4M3) && scale_mode == 3)
+    return TMO_ERR_UNSUPPORTED_MODE;
   if (!v_cache && num_blocks > 0) return TMO_ERR_INVALID_ARGUMENT;
   if (head_size > 512) return TMO_ERR_INVALID_ARGUMENT;
   // contiguous per-token scales [num_blocks, Hkv, block_size]
   const int64_t sb = num_kv_heads * block_size, sh = block_size;
   return tmo_hip_cached_kv_attn(
       q, q_stride_seq, 0, q_stride_head, nullptr, 1, 0, k_cache, v_cache, head_size, head_size,
-      k_scale, v_scale, scale_mode, sb, sh, sb, sh, block_tables, max_blocks, context_lens,
+      k_scale, v_scale, scale_mode, TMO_DTYPE_F32, sb, sh, sb, sh, block_tables, max_blocks,
+      context_lens,
       alibi_slopes, nullptr, out, out_stride_seq, 0, out_stride_head, lse, lse_stride_seq, 0,
       lse_stride_head, batch, num_q_heads, num_kv_heads, head_size, head_size, num_blocks,
       block_size, max_context_len, window_left, softmax_scale, q_dtype, cache_dtype, splits,

@@ -1,5 +1,6 @@
-// dequant_from_paged_cache for gfx950: gathers each sequence's int8 pages through its block
-// table and writes RNE(fp32(code) * scale) as bf16 / fp16 into packed [sum(ctx), H, D] rows.
+// dequant_from_paged_cache for gfx950: gathers each sequence's int8 (or float8_e4m3fn) pages
+// through its block table and writes RNE(fp32(code) * scale) as bf16 / fp16 into packed
+// [sum(ctx), H, D] rows; scales fp32 or bf16.
 //
 // Semantics: reference _ops.py:3734-3824 (math block :3749-3774; cast order of the linear
 // sibling :3677; quant_mode 0 per-channel scale [H, D], 1 per-token scale [NB, H, BS]).
@@ -25,8 +26,8 @@ struct DequantParams {
   int64_t out_st[2];  // elements
   int64_t out_sh[2];  // elements
   int64_t total_rows;
-  const int8_t* cache[2];
-  const float* scale[2];
+  const int8_t* cache[2];  // int8 codes, or float8_e4m3fn bytes when fp8
+  const void* scale[2];    // fp32, or bf16 when s_bf16
   const int32_t* ctx_len;
   const int32_t* seq_off;  // nullable
   const int32_t* block_tables;
@@ -43,7 +44,46 @@ struct DequantParams {
   int32_t part_shift;  // log2(work items per page)  (page-list path)
   int32_t mode;      // 0 per-channel, 1 per-token
   int32_t nkv;
+  int32_t fp8;       // float8_e4m3fn caches
+  int32_t s_bf16;    // bf16 scales
 };
+
+// Code / scale formats of the vector kernels as one template argument: bit 1 set for
+// float8_e4m3fn caches (else int8), bit 0 for bf16 scales (else fp32).
+constexpr bool cs_fp8(int cs) { return (cs & 2) != 0; }
+constexpr bool cs_bf16(int cs) { return (cs & 1) != 0; }
+
+// 16 outputs of one 16-code unit (w) with the per-channel scales of channels d0 .. d0 + 15 of
+// head h (in L2: loaded here, next to their use) or one per-token scale s.
+template <int kCS>
+__device__ __forceinline__ void decode16(const u32x4& w, const void* scale, int64_t chan0,
+                                         bool per_token, float s, float* f) {
+  if (per_token) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) f[e] = code_byte(w[e >> 2], e & 3, cs_fp8(kCS)) * s;
+    return;
+  }
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    u32x4 sv[2];
+    if constexpr (cs_bf16(kCS)) {
+      sv[0] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(scale) + chan0 + 8 * half);
+    } else {
+      const u32x4* sp = reinterpret_cast<const u32x4*>(static_cast<const float*>(scale) + chan0 + 8 * half);
+      sv[0] = sp[0];
+      sv[1] = sp[1];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      f[8 * half + e] = code_byte(w[2 * half + e / 4], e & 3, cs_fp8(kCS)) * scale_of8<cs_bf16(kCS)>(sv, e);
+  }
+}
+
+// The per-token scale of page row srow, read in the scale tensor's own type.
+template <int kCS>
+__device__ __forceinline__ float token_scale(const void* scale, int64_t srow) {
+  return scale_at(scale, srow, cs_bf16(kCS));
+}
 
 // Exclusive prefix sum of ctx_len[0..i), computed by the whole workgroup.
 __device__ int64_t seq_begin(const DequantParams& p, int64_t i, int64_t* red) {
@@ -94,7 +134,7 @@ __device__ __forceinline__ void store16(F32, void* base, int64_t elem, const flo
 
 // Vector path: head_dim % 16 == 0 with head_dim/16 and block_size powers of two, 16-byte
 // aligned caches and output rows.
-template <class Tag, int kIters>
+template <class Tag, int kIters, int kCS>
 __global__ __launch_bounds__(256) void dequant_paged_vec(DequantParams p) {
   __shared__ int64_t red[256 / kWave];
   const int64_t i = blockIdx.x / p.grid_blocks;  // sequence
@@ -137,21 +177,10 @@ __global__ __launch_bounds__(256) void dequant_paged_vec(DequantParams p) {
       for (int kv = 0; kv < 2; ++kv) {
         if (kv >= p.nkv) continue;
         float f[16];
-        if (p.mode == 1) {
-          const float s = p.scale[kv][((blk * p.heads + h) << p.bs_shift) + o];
-#pragma unroll
-          for (int e = 0; e < 16; ++e)
-            f[e] = (float)(int8_t)(w[kv][it][e >> 2] >> (8 * (e & 3))) * s;
-        } else {
-          const u32x4* sp = reinterpret_cast<const u32x4*>(p.scale[kv] + (int64_t)h * p.head_dim + d0);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const u32x4 sv = sp[q];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              f[4 * q + e] = (float)(int8_t)(w[kv][it][q] >> (8 * e)) * __uint_as_float(sv[e]);
-          }
-        }
+        const float s = p.mode == 1
+                            ? token_scale<kCS>(p.scale[kv], ((blk * p.heads + h) << p.bs_shift) + o)
+                            : 0.0f;
+        decode16<kCS>(w[kv][it], p.scale[kv], (int64_t)h * p.head_dim + d0, p.mode == 1, s, f);
         store16(Tag{}, p.out[kv], row * p.out_st[kv] + (int64_t)h * p.out_sh[kv] + d0, f);
       }
     }
@@ -225,7 +254,7 @@ __device__ __forceinline__ T block_scan(T v, T* tmp, T& total) {
 // cache layout (d16, then token, then head: a wavefront reads 1 KiB of one head page and
 // writes 256 B runs of 8 output rows), which measured faster on MI355X than the
 // output-row-major order.
-template <class Tag, int kIters>
+template <class Tag, int kIters, int kCS>
 __global__ __launch_bounds__(256) void dequant_paged_persistent(DequantParams p) {
   extern __shared__ int64_t lds[];
   int64_t* tok_start = lds;                                           // [batch]
@@ -291,7 +320,7 @@ __global__ __launch_bounds__(256) void dequant_paged_persistent(DequantParams p)
           for (int kv = 0; kv < 2; ++kv) {
             if (kv < p.nkv) {
               w[kv][it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.cache[kv] + off));
-              if (p.mode == 1) sc[kv][it] = p.scale[kv][srow];
+              if (p.mode == 1) sc[kv][it] = token_scale<kCS>(p.scale[kv], srow);
             }
           }
         }
@@ -308,22 +337,8 @@ __global__ __launch_bounds__(256) void dequant_paged_persistent(DequantParams p)
         for (int kv = 0; kv < 2; ++kv) {
           if (kv >= p.nkv) continue;
           float f[16];
-          if (p.mode == 1) {
-            const float s = sc[kv][it];
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-              f[e] = (float)(int8_t)(w[kv][it][e >> 2] >> (8 * (e & 3))) * s;
-          } else {
-            const u32x4* sp =
-                reinterpret_cast<const u32x4*>(p.scale[kv] + (int64_t)q.h * p.head_dim + d0);
-#pragma unroll
-            for (int qq = 0; qq < 4; ++qq) {
-              const u32x4 sv = sp[qq];
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                f[4 * qq + e] = (float)(int8_t)(w[kv][it][qq] >> (8 * e)) * __uint_as_float(sv[e]);
-            }
-          }
+          decode16<kCS>(w[kv][it], p.scale[kv], (int64_t)q.h * p.head_dim + d0, p.mode == 1,
+                        p.mode == 1 ? sc[kv][it] : 0.0f, f);
           store16(Tag{}, p.out[kv], row * p.out_st[kv] + (int64_t)q.h * p.out_sh[kv] + d0, f);
         }
       }
@@ -424,7 +439,7 @@ __global__ __launch_bounds__(256) void dequant_page_list(DequantParams p, PageEn
   list[page_start + j] = e;
 }
 
-template <class Tag, int kMode, int kKV>
+template <class Tag, int kMode, int kKV, int kCS>
 __global__ __launch_bounds__(256) void dequant_paged_list(DequantParams p,
                                                           const PageEntry* __restrict__ list,
                                                           const int64_t* __restrict__ total) {
@@ -462,24 +477,27 @@ __global__ __launch_bounds__(256) void dequant_paged_list(DequantParams p,
     for (int kv = 0; kv < kKV; ++kv) {
       c[kv] = __builtin_nontemporal_load(
           reinterpret_cast<const u32x2*>(p.cache[kv] + e.blk * page_codes + (int64_t)u * 8));
-      if constexpr (kMode == 1) sc[kv] = p.scale[kv][e.blk * page_rows + (u >> u8)];
+      if constexpr (kMode == 1) sc[kv] = token_scale<kCS>(p.scale[kv], e.blk * page_rows + (u >> u8));
     }
 #pragma unroll
     for (int kv = 0; kv < kKV; ++kv) {
       float f[8];
       if constexpr (kMode == 1) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) f[k] = (float)(int8_t)(c[kv][k >> 2] >> (8 * (k & 3))) * sc[kv];
+        for (int k = 0; k < 8; ++k) f[k] = code_byte(c[kv][k >> 2], k & 3, cs_fp8(kCS)) * sc[kv];
       } else {
-        const u32x4* sp =
-            reinterpret_cast<const u32x4*>(p.scale[kv] + (int64_t)h * p.head_dim + d0);
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const u32x4 sv = sp[q];
-#pragma unroll
-          for (int k = 0; k < 4; ++k)
-            f[4 * q + k] = (float)(int8_t)(c[kv][q] >> (8 * k)) * __uint_as_float(sv[k]);
+        u32x4 sv[2];
+        const int64_t c0 = (int64_t)h * p.head_dim + d0;
+        if constexpr (cs_bf16(kCS)) {
+          sv[0] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.scale[kv]) + c0);
+        } else {
+          const u32x4* sp = reinterpret_cast<const u32x4*>(static_cast<const float*>(p.scale[kv]) + c0);
+          sv[0] = sp[0];
+          sv[1] = sp[1];
         }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          f[k] = code_byte(c[kv][k >> 2], k & 3, cs_fp8(kCS)) * scale_of8<cs_bf16(kCS)>(sv, k);
       }
       if (ok) store8(Tag{}, p.out[kv], row * p.out_st[kv] + (int64_t)h * p.out_sh[kv] + d0, f);
     }
@@ -516,14 +534,15 @@ __global__ __launch_bounds__(256) void dequant_paged_generic(DequantParams p) {
       const int8_t* codes = p.cache[kv] + prow * p.head_dim;
       const int64_t obase = row * p.out_st[kv] + (int64_t)h * p.out_sh[kv];
       for (int d = lane; d < p.head_dim; d += kWave) {
-        const float s = p.mode == 1 ? p.scale[kv][prow] : p.scale[kv][(int64_t)h * p.head_dim + d];
-        store1(Tag{}, p.out[kv], obase + d, (float)codes[d] * s);
+        const float s = scale_at(p.scale[kv], p.mode == 1 ? prow : (int64_t)h * p.head_dim + d,
+                                 p.s_bf16);
+        store1(Tag{}, p.out[kv], obase + d, code_byte((uint8_t)codes[d], 0, p.fp8) * s);
       }
     }
   }
 }
 
-template <class Tag>
+template <class Tag, int kCS>
 int launch(DequantParams p, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   constexpr int kBytes = Tag::kBytes;
   const int64_t blocks = p.batch * p.grid_blocks;
@@ -568,10 +587,12 @@ int launch(DequantParams p, void* workspace, int64_t workspace_bytes, hipStream_
     const int64_t want = std::min<int64_t>(bound, cap) << part_shift;
     const dim3 g((unsigned)want);
     if (p.nkv == 2)
-      return p.mode == 1 ? launch_kernel(dequant_paged_list<Tag, 1, 2>, g, block, stream, p, list, total)
-                         : launch_kernel(dequant_paged_list<Tag, 0, 2>, g, block, stream, p, list, total);
-    return p.mode == 1 ? launch_kernel(dequant_paged_list<Tag, 1, 1>, g, block, stream, p, list, total)
-                       : launch_kernel(dequant_paged_list<Tag, 0, 1>, g, block, stream, p, list, total);
+      return p.mode == 1
+                 ? launch_kernel(dequant_paged_list<Tag, 1, 2, kCS>, g, block, stream, p, list, total)
+                 : launch_kernel(dequant_paged_list<Tag, 0, 2, kCS>, g, block, stream, p, list, total);
+    return p.mode == 1
+               ? launch_kernel(dequant_paged_list<Tag, 1, 1, kCS>, g, block, stream, p, list, total)
+               : launch_kernel(dequant_paged_list<Tag, 0, 1, kCS>, g, block, stream, p, list, total);
   }
   if (p.h_shift >= 0 && p.batch <= kPersistentMaxSeqs &&
       ((int64_t)p.heads << (bs_shift + u_shift)) % 256 == 0) {
@@ -581,21 +602,33 @@ int launch(DequantParams p, void* workspace, int64_t workspace_bytes, hipStream_
       return TMO_ERR_LAUNCH;
     const int64_t want = std::min<int64_t>(blocks, (int64_t)cus * TMO_DEQUANT_WG_PER_CU);
     const unsigned lds = (unsigned)(p.batch * 8 + (2 * p.batch + 1) * 4);
-    return launch_kernel(dequant_paged_persistent<Tag, TMO_DEQUANT_ITERS>, dim3((unsigned)want), block, stream, p,
-                         lds);
+    return launch_kernel(dequant_paged_persistent<Tag, TMO_DEQUANT_ITERS, kCS>, dim3((unsigned)want),
+                         block, stream, p, lds);
   }
-  return launch_kernel(dequant_paged_vec<Tag, 4>, grid, block, stream, p);
+  return launch_kernel(dequant_paged_vec<Tag, 4, kCS>, grid, block, stream, p);
+}
+
+// The kernels for the cache / scale formats of p (int8 or float8_e4m3fn codes, fp32 or bf16
+// scales).
+template <class Tag>
+int launch_cs(const DequantParams& p, void* workspace, int64_t workspace_bytes, hipStream_t s) {
+  switch ((p.fp8 ? 2 : 0) | (p.s_bf16 ? 1 : 0)) {
+    case 0: return launch<Tag, 0>(p, workspace, workspace_bytes, s);
+    case 1: return launch<Tag, 1>(p, workspace, workspace_bytes, s);
+    case 2: return launch<Tag, 2>(p, workspace, workspace_bytes, s);
+    default: return launch<Tag, 3>(p, workspace, workspace_bytes, s);
+  }
 }
 
 int dequant_paged(void* key, void* value, int64_t key_stride_token, int64_t key_stride_head,
                   int64_t value_stride_token, int64_t value_stride_head, int64_t total_rows,
-                  const int8_t* key_cache, const int8_t* value_cache, const float* key_scale,
-                  const float* value_scale, const int32_t* context_lengths,
+                  const void* key_cache, const void* value_cache, const void* key_scale,
+                  const void* value_scale, const int32_t* context_lengths,
                   const int32_t* context_seq_offset, const int32_t* block_tables, int64_t batch,
                   int64_t max_blocks_per_seq, int64_t max_context_len, int64_t num_blocks,
                   int64_t num_heads, int64_t block_size, int64_t head_size, int quant_mode,
-                  int quant_bit, int out_dtype, void* workspace, int64_t workspace_bytes,
-                  void* stream);
+                  int quant_bit, int out_dtype, int cache_dtype, int scale_dtype,
+                  void* workspace, int64_t workspace_bytes, void* stream);
 
 }  // namespace
 }  // namespace tmo
@@ -603,18 +636,18 @@ int dequant_paged(void* key, void* value, int64_t key_stride_token, int64_t key_
 extern "C" int tmo_hip_dequant_from_paged_cache(
     void* key, void* value, int64_t key_stride_token, int64_t key_stride_head,
     int64_t value_stride_token, int64_t value_stride_head, int64_t total_rows,
-    const int8_t* key_cache, const int8_t* value_cache, const float* key_scale,
-    const float* value_scale, const int32_t* context_lengths, const int32_t* context_seq_offset,
+    const void* key_cache, const void* value_cache, const void* key_scale,
+    const void* value_scale, const int32_t* context_lengths, const int32_t* context_seq_offset,
     const int32_t* block_tables, int64_t batch, int64_t max_blocks_per_seq,
     int64_t max_context_len, int64_t num_blocks, int64_t num_heads, int64_t block_size,
-    int64_t head_size, int quant_mode, int quant_bit, int out_dtype, void* workspace,
-    int64_t workspace_bytes, void* stream) {
+    int64_t head_size, int quant_mode, int quant_bit, int out_dtype, int cache_dtype,
+    int scale_dtype, void* workspace, int64_t workspace_bytes, void* stream) {
   return tmo::dequant_paged(key, value, key_stride_token, key_stride_head, value_stride_token,
                             value_stride_head, total_rows, key_cache, value_cache, key_scale,
                             value_scale, context_lengths, context_seq_offset, block_tables, batch,
                             max_blocks_per_seq, max_context_len, num_blocks, num_heads,
-                            block_size, head_size, quant_mode, quant_bit, out_dtype, workspace,
-                            workspace_bytes, stream);
+                            block_size, head_size, quant_mode, quant_bit, out_dtype, cache_dtype,
+                            scale_dtype, workspace, workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------------- allocation-free entry
@@ -660,11 +693,12 @@ int scratch_of_current_device(void** out) {
 extern "C" int tmo_hip_dequant_from_paged_cache_noalloc(
     void* key, void* value, int64_t key_stride_token, int64_t key_stride_head,
     int64_t value_stride_token, int64_t value_stride_head, int64_t total_rows,
-    const int8_t* key_cache, const int8_t* value_cache, const float* key_scale,
-    const float* value_scale, const int32_t* context_lengths, const int32_t* context_seq_offset,
+    const void* key_cache, const void* value_cache, const void* key_scale,
+    const void* value_scale, const int32_t* context_lengths, const int32_t* context_seq_offset,
     const int32_t* block_tables, int64_t batch, int64_t max_blocks_per_seq,
     int64_t max_context_len, int64_t num_blocks, int64_t num_heads, int64_t block_size,
-    int64_t head_size, int quant_mode, int quant_bit, int out_dtype, void* stream) {
+    int64_t head_size, int quant_mode, int quant_bit, int out_dtype, int cache_dtype,
+    int scale_dtype, void* stream) {
   using namespace tmo;
   if (batch < 0 || max_blocks_per_seq < 0) return TMO_ERR_INVALID_ARGUMENT;
   if (batch > 0 && max_blocks_per_seq > (TMO_HIP_DEQUANT_SCRATCH_BYTES - kListHeader) /
@@ -682,7 +716,7 @@ extern "C" int tmo_hip_dequant_from_paged_cache_noalloc(
                        value_stride_head, total_rows, key_cache, value_cache, key_scale,
                        value_scale, context_lengths, context_seq_offset, block_tables, batch,
                        max_blocks_per_seq, max_context_len, num_blocks, num_heads, block_size,
-                       head_size, quant_mode, quant_bit, out_dtype, ws,
+                       head_size, quant_mode, quant_bit, out_dtype, cache_dtype, scale_dtype, ws,
                        need > 0 ? (int64_t)TMO_HIP_DEQUANT_SCRATCH_BYTES : 0, stream);
 }
 
@@ -691,16 +725,19 @@ namespace {
 
 int dequant_paged(void* key, void* value, int64_t key_stride_token, int64_t key_stride_head,
                   int64_t value_stride_token, int64_t value_stride_head, int64_t total_rows,
-                  const int8_t* key_cache, const int8_t* value_cache, const float* key_scale,
-                  const float* value_scale, const int32_t* context_lengths,
+                  const void* key_cache, const void* value_cache, const void* key_scale,
+                  const void* value_scale, const int32_t* context_lengths,
                   const int32_t* context_seq_offset, const int32_t* block_tables, int64_t batch,
                   int64_t max_blocks_per_seq, int64_t max_context_len, int64_t num_blocks,
                   int64_t num_heads, int64_t block_size, int64_t head_size, int quant_mode,
-                  int quant_bit, int out_dtype, void* workspace, int64_t workspace_bytes,
-                  void* stream) {
+                  int quant_bit, int out_dtype, int cache_dtype, int scale_dtype,
+                  void* workspace, int64_t workspace_bytes, void* stream) {
   if (workspace_bytes < 0 || (workspace_bytes > 0 && workspace == nullptr))
     return TMO_ERR_INVALID_ARGUMENT;
   if (out_dtype != TMO_DTYPE_F16 && out_dtype != TMO_DTYPE_BF16 && out_dtype != TMO_DTYPE_F32)
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if ((cache_dtype != TMO_DTYPE_I8 && cache_dtype != TMO_DTYPE_F8E4M3) ||
+      (scale_dtype != TMO_DTYPE_F32 && scale_dtype != TMO_DTYPE_BF16))
     return TMO_ERR_UNSUPPORTED_DTYPE;
   if (quant_bit != 8 || (quant_mode != 0 && quant_mode != 1)) return TMO_ERR_UNSUPPORTED_MODE;
   if (!key || !key_cache || !key_scale || !context_lengths || !block_tables)
@@ -730,8 +767,8 @@ int dequant_paged(void* key, void* value, int64_t key_stride_token, int64_t key_
   p.out_sh[0] = key_stride_head;
   p.out_sh[1] = value_stride_head;
   p.total_rows = total_rows;
-  p.cache[0] = key_cache;
-  p.cache[1] = value_cache;
+  p.cache[0] = static_cast<const int8_t*>(key_cache);
+  p.cache[1] = static_cast<const int8_t*>(value_cache);
   p.scale[0] = key_scale;
   p.scale[1] = value_scale;
   p.ctx_len = context_lengths;
@@ -746,11 +783,13 @@ int dequant_paged(void* key, void* value, int64_t key_stride_token, int64_t key_
   p.head_dim = (int32_t)head_size;
   p.mode = quant_mode;
   p.nkv = has_v ? 2 : 1;
+  p.fp8 = cache_dtype == TMO_DTYPE_F8E4M3;
+  p.s_bf16 = scale_dtype == TMO_DTYPE_BF16;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (out_dtype) {
-    case TMO_DTYPE_F16: return launch<F16>(p, workspace, workspace_bytes, s);
-    case TMO_DTYPE_BF16: return launch<BF16>(p, workspace, workspace_bytes, s);
-    default: return launch<F32>(p, workspace, workspace_bytes, s);
+    case TMO_DTYPE_F16: return launch_cs<F16>(p, workspace, workspace_bytes, s);
+    case TMO_DTYPE_BF16: return launch_cs<BF16>(p, workspace, workspace_bytes, s);
+    default: return launch_cs<F32>(p, workspace, workspace_bytes, s);
   }
 }
 

@@ -527,6 +527,42 @@ __device__ __forceinline__ uint8_t encode1_fp8(float v, float s) {
   return (uint8_t)fp8e4m3_bits(__builtin_amdgcn_fmed3f(v / s, -448.0f, 448.0f));  // IEEE divide
 }
 
+// ---------------------------------------------------------------------------- cache readers
+
+// float8_e4m3fn byte k (0..3) of a dword as fp32: gfx950's v_cvt_f32_fp8 decodes the OCP
+// e4m3fn format exactly (every e4m3fn value is an fp32, f16 and bf16 value);
+// tests/native/gfx950_builtins.hip ("fp8dec") checks all 256 codes in every byte position.
+__device__ __forceinline__ float fp8_value(uint32_t w, int k) {
+  switch (k) {
+    case 0: return __builtin_amdgcn_cvt_f32_fp8((int)w, 0);
+    case 1: return __builtin_amdgcn_cvt_f32_fp8((int)w, 1);
+    case 2: return __builtin_amdgcn_cvt_f32_fp8((int)w, 2);
+    default: return __builtin_amdgcn_cvt_f32_fp8((int)w, 3);
+  }
+}
+
+// Byte k of a dword of cache codes as fp32: an int8 code, or a float8_e4m3fn value.
+__device__ __forceinline__ float code_byte(uint32_t w, int k, bool fp8) {
+  return fp8 ? fp8_value(w, k) : (float)(int8_t)(w >> (8 * k));
+}
+
+// Scale element i of an fp32 or bf16 scale tensor (bf16 widens to fp32 exactly).
+__device__ __forceinline__ float scale_at(const void* s, int64_t i, int bf16) {
+  return bf16 ? __uint_as_float((uint32_t) static_cast<const uint16_t*>(s)[i] << 16)
+              : static_cast<const float*>(s)[i];
+}
+
+// Element e (0..7) of 8 consecutive scales held raw: fp32 in w[0], w[1] (4 each), or bf16 in
+// w[0] (8).
+template <bool kBf16>
+__device__ __forceinline__ float scale_of8(const u32x4 (&w)[2], int e) {
+  if constexpr (kBf16) {
+    const uint32_t x = w[0][e / 2];
+    return __uint_as_float((e & 1) ? (x & 0xffff0000u) : (x << 16));
+  }
+  return __uint_as_float(w[e / 4][e % 4]);
+}
+
 // ---------------------------------------------------------------------------- stores
 
 // Non-temporal 4- and 8-byte vector stores of int8 codes.  __builtin_nontemporal_store carries

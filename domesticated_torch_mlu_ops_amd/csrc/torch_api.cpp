@@ -400,14 +400,21 @@ void dequant_from_paged_cache(at::Tensor& key, const c10::optional<at::Tensor>& 
   TORCH_CHECK(dt == TMO_DTYPE_F16 || dt == TMO_DTYPE_BF16 || dt == TMO_DTYPE_F32,
               "dequant_from_paged_cache: key must be half, bfloat16 or float, got ",
               key.scalar_type());
-  TORCH_CHECK(key_cache.scalar_type() == at::kChar, "key_cache must be int8");
+  // int8 codes (the reference's type, _ops.py:3803-3804), or the float8_e4m3fn pages that
+  // quant_to_paged_cache / offline_quant_to_paged_cache write
+  const int cdt = dtype_code(key_cache.scalar_type());
+  TORCH_CHECK(cdt == TMO_DTYPE_I8 || cdt == TMO_DTYPE_F8E4M3,
+              "key_cache must be int8 or float8_e4m3fn, got ", key_cache.scalar_type());
   const int64_t NB = key_cache.size(0), H = key_cache.size(1), BS = key_cache.size(2),
                 D = key_cache.size(3);
   TORCH_CHECK(key.size(1) == H && key.size(2) == D, "key ", key.sizes(), " does not match key_cache ",
               key_cache.sizes());
+  // scales: float32 or bfloat16 (_ops.py:3805-3806), both tensors of one type
+  const at::ScalarType sdt = key_cache_quant_scale.scalar_type();
   auto check_scale = [&](const at::Tensor& s, const char* name) {
-    TORCH_CHECK(s.scalar_type() == at::kFloat && s.is_contiguous(), name,
-                " must be a contiguous float32 tensor");
+    TORCH_CHECK((s.scalar_type() == at::kFloat || s.scalar_type() == at::kBFloat16) &&
+                    s.scalar_type() == sdt && s.is_contiguous(),
+                name, " must be a contiguous float32 or bfloat16 tensor (K and V scales of one type)");
     if (quant_mode == 0) {
       TORCH_CHECK(s.dim() == 2 && s.size(0) == H && s.size(1) == D, name,
                   " must be [heads, head_size] for quant_mode 0, got ", s.sizes());
@@ -441,7 +448,8 @@ void dequant_from_paged_cache(at::Tensor& key, const c10::optional<at::Tensor>& 
     check_device(*value_cache_quant_scale, key, "value_cache_quant_scale");
     TORCH_CHECK(value->sizes() == key.sizes() && value->scalar_type() == key.scalar_type(),
                 "value must match key");
-    TORCH_CHECK(value_cache->sizes() == key_cache.sizes() && value_cache->scalar_type() == at::kChar,
+    TORCH_CHECK(value_cache->sizes() == key_cache.sizes() &&
+                    value_cache->scalar_type() == key_cache.scalar_type(),
                 "value_cache must match key_cache");
     check_scale(*value_cache_quant_scale, "value_cache_quant_scale");
   }
@@ -456,14 +464,14 @@ void dequant_from_paged_cache(at::Tensor& key, const c10::optional<at::Tensor>& 
   const int st = tmo_hip_dequant_from_paged_cache(
       key.data_ptr(), has_v ? value->data_ptr() : nullptr, key.stride(0), key.stride(1),
       has_v ? value->stride(0) : 0, has_v ? value->stride(1) : 0, key.size(0),
-      key_cache.data_ptr<int8_t>(), has_v ? value_cache->data_ptr<int8_t>() : nullptr,
-      key_cache_quant_scale.data_ptr<float>(),
-      has_v ? value_cache_quant_scale->data_ptr<float>() : nullptr,
+      key_cache.data_ptr(), has_v ? value_cache->data_ptr() : nullptr,
+      key_cache_quant_scale.data_ptr(), has_v ? value_cache_quant_scale->data_ptr() : nullptr,
       context_lengths.data_ptr<int32_t>(),
       context_seq_offset ? context_seq_offset->data_ptr<int32_t>() : nullptr,
       block_tables.data_ptr<int32_t>(), B, block_tables.size(1), max_ctx, NB, H, BS, D,
-      (int)quant_mode, (int)quant_bit, dt, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
-      stream_of(key));
+      (int)quant_mode, (int)quant_bit, dt, cdt,
+      sdt == at::kBFloat16 ? TMO_DTYPE_BF16 : TMO_DTYPE_F32,
+      ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(key));
   check_status(st, "dequant_from_paged_cache");
 }
 
@@ -1032,7 +1040,8 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
               op, ": compute_dtype must be float, half or bfloat16 (the softmax runs in fp32)");
   TORCH_CHECK(windows_size_right.expect_int() == -1, op, ": windows_size_right must be -1");
   TORCH_CHECK(kv_cache_quant_bit_size == -1 || kv_cache_quant_bit_size == 8, op,
-              ": kv_cache_quant_bit_size must be -1 or 8, got ", kv_cache_quant_bit_size);
+              ": kv_cache_quant_bit_size must be -1 or 8 (int8 / float8_e4m3fn), got ",
+              kv_cache_quant_bit_size);
   check_device(q_ori, q_ori, "q");
   // q forms (reference _ops.py:824): [batch, seq_q, heads, head_size] (seq_q tokens for every
   // sequence), [total_q, heads, head_size] with cu_seq_q [batch + 1], or [batch, heads,
@@ -1067,7 +1076,10 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
                 op, ": cu_seq_q must be a contiguous int32 [batch + 1] tensor, got ", c.sizes());
     cu = c.data_ptr<int32_t>();
     total_q = q.size(0);
-    // max_seq_q <= 0: unknown, read from cu_seq_q (one device-to-host copy)
+    // max_seq_q <= 0: unknown, read from cu_seq_q (one device-to-host copy).  A positive
+    // max_seq_q is trusted, as the reference trusts max_context_len ("if 0 < max_context_len <
+    // max(context_lens), the correctness is not guaranteed", _ops.py:847): query tokens of a
+    // sequence at or past it are not computed and their output rows are left as they were.
     seq_q = max_seq_q.expect_int();
     if (seq_q <= 0)
       seq_q = B == 0 ? 0 : std::max<int64_t>(0, (c.slice(0, 1) - c.slice(0, 0, B)).max().item<int64_t>());
@@ -1117,9 +1129,12 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
               " must be a multiple of the KV heads ", Hkv);
   TORCH_CHECK(D <= 4096 && Dv <= 512, op, ": head sizes up to 4096 (keys) and 512 (values)");
   const int cdt = dtype_code(k_cache.scalar_type());
-  const bool int8 = cdt == TMO_DTYPE_I8;
+  // quantised caches: int8 codes or float8_e4m3fn values (_ops.py:868; bit size 8 covers both,
+  // _ops.py:1061), with per-token / per-channel / per-group scales
+  const bool int8 = cdt == TMO_DTYPE_I8 || cdt == TMO_DTYPE_F8E4M3;
   TORCH_CHECK(int8 == (kv_cache_quant_bit_size == 8), op,
-              ": kv_cache_quant_bit_size 8 goes with int8 caches, -1 with caches of q's dtype");
+              ": kv_cache_quant_bit_size 8 goes with int8 or float8_e4m3fn caches, -1 with caches ",
+              "of q's dtype");
   TORCH_CHECK(int8 || cdt == qdt, op, ": unquantised caches must have q's dtype");
   // scales: per token [NB, Hkv, BS] (or [..., 1]; any strides in the first two dims), per
   // channel [Hkv, D] / [Hkv, Dv], per tensor [1], per group K [NB, Hkv, BS, D / 32] with
@@ -1134,8 +1149,10 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
     const at::Tensor& vsc = *v_cache_quant_scale;
     check_device(ksc, q_ori, "k_cache_quant_scale");
     check_device(vsc, q_ori, "v_cache_quant_scale");
-    TORCH_CHECK(ksc.scalar_type() == at::kFloat && vsc.scalar_type() == at::kFloat, op,
-                ": cache scales must be float32");
+    // float32 or bfloat16 (_ops.py:872), both of one type
+    TORCH_CHECK((ksc.scalar_type() == at::kFloat || ksc.scalar_type() == at::kBFloat16) &&
+                    vsc.scalar_type() == ksc.scalar_type(),
+                op, ": cache scales must be float32 or bfloat16 (K and V of one type)");
     const bool group = ksc.dim() == 4 && vsc.dim() == 4 && D % 32 == 0 && BS % 32 == 0 &&
                        ksc.sizes() == at::IntArrayRef({NB, Hkv, BS, D / 32}) &&
                        vsc.sizes() == at::IntArrayRef({NB, Hkv, BS / 32, Dv});
@@ -1244,7 +1261,8 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   const int st = tmo_hip_cached_kv_attn(
       q.data_ptr(), q_sb, q_ss, q.stride(-2), cu, seq_q, total_q, k_cache.data_ptr(),
       v_cache.has_value() ? v_cache->data_ptr() : nullptr, kdim, vdim,
-      int8 ? ks.data_ptr<float>() : nullptr, int8 ? vs.data_ptr<float>() : nullptr, smode,
+      int8 ? ks.data_ptr() : nullptr, int8 ? vs.data_ptr() : nullptr, smode,
+      int8 && ks.scalar_type() == at::kBFloat16 ? TMO_DTYPE_BF16 : TMO_DTYPE_F32,
       ks_sb, ks_sh, vs_sb, vs_sh, block_tables.data_ptr<int32_t>(), block_tables.size(1),
       context_lens.data_ptr<int32_t>(), alibi, sink_p, out.data_ptr(), o_sb, o_ss,
       out.stride(-2), lse, lse_sb, lse_ss, lse_sh, B, Hq, Hkv, D, Dv, NB, BS, max_ctx, window,

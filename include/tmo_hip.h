@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 14
+#define TMO_HIP_ABI_VERSION 15
 
 /* element types */
 enum tmo_dtype {
@@ -196,6 +196,10 @@ int tmo_hip_fused_rope_linear(void* qkv, int64_t num_tokens, int64_t seq_len,
  * Replaces tmo::torch_api::dequant_from_paged_cache (reference include/torch_mlu_ops.h:650-661),
  * called by torch_mlu_ops.dequant_from_paged_cache (reference _ops.py:3734-3824).
  * out_dtype: F16, BF16 (or F32).  value, value_cache, value_scale: all NULL or all set.
+ * cache_dtype: TMO_DTYPE_I8 (int8 codes, the reference's type, _ops.py:3803-3804) or
+ * TMO_DTYPE_F8E4M3 (float8_e4m3fn values, as quant_to_paged_cache writes them; an extension:
+ * out = RNE_out(fp32(e4m3 value) * scale)).  scale_dtype: TMO_DTYPE_F32 or TMO_DTYPE_BF16
+ * (_ops.py:3805-3806; a bf16 scale widens to fp32 exactly, so the product is the same).
  * `workspace`: NULL (workspace_bytes 0), or device memory of at least
  * tmo_hip_dequant_workspace_bytes(...) bytes, 16-byte aligned, used by this call only (calls
  * that share one workspace must be ordered on a stream).  With it the call runs as a small
@@ -206,8 +210,8 @@ int tmo_hip_dequant_from_paged_cache(void* key, void* value,
                                      int64_t key_stride_token, int64_t key_stride_head,
                                      int64_t value_stride_token, int64_t value_stride_head,
                                      int64_t total_rows,
-                                     const int8_t* key_cache, const int8_t* value_cache,
-                                     const float* key_scale, const float* value_scale,
+                                     const void* key_cache, const void* value_cache,
+                                     const void* key_scale, const void* value_scale,
                                      const int32_t* context_lengths,
                                      const int32_t* context_seq_offset,
                                      const int32_t* block_tables,
@@ -216,6 +220,7 @@ int tmo_hip_dequant_from_paged_cache(void* key, void* value,
                                      int64_t num_blocks, int64_t num_heads,
                                      int64_t block_size, int64_t head_size,
                                      int quant_mode, int quant_bit, int out_dtype,
+                                     int cache_dtype, int scale_dtype,
                                      void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes for tmo_hip_dequant_from_paged_cache's page-list path: 16 + 16 per page the
@@ -244,8 +249,8 @@ int tmo_hip_dequant_from_paged_cache_noalloc(void* key, void* value,
                                              int64_t key_stride_token, int64_t key_stride_head,
                                              int64_t value_stride_token, int64_t value_stride_head,
                                              int64_t total_rows,
-                                             const int8_t* key_cache, const int8_t* value_cache,
-                                             const float* key_scale, const float* value_scale,
+                                             const void* key_cache, const void* value_cache,
+                                             const void* key_scale, const void* value_scale,
                                              const int32_t* context_lengths,
                                              const int32_t* context_seq_offset,
                                              const int32_t* block_tables,
@@ -254,7 +259,7 @@ int tmo_hip_dequant_from_paged_cache_noalloc(void* key, void* value,
                                              int64_t num_blocks, int64_t num_heads,
                                              int64_t block_size, int64_t head_size,
                                              int quant_mode, int quant_bit, int out_dtype,
-                                             void* stream);
+                                             int cache_dtype, int scale_dtype, void* stream);
 
 /*
  * scaled_quantize_per_token -- "dynamic_per_token" int8 quantisation with an optional smooth
@@ -441,8 +446,11 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
  * with their own strides.
  * Caches [num_blocks, Hkv, block_size, k_cache_dim / v_cache_dim] contiguous: k_j is the first
  * head_size channels of its K row, v_j the first head_size_v of its V row -- of its K row when
- * v_cache is null (K and V in one cache, reference _ops.py:828-831; v_cache_dim unused).  Int8
- * caches (cache_dtype TMO_DTYPE_I8) hold k = code * scale, fp32 scales by scale_mode:
+ * v_cache is null (K and V in one cache, reference _ops.py:828-831; v_cache_dim unused).
+ * Quantised caches -- int8 codes (cache_dtype TMO_DTYPE_I8) or float8_e4m3fn values
+ * (TMO_DTYPE_F8E4M3; _ops.py:868, kv_cache_quant_bit_size 8 "int8/float8_e4m3fn") -- hold
+ * k = code * scale, with fp32 or bf16 scales (scale_dtype TMO_DTYPE_F32 / TMO_DTYPE_BF16,
+ * _ops.py:872; ignored for other caches) by scale_mode:
  *   1 per token: [num_blocks, Hkv, block_size] with element strides (scale_stride_block,
  *     scale_stride_head, 1) -- any strides in the first two dims (_ops.py:838);
  *   2 per channel: [Hkv, head_size] (K) and [Hkv, head_size_v] (V), contiguous;
@@ -453,8 +461,9 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
  * logits.  Head sizes: head_size up to 4096, head_size_v up to 512; the MFMA kernels take K and
  * V head sizes and cache rows all equal to 64, 128 or 256 with per-token or per-channel
  * scales, a VALU kernel the rest.
- * Arithmetic: fp32 accumulation (MFMA with bf16/f16 operands: int8 codes are exact; q and the
- * probabilities are split into two operands when one is not exact), softmax in fp32.
+ * Arithmetic: fp32 accumulation (MFMA with bf16/f16 operands: int8 codes and e4m3fn values are
+ * exact; q and the probabilities are split into two operands when one is not exact), softmax
+ * in fp32.
  * splits > 1 divides each sequence's keys over that many workgroups per KV head; it needs
  * `workspace` of at least tmo_hip_cached_kv_attn_workspace_bytes(...) bytes (device memory).
  * max_context_len <= 0 (negative included) means an unknown maximum: one split per sequence
@@ -467,8 +476,9 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
 int tmo_hip_cached_kv_attn(const void* q, int64_t q_stride_batch, int64_t q_stride_token,
                            int64_t q_stride_head, const int32_t* cu_seq_q, int64_t seq_q,
                            int64_t total_q, const void* k_cache, const void* v_cache,
-                           int64_t k_cache_dim, int64_t v_cache_dim, const float* k_scale,
-                           const float* v_scale, int scale_mode, int64_t k_scale_stride_block,
+                           int64_t k_cache_dim, int64_t v_cache_dim, const void* k_scale,
+                           const void* v_scale, int scale_mode, int scale_dtype,
+                           int64_t k_scale_stride_block,
                            int64_t k_scale_stride_head, int64_t v_scale_stride_block,
                            int64_t v_scale_stride_head, const int32_t* block_tables,
                            int64_t max_blocks, const int32_t* context_lens,
@@ -491,7 +501,7 @@ int64_t tmo_hip_cached_kv_attn_workspace_bytes(int64_t batch, int64_t num_kv_hea
 /*
  * single_query_cached_kv_attn -- tmo_hip_cached_kv_attn with one query token per sequence
  * (seq_q 1, no cu_seq_q, no sink), separate K and V caches [num_blocks, Hkv, block_size,
- * head_size], scale_mode 1 (contiguous per-token scales) or 2: q / out [batch, Hq, head_size]
+ * head_size], fp32 scales, scale_mode 1 (contiguous per-token scales) or 2: q / out [batch, Hq, head_size]
  * rows with the given strides, lse (nullable) at i * lse_stride_seq + hq * lse_stride_head;
  * head_size up to 512.  Replaces the same reference interface for the decode step (reference
  * include/torch_mlu_ops.h:107-130, _ops.py:777-900).

@@ -46,7 +46,7 @@ def lib() -> ctypes.CDLL:
             [c_void_p] * 5 + [c_int64] * 5 + [c_int, c_int]
         L.oracle_reshape_paged_cache.argtypes = [c_void_p, c_void_p, c_int] + [c_int64] * 4 + \
             [c_void_p] * 3 + [c_int64] * 5 + [c_int, c_int]
-        L.oracle_dequant_from_paged_cache.argtypes = [c_void_p, c_void_p, c_int] + [c_int64] * 5 + \
+        L.oracle_dequant_from_paged_cache.argtypes = [c_void_p, c_void_p, c_int, c_int] + [c_int64] * 5 + \
             [c_void_p] * 7 + [c_int64] * 6 + [c_int, c_int]
         L.oracle_scaled_quantize_per_token.argtypes = [c_void_p, c_int] + [c_int64] * 4 + \
             [c_void_p] * 3 + [c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
@@ -78,7 +78,7 @@ def lib() -> ctypes.CDLL:
              c_double, c_void_p, c_void_p, c_int]
         L.oracle_cached_kv_attn.restype = c_int
         for name in ("oracle_f32_to_bf16", "oracle_f32_to_f16", "oracle_f16_to_f32",
-                     "oracle_f32_to_e4m3"):
+                     "oracle_f32_to_e4m3", "oracle_e4m3_to_f32"):
             getattr(L, name).argtypes = [c_void_p, c_void_p, c_int64]
         for name in ("oracle_quant_to_paged_cache", "oracle_reshape_paged_cache",
                      "oracle_dequant_from_paged_cache", "oracle_scaled_quantize_per_token",
@@ -205,6 +205,14 @@ def fused_rope_linear(qkv, k_cache, v_cache, sin_cache, cos_cache, position_id, 
                      v_scale, slot, eps, q_gamma, rope_dim_offset, nthreads, norm_type, k_beta)
 
 
+def e4m3_to_f32(bits: torch.Tensor) -> torch.Tensor:
+    """The values (fp32) of float8_e4m3fn bit patterns (uint8); S.1111.111 is NaN."""
+    bits = bits.to(torch.uint8).contiguous()
+    out = torch.empty(bits.shape, dtype=torch.float32)
+    lib().oracle_e4m3_to_f32(_ptr(bits), _ptr(out), bits.numel())
+    return out
+
+
 def f32_to_e4m3(x: torch.Tensor) -> torch.Tensor:
     """float8_e4m3fn bit patterns (uint8) of fp32 values |x| <= 448, round to nearest even."""
     x = x.to(torch.float32).contiguous()
@@ -214,6 +222,7 @@ def f32_to_e4m3(x: torch.Tensor) -> torch.Tensor:
 
 
 _CACHE_DT = {torch.int8: 3, torch.float8_e4m3fn: 4}
+_ATTN_CACHE_DT = {**_DT, torch.float8_e4m3fn: 4}
 
 
 def _rows_view(t: Optional[torch.Tensor]):
@@ -271,8 +280,9 @@ def single_query_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_s
                       k_scale=None, v_scale=None, alibi_slopes=None, window_left: int = -1,
                       nthreads: Optional[int] = None):
     """reference _ops.py:777-900 for one query token per sequence (decision D12 of
-    tmo_oracle.c), in float64.  q [B, Hq, D] or [B, 1, Hq, D]; caches [NB, Hkv, BS, D] (int8
-    with k_scale/v_scale [NB, Hkv, BS] per token or [Hkv, D] per channel, or float);
+    tmo_oracle.c), in float64.  q [B, Hq, D] or [B, 1, Hq, D]; caches [NB, Hkv, BS, D] (int8 or
+    float8_e4m3fn with k_scale/v_scale [NB, Hkv, BS] per token or [Hkv, D] per channel, fp32
+    or bf16, or float);
     block_tables [B, max_blocks]; returns (out [B, Hq, D] float64, lse [B, Hq] float64)."""
     if q.dim() == 4:
         assert q.shape[1] == 1
@@ -280,10 +290,10 @@ def single_query_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_s
     assert q.stride(-1) == 1 and k_cache.is_contiguous() and v_cache.is_contiguous()
     B, Hq, D = q.shape
     NB, Hkv, BS, _ = k_cache.shape
-    cdt = _DT[k_cache.dtype]
+    cdt = _ATTN_CACHE_DT[k_cache.dtype]
     mode = 0
     ks = vs = None
-    if k_cache.dtype == torch.int8:
+    if k_cache.dtype in (torch.int8, torch.float8_e4m3fn):
         ks = k_scale.to(torch.float32).contiguous()
         vs = v_scale.to(torch.float32).contiguous()
         mode = 2 if ks.dim() == 2 else 1
@@ -329,11 +339,11 @@ def cached_kv_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scal
     NB, Hkv, BS, krow = k_cache.shape
     vrow = vc.shape[3]
     Dv = head_size_v if head_size_v is not None else (vrow if v_cache is not None else D)
-    cdt = _DT[k_cache.dtype]
+    cdt = _ATTN_CACHE_DT[k_cache.dtype]
     mode = 0
     ks = vs = None
     strides = [0, 0, 0, 0]
-    if k_cache.dtype == torch.int8:
+    if k_cache.dtype in (torch.int8, torch.float8_e4m3fn):
         def one(sc):
             sc = sc.to(torch.float32)
             if sc.dim() == 4 and sc.shape[3] == 1:
@@ -382,7 +392,8 @@ def reshape_paged_cache(k, v, k_cache, v_cache, slot_mapping, direction: bool = 
 def dequant_from_paged_cache(key, value, key_cache, value_cache, key_scale, value_scale,
                              context_lengths, context_seq_offset, block_tables,
                              quant_mode: int, nthreads: Optional[int] = None) -> None:
-    """reference _ops.py:3734-3824 (quant_mode 0/1, 8-bit); in place on CPU tensors."""
+    """reference _ops.py:3734-3824 (quant_mode 0/1, 8-bit); in place on CPU tensors.  Caches
+    int8 or float8_e4m3fn; scales fp32 or bf16 (widened to fp32, exactly)."""
     assert key.stride(2) == 1 and key_cache.is_contiguous() and block_tables.is_contiguous()
     NB, H, BS, D = key_cache.shape
     B, MB = block_tables.shape
@@ -390,8 +401,11 @@ def dequant_from_paged_cache(key, value, key_cache, value_cache, key_scale, valu
     cso = context_seq_offset.to(torch.int32).contiguous() if context_seq_offset is not None else None
     ctx = context_lengths.to(torch.int32).contiguous()
     bt = block_tables.to(torch.int32).contiguous()
+    key_scale = key_scale.to(torch.float32).contiguous()
+    value_scale = value_scale.to(torch.float32).contiguous() if value_scale is not None else None
     rc = lib().oracle_dequant_from_paged_cache(
-        _ptr(key), _ptr(value), _DT[key.dtype], key.stride(0), key.stride(1),
+        _ptr(key), _ptr(value), _DT[key.dtype], _CACHE_DT[key_cache.dtype], key.stride(0),
+        key.stride(1),
         value.stride(0) if value is not None else 0, value.stride(1) if value is not None else 0,
         key.shape[0], _ptr(key_cache), _ptr(value_cache), _ptr(key_scale), _ptr(value_scale),
         _ptr(ctx), _ptr(cso), _ptr(bt), B, MB, NB, H, BS, D, int(quant_mode),

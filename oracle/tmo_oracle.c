@@ -61,7 +61,7 @@
  *       int8 as D1-D3, fp8 e4m3fn with scale = RN(amax / 448), codes e4m3fn_RNE(clip(RN(x /
  *       scale), -448, 448)) and an all-zero group giving scale 0 and codes 0 (_ops.py:1728-1745).
  *   D12 single_query_cached_kv_attn (_ops.py:777-900): the docstring math in double with
- *       k = code * scale exact.  A sequence's nq query tokens (q [batch, seq_q, ...] or rows
+ *       k = code * scale exact (code: an int8, or a float8_e4m3fn value, _ops.py:868).  A sequence's nq query tokens (q [batch, seq_q, ...] or rows
  *       cu_seq_q[i] .. cu_seq_q[i+1] - 1 of a [total_q, ...] q, _ops.py:824, 860-861) are its
  *       last nq positions: token s sits at position P = L - nq + s and sees keys j <= P
  *       (causal within the new tokens; one token: P = L - 1), and with a left window keys
@@ -259,6 +259,30 @@ static uint8_t f32_to_e4m3(float f) {
 
 void oracle_f32_to_e4m3(const float* in, uint8_t* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = f32_to_e4m3(in[i]);
+}
+
+/*
+ * float8_e4m3fn -> its value (the reader of the pages the fp8 branch writes): sign, exponent
+ * field e (bias 7) and fraction m; e = 0 is subnormal, m * 2^-9; otherwise (8 + m) * 2^(e-10);
+ * S.1111.111 is NaN (the format has no infinities).
+ */
+static double e4m3_to_f64(uint8_t b) {
+    const int e = (b >> 3) & 15, m = b & 7;
+    double v;
+    if (e == 15 && m == 7) v = NAN;
+    else if (e == 0) v = ldexp((double)m, -9);
+    else v = ldexp((double)(8 + m), e - 10);
+    return (b & 0x80) ? -v : v;
+}
+
+void oracle_e4m3_to_f32(const uint8_t* in, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = (float)e4m3_to_f64(in[i]);
+}
+
+/* Code byte of a quantised cache as a number: int8, or a float8_e4m3fn value. */
+static inline double cache_code(const void* base, int64_t idx, int cache_dtype) {
+    if (cache_dtype == DT_F8E4M3) return e4m3_to_f64(((const uint8_t*)base)[idx]);
+    return (double)((const int8_t*)base)[idx];
 }
 
 /* ------------------------------------------------------------------ row quantiser */
@@ -933,6 +957,7 @@ typedef struct {
     const int8_t* cache[2];
     const float* scale[2];
     int nkv;
+    int cache_dtype;          /* DT_I8 or DT_F8E4M3 */
     const int32_t* ctx_len;
     const int64_t* seq_off;
     const int32_t* bt;
@@ -954,12 +979,14 @@ static void dpc_range(void* p, int64_t lo, int64_t hi) {
             if (row < 0 || row >= c->total) continue;
             for (int kv = 0; kv < c->nkv; ++kv) {
                 for (int64_t h = 0; h < c->H; ++h) {
-                    const int8_t* codes = c->cache[kv] + ((blk * c->H + h) * c->BS + o) * c->D;
+                    const int64_t cbase = ((blk * c->H + h) * c->BS + o) * c->D;
                     int64_t obase = row * c->st[kv] + h * c->sh[kv];
                     for (int64_t d = 0; d < c->D; ++d) {
                         float s = c->mode == 0 ? c->scale[kv][h * c->D + d]          /* [H, D] */
                                                : c->scale[kv][(blk * c->H + h) * c->BS + o];
-                        store_elem(c->out[kv], obase + d, c->dtype, (float)codes[d] * s);  /* D6 */
+                        /* D6: the code (an int8, or an e4m3fn value) is exact in fp32 */
+                        const float code = (float)cache_code(c->cache[kv], cbase + d, c->cache_dtype);
+                        store_elem(c->out[kv], obase + d, c->dtype, code * s);
                     }
                 }
             }
@@ -970,16 +997,20 @@ static void dpc_range(void* p, int64_t lo, int64_t hi) {
 /* _ops.py:3734-3824: dequant_from_paged_cache(key, value, key_cache, value_cache, key_scale,
  * value_scale, context_lengths, max_context_len, context_seq_offset, block_tables, quant_mode,
  * quant_bit).  quant_mode 0: scale [H, D]; 1: scale [NB, H, BS] (_ops.py:3765-3771).
- * context_seq_offset NULL -> exclusive cumsum of context_lengths (_ops.py:3758). */
-int oracle_dequant_from_paged_cache(void* key, void* value, int out_dtype,
+ * context_seq_offset NULL -> exclusive cumsum of context_lengths (_ops.py:3758).  Caches of
+ * int8 codes (DT_I8, the reference's type) or float8_e4m3fn values (DT_F8E4M3, the pages the
+ * fp8 branch of quant_to_paged_cache writes).  fp32 scales (a bf16 scale tensor widens to
+ * fp32 exactly, so callers pass it widened). */
+int oracle_dequant_from_paged_cache(void* key, void* value, int out_dtype, int cache_dtype,
                                     int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh,
-                                    int64_t total_rows, const int8_t* key_cache,
-                                    const int8_t* value_cache, const float* key_scale,
+                                    int64_t total_rows, const void* key_cache,
+                                    const void* value_cache, const float* key_scale,
                                     const float* value_scale, const int32_t* context_lengths,
                                     const int32_t* context_seq_offset, const int32_t* block_tables,
                                     int64_t B, int64_t max_blocks, int64_t NB, int64_t H,
                                     int64_t BS, int64_t D, int quant_mode, int nthreads) {
     if (out_dtype != DT_F16 && out_dtype != DT_BF16 && out_dtype != DT_F32) return -2;
+    if (cache_dtype != DT_I8 && cache_dtype != DT_F8E4M3) return -2;
     if (quant_mode != 0 && quant_mode != 1) return -3;
     if (B < 0 || H <= 0 || D <= 0 || BS <= 0 || max_blocks < 0) return -1;
     int64_t* off = (int64_t*)malloc((size_t)(B > 0 ? B : 1) * sizeof(int64_t));
@@ -988,8 +1019,10 @@ int oracle_dequant_from_paged_cache(void* key, void* value, int out_dtype,
         off[i] = context_seq_offset ? (int64_t)context_seq_offset[i] : acc;
         acc += context_lengths[i];
     }
-    dpc_ctx c = {{key, value}, {k_st, v_st}, {k_sh, v_sh}, {key_cache, value_cache},
-                 {key_scale, value_scale}, (value && value_cache) ? 2 : 1, context_lengths, off,
+    dpc_ctx c = {{key, value}, {k_st, v_st}, {k_sh, v_sh},
+                 {(const int8_t*)key_cache, (const int8_t*)value_cache},
+                 {key_scale, value_scale}, (value && value_cache) ? 2 : 1, cache_dtype,
+                 context_lengths, off,
                  block_tables, B, max_blocks, NB, H, BS, D, total_rows, quant_mode, out_dtype};
     parallel_for(B, nthreads, dpc_range, &c);
     free(off);
@@ -1098,8 +1131,8 @@ typedef struct {
 /* Key channel d (< D) of row `row` of page blk, KV head hk: the first D of the row's krow. */
 static double key_val(const sqa_ctx* c, int64_t blk, int64_t hk, int64_t row, int64_t d) {
     const int64_t r = (blk * c->Hkv + hk) * c->BS + row;
-    if (c->c_dtype == DT_I8) {
-        double code = (double)((const int8_t*)c->kc)[r * c->krow + d];
+    if (c->c_dtype == DT_I8 || c->c_dtype == DT_F8E4M3) {
+        double code = cache_code(c->kc, r * c->krow + d, c->c_dtype);
         if (c->smode == 1) return code * (double)c->ks[blk * c->ks_sb + hk * c->ks_sh + row];
         if (c->smode == 2) return code * (double)c->ks[hk * c->D + d];
         if (c->smode == 3) return code * (double)c->ks[r * (c->D / 32) + d / 32];
@@ -1111,8 +1144,8 @@ static double key_val(const sqa_ctx* c, int64_t blk, int64_t hk, int64_t row, in
 /* Value channel d (< Dv): per-group V scales hold one number per 32 rows of a page and channel. */
 static double value_val(const sqa_ctx* c, int64_t blk, int64_t hk, int64_t row, int64_t d) {
     const int64_t r = (blk * c->Hkv + hk) * c->BS + row;
-    if (c->c_dtype == DT_I8) {
-        double code = (double)((const int8_t*)c->vc)[r * c->vrow + d];
+    if (c->c_dtype == DT_I8 || c->c_dtype == DT_F8E4M3) {
+        double code = cache_code(c->vc, r * c->vrow + d, c->c_dtype);
         if (c->smode == 1) return code * (double)c->vs[blk * c->vs_sb + hk * c->vs_sh + row];
         if (c->smode == 2) return code * (double)c->vs[hk * c->Dv + d];
         if (c->smode == 3)
@@ -1189,7 +1222,8 @@ static void sqa_range(void* p, int64_t lo, int64_t hi) {
  * query tokens) over keys j in [max(0, P - window_left), min(P, L - 1)] (all of [0, P] when
  * window_left < 0), key j at row j % BS of page block_tables[i, j / BS]: its first D channels
  * are k_j, the first Dv of the V cache's row (or of the same K row, _ops.py:828-831, when the
- * caller passes the K cache as V) v_j.  Int8 caches hold code * scale exactly, scale_mode 1:
+ * caller passes the K cache as V) v_j.  Int8 caches (and float8_e4m3fn caches, _ops.py:868,
+ * their code the e4m3fn value) hold code * scale exactly, scale_mode 1:
  * per token, [NB, Hkv, BS] at blk * s_sb + hk * s_sh + row; 2: per channel [Hkv, D] / [Hkv,
  * Dv]; 3: per group (_ops.py:841-842), K [NB, Hkv, BS, D / 32] (one per token and 32
  * channels), V [NB, Hkv, BS / 32, Dv] (one per 32 rows of a page and channel); other caches
@@ -1208,16 +1242,18 @@ int oracle_cached_kv_attn(const void* q, int q_dtype, int64_t q_st, int64_t q_sh
                           const int32_t* context_lens, int64_t B, int64_t Hq,
                           const float* alibi, const float* sink, int64_t window_left,
                           double softmax_scale, double* out, double* lse, int nthreads) {
-    if (elem_size(q_dtype) == 0 || q_dtype == DT_I8 || elem_size(cache_dtype) == 0) return -2;
-    if (cache_dtype == DT_I8 && (scale_mode < 1 || scale_mode > 3)) return -3;
+    const int quant = cache_dtype == DT_I8 || cache_dtype == DT_F8E4M3;
+    if (elem_size(q_dtype) == 0 || q_dtype == DT_I8 || (!quant && elem_size(cache_dtype) == 0))
+        return -2;
+    if (quant && (scale_mode < 1 || scale_mode > 3)) return -3;
     if (B < 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || BS <= 0 || D <= 0 || Dv <= 0 ||
         k_row < D || v_row < Dv || max_blocks < 0 || T < 0 ||
         (!cu_seq_q && (S <= 0 || T != B * S)))
         return -1;
-    if (cache_dtype == DT_I8 && scale_mode == 3 && (D % 32 != 0 || BS % 32 != 0)) return -1;
+    if (quant && scale_mode == 3 && (D % 32 != 0 || BS % 32 != 0)) return -1;
     sqa_ctx c = {q, q_dtype, q_st, q_sh, cu_seq_q, S, T, k_cache, v_cache, cache_dtype, NB, Hkv,
                  BS, D, Dv, k_row, v_row, Hq, max_blocks, B, k_scale, v_scale,
-                 cache_dtype == DT_I8 ? scale_mode : 0, ks_sb, ks_sh, vs_sb, vs_sh,
+                 quant ? scale_mode : 0, ks_sb, ks_sh, vs_sb, vs_sh,
                  block_tables, context_lens, alibi, sink, window_left, softmax_scale, out, lse};
     parallel_for(T * Hq, nthreads, sqa_range, &c);
     return 0;

@@ -20,6 +20,11 @@
 //        v_cvt_f32_f64 with y64 = recip64(s)) against the IEEE quotient x / s for every bf16
 //        and every fp16 pair 0 <= x <= amax with s = amax / 127 on the fast path: the int8
 //        codes always, the quotient bits wherever the IEEE quotient is normal or 0.
+//   fp8dec: the float8_e4m3fn readers of the attention and dequant kernels -- fp8_value
+//        (v_cvt_f32_fp8, byte k of a dword) and the two-code v_cvt_pk_f32_fp8 +
+//        v_cvt_pkrtz_f16_f32 path to f16 operands -- equal the closed-form value
+//        (-1)^s (8 + m) 2^(e - 10) (m 2^-9 for e = 0) for every non-NaN code in every byte
+//        position (and NaN codes decode to NaN).
 //   sqrt: __builtin_sqrtf (the fused rope's rms) is correctly rounded for every positive
 //        finite fp32 x: with m- and m+ the midpoints between r = sqrtf(x) and its neighbours,
 //        m-^2 < x < m+^2 (25-bit midpoints square exactly in fp64; no x sits on a midpoint);
@@ -63,6 +68,44 @@ __global__ void check_fp8(uint32_t hi, unsigned long long* bad) {
       for (int j = 0; j < 4; ++j)
         if (((hw >> (8 * j)) & 0xffu) != tmo::fp8e4m3_bits(f[j])) ++b;
     }
+  }
+  if (b) atomicAdd(bad, b);
+}
+
+// The e4m3fn value of code c by the closed form (a power-of-two scaling of an integer: exact).
+__device__ float e4m3_closed_form(uint32_t c) {
+  const int e = (c >> 3) & 15, m = c & 7;
+  const float v = e == 0 ? __builtin_ldexpf((float)m, -9) : __builtin_ldexpf((float)(8 + m), e - 10);
+  return (c & 0x80u) ? -v : v;
+}
+
+// Thread t: code c = t % 256 in byte position k = (t / 256) % 4 of a dword whose other bytes
+// are other codes; checks fp8_value and the f16 operand path for the whole dword.
+__global__ __launch_bounds__(256) void check_fp8dec(unsigned long long* bad) {
+  const uint32_t t = blockIdx.x * 256 + threadIdx.x;  // 1024 threads
+  const uint32_t c = t & 255u, k = (t >> 8) & 3u;
+  uint32_t w = 0;
+  for (uint32_t j = 0; j < 4; ++j) w |= ((j == k ? c : (c * 37u + 11u * j + 5u) & 255u) << (8 * j));
+  unsigned long long b = 0;
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  const uint32_t h0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo[0], lo[1]));
+  const uint32_t h1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(hi[0], hi[1]));
+  for (uint32_t j = 0; j < 4; ++j) {
+    const uint32_t cj = (w >> (8 * j)) & 255u;
+    const float got = tmo::fp8_value(w, (int)j);
+    const float pk = j < 2 ? lo[j] : hi[j - 2];
+    const uint32_t hb = ((j < 2 ? h0 : h1) >> (16 * (j & 1))) & 0xffffu;
+    const float f16v = (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+    if ((cj & 0x7fu) == 0x7fu) {
+      if (!__builtin_isnan(got) || !__builtin_isnan(pk)) ++b;
+      continue;
+    }
+    const float want = e4m3_closed_form(cj);
+    if (__float_as_uint(got) != __float_as_uint(want)) ++b;
+    if (__float_as_uint(pk) != __float_as_uint(want)) ++b;
+    if (__float_as_uint(f16v) != __float_as_uint(want)) ++b;
   }
   if (b) atomicAdd(bad, b);
 }
@@ -257,6 +300,9 @@ int main(int argc, char** argv) {
     std::memcpy(&hi, &fhi, 4);
     checked = 2ull * ((unsigned long long)(hi / 4) + 1) * 4;
     check_fp8<<<dim3(8192), dim3(256)>>>(hi, d_bad);
+  } else if (!std::strcmp(mode, "fp8dec")) {
+    checked = 1024ull * 4;
+    check_fp8dec<<<dim3(4), dim3(256)>>>(d_bad);
   } else if (!std::strcmp(mode, "mfma")) {
     const unsigned long long b = run_mfma(checked);
     if (b == ~0ull) {

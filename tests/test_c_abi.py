@@ -35,7 +35,7 @@ def lib():
     L.tmo_hip_quant_to_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 5 + [I64] * 5 + [INT, INT, P]
     L.tmo_hip_reshape_paged_cache.argtypes = [P, P] + [I64] * 4 + [P] * 3 + [I64] * 5 + [INT, INT, P]
     L.tmo_hip_dequant_from_paged_cache.argtypes = [P, P] + [I64] * 5 + [P] * 7 + [I64] * 7 + \
-        [INT, INT, INT, P, I64, P]
+        [INT] * 5 + [P, I64, P]
     L.tmo_hip_dequant_workspace_bytes.argtypes = [I64] * 4
     L.tmo_hip_dequant_workspace_bytes.restype = I64
     L.tmo_hip_scaled_quantize_per_token.argtypes = [P] + [I64] * 4 + [P] * 3 + [I64, P, I64, P, I64, P, I64, INT, P]
@@ -61,7 +61,7 @@ def lib():
     L.tmo_hip_attn_workspace_bytes.argtypes = [I64] * 6
     L.tmo_hip_attn_workspace_bytes.restype = I64
     L.tmo_hip_cached_kv_attn.argtypes = [P, I64, I64, I64, P, I64, I64, P, P, I64, I64, P, P, INT,
-                                         I64, I64, I64, I64, P, I64, P, P, P, P, I64, I64, I64,
+                                         INT, I64, I64, I64, I64, P, I64, P, P, P, P, I64, I64, I64,
                                          P, I64, I64, I64] + [I64] * 9 + \
         [ctypes.c_float, INT, INT, I64, P, I64, P]
     L.tmo_hip_cached_kv_attn_workspace_bytes.argtypes = [I64] * 6
@@ -139,15 +139,18 @@ def test_reshape_validation(lib):
 
 def test_dequant_validation(lib):
     def call(mode=1, bit=8, dtype=2, key=FAKE, value=None, vc=None, vs=None, B=2, H=8, total=10,
-             ws=None, ws_bytes=0):
+             ws=None, ws_bytes=0, cdt=3, sdt=0):
         return lib.tmo_hip_dequant_from_paged_cache(
             key, value, 1024, 128, 1024, 128, total, FAKE, vc, FAKE, vs, FAKE, None, FAKE, B, 4,
-            64, 16, H, 16, 128, mode, bit, dtype, ws, ws_bytes, None)
+            64, 16, H, 16, 128, mode, bit, dtype, cdt, sdt, ws, ws_bytes, None)
     assert call(ws_bytes=-1) == EINVAL
     assert call(ws_bytes=64) == EINVAL          # bytes without a pointer
     assert call(mode=2) == EMODE
     assert call(bit=4) == EMODE
     assert call(dtype=3) == EDTYPE
+    assert call(cdt=2) == EDTYPE                # caches: int8 or float8_e4m3fn
+    assert call(sdt=1) == EDTYPE                # scales: fp32 or bf16
+    assert call(cdt=4, sdt=2, B=0) == 0         # float8_e4m3fn pages, bf16 scales
     assert call(key=None) == EINVAL
     assert call(value=FAKE) == EINVAL
     assert call(H=0) == EINVAL
@@ -161,14 +164,14 @@ def test_dequant_noalloc_validation(lib):
     would not fit the library's static scratch (TMO_HIP_DEQUANT_SCRATCH_BYTES)."""
     fn = lib.tmo_hip_dequant_from_paged_cache_noalloc
     fn.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int64] * 5 + [ctypes.c_void_p] * 7 + \
-        [ctypes.c_int64] * 7 + [ctypes.c_int] * 3 + [ctypes.c_void_p]
+        [ctypes.c_int64] * 7 + [ctypes.c_int] * 5 + [ctypes.c_void_p]
     m = re.search(r"#define\s+TMO_HIP_DEQUANT_SCRATCH_BYTES\s+(\d+)", HEADER.read_text())
     pages = (int(m.group(1)) - 16) // 16 // 8 * 8      # 262136 with 4 MiB
     too_small = header_enum("TMO_ERR_SCRATCH_TOO_SMALL")
 
     def call(B, MB):
         return fn(FAKE, None, 1024, 128, 0, 0, 10, FAKE, None, FAKE, None, FAKE, None, FAKE, B,
-                  MB, 64, 16, 8, 16, 128, 1, 8, 2, None)
+                  MB, 64, 16, 8, 16, 128, 1, 8, 2, 3, 0, None)
     assert pages == 262136
     assert call(1, pages + 1) == too_small
     assert call(pages // 8 + 1, 8) == too_small
@@ -369,13 +372,16 @@ def test_attention_validation(lib):
 def test_multi_token_attention_validation(lib):
     def call(q=FAKE, cu=None, S=4, T=0, B=2, Hq=8, Hkv=2, D=128, Dv=128, kdim=128, vdim=128,
              vc=FAKE, smode=1, ssb=32, BS=16, splits=1, ws=None, wsb=0, qdt=2, cdt=3,
-             qss=128 * 8, oss=128 * 8, sink=None):
+             qss=128 * 8, oss=128 * 8, sink=None, sdt=0):
         return lib.tmo_hip_cached_kv_attn(
-            q, 4 * 1024, qss, 128, cu, S, T, FAKE, vc, kdim, vdim, FAKE, FAKE, smode, ssb, 16,
+            q, 4 * 1024, qss, 128, cu, S, T, FAKE, vc, kdim, vdim, FAKE, FAKE, smode, sdt, ssb, 16,
             32, 16, FAKE, 4, FAKE, None, sink, FAKE, 4 * 1024, oss, 128, None, 0, 0, 0, B, Hq,
             Hkv, D, Dv, 16, BS, 64, -1, 0.1, qdt, cdt, splits, ws, wsb, None)
     assert call(qdt=3) == EDTYPE
     assert call(smode=4) == EMODE and call(smode=0) == EMODE
+    assert call(sdt=1) == EDTYPE                   # scales: fp32 or bf16
+    assert call(cdt=4, sdt=2, B=0) == 0            # float8_e4m3fn caches, bf16 scales
+    assert call(cdt=4, smode=0) == EMODE           # ... which need a scale mode
     assert call(q=None) == EINVAL
     assert call(kdim=64) == EINVAL                 # a K row shorter than the key head size
     assert call(vdim=64) == EINVAL                 # a V row shorter than the value head size

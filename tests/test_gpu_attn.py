@@ -55,7 +55,7 @@ def _vmax(case, vs, Dv=None):
 def run_attn(tmo, ref, dev, case, scale=0.0883883, window=-1, four_d=True, with_lse=True,
              bit=None, per_tensor=False, max_ctx=None):
     q = case.q
-    kbit = 8 if case.k_cache.dtype == torch.int8 else -1
+    kbit = 8 if case.k_cache.dtype in (torch.int8, torch.float8_e4m3fn) else -1
     ks, vs = case.k_scale, case.v_scale
     if per_tensor:
         ks, vs = torch.tensor([0.0137]), torch.tensor([0.0211])
@@ -103,6 +103,60 @@ def test_attn_dtypes_and_cache_kinds(tmo, ref, dev, dtype, kv):
 def test_attn_per_tensor_scales(tmo, ref, dev):
     case = W.attn_case(torch.bfloat16, 12, kv="int8_token", B=4, Hq=4, Hkv=4, D=128, max_ctx=90)
     run_attn(tmo, ref, dev, case, per_tensor=True)
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kv", ["fp8_token", "fp8_channel", "fp8_group", "int8_token",
+                                "int8_channel"])
+@pytest.mark.parametrize("D", [64, 128, 256, 96])
+def test_attn_fp8_pages_and_bf16_scales(tmo, ref, dev, D, kv, scale_dtype):
+    """float8_e4m3fn pages (_ops.py:868; kv_cache_quant_bit_size 8) and bf16 scale tensors
+    (_ops.py:872), on the MFMA kernels (head sizes 64 / 128 / 256, per-token and per-channel
+    scales) and the VALU kernel (per-group scales, head size 96), against the float64 oracle
+    at the stated tolerance."""
+    if kv.endswith("group") and D % 32:
+        pytest.skip("per-group scales need head_size % 32 == 0")
+    case = W.attn_case(torch.bfloat16, 41 + D, kv=kv, B=5, Hq=8, Hkv=2, D=D, BS=32, NB=64,
+                       max_ctx=300, scale_dtype=scale_dtype)
+    case.block_tables[3, 2] = -1                          # a missing page
+    # the oracle's general entry (per-group scales included), one query token per sequence
+    run_attn_mq(tmo, ref, dev, case, case.q, scale=1.0 / math.sqrt(D))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_attn_fp8_pages_multi_token_and_splits(tmo, ref, dev, dtype):
+    """fp8 pages with several query tokens per sequence (cu_seq_q), a sink and contexts long
+    enough for several splits."""
+    case = W.attn_case(dtype, 45, kv="fp8_token", B=4, Hq=16, Hkv=2, D=128, BS=16, NB=700,
+                       max_ctx=2500, scale_dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(46)
+    nq = torch.tensor([1, 3, 4, 2], dtype=torch.int32)
+    cu = torch.cat((torch.zeros(1, dtype=torch.int32), nq.cumsum(0).to(torch.int32)))
+    q = torch.randn(int(nq.sum()), 16, 128, generator=g).to(dtype)
+    sink = torch.randn(16, generator=g)
+    run_attn_mq(tmo, ref, dev, case, q, cu=cu, sink=sink)
+
+
+def test_attn_decode_on_configs4_fp8_pages(tmo, ref, dev):
+    """configs[4]'s page layout with float8_e4m3fn pages written by this build's own
+    quant_to_paged_cache (fp8 branch: scale = amax / 448 per token and head) from bf16 K/V,
+    read by the attention with 32 query heads, on a sample of 6 sequences against the oracle."""
+    layout = W.cfg5()
+    sel = torch.tensor([0, 1, 7, 20, 41, 63])
+    ctx = layout.context_lengths[sel].contiguous()
+    bt = layout.block_tables[sel].contiguous()
+    used = [bt[i, :(c + 15) // 16] for i, c in enumerate(ctx.tolist())]
+    pages = torch.unique(torch.cat(used))
+    bt2 = torch.full_like(bt, -1)
+    for i, u in enumerate(used):
+        bt2[i, :u.numel()] = torch.searchsorted(pages, u).to(torch.int32)
+    NB = pages.numel()
+    sub = W.DequantLayout("cfg5_sample", ctx, bt2, NB, 16)
+    kc, vc, ks, vs = W.cfg5_fill(sub, dev, seed=77, cache_dtype=torch.float8_e4m3fn)
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(len(sel), 32, 128, generator=g).to(torch.bfloat16)
+    case = W.AttnCase(q, kc.cpu(), vc.cpu(), ks.cpu(), vs.cpu(), bt2, ctx)
+    run_attn(tmo, ref, dev, case)
 
 
 @pytest.mark.parametrize("kv", ["int8_token", "plain"])
@@ -207,7 +261,7 @@ def run_attn_mq(tmo, ref, dev, case, q, cu=None, sink=None, scale=0.0883883, win
     """Several query tokens per sequence: q [B, S, Hq, D] or [T, Hq, D] with cu.  The output
     ([..., Dv], Dv the V cache's head size or q's by default) starts as a sentinel, which rows
     of no sequence must keep.  case.v_cache None: K and V in one cache."""
-    kbit = 8 if case.k_cache.dtype == torch.int8 else -1
+    kbit = 8 if case.k_cache.dtype in (torch.int8, torch.float8_e4m3fn) else -1
     Dv = Dv or (case.v_cache.shape[-1] if case.v_cache is not None else q.shape[-1])
     cpu = lambda t: t.cpu() if t is not None else None            # noqa: E731
     on_dev = lambda t: t if t is None or t.is_cuda else t.to(dev)  # noqa: E731  (views kept)

@@ -588,6 +588,42 @@ def test_dequant_cfg5_full(tmo, ref, dev):
     _dequant_both(tmo, ref, dev, layout, caches, torch.bfloat16, 1)
 
 
+def test_dequant_cfg5_full_fp8_pages_bf16_scales(tmo, ref, dev):
+    """configs[4] at full size with float8_e4m3fn pages written by this build's
+    quant_to_paged_cache (fp8 branch), their fp32 scales read once as written and once
+    rounded to bf16 (_ops.py:3805-3806): bit-exact against the oracle."""
+    layout = W.cfg5()
+    print(f"[dequant fp8] cfg5 sum(ctx)={layout.total_tokens}", flush=True)
+    kc, vc, ks, vs = W.cfg5_fill(layout, dev, cache_dtype=torch.float8_e4m3fn)
+    _dequant_both(tmo, ref, dev, layout, (kc, vc, ks, vs), torch.bfloat16, 1)
+    _dequant_both(tmo, ref, dev, layout, (kc, vc, ks.to(torch.bfloat16), vs.to(torch.bfloat16)),
+                  torch.bfloat16, 1)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("cache,scale_dtype", [("fp8", torch.float32), ("fp8", torch.bfloat16),
+                                               ("int8", torch.bfloat16)])
+@pytest.mark.parametrize("D,BS,H", [(128, 16, 4), (128, 16, 3), (80, 16, 4)])
+def test_dequant_fp8_pages_and_bf16_scales(tmo, ref, dev, out_dtype, mode, cache, scale_dtype,
+                                           D, BS, H):
+    """float8_e4m3fn pages and bf16 scales on the page-list kernels, the per-page kernel and
+    the scalar kernel, both modes, every output type, with and without V."""
+    layout, (kc, vc, ks, vs) = _small_layout(seed=D + H + mode + 3, D=D, BS=BS, NB=64, H=H)
+    if cache == "fp8":
+        g = torch.Generator().manual_seed(D + H)
+        kc, vc = W.fp8_codes(kc.shape, g), W.fp8_codes(vc.shape, g)
+        ks, vs = ks * 0.01, vs * 0.01
+    if mode == 0:
+        g = torch.Generator().manual_seed(98)
+        ks = torch.rand(H, D, generator=g) * 0.05
+        vs = torch.rand(H, D, generator=g) * 0.05
+    ks, vs = ks.to(scale_dtype), vs.to(scale_dtype)
+    caches = tuple(t.to(dev) for t in (kc, vc, ks, vs))
+    _dequant_both(tmo, ref, dev, layout, caches, out_dtype, mode)
+    _dequant_both(tmo, ref, dev, layout, caches, out_dtype, mode, with_v=False)
+
+
 def _small_layout(seed, B=5, NB=40, BS=16, H=4, D=128, max_ctx=100):
     g = torch.Generator().manual_seed(seed)
     ctx = torch.randint(1, max_ctx + 1, (B,), generator=g).to(torch.int32)
@@ -678,7 +714,7 @@ def _dequant_c_abi(out_k, out_v, caches, layout, mode, seq_offset, max_ctx, work
     L = _loader.c_abi()
     P, I64, INT = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
     L.tmo_hip_dequant_from_paged_cache.argtypes = [P, P] + [I64] * 5 + [P] * 7 + [I64] * 7 + \
-        [INT, INT, INT, P, I64, P]
+        [INT] * 5 + [P, I64, P]
     L.tmo_hip_dequant_workspace_bytes.argtypes = [I64] * 4
     L.tmo_hip_dequant_workspace_bytes.restype = I64
     kc, vc, ks, vs = caches
@@ -700,7 +736,7 @@ def _dequant_c_abi(out_k, out_v, caches, layout, mode, seq_offset, max_ctx, work
         vc.data_ptr() if out_v is not None else None, ks.data_ptr(),
         vs.data_ptr() if out_v is not None else None, ctx.data_ptr(),
         off.data_ptr() if off is not None else None, bt.data_ptr(), B, MB, max_ctx, NB, H, BS, D,
-        mode, 8, dt, ws.data_ptr() if ws is not None else None, ws_bytes, None)
+        mode, 8, dt, 3, 0, ws.data_ptr() if ws is not None else None, ws_bytes, None)
     torch.cuda.synchronize()
     assert st == 0
 

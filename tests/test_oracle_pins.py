@@ -314,6 +314,38 @@ def torch_dequant(kc, ks, ctx, bt, mode, out_dtype, offsets):
 
 @pytest.mark.parametrize("out_dtype", DTYPES)
 @pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("cache", ["int8", "fp8"])
+@pytest.mark.parametrize("scale_dtype", [torch.float32, torch.bfloat16])
+def test_dequant_fp8_pages_and_bf16_scales_match_torch(ref, out_dtype, mode, cache, scale_dtype):
+    """The reference math with bf16 scale tensors (_ops.py:3805-3806) and with the
+    float8_e4m3fn pages quant_to_paged_cache writes: (code.to(float32) * scale).to(out_dtype)
+    executed by torch, whose float8_e4m3fn and bfloat16 casts to float32 are exact -- bit for
+    bit against the oracle, which widens a bf16 scale itself."""
+    g = torch.Generator().manual_seed(11 + mode)
+    B, NB, H, BS, D = 4, 40, 2, 16, 32
+    ctx = torch.tensor([16, 3, 45, 31], dtype=torch.int32)
+    bt = torch.randperm(NB, generator=g)[: B * 3].reshape(B, 3).to(torch.int32)
+    if cache == "int8":
+        kc = torch.randint(-128, 128, (NB, H, BS, D), generator=g, dtype=torch.int8)
+    else:
+        kc = W.fp8_codes((NB, H, BS, D), g)
+    ks = (torch.rand(NB, H, BS, generator=g) * 0.1) if mode == 1 else \
+        (torch.rand(H, D, generator=g) * 0.1)
+    ks.view(-1)[0] = 3e36 if scale_dtype == torch.float32 else 1e30   # beyond fp16 / bf16
+    ks = ks.to(scale_dtype)
+    total = int(ctx.sum())
+    got = torch.full((total, H, D), -1.0).to(out_dtype)
+    ref.dequant_from_paged_cache(got, None, kc, None, ks, None, ctx, None, bt, mode)
+    offsets = (torch.cumsum(ctx, 0) - ctx).to(torch.int32)
+    want = torch_dequant(kc, ks.to(torch.float32), ctx, bt, mode, out_dtype, offsets)
+    for start, rows in want.items():
+        assert torch.equal(bits(got[start:start + rows.shape[0]]), bits(rows))
+    if cache == "fp8":  # the fp8 codes decode to their e4m3fn values: |out| <= 448 * scale
+        assert (got.float().abs() <= 448 * ks.float().max() * 1.01).all() or out_dtype != torch.float32
+
+
+@pytest.mark.parametrize("out_dtype", DTYPES)
+@pytest.mark.parametrize("mode", [0, 1])
 @pytest.mark.parametrize("with_offsets", [False, True])
 def test_dequant_matches_torch_docstring_math(ref, out_dtype, mode, with_offsets):
     g = torch.Generator().manual_seed(mode * 7 + int(with_offsets))
@@ -520,6 +552,26 @@ def test_offline_quant_matches_torch_docstring_math(ref, dtype, cache_dtype, per
 def _e4m3_value(c: int) -> Fraction:
     e, m = c >> 3, c & 7
     return Fraction(m, 512) if e == 0 else Fraction(8 + m, 8) * Fraction(2) ** (e - 7)
+
+
+def test_e4m3_reader_matches_torch_and_closed_form(ref):
+    """The oracle's float8_e4m3fn reader (the pages' consumers: attention and dequant) on all
+    256 codes: equal to torch's float8_e4m3fn -> float32 cast, and to the closed form
+    (-1)^s (8 + m) 2^(e - 10) (m 2^-9 for e = 0); S.1111.111 is NaN and nothing else is."""
+    b = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    mine = ref.e4m3_to_f32(b)
+    want = b.view(torch.float8_e4m3fn).to(torch.float32)
+    nan = torch.isnan(want)
+    assert nan.nonzero().flatten().tolist() == [0x7F, 0xFF]
+    assert torch.equal(torch.isnan(mine), nan)
+    assert torch.equal(bits(mine[~nan]), bits(want[~nan]))
+    for c in range(256):
+        if c & 0x7F == 0x7F:
+            continue
+        v = _e4m3_value(c & 0x7F) * (-1 if c & 0x80 else 1)
+        assert Fraction(float(mine[c])) == v, c
+    assert float(mine[0x08]) == 2.0 ** -6 and float(mine[0x01]) == 2.0 ** -9
+    assert float(mine[0x7E]) == 448.0 and float(mine[0x80]) == 0.0 and str(float(mine[0x80])) == "-0.0"
 
 
 def _exact_e4m3(q: Fraction) -> int:
@@ -1310,6 +1362,38 @@ def torch_attn(case, scale, window=-1):
         out[i] = (p[:, :, None] * V.transpose(0, 1)).sum(1)
         lse[i] = torch.logsumexp(s, dim=-1)
     return out, lse
+
+
+@pytest.mark.parametrize("kv", ["fp8_token", "fp8_channel", "int8_token", "int8_channel"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_attn_fp8_pages_and_bf16_scales_match_torch_float64(ref, dtype, kv):
+    """float8_e4m3fn caches (_ops.py:868) and bf16 scales (_ops.py:872): the docstring math in
+    float64 by torch -- the e4m3fn value (torch's exact cast) times the widened bf16 scale --
+    against the oracle, with a missing page, a window and ALiBi."""
+    case = W.attn_case(dtype, 31, kv=kv, Hq=8, Hkv=2, D=64, max_ctx=70,
+                       scale_dtype=torch.bfloat16)
+    case.block_tables[2, 1] = -1
+    for window, alibi in ((-1, False), (9, False), (-1, True)):
+        case.alibi = (0.5 ** torch.arange(1, 9, dtype=torch.float32)).repeat(5, 1) if alibi else None
+        out, lse = ref.single_query_attn(case.q, case.k_cache, case.v_cache, case.block_tables,
+                                         case.context_lens, 0.125, case.k_scale, case.v_scale,
+                                         case.alibi, window)
+        want, wlse = torch_attn(case, 0.125, window)
+        assert torch.allclose(out, want, rtol=1e-12, atol=1e-12)
+        assert torch.allclose(lse, wlse, rtol=1e-12, atol=1e-12)
+    # the fp8 pages are read as their values: an fp8 cache holding x and an fp32 one holding
+    # the same numbers give the same result
+    if kv.startswith("fp8"):
+        plain = W.AttnCase(case.q, case.k_cache.to(torch.float32), case.v_cache.to(torch.float32),
+                           None, None, case.block_tables, case.context_lens)
+        fold = (lambda c, s: c * (s.float()[..., None] if s.dim() == 3 else s.float()[None, :, None, :]))
+        plain.k_cache = fold(plain.k_cache, case.k_scale)
+        plain.v_cache = fold(plain.v_cache, case.v_scale)
+        case.alibi = None
+        out, _ = ref.single_query_attn(case.q, case.k_cache, case.v_cache, case.block_tables,
+                                       case.context_lens, 0.125, case.k_scale, case.v_scale)
+        want, _ = torch_attn(plain, 0.125)
+        assert torch.allclose(out, want, rtol=1e-6, atol=1e-9)
 
 
 @pytest.mark.parametrize("kv", ["int8_token", "int8_channel", "plain"])

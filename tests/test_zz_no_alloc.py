@@ -19,7 +19,7 @@ SCRATCH_TOO_SMALL = -5
 def _lib():
     from domesticated_torch_mlu_ops_amd import _loader
     L = _loader.c_abi()
-    args = [P, P] + [I64] * 5 + [P] * 7 + [I64] * 7 + [INT, INT, INT]
+    args = [P, P] + [I64] * 5 + [P] * 7 + [I64] * 7 + [INT] * 5
     L.tmo_hip_dequant_from_paged_cache.argtypes = args + [P, I64, P]
     L.tmo_hip_dequant_from_paged_cache_noalloc.argtypes = args + [P]
     L.tmo_hip_dequant_workspace_bytes.argtypes = [I64] * 4
@@ -49,7 +49,7 @@ def _call(L, fn, out_k, out_v, caches, layout, workspace=None):
     args = [out_k.data_ptr(), out_v.data_ptr(), out_k.stride(0), out_k.stride(1), out_v.stride(0),
             out_v.stride(1), out_k.shape[0], kc.data_ptr(), vc.data_ptr(), ks.data_ptr(),
             vs.data_ptr(), ctx.data_ptr(), None, bt.data_ptr(), B, MB,
-            layout.max_context_len, NB, H, BS, D, 1, 8, 2]
+            layout.max_context_len, NB, H, BS, D, 1, 8, 2, 3, 0]
     torch.cuda.synchronize()
     if fn == "noalloc":
         st = L.tmo_hip_dequant_from_paged_cache_noalloc(*args, None)

@@ -188,17 +188,20 @@ def cfg5() -> DequantLayout:
     return DequantLayout("cfg5", ctx, bt, 131072)
 
 
-def cfg5_fill(layout: DequantLayout, device, seed: int = 1005, heads: int = H, dim: int = D):
-    """Int8 pages + fp32 per-token scales for every page a sequence of ``layout`` uses,
-    produced the way a serving engine fills them: config-3-style bf16 K/V (N(0,1), one x20
-    channel per head) quantised with quant_to_paged_cache on ``device``.  Generated on the
-    device (a CPU draw of ~2e9 values would dominate the run); unused pages keep the
-    sentinel.  Returns (k_cache, v_cache, k_scale, v_scale)."""
+def cfg5_fill(layout: DequantLayout, device, seed: int = 1005, heads: int = H, dim: int = D,
+              cache_dtype=torch.int8):
+    """Int8 (or float8_e4m3fn, ``cache_dtype``) pages + fp32 per-token scales for every page a
+    sequence of ``layout`` uses, produced the way a serving engine fills them: config-3-style
+    bf16 K/V (N(0,1), one x20 channel per head) quantised with quant_to_paged_cache on
+    ``device``.  Generated on the device (a CPU draw of ~2e9 values would dominate the run);
+    unused pages keep the sentinel.  Returns (k_cache, v_cache, k_scale, v_scale)."""
     import domesticated_torch_mlu_ops_amd as tmo
 
     NB, bs = layout.num_blocks, layout.block_size
-    kc = torch.full((NB, heads, bs, dim), CACHE_SENTINEL, dtype=torch.int8, device=device)
-    vc = torch.full_like(kc, CACHE_SENTINEL)
+    kc = torch.full((NB, heads, bs, dim), CACHE_SENTINEL, dtype=torch.uint8,
+                    device=device).view(cache_dtype)
+    vc = torch.full((NB, heads, bs, dim), CACHE_SENTINEL, dtype=torch.uint8,
+                    device=device).view(cache_dtype)
     ks = torch.full((NB, heads, bs), SCALE_SENTINEL, dtype=torch.float32, device=device)
     vs = torch.full_like(ks, SCALE_SENTINEL)
     g = torch.Generator(device=device).manual_seed(seed)
@@ -351,12 +354,25 @@ class AttnCase:
         return int(self.context_lens.max()) if self.context_lens.numel() else 0
 
 
+def fp8_codes(shape, g) -> torch.Tensor:
+    """float8_e4m3fn cache values as a quantiser leaves them: N(0, 1) * 96 rounded to e4m3fn
+    (torch's RNE cast) and clipped to +-448, with every 97th value replaced by a subnormal
+    code (|m| * 2^-9) and every 211th by +-448."""
+    x = (torch.randn(shape, generator=g) * 96).clamp(-448, 448)
+    flat = x.view(-1)
+    sub = torch.randint(1, 8, flat[::97].shape, generator=g).to(torch.float32) * 2.0 ** -9
+    flat[::97] = torch.where(flat[::97] < 0, -sub, sub)
+    flat[::211] = torch.where(flat[::211] < 0, -448.0, 448.0)
+    return x.to(torch.float8_e4m3fn)
+
+
 def attn_case(dtype, seed: int, kv: str = "int8_token", B: int = 5, Hq: int = 8, Hkv: int = 2,
               D: int = 128, BS: int = 16, NB: int = 64, max_ctx: int = 200,
-              alibi: bool = False) -> AttnCase:
+              alibi: bool = False, scale_dtype=torch.float32) -> AttnCase:
     """Decode attention inputs: q ~ N(0, 1) in `dtype`; caches int8 (`kv` "int8_token" /
-    "int8_channel" / "int8_group", codes uniform in [-127, 127] with scales ~U[0.005, 0.03))
-    or of q's dtype
+    "int8_channel" / "int8_group", codes uniform in [-127, 127] with scales ~U[0.005, 0.03)),
+    float8_e4m3fn (`kv` "fp8_token" / "fp8_channel" / "fp8_group", fp8_codes with scales
+    ~U[0.0003, 0.0015)), scales in `scale_dtype` (float32 or bfloat16), or of q's dtype
     (`kv` "plain", N(0, 1)); context lengths in [1, max_ctx] (the first max_ctx, one 1); each
     sequence's pages a random choice of distinct blocks."""
     g = torch.Generator().manual_seed(seed)
@@ -369,14 +385,20 @@ def attn_case(dtype, seed: int, kv: str = "int8_token", B: int = 5, Hq: int = 8,
     assert B * MB <= NB, "not enough blocks for distinct pages"
     bt = torch.randperm(NB, generator=g)[:B * MB].reshape(B, MB).to(torch.int32)
     ks = vs = None
-    if kv.startswith("int8"):
-        kc = torch.randint(-127, 128, (NB, Hkv, BS, D), generator=g, dtype=torch.int8)
-        vc = torch.randint(-127, 128, (NB, Hkv, BS, D), generator=g, dtype=torch.int8)
-        shape = {"int8_token": (NB, Hkv, BS), "int8_channel": (Hkv, D),
-                 "int8_group": (NB, Hkv, BS, D // 32)}[kv]
-        ks = 0.005 + 0.025 * torch.rand(shape, generator=g)
-        vshape = (NB, Hkv, BS // 32, D) if kv == "int8_group" else shape
-        vs = 0.005 + 0.025 * torch.rand(vshape, generator=g)
+    if kv.startswith("int8") or kv.startswith("fp8"):
+        form = kv.split("_")[1]
+        if kv.startswith("int8"):
+            kc = torch.randint(-127, 128, (NB, Hkv, BS, D), generator=g, dtype=torch.int8)
+            vc = torch.randint(-127, 128, (NB, Hkv, BS, D), generator=g, dtype=torch.int8)
+            lo, span = 0.005, 0.025
+        else:
+            kc = fp8_codes((NB, Hkv, BS, D), g)
+            vc = fp8_codes((NB, Hkv, BS, D), g)
+            lo, span = 0.0003, 0.0012
+        shape = {"token": (NB, Hkv, BS), "channel": (Hkv, D), "group": (NB, Hkv, BS, D // 32)}[form]
+        ks = (lo + span * torch.rand(shape, generator=g)).to(scale_dtype)
+        vshape = (NB, Hkv, BS // 32, D) if form == "group" else shape
+        vs = (lo + span * torch.rand(vshape, generator=g)).to(scale_dtype)
     else:
         kc = torch.randn(NB, Hkv, BS, D, generator=g).to(dtype)
         vc = torch.randn(NB, Hkv, BS, D, generator=g).to(dtype)
