@@ -554,13 +554,20 @@ def single_query_cached_kv_attn(
     head_size]``.  A sequence's nq tokens are its last nq positions: token s (position
     ``P = L - nq + s``) sees keys ``[max(0, P - windows_size_left), P]``, ALiBi adds
     ``slope * (j - P)``, and ``sink`` (``[heads]`` float logits) joins the softmax
-    denominator only.  Computed in fp32 (MFMA with exact bf16/f16 operands).  With
+    denominator only.  ``kv_cache_quant_bit_size=4``: int8 caches of signed int4 pairs (even
+    element in the high nibble), K ``[num_blocks, kv_heads, block_size, head_size // 2]``, V
+    ``[num_blocks, kv_heads, block_size // 2, head_size_v]`` (rows paired) or ``[...,
+    block_size, head_size_v // 2]`` (channels paired), scales as for int8.  ``mask``
+    (``[batch, seq_q, mask_len]`` in ``compute_dtype``; seq_q <= 16, mask_len <= 64, a
+    multiple of seq_q; not with float32 q) is added to the logits of each sequence's last
+    ``mask_len`` keys.  Computed in fp32 (MFMA with exact bf16/f16 operands).  With
     ``return_lse`` also returns ``ln`` of the softmax denominator, ``[batch, heads, seq_q]``
-    (or ``[heads, total_q]`` for 3-D q).  ``mask`` and quantised q / output raise
-    ``RuntimeError``.  A positive ``max_seq_q`` is trusted: query tokens past it are not
-    computed (as the reference says of an understated ``max_context_len``).
+    (or ``[heads, total_q]`` for 3-D q).  Quantised q / output raise ``RuntimeError``.  A
+    positive ``max_seq_q`` is trusted: query tokens past it are not computed (as the
+    reference says of an understated ``max_context_len``).
 
-    Reference: ``_ops.py:777-900`` (math ``:800-817``).  Returns ``out`` or ``(out, lse)``.
+    Reference: ``_ops.py:777-900`` (math ``:800-817``; int4 ``:826-829``, ``:852``; mask
+    ``:860``).  Returns ``out`` or ``(out, lse)``.
     """
     tmo_out = out
     if out is None:

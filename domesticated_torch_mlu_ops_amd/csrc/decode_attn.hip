@@ -89,6 +89,11 @@ struct AttnParams {
   int32_t q_dtype;               // TMO_DTYPE_*
   int32_t q_vec;                 // q rows 16-byte aligned 2-byte values: vector q loads
   int32_t c_dtype;               // cache TMO_DTYPE_*
+  int32_t v_ch;                  // int4 caches: V pairs channels (else the rows of a page)
+  const void* mask;              // [B, S, mask_len] logit terms of the last keys, or null
+  int32_t mask_dtype;            // F32 / F16 / BF16
+  int32_t mask_len;
+  int64_t m_sb, m_ss;            // mask strides (sequence, token); last dim contiguous
   int32_t splits;
   int64_t split_tokens;          // multiple of 64
   float* ws;                     // [B, Hkv, splits, ncols, Dv + 2] when splits > 1
@@ -115,6 +120,15 @@ __device__ __forceinline__ void store_out(const AttnParams& p, int64_t e, float 
     case TMO_DTYPE_BF16: store1(BF16{}, p.out, e, v); break;
     case TMO_DTYPE_F16: store1(F16{}, p.out, e, v); break;
     default: store1(F32{}, p.out, e, v); break;
+  }
+}
+
+// Mask element e (a logit term, natural-log units) as fp32.
+__device__ __forceinline__ float mask_value(const AttnParams& p, int64_t e) {
+  switch (p.mask_dtype) {
+    case TMO_DTYPE_BF16: return load1(BF16{}, p.mask, e);
+    case TMO_DTYPE_F16: return load1(F16{}, p.mask, e);
+    default: return load1(F32{}, p.mask, e);
   }
 }
 
@@ -431,6 +445,8 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   }
   const float alibi = (p.alibi && qvalid) ? p.alibi[i * p.Hq + hq] * kLog2e : 0.0f;
   const float score_scale = p.scale_log2 * inv_sigma;  // inv_sigma: an exact power of two
+  // mask: terms for keys [mask_lo, L), element mask_row + m for key mask_lo + m
+  const int32_t mask_lo = (int32_t)sq.L - p.mask_len;
 
   float mrun = -__builtin_inff();   // running max (base 2) of this lane's column
   float lpart = 0.0f;               // this lane's share of the running sum
@@ -551,6 +567,20 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
         if (j < klo || j > khi) v = -__builtin_inff();
         sc[e] = v;
         tmax = fmaxf(tmax, v);
+      }
+      // mask terms of the last mask_len keys: only the tiles that reach them (wave-uniform)
+      if (p.mask && t0 + 15 >= mask_lo) {
+        // the column's row of terms (recomputed here: nothing stays live across the tiles;
+        // a padding column reads token S - 1's row, in bounds, and its scores stay -inf)
+        const int ct = (cb * 16 + col) / p.g;
+        const int64_t mask_row = i * p.m_sb + (int64_t)(ct < p.S ? ct : p.S - 1) * p.m_ss;
+        tmax = -__builtin_inff();
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int32_t j = t0 + 4 * grp + e;
+          if (j >= mask_lo) sc[e] += mask_value(p, mask_row + (j - mask_lo)) * kLog2e;
+          tmax = fmaxf(tmax, sc[e]);
+        }
       }
       tmax = col_max(tmax);
       // No branch on the column's state: the MFMAs below need the whole wavefront.  The
@@ -892,13 +922,26 @@ __device__ __forceinline__ float code_value(const void* base, int64_t e, int cac
   return fp8_value(static_cast<const uint8_t*>(base)[e], 0);
 }
 
+// Signed 4-bit code `odd` of byte e of an int4-pair cache: the even element of a pair in the
+// high nibble, the odd one in the low nibble, sign-extended.
+__device__ __forceinline__ float nibble_value(const void* base, int64_t e, int odd) {
+  const int32_t b = static_cast<const int8_t*>(base)[e];
+  return (float)(odd ? (int32_t)((uint32_t)b << 28) >> 28 : b >> 4);
+}
+
+__device__ __forceinline__ bool quant_cache(int cache_dtype) {
+  return cache_dtype == TMO_DTYPE_I8 || cache_dtype == TMO_DTYPE_F8E4M3 ||
+         cache_dtype == TMO_DTYPE_I4;
+}
+
 // Key channel d of row `row` of page blk, KV head hk.
 __device__ __forceinline__ float key_value(const AttnParams& p, int64_t blk, int hk, int64_t row,
                                            int d, int cache_dtype) {
   const int64_t r = (blk * p.Hkv + hk) * p.BS + row;
-  if (cache_dtype != TMO_DTYPE_I8 && cache_dtype != TMO_DTYPE_F8E4M3)
-    return plain_value(p.kc, r * p.k_row + d, cache_dtype);
-  const float code = code_value(p.kc, r * p.k_row + d, cache_dtype);
+  if (!quant_cache(cache_dtype)) return plain_value(p.kc, r * p.k_row + d, cache_dtype);
+  // int4: K pairs adjacent channels, k_row bytes per row
+  const float code = cache_dtype == TMO_DTYPE_I4 ? nibble_value(p.kc, r * p.k_row + (d >> 1), d & 1)
+                                                 : code_value(p.kc, r * p.k_row + d, cache_dtype);
   switch (p.smode) {
     case 1: return code * scale_at(p.ks, blk * p.ks_sb + hk * p.ks_sh + row, p.s_bf16);
     case 2: return code * scale_at(p.ks, (int64_t)hk * p.D + d, p.s_bf16);
@@ -910,9 +953,15 @@ __device__ __forceinline__ float key_value(const AttnParams& p, int64_t blk, int
 __device__ __forceinline__ float value_value(const AttnParams& p, int64_t blk, int hk, int64_t row,
                                              int d, int cache_dtype) {
   const int64_t r = (blk * p.Hkv + hk) * p.BS + row;
-  if (cache_dtype != TMO_DTYPE_I8 && cache_dtype != TMO_DTYPE_F8E4M3)
-    return plain_value(p.vc, r * p.v_row + d, cache_dtype);
-  const float code = code_value(p.vc, r * p.v_row + d, cache_dtype);
+  if (!quant_cache(cache_dtype)) return plain_value(p.vc, r * p.v_row + d, cache_dtype);
+  float code;
+  if (cache_dtype != TMO_DTYPE_I4)
+    code = code_value(p.vc, r * p.v_row + d, cache_dtype);
+  else if (p.v_ch)  // int4, V pairing channels: as K
+    code = nibble_value(p.vc, r * p.v_row + (d >> 1), d & 1);
+  else  // int4, V pairing the rows of a page: [NB, Hkv, BS / 2, v_row]
+    code = nibble_value(p.vc, ((blk * p.Hkv + hk) * (p.BS >> 1) + (row >> 1)) * p.v_row + d,
+                        (int)(row & 1));
   switch (p.smode) {
     case 1: return code * scale_at(p.vs, blk * p.vs_sb + hk * p.vs_sh + row, p.s_bf16);
     case 2: return code * scale_at(p.vs, (int64_t)hk * p.Dv + d, p.s_bf16);
@@ -961,6 +1010,8 @@ __global__ __launch_bounds__(256) void attn_generic(AttnParams p) {
           dot += load_q(p, qe + d) * key_value(p, blk, hk, r, d, cache_dtype);
         s = dot * p.scale_log2;
         if (p.alibi) s += alibi * (float)(j - P);
+        if (p.mask && j >= sq.L - p.mask_len)
+          s += mask_value(p, i * p.m_sb + tok * p.m_ss + (j - (sq.L - p.mask_len))) * kLog2e;
       } else {
         blk = -1;
       }
@@ -1054,18 +1105,26 @@ extern "C" int tmo_hip_cached_kv_attn(
     const void* v_scale, int scale_mode, int scale_dtype, int64_t k_scale_stride_block,
     int64_t k_scale_stride_head, int64_t v_scale_stride_block, int64_t v_scale_stride_head,
     const int32_t* block_tables, int64_t max_blocks, const int32_t* context_lens,
-    const float* alibi_slopes, const float* sink, void* out, int64_t out_stride_batch,
-    int64_t out_stride_token, int64_t out_stride_head, float* lse, int64_t lse_stride_batch,
-    int64_t lse_stride_token, int64_t lse_stride_head, int64_t batch, int64_t num_q_heads,
-    int64_t num_kv_heads, int64_t head_size, int64_t head_size_v, int64_t num_blocks,
-    int64_t block_size, int64_t max_context_len, int64_t window_left, float softmax_scale,
-    int q_dtype, int cache_dtype, int64_t splits, void* workspace, int64_t workspace_bytes,
-    void* stream) {
+    const float* alibi_slopes, const float* sink, const void* mask, int mask_dtype,
+    int64_t mask_len, int64_t mask_stride_batch, int64_t mask_stride_token, void* out,
+    int64_t out_stride_batch, int64_t out_stride_token, int64_t out_stride_head, float* lse,
+    int64_t lse_stride_batch, int64_t lse_stride_token, int64_t lse_stride_head, int64_t batch,
+    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_size, int64_t head_size_v,
+    int64_t num_blocks, int64_t block_size, int64_t max_context_len, int64_t window_left,
+    float softmax_scale, int q_dtype, int cache_dtype, int v_pair_channels, int64_t splits,
+    void* workspace, int64_t workspace_bytes, void* stream) {
   if (q_dtype != TMO_DTYPE_BF16 && q_dtype != TMO_DTYPE_F16 && q_dtype != TMO_DTYPE_F32)
     return TMO_ERR_UNSUPPORTED_DTYPE;
-  // quantised caches: int8 codes or float8_e4m3fn values, times fp32 or bf16 scales
-  const bool quant = cache_dtype == TMO_DTYPE_I8 || cache_dtype == TMO_DTYPE_F8E4M3;
+  // quantised caches: int8 codes, float8_e4m3fn values or int4 pairs, times fp32 or bf16 scales
+  const bool int4 = cache_dtype == TMO_DTYPE_I4;
+  const bool quant = cache_dtype == TMO_DTYPE_I8 || cache_dtype == TMO_DTYPE_F8E4M3 || int4;
   if (!quant && cache_dtype != q_dtype) return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (mask && mask_dtype != TMO_DTYPE_F32 && mask_dtype != TMO_DTYPE_F16 &&
+      mask_dtype != TMO_DTYPE_BF16)
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (mask && (mask_len <= 0 || mask_len > 0x7fffffffLL || mask_stride_batch < 0 ||
+               mask_stride_token < 0))
+    return TMO_ERR_INVALID_ARGUMENT;
   if (quant && scale_dtype != TMO_DTYPE_F32 && scale_dtype != TMO_DTYPE_BF16)
     return TMO_ERR_UNSUPPORTED_DTYPE;
   if (quant && (scale_mode < 1 || scale_mode > 3)) return TMO_ERR_UNSUPPORTED_MODE;
@@ -1077,8 +1136,11 @@ extern "C" int tmo_hip_cached_kv_attn(
     return TMO_ERR_INVALID_ARGUMENT;
   if (quant && (!k_scale || !v_scale) && (num_blocks > 0 || scale_mode != 1))
     return TMO_ERR_INVALID_ARGUMENT;
-  // v_cache null: the values are the first head_size_v channels of the K cache's rows
+  // v_cache null: the values are the first head_size_v channels of the K cache's rows (not
+  // for int4 pairs, whose K and V caches pair different axes: null only with an empty cache)
+  const bool v_null = !v_cache;
   if (!v_cache) {
+    if (int4 && num_blocks > 0) return TMO_ERR_INVALID_ARGUMENT;
     v_cache = k_cache;
     v_cache_dim = k_cache_dim;
   }
@@ -1088,7 +1150,7 @@ extern "C" int tmo_hip_cached_kv_attn(
   if (max_context_len < 0) max_context_len = 0;
   if (batch < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
       head_size <= 0 || head_size > 4096 || head_size_v <= 0 || head_size_v > 512 ||
-      k_cache_dim < head_size || v_cache_dim < head_size_v || num_blocks < 0 ||
+      num_blocks < 0 ||
       block_size <= 0 || max_blocks < 0 || splits < 1 || seq_q < 0 || q_stride_batch < 0 ||
       q_stride_token < 0 || q_stride_head < 0 || out_stride_batch < 0 || out_stride_token < 0 ||
       out_stride_head < 0 || (cu_seq_q && total_q < 0))
@@ -1098,6 +1160,13 @@ extern "C" int tmo_hip_cached_kv_attn(
        v_scale_stride_head < 0))
     return TMO_ERR_INVALID_ARGUMENT;
   if (quant && scale_mode == 3 && (head_size % 32 != 0 || block_size % 32 != 0))
+    return TMO_ERR_INVALID_ARGUMENT;
+  // cache rows: elements, or bytes of int4 pairs (K: head_size / 2 channel pairs; V: pairs of
+  // rows -- [num_blocks, Hkv, block_size / 2, v_cache_dim], block_size even -- or of channels)
+  if (!int4 ? (k_cache_dim < head_size || v_cache_dim < head_size_v)
+            : (2 * k_cache_dim < head_size ||
+               (!v_null && (v_pair_channels ? 2 * v_cache_dim < head_size_v
+                                            : (v_cache_dim < head_size_v || block_size % 2 != 0)))))
     return TMO_ERR_INVALID_ARGUMENT;
   const int64_t g = num_q_heads / num_kv_heads;
   if (batch > 65535 || num_kv_heads > 65535 || splits > 65535 || num_q_heads > 0x7fffffffLL ||
@@ -1174,7 +1243,7 @@ extern "C" int tmo_hip_cached_kv_attn(
   // The MFMA kernel always issues its tile loads (a wave with no valid page yet reads page 0,
   // see attn_mfma), so an empty cache takes attn_generic, whose loads are all under the page
   // check: every output row is then 0 and its lse -inf (nothing to attend to).
-  bool mfma = num_blocks > 0 && (head_size == 64 || head_size == 128 || head_size == 256) &&
+  bool mfma = num_blocks > 0 && !int4 && (head_size == 64 || head_size == 128 || head_size == 256) &&
               head_size_v == head_size && k_cache_dim == head_size &&
               v_cache_dim == head_size && block_size % 16 == 0 && al(k_cache, 16) &&
               al(v_cache, 16) && q_dtype != TMO_DTYPE_F32;
@@ -1186,6 +1255,12 @@ extern "C" int tmo_hip_cached_kv_attn(
              k_scale_stride_head % 4 == 0 && v_scale_stride_block % 4 == 0 &&
              v_scale_stride_head % 4 == 0));
   p.c_dtype = cache_dtype;
+  p.v_ch = int4 && v_pair_channels;
+  p.mask = mask;
+  p.mask_dtype = mask_dtype;
+  p.mask_len = (int32_t)mask_len;
+  p.m_sb = mask_stride_batch;
+  p.m_ss = mask_stride_token;
   if (!mfma) {
     p.splits = 1;
     p.split_tokens = 1;
@@ -1226,12 +1301,12 @@ extern "C" int tmo_hip_single_query_cached_kv_attn(
   if (head_size > 512) return TMO_ERR_INVALID_ARGUMENT;
   // contiguous per-token scales [num_blocks, Hkv, block_size]
   const int64_t sb = num_kv_heads * block_size, sh = block_size;
+  if (cache_dtype == TMO_DTYPE_I4) return TMO_ERR_UNSUPPORTED_DTYPE;
   return tmo_hip_cached_kv_attn(
       q, q_stride_seq, 0, q_stride_head, nullptr, 1, 0, k_cache, v_cache, head_size, head_size,
       k_scale, v_scale, scale_mode, TMO_DTYPE_F32, sb, sh, sb, sh, block_tables, max_blocks,
-      context_lens,
-      alibi_slopes, nullptr, out, out_stride_seq, 0, out_stride_head, lse, lse_stride_seq, 0,
-      lse_stride_head, batch, num_q_heads, num_kv_heads, head_size, head_size, num_blocks,
-      block_size, max_context_len, window_left, softmax_scale, q_dtype, cache_dtype, splits,
-      workspace, workspace_bytes, stream);
+      context_lens, alibi_slopes, nullptr, nullptr, 0, 0, 0, 0, out, out_stride_seq, 0,
+      out_stride_head, lse, lse_stride_seq, 0, lse_stride_head, batch, num_q_heads,
+      num_kv_heads, head_size, head_size, num_blocks, block_size, max_context_len, window_left,
+      softmax_scale, q_dtype, cache_dtype, 0, splits, workspace, workspace_bytes, stream);
 }

@@ -1035,13 +1035,14 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   const char* op = "single_query_cached_kv_attn";
   TORCH_CHECK(!q_quant_scale.has_value() && !out_quant_scale.has_value(), op,
               ": quantised q / output are not supported by this build");
-  TORCH_CHECK(!mask.has_value(), op, ": mask is not supported by this build");
   TORCH_CHECK(compute_dtype == "float" || compute_dtype == "half" || compute_dtype == "bfloat16",
               op, ": compute_dtype must be float, half or bfloat16 (the softmax runs in fp32)");
   TORCH_CHECK(windows_size_right.expect_int() == -1, op, ": windows_size_right must be -1");
-  TORCH_CHECK(kv_cache_quant_bit_size == -1 || kv_cache_quant_bit_size == 8, op,
-              ": kv_cache_quant_bit_size must be -1 or 8 (int8 / float8_e4m3fn), got ",
-              kv_cache_quant_bit_size);
+  TORCH_CHECK(kv_cache_quant_bit_size == -1 || kv_cache_quant_bit_size == 8 ||
+                  kv_cache_quant_bit_size == 4,
+              op, ": kv_cache_quant_bit_size must be -1, 8 (int8 / float8_e4m3fn) or 4 (int4 ",
+              "pairs in int8), got ", kv_cache_quant_bit_size);
+  const bool int4 = kv_cache_quant_bit_size == 4;
   check_device(q_ori, q_ori, "q");
   // q forms (reference _ops.py:824): [batch, seq_q, heads, head_size] (seq_q tokens for every
   // sequence), [total_q, heads, head_size] with cu_seq_q [batch + 1], or [batch, heads,
@@ -1111,7 +1112,32 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
               op, ": output must be q's shape with head_size_v channels, in q's dtype");
   const int64_t Dv = output.size(-1);
   int64_t vdim = kdim;
-  if (v_cache.has_value()) {
+  int v_pair_channels = 0;
+  if (int4) {
+    // int4 pairs (_ops.py:826-829, 852, 868): K [NB, Hkv, BS, D / 2] pairing channels; V
+    // pairing the rows of a page, [NB, Hkv, BS / 2, Dv] (the layout the reference's output
+    // allocation reads head_size_v from, _ops.py:887), or channels, [NB, Hkv, BS, Dv / 2]
+    TORCH_CHECK(k_cache.scalar_type() == at::kChar, op,
+                ": kv_cache_quant_bit_size 4 needs int8 caches of int4 pairs");
+    TORCH_CHECK(v_cache.has_value(), op, ": int4 caches need a separate v_cache");
+    const at::Tensor& vc = *v_cache;
+    check_device(vc, q_ori, "v_cache");
+    TORCH_CHECK(vc.dim() == 4 && vc.is_contiguous() && vc.size(0) == NB && vc.size(1) == Hkv &&
+                    vc.scalar_type() == at::kChar,
+                op, ": v_cache must be a contiguous int8 [num_blocks, kv_heads, ...] tensor");
+    TORCH_CHECK(2 * kdim == D, op, ": int4 k_cache's last dim must be head_size / 2 = ", D / 2,
+                ", got ", kdim);
+    vdim = vc.size(3);
+    if (2 * vc.size(2) == BS && vdim == Dv) {
+      v_pair_channels = 0;
+    } else if (vc.size(2) == BS && 2 * vdim == Dv) {
+      v_pair_channels = 1;
+    } else {
+      TORCH_CHECK(false, op, ": int4 v_cache must be [num_blocks, kv_heads, block_size / 2, ",
+                  "head_size_v] (row pairs) or [num_blocks, kv_heads, block_size, head_size_v / 2] ",
+                  "(channel pairs), got ", vc.sizes(), " with block_size ", BS, ", head_size_v ", Dv);
+    }
+  } else if (v_cache.has_value()) {
     const at::Tensor& vc = *v_cache;
     check_device(vc, q_ori, "v_cache");
     TORCH_CHECK(vc.dim() == 4 && vc.is_contiguous() && vc.size(0) == NB && vc.size(1) == Hkv &&
@@ -1128,11 +1154,11 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   TORCH_CHECK(Hkv > 0 && Hq % Hkv == 0, op, ": query heads ", Hq,
               " must be a multiple of the KV heads ", Hkv);
   TORCH_CHECK(D <= 4096 && Dv <= 512, op, ": head sizes up to 4096 (keys) and 512 (values)");
-  const int cdt = dtype_code(k_cache.scalar_type());
+  const int cdt = int4 ? TMO_DTYPE_I4 : dtype_code(k_cache.scalar_type());
   // quantised caches: int8 codes or float8_e4m3fn values (_ops.py:868; bit size 8 covers both,
-  // _ops.py:1061), with per-token / per-channel / per-group scales
-  const bool int8 = cdt == TMO_DTYPE_I8 || cdt == TMO_DTYPE_F8E4M3;
-  TORCH_CHECK(int8 == (kv_cache_quant_bit_size == 8), op,
+  // _ops.py:1061), or int4 pairs (bit size 4), with per-token / per-channel / per-group scales
+  const bool int8 = cdt == TMO_DTYPE_I8 || cdt == TMO_DTYPE_F8E4M3 || int4;
+  TORCH_CHECK(int4 || int8 == (kv_cache_quant_bit_size == 8), op,
               ": kv_cache_quant_bit_size 8 goes with int8 or float8_e4m3fn caches, -1 with caches ",
               "of q's dtype");
   TORCH_CHECK(int8 || cdt == qdt, op, ": unquantised caches must have q's dtype");
@@ -1234,6 +1260,34 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
     }
     lse = l.data_ptr<float>();
   }
+  // mask [batch, seq_q, mask_len] (_ops.py:860): logit terms for each sequence's last
+  // mask_len keys, in compute_dtype, within the reference's stated limits (seq_q <= 16,
+  // mask_len <= 64, mask_len % seq_q == 0, not with float32 q)
+  const void* mask_p = nullptr;
+  int mask_dt = TMO_DTYPE_F32;
+  int64_t mask_len = 0, m_sb = 0, m_ss = 0;
+  at::Tensor mk;
+  if (mask.has_value()) {
+    mk = *mask;
+    check_device(mk, q_ori, "mask");
+    const at::ScalarType want = compute_dtype == "float" ? at::kFloat
+                                : compute_dtype == "half" ? at::kHalf : at::kBFloat16;
+    TORCH_CHECK(mk.scalar_type() == want, op, ": mask must be of compute_dtype (", compute_dtype,
+                "), got ", mk.scalar_type());
+    TORCH_CHECK(qdt != TMO_DTYPE_F32, op, ": mask is not supported with float32 q");
+    TORCH_CHECK(mk.dim() == 3 && mk.size(0) == B && mk.size(1) == seq_q, op,
+                ": mask must be [batch, seq_q, mask_len] = [", B, ", ", seq_q, ", mask_len], got ",
+                mk.sizes());
+    mask_len = mk.size(2);
+    TORCH_CHECK(seq_q <= 16 && mask_len >= 1 && mask_len <= 64 && mask_len % seq_q == 0, op,
+                ": mask needs seq_q <= 16, 1 <= mask_len <= 64 and mask_len % seq_q == 0, got ",
+                "seq_q ", seq_q, ", mask_len ", mask_len);
+    if (mask_len > 1 && mk.stride(2) != 1) mk = mk.contiguous();
+    mask_p = mk.data_ptr();
+    mask_dt = dtype_code(mk.scalar_type());
+    m_sb = mk.stride(0);
+    m_ss = mk.stride(1);
+  }
   // max_context_len <= 0: an uncertain maximum (reference docstring); negative counts as 0
   const int64_t max_ctx = std::max<int64_t>(0, max_context_len.expect_int());
   const int64_t window = windows_size_left.expect_int();
@@ -1264,10 +1318,10 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
       int8 ? ks.data_ptr() : nullptr, int8 ? vs.data_ptr() : nullptr, smode,
       int8 && ks.scalar_type() == at::kBFloat16 ? TMO_DTYPE_BF16 : TMO_DTYPE_F32,
       ks_sb, ks_sh, vs_sb, vs_sh, block_tables.data_ptr<int32_t>(), block_tables.size(1),
-      context_lens.data_ptr<int32_t>(), alibi, sink_p, out.data_ptr(), o_sb, o_ss,
-      out.stride(-2), lse, lse_sb, lse_ss, lse_sh, B, Hq, Hkv, D, Dv, NB, BS, max_ctx, window,
-      static_cast<float>(softmax_scale), qdt, cdt, splits, ws_bytes > 0 ? ws.data_ptr() : nullptr,
-      ws_bytes, stream_of(q_ori));
+      context_lens.data_ptr<int32_t>(), alibi, sink_p, mask_p, mask_dt, mask_len, m_sb, m_ss,
+      out.data_ptr(), o_sb, o_ss, out.stride(-2), lse, lse_sb, lse_ss, lse_sh, B, Hq, Hkv, D, Dv,
+      NB, BS, max_ctx, window, static_cast<float>(softmax_scale), qdt, cdt, v_pair_channels,
+      splits, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(q_ori));
   check_status(st, op);
 }
 

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 15
+#define TMO_HIP_ABI_VERSION 16
 
 /* element types */
 enum tmo_dtype {
@@ -38,7 +38,9 @@ enum tmo_dtype {
     TMO_DTYPE_F16 = 1,
     TMO_DTYPE_BF16 = 2,
     TMO_DTYPE_I8 = 3,
-    TMO_DTYPE_F8E4M3 = 4 /* float8_e4m3fn: 1-4-3, bias 7, no infinities, max 448 */
+    TMO_DTYPE_F8E4M3 = 4, /* float8_e4m3fn: 1-4-3, bias 7, no infinities, max 448 */
+    TMO_DTYPE_I4 = 5      /* int8 storage of signed 4-bit pairs: the even element of a pair in
+                           * the high nibble, the odd one in the low nibble */
 };
 
 /* return codes */
@@ -457,10 +459,24 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
  *   3 per group (_ops.py:841-842): K [num_blocks, Hkv, block_size, head_size / 32] (one per
  *     token and 32 channels), V [num_blocks, Hkv, block_size / 32, head_size_v] (one per 32 rows
  *     of a page and channel), contiguous; head_size and block_size multiples of 32.
+ * int4 caches (cache_dtype TMO_DTYPE_I4; _ops.py:826-829, 852, "int8(pairwise-int4)" :868)
+ * hold two signed 4-bit codes per byte -- the even element of a pair in the high nibble, the
+ * odd one in the low nibble (the reference's unpack `byte >> 4`, `byte << 4 >> 4`,
+ * _ops.py:3681-3682) -- with the same scale modes.  Row lengths then count bytes: K
+ * [num_blocks, Hkv, block_size, k_cache_dim >= head_size / 2] pairs adjacent channels; V
+ * pairs adjacent rows of a page, [num_blocks, Hkv, block_size / 2, v_cache_dim >=
+ * head_size_v] with block_size even (v_pair_channels 0: the layout whose last dim is
+ * head_size_v, as the reference's own output allocation reads it, _ops.py:887, and
+ * fused_rope's v_cache_lp, _ops.py:3534), or adjacent channels, [num_blocks, Hkv, block_size,
+ * v_cache_dim >= head_size_v / 2] (v_pair_channels 1).  v_cache must not be null.
  * Other caches are of q's dtype (F32, F16 or BF16).  sink (nullable): [Hq] fp32 natural-log
- * logits.  Head sizes: head_size up to 4096, head_size_v up to 512; the MFMA kernels take K and
- * V head sizes and cache rows all equal to 64, 128 or 256 with per-token or per-channel
- * scales, a VALU kernel the rest.
+ * logits.  mask (nullable; _ops.py:860): logit terms of mask_dtype (F32, F16 or BF16) for the
+ * last mask_len keys of each sequence -- key j >= L - mask_len of query token s of sequence i
+ * gets s_j += mask[i * mask_stride_batch + s * mask_stride_token + j - (L - mask_len)] after
+ * softmax_scale and ALiBi (L clamped to the block table; -inf removes the key).  Head sizes:
+ * head_size up to 4096, head_size_v up to 512; the MFMA kernels take int8, float8_e4m3fn and
+ * unquantised K and V head sizes and cache rows all equal to 64, 128 or 256 with per-token or
+ * per-channel scales, a VALU kernel the rest (int4 caches included).
  * Arithmetic: fp32 accumulation (MFMA with bf16/f16 operands: int8 codes and e4m3fn values are
  * exact; q and the probabilities are split into two operands when one is not exact), softmax
  * in fp32.
@@ -469,7 +485,7 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
  * max_context_len <= 0 (negative included) means an unknown maximum: one split per sequence
  * unless `splits` says otherwise; it never limits the keys read.
  * Replaces tmo::torch_api::single_query_cached_kv_attn (reference
- * include/torch_mlu_ops.h:107-130) without q/out quantisation or mask, called by
+ * include/torch_mlu_ops.h:107-130) without q/out quantisation, called by
  * torch_mlu_ops.single_query_cached_kv_attn (reference _ops.py:777-900; q forms :824,
  * cu_seq_q / max_seq_q :860-861, sink :864).
  */
@@ -482,15 +498,17 @@ int tmo_hip_cached_kv_attn(const void* q, int64_t q_stride_batch, int64_t q_stri
                            int64_t k_scale_stride_head, int64_t v_scale_stride_block,
                            int64_t v_scale_stride_head, const int32_t* block_tables,
                            int64_t max_blocks, const int32_t* context_lens,
-                           const float* alibi_slopes, const float* sink, void* out,
+                           const float* alibi_slopes, const float* sink, const void* mask,
+                           int mask_dtype, int64_t mask_len, int64_t mask_stride_batch,
+                           int64_t mask_stride_token, void* out,
                            int64_t out_stride_batch, int64_t out_stride_token,
                            int64_t out_stride_head, float* lse, int64_t lse_stride_batch,
                            int64_t lse_stride_token, int64_t lse_stride_head, int64_t batch,
                            int64_t num_q_heads, int64_t num_kv_heads, int64_t head_size,
                            int64_t head_size_v, int64_t num_blocks, int64_t block_size,
                            int64_t max_context_len, int64_t window_left, float softmax_scale,
-                           int q_dtype, int cache_dtype, int64_t splits, void* workspace,
-                           int64_t workspace_bytes, void* stream);
+                           int q_dtype, int cache_dtype, int v_pair_channels, int64_t splits,
+                           void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes tmo_hip_cached_kv_attn needs for `splits` with up to seq_q tokens per
  * sequence (0 when splits <= 1). */

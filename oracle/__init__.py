@@ -72,9 +72,10 @@ def lib() -> ctypes.CDLL:
              c_int64, c_double, c_void_p, c_void_p, c_int]
         L.oracle_single_query_attn.restype = c_int
         L.oracle_cached_kv_attn.argtypes = [c_void_p, c_int, c_int64, c_int64, c_void_p,
-                                            c_int64, c_int64, c_void_p, c_void_p, c_int] + \
+                                            c_int64, c_int64, c_void_p, c_void_p, c_int, c_int] + \
             [c_int64] * 7 + [c_void_p, c_void_p, c_int] + [c_int64] * 4 + \
-            [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+            [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
+             c_void_p, c_int, c_int64, c_int64, c_int64, c_int64,
              c_double, c_void_p, c_void_p, c_int]
         L.oracle_cached_kv_attn.restype = c_int
         for name in ("oracle_f32_to_bf16", "oracle_f32_to_f16", "oracle_f16_to_f32",
@@ -314,7 +315,7 @@ def single_query_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_s
 def cached_kv_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scale: float,
                    k_scale=None, v_scale=None, alibi_slopes=None, window_left: int = -1,
                    cu_seq_q=None, sink=None, head_size_v: Optional[int] = None,
-                   nthreads: Optional[int] = None):
+                   int4: bool = False, mask=None, nthreads: Optional[int] = None):
     """reference _ops.py:777-900 with several query tokens per sequence (decision D12 of
     tmo_oracle.c), in float64.  q [B, S, Hq, D] (S tokens per sequence), or [T, Hq, D] with
     cu_seq_q [B + 1] (rows cu_seq_q[i] .. cu_seq_q[i + 1] - 1 are sequence i's), or [B, Hq, D]
@@ -325,7 +326,10 @@ def cached_kv_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scal
     token, [Hkv, D or Dv] per channel, or per group K [NB, Hkv, BS, D / 32] and V [NB, Hkv,
     BS / 32, Dv].  sink [Hq] or None.  Returns (out, lse) float64 of q's leading shape:
     [B, S, Hq, Dv] / [B, S, Hq] for 4-D q, [T, Hq, Dv] / [T, Hq] otherwise; rows that no
-    sequence of cu_seq_q holds are NaN."""
+    sequence of cu_seq_q holds are NaN.  int4 (kv_cache_quant_bit_size 4, decision D16): int8
+    caches of 4-bit pairs, K [NB, Hkv, BS, D / 2] pairing channels, V [NB, Hkv, BS / 2, Dv]
+    pairing rows or [NB, Hkv, BS, Dv / 2] pairing channels.  mask [B, S, mask_len] (float32 /
+    float16 / bfloat16, D16) is added to the logits of each sequence's last mask_len keys."""
     four = q.dim() == 4
     if four:
         B, S = q.shape[:2]
@@ -338,13 +342,21 @@ def cached_kv_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scal
     T, Hq, D = q.shape
     NB, Hkv, BS, krow = k_cache.shape
     vrow = vc.shape[3]
-    Dv = head_size_v if head_size_v is not None else (vrow if v_cache is not None else D)
-    cdt = _ATTN_CACHE_DT[k_cache.dtype]
+    v_ch = 0
+    if int4:
+        assert k_cache.dtype == torch.int8 and v_cache is not None
+        v_ch = int(vc.shape[2] == BS)    # else [NB, Hkv, BS / 2, Dv]: row pairs
+        assert v_ch or 2 * vc.shape[2] == BS
+        cdt = 5
+        Dv = head_size_v if head_size_v is not None else (2 * vrow if v_ch else vrow)
+    else:
+        Dv = head_size_v if head_size_v is not None else (vrow if v_cache is not None else D)
+        cdt = _ATTN_CACHE_DT[k_cache.dtype]
     mode = 0
     ks = vs = None
     strides = [0, 0, 0, 0]
     if k_cache.dtype in (torch.int8, torch.float8_e4m3fn):
-        def one(sc):
+        def one(sc):  # noqa: E306
             sc = sc.to(torch.float32)
             if sc.dim() == 4 and sc.shape[3] == 1:
                 sc = sc[..., 0]
@@ -361,12 +373,18 @@ def cached_kv_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scal
     assert cu is None or (not four and cu.numel() == B + 1)
     al = alibi_slopes.to(torch.float32).contiguous() if alibi_slopes is not None else None
     sk = sink.to(torch.float32).contiguous() if sink is not None else None
+    mk, mdt, mlen, msb, mss = None, 0, 0, 0, 0
+    if mask is not None:
+        mk = mask.contiguous()
+        assert mk.dim() == 3 and mk.shape[0] == B
+        mdt, mlen, msb, mss = _DT[mk.dtype], mk.shape[2], mk.stride(0), mk.stride(1)
     out = torch.full((T, Hq, Dv), float("nan"), dtype=torch.float64)
     lse = torch.full((T, Hq), float("nan"), dtype=torch.float64)
     rc = lib().oracle_cached_kv_attn(
         _ptr(q), _DT[q.dtype], q.stride(0), q.stride(1), _ptr(cu), S, T, _ptr(k_cache),
-        _ptr(vc), cdt, NB, Hkv, BS, D, Dv, krow, vrow, _ptr(ks), _ptr(vs), mode, *strides,
-        _ptr(bt), bt.shape[1], _ptr(lens), B, Hq, _ptr(al), _ptr(sk), int(window_left),
+        _ptr(vc), cdt, v_ch, NB, Hkv, BS, D, Dv, krow, vrow, _ptr(ks), _ptr(vs), mode, *strides,
+        _ptr(bt), bt.shape[1], _ptr(lens), B, Hq, _ptr(al), _ptr(sk), _ptr(mk), mdt, mlen, msb,
+        mss, int(window_left),
         float(softmax_scale), _ptr(out), _ptr(lse), nthreads or default_threads())
     _check(rc, "cached_kv_attn")
     if four:

@@ -89,6 +89,25 @@
  *       [p / 2, d] = (code of position 2 (p / 2), code of position 2 (p / 2) + 1) at channel
  *       d; writing one position leaves the other nibble of its byte as it was.  Scales stay
  *       one per (position, head) (or per group of D / group_num channels) for K and V.
+ *   D16 single_query_cached_kv_attn's int4 caches and mask (_ops.py:826-829, 852, 860, 868,
+ *       887).  kv_cache_quant_bit_size 4: int8 caches of signed 4-bit pairs in D15's nibble
+ *       order (even element high, odd low, sign-extending reads), k = code * scale as D12.
+ *       K pairs adjacent channels (k_cache [NB, Hkv, BS, D / 2], "cache_dim = head_size_qk //
+ *       2").  V pairs adjacent positions of a page, v_cache [NB, Hkv, BS / 2, Dv]: byte
+ *       [r / 2, d] holds rows 2 (r / 2) and 2 (r / 2) + 1 of channel d -- the layout whose last
+ *       dim is head_size_v, which the reference's own output allocation reads
+ *       (`head_size_v = v_cache.shape[-1]`, _ops.py:887; also
+ *       single_query_mixed_cached_kv_attn's, _ops.py:975, fed fused_rope's v_cache_lp
+ *       [.., max_decode_len / 2, head_size], _ops.py:3534); or, when v_cache is
+ *       [NB, Hkv, BS, Dv / 2] ("the same as k_cache, except cache_dim", _ops.py:830), pairs of
+ *       adjacent channels as K.  mask [batch, seq_q, mask_len] (_ops.py:860): an additive
+ *       logit term for the last mask_len keys of the sequence -- key j >= L - mask_len of
+ *       query token s gets s_j += mask[i, s, j - (L - mask_len)] after softmax_scale and
+ *       alibi (L the sequence's context length as clamped to its block table); -inf removes
+ *       the key.  The reference states the shape and limits (seq_q <= 16, mask_len <= 64,
+ *       mask_len % seq_q == 0) but not which keys the columns address: the last mask_len
+ *       keys -- the newest tokens, the ones a speculative-decoding tree mask covers -- is this
+ *       build's reading.
  *   D9  offline (static-scale) quantisation divides: code = clip(RNE(RN(fp32(x) / s)), -128, 127)
  *       for int8, fp8 = e4m3fn_RNE(clip(RN(fp32(x) / s), -448, 448)), s the fp32 per-channel
  *       scale or the per-tensor scalar rounded to fp32 (_ops.py:1652-1670; the division is
@@ -106,7 +125,8 @@
 #include <stdlib.h>
 #include <string.h>
 
-enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_I8 = 3, DT_F8E4M3 = 4 };
+/* DT_I4: int8 storage of signed 4-bit pairs (D15 / D16 nibble order) */
+enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_I8 = 3, DT_F8E4M3 = 4, DT_I4 = 5 };
 
 /* ------------------------------------------------------------------ conversions */
 
@@ -1120,19 +1140,23 @@ typedef struct {
     const void* q; int q_dtype; int64_t q_st, q_sh;      /* q rows [T, Hq, D], element strides */
     const int32_t* cu; int64_t S, T;                     /* cu_seq_q [B + 1], or S tokens each */
     const void* kc; const void* vc; int c_dtype;         /* caches [NB, Hkv, BS, krow / vrow] */
+    int v_ch;                                            /* DT_I4: V pairs channels (else rows) */
     int64_t NB, Hkv, BS, D, Dv, krow, vrow, Hq, MB, B;
     const float* ks; const float* vs; int smode;         /* 0 none, 1 token, 2 channel, 3 group */
     int64_t ks_sb, ks_sh, vs_sb, vs_sh;                  /* per-token scale strides */
     const int32_t* bt; const int32_t* lens;
     const float* alibi; const float* sink; int64_t window; double scale;
+    const void* mask; int mask_dtype; int64_t mask_len, m_sb, m_ss;  /* D16, or mask NULL */
     double* out; double* lse;                            /* [T, Hq, Dv], [T, Hq] */
 } sqa_ctx;
 
 /* Key channel d (< D) of row `row` of page blk, KV head hk: the first D of the row's krow. */
 static double key_val(const sqa_ctx* c, int64_t blk, int64_t hk, int64_t row, int64_t d) {
     const int64_t r = (blk * c->Hkv + hk) * c->BS + row;
-    if (c->c_dtype == DT_I8 || c->c_dtype == DT_F8E4M3) {
-        double code = cache_code(c->kc, r * c->krow + d, c->c_dtype);
+    if (c->c_dtype == DT_I8 || c->c_dtype == DT_F8E4M3 || c->c_dtype == DT_I4) {
+        double code = c->c_dtype == DT_I4
+                          ? (double)get_nibble(((const uint8_t*)c->kc)[r * c->krow + d / 2], (int)(d & 1))
+                          : cache_code(c->kc, r * c->krow + d, c->c_dtype);
         if (c->smode == 1) return code * (double)c->ks[blk * c->ks_sb + hk * c->ks_sh + row];
         if (c->smode == 2) return code * (double)c->ks[hk * c->D + d];
         if (c->smode == 3) return code * (double)c->ks[r * (c->D / 32) + d / 32];
@@ -1144,8 +1168,15 @@ static double key_val(const sqa_ctx* c, int64_t blk, int64_t hk, int64_t row, in
 /* Value channel d (< Dv): per-group V scales hold one number per 32 rows of a page and channel. */
 static double value_val(const sqa_ctx* c, int64_t blk, int64_t hk, int64_t row, int64_t d) {
     const int64_t r = (blk * c->Hkv + hk) * c->BS + row;
-    if (c->c_dtype == DT_I8 || c->c_dtype == DT_F8E4M3) {
-        double code = cache_code(c->vc, r * c->vrow + d, c->c_dtype);
+    if (c->c_dtype == DT_I8 || c->c_dtype == DT_F8E4M3 || c->c_dtype == DT_I4) {
+        double code;
+        if (c->c_dtype != DT_I4)
+            code = cache_code(c->vc, r * c->vrow + d, c->c_dtype);
+        else if (c->v_ch)  /* D16: channel pairs */
+            code = get_nibble(((const uint8_t*)c->vc)[r * c->vrow + d / 2], (int)(d & 1));
+        else               /* D16: row pairs [NB, Hkv, BS / 2, vrow] */
+            code = get_nibble(((const uint8_t*)c->vc)[((blk * c->Hkv + hk) * (c->BS / 2) + row / 2) * c->vrow + d],
+                              (int)(row & 1));
         if (c->smode == 1) return code * (double)c->vs[blk * c->vs_sb + hk * c->vs_sh + row];
         if (c->smode == 2) return code * (double)c->vs[hk * c->Dv + d];
         if (c->smode == 3)
@@ -1196,6 +1227,9 @@ static void sqa_range(void* p, int64_t lo, int64_t hi) {
                        key_val(c, blk, hk, row, d);
             s[j] = c->scale * acc;
             if (c->alibi) s[j] += (double)c->alibi[i * c->Hq + hq] * (double)(j - P);
+            if (c->mask && j >= L - c->mask_len)   /* D16: the last mask_len keys */
+                s[j] += (double)load_elem(c->mask, i * c->m_sb + tok * c->m_ss + (j - (L - c->mask_len)),
+                                          c->mask_dtype);
             if (s[j] > m) m = s[j];
         }
         double l = 0.0;
@@ -1230,31 +1264,43 @@ static void sqa_range(void* p, int64_t lo, int64_t hi) {
  * the stored value.  Query head hq reads KV head hq / (Hq / Hkv).  Query rows: q [T, Hq, D] with row t
  * at t * q_st; cu_seq_q null: S tokens per sequence, sequence i's at rows i S .. i S + S - 1
  * (T = B S); else rows cu_seq_q[i] .. cu_seq_q[i + 1] - 1 (rows of no sequence untouched).
- * No key: out 0, lse = sink or -inf.  out [T, Hq, Dv], lse [T, Hq]. */
+ * No key: out 0, lse = sink or -inf.  out [T, Hq, Dv], lse [T, Hq].
+ * DT_I4 caches (D16): k_row / v_row count bytes; K pairs channels, V pairs the rows of a page
+ * ([NB, Hkv, BS / 2, v_row], v_ch 0) or channels (v_ch 1).  mask (D16, nullable): element
+ * i * mask_sb + s * mask_ss + m of mask_dtype (F32 / F16 / BF16) is added to the logit of key
+ * L - mask_len + m of query token s of sequence i. */
 int oracle_cached_kv_attn(const void* q, int q_dtype, int64_t q_st, int64_t q_sh,
                           const int32_t* cu_seq_q, int64_t S, int64_t T,
-                          const void* k_cache, const void* v_cache, int cache_dtype,
+                          const void* k_cache, const void* v_cache, int cache_dtype, int v_ch,
                           int64_t NB, int64_t Hkv, int64_t BS, int64_t D, int64_t Dv,
                           int64_t k_row, int64_t v_row,
                           const float* k_scale, const float* v_scale, int scale_mode,
                           int64_t ks_sb, int64_t ks_sh, int64_t vs_sb, int64_t vs_sh,
                           const int32_t* block_tables, int64_t max_blocks,
                           const int32_t* context_lens, int64_t B, int64_t Hq,
-                          const float* alibi, const float* sink, int64_t window_left,
-                          double softmax_scale, double* out, double* lse, int nthreads) {
-    const int quant = cache_dtype == DT_I8 || cache_dtype == DT_F8E4M3;
+                          const float* alibi, const float* sink, const void* mask,
+                          int mask_dtype, int64_t mask_len, int64_t mask_sb, int64_t mask_ss,
+                          int64_t window_left, double softmax_scale, double* out, double* lse,
+                          int nthreads) {
+    const int quant = cache_dtype == DT_I8 || cache_dtype == DT_F8E4M3 || cache_dtype == DT_I4;
     if (elem_size(q_dtype) == 0 || q_dtype == DT_I8 || (!quant && elem_size(cache_dtype) == 0))
         return -2;
     if (quant && (scale_mode < 1 || scale_mode > 3)) return -3;
     if (B < 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || BS <= 0 || D <= 0 || Dv <= 0 ||
-        k_row < D || v_row < Dv || max_blocks < 0 || T < 0 ||
+        (cache_dtype != DT_I4 && (k_row < D || v_row < Dv)) || max_blocks < 0 || T < 0 ||
         (!cu_seq_q && (S <= 0 || T != B * S)))
         return -1;
     if (quant && scale_mode == 3 && (D % 32 != 0 || BS % 32 != 0)) return -1;
-    sqa_ctx c = {q, q_dtype, q_st, q_sh, cu_seq_q, S, T, k_cache, v_cache, cache_dtype, NB, Hkv,
+    if (cache_dtype == DT_I4 && (k_row * 2 < D || (v_ch ? v_row * 2 < Dv : (v_row < Dv || BS % 2 != 0))))
+        return -1;
+    if (mask && (mask_len < 0 || (mask_dtype != DT_F32 && mask_dtype != DT_F16 && mask_dtype != DT_BF16)))
+        return -1;
+    sqa_ctx c = {q, q_dtype, q_st, q_sh, cu_seq_q, S, T, k_cache, v_cache, cache_dtype,
+                 cache_dtype == DT_I4 && v_ch, NB, Hkv,
                  BS, D, Dv, k_row, v_row, Hq, max_blocks, B, k_scale, v_scale,
                  quant ? scale_mode : 0, ks_sb, ks_sh, vs_sb, vs_sh,
-                 block_tables, context_lens, alibi, sink, window_left, softmax_scale, out, lse};
+                 block_tables, context_lens, alibi, sink, window_left, softmax_scale,
+                 mask, mask_dtype, mask_len, mask_sb, mask_ss, out, lse};
     parallel_for(T * Hq, nthreads, sqa_range, &c);
     return 0;
 }
@@ -1270,9 +1316,10 @@ int oracle_single_query_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q
                              const float* alibi, int64_t window_left, double softmax_scale,
                              double* out, double* lse, int nthreads) {
     if (scale_mode == 3) return -3;
+    if (cache_dtype == DT_I4) return -2;
     return oracle_cached_kv_attn(q, q_dtype, q_sb, q_sh, NULL, 1, B < 0 ? 0 : B, k_cache,
-                                 v_cache, cache_dtype, NB, Hkv, BS, D, D, D, D, k_scale, v_scale,
+                                 v_cache, cache_dtype, 0, NB, Hkv, BS, D, D, D, D, k_scale, v_scale,
                                  scale_mode, Hkv * BS, BS, Hkv * BS, BS, block_tables,
-                                 max_blocks, context_lens, B, Hq, alibi, NULL, window_left,
-                                 softmax_scale, out, lse, nthreads);
+                                 max_blocks, context_lens, B, Hq, alibi, NULL, NULL, 0, 0, 0, 0,
+                                 window_left, softmax_scale, out, lse, nthreads);
 }

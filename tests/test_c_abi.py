@@ -61,9 +61,11 @@ def lib():
     L.tmo_hip_attn_workspace_bytes.argtypes = [I64] * 6
     L.tmo_hip_attn_workspace_bytes.restype = I64
     L.tmo_hip_cached_kv_attn.argtypes = [P, I64, I64, I64, P, I64, I64, P, P, I64, I64, P, P, INT,
-                                         INT, I64, I64, I64, I64, P, I64, P, P, P, P, I64, I64, I64,
+                                         INT, I64, I64, I64, I64, P, I64, P, P, P,
+                                         P, INT, I64, I64, I64,
+                                         P, I64, I64, I64,
                                          P, I64, I64, I64] + [I64] * 9 + \
-        [ctypes.c_float, INT, INT, I64, P, I64, P]
+        [ctypes.c_float, INT, INT, INT, I64, P, I64, P]
     L.tmo_hip_cached_kv_attn_workspace_bytes.argtypes = [I64] * 6
     L.tmo_hip_cached_kv_attn_workspace_bytes.restype = I64
     return L
@@ -372,11 +374,13 @@ def test_attention_validation(lib):
 def test_multi_token_attention_validation(lib):
     def call(q=FAKE, cu=None, S=4, T=0, B=2, Hq=8, Hkv=2, D=128, Dv=128, kdim=128, vdim=128,
              vc=FAKE, smode=1, ssb=32, BS=16, splits=1, ws=None, wsb=0, qdt=2, cdt=3,
-             qss=128 * 8, oss=128 * 8, sink=None, sdt=0):
+             qss=128 * 8, oss=128 * 8, sink=None, sdt=0, mask=None, mdt=0, mlen=8, msb=32,
+             mss=8, vch=0, NB=16):
         return lib.tmo_hip_cached_kv_attn(
             q, 4 * 1024, qss, 128, cu, S, T, FAKE, vc, kdim, vdim, FAKE, FAKE, smode, sdt, ssb, 16,
-            32, 16, FAKE, 4, FAKE, None, sink, FAKE, 4 * 1024, oss, 128, None, 0, 0, 0, B, Hq,
-            Hkv, D, Dv, 16, BS, 64, -1, 0.1, qdt, cdt, splits, ws, wsb, None)
+            32, 16, FAKE, 4, FAKE, None, sink, mask, mdt, mlen, msb, mss, FAKE, 4 * 1024, oss,
+            128, None, 0, 0, 0, B, Hq, Hkv, D, Dv, NB, BS, 64, -1, 0.1, qdt, cdt, vch, splits, ws,
+            wsb, None)
     assert call(qdt=3) == EDTYPE
     assert call(smode=4) == EMODE and call(smode=0) == EMODE
     assert call(sdt=1) == EDTYPE                   # scales: fp32 or bf16
@@ -406,4 +410,21 @@ def test_multi_token_attention_validation(lib):
     assert call(splits=3, ws=FAKE, wsb=need - 4) == EINVAL
     assert call(B=0) == 0 and call(S=0) == 0       # nothing to compute
     assert call(S=0, cu=FAKE, T=5, sink=FAKE) == 0
+    # mask: float32 / float16 / bfloat16 logit terms, a positive length, non-negative strides
+    assert call(mask=FAKE, mdt=2, B=0) == 0 and call(mask=FAKE, mdt=1, B=0) == 0
+    assert call(mask=FAKE, mdt=3) == EDTYPE and call(mask=FAKE, mdt=4) == EDTYPE
+    assert call(mask=FAKE, mlen=0) == EINVAL and call(mask=FAKE, msb=-1) == EINVAL
+    assert call(mask=FAKE, mss=-1) == EINVAL
+    assert call(mask=None, mdt=9, mlen=-5, B=0) == 0            # ignored without a mask
+    # int4 pairs (cdt 5): K rows of head_size / 2 bytes; V rows pairs (block_size / 2 rows of
+    # head_size_v bytes, block_size even) or channel pairs (head_size_v / 2 bytes)
+    assert call(cdt=5, kdim=64, vdim=128, B=0) == 0
+    assert call(cdt=5, kdim=64, vdim=64, vch=1, B=0) == 0
+    assert call(cdt=5, kdim=63, vdim=128) == EINVAL             # K row under head_size / 2
+    assert call(cdt=5, kdim=64, vdim=64) == EINVAL              # row pairs need head_size_v bytes
+    assert call(cdt=5, kdim=64, vdim=63, vch=1) == EINVAL
+    assert call(cdt=5, kdim=64, vdim=128, BS=15) == EINVAL      # odd block_size: no row pairs
+    assert call(cdt=5, kdim=64, vdim=128, vc=None) == EINVAL    # int4 needs its own V cache
+    assert call(cdt=5, kdim=64, vdim=128, vc=None, NB=0, B=0) == 0
+    assert call(cdt=5, kdim=64, vdim=128, smode=0) == EMODE     # int4 codes need scales
 

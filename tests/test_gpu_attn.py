@@ -17,7 +17,9 @@ D] and the 3-D q with cu_seq_q, causal within the new tokens) and the sink are h
 same bar against the oracle's cached_kv_attn, with rows of no sequence left untouched; so are
 the other cache forms: K and V in one cache (v_cache None, value head size below, equal to or
 above the key's, a 576 / 512 latent-cache shape), value head sizes other than the key's,
-per-group scales and per-token scales with strides in their first two dims.
+per-group scales and per-token scales with strides in their first two dims; and so are int4
+pair caches (V pairing rows or channels) and masks (terms for the last mask_len keys, decision
+D16 of oracle/tmo_oracle.c) on the MFMA and generic kernels, over splits.
 """
 import math
 
@@ -34,8 +36,11 @@ ATOL = {torch.bfloat16: 2.0 ** -14, torch.float16: 2.0 ** -14, torch.float32: 2.
 
 def _vmax(case, vs, Dv=None):
     """The largest |v| entry: the first Dv channels of the V cache (of the K cache when the
-    case has none), dequantised."""
-    v = (case.k_cache if case.v_cache is None else case.v_cache).double()
+    case has none), dequantised (int4 pairs unpacked first)."""
+    v = (case.k_cache if case.v_cache is None else case.v_cache)
+    if case.int4:
+        v = W.unpack_int4(v, 2 if 2 * v.shape[2] == case.k_cache.shape[2] else 3)
+    v = v.double()
     if Dv is not None:
         v = v[..., :Dv]
     if vs is not None:
@@ -257,18 +262,25 @@ def test_attn_decode_on_configs4_pages(tmo, ref, dev):
 
 
 def run_attn_mq(tmo, ref, dev, case, q, cu=None, sink=None, scale=0.0883883, window=-1,
-                max_seq_q=-1, max_ctx=None, with_lse=True, Dv=None):
+                max_seq_q=-1, max_ctx=None, with_lse=True, Dv=None, mask=None,
+                compute_dtype=torch.float32):
     """Several query tokens per sequence: q [B, S, Hq, D] or [T, Hq, D] with cu.  The output
     ([..., Dv], Dv the V cache's head size or q's by default) starts as a sentinel, which rows
-    of no sequence must keep.  case.v_cache None: K and V in one cache."""
+    of no sequence must keep.  case.v_cache None: K and V in one cache.  case.int4: int4-pair
+    caches (kv_cache_quant_bit_size 4).  mask [B, S, mask_len] in compute_dtype."""
     kbit = 8 if case.k_cache.dtype in (torch.int8, torch.float8_e4m3fn) else -1
+    if case.int4:
+        kbit = 4
+        v_ch = case.v_cache.shape[2] == case.k_cache.shape[2]
+        Dv = Dv or case.v_cache.shape[-1] * (2 if v_ch else 1)
     Dv = Dv or (case.v_cache.shape[-1] if case.v_cache is not None else q.shape[-1])
     cpu = lambda t: t.cpu() if t is not None else None            # noqa: E731
     on_dev = lambda t: t if t is None or t.is_cuda else t.to(dev)  # noqa: E731  (views kept)
     ks, vs = cpu(case.k_scale), cpu(case.v_scale)
     want, wlse = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables,
                                     case.context_lens, scale, ks, vs, case.alibi, window,
-                                    cu_seq_q=cu, sink=sink, head_size_v=Dv)
+                                    cu_seq_q=cu, sink=sink, head_size_v=Dv, int4=case.int4,
+                                    mask=mask)
     out = torch.full(q.shape[:-1] + (Dv,), 7.0, dtype=q.dtype, device=dev)
     res = tmo.single_query_cached_kv_attn(
         q.to(dev), case.k_cache.to(dev),
@@ -277,7 +289,8 @@ def run_attn_mq(tmo, ref, dev, case, q, cu=None, sink=None, scale=0.0883883, win
         on_dev(case.v_scale),
         case.alibi.to(dev) if case.alibi is not None else None,
         case.max_context_len if max_ctx is None else max_ctx, window, -1, scale,
-        return_lse=with_lse, kv_cache_quant_bit_size=kbit,
+        return_lse=with_lse, kv_cache_quant_bit_size=kbit, compute_dtype=compute_dtype,
+        mask=mask.to(dev) if mask is not None else None,
         cu_seq_q=cu.to(dev) if cu is not None else None, max_seq_q=max_seq_q,
         sink=sink.to(dev) if sink is not None else None)
     torch.cuda.synchronize()
@@ -465,3 +478,99 @@ def test_attn_strided_token_scales(tmo, ref, dev, pad):
     strided = W.AttnCase(case.q, case.k_cache, case.v_cache, *views, case.block_tables,
                          case.context_lens)
     run_attn_mq(tmo, ref, dev, strided, q)
+
+
+# ---------------------------------------------------------------------------- int4 caches, mask
+
+@pytest.mark.parametrize("v_pairs", ["rows", "channels"])
+@pytest.mark.parametrize("kv", ["int4_token", "int4_channel", "int4_group"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_attn_int4_caches(tmo, ref, dev, dtype, kv, v_pairs):
+    """kv_cache_quant_bit_size 4: int8 caches of int4 pairs, K pairing channels, V pairing the
+    rows of a page or channels; per-token / per-channel / per-group scales; one and several
+    query tokens (4-D and cu_seq_q), a sink, a window, ALiBi and a missing page."""
+    BS = 32 if kv == "int4_group" else 16
+    case = W.attn_case(dtype, 91, kv=kv, B=5, Hq=8, Hkv=2, D=128, BS=BS, NB=64, max_ctx=180,
+                       v_pairs=v_pairs)
+    case.block_tables[2, 1] = -1
+    for S in (1, 3):
+        q = W.attn_queries(dtype, 92 + S, B=5, Hq=8, D=128, S=S)
+        run_attn_mq(tmo, ref, dev, case, q, sink=SINK8 if S == 3 else None)
+    q3, cu = W.attn_queries(dtype, 96, B=5, Hq=8, D=128, counts=[4, 1, 0, 2, 6])
+    case.alibi = (0.5 ** torch.arange(1, 9, dtype=torch.float32)).repeat(5, 1)
+    run_attn_mq(tmo, ref, dev, case, q3, cu=cu, window=40)
+
+
+def test_attn_int4_long_contexts(tmo, ref, dev):
+    """int4 pages over a few thousand keys, 32 query heads over 8 KV heads, with splits."""
+    case = W.attn_case(torch.bfloat16, 97, kv="int4_token", B=3, Hq=32, Hkv=8, D=128, BS=16,
+                       NB=800, max_ctx=4000)
+    q = W.attn_queries(torch.bfloat16, 98, B=3, Hq=32, D=128, S=1)
+    run_attn_mq(tmo, ref, dev, case, q)
+
+
+def _mask(seed, B, S, ml, dtype, neg_inf_every=7):
+    g = torch.Generator().manual_seed(seed)
+    m = torch.randn(B, S, ml, generator=g) * 2
+    m.view(-1)[::neg_inf_every] = float("-inf")
+    return m.to(dtype)
+
+
+@pytest.mark.parametrize("D", [128, 64, 96])
+@pytest.mark.parametrize("kv", ["int8_token", "int8_channel", "plain", "fp8_token"])
+def test_attn_mask(tmo, ref, dev, kv, D):
+    """mask [batch, seq_q, mask_len] in compute_dtype: float32, bfloat16 and float16 terms for
+    the last mask_len keys, -inf entries removing keys; the MFMA kernels (D 64 / 128) and the
+    generic one (D 96); 4-D q and cu_seq_q, with a sink, a window and ALiBi."""
+    dtype = torch.bfloat16
+    case = W.attn_case(dtype, 101, kv=kv, B=5, Hq=8, Hkv=2, D=D, NB=64, max_ctx=180)
+    case.block_tables[3, 0] = -1
+    q4 = W.attn_queries(dtype, 102, B=5, Hq=8, D=D, S=4)
+    for ml, cdt in ((4, torch.float32), (16, torch.bfloat16), (64, torch.float16)):
+        mask = _mask(103 + ml, 5, 4, ml, cdt)
+        run_attn_mq(tmo, ref, dev, case, q4, mask=mask, compute_dtype=cdt,
+                    sink=SINK8 if ml == 16 else None)
+    q3, cu = W.attn_queries(dtype, 104, B=5, Hq=8, D=D, counts=[2, 1, 0, 2, 2])
+    case.alibi = (0.5 ** torch.arange(1, 9, dtype=torch.float32)).repeat(5, 1)
+    mask = _mask(105, 5, 2, 8, torch.float32)
+    run_attn_mq(tmo, ref, dev, case, q3, cu=cu, max_seq_q=2, mask=mask, window=30)
+
+
+def test_attn_mask_over_splits_and_int4(tmo, ref, dev):
+    """A mask over the last 64 keys of contexts long enough to be split over several
+    workgroups (the mask terms land in the last split), and a mask on int4 pages."""
+    case = W.attn_case(torch.float16, 106, kv="int8_token", B=3, Hq=32, Hkv=8, D=128, BS=16,
+                       NB=800, max_ctx=4000)
+    q = W.attn_queries(torch.float16, 107, B=3, Hq=32, D=128, S=2)
+    run_attn_mq(tmo, ref, dev, case, q, mask=_mask(108, 3, 2, 64, torch.float16),
+                compute_dtype=torch.float16)
+    c4 = W.attn_case(torch.bfloat16, 109, kv="int4_channel", B=4, Hq=8, Hkv=2, D=128,
+                     max_ctx=100)
+    q = W.attn_queries(torch.bfloat16, 110, B=4, Hq=8, D=128, S=2)
+    run_attn_mq(tmo, ref, dev, c4, q, mask=_mask(111, 4, 2, 32, torch.float32))
+
+
+def test_attn_mask_and_int4_rejections(tmo, dev):
+    """The reference's stated limits raise: mask_len above 64 or not a multiple of seq_q, a
+    mask dtype other than compute_dtype, float32 q with a mask; int4 caches of the wrong
+    shapes."""
+    case = W.attn_case(torch.bfloat16, 112, kv="int8_token", B=2, Hq=4, Hkv=2, D=64, max_ctx=40)
+    q = W.attn_queries(torch.bfloat16, 113, B=2, Hq=4, D=64, S=2).to(dev)
+    args = lambda c: (c.k_cache.to(dev), c.v_cache.to(dev), None, c.block_tables.to(dev),  # noqa: E731
+                      c.context_lens.to(dev), c.k_scale.to(dev), c.v_scale.to(dev), None, 40,
+                      -1, -1, 0.1)
+    for m, cdt in ((torch.zeros(2, 2, 66), torch.float32), (torch.zeros(2, 2, 3), torch.float32),
+                   (torch.zeros(2, 2, 8), torch.bfloat16), (torch.zeros(2, 3, 8), torch.float32)):
+        with pytest.raises(RuntimeError):
+            tmo.single_query_cached_kv_attn(q, *args(case), kv_cache_quant_bit_size=8,
+                                            mask=m.to(dev), compute_dtype=cdt)
+    with pytest.raises(RuntimeError):
+        tmo.single_query_cached_kv_attn(q.float(), *args(case), kv_cache_quant_bit_size=8,
+                                        mask=torch.zeros(2, 2, 8, device=dev))
+    c4 = W.attn_case(torch.bfloat16, 114, kv="int4_token", B=2, Hq=4, Hkv=2, D=64, max_ctx=40)
+    with pytest.raises(RuntimeError):                # int8-shaped pages read as int4
+        tmo.single_query_cached_kv_attn(q, *args(case), kv_cache_quant_bit_size=4)
+    bad = W.AttnCase(c4.q, c4.k_cache, c4.v_cache[:, :, :4].contiguous(), c4.k_scale,
+                     c4.v_scale, c4.block_tables, c4.context_lens, int4=True)
+    with pytest.raises(RuntimeError):                # V neither row nor channel pairs
+        tmo.single_query_cached_kv_attn(q, *args(bad), kv_cache_quant_bit_size=4)

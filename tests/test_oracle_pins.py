@@ -1445,14 +1445,15 @@ def test_attn_closed_forms(ref):
     assert torch.allclose(out[0], V[-1].expand(2, 16), rtol=0, atol=1e-300)
 
 
-def torch_attn_mq(case, q, scale, window=-1, cu=None, sink=None, Dv=None):
+def torch_attn_mq(case, q, scale, window=-1, cu=None, sink=None, Dv=None, mask=None):
     """_ops.py:786-800 for several query tokens per sequence, in float64 by torch: every
     sequence's keys dequantised through its block table, a [heads, tokens, keys] logit matrix
     with query token s of nq at position P = L - nq + s seeing keys j in [P - window, P], ALiBi
     slope * (j - P), the sink as an extra logit column whose value row is zero.  q [B, S, Hq,
     D], or [T, Hq, D] with cu [B + 1]; keys the first D channels of k_cache rows, values the
-    first Dv of v_cache rows (k_cache's when v_cache is None); returns out / lse shaped like
-    q's leading dims (rows of no sequence NaN)."""
+    first Dv of v_cache rows (k_cache's when v_cache is None); mask [B, S, mask_len] adds
+    mask[i, s, m] to key L - mask_len + m of token s (decision D16); returns out / lse shaped
+    like q's leading dims (rows of no sequence NaN)."""
     kc, bt = case.k_cache, case.block_tables
     vc = kc if case.v_cache is None else case.v_cache
     NB, Hkv, BS, _ = kc.shape
@@ -1495,6 +1496,12 @@ def torch_attn_mq(case, q, scale, window=-1, cu=None, sink=None, Dv=None):
         P = L - nq + torch.arange(nq)
         if case.alibi is not None:
             s = s + case.alibi[i].double()[:, None, None] * (j[None, :] - P[:, None]).double()[None]
+        if mask is not None:
+            col = j - (L - mask.shape[2])
+            sel = col >= 0
+            add = torch.zeros(nq, j.numel(), dtype=torch.float64)
+            add[:, sel] = mask[i, :nq][:, col[sel]].double()
+            s = s + add[None]
         ok = (j[None, :] <= P[:, None]) & keep[None, :]
         if window >= 0:
             ok &= j[None, :] >= P[:, None] - window
@@ -1663,4 +1670,144 @@ def test_attn_cache_form_identities(ref):
                            0.1, ks_grp, vs_grp)
     b = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables, case.context_lens,
                            0.1, case.k_scale, vs_tok)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+# ---------------------------------------------------------------------------- int4 caches, mask (D16)
+
+def _unpack_ref(b: torch.Tensor, dim: int) -> torch.Tensor:
+    """The reference's own unpack expression on int8 bytes (_ops.py:3681-3682:
+    `unpack[0::2] = byte >> 4; unpack[1::2] = byte << 4 >> 4`), pairs along `dim`."""
+    b = b.movedim(dim, -1)
+    out = torch.empty(b.shape[:-1] + (2 * b.shape[-1],), dtype=torch.int8)
+    out[..., 0::2] = b >> 4
+    out[..., 1::2] = b << 4 >> 4
+    return out.movedim(-1, dim).contiguous()
+
+
+def _int4_codes(case, v_pairs):
+    """The case with its int4 pages unpacked by the reference's expression: int8 codes."""
+    kc = _unpack_ref(case.k_cache, 3)
+    vc = _unpack_ref(case.v_cache, 2 if v_pairs == "rows" else 3)
+    return W.AttnCase(case.q, kc, vc, case.k_scale, case.v_scale, case.block_tables,
+                      case.context_lens, case.alibi)
+
+
+@pytest.mark.parametrize("v_pairs", ["rows", "channels"])
+@pytest.mark.parametrize("kv", ["int4_token", "int4_channel", "int4_group"])
+def test_attn_int4_matches_torch_float64(ref, kv, v_pairs):
+    """int4 caches (kv_cache_quant_bit_size 4, _ops.py:826-829, 852): the pages unpacked by the
+    reference's own expression, dequantised and attended in float64 by torch, against the
+    oracle reading the packed pages -- V pairing rows ([NB, Hkv, BS / 2, Dv]) and channels
+    ([NB, Hkv, BS, Dv / 2]); several query tokens, windows, ALiBi, a sink, a missing page."""
+    BS = 32 if kv == "int4_group" else 16
+    case = W.attn_case(torch.bfloat16, 61, kv=kv, Hq=8, Hkv=2, D=64, BS=BS, max_ctx=70,
+                       v_pairs=v_pairs)
+    case.block_tables[2, 1] = -1
+    codes = _int4_codes(case, v_pairs)
+    q4 = W.attn_queries(torch.bfloat16, 62, B=5, Hq=8, D=64, S=3)
+    q3, cu = W.attn_queries(torch.bfloat16, 63, B=5, Hq=8, D=64, counts=[4, 2, 0, 7, 1])
+    sink = torch.linspace(-2.0, 1.0, 8)
+    for window, alibi, sk in ((-1, False, None), (9, False, sink), (-1, True, sink)):
+        al = (0.5 ** torch.arange(1, 9, dtype=torch.float32)).repeat(5, 1) if alibi else None
+        case.alibi = codes.alibi = al
+        for q, c in ((q4, None), (q3, cu)):
+            out, lse = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables,
+                                          case.context_lens, 0.125, case.k_scale, case.v_scale,
+                                          al, window, cu_seq_q=c, sink=sk, int4=True)
+            want, wlse = torch_attn_mq(codes, q, 0.125, window, c, sk)
+            assert out.shape == want.shape
+            assert torch.allclose(out, want, rtol=1e-12, atol=1e-12, equal_nan=True)
+            assert torch.allclose(lse, wlse, rtol=1e-12, atol=1e-12, equal_nan=True)
+
+
+def test_attn_int4_identities(ref):
+    """An int4 cache equals the int8 cache of its unpacked codes bit for bit (the codes are
+    read, nothing else changes); the two V layouts of the same codes agree bit for bit."""
+    rows = W.attn_case(torch.float16, 64, kv="int4_token", B=4, Hq=4, Hkv=2, D=32, max_ctx=60)
+    codes = _int4_codes(rows, "rows")
+    vch = W.pack_int4(codes.v_cache, 3)
+    q = W.attn_queries(torch.float16, 65, B=4, Hq=4, D=32, S=2)
+    a = ref.cached_kv_attn(q, rows.k_cache, rows.v_cache, rows.block_tables, rows.context_lens,
+                           0.2, rows.k_scale, rows.v_scale, int4=True)
+    b = ref.cached_kv_attn(q, codes.k_cache, codes.v_cache, rows.block_tables,
+                           rows.context_lens, 0.2, rows.k_scale, rows.v_scale)
+    c = ref.cached_kv_attn(q, rows.k_cache, vch, rows.block_tables, rows.context_lens, 0.2,
+                           rows.k_scale, rows.v_scale, int4=True)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    assert torch.equal(a[0], c[0]) and torch.equal(a[1], c[1])
+    assert int(codes.k_cache.min()) == -8 and int(codes.k_cache.max()) == 7
+
+
+def _mask(seed, B, S, ml, dtype=torch.float32, neg_inf_every=0):
+    g = torch.Generator().manual_seed(seed)
+    m = torch.randn(B, S, ml, generator=g) * 2
+    if neg_inf_every:
+        m.view(-1)[::neg_inf_every] = float("-inf")
+    return m.to(dtype)
+
+
+@pytest.mark.parametrize("kv", ["int8_token", "plain", "int4_channel"])
+def test_attn_mask_matches_torch_float64(ref, kv):
+    """mask [batch, seq_q, mask_len] (_ops.py:860; D16): added to the logits of the last
+    mask_len keys, -inf entries removing keys; 4-D and cu_seq_q query forms, with windows,
+    ALiBi and a sink, in float32 / float16 / bfloat16, against torch in float64."""
+    dtype = torch.bfloat16
+    case = W.attn_case(dtype, 71, kv=kv, Hq=8, Hkv=2, D=64, max_ctx=90)
+    case.block_tables[3, 0] = -1
+    codes = _int4_codes(case, "rows") if case.int4 else case
+    q4 = W.attn_queries(dtype, 72, B=5, Hq=8, D=64, S=4)
+    q3, cu = W.attn_queries(dtype, 73, B=5, Hq=8, D=64, counts=[4, 1, 0, 3, 2])
+    sink = torch.linspace(-1.0, 1.0, 8)
+    for ml, mdt, window, alibi, sk in ((4, torch.float32, -1, False, None),
+                                       (16, torch.bfloat16, 9, False, sink),
+                                       (64, torch.float16, -1, True, sink),
+                                       (8, torch.float32, 2, True, None)):
+        al = (0.5 ** torch.arange(1, 9, dtype=torch.float32)).repeat(5, 1) if alibi else None
+        case.alibi = codes.alibi = al
+        mask = _mask(74 + ml, 5, 4, ml, mdt, neg_inf_every=7)
+        for q, c in ((q4, None), (q3, cu)):
+            out, lse = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables,
+                                          case.context_lens, 0.125, case.k_scale, case.v_scale,
+                                          al, window, cu_seq_q=c, sink=sk, int4=case.int4,
+                                          mask=mask)
+            want, wlse = torch_attn_mq(codes, q, 0.125, window, c, sk, mask=mask)
+            assert torch.allclose(out, want, rtol=1e-12, atol=1e-12, equal_nan=True)
+            assert torch.allclose(lse, wlse, rtol=1e-12, atol=1e-12, equal_nan=True)
+
+
+def test_attn_mask_identities(ref):
+    """A zero mask is no mask, bit for bit.  A constant c over every key of a sequence (mask_len
+    >= L) leaves out unchanged and adds c to the lse.  -inf over a token's last m keys equals
+    the same token seeing only the keys before them (a shorter context, with the token moved
+    back): the mask removes keys exactly.  A bfloat16 mask equals the float32 mask of the same
+    values."""
+    case = W.attn_case(torch.float16, 81, kv="int8_token", B=4, Hq=4, Hkv=2, D=32, max_ctx=40)
+    q = W.attn_queries(torch.float16, 82, B=4, Hq=4, D=32, S=1)
+    args = (case.k_cache, case.v_cache, case.block_tables, case.context_lens, 0.3,
+            case.k_scale, case.v_scale)
+    base = ref.cached_kv_attn(q, *args)
+    zero = ref.cached_kv_attn(q, *args, mask=torch.zeros(4, 1, 8))
+    assert torch.equal(base[0], zero[0]) and torch.equal(base[1], zero[1])
+    c = 1.75
+    const = ref.cached_kv_attn(q, *args, mask=torch.full((4, 1, 64), c))   # every L <= 40
+    assert torch.allclose(const[0], base[0], rtol=1e-13, atol=1e-15)
+    assert torch.allclose(const[1], base[1] + c, rtol=1e-13, atol=1e-13)
+    m = 3
+    cut = torch.zeros(4, 1, m)
+    cut[:] = float("-inf")
+    masked = ref.cached_kv_attn(q, *args, mask=cut)
+    shorter = case.context_lens - m
+    for i in range(4):
+        if int(case.context_lens[i]) <= m:
+            assert torch.all(masked[0][i] == 0) and torch.all(masked[1][i] == float("-inf"))
+            continue
+        lens = case.context_lens.clone()
+        lens[i] = shorter[i]
+        o, l = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables, lens, 0.3,
+                                  case.k_scale, case.v_scale)
+        assert torch.equal(masked[0][i], o[i]) and torch.equal(masked[1][i], l[i])
+    vals = _mask(83, 4, 1, 16, torch.bfloat16)
+    a = ref.cached_kv_attn(q, *args, mask=vals)
+    b = ref.cached_kv_attn(q, *args, mask=vals.float())
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])

@@ -348,6 +348,7 @@ class AttnCase:
     block_tables: torch.Tensor       # [B, max_blocks] int32
     context_lens: torch.Tensor       # [B] int32
     alibi: Optional[torch.Tensor] = None
+    int4: bool = False               # int8 caches of 4-bit pairs (kv_cache_quant_bit_size 4)
 
     @property
     def max_context_len(self) -> int:
@@ -366,15 +367,36 @@ def fp8_codes(shape, g) -> torch.Tensor:
     return x.to(torch.float8_e4m3fn)
 
 
+def pack_int4(codes: torch.Tensor, dim: int) -> torch.Tensor:
+    """Signed 4-bit codes (int8 in [-8, 7]) -> int8 bytes of pairs along `dim`: the even
+    element in the high nibble, the odd one in the low nibble."""
+    c = codes.movedim(dim, -1).to(torch.int16)
+    b = ((c[..., 0::2] & 0xF) << 4) | (c[..., 1::2] & 0xF)
+    return b.to(torch.uint8).view(torch.int8).movedim(-1, dim).contiguous()
+
+
+def unpack_int4(b: torch.Tensor, dim: int) -> torch.Tensor:
+    """pack_int4's inverse: int8 bytes of 4-bit pairs along `dim` -> int8 codes in [-8, 7]."""
+    u = b.movedim(dim, -1).view(torch.uint8).to(torch.int16)
+    hi, lo = (u >> 4) & 0xF, u & 0xF
+    c = torch.stack([hi, lo], dim=-1).reshape(u.shape[:-1] + (2 * u.shape[-1],))
+    c = torch.where(c >= 8, c - 16, c)
+    return c.to(torch.int8).movedim(-1, dim).contiguous()
+
+
 def attn_case(dtype, seed: int, kv: str = "int8_token", B: int = 5, Hq: int = 8, Hkv: int = 2,
               D: int = 128, BS: int = 16, NB: int = 64, max_ctx: int = 200,
-              alibi: bool = False, scale_dtype=torch.float32) -> AttnCase:
+              alibi: bool = False, scale_dtype=torch.float32,
+              v_pairs: str = "rows") -> AttnCase:
     """Decode attention inputs: q ~ N(0, 1) in `dtype`; caches int8 (`kv` "int8_token" /
     "int8_channel" / "int8_group", codes uniform in [-127, 127] with scales ~U[0.005, 0.03)),
     float8_e4m3fn (`kv` "fp8_token" / "fp8_channel" / "fp8_group", fp8_codes with scales
     ~U[0.0003, 0.0015)), scales in `scale_dtype` (float32 or bfloat16), or of q's dtype
-    (`kv` "plain", N(0, 1)); context lengths in [1, max_ctx] (the first max_ctx, one 1); each
-    sequence's pages a random choice of distinct blocks."""
+    (`kv` "plain", N(0, 1)); or int4 pairs (`kv` "int4_token" / "int4_channel" / "int4_group",
+    codes uniform in [-8, 7], scales ~U[0.05, 0.3)): K [NB, Hkv, BS, D / 2] pairing channels, V
+    [NB, Hkv, BS / 2, D] pairing rows (`v_pairs` "rows") or [NB, Hkv, BS, D / 2] (`v_pairs`
+    "channels"); context lengths in [1, max_ctx] (the first max_ctx, one 1); each sequence's
+    pages a random choice of distinct blocks."""
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(B, Hq, D, generator=g).to(dtype)
     lens = torch.randint(1, max_ctx + 1, (B,), generator=g).to(torch.int32)
@@ -385,9 +407,14 @@ def attn_case(dtype, seed: int, kv: str = "int8_token", B: int = 5, Hq: int = 8,
     assert B * MB <= NB, "not enough blocks for distinct pages"
     bt = torch.randperm(NB, generator=g)[:B * MB].reshape(B, MB).to(torch.int32)
     ks = vs = None
-    if kv.startswith("int8") or kv.startswith("fp8"):
+    if kv.startswith("int8") or kv.startswith("fp8") or kv.startswith("int4"):
         form = kv.split("_")[1]
-        if kv.startswith("int8"):
+        if kv.startswith("int4"):
+            kc = pack_int4(torch.randint(-8, 8, (NB, Hkv, BS, D), generator=g, dtype=torch.int8), 3)
+            vcodes = torch.randint(-8, 8, (NB, Hkv, BS, D), generator=g, dtype=torch.int8)
+            vc = pack_int4(vcodes, 2 if v_pairs == "rows" else 3)
+            lo, span = 0.05, 0.25
+        elif kv.startswith("int8"):
             kc = torch.randint(-127, 128, (NB, Hkv, BS, D), generator=g, dtype=torch.int8)
             vc = torch.randint(-127, 128, (NB, Hkv, BS, D), generator=g, dtype=torch.int8)
             lo, span = 0.005, 0.025
@@ -403,7 +430,7 @@ def attn_case(dtype, seed: int, kv: str = "int8_token", B: int = 5, Hq: int = 8,
         kc = torch.randn(NB, Hkv, BS, D, generator=g).to(dtype)
         vc = torch.randn(NB, Hkv, BS, D, generator=g).to(dtype)
     al = (0.5 ** torch.arange(1, Hq + 1, dtype=torch.float32)).repeat(B, 1) if alibi else None
-    return AttnCase(q, kc, vc, ks, vs, bt, lens, al)
+    return AttnCase(q, kc, vc, ks, vs, bt, lens, al, int4=kv.startswith("int4"))
 
 
 def attn_queries(dtype, seed: int, B: int, Hq: int, D: int, S: Optional[int] = None,
