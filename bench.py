@@ -715,6 +715,12 @@ def main():
     tjson = json.loads(tfile.read_text()) if tfile.exists() else {}
     profiled = {k: v["dispatch_us"] for k, v in tjson.items()
                 if isinstance(v, dict) and "dispatch_us" in v}
+    # where roofline.traffic and us_per_dispatch_rocprof come from: the committed profile, not
+    # this run (rocprofv3 cannot run inside the timed process)
+    src = tjson.get("_source", {})
+    profile_source = (f"profiles/traffic.json: rocprofv3 kernel trace and FETCH_SIZE / WRITE_SIZE "
+                      f"counters of commit {src.get('commit', 'unknown')} ({src.get('date', '?')}), "
+                      f"not this run")
     per = {}
     for name in todo:
         t0 = time.perf_counter()
@@ -796,9 +802,10 @@ def main():
                    "frac_of_peak": head["frac_of_peak"]},
         "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": head["frac_of_peak"], "traffic": traffic,
-                     "kernel": head["kernel"]},
+                     "traffic_source": profile_source, "kernel": head["kernel"]},
         "cpu_baseline": cpu,
         "per_config": per,
+        "us_per_dispatch_rocprof_source": profile_source,
         "settle_s": SETTLE_S,
         "launch_floor_us": round(floor, 3) if floor is not None else None,
         "copy_ceiling_GB_s": round(ceiling, 1) if ceiling is not None else None,
