@@ -57,6 +57,7 @@ WORKLOADS = {
     "linear_reshape": "reshape_linear_cache, 8 packed sequences x 4096 tokens x 8 KV heads x 128 bf16 -> bf16 linear cache [8, 8, 8192, 128]",
     "decode_attn": "single_query_cached_kv_attn, one bf16 query token x 32 heads per sequence over configs[4]'s int8 pages (64 seqs, ctx ~U[1024,32768], 8 KV heads x 128, per-token scales)",
     "reshape_paged": "reshape_paged_cache on configs[2]'s shape: 32768 tokens x 8 KV heads x 128 bf16 K/V scattered into bf16 pages (65536 blocks x 16)",
+    "decode_attn_int4": "single_query_cached_kv_attn (kv_cache_quant_bit_size 4), one bf16 query token x 32 heads per sequence over configs[4]'s layout as int4 pages (K pairing channels [NB, 8, 16, 64], V pairing rows [NB, 8, 8, 128], per-token fp32 scales)",
 }
 KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<BF16,16,1,false>",
            "cfg3": "quant_paged_vec<BF16,16,1,false>", "cfg4": "sq_dense<BF16,8,false,true>",
@@ -68,7 +69,7 @@ KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<
            "fused_rope_70b": "fused_rope_tok<BF16,16,3,0,512>",
            "linear_quant": "lin_quant<BF16,16,false,false,true>", "linear_dequant": "lin_dequant<BF16,16>",
            "linear_reshape": "lin_copy<16,true>", "decode_attn": "attn_mfma<128,0,false>",
-           "reshape_paged": "reshape_paged_rows<16>"}
+           "reshape_paged": "reshape_paged_rows<16>", "decode_attn_int4": "attn_mfma<128,4,false>"}
 
 
 def parse_args():
@@ -340,20 +341,38 @@ def bench_linear(torch, tmo, op: str, dev, steps, warmup):
 ATTN_HQ = 32
 
 
-def attn_bytes(layout, hq: int = ATTN_HQ, heads: int = 8, dim: int = W_D) -> int:
-    """Algorithmic bytes of decode attention over `layout`: every key's K and V codes and
-    scales once per KV head, q read and out written, block-table entries and lengths."""
+def attn_bytes(layout, hq: int = ATTN_HQ, heads: int = 8, dim: int = W_D,
+               int4: bool = False) -> int:
+    """Algorithmic bytes of decode attention over `layout`: every key's K and V codes (dim
+    bytes each, dim / 2 for int4 pairs) and scales once per KV head, q read and out written,
+    block-table entries and lengths."""
     pages = int(((layout.context_lengths + layout.block_size - 1) // layout.block_size).sum())
     B = layout.context_lengths.numel()
-    return (layout.total_tokens * heads * 2 * (dim + 4) + 2 * B * hq * dim * 2 + 4 * pages
+    code = dim // 2 if int4 else dim
+    return (layout.total_tokens * heads * 2 * (code + 4) + 2 * B * hq * dim * 2 + 4 * pages
             + 4 * B)
 
 
-def bench_decode_attn(torch, tmo, W, layout, dev, steps, warmup):
+def int4_pages(torch, W, layout, dev, seed: int = 1009):
+    """int4 pages over configs[4]'s layout: random codes in [-8, 7] packed K pairing channels
+    [NB, 8, 16, 64] and V pairing rows [NB, 8, 8, 128], per-token fp32 scales."""
+    NB, bs = layout.num_blocks, layout.block_size
+    g = torch.Generator(device=dev).manual_seed(seed)
+    def codes():
+        return torch.randint(-8, 8, (NB, W.H, bs, W.D), generator=g, device=dev,
+                             dtype=torch.int8)
+    kc = W.pack_int4(codes(), 3)
+    vc = W.pack_int4(codes(), 2)
+    ks = 0.05 + 0.25 * torch.rand((NB, W.H, bs), generator=g, device=dev)
+    vs = 0.05 + 0.25 * torch.rand((NB, W.H, bs), generator=g, device=dev)
+    return kc, vc, ks, vs
+
+
+def bench_decode_attn(torch, tmo, W, layout, dev, steps, warmup, int4: bool = False):
     """single_query_cached_kv_attn over configs[4]'s filled pages: one call per step (the pages
-    are ~2.4 GB, far beyond the MALL)."""
-    alg = attn_bytes(layout)
-    kc, vc, ks, vs = W.cfg5_fill(layout, dev)
+    are ~2.4 GB -- 1.2 GB as int4 -- far beyond the MALL)."""
+    alg = attn_bytes(layout, int4=int4)
+    kc, vc, ks, vs = int4_pages(torch, W, layout, dev) if int4 else W.cfg5_fill(layout, dev)
     B = layout.context_lengths.numel()
     g = torch.Generator(device=dev).manual_seed(17)
     q = torch.randn((B, 1, ATTN_HQ, W_D), generator=g, device=dev).to(torch.bfloat16)
@@ -362,7 +381,8 @@ def bench_decode_attn(torch, tmo, W, layout, dev, steps, warmup):
     bt = layout.block_tables.to(dev)
     mctx = layout.max_context_len
     calls = [lambda: tmo.single_query_cached_kv_attn(q, kc, vc, out, bt, ctx, ks, vs, None, mctx,
-                                                     -1, -1, W_D ** -0.5, False, 8)]
+                                                     -1, -1, W_D ** -0.5, False,
+                                                     4 if int4 else 8)]
     ms = time_graph(torch, calls, steps, warmup)
     return ms, alg, layout.total_tokens, 1
 
@@ -447,15 +467,17 @@ def profile_pass(torch, tmo, W, names, dev, n: int) -> None:
                                                                       gm, gm, sl, ks, vs)
         elif name.startswith("linear"):
             fn = linear_call(torch, tmo, name, dev, torch.Generator(device=dev).manual_seed(13))
-        elif name == "decode_attn":
+        elif name in ("decode_attn", "decode_attn_int4"):
             layout = W.cfg5()
-            kc, vc, ks, vs = W.cfg5_fill(layout, dev)
+            i4 = name == "decode_attn_int4"
+            kc, vc, ks, vs = int4_pages(torch, W, layout, dev) if i4 else W.cfg5_fill(layout, dev)
             q = torch.randn((64, 1, ATTN_HQ, W_D), device=dev).to(torch.bfloat16)
             out = torch.empty_like(q)
             ctx, bt = layout.context_lengths.to(dev), layout.block_tables.to(dev)
             mctx = layout.max_context_len
             fn = lambda: tmo.single_query_cached_kv_attn(q, kc, vc, out, bt, ctx, ks, vs, None,
-                                                         mctx, -1, -1, W_D ** -0.5, False, 8)
+                                                         mctx, -1, -1, W_D ** -0.5, False,
+                                                         4 if i4 else 8)
         elif name.startswith("cfg4"):
             case = getattr(W, name)()
             x, sm = case.x.to(dev), case.smooth.to(dev)
@@ -578,7 +600,8 @@ def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
                                              norm_type="layernorm" if ln else "rmsnorm",
                                              k_beta=gm if ln else None)
         alg, units, desc = fused_rope_bytes(n, hq=hq), n, f"fused rope of one {n}-token sequence"
-    elif workload == "decode_attn":
+    elif workload in ("decode_attn", "decode_attn_int4"):
+        i4 = workload == "decode_attn_int4"
         layout = W.cfg5()
         nseq = 2
         ctx = layout.context_lengths[:nseq].contiguous()
@@ -590,16 +613,22 @@ def cpu_baseline(torch, W, workload: str, seconds: float) -> dict:
             p0 += pn
         sub = W.DequantLayout("cfg5-sample", ctx, bt, p0)
         g = torch.Generator().manual_seed(5)
-        kc = torch.randint(-127, 128, (p0, W.H, W.BS, W.D), generator=g, dtype=torch.int8)
-        vc = torch.randint(-127, 128, (p0, W.H, W.BS, W.D), generator=g, dtype=torch.int8)
+        lo, hi = (-8, 8) if i4 else (-127, 128)
+        kc = torch.randint(lo, hi, (p0, W.H, W.BS, W.D), generator=g, dtype=torch.int8)
+        vc = torch.randint(lo, hi, (p0, W.H, W.BS, W.D), generator=g, dtype=torch.int8)
         ks = torch.rand(p0, W.H, W.BS, generator=g) * 0.05
         vs = torch.rand(p0, W.H, W.BS, generator=g) * 0.05
         q = torch.randn(nseq, ATTN_HQ, W.D, generator=g).to(torch.bfloat16)
-        fn = lambda: oracle.single_query_attn(q, kc, vc, bt, ctx, W.D ** -0.5, ks, vs,
-                                              nthreads=nthreads)
-        alg, units = attn_bytes(sub), sub.total_tokens
+        if i4:
+            kc, vc = W.pack_int4(kc, 3), W.pack_int4(vc, 2)
+            fn = lambda: oracle.cached_kv_attn(q, kc, vc, bt, ctx, W.D ** -0.5, ks, vs,
+                                               int4=True, nthreads=nthreads)
+        else:
+            fn = lambda: oracle.single_query_attn(q, kc, vc, bt, ctx, W.D ** -0.5, ks, vs,
+                                                  nthreads=nthreads)
+        alg, units = attn_bytes(sub, int4=i4), sub.total_tokens
         desc = (f"float64 decode attention of the first {nseq} sequences of cfg5 ({units} keys, "
-                f"{ATTN_HQ} query heads)")
+                f"{ATTN_HQ} query heads{', int4 pages' if i4 else ''})")
     elif workload.startswith("linear"):
         nb, S, H = LIN_B, 1024, W.H   # every sequence (the oracle threads over sequences)
         op = {"linear_reshape": 0, "linear_quant": 1, "linear_dequant": 3}[workload]
@@ -702,7 +731,7 @@ def main():
     todo = [args.workload] if args.configs == "headline" else \
         ["cfg1", "cfg2", "cfg3", "cfg4", "cfg4_moe", "cfg5", "offline_i8", "offline_f8",
          "fused_rope", "fused_rope_ln", "fused_rope_70b", "linear_quant", "linear_dequant",
-         "linear_reshape", "decode_attn", "reshape_paged"]
+         "linear_reshape", "decode_attn", "reshape_paged", "decode_attn_int4"]
     if args.workload not in todo:
         todo.append(args.workload)
     if args.profile_pass:
@@ -744,10 +773,11 @@ def main():
         elif name.startswith("linear"):
             ms, alg, units, sets = bench_linear(torch, tmo, name, dev, max(20, args.steps // 4),
                                                 max(4, args.warmup // 4))
-        elif name == "decode_attn":
+        elif name in ("decode_attn", "decode_attn_int4"):
             ms, alg, units, sets = bench_decode_attn(torch, tmo, W, W.cfg5(), dev,
                                                      max(10, args.steps // 40),
-                                                     max(2, args.warmup // 10))
+                                                     max(2, args.warmup // 10),
+                                                     int4=name == "decode_attn_int4")
         else:
             ms, alg, units, sets = bench_dequant(torch, tmo, W, W.cfg5(), dev,
                                                  max(10, args.steps // 40), max(2, args.warmup // 10))
@@ -796,7 +826,8 @@ def main():
                           "linear_dequant": "int8 codes + fp32 scales in; bf16 out",
                           "linear_reshape": "bf16 in; bf16 out",
                           "reshape_paged": "bf16 K/V rows in; bf16 pages out",
-                          "decode_attn": "bf16 q, int8 K/V pages + fp32 scales in; bf16 out; fp32 softmax"}
+                          "decode_attn": "bf16 q, int8 K/V pages + fp32 scales in; bf16 out; fp32 softmax",
+                          "decode_attn_int4": "bf16 q, int4 K/V pages + fp32 scales in; bf16 out; fp32 softmax"}
                    .get(args.workload, "bf16 in; int8 codes + fp32 scales out"),
                    "tokens_per_s": head["units_per_s"],
                    "frac_of_peak": head["frac_of_peak"]},

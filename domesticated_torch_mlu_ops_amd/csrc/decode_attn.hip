@@ -8,10 +8,11 @@
 // token: P = L - 1), over keys j in [max(0, P - window_left), P]; key j at row j % BS of page
 // block_tables[i, j / BS] (pages outside [0, NB) are masked): k_j its first D channels, v_j
 // the first Dv of the V cache's row, or of the K row when both live in one cache; query head
-// hq reads KV head hq / (Hq / Hkv).  Caches are int8 codes or float8_e4m3fn values with fp32 or
-// bf16 scales (k = code * scale) per token [NB, Hkv, BS] (strided in the first two dims), per
-// channel [Hkv, D], or per group (K [NB, Hkv, BS, D / 32], V [NB, Hkv, BS / 32, Dv]), or of
-// q's dtype.
+// hq reads KV head hq / (Hq / Hkv).  Caches are int8 codes, float8_e4m3fn values or int4 pairs
+// (K pairing channels, V pairing the rows of a page or channels) with fp32 or bf16 scales (k =
+// code * scale) per token [NB, Hkv, BS] (strided in the first two dims), per channel [Hkv, D],
+// or per group (K [NB, Hkv, BS, D / 32], V [NB, Hkv, BS / 32, Dv]), or of q's dtype.  A mask
+// adds its terms to the logits of each sequence's last mask_len keys.
 //
 // MFMA path (bf16 or f16 operands, fp32 accumulation; K and V head sizes and cache rows all 64
 // / 128 / 256, block_size a multiple of 16, per-token or per-channel scales): the query columns of a (sequence, KV head) are its (token, query head)
@@ -24,7 +25,8 @@
 //     channels c D/4 + 4m .. + 3 of every lane group (a permutation of the reduction order).
 //     Int8 codes enter as exact f16 values 1152 + code (two byte permutes per four codes) against
 //     a power-of-two scaled f16 q, and 1152 * sum(q) is subtracted from the fp32 result; the
-//     per-token scale and softmax_scale * log2(e) then multiply it.
+//     per-token scale and softmax_scale * log2(e) then multiply it.  Int4 codes enter as
+//     3 + code / 8 (int4_f16), 3 * sum(q) is subtracted and the factor 8 joins the scale.
 //   * The result layout (lane holds tokens 4c .. 4c + 3 of query column l % 16) IS the B
 //     operand layout of O^T = V^T P^T, so the probabilities feed the second product without a
 //     shuffle.  V^T's operand needs four tokens of one channel per lane: lane (n, c) reads
@@ -255,12 +257,38 @@ __device__ __forceinline__ f16x4 fp8_f16(uint32_t w) {
   return __builtin_bit_cast(f16x4, h);
 }
 
+// Eight int4 codes (one dword of a K row: byte b holds channels 2b (high nibble) and 2b + 1
+// (low nibble)) -> the f16 operands of channels 4h + {0, 2, 1, 3}, h = `half` (bytes 2h and
+// 2h + 1), as 2 + u / 8 with u = code + 8 (the nibble with its top bit flipped): the f16
+// pattern 0x4000 | u << 6 has exponent 1 and u in the top four mantissa bits, so the value
+// 3 + code / 8 is exact.  Each f16 pair is one byte permute (the two high or two low nibbles
+// into the pair's low bytes) and one shift-or.  The QK product then carries 3 * sum(q) and a
+// factor 1/8; the channel order within the operand is matched by q's.
+__device__ __forceinline__ f16x4 int4_f16(uint32_t w, int half) {
+  const uint32_t x = w ^ 0x88888888u;
+  const uint32_t hi = x & 0xf0f0f0f0u, lo = x & 0x0f0f0f0fu;
+  const uint32_t sel = half ? 0x0c030c02u : 0x0c010c00u;  // [byte 2h, 0, byte 2h + 1, 0]
+  u32x2 h;
+  h[0] = (__builtin_amdgcn_perm(hi, hi, sel) << 2) | 0x40004000u;  // channels 4h, 4h + 2
+  h[1] = (__builtin_amdgcn_perm(lo, lo, sel) << 6) | 0x40004000u;  // channels 4h + 1, 4h + 3
+  return __builtin_bit_cast(f16x4, h);
+}
+constexpr float kInt4Bias = 3.0f;
+// Channel of operand element e of QK MFMA m within the lane's run: int4 operands hold
+// channels 4m + {0, 2, 1, 3}
+__host__ __device__ constexpr int qk_channel(bool int4, int m, int e) {
+  return 4 * m + (int4 ? (((e & 1) << 1) | (e >> 1)) : e);
+}
+
 // kKind: 0 int8 caches (f16 QK, bf16 PV), 1 bf16 caches, 2 f16 caches, 3 float8_e4m3fn caches
-// (as int8: f16 QK against the exact code values, no bias; bf16 PV).  kQLo: q needs a lo
-// operand.  kSB: the scale tensors are bf16 (else fp32).
+// (as int8: f16 QK against the exact code values, no bias; bf16 PV), 4 int4 pairs (K pairing
+// channels, V pairing the rows of a page; f16 QK through int4_f16, bf16 PV of the exact
+// codes).  kQLo: q needs a lo operand.  kSB: the scale tensors are bf16 (else fp32).  kMask:
+// a mask is given (its terms are added in the tiles that reach the last mask_len keys; the
+// instances without one carry none of that code and its registers).
 // Workgroups per CU the register allocation must allow: three (168 registers per lane) for
 // the quantised-cache kernels up to head_size 128, fewer where that would spill.
-constexpr bool attn_quant(int kind) { return kind == 0 || kind == 3; }
+constexpr bool attn_quant(int kind) { return kind == 0 || kind == 3 || kind == 4; }
 constexpr int attn_min_blocks(int d, int kind) {
   return d == 256 ? 1 : (!attn_quant(kind) && d == 128 ? 2 : 3);
 }
@@ -269,7 +297,7 @@ constexpr int attn_min_blocks(int d, int kind) {
 #define TMO_ATTN_DEPTH 2
 #endif
 
-template <int kD, int kKind, bool kQLo, bool kSB>
+template <int kD, int kKind, bool kQLo, bool kSB, bool kMask>
 __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(AttnParams p) {
   constexpr bool kQuant = attn_quant(kKind);  // codes with per-token / per-channel scales
   // tiles in flight per wavefront: three register sets where they fit the register budget of
@@ -282,6 +310,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   constexpr int kDV = kD / 16;      // channels per lane in the V layout
   constexpr int kQK = kD / 16;      // QK MFMAs per tile
   constexpr int kEs = kQuant ? 1 : 2;  // cache element bytes
+  constexpr bool kInt4 = kKind == 4;
 
   const int lane = threadIdx.x & (kWave - 1);
   // wave-uniform (readfirstlane): the tile indices, page numbers and page offsets derived from it
@@ -377,7 +406,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
     for (int m = 0; m < kQK; ++m) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int c = 4 * m + e;  // channel within the lane's run
+        const int c = qk_channel(kInt4, m, e);  // channel within the lane's run
         const uint32_t w = qraw[c / 8][(c % 8) / 2];
         const uint32_t h = (c & 1) ? (w >> 16) : (w & 0xffffu);
         float x = bf ? __uint_as_float(h << 16) : f16_bits_to_f32(h);
@@ -398,7 +427,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
     for (int m = 0; m < kQK; ++m) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int d = grp * kDC + 4 * m + e;
+        const int d = grp * kDC + qk_channel(kInt4, m, e);
         float x = qvalid ? load_q(p, i * p.q_sb + qrow * p.q_ss + (int64_t)hq * p.q_sh + d) : 0.0f;
         if (kQuant && p.smode == 2) x *= scale_at(p.ks, (int64_t)hk * kD + d, kSB);
         qx[m][e] = x;
@@ -430,6 +459,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
       }
     }
     if constexpr (kKind == 0) qk_off = kCodeBias * col_sum(qsum);
+    if constexpr (kInt4) qk_off = kInt4Bias * col_sum(qsum);
   } else {
 #pragma unroll
     for (int m = 0; m < kQK; ++m) {
@@ -444,7 +474,8 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
     }
   }
   const float alibi = (p.alibi && qvalid) ? p.alibi[i * p.Hq + hq] * kLog2e : 0.0f;
-  const float score_scale = p.scale_log2 * inv_sigma;  // inv_sigma: an exact power of two
+  // inv_sigma: an exact power of two; int4 operands carry the codes / 8
+  const float score_scale = p.scale_log2 * inv_sigma * (kInt4 ? 8.0f : 1.0f);
   // mask: terms for keys [mask_lo, L), element mask_row + m for key mask_lo + m
   const int32_t mask_lo = (int32_t)sq.L - p.mask_len;
 
@@ -456,19 +487,26 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
 
   const char* kbase = static_cast<const char*>(p.kc);
   const char* vbase = static_cast<const char*>(p.vc);
-  const int64_t page_bytes = (int64_t)p.BS * kD * kEs;      // one head's page
+  // cache row bytes: K rows of kD elements (int4: kD / 2 bytes of channel pairs); V rows of kD
+  // elements (int4: pair rows of kD bytes, each two tokens, so a page is BS / 2 of them and
+  // the same bytes as a K page)
+  constexpr int kKRow = kInt4 ? kD / 2 : kD * kEs;
+  constexpr int kVRow = kInt4 ? kD : kD * kEs;
+  constexpr int kVRows = kInt4 ? 2 : 4;                     // V rows per lane: tokens 4 grp .. + 3
+  const int64_t page_bytes = (int64_t)p.BS * kKRow;         // one head's page
   // per-lane offsets inside a 16-row piece of a page: K token `col`, channels grp * kDC ..;
   // V tokens 4 grp .. + 3, channels col * kDV ..
-  const int32_t k_lane = col * kD * kEs + grp * kDC * kEs;
-  const int32_t v_lane = 4 * grp * kD * kEs + col * kDV * kEs;
-  constexpr int kKW = kDC * kEs / 4, kVW = kDV * kEs / 4;   // dwords per lane
+  const int32_t k_lane = col * kKRow + grp * (kInt4 ? kDC / 2 : kDC * kEs);
+  const int32_t v_lane = kVRows * grp * kVRow + col * kDV * (kInt4 ? 1 : kEs);
+  constexpr int kKW = kInt4 ? kDC / 8 : kDC * kEs / 4;      // dwords per lane
+  constexpr int kVW = kInt4 ? kDV / 4 : kDV * kEs / 4;
 
   // Raw tile: this lane's K piece, its V pieces of four tokens, the per-token scales.
   // The per-token scales stay raw until the tile is computed (fp32 words, or bf16 pairs in
   // ks[0..1] / vs[0..1]): widening them at load time would wait for the loads there.
   struct Raw {
     uint32_t kw[kKW];
-    uint32_t vw[4][kVW];
+    uint32_t vw[kVRows][kVW];
     uint32_t ks[4], vs[4];
   };
   auto raw_scale = [](const uint32_t (&w)[4], int e) -> float {
@@ -478,17 +516,27 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   auto load_tile = [&](Raw& r, int32_t tl, int64_t blk) {
     const int32_t t0 = tl * 16;
     const int32_t row0 = t0 - page_of(tl) * p.BS;
-    const int64_t piece = (blk * p.Hkv + hk) * page_bytes + (int64_t)row0 * kD * kEs;
+    // the piece's offset in a K page; in an int4 V page (pair rows of kD bytes) row0 / 2 * kD
+    // is the same number
+    const int64_t piece = (blk * p.Hkv + hk) * page_bytes + (int64_t)row0 * kKRow;
     const char* krow = kbase + piece + k_lane;
+    if constexpr (kKW >= 4) {
 #pragma unroll
-    for (int u = 0; u < kKW / 4; ++u) {
-      const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(krow) + u);
+      for (int u = 0; u < kKW / 4; ++u) {
+        const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(krow) + u);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) r.kw[4 * u + e] = w[e];
+        for (int e = 0; e < 4; ++e) r.kw[4 * u + e] = w[e];
+      }
+    } else if constexpr (kKW == 2) {
+      const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(krow));
+      r.kw[0] = w[0];
+      r.kw[1] = w[1];
+    } else {
+      r.kw[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(krow));
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const char* vrow = vbase + piece + v_lane + e * kD * kEs;
+    for (int e = 0; e < kVRows; ++e) {
+      const char* vrow = vbase + piece + v_lane + e * kVRow;
       if constexpr (kVW == 4) {
         const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vrow));
 #pragma unroll
@@ -544,6 +592,8 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
         VQ a;
         if constexpr (kKind == 0) {
           a = codes_f16(r.kw[m]);
+        } else if constexpr (kInt4) {
+          a = int4_f16(r.kw[m >> 1], m & 1);
         } else if constexpr (kKind == 3) {
           a = fp8_f16(r.kw[m]);
         } else {
@@ -569,7 +619,7 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
         tmax = fmaxf(tmax, v);
       }
       // mask terms of the last mask_len keys: only the tiles that reach them (wave-uniform)
-      if (p.mask && t0 + 15 >= mask_lo) {
+      if (kMask && t0 + 15 >= mask_lo) {
         // the column's row of terms (recomputed here: nothing stays live across the tiles;
         // a padding column reads token S - 1's row, in bounds, and its scores stay -inf)
         const int ct = (cb * 16 + col) / p.g;
@@ -648,6 +698,15 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int8_t code = (int8_t)(r.vw[e][j >> 2] >> (8 * (j & 3)));
+            b4[e] = (short)(__float_as_uint((float)code) >> 16);
+          }
+        } else if constexpr (kInt4) {
+          // channel j's byte of pair row e / 2 holds tokens 4 grp + e (high nibble, e even)
+          // and + 1 (low nibble): the sign-extended nibble, exact as bf16
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int code = __builtin_amdgcn_sbfe((int)r.vw[e >> 1][j >> 2],
+                                                   8 * (j & 3) + ((e & 1) ? 0 : 4), 4);
             b4[e] = (short)(__float_as_uint((float)code) >> 16);
           }
         } else if constexpr (kKind == 3) {
@@ -1058,8 +1117,13 @@ __global__ __launch_bounds__(256) void attn_generic(AttnParams p) {
 template <int kD, int kKind, bool kSB>
 int launch_mfma_d(const AttnParams& p, bool qlo, hipStream_t st) {
   const dim3 grid((unsigned)(p.splits * p.ncb), (unsigned)p.Hkv, (unsigned)p.B), block(256);
-  int rc = qlo ? launch_kernel(attn_mfma<kD, kKind, true, kSB>, grid, block, st, p)
-               : launch_kernel(attn_mfma<kD, kKind, false, kSB>, grid, block, st, p);
+  int rc;
+  if (p.mask)
+    rc = qlo ? launch_kernel(attn_mfma<kD, kKind, true, kSB, true>, grid, block, st, p)
+             : launch_kernel(attn_mfma<kD, kKind, false, kSB, true>, grid, block, st, p);
+  else
+    rc = qlo ? launch_kernel(attn_mfma<kD, kKind, true, kSB, false>, grid, block, st, p)
+             : launch_kernel(attn_mfma<kD, kKind, false, kSB, false>, grid, block, st, p);
   if (rc != TMO_OK || p.splits == 1) return rc;
   const int64_t rows = (int64_t)p.B * p.S * p.Hq;
   return launch_kernel(attn_combine, dim3((unsigned)((rows + 3) / 4)), block, st, p);
@@ -1243,9 +1307,11 @@ extern "C" int tmo_hip_cached_kv_attn(
   // The MFMA kernel always issues its tile loads (a wave with no valid page yet reads page 0,
   // see attn_mfma), so an empty cache takes attn_generic, whose loads are all under the page
   // check: every output row is then 0 and its lse -inf (nothing to attend to).
-  bool mfma = num_blocks > 0 && !int4 && (head_size == 64 || head_size == 128 || head_size == 256) &&
-              head_size_v == head_size && k_cache_dim == head_size &&
-              v_cache_dim == head_size && block_size % 16 == 0 && al(k_cache, 16) &&
+  // int4 pages: K rows of head_size / 2 bytes, V pairing rows (pair rows of head_size bytes)
+  bool mfma = num_blocks > 0 && (head_size == 64 || head_size == 128 || head_size == 256) &&
+              head_size_v == head_size &&
+              k_cache_dim == (int4 ? head_size / 2 : head_size) && v_cache_dim == head_size &&
+              !(int4 && v_pair_channels) && block_size % 16 == 0 && al(k_cache, 16) &&
               al(v_cache, 16) && q_dtype != TMO_DTYPE_F32;
   if (quant)
     mfma = mfma && scale_mode != 3 &&
@@ -1281,6 +1347,9 @@ extern "C" int tmo_hip_cached_kv_attn(
   if (cache_dtype == TMO_DTYPE_F8E4M3)
     return p.s_bf16 ? launch_mfma<3, true>(p, scale_mode == 2, st)
                     : launch_mfma<3, false>(p, scale_mode == 2, st);
+  if (int4)
+    return p.s_bf16 ? launch_mfma<4, true>(p, scale_mode == 2, st)
+                    : launch_mfma<4, false>(p, scale_mode == 2, st);
   if (cache_dtype == TMO_DTYPE_BF16) return launch_mfma<1, false>(p, false, st);
   return launch_mfma<2, false>(p, false, st);
 }

@@ -474,9 +474,10 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
  * last mask_len keys of each sequence -- key j >= L - mask_len of query token s of sequence i
  * gets s_j += mask[i * mask_stride_batch + s * mask_stride_token + j - (L - mask_len)] after
  * softmax_scale and ALiBi (L clamped to the block table; -inf removes the key).  Head sizes:
- * head_size up to 4096, head_size_v up to 512; the MFMA kernels take int8, float8_e4m3fn and
- * unquantised K and V head sizes and cache rows all equal to 64, 128 or 256 with per-token or
- * per-channel scales, a VALU kernel the rest (int4 caches included).
+ * head_size up to 4096, head_size_v up to 512; the MFMA kernels take K and V head sizes of 64,
+ * 128 or 256 (equal, with cache rows of that many elements -- int4: K rows of head_size / 2
+ * bytes, V pairing rows) and per-token or per-channel scales, a VALU kernel the rest (int4
+ * V pairing channels included).
  * Arithmetic: fp32 accumulation (MFMA with bf16/f16 operands: int8 codes and e4m3fn values are
  * exact; q and the probabilities are split into two operands when one is not exact), softmax
  * in fp32.

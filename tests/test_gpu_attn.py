@@ -501,6 +501,42 @@ def test_attn_int4_caches(tmo, ref, dev, dtype, kv, v_pairs):
     run_attn_mq(tmo, ref, dev, case, q3, cu=cu, window=40)
 
 
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("kv,sdt", [("int4_token", torch.float32), ("int4_channel", torch.bfloat16),
+                                    ("int4_token", torch.bfloat16)])
+def test_attn_int4_mfma_head_sizes(tmo, ref, dev, D, kv, sdt):
+    """int4 pages (V pairing rows) of head sizes 64 and 256 on the MFMA kernel, per-token or
+    per-channel scales in float32 or bfloat16, one and three query tokens."""
+    case = W.attn_case(torch.bfloat16, 120 + D, kv=kv, B=4, Hq=8, Hkv=2, D=D, NB=64,
+                       max_ctx=150, scale_dtype=sdt)
+    for S in (1, 3):
+        q = W.attn_queries(torch.bfloat16, 121 + S, B=4, Hq=8, D=D, S=S)
+        run_attn_mq(tmo, ref, dev, case, q, sink=SINK8 if S == 3 else None)
+
+
+def test_attn_decode_on_configs4_int4_pages(tmo, ref, dev):
+    """configs[4]'s page layout with int4 pages (K pairing channels, V pairing rows, per-token
+    fp32 scales), 32 query heads, on a sample of 6 sequences against the oracle."""
+    layout = W.cfg5()
+    sel = torch.tensor([0, 1, 7, 20, 41, 63])
+    ctx = layout.context_lengths[sel].contiguous()
+    bt = layout.block_tables[sel].contiguous()
+    used = [bt[i, :(c + 15) // 16] for i, c in enumerate(ctx.tolist())]
+    pages = torch.unique(torch.cat(used))
+    bt2 = torch.full_like(bt, -1)
+    for i, u in enumerate(used):
+        bt2[i, :u.numel()] = torch.searchsorted(pages, u).to(torch.int32)
+    g = torch.Generator().manual_seed(8)
+    NB = pages.numel()
+    kc = W.pack_int4(torch.randint(-8, 8, (NB, 8, 16, 128), generator=g, dtype=torch.int8), 3)
+    vc = W.pack_int4(torch.randint(-8, 8, (NB, 8, 16, 128), generator=g, dtype=torch.int8), 2)
+    ks = 0.05 + 0.25 * torch.rand(NB, 8, 16, generator=g)
+    vs = 0.05 + 0.25 * torch.rand(NB, 8, 16, generator=g)
+    q = torch.randn(len(sel), 1, 32, 128, generator=g).to(torch.bfloat16)
+    case = W.AttnCase(q[:, 0], kc, vc, ks, vs, bt2, ctx, int4=True)
+    run_attn_mq(tmo, ref, dev, case, q)
+
+
 def test_attn_int4_long_contexts(tmo, ref, dev):
     """int4 pages over a few thousand keys, 32 query heads over 8 KV heads, with splits."""
     case = W.attn_case(torch.bfloat16, 97, kv="int4_token", B=3, Hq=32, Hkv=8, D=128, BS=16,
