@@ -60,7 +60,7 @@ WORKLOADS = {
     "decode_attn_int4": "single_query_cached_kv_attn (kv_cache_quant_bit_size 4), one bf16 query token x 32 heads per sequence over configs[4]'s layout as int4 pages (K pairing channels [NB, 8, 16, 64], V pairing rows [NB, 8, 8, 128], per-token fp32 scales)",
 }
 KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<BF16,16,1,false>",
-           "cfg3": "quant_paged_vec<BF16,16,1,false>", "cfg4": "sq_dense<BF16,8,false,true>",
+           "cfg3": "quant_paged_vec<BF16,16,1,false>", "cfg4": "sq_dense_wg<BF16,2,false,true>",
            "cfg4_moe": "sq_grp<BF16,8,4,true,true>", "cfg5": "dequant_paged_list<BF16,1,2>",
            "offline_i8": "quant_paged_static_vec<BF16,16,false>",
            "offline_f8": "quant_paged_static_vec<BF16,16,true>",
@@ -68,8 +68,8 @@ KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<
            "fused_rope_ln": "fused_rope_tok<BF16,16,3,1,256>",
            "fused_rope_70b": "fused_rope_tok<BF16,16,3,0,512>",
            "linear_quant": "lin_quant<BF16,16,false,false,true>", "linear_dequant": "lin_dequant<BF16,16>",
-           "linear_reshape": "lin_copy<16,true>", "decode_attn": "attn_mfma<128,0,false>",
-           "reshape_paged": "reshape_paged_rows<16>", "decode_attn_int4": "attn_mfma<128,4,false>"}
+           "linear_reshape": "lin_copy<16,true>", "decode_attn": "attn_mfma<128,0,false,false,false>",
+           "reshape_paged": "reshape_paged_rows<16>", "decode_attn_int4": "attn_mfma<128,4,false,false,false>"}
 
 
 def parse_args():
