@@ -61,7 +61,7 @@ WORKLOADS = {
 }
 KERNELS = {"cfg1": "quant_paged_vec<BF16,16,1,false>", "cfg2": "quant_paged_vec<BF16,16,1,false>",
            "cfg3": "quant_paged_vec<BF16,16,1,false>", "cfg4": "sq_dense_wg<BF16,2,false,true>",
-           "cfg4_moe": "sq_grp<BF16,8,4,true,true>", "cfg5": "dequant_paged_list<BF16,1,2>",
+           "cfg4_moe": "sq_grp<BF16,8,4,true,true>", "cfg5": "dequant_paged_list<BF16,1,2,0>",
            "offline_i8": "quant_paged_static_vec<BF16,16,false>",
            "offline_f8": "quant_paged_static_vec<BF16,16,true>",
            "fused_rope": "fused_rope_tok<BF16,16,3,0,256>",
