@@ -562,12 +562,17 @@ def single_query_cached_kv_attn(
     multiple of seq_q; not with float32 q) is added to the logits of each sequence's last
     ``mask_len`` keys.  Computed in fp32 (MFMA with exact bf16/f16 operands).  With
     ``return_lse`` also returns ``ln`` of the softmax denominator, ``[batch, heads, seq_q]``
-    (or ``[heads, total_q]`` for 3-D q).  Quantised q / output raise ``RuntimeError``.  A
-    positive ``max_seq_q`` is trusted: query tokens past it are not computed (as the
-    reference says of an understated ``max_context_len``).
+    (or ``[heads, total_q]`` for 3-D q).  An int8 or ``torch.float8_e4m3fn`` q holds codes
+    times ``q_quant_scale`` (``[1]``, q's shape without head_size, or that with a last dim of
+    scale_num channel groups; float32 or bfloat16) and the output is ``out_dtype`` (half for
+    a float8 q); such a q reads quantised caches, or caches of its own dtype
+    (``kv_cache_quant_bit_size=-1``) as codes with unit scales.  ``block_tables`` may be
+    ``[batch, kv_heads or heads, max_blocks]`` (sparse KV: each head its own pages).
+    ``out_quant_scale`` must be None.  A positive ``max_seq_q`` is trusted: query tokens past
+    it are not computed (as the reference says of an understated ``max_context_len``).
 
     Reference: ``_ops.py:777-900`` (math ``:800-817``; int4 ``:826-829``, ``:852``; mask
-    ``:860``).  Returns ``out`` or ``(out, lse)``.
+    ``:860``; quantised q ``:853-858``; sparse KV ``:834``).  Returns ``out`` or ``(out, lse)``.
     """
     tmo_out = out
     if out is None:

@@ -88,7 +88,14 @@ struct AttnParams {
   int32_t B, Hq, Hkv, g, D, Dv, BS;  // D: query / key head size, Dv: value head size
   int32_t bs_shift;              // log2(BS) when BS is a power of two, else -1
   int64_t NB;
-  int32_t q_dtype;               // TMO_DTYPE_*
+  int32_t q_dtype;               // TMO_DTYPE_*: F32 / F16 / BF16, or I8 / F8E4M3 codes (qs)
+  int32_t o_dtype;               // output TMO_DTYPE_* (q's for unquantised q)
+  const void* qs;                // q scales of I8 / F8E4M3 q: fp32, or bf16 when qs_bf16
+  int32_t qs_mode;               // 0 none, 1 per tensor, 2 per (token, head), 3 per channel group
+  int32_t qs_bf16;
+  int64_t qs_sb, qs_ss, qs_sh;   // q scale strides (sequence, token, head), as q's
+  int32_t qs_group;              // mode 3: channels per scale (head_size / scale_num)
+  int64_t bt_heads;              // block-table rows per sequence: 0 ([B, MB]), Hkv or Hq
   int32_t q_vec;                 // q rows 16-byte aligned 2-byte values: vector q loads
   int32_t c_dtype;               // cache TMO_DTYPE_*
   int32_t v_ch;                  // int4 caches: V pairs channels (else the rows of a page)
@@ -109,16 +116,38 @@ __device__ __forceinline__ uint16_t bf16_bits_rne(float x) {
 }
 __device__ __forceinline__ float bf16_value(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
+// Query element e as stored: a float, or an int8 / float8_e4m3fn code (its scale applies
+// separately: q_scale_of below).
 __device__ __forceinline__ float load_q(const AttnParams& p, int64_t e) {
   switch (p.q_dtype) {
     case TMO_DTYPE_BF16: return load1(BF16{}, p.q, e);
     case TMO_DTYPE_F16: return load1(F16{}, p.q, e);
+    case TMO_DTYPE_I8: return (float)static_cast<const int8_t*>(p.q)[e];
+    case TMO_DTYPE_F8E4M3: return fp8_value(static_cast<const uint8_t*>(p.q)[e], 0);
     default: return load1(F32{}, p.q, e);
   }
 }
 
+// Scale of quantised q: the whole row's (per tensor, per token and head) -- `base` the row's
+// scale element i * qs_sb + row * qs_ss + hq * qs_sh -- or, per channel group, channel d's.
+__device__ __forceinline__ float q_row_scale(const AttnParams& p, int64_t base) {
+  if (p.qs_mode == 1) return scale_at(p.qs, 0, p.qs_bf16);
+  if (p.qs_mode == 2) return scale_at(p.qs, base, p.qs_bf16);
+  return 1.0f;
+}
+__device__ __forceinline__ float q_group_scale(const AttnParams& p, int64_t base, int d) {
+  return p.qs_mode == 3 ? scale_at(p.qs, base + d / p.qs_group, p.qs_bf16) : 1.0f;
+}
+
+// The block-table row of sequence i for query head hq (KV head hk): sparse-KV tables hold one
+// per KV head or per query head.
+__device__ __forceinline__ const int32_t* bt_row_of(const AttnParams& p, int64_t i, int hq, int hk) {
+  const int64_t r = p.bt_heads == 0 ? i : i * p.bt_heads + (p.bt_heads == p.Hq ? hq : hk);
+  return p.bt + r * p.max_blocks;
+}
+
 __device__ __forceinline__ void store_out(const AttnParams& p, int64_t e, float v) {
-  switch (p.q_dtype) {
+  switch (p.o_dtype) {
     case TMO_DTYPE_BF16: store1(BF16{}, p.out, e, v); break;
     case TMO_DTYPE_F16: store1(F16{}, p.out, e, v); break;
     default: store1(F32{}, p.out, e, v); break;
@@ -366,7 +395,8 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   }
   const int32_t first_tile = (int32_t)(bbeg >> 4);
   const int32_t end_tile = (int32_t)((bend + 15) >> 4);
-  const int32_t* bt_row = p.bt + i * p.max_blocks;
+  // the MFMA kernel takes tables of one row per sequence or per KV head
+  const int32_t* bt_row = p.bt + (p.bt_heads ? i * p.bt_heads + hk : i) * p.max_blocks;
   auto page_of = [&](int32_t tl) -> int32_t {
     const int32_t t0 = tl * 16;
     return p.bs_shift >= 0 ? t0 >> p.bs_shift : t0 / p.BS;
@@ -429,6 +459,8 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
       for (int e = 0; e < 4; ++e) {
         const int d = grp * kDC + qk_channel(kInt4, m, e);
         float x = qvalid ? load_q(p, i * p.q_sb + qrow * p.q_ss + (int64_t)hq * p.q_sh + d) : 0.0f;
+        if (kQuant && p.qs_mode == 3 && qvalid)  // group-wise q scales (kQLo holds the rest)
+          x *= q_group_scale(p, i * p.qs_sb + qrow * p.qs_ss + (int64_t)hq * p.qs_sh, d);
         if (kQuant && p.smode == 2) x *= scale_at(p.ks, (int64_t)hk * kD + d, kSB);
         qx[m][e] = x;
         qabs = fmaxf(qabs, fabsf(x));
@@ -474,8 +506,12 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
     }
   }
   const float alibi = (p.alibi && qvalid) ? p.alibi[i * p.Hq + hq] * kLog2e : 0.0f;
-  // inv_sigma: an exact power of two; int4 operands carry the codes / 8
-  const float score_scale = p.scale_log2 * inv_sigma * (kInt4 ? 8.0f : 1.0f);
+  // inv_sigma: an exact power of two; int4 operands carry the codes / 8; a per-tensor or
+  // per-token q scale multiplies the column's scores (its q operand holds the exact codes)
+  const float q_rs = (kQuant && qvalid && p.qs_mode)
+                         ? q_row_scale(p, i * p.qs_sb + qrow * p.qs_ss + (int64_t)hq * p.qs_sh)
+                         : 1.0f;
+  const float score_scale = p.scale_log2 * inv_sigma * (kInt4 ? 8.0f : 1.0f) * q_rs;
   // mask: terms for keys [mask_lo, L), element mask_row + m for key mask_lo + m
   const int32_t mask_lo = (int32_t)sq.L - p.mask_len;
 
@@ -1056,18 +1092,22 @@ __global__ __launch_bounds__(256) void attn_generic(AttnParams p) {
   for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
   const int64_t qrow = sq.row0 + tok;
   const int64_t qe = i * p.q_sb + qrow * p.q_ss + (int64_t)hq * p.q_sh;
+  const int64_t qse = i * p.qs_sb + qrow * p.qs_ss + (int64_t)hq * p.qs_sh;  // quantised q
+  const float q_rs = p.qs_mode ? q_row_scale(p, qse) : 1.0f;
+  const int32_t* btr = bt_row_of(p, i, hq, hk);
   for (int64_t j0 = jb; j0 < je; j0 += kWave) {
     const int64_t j = j0 + lane;
     float s = -__builtin_inff();
     int blk = -1, r = 0;
     if (j < je) {
-      blk = p.bt[i * p.max_blocks + j / p.BS];
+      blk = btr[j / p.BS];
       r = (int)(j % p.BS);
       if (blk >= 0 && blk < p.NB) {
         float dot = 0.0f;
         for (int d = 0; d < p.D; ++d)
-          dot += load_q(p, qe + d) * key_value(p, blk, hk, r, d, cache_dtype);
-        s = dot * p.scale_log2;
+          dot += load_q(p, qe + d) * q_group_scale(p, qse, d) *
+                 key_value(p, blk, hk, r, d, cache_dtype);
+        s = dot * q_rs * p.scale_log2;
         if (p.alibi) s += alibi * (float)(j - P);
         if (p.mask && j >= sq.L - p.mask_len)
           s += mask_value(p, i * p.m_sb + tok * p.m_ss + (j - (sq.L - p.mask_len))) * kLog2e;
@@ -1164,25 +1204,46 @@ extern "C" int64_t tmo_hip_attn_workspace_bytes(int64_t batch, int64_t num_kv_he
 
 extern "C" int tmo_hip_cached_kv_attn(
     const void* q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head,
+    const void* q_scale, int q_scale_mode, int q_scale_dtype, int64_t q_scale_stride_batch,
+    int64_t q_scale_stride_token, int64_t q_scale_stride_head, int64_t q_scale_groups,
     const int32_t* cu_seq_q, int64_t seq_q, int64_t total_q, const void* k_cache,
     const void* v_cache, int64_t k_cache_dim, int64_t v_cache_dim, const void* k_scale,
     const void* v_scale, int scale_mode, int scale_dtype, int64_t k_scale_stride_block,
     int64_t k_scale_stride_head, int64_t v_scale_stride_block, int64_t v_scale_stride_head,
-    const int32_t* block_tables, int64_t max_blocks, const int32_t* context_lens,
-    const float* alibi_slopes, const float* sink, const void* mask, int mask_dtype,
+    const int32_t* block_tables, int64_t max_blocks, int64_t block_table_heads,
+    const int32_t* context_lens, const float* alibi_slopes, const float* sink, const void* mask,
+    int mask_dtype,
     int64_t mask_len, int64_t mask_stride_batch, int64_t mask_stride_token, void* out,
     int64_t out_stride_batch, int64_t out_stride_token, int64_t out_stride_head, float* lse,
     int64_t lse_stride_batch, int64_t lse_stride_token, int64_t lse_stride_head, int64_t batch,
     int64_t num_q_heads, int64_t num_kv_heads, int64_t head_size, int64_t head_size_v,
     int64_t num_blocks, int64_t block_size, int64_t max_context_len, int64_t window_left,
-    float softmax_scale, int q_dtype, int cache_dtype, int v_pair_channels, int64_t splits,
-    void* workspace, int64_t workspace_bytes, void* stream) {
-  if (q_dtype != TMO_DTYPE_BF16 && q_dtype != TMO_DTYPE_F16 && q_dtype != TMO_DTYPE_F32)
+    float softmax_scale, int q_dtype, int cache_dtype, int v_pair_channels, int out_dtype,
+    int64_t splits, void* workspace, int64_t workspace_bytes, void* stream) {
+  // q: floats (the output of q's dtype), or int8 / float8_e4m3fn codes with q_scale (the
+  // output of out_dtype) over quantised caches
+  const bool qquant = q_dtype == TMO_DTYPE_I8 || q_dtype == TMO_DTYPE_F8E4M3;
+  if (q_dtype != TMO_DTYPE_BF16 && q_dtype != TMO_DTYPE_F16 && q_dtype != TMO_DTYPE_F32 && !qquant)
     return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (out_dtype != TMO_DTYPE_BF16 && out_dtype != TMO_DTYPE_F16 && out_dtype != TMO_DTYPE_F32)
+    return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (!qquant && out_dtype != q_dtype) return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (qquant) {
+    if (q_scale_mode < 1 || q_scale_mode > 3) return TMO_ERR_UNSUPPORTED_MODE;
+    if (q_scale_dtype != TMO_DTYPE_F32 && q_scale_dtype != TMO_DTYPE_BF16)
+      return TMO_ERR_UNSUPPORTED_DTYPE;
+    if (!q_scale || q_scale_stride_batch < 0 || q_scale_stride_token < 0 ||
+        q_scale_stride_head < 0 ||
+        (q_scale_mode == 3 && (q_scale_groups <= 0 || head_size % q_scale_groups != 0)))
+      return TMO_ERR_INVALID_ARGUMENT;
+  }
+  if (block_table_heads != 0 && block_table_heads != num_kv_heads &&
+      block_table_heads != num_q_heads)
+    return TMO_ERR_INVALID_ARGUMENT;
   // quantised caches: int8 codes, float8_e4m3fn values or int4 pairs, times fp32 or bf16 scales
   const bool int4 = cache_dtype == TMO_DTYPE_I4;
   const bool quant = cache_dtype == TMO_DTYPE_I8 || cache_dtype == TMO_DTYPE_F8E4M3 || int4;
-  if (!quant && cache_dtype != q_dtype) return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (!quant && cache_dtype != q_dtype) return TMO_ERR_UNSUPPORTED_DTYPE;  // quantised q: quantised caches
   if (mask && mask_dtype != TMO_DTYPE_F32 && mask_dtype != TMO_DTYPE_F16 &&
       mask_dtype != TMO_DTYPE_BF16)
     return TMO_ERR_UNSUPPORTED_DTYPE;
@@ -1293,7 +1354,17 @@ extern "C" int tmo_hip_cached_kv_attn(
   p.bs_shift = ilog2_if_pow2(block_size);
   p.NB = num_blocks;
   p.q_dtype = q_dtype;
-  p.q_vec = q_dtype != TMO_DTYPE_F32 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+  p.o_dtype = out_dtype;
+  p.qs = qquant ? q_scale : nullptr;
+  p.qs_mode = qquant ? q_scale_mode : 0;
+  p.qs_bf16 = qquant && q_scale_dtype == TMO_DTYPE_BF16;
+  p.qs_sb = cu_seq_q ? 0 : q_scale_stride_batch;
+  p.qs_ss = q_scale_stride_token;
+  p.qs_sh = q_scale_stride_head;
+  p.qs_group = qquant && q_scale_mode == 3 ? (int32_t)(head_size / q_scale_groups) : 1;
+  p.bt_heads = block_table_heads;
+  p.q_vec = (q_dtype == TMO_DTYPE_BF16 || q_dtype == TMO_DTYPE_F16) &&
+            reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
             p.q_sb % 8 == 0 && q_stride_token % 8 == 0 && q_stride_head % 8 == 0 &&
             (!quant || scale_mode != 2 || reinterpret_cast<uintptr_t>(k_scale) % 16 == 0);
   p.ws = static_cast<float*>(workspace);
@@ -1312,7 +1383,8 @@ extern "C" int tmo_hip_cached_kv_attn(
               head_size_v == head_size &&
               k_cache_dim == (int4 ? head_size / 2 : head_size) && v_cache_dim == head_size &&
               !(int4 && v_pair_channels) && block_size % 16 == 0 && al(k_cache, 16) &&
-              al(v_cache, 16) && q_dtype != TMO_DTYPE_F32;
+              al(v_cache, 16) && q_dtype != TMO_DTYPE_F32 &&
+              (block_table_heads != num_q_heads || num_q_heads == num_kv_heads);
   if (quant)
     mfma = mfma && scale_mode != 3 &&
            (scale_mode != 1 ||
@@ -1339,17 +1411,16 @@ extern "C" int tmo_hip_cached_kv_attn(
   int64_t per = (max_context_len + splits - 1) / splits;
   per = (per + 63) / 64 * 64;
   p.split_tokens = per > 0 ? per : 64;
-  // quantised caches: bf16 and f16 q are exact f16 operands after the power-of-two scaling; q
-  // folded with per-channel key scales needs the lo operand
+  // quantised caches: bf16 and f16 q, and int8 / float8_e4m3fn q codes, are exact f16 operands
+  // after the power-of-two scaling; q folded with per-channel key scales or group-wise q
+  // scales needs the lo operand
+  const bool qlo = scale_mode == 2 || p.qs_mode == 3;
   if (cache_dtype == TMO_DTYPE_I8)
-    return p.s_bf16 ? launch_mfma<0, true>(p, scale_mode == 2, st)
-                    : launch_mfma<0, false>(p, scale_mode == 2, st);
+    return p.s_bf16 ? launch_mfma<0, true>(p, qlo, st) : launch_mfma<0, false>(p, qlo, st);
   if (cache_dtype == TMO_DTYPE_F8E4M3)
-    return p.s_bf16 ? launch_mfma<3, true>(p, scale_mode == 2, st)
-                    : launch_mfma<3, false>(p, scale_mode == 2, st);
+    return p.s_bf16 ? launch_mfma<3, true>(p, qlo, st) : launch_mfma<3, false>(p, qlo, st);
   if (int4)
-    return p.s_bf16 ? launch_mfma<4, true>(p, scale_mode == 2, st)
-                    : launch_mfma<4, false>(p, scale_mode == 2, st);
+    return p.s_bf16 ? launch_mfma<4, true>(p, qlo, st) : launch_mfma<4, false>(p, qlo, st);
   if (cache_dtype == TMO_DTYPE_BF16) return launch_mfma<1, false>(p, false, st);
   return launch_mfma<2, false>(p, false, st);
 }
@@ -1371,11 +1442,13 @@ extern "C" int tmo_hip_single_query_cached_kv_attn(
   // contiguous per-token scales [num_blocks, Hkv, block_size]
   const int64_t sb = num_kv_heads * block_size, sh = block_size;
   if (cache_dtype == TMO_DTYPE_I4) return TMO_ERR_UNSUPPORTED_DTYPE;
+  if (q_dtype == TMO_DTYPE_I8 || q_dtype == TMO_DTYPE_F8E4M3) return TMO_ERR_UNSUPPORTED_DTYPE;
   return tmo_hip_cached_kv_attn(
-      q, q_stride_seq, 0, q_stride_head, nullptr, 1, 0, k_cache, v_cache, head_size, head_size,
-      k_scale, v_scale, scale_mode, TMO_DTYPE_F32, sb, sh, sb, sh, block_tables, max_blocks,
-      context_lens, alibi_slopes, nullptr, nullptr, 0, 0, 0, 0, out, out_stride_seq, 0,
-      out_stride_head, lse, lse_stride_seq, 0, lse_stride_head, batch, num_q_heads,
-      num_kv_heads, head_size, head_size, num_blocks, block_size, max_context_len, window_left,
-      softmax_scale, q_dtype, cache_dtype, 0, splits, workspace, workspace_bytes, stream);
+      q, q_stride_seq, 0, q_stride_head, nullptr, 0, TMO_DTYPE_F32, 0, 0, 0, 0, nullptr, 1, 0,
+      k_cache, v_cache, head_size, head_size, k_scale, v_scale, scale_mode, TMO_DTYPE_F32, sb,
+      sh, sb, sh, block_tables, max_blocks, 0, context_lens, alibi_slopes, nullptr, nullptr, 0,
+      0, 0, 0, out, out_stride_seq, 0, out_stride_head, lse, lse_stride_seq, 0,
+      lse_stride_head, batch, num_q_heads, num_kv_heads, head_size, head_size, num_blocks,
+      block_size, max_context_len, window_left, softmax_scale, q_dtype, cache_dtype, 0, q_dtype,
+      splits, workspace, workspace_bytes, stream);
 }

@@ -1033,8 +1033,8 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
                                  const c10::optional<torch::Tensor>& cu_seq_q,
                                  c10::SymInt max_seq_q, const c10::optional<torch::Tensor>& sink) {
   const char* op = "single_query_cached_kv_attn";
-  TORCH_CHECK(!q_quant_scale.has_value() && !out_quant_scale.has_value(), op,
-              ": quantised q / output are not supported by this build");
+  TORCH_CHECK(!out_quant_scale.has_value(), op,
+              ": out_quant_scale is a reserved parameter and must be None (_ops.py:857)");
   TORCH_CHECK(compute_dtype == "float" || compute_dtype == "half" || compute_dtype == "bfloat16",
               op, ": compute_dtype must be float, half or bfloat16 (the softmax runs in fp32)");
   TORCH_CHECK(windows_size_right.expect_int() == -1, op, ": windows_size_right must be -1");
@@ -1055,9 +1055,16 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   TORCH_CHECK(!(four && cu_seq_q.has_value()), op, ": cu_seq_q goes with a 3-D q");
   const at::Tensor& q = q_ori;
   TORCH_CHECK(q.size(-1) <= 1 || q.stride(-1) == 1, "q must have a contiguous last dim");
-  const int qdt = dtype_code(q.scalar_type());
-  TORCH_CHECK(qdt == TMO_DTYPE_F32 || qdt == TMO_DTYPE_F16 || qdt == TMO_DTYPE_BF16, op,
-              ": q must be float, half or bfloat16, got ", q.scalar_type());
+  // q: float, half, bfloat16, or int8 / float8_e4m3fn codes with q_quant_scale (_ops.py:853-856,
+  // 868); the output then has its own dtype (float8_e4m3fn q: half, _ops.py:858)
+  const bool qquant = q.scalar_type() == at::kChar || q.scalar_type() == at::kFloat8_e4m3fn;
+  const int qdt = q.scalar_type() == at::kChar ? TMO_DTYPE_I8
+                  : q.scalar_type() == at::kFloat8_e4m3fn ? TMO_DTYPE_F8E4M3
+                                                          : dtype_code(q.scalar_type());
+  TORCH_CHECK(qdt == TMO_DTYPE_F32 || qdt == TMO_DTYPE_F16 || qdt == TMO_DTYPE_BF16 || qquant, op,
+              ": q must be float, half, bfloat16, int8 or float8_e4m3fn, got ", q.scalar_type());
+  TORCH_CHECK(qquant == q_quant_scale.has_value(), op,
+              ": q_quant_scale goes with (and only with) an int8 or float8_e4m3fn q");
   const int64_t Hq = q.size(-2), D = q.size(-1);
   check_device(context_lens, q_ori, "context_lens");
   TORCH_CHECK(context_lens.scalar_type() == at::kInt && context_lens.dim() == 1 &&
@@ -1107,9 +1114,17 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   const int64_t kdim = k_cache.size(3);
   check_device(output, q_ori, "output");
   TORCH_CHECK(output.dim() == q_ori.dim() &&
-                  output.sizes().slice(0, q_ori.dim() - 1) == q_ori.sizes().slice(0, q_ori.dim() - 1) &&
-                  output.scalar_type() == q.scalar_type(),
-              op, ": output must be q's shape with head_size_v channels, in q's dtype");
+                  output.sizes().slice(0, q_ori.dim() - 1) == q_ori.sizes().slice(0, q_ori.dim() - 1),
+              op, ": output must be q's shape with head_size_v channels");
+  const int odt = dtype_code(output.scalar_type());
+  if (qquant) {
+    TORCH_CHECK(odt == TMO_DTYPE_F32 || odt == TMO_DTYPE_F16 || odt == TMO_DTYPE_BF16, op,
+                ": the output of a quantised q must be float, half or bfloat16");
+    TORCH_CHECK(q.scalar_type() != at::kFloat8_e4m3fn || odt == TMO_DTYPE_F16, op,
+                ": the output must be half when q is float8_e4m3fn (_ops.py:858)");
+  } else {
+    TORCH_CHECK(output.scalar_type() == q.scalar_type(), op, ": output must have q's dtype");
+  }
   const int64_t Dv = output.size(-1);
   int64_t vdim = kdim;
   int v_pair_channels = 0;
@@ -1158,7 +1173,10 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   // quantised caches: int8 codes or float8_e4m3fn values (_ops.py:868; bit size 8 covers both,
   // _ops.py:1061), or int4 pairs (bit size 4), with per-token / per-channel / per-group scales
   const bool int8 = cdt == TMO_DTYPE_I8 || cdt == TMO_DTYPE_F8E4M3 || int4;
-  TORCH_CHECK(int4 || int8 == (kv_cache_quant_bit_size == 8), op,
+  // caches "the same as q" (kv_cache_quant_bit_size -1, _ops.py:852) under an int8 /
+  // float8_e4m3fn q: codes read as they are, i.e. with unit scales
+  const bool same_as_q = qquant && kv_cache_quant_bit_size == -1 && cdt == qdt;
+  TORCH_CHECK(int4 || same_as_q || int8 == (kv_cache_quant_bit_size == 8), op,
               ": kv_cache_quant_bit_size 8 goes with int8 or float8_e4m3fn caches, -1 with caches ",
               "of q's dtype");
   TORCH_CHECK(int8 || cdt == qdt, op, ": unquantised caches must have q's dtype");
@@ -1168,7 +1186,13 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   int smode = 0;
   at::Tensor ks, vs;
   int64_t ks_sb = 0, ks_sh = 0, vs_sb = 0, vs_sh = 0;
-  if (int8) {
+  if (same_as_q) {
+    TORCH_CHECK(!k_cache_quant_scale.has_value() && !v_cache_quant_scale.has_value(), op,
+                ": caches of q's dtype take no scales");
+    smode = 2;
+    ks = at::ones({Hkv, D}, q_ori.options().dtype(at::kFloat));
+    vs = at::ones({Hkv, Dv}, q_ori.options().dtype(at::kFloat));
+  } else if (int8) {
     TORCH_CHECK(k_cache_quant_scale.has_value() && v_cache_quant_scale.has_value(), op,
                 ": int8 caches need k_cache_quant_scale and v_cache_quant_scale");
     const at::Tensor& ksc = *k_cache_quant_scale;
@@ -1221,11 +1245,56 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
       vs = norm(vsc, Dv, vs_sb, vs_sh, "v_cache_quant_scale");
     }
   }
+  // block tables [batch, max_blocks], or sparse-KV [batch, kv_heads or heads, max_blocks]
+  // (_ops.py:834): each KV head's (query head's) own pages
   check_device(block_tables, q_ori, "block_tables");
-  TORCH_CHECK(block_tables.scalar_type() == at::kInt && block_tables.dim() == 2 &&
-                  block_tables.size(0) == B && block_tables.is_contiguous(),
-              op, ": block_tables must be a contiguous int32 [batch, max_blocks] tensor, got ",
-              block_tables.sizes());
+  TORCH_CHECK(block_tables.scalar_type() == at::kInt && block_tables.is_contiguous() &&
+                  block_tables.size(0) == B &&
+                  (block_tables.dim() == 2 ||
+                   (block_tables.dim() == 3 &&
+                    (block_tables.size(1) == Hkv || block_tables.size(1) == Hq))),
+              op, ": block_tables must be a contiguous int32 [batch, max_blocks] or [batch, ",
+              "kv_heads or heads, max_blocks] tensor, got ", block_tables.sizes());
+  const int64_t bt_heads = block_tables.dim() == 3 ? block_tables.size(1) : 0;
+  // q_quant_scale (_ops.py:853-856): [1] per tensor, q's leading shape per token and head, or
+  // that shape plus scale_num per channel group; float32 or bfloat16 (_ops.py:871)
+  int qs_mode = 0, qs_dt = TMO_DTYPE_F32;
+  int64_t qs_sb = 0, qs_ss = 0, qs_sh = 0, qs_groups = 0;
+  at::Tensor qst;
+  if (qquant) {
+    qst = *q_quant_scale;
+    check_device(qst, q_ori, "q_quant_scale");
+    TORCH_CHECK(qst.scalar_type() == at::kFloat || qst.scalar_type() == at::kBFloat16, op,
+                ": q_quant_scale must be float32 or bfloat16");
+    qs_dt = qst.scalar_type() == at::kBFloat16 ? TMO_DTYPE_BF16 : TMO_DTYPE_F32;
+    const auto lead = q.sizes().slice(0, q.dim() - 1);
+    if (qst.numel() == 1) {
+      qs_mode = 1;
+      qst = qst.reshape({1}).contiguous();
+    } else if (qst.sizes() == lead) {
+      qs_mode = 2;
+      if (four) {
+        qs_sb = qst.stride(0), qs_ss = qst.stride(1), qs_sh = qst.stride(2);
+      } else {
+        (cu ? qs_ss : qs_sb) = qst.stride(0);
+        qs_sh = qst.stride(1);
+      }
+    } else {
+      TORCH_CHECK(qst.dim() == q.dim() && qst.sizes().slice(0, q.dim() - 1) == lead &&
+                      qst.size(-1) > 0 && D % qst.size(-1) == 0,
+                  op, ": q_quant_scale must be [1], q's shape without head_size, or that with ",
+                  "a last dim dividing head_size, got ", qst.sizes());
+      qs_mode = 3;
+      qst = qst.contiguous();
+      qs_groups = qst.size(-1);
+      if (four) {
+        qs_sb = qst.stride(0), qs_ss = qst.stride(1), qs_sh = qst.stride(2);
+      } else {
+        (cu ? qs_ss : qs_sb) = qst.stride(0);
+        qs_sh = qst.stride(1);
+      }
+    }
+  }
   const float* alibi = nullptr;
   if (alibi_slopes.has_value()) {
     check_device(*alibi_slopes, q_ori, "alibi_slopes");
@@ -1312,16 +1381,19 @@ void single_query_cached_kv_attn(const torch::Tensor& q_ori, const torch::Tensor
   const int64_t ws_bytes = tmo_hip_cached_kv_attn_workspace_bytes(B, Hkv, Hq, Dv, seq_q, splits);
   if (ws_bytes > 0)
     ws = at::empty({(ws_bytes + 3) / 4}, q_ori.options().dtype(at::kFloat));
+  const bool scaled = int8 || same_as_q;
   const int st = tmo_hip_cached_kv_attn(
-      q.data_ptr(), q_sb, q_ss, q.stride(-2), cu, seq_q, total_q, k_cache.data_ptr(),
+      q.data_ptr(), q_sb, q_ss, q.stride(-2), qquant ? qst.data_ptr() : nullptr, qs_mode, qs_dt,
+      qs_sb, qs_ss, qs_sh, qs_groups, cu, seq_q, total_q, k_cache.data_ptr(),
       v_cache.has_value() ? v_cache->data_ptr() : nullptr, kdim, vdim,
-      int8 ? ks.data_ptr() : nullptr, int8 ? vs.data_ptr() : nullptr, smode,
-      int8 && ks.scalar_type() == at::kBFloat16 ? TMO_DTYPE_BF16 : TMO_DTYPE_F32,
-      ks_sb, ks_sh, vs_sb, vs_sh, block_tables.data_ptr<int32_t>(), block_tables.size(1),
-      context_lens.data_ptr<int32_t>(), alibi, sink_p, mask_p, mask_dt, mask_len, m_sb, m_ss,
-      out.data_ptr(), o_sb, o_ss, out.stride(-2), lse, lse_sb, lse_ss, lse_sh, B, Hq, Hkv, D, Dv,
-      NB, BS, max_ctx, window, static_cast<float>(softmax_scale), qdt, cdt, v_pair_channels,
-      splits, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(q_ori));
+      scaled ? ks.data_ptr() : nullptr, scaled ? vs.data_ptr() : nullptr, smode,
+      scaled && ks.scalar_type() == at::kBFloat16 ? TMO_DTYPE_BF16 : TMO_DTYPE_F32,
+      ks_sb, ks_sh, vs_sb, vs_sh, block_tables.data_ptr<int32_t>(), block_tables.size(-1),
+      bt_heads, context_lens.data_ptr<int32_t>(), alibi, sink_p, mask_p, mask_dt, mask_len, m_sb,
+      m_ss, out.data_ptr(), o_sb, o_ss, out.stride(-2), lse, lse_sb, lse_ss, lse_sh, B, Hq, Hkv,
+      D, Dv, NB, BS, max_ctx, window, static_cast<float>(softmax_scale), qdt, cdt,
+      v_pair_channels, odt, splits, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
+      stream_of(q_ori));
   check_status(st, op);
 }
 

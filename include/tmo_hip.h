@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TMO_HIP_ABI_VERSION 16
+#define TMO_HIP_ABI_VERSION 17
 
 /* element types */
 enum tmo_dtype {
@@ -444,8 +444,17 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
  *     of a [total_q, Hq, D] q, row t at t * q_stride_token (q_stride_batch unused); seq_q is
  *     an upper bound of the counts (tokens past it are not computed) and rows outside
  *     [0, total_q) are skipped.
- * out (q's dtype, head_size_v channels) and lse (nullable, fp32) are addressed the same way
- * with their own strides.
+ * out (out_dtype, head_size_v channels) and lse (nullable, fp32) are addressed the same way
+ * with their own strides.  q of F32 / F16 / BF16 takes out_dtype = q_dtype.  q of
+ * TMO_DTYPE_I8 / TMO_DTYPE_F8E4M3 holds codes (_ops.py:853-856, 868; quantised caches only):
+ * q = code * q_scale, with q_scale (fp32 or bf16, q_scale_dtype) by q_scale_mode 1 per tensor
+ * (one value), 2 per token and head (element i * q_scale_stride_batch + token row *
+ * q_scale_stride_token + hq * q_scale_stride_head, addressed like q), 3 per group of
+ * head_size / q_scale_groups channels (that element plus d / group, the strides counting
+ * groups); out_dtype F32, F16 or BF16.
+ * block_tables: [batch, max_blocks] (block_table_heads 0), or sparse-KV tables [batch,
+ * block_table_heads, max_blocks] with block_table_heads = Hkv (each KV head its own pages) or
+ * Hq (each query head its own; _ops.py:834).
  * Caches [num_blocks, Hkv, block_size, k_cache_dim / v_cache_dim] contiguous: k_j is the first
  * head_size channels of its K row, v_j the first head_size_v of its V row -- of its K row when
  * v_cache is null (K and V in one cache, reference _ops.py:828-831; v_cache_dim unused).
@@ -477,7 +486,7 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
  * head_size up to 4096, head_size_v up to 512; the MFMA kernels take K and V head sizes of 64,
  * 128 or 256 (equal, with cache rows of that many elements -- int4: K rows of head_size / 2
  * bytes, V pairing rows) and per-token or per-channel scales, a VALU kernel the rest (int4
- * V pairing channels included).
+ * V pairing channels and per-query-head tables with grouped heads included).
  * Arithmetic: fp32 accumulation (MFMA with bf16/f16 operands: int8 codes and e4m3fn values are
  * exact; q and the probabilities are split into two operands when one is not exact), softmax
  * in fp32.
@@ -486,19 +495,24 @@ int tmo_hip_reshape_from_cache(void* key, void* value,
  * max_context_len <= 0 (negative included) means an unknown maximum: one split per sequence
  * unless `splits` says otherwise; it never limits the keys read.
  * Replaces tmo::torch_api::single_query_cached_kv_attn (reference
- * include/torch_mlu_ops.h:107-130) without q/out quantisation, called by
+ * include/torch_mlu_ops.h:107-130) without out quantisation (out_quant_scale is reserved
+ * there), called by
  * torch_mlu_ops.single_query_cached_kv_attn (reference _ops.py:777-900; q forms :824,
  * cu_seq_q / max_seq_q :860-861, sink :864).
  */
 int tmo_hip_cached_kv_attn(const void* q, int64_t q_stride_batch, int64_t q_stride_token,
-                           int64_t q_stride_head, const int32_t* cu_seq_q, int64_t seq_q,
+                           int64_t q_stride_head, const void* q_scale, int q_scale_mode,
+                           int q_scale_dtype, int64_t q_scale_stride_batch,
+                           int64_t q_scale_stride_token, int64_t q_scale_stride_head,
+                           int64_t q_scale_groups, const int32_t* cu_seq_q, int64_t seq_q,
                            int64_t total_q, const void* k_cache, const void* v_cache,
                            int64_t k_cache_dim, int64_t v_cache_dim, const void* k_scale,
                            const void* v_scale, int scale_mode, int scale_dtype,
                            int64_t k_scale_stride_block,
                            int64_t k_scale_stride_head, int64_t v_scale_stride_block,
                            int64_t v_scale_stride_head, const int32_t* block_tables,
-                           int64_t max_blocks, const int32_t* context_lens,
+                           int64_t max_blocks, int64_t block_table_heads,
+                           const int32_t* context_lens,
                            const float* alibi_slopes, const float* sink, const void* mask,
                            int mask_dtype, int64_t mask_len, int64_t mask_stride_batch,
                            int64_t mask_stride_token, void* out,
@@ -508,8 +522,9 @@ int tmo_hip_cached_kv_attn(const void* q, int64_t q_stride_batch, int64_t q_stri
                            int64_t num_q_heads, int64_t num_kv_heads, int64_t head_size,
                            int64_t head_size_v, int64_t num_blocks, int64_t block_size,
                            int64_t max_context_len, int64_t window_left, float softmax_scale,
-                           int q_dtype, int cache_dtype, int v_pair_channels, int64_t splits,
-                           void* workspace, int64_t workspace_bytes, void* stream);
+                           int q_dtype, int cache_dtype, int v_pair_channels, int out_dtype,
+                           int64_t splits, void* workspace, int64_t workspace_bytes,
+                           void* stream);
 
 /* Workspace bytes tmo_hip_cached_kv_attn needs for `splits` with up to seq_q tokens per
  * sequence (0 when splits <= 1). */

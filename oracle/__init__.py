@@ -71,10 +71,12 @@ def lib() -> ctypes.CDLL:
             [c_void_p, c_void_p, c_int, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p,
              c_int64, c_double, c_void_p, c_void_p, c_int]
         L.oracle_single_query_attn.restype = c_int
-        L.oracle_cached_kv_attn.argtypes = [c_void_p, c_int, c_int64, c_int64, c_void_p,
-                                            c_int64, c_int64, c_void_p, c_void_p, c_int, c_int] + \
+        L.oracle_cached_kv_attn.argtypes = [c_void_p, c_int, c_int64, c_int64,
+                                            c_void_p, c_int, c_int64, c_int64, c_int64,
+                                            c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int,
+                                            c_int] + \
             [c_int64] * 7 + [c_void_p, c_void_p, c_int] + [c_int64] * 4 + \
-            [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
+            [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
              c_void_p, c_int, c_int64, c_int64, c_int64, c_int64,
              c_double, c_void_p, c_void_p, c_int]
         L.oracle_cached_kv_attn.restype = c_int
@@ -315,7 +317,8 @@ def single_query_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_s
 def cached_kv_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scale: float,
                    k_scale=None, v_scale=None, alibi_slopes=None, window_left: int = -1,
                    cu_seq_q=None, sink=None, head_size_v: Optional[int] = None,
-                   int4: bool = False, mask=None, nthreads: Optional[int] = None):
+                   int4: bool = False, mask=None, q_scale=None,
+                   nthreads: Optional[int] = None):
     """reference _ops.py:777-900 with several query tokens per sequence (decision D12 of
     tmo_oracle.c), in float64.  q [B, S, Hq, D] (S tokens per sequence), or [T, Hq, D] with
     cu_seq_q [B + 1] (rows cu_seq_q[i] .. cu_seq_q[i + 1] - 1 are sequence i's), or [B, Hq, D]
@@ -329,8 +332,23 @@ def cached_kv_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scal
     sequence of cu_seq_q holds are NaN.  int4 (kv_cache_quant_bit_size 4, decision D16): int8
     caches of 4-bit pairs, K [NB, Hkv, BS, D / 2] pairing channels, V [NB, Hkv, BS / 2, Dv]
     pairing rows or [NB, Hkv, BS, Dv / 2] pairing channels.  mask [B, S, mask_len] (float32 /
-    float16 / bfloat16, D16) is added to the logits of each sequence's last mask_len keys."""
+    float16 / bfloat16, D16) is added to the logits of each sequence's last mask_len keys.
+    q of int8 / float8_e4m3fn (D17) holds codes times q_scale: [1] per tensor, q's leading
+    shape per token and head, or that shape plus scale_num per channel group.  block_tables
+    [B, Hkv or Hq, max_blocks] (D17): each KV head's (or query head's) own pages."""
     four = q.dim() == 4
+    qs, qs_mode, qs_st, qs_sh, qs_groups = None, 0, 0, 0, 0
+    if q.dtype in (torch.int8, torch.float8_e4m3fn):
+        assert q_scale is not None
+        qsc = q_scale.to(torch.float32)
+        if qsc.numel() == 1:
+            qs, qs_mode = qsc.reshape(1).contiguous(), 1
+        elif tuple(qsc.shape) == tuple(q.shape[:-1]):
+            qs, qs_mode = qsc.reshape(-1, q.shape[-2]).contiguous(), 2
+            qs_st, qs_sh = q.shape[-2], 1
+        else:
+            assert qsc.dim() == q.dim() and tuple(qsc.shape[:-1]) == tuple(q.shape[:-2]) + (q.shape[-2],)
+            qs, qs_mode, qs_groups = qsc.contiguous(), 3, qsc.shape[-1]
     if four:
         B, S = q.shape[:2]
         q = q.reshape(B * S, q.shape[2], q.shape[3])
@@ -368,6 +386,7 @@ def cached_kv_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scal
         vs, vmode, strides[2:4] = one(v_scale)
         assert vmode == mode
     bt = block_tables.to(torch.int32).contiguous()
+    bt_heads = bt.shape[1] if bt.dim() == 3 else 0
     lens = context_lens.to(torch.int32).contiguous()
     cu = cu_seq_q.to(torch.int32).contiguous() if cu_seq_q is not None else None
     assert cu is None or (not four and cu.numel() == B + 1)
@@ -381,9 +400,10 @@ def cached_kv_attn(q, k_cache, v_cache, block_tables, context_lens, softmax_scal
     out = torch.full((T, Hq, Dv), float("nan"), dtype=torch.float64)
     lse = torch.full((T, Hq), float("nan"), dtype=torch.float64)
     rc = lib().oracle_cached_kv_attn(
-        _ptr(q), _DT[q.dtype], q.stride(0), q.stride(1), _ptr(cu), S, T, _ptr(k_cache),
+        _ptr(q), _ATTN_CACHE_DT[q.dtype], q.stride(0), q.stride(1), _ptr(qs), qs_mode, qs_st,
+        qs_sh, qs_groups, _ptr(cu), S, T, _ptr(k_cache),
         _ptr(vc), cdt, v_ch, NB, Hkv, BS, D, Dv, krow, vrow, _ptr(ks), _ptr(vs), mode, *strides,
-        _ptr(bt), bt.shape[1], _ptr(lens), B, Hq, _ptr(al), _ptr(sk), _ptr(mk), mdt, mlen, msb,
+        _ptr(bt), bt.shape[-1], bt_heads, _ptr(lens), B, Hq, _ptr(al), _ptr(sk), _ptr(mk), mdt, mlen, msb,
         mss, int(window_left),
         float(softmax_scale), _ptr(out), _ptr(lse), nthreads or default_threads())
     _check(rc, "cached_kv_attn")

@@ -108,6 +108,14 @@
  *       mask_len % seq_q == 0) but not which keys the columns address: the last mask_len
  *       keys -- the newest tokens, the ones a speculative-decoding tree mask covers -- is this
  *       build's reading.
+ *   D17 single_query_cached_kv_attn's quantised q and sparse-KV block tables (_ops.py:834,
+ *       853-856, 862, 868-875, 887-890).  q of int8 or float8_e4m3fn holds codes: q = code *
+ *       q_quant_scale, the scale per tensor ([1]), per token and head ([total_q, heads] or
+ *       [batch, seq_q, heads]) or per group of head_size / scale_num channels ([batch, seq_q,
+ *       heads, scale_num]), the product taken exactly; the output is out_dtype.  Sparse KV:
+ *       block_tables [batch, head_num_kv, max_blocks] or [batch, head_num_q, max_blocks]
+ *       give each KV head (or each query head) its own pages; context lengths stay per
+ *       sequence.
  *   D9  offline (static-scale) quantisation divides: code = clip(RNE(RN(fp32(x) / s)), -128, 127)
  *       for int8, fp8 = e4m3fn_RNE(clip(RN(fp32(x) / s), -448, 448)), s the fp32 per-channel
  *       scale or the per-tensor scalar rounded to fp32 (_ops.py:1652-1670; the division is
@@ -1138,10 +1146,12 @@ int oracle_scaled_quantize_per_token(const void* x, int dtype, int64_t n0, int64
 
 typedef struct {
     const void* q; int q_dtype; int64_t q_st, q_sh;      /* q rows [T, Hq, D], element strides */
+    const float* qs; int qs_mode; int64_t qs_st, qs_sh, qs_groups;  /* D17 q scales */
     const int32_t* cu; int64_t S, T;                     /* cu_seq_q [B + 1], or S tokens each */
     const void* kc; const void* vc; int c_dtype;         /* caches [NB, Hkv, BS, krow / vrow] */
     int v_ch;                                            /* DT_I4: V pairs channels (else rows) */
     int64_t NB, Hkv, BS, D, Dv, krow, vrow, Hq, MB, B;
+    int64_t bt_heads;                                    /* D17: 0, Hkv or Hq block-table rows */
     const float* ks; const float* vs; int smode;         /* 0 none, 1 token, 2 channel, 3 group */
     int64_t ks_sb, ks_sh, vs_sb, vs_sh;                  /* per-token scale strides */
     const int32_t* bt; const int32_t* lens;
@@ -1186,6 +1196,20 @@ static double value_val(const sqa_ctx* c, int64_t blk, int64_t hk, int64_t row, 
     return (double)load_elem(c->vc, r * c->vrow + d, c->c_dtype);
 }
 
+/* Query element d of row t, head hq (D17): the stored value, or for int8 / float8_e4m3fn q
+ * the code times its scale -- per tensor (qs[0]), per (row, head) (qs[t * qs_st + hq * qs_sh])
+ * or per group of D / qs_groups channels (qs[(t * Hq + hq) * qs_groups + d / (D / qs_groups)]);
+ * the product is exact in double. */
+static double q_val(const sqa_ctx* c, int64_t t, int64_t hq, int64_t d) {
+    const int64_t e = t * c->q_st + hq * c->q_sh + d;
+    if (c->q_dtype != DT_I8 && c->q_dtype != DT_F8E4M3) return (double)load_elem(c->q, e, c->q_dtype);
+    double x = cache_code(c->q, e, c->q_dtype);
+    if (c->qs_mode == 1) x *= (double)c->qs[0];
+    else if (c->qs_mode == 2) x *= (double)c->qs[t * c->qs_st + hq * c->qs_sh];
+    else if (c->qs_mode == 3) x *= (double)c->qs[(t * c->Hq + hq) * c->qs_groups + d / (c->D / c->qs_groups)];
+    return x;
+}
+
 /* The sequence of query row t and the row's token index in it; -1 when no sequence holds t. */
 static int64_t sqa_seq(const sqa_ctx* c, int64_t t, int64_t* s, int64_t* nq) {
     if (!c->cu) {
@@ -1210,6 +1234,8 @@ static void sqa_range(void* p, int64_t lo, int64_t hi) {
         int64_t t = w / c->Hq, hq = w % c->Hq, hk = hq / g, tok, nq;
         int64_t i = sqa_seq(c, t, &tok, &nq);
         if (i < 0) continue;                        /* a row no sequence holds: untouched */
+        /* D17: the sequence's block table, or its KV head's / query head's row of it */
+        const int32_t* btr = c->bt + (c->bt_heads == 0 ? i : i * c->bt_heads + (c->bt_heads == c->Hq ? hq : hk)) * c->MB;
         int64_t L = c->lens[i];
         if (L > c->MB * c->BS) L = c->MB * c->BS;
         const int64_t P = L - nq + tok;             /* the token's position: keys j <= P */
@@ -1219,11 +1245,11 @@ static void sqa_range(void* p, int64_t lo, int64_t hi) {
         for (int64_t d = 0; d < c->Dv; ++d) o[d] = 0.0;
         double m = c->sink ? (double)c->sink[hq] : -INFINITY;
         for (int64_t j = j0; j < jend; ++j) {
-            int64_t blk = c->bt[i * c->MB + j / c->BS], row = j % c->BS;
+            int64_t blk = btr[j / c->BS], row = j % c->BS;
             if (blk < 0 || blk >= c->NB) { s[j] = -INFINITY; continue; }   /* missing page: masked */
             double acc = 0.0;
             for (int64_t d = 0; d < c->D; ++d)
-                acc += (double)load_elem(c->q, t * c->q_st + hq * c->q_sh + d, c->q_dtype) *
+                acc += q_val(c, t, hq, d) *
                        key_val(c, blk, hk, row, d);
             s[j] = c->scale * acc;
             if (c->alibi) s[j] += (double)c->alibi[i * c->Hq + hq] * (double)(j - P);
@@ -1239,7 +1265,7 @@ static void sqa_range(void* p, int64_t lo, int64_t hi) {
                 if (s[j] == -INFINITY) continue;
                 double pj = exp(s[j] - m);
                 l += pj;
-                int64_t blk = c->bt[i * c->MB + j / c->BS], row = j % c->BS;
+                int64_t blk = btr[j / c->BS], row = j % c->BS;
                 for (int64_t d = 0; d < c->Dv; ++d) o[d] += pj * value_val(c, blk, hk, row, d);
             }
             for (int64_t d = 0; d < c->Dv; ++d) o[d] /= l;
@@ -1268,22 +1294,32 @@ static void sqa_range(void* p, int64_t lo, int64_t hi) {
  * DT_I4 caches (D16): k_row / v_row count bytes; K pairs channels, V pairs the rows of a page
  * ([NB, Hkv, BS / 2, v_row], v_ch 0) or channels (v_ch 1).  mask (D16, nullable): element
  * i * mask_sb + s * mask_ss + m of mask_dtype (F32 / F16 / BF16) is added to the logit of key
- * L - mask_len + m of query token s of sequence i. */
+ * L - mask_len + m of query token s of sequence i.
+ * D17: q of DT_I8 / DT_F8E4M3 holds codes with q_scale (q_scale_mode 1 per tensor, 2 per
+ * (row, head) at t * qs_st + hq * qs_sh, 3 per group of D / qs_groups channels, contiguous
+ * [T, Hq, qs_groups]); bt_heads 0: block_tables [B, max_blocks]; Hkv or Hq: [B, bt_heads,
+ * max_blocks], the row of the query head's KV head or of the query head itself. */
 int oracle_cached_kv_attn(const void* q, int q_dtype, int64_t q_st, int64_t q_sh,
-                          const int32_t* cu_seq_q, int64_t S, int64_t T,
+                          const float* q_scale, int q_scale_mode, int64_t qs_st, int64_t qs_sh,
+                          int64_t qs_groups, const int32_t* cu_seq_q, int64_t S, int64_t T,
                           const void* k_cache, const void* v_cache, int cache_dtype, int v_ch,
                           int64_t NB, int64_t Hkv, int64_t BS, int64_t D, int64_t Dv,
                           int64_t k_row, int64_t v_row,
                           const float* k_scale, const float* v_scale, int scale_mode,
                           int64_t ks_sb, int64_t ks_sh, int64_t vs_sb, int64_t vs_sh,
-                          const int32_t* block_tables, int64_t max_blocks,
+                          const int32_t* block_tables, int64_t max_blocks, int64_t bt_heads,
                           const int32_t* context_lens, int64_t B, int64_t Hq,
                           const float* alibi, const float* sink, const void* mask,
                           int mask_dtype, int64_t mask_len, int64_t mask_sb, int64_t mask_ss,
                           int64_t window_left, double softmax_scale, double* out, double* lse,
                           int nthreads) {
     const int quant = cache_dtype == DT_I8 || cache_dtype == DT_F8E4M3 || cache_dtype == DT_I4;
-    if (elem_size(q_dtype) == 0 || q_dtype == DT_I8 || (!quant && elem_size(cache_dtype) == 0))
+    const int qquant = q_dtype == DT_I8 || q_dtype == DT_F8E4M3;
+    if (qquant && (q_scale_mode < 1 || q_scale_mode > 3 || !q_scale ||
+                   (q_scale_mode == 3 && (qs_groups <= 0 || D % qs_groups != 0))))
+        return -3;
+    if (bt_heads != 0 && bt_heads != Hkv && bt_heads != Hq) return -1;
+    if ((!qquant && elem_size(q_dtype) == 0) || (!quant && elem_size(cache_dtype) == 0))
         return -2;
     if (quant && (scale_mode < 1 || scale_mode > 3)) return -3;
     if (B < 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0 || BS <= 0 || D <= 0 || Dv <= 0 ||
@@ -1295,9 +1331,10 @@ int oracle_cached_kv_attn(const void* q, int q_dtype, int64_t q_st, int64_t q_sh
         return -1;
     if (mask && (mask_len < 0 || (mask_dtype != DT_F32 && mask_dtype != DT_F16 && mask_dtype != DT_BF16)))
         return -1;
-    sqa_ctx c = {q, q_dtype, q_st, q_sh, cu_seq_q, S, T, k_cache, v_cache, cache_dtype,
+    sqa_ctx c = {q, q_dtype, q_st, q_sh, q_scale, qquant ? q_scale_mode : 0, qs_st, qs_sh, qs_groups,
+                 cu_seq_q, S, T, k_cache, v_cache, cache_dtype,
                  cache_dtype == DT_I4 && v_ch, NB, Hkv,
-                 BS, D, Dv, k_row, v_row, Hq, max_blocks, B, k_scale, v_scale,
+                 BS, D, Dv, k_row, v_row, Hq, max_blocks, B, bt_heads, k_scale, v_scale,
                  quant ? scale_mode : 0, ks_sb, ks_sh, vs_sb, vs_sh,
                  block_tables, context_lens, alibi, sink, window_left, softmax_scale,
                  mask, mask_dtype, mask_len, mask_sb, mask_ss, out, lse};
@@ -1316,10 +1353,10 @@ int oracle_single_query_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q
                              const float* alibi, int64_t window_left, double softmax_scale,
                              double* out, double* lse, int nthreads) {
     if (scale_mode == 3) return -3;
-    if (cache_dtype == DT_I4) return -2;
-    return oracle_cached_kv_attn(q, q_dtype, q_sb, q_sh, NULL, 1, B < 0 ? 0 : B, k_cache,
-                                 v_cache, cache_dtype, 0, NB, Hkv, BS, D, D, D, D, k_scale, v_scale,
-                                 scale_mode, Hkv * BS, BS, Hkv * BS, BS, block_tables,
-                                 max_blocks, context_lens, B, Hq, alibi, NULL, NULL, 0, 0, 0, 0,
-                                 window_left, softmax_scale, out, lse, nthreads);
+    if (cache_dtype == DT_I4 || q_dtype == DT_I8 || q_dtype == DT_F8E4M3) return -2;
+    return oracle_cached_kv_attn(q, q_dtype, q_sb, q_sh, NULL, 0, 0, 0, 0, NULL, 1, B < 0 ? 0 : B,
+                                 k_cache, v_cache, cache_dtype, 0, NB, Hkv, BS, D, D, D, D,
+                                 k_scale, v_scale, scale_mode, Hkv * BS, BS, Hkv * BS, BS,
+                                 block_tables, max_blocks, 0, context_lens, B, Hq, alibi, NULL,
+                                 NULL, 0, 0, 0, 0, window_left, softmax_scale, out, lse, nthreads);
 }

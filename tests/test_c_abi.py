@@ -60,12 +60,13 @@ def lib():
         [ctypes.c_float, INT, INT, I64, P, I64, P]
     L.tmo_hip_attn_workspace_bytes.argtypes = [I64] * 6
     L.tmo_hip_attn_workspace_bytes.restype = I64
-    L.tmo_hip_cached_kv_attn.argtypes = [P, I64, I64, I64, P, I64, I64, P, P, I64, I64, P, P, INT,
-                                         INT, I64, I64, I64, I64, P, I64, P, P, P,
+    L.tmo_hip_cached_kv_attn.argtypes = [P, I64, I64, I64, P, INT, INT, I64, I64, I64, I64,
+                                         P, I64, I64, P, P, I64, I64, P, P, INT,
+                                         INT, I64, I64, I64, I64, P, I64, I64, P, P, P,
                                          P, INT, I64, I64, I64,
                                          P, I64, I64, I64,
                                          P, I64, I64, I64] + [I64] * 9 + \
-        [ctypes.c_float, INT, INT, INT, I64, P, I64, P]
+        [ctypes.c_float, INT, INT, INT, INT, I64, P, I64, P]
     L.tmo_hip_cached_kv_attn_workspace_bytes.argtypes = [I64] * 6
     L.tmo_hip_cached_kv_attn_workspace_bytes.restype = I64
     return L
@@ -375,12 +376,12 @@ def test_multi_token_attention_validation(lib):
     def call(q=FAKE, cu=None, S=4, T=0, B=2, Hq=8, Hkv=2, D=128, Dv=128, kdim=128, vdim=128,
              vc=FAKE, smode=1, ssb=32, BS=16, splits=1, ws=None, wsb=0, qdt=2, cdt=3,
              qss=128 * 8, oss=128 * 8, sink=None, sdt=0, mask=None, mdt=0, mlen=8, msb=32,
-             mss=8, vch=0, NB=16):
+             mss=8, vch=0, NB=16, qs=None, qsm=0, qsdt=0, qsst=8, qsg=0, bth=0, odt=None):
         return lib.tmo_hip_cached_kv_attn(
-            q, 4 * 1024, qss, 128, cu, S, T, FAKE, vc, kdim, vdim, FAKE, FAKE, smode, sdt, ssb, 16,
-            32, 16, FAKE, 4, FAKE, None, sink, mask, mdt, mlen, msb, mss, FAKE, 4 * 1024, oss,
-            128, None, 0, 0, 0, B, Hq, Hkv, D, Dv, NB, BS, 64, -1, 0.1, qdt, cdt, vch, splits, ws,
-            wsb, None)
+            q, 4 * 1024, qss, 128, qs, qsm, qsdt, 32, qsst, 1, qsg, cu, S, T, FAKE, vc, kdim, vdim,
+            FAKE, FAKE, smode, sdt, ssb, 16, 32, 16, FAKE, 4, bth, FAKE, None, sink, mask, mdt,
+            mlen, msb, mss, FAKE, 4 * 1024, oss, 128, None, 0, 0, 0, B, Hq, Hkv, D, Dv, NB, BS, 64,
+            -1, 0.1, qdt, cdt, vch, qdt if odt is None else odt, splits, ws, wsb, None)
     assert call(qdt=3) == EDTYPE
     assert call(smode=4) == EMODE and call(smode=0) == EMODE
     assert call(sdt=1) == EDTYPE                   # scales: fp32 or bf16
@@ -427,4 +428,20 @@ def test_multi_token_attention_validation(lib):
     assert call(cdt=5, kdim=64, vdim=128, vc=None) == EINVAL    # int4 needs its own V cache
     assert call(cdt=5, kdim=64, vdim=128, vc=None, NB=0, B=0) == 0
     assert call(cdt=5, kdim=64, vdim=128, smode=0) == EMODE     # int4 codes need scales
+    # int8 / float8_e4m3fn q: codes with q scales (modes 1-3, fp32 or bf16), an output dtype of
+    # its own, quantised caches only
+    assert call(qdt=3, qs=FAKE, qsm=2, odt=1, B=0) == 0
+    assert call(qdt=4, qs=FAKE, qsm=1, qsdt=2, odt=1, B=0) == 0
+    assert call(qdt=3, qs=FAKE, qsm=3, qsg=4, odt=2, B=0) == 0
+    assert call(qdt=3, qs=FAKE, qsm=3, qsg=3, odt=2) == EINVAL   # groups must divide head_size
+    assert call(qdt=3, qs=None, qsm=2, odt=1) == EINVAL
+    assert call(qdt=3, qs=FAKE, qsm=0, odt=1) == EMODE and call(qdt=3, qs=FAKE, qsm=4, odt=1) == EMODE
+    assert call(qdt=3, qs=FAKE, qsm=2, qsdt=1, odt=1) == EDTYPE   # q scales: fp32 or bf16
+    assert call(qdt=3, qs=FAKE, qsm=2, odt=3) == EDTYPE             # output: a float type
+    assert call(qdt=3, qs=FAKE, qsm=2, qsst=-1, odt=1) == EINVAL
+    assert call(qdt=3, qs=FAKE, qsm=2, odt=1, cdt=2, smode=0) == EDTYPE  # plain caches need q's dtype
+    assert call(qdt=2, odt=1) == EDTYPE                           # float q: out has q's dtype
+    # sparse-KV tables: one row per KV head or per query head
+    assert call(bth=2, B=0) == 0 and call(bth=8, B=0) == 0
+    assert call(bth=3) == EINVAL
 

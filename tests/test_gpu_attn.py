@@ -263,12 +263,20 @@ def test_attn_decode_on_configs4_pages(tmo, ref, dev):
 
 def run_attn_mq(tmo, ref, dev, case, q, cu=None, sink=None, scale=0.0883883, window=-1,
                 max_seq_q=-1, max_ctx=None, with_lse=True, Dv=None, mask=None,
-                compute_dtype=torch.float32):
+                compute_dtype=torch.float32, q_scale=None, out_dtype=None, kbit=None,
+                ref_scales=None):
     """Several query tokens per sequence: q [B, S, Hq, D] or [T, Hq, D] with cu.  The output
     ([..., Dv], Dv the V cache's head size or q's by default) starts as a sentinel, which rows
     of no sequence must keep.  case.v_cache None: K and V in one cache.  case.int4: int4-pair
-    caches (kv_cache_quant_bit_size 4).  mask [B, S, mask_len] in compute_dtype."""
+    caches (kv_cache_quant_bit_size 4).  mask [B, S, mask_len] in compute_dtype.  q_scale:
+    int8 / float8_e4m3fn q codes' scales, the output in out_dtype (half by default).  kbit
+    overrides the cache bit size (-1 with code caches of q's dtype: ref_scales are the unit
+    scales the oracle reads them with).  case.block_tables may be [B, heads, max_blocks]."""
+    kb = kbit
     kbit = 8 if case.k_cache.dtype in (torch.int8, torch.float8_e4m3fn) else -1
+    if kb is not None:
+        kbit = kb
+    odt = out_dtype or (torch.float16 if q_scale is not None else q.dtype)
     if case.int4:
         kbit = 4
         v_ch = case.v_cache.shape[2] == case.k_cache.shape[2]
@@ -277,11 +285,12 @@ def run_attn_mq(tmo, ref, dev, case, q, cu=None, sink=None, scale=0.0883883, win
     cpu = lambda t: t.cpu() if t is not None else None            # noqa: E731
     on_dev = lambda t: t if t is None or t.is_cuda else t.to(dev)  # noqa: E731  (views kept)
     ks, vs = cpu(case.k_scale), cpu(case.v_scale)
+    rks, rvs = ref_scales if ref_scales is not None else (ks, vs)
     want, wlse = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables,
-                                    case.context_lens, scale, ks, vs, case.alibi, window,
+                                    case.context_lens, scale, rks, rvs, case.alibi, window,
                                     cu_seq_q=cu, sink=sink, head_size_v=Dv, int4=case.int4,
-                                    mask=mask)
-    out = torch.full(q.shape[:-1] + (Dv,), 7.0, dtype=q.dtype, device=dev)
+                                    mask=mask, q_scale=q_scale)
+    out = torch.full(q.shape[:-1] + (Dv,), 7.0, dtype=odt, device=dev)
     res = tmo.single_query_cached_kv_attn(
         q.to(dev), case.k_cache.to(dev),
         case.v_cache.to(dev) if case.v_cache is not None else None, out,
@@ -292,14 +301,15 @@ def run_attn_mq(tmo, ref, dev, case, q, cu=None, sink=None, scale=0.0883883, win
         return_lse=with_lse, kv_cache_quant_bit_size=kbit, compute_dtype=compute_dtype,
         mask=mask.to(dev) if mask is not None else None,
         cu_seq_q=cu.to(dev) if cu is not None else None, max_seq_q=max_seq_q,
-        sink=sink.to(dev) if sink is not None else None)
+        sink=sink.to(dev) if sink is not None else None,
+        q_quant_scale=q_scale.to(dev) if q_scale is not None else None, out_dtype=odt)
     torch.cuda.synchronize()
     got = out.cpu().double()
     held = ~want.isnan()
     assert (got[~held] == 7.0).all(), "a row of no sequence was written"
-    vmax = _vmax(case, vs, Dv)
+    vmax = _vmax(case, rvs, Dv)
     err = (got - want).abs()
-    lim = RTOL[q.dtype] * want.abs() + ATOL[q.dtype] * vmax
+    lim = RTOL[odt] * want.abs() + ATOL[odt] * vmax
     bad = (err > lim) & held
     assert not bad.any(), (f"{int(bad.sum())} outputs off; worst {float((err / lim)[held].max()):.3g}x "
                            f"the tolerance at {tuple(bad.nonzero()[0].tolist())}")
@@ -610,3 +620,121 @@ def test_attn_mask_and_int4_rejections(tmo, dev):
                      c4.v_scale, c4.block_tables, c4.context_lens, int4=True)
     with pytest.raises(RuntimeError):                # V neither row nor channel pairs
         tmo.single_query_cached_kv_attn(q, *args(bad), kv_cache_quant_bit_size=4)
+
+
+# ---------------------------------------------------------------------------- quantised q, sparse-KV tables
+
+def _q_codes(dtype, shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    if dtype == torch.int8:
+        return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
+    return W.fp8_codes(shape, g)
+
+
+def _q_scale(form, lead, seed, dtype=torch.float32, groups=4):
+    g = torch.Generator().manual_seed(seed)
+    if form == "tensor":
+        return torch.tensor([0.0123]).to(dtype)
+    if form == "token":
+        return (0.002 + 0.02 * torch.rand(lead, generator=g)).to(dtype)
+    return (0.002 + 0.02 * torch.rand(tuple(lead) + (groups,), generator=g)).to(dtype)
+
+
+@pytest.mark.parametrize("kv,D", [("int8_token", 128), ("int8_token", 96), ("int8_channel", 128),
+                                  ("int8_channel", 96), ("fp8_token", 128), ("fp8_token", 96),
+                                  ("int4_token", 128)])
+@pytest.mark.parametrize("form", ["tensor", "token", "group"])
+@pytest.mark.parametrize("qdt", [torch.int8, torch.float8_e4m3fn])
+def test_attn_quantised_q(tmo, ref, dev, qdt, form, kv, D):
+    """int8 / float8_e4m3fn q with q_quant_scale per tensor, per token and head, or per channel
+    group (float32 and bfloat16 scales), over int8 / fp8 / int4 pages, on the MFMA (128) and
+    generic (96) kernels; 4-D q and cu_seq_q; the output in half (bfloat16 too for int8 q)."""
+    case = W.attn_case(torch.bfloat16, 140, kv=kv, B=5, Hq=8, Hkv=2, D=D, NB=64, max_ctx=150)
+    q4 = _q_codes(qdt, (5, 2, 8, D), 141)
+    qs4 = _q_scale(form, (5, 2, 8), 142, torch.bfloat16 if form == "token" else torch.float32)
+    run_attn_mq(tmo, ref, dev, case, q4, q_scale=qs4, sink=SINK8)
+    q3 = _q_codes(qdt, (9, 8, D), 143)
+    cu = torch.tensor([0, 3, 4, 4, 8, 9], dtype=torch.int32)
+    qs3 = _q_scale(form, (9, 8), 144)
+    odt = torch.bfloat16 if qdt == torch.int8 else torch.float16
+    run_attn_mq(tmo, ref, dev, case, q3, cu=cu, q_scale=qs3, out_dtype=odt, window=50)
+
+
+def test_attn_quantised_q_long_contexts(tmo, ref, dev):
+    """int8 q with per-token scales over a few thousand int8 keys, split over workgroups."""
+    case = W.attn_case(torch.bfloat16, 145, kv="int8_token", B=3, Hq=32, Hkv=8, D=128, BS=16,
+                       NB=800, max_ctx=4000)
+    q = _q_codes(torch.int8, (3, 1, 32, 128), 146)
+    run_attn_mq(tmo, ref, dev, case, q, q_scale=_q_scale("token", (3, 1, 32), 147))
+
+
+@pytest.mark.parametrize("qdt", [torch.int8, torch.float8_e4m3fn])
+def test_attn_quantised_q_same_as_q_caches(tmo, ref, dev, qdt):
+    """kv_cache_quant_bit_size -1 with caches of q's dtype (int8 / float8_e4m3fn codes, no cache
+    scales): the codes read as they are, i.e. with unit scales."""
+    case = W.attn_case(torch.bfloat16, 148, kv="int8_token" if qdt == torch.int8 else "fp8_token",
+                       B=4, Hq=8, Hkv=2, D=128, NB=64, max_ctx=120)
+    if qdt == torch.int8:   # small codes keep the unit-scale logits in range
+        case.k_cache = (case.k_cache // 16).contiguous()
+    ones = (torch.ones(2, 128), torch.ones(2, 128))
+    case.k_scale = case.v_scale = None
+    q = _q_codes(qdt, (4, 1, 8, 128), 149)
+    run_attn_mq(tmo, ref, dev, case, q, q_scale=torch.tensor([0.002]), kbit=-1, ref_scales=ones)
+
+
+def _sparse_tables(case, per, seed):
+    g = torch.Generator().manual_seed(seed)
+    bt = case.block_tables
+    rows = [bt]
+    for _ in range(per - 1):
+        rows.append(bt.reshape(-1)[torch.randperm(bt.numel(), generator=g)].reshape(bt.shape))
+    return torch.stack(rows, dim=1).contiguous()
+
+
+@pytest.mark.parametrize("kv,D", [("int8_token", 128), ("int8_token", 96), ("plain", 128),
+                                  ("plain", 96), ("int4_token", 128)])
+@pytest.mark.parametrize("per", ["kv", "q"])
+def test_attn_sparse_tables(tmo, ref, dev, kv, per, D):
+    """block_tables [batch, kv_heads or heads, max_blocks]: each KV head's (or query head's)
+    own pages; per-KV-head tables on the MFMA kernel, per-query-head tables with grouped heads
+    and head size 96 on the generic one; a missing page; 4-D q and cu_seq_q."""
+    case = W.attn_case(torch.bfloat16, 150, kv=kv, B=5, Hq=8, Hkv=2, D=D, NB=64, max_ctx=150)
+    case.block_tables = _sparse_tables(case, 2 if per == "kv" else 8, 151)
+    case.block_tables[2, 1, 1] = -1
+    q = W.attn_queries(torch.bfloat16, 152, B=5, Hq=8, D=D, S=2)
+    run_attn_mq(tmo, ref, dev, case, q, sink=SINK8)
+    q3, cu = W.attn_queries(torch.bfloat16, 153, B=5, Hq=8, D=D, counts=[3, 1, 0, 2, 4])
+    run_attn_mq(tmo, ref, dev, case, q3, cu=cu)
+
+
+def test_attn_sparse_tables_over_splits(tmo, ref, dev):
+    """Per-KV-head tables over a few thousand keys, 32 query heads, split over workgroups."""
+    case = W.attn_case(torch.bfloat16, 154, kv="int8_token", B=3, Hq=32, Hkv=8, D=128, BS=16,
+                       NB=800, max_ctx=4000)
+    case.block_tables = _sparse_tables(case, 8, 155)
+    q = W.attn_queries(torch.bfloat16, 156, B=3, Hq=32, D=128, S=1)
+    run_attn_mq(tmo, ref, dev, case, q)
+
+
+def test_attn_quantised_q_rejections(tmo, dev):
+    """q_quant_scale needs an int8 / float8_e4m3fn q and the reverse; float8_e4m3fn q takes a
+    half output; a float output needs a float dtype; block tables of another head count."""
+    case = W.attn_case(torch.bfloat16, 157, kv="int8_token", B=2, Hq=4, Hkv=2, D=64, max_ctx=40)
+    kc, vc = case.k_cache.to(dev), case.v_cache.to(dev)
+    bt, lens = case.block_tables.to(dev), case.context_lens.to(dev)
+    ks, vs = case.k_scale.to(dev), case.v_scale.to(dev)
+    qb = torch.randn(2, 1, 4, 64, device=dev).to(torch.bfloat16)
+    qi = torch.randint(-5, 5, (2, 1, 4, 64), device=dev, dtype=torch.int8)
+    qf = qi.to(torch.float8_e4m3fn)
+    s1 = torch.tensor([0.01], device=dev)
+    def call(q, out_dtype, qs, bt_=bt):
+        out = torch.empty(q.shape, dtype=out_dtype, device=dev)
+        return tmo.single_query_cached_kv_attn(q, kc, vc, out, bt_, lens, ks, vs, None, 40, -1, -1,
+                                               0.1, kv_cache_quant_bit_size=8, q_quant_scale=qs)
+    call(qi, torch.float16, s1)                                      # accepted
+    for q, odt, qs in ((qb, torch.bfloat16, s1), (qi, torch.float16, None),
+                       (qf, torch.bfloat16, s1), (qi, torch.int8, s1)):
+        with pytest.raises(RuntimeError):
+            call(q, odt, qs)
+    with pytest.raises(RuntimeError):
+        call(qb, torch.bfloat16, None, bt[:, None].expand(2, 3, -1).contiguous())

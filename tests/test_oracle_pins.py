@@ -1811,3 +1811,110 @@ def test_attn_mask_identities(ref):
     a = ref.cached_kv_attn(q, *args, mask=vals)
     b = ref.cached_kv_attn(q, *args, mask=vals.float())
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+# ---------------------------------------------------------------------------- quantised q, sparse-KV tables (D17)
+
+def _q_codes(dtype, shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    if dtype == torch.int8:
+        return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
+    return W.fp8_codes(shape, g)
+
+
+def _q_real(q, qs):
+    """q codes times q_quant_scale in float64: per tensor, per (token, head), per channel group."""
+    x = q.double()
+    s = qs.double()
+    if s.numel() == 1:
+        return x * s.reshape(())
+    if tuple(s.shape) == tuple(q.shape[:-1]):
+        return x * s[..., None]
+    G = s.shape[-1]
+    return x * s.repeat_interleave(q.shape[-1] // G, dim=-1)
+
+
+@pytest.mark.parametrize("qdt", [torch.int8, torch.float8_e4m3fn])
+@pytest.mark.parametrize("form", ["tensor", "token", "group"])
+def test_attn_quantised_q_matches_torch_float64(ref, qdt, form):
+    """int8 / float8_e4m3fn q with q_quant_scale (_ops.py:853-856, 868): the codes times their
+    scale in float64, attended by torch, against the oracle reading the codes -- 4-D q and
+    cu_seq_q, int8 pages, a sink, ALiBi."""
+    case = W.attn_case(torch.bfloat16, 131, kv="int8_token", Hq=8, Hkv=2, D=64, max_ctx=70)
+    q4 = _q_codes(qdt, (5, 3, 8, 64), 132)
+    q3 = _q_codes(qdt, (14, 8, 64), 133)
+    cu = torch.tensor([0, 4, 6, 6, 13, 14], dtype=torch.int32)
+    g = torch.Generator().manual_seed(134)
+    for q, c in ((q4, None), (q3, cu)):
+        lead = q.shape[:-1]
+        qs = {"tensor": torch.tensor([0.0123]),
+              "token": 0.002 + 0.02 * torch.rand(lead, generator=g),
+              "group": 0.002 + 0.02 * torch.rand(lead + (4,), generator=g)}[form]
+        case.alibi = (0.5 ** torch.arange(1, 9, dtype=torch.float32)).repeat(5, 1)
+        out, lse = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables,
+                                      case.context_lens, 0.125, case.k_scale, case.v_scale,
+                                      case.alibi, -1, cu_seq_q=c, sink=torch.linspace(-1, 1, 8),
+                                      q_scale=qs)
+        want, wlse = torch_attn_mq(case, _q_real(q, qs), 0.125, -1, c, torch.linspace(-1, 1, 8))
+        assert torch.allclose(out, want, rtol=1e-12, atol=1e-12, equal_nan=True)
+        assert torch.allclose(lse, wlse, rtol=1e-12, atol=1e-12, equal_nan=True)
+
+
+def test_attn_quantised_q_identities(ref):
+    """float8_e4m3fn q codes with a unit per-tensor scale equal a bfloat16 q holding the same
+    values (every e4m3fn value is a bfloat16 value) bit for bit; a per-token scale s equals
+    the per-tensor scale s when every token and head carries s."""
+    case = W.attn_case(torch.float16, 135, kv="int8_token", B=4, Hq=4, Hkv=2, D=32, max_ctx=50)
+    q = _q_codes(torch.float8_e4m3fn, (4, 2, 4, 32), 136)
+    args = (case.k_cache, case.v_cache, case.block_tables, case.context_lens, 0.2, case.k_scale,
+            case.v_scale)
+    a = ref.cached_kv_attn(q, *args, q_scale=torch.tensor([1.0]))
+    b = ref.cached_kv_attn(q.to(torch.bfloat16), *args)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    s = 0.0371
+    a = ref.cached_kv_attn(q, *args, q_scale=torch.full((4, 2, 4), s))
+    b = ref.cached_kv_attn(q, *args, q_scale=torch.tensor([s]))
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def _sparse_tables(case, per, seed):
+    """[B, per, max_blocks] tables: each head a different permutation of the case's pages (the
+    same pages, so every head reads valid blocks), head 0 the case's own table."""
+    g = torch.Generator().manual_seed(seed)
+    bt = case.block_tables
+    rows = [bt]
+    for _ in range(per - 1):
+        perm = torch.randperm(bt.numel(), generator=g)
+        rows.append(bt.reshape(-1)[perm].reshape(bt.shape))
+    return torch.stack(rows, dim=1).contiguous()
+
+
+@pytest.mark.parametrize("per", ["kv", "q"])
+def test_attn_sparse_tables_match_torch_float64(ref, per):
+    """block_tables [batch, head_num_kv or head_num_q, max_blocks] (_ops.py:834): each head
+    reads its own pages -- torch float64 over one head at a time with its row as the table,
+    against the oracle over all heads; with every row equal to the 2-D table, the 2-D result
+    bit for bit."""
+    case = W.attn_case(torch.bfloat16, 137, kv="int8_token", Hq=8, Hkv=2, D=32, max_ctx=60)
+    n = 2 if per == "kv" else 8
+    bt3 = _sparse_tables(case, n, 138)
+    q = W.attn_queries(torch.bfloat16, 139, B=5, Hq=8, D=32, S=2)
+    out, lse = ref.cached_kv_attn(q, case.k_cache, case.v_cache, bt3, case.context_lens, 0.3,
+                                  case.k_scale, case.v_scale)
+    g = 8 // 2
+    for hq in range(8):
+        hk = hq // g
+        row = bt3[:, hk if per == "kv" else hq]
+        sub = W.AttnCase(case.q, case.k_cache[:, hk:hk + 1].contiguous(),
+                         case.v_cache[:, hk:hk + 1].contiguous(),
+                         case.k_scale[:, hk:hk + 1].contiguous(), case.v_scale[:, hk:hk + 1].contiguous(),
+                         row.contiguous(), case.context_lens)
+        want, wlse = torch_attn_mq(sub, q[:, :, hq:hq + 1], 0.3)
+        assert torch.allclose(out[:, :, hq:hq + 1], want, rtol=1e-12, atol=1e-12)
+        assert torch.allclose(lse[:, :, hq:hq + 1], wlse, rtol=1e-12, atol=1e-12)
+    same = case.block_tables[:, None].expand(5, n, -1).contiguous()
+    a = ref.cached_kv_attn(q, case.k_cache, case.v_cache, same, case.context_lens, 0.3,
+                           case.k_scale, case.v_scale)
+    b = ref.cached_kv_attn(q, case.k_cache, case.v_cache, case.block_tables, case.context_lens,
+                           0.3, case.k_scale, case.v_scale)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
