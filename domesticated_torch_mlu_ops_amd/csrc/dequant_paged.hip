@@ -659,7 +659,8 @@ extern "C" int tmo_hip_dequant_from_paged_cache(
 // hipGetSymbolAddress (that device current) and kept in scratch_addr[]; host code passes only
 // that address to kernels.  Nothing in it has to start at zero: the pre-pass writes the page
 // count and every entry the main kernel uses before that kernel runs (stream order).  Calls
-// that overlap on one GPU (different streams, or other host threads) race on it.
+// on one GPU are ordered on it by the entry point itself (order_calls below); calls captured
+// into a HIP graph are ordered by that graph.
 static __device__ __align__(256) unsigned char scratch[TMO_HIP_DEQUANT_SCRATCH_BYTES];
 
 namespace tmo {
@@ -687,6 +688,21 @@ int scratch_of_current_device(void** out) {
   return TMO_OK;
 }
 
+// Ordering of the calls that share one GPU's scratch.  Host threads enqueue one at a time
+// (the device's mutex, held from the wait to the record); a call on a stream other than the
+// previous call's first makes its stream wait for the event recorded after the previous
+// call's kernels (hipStreamWaitEvent: a queue dependency, no host wait), so the two calls'
+// uses of the scratch never overlap; calls on one stream are already in order.  The event is
+// created on the first such call on the device and kept until the process ends.  A stream
+// under capture takes no event operation: the graph it is recorded into orders the call.
+struct CallOrder {
+  std::mutex mu;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool any = false;
+};
+CallOrder call_order[kMaxScratchDevices];
+
 }  // namespace
 }  // namespace tmo
 
@@ -708,16 +724,37 @@ extern "C" int tmo_hip_dequant_from_paged_cache_noalloc(
                                                        max_context_len, block_size);
   if (need > TMO_HIP_DEQUANT_SCRATCH_BYTES) return TMO_ERR_SCRATCH_TOO_SMALL;
   void* ws = nullptr;
-  if (need > 0) {
-    const int st = scratch_of_current_device(&ws);
-    if (st != TMO_OK) return st;
+  auto run = [&]() {
+    return dequant_paged(key, value, key_stride_token, key_stride_head, value_stride_token,
+                         value_stride_head, total_rows, key_cache, value_cache, key_scale,
+                         value_scale, context_lengths, context_seq_offset, block_tables, batch,
+                         max_blocks_per_seq, max_context_len, num_blocks, num_heads, block_size,
+                         head_size, quant_mode, quant_bit, out_dtype, cache_dtype, scale_dtype,
+                         ws, need > 0 ? (int64_t)TMO_HIP_DEQUANT_SCRATCH_BYTES : 0, stream);
+  };
+  if (need == 0) return run();  // nothing to do: no scratch, no kernel
+  const int st = scratch_of_current_device(&ws);
+  if (st != TMO_OK) return st;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return TMO_ERR_LAUNCH;
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(hs, &cap) != hipSuccess) return TMO_ERR_LAUNCH;
+  if (cap != hipStreamCaptureStatusNone) return run();
+  CallOrder& o = call_order[dev];
+  std::lock_guard<std::mutex> lock(o.mu);
+  if (o.any && o.last != hs && hipStreamWaitEvent(hs, o.done, 0) != hipSuccess)
+    return TMO_ERR_LAUNCH;
+  const int rc = run();
+  if (rc != TMO_OK) return rc;
+  if (!o.done && hipEventCreateWithFlags(&o.done, hipEventDisableTiming) != hipSuccess) {
+    o.done = nullptr;
+    return TMO_ERR_LAUNCH;
   }
-  return dequant_paged(key, value, key_stride_token, key_stride_head, value_stride_token,
-                       value_stride_head, total_rows, key_cache, value_cache, key_scale,
-                       value_scale, context_lengths, context_seq_offset, block_tables, batch,
-                       max_blocks_per_seq, max_context_len, num_blocks, num_heads, block_size,
-                       head_size, quant_mode, quant_bit, out_dtype, cache_dtype, scale_dtype, ws,
-                       need > 0 ? (int64_t)TMO_HIP_DEQUANT_SCRATCH_BYTES : 0, stream);
+  if (hipEventRecord(o.done, hs) != hipSuccess) return TMO_ERR_LAUNCH;
+  o.last = hs;
+  o.any = true;
+  return TMO_OK;
 }
 
 namespace tmo {

@@ -244,8 +244,11 @@ int64_t tmo_hip_dequant_workspace_bytes(int64_t batch, int64_t max_blocks_per_se
  * until the process ends, so batch * max_blocks_per_seq may be at most 262136 pages; a larger
  * call returns TMO_ERR_SCRATCH_TOO_SMALL before enqueueing anything (use the entry point above
  * with a workspace).  `stream` must belong to the current device.  Every call on one GPU
- * shares that array: calls that overlap on a GPU (other streams, other host threads) race, so
- * order them on one stream.
+ * shares that array, and the entry point orders the calls on it: host threads enqueue one at
+ * a time, and a call on a stream other than the previous call's makes its stream wait (on the
+ * GPU, hipStreamWaitEvent) for the previous call's kernels.  A call made while its stream is
+ * being captured into a HIP graph takes no event operation: the graph orders it, and two
+ * graphs holding such calls must not be replayed at the same time on one GPU.
  */
 int tmo_hip_dequant_from_paged_cache_noalloc(void* key, void* value,
                                              int64_t key_stride_token, int64_t key_stride_head,

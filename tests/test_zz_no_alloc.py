@@ -2,7 +2,9 @@
 library's static device scratch) against tmo_hip_dequant_from_paged_cache with a caller
 workspace, through the C ABI: two calls in a row on one GPU, the second with a smaller input,
 each bit-exact against the allocating entry point's output and the oracle; the bytes past the
-smaller call's rows keep their sentinel; a call beyond the scratch is refused."""
+smaller call's rows keep their sentinel; two calls enqueued on two streams with no host wait
+between them (the entry point orders them on the shared scratch) give the same results as one
+after the other; a call beyond the scratch is refused."""
 import ctypes
 
 import pytest
@@ -40,7 +42,8 @@ def _layout(seed, B, MB, NB, H=8, BS=16, D=128):
     return W.DequantLayout(f"noalloc{seed}", ctx, bt, NB, BS), (kc, vc, ks, vs)
 
 
-def _call(L, fn, out_k, out_v, caches, layout, workspace=None):
+def _args(out_k, out_v, caches, layout):
+    """C-ABI arguments (and the device index tensors they point into, to keep alive)."""
     kc, vc, ks, vs = caches
     NB, H, BS, D = kc.shape
     ctx = layout.context_lengths.to(out_k.device)
@@ -50,6 +53,11 @@ def _call(L, fn, out_k, out_v, caches, layout, workspace=None):
             out_v.stride(1), out_k.shape[0], kc.data_ptr(), vc.data_ptr(), ks.data_ptr(),
             vs.data_ptr(), ctx.data_ptr(), None, bt.data_ptr(), B, MB,
             layout.max_context_len, NB, H, BS, D, 1, 8, 2, 3, 0]
+    return args, (ctx, bt)
+
+
+def _call(L, fn, out_k, out_v, caches, layout, workspace=None):
+    args, keep = _args(out_k, out_v, caches, layout)
     torch.cuda.synchronize()
     if fn == "noalloc":
         st = L.tmo_hip_dequant_from_paged_cache_noalloc(*args, None)
@@ -85,6 +93,40 @@ def test_noalloc_matches_workspace_entry_point(ref, dev):
             a = outs["noalloc"][i].view(torch.int16)
             assert torch.equal(a, outs["workspace"][i].view(torch.int16)), name
             assert torch.equal(a, (want_k, want_v)[i].view(torch.int16)), name
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(dev):
+    """A large call on one stream and a small one on another, enqueued back to back: the
+    second call's page-list pass rewrites the shared scratch, so it must wait for the first
+    call's kernels; each output is compared with the allocating entry point's, computed one
+    call at a time."""
+    L = _lib()
+    cases = []
+    for seed, B, MB, NB in ((4, 64, 64, 4096), (5, 5, 7, 64)):
+        layout, caches_h = _layout(seed, B, MB, NB)
+        caches = tuple(t.to(dev) for t in caches_h)
+        total = layout.total_tokens
+        print(f"[noalloc streams] B={B} pages/seq={MB} tokens={total}", flush=True)
+        ws = torch.empty(L.tmo_hip_dequant_workspace_bytes(B, MB, layout.max_context_len, 16),
+                         dtype=torch.uint8, device=dev)
+        wk = torch.full((total, 8, 128), -3.0, device=dev).to(torch.bfloat16)
+        wv = wk.clone()
+        assert _call(L, "workspace", wk, wv, caches, layout, ws) == 0
+        ok = torch.full((total, 8, 128), -5.0, device=dev).to(torch.bfloat16)
+        ov = ok.clone()
+        cases.append((layout, caches, (wk.cpu(), wv.cpu()), (ok, ov)))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    keep = []
+    torch.cuda.synchronize()
+    for (layout, caches, _, (ok, ov)), st in zip(cases, streams):
+        args, k = _args(ok, ov, caches, layout)
+        keep.append(k)
+        assert L.tmo_hip_dequant_from_paged_cache_noalloc(*args, ctypes.c_void_p(st.cuda_stream)) == 0
+    torch.cuda.synchronize()
+    for layout, _, want, got in cases:
+        for i, name in enumerate(("key", "value")):
+            assert torch.equal(got[i].cpu().view(torch.int16), want[i].view(torch.int16)), \
+                (layout.name, name)
 
 
 def test_noalloc_refuses_calls_beyond_the_scratch(dev):
