@@ -15,9 +15,10 @@
 // scale stores one contiguous run.  K and V of the same (token, head) are handled by the same
 // lanes, and each lane group takes several tokens, so every lane has several independent
 // 16-byte loads in flight.  The row amax
-// is a DPP reduction inside the lane group; the divide is the reciprocal + two-FMA-step
-// quotient of tmo_device.h (bit-identical to IEEE division); codes and scales are written
-// with non-temporal stores (the cache is written once per step and read by other kernels).
+// is a DPP reduction inside the lane group; the divide is the fp64-product quotient of
+// tmo_device.h (div_recip64, bit-identical to IEEE division); codes are written with
+// non-temporal stores (the cache is written once per step and read by other kernels), the
+// 4-byte scales with plain stores (neighbouring heads' scales share a line).
 #include "tmo_device.h"
 
 namespace tmo {
@@ -149,7 +150,9 @@ __global__ __launch_bounds__(256) void quant_paged_vec(QuantPagedParams p) {
             store_nt(reinterpret_cast<uint32_t*>(dst), c[0]);
           }
         }
-        if (lane == 0) __builtin_nontemporal_store(rs.s, p.scale[kv] + page_row);
+        // A plain store: the 4-byte scales of neighbouring heads share a line, which the L2 of
+        // the tile's XCD merges (configs[0]: 2.96 -> 2.69 us per call, larger calls unchanged)
+        if (lane == 0) p.scale[kv][page_row] = rs.s;
       }
     }
   }
