@@ -2,7 +2,9 @@
 the CPU oracle (oracle/tmo_oracle.c, pinned by tests/test_oracle_pins.py) gives for them, and
 MANIFEST.sha256.  The fixtures freeze those pinned results as data, so that a change to the
 oracle or to a kernel that alters any code, scale or output bit fails tests/test_golden.py
-(oracle) or tests/test_gpu_golden.py (HIP kernels) even when both change together.
+(oracle) or tests/test_gpu_golden.py (HIP kernels) even when both change together;
+tests/test_golden_torch.py checks every stored output against the torch restatements of the
+reference math, independently of the oracle.
 
     python tests/golden/make_fixtures.py        # from the repository root; CPU only
 
