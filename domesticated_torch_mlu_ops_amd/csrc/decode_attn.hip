@@ -725,6 +725,23 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
         }
       }
 
+      // int4 V: the nibbles of token 4 grp + e moved into the high half of their bytes, so
+      // each byte read as signed is 16 x the code (the low nibble shifted up, the other half
+      // cleared; one mask per dword, kept whole in a register -- left to the combiner, the
+      // masks were split into per-byte shifts and extractions)
+      uint32_t vm[kInt4 ? 4 : 1][kInt4 ? kVW : 1];
+      if constexpr (kInt4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int u = 0; u < kVW; ++u) {
+            const uint32_t w = r.vw[e >> 1][u];
+            uint32_t m = ((e & 1) ? (w << 4) : w) & 0xF0F0F0F0u;
+            asm("" : "+v"(m));
+            vm[e][u] = m;
+          }
+      }
+
       // ---- O^T += V^T P^T: MFMA j takes channel col * kDV + j of tokens 4 grp .. + 3
 #pragma unroll
       for (int j = 0; j < kDV; ++j) {
@@ -738,12 +755,13 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
           }
         } else if constexpr (kInt4) {
           // channel j's byte of pair row e / 2 holds tokens 4 grp + e (high nibble, e even)
-          // and + 1 (low nibble): the sign-extended nibble, exact as bf16
+          // and + 1 (low nibble); byte j & 3 of the masked dword is 16 x the code: one
+          // sign-extending byte conversion, as for int8 codes, exact as bf16.  The factor 16
+          // leaves with the normalisation (exactly: a power of two).
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int code = __builtin_amdgcn_sbfe((int)r.vw[e >> 1][j >> 2],
-                                                   8 * (j & 3) + ((e & 1) ? 0 : 4), 4);
-            b4[e] = (short)(__float_as_uint((float)code) >> 16);
+            const int8_t c16 = (int8_t)(vm[e][j >> 2] >> (8 * (j & 3)));
+            b4[e] = (short)(__float_as_uint((float)c16) >> 16);
           }
         } else if constexpr (kKind == 3) {
           // the e4m3fn value's fp32 pattern truncated to bf16 is exact (<= 4 significant bits)
@@ -858,7 +876,10 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   if (!qvalid) return;
   const bool direct = p.splits == 1;
   float lse_v;
-  const float inv = direct ? finish(p, hq, mx, lt, &lse_v) : (lt > 0.0f ? 1.0f / lt : 0.0f);
+  // int4 V operands carry 16 x the codes: the power-of-two factor is exact, so the outputs
+  // are those of the codes themselves bit for bit
+  const float inv = (direct ? finish(p, hq, mx, lt, &lse_v) : (lt > 0.0f ? 1.0f / lt : 0.0f)) *
+                    (kInt4 ? 0.0625f : 1.0f);
   float* ws_row = p.ws + ((((i * p.Hkv + hk) * p.splits + split) * p.ncols + c) * (int64_t)(kD + 2));
   if (!direct && grp == 0) {
     ws_row[0] = mx;
