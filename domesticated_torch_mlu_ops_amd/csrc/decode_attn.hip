@@ -380,6 +380,19 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
   if (p.window >= 0 && pos - (int32_t)p.window > klo) klo = pos - (int32_t)p.window;
   if (pos < khi) khi = pos;
   if (!qvalid) khi = klo - 1;
+  // Tiles inside every valid column's keys need no per-key range test: [t0, t0 + 15] within
+  // [wklo, wkhi], the largest klo and the smallest khi over the block's valid columns
+  // (wave-uniform; the 16 columns are the lanes of each row, order-preserving u32 maxima).
+  // Padding columns then carry scores of keys outside their range, which no output reads.
+  int32_t wklo, wkhi;
+  {
+    const uint32_t lo = qvalid ? ((uint32_t)klo ^ 0x80000000u) : 0u;
+    const uint32_t hi = qvalid ? ~((uint32_t)khi ^ 0x80000000u) : 0u;
+    wklo = (int32_t)((uint32_t)__builtin_amdgcn_readfirstlane((int)group_max_u32<16>(lo)) ^
+                     0x80000000u);
+    wkhi = (int32_t)(~(uint32_t)__builtin_amdgcn_readfirstlane((int)group_max_u32<16>(hi)) ^
+                     0x80000000u);
+  }
   // The block's tiles: from its first valid token's window start to its last token's P
   // (wave-uniform: every lane computes the same numbers)
   int64_t bbeg = rg.begin, bend = rg.end;
@@ -646,14 +659,24 @@ __global__ __launch_bounds__(256, (attn_min_blocks(kD, kKind))) void attn_mfma(A
       float sc[4];
       float tmax = -__builtin_inff();
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int32_t j = t0 + 4 * grp + e;
-        float v = (s[e] - qk_off) * (raw_scale(r.ks, e) * score_scale);
-        if (p.alibi) v += alibi * (float)(j - pos);
-        if (j < klo || j > khi) v = -__builtin_inff();
-        sc[e] = v;
-        tmax = fmaxf(tmax, v);
+      for (int e = 0; e < 4; ++e) sc[e] = (s[e] - qk_off) * (raw_scale(r.ks, e) * score_scale);
+      // ALiBi and the key-range test as wave-uniform branches (if-converted, both ran on
+      // every tile: ~36 VALU per tile, a tenth of the int4 kernel's)
+      if (p.alibi) {
+        keep_branch();
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[e] += alibi * (float)(t0 + 4 * grp + e - pos);
       }
+      if (t0 < wklo || t0 + 15 > wkhi) {
+        keep_branch();
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int32_t j = t0 + 4 * grp + e;
+          if (j < klo || j > khi) sc[e] = -__builtin_inff();
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, sc[e]);
       // mask terms of the last mask_len keys: only the tiles that reach them (wave-uniform)
       if (kMask && t0 + 15 >= mask_lo) {
         // the column's row of terms (recomputed here: nothing stays live across the tiles;
