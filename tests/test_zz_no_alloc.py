@@ -4,7 +4,8 @@ workspace, through the C ABI: two calls in a row on one GPU, the second with a s
 each bit-exact against the allocating entry point's output and the oracle; the bytes past the
 smaller call's rows keep their sentinel; two calls enqueued on two streams with no host wait
 between them (the entry point orders them on the shared scratch) give the same results as one
-after the other; a call beyond the scratch is refused."""
+after the other, and so do calls from two host threads on their own streams; a call beyond the
+scratch is refused."""
 import ctypes
 
 import pytest
@@ -127,6 +128,55 @@ def test_noalloc_calls_on_two_streams_are_ordered(dev):
         for i, name in enumerate(("key", "value")):
             assert torch.equal(got[i].cpu().view(torch.int16), want[i].view(torch.int16)), \
                 (layout.name, name)
+
+
+def test_noalloc_calls_from_two_host_threads(dev):
+    """Two host threads, each enqueueing calls on its own stream with no host wait between
+    them (ctypes releases the GIL during the call, so the enqueues interleave): every output
+    equals the allocating entry point's."""
+    import threading
+    L = _lib()
+    cases = []
+    for seed, B, MB, NB in ((6, 32, 48, 2048), (7, 9, 11, 128)):
+        layout, caches_h = _layout(seed, B, MB, NB)
+        caches = tuple(t.to(dev) for t in caches_h)
+        total = layout.total_tokens
+        print(f"[noalloc threads] B={B} pages/seq={MB} tokens={total}", flush=True)
+        ws = torch.empty(L.tmo_hip_dequant_workspace_bytes(B, MB, layout.max_context_len, 16),
+                         dtype=torch.uint8, device=dev)
+        wk = torch.full((total, 8, 128), -3.0, device=dev).to(torch.bfloat16)
+        wv = wk.clone()
+        assert _call(L, "workspace", wk, wv, caches, layout, ws) == 0
+        outs = [(torch.full((total, 8, 128), -5.0, device=dev).to(torch.bfloat16),
+                 torch.full((total, 8, 128), -5.0, device=dev).to(torch.bfloat16))
+                for _ in range(4)]
+        cases.append((layout, caches, (wk.cpu(), wv.cpu()), outs))
+    torch.cuda.synchronize()
+    status = []
+
+    def worker(case):
+        layout, caches, _, outs = case
+        st = torch.cuda.Stream()
+        keep = []
+        for ok, ov in outs:
+            args, k = _args(ok, ov, caches, layout)
+            keep.append(k)
+            status.append(L.tmo_hip_dequant_from_paged_cache_noalloc(
+                *args, ctypes.c_void_p(st.cuda_stream)))
+        st.synchronize()
+
+    threads = [threading.Thread(target=worker, args=(c,)) for c in cases]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert status == [0] * 8
+    for layout, _, want, outs in cases:
+        for ok, ov in outs:
+            for got, w, name in ((ok, want[0], "key"), (ov, want[1], "value")):
+                assert torch.equal(got.cpu().view(torch.int16), w.view(torch.int16)), \
+                    (layout.name, name)
 
 
 def test_noalloc_refuses_calls_beyond_the_scratch(dev):
